@@ -1,0 +1,111 @@
+/*
+ * dressi_oracle.h -- CPU restatement of the reference's HardSoftRas
+ * silhouette hot path. TEST INFRASTRUCTURE ONLY: used by tests/, by
+ * __graft_entry__.smoke() as the checker, and by bench.py's cpu_baseline
+ * leg. The product path (opendressi_amd/, include/dressi_hip.h) never links,
+ * loads or calls it.
+ *
+ * Layout conventions follow the reference: {N,1} arrays are tightly packed
+ * logical channels (VEC3 = 3 floats, VEC4 = 4 floats), face indices are
+ * stored as floats, {V,deg} adjacency is row-major (d*V + v) with -1 padding,
+ * screen images are row-major with row 0 at NDC y = -1.
+ */
+#ifndef DRESSI_ORACLE_H
+#define DRESSI_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scene generation ---------------------------------------------------- */
+/* examples/common/geometry_utils.cpp:24-84 (GenerateIcosphere); counts only
+ * when pos/faces are NULL */
+int or_icosphere(uint32_t level, uint32_t* n_verts, uint32_t* n_faces,
+                 float* pos, float* faces);
+/* examples/common/asset_utils.cpp:719-766 (Mul, LookAt, PerspectiveVk) */
+void or_mat4_mul(const float a[16], const float b[16], float r[16]);
+void or_look_at(const float eye[3], const float center[3], const float up[3],
+                float m[16]);
+void or_perspective_vk(float fovy_rad, float aspect, float z_near,
+                       float z_far, float m[16]);
+/* SplitMix64 -> Box-Muller standard normals (scene noise; no reference
+ * counterpart -- the configs only say "seeded N(0, s)") */
+void or_randn(uint64_t seed, uint32_t n, float* out);
+/* examples/common/asset_utils.cpp:768-782 (TransformToClip) */
+void or_transform_to_clip(const float* pos, uint32_t n_verts,
+                          const float mvp[16], float* clip);
+
+/* ---- mesh topology ------------------------------------------------------- */
+/* src/core/mesh_utils.cpp:53-71 (VertexFacesTex). Returns max degree;
+ * writes deg*V floats when out != NULL and cap >= deg*V. */
+uint32_t or_vertex_faces_tex(const float* faces, uint32_t n_faces,
+                             uint32_t n_verts, float* out, uint32_t cap);
+
+/* ---- ops (each mirrors one reference op's CPU kernel) ---------------------- */
+void or_soft_clip(const float* clip, uint32_t n_verts, const float* faces,
+                  uint32_t n_faces, uint32_t w, uint32_t h, float radius,
+                  float* out);
+void or_rasterize_soft(const float* soft_clip, const float* face_id,
+                       const float* faces_soft, const float* hard_clip,
+                       uint32_t n_verts, const float* faces_tex,
+                       uint32_t n_faces, uint32_t w, uint32_t h, float radius,
+                       const float* prev, float* out);
+void or_rasterize(const float* clip, uint32_t n_verts, const float* attr,
+                  uint32_t n_comp, const float* faces, uint32_t n_faces,
+                  uint32_t w, uint32_t h, float* out);
+void or_rasterize_face_id(const float* clip, uint32_t n_verts,
+                          const float* faces, uint32_t n_faces, uint32_t w,
+                          uint32_t h, float* out);
+void or_lookup_faces(const float* attr, uint32_t n_comp, const float* faces,
+                     uint32_t n_faces, uint32_t corner, float* out);
+void or_lookup_faces_bwd(const float* gy, uint32_t n_comp, const float* faces,
+                         uint32_t n_faces, const float* vtx_faces,
+                         uint32_t n_verts, uint32_t max_deg, uint32_t corner,
+                         float* out);
+void or_face_fetch(const float* attr, uint32_t n_comp, uint32_t n_faces,
+                   const float* idx, uint32_t w, uint32_t h, float* out);
+void or_face_fetch_bwd(const float* gy, uint32_t n_comp, const float* idx,
+                       uint32_t w, uint32_t h, const float* prj0,
+                       const float* prj1, const float* prj2, uint32_t n_faces,
+                       float seed, float radius, uint32_t n_samples,
+                       float* out);
+uint32_t or_wang_hash(uint32_t x);
+float or_hash_to_unit(uint32_t f, uint32_t s, uint32_t seed, uint32_t salt);
+
+/* ---- the HardSoftRas silhouette iteration ---------------------------------- */
+/* Per-pixel forward of the example's soft-probability chain + silhouette
+ * composition + L2 term (examples/silhouette_optimization/run.cpp:253-342,
+ * 382-393). `rs` is the RasterizeSoft output image (VEC4), `tri[k]` the
+ * LookupFaces outputs {F,4}. Writes pred and the per-view loss image. */
+void or_hsr_forward(const float* rs, const float* tri0, const float* tri1,
+                    const float* tri2, uint32_t n_faces, const float* target,
+                    uint32_t w, uint32_t h, float radius, float* pred,
+                    float* view_loss);
+/* Per-pixel backward of the same chain: the gradient images (VEC4 {S,S})
+ * reaching FaceFetch(tri0/1/2), as the reference's BuildBackward composes
+ * them (src/core/build_backward.cpp:62-149). */
+void or_hsr_backward(const float* rs, const float* tri0, const float* tri1,
+                     const float* tri2, uint32_t n_faces, const float* target,
+                     uint32_t w, uint32_t h, float radius, float* gy0,
+                     float* gy1, float* gy2);
+
+/* Whole fit, same contract as the reference harness (oracle/ref_harness.cpp
+ * refh_hsr_fit): all outputs nullable. `n_threads` > 1 splits the per-view
+ * work over POSIX threads (views are independent until the pos gradient). */
+int or_hsr_fit(const float* pos0, uint32_t n_verts, const float* faces,
+               uint32_t n_faces, const float* tgt_pos, uint32_t n_tverts,
+               const float* tgt_faces, uint32_t n_tfaces, const float* mvps,
+               uint32_t n_views, uint32_t screen_px, float radius_px,
+               uint32_t samples, float lr, uint32_t iters, float* out_pos,
+               float* out_m, float* out_v, float* out_t, float* out_loss,
+               float* out_grad0, float* out_pred0, float* out_target,
+               float* out_rs0, float* out_lossimg0);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DRESSI_ORACLE_H */

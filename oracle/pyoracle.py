@@ -1,0 +1,284 @@
+"""ctypes front-end of the CPU oracle (liboracle.so) and of the reference's own
+CPU build (oracle/_ref/libdressi_ref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() (as the
+checker) and bench.py's cpu_baseline leg. The product package never imports
+this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libdressi_ref.so")
+REF_ROOT = "/root/reference"
+
+_F = C.POINTER(C.c_float)
+_U32 = C.c_uint32
+
+
+def build(ref: bool = False) -> None:
+    """Compile liboracle.so (and, when asked and the reference checkout is
+    present, the reference harness)."""
+    subprocess.run(["make", "-s", "-C", HERE, "liboracle.so"], check=True)
+    if ref and os.path.isdir(REF_ROOT):
+        subprocess.run(["make", "-s", "-C", HERE, "ref", f"REF={REF_ROOT}"], check=True)
+
+
+def _fp(a):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], (a.dtype, a.flags)
+    return a.ctypes.data_as(_F)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class _Lib:
+    prefix = ""
+
+    def __init__(self, path: str):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.lib = C.CDLL(path)
+
+    def fn(self, name):
+        return getattr(self.lib, self.prefix + name)
+
+    # ---- ops shared by both libraries (same argument lists) ---------------
+    def soft_clip(self, clip, faces, w, h, radius):
+        clip, faces = _f32(clip), _f32(faces)
+        nv, nf = clip.shape[0], faces.shape[0]
+        out = np.zeros((3 * nf, 4), np.float32)
+        self._call("soft_clip", _fp(clip), _U32(nv), _fp(faces), _U32(nf), _U32(w), _U32(h),
+                   C.c_float(radius), _fp(out))
+        return out
+
+    def rasterize(self, clip, attr, faces, w, h):
+        clip, attr, faces = _f32(clip), _f32(attr), _f32(faces)
+        if attr.ndim == 1:
+            attr = attr[:, None]
+        nc = attr.shape[1]
+        out = np.zeros((h, w, nc), np.float32)
+        self._call("rasterize", _fp(clip), _U32(clip.shape[0]), _fp(attr), _U32(nc), _fp(faces),
+                   _U32(faces.shape[0]), _U32(w), _U32(h), _fp(out))
+        return out
+
+    def rasterize_face_id(self, clip, faces, w, h):
+        clip, faces = _f32(clip), _f32(faces)
+        out = np.zeros((h, w), np.float32)
+        self._call("rasterize_face_id", _fp(clip), _U32(clip.shape[0]), _fp(faces),
+                   _U32(faces.shape[0]), _U32(w), _U32(h), _fp(out))
+        return out
+
+    def face_fetch(self, attr, idx):
+        attr, idx = _f32(attr), _f32(idx)
+        nc = attr.shape[1]
+        h, w = idx.shape
+        out = np.zeros((h, w, nc), np.float32)
+        self._call("face_fetch", _fp(attr), _U32(nc), _U32(attr.shape[0]), _fp(idx), _U32(w),
+                   _U32(h), _fp(out))
+        return out
+
+    def face_fetch_bwd(self, gy, idx, prj0, prj1, prj2, seed, radius, n_samples):
+        gy, idx = _f32(gy), _f32(idx)
+        prj0, prj1, prj2 = _f32(prj0), _f32(prj1), _f32(prj2)
+        h, w = idx.shape
+        nc = gy.shape[-1]
+        nf = prj0.shape[0]
+        out = np.zeros((nf, nc), np.float32)
+        self._call("face_fetch_bwd", _fp(gy), _U32(nc), _fp(idx), _U32(w), _U32(h), _fp(prj0),
+                   _fp(prj1), _fp(prj2), _U32(nf), C.c_float(seed), C.c_float(radius),
+                   _U32(n_samples), _fp(out))
+        return out
+
+    def lookup_faces_bwd(self, gy, faces, vtx_faces, corner):
+        gy, faces, vtx_faces = _f32(gy), _f32(faces), _f32(vtx_faces)
+        nc = gy.shape[1]
+        deg, nv = vtx_faces.shape
+        out = np.zeros((nv, nc), np.float32)
+        self._call("lookup_faces_bwd", _fp(gy), _U32(nc), _fp(faces), _U32(faces.shape[0]),
+                   _fp(vtx_faces), _U32(nv), _U32(deg), _U32(corner), _fp(out))
+        return out
+
+    def hsr_fit(self, pos0, faces, tgt_pos, tgt_faces, mvps, screen, radius=3.0, samples=8,
+                lr=1e-3, iters=1, want_images=True):
+        pos0, faces = _f32(pos0), _f32(faces)
+        tgt_pos, tgt_faces, mvps = _f32(tgt_pos), _f32(tgt_faces), _f32(mvps)
+        nv, nf = pos0.shape[0], faces.shape[0]
+        n = mvps.shape[0]
+        s = screen
+        r = dict(pos=np.zeros((nv, 3), np.float32), m=np.zeros((nv, 3), np.float32),
+                 v=np.zeros((nv, 3), np.float32), t=np.zeros(1, np.float32),
+                 loss=np.zeros(max(iters, 1), np.float32), grad0=np.zeros((nv, 3), np.float32))
+        if want_images:
+            r.update(pred0=np.zeros((n, s, s), np.float32), target=np.zeros((n, s, s), np.float32),
+                     rs0=np.zeros((n, s, s, 4), np.float32), lossimg0=np.zeros((s, s), np.float32))
+        g = r.get
+        self._call("hsr_fit", _fp(pos0), _U32(nv), _fp(faces), _U32(nf), _fp(tgt_pos),
+                   _U32(tgt_pos.shape[0]), _fp(tgt_faces), _U32(tgt_faces.shape[0]), _fp(mvps),
+                   _U32(n), _U32(s), C.c_float(radius), _U32(samples), C.c_float(lr),
+                   _U32(iters), _fp(r["pos"]), _fp(r["m"]), _fp(r["v"]), _fp(r["t"]),
+                   _fp(r["loss"]), _fp(r["grad0"]), _fp(g("pred0")), _fp(g("target")),
+                   _fp(g("rs0")), _fp(g("lossimg0")))
+        return r
+
+
+class Oracle(_Lib):
+    """The C restatement (oracle/dressi_oracle.c)."""
+
+    prefix = "or_"
+
+    def __init__(self, path: str = ORACLE_SO):
+        super().__init__(path)
+        self.fn("hash_to_unit").restype = C.c_float
+        self.fn("wang_hash").restype = C.c_uint32
+        self.fn("vertex_faces_tex").restype = C.c_uint32
+
+    def _call(self, name, *args):
+        self.fn(name)(*args)
+
+    def rasterize_soft(self, soft_clip, face_id, faces_soft, hard_clip, faces_tex, w, h, radius,
+                       prev=None, vtx_faces=None):
+        sc, fi, fs = _f32(soft_clip), _f32(face_id), _f32(faces_soft)
+        hc, ft = _f32(hard_clip), _f32(faces_tex)
+        out = np.zeros((h, w, 4), np.float32)
+        self.fn("rasterize_soft")(_fp(sc), _fp(fi), _fp(fs), _fp(hc), _U32(hc.shape[0]), _fp(ft),
+                                  _U32(ft.shape[0]), _U32(w), _U32(h), C.c_float(radius),
+                                  _fp(None if prev is None else _f32(prev)), _fp(out))
+        return out
+
+    def lookup_faces(self, attr, faces, corner):
+        attr, faces = _f32(attr), _f32(faces)
+        out = np.zeros((faces.shape[0], attr.shape[1]), np.float32)
+        self.fn("lookup_faces")(_fp(attr), _U32(attr.shape[1]), _fp(faces), _U32(faces.shape[0]),
+                                _U32(corner), _fp(out))
+        return out
+
+    def vertex_faces_tex(self, faces, n_verts):
+        faces = _f32(faces)
+        deg = self.fn("vertex_faces_tex")(_fp(faces), _U32(faces.shape[0]), _U32(n_verts), None,
+                                          _U32(0))
+        out = np.zeros((deg, n_verts), np.float32)
+        self.fn("vertex_faces_tex")(_fp(faces), _U32(faces.shape[0]), _U32(n_verts), _fp(out),
+                                    _U32(out.size))
+        return out
+
+    def icosphere(self, level):
+        nv, nf = _U32(), _U32()
+        self.fn("icosphere")(_U32(level), C.byref(nv), C.byref(nf), None, None)
+        pos = np.zeros((nv.value, 3), np.float32)
+        faces = np.zeros((nf.value, 3), np.float32)
+        self.fn("icosphere")(_U32(level), C.byref(nv), C.byref(nf), _fp(pos), _fp(faces))
+        return pos, faces
+
+    def look_at(self, eye, center=(0, 0, 0), up=(0, 1, 0)):
+        e, c, u = _f32(eye), _f32(center), _f32(up)
+        m = np.zeros(16, np.float32)
+        self.fn("look_at")(_fp(e), _fp(c), _fp(u), _fp(m))
+        return m
+
+    def perspective_vk(self, fovy, aspect, zn, zf):
+        m = np.zeros(16, np.float32)
+        self.fn("perspective_vk")(C.c_float(fovy), C.c_float(aspect), C.c_float(zn),
+                                  C.c_float(zf), _fp(m))
+        return m
+
+    def mat4_mul(self, a, b):
+        r = np.zeros(16, np.float32)
+        self.fn("mat4_mul")(_fp(_f32(a)), _fp(_f32(b)), _fp(r))
+        return r
+
+    def randn(self, seed, n):
+        out = np.zeros(n, np.float32)
+        self.fn("randn")(C.c_uint64(seed), _U32(n), _fp(out))
+        return out
+
+    def transform_to_clip(self, pos, mvp):
+        pos = _f32(pos)
+        out = np.zeros((pos.shape[0], 4), np.float32)
+        self.fn("transform_to_clip")(_fp(pos), _U32(pos.shape[0]), _fp(_f32(mvp)), _fp(out))
+        return out
+
+    def hash_to_unit(self, f, s, seed, salt):
+        return self.fn("hash_to_unit")(_U32(f), _U32(s), _U32(seed), _U32(salt))
+
+    def wang_hash(self, x):
+        return self.fn("wang_hash")(_U32(x))
+
+    def hsr_forward(self, rs, tri0, tri1, tri2, target, radius):
+        rs, target = _f32(rs), _f32(target)
+        h, w = target.shape
+        pred = np.zeros((h, w), np.float32)
+        vl = np.zeros((h, w), np.float32)
+        self.fn("hsr_forward")(_fp(rs), _fp(_f32(tri0)), _fp(_f32(tri1)), _fp(_f32(tri2)),
+                               _U32(tri0.shape[0]), _fp(target), _U32(w), _U32(h),
+                               C.c_float(radius), _fp(pred), _fp(vl))
+        return pred, vl
+
+    def hsr_backward(self, rs, tri0, tri1, tri2, target, radius):
+        rs, target = _f32(rs), _f32(target)
+        h, w = target.shape
+        gys = [np.zeros((h, w, 4), np.float32) for _ in range(3)]
+        self.fn("hsr_backward")(_fp(rs), _fp(_f32(tri0)), _fp(_f32(tri1)), _fp(_f32(tri2)),
+                                _U32(tri0.shape[0]), _fp(target), _U32(w), _U32(h),
+                                C.c_float(radius), *[_fp(g) for g in gys])
+        return gys
+
+
+class Reference(_Lib):
+    """The reference's own CPU evaluator (oracle/_ref, built from the reference
+    sources by oracle/Makefile)."""
+
+    prefix = "refh_"
+
+    def __init__(self, path: str = REF_SO):
+        super().__init__(path)
+        self.fn("last_error").restype = C.c_char_p
+
+    def _call(self, name, *args):
+        rc = self.fn(name)(*args)
+        if rc != 0:
+            raise RuntimeError(self.fn("last_error")().decode())
+
+    def rasterize_soft(self, soft_clip, face_id, faces_soft, hard_clip, faces_tex, w, h, radius,
+                       prev=None, vtx_faces=None):
+        sc, fi, fs = _f32(soft_clip), _f32(face_id), _f32(faces_soft)
+        hc, ft = _f32(hard_clip), _f32(faces_tex)
+        if vtx_faces is None:
+            vtx_faces = np.full((1, hc.shape[0]), -1, np.float32)
+        vf = _f32(vtx_faces)
+        out = np.zeros((h, w, 4), np.float32)
+        self._call("rasterize_soft", _fp(sc), _fp(fi), _fp(fs), _fp(hc), _U32(hc.shape[0]),
+                   _fp(ft), _fp(vf), _U32(vf.shape[0]), _U32(ft.shape[0]), _U32(w), _U32(h),
+                   C.c_float(radius), _fp(None if prev is None else _f32(prev)), _fp(out))
+        return out
+
+    def vertex_faces_tex(self, faces, n_verts):
+        faces = _f32(faces)
+        deg = _U32()
+        self._call("vertex_faces_tex", _fp(faces), _U32(faces.shape[0]), _U32(n_verts),
+                   C.byref(deg), None, _U32(0))
+        out = np.zeros((deg.value, n_verts), np.float32)
+        self._call("vertex_faces_tex", _fp(faces), _U32(faces.shape[0]), _U32(n_verts),
+                   C.byref(deg), _fp(out), _U32(out.size))
+        return out
+
+    def icosphere(self, level):
+        nv, nf = _U32(), _U32()
+        self._call("icosphere", _U32(level), C.byref(nv), C.byref(nf), None, None)
+        pos = np.zeros((nv.value, 3), np.float32)
+        faces = np.zeros((nf.value, 3), np.float32)
+        self._call("icosphere", _U32(level), C.byref(nv), C.byref(nf), _fp(pos), _fp(faces))
+        return pos, faces
+
+
+def have_reference() -> bool:
+    return os.path.exists(REF_SO)

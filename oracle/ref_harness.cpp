@@ -1,0 +1,534 @@
+// Reference-CPU harness: TEST INFRASTRUCTURE ONLY.
+//
+// This file is compiled together with the reference's own CPU sources
+// (src/core/*.cpp and examples/common/geometry_utils.cpp, read in place from
+// the reference checkout by oracle/Makefile) into oracle/_ref/libdressi_ref.so.
+// It drives the reference's graph API + CpuEvaluator, so its outputs are the
+// reference's own numbers. They are used to pin the C restatement in
+// oracle/dressi_oracle.c (golden fixtures under tests/golden/) and as the
+// "reference" CPU baseline. Nothing in the product path loads it.
+//
+// Every entry point is extern "C" with plain pointers so ctypes can call it.
+// Return value: 0 on success, -1 on error (message via refh_last_error()).
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "core/build_backward.h"
+#include "core/cpu_eval.h"
+#include "core/node.h"
+#include "dressi/dressi.h"
+#include "dressi/mesh_utils.h"
+
+#include "geometry_utils.h"
+
+using namespace dressi;
+
+namespace {
+
+thread_local std::string g_err;
+
+CpuTensor Tensor(VType vt, ImgSize sz, const float* data) {
+    CpuTensor t;
+    t.vtype = vt;
+    t.size = sz;
+    t.data.assign(data, data + size_t(sz.w) * sz.h * NumComponents(vt));
+    return t;
+}
+
+CpuTensor Fill(VType vt, ImgSize sz, float v) {
+    CpuTensor t;
+    t.vtype = vt;
+    t.size = sz;
+    t.data.assign(size_t(sz.w) * sz.h * NumComponents(vt), v);
+    return t;
+}
+
+void CopyOut(const CpuTensor& t, float* out) {
+    if (out) {
+        std::memcpy(out, t.data.data(), t.data.size() * sizeof(float));
+    }
+}
+
+VType VecOf(uint32_t n) { return VecVTypeOf(n); }
+
+template <typename Fn>
+int Guard(Fn&& fn) {
+    try {
+        fn();
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// Clip transform as an image-op chain (the silhouette example's
+// TransformToClipVar expression: one row per clip component, column-major
+// MVP), written with the same C++ expression shape so that node creation
+// order matches the example build.
+Variable ClipOf(const Variable& pos, const float* mvp) {
+    Variable x = F::GetX(pos);
+    Variable y = F::GetY(pos);
+    Variable z = F::GetZ(pos);
+    const auto row = [&](int r) {
+        return x * mvp[size_t(0 * 4 + r)] + y * mvp[size_t(1 * 4 + r)] +
+               z * mvp[size_t(2 * 4 + r)] + mvp[size_t(3 * 4 + r)];
+    };
+    return F::Vec4(row(0), row(1), row(2), row(3));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* refh_last_error() { return g_err.c_str(); }
+
+// F::SoftClip: clip {V,1} VEC4 + faces {F,1} VEC3 -> {3F,1} VEC4
+int refh_soft_clip(const float* clip, uint32_t n_verts, const float* faces,
+                   uint32_t n_faces, uint32_t w, uint32_t h, float radius,
+                   float* out) {
+    return Guard([&] {
+        Variable vc(VEC4, {n_verts, 1});
+        Variable vf(VEC3, {n_faces, 1});
+        Variable y = F::SoftClip(vc, vf, {w, h}, radius);
+        CpuEvaluator ev;
+        ev.bind(vc, Tensor(VEC4, {n_verts, 1}, clip));
+        ev.bind(vf, Tensor(VEC3, {n_faces, 1}, faces));
+        CopyOut(ev.eval(y), out);
+    });
+}
+
+// F::RasterizeSoft (and its peel overload when prev != nullptr)
+int refh_rasterize_soft(const float* soft_clip, const float* face_id,
+                        const float* faces_soft, const float* hard_clip,
+                        uint32_t n_verts, const float* faces_tex,
+                        const float* vtx_faces, uint32_t max_deg,
+                        uint32_t n_faces, uint32_t w, uint32_t h, float radius,
+                        const float* prev, float* out) {
+    return Guard([&] {
+        Variable sc(VEC4, {3 * n_faces, 1});
+        Variable fid(FLOAT, {3 * n_faces, 1});
+        Variable fs(IVEC3, {n_faces, 1});
+        Variable hc(VEC4, {n_verts, 1});
+        Variable ft(VEC3, {n_faces, 1});
+        Variable vf(FLOAT, {n_verts, max_deg});
+        Variable pv(FLOAT, {w, h});
+        Variable y = prev ? F::RasterizeSoft(sc, fid, fs, hc, ft, vf, pv,
+                                             {w, h}, radius)
+                          : F::RasterizeSoft(sc, fid, fs, hc, ft, vf, {w, h},
+                                             radius);
+        CpuEvaluator ev;
+        ev.bind(sc, Tensor(VEC4, {3 * n_faces, 1}, soft_clip));
+        ev.bind(fid, Tensor(FLOAT, {3 * n_faces, 1}, face_id));
+        ev.bind(fs, Tensor(IVEC3, {n_faces, 1}, faces_soft));
+        ev.bind(hc, Tensor(VEC4, {n_verts, 1}, hard_clip));
+        ev.bind(ft, Tensor(VEC3, {n_faces, 1}, faces_tex));
+        ev.bind(vf, Tensor(FLOAT, {n_verts, max_deg}, vtx_faces));
+        if (prev) {
+            ev.bind(pv, Tensor(FLOAT, {w, h}, prev));
+        }
+        CopyOut(ev.eval(y), out);
+    });
+}
+
+// F::Rasterize (hard, perspective-correct attribute interpolation)
+int refh_rasterize(const float* clip, uint32_t n_verts, const float* attr,
+                   uint32_t n_comp, const float* faces, uint32_t n_faces,
+                   uint32_t w, uint32_t h, float* out) {
+    return Guard([&] {
+        Variable vc(VEC4, {n_verts, 1});
+        Variable va(VecOf(n_comp), {n_verts, 1});
+        Variable vf(IVEC3, {n_faces, 1});
+        Variable y = F::Rasterize(vc, va, vf, {w, h});
+        CpuEvaluator ev;
+        ev.bind(vc, Tensor(VEC4, {n_verts, 1}, clip));
+        ev.bind(va, Tensor(VecOf(n_comp), {n_verts, 1}, attr));
+        ev.bind(vf, Tensor(IVEC3, {n_faces, 1}, faces));
+        CopyOut(ev.eval(y), out);
+    });
+}
+
+// F::RasterizeFaceId: float(f) + 1, 0 = background
+int refh_rasterize_face_id(const float* clip, uint32_t n_verts,
+                           const float* faces, uint32_t n_faces, uint32_t w,
+                           uint32_t h, float* out) {
+    return Guard([&] {
+        Variable vc(VEC4, {n_verts, 1});
+        Variable va(FLOAT, {n_verts, 1});
+        Variable vf(IVEC3, {n_faces, 1});
+        Variable y = F::RasterizeFaceId(vc, va, vf, {w, h});
+        CpuEvaluator ev;
+        ev.bind(vc, Tensor(VEC4, {n_verts, 1}, clip));
+        ev.bind(va, Fill(FLOAT, {n_verts, 1}, 1.f));
+        ev.bind(vf, Tensor(IVEC3, {n_faces, 1}, faces));
+        CopyOut(ev.eval(y), out);
+    });
+}
+
+// Backward of F::FaceFetch w.r.t. tri_attr (the stochastic / exact gather),
+// obtained from the op's own backward generator.
+int refh_face_fetch_bwd(const float* gy, uint32_t n_comp, const float* idx,
+                        uint32_t w, uint32_t h, const float* prj0,
+                        const float* prj1, const float* prj2,
+                        uint32_t n_faces, float seed, float radius,
+                        uint32_t n_samples, float* out) {
+    return Guard([&] {
+        Variable attr(VecOf(n_comp), {n_faces, 1});
+        Variable vidx(FLOAT, {w, h});
+        Variable p0(VEC4, {n_faces, 1});
+        Variable p1(VEC4, {n_faces, 1});
+        Variable p2(VEC4, {n_faces, 1});
+        Variable vs(FLOAT, {1, 1});
+        Variable vgy(VecOf(n_comp), {w, h});
+        Variable y = F::FaceFetch(attr, vidx, p0, p1, p2, vs, radius,
+                                  n_samples);
+        Variable g = y.getCreator().buildBwd(vgy, 0);
+        CpuEvaluator ev;
+        ev.bind(vidx, Tensor(FLOAT, {w, h}, idx));
+        ev.bind(p0, Tensor(VEC4, {n_faces, 1}, prj0));
+        ev.bind(p1, Tensor(VEC4, {n_faces, 1}, prj1));
+        ev.bind(p2, Tensor(VEC4, {n_faces, 1}, prj2));
+        ev.bind(vs, Fill(FLOAT, {1, 1}, seed));
+        ev.bind(vgy, Tensor(VecOf(n_comp), {w, h}, gy));
+        CopyOut(ev.eval(g), out);
+    });
+}
+
+// F::FaceFetch forward
+int refh_face_fetch(const float* attr, uint32_t n_comp, uint32_t n_faces,
+                    const float* idx, uint32_t w, uint32_t h, float* out) {
+    return Guard([&] {
+        Variable va(VecOf(n_comp), {n_faces, 1});
+        Variable vidx(FLOAT, {w, h});
+        Variable p(VEC4, {n_faces, 1});
+        Variable vs(FLOAT, {1, 1});
+        Variable y = F::FaceFetch(va, vidx, p, p, p, vs, 1.f, 4);
+        CpuEvaluator ev;
+        ev.bind(va, Tensor(VecOf(n_comp), {n_faces, 1}, attr));
+        ev.bind(vidx, Tensor(FLOAT, {w, h}, idx));
+        ev.bind(p, Fill(VEC4, {n_faces, 1}, 1.f));
+        ev.bind(vs, Fill(FLOAT, {1, 1}, 0.f));
+        CopyOut(ev.eval(y), out);
+    });
+}
+
+// Backward of F::LookupFaces w.r.t. vtx_attr (exact adjacency gather)
+int refh_lookup_faces_bwd(const float* gy, uint32_t n_comp,
+                          const float* faces, uint32_t n_faces,
+                          const float* vtx_faces, uint32_t n_verts,
+                          uint32_t max_deg, uint32_t corner, float* out) {
+    return Guard([&] {
+        Variable attr(VecOf(n_comp), {n_verts, 1});
+        Variable vf(VEC3, {n_faces, 1});
+        Variable vvf(FLOAT, {n_verts, max_deg});
+        Variable vgy(VecOf(n_comp), {n_faces, 1});
+        Variable y = F::LookupFaces(attr, vf, vvf, corner);
+        Variable g = y.getCreator().buildBwd(vgy, 0);
+        CpuEvaluator ev;
+        ev.bind(vf, Tensor(VEC3, {n_faces, 1}, faces));
+        ev.bind(vvf, Tensor(FLOAT, {n_verts, max_deg}, vtx_faces));
+        ev.bind(vgy, Tensor(VecOf(n_comp), {n_faces, 1}, gy));
+        CopyOut(ev.eval(g), out);
+    });
+}
+
+// VertexFacesTex: returns max degree in *deg_out; writes V*deg floats when
+// `out` is non-null and `cap` >= V*deg
+int refh_vertex_faces_tex(const float* faces, uint32_t n_faces,
+                          uint32_t n_verts, uint32_t* deg_out, float* out,
+                          uint32_t cap) {
+    return Guard([&] {
+        CpuImage fi(n_faces, 1, 3);
+        std::memcpy(fi.data.data(), faces, sizeof(float) * 3 * n_faces);
+        const CpuImage t = VertexFacesTex(fi, n_verts);
+        *deg_out = t.height;
+        if (out && cap >= t.data.size()) {
+            std::memcpy(out, t.data.data(), t.data.size() * sizeof(float));
+        }
+    });
+}
+
+// GenerateIcosphere (examples/common/geometry_utils.cpp): counts only when
+// pos/faces are null
+int refh_icosphere(uint32_t level, uint32_t* n_verts, uint32_t* n_faces,
+                   float* pos, float* faces) {
+    return Guard([&] {
+        const dressi_examples::Mesh m =
+                dressi_examples::GenerateIcosphere(level);
+        *n_verts = m.pos.width;
+        *n_faces = m.faces.width;
+        if (pos) {
+            std::memcpy(pos, m.pos.data.data(),
+                        m.pos.data.size() * sizeof(float));
+        }
+        if (faces) {
+            std::memcpy(faces, m.faces.data.data(),
+                        m.faces.data.size() * sizeof(float));
+        }
+    });
+}
+
+// GenerateUvSphere (examples/common/geometry_utils.cpp)
+int refh_uv_sphere(uint32_t stacks, uint32_t slices, uint32_t* n_verts,
+                   uint32_t* n_faces, float* pos, float* uv, float* faces) {
+    return Guard([&] {
+        const dressi_examples::Mesh m =
+                dressi_examples::GenerateUvSphere(stacks, slices);
+        *n_verts = m.pos.width;
+        *n_faces = m.faces.width;
+        if (pos) {
+            std::memcpy(pos, m.pos.data.data(),
+                        m.pos.data.size() * sizeof(float));
+        }
+        if (uv) {
+            std::memcpy(uv, m.uv.data.data(),
+                        m.uv.data.size() * sizeof(float));
+        }
+        if (faces) {
+            std::memcpy(faces, m.faces.data.data(),
+                        m.faces.data.size() * sizeof(float));
+        }
+    });
+}
+
+// The HardSoftRas silhouette fit of the reference example (technique
+// hardsoftras, peels = 1, no regularizers), run on the reference's
+// CpuEvaluator with DressiAD's end-of-frame copy-back semantics:
+// per iteration every root is evaluated from the pre-update leaves, then
+// pos/m/v/t are overwritten by their updated values.
+//
+//   pos0 {V,3}, faces {F,3} (float ids), tgt_pos {Vt,3}, tgt_faces {Ft,3},
+//   mvps N x 16 column-major. Outputs (all nullable):
+//   out_pos/m/v {V,3}, out_t {1}, out_loss {iters}: sum of the loss image,
+//   out_grad0 {V,3}: d loss / d pos at iteration 0, out_pred0 {N,S,S},
+//   out_target {N,S,S}, out_rs0 {N,S,S,4}: RasterizeSoft at iteration 0,
+//   out_lossimg0 {S,S}.
+int refh_hsr_fit(const float* pos0, uint32_t n_verts, const float* faces,
+                 uint32_t n_faces, const float* tgt_pos, uint32_t n_tverts,
+                 const float* tgt_faces, uint32_t n_tfaces, const float* mvps,
+                 uint32_t n_views, uint32_t screen_px, float radius_px,
+                 uint32_t samples, float lr, uint32_t iters, float* out_pos,
+                 float* out_m, float* out_v, float* out_t, float* out_loss,
+                 float* out_grad0, float* out_pred0, float* out_target,
+                 float* out_rs0, float* out_lossimg0) {
+    return Guard([&] {
+        const ImgSize screen = {screen_px, screen_px};
+        CpuImage s_faces_img(n_faces, 1, 3);
+        std::memcpy(s_faces_img.data.data(), faces,
+                    sizeof(float) * 3 * n_faces);
+        const CpuImage s_vf_img = VertexFacesTex(s_faces_img, n_verts);
+
+        Variable b_ones(FLOAT, {n_tverts, 1});
+        Variable b_faces_i(IVEC3, {n_tfaces, 1});
+        Variable s_faces_f(VEC3, {n_faces, 1});
+        Variable s_vtx_faces(FLOAT, s_vf_img.getImgSize());
+        Variable s_face_id(FLOAT, {n_faces * 3, 1});
+        Variable s_faces_soft(IVEC3, {n_faces, 1});
+        Variable pos(VEC3, {n_verts, 1});
+        Variable adam_m(VEC3, {n_verts, 1});
+        Variable adam_v(VEC3, {n_verts, 1});
+        Variable adam_t(FLOAT, {1, 1});
+
+        const float sigma_scale = 7.f / radius_px;
+        std::vector<Variable> rs_vars;
+        const auto build_pred = [&](const Variable& clip_v) -> Variable {
+            Variable soft_clip =
+                    F::SoftClip(clip_v, s_faces_f, screen, radius_px);
+            Variable tri0 = F::LookupFaces(clip_v, s_faces_f, s_vtx_faces, 0);
+            Variable tri1 = F::LookupFaces(clip_v, s_faces_f, s_vtx_faces, 1);
+            Variable tri2 = F::LookupFaces(clip_v, s_faces_f, s_vtx_faces, 2);
+            Variable pc = F::ScreenCoord(screen);
+            Variable zero = F::Float(0.f);
+            Variable one = F::Float(1.f);
+            const auto soft_prob = [&](const Variable& idx) {
+                Variable mask = F::Greater(idx, F::Float(0.5f));
+                const auto fetch = [&](const Variable& tri) {
+                    return F::FaceFetch(tri, idx, tri0, tri1, tri2, adam_t,
+                                        radius_px, samples);
+                };
+                const auto screen_of = [&](const Variable& c) {
+                    Variable w = F::GetW(c) + (1.f - mask);
+                    Variable sx = (F::GetX(c) / w * 0.5f + 0.5f) *
+                                  float(screen.w);
+                    Variable sy = (F::GetY(c) / w * 0.5f + 0.5f) *
+                                  float(screen.h);
+                    return F::Vec2(sx, sy);
+                };
+                Variable s0 = screen_of(fetch(tri0));
+                Variable s1 = screen_of(fetch(tri1));
+                Variable s2 = screen_of(fetch(tri2));
+                const auto edge_dist = [&](const Variable& a,
+                                           const Variable& b) {
+                    Variable e = b - a;
+                    Variable t = F::Clamp(F::Dot(pc - a, e) /
+                                                  (F::Dot(e, e) + 1e-12f),
+                                          zero, one);
+                    Variable dd = pc - (a + t * e);
+                    return F::Sqrt(F::Dot(dd, dd) + 1e-12f);
+                };
+                const auto edge_cross = [&](const Variable& a,
+                                            const Variable& b) {
+                    Variable e = b - a;
+                    return F::GetX(e) * (F::GetY(pc) - F::GetY(a)) -
+                           F::GetY(e) * (F::GetX(pc) - F::GetX(a));
+                };
+                Variable dmin = F::Min(F::Min(edge_dist(s0, s1),
+                                              edge_dist(s1, s2)),
+                                       edge_dist(s2, s0));
+                Variable cr0 = edge_cross(s0, s1);
+                Variable cr1 = edge_cross(s1, s2);
+                Variable cr2 = edge_cross(s2, s0);
+                Variable inside =
+                        F::Min(F::Step(zero, cr0) * F::Step(zero, cr1) *
+                                               F::Step(zero, cr2) +
+                                       F::Step(zero, -cr0) *
+                                               F::Step(zero, -cr1) *
+                                               F::Step(zero, -cr2),
+                               one);
+                Variable dist = (inside * 2.f - 1.f) * dmin;
+                return mask * F::Sigmoid(dist * sigma_scale);
+            };
+            Variable one_minus = one;
+            Variable rs = F::StopGradient(F::RasterizeSoft(
+                    soft_clip, s_face_id, s_faces_soft, clip_v, s_faces_f,
+                    s_vtx_faces, screen, radius_px));
+            rs_vars.push_back(rs);
+            Variable dist_c = F::GetX(rs);
+            Variable cov = F::GetW(rs);
+            Variable ge = F::Step(zero, dist_c);
+            Variable idx = (F::GetY(rs) + 1.f) * cov;
+            one_minus = one_minus * (1.f - soft_prob(idx));
+            Variable hard = cov * ge;
+            Variable soft_sil = 1.f - one_minus;
+            return F::Max(hard, soft_sil);
+        };
+
+        Variables targets, preds, view_losses;
+        std::vector<Variable> tgt_clips;
+        for (uint32_t v = 0; v < n_views; v++) {
+            tgt_clips.emplace_back(VEC4, ImgSize{n_tverts, 1});
+            targets.push_back(F::StopGradient(F::Rasterize(
+                    tgt_clips.back(), b_ones, b_faces_i, screen)));
+            preds.push_back(build_pred(ClipOf(pos, mvps + 16 * v)));
+            Variable diff = targets[v] - preds[v];
+            view_losses.push_back(diff * diff *
+                                  (1.f / float(screen.w * screen.h)));
+        }
+        Variable loss = F::SumPixelWise(view_losses);
+        Variable pos_mut = pos;
+        pos_mut.setRequiresGradRecursively();
+
+        auto [xs, gxs] = BuildBackward(loss);
+        DRESSI_CHECK(xs.size() == 1 && xs[0] == pos,
+                     "expected pos as the only requires-grad leaf");
+        const Variable g = gxs[0];
+        const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+        Variable t_new = adam_t + 1.f;
+        Variable m_new = adam_m * b1 + g * (1.f - b1);
+        Variable v_new = adam_v * b2 + g * g * (1.f - b2);
+        Variable bc1 = 1.f - F::Pow(F::Float(b1), t_new);
+        Variable bc2 = 1.f - F::Pow(F::Float(b2), t_new);
+        Variable step = (m_new / bc1) / (F::Sqrt(v_new / bc2) + eps) * lr;
+        Variable pos_new = pos - step;
+
+        // Static leaves
+        std::vector<float> ones(n_tverts, 1.f);
+        CpuTensor t_b_ones = Tensor(FLOAT, {n_tverts, 1}, ones.data());
+        CpuTensor t_b_faces = Tensor(IVEC3, {n_tfaces, 1}, tgt_faces);
+        CpuTensor t_s_faces = Tensor(VEC3, {n_faces, 1}, faces);
+        CpuTensor t_vf = Tensor(FLOAT, s_vf_img.getImgSize(),
+                                s_vf_img.data.data());
+        std::vector<float> fid_img(size_t(n_faces) * 3), fsoft(n_faces * 3);
+        for (uint32_t f = 0; f < n_faces; f++) {
+            for (uint32_t k = 0; k < 3; k++) {
+                fid_img[f * 3 + k] = float(f);
+                fsoft[f * 3 + k] = float(f * 3 + k);
+            }
+        }
+        CpuTensor t_fid = Tensor(FLOAT, {n_faces * 3, 1}, fid_img.data());
+        CpuTensor t_fsoft = Tensor(IVEC3, {n_faces, 1}, fsoft.data());
+        std::vector<CpuTensor> t_tgt_clips;
+        for (uint32_t v = 0; v < n_views; v++) {
+            const float* m = mvps + 16 * v;
+            CpuTensor c = Fill(VEC4, {n_tverts, 1}, 0.f);
+            for (uint32_t i = 0; i < n_tverts; i++) {
+                const float p[4] = {tgt_pos[i * 3 + 0], tgt_pos[i * 3 + 1],
+                                    tgt_pos[i * 3 + 2], 1.f};
+                for (int row = 0; row < 4; row++) {
+                    float acc = 0.f;
+                    for (int k = 0; k < 4; k++) {
+                        acc += m[k * 4 + row] * p[k];
+                    }
+                    c.data[size_t(i) * 4 + row] = acc;
+                }
+            }
+            t_tgt_clips.push_back(std::move(c));
+        }
+
+        CpuTensor t_pos = Tensor(VEC3, {n_verts, 1}, pos0);
+        CpuTensor t_m = Fill(VEC3, {n_verts, 1}, 0.f);
+        CpuTensor t_v = Fill(VEC3, {n_verts, 1}, 0.f);
+        CpuTensor t_t = Fill(FLOAT, {1, 1}, 0.f);
+        for (uint32_t it = 0; it < iters; it++) {
+            CpuEvaluator ev;
+            ev.bind(b_ones, t_b_ones);
+            ev.bind(b_faces_i, t_b_faces);
+            ev.bind(s_faces_f, t_s_faces);
+            ev.bind(s_vtx_faces, t_vf);
+            ev.bind(s_face_id, t_fid);
+            ev.bind(s_faces_soft, t_fsoft);
+            for (uint32_t v = 0; v < n_views; v++) {
+                ev.bind(tgt_clips[v], t_tgt_clips[v]);
+            }
+            ev.bind(pos, t_pos);
+            ev.bind(adam_m, t_m);
+            ev.bind(adam_v, t_v);
+            ev.bind(adam_t, t_t);
+
+            const CpuTensor li = ev.eval(loss);
+            if (out_loss) {
+                double s = 0.0;
+                for (float x : li.data) {
+                    s += x;
+                }
+                out_loss[it] = float(s);
+            }
+            if (it == 0) {
+                CopyOut(li, out_lossimg0);
+                if (out_grad0) {
+                    CopyOut(ev.eval(g), out_grad0);
+                }
+                const size_t px = size_t(screen.w) * screen.h;
+                for (uint32_t v = 0; v < n_views; v++) {
+                    if (out_pred0) {
+                        CopyOut(ev.eval(preds[v]), out_pred0 + v * px);
+                    }
+                    if (out_target) {
+                        CopyOut(ev.eval(targets[v]), out_target + v * px);
+                    }
+                    if (out_rs0) {
+                        CopyOut(ev.eval(rs_vars[v]), out_rs0 + v * px * 4);
+                    }
+                }
+            }
+            CpuTensor n_pos = ev.eval(pos_new);
+            CpuTensor n_m = ev.eval(m_new);
+            CpuTensor n_v = ev.eval(v_new);
+            CpuTensor n_t = ev.eval(t_new);
+            t_pos = std::move(n_pos);
+            t_m = std::move(n_m);
+            t_v = std::move(n_v);
+            t_t = std::move(n_t);
+        }
+        CopyOut(t_pos, out_pos);
+        CopyOut(t_m, out_m);
+        CopyOut(t_v, out_v);
+        CopyOut(t_t, out_t);
+    });
+}
+
+}  // extern "C"
