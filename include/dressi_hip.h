@@ -1,0 +1,253 @@
+/*
+ * dressi_hip.h -- C ABI of the MI355X-native Dressi-AD hot path.
+ *
+ * The library (opendressi_amd/libdressi_hip.so) replaces the reference's
+ * Vulkan executor seam for the HardSoftRas silhouette path: the GLSL op
+ * emitters + generated substages (src/codegen/glsl_codegen.cpp), the packer
+ * (src/pack/) and the Vulkan plan/submit/transfer layer
+ * (src/vk/executor.h:43-66, src/vk/transfer.h:16-91). Every entry point is
+ * plain C: status-code return, sizes explicit, device buffers as raw
+ * pointers, streams as opaque handles (hipStream_t). Nothing in a signature
+ * is a torch type. Each declaration names the reference interface it
+ * replaces (paths relative to the reference checkout).
+ *
+ * Layout conventions are the reference's logical ones: {N,1} arrays are
+ * tightly packed channels (VEC3 = 3 floats, VEC4 = 4 floats), face indices
+ * are floats (exact below 2^24), {V,deg} adjacency is row-major (d*V + v)
+ * with -1 padding, screen images are row-major, row 0 = NDC y = -1, pixel
+ * centres at +0.5, depth = z/w in [0,1].
+ *
+ * Errors: every call returns DRESSI_OK (0) or a negative dressi_status; the
+ * message of the last failure on the calling thread is dressi_last_error()
+ * (the reference throws DressiError "msg (file:line)", include/dressi/types.h:110-123).
+ * Threading: a context is not thread-safe; calls on one context are
+ * externally serialised (reference: src/vk/transfer.cpp:20-21).
+ */
+#ifndef DRESSI_HIP_H
+#define DRESSI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum dressi_status {
+    DRESSI_OK = 0,
+    DRESSI_ERR_INVALID = -1,     /* bad argument / shape (DRESSI_CHECK) */
+    DRESSI_ERR_HIP = -2,         /* HIP runtime failure ("GPU execution failed") */
+    DRESSI_ERR_NO_DEVICE = -3,   /* no usable HIP device */
+    DRESSI_ERR_UNSUPPORTED = -4  /* configuration outside what is built */
+} dressi_status;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* dressi_last_error(void);
+/* Library version string. */
+const char* dressi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Context, memory, transfers                                               */
+/* ------------------------------------------------------------------------ */
+typedef struct dressi_ctx dressi_ctx;
+
+/* Creates a context on `device` with its own default-priority stream.
+ * Replaces DressiAD::createContext / CreateVkContext
+ * (include/dressi/dressi_ad.h:336-338, src/vk/context.h:11-40). */
+int dressi_ctx_create(int device, dressi_ctx** out);
+int dressi_ctx_destroy(dressi_ctx* ctx);
+/* Use a caller-owned stream (e.g. the current torch stream) instead of the
+ * context's own; NULL restores the context stream. */
+int dressi_ctx_set_stream(dressi_ctx* ctx, void* stream);
+void* dressi_ctx_stream(dressi_ctx* ctx);
+/* Waits for all work queued on the context stream (the reference's fence
+ * wait, src/vk/executor.cpp:1020-1027). */
+int dressi_ctx_synchronize(dressi_ctx* ctx);
+/* Device name (DressiAD::getDeviceName, include/dressi/dressi_ad.h:380-382). */
+int dressi_ctx_device_name(dressi_ctx* ctx, char* buf, size_t len);
+
+int dressi_malloc(dressi_ctx* ctx, void** ptr, size_t bytes);
+int dressi_free(dressi_ctx* ctx, void* ptr);
+/* Stream-ordered copies; the *_sync variants wait for completion.
+ * Replace SendImageToDevice / ReceiveImageFromDevice (src/vk/transfer.h:16-91). */
+int dressi_memcpy_h2d(dressi_ctx* ctx, void* dst, const void* src, size_t bytes);
+int dressi_memcpy_d2h(dressi_ctx* ctx, void* dst, const void* src, size_t bytes);
+int dressi_memset(dressi_ctx* ctx, void* dst, int value, size_t bytes);
+
+/* ------------------------------------------------------------------------ */
+/* Per-op kernels (device pointers, stream-ordered on the context stream).  */
+/* Each reproduces one reference op's CPU semantics exactly.                */
+/* ------------------------------------------------------------------------ */
+
+/* F::SoftClip (src/core/f_ops.cpp:1890-1981; GLSL glsl_codegen.cpp:1440-1491):
+ * clip {V,1} VEC4, faces {F,1} float VEC3 -> out {3F,1} VEC4. */
+int dressi_soft_clip(dressi_ctx* ctx, const float* clip, uint32_t n_verts,
+                     const float* faces, uint32_t n_faces, uint32_t width,
+                     uint32_t height, float radius_px, float* out);
+
+/* F::RasterizeSoft and its peel overload (src/core/f_ops.cpp:1362-1465,
+ * CPU RasterizeSoftCpu src/core/cpu_raster.cpp:241-355; raster stage
+ * src/vk/executor.cpp:347-498): tile-binned, depth | face-id resolved
+ * per pixel with the reference's tie rule. out {S,S} VEC4 =
+ * (signed_dist_px, face_id, hard_z, coverage), background 0.
+ * soft_clip {3F,1} VEC4, face_id {3F,1}, faces_soft {F,1} float VEC3,
+ * hard_clip {V,1} VEC4, faces_tex {F,1} float VEC3; prev_shifted_depth
+ * {S,S} or NULL. */
+int dressi_rasterize_soft(dressi_ctx* ctx, const float* soft_clip,
+                          const float* face_id, const float* faces_soft,
+                          const float* hard_clip, uint32_t n_verts,
+                          const float* faces_tex, uint32_t n_faces,
+                          uint32_t width, uint32_t height, float radius_px,
+                          const float* prev_shifted_depth, float* out);
+
+/* F::Rasterize (src/core/f_ops.cpp:1182-1207, CPU RasterizeHardCpu
+ * src/core/cpu_raster.cpp:195-225): depth-tested, perspective-correct
+ * attribute interpolation; out {S,S} x n_comp, background 0. */
+int dressi_rasterize(dressi_ctx* ctx, const float* clip, uint32_t n_verts,
+                     const float* attr, uint32_t n_comp, const float* faces,
+                     uint32_t n_faces, uint32_t width, uint32_t height,
+                     float* out);
+
+/* F::RasterizeFaceId (src/core/f_ops.cpp:2183-2209, CPU
+ * RasterizeFaceIdCpu src/core/cpu_raster.cpp:357-369): float(f)+1, 0 bg. */
+int dressi_rasterize_face_id(dressi_ctx* ctx, const float* clip,
+                             uint32_t n_verts, const float* faces,
+                             uint32_t n_faces, uint32_t width,
+                             uint32_t height, float* out);
+
+/* F::LookupFaces forward / backward (src/core/f_ops.cpp:1521-1619):
+ * out{F} = attr[faces[f][corner]]; bwd: per vertex, rows d ascending of
+ * vtx_faces {V,max_deg} whose face has the vertex at `corner`. */
+int dressi_lookup_faces(dressi_ctx* ctx, const float* attr, uint32_t n_comp,
+                        uint32_t n_attr, const float* faces, uint32_t n_faces,
+                        uint32_t corner, float* out);
+int dressi_lookup_faces_bwd(dressi_ctx* ctx, const float* gy, uint32_t n_comp,
+                            const float* faces, uint32_t n_faces,
+                            const float* vtx_faces, uint32_t n_verts,
+                            uint32_t max_deg, uint32_t corner, float* out);
+
+/* F::FaceFetch forward / backward (src/core/f_ops.cpp:1631-1799; hash
+ * :1473-1487). bwd: n_samples > 0 the stochastic Wang-hash edge-sample
+ * gather seeded by `seed` (read from device memory, {1,1}), n_samples == 0
+ * the exact bbox+-1 scan. */
+int dressi_face_fetch(dressi_ctx* ctx, const float* attr, uint32_t n_comp,
+                      uint32_t n_faces, const float* idx, uint32_t width,
+                      uint32_t height, float* out);
+int dressi_face_fetch_bwd(dressi_ctx* ctx, const float* gy, uint32_t n_comp,
+                          const float* idx, uint32_t width, uint32_t height,
+                          const float* prj0, const float* prj1,
+                          const float* prj2, uint32_t n_faces,
+                          const float* seed, float radius_px,
+                          uint32_t n_samples, float* out);
+
+/* ------------------------------------------------------------------------ */
+/* Host-side mesh topology and scene builders                               */
+/* ------------------------------------------------------------------------ */
+/* GenerateIcosphere (examples/common/geometry_utils.cpp:24-84). Counts only
+ * when pos/faces are NULL. pos {V,3}, faces {F,3} float ids. */
+int dressi_icosphere(uint32_t level, uint32_t* n_verts, uint32_t* n_faces,
+                     float* pos, float* faces);
+/* VertexFacesTex (src/core/mesh_utils.cpp:53-71): returns max degree in
+ * *max_deg; writes max_deg*V floats when out != NULL and cap suffices. */
+int dressi_vertex_faces_tex(const float* faces, uint32_t n_faces,
+                            uint32_t n_verts, uint32_t* max_deg, float* out,
+                            size_t cap);
+/* LookAt / PerspectiveVk / Mul (examples/common/asset_utils.cpp:719-766),
+ * column-major. */
+void dressi_look_at(const float eye[3], const float center[3],
+                    const float up[3], float m[16]);
+void dressi_perspective_vk(float fovy_rad, float aspect, float z_near,
+                           float z_far, float m[16]);
+void dressi_mat4_mul(const float a[16], const float b[16], float r[16]);
+
+/* ------------------------------------------------------------------------ */
+/* Fused HardSoftRas silhouette iteration                                   */
+/* ------------------------------------------------------------------------ */
+/* One plan = the reference's GpuPlan for the silhouette example graph
+ * (examples/silhouette_optimization/run.cpp:229-437 with technique
+ * hardsoftras, peels = 1, no regularizers): per iteration
+ *   clip = MVP_v * pos (per view)            TransformToClipVar
+ *   SoftClip, RasterizeSoft (StopGradient)    a5, a6
+ *   D = mask * sigmoid(dist * 7 / r), pred = max(cov*step(0,dist), D)
+ *   loss = sum_v (target_v - pred_v)^2 / (W*H)  (image)
+ *   backward: FaceFetchBwd (n samples, seed = t) + LookupFacesBwd + clip->pos
+ *   Adam (b1 .9, b2 .999, eps 1e-8), state copy-back
+ * captured once into a hipGraph (zero per-iteration host work).
+ * Replaces BuildGpuPlan/ExecuteGpuPlan (src/vk/executor.h:43-66) as driven
+ * by DressiAD::execStep (src/dressi_ad.cpp:280-530). */
+typedef struct dressi_hsr_plan dressi_hsr_plan;
+
+typedef struct dressi_hsr_desc {
+    uint32_t n_verts;     /* V of the optimised mesh */
+    uint32_t n_faces;     /* F */
+    uint32_t n_views;     /* N (>= 1) */
+    uint32_t width;       /* screen S (width == height in the configs) */
+    uint32_t height;
+    float radius_px;      /* soft radius r (3) */
+    uint32_t n_samples;   /* FaceFetchBwd samples per face (8) */
+    float lr;             /* Adam learning rate */
+    float beta1, beta2, eps; /* 0.9, 0.999, 1e-8 */
+    uint32_t flags;       /* DRESSI_HSR_* */
+} dressi_hsr_desc;
+
+/* Also write per-view pred images each iteration (markOutput(pred)). */
+#define DRESSI_HSR_KEEP_PRED 1u
+/* Keep d loss / d pos of the last iteration readable (setGradOutputsEnabled,
+ * include/dressi/dressi_ad.h:362-370). */
+#define DRESSI_HSR_KEEP_GRAD 2u
+
+int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc,
+                      dressi_hsr_plan** out);
+int dressi_hsr_destroy(dressi_hsr_plan* plan);
+
+/* Static leaves from host memory (sendImg before the first execStep):
+ * faces {F,3} float ids, mvps N x 16 column-major. */
+int dressi_hsr_set_mesh(dressi_hsr_plan* plan, const float* faces,
+                        const float* mvps);
+/* Target silhouettes: either uploaded ({N,S,S}) or rasterised once on the
+ * GPU from a target mesh: StopGradient(Rasterize(MVP_v * tgt_pos, ones,
+ * tgt_faces)) (run.cpp:347-351). */
+int dressi_hsr_set_targets(dressi_hsr_plan* plan, const float* targets);
+int dressi_hsr_render_targets(dressi_hsr_plan* plan, const float* tgt_pos,
+                              uint32_t n_tverts, const float* tgt_faces,
+                              uint32_t n_tfaces);
+/* Optimiser state pos/m/v {V,3} and t from host (m, v may be NULL = 0). */
+int dressi_hsr_set_state(dressi_hsr_plan* plan, const float* pos,
+                         const float* m, const float* v, float t);
+int dressi_hsr_get_state(dressi_hsr_plan* plan, float* pos, float* m,
+                         float* v, float* t);
+
+/* Enqueue `n_iters` iterations on the context stream (graph launches; no
+ * host sync). DressiAD::execStep x n (src/dressi_ad.cpp:280-530). */
+int dressi_hsr_step(dressi_hsr_plan* plan, uint32_t n_iters);
+/* Same, without the hipGraph (eager launches) -- for tests / profiling. */
+int dressi_hsr_step_eager(dressi_hsr_plan* plan, uint32_t n_iters);
+
+/* Buffers readable after a step (recvImg): */
+enum dressi_hsr_buffer {
+    DRESSI_HSR_LOSS = 0,    /* {S,S} float: the loss image */
+    DRESSI_HSR_PRED = 1,    /* {N,S,S} float (needs DRESSI_HSR_KEEP_PRED) */
+    DRESSI_HSR_TARGET = 2,  /* {N,S,S} float */
+    DRESSI_HSR_FACE_ID = 3, /* {N,S,S} uint32: face + 1 of RasterizeSoft, 0 bg */
+    DRESSI_HSR_GRAD = 4,    /* {V,3} float (needs DRESSI_HSR_KEEP_GRAD) */
+    DRESSI_HSR_POS = 5,     /* {V,3} float */
+    DRESSI_HSR_CLIP = 6     /* {N,V,4} float: clip positions of the last step */
+};
+/* Device pointer of a plan buffer (zero-copy access) and its size. */
+int dressi_hsr_buffer(dressi_hsr_plan* plan, int which, void** ptr,
+                      size_t* bytes);
+/* Synchronous copy of a plan buffer to host memory. */
+int dressi_hsr_read(dressi_hsr_plan* plan, int which, void* host,
+                    size_t bytes);
+/* Launch-time profile of one eager iteration: fills up to `cap` kernel
+ * names / average microseconds (HIP events on the plan stream). Returns
+ * the kernel count in *n. */
+int dressi_hsr_profile(dressi_hsr_plan* plan, uint32_t iters, char* names,
+                       size_t name_stride, float* usec, uint32_t cap,
+                       uint32_t* n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DRESSI_HIP_H */

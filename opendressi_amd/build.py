@@ -1,0 +1,58 @@
+"""Build recipe of the HIP library (opendressi_amd/libdressi_hip.so) for gfx950.
+
+    python -m opendressi_amd.build
+
+hipcc cross-compiles without a GPU. Flags:
+  -ffp-contract=off                         no FMA contraction: coverage, face
+                                            ids and depth decisions must be
+                                            bit-identical to the reference's
+                                            (unfused) CPU arithmetic
+  -fhip-fp32-correctly-rounded-divide-sqrt  IEEE division / sqrt
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                                            no packed FP32 instructions
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+LIB = os.path.join(PKG, "libdressi_hip.so")
+SOURCES = ["runtime.hip", "raster.hip", "hsr.hip"]
+HEADERS = ["internal.h", "dressi_math.h", "raster_core.h", "soft_clip.h", "hsr_chain.h"]
+ARCH = os.environ.get("DRESSI_OFFLOAD_ARCH", "gfx950")
+
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-result", "-Wno-unused-value",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
+        if cand and (os.path.isabs(cand) and os.path.exists(cand) or not os.path.isabs(cand)):
+            return cand
+    return "hipcc"
+
+
+def build(verbose: bool = False) -> str:
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), *FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp, *srcs]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("hipcc failed building libdressi_hip.so")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

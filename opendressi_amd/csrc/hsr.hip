@@ -1,0 +1,1051 @@
+// hsr.hip -- the fused HardSoftRas silhouette iteration (forward + backward +
+// Adam as one hipGraph) and the per-op LookupFaces / FaceFetch kernels.
+#include <cstring>
+#include <vector>
+
+#include "hsr_chain.h"
+#include "raster_core.h"
+#include "soft_clip.h"
+
+namespace dressi {
+
+constexpr uint32_t kMaxViews = 8;
+
+// ---------------------------------------------------------------------------
+// Static reduction trees: SumContribs / SumPixelWise (src/core/build_backward.cpp:41-58,
+// src/core/f_ops.cpp:921-948) fold n inputs in levels of <= 4-ary sequential
+// sums; a lone trailing input passes through unchanged.
+// ---------------------------------------------------------------------------
+template <int N, int D>
+struct Tree {
+    static __device__ __forceinline__ void run(const float (&v)[N][D], float (&out)[D]) {
+        constexpr int M = (N + 3) / 4;
+        float nxt[M][D];
+#pragma unroll
+        for (int i = 0; i < M; i++) {
+            const int cnt = (N - 4 * i) < 4 ? (N - 4 * i) : 4;
+#pragma unroll
+            for (int c = 0; c < D; c++) {
+                if (cnt == 1) {
+                    nxt[i][c] = v[4 * i][c];
+                } else {
+                    float acc = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        if (j < cnt) {
+                            acc += v[4 * i + j][c];
+                        }
+                    }
+                    nxt[i][c] = acc;
+                }
+            }
+        }
+        Tree<M, D>::run(nxt, out);
+    }
+};
+template <int D>
+struct Tree<1, D> {
+    static __device__ __forceinline__ void run(const float (&v)[1][D], float (&out)[D]) {
+#pragma unroll
+        for (int c = 0; c < D; c++) {
+            out[c] = v[0][c];
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Kernels of one iteration
+// ---------------------------------------------------------------------------
+struct HsrDev {
+    RasterGeom g;
+    uint32_t n_verts, max_deg, n_samples, flags;
+    float radius, sigma_scale, inv_px, lr, b1, b2, eps;
+    float* pos;
+    float* m;
+    float* v;
+    float* t;
+    uint32_t* done;
+    const int32_t* faces;     // [F][3]
+    const int32_t* vf;        // [deg][V], -1 pad
+    const uint8_t* vf_mask;   // [deg][V], bit k: faces[vf][k] == v
+    const float* mvps;        // [N][16]
+    const float* targets;     // [N][S][S]
+    float4* clip;             // [N][V]
+    SoftRec* recs;            // [N][F]
+    BinBuffers bins;
+    uint32_t* ids;            // [N][S][S] face + 1
+    float* loss;              // [S][S]
+    float* pred;              // [N][S][S] or null
+    float4* gtri;             // [N][3][F]
+    float* grad;              // [V][3] or null
+};
+
+// clip_v = MVP_view * (pos, 1)  (TransformToClipVar)
+__global__ __launch_bounds__(256) void k_hsr_clip(HsrDev d) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t view = blockIdx.y;
+    if (i >= d.n_verts) {
+        return;
+    }
+    const float* m = d.mvps + view * 16;
+    d.clip[(size_t)view * d.n_verts + i] =
+            mvp_transform(m, d.pos[i * 3 + 0], d.pos[i * 3 + 1], d.pos[i * 3 + 2]);
+}
+
+// SoftClip + RasterizeSoft setup per (view, face), then the bin counts.
+__global__ __launch_bounds__(256) void k_hsr_setup(HsrDev d) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= d.g.n_views * d.g.n_faces) {
+        return;
+    }
+    const uint32_t view = i / d.g.n_faces;
+    const uint32_t f = i - view * d.g.n_faces;
+    float4 hc[3], sc[3];
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        hc[k] = d.clip[(size_t)view * d.n_verts + d.faces[f * 3 + k]];
+    }
+    soft_clip_face(hc, d.g.width, d.g.height, d.radius, sc);
+    SoftRec r;
+    soft_setup(sc, hc, (float)f, d.g.width, d.g.height, &r);
+    d.recs[i] = r;
+    if (r.bx0 > r.bx1 || r.by0 > r.by1) {
+        return;
+    }
+    uint32_t* cnt = d.bins.counts + (size_t)view * d.g.n_tiles;
+    for (int ty = r.by0 / kTile; ty <= r.by1 / kTile; ty++) {
+        for (int tx = r.bx0 / kTile; tx <= r.bx1 / kTile; tx++) {
+            atomicAdd(&cnt[ty * d.g.tiles_x + tx], 1u);
+        }
+    }
+}
+
+// One workgroup per 16x16 tile, all views: resolve the RasterizeSoft winner
+// of every view, write the face-id buffer, evaluate pred and the loss image
+// (SumPixelWise over views).
+template <int NV>
+__global__ __launch_bounds__(kTileThreads) void k_hsr_raster(HsrDev d) {
+    __shared__ SoftRec lds_rec[kTileThreads];
+    __shared__ uint32_t lds_face[kTileThreads];
+    const uint32_t tile = blockIdx.x;
+    const int px = (int)((tile % d.g.tiles_x) * kTile + (threadIdx.x % kTile));
+    const int py = (int)((tile / d.g.tiles_x) * kTile + (threadIdx.x / kTile));
+    const bool on = px < (int)d.g.width && py < (int)d.g.height;
+    const size_t npx = (size_t)d.g.width * d.g.height;
+    const size_t o = (size_t)py * d.g.width + px;
+    const float W = (float)d.g.width, H = (float)d.g.height;
+    float lv[NV][1];
+#pragma unroll
+    for (int view = 0; view < NV; view++) {
+        uint64_t best = kEmptyKey;
+        float bd = 0.f, bhz = 0.f;
+        walk_bin(d.recs + (size_t)view * d.g.n_faces, d.bins, view * d.g.n_tiles + tile,
+                 d.g.n_faces, lds_rec, lds_face, [&](const SoftRec& r, uint32_t f) {
+                     soft_fragment(r, f, px, py, d.radius, nullptr, d.g.width, &best, &bd, &bhz);
+                 });
+        float pred = 0.f;
+        uint32_t id = 0;
+        if (on && best != kEmptyKey) {
+            const uint32_t f = key_face(best);
+            id = f + 1;
+            float4 c[3];
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                c[k] = d.clip[(size_t)view * d.n_verts + d.faces[f * 3 + k]];
+            }
+            PixelFw st;
+            pixel_fw(c, 1.f, bd, 1.f, (float)px + 0.5f, (float)py + 0.5f, W, H, d.sigma_scale,
+                     st);
+            pred = st.pred;
+        }
+        float tgt = 0.f;
+        if (on) {
+            d.ids[view * npx + o] = id;
+            if (d.pred) {
+                d.pred[view * npx + o] = pred;
+            }
+            tgt = d.targets[view * npx + o];
+        }
+        const float diff = tgt - pred;
+        lv[view][0] = diff * diff * d.inv_px;
+    }
+    if (on) {
+        float out[1];
+        Tree<NV, 1>::run(lv, out);
+        d.loss[o] = out[0];
+    }
+}
+
+// FaceFetchBwd (stochastic, n samples, seed = t) fused with the pixel
+// chain's backward at each accepted sample: per (view, face) the three
+// corner-clip gradients (src/core/f_ops.cpp:1646-1729, 1700-1727).
+__global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= d.g.n_views * d.g.n_faces) {
+        return;
+    }
+    const uint32_t view = i / d.g.n_faces;
+    const uint32_t f = i - view * d.g.n_faces;
+    const float W = (float)d.g.width, H = (float)d.g.height;
+    float4 c[3];
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        c[k] = d.clip[(size_t)view * d.n_verts + d.faces[f * 3 + k]];
+    }
+    float4 acc[3];
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float4* dst = d.gtri + (size_t)view * 3 * d.g.n_faces;
+    bool ok = c[0].w > 1e-6f && c[1].w > 1e-6f && c[2].w > 1e-6f;
+    if (ok && d.n_samples > 0) {
+        float s[3][2];
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            s[k][0] = (c[k].x / c[k].w * 0.5f + 0.5f) * W;
+            s[k][1] = (c[k].y / c[k].w * 0.5f + 0.5f) * H;
+        }
+        // hard triangle of the rasterizer (for the dist channel's sign)
+        float hx[3], hy[3];
+        for (int k = 0; k < 3; k++) {
+            const ScreenVert v = project_to_screen(c[k].x, c[k].y, c[k].z, c[k].w, W, H);
+            hx[k] = v.x;
+            hy[k] = v.y;
+        }
+        HardTri ht;
+        hard_tri_init(&ht, hx, hy);
+        const uint32_t seed_u = (uint32_t)(int64_t)(*d.t + 0.5f);
+        const size_t npx = (size_t)d.g.width * d.g.height;
+        const uint32_t* ids = d.ids + view * npx;
+        const float* tgt = d.targets + view * npx;
+        for (uint32_t smp = 0; smp < d.n_samples; smp++) {
+            const int e = (int)(smp % 3);
+            const float* a = s[e];
+            const float* b = s[(e + 1) % 3];
+            const float ex = b[0] - a[0];
+            const float ey = b[1] - a[1];
+            const float len = sqrtf(ex * ex + ey * ey);
+            if (len < 1e-6f) {
+                continue;
+            }
+            const float u = hash_to_unit(f, smp, seed_u, 0);
+            const float off = (hash_to_unit(f, smp, seed_u, 1) * 2.f - 1.f) * d.radius;
+            const float spx = a[0] + u * ex - off * (ey / len);
+            const float spy = a[1] + u * ey + off * (ex / len);
+            const int ix = (int)floorf(spx);
+            const int iy = (int)floorf(spy);
+            if (ix < 0 || iy < 0 || ix >= (int)d.g.width || iy >= (int)d.g.height) {
+                continue;
+            }
+            const size_t p = (size_t)iy * d.g.width + ix;
+            if (ids[p] != f + 1) {
+                continue;
+            }
+            const float pcx = (float)ix + 0.5f, pcy = (float)iy + 0.5f;
+            const float dist_c = signed_dist(pcx, pcy, ht.ax, ht.ay, ht.ex, ht.ey, ht.len2);
+            PixelFw st;
+            pixel_fw(c, 1.f, dist_c, 1.f, pcx, pcy, W, H, d.sigma_scale, st);
+            float4 g[3];
+            pixel_bw(st, c, 1.f, tgt[p], d.inv_px, W, H, d.sigma_scale, g);
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                acc[k].x += g[k].x;
+                acc[k].y += g[k].y;
+                acc[k].z += g[k].z;
+                acc[k].w += g[k].w;
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        dst[(size_t)k * d.g.n_faces + f] = acc[k];
+    }
+}
+
+// LookupFacesBwd x3 + clip->pos chain over all views + Adam, one thread per
+// vertex. The last workgroup to finish advances t (all reads of t precede
+// every workgroup's arrival on the counter).
+template <int NV>
+__global__ __launch_bounds__(256) void k_hsr_vertex_adam(HsrDev d) {
+    const uint32_t vtx = blockIdx.x * blockDim.x + threadIdx.x;
+    const float t = *d.t;
+    if (vtx < d.n_verts) {
+        // contributions to pos, newest first: GetZ, GetY, GetX of view N-1 .. 0
+        float contrib[3 * NV][3];
+#pragma unroll
+        for (int vi = 0; vi < NV; vi++) {
+            const int view = NV - 1 - vi;
+            const float4* gt = d.gtri + (size_t)view * 3 * d.g.n_faces;
+            float lfb[3][4];
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                lfb[k][0] = lfb[k][1] = lfb[k][2] = lfb[k][3] = 0.f;
+            }
+            for (uint32_t dd = 0; dd < d.max_deg; dd++) {
+                const int32_t f = d.vf[(size_t)dd * d.n_verts + vtx];
+                if (f < 0) {
+                    continue;
+                }
+                const uint32_t mask = d.vf_mask[(size_t)dd * d.n_verts + vtx];
+#pragma unroll
+                for (int k = 0; k < 3; k++) {
+                    if (mask & (1u << k)) {
+                        const float4 gg = gt[(size_t)k * d.g.n_faces + f];
+                        lfb[k][0] += gg.x;
+                        lfb[k][1] += gg.y;
+                        lfb[k][2] += gg.z;
+                        lfb[k][3] += gg.w;
+                    }
+                }
+            }
+            // clip_v gradient: LookupFaces 2, 1, 0 (newest first), one 3-ary sum
+            float gc[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float acc = 0.f;
+                acc += lfb[2][r];
+                acc += lfb[1][r];
+                acc += lfb[0][r];
+                gc[r] = acc;
+            }
+            const float* m = d.mvps + view * 16;
+            float gxyz[3];
+#pragma unroll
+            for (int comp = 0; comp < 3; comp++) {
+                float acc = 0.f;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    acc += gc[r] * m[comp * 4 + r];
+                }
+                gxyz[comp] = acc;
+            }
+#pragma unroll
+            for (int q = 0; q < 3; q++) {
+                const int comp = 2 - q;
+                contrib[vi * 3 + q][0] = 0.f;
+                contrib[vi * 3 + q][1] = 0.f;
+                contrib[vi * 3 + q][2] = 0.f;
+                contrib[vi * 3 + q][comp] = gxyz[comp];
+            }
+        }
+        float g[3];
+        Tree<3 * NV, 3>::run(contrib, g);
+        if (d.grad) {
+#pragma unroll
+            for (int c = 0; c < 3; c++) {
+                d.grad[vtx * 3 + c] = g[c];
+            }
+        }
+        // in-graph Adam (examples/silhouette_optimization/run.cpp:421-436)
+        const float t_new = t + 1.f;
+        const float bc1 = 1.f - powf(d.b1, t_new);
+        const float bc2 = 1.f - powf(d.b2, t_new);
+        const float cb1 = 1.f - d.b1, cb2 = 1.f - d.b2;
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+            const size_t j = (size_t)vtx * 3 + c;
+            const float m_new = d.m[j] * d.b1 + g[c] * cb1;
+            const float v_new = d.v[j] * d.b2 + g[c] * g[c] * cb2;
+            const float step = (m_new / bc1) / (sqrtf(v_new / bc2) + d.eps) * d.lr;
+            d.pos[j] = d.pos[j] - step;
+            d.m[j] = m_new;
+            d.v[j] = v_new;
+        }
+    }
+    __shared__ bool last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        last = atomicAdd(d.done, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (last && threadIdx.x == 0) {
+        *d.t = t + 1.f;
+        *d.done = 0;
+    }
+}
+
+// Per-op kernels ------------------------------------------------------------
+
+__global__ void k_lookup_faces(const float* attr, uint32_t n_comp, const float* faces,
+                               uint32_t n_faces, uint32_t n_attr, uint32_t corner, uint32_t* err,
+                               float* out) {
+    const uint32_t f = blockIdx.x * blockDim.x + threadIdx.x;
+    if (f >= n_faces) {
+        return;
+    }
+    const uint32_t vi = fid_u(faces[(size_t)f * 3 + corner]);
+    if (vi >= n_attr) {
+        atomicOr(err, 32u);
+        return;
+    }
+    for (uint32_t c = 0; c < n_comp; c++) {
+        out[(size_t)f * n_comp + c] = attr[(size_t)vi * n_comp + c];
+    }
+}
+
+__global__ void k_lookup_faces_bwd(const float* gy, uint32_t n_comp, const float* faces,
+                                   uint32_t n_faces, const float* vtx_faces, uint32_t n_verts,
+                                   uint32_t max_deg, uint32_t corner, uint32_t* err,
+                                   float* out) {
+    const uint32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= n_verts) {
+        return;
+    }
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t dd = 0; dd < max_deg; dd++) {
+        const float fv = vtx_faces[(size_t)dd * n_verts + v];
+        if (fv < -0.5f) {
+            continue;
+        }
+        const uint32_t f = fid_u(fv);
+        if (f >= n_faces) {
+            atomicOr(err, 64u);
+            continue;
+        }
+        if (fid_u(faces[(size_t)f * 3 + corner]) != v) {
+            continue;
+        }
+        for (uint32_t c = 0; c < n_comp; c++) {
+            acc[c] += gy[(size_t)f * n_comp + c];
+        }
+    }
+    for (uint32_t c = 0; c < n_comp; c++) {
+        out[(size_t)v * n_comp + c] = acc[c];
+    }
+}
+
+__global__ void k_face_fetch(const float* attr, uint32_t n_comp, uint32_t n_faces,
+                             const float* idx, size_t npx, float* out) {
+    const size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= npx) {
+        return;
+    }
+    const int f = (int)(idx[p] + 0.5f) - 1;
+    const bool ok = f >= 0 && (uint32_t)f < n_faces;
+    for (uint32_t c = 0; c < n_comp; c++) {
+        out[p * n_comp + c] = ok ? attr[(size_t)f * n_comp + c] : 0.f;
+    }
+}
+
+__global__ void k_face_fetch_bwd(const float* gy, uint32_t n_comp, const float* idx, uint32_t w,
+                                 uint32_t h, const float4* prj0, const float4* prj1,
+                                 const float4* prj2, uint32_t n_faces, const float* seed,
+                                 float radius, uint32_t n_samples, float* out) {
+    const uint32_t f = blockIdx.x * blockDim.x + threadIdx.x;
+    if (f >= n_faces) {
+        return;
+    }
+    const float4 c[3] = {prj0[f], prj1[f], prj2[f]};
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    bool ok = c[0].w > 1e-6f && c[1].w > 1e-6f && c[2].w > 1e-6f;
+    if (ok) {
+        float s[3][2];
+        for (int k = 0; k < 3; k++) {
+            s[k][0] = (c[k].x / c[k].w * 0.5f + 0.5f) * (float)w;
+            s[k][1] = (c[k].y / c[k].w * 0.5f + 0.5f) * (float)h;
+        }
+        if (n_samples == 0) {
+            int x0 = (int)floorf(smin(smin(s[0][0], s[1][0]), s[2][0]) - 1.f);
+            int x1 = (int)ceilf(smax(smax(s[0][0], s[1][0]), s[2][0]) + 1.f);
+            int y0 = (int)floorf(smin(smin(s[0][1], s[1][1]), s[2][1]) - 1.f);
+            int y1 = (int)ceilf(smax(smax(s[0][1], s[1][1]), s[2][1]) + 1.f);
+            x0 = x0 > 0 ? x0 : 0;
+            y0 = y0 > 0 ? y0 : 0;
+            x1 = x1 < (int)w - 1 ? x1 : (int)w - 1;
+            y1 = y1 < (int)h - 1 ? y1 : (int)h - 1;
+            for (int iy = y0; iy <= y1; iy++) {
+                for (int ix = x0; ix <= x1; ix++) {
+                    const size_t p = (size_t)iy * w + ix;
+                    if (fid_u(idx[p]) != f + 1) {
+                        continue;
+                    }
+                    for (uint32_t q = 0; q < n_comp; q++) {
+                        acc[q] += gy[p * n_comp + q];
+                    }
+                }
+            }
+        } else {
+            const uint32_t seed_u = (uint32_t)(int64_t)(*seed + 0.5f);
+            for (uint32_t smp = 0; smp < n_samples; smp++) {
+                const int e = (int)(smp % 3);
+                const float* a = s[e];
+                const float* b = s[(e + 1) % 3];
+                const float ex = b[0] - a[0];
+                const float ey = b[1] - a[1];
+                const float len = sqrtf(ex * ex + ey * ey);
+                if (len < 1e-6f) {
+                    continue;
+                }
+                const float u = hash_to_unit(f, smp, seed_u, 0);
+                const float off = (hash_to_unit(f, smp, seed_u, 1) * 2.f - 1.f) * radius;
+                const float spx = a[0] + u * ex - off * (ey / len);
+                const float spy = a[1] + u * ey + off * (ex / len);
+                const int ix = (int)floorf(spx);
+                const int iy = (int)floorf(spy);
+                if (ix < 0 || iy < 0 || ix >= (int)w || iy >= (int)h) {
+                    continue;
+                }
+                const size_t p = (size_t)iy * w + ix;
+                if (fid_u(idx[p]) != f + 1) {
+                    continue;
+                }
+                for (uint32_t q = 0; q < n_comp; q++) {
+                    acc[q] += gy[p * n_comp + q];
+                }
+            }
+        }
+    }
+    for (uint32_t q = 0; q < n_comp; q++) {
+        out[(size_t)f * n_comp + q] = acc[q];
+    }
+}
+
+}  // namespace dressi
+
+// ---------------------------------------------------------------------------
+// The plan
+// ---------------------------------------------------------------------------
+using namespace dressi;
+
+struct dressi_hsr_plan {
+    dressi_ctx* ctx = nullptr;
+    dressi_hsr_desc desc{};
+    HsrDev d{};
+    std::vector<void*> allocs;
+    void* bin_mem = nullptr;
+    bool mesh_set = false, targets_set = false, state_set = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    hipStream_t graph_stream = nullptr;  // stream the exec was instantiated for
+};
+
+namespace {
+
+template <typename T>
+int plan_alloc(dressi_hsr_plan* p, T** out, size_t count) {
+    void* ptr = nullptr;
+    DRESSI_TRY_HIP(hipMalloc(&ptr, sizeof(T) * (count ? count : 1)));
+    p->allocs.push_back(ptr);
+    *out = (T*)ptr;
+    return DRESSI_OK;
+}
+
+int enqueue_iteration(dressi_hsr_plan* p, hipStream_t s) {
+    const HsrDev& d = p->d;
+    const RasterGeom& g = d.g;
+    hipLaunchKernelGGL(k_hsr_clip, dim3(div_up(d.n_verts, 256), g.n_views), dim3(256), 0, s, d);
+    DRESSI_CHECK_LAUNCH();
+    const uint32_t nvf = g.n_views * g.n_faces;
+    hipLaunchKernelGGL(k_hsr_setup, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
+    DRESSI_CHECK_LAUNCH();
+    if (int rc = launch_scan_bins(s, d.bins)) return rc;
+    if (int rc = launch_bin_soft(s, g, d.recs, d.bins)) return rc;
+    switch (g.n_views) {
+#define DRESSI_NV(N)                                                                          \
+    case N:                                                                                   \
+        hipLaunchKernelGGL(k_hsr_raster<N>, dim3(g.n_tiles), dim3(kTileThreads), 0, s, d);    \
+        break;
+        DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
+        DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)
+#undef DRESSI_NV
+        default:
+            set_error("n_views %u unsupported", g.n_views);
+            return DRESSI_ERR_UNSUPPORTED;
+    }
+    DRESSI_CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_hsr_face_bwd, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
+    DRESSI_CHECK_LAUNCH();
+    const dim3 vg(div_up(d.n_verts, 256));
+    switch (g.n_views) {
+#define DRESSI_NV(N)                                                                  \
+    case N:                                                                           \
+        hipLaunchKernelGGL(k_hsr_vertex_adam<N>, vg, dim3(256), 0, s, d);             \
+        break;
+        DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
+        DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)
+#undef DRESSI_NV
+    }
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+int ready(dressi_hsr_plan* p) {
+    DRESSI_REQUIRE(p, "NULL plan");
+    DRESSI_REQUIRE(p->mesh_set, "dressi_hsr_set_mesh() must be called before stepping");
+    DRESSI_REQUIRE(p->targets_set, "targets must be set (set_targets / render_targets)");
+    DRESSI_REQUIRE(p->state_set, "dressi_hsr_set_state() must be called before stepping");
+    DRESSI_TRY_HIP(hipSetDevice(p->ctx->device));
+    return DRESSI_OK;
+}
+
+void drop_graph(dressi_hsr_plan* p) {
+    if (p->exec) {
+        hipGraphExecDestroy(p->exec);
+        p->exec = nullptr;
+    }
+    if (p->graph) {
+        hipGraphDestroy(p->graph);
+        p->graph = nullptr;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_plan** out) {
+    DRESSI_REQUIRE(ctx && desc && out, "bad arguments");
+    DRESSI_REQUIRE(desc->n_verts > 0 && desc->n_faces > 0, "empty mesh");
+    DRESSI_REQUIRE(desc->n_views >= 1 && desc->n_views <= kMaxViews,
+                   "n_views must be in [1, %u]", kMaxViews);
+    DRESSI_REQUIRE(desc->width > 0 && desc->height > 0, "empty screen");
+    DRESSI_REQUIRE(desc->radius_px > 0.f, "radius_px must be > 0");
+    DRESSI_REQUIRE((uint64_t)desc->n_views * desc->n_faces < (1ull << 31), "too many faces");
+    DRESSI_TRY_HIP(hipSetDevice(ctx->device));
+    dressi_hsr_plan* p = new dressi_hsr_plan();
+    p->ctx = ctx;
+    p->desc = *desc;
+    HsrDev& d = p->d;
+    d.g = make_geom(desc->width, desc->height, desc->n_views, desc->n_faces);
+    d.n_verts = desc->n_verts;
+    d.n_samples = desc->n_samples;
+    d.flags = desc->flags;
+    d.radius = desc->radius_px;
+    d.sigma_scale = 7.f / desc->radius_px;
+    d.inv_px = 1.f / (float)(desc->width * desc->height);
+    d.lr = desc->lr;
+    d.b1 = desc->beta1;
+    d.b2 = desc->beta2;
+    d.eps = desc->eps;
+    const size_t V = desc->n_verts, F = desc->n_faces, N = desc->n_views;
+    const size_t npx = (size_t)desc->width * desc->height;
+    int rc = DRESSI_OK;
+    float4* gtri = nullptr;
+    rc = rc ? rc : plan_alloc(p, &d.pos, V * 3);
+    rc = rc ? rc : plan_alloc(p, &d.m, V * 3);
+    rc = rc ? rc : plan_alloc(p, &d.v, V * 3);
+    rc = rc ? rc : plan_alloc(p, &d.t, 1);
+    rc = rc ? rc : plan_alloc(p, &d.done, 1);
+    rc = rc ? rc : plan_alloc(p, (float**)&d.mvps, N * 16);
+    rc = rc ? rc : plan_alloc(p, (float**)&d.targets, N * npx);
+    rc = rc ? rc : plan_alloc(p, &d.clip, N * V);
+    rc = rc ? rc : plan_alloc(p, &d.recs, N * F);
+    rc = rc ? rc : plan_alloc(p, &d.ids, N * npx);
+    rc = rc ? rc : plan_alloc(p, &d.loss, npx);
+    rc = rc ? rc : plan_alloc(p, &gtri, N * 3 * F);
+    if (!rc && (desc->flags & DRESSI_HSR_KEEP_PRED)) rc = plan_alloc(p, &d.pred, N * npx);
+    if (!rc && (desc->flags & DRESSI_HSR_KEEP_GRAD)) rc = plan_alloc(p, &d.grad, V * 3);
+    d.gtri = gtri;
+    if (!rc) {
+        const uint32_t cap = default_bin_cap(d.g, 16);
+        uint32_t* bm = nullptr;
+        const size_t bytes = bin_bytes(d.g.n_tiles * d.g.n_views, cap);
+        rc = plan_alloc(p, &bm, bytes / sizeof(uint32_t) + 1);
+        if (!rc) {
+            bin_carve(bm, d.g.n_tiles * d.g.n_views, cap, &d.bins);
+        }
+    }
+    if (!rc) {
+        hipError_t e = hipMemsetAsync(d.bins.counts, 0, sizeof(uint32_t) * d.bins.n_bins, ctx->stream);
+        if (e == hipSuccess) e = hipMemsetAsync(d.done, 0, sizeof(uint32_t), ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            set_error("plan init failed: %s", hipGetErrorString(e));
+            rc = DRESSI_ERR_HIP;
+        }
+    }
+    if (rc) {
+        dressi_hsr_destroy(p);
+        return rc;
+    }
+    *out = p;
+    return DRESSI_OK;
+}
+
+int dressi_hsr_destroy(dressi_hsr_plan* p) {
+    if (!p) {
+        return DRESSI_OK;
+    }
+    hipSetDevice(p->ctx->device);
+    hipStreamSynchronize(p->ctx->stream);
+    drop_graph(p);
+    for (void* a : p->allocs) {
+        hipFree(a);
+    }
+    delete p;
+    return DRESSI_OK;
+}
+
+int dressi_hsr_set_mesh(dressi_hsr_plan* p, const float* faces, const float* mvps) {
+    DRESSI_REQUIRE(p && faces && mvps, "bad arguments");
+    DRESSI_TRY_HIP(hipSetDevice(p->ctx->device));
+    const uint32_t V = p->desc.n_verts, F = p->desc.n_faces;
+    std::vector<int32_t> fi((size_t)F * 3);
+    for (size_t i = 0; i < fi.size(); i++) {
+        const float x = faces[i];
+        DRESSI_REQUIRE(x >= 0.f && x < (float)V, "face index out of range at %zu", i);
+        fi[i] = (int32_t)(uint32_t)(int64_t)(x + 0.5f);
+    }
+    // vertex -> incident faces (src/core/mesh_utils.cpp:53-71) plus a per-slot
+    // corner mask: bit k set when faces[f][k] == v (LookupFacesBwd's test)
+    std::vector<std::vector<uint32_t>> vf(V);
+    for (uint32_t f = 0; f < F; f++) {
+        for (int k = 0; k < 3; k++) {
+            vf[fi[f * 3 + k]].push_back(f);
+        }
+    }
+    uint32_t deg = 1;
+    for (const auto& l : vf) {
+        deg = l.size() > deg ? (uint32_t)l.size() : deg;
+    }
+    std::vector<int32_t> vft((size_t)deg * V, -1);
+    std::vector<uint8_t> vfm((size_t)deg * V, 0);
+    for (uint32_t v = 0; v < V; v++) {
+        for (size_t dd = 0; dd < vf[v].size(); dd++) {
+            const uint32_t f = vf[v][dd];
+            vft[dd * V + v] = (int32_t)f;
+            uint8_t m = 0;
+            for (int k = 0; k < 3; k++) {
+                m |= (uint32_t)fi[f * 3 + k] == v ? (uint8_t)(1u << k) : 0;
+            }
+            vfm[dd * V + v] = m;
+        }
+    }
+    hipStream_t s = p->ctx->stream;
+    int32_t* dfaces = nullptr;
+    int32_t* dvf = nullptr;
+    uint8_t* dvfm = nullptr;
+    if (!p->mesh_set) {
+        if (int rc = plan_alloc(p, &dfaces, fi.size())) return rc;
+        if (int rc = plan_alloc(p, &dvf, vft.size())) return rc;
+        if (int rc = plan_alloc(p, &dvfm, vfm.size())) return rc;
+        p->d.faces = dfaces;
+        p->d.vf = dvf;
+        p->d.vf_mask = dvfm;
+        p->d.max_deg = deg;
+    } else {
+        DRESSI_REQUIRE(deg == p->d.max_deg, "topology change needs a new plan");
+    }
+    DRESSI_TRY_HIP(hipMemcpyAsync((void*)p->d.faces, fi.data(), fi.size() * 4, hipMemcpyHostToDevice, s));
+    DRESSI_TRY_HIP(hipMemcpyAsync((void*)p->d.vf, vft.data(), vft.size() * 4, hipMemcpyHostToDevice, s));
+    DRESSI_TRY_HIP(hipMemcpyAsync((void*)p->d.vf_mask, vfm.data(), vfm.size(), hipMemcpyHostToDevice, s));
+    DRESSI_TRY_HIP(hipMemcpyAsync((void*)p->d.mvps, mvps, sizeof(float) * 16 * p->desc.n_views,
+                                  hipMemcpyHostToDevice, s));
+    DRESSI_TRY_HIP(hipStreamSynchronize(s));
+    p->mesh_set = true;
+    drop_graph(p);
+    return DRESSI_OK;
+}
+
+int dressi_hsr_set_targets(dressi_hsr_plan* p, const float* targets) {
+    DRESSI_REQUIRE(p && targets, "bad arguments");
+    DRESSI_TRY_HIP(hipSetDevice(p->ctx->device));
+    const size_t n = (size_t)p->desc.n_views * p->desc.width * p->desc.height;
+    DRESSI_TRY_HIP(hipMemcpyAsync((void*)p->d.targets, targets, n * 4, hipMemcpyHostToDevice,
+                                  p->ctx->stream));
+    DRESSI_TRY_HIP(hipStreamSynchronize(p->ctx->stream));
+    p->targets_set = true;
+    return DRESSI_OK;
+}
+
+int dressi_hsr_render_targets(dressi_hsr_plan* p, const float* tgt_pos, uint32_t n_tverts,
+                              const float* tgt_faces, uint32_t n_tfaces) {
+    DRESSI_REQUIRE(p && tgt_pos && tgt_faces && n_tverts > 0 && n_tfaces > 0, "bad arguments");
+    DRESSI_REQUIRE(p->mesh_set, "dressi_hsr_set_mesh() first (the MVPs)");
+    DRESSI_TRY_HIP(hipSetDevice(p->ctx->device));
+    const uint32_t N = p->desc.n_views;
+    std::vector<int32_t> fi((size_t)n_tfaces * 3);
+    for (size_t i = 0; i < fi.size(); i++) {
+        DRESSI_REQUIRE(tgt_faces[i] >= 0.f && tgt_faces[i] < (float)n_tverts,
+                       "target face index out of range at %zu", i);
+        fi[i] = (int32_t)(uint32_t)(int64_t)tgt_faces[i];
+    }
+    // target clips on the host: TransformToClip (asset_utils.cpp:768-782)
+    std::vector<float> mv((size_t)N * 16);
+    DRESSI_TRY_HIP(hipMemcpy(mv.data(), p->d.mvps, mv.size() * 4, hipMemcpyDeviceToHost));
+    std::vector<float> clip((size_t)N * n_tverts * 4);
+    for (uint32_t v = 0; v < N; v++) {
+        for (uint32_t i = 0; i < n_tverts; i++) {
+            const float4 c = mvp_transform(&mv[v * 16], tgt_pos[i * 3], tgt_pos[i * 3 + 1],
+                                           tgt_pos[i * 3 + 2]);
+            float* o = &clip[((size_t)v * n_tverts + i) * 4];
+            o[0] = c.x;
+            o[1] = c.y;
+            o[2] = c.z;
+            o[3] = c.w;
+        }
+    }
+    const RasterGeom g = make_geom(p->desc.width, p->desc.height, N, n_tfaces);
+    const uint32_t cap = default_bin_cap(g, 8);
+    dressi_ctx* ctx = p->ctx;
+    void *dclip = nullptr, *dfi = nullptr, *recs = nullptr, *bins = nullptr, *ones = nullptr;
+    if (int rc = ctx_workspace(ctx, 0, sizeof(HardRec) * (size_t)N * n_tfaces, &recs)) return rc;
+    if (int rc = ctx_workspace(ctx, 1, bin_bytes(g.n_tiles * N, cap), &bins)) return rc;
+    if (int rc = ctx_workspace(ctx, 2, fi.size() * 4, &dfi)) return rc;
+    if (int rc = ctx_workspace(ctx, 3, clip.size() * 4, &dclip)) return rc;
+    if (int rc = ctx_workspace(ctx, 4, (size_t)n_tverts * 4, &ones)) return rc;
+    std::vector<float> one(n_tverts, 1.f);
+    hipStream_t s = ctx->stream;
+    DRESSI_TRY_HIP(hipMemcpyAsync(dfi, fi.data(), fi.size() * 4, hipMemcpyHostToDevice, s));
+    DRESSI_TRY_HIP(hipMemcpyAsync(dclip, clip.data(), clip.size() * 4, hipMemcpyHostToDevice, s));
+    DRESSI_TRY_HIP(hipMemcpyAsync(ones, one.data(), one.size() * 4, hipMemcpyHostToDevice, s));
+    BinBuffers b;
+    bin_carve(bins, g.n_tiles * N, cap, &b);
+    DRESSI_TRY_HIP(hipMemsetAsync(b.counts, 0, sizeof(uint32_t) * b.n_bins, s));
+    if (int rc = launch_hard_setup(s, g, (const float*)dclip, n_tverts, (const int32_t*)dfi,
+                                   (HardRec*)recs)) return rc;
+    if (int rc = launch_count_hard(s, g, (const HardRec*)recs, b)) return rc;
+    if (int rc = launch_scan_bins(s, b)) return rc;
+    if (int rc = launch_bin_hard(s, g, (const HardRec*)recs, b)) return rc;
+    if (int rc = launch_raster_hard(s, g, (const HardRec*)recs, b, (const float*)ones, 1, 0,
+                                    (float*)p->d.targets)) return rc;
+    DRESSI_TRY_HIP(hipStreamSynchronize(s));
+    p->targets_set = true;
+    return DRESSI_OK;
+}
+
+int dressi_hsr_set_state(dressi_hsr_plan* p, const float* pos, const float* m, const float* v,
+                         float t) {
+    DRESSI_REQUIRE(p && pos, "bad arguments");
+    DRESSI_TRY_HIP(hipSetDevice(p->ctx->device));
+    hipStream_t s = p->ctx->stream;
+    const size_t n = (size_t)p->desc.n_verts * 3 * 4;
+    DRESSI_TRY_HIP(hipMemcpyAsync(p->d.pos, pos, n, hipMemcpyHostToDevice, s));
+    if (m) {
+        DRESSI_TRY_HIP(hipMemcpyAsync(p->d.m, m, n, hipMemcpyHostToDevice, s));
+    } else {
+        DRESSI_TRY_HIP(hipMemsetAsync(p->d.m, 0, n, s));
+    }
+    if (v) {
+        DRESSI_TRY_HIP(hipMemcpyAsync(p->d.v, v, n, hipMemcpyHostToDevice, s));
+    } else {
+        DRESSI_TRY_HIP(hipMemsetAsync(p->d.v, 0, n, s));
+    }
+    DRESSI_TRY_HIP(hipMemcpyAsync(p->d.t, &t, 4, hipMemcpyHostToDevice, s));
+    DRESSI_TRY_HIP(hipStreamSynchronize(s));
+    p->state_set = true;
+    return DRESSI_OK;
+}
+
+int dressi_hsr_get_state(dressi_hsr_plan* p, float* pos, float* m, float* v, float* t) {
+    DRESSI_REQUIRE(p, "bad arguments");
+    DRESSI_TRY_HIP(hipSetDevice(p->ctx->device));
+    hipStream_t s = p->ctx->stream;
+    const size_t n = (size_t)p->desc.n_verts * 3 * 4;
+    if (pos) DRESSI_TRY_HIP(hipMemcpyAsync(pos, p->d.pos, n, hipMemcpyDeviceToHost, s));
+    if (m) DRESSI_TRY_HIP(hipMemcpyAsync(m, p->d.m, n, hipMemcpyDeviceToHost, s));
+    if (v) DRESSI_TRY_HIP(hipMemcpyAsync(v, p->d.v, n, hipMemcpyDeviceToHost, s));
+    if (t) DRESSI_TRY_HIP(hipMemcpyAsync(t, p->d.t, 4, hipMemcpyDeviceToHost, s));
+    DRESSI_TRY_HIP(hipStreamSynchronize(s));
+    return DRESSI_OK;
+}
+
+int dressi_hsr_step_eager(dressi_hsr_plan* p, uint32_t n_iters) {
+    if (int rc = ready(p)) return rc;
+    for (uint32_t i = 0; i < n_iters; i++) {
+        if (int rc = enqueue_iteration(p, p->ctx->stream)) return rc;
+    }
+    return DRESSI_OK;
+}
+
+int dressi_hsr_step(dressi_hsr_plan* p, uint32_t n_iters) {
+    if (int rc = ready(p)) return rc;
+    hipStream_t s = p->ctx->stream;
+    if (!p->exec || p->graph_stream != s) {
+        drop_graph(p);
+        // capture one iteration on a private stream, then replay on `s`
+        hipStream_t cap_stream = nullptr;
+        DRESSI_TRY_HIP(hipStreamCreateWithFlags(&cap_stream, hipStreamNonBlocking));
+        hipError_t e = hipStreamBeginCapture(cap_stream, hipStreamCaptureModeThreadLocal);
+        int rc = DRESSI_OK;
+        if (e == hipSuccess) {
+            rc = enqueue_iteration(p, cap_stream);
+            hipError_t e2 = hipStreamEndCapture(cap_stream, &p->graph);
+            if (!rc && e2 != hipSuccess) {
+                set_error("graph capture failed: %s", hipGetErrorString(e2));
+                rc = DRESSI_ERR_HIP;
+            }
+        } else {
+            set_error("hipStreamBeginCapture failed: %s", hipGetErrorString(e));
+            rc = DRESSI_ERR_HIP;
+        }
+        hipStreamDestroy(cap_stream);
+        if (rc) {
+            drop_graph(p);
+            return rc;
+        }
+        DRESSI_TRY_HIP(hipGraphInstantiate(&p->exec, p->graph, nullptr, nullptr, 0));
+        p->graph_stream = s;
+    }
+    for (uint32_t i = 0; i < n_iters; i++) {
+        DRESSI_TRY_HIP(hipGraphLaunch(p->exec, s));
+    }
+    return DRESSI_OK;
+}
+
+int dressi_hsr_buffer(dressi_hsr_plan* p, int which, void** ptr, size_t* bytes) {
+    DRESSI_REQUIRE(p && ptr, "bad arguments");
+    const size_t npx = (size_t)p->desc.width * p->desc.height;
+    const size_t N = p->desc.n_views, V = p->desc.n_verts;
+    void* q = nullptr;
+    size_t b = 0;
+    switch (which) {
+        case DRESSI_HSR_LOSS: q = p->d.loss; b = npx * 4; break;
+        case DRESSI_HSR_PRED: q = p->d.pred; b = N * npx * 4; break;
+        case DRESSI_HSR_TARGET: q = (void*)p->d.targets; b = N * npx * 4; break;
+        case DRESSI_HSR_FACE_ID: q = p->d.ids; b = N * npx * 4; break;
+        case DRESSI_HSR_GRAD: q = p->d.grad; b = V * 12; break;
+        case DRESSI_HSR_POS: q = p->d.pos; b = V * 12; break;
+        case DRESSI_HSR_CLIP: q = p->d.clip; b = N * V * 16; break;
+        default: DRESSI_REQUIRE(false, "unknown plan buffer %d", which);
+    }
+    DRESSI_REQUIRE(q != nullptr, "buffer %d not kept by this plan (see DRESSI_HSR_* flags)", which);
+    *ptr = q;
+    if (bytes) {
+        *bytes = b;
+    }
+    return DRESSI_OK;
+}
+
+int dressi_hsr_read(dressi_hsr_plan* p, int which, void* host, size_t bytes) {
+    void* q = nullptr;
+    size_t b = 0;
+    if (int rc = dressi_hsr_buffer(p, which, &q, &b)) return rc;
+    DRESSI_REQUIRE(host && bytes >= b, "host buffer too small (%zu < %zu)", bytes, b);
+    DRESSI_TRY_HIP(hipSetDevice(p->ctx->device));
+    DRESSI_TRY_HIP(hipMemcpyAsync(host, q, b, hipMemcpyDeviceToHost, p->ctx->stream));
+    DRESSI_TRY_HIP(hipStreamSynchronize(p->ctx->stream));
+    return DRESSI_OK;
+}
+
+int dressi_hsr_profile(dressi_hsr_plan* p, uint32_t iters, char* names, size_t name_stride,
+                       float* usec, uint32_t cap, uint32_t* n) {
+    if (int rc = ready(p)) return rc;
+    DRESSI_REQUIRE(n, "bad arguments");
+    // per-kernel timing: replay the iteration with events between launches
+    static const char* kNames[] = {"k_hsr_clip", "k_hsr_setup", "k_scan", "k_bin",
+                                   "k_hsr_raster", "k_hsr_face_bwd", "k_hsr_vertex_adam"};
+    const uint32_t nk = 7;
+    *n = nk;
+    hipStream_t s = p->ctx->stream;
+    std::vector<hipEvent_t> ev(nk + 1);
+    for (auto& e : ev) {
+        DRESSI_TRY_HIP(hipEventCreate(&e));
+    }
+    std::vector<double> acc(nk, 0.0);
+    const HsrDev& d = p->d;
+    const RasterGeom& g = d.g;
+    const uint32_t nvf = g.n_views * g.n_faces;
+    for (uint32_t it = 0; it < (iters ? iters : 1); it++) {
+        DRESSI_TRY_HIP(hipEventRecord(ev[0], s));
+        hipLaunchKernelGGL(k_hsr_clip, dim3(div_up(d.n_verts, 256), g.n_views), dim3(256), 0, s, d);
+        DRESSI_TRY_HIP(hipEventRecord(ev[1], s));
+        hipLaunchKernelGGL(k_hsr_setup, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
+        DRESSI_TRY_HIP(hipEventRecord(ev[2], s));
+        if (int rc = launch_scan_bins(s, d.bins)) return rc;
+        DRESSI_TRY_HIP(hipEventRecord(ev[3], s));
+        if (int rc = launch_bin_soft(s, g, d.recs, d.bins)) return rc;
+        DRESSI_TRY_HIP(hipEventRecord(ev[4], s));
+        switch (g.n_views) {
+#define DRESSI_NV(N) \
+    case N: hipLaunchKernelGGL(k_hsr_raster<N>, dim3(g.n_tiles), dim3(kTileThreads), 0, s, d); break;
+            DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
+            DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)
+#undef DRESSI_NV
+        }
+        DRESSI_TRY_HIP(hipEventRecord(ev[5], s));
+        hipLaunchKernelGGL(k_hsr_face_bwd, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
+        DRESSI_TRY_HIP(hipEventRecord(ev[6], s));
+        switch (g.n_views) {
+#define DRESSI_NV(N) \
+    case N: hipLaunchKernelGGL(k_hsr_vertex_adam<N>, dim3(div_up(d.n_verts, 256)), dim3(256), 0, s, d); break;
+            DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
+            DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)
+#undef DRESSI_NV
+        }
+        DRESSI_TRY_HIP(hipEventRecord(ev[7], s));
+        DRESSI_CHECK_LAUNCH();
+        DRESSI_TRY_HIP(hipEventSynchronize(ev[7]));
+        for (uint32_t k = 0; k < nk; k++) {
+            float ms = 0.f;
+            DRESSI_TRY_HIP(hipEventElapsedTime(&ms, ev[k], ev[k + 1]));
+            acc[k] += ms;
+        }
+    }
+    for (uint32_t k = 0; k < nk && k < cap; k++) {
+        if (usec) {
+            usec[k] = (float)(acc[k] * 1000.0 / (iters ? iters : 1));
+        }
+        if (names && name_stride > 0) {
+            snprintf(names + k * name_stride, name_stride, "%s", kNames[k]);
+        }
+    }
+    for (auto& e : ev) {
+        hipEventDestroy(e);
+    }
+    return DRESSI_OK;
+}
+
+// Per-op entry points --------------------------------------------------------
+
+int dressi_lookup_faces(dressi_ctx* ctx, const float* attr, uint32_t n_comp, uint32_t n_attr,
+                        const float* faces, uint32_t n_faces, uint32_t corner, float* out) {
+    DRESSI_REQUIRE(ctx && attr && faces && out, "bad arguments");
+    DRESSI_REQUIRE(corner < 3, "LookupFaces: corner must be 0, 1 or 2");
+    DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "n_comp must be 1..4");
+    if (!n_faces) return DRESSI_OK;
+    DRESSI_TRY_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(k_lookup_faces, dim3(div_up(n_faces, 256)), dim3(256), 0, ctx->stream,
+                       attr, n_comp, faces, n_faces, n_attr, corner, ctx->d_err, out);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+int dressi_lookup_faces_bwd(dressi_ctx* ctx, const float* gy, uint32_t n_comp,
+                            const float* faces, uint32_t n_faces, const float* vtx_faces,
+                            uint32_t n_verts, uint32_t max_deg, uint32_t corner, float* out) {
+    DRESSI_REQUIRE(ctx && gy && faces && vtx_faces && out, "bad arguments");
+    DRESSI_REQUIRE(corner < 3, "LookupFacesBwd: corner must be 0, 1 or 2");
+    DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "n_comp must be 1..4");
+    if (!n_verts) return DRESSI_OK;
+    DRESSI_TRY_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(k_lookup_faces_bwd, dim3(div_up(n_verts, 256)), dim3(256), 0, ctx->stream,
+                       gy, n_comp, faces, n_faces, vtx_faces, n_verts, max_deg, corner,
+                       ctx->d_err, out);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+int dressi_face_fetch(dressi_ctx* ctx, const float* attr, uint32_t n_comp, uint32_t n_faces,
+                      const float* idx, uint32_t width, uint32_t height, float* out) {
+    DRESSI_REQUIRE(ctx && attr && idx && out, "bad arguments");
+    DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "n_comp must be 1..4");
+    const size_t npx = (size_t)width * height;
+    if (!npx) return DRESSI_OK;
+    DRESSI_TRY_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(k_face_fetch, dim3((unsigned)((npx + 255) / 256)), dim3(256), 0,
+                       ctx->stream, attr, n_comp, n_faces, idx, npx, out);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+int dressi_face_fetch_bwd(dressi_ctx* ctx, const float* gy, uint32_t n_comp, const float* idx,
+                          uint32_t width, uint32_t height, const float* prj0, const float* prj1,
+                          const float* prj2, uint32_t n_faces, const float* seed,
+                          float radius_px, uint32_t n_samples, float* out) {
+    DRESSI_REQUIRE(ctx && gy && idx && prj0 && prj1 && prj2 && seed && out, "bad arguments");
+    DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "n_comp must be 1..4");
+    DRESSI_REQUIRE(radius_px > 0.f || n_samples == 0,
+                   "FaceFetch: radius must be positive (or n_samples == 0)");
+    if (!n_faces) return DRESSI_OK;
+    DRESSI_TRY_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(k_face_fetch_bwd, dim3(div_up(n_faces, 256)), dim3(256), 0, ctx->stream,
+                       gy, n_comp, idx, width, height, (const float4*)prj0, (const float4*)prj1,
+                       (const float4*)prj2, n_faces, seed, radius_px, n_samples, out);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,131 @@
+"""Per-op entry points on PyTorch-ROCm device tensors (zero copy).
+
+Each function mirrors one reference op (src/core/f_ops.cpp) with the
+reference's logical layouts: {N,1} arrays as (N, C) float32 tensors, faces as
+float ids, screen images as (H, W[, C]). Inputs must be contiguous float32
+tensors on the context's device; the work is ordered on torch's current
+stream. PyTorch is only the memory/stream provider here.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from ._lib import check, lib
+from .runtime import Context
+
+
+def _ptr(t: torch.Tensor | None, name: str) -> C.c_void_p:
+    if t is None:
+        return C.c_void_p(0)
+    if t.dtype != torch.float32 or not t.is_contiguous() or t.device.type != "cuda":
+        raise ValueError(f"{name}: expected a contiguous float32 device tensor, got "
+                         f"{t.dtype} {tuple(t.shape)} on {t.device}")
+    return C.c_void_p(t.data_ptr())
+
+
+def _prep(ctx: Context) -> None:
+    ctx.use_torch_stream()
+
+
+def soft_clip(ctx: Context, clip: torch.Tensor, faces: torch.Tensor, width: int, height: int,
+              radius_px: float) -> torch.Tensor:
+    """F::SoftClip (src/core/f_ops.cpp:1890-1981) -> (3F, 4)."""
+    _prep(ctx)
+    out = torch.empty((faces.shape[0] * 3, 4), dtype=torch.float32, device=clip.device)
+    check(lib.dressi_soft_clip(ctx.handle, _ptr(clip, "clip"), clip.shape[0],
+                               _ptr(faces, "faces"), faces.shape[0], width, height,
+                               float(radius_px), _ptr(out, "out")))
+    return out
+
+
+def rasterize_soft(ctx: Context, soft_clip: torch.Tensor, face_id: torch.Tensor,
+                   faces_soft: torch.Tensor, hard_clip: torch.Tensor, faces_tex: torch.Tensor,
+                   width: int, height: int, radius_px: float,
+                   prev_shifted_depth: torch.Tensor | None = None) -> torch.Tensor:
+    """F::RasterizeSoft (src/core/f_ops.cpp:1362-1465) -> (H, W, 4) =
+    (signed_dist_px, face_id, hard_z, coverage)."""
+    _prep(ctx)
+    out = torch.empty((height, width, 4), dtype=torch.float32, device=soft_clip.device)
+    check(lib.dressi_rasterize_soft(
+        ctx.handle, _ptr(soft_clip, "soft_clip"), _ptr(face_id, "face_id"),
+        _ptr(faces_soft, "faces_soft"), _ptr(hard_clip, "hard_clip"), hard_clip.shape[0],
+        _ptr(faces_tex, "faces_tex"), faces_tex.shape[0], width, height, float(radius_px),
+        _ptr(prev_shifted_depth, "prev_shifted_depth"), _ptr(out, "out")))
+    return out
+
+
+def rasterize(ctx: Context, clip: torch.Tensor, attr: torch.Tensor, faces: torch.Tensor,
+              width: int, height: int) -> torch.Tensor:
+    """F::Rasterize (src/core/f_ops.cpp:1182-1207) -> (H, W, C)."""
+    _prep(ctx)
+    attr2 = attr if attr.dim() == 2 else attr.reshape(-1, 1)
+    nc = attr2.shape[1]
+    out = torch.empty((height, width, nc), dtype=torch.float32, device=clip.device)
+    check(lib.dressi_rasterize(ctx.handle, _ptr(clip, "clip"), clip.shape[0], _ptr(attr2, "attr"),
+                               nc, _ptr(faces, "faces"), faces.shape[0], width, height,
+                               _ptr(out, "out")))
+    return out
+
+
+def rasterize_face_id(ctx: Context, clip: torch.Tensor, faces: torch.Tensor, width: int,
+                      height: int) -> torch.Tensor:
+    """F::RasterizeFaceId (src/core/f_ops.cpp:2183-2209) -> (H, W)."""
+    _prep(ctx)
+    out = torch.empty((height, width), dtype=torch.float32, device=clip.device)
+    check(lib.dressi_rasterize_face_id(ctx.handle, _ptr(clip, "clip"), clip.shape[0],
+                                       _ptr(faces, "faces"), faces.shape[0], width, height,
+                                       _ptr(out, "out")))
+    return out
+
+
+def lookup_faces(ctx: Context, attr: torch.Tensor, faces: torch.Tensor, corner: int) -> torch.Tensor:
+    """F::LookupFaces (src/core/f_ops.cpp:1568-1619) -> (F, C)."""
+    _prep(ctx)
+    out = torch.empty((faces.shape[0], attr.shape[1]), dtype=torch.float32, device=attr.device)
+    check(lib.dressi_lookup_faces(ctx.handle, _ptr(attr, "attr"), attr.shape[1], attr.shape[0],
+                                  _ptr(faces, "faces"), faces.shape[0], corner, _ptr(out, "out")))
+    return out
+
+
+def lookup_faces_bwd(ctx: Context, gy: torch.Tensor, faces: torch.Tensor,
+                     vtx_faces: torch.Tensor, corner: int) -> torch.Tensor:
+    """LookupFacesBwd (src/core/f_ops.cpp:1521-1565) -> (V, C)."""
+    _prep(ctx)
+    deg, nv = vtx_faces.shape
+    out = torch.empty((nv, gy.shape[1]), dtype=torch.float32, device=gy.device)
+    check(lib.dressi_lookup_faces_bwd(ctx.handle, _ptr(gy, "gy"), gy.shape[1], _ptr(faces, "faces"),
+                                      faces.shape[0], _ptr(vtx_faces, "vtx_faces"), nv, deg,
+                                      corner, _ptr(out, "out")))
+    return out
+
+
+def face_fetch(ctx: Context, attr: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """F::FaceFetch forward (src/core/f_ops.cpp:1736-1799) -> (H, W, C)."""
+    _prep(ctx)
+    h, w = idx.shape
+    out = torch.empty((h, w, attr.shape[1]), dtype=torch.float32, device=attr.device)
+    check(lib.dressi_face_fetch(ctx.handle, _ptr(attr, "attr"), attr.shape[1], attr.shape[0],
+                                _ptr(idx, "idx"), w, h, _ptr(out, "out")))
+    return out
+
+
+def face_fetch_bwd(ctx: Context, gy: torch.Tensor, idx: torch.Tensor, prj0: torch.Tensor,
+                   prj1: torch.Tensor, prj2: torch.Tensor, seed: torch.Tensor, radius_px: float,
+                   n_samples: int) -> torch.Tensor:
+    """FaceFetchBwd (src/core/f_ops.cpp:1631-1733) -> (F, C); `seed` is a
+    1-element device tensor (the in-graph iteration counter)."""
+    _prep(ctx)
+    h, w = idx.shape
+    nc = gy.shape[-1]
+    out = torch.empty((prj0.shape[0], nc), dtype=torch.float32, device=gy.device)
+    check(lib.dressi_face_fetch_bwd(ctx.handle, _ptr(gy, "gy"), nc, _ptr(idx, "idx"), w, h,
+                                    _ptr(prj0, "prj0"), _ptr(prj1, "prj1"), _ptr(prj2, "prj2"),
+                                    prj0.shape[0], _ptr(seed, "seed"), float(radius_px), n_samples,
+                                    _ptr(out, "out")))
+    return out
+
+
+__all__ = ["soft_clip", "rasterize_soft", "rasterize", "rasterize_face_id", "lookup_faces",
+           "lookup_faces_bwd", "face_fetch", "face_fetch_bwd"]
