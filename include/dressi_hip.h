@@ -159,6 +159,11 @@ void dressi_look_at(const float eye[3], const float center[3],
 void dressi_perspective_vk(float fovy_rad, float aspect, float z_near,
                            float z_far, float m[16]);
 void dressi_mat4_mul(const float a[16], const float b[16], float r[16]);
+/* The single-precision exp the kernels use for F::Sigmoid
+ * (src/core/f_ops.cpp:564-575 calls std::exp(float)), evaluated on the host:
+ * bit-identical to the C library's expf that the reference CPU evaluator
+ * calls, so device sigmoids match the reference exactly. */
+float dressi_expf(float x);
 
 /* ------------------------------------------------------------------------ */
 /* Fused HardSoftRas silhouette iteration                                   */

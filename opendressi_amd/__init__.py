@@ -1,14 +1,26 @@
 """opendressi_amd -- MI355X-native Dressi-AD HardSoftRas silhouette hot path.
 
 Hand-written gfx950 HIP kernels behind the C ABI of include/dressi_hip.h
-(libdressi_hip.so, built in-tree by opendressi_amd.build). Importing the
-package loads the library and fails loudly when it is missing.
+(libdressi_hip.so, built in-tree by opendressi_amd.build). The first use of
+any export loads the library and fails loudly when it is missing; importing
+the package itself (e.g. to run the build) does not.
 """
-from ._lib import DressiError, EXPORTED, LIB_PATH
-from .runtime import (Context, icosphere, look_at, mat4_mul, perspective_vk, randn,
-                      vertex_faces_tex)
-from .silhouette import WORKLOADS, SilhouetteFit, Workload, camera_mvps, make_scene
+import importlib
 
-__all__ = ["DressiError", "EXPORTED", "LIB_PATH", "Context", "icosphere", "look_at", "mat4_mul",
-           "perspective_vk", "randn", "vertex_faces_tex", "WORKLOADS", "SilhouetteFit",
-           "Workload", "camera_mvps", "make_scene"]
+_EXPORTS = {
+    "DressiError": "._lib", "EXPORTED": "._lib", "LIB_PATH": "._lib",
+    "Context": ".runtime", "icosphere": ".runtime", "look_at": ".runtime",
+    "mat4_mul": ".runtime", "perspective_vk": ".runtime", "randn": ".runtime",
+    "vertex_faces_tex": ".runtime",
+    "WORKLOADS": ".silhouette", "SilhouetteFit": ".silhouette", "Workload": ".silhouette",
+    "camera_mvps": ".silhouette", "make_scene": ".silhouette",
+}
+
+__all__ = sorted(_EXPORTS)
+
+
+def __getattr__(name):
+    mod = _EXPORTS.get(name)
+    if mod is None:
+        raise AttributeError(f"module 'opendressi_amd' has no attribute {name!r}")
+    return getattr(importlib.import_module(mod, __name__), name)

@@ -63,6 +63,7 @@ _SIGS = {
     "dressi_look_at": (None, [_FP, _FP, _FP, _FP]),
     "dressi_perspective_vk": (None, [_F, _F, _F, _F, _FP]),
     "dressi_mat4_mul": (None, [_FP, _FP, _FP]),
+    "dressi_expf": (_F, [_F]),
     "dressi_hsr_create": (_I, [_P, C.POINTER(HsrDesc), C.POINTER(_P)]),
     "dressi_hsr_destroy": (_I, [_P]),
     "dressi_hsr_set_mesh": (_I, [_P, _FP, _FP]),
@@ -86,6 +87,11 @@ def load(path: str = LIB_PATH) -> C.CDLL:
             f"{path} is missing: build the HIP library first "
             "(python -m opendressi_amd.build or __graft_entry__.build()); "
             "there is no CPU fallback")
+    # PyTorch-ROCm bundles its own libamdhip64.so.7. Loading torch first makes
+    # the library's libamdhip64.so.7 dependency resolve to that same runtime;
+    # loading the library first would map a second HIP + HSA runtime into the
+    # process and torch's device initialisation then fails.
+    import torch  # noqa: F401
     lib = C.CDLL(path)
     for name, (res, args) in _SIGS.items():
         fn = getattr(lib, name)

@@ -78,7 +78,14 @@ struct HsrDev {
     float* pred;              // [N][S][S] or null
     float4* gtri;             // [N][3][F]
     float* grad;              // [V][3] or null
+    // Adam bias corrections 1 - b1^t, 1 - b2^t for t = 1 .. bc_len, filled
+    // on the host with the C library's powf (the reference evaluator's
+    // F::Pow), so the in-graph Adam matches it bit for bit
+    const float2* bc_tab;
+    uint32_t bc_len;
 };
+
+constexpr uint32_t kBiasTableLen = 1u << 16;
 
 // clip_v = MVP_view * (pos, 1)  (TransformToClipVar)
 __global__ __launch_bounds__(256) void k_hsr_clip(HsrDev d) {
@@ -339,8 +346,15 @@ __global__ __launch_bounds__(256) void k_hsr_vertex_adam(HsrDev d) {
         }
         // in-graph Adam (examples/silhouette_optimization/run.cpp:421-436)
         const float t_new = t + 1.f;
-        const float bc1 = 1.f - powf(d.b1, t_new);
-        const float bc2 = 1.f - powf(d.b2, t_new);
+        float bc1, bc2;
+        if (t_new >= 1.f && t_new <= (float)d.bc_len && t_new == floorf(t_new)) {
+            const float2 bc = d.bc_tab[(uint32_t)t_new - 1];
+            bc1 = bc.x;
+            bc2 = bc.y;
+        } else {
+            bc1 = 1.f - powf(d.b1, t_new);
+            bc2 = 1.f - powf(d.b2, t_new);
+        }
         const float cb1 = 1.f - d.b1, cb2 = 1.f - d.b2;
 #pragma unroll
         for (int c = 0; c < 3; c++) {
@@ -638,6 +652,23 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
     if (!rc && (desc->flags & DRESSI_HSR_KEEP_PRED)) rc = plan_alloc(p, &d.pred, N * npx);
     if (!rc && (desc->flags & DRESSI_HSR_KEEP_GRAD)) rc = plan_alloc(p, &d.grad, V * 3);
     d.gtri = gtri;
+    float2* bc = nullptr;
+    if (!rc) rc = plan_alloc(p, &bc, kBiasTableLen);
+    if (!rc) {
+        std::vector<float2> tab(kBiasTableLen);
+        for (uint32_t i = 0; i < kBiasTableLen; i++) {
+            const float tn = (float)(i + 1);
+            tab[i] = make_float2(1.f - powf(desc->beta1, tn), 1.f - powf(desc->beta2, tn));
+        }
+        hipError_t e = hipMemcpy(bc, tab.data(), sizeof(float2) * kBiasTableLen,
+                                 hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            set_error("bias table upload failed: %s", hipGetErrorString(e));
+            rc = DRESSI_ERR_HIP;
+        }
+        d.bc_tab = bc;
+        d.bc_len = kBiasTableLen;
+    }
     if (!rc) {
         const uint32_t cap = default_bin_cap(d.g, 16);
         uint32_t* bm = nullptr;

@@ -15,8 +15,8 @@
 // contributions of a variable are summed in descending node-creation order,
 // which for the example's expressions (g++ evaluates call arguments right to
 // left) is listed at each sum below. Every op is replayed with the same
-// float operations, so the result matches the reference evaluator up to the
-// last-ulp differences of expf.
+// float operations and the sigmoid's exp is libc_expf, so the results are
+// bit-identical to the reference evaluator's.
 #pragma once
 
 #include "dressi_math.h"
@@ -112,7 +112,7 @@ __device__ __forceinline__ void pixel_fw(const float4 c[3], float mask, float di
     }
     st.inside = smin(sp + sn, 1.f);
     const float dist = (st.inside * 2.f - 1.f) * st.dmin;
-    st.sig = 1.f / (1.f + expf(-(dist * sigma_scale)));
+    st.sig = 1.f / (1.f + libc_expf(-(dist * sigma_scale)));
     const float D = mask * st.sig;
     st.soft_sil = 1.f - 1.f * (1.f - D);
     st.hard = cov * step_f(0.f, dist_c);

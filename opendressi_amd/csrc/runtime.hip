@@ -340,6 +340,8 @@ void dressi_perspective_vk(float fovy_rad, float aspect, float z_near, float z_f
     m[14] = z_near * z_far / (z_near - z_far);
 }
 
+float dressi_expf(float x) { return libc_expf(x); }
+
 // examples/common/asset_utils.cpp:719-731 (Mul, column-major)
 void dressi_mat4_mul(const float a[16], const float b[16], float r[16]) {
     float t[16];

@@ -105,3 +105,26 @@ def test_errors_are_reported_without_a_device():
     with pytest.raises(od.DressiError):
         from opendressi_amd._lib import check
         check(lib.dressi_hsr_step(None, 1))
+
+
+def test_kernel_expf_matches_c_library():
+    """The sigmoid's exp (shared host/device code) against the C library expf
+    the reference evaluator calls: random inputs over the sigmoid's range,
+    special values, and the two hard-rounding inputs where a non-fused range
+    reduction differs."""
+    import ctypes as C
+    import struct
+
+    from opendressi_amd._lib import lib
+    libm = C.CDLL("libm.so.6")
+    libm.expf.restype = C.c_float
+    libm.expf.argtypes = [C.c_float]
+    rng = np.random.default_rng(3)
+    xs = np.concatenate([rng.uniform(-110, 90, 20000), rng.uniform(-3, 3, 20000),
+                         [0.0, -0.0, 88.72, 88.73, -103.9, -104.0, float("inf"), float("-inf"),
+                          struct.unpack("<f", struct.pack("<I", 0x42024A2F))[0],  # 0x1.04845ep+5
+                          struct.unpack("<f", struct.pack("<I", 0xC27C65D9))[0]]])  # -0x1.f8cbb2p+5
+    xs = xs.astype(np.float32)
+    bad = [float(x) for x in xs
+           if struct.pack("<f", lib.dressi_expf(float(x))) != struct.pack("<f", libm.expf(float(x)))]
+    assert not bad, bad[:5]
