@@ -233,10 +233,11 @@ enum dressi_hsr_buffer {
     DRESSI_HSR_LOSS = 0,    /* {S,S} float: the loss image */
     DRESSI_HSR_PRED = 1,    /* {N,S,S} float (needs DRESSI_HSR_KEEP_PRED) */
     DRESSI_HSR_TARGET = 2,  /* {N,S,S} float */
-    DRESSI_HSR_FACE_ID = 3, /* {N,S,S} uint32: face + 1 of RasterizeSoft, 0 bg */
+    DRESSI_HSR_FACE_ID = 3, /* {N,S,S} uint32: face + 1 of RasterizeSoft, 0 bg;
+                               bit 31 set when the winning fragment lies
+                               outside its hard triangle (signed dist < 0) */
     DRESSI_HSR_GRAD = 4,    /* {V,3} float (needs DRESSI_HSR_KEEP_GRAD) */
-    DRESSI_HSR_POS = 5,     /* {V,3} float */
-    DRESSI_HSR_CLIP = 6     /* {N,V,4} float: clip positions of the last step */
+    DRESSI_HSR_POS = 5      /* {V,3} float */
 };
 /* Device pointer of a plan buffer (zero-copy access) and its size. */
 int dressi_hsr_buffer(dressi_hsr_plan* plan, int which, void** ptr,

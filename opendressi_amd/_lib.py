@@ -33,7 +33,8 @@ class HsrDesc(C.Structure):
 
 HSR_KEEP_PRED = 1
 HSR_KEEP_GRAD = 2
-BUF_LOSS, BUF_PRED, BUF_TARGET, BUF_FACE_ID, BUF_GRAD, BUF_POS, BUF_CLIP = range(7)
+BUF_LOSS, BUF_PRED, BUF_TARGET, BUF_FACE_ID, BUF_GRAD, BUF_POS = range(6)
+FACE_ID_RIM = 0x80000000  # bit of a face-id entry: winner outside its hard triangle
 
 # name -> (restype, argtypes)
 _SIGS = {

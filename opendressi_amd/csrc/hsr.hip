@@ -70,10 +70,9 @@ struct HsrDev {
     const uint8_t* vf_mask;   // [deg][V], bit k: faces[vf][k] == v
     const float* mvps;        // [N][16]
     const float* targets;     // [N][S][S]
-    float4* clip;             // [N][V]
     SoftRec* recs;            // [N][F]
-    BinBuffers bins;
-    uint32_t* ids;            // [N][S][S] face + 1
+    BinBuffers bins;          // fixed-capacity soft bins, N x tiles
+    uint32_t* ids;            // [N][S][S] face + 1 (bit 31: rim winner), 0 bg
     float* loss;              // [S][S]
     float* pred;              // [N][S][S] or null
     float4* gtri;             // [N][3][F]
@@ -83,60 +82,59 @@ struct HsrDev {
     // F::Pow), so the in-graph Adam matches it bit for bit
     const float2* bc_tab;
     uint32_t bc_len;
+    // profiling only: the raster leaves the bins filled so it can be replayed
+    uint32_t keep_bins;
 };
 
 constexpr uint32_t kBiasTableLen = 1u << 16;
+constexpr uint32_t kRimFlag = 0x80000000u;
 
-// clip_v = MVP_view * (pos, 1)  (TransformToClipVar)
-__global__ __launch_bounds__(256) void k_hsr_clip(HsrDev d) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    const uint32_t view = blockIdx.y;
-    if (i >= d.n_verts) {
-        return;
-    }
+// Corner clips of face f in one view: TransformToClipVar of its vertices.
+__device__ __forceinline__ void face_clips(const HsrDev& d, uint32_t view, uint32_t f,
+                                           float4 c[3]) {
     const float* m = d.mvps + view * 16;
-    d.clip[(size_t)view * d.n_verts + i] =
-            mvp_transform(m, d.pos[i * 3 + 0], d.pos[i * 3 + 1], d.pos[i * 3 + 2]);
-}
-
-// SoftClip + RasterizeSoft setup per (view, face), then the bin counts.
-__global__ __launch_bounds__(256) void k_hsr_setup(HsrDev d) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= d.g.n_views * d.g.n_faces) {
-        return;
-    }
-    const uint32_t view = i / d.g.n_faces;
-    const uint32_t f = i - view * d.g.n_faces;
-    float4 hc[3], sc[3];
 #pragma unroll
     for (int k = 0; k < 3; k++) {
-        hc[k] = d.clip[(size_t)view * d.n_verts + d.faces[f * 3 + k]];
+        const int32_t vi = d.faces[f * 3 + k];
+        c[k] = mvp_transform(m, d.pos[vi * 3 + 0], d.pos[vi * 3 + 1], d.pos[vi * 3 + 2]);
     }
-    soft_clip_face(hc, d.g.width, d.g.height, d.radius, sc);
+}
+
+// SoftClip + RasterizeSoft setup per (view, face), appended to the soft bins.
+__global__ __launch_bounds__(256) void k_hsr_setup(HsrDev d) {
+    __shared__ BinLds blds;
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = i < d.g.n_views * d.g.n_faces;
+    const uint32_t view = live ? i / d.g.n_faces : 0;
+    const uint32_t f = live ? i - view * d.g.n_faces : 0;
     SoftRec r;
-    soft_setup(sc, hc, (float)f, d.g.width, d.g.height, &r);
-    d.recs[i] = r;
-    if (r.bx0 > r.bx1 || r.by0 > r.by1) {
-        return;
+    r.bx0 = 1;
+    r.bx1 = 0;
+    r.by0 = 1;
+    r.by1 = 0;
+    if (live) {
+        float4 hc[3], sc[3];
+        face_clips(d, view, f, hc);
+        soft_clip_face(hc, d.g.width, d.g.height, d.radius, sc);
+        soft_setup(sc, hc, (float)f, d.g.width, d.g.height, &r);
+        d.recs[i] = r;
     }
-    uint32_t* cnt = d.bins.counts + (size_t)view * d.g.n_tiles;
-    for (int ty = r.by0 / kTile; ty <= r.by1 / kTile; ty++) {
-        for (int tx = r.bx0 / kTile; tx <= r.bx1 / kTile; tx++) {
-            atomicAdd(&cnt[ty * d.g.tiles_x + tx], 1u);
-        }
-    }
+    const bool valid = live && r.bx0 <= r.bx1 && r.by0 <= r.by1;
+    bin_append(d.bins, d.g, valid, view, f, r.bx0, r.by0, r.bx1, r.by1, blds);
 }
 
 // One workgroup per 16x16 tile, all views: resolve the RasterizeSoft winner
 // of every view, write the face-id buffer, evaluate pred and the loss image
-// (SumPixelWise over views).
+// (SumPixelWise over views), and clear the tile's bin counters.
 template <int NV>
 __global__ __launch_bounds__(kTileThreads) void k_hsr_raster(HsrDev d) {
-    __shared__ SoftRec lds_rec[kTileThreads];
-    __shared__ uint32_t lds_face[kTileThreads];
+    __shared__ TileLds lds;
     const uint32_t tile = blockIdx.x;
-    const int px = (int)((tile % d.g.tiles_x) * kTile + (threadIdx.x % kTile));
-    const int py = (int)((tile / d.g.tiles_x) * kTile + (threadIdx.x / kTile));
+    const uint32_t tx = tile % d.g.tiles_x, ty = tile / d.g.tiles_x;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int px = (int)tx * kTile + (wave & 1) * 8 + (lane & 7);
+    const int py = (int)ty * kTile + (wave >> 1) * 8 + (lane >> 3);
     const bool on = px < (int)d.g.width && py < (int)d.g.height;
     const size_t npx = (size_t)d.g.width * d.g.height;
     const size_t o = (size_t)py * d.g.width + px;
@@ -144,26 +142,27 @@ __global__ __launch_bounds__(kTileThreads) void k_hsr_raster(HsrDev d) {
     float lv[NV][1];
 #pragma unroll
     for (int view = 0; view < NV; view++) {
-        uint64_t best = kEmptyKey;
-        float bd = 0.f, bhz = 0.f;
-        walk_bin(d.recs + (size_t)view * d.g.n_faces, d.bins, view * d.g.n_tiles + tile,
-                 d.g.n_faces, lds_rec, lds_face, [&](const SoftRec& r, uint32_t f) {
-                     soft_fragment(r, f, px, py, d.radius, nullptr, d.g.width, &best, &bd, &bhz);
-                 });
+        const uint32_t bin = view * d.g.n_tiles + tile;
+        const BinView bv = bin_view(d.bins, bin, d.g.n_faces);
+        const PixelBest best = resolve_tile(d.recs + (size_t)view * d.g.n_faces, bv, tx, ty,
+                                            d.radius, nullptr, d.g.width, lds);
         float pred = 0.f;
         uint32_t id = 0;
-        if (on && best != kEmptyKey) {
-            const uint32_t f = key_face(best);
-            id = f + 1;
-            float4 c[3];
-#pragma unroll
-            for (int k = 0; k < 3; k++) {
-                c[k] = d.clip[(size_t)view * d.n_verts + d.faces[f * 3 + k]];
+        if (on && best.key != kEmptyKey) {
+            const uint32_t f = key_face(best.key);
+            if (best.hard) {
+                // cov * step(0, dist) = 1 and soft_sil <= 1: max(1, soft_sil) = 1
+                pred = 1.f;
+                id = f + 1;
+            } else {
+                float4 c[3];
+                face_clips(d, view, f, c);
+                PixelFw st;
+                pixel_fw(c, 1.f, -1.f, 1.f, (float)px + 0.5f, (float)py + 0.5f, W, H,
+                         d.sigma_scale, st);
+                pred = st.pred;
+                id = (f + 1) | kRimFlag;
             }
-            PixelFw st;
-            pixel_fw(c, 1.f, bd, 1.f, (float)px + 0.5f, (float)py + 0.5f, W, H, d.sigma_scale,
-                     st);
-            pred = st.pred;
         }
         float tgt = 0.f;
         if (on) {
@@ -175,6 +174,9 @@ __global__ __launch_bounds__(kTileThreads) void k_hsr_raster(HsrDev d) {
         }
         const float diff = tgt - pred;
         lv[view][0] = diff * diff * d.inv_px;
+        if (threadIdx.x == 0 && !d.keep_bins) {
+            d.bins.counts[bin] = 0;  // every lane read it before resolve_tile's barriers
+        }
     }
     if (on) {
         float out[1];
@@ -185,7 +187,9 @@ __global__ __launch_bounds__(kTileThreads) void k_hsr_raster(HsrDev d) {
 
 // FaceFetchBwd (stochastic, n samples, seed = t) fused with the pixel
 // chain's backward at each accepted sample: per (view, face) the three
-// corner-clip gradients (src/core/f_ops.cpp:1646-1729, 1700-1727).
+// corner-clip gradients (src/core/f_ops.cpp:1646-1729, 1700-1727). Samples on
+// pixels whose winner is a hard-branch fragment contribute exactly zero
+// (pred = max(1, soft) passes no gradient to soft) and are skipped.
 __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= d.g.n_views * d.g.n_faces) {
@@ -195,17 +199,14 @@ __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
     const uint32_t f = i - view * d.g.n_faces;
     const float W = (float)d.g.width, H = (float)d.g.height;
     float4 c[3];
-#pragma unroll
-    for (int k = 0; k < 3; k++) {
-        c[k] = d.clip[(size_t)view * d.n_verts + d.faces[f * 3 + k]];
-    }
+    face_clips(d, view, f, c);
     float4 acc[3];
 #pragma unroll
     for (int k = 0; k < 3; k++) {
         acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float4* dst = d.gtri + (size_t)view * 3 * d.g.n_faces;
-    bool ok = c[0].w > 1e-6f && c[1].w > 1e-6f && c[2].w > 1e-6f;
+    const bool ok = c[0].w > 1e-6f && c[1].w > 1e-6f && c[2].w > 1e-6f;
     if (ok && d.n_samples > 0) {
         float s[3][2];
 #pragma unroll
@@ -213,15 +214,6 @@ __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
             s[k][0] = (c[k].x / c[k].w * 0.5f + 0.5f) * W;
             s[k][1] = (c[k].y / c[k].w * 0.5f + 0.5f) * H;
         }
-        // hard triangle of the rasterizer (for the dist channel's sign)
-        float hx[3], hy[3];
-        for (int k = 0; k < 3; k++) {
-            const ScreenVert v = project_to_screen(c[k].x, c[k].y, c[k].z, c[k].w, W, H);
-            hx[k] = v.x;
-            hy[k] = v.y;
-        }
-        HardTri ht;
-        hard_tri_init(&ht, hx, hy);
         const uint32_t seed_u = (uint32_t)(int64_t)(*d.t + 0.5f);
         const size_t npx = (size_t)d.g.width * d.g.height;
         const uint32_t* ids = d.ids + view * npx;
@@ -246,13 +238,13 @@ __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
                 continue;
             }
             const size_t p = (size_t)iy * d.g.width + ix;
-            if (ids[p] != f + 1) {
-                continue;
+            const uint32_t id = ids[p];
+            if (id != ((f + 1) | kRimFlag)) {
+                continue;  // other face, or a hard-branch winner (zero gradient)
             }
             const float pcx = (float)ix + 0.5f, pcy = (float)iy + 0.5f;
-            const float dist_c = signed_dist(pcx, pcy, ht.ax, ht.ay, ht.ex, ht.ey, ht.len2);
             PixelFw st;
-            pixel_fw(c, 1.f, dist_c, 1.f, pcx, pcy, W, H, d.sigma_scale, st);
+            pixel_fw(c, 1.f, -1.f, 1.f, pcx, pcy, W, H, d.sigma_scale, st);
             float4 g[3];
             pixel_bw(st, c, 1.f, tgt[p], d.inv_px, W, H, d.sigma_scale, g);
 #pragma unroll
@@ -546,42 +538,57 @@ int plan_alloc(dressi_hsr_plan* p, T** out, size_t count) {
     return DRESSI_OK;
 }
 
-int enqueue_iteration(dressi_hsr_plan* p, hipStream_t s) {
-    const HsrDev& d = p->d;
+// Kernel k of one iteration: 0 setup + binning, 1 raster / forward,
+// 2 face backward, 3 vertex backward + Adam.
+constexpr int kIterKernels = 4;
+const char* const kIterKernelNames[kIterKernels] = {"k_hsr_setup", "k_hsr_raster",
+                                                    "k_hsr_face_bwd", "k_hsr_vertex_adam"};
+
+int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
     const RasterGeom& g = d.g;
-    hipLaunchKernelGGL(k_hsr_clip, dim3(div_up(d.n_verts, 256), g.n_views), dim3(256), 0, s, d);
-    DRESSI_CHECK_LAUNCH();
     const uint32_t nvf = g.n_views * g.n_faces;
-    hipLaunchKernelGGL(k_hsr_setup, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
-    DRESSI_CHECK_LAUNCH();
-    if (int rc = launch_scan_bins(s, d.bins)) return rc;
-    if (int rc = launch_bin_soft(s, g, d.recs, d.bins)) return rc;
-    switch (g.n_views) {
+    switch (k) {
+        case 0:
+            hipLaunchKernelGGL(k_hsr_setup, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
+            break;
+        case 1:
+            switch (g.n_views) {
 #define DRESSI_NV(N)                                                                          \
     case N:                                                                                   \
         hipLaunchKernelGGL(k_hsr_raster<N>, dim3(g.n_tiles), dim3(kTileThreads), 0, s, d);    \
         break;
-        DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
-        DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)
+                DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
+                DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)
 #undef DRESSI_NV
+                default:
+                    set_error("n_views %u unsupported", g.n_views);
+                    return DRESSI_ERR_UNSUPPORTED;
+            }
+            break;
+        case 2:
+            hipLaunchKernelGGL(k_hsr_face_bwd, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
+            break;
         default:
-            set_error("n_views %u unsupported", g.n_views);
-            return DRESSI_ERR_UNSUPPORTED;
-    }
-    DRESSI_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_hsr_face_bwd, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
-    DRESSI_CHECK_LAUNCH();
-    const dim3 vg(div_up(d.n_verts, 256));
-    switch (g.n_views) {
-#define DRESSI_NV(N)                                                                  \
-    case N:                                                                           \
-        hipLaunchKernelGGL(k_hsr_vertex_adam<N>, vg, dim3(256), 0, s, d);             \
+            switch (g.n_views) {
+#define DRESSI_NV(N)                                                                          \
+    case N:                                                                                   \
+        hipLaunchKernelGGL(k_hsr_vertex_adam<N>, dim3(div_up(d.n_verts, 256)), dim3(256), 0,  \
+                           s, d);                                                             \
         break;
-        DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
-        DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)
+                DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
+                DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)
 #undef DRESSI_NV
+            }
+            break;
     }
     DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+int enqueue_iteration(dressi_hsr_plan* p, hipStream_t s) {
+    for (int k = 0; k < kIterKernels; k++) {
+        if (int rc = launch_iter_kernel(p->d, s, k)) return rc;
+    }
     return DRESSI_OK;
 }
 
@@ -644,7 +651,6 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
     rc = rc ? rc : plan_alloc(p, &d.done, 1);
     rc = rc ? rc : plan_alloc(p, (float**)&d.mvps, N * 16);
     rc = rc ? rc : plan_alloc(p, (float**)&d.targets, N * npx);
-    rc = rc ? rc : plan_alloc(p, &d.clip, N * V);
     rc = rc ? rc : plan_alloc(p, &d.recs, N * F);
     rc = rc ? rc : plan_alloc(p, &d.ids, N * npx);
     rc = rc ? rc : plan_alloc(p, &d.loss, npx);
@@ -670,12 +676,11 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
         d.bc_len = kBiasTableLen;
     }
     if (!rc) {
-        const uint32_t cap = default_bin_cap(d.g, 16);
         uint32_t* bm = nullptr;
-        const size_t bytes = bin_bytes(d.g.n_tiles * d.g.n_views, cap);
+        const size_t bytes = fixed_bin_bytes(d.g.n_tiles * d.g.n_views, kSoftBinCap);
         rc = plan_alloc(p, &bm, bytes / sizeof(uint32_t) + 1);
         if (!rc) {
-            bin_carve(bm, d.g.n_tiles * d.g.n_views, cap, &d.bins);
+            fixed_bin_carve(bm, d.g.n_tiles * d.g.n_views, kSoftBinCap, &d.bins);
         }
     }
     if (!rc) {
@@ -929,7 +934,6 @@ int dressi_hsr_buffer(dressi_hsr_plan* p, int which, void** ptr, size_t* bytes) 
         case DRESSI_HSR_FACE_ID: q = p->d.ids; b = N * npx * 4; break;
         case DRESSI_HSR_GRAD: q = p->d.grad; b = V * 12; break;
         case DRESSI_HSR_POS: q = p->d.pos; b = V * 12; break;
-        case DRESSI_HSR_CLIP: q = p->d.clip; b = N * V * 16; break;
         default: DRESSI_REQUIRE(false, "unknown plan buffer %d", which);
     }
     DRESSI_REQUIRE(q != nullptr, "buffer %d not kept by this plan (see DRESSI_HSR_* flags)", which);
@@ -955,68 +959,66 @@ int dressi_hsr_profile(dressi_hsr_plan* p, uint32_t iters, char* names, size_t n
                        float* usec, uint32_t cap, uint32_t* n) {
     if (int rc = ready(p)) return rc;
     DRESSI_REQUIRE(n, "bad arguments");
-    // per-kernel timing: replay the iteration with events between launches
-    static const char* kNames[] = {"k_hsr_clip", "k_hsr_setup", "k_scan", "k_bin",
-                                   "k_hsr_raster", "k_hsr_face_bwd", "k_hsr_vertex_adam"};
-    const uint32_t nk = 7;
-    *n = nk;
+    // Average device time per launch of each kernel of the iteration, from
+    // HIP events on the plan stream around `iters` back-to-back launches of
+    // that kernel alone (the setup / raster replays are idempotent: the setup
+    // recomputes the same records, the raster replays keep the bins; the
+    // backward kernels replay one iteration's state). Advances the plan by
+    // one iteration.
+    const uint32_t reps = iters ? iters : 1;
+    *n = kIterKernels;
     hipStream_t s = p->ctx->stream;
-    std::vector<hipEvent_t> ev(nk + 1);
-    for (auto& e : ev) {
-        DRESSI_TRY_HIP(hipEventCreate(&e));
-    }
-    std::vector<double> acc(nk, 0.0);
-    const HsrDev& d = p->d;
-    const RasterGeom& g = d.g;
-    const uint32_t nvf = g.n_views * g.n_faces;
-    for (uint32_t it = 0; it < (iters ? iters : 1); it++) {
-        DRESSI_TRY_HIP(hipEventRecord(ev[0], s));
-        hipLaunchKernelGGL(k_hsr_clip, dim3(div_up(d.n_verts, 256), g.n_views), dim3(256), 0, s, d);
-        DRESSI_TRY_HIP(hipEventRecord(ev[1], s));
-        hipLaunchKernelGGL(k_hsr_setup, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
-        DRESSI_TRY_HIP(hipEventRecord(ev[2], s));
-        if (int rc = launch_scan_bins(s, d.bins)) return rc;
-        DRESSI_TRY_HIP(hipEventRecord(ev[3], s));
-        if (int rc = launch_bin_soft(s, g, d.recs, d.bins)) return rc;
-        DRESSI_TRY_HIP(hipEventRecord(ev[4], s));
-        switch (g.n_views) {
-#define DRESSI_NV(N) \
-    case N: hipLaunchKernelGGL(k_hsr_raster<N>, dim3(g.n_tiles), dim3(kTileThreads), 0, s, d); break;
-            DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
-            DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)
-#undef DRESSI_NV
+    hipEvent_t e0, e1;
+    DRESSI_TRY_HIP(hipEventCreate(&e0));
+    DRESSI_TRY_HIP(hipEventCreate(&e1));
+    HsrDev keep = p->d;
+    keep.keep_bins = 1;
+    float ms[kIterKernels] = {0.f, 0.f, 0.f, 0.f};
+    int rc = DRESSI_OK;
+    for (int k = 0; k < kIterKernels && !rc; k++) {
+        if (k == 0) {
+            // one setup fills the bins; replays would append duplicates, so
+            // time them on a copy whose bins are cleared by a raster pass
+            for (uint32_t r = 0; r < reps && !rc; r++) {
+                DRESSI_TRY_HIP(hipEventRecord(e0, s));
+                rc = launch_iter_kernel(p->d, s, 0);
+                DRESSI_TRY_HIP(hipEventRecord(e1, s));
+                DRESSI_TRY_HIP(hipEventSynchronize(e1));
+                float t = 0.f;
+                DRESSI_TRY_HIP(hipEventElapsedTime(&t, e0, e1));
+                ms[0] += t / reps;
+                if (!rc && r + 1 < reps) {
+                    rc = launch_iter_kernel(p->d, s, 1);  // consumes and clears the bins
+                }
+            }
+            continue;
         }
-        DRESSI_TRY_HIP(hipEventRecord(ev[5], s));
-        hipLaunchKernelGGL(k_hsr_face_bwd, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
-        DRESSI_TRY_HIP(hipEventRecord(ev[6], s));
-        switch (g.n_views) {
-#define DRESSI_NV(N) \
-    case N: hipLaunchKernelGGL(k_hsr_vertex_adam<N>, dim3(div_up(d.n_verts, 256)), dim3(256), 0, s, d); break;
-            DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
-            DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)
-#undef DRESSI_NV
+        const HsrDev& dk = k == 1 ? keep : p->d;
+        DRESSI_TRY_HIP(hipEventRecord(e0, s));
+        for (uint32_t r = 0; r < (k == 3 ? 1u : reps) && !rc; r++) {
+            rc = launch_iter_kernel(dk, s, k);
         }
-        DRESSI_TRY_HIP(hipEventRecord(ev[7], s));
-        DRESSI_CHECK_LAUNCH();
-        DRESSI_TRY_HIP(hipEventSynchronize(ev[7]));
-        for (uint32_t k = 0; k < nk; k++) {
-            float ms = 0.f;
-            DRESSI_TRY_HIP(hipEventElapsedTime(&ms, ev[k], ev[k + 1]));
-            acc[k] += ms;
+        DRESSI_TRY_HIP(hipEventRecord(e1, s));
+        DRESSI_TRY_HIP(hipEventSynchronize(e1));
+        DRESSI_TRY_HIP(hipEventElapsedTime(&ms[k], e0, e1));
+        if (k != 3) {
+            ms[k] /= reps;
+        }
+        if (k == 1 && !rc) {
+            rc = launch_iter_kernel(p->d, s, 1);  // the clearing pass
         }
     }
-    for (uint32_t k = 0; k < nk && k < cap; k++) {
+    for (uint32_t k = 0; k < (uint32_t)kIterKernels && k < cap; k++) {
         if (usec) {
-            usec[k] = (float)(acc[k] * 1000.0 / (iters ? iters : 1));
+            usec[k] = ms[k] * 1000.f;
         }
         if (names && name_stride > 0) {
-            snprintf(names + k * name_stride, name_stride, "%s", kNames[k]);
+            snprintf(names + k * name_stride, name_stride, "%s", kIterKernelNames[k]);
         }
     }
-    for (auto& e : ev) {
-        hipEventDestroy(e);
-    }
-    return DRESSI_OK;
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    return rc;
 }
 
 // Per-op entry points --------------------------------------------------------

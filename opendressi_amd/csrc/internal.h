@@ -59,8 +59,10 @@ void clear_error();
         }                                                                      \
     } while (0)
 
-// Workspace slot `i` of at least `bytes` (grow-only; contents undefined).
+// Workspace slot `i` of at least `bytes` (grow-only; contents undefined, or
+// zero-filled on (re)allocation with ctx_workspace_zeroed).
 int ctx_workspace(dressi_ctx* ctx, int slot, size_t bytes, void** out);
+int ctx_workspace_zeroed(dressi_ctx* ctx, int slot, size_t bytes, void** out);
 
 inline uint32_t div_up(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 
@@ -71,21 +73,29 @@ constexpr int kTile = 16;
 constexpr int kTileThreads = kTile * kTile;
 
 // Per (view, face) setup record of the soft rasterizer: soft triangle
-// (coverage), hard triangle (signed distance + hard z) and the inclusive
-// pixel bbox. 36 words.
-struct SoftRec {
+// (coverage), hard triangle (signed distance, edge-function filter, hard z)
+// and the inclusive soft pixel bbox. 41 words, padded to 44 so that it
+// moves with 16-byte loads.
+struct alignas(16) SoftRec {
     float sx[3], sy[3];
     float s_inv_area;
     float sz[3];
     float hx[3], hy[3], ex[3], ey[3], len2[3];
+    float cc[3], thr[3];  // edge-function filter: ex*py - ey*px + cc, threshold
     float hz[3];
     float h_inv_area;
-    int h_area_ok;
+    uint32_t flags;          // kRecHardArea | kRecSliver
     int bx0, by0, bx1, by1;  // bx0 > bx1: face produces no fragment
     float fid;               // face_id value written to the output
-    int pad;
 };
-static_assert(sizeof(SoftRec) == 36 * 4, "SoftRec layout");
+static_assert(sizeof(SoftRec) == 44 * 4, "SoftRec layout");
+// SoftRec::flags: the hard triangle's |area| passes the 1e-6 test (hard z is
+// interpolated, else 0.5) ...
+constexpr uint32_t kRecHardArea = 1u;
+// ... and the hard triangle is too thin for the bbox culls of the resolver
+// (a pixel the reference's winding test calls inside may lie more than 1 px
+// outside its bbox): the face is then evaluated over its whole soft bbox.
+constexpr uint32_t kRecSliver = 2u;
 
 // Per (view, face) setup record of the hard rasterizer (RasterizeCore).
 struct HardRec {
@@ -97,14 +107,33 @@ struct HardRec {
 static_assert(sizeof(HardRec) == 20 * 4, "HardRec layout");
 
 // Device buffers of one binning problem: `n_bins` = views x tiles.
+// Scan-based bins (hard rasterizer): counts -> offsets -> list[cap].
+// Fixed-capacity bins (soft rasterizer): list[bin * cap + slot], counts
+// cleared by the consumer; offsets / cursor unused.
 struct BinBuffers {
     uint32_t* counts = nullptr;   // [n_bins], zero between uses
     uint32_t* offsets = nullptr;  // [n_bins + 1]
     uint32_t* cursor = nullptr;   // [n_bins]
-    uint32_t* list = nullptr;     // [cap] face indices
+    uint32_t* list = nullptr;     // [cap] or [n_bins][cap] face indices
     uint32_t cap = 0;
     uint32_t n_bins = 0;
 };
+
+// Fixed-capacity soft bins: n_bins counters + n_bins * cap entries.
+inline size_t fixed_bin_bytes(uint32_t n_bins, uint32_t cap) {
+    return sizeof(uint32_t) * ((size_t)n_bins + (size_t)n_bins * cap) + 256;
+}
+inline void fixed_bin_carve(void* base, uint32_t n_bins, uint32_t cap, BinBuffers* b) {
+    uint32_t* p = (uint32_t*)base;
+    b->counts = p;
+    b->offsets = nullptr;
+    b->cursor = nullptr;
+    b->list = p + n_bins;
+    b->cap = cap;
+    b->n_bins = n_bins;
+}
+// Entries per soft bin (a 16x16 tile of one view).
+constexpr uint32_t kSoftBinCap = 1024;
 
 struct RasterGeom {
     uint32_t width, height, tiles_x, tiles_y, n_tiles, n_views, n_faces;
@@ -124,9 +153,7 @@ inline RasterGeom make_geom(uint32_t w, uint32_t h, uint32_t views, uint32_t fac
 
 // Kernels shared between raster.hip and hsr.hip (launch helpers).
 int launch_scan_bins(hipStream_t s, const BinBuffers& b);
-int launch_bin_soft(hipStream_t s, const RasterGeom& g, const SoftRec* recs, const BinBuffers& b);
 int launch_bin_hard(hipStream_t s, const RasterGeom& g, const HardRec* recs, const BinBuffers& b);
-int launch_count_soft(hipStream_t s, const RasterGeom& g, const SoftRec* recs, const BinBuffers& b);
 int launch_count_hard(hipStream_t s, const RasterGeom& g, const HardRec* recs, const BinBuffers& b);
 // Hard raster of a clip-space mesh into `out` ({views,S,S} x n_comp):
 // mode 0 = attribute interpolation, 1 = face id + 1. `clip` is [views][V]

@@ -109,20 +109,6 @@ int launch_scan_bins(hipStream_t s, const BinBuffers& b) {
     return DRESSI_OK;
 }
 
-int launch_count_soft(hipStream_t s, const RasterGeom& g, const SoftRec* recs, const BinBuffers& b) {
-    const uint32_t n = g.n_views * g.n_faces;
-    hipLaunchKernelGGL(k_count<SoftRec>, dim3(div_up(n, 256)), dim3(256), 0, s, g, recs, b);
-    DRESSI_CHECK_LAUNCH();
-    return DRESSI_OK;
-}
-
-int launch_bin_soft(hipStream_t s, const RasterGeom& g, const SoftRec* recs, const BinBuffers& b) {
-    const uint32_t n = g.n_views * g.n_faces;
-    hipLaunchKernelGGL(k_bin<SoftRec>, dim3(div_up(n, 256)), dim3(256), 0, s, g, recs, b);
-    DRESSI_CHECK_LAUNCH();
-    return DRESSI_OK;
-}
-
 int launch_count_hard(hipStream_t s, const RasterGeom& g, const HardRec* recs, const BinBuffers& b) {
     const uint32_t n = g.n_views * g.n_faces;
     hipLaunchKernelGGL(k_count<HardRec>, dim3(div_up(n, 256)), dim3(256), 0, s, g, recs, b);
@@ -241,85 +227,103 @@ int launch_raster_hard(hipStream_t s, const RasterGeom& g, const HardRec* recs,
 // Per-op soft rasterizer (RasterizeSoft)
 // ---------------------------------------------------------------------------
 
+// Fill kernel for counters (graph-capture safe, unlike a memset node).
+__global__ void k_fill_u32(uint32_t* p, uint32_t n, uint32_t v) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        p[i] = v;
+    }
+}
+
 // One thread per face: soft corners via faces_soft, face id from the last
-// soft corner, hard corners via faces_tex[hard face] (cpu_raster.cpp:257-303).
+// soft corner, hard corners via faces_tex[hard face] (cpu_raster.cpp:257-303);
+// the face is appended to the fixed-capacity bins of the tiles its soft
+// pixel bbox touches.
 __global__ __launch_bounds__(256) void k_soft_setup_op(RasterGeom g, const float4* soft_clip,
                                                         const float* face_id,
                                                         const float* faces_soft,
                                                         const float4* hard_clip,
                                                         uint32_t n_verts,
-                                                        const float* faces_tex,
+                                                        const float* faces_tex, BinBuffers b,
                                                         uint32_t* err, SoftRec* recs) {
+    __shared__ BinLds blds;
     const uint32_t f = blockIdx.x * blockDim.x + threadIdx.x;
-    if (f >= g.n_faces) {
-        return;
-    }
     SoftRec r;
     r.bx0 = 1;
     r.bx1 = 0;
     r.by0 = 1;
     r.by1 = 0;
-    float4 sc[3], hc[3];
-    float fid = 0.f;
-    const uint32_t n_soft = 3 * g.n_faces;
-    for (int k = 0; k < 3; k++) {
-        const uint32_t vi = (uint32_t)(int64_t)faces_soft[(size_t)f * 3 + k];
-        if (vi >= n_soft) {
-            atomicOr(err, 1u);
-            recs[f] = r;
-            return;
+    r.flags = 0;
+    if (f < g.n_faces) {
+        float4 sc[3], hc[3];
+        float fid = 0.f;
+        bool ok = true;
+        const uint32_t n_soft = 3 * g.n_faces;
+        for (int k = 0; k < 3 && ok; k++) {
+            const uint32_t vi = (uint32_t)(int64_t)faces_soft[(size_t)f * 3 + k];
+            if (vi >= n_soft) {
+                atomicOr(err, 1u);
+                ok = false;
+                break;
+            }
+            sc[k] = soft_clip[vi];
+            if (!clip_w_valid(sc[k].w)) {
+                ok = false;  // the reference skips the face at the first bad corner
+                break;
+            }
+            fid = face_id[vi];
         }
-        sc[k] = soft_clip[vi];
-        if (!clip_w_valid(sc[k].w)) {
-            recs[f] = r;  // the reference skips the face at the first bad corner
-            return;
+        const uint32_t hf = ok ? fid_u(fid) : 0u;
+        if (ok && hf >= g.n_faces) {
+            atomicOr(err, 2u);
+            ok = false;
         }
-        fid = face_id[vi];
-    }
-    const uint32_t hf = fid_u(fid);
-    if (hf >= g.n_faces) {
-        atomicOr(err, 2u);
+        for (int k = 0; k < 3 && ok; k++) {
+            const uint32_t vi = fid_u(faces_tex[(size_t)hf * 3 + k]);
+            if (vi >= n_verts) {
+                atomicOr(err, 4u);
+                ok = false;
+                break;
+            }
+            hc[k] = hard_clip[vi];
+        }
+        if (ok) {
+            soft_setup(sc, hc, fid, g.width, g.height, &r);
+        }
         recs[f] = r;
-        return;
     }
-    for (int k = 0; k < 3; k++) {
-        const uint32_t vi = fid_u(faces_tex[(size_t)hf * 3 + k]);
-        if (vi >= n_verts) {
-            atomicOr(err, 4u);
-            recs[f] = r;
-            return;
-        }
-        hc[k] = hard_clip[vi];
-    }
-    soft_setup(sc, hc, fid, g.width, g.height, &r);
-    recs[f] = r;
+    const bool valid = f < g.n_faces && r.bx0 <= r.bx1 && r.by0 <= r.by1;
+    bin_append(b, g, valid, 0u, f, r.bx0, r.by0, r.bx1, r.by1, blds);
 }
 
+// One workgroup per 16x16 tile: resolves the winner, then re-evaluates its
+// signed distance and hard z (the output channels) from its record.
 __global__ __launch_bounds__(kTileThreads) void k_raster_soft_op(RasterGeom g,
                                                                  const SoftRec* recs,
                                                                  BinBuffers b, float radius,
                                                                  const float* prev,
                                                                  float4* out) {
-    __shared__ SoftRec lds_rec[kTileThreads];
-    __shared__ uint32_t lds_face[kTileThreads];
+    __shared__ TileLds lds;
     const uint32_t tile = blockIdx.x;
-    const int px = (int)((tile % g.tiles_x) * kTile + (threadIdx.x % kTile));
-    const int py = (int)((tile / g.tiles_x) * kTile + (threadIdx.x / kTile));
-    uint64_t best = kEmptyKey;
-    float bd = 0.f, bhz = 0.f, bfid = 0.f;
-    walk_bin(recs, b, tile, g.n_faces, lds_rec, lds_face, [&](const SoftRec& r, uint32_t f) {
-        const uint64_t before = best;
-        soft_fragment(r, f, px, py, radius, prev, g.width, &best, &bd, &bhz);
-        if (best != before) {
-            bfid = r.fid;
-        }
-    });
+    const uint32_t tx = tile % g.tiles_x, ty = tile / g.tiles_x;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int px = (int)tx * kTile + (wave & 1) * 8 + (lane & 7);
+    const int py = (int)ty * kTile + (wave >> 1) * 8 + (lane >> 3);
+    const BinView bv = bin_view(b, tile, g.n_faces);
+    const PixelBest best = resolve_tile(recs, bv, tx, ty, radius, prev, g.width, lds);
     if (px >= (int)g.width || py >= (int)g.height) {
         return;
     }
-    const size_t o = (size_t)py * g.width + px;
-    out[o] = best == kEmptyKey ? make_float4(0.f, 0.f, 0.f, 0.f)
-                               : make_float4(bd, bfid, bhz, 1.f);
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (best.key != kEmptyKey) {
+        const SoftRec& r = recs[key_face(best.key)];
+        const float p0 = (float)px + 0.5f;
+        const float p1 = (float)py + 0.5f;
+        const float dist = signed_dist(p0, p1, r.hx, r.hy, r.ex, r.ey, r.len2);
+        o = make_float4(dist, r.fid, hard_z_at(r, p0, p1), 1.f);
+    }
+    out[(size_t)py * g.width + px] = o;
 }
 
 __global__ void k_soft_clip(const float4* clip, uint32_t n_verts, const float* faces,
@@ -399,24 +403,20 @@ int dressi_rasterize_soft(dressi_ctx* ctx, const float* soft_clip, const float* 
     DRESSI_REQUIRE(radius_px > 0.f, "RasterizeSoft: radius_px must be > 0");
     DRESSI_REQUIRE(width > 0 && height > 0, "RasterizeSoft: empty screen");
     const RasterGeom g = make_geom(width, height, 1, n_faces);
-    const uint32_t cap = default_bin_cap(g, 8);
     void *recs = nullptr, *bins = nullptr;
     if (int rc = ctx_workspace(ctx, 0, sizeof(SoftRec) * (size_t)(n_faces ? n_faces : 1), &recs)) return rc;
-    if (int rc = ctx_workspace(ctx, 1, bin_bytes(g.n_tiles, cap), &bins)) return rc;
+    if (int rc = ctx_workspace(ctx, 1, fixed_bin_bytes(g.n_tiles, kSoftBinCap), &bins)) return rc;
     BinBuffers b;
-    bin_carve(bins, g.n_tiles, cap, &b);
-    DRESSI_TRY_HIP(hipMemsetAsync(b.counts, 0, sizeof(uint32_t) * g.n_tiles, ctx->stream));
+    fixed_bin_carve(bins, g.n_tiles, kSoftBinCap, &b);
+    hipLaunchKernelGGL(k_fill_u32, dim3(div_up(g.n_tiles, 256)), dim3(256), 0, ctx->stream,
+                       b.counts, g.n_tiles, 0u);
+    DRESSI_CHECK_LAUNCH();
     if (n_faces) {
         hipLaunchKernelGGL(k_soft_setup_op, dim3(div_up(n_faces, 256)), dim3(256), 0,
                            ctx->stream, g, (const float4*)soft_clip, face_id, faces_soft,
-                           (const float4*)hard_clip, n_verts, faces_tex, ctx->d_err,
+                           (const float4*)hard_clip, n_verts, faces_tex, b, ctx->d_err,
                            (SoftRec*)recs);
         DRESSI_CHECK_LAUNCH();
-        if (int rc = launch_count_soft(ctx->stream, g, (const SoftRec*)recs, b)) return rc;
-    }
-    if (int rc = launch_scan_bins(ctx->stream, b)) return rc;
-    if (n_faces) {
-        if (int rc = launch_bin_soft(ctx->stream, g, (const SoftRec*)recs, b)) return rc;
     }
     hipLaunchKernelGGL(k_raster_soft_op, dim3(g.n_tiles), dim3(kTileThreads), 0, ctx->stream, g,
                        (const SoftRec*)recs, b, radius_px, prev_shifted_depth, (float4*)out);

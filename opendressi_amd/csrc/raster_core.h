@@ -1,22 +1,48 @@
-// raster_core.h -- device side of the tile-binned rasterizer.
+// raster_core.h -- device side of the tile-binned soft rasterizer.
 //
-// The reference rasterizes face by face over each face's pixel bbox and
-// keeps, per pixel, the fragment of minimum depth with later faces winning
-// ties (src/core/cpu_raster.cpp:31-110, 241-355). Here every 16x16 tile is
-// one workgroup: the faces binned to the tile are staged through LDS in
-// chunks of 256 setup records and each lane (one pixel) folds the fragments
-// it covers into a 64-bit (depth | ~face) key. The min over keys is
-// order-independent, so the atomically filled, unordered tile lists still
-// give the reference's deterministic winner.
+// Reference semantics (src/core/cpu_raster.cpp:241-355): faces are rasterised
+// one after another over their soft pixel bbox; a fragment passes when the
+// pixel centre is inside the soft triangle (inclusive barycentrics) with soft
+// z in [0,1]; its depth is the Eq.3 shift of the signed distance to the hard
+// triangle (0.5 * clamp(hard_z) when dist >= 0, else
+// 0.5 + 0.5 * min(-dist / r, 1)); the minimum depth wins, later faces win ties.
+//
+// Here one 256-lane workgroup owns a 16x16 tile of one view, each wave an 8x8
+// block. The faces binned to the tile are staged through LDS; every lane
+// folds the fragments of its pixel into a 64-bit (depth | ~face) key, whose
+// minimum is the reference's winner independent of processing order. The
+// work is split so that, exactly:
+//  * phase A folds hard-branch fragments (pixel inside the hard triangle:
+//    depth <= 0.5, no distance needed) and any fragment close enough to a
+//    hard edge that the classification needs the full reference evaluation;
+//  * phase B folds every other (rim) fragment, but only for lanes whose best
+//    depth after phase A is >= 0.5 -- rim depths are >= 0.5, so elsewhere
+//    they cannot win. Faces whose hard triangle lies more than r + 1 px from
+//    the wave's block contribute depth exactly 1.0 there (-dist/r > 1), so
+//    only their coverage is tested.
+// Each wave culls the staged records against its block in parallel (one
+// record per lane, ballot-compacted) before the per-pixel loops.
 #pragma once
 
 #include "internal.h"
 
 namespace dressi {
 
+// The smallest |edge function| that can still belong to a pixel centre lying
+// exactly on the edge segment (signed distance -0.0 with a negative winding
+// test, which the reference puts in the hard branch): with p == q = a + t e
+// computed in float, |e x (p - a)| <= u (2|ex||ey| + 4|ex|(|py|+|ay|) +
+// 4|ey|(|px|+|ax|)) + O(u^2), u = 2^-24. 2^-20 (...) bounds it with a wide
+// margin. Fragments below the bound take the full reference evaluation.
+__device__ __forceinline__ float boundary_eps(float ex, float ey, float ax, float ay, float px,
+                                              float py) {
+    return 0x1p-20f * (fabsf(ex) * fabsf(ey) + fabsf(ex) * (fabsf(py) + fabsf(ay)) +
+                       fabsf(ey) * (fabsf(px) + fabsf(ax)));
+}
+
 // Soft raster setup of one face (src/core/cpu_raster.cpp:257-303 for the
-// soft/hard projections, cpu_raster.cpp:177-193 for the barycentric
-// constants). `sc` = soft corner clips, `hc` = hard corner clips.
+// soft/hard projections, :177-193 for the barycentric constants).
+// `sc` = soft corner clips, `hc` = hard corner clips.
 __device__ __forceinline__ void soft_setup(const float4 sc[3], const float4 hc[3], float fid,
                                            uint32_t w, uint32_t h, SoftRec* r) {
     r->bx0 = 1;
@@ -52,8 +78,8 @@ __device__ __forceinline__ void soft_setup(const float4 sc[3], const float4 hc[3
     }
     r->s_inv_area = 1.f / s_area;
     const float h_area = tri_area(hx[0], hy[0], hx[1], hy[1], hx[2], hy[2]);
-    r->h_area_ok = fabsf(h_area) < kDistEps ? 0 : 1;
-    r->h_inv_area = r->h_area_ok ? 1.f / h_area : 0.f;
+    const bool area_ok = !(fabsf(h_area) < kDistEps);
+    r->h_inv_area = area_ok ? 1.f / h_area : 0.f;
     for (int k = 0; k < 3; k++) {
         r->sx[k] = sx[k];
         r->sy[k] = sy[k];
@@ -66,49 +92,309 @@ __device__ __forceinline__ void soft_setup(const float4 sc[3], const float4 hc[3
         r->ex[k] = ht.ex[k];
         r->ey[k] = ht.ey[k];
         r->len2[k] = ht.len2[k];
+        // affine form of the edge function, cr = ex*py - ey*px + cc, used
+        // only as a filter: |fma form - reference form| stays below
+        // 2^-21 (|ex|(|py|+|ay|) + |ey|(|px|+|ax|)) on screen coordinates
+        r->cc[k] = ht.ey[k] * ht.ax[k] - ht.ex[k] * ht.ay[k];
+        // filter threshold: boundary_eps + that error, with the screen size
+        // bounding |px|, |py| (positive for every finite edge)
+        r->thr[k] = 0x1p-19f * (fabsf(ht.ex[k]) * fabsf(ht.ey[k]) +
+                                fabsf(ht.ex[k]) * (H + 1.f + fabsf(ht.ay[k])) +
+                                fabsf(ht.ey[k]) * (W + 1.f + fabsf(ht.ax[k])));
     }
+    // thr[k] also bounds the rounding error of the reference's edge function
+    // (8x margin), so a pixel centre its winding test puts inside has exact
+    // barycentrics >= -m, m = max thr / |2 area|, and lies within the hard
+    // bbox widened by 2 m max(bbox w, h). Unless that is < 0.51 px (|2 area|
+    // > 4 thr w; the 4 also absorbs the rounding of h_area) the face is a
+    // sliver and the resolver may not cull it by its hard bbox.
+    const float thr_max = smax(smax(r->thr[0], r->thr[1]), r->thr[2]);
+    const float wmax = smax(smax(smax(hx[0], hx[1]), hx[2]) - smin(smin(hx[0], hx[1]), hx[2]),
+                            smax(smax(hy[0], hy[1]), hy[2]) - smin(smin(hy[0], hy[1]), hy[2]));
+    const bool sliver = !(fabsf(h_area) > 4.f * thr_max * wmax) || !(fabsf(h_area) < INFINITY);
+    r->flags = (area_ok ? kRecHardArea : 0u) | (sliver ? kRecSliver : 0u);
     pixel_bbox(sx[0], sx[1], sx[2], sy[0], sy[1], sy[2], (int)w, (int)h, &r->bx0, &r->by0,
                &r->bx1, &r->by1);
 }
 
-// One soft fragment (cpu_raster.cpp:307-351). Folds into (best, dist, hz).
-__device__ __forceinline__ void soft_fragment(const SoftRec& r, uint32_t f, int px, int py,
-                                              float radius, const float* prev_depth,
-                                              uint32_t width, uint64_t* best,
-                                              float* best_dist, float* best_hz) {
-    if (px < r.bx0 || px > r.bx1 || py < r.by0 || py > r.by1) {
-        return;
+// Result of one pixel's fold: key + whether the winner is a hard-branch
+// fragment (signed distance >= 0).
+struct PixelBest {
+    uint64_t key;
+    bool hard;
+};
+
+__device__ __forceinline__ void fold(PixelBest& b, float depth, uint32_t f, bool hard) {
+    const uint64_t key = depth_key(depth, f);
+    if (key < b.key) {
+        b.key = key;
+        b.hard = hard;
     }
-    const float p0 = (float)px + 0.5f;
-    const float p1 = (float)py + 0.5f;
+}
+
+// Exact soft-coverage test of the reference (barycentrics >= 0, soft z in
+// [0,1]); the pixel bbox test is done by the caller.
+__device__ __forceinline__ bool soft_covers(const SoftRec& r, float p0, float p1) {
     float l0, l1, l2;
-    barycentric(p0, p1, r.sx[0], r.sy[0], r.sx[1], r.sy[1], r.sx[2], r.sy[2], r.s_inv_area,
-                &l0, &l1, &l2);
+    barycentric(p0, p1, r.sx[0], r.sy[0], r.sx[1], r.sy[1], r.sx[2], r.sy[2], r.s_inv_area, &l0,
+                &l1, &l2);
     if (l0 < 0.f || l1 < 0.f || l2 < 0.f) {
-        return;
+        return false;
     }
     const float soft_z = l0 * r.sz[0] + l1 * r.sz[1] + l2 * r.sz[2];
-    if (soft_z < 0.f || soft_z > 1.f) {
-        return;
-    }
-    const float dist = signed_dist(p0, p1, r.hx, r.hy, r.ex, r.ey, r.len2);
+    return !(soft_z < 0.f || soft_z > 1.f);
+}
+
+__device__ __forceinline__ float hard_z_at(const SoftRec& r, float p0, float p1) {
     float hard_z = 0.5f;
-    if (r.h_area_ok) {
+    if (r.flags & kRecHardArea) {
         float h0, h1, h2;
         barycentric(p0, p1, r.hx[0], r.hy[0], r.hx[1], r.hy[1], r.hx[2], r.hy[2], r.h_inv_area,
                     &h0, &h1, &h2);
         hard_z = h0 * r.hz[0] + h1 * r.hz[1] + h2 * r.hz[2];
     }
-    const float depth = eq3_depth(dist, hard_z, radius);
-    if (prev_depth && depth <= prev_depth[(size_t)py * width + px] + 1e-4f) {
+    return hard_z;
+}
+
+// Fragment class w.r.t. the hard triangle: 0 = hard branch (all edge
+// functions share a sign; dist >= 0), 1 = rim (mixed signs, every edge
+// function clear of the boundary bound: dist < 0), 2 = needs the full
+// reference evaluation (near an edge).
+__device__ __forceinline__ int frag_class(const SoftRec& r, float p0, float p1) {
+    float e[3];
+    bool pos = true, neg = true, clear = true;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        e[k] = fmaf(r.ex[k], p1, fmaf(-r.ey[k], p0, r.cc[k]));
+        const bool big = fabsf(e[k]) > r.thr[k];
+        clear = clear && big;
+        pos = pos && e[k] > 0.f;
+        neg = neg && e[k] < 0.f;
+    }
+    if (clear) {
+        return (pos || neg) ? 0 : 1;
+    }
+    // exact reference crosses (cpu_raster.cpp:141-144) and boundary test
+    int n_pos = 0, n_neg = 0;
+    bool near = false;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        const float cr = r.ex[k] * (p1 - r.hy[k]) - r.ey[k] * (p0 - r.hx[k]);
+        n_pos += (cr >= 0.f);
+        n_neg += (cr <= 0.f);
+        near = near || fabsf(cr) <= boundary_eps(r.ex[k], r.ey[k], r.hx[k], r.hy[k], p0, p1);
+    }
+    if (n_pos == 3 || n_neg == 3) {
+        return 0;
+    }
+    return near ? 2 : 1;
+}
+
+// Phase A fragment: hard branch and full-evaluation fragments.
+__device__ __forceinline__ void frag_phase_a(const SoftRec& r, uint32_t f, int px, int py,
+                                             float radius, const float* prev, uint32_t width,
+                                             PixelBest& b) {
+    if (px < r.bx0 || px > r.bx1 || py < r.by0 || py > r.by1) {
         return;
     }
-    const uint64_t key = depth_key(depth, f);
-    if (key < *best) {
-        *best = key;
-        *best_dist = dist;
-        *best_hz = hard_z;
+    const float p0 = (float)px + 0.5f;
+    const float p1 = (float)py + 0.5f;
+    const int cls = frag_class(r, p0, p1);
+    if (cls == 1) {
+        return;
     }
+    if (!soft_covers(r, p0, p1)) {
+        return;
+    }
+    float depth;
+    bool hard;
+    if (cls == 0) {
+        depth = 0.5f * smin(smax(hard_z_at(r, p0, p1), 0.f), 1.f);
+        hard = true;
+    } else {
+        const float dist = signed_dist(p0, p1, r.hx, r.hy, r.ex, r.ey, r.len2);
+        depth = eq3_depth(dist, hard_z_at(r, p0, p1), radius);
+        hard = dist >= 0.f;
+    }
+    if (prev && depth <= prev[(size_t)py * width + px] + 1e-4f) {
+        return;
+    }
+    fold(b, depth, f, hard);
+}
+
+// Phase B fragment (lanes whose best depth is >= 0.5): every fragment phase
+// A did not fold. `in_a`: the face passed phase A's cull for this block (its
+// class 0 / 2 fragments were folded there). `near`: the face's hard triangle
+// is within r + 1 px of the wave's block; otherwise every covered pixel of
+// the block is more than r + 1 px from it and its depth is exactly 1.0.
+__device__ __forceinline__ void frag_phase_b(const SoftRec& r, uint32_t f, int px, int py,
+                                             float radius, const float* prev, uint32_t width,
+                                             bool near, bool in_a, PixelBest& b) {
+    if (px < r.bx0 || px > r.bx1 || py < r.by0 || py > r.by1) {
+        return;
+    }
+    const float p0 = (float)px + 0.5f;
+    const float p1 = (float)py + 0.5f;
+    float depth;
+    bool hard = false;
+    if (near) {
+        if (in_a && frag_class(r, p0, p1) != 1) {
+            return;  // folded in phase A
+        }
+        if (!soft_covers(r, p0, p1)) {
+            return;
+        }
+        const float dist = signed_dist(p0, p1, r.hx, r.hy, r.ex, r.ey, r.len2);
+        hard = dist >= 0.f;
+        depth = eq3_depth(dist, hard ? hard_z_at(r, p0, p1) : 0.5f, radius);
+    } else {
+        if (depth_key(1.f, f) >= b.key) {
+            return;  // cannot beat the current winner
+        }
+        if (!soft_covers(r, p0, p1)) {
+            return;
+        }
+        depth = 1.f;
+    }
+    if (prev && depth <= prev[(size_t)py * width + px] + 1e-4f) {
+        return;
+    }
+    fold(b, depth, f, hard);
+}
+
+// Per-tile LDS of the resolver
+struct TileLds {
+    SoftRec rec[kTileThreads];
+    uint32_t face[kTileThreads];
+    uint16_t surv[4][kTileThreads];
+};
+
+// Number of list entries of a bin and whether it overflowed (then every face
+// of the view is walked; each face's own bbox keeps the result exact).
+struct BinView {
+    const uint32_t* list;
+    uint32_t n;
+    bool implicit;
+};
+
+__device__ __forceinline__ BinView bin_view(const BinBuffers& b, uint32_t bin, uint32_t n_faces) {
+    BinView v;
+    const uint32_t cnt = b.counts[bin];
+    v.implicit = cnt > b.cap;
+    v.n = v.implicit ? n_faces : cnt;
+    v.list = b.list + (size_t)bin * b.cap;
+    return v;
+}
+
+// The record's hard-triangle bbox widened by `d` px overlaps the pixel-centre
+// rectangle [cx0, cx1] x [cy0, cy1] (always true for slivers).
+__device__ __forceinline__ bool hard_bbox_near(const SoftRec& r, float cx0, float cx1, float cy0,
+                                               float cy1, float d) {
+    if (r.flags & kRecSliver) {
+        return true;
+    }
+    const float mnx = smin(smin(r.hx[0], r.hx[1]), r.hx[2]);
+    const float mxx = smax(smax(r.hx[0], r.hx[1]), r.hx[2]);
+    const float mny = smin(smin(r.hy[0], r.hy[1]), r.hy[2]);
+    const float mxy = smax(smax(r.hy[0], r.hy[1]), r.hy[2]);
+    return !(cx0 > mxx + d || cx1 < mnx - d || cy0 > mxy + d || cy1 < mny - d);
+}
+
+// Resolves the winner of every pixel of one (view, tile). All lanes of the
+// workgroup must call it (it synchronises). `recs` points at the view's
+// records. Pixels off screen fold nothing (their bbox tests fail).
+__device__ __forceinline__ PixelBest resolve_tile(const SoftRec* recs, const BinView& bv,
+                                                  uint32_t tile_x, uint32_t tile_y, float radius,
+                                                  const float* prev, uint32_t width,
+                                                  TileLds& lds) {
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int bx = (int)tile_x * kTile + (wave & 1) * 8;
+    const int by = (int)tile_y * kTile + (wave >> 1) * 8;
+    const int px = bx + (lane & 7);
+    const int py = by + (lane >> 3);
+    // pixel-centre rectangle of the wave's block
+    const float cx0 = (float)bx + 0.5f, cx1 = (float)bx + 7.5f;
+    const float cy0 = (float)by + 0.5f, cy1 = (float)by + 7.5f;
+    const float near_d = radius + 1.f;
+    PixelBest best;
+    best.key = kEmptyKey;
+    best.hard = false;
+    const uint32_t half = 0x3f000000u;  // bits of 0.5f
+    for (int phase = 0; phase < 2; phase++) {
+        if (phase == 1) {
+            const bool need = (uint32_t)(best.key >> 32) >= half;
+            if (!__syncthreads_or(need)) {
+                break;
+            }
+        }
+        const bool wave_need =
+                phase == 0 || __any((uint32_t)(best.key >> 32) >= half);
+        for (uint32_t base = 0; base < bv.n; base += kTileThreads) {
+            const uint32_t cnt = (bv.n - base) < (uint32_t)kTileThreads ? (bv.n - base)
+                                                                          : kTileThreads;
+            // reuse the staged chunk when the list fits one chunk
+            if (!(phase == 1 && bv.n <= (uint32_t)kTileThreads)) {
+                __syncthreads();
+                if (threadIdx.x < cnt) {
+                    const uint32_t f = bv.implicit ? base + threadIdx.x : bv.list[base + threadIdx.x];
+                    lds.face[threadIdx.x] = f;
+                    lds.rec[threadIdx.x] = recs[f];
+                }
+                __syncthreads();
+            }
+            if (!wave_need) {
+                continue;
+            }
+            // wave-parallel cull against the 8x8 block
+            uint32_t n_surv = 0;
+            for (uint32_t j0 = 0; j0 < cnt; j0 += 64) {
+                const uint32_t j = j0 + lane;
+                bool keep = false;
+                if (j < cnt) {
+                    const SoftRec& r = lds.rec[j];
+                    if (r.bx0 <= bx + 7 && r.bx1 >= bx && r.by0 <= by + 7 && r.by1 >= by) {
+                        if (phase == 0) {
+                            // hard-branch fragments lie within the hard
+                            // triangle's bbox (+1 px slack)
+                            keep = hard_bbox_near(r, cx0, cx1, cy0, cy1, 1.f);
+                        } else {
+                            keep = true;
+                        }
+                    }
+                }
+                const uint64_t m = __ballot(keep);
+                if (keep) {
+                    const uint32_t rank = __popcll(m & ((1ull << lane) - 1ull));
+                    lds.surv[wave][n_surv + rank] = (uint16_t)j;
+                }
+                n_surv += __popcll(m);
+            }
+            // the survivor list is written and read by this wave only
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (phase == 0) {
+                for (uint32_t s = 0; s < n_surv; s++) {
+                    const uint32_t j = lds.surv[wave][s];
+                    frag_phase_a(lds.rec[j], lds.face[j], px, py, radius, prev, width, best);
+                }
+            } else {
+                const bool lane_need = (uint32_t)(best.key >> 32) >= half;
+                for (uint32_t s = 0; s < n_surv; s++) {
+                    const uint32_t j = lds.surv[wave][s];
+                    const SoftRec& r = lds.rec[j];
+                    const bool in_a = hard_bbox_near(r, cx0, cx1, cy0, cy1, 1.f);
+                    const bool near = hard_bbox_near(r, cx0, cx1, cy0, cy1, near_d);
+                    if (lane_need) {
+                        frag_phase_b(r, lds.face[j], px, py, radius, prev, width, near, in_a,
+                                     best);
+                    }
+                }
+            }
+        }
+    }
+    return best;
 }
 
 // Hard raster setup (RasterizeCore, cpu_raster.cpp:42-94).
@@ -165,10 +451,10 @@ __device__ __forceinline__ void hard_fragment(const HardRec& r, uint32_t f, int 
     }
 }
 
-// Walks the faces binned to one (view, tile): chunks of up to 256 records are
-// staged through LDS and every lane folds each record via `frag(rec, f)`.
-// When the bin's list overflowed the capacity the walk covers all faces
-// (each face's own bbox test keeps the result exact).
+// Walks the faces binned to one (view, tile) of the hard rasterizer (scan
+// based bins): chunks of up to 256 records are staged through LDS and every
+// lane folds each record via `frag(rec, f)`. When the bin's list overflowed
+// the capacity the walk covers all faces.
 template <typename Rec, typename Frag>
 __device__ __forceinline__ void walk_bin(const Rec* recs, const BinBuffers& b, uint32_t bin,
                                          uint32_t n_faces, Rec* lds_rec, uint32_t* lds_face,
@@ -188,6 +474,90 @@ __device__ __forceinline__ void walk_bin(const Rec* recs, const BinBuffers& b, u
         __syncthreads();
         for (uint32_t j = 0; j < cnt; j++) {
             frag(lds_rec[j], lds_face[j]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fixed-capacity soft bins, appended from the setup kernels. Lanes of one
+// workgroup first count their tiles in an LDS window (one global atomic per
+// touched tile), then write their slots; lanes whose tiles fall outside the
+// window (or workgroups spanning two views) append with direct atomics.
+// All lanes of the workgroup must call it.
+// ---------------------------------------------------------------------------
+constexpr int kBinWin = 32;  // LDS window of 32 x 32 tiles
+
+struct BinLds {
+    uint32_t cnt[kBinWin * kBinWin];
+    uint32_t base[kBinWin * kBinWin];
+    int win[4];  // tx0, ty0, view0, mixed-view flag
+};
+
+__device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom& g, bool valid,
+                                           uint32_t view, uint32_t f, int bx0, int by0, int bx1,
+                                           int by1, BinLds& lds) {
+    const int tx0 = bx0 / kTile, tx1 = bx1 / kTile, ty0 = by0 / kTile, ty1 = by1 / kTile;
+    if (threadIdx.x == 0) {
+        lds.win[0] = 0x7fffffff;
+        lds.win[1] = 0x7fffffff;
+        lds.win[2] = -1;
+        lds.win[3] = 0;
+    }
+    for (int i = threadIdx.x; i < kBinWin * kBinWin; i += blockDim.x) {
+        lds.cnt[i] = 0;
+    }
+    __syncthreads();
+    if (valid) {
+        atomicMin(&lds.win[0], tx0);
+        atomicMin(&lds.win[1], ty0);
+        atomicMax(&lds.win[2], (int)view);
+    }
+    __syncthreads();
+    if (valid && (int)view != lds.win[2]) {
+        lds.win[3] = 1;
+    }
+    __syncthreads();
+    const int wx0 = lds.win[0], wy0 = lds.win[1];
+    const bool mixed = lds.win[3] != 0;
+    const bool local = valid && !mixed && tx1 - wx0 < kBinWin && ty1 - wy0 < kBinWin;
+    if (local) {
+        for (int ty = ty0; ty <= ty1; ty++) {
+            for (int tx = tx0; tx <= tx1; tx++) {
+                atomicAdd(&lds.cnt[(ty - wy0) * kBinWin + (tx - wx0)], 1u);
+            }
+        }
+    } else if (valid) {
+        for (int ty = ty0; ty <= ty1; ty++) {
+            for (int tx = tx0; tx <= tx1; tx++) {
+                const uint32_t bin = view * g.n_tiles + ty * g.tiles_x + tx;
+                const uint32_t slot = atomicAdd(&b.counts[bin], 1u);
+                if (slot < b.cap) {
+                    b.list[(size_t)bin * b.cap + slot] = f;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t view0 = (uint32_t)max(lds.win[2], 0);
+    for (int i = threadIdx.x; i < kBinWin * kBinWin; i += blockDim.x) {
+        const uint32_t c = lds.cnt[i];
+        if (c) {
+            const int tx = wx0 + i % kBinWin, ty = wy0 + i / kBinWin;
+            lds.base[i] = atomicAdd(&b.counts[view0 * g.n_tiles + ty * g.tiles_x + tx], c);
+            lds.cnt[i] = 0;
+        }
+    }
+    __syncthreads();
+    if (local) {
+        for (int ty = ty0; ty <= ty1; ty++) {
+            for (int tx = tx0; tx <= tx1; tx++) {
+                const int li = (ty - wy0) * kBinWin + (tx - wx0);
+                const uint32_t slot = lds.base[li] + atomicAdd(&lds.cnt[li], 1u);
+                if (slot < b.cap) {
+                    const uint32_t bin = view * g.n_tiles + ty * g.tiles_x + tx;
+                    b.list[(size_t)bin * b.cap + slot] = f;
+                }
+            }
         }
     }
 }

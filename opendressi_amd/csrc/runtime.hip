@@ -21,6 +21,17 @@ void set_error(const char* fmt, ...) {
 
 void clear_error() { g_last_error.clear(); }
 
+int ctx_workspace_zeroed(dressi_ctx* ctx, int slot, size_t bytes, void** out) {
+    const bool grow = (int)ctx->ws_ptr.size() <= slot || ctx->ws_size[slot] < bytes;
+    if (int rc = ctx_workspace(ctx, slot, bytes, out)) {
+        return rc;
+    }
+    if (grow) {
+        DRESSI_TRY_HIP(hipMemsetAsync(*out, 0, ctx->ws_size[slot], ctx->stream));
+    }
+    return DRESSI_OK;
+}
+
 int ctx_workspace(dressi_ctx* ctx, int slot, size_t bytes, void** out) {
     if ((int)ctx->ws_ptr.size() <= slot) {
         ctx->ws_ptr.resize(slot + 1, nullptr);

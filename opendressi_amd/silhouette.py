@@ -164,7 +164,7 @@ class SilhouetteFit:
         shapes = {_lib.BUF_LOSS: ((s, s), np.float32), _lib.BUF_PRED: ((n, s, s), np.float32),
                   _lib.BUF_TARGET: ((n, s, s), np.float32),
                   _lib.BUF_FACE_ID: ((n, s, s), np.uint32), _lib.BUF_GRAD: ((v, 3), np.float32),
-                  _lib.BUF_POS: ((v, 3), np.float32), _lib.BUF_CLIP: ((n, v, 4), np.float32)}
+                  _lib.BUF_POS: ((v, 3), np.float32)}
         shape, dt = shapes[which]
         out = np.zeros(shape, dt)
         check(lib.dressi_hsr_read(self.handle, which, out.ctypes.data_as(C.c_void_p), out.nbytes))

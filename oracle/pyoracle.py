@@ -280,5 +280,15 @@ class Reference(_Lib):
         return pos, faces
 
 
+def face_id_buffer(rs):
+    """The fused plan's face-id buffer for RasterizeSoft output `rs` (dist,
+    fid, hard z, coverage): face + 1 where covered, 0 elsewhere, bit 31 set
+    where the winning fragment is a rim fragment (signed distance < 0)."""
+    rs = np.asarray(rs, np.float32)
+    ids = np.where(rs[..., 3] > 0, rs[..., 1] + 1, 0).astype(np.uint32)
+    rim = (rs[..., 3] > 0) & (rs[..., 0] < 0)
+    return ids | np.where(rim, np.uint32(0x80000000), np.uint32(0))
+
+
 def have_reference() -> bool:
     return os.path.exists(REF_SO)

@@ -30,8 +30,10 @@ def rel_err(a, b):
 
 
 def ids_of_rs(rs):
-    """face + 1 where covered, 0 elsewhere, from RasterizeSoft's (dist, fid, z, cov)."""
-    return np.where(rs[..., 3] > 0, rs[..., 1] + 1, 0).astype(np.uint32)
+    """The plan's face-id buffer (face + 1, bit 31 = rim winner) from
+    RasterizeSoft's (dist, fid, z, cov)."""
+    from oracle.pyoracle import face_id_buffer
+    return face_id_buffer(rs)
 
 
 def _fit(ctx, g, keep=True):
