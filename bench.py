@@ -37,11 +37,26 @@ def iteration_bytes(n_views: int, s: int, n_faces: int, n_verts: int) -> float:
     return n_views * (20.0 * s * s + 300.0 * n_faces + 88.0 * n_verts) + 4.0 * s * s + 72.0 * n_verts
 
 
-def raster_bytes(n_views: int, s: int, n_faces: int) -> float:
-    """Compulsory bytes of one launch of the fused raster/forward kernel:
-    target image read + face-id image write per view, the loss image write,
-    and the soft + hard corner clips of every face per view (6 x 16 B)."""
-    return n_views * (8.0 * s * s + 96.0 * n_faces) + 4.0 * s * s
+def kernel_bytes(n_views: int, s: int, n_faces: int, n_verts: int, samples: int = 8) -> dict:
+    """Algorithmic bytes per launch of each kernel of the iteration.
+
+    setup:      positions (12 B/vertex) and faces (12 B/face) in, soft + hard
+                corner clips (96 B/face) out, per view
+    raster:     soft + hard corner clips in, 4-byte face-id image out, per view
+    loss:       face-id + target image in per view, loss image out
+    face_bwd:   corner clips (48 B) in, corner gradients (48 B) out, and a
+                face-id + target read (8 B) per sample, per face and view
+    vertex_adam: adjacency (24 B) + corner gradients (96 B) per vertex and
+                view, Adam pos/m/v read + write (72 B/vertex)
+    """
+    n, S2, F, V = n_views, float(s) * s, float(n_faces), float(n_verts)
+    return {
+        "k_hsr_setup": n * (12.0 * V + 12.0 * F + 96.0 * F),
+        "k_hsr_raster": n * (4.0 * S2 + 96.0 * F),
+        "k_hsr_loss": n * 8.0 * S2 + 4.0 * S2,
+        "k_hsr_face_bwd": n * F * (96.0 + 8.0 * samples),
+        "k_hsr_vertex_adam": n * 120.0 * V + 72.0 * V,
+    }
 
 
 def cpu_info() -> str:
@@ -111,9 +126,10 @@ def main() -> int:
     prof = fit.profile(args.profile_iters)
     dom = max(prof, key=prof.get)
     dom_us = prof[dom]
-    rbytes = raster_bytes(nviews, s, nf)
+    kbytes = kernel_bytes(nviews, s, nf, nv)
+    dbytes = kbytes[dom]
     ibytes = iteration_bytes(nviews, s, nf, nv)
-    achieved = rbytes / (dom_us * 1e-6) if dom == "k_hsr_raster" else None
+    achieved = dbytes / (dom_us * 1e-6)
     fit.close()
 
     line = {
@@ -134,11 +150,11 @@ def main() -> int:
                                 f"Adam lr {w.lr}"),
                    "screen": s, "views": nviews, "verts": nv, "faces": nf},
         "roofline": {"bound": "hbm", "kernel": dom,
-                     "achieved": (achieved / 1e9) if achieved else None,
+                     "achieved": achieved / 1e9,
                      "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": (achieved / HBM_PEAK) if achieved else None,
+                     "frac": achieved / HBM_PEAK,
                      "traffic": None,
-                     "algorithmic_bytes_per_launch": rbytes,
+                     "algorithmic_bytes_per_launch": dbytes,
                      "avg_launch_us": dom_us},
         "iteration_roofline": {"algorithmic_bytes": ibytes,
                                "achieved_GBps": ibytes * its / 1e9,

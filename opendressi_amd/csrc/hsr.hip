@@ -71,7 +71,9 @@ struct HsrDev {
     const float* mvps;        // [N][16]
     const float* targets;     // [N][S][S]
     SoftRec* recs;            // [N][F]
-    BinBuffers bins;          // fixed-capacity soft bins, N x tiles
+    CullRec* cull;            // [N][F]
+    BinBuffers bins;          // fixed-capacity soft bins, N x tiles; the
+                              // face backward clears the counters
     uint32_t* ids;            // [N][S][S] face + 1 (bit 31: rim winner), 0 bg
     float* loss;              // [S][S]
     float* pred;              // [N][S][S] or null
@@ -82,8 +84,6 @@ struct HsrDev {
     // F::Pow), so the in-graph Adam matches it bit for bit
     const float2* bc_tab;
     uint32_t bc_len;
-    // profiling only: the raster leaves the bins filled so it can be replayed
-    uint32_t keep_bins;
 };
 
 constexpr uint32_t kBiasTableLen = 1u << 16;
@@ -118,71 +118,82 @@ __global__ __launch_bounds__(256) void k_hsr_setup(HsrDev d) {
         soft_clip_face(hc, d.g.width, d.g.height, d.radius, sc);
         soft_setup(sc, hc, (float)f, d.g.width, d.g.height, &r);
         d.recs[i] = r;
+        d.cull[i] = cull_setup(r);
     }
     const bool valid = live && r.bx0 <= r.bx1 && r.by0 <= r.by1;
     bin_append(d.bins, d.g, valid, view, f, r.bx0, r.by0, r.bx1, r.by1, blds);
 }
 
-// One workgroup per 16x16 tile, all views: resolve the RasterizeSoft winner
-// of every view, write the face-id buffer, evaluate pred and the loss image
-// (SumPixelWise over views), and clear the tile's bin counters.
-template <int NV>
-__global__ __launch_bounds__(kTileThreads) void k_hsr_raster(HsrDev d) {
-    __shared__ TileLds lds;
-    const uint32_t tile = blockIdx.x;
-    const uint32_t tx = tile % d.g.tiles_x, ty = tile / d.g.tiles_x;
-    const int wave = threadIdx.x >> 6;
+// Visibility: one single-wave workgroup per (view, 8x8 block) resolves the
+// RasterizeSoft winner of every pixel and writes the face-id buffer (face +
+// 1, bit 31 for rim winners, 0 for background). Workgroup w runs on XCD
+// w % 8: tiles are dealt to the XCDs round robin (neighbouring tiles, and so
+// the costly silhouette bands, spread over all of them), and the four
+// blocks of a tile of a view are consecutive on one XCD.
+__global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
+    const uint32_t per = (d.g.n_tiles + 7u) / 8u;
+    const uint32_t k = blockIdx.x >> 3;
+    const uint32_t q = k & 3u;
+    const uint32_t view = (k >> 2) % d.g.n_views;
+    const uint32_t lt = (k >> 2) / d.g.n_views;
+    const uint32_t tile = lt * 8u + (blockIdx.x & 7u);
+    const int bx = (int)((tile % d.g.tiles_x) * kTile + (q & 1u) * 8u);
+    const int by = (int)((tile / d.g.tiles_x) * kTile + (q >> 1) * 8u);
+    if (lt >= per || tile >= d.g.n_tiles || bx >= (int)d.g.width || by >= (int)d.g.height) {
+        return;
+    }
     const int lane = threadIdx.x & 63;
-    const int px = (int)tx * kTile + (wave & 1) * 8 + (lane & 7);
-    const int py = (int)ty * kTile + (wave >> 1) * 8 + (lane >> 3);
-    const bool on = px < (int)d.g.width && py < (int)d.g.height;
+    const int px = bx + (lane & 7);
+    const int py = by + (lane >> 3);
+    const size_t vf = (size_t)view * d.g.n_faces;
+    const BinView bv = bin_view(d.bins, view * d.g.n_tiles + tile, d.g.n_faces);
+    const PixelBest best = resolve_block(d.recs + vf, d.cull + vf, bv, bx, by, d.radius, nullptr,
+                                         d.g.width);
+    if (px < (int)d.g.width && py < (int)d.g.height) {
+        uint32_t id = 0;
+        if (best.key != kEmptyKey) {
+            id = (key_face(best.key) + 1) | (best.hard ? 0u : kRimFlag);
+        }
+        d.ids[(size_t)view * d.g.width * d.g.height + (size_t)py * d.g.width + px] = id;
+    }
+}
+
+// Forward tail per pixel: pred of every view from its face-id entry
+// (background 0; a hard-branch winner gives cov * step(0, dist) = 1 >= the
+// soft silhouette, so max(hard, soft) = 1; a rim winner evaluates the pixel
+// chain), the L2 loss per view and their SumPixelWise over views.
+template <int NV>
+__global__ __launch_bounds__(256) void k_hsr_loss(HsrDev d) {
+    const uint32_t x = blockIdx.x * 64 + (threadIdx.x & 63);
+    const uint32_t y = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (x >= d.g.width || y >= d.g.height) {
+        return;
+    }
     const size_t npx = (size_t)d.g.width * d.g.height;
-    const size_t o = (size_t)py * d.g.width + px;
+    const size_t o = (size_t)y * d.g.width + x;
     const float W = (float)d.g.width, H = (float)d.g.height;
     float lv[NV][1];
 #pragma unroll
     for (int view = 0; view < NV; view++) {
-        const uint32_t bin = view * d.g.n_tiles + tile;
-        const BinView bv = bin_view(d.bins, bin, d.g.n_faces);
-        const PixelBest best = resolve_tile(d.recs + (size_t)view * d.g.n_faces, bv, tx, ty,
-                                            d.radius, nullptr, d.g.width, lds);
-        float pred = 0.f;
-        uint32_t id = 0;
-        if (on && best.key != kEmptyKey) {
-            const uint32_t f = key_face(best.key);
-            if (best.hard) {
-                // cov * step(0, dist) = 1 and soft_sil <= 1: max(1, soft_sil) = 1
-                pred = 1.f;
-                id = f + 1;
-            } else {
-                float4 c[3];
-                face_clips(d, view, f, c);
-                PixelFw st;
-                pixel_fw(c, 1.f, -1.f, 1.f, (float)px + 0.5f, (float)py + 0.5f, W, H,
-                         d.sigma_scale, st);
-                pred = st.pred;
-                id = (f + 1) | kRimFlag;
-            }
+        const uint32_t id = d.ids[view * npx + o];
+        float pred = id ? 1.f : 0.f;
+        if (id & kRimFlag) {
+            float4 c[3];
+            face_clips(d, view, (id & ~kRimFlag) - 1, c);
+            PixelFw st;
+            pixel_fw(c, 1.f, -1.f, 1.f, (float)x + 0.5f, (float)y + 0.5f, W, H, d.sigma_scale,
+                     st);
+            pred = st.pred;
         }
-        float tgt = 0.f;
-        if (on) {
-            d.ids[view * npx + o] = id;
-            if (d.pred) {
-                d.pred[view * npx + o] = pred;
-            }
-            tgt = d.targets[view * npx + o];
+        if (d.pred) {
+            d.pred[view * npx + o] = pred;
         }
-        const float diff = tgt - pred;
+        const float diff = d.targets[view * npx + o] - pred;
         lv[view][0] = diff * diff * d.inv_px;
-        if (threadIdx.x == 0 && !d.keep_bins) {
-            d.bins.counts[bin] = 0;  // every lane read it before resolve_tile's barriers
-        }
     }
-    if (on) {
-        float out[1];
-        Tree<NV, 1>::run(lv, out);
-        d.loss[o] = out[0];
-    }
+    float out[1];
+    Tree<NV, 1>::run(lv, out);
+    d.loss[o] = out[0];
 }
 
 // FaceFetchBwd (stochastic, n samples, seed = t) fused with the pixel
@@ -192,6 +203,10 @@ __global__ __launch_bounds__(kTileThreads) void k_hsr_raster(HsrDev d) {
 // (pred = max(1, soft) passes no gradient to soft) and are skipped.
 __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    // the raster is done with this iteration's bins: clear their counters
+    for (uint32_t b = i; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
+        d.bins.counts[b] = 0;
+    }
     if (i >= d.g.n_views * d.g.n_faces) {
         return;
     }
@@ -538,10 +553,10 @@ int plan_alloc(dressi_hsr_plan* p, T** out, size_t count) {
     return DRESSI_OK;
 }
 
-// Kernel k of one iteration: 0 setup + binning, 1 raster / forward,
-// 2 face backward, 3 vertex backward + Adam.
-constexpr int kIterKernels = 4;
-const char* const kIterKernelNames[kIterKernels] = {"k_hsr_setup", "k_hsr_raster",
+// Kernel k of one iteration: 0 setup + binning, 1 visibility raster,
+// 2 pred + loss, 3 face backward, 4 vertex backward + Adam.
+constexpr int kIterKernels = 5;
+const char* const kIterKernelNames[kIterKernels] = {"k_hsr_setup", "k_hsr_raster", "k_hsr_loss",
                                                     "k_hsr_face_bwd", "k_hsr_vertex_adam"};
 
 int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
@@ -552,10 +567,14 @@ int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
             hipLaunchKernelGGL(k_hsr_setup, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
             break;
         case 1:
+            hipLaunchKernelGGL(k_hsr_raster, dim3(block_grid(g) * g.n_views), dim3(64), 0, s, d);
+            break;
+        case 2: {
+            const dim3 grid(div_up(g.width, 64), div_up(g.height, 4));
             switch (g.n_views) {
 #define DRESSI_NV(N)                                                                          \
     case N:                                                                                   \
-        hipLaunchKernelGGL(k_hsr_raster<N>, dim3(g.n_tiles), dim3(kTileThreads), 0, s, d);    \
+        hipLaunchKernelGGL(k_hsr_loss<N>, grid, dim3(256), 0, s, d);                          \
         break;
                 DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
                 DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)
@@ -565,7 +584,8 @@ int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
                     return DRESSI_ERR_UNSUPPORTED;
             }
             break;
-        case 2:
+        }
+        case 3:
             hipLaunchKernelGGL(k_hsr_face_bwd, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
             break;
         default:
@@ -652,6 +672,7 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
     rc = rc ? rc : plan_alloc(p, (float**)&d.mvps, N * 16);
     rc = rc ? rc : plan_alloc(p, (float**)&d.targets, N * npx);
     rc = rc ? rc : plan_alloc(p, &d.recs, N * F);
+    rc = rc ? rc : plan_alloc(p, &d.cull, N * F);
     rc = rc ? rc : plan_alloc(p, &d.ids, N * npx);
     rc = rc ? rc : plan_alloc(p, &d.loss, npx);
     rc = rc ? rc : plan_alloc(p, &gtri, N * 3 * F);
@@ -959,56 +980,54 @@ int dressi_hsr_profile(dressi_hsr_plan* p, uint32_t iters, char* names, size_t n
                        float* usec, uint32_t cap, uint32_t* n) {
     if (int rc = ready(p)) return rc;
     DRESSI_REQUIRE(n, "bad arguments");
-    // Average device time per launch of each kernel of the iteration, from
-    // HIP events on the plan stream around `iters` back-to-back launches of
-    // that kernel alone (the setup / raster replays are idempotent: the setup
-    // recomputes the same records, the raster replays keep the bins; the
-    // backward kernels replay one iteration's state). Advances the plan by
-    // one iteration.
+    // Average device time per launch of each kernel of the iteration: after
+    // one eager iteration and one setup, each kernel is launched `iters`
+    // times back to back between two HIP events on the plan stream. The
+    // raster, loss and face backward replays are idempotent; the vertex
+    // kernel advances Adam each time (the optimisation moves iters + 1
+    // steps); the setup replays append to the bins, which a final face
+    // backward clears.
     const uint32_t reps = iters ? iters : 1;
     *n = kIterKernels;
     hipStream_t s = p->ctx->stream;
-    hipEvent_t e0, e1;
-    DRESSI_TRY_HIP(hipEventCreate(&e0));
-    DRESSI_TRY_HIP(hipEventCreate(&e1));
-    HsrDev keep = p->d;
-    keep.keep_bins = 1;
-    float ms[kIterKernels] = {0.f, 0.f, 0.f, 0.f};
+    // timing order: raster, loss, face bwd, vertex, setup
+    const int order[kIterKernels] = {1, 2, 3, 4, 0};
+    hipEvent_t ev[kIterKernels + 1] = {};
     int rc = DRESSI_OK;
-    for (int k = 0; k < kIterKernels && !rc; k++) {
-        if (k == 0) {
-            // one setup fills the bins; replays would append duplicates, so
-            // time them on a copy whose bins are cleared by a raster pass
-            for (uint32_t r = 0; r < reps && !rc; r++) {
-                DRESSI_TRY_HIP(hipEventRecord(e0, s));
-                rc = launch_iter_kernel(p->d, s, 0);
-                DRESSI_TRY_HIP(hipEventRecord(e1, s));
-                DRESSI_TRY_HIP(hipEventSynchronize(e1));
-                float t = 0.f;
-                DRESSI_TRY_HIP(hipEventElapsedTime(&t, e0, e1));
-                ms[0] += t / reps;
-                if (!rc && r + 1 < reps) {
-                    rc = launch_iter_kernel(p->d, s, 1);  // consumes and clears the bins
-                }
-            }
-            continue;
-        }
-        const HsrDev& dk = k == 1 ? keep : p->d;
-        DRESSI_TRY_HIP(hipEventRecord(e0, s));
-        for (uint32_t r = 0; r < (k == 3 ? 1u : reps) && !rc; r++) {
-            rc = launch_iter_kernel(dk, s, k);
-        }
-        DRESSI_TRY_HIP(hipEventRecord(e1, s));
-        DRESSI_TRY_HIP(hipEventSynchronize(e1));
-        DRESSI_TRY_HIP(hipEventElapsedTime(&ms[k], e0, e1));
-        if (k != 3) {
-            ms[k] /= reps;
-        }
-        if (k == 1 && !rc) {
-            rc = launch_iter_kernel(p->d, s, 1);  // the clearing pass
+    for (int i = 0; i <= kIterKernels && !rc; i++) {
+        if (hipEventCreate(&ev[i]) != hipSuccess) {
+            set_error("hipEventCreate failed");
+            rc = DRESSI_ERR_HIP;
         }
     }
-    for (uint32_t k = 0; k < (uint32_t)kIterKernels && k < cap; k++) {
+    if (!rc) rc = enqueue_iteration(p, s);
+    if (!rc) rc = launch_iter_kernel(p->d, s, 0);
+    for (int i = 0; i < kIterKernels && !rc; i++) {
+        if (hipEventRecord(ev[i], s) != hipSuccess) {
+            set_error("hipEventRecord failed");
+            rc = DRESSI_ERR_HIP;
+            break;
+        }
+        for (uint32_t r = 0; r < reps && !rc; r++) {
+            rc = launch_iter_kernel(p->d, s, order[i]);
+        }
+    }
+    if (!rc && hipEventRecord(ev[kIterKernels], s) != hipSuccess) {
+        set_error("hipEventRecord failed");
+        rc = DRESSI_ERR_HIP;
+    }
+    if (!rc) rc = launch_iter_kernel(p->d, s, 3);  // clears the replayed bins
+    if (!rc && hipEventSynchronize(ev[kIterKernels]) != hipSuccess) {
+        set_error("event synchronisation failed");
+        rc = DRESSI_ERR_HIP;
+    }
+    float ms[kIterKernels] = {};
+    for (int i = 0; i < kIterKernels && !rc; i++) {
+        float t = 0.f;
+        hipEventElapsedTime(&t, ev[i], ev[i + 1]);
+        ms[order[i]] = t / reps;
+    }
+    for (uint32_t k = 0; k < (uint32_t)kIterKernels && k < cap && !rc; k++) {
         if (usec) {
             usec[k] = ms[k] * 1000.f;
         }
@@ -1016,8 +1035,14 @@ int dressi_hsr_profile(dressi_hsr_plan* p, uint32_t iters, char* names, size_t n
             snprintf(names + k * name_stride, name_stride, "%s", kIterKernelNames[k]);
         }
     }
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
+    for (hipEvent_t e : ev) {
+        if (e) {
+            hipEventDestroy(e);
+        }
+    }
+    if (!rc) {
+        DRESSI_TRY_HIP(hipStreamSynchronize(s));
+    }
     return rc;
 }
 

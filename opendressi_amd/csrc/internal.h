@@ -74,28 +74,34 @@ constexpr int kTileThreads = kTile * kTile;
 
 // Per (view, face) setup record of the soft rasterizer: soft triangle
 // (coverage), hard triangle (signed distance, edge-function filter, hard z)
-// and the inclusive soft pixel bbox. 41 words, padded to 44 so that it
-// moves with 16-byte loads.
+// and the inclusive soft pixel bbox. 43 words, padded to 44 so that it
+// moves with 16-byte loads; the first 16 words (edge functions, orientation,
+// flags, hard-branch margin) are what the block cull reads per lane.
 struct alignas(16) SoftRec {
-    float sx[3], sy[3];
-    float s_inv_area;
-    float sz[3];
-    float hx[3], hy[3], ex[3], ey[3], len2[3];
+    float ex[3], ey[3];   // hard edges a[k+1] - a[k]
     float cc[3], thr[3];  // edge-function filter: ex*py - ey*px + cc, threshold
-    float hz[3];
-    float h_inv_area;
-    uint32_t flags;          // kRecHardArea | kRecSliver
+    float h_inv_area;     // 1 / (2 x signed hard area), 0 if below 1e-6
+    uint32_t flags;       // kRecHardArea | kRecSliver | kRecPos
+    float s_inv_area;
+    float a_margin;       // hard-branch pixels lie within the hard bbox +- this (px)
+    float hx[3], hy[3], len2[3], hz[3];
+    float sx[3], sy[3], sz[3];
     int bx0, by0, bx1, by1;  // bx0 > bx1: face produces no fragment
+    float s_margin;          // soft coverage margin for the block cull, < 0: none
     float fid;               // face_id value written to the output
 };
 static_assert(sizeof(SoftRec) == 44 * 4, "SoftRec layout");
 // SoftRec::flags: the hard triangle's |area| passes the 1e-6 test (hard z is
 // interpolated, else 0.5) ...
 constexpr uint32_t kRecHardArea = 1u;
-// ... and the hard triangle is too thin for the bbox culls of the resolver
-// (a pixel the reference's winding test calls inside may lie more than 1 px
-// outside its bbox): the face is then evaluated over its whole soft bbox.
+// ... and the hard triangle is thin (the winding test's inside may reach
+// more than 0.51 px beyond its bbox): it takes the general classifier, and
+// its a_margin widens the culls (infinite when no bound holds: the whole
+// soft bbox).
 constexpr uint32_t kRecSliver = 2u;
+// ... and the signed hard area is positive (the orientation that the
+// winding test's "inside" takes for a non-sliver face).
+constexpr uint32_t kRecPos = 4u;
 
 // Per (view, face) setup record of the hard rasterizer (RasterizeCore).
 struct HardRec {

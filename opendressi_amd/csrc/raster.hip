@@ -245,7 +245,8 @@ __global__ __launch_bounds__(256) void k_soft_setup_op(RasterGeom g, const float
                                                         const float4* hard_clip,
                                                         uint32_t n_verts,
                                                         const float* faces_tex, BinBuffers b,
-                                                        uint32_t* err, SoftRec* recs) {
+                                                        uint32_t* err, SoftRec* recs,
+                                                        CullRec* cull) {
     __shared__ BinLds blds;
     const uint32_t f = blockIdx.x * blockDim.x + threadIdx.x;
     SoftRec r;
@@ -291,27 +292,27 @@ __global__ __launch_bounds__(256) void k_soft_setup_op(RasterGeom g, const float
             soft_setup(sc, hc, fid, g.width, g.height, &r);
         }
         recs[f] = r;
+        cull[f] = cull_setup(r);
     }
     const bool valid = f < g.n_faces && r.bx0 <= r.bx1 && r.by0 <= r.by1;
     bin_append(b, g, valid, 0u, f, r.bx0, r.by0, r.bx1, r.by1, blds);
 }
 
-// One workgroup per 16x16 tile: resolves the winner, then re-evaluates its
-// signed distance and hard z (the output channels) from its record.
-__global__ __launch_bounds__(kTileThreads) void k_raster_soft_op(RasterGeom g,
-                                                                 const SoftRec* recs,
-                                                                 BinBuffers b, float radius,
-                                                                 const float* prev,
-                                                                 float4* out) {
-    __shared__ TileLds lds;
-    const uint32_t tile = blockIdx.x;
-    const uint32_t tx = tile % g.tiles_x, ty = tile / g.tiles_x;
-    const int wave = threadIdx.x >> 6;
+// One wave per 8x8 block: resolves the winner, then re-evaluates its signed
+// distance and hard z (the output channels) from its record.
+__global__ __launch_bounds__(64) void k_raster_soft_op(RasterGeom g, const SoftRec* recs,
+                                                       const CullRec* cull, BinBuffers b,
+                                                       float radius, const float* prev,
+                                                       float4* out) {
+    const BlockPos blk = block_pos(blockIdx.x, g);
+    if (!blk.valid) {
+        return;
+    }
     const int lane = threadIdx.x & 63;
-    const int px = (int)tx * kTile + (wave & 1) * 8 + (lane & 7);
-    const int py = (int)ty * kTile + (wave >> 1) * 8 + (lane >> 3);
-    const BinView bv = bin_view(b, tile, g.n_faces);
-    const PixelBest best = resolve_tile(recs, bv, tx, ty, radius, prev, g.width, lds);
+    const int px = blk.bx + (lane & 7);
+    const int py = blk.by + (lane >> 3);
+    const BinView bv = bin_view(b, blk.tile, g.n_faces);
+    const PixelBest best = resolve_block(recs, cull, bv, blk.bx, blk.by, radius, prev, g.width);
     if (px >= (int)g.width || py >= (int)g.height) {
         return;
     }
@@ -403,9 +404,11 @@ int dressi_rasterize_soft(dressi_ctx* ctx, const float* soft_clip, const float* 
     DRESSI_REQUIRE(radius_px > 0.f, "RasterizeSoft: radius_px must be > 0");
     DRESSI_REQUIRE(width > 0 && height > 0, "RasterizeSoft: empty screen");
     const RasterGeom g = make_geom(width, height, 1, n_faces);
-    void *recs = nullptr, *bins = nullptr;
-    if (int rc = ctx_workspace(ctx, 0, sizeof(SoftRec) * (size_t)(n_faces ? n_faces : 1), &recs)) return rc;
+    void *recs = nullptr, *bins = nullptr, *cull = nullptr;
+    const size_t nf1 = n_faces ? n_faces : 1;
+    if (int rc = ctx_workspace(ctx, 0, sizeof(SoftRec) * nf1, &recs)) return rc;
     if (int rc = ctx_workspace(ctx, 1, fixed_bin_bytes(g.n_tiles, kSoftBinCap), &bins)) return rc;
+    if (int rc = ctx_workspace(ctx, 3, sizeof(CullRec) * nf1, &cull)) return rc;
     BinBuffers b;
     fixed_bin_carve(bins, g.n_tiles, kSoftBinCap, &b);
     hipLaunchKernelGGL(k_fill_u32, dim3(div_up(g.n_tiles, 256)), dim3(256), 0, ctx->stream,
@@ -415,11 +418,12 @@ int dressi_rasterize_soft(dressi_ctx* ctx, const float* soft_clip, const float* 
         hipLaunchKernelGGL(k_soft_setup_op, dim3(div_up(n_faces, 256)), dim3(256), 0,
                            ctx->stream, g, (const float4*)soft_clip, face_id, faces_soft,
                            (const float4*)hard_clip, n_verts, faces_tex, b, ctx->d_err,
-                           (SoftRec*)recs);
+                           (SoftRec*)recs, (CullRec*)cull);
         DRESSI_CHECK_LAUNCH();
     }
-    hipLaunchKernelGGL(k_raster_soft_op, dim3(g.n_tiles), dim3(kTileThreads), 0, ctx->stream, g,
-                       (const SoftRec*)recs, b, radius_px, prev_shifted_depth, (float4*)out);
+    hipLaunchKernelGGL(k_raster_soft_op, dim3(block_grid(g)), dim3(64), 0, ctx->stream, g,
+                       (const SoftRec*)recs, (const CullRec*)cull, b, radius_px,
+                       prev_shifted_depth, (float4*)out);
     DRESSI_CHECK_LAUNCH();
     return DRESSI_OK;
 }

@@ -7,11 +7,12 @@
 // triangle (0.5 * clamp(hard_z) when dist >= 0, else
 // 0.5 + 0.5 * min(-dist / r, 1)); the minimum depth wins, later faces win ties.
 //
-// Here one 256-lane workgroup owns a 16x16 tile of one view, each wave an 8x8
-// block. The faces binned to the tile are staged through LDS; every lane
-// folds the fragments of its pixel into a 64-bit (depth | ~face) key, whose
-// minimum is the reference's winner independent of processing order. The
-// work is split so that, exactly:
+// Here one wave owns an 8x8 block of one view. Faces are binned per 16x16
+// tile; the wave culls its tile's list against the block (one entry per
+// lane, ballot) and walks the survivors with the face record in scalar
+// registers; every lane folds the fragments of its pixel into a 64-bit
+// (depth | ~face) key, whose minimum is the reference's winner independent of
+// processing order. The work is split so that, exactly:
 //  * phase A folds hard-branch fragments (pixel inside the hard triangle:
 //    depth <= 0.5, no distance needed) and any fragment close enough to a
 //    hard edge that the classification needs the full reference evaluation;
@@ -20,8 +21,6 @@
 //    they cannot win. Faces whose hard triangle lies more than r + 1 px from
 //    the wave's block contribute depth exactly 1.0 there (-dist/r > 1), so
 //    only their coverage is tested.
-// Each wave culls the staged records against its block in parallel (one
-// record per lane, ballot-compacted) before the per-pixel loops.
 #pragma once
 
 #include "internal.h"
@@ -77,6 +76,26 @@ __device__ __forceinline__ void soft_setup(const float4 sc[3], const float4 hc[3
         return;
     }
     r->s_inv_area = 1.f / s_area;
+    // Soft coverage margin (edge-function units) for the block cull. A pixel
+    // the reference's float barycentrics call covered has, for the computed
+    // area's sign s, s * E_k(p) >= -m on each exact edge function E_k
+    // (twice the signed area of p and the edge): the rounding of E_k itself,
+    // of the 1 / area scaling and of l2 = 1 - l0 - l1 stays below
+    // 8u Q (2 + P / |2 area|) with Q = sum_k (|x_k| + |x_k+1| + W) (|y_k| +
+    // |y_k+1| + H) and P = |x1 - x0| |y2 - y0| + |y1 - y0| |x2 - x0|; the
+    // factor 16u (5 + P / |2 area|) also covers the block evaluation. Only
+    // when |2 area| > 2^-20 P is the computed sign the exact one.
+    {
+        float q = 0.f;
+        for (int k = 0; k < 3; k++) {
+            const int k1 = (k + 1) % 3;
+            q += (fabsf(sx[k]) + fabsf(sx[k1]) + W) * (fabsf(sy[k]) + fabsf(sy[k1]) + H);
+        }
+        const float pa = fabsf(sx[1] - sx[0]) * fabsf(sy[2] - sy[0]) +
+                         fabsf(sy[1] - sy[0]) * fabsf(sx[2] - sx[0]);
+        const float m = 0x1p-20f * q * (5.f + pa / fabsf(s_area));
+        r->s_margin = (fabsf(s_area) > 0x1p-20f * pa && m < INFINITY) ? m : -1.f;
+    }
     const float h_area = tri_area(hx[0], hy[0], hx[1], hy[1], hx[2], hy[2]);
     const bool area_ok = !(fabsf(h_area) < kDistEps);
     r->h_inv_area = area_ok ? 1.f / h_area : 0.f;
@@ -111,8 +130,32 @@ __device__ __forceinline__ void soft_setup(const float4 sc[3], const float4 hc[3
     const float thr_max = smax(smax(r->thr[0], r->thr[1]), r->thr[2]);
     const float wmax = smax(smax(smax(hx[0], hx[1]), hx[2]) - smin(smin(hx[0], hx[1]), hx[2]),
                             smax(smax(hy[0], hy[1]), hy[2]) - smin(smin(hy[0], hy[1]), hy[2]));
-    const bool sliver = !(fabsf(h_area) > 4.f * thr_max * wmax) || !(fabsf(h_area) < INFINITY);
-    r->flags = (area_ok ? kRecHardArea : 0u) | (sliver ? kRecSliver : 0u);
+    // (|2 area| > 8 thr also rules out a winding test that calls a pixel
+    // inside with the orientation opposite to the area's sign: the three
+    // exact edge functions sum to 2 area)
+    // (a hard area below the 1e-6 test leaves no orientation: also a sliver)
+    const bool sliver = !area_ok || !(fabsf(h_area) > smax(4.f * thr_max * wmax, 8.f * thr_max)) ||
+                        !(fabsf(h_area) < INFINITY);
+    r->flags = (area_ok ? kRecHardArea : 0u) | (sliver ? kRecSliver : 0u) |
+               (h_area > 0.f ? kRecPos : 0u);
+    // Hard-branch margin. Non-slivers: 1 px (the bound above gives 0.51).
+    // Slivers whose |2 area| exceeds 16 thr (the winding test cannot take the
+    // opposite orientation) and whose computed area has the exact sign
+    // (|2 area| > 2^-20 P, P the products of its corner differences): exact
+    // barycentrics >= -m with m <= 2 thr / |2 area| (the computed area is
+    // within a factor 2), so inside pixels lie within the bbox widened by
+    // 2 m wmax. Other slivers: no bound.
+    if (!sliver) {
+        r->a_margin = 1.f;
+    } else {
+        const float pa = fabsf(hx[1] - hx[0]) * fabsf(hy[2] - hy[0]) +
+                         fabsf(hy[1] - hy[0]) * fabsf(hx[2] - hx[0]);
+        const float ah = fabsf(h_area);
+        const float mg = 1.f + 4.f * thr_max * wmax / ah;
+        r->a_margin = (area_ok && ah > 16.f * thr_max && ah > 0x1p-20f * pa && mg < 1e6f)
+                              ? mg
+                              : INFINITY;
+    }
     pixel_bbox(sx[0], sx[1], sx[2], sy[0], sy[1], sy[2], (int)w, (int)h, &r->bx0, &r->by0,
                &r->bx1, &r->by1);
 }
@@ -156,16 +199,41 @@ __device__ __forceinline__ float hard_z_at(const SoftRec& r, float p0, float p1)
     return hard_z;
 }
 
-// Fragment class w.r.t. the hard triangle: 0 = hard branch (all edge
-// functions share a sign; dist >= 0), 1 = rim (mixed signs, every edge
-// function clear of the boundary bound: dist < 0), 2 = needs the full
-// reference evaluation (near an edge).
+// Fragment class w.r.t. the hard triangle: 0 = hard branch (dist >= 0),
+// 1 = rim (dist < 0, and not -0), 2 = needs the full reference evaluation.
+// Non-sliver faces: the winding test can only say inside with the area's
+// orientation s, so every s * edge function clear above its threshold gives
+// 0, and one clearly below -threshold gives 1 (the pixel is strictly
+// outside, at least thr / |e| >= 2^-19 min(W, H) px from the edge line, far
+// above the rounding of the distance, so d2 > 0). Slivers: all edge functions
+// clear with one sign gives 0, with mixed signs 1; else the exact crosses
+// decide, and a pixel within the boundary bound of an edge gives 2.
 __device__ __forceinline__ int frag_class(const SoftRec& r, float p0, float p1) {
     float e[3];
-    bool pos = true, neg = true, clear = true;
 #pragma unroll
     for (int k = 0; k < 3; k++) {
         e[k] = fmaf(r.ex[k], p1, fmaf(-r.ey[k], p0, r.cc[k]));
+    }
+    if (!(r.flags & kRecSliver)) {
+        bool in = true, out = false;
+        if (r.flags & kRecPos) {
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                in = in && e[k] > r.thr[k];
+                out = out || e[k] < -r.thr[k];
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                in = in && e[k] < -r.thr[k];
+                out = out || e[k] > r.thr[k];
+            }
+        }
+        return in ? 0 : (out ? 1 : 2);
+    }
+    bool pos = true, neg = true, clear = true;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
         const bool big = fabsf(e[k]) > r.thr[k];
         clear = clear && big;
         pos = pos && e[k] > 0.f;
@@ -190,20 +258,18 @@ __device__ __forceinline__ int frag_class(const SoftRec& r, float p0, float p1) 
     return near ? 2 : 1;
 }
 
-// Phase A fragment: hard branch and full-evaluation fragments.
+// Phase A fragment: hard branch and full-evaluation fragments. `inside`:
+// the wave's block lies inside the soft bbox (no per-pixel bbox test).
 __device__ __forceinline__ void frag_phase_a(const SoftRec& r, uint32_t f, int px, int py,
-                                             float radius, const float* prev, uint32_t width,
-                                             PixelBest& b) {
-    if (px < r.bx0 || px > r.bx1 || py < r.by0 || py > r.by1) {
+                                             bool inside, float radius, const float* prev,
+                                             uint32_t width, PixelBest& b) {
+    if (!inside && (px < r.bx0 || px > r.bx1 || py < r.by0 || py > r.by1)) {
         return;
     }
     const float p0 = (float)px + 0.5f;
     const float p1 = (float)py + 0.5f;
     const int cls = frag_class(r, p0, p1);
     if (cls == 1) {
-        return;
-    }
-    if (!soft_covers(r, p0, p1)) {
         return;
     }
     float depth;
@@ -219,7 +285,14 @@ __device__ __forceinline__ void frag_phase_a(const SoftRec& r, uint32_t f, int p
     if (prev && depth <= prev[(size_t)py * width + px] + 1e-4f) {
         return;
     }
-    fold(b, depth, f, hard);
+    // the fragment exists only where the soft triangle covers the pixel;
+    // testing that after the depth compare skips it for losing fragments
+    const uint64_t key = depth_key(depth, f);
+    if (key >= b.key || !soft_covers(r, p0, p1)) {
+        return;
+    }
+    b.key = key;
+    b.hard = hard;
 }
 
 // Phase B fragment (lanes whose best depth is >= 0.5): every fragment phase
@@ -262,12 +335,136 @@ __device__ __forceinline__ void frag_phase_b(const SoftRec& r, uint32_t f, int p
     fold(b, depth, f, hard);
 }
 
-// Per-tile LDS of the resolver
-struct TileLds {
-    SoftRec rec[kTileThreads];
-    uint32_t face[kTileThreads];
-    uint16_t surv[4][kTileThreads];
+// Per (view, face) cull record: the soft pixel bbox and the pixels whose
+// centres may lie within the hard triangle's bbox +-1 px (all of the soft
+// bbox for slivers or non-finite corners), inclusive ranges. 16 bytes.
+struct CullRec {
+    int16_t sx0, sy0, sx1, sy1;
+    int16_t ax0, ay0, ax1, ay1;
 };
+static_assert(sizeof(CullRec) == 16, "CullRec layout");
+
+__device__ __forceinline__ CullRec cull_setup(const SoftRec& r) {
+    CullRec c;
+    if (r.bx0 > r.bx1 || r.by0 > r.by1) {
+        c.sx0 = c.sy0 = c.ax0 = c.ay0 = 1;
+        c.sx1 = c.sy1 = c.ax1 = c.ay1 = 0;
+        return c;
+    }
+    c.sx0 = (int16_t)r.bx0;
+    c.sy0 = (int16_t)r.by0;
+    c.sx1 = (int16_t)r.bx1;
+    c.sy1 = (int16_t)r.by1;
+    int ax0 = r.bx0, ay0 = r.by0, ax1 = r.bx1, ay1 = r.by1;
+    if (r.a_margin < INFINITY) {
+        // centre px + 0.5 in [min - a, max + a]  <=>  px in [min - a - 0.5,
+        // max + a - 0.5]; one extra pixel each side absorbs the rounding.
+        // fminf / fmaxf keep NaN corners conservative (the whole soft bbox).
+        const float a = r.a_margin;
+        const float mnx = smin(smin(r.hx[0], r.hx[1]), r.hx[2]);
+        const float mxx = smax(smax(r.hx[0], r.hx[1]), r.hx[2]);
+        const float mny = smin(smin(r.hy[0], r.hy[1]), r.hy[2]);
+        const float mxy = smax(smax(r.hy[0], r.hy[1]), r.hy[2]);
+        const int lx = (int)fmaxf(floorf(mnx - a - 0.5f), -4.f) - 1;
+        const int hx = (int)fminf(ceilf(mxx + a - 0.5f), 32000.f) + 1;
+        const int ly = (int)fmaxf(floorf(mny - a - 0.5f), -4.f) - 1;
+        const int hy = (int)fminf(ceilf(mxy + a - 0.5f), 32000.f) + 1;
+        ax0 = max(ax0, lx);
+        ax1 = min(ax1, hx);
+        ay0 = max(ay0, ly);
+        ay1 = min(ay1, hy);
+    }
+    c.ax0 = (int16_t)ax0;
+    c.ay0 = (int16_t)ay0;
+    c.ax1 = (int16_t)ax1;
+    c.ay1 = (int16_t)ay1;
+    return c;
+}
+
+// Separating-axis test of a hard triangle with a finite a_margin (non-sliver
+// or bounded sliver) against the 8x8 block
+// along its three edge normals. A pixel centre the reference's winding test
+// puts inside (or on the boundary) has, for the triangle's orientation s,
+// s * (exact edge function) >= -thr[k] on every edge, and the filter form
+// and this corner maximum add at most thr[k] / 4 of rounding: the block can
+// hold such a pixel only if no edge's maximum over its pixel centres is below
+// -2 thr[k]. `w` = the record's first 16 words.
+__device__ __forceinline__ bool edges_reach_block(const float* w, int bx, int by) {
+    if (!(w[15] < INFINITY)) {
+        return true;  // no hard-branch bound (a_margin)
+    }
+    const float s = w[12] > 0.f ? 1.f : -1.f;  // orientation (sign of 1 / area)
+    const float x0 = (float)bx + 0.5f, x1 = (float)bx + 7.5f;
+    const float y0 = (float)by + 0.5f, y1 = (float)by + 7.5f;
+    bool hit = true;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        const float a = s * w[k];       // s * ex
+        const float b = -s * w[3 + k];  // -s * ey
+        const float m = s * w[6 + k] + smax(a * y0, a * y1) + smax(b * x0, b * x1);
+        hit = hit && !(m < -2.f * w[9 + k]);
+    }
+    return hit;
+}
+
+// Separating-axis test of the soft triangle against the 8x8 block along its
+// three edge normals, with the record's soft margin: false only when no
+// pixel centre of the block can be covered (per lane, one face per lane).
+__device__ __forceinline__ bool soft_reaches_block(const SoftRec* rec, int bx, int by) {
+    const float m = rec->s_margin;
+    if (!(m >= 0.f)) {
+        return true;
+    }
+    const float4 a = *(const float4*)&rec->sx[0];  // sx0 sx1 sx2 sy0
+    const float2 b = *(const float2*)&rec->sy[1];  // sy1 sy2
+    const float x[3] = {a.x, a.y, a.z};
+    const float y[3] = {a.w, b.x, b.y};
+    const float s = rec->s_inv_area > 0.f ? 1.f : -1.f;
+    const float x0 = (float)bx + 0.5f, x1 = (float)bx + 7.5f;
+    const float y0 = (float)by + 0.5f, y1 = (float)by + 7.5f;
+    bool hit = true;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        const int k1 = (k + 1) % 3;
+        const float ex = s * (x[k1] - x[k]);
+        const float ey = s * (y[k1] - y[k]);
+        // max over the block of s * (ex (py - y_k) - ey (px - x_k))
+        const float g = smax(ex * (y0 - y[k]), ex * (y1 - y[k])) +
+                        smax(-ey * (x0 - x[k]), -ey * (x1 - x[k]));
+        hit = hit && !(g < -m);
+    }
+    return hit;
+}
+
+// Inclusive box [x0, x1] x [y0, y1] meets the 8x8 block at (bx, by).
+__device__ __forceinline__ bool box_hits(int x0, int y0, int x1, int y1, int bx, int by) {
+    return x0 <= bx + 7 && x1 >= bx && y0 <= by + 7 && y1 >= by;
+}
+
+// The face takes part in phase A for the block: its soft bbox and A-box meet
+// the block and its edges do not separate it (per lane, one face per lane).
+// `soft` = also test the soft bbox (phase B has tested it already).
+__device__ __forceinline__ bool block_in_a(const SoftRec* recs, const CullRec* cull, uint32_t f,
+                                           int bx, int by, bool soft) {
+    const CullRec c = cull[f];
+    if (soft && !box_hits(c.sx0, c.sy0, c.sx1, c.sy1, bx, by)) {
+        return false;
+    }
+    if (!box_hits(c.ax0, c.ay0, c.ax1, c.ay1, bx, by)) {
+        return false;
+    }
+    const float4* q = (const float4*)(recs + f);
+    float w[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 v = q[i];
+        w[4 * i + 0] = v.x;
+        w[4 * i + 1] = v.y;
+        w[4 * i + 2] = v.z;
+        w[4 * i + 3] = v.w;
+    }
+    return edges_reach_block(w, bx, by);
+}
 
 // Number of list entries of a bin and whether it overflowed (then every face
 // of the view is walked; each face's own bbox keeps the result exact).
@@ -286,13 +483,38 @@ __device__ __forceinline__ BinView bin_view(const BinBuffers& b, uint32_t bin, u
     return v;
 }
 
-// The record's hard-triangle bbox widened by `d` px overlaps the pixel-centre
-// rectangle [cx0, cx1] x [cy0, cy1] (always true for slivers).
+// 8x8 pixel block of a workgroup. Workgroups are dispatched to the 8 XCDs
+// round robin (workgroup i runs on XCD i % 8): tiles are dealt to the XCDs
+// round robin too, and the four blocks of a 16x16 tile run on one XCD.
+struct BlockPos {
+    uint32_t tile;
+    int bx, by;
+    bool valid;
+};
+
+inline uint32_t block_grid(const RasterGeom& g) { return 32u * ((g.n_tiles + 7u) / 8u); }
+
+__device__ __forceinline__ BlockPos block_pos(uint32_t wg, const RasterGeom& g) {
+    const uint32_t per = (g.n_tiles + 7u) / 8u;
+    const uint32_t k = wg >> 3;
+    BlockPos b;
+    b.tile = (k >> 2) * 8u + (wg & 7u);
+    const uint32_t q = k & 3u;
+    b.bx = (int)((b.tile % g.tiles_x) * kTile + (q & 1u) * 8u);
+    b.by = (int)((b.tile / g.tiles_x) * kTile + (q >> 1) * 8u);
+    b.valid = (k >> 2) < per && b.tile < g.n_tiles && b.bx < (int)g.width && b.by < (int)g.height;
+    return b;
+}
+
+// The record's hard-triangle bbox widened by a_margin + `d` px overlaps the
+// pixel-centre rectangle [cx0, cx1] x [cy0, cy1] (always true without a
+// bound).
 __device__ __forceinline__ bool hard_bbox_near(const SoftRec& r, float cx0, float cx1, float cy0,
                                                float cy1, float d) {
-    if (r.flags & kRecSliver) {
+    if (!(r.a_margin < INFINITY)) {
         return true;
     }
+    d += r.a_margin;
     const float mnx = smin(smin(r.hx[0], r.hx[1]), r.hx[2]);
     const float mxx = smax(smax(r.hx[0], r.hx[1]), r.hx[2]);
     const float mny = smin(smin(r.hy[0], r.hy[1]), r.hy[2]);
@@ -300,97 +522,89 @@ __device__ __forceinline__ bool hard_bbox_near(const SoftRec& r, float cx0, floa
     return !(cx0 > mxx + d || cx1 < mnx - d || cy0 > mxy + d || cy1 < mny - d);
 }
 
-// Resolves the winner of every pixel of one (view, tile). All lanes of the
-// workgroup must call it (it synchronises). `recs` points at the view's
-// records. Pixels off screen fold nothing (their bbox tests fail).
-__device__ __forceinline__ PixelBest resolve_tile(const SoftRec* recs, const BinView& bv,
-                                                  uint32_t tile_x, uint32_t tile_y, float radius,
-                                                  const float* prev, uint32_t width,
-                                                  TileLds& lds) {
-    const int wave = threadIdx.x >> 6;
+// Uniform record read: the face index is wave-uniform, so the record comes
+// in through scalar loads (the constant address space) instead of LDS.
+typedef const __attribute__((address_space(4))) uint32_t* UniformWordPtr;
+
+__device__ __forceinline__ SoftRec load_rec_uniform(const SoftRec* recs, uint32_t f) {
+    constexpr int kWords = (int)(sizeof(SoftRec) / 4);
+    const UniformWordPtr src = (UniformWordPtr)(recs + f);
+    union {
+        SoftRec r;
+        uint32_t w[kWords];
+    } u;
+#pragma unroll
+    for (int i = 0; i < kWords; i++) {
+        u.w[i] = src[i];
+    }
+    return u.r;
+}
+
+// Resolves the winner of every pixel of one 8x8 block (lane = pixel, one
+// wave, no cross-wave synchronisation). `recs` / `cull` point at the view's
+// records. Phase A folds the class 0 / 2 fragments of faces whose A-box
+// meets the block; phase B, run only if some lane's best depth is >= 0.5,
+// folds the rest for those lanes. Every hard-branch fragment (depth <= 0.5)
+// lies within its face's A-box, so lanes whose best is < 0.5 after phase A
+// are final.
+__device__ __forceinline__ PixelBest resolve_block(const SoftRec* recs, const CullRec* cull,
+                                                   const BinView& bv, int bx, int by,
+                                                   float radius, const float* prev,
+                                                   uint32_t width) {
     const int lane = threadIdx.x & 63;
-    const int bx = (int)tile_x * kTile + (wave & 1) * 8;
-    const int by = (int)tile_y * kTile + (wave >> 1) * 8;
     const int px = bx + (lane & 7);
     const int py = by + (lane >> 3);
-    // pixel-centre rectangle of the wave's block
-    const float cx0 = (float)bx + 0.5f, cx1 = (float)bx + 7.5f;
-    const float cy0 = (float)by + 0.5f, cy1 = (float)by + 7.5f;
-    const float near_d = radius + 1.f;
     PixelBest best;
     best.key = kEmptyKey;
     best.hard = false;
-    const uint32_t half = 0x3f000000u;  // bits of 0.5f
-    for (int phase = 0; phase < 2; phase++) {
-        if (phase == 1) {
-            const bool need = (uint32_t)(best.key >> 32) >= half;
-            if (!__syncthreads_or(need)) {
-                break;
-            }
+    for (uint32_t base = 0; base < bv.n; base += 64) {
+        const uint32_t e = base + (uint32_t)lane;
+        uint32_t f = 0;
+        bool keep = false;
+        if (e < bv.n) {
+            f = bv.implicit ? e : bv.list[e];
+            keep = block_in_a(recs, cull, f, bx, by, true);
         }
-        const bool wave_need =
-                phase == 0 || __any((uint32_t)(best.key >> 32) >= half);
-        for (uint32_t base = 0; base < bv.n; base += kTileThreads) {
-            const uint32_t cnt = (bv.n - base) < (uint32_t)kTileThreads ? (bv.n - base)
-                                                                          : kTileThreads;
-            // reuse the staged chunk when the list fits one chunk
-            if (!(phase == 1 && bv.n <= (uint32_t)kTileThreads)) {
-                __syncthreads();
-                if (threadIdx.x < cnt) {
-                    const uint32_t f = bv.implicit ? base + threadIdx.x : bv.list[base + threadIdx.x];
-                    lds.face[threadIdx.x] = f;
-                    lds.rec[threadIdx.x] = recs[f];
-                }
-                __syncthreads();
-            }
-            if (!wave_need) {
-                continue;
-            }
-            // wave-parallel cull against the 8x8 block
-            uint32_t n_surv = 0;
-            for (uint32_t j0 = 0; j0 < cnt; j0 += 64) {
-                const uint32_t j = j0 + lane;
-                bool keep = false;
-                if (j < cnt) {
-                    const SoftRec& r = lds.rec[j];
-                    if (r.bx0 <= bx + 7 && r.bx1 >= bx && r.by0 <= by + 7 && r.by1 >= by) {
-                        if (phase == 0) {
-                            // hard-branch fragments lie within the hard
-                            // triangle's bbox (+1 px slack)
-                            keep = hard_bbox_near(r, cx0, cx1, cy0, cy1, 1.f);
-                        } else {
-                            keep = true;
-                        }
-                    }
-                }
-                const uint64_t m = __ballot(keep);
-                if (keep) {
-                    const uint32_t rank = __popcll(m & ((1ull << lane) - 1ull));
-                    lds.surv[wave][n_surv + rank] = (uint16_t)j;
-                }
-                n_surv += __popcll(m);
-            }
-            // the survivor list is written and read by this wave only
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            if (phase == 0) {
-                for (uint32_t s = 0; s < n_surv; s++) {
-                    const uint32_t j = lds.surv[wave][s];
-                    frag_phase_a(lds.rec[j], lds.face[j], px, py, radius, prev, width, best);
-                }
-            } else {
-                const bool lane_need = (uint32_t)(best.key >> 32) >= half;
-                for (uint32_t s = 0; s < n_surv; s++) {
-                    const uint32_t j = lds.surv[wave][s];
-                    const SoftRec& r = lds.rec[j];
-                    const bool in_a = hard_bbox_near(r, cx0, cx1, cy0, cy1, 1.f);
-                    const bool near = hard_bbox_near(r, cx0, cx1, cy0, cy1, near_d);
-                    if (lane_need) {
-                        frag_phase_b(r, lds.face[j], px, py, radius, prev, width, near, in_a,
-                                     best);
-                    }
-                }
+        uint64_t m = __ballot(keep);
+        while (m) {
+            const int j = __builtin_ctzll(m);
+            m &= m - 1;
+            const uint32_t fj = (uint32_t)__builtin_amdgcn_readlane((int)f, j);
+            const SoftRec r = load_rec_uniform(recs, fj);
+            const bool inside = r.bx0 <= bx && r.bx1 >= bx + 7 && r.by0 <= by && r.by1 >= by + 7;
+            frag_phase_a(r, fj, px, py, inside, radius, prev, width, best);
+        }
+    }
+    const bool need = (uint32_t)(best.key >> 32) >= 0x3f000000u;  // best depth >= 0.5
+    if (!__any(need)) {
+        return best;
+    }
+    const float near_d = radius;  // + the face's a_margin
+    const float cx0 = (float)bx + 0.5f, cx1 = (float)bx + 7.5f;
+    const float cy0 = (float)by + 0.5f, cy1 = (float)by + 7.5f;
+    for (uint32_t base = 0; base < bv.n; base += 64) {
+        const uint32_t e = base + (uint32_t)lane;
+        uint32_t f = 0;
+        bool keep = false, in_a = false;
+        if (e < bv.n) {
+            f = bv.implicit ? e : bv.list[e];
+            const CullRec c = cull[f];
+            keep = box_hits(c.sx0, c.sy0, c.sx1, c.sy1, bx, by) && soft_reaches_block(recs + f, bx, by);
+            in_a = keep && block_in_a(recs, cull, f, bx, by, false);
+        }
+        uint64_t m = __ballot(keep);
+        const uint64_t ma = __ballot(in_a);
+        while (m) {
+            const int j = __builtin_ctzll(m);
+            m &= m - 1;
+            const uint32_t fj = (uint32_t)__builtin_amdgcn_readlane((int)f, j);
+            const SoftRec r = load_rec_uniform(recs, fj);
+            const bool a = (ma >> j) & 1ull;
+            // the far path (depth exactly 1.0) needs the pixel more than r
+            // from the hard triangle: never for faces folded in phase A
+            const bool near = a || hard_bbox_near(r, cx0, cx1, cy0, cy1, near_d);
+            if (need) {
+                frag_phase_b(r, fj, px, py, radius, prev, width, near, a, best);
             }
         }
     }
