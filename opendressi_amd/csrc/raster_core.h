@@ -76,15 +76,17 @@ __device__ __forceinline__ void soft_setup(const float4 sc[3], const float4 hc[3
         return;
     }
     r->s_inv_area = 1.f / s_area;
-    // Soft coverage margin (edge-function units) for the block cull. A pixel
-    // the reference's float barycentrics call covered has, for the computed
-    // area's sign s, s * E_k(p) >= -m on each exact edge function E_k
-    // (twice the signed area of p and the edge): the rounding of E_k itself,
-    // of the 1 / area scaling and of l2 = 1 - l0 - l1 stays below
-    // 8u Q (2 + P / |2 area|) with Q = sum_k (|x_k| + |x_k+1| + W) (|y_k| +
-    // |y_k+1| + H) and P = |x1 - x0| |y2 - y0| + |y1 - y0| |x2 - x0|; the
-    // factor 16u (5 + P / |2 area|) also covers the block evaluation. Only
-    // when |2 area| > 2^-20 P is the computed sign the exact one.
+    // Soft coverage margin (edge-function units) for the block cull. With s
+    // the computed area's sign (exact when |2 area| > 2^-20 P), a pixel the
+    // reference's float barycentrics call covered has s * E_k(p) >= -m on
+    // each exact edge function E_k (twice the signed area of p and the
+    // edge): l0, l1 >= 0 only lose the rounding of E_0, E_1 (<= 4u P_k; the
+    // 1 / area factor scales them without changing their sign), and
+    // l2 = 1 - l0 - l1 >= 0 adds that, the relative error of the area
+    // (<= 4u P) and the final rounding (u (|2 area| + P_0 + P_1)). With
+    // Q = sum_k (|x_k| + |x_k+1| + W) (|y_k| + |y_k+1| + H) >= sum_k P_k and
+    // P = |x1 - x0| |y2 - y0| + |y1 - y0| |x2 - x0|, m = 16u (Q + P +
+    // |2 area|) covers these and the block evaluation.
     {
         float q = 0.f;
         for (int k = 0; k < 3; k++) {
@@ -93,7 +95,7 @@ __device__ __forceinline__ void soft_setup(const float4 sc[3], const float4 hc[3
         }
         const float pa = fabsf(sx[1] - sx[0]) * fabsf(sy[2] - sy[0]) +
                          fabsf(sy[1] - sy[0]) * fabsf(sx[2] - sx[0]);
-        const float m = 0x1p-20f * q * (5.f + pa / fabsf(s_area));
+        const float m = 0x1p-20f * (q + pa + fabsf(s_area));
         r->s_margin = (fabsf(s_area) > 0x1p-20f * pa && m < INFINITY) ? m : -1.f;
     }
     const float h_area = tri_area(hx[0], hy[0], hx[1], hy[1], hx[2], hy[2]);
