@@ -59,6 +59,23 @@ def kernel_bytes(n_views: int, s: int, n_faces: int, n_verts: int, samples: int 
     }
 
 
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE per dispatch,
+    scaled by the counters' reading for a plain copy of known size), or None
+    when that summary is for another kernel or workload."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as fh:
+            rec = json.load(fh)
+    except (OSError, ValueError):
+        return None
+    for k in rec.get("kernels", []):
+        if k.get("kernel") == kernel and rec.get("workload") == workload:
+            return k["fetch_bytes"] + k["write_bytes"]
+    return None
+
+
 def cpu_info() -> str:
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
@@ -100,6 +117,9 @@ def main() -> int:
     ap.add_argument("--workload", default="c4_hsr")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-iters", type=int, default=20)
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="after the JSON line, run a plain device copy of this many MiB "
+                         "(the reference kernel for scaling rocprofv3 FETCH/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the multi-GPU path "
@@ -130,6 +150,7 @@ def main() -> int:
     dbytes = kbytes[dom]
     ibytes = iteration_bytes(nviews, s, nf, nv)
     achieved = dbytes / (dom_us * 1e-6)
+    traffic = measured_traffic(dom, args.workload)
     fit.close()
 
     line = {
@@ -153,7 +174,7 @@ def main() -> int:
                      "achieved": achieved / 1e9,
                      "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK,
-                     "traffic": None,
+                     "traffic": traffic,
                      "algorithmic_bytes_per_launch": dbytes,
                      "avg_launch_us": dom_us},
         "iteration_roofline": {"algorithmic_bytes": ibytes,
@@ -167,6 +188,14 @@ def main() -> int:
         line["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(line), flush=True)
     ctx.close()
+    if args.copy_mb > 0:
+        import torch
+        n = args.copy_mb * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     return 0
 
 

@@ -981,16 +981,17 @@ int dressi_hsr_profile(dressi_hsr_plan* p, uint32_t iters, char* names, size_t n
     if (int rc = ready(p)) return rc;
     DRESSI_REQUIRE(n, "bad arguments");
     // Average device time per launch of each kernel of the iteration: after
-    // one eager iteration and one setup, each kernel is launched `iters`
-    // times back to back between two HIP events on the plan stream. The
-    // raster, loss and face backward replays are idempotent; the vertex
-    // kernel advances Adam each time (the optimisation moves iters + 1
-    // steps); the setup replays append to the bins, which a final face
-    // backward clears.
+    // one eager iteration and one setup, the raster, loss, face backward and
+    // vertex kernels are each launched `iters` times back to back between
+    // two HIP events on the plan stream (the first three are idempotent; the
+    // vertex kernel advances Adam each time). The setup appends to the bins,
+    // so it is timed as `iters` (setup, face backward) pairs -- the face
+    // backward clears the bins -- minus the face backward's own time. The
+    // optimisation moves 2 iters + 1 steps.
     const uint32_t reps = iters ? iters : 1;
     *n = kIterKernels;
     hipStream_t s = p->ctx->stream;
-    // timing order: raster, loss, face bwd, vertex, setup
+    // timed groups: raster, loss, face bwd, vertex, (setup + face bwd)
     const int order[kIterKernels] = {1, 2, 3, 4, 0};
     hipEvent_t ev[kIterKernels + 1] = {};
     int rc = DRESSI_OK;
@@ -1010,22 +1011,28 @@ int dressi_hsr_profile(dressi_hsr_plan* p, uint32_t iters, char* names, size_t n
         }
         for (uint32_t r = 0; r < reps && !rc; r++) {
             rc = launch_iter_kernel(p->d, s, order[i]);
+            if (!rc && order[i] == 0) {
+                rc = launch_iter_kernel(p->d, s, 3);
+            }
         }
     }
-    if (!rc && hipEventRecord(ev[kIterKernels], s) != hipSuccess) {
-        set_error("hipEventRecord failed");
-        rc = DRESSI_ERR_HIP;
-    }
-    if (!rc) rc = launch_iter_kernel(p->d, s, 3);  // clears the replayed bins
-    if (!rc && hipEventSynchronize(ev[kIterKernels]) != hipSuccess) {
+    if (!rc && (hipEventRecord(ev[kIterKernels], s) != hipSuccess ||
+                hipEventSynchronize(ev[kIterKernels]) != hipSuccess)) {
         set_error("event synchronisation failed");
         rc = DRESSI_ERR_HIP;
     }
     float ms[kIterKernels] = {};
     for (int i = 0; i < kIterKernels && !rc; i++) {
         float t = 0.f;
-        hipEventElapsedTime(&t, ev[i], ev[i + 1]);
+        if (hipEventElapsedTime(&t, ev[i], ev[i + 1]) != hipSuccess) {
+            set_error("hipEventElapsedTime failed");
+            rc = DRESSI_ERR_HIP;
+            break;
+        }
         ms[order[i]] = t / reps;
+    }
+    if (!rc) {
+        ms[0] = ms[0] > ms[3] ? ms[0] - ms[3] : 0.f;
     }
     for (uint32_t k = 0; k < (uint32_t)kIterKernels && k < cap && !rc; k++) {
         if (usec) {
