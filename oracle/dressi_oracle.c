@@ -1308,3 +1308,457 @@ int or_hsr_fit(const float* pos0, uint32_t n_verts, const float* faces,
     free(lacc);
     return 0;
 }
+
+/* ===================================================================== */
+/* Screen-space antialiasing (Dr.Hair-style AA, technique "aa")           */
+/* ===================================================================== */
+
+/* f_ops.cpp:2213-2214 (kAaOffs) */
+static const int k_aa_offs[8][2] = {{-1, -1}, {0, -1}, {1, -1}, {-1, 0},
+                                    {1, 0},   {-1, 1}, {0, 1},  {1, 1}};
+
+/* src/core/cpu_raster.cpp:371-454 (EvalAaPair). `tri` holds float(face)+1
+ * (0 = background); `faces` float VEC3. Owner preference: the neighbour's
+ * triangle first (the edge crossed walking s -> n; max crossing parameter),
+ * then s's own (min crossing parameter). */
+int or_eval_aa_pair(const float* tri, const float* clip, uint32_t n_verts,
+                    const float* faces, uint32_t n_faces, uint32_t w, uint32_t h,
+                    int sx, int sy, int nx, int ny, or_aa_pair* out) {
+    const int its = (int)(tri[(size_t)sy * w + sx] + 0.5f);
+    const int itn = (int)(tri[(size_t)ny * w + nx] + 0.5f);
+    if (its == itn) {
+        return 0;
+    }
+    const float ps[2] = {(float)sx + 0.5f, (float)sy + 0.5f};
+    const float pn[2] = {(float)nx + 0.5f, (float)ny + 0.5f};
+    for (int o = 0; o < 2; o++) {
+        const int owner = o == 0 ? itn : its;
+        if (owner == 0) {
+            continue;
+        }
+        const uint32_t f = (uint32_t)(owner - 1);
+        if (f >= n_faces) {
+            continue;
+        }
+        uint32_t vi[3];
+        float q[3][2];
+        int ok = 1;
+        for (int k = 0; k < 3; k++) {
+            vi[k] = (uint32_t)(int64_t)(faces[(size_t)f * 3 + k] + 0.5f);
+            if (vi[k] >= n_verts ||
+                !project_clip_to_screen(&clip[(size_t)vi[k] * 4], w, h, q[k], NULL)) {
+                ok = 0;
+                break;
+            }
+        }
+        if (!ok) {
+            continue;
+        }
+        int best_j = -1;
+        float best_t = 0.f;
+        for (int j = 0; j < 3; j++) {
+            const float* a = q[j];
+            const float* b = q[(j + 1) % 3];
+            const float es = (b[0] - a[0]) * (ps[1] - a[1]) - (b[1] - a[1]) * (ps[0] - a[0]);
+            const float en = (b[0] - a[0]) * (pn[1] - a[1]) - (b[1] - a[1]) * (pn[0] - a[0]);
+            if (es * en >= 0.f) {
+                continue;
+            }
+            const float t = es / (es - en);
+            if (best_j < 0 || (o == 0 ? t > best_t : t < best_t)) {
+                best_t = t;
+                best_j = j;
+            }
+        }
+        if (best_j < 0) {
+            continue;
+        }
+        const float* a = q[best_j];
+        const float* b = q[(best_j + 1) % 3];
+        const float ex = b[0] - a[0];
+        const float ey = b[1] - a[1];
+        const float len = sqrtf(ex * ex + ey * ey);
+        if (len < 1e-6f) {
+            continue;
+        }
+        const float es = ex * (ps[1] - a[1]) - ey * (ps[0] - a[0]);
+        out->r = smin(fabsf(es) / len, 1.f);
+        out->ia = vi[best_j];
+        out->ib = vi[(best_j + 1) % 3];
+        out->qa[0] = a[0];
+        out->qa[1] = a[1];
+        out->qb[0] = b[0];
+        out->qb[1] = b[1];
+        out->es = es;
+        out->len = len;
+        return 1;
+    }
+    return 0;
+}
+
+static int aa_in(int x, int y, uint32_t w, uint32_t h) {
+    return !(x < 0 || y < 0 || x >= (int)w || y >= (int)h);
+}
+
+/* f_ops.cpp:2544-2576 (AntiAlias CPU): c_aa = (c + sum_k [r c + (1-r) c_n]) / 9,
+ * inactive or off-screen neighbours add c. */
+void or_antialias(const float* img, uint32_t n_comp, const float* tri,
+                  const float* clip, uint32_t n_verts, const float* faces,
+                  uint32_t n_faces, uint32_t w, uint32_t h, float* out) {
+    for (int y = 0; y < (int)h; y++) {
+        for (int x = 0; x < (int)w; x++) {
+            const size_t so = ((size_t)y * w + x) * n_comp;
+            const float* cs = &img[so];
+            float* dst = &out[so];
+            for (uint32_t c = 0; c < n_comp; c++) {
+                dst[c] = cs[c];
+            }
+            for (int k = 0; k < 8; k++) {
+                const int nx = x + k_aa_offs[k][0];
+                const int ny = y + k_aa_offs[k][1];
+                or_aa_pair pr;
+                if (!aa_in(nx, ny, w, h) ||
+                    !or_eval_aa_pair(tri, clip, n_verts, faces, n_faces, w, h, x, y, nx, ny, &pr)) {
+                    for (uint32_t c = 0; c < n_comp; c++) {
+                        dst[c] += cs[c];
+                    }
+                    continue;
+                }
+                const float* cn = &img[((size_t)ny * w + nx) * n_comp];
+                for (uint32_t c = 0; c < n_comp; c++) {
+                    dst[c] += pr.r * cs[c] + (1.f - pr.r) * cn[c];
+                }
+            }
+            for (uint32_t c = 0; c < n_comp; c++) {
+                dst[c] /= 9.f;
+            }
+        }
+    }
+}
+
+/* f_ops.cpp:2231-2275 (AntiAliasBwdImg CPU) */
+void or_antialias_bwd_img(const float* gy, uint32_t n_comp, const float* tri,
+                          const float* clip, uint32_t n_verts, const float* faces,
+                          uint32_t n_faces, uint32_t w, uint32_t h, float* out) {
+    memset(out, 0, sizeof(float) * (size_t)w * h * n_comp);
+    for (int y = 0; y < (int)h; y++) {
+        for (int x = 0; x < (int)w; x++) {
+            const size_t so = ((size_t)y * w + x) * n_comp;
+            float alpha_sum = 0.f;
+            float* dst = &out[so];
+            for (int k = 0; k < 8; k++) {
+                const int nx = x + k_aa_offs[k][0];
+                const int ny = y + k_aa_offs[k][1];
+                if (!aa_in(nx, ny, w, h)) {
+                    alpha_sum += 1.f;
+                    continue;
+                }
+                or_aa_pair pr;
+                alpha_sum += or_eval_aa_pair(tri, clip, n_verts, faces, n_faces, w, h, x, y, nx,
+                                             ny, &pr)
+                                     ? pr.r
+                                     : 1.f;
+                or_aa_pair pr2;
+                if (or_eval_aa_pair(tri, clip, n_verts, faces, n_faces, w, h, nx, ny, x, y, &pr2)) {
+                    const size_t no = ((size_t)ny * w + nx) * n_comp;
+                    for (uint32_t c = 0; c < n_comp; c++) {
+                        dst[c] += (1.f - pr2.r) * gy[no + c];
+                    }
+                }
+            }
+            for (uint32_t c = 0; c < n_comp; c++) {
+                dst[c] += gy[so + c] * (1.f + alpha_sum);
+                dst[c] /= 9.f;
+            }
+        }
+    }
+}
+
+/* One active pair's contribution (f_ops.cpp:2345-2386): (1/9) dot(gy(s),
+ * c(s) - c(n)) times d r / d q_a, d r / d q_b through the screen -> clip
+ * Jacobian (x: 0.5 W / w, y: 0.5 H / w, w: -(..)/w^2, z: 0). `only_v`:
+ * add only endpoint `v` into dst_v, else scatter to both endpoints' rows. */
+static void aa_accumulate(const float* gy, const float* img, uint32_t n_comp,
+                          const float* clip, uint32_t w, uint32_t h, uint32_t v,
+                          int x, int y, int nx, int ny, const or_aa_pair* pr,
+                          int only_v, float* dst_v, float* out) {
+    const size_t so = ((size_t)y * w + x) * n_comp;
+    const size_t no = ((size_t)ny * w + nx) * n_comp;
+    float gr = 0.f;
+    for (uint32_t c = 0; c < n_comp; c++) {
+        gr += gy[so + c] * (img[so + c] - img[no + c]);
+    }
+    gr /= 9.f;
+    if (gr == 0.f) {
+        return;
+    }
+    const float ps[2] = {(float)x + 0.5f, (float)y + 0.5f};
+    const float sgn = pr->es >= 0.f ? 1.f : -1.f;
+    const float inv_l = 1.f / pr->len;
+    const float l3 = fabsf(pr->es) * inv_l * inv_l * inv_l;
+    const float ex = pr->qb[0] - pr->qa[0];
+    const float ey = pr->qb[1] - pr->qa[1];
+    const float dqa[2] = {sgn * inv_l * (pr->qb[1] - ps[1]) + l3 * ex,
+                          sgn * inv_l * (ps[0] - pr->qb[0]) + l3 * ey};
+    const float dqb[2] = {sgn * inv_l * (ps[1] - pr->qa[1]) - l3 * ex,
+                          sgn * inv_l * (pr->qa[0] - ps[0]) - l3 * ey};
+    const uint32_t ids[2] = {pr->ia, pr->ib};
+    const float* dqs[2] = {dqa, dqb};
+    const float w_scr = (float)w, h_scr = (float)h;
+    for (int e = 0; e < 2; e++) {
+        if (only_v && ids[e] != v) {
+            continue;
+        }
+        const float gqx = gr * dqs[e][0];
+        const float gqy = gr * dqs[e][1];
+        const float* c = &clip[(size_t)ids[e] * 4];
+        float* dst = only_v ? dst_v : &out[(size_t)ids[e] * 4];
+        dst[0] += gqx * 0.5f * w_scr / c[3];
+        dst[1] += gqy * 0.5f * h_scr / c[3];
+        dst[3] += -(gqx * 0.5f * w_scr * c[0] + gqy * 0.5f * h_scr * c[1]) / (c[3] * c[3]);
+    }
+}
+
+/* f_ops.cpp:2321-2474 (AntiAliasBwdVtx CPU). n_samples = 0: exact scatter
+ * over every active pair with r < 1, out {V,1} VEC4. n_samples > 0: per
+ * (vertex v, incident face slot d), n jittered samples along the face's
+ * edges (salts 2 and 3, +-2 px band), accumulated into row (d, v) of out
+ * {V, max_deg} VEC4 when `wide`, else into row v. */
+void or_antialias_bwd_vtx(const float* gy, const float* img, uint32_t n_comp,
+                          const float* tri, const float* clip, uint32_t n_verts,
+                          const float* faces, uint32_t n_faces, const float* vtx_faces,
+                          uint32_t max_deg, float seed, uint32_t n_samples, int wide,
+                          uint32_t w, uint32_t h, float* out) {
+    const size_t rows = wide ? max_deg : 1;
+    memset(out, 0, sizeof(float) * 4 * (size_t)n_verts * rows);
+    if (n_samples == 0) {
+        for (int y = 0; y < (int)h; y++) {
+            for (int x = 0; x < (int)w; x++) {
+                for (int k = 0; k < 8; k++) {
+                    const int nx = x + k_aa_offs[k][0];
+                    const int ny = y + k_aa_offs[k][1];
+                    if (!aa_in(nx, ny, w, h)) {
+                        continue;
+                    }
+                    or_aa_pair pr;
+                    if (!or_eval_aa_pair(tri, clip, n_verts, faces, n_faces, w, h, x, y, nx, ny,
+                                         &pr) ||
+                        pr.r >= 1.f) {
+                        continue;
+                    }
+                    aa_accumulate(gy, img, n_comp, clip, w, h, 0, x, y, nx, ny, &pr, 0, NULL,
+                                  out);
+                }
+            }
+        }
+        return;
+    }
+    const uint32_t seed_u = (uint32_t)(int64_t)(seed + 0.5f);
+    const float w_scr = (float)w, h_scr = (float)h;
+    for (uint32_t v = 0; v < n_verts; v++) {
+        for (uint32_t d = 0; d < max_deg; d++) {
+            float* dst_v = wide ? &out[((size_t)d * n_verts + v) * 4] : &out[(size_t)v * 4];
+            const float fv = vtx_faces[(size_t)d * n_verts + v];
+            if (fv < -0.5f) {
+                continue;
+            }
+            const uint32_t f = (uint32_t)(int64_t)(fv + 0.5f);
+            float s3[3][2];
+            int ok = 1;
+            for (int k = 0; k < 3; k++) {
+                const uint32_t vi = (uint32_t)(int64_t)(faces[(size_t)f * 3 + k] + 0.5f);
+                const float* c = &clip[(size_t)vi * 4];
+                if (c[3] <= 1e-6f) {
+                    ok = 0;
+                    break;
+                }
+                s3[k][0] = (c[0] / c[3] * 0.5f + 0.5f) * w_scr;
+                s3[k][1] = (c[1] / c[3] * 0.5f + 0.5f) * h_scr;
+            }
+            if (!ok) {
+                continue;
+            }
+            for (uint32_t smp = 0; smp < n_samples; smp++) {
+                const int e = (int)(smp % 3);
+                const float* a = s3[e];
+                const float* b = s3[(e + 1) % 3];
+                const float ex = b[0] - a[0];
+                const float ey = b[1] - a[1];
+                const float len = sqrtf(ex * ex + ey * ey);
+                if (len < 1e-6f) {
+                    continue;
+                }
+                const float u = or_hash_to_unit(f, smp, seed_u, 2);
+                const float o = (or_hash_to_unit(f, smp, seed_u, 3) * 2.f - 1.f) * 2.f;
+                const int x = (int)floorf(a[0] + u * ex - o * (ey / len));
+                const int y = (int)floorf(a[1] + u * ey + o * (ex / len));
+                if (!aa_in(x, y, w, h)) {
+                    continue;
+                }
+                for (int k = 0; k < 8; k++) {
+                    const int nx = x + k_aa_offs[k][0];
+                    const int ny = y + k_aa_offs[k][1];
+                    if (!aa_in(nx, ny, w, h)) {
+                        continue;
+                    }
+                    or_aa_pair pr;
+                    if (!or_eval_aa_pair(tri, clip, n_verts, faces, n_faces, w, h, x, y, nx, ny,
+                                         &pr) ||
+                        pr.r >= 1.f) {
+                        continue;
+                    }
+                    if (pr.ia != v && pr.ib != v) {
+                        continue;
+                    }
+                    aa_accumulate(gy, img, n_comp, clip, w, h, v, x, y, nx, ny, &pr, 1, dst_v,
+                                  NULL);
+                }
+            }
+        }
+    }
+}
+
+/* f_ops.cpp:1227-1244 (ColSum CPU): per column, rows summed in order */
+void or_col_sum(const float* x, uint32_t n_comp, uint32_t w, uint32_t h, float* out) {
+    memset(out, 0, sizeof(float) * (size_t)w * n_comp);
+    for (uint32_t r = 0; r < h; r++) {
+        for (uint32_t xw = 0; xw < w; xw++) {
+            for (uint32_t c = 0; c < n_comp; c++) {
+                out[(size_t)xw * n_comp + c] += x[((size_t)r * w + xw) * n_comp + c];
+            }
+        }
+    }
+}
+
+/* The AA silhouette fit of the reference example (technique aa, no
+ * regularizers; run.cpp:229-238, 346-357, 382-437): per view
+ * pred = AntiAlias(Rasterize(clip, 1), RasterizeFaceId(clip), clip, faces,
+ * vtx_faces, t, samples), target = StopGradient(AntiAlias(Rasterize(tgt),
+ * RasterizeFaceId(tgt), tgt_clip, tgt_faces, tgt_vtx_faces, 0, 0)), L2 loss
+ * image summed over views; backward: d loss / d pred -> AntiAliasBwdVtx
+ * (wide) -> ColSum -> TransformToClipVar -> pos; in-graph Adam.
+ * Outputs (nullable): as or_hsr_fit, with out_tri0 {N,S,S} the face-id
+ * images of iteration 0. */
+int or_aa_fit(const float* pos0, uint32_t n_verts, const float* faces, uint32_t n_faces,
+              const float* tgt_pos, uint32_t n_tverts, const float* tgt_faces,
+              uint32_t n_tfaces, const float* mvps, uint32_t n_views, uint32_t screen_px,
+              uint32_t samples, float lr, uint32_t iters, float* out_pos, float* out_m,
+              float* out_v, float* out_t, float* out_loss, float* out_grad0,
+              float* out_pred0, float* out_target, float* out_tri0, float* out_lossimg0) {
+    const uint32_t s = screen_px;
+    const size_t npx = (size_t)s * s;
+    const float inv_px = 1.f / (float)(s * s);
+    const uint32_t max_deg = or_vertex_faces_tex(faces, n_faces, n_verts, NULL, 0);
+    float* vf = (float*)malloc(sizeof(float) * max_deg * n_verts);
+    or_vertex_faces_tex(faces, n_faces, n_verts, vf, max_deg * n_verts);
+    float* targets = (float*)malloc(sizeof(float) * npx * n_views);
+    float* img = (float*)malloc(sizeof(float) * npx);
+    float* tri = (float*)malloc(sizeof(float) * npx);
+    {
+        float* tclip = (float*)malloc(sizeof(float) * 4 * n_tverts);
+        float* ones = (float*)malloc(sizeof(float) * n_tverts);
+        for (uint32_t i = 0; i < n_tverts; i++) {
+            ones[i] = 1.f;
+        }
+        for (uint32_t v = 0; v < n_views; v++) {
+            or_transform_to_clip(tgt_pos, n_tverts, mvps + 16 * v, tclip);
+            or_rasterize(tclip, n_tverts, ones, 1, tgt_faces, n_tfaces, s, s, img);
+            or_rasterize_face_id(tclip, n_tverts, tgt_faces, n_tfaces, s, s, tri);
+            or_antialias(img, 1, tri, tclip, n_tverts, tgt_faces, n_tfaces, s, s,
+                         targets + v * npx);
+        }
+        free(tclip);
+        free(ones);
+    }
+    float* ones = (float*)malloc(sizeof(float) * n_verts);
+    for (uint32_t i = 0; i < n_verts; i++) {
+        ones[i] = 1.f;
+    }
+    float* pos = (float*)malloc(sizeof(float) * 3 * n_verts);
+    float* m = (float*)calloc(3 * (size_t)n_verts, sizeof(float));
+    float* vv = (float*)calloc(3 * (size_t)n_verts, sizeof(float));
+    float t = 0.f;
+    memcpy(pos, pos0, sizeof(float) * 3 * n_verts);
+    float* clip = (float*)malloc(sizeof(float) * 4 * n_verts);
+    float* pred = (float*)malloc(sizeof(float) * npx);
+    float* gy = (float*)malloc(sizeof(float) * npx);
+    float* vloss = (float*)malloc(sizeof(float) * npx * n_views);
+    float* loss = (float*)malloc(sizeof(float) * npx);
+    float* wide = (float*)malloc(sizeof(float) * 4 * (size_t)n_verts * max_deg);
+    float* gclip = (float*)malloc(sizeof(float) * 4 * n_verts * n_views);
+    float* gpos = (float*)malloc(sizeof(float) * 3 * n_verts);
+    float* lacc = (float*)malloc(sizeof(float) * n_views);
+    for (uint32_t it = 0; it < iters; it++) {
+        for (uint32_t v = 0; v < n_views; v++) {
+            const float* target = targets + v * npx;
+            or_transform_to_clip(pos, n_verts, mvps + 16 * v, clip);
+            or_rasterize(clip, n_verts, ones, 1, faces, n_faces, s, s, img);
+            or_rasterize_face_id(clip, n_verts, faces, n_faces, s, s, tri);
+            or_antialias(img, 1, tri, clip, n_verts, faces, n_faces, s, s, pred);
+            for (size_t p = 0; p < npx; p++) {
+                const float diff = target[p] - pred[p];
+                vloss[v * npx + p] = diff * diff * inv_px;
+                const float cd = inv_px * diff; /* Mul(gy = c, diff) */
+                gy[p] = -(cd + cd);             /* Mul(diff, diff), Sub(target, pred) */
+            }
+            or_antialias_bwd_vtx(gy, img, 1, tri, clip, n_verts, faces, n_faces, vf, max_deg, t,
+                                 samples, 1, s, s, wide);
+            or_col_sum(wide, 4, n_verts, max_deg, gclip + (size_t)v * 4 * n_verts);
+            if (it == 0) {
+                if (out_pred0) {
+                    memcpy(out_pred0 + v * npx, pred, sizeof(float) * npx);
+                }
+                if (out_tri0) {
+                    memcpy(out_tri0 + v * npx, tri, sizeof(float) * npx);
+                }
+            }
+        }
+        for (size_t p = 0; p < npx; p++) {
+            for (uint32_t v = 0; v < n_views; v++) {
+                lacc[v] = vloss[v * npx + p];
+            }
+            sum_tree(lacc, n_views, 1);
+            loss[p] = lacc[0];
+        }
+        if (out_loss) {
+            double acc = 0.0;
+            for (size_t p = 0; p < npx; p++) {
+                acc += loss[p];
+            }
+            out_loss[it] = (float)acc;
+        }
+        pos_grad(gclip, mvps, n_views, n_verts, gpos);
+        if (it == 0) {
+            if (out_lossimg0) {
+                memcpy(out_lossimg0, loss, sizeof(float) * npx);
+            }
+            if (out_grad0) {
+                memcpy(out_grad0, gpos, sizeof(float) * 3 * n_verts);
+            }
+        }
+        adam_step(pos, m, vv, &t, gpos, 3 * n_verts, lr);
+    }
+    if (out_target) memcpy(out_target, targets, sizeof(float) * npx * n_views);
+    if (out_pos) memcpy(out_pos, pos, sizeof(float) * 3 * n_verts);
+    if (out_m) memcpy(out_m, m, sizeof(float) * 3 * n_verts);
+    if (out_v) memcpy(out_v, vv, sizeof(float) * 3 * n_verts);
+    if (out_t) *out_t = t;
+    free(vf);
+    free(targets);
+    free(img);
+    free(tri);
+    free(ones);
+    free(pos);
+    free(m);
+    free(vv);
+    free(clip);
+    free(pred);
+    free(gy);
+    free(vloss);
+    free(loss);
+    free(wide);
+    free(gclip);
+    free(gpos);
+    free(lacc);
+    return 0;
+}

@@ -104,6 +104,44 @@ int or_hsr_fit(const float* pos0, uint32_t n_verts, const float* faces,
                float* out_grad0, float* out_pred0, float* out_target,
                float* out_rs0, float* out_lossimg0);
 
+/* ---- screen-space antialiasing (technique aa) ------------------------- */
+/* src/core/cpu_raster.h:67-80 (AaPair) */
+typedef struct {
+    float r;
+    uint32_t ia, ib;
+    float qa[2], qb[2];
+    float es, len;
+} or_aa_pair;
+/* src/core/cpu_raster.cpp:371-454 (EvalAaPair) */
+int or_eval_aa_pair(const float* tri, const float* clip, uint32_t n_verts,
+                    const float* faces, uint32_t n_faces, uint32_t w, uint32_t h,
+                    int sx, int sy, int nx, int ny, or_aa_pair* out);
+/* src/core/f_ops.cpp:2480-2579 (AntiAlias) */
+void or_antialias(const float* img, uint32_t n_comp, const float* tri,
+                  const float* clip, uint32_t n_verts, const float* faces,
+                  uint32_t n_faces, uint32_t w, uint32_t h, float* out);
+/* src/core/f_ops.cpp:2220-2278 (AntiAliasBwdImg) */
+void or_antialias_bwd_img(const float* gy, uint32_t n_comp, const float* tri,
+                          const float* clip, uint32_t n_verts, const float* faces,
+                          uint32_t n_faces, uint32_t w, uint32_t h, float* out);
+/* src/core/f_ops.cpp:2284-2476 (AntiAliasBwdVtx); out {V, wide ? max_deg : 1}
+ * VEC4 */
+void or_antialias_bwd_vtx(const float* gy, const float* img, uint32_t n_comp,
+                          const float* tri, const float* clip, uint32_t n_verts,
+                          const float* faces, uint32_t n_faces, const float* vtx_faces,
+                          uint32_t max_deg, float seed, uint32_t n_samples, int wide,
+                          uint32_t w, uint32_t h, float* out);
+/* src/core/f_ops.cpp:1218-1246 (ColSum) */
+void or_col_sum(const float* x, uint32_t n_comp, uint32_t w, uint32_t h, float* out);
+/* examples/silhouette_optimization/run.cpp:229-238, 346-357, 382-437
+ * (technique aa, no regularizers) */
+int or_aa_fit(const float* pos0, uint32_t n_verts, const float* faces, uint32_t n_faces,
+              const float* tgt_pos, uint32_t n_tverts, const float* tgt_faces,
+              uint32_t n_tfaces, const float* mvps, uint32_t n_views, uint32_t screen_px,
+              uint32_t samples, float lr, uint32_t iters, float* out_pos, float* out_m,
+              float* out_v, float* out_t, float* out_loss, float* out_grad0,
+              float* out_pred0, float* out_target, float* out_tri0, float* out_lossimg0);
+
 #ifdef __cplusplus
 }
 #endif

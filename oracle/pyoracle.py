@@ -131,6 +131,30 @@ class _Lib:
         return r
 
 
+    def aa_fit(self, pos0, faces, tgt_pos, tgt_faces, mvps, screen, samples=8, lr=1e-3,
+               iters=1, want_images=True):
+        """The AA silhouette fit (technique aa): dict pos, m, v, t, loss, grad0
+        and, with want_images, pred0 / target / tri0 {N,S,S}, lossimg0 {S,S}."""
+        pos0, faces = _f32(pos0), _f32(faces)
+        tgt_pos, tgt_faces, mvps = _f32(tgt_pos), _f32(tgt_faces), _f32(mvps)
+        nv, nf = pos0.shape[0], faces.shape[0]
+        n = mvps.shape[0]
+        s = screen
+        r = dict(pos=np.zeros((nv, 3), np.float32), m=np.zeros((nv, 3), np.float32),
+                 v=np.zeros((nv, 3), np.float32), t=np.zeros(1, np.float32),
+                 loss=np.zeros(max(iters, 1), np.float32), grad0=np.zeros((nv, 3), np.float32))
+        if want_images:
+            r.update(pred0=np.zeros((n, s, s), np.float32), target=np.zeros((n, s, s), np.float32),
+                     tri0=np.zeros((n, s, s), np.float32), lossimg0=np.zeros((s, s), np.float32))
+        g = r.get
+        self._call("aa_fit", _fp(pos0), _U32(nv), _fp(faces), _U32(nf), _fp(tgt_pos),
+                   _U32(tgt_pos.shape[0]), _fp(tgt_faces), _U32(tgt_faces.shape[0]), _fp(mvps),
+                   _U32(n), _U32(s), _U32(samples), C.c_float(lr), _U32(iters), _fp(r["pos"]),
+                   _fp(r["m"]), _fp(r["v"]), _fp(r["t"]), _fp(r["loss"]), _fp(r["grad0"]),
+                   _fp(g("pred0")), _fp(g("target")), _fp(g("tri0")), _fp(g("lossimg0")))
+        return r
+
+
 class Oracle(_Lib):
     """The C restatement (oracle/dressi_oracle.c)."""
 
@@ -213,6 +237,48 @@ class Oracle(_Lib):
     def wang_hash(self, x):
         return self.fn("wang_hash")(_U32(x))
 
+    def antialias(self, img, tri, clip, faces):
+        img, tri, clip, faces = _f32(img), _f32(tri), _f32(clip), _f32(faces)
+        h, w = tri.shape
+        nc = 1 if img.ndim == 2 else img.shape[2]
+        out = np.zeros(img.shape, np.float32)
+        self.fn("antialias")(_fp(img), _U32(nc), _fp(tri), _fp(clip), _U32(clip.shape[0]),
+                             _fp(faces), _U32(faces.shape[0]), _U32(w), _U32(h), _fp(out))
+        return out
+
+    def antialias_bwd_img(self, gy, tri, clip, faces):
+        gy, tri, clip, faces = _f32(gy), _f32(tri), _f32(clip), _f32(faces)
+        h, w = tri.shape
+        nc = 1 if gy.ndim == 2 else gy.shape[2]
+        out = np.zeros(gy.shape, np.float32)
+        self.fn("antialias_bwd_img")(_fp(gy), _U32(nc), _fp(tri), _fp(clip),
+                                     _U32(clip.shape[0]), _fp(faces), _U32(faces.shape[0]),
+                                     _U32(w), _U32(h), _fp(out))
+        return out
+
+    def antialias_bwd_vtx(self, gy, img, tri, clip, faces, vtx_faces, seed, n_samples,
+                          wide=True):
+        """n_samples > 0 and wide: the {deg, V, 4} partials; else {V, 4}."""
+        gy, img, tri, clip = _f32(gy), _f32(img), _f32(tri), _f32(clip)
+        faces, vtx_faces = _f32(faces), _f32(vtx_faces)
+        h, w = tri.shape
+        nc = 1 if gy.ndim == 2 else gy.shape[2]
+        deg, nv = vtx_faces.shape
+        is_wide = bool(wide and n_samples > 0)
+        out = np.zeros((deg if is_wide else 1, nv, 4), np.float32)
+        self.fn("antialias_bwd_vtx")(_fp(gy), _fp(img), _U32(nc), _fp(tri), _fp(clip),
+                                     _U32(nv), _fp(faces), _U32(faces.shape[0]), _fp(vtx_faces),
+                                     _U32(deg), C.c_float(seed), _U32(n_samples),
+                                     C.c_int(1 if is_wide else 0), _U32(w), _U32(h), _fp(out))
+        return out if is_wide else out[0]
+
+    def col_sum(self, x):
+        x = _f32(x)
+        h, w, nc = x.shape
+        out = np.zeros((w, nc), np.float32)
+        self.fn("col_sum")(_fp(x), _U32(nc), _U32(w), _U32(h), _fp(out))
+        return out
+
     def hsr_forward(self, rs, tri0, tri1, tri2, target, radius):
         rs, target = _f32(rs), _f32(target)
         h, w = target.shape
@@ -280,6 +346,33 @@ class Reference(_Lib):
         return pos, faces
 
 
+def _ref_antialias(self, img, tri, clip, faces, vtx_faces):
+    img, tri, clip, faces, vtx_faces = (_f32(a) for a in (img, tri, clip, faces, vtx_faces))
+    h, w = tri.shape
+    nc = 1 if img.ndim == 2 else img.shape[2]
+    deg, nv = vtx_faces.shape
+    out = np.zeros(img.shape, np.float32)
+    self._call("antialias", _fp(img), _U32(nc), _fp(tri), _fp(clip), _U32(nv), _fp(faces),
+               _U32(faces.shape[0]), _fp(vtx_faces), _U32(deg), _U32(w), _U32(h), _fp(out))
+    return out
+
+
+def _ref_antialias_bwd(self, gy, img, tri, clip, faces, vtx_faces, seed, n_samples):
+    """(g_img {like gy}, wide {deg, V, 4} or None, g_vtx {V, 4})."""
+    gy, img, tri, clip, faces, vtx_faces = (_f32(a) for a in (gy, img, tri, clip, faces,
+                                                              vtx_faces))
+    h, w = tri.shape
+    nc = 1 if gy.ndim == 2 else gy.shape[2]
+    deg, nv = vtx_faces.shape
+    g_img = np.zeros(gy.shape, np.float32)
+    wide = np.zeros((deg, nv, 4), np.float32) if n_samples > 0 else None
+    g_vtx = np.zeros((nv, 4), np.float32)
+    self._call("antialias_bwd", _fp(gy), _fp(img), _U32(nc), _fp(tri), _fp(clip), _U32(nv),
+               _fp(faces), _U32(faces.shape[0]), _fp(vtx_faces), _U32(deg), C.c_float(seed),
+               _U32(n_samples), _U32(w), _U32(h), _fp(g_img), _fp(wide), _fp(g_vtx))
+    return g_img, wide, g_vtx
+
+
 def face_id_buffer(rs):
     """The fused plan's face-id buffer for RasterizeSoft output `rs` (dist,
     fid, hard z, coverage): face + 1 where covered, 0 elsewhere, bit 31 set
@@ -292,3 +385,7 @@ def face_id_buffer(rs):
 
 def have_reference() -> bool:
     return os.path.exists(REF_SO)
+
+
+Reference.antialias = _ref_antialias
+Reference.antialias_bwd = _ref_antialias_bwd

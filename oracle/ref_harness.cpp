@@ -531,4 +531,233 @@ int refh_hsr_fit(const float* pos0, uint32_t n_verts, const float* faces,
     });
 }
 
+// F::AntiAlias forward: img {w,h} n_comp, tri {w,h} FLOAT (face + 1),
+// clip {V,1} VEC4, faces {F,1} VEC3, vtx_faces {V,deg}
+int refh_antialias(const float* img, uint32_t n_comp, const float* tri,
+                   const float* clip, uint32_t n_verts, const float* faces,
+                   uint32_t n_faces, const float* vtx_faces, uint32_t max_deg,
+                   uint32_t w, uint32_t h, float* out) {
+    return Guard([&] {
+        Variable vimg(VecOf(n_comp), {w, h});
+        Variable vtri(FLOAT, {w, h});
+        Variable vc(VEC4, {n_verts, 1});
+        Variable vf(VEC3, {n_faces, 1});
+        Variable vvf(FLOAT, {n_verts, max_deg});
+        Variable vs(FLOAT, {1, 1});
+        Variable y = F::AntiAlias(vimg, vtri, vc, vf, vvf, vs, 0);
+        CpuEvaluator ev;
+        ev.bind(vimg, Tensor(VecOf(n_comp), {w, h}, img));
+        ev.bind(vtri, Tensor(FLOAT, {w, h}, tri));
+        ev.bind(vc, Tensor(VEC4, {n_verts, 1}, clip));
+        ev.bind(vf, Tensor(VEC3, {n_faces, 1}, faces));
+        ev.bind(vvf, Tensor(FLOAT, {n_verts, max_deg}, vtx_faces));
+        ev.bind(vs, Fill(FLOAT, {1, 1}, 0.f));
+        CopyOut(ev.eval(y), out);
+    });
+}
+
+// Backward of F::AntiAlias w.r.t. img (AntiAliasBwdImg) and w.r.t. vtx_clip
+// (AntiAliasBwdVtx: n > 0 -> ColSum of the {V,deg} wide partials, written to
+// out_wide / out_vtx; n = 0 -> the exact {V,1} scatter in out_vtx), from the
+// op's own backward generator. Any output may be null.
+int refh_antialias_bwd(const float* gy, const float* img, uint32_t n_comp,
+                       const float* tri, const float* clip, uint32_t n_verts,
+                       const float* faces, uint32_t n_faces, const float* vtx_faces,
+                       uint32_t max_deg, float seed, uint32_t n_samples, uint32_t w,
+                       uint32_t h, float* out_img, float* out_wide, float* out_vtx) {
+    return Guard([&] {
+        Variable vimg(VecOf(n_comp), {w, h});
+        Variable vtri(FLOAT, {w, h});
+        Variable vc(VEC4, {n_verts, 1});
+        Variable vf(VEC3, {n_faces, 1});
+        Variable vvf(FLOAT, {n_verts, max_deg});
+        Variable vs(FLOAT, {1, 1});
+        Variable vgy(VecOf(n_comp), {w, h});
+        Variable y = F::AntiAlias(vimg, vtri, vc, vf, vvf, vs, n_samples);
+        Variable g_img = y.getCreator().buildBwd(vgy, 0);
+        Variable g_vtx = y.getCreator().buildBwd(vgy, 2);
+        CpuEvaluator ev;
+        ev.bind(vimg, Tensor(VecOf(n_comp), {w, h}, img));
+        ev.bind(vtri, Tensor(FLOAT, {w, h}, tri));
+        ev.bind(vc, Tensor(VEC4, {n_verts, 1}, clip));
+        ev.bind(vf, Tensor(VEC3, {n_faces, 1}, faces));
+        ev.bind(vvf, Tensor(FLOAT, {n_verts, max_deg}, vtx_faces));
+        ev.bind(vs, Fill(FLOAT, {1, 1}, seed));
+        ev.bind(vgy, Tensor(VecOf(n_comp), {w, h}, gy));
+        if (out_img) {
+            CopyOut(ev.eval(g_img), out_img);
+        }
+        if (out_vtx) {
+            CopyOut(ev.eval(g_vtx), out_vtx);
+        }
+        if (out_wide && n_samples > 0) {
+            CopyOut(ev.eval(g_vtx.getCreator().getInputVars()[0]), out_wide);
+        }
+    });
+}
+
+// The AA silhouette fit of the reference example (technique aa, no
+// regularizers): same driver and outputs as refh_hsr_fit, with out_tri0
+// {N,S,S} the RasterizeFaceId images of iteration 0 in place of out_rs0.
+int refh_aa_fit(const float* pos0, uint32_t n_verts, const float* faces,
+                uint32_t n_faces, const float* tgt_pos, uint32_t n_tverts,
+                const float* tgt_faces, uint32_t n_tfaces, const float* mvps,
+                uint32_t n_views, uint32_t screen_px, uint32_t samples, float lr,
+                uint32_t iters, float* out_pos, float* out_m, float* out_v,
+                float* out_t, float* out_loss, float* out_grad0, float* out_pred0,
+                float* out_target, float* out_tri0, float* out_lossimg0) {
+    return Guard([&] {
+        const ImgSize screen = {screen_px, screen_px};
+        CpuImage s_faces_img(n_faces, 1, 3);
+        std::memcpy(s_faces_img.data.data(), faces, sizeof(float) * 3 * n_faces);
+        const CpuImage s_vf_img = VertexFacesTex(s_faces_img, n_verts);
+        CpuImage b_faces_img(n_tfaces, 1, 3);
+        std::memcpy(b_faces_img.data.data(), tgt_faces, sizeof(float) * 3 * n_tfaces);
+        const CpuImage b_vf_img = VertexFacesTex(b_faces_img, n_tverts);
+
+        Variable b_ones(FLOAT, {n_tverts, 1});
+        Variable b_faces_i(IVEC3, {n_tfaces, 1});
+        Variable b_faces_f(VEC3, {n_tfaces, 1});
+        Variable b_vtx_faces(FLOAT, b_vf_img.getImgSize());
+        Variable s_ones(FLOAT, {n_verts, 1});
+        Variable s_faces_i(IVEC3, {n_faces, 1});
+        Variable s_faces_f(VEC3, {n_faces, 1});
+        Variable s_vtx_faces(FLOAT, s_vf_img.getImgSize());
+        Variable pos(VEC3, {n_verts, 1});
+        Variable adam_m(VEC3, {n_verts, 1});
+        Variable adam_v(VEC3, {n_verts, 1});
+        Variable adam_t(FLOAT, {1, 1});
+        Variable zero_seed(FLOAT, {1, 1});
+
+        std::vector<Variable> tri_vars;
+        const auto build_pred = [&](const Variable& clip_v) -> Variable {
+            Variable mask = F::Rasterize(clip_v, s_ones, s_faces_i, screen);
+            Variable tri = F::RasterizeFaceId(clip_v, s_ones, s_faces_i, screen);
+            tri_vars.push_back(tri);
+            return F::AntiAlias(mask, tri, clip_v, s_faces_f, s_vtx_faces, adam_t, samples);
+        };
+        const auto build_target = [&](const Variable& tgt_clip) -> Variable {
+            Variable t_mask = F::Rasterize(tgt_clip, b_ones, b_faces_i, screen);
+            Variable t_tri = F::RasterizeFaceId(tgt_clip, b_ones, b_faces_i, screen);
+            return F::StopGradient(F::AntiAlias(t_mask, t_tri, tgt_clip, b_faces_f,
+                                                b_vtx_faces, zero_seed, 0));
+        };
+        Variables targets, preds, view_losses;
+        std::vector<Variable> tgt_clips;
+        for (uint32_t v = 0; v < n_views; v++) {
+            tgt_clips.emplace_back(VEC4, ImgSize{n_tverts, 1});
+            targets.push_back(build_target(tgt_clips.back()));
+            preds.push_back(build_pred(ClipOf(pos, mvps + 16 * v)));
+            Variable diff = targets[v] - preds[v];
+            view_losses.push_back(diff * diff * (1.f / float(screen.w * screen.h)));
+        }
+        Variable loss = F::SumPixelWise(view_losses);
+        Variable pos_mut = pos;
+        pos_mut.setRequiresGradRecursively();
+
+        auto [xs, gxs] = BuildBackward(loss);
+        DRESSI_CHECK(xs.size() == 1 && xs[0] == pos,
+                     "expected pos as the only requires-grad leaf");
+        const Variable g = gxs[0];
+        const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+        Variable t_new = adam_t + 1.f;
+        Variable m_new = adam_m * b1 + g * (1.f - b1);
+        Variable v_new = adam_v * b2 + g * g * (1.f - b2);
+        Variable bc1 = 1.f - F::Pow(F::Float(b1), t_new);
+        Variable bc2 = 1.f - F::Pow(F::Float(b2), t_new);
+        Variable step = (m_new / bc1) / (F::Sqrt(v_new / bc2) + eps) * lr;
+        Variable pos_new = pos - step;
+
+        std::vector<float> b_ones_v(n_tverts, 1.f), s_ones_v(n_verts, 1.f);
+        CpuTensor t_b_ones = Tensor(FLOAT, {n_tverts, 1}, b_ones_v.data());
+        CpuTensor t_s_ones = Tensor(FLOAT, {n_verts, 1}, s_ones_v.data());
+        CpuTensor t_b_faces = Tensor(IVEC3, {n_tfaces, 1}, tgt_faces);
+        CpuTensor t_b_faces_f = Tensor(VEC3, {n_tfaces, 1}, tgt_faces);
+        CpuTensor t_b_vf = Tensor(FLOAT, b_vf_img.getImgSize(), b_vf_img.data.data());
+        CpuTensor t_s_faces_i = Tensor(IVEC3, {n_faces, 1}, faces);
+        CpuTensor t_s_faces = Tensor(VEC3, {n_faces, 1}, faces);
+        CpuTensor t_vf = Tensor(FLOAT, s_vf_img.getImgSize(), s_vf_img.data.data());
+        std::vector<CpuTensor> t_tgt_clips;
+        for (uint32_t v = 0; v < n_views; v++) {
+            const float* m = mvps + 16 * v;
+            CpuTensor c = Fill(VEC4, {n_tverts, 1}, 0.f);
+            for (uint32_t i = 0; i < n_tverts; i++) {
+                const float p[4] = {tgt_pos[i * 3 + 0], tgt_pos[i * 3 + 1],
+                                    tgt_pos[i * 3 + 2], 1.f};
+                for (int row = 0; row < 4; row++) {
+                    float acc = 0.f;
+                    for (int k = 0; k < 4; k++) {
+                        acc += m[k * 4 + row] * p[k];
+                    }
+                    c.data[size_t(i) * 4 + row] = acc;
+                }
+            }
+            t_tgt_clips.push_back(std::move(c));
+        }
+
+        CpuTensor t_pos = Tensor(VEC3, {n_verts, 1}, pos0);
+        CpuTensor t_m = Fill(VEC3, {n_verts, 1}, 0.f);
+        CpuTensor t_v = Fill(VEC3, {n_verts, 1}, 0.f);
+        CpuTensor t_t = Fill(FLOAT, {1, 1}, 0.f);
+        for (uint32_t it = 0; it < iters; it++) {
+            CpuEvaluator ev;
+            ev.bind(b_ones, t_b_ones);
+            ev.bind(b_faces_i, t_b_faces);
+            ev.bind(b_faces_f, t_b_faces_f);
+            ev.bind(b_vtx_faces, t_b_vf);
+            ev.bind(s_ones, t_s_ones);
+            ev.bind(s_faces_i, t_s_faces_i);
+            ev.bind(s_faces_f, t_s_faces);
+            ev.bind(s_vtx_faces, t_vf);
+            ev.bind(zero_seed, Fill(FLOAT, {1, 1}, 0.f));
+            for (uint32_t v = 0; v < n_views; v++) {
+                ev.bind(tgt_clips[v], t_tgt_clips[v]);
+            }
+            ev.bind(pos, t_pos);
+            ev.bind(adam_m, t_m);
+            ev.bind(adam_v, t_v);
+            ev.bind(adam_t, t_t);
+
+            const CpuTensor li = ev.eval(loss);
+            if (out_loss) {
+                double acc = 0.0;
+                for (float x : li.data) {
+                    acc += x;
+                }
+                out_loss[it] = float(acc);
+            }
+            if (it == 0) {
+                CopyOut(li, out_lossimg0);
+                if (out_grad0) {
+                    CopyOut(ev.eval(g), out_grad0);
+                }
+                const size_t px = size_t(screen.w) * screen.h;
+                for (uint32_t v = 0; v < n_views; v++) {
+                    if (out_pred0) {
+                        CopyOut(ev.eval(preds[v]), out_pred0 + v * px);
+                    }
+                    if (out_target) {
+                        CopyOut(ev.eval(targets[v]), out_target + v * px);
+                    }
+                    if (out_tri0) {
+                        CopyOut(ev.eval(tri_vars[v]), out_tri0 + v * px);
+                    }
+                }
+            }
+            CpuTensor n_pos = ev.eval(pos_new);
+            CpuTensor n_m = ev.eval(m_new);
+            CpuTensor n_v = ev.eval(v_new);
+            CpuTensor n_t = ev.eval(t_new);
+            t_pos = std::move(n_pos);
+            t_m = std::move(n_m);
+            t_v = std::move(n_v);
+            t_t = std::move(n_t);
+        }
+        CopyOut(t_pos, out_pos);
+        CopyOut(t_m, out_m);
+        CopyOut(t_v, out_v);
+        CopyOut(t_t, out_t);
+    });
+}
+
 }  // extern "C"

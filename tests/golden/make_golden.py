@@ -115,10 +115,63 @@ def op_fixtures(o, r):
     print("wrote ops_unit.npz", len(arrs), "arrays")
 
 
+def aa_fixtures(o, r):
+    """AntiAlias fwd / bwd scenes of tests/test_antialias.cpp:153-273 (16x16):
+    the generic-position triangle, the same with one w = 1.3 vertex, and the
+    occlusion scene (full-screen back triangle, shaded front triangle)."""
+    s = 16
+    scenes = {
+        "generic": ([clip_of_screen(4.3, 3.8, 0.5, s), clip_of_screen(12.4, 5.2, 0.5, s),
+                     clip_of_screen(5.1, 12.6, 0.5, s)], [[0, 1, 2]], None),
+        "w13": ([clip_of_screen(4.3, 3.8, 0.5, s), clip_of_screen(12.4, 5.2, 0.5, s, 1.3),
+                 clip_of_screen(5.1, 12.6, 0.5, s)], [[0, 1, 2]], None),
+        "occlusion": ([clip_of_screen(-40, -40, 0.8, s), clip_of_screen(100, -40, 0.8, s),
+                       clip_of_screen(-40, 100, 0.8, s), clip_of_screen(5.2, 4.7, 0.2, s),
+                       clip_of_screen(11.6, 6.3, 0.2, s), clip_of_screen(6.4, 11.8, 0.2, s)],
+                      [[0, 1, 2], [3, 4, 5]], [0.2, 0.2, 0.2, 0.9, 0.9, 0.9]),
+    }
+    rng = np.random.default_rng(11)
+    arrs = {}
+    for name, (clip, faces, shade) in scenes.items():
+        clip = np.array(clip, np.float32)
+        faces = np.array(faces, np.float32)
+        attr = np.ones(len(clip), np.float32) if shade is None else np.array(shade, np.float32)
+        img = r.rasterize(clip, attr, faces, s, s)[..., 0]
+        tri = r.rasterize_face_id(clip, faces, s, s)
+        vf = r.vertex_faces_tex(faces, len(clip))
+        gy = rng.standard_normal((s, s)).astype(np.float32)
+        g_img, wide, g_vtx = r.antialias_bwd(gy, img, tri, clip, faces, vf, 7.0, 8)
+        _, _, g_vtx0 = r.antialias_bwd(gy, img, tri, clip, faces, vf, 7.0, 0)
+        arrs.update({f"in_{name}_clip": clip, f"in_{name}_faces": faces,
+                     f"in_{name}_img": img, f"in_{name}_tri": tri, f"in_{name}_vf": vf,
+                     f"in_{name}_gy": gy,
+                     f"out_{name}_aa": r.antialias(img, tri, clip, faces, vf),
+                     f"out_{name}_bwd_img": g_img, f"out_{name}_bwd_vtx_wide_n8_seed7": wide,
+                     f"out_{name}_bwd_vtx_n8_seed7": g_vtx, f"out_{name}_bwd_vtx_n0": g_vtx0})
+    np.savez_compressed(os.path.join(OUT, "aa_unit.npz"), **arrs)
+    print("wrote aa_unit.npz", len(arrs), "arrays")
+
+
+def aa_fit_fixture(o, r, name, level, noise, seed, mvps, screen, iters, lr, images):
+    pos, faces = o.icosphere(level)
+    tgt = (pos * (1.0 + noise * o.randn(seed, len(pos)))[:, None]).astype(np.float32)
+    res = r.aa_fit(pos, faces, tgt, faces, mvps, screen, lr=lr, iters=iters, want_images=images)
+    arrs = dict(in_pos=pos, in_faces=faces, in_tgt_pos=tgt, in_mvps=mvps,
+                in_cfg=np.array([screen, iters, 8, lr], np.float64))
+    arrs.update({"out_" + k: v for k, v in res.items()})
+    np.savez_compressed(os.path.join(OUT, name), **arrs)
+    print("wrote", name, {k: v.shape for k, v in arrs.items()})
+
+
 def main():
     build(ref=True)
     o, r = Oracle(), Reference()
     op_fixtures(o, r)
+    aa_fixtures(o, r)
+    aa_fit_fixture(o, r, "aa_ico3_64px_5it.npz", 3, 0.05, 1, front_mvp(o), 64, 5, 1e-3, True)
+    aa_fit_fixture(o, r, "aa_ico4_4view_128px_3it.npz", 4, 0.05, 2, orbit_mvps(o, 4), 128, 3,
+                   1e-3, True)
+    aa_fit_fixture(o, r, "aa_c1_256px_50it.npz", 3, 0.05, 1, front_mvp(o), 256, 50, 1e-3, False)
     # C1-shaped fits: ico3 front camera. Small screens keep the files small;
     # the 256^2 x 50-iteration run stores only the parameter trajectory.
     fit_fixture(o, r, "hsr_ico3_64px_5it.npz", 3, 0.05, 1, front_mvp(o), 64, 5, 1e-3, True)
