@@ -29,6 +29,34 @@ METRIC = "fwd+bwd+Adam iterations/sec at 512²/2048² silhouette; achieved HBM G
 HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
 
 
+def iteration_bytes_aa(n_views: int, s: int, n_faces: int, n_verts: int) -> float:
+    """Compulsory bytes of one AA-technique iteration (per pixel and view:
+    target read, 8-byte visibility write and read; per view: clip, faces,
+    adjacency, per-vertex gradient; loss image; Adam state)."""
+    return n_views * (20.0 * s * s + 12.0 * n_faces + 88.0 * n_verts) + 4.0 * s * s + 72.0 * n_verts
+
+
+def kernel_bytes_aa(n_views: int, s: int, n_faces: int, n_verts: int, samples: int = 8) -> dict:
+    """Algorithmic bytes per launch of the AA-technique kernels.
+
+    setup:   positions (12 B/vertex) and faces in, clip (16 B/vertex) and the
+             screen triangles (36 B/face) out, per view
+    raster:  screen triangles in, 4-byte face-id image out, per view
+    fwd:     face-id + target in, pred out per view, loss image out
+    face_bwd: corner clips (48 B) in, corner gradients (48 B) out, and a
+             face-id + pred + target read (12 B) per sample, per face and view
+    vertex_adam: as the HardSoftRas vertex kernel
+    """
+    n, S2, F, V = n_views, float(s) * s, float(n_faces), float(n_verts)
+    return {
+        "k_aa_setup": n * (28.0 * V + 48.0 * F),
+        "k_aa_raster": n * (4.0 * S2 + 36.0 * F),
+        "k_aa_fwd": n * 12.0 * S2 + 4.0 * S2,
+        "k_aa_face_bwd": n * F * (96.0 + 12.0 * samples),
+        "k_aa_vertex_adam": n * 120.0 * V + 72.0 * V,
+    }
+
+
 def iteration_bytes(n_views: int, s: int, n_faces: int, n_verts: int) -> float:
     """Compulsory bytes of one HSR iteration (per pixel and view: target read,
     8-byte visibility write and read; per view: clip, soft clip, corner clips,
@@ -99,8 +127,9 @@ def cpu_baseline(workload) -> dict:
     pos, faces, tgt, mvps = od.make_scene(workload)
     o = Oracle()
     t0 = time.perf_counter()
-    o.hsr_fit(pos, faces, tgt, faces, mvps[:1], workload.screen, lr=workload.lr, iters=1,
-              want_images=False)
+    fit = o.aa_fit if workload.technique == "aa" else o.hsr_fit
+    fit(pos, faces, tgt, faces, mvps[:1], workload.screen, lr=workload.lr, iters=1,
+        want_images=False)
     dt = time.perf_counter() - t0
     per_iter = dt * len(mvps)
     return {"value": 1.0 / per_iter, "unit": "iterations/s", "cores": 1, "kind": "port",
@@ -146,9 +175,10 @@ def main() -> int:
     prof = fit.profile(args.profile_iters)
     dom = max(prof, key=prof.get)
     dom_us = prof[dom]
-    kbytes = kernel_bytes(nviews, s, nf, nv)
+    aa = w.technique == "aa"
+    kbytes = (kernel_bytes_aa if aa else kernel_bytes)(nviews, s, nf, nv)
     dbytes = kbytes[dom]
-    ibytes = iteration_bytes(nviews, s, nf, nv)
+    ibytes = (iteration_bytes_aa if aa else iteration_bytes)(nviews, s, nf, nv)
     achieved = dbytes / (dom_us * 1e-6)
     traffic = measured_traffic(dom, args.workload)
     fit.close()
@@ -166,8 +196,9 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": (f"{w.name}: HardSoftRas silhouette fit, {s}x{s} x {nviews} views, "
-                                f"icosphere L{w.level} ({nv} v / {nf} f), r=3 px, 8 samples, "
+        "config": {"workload": (f"{w.name}: {'AA' if aa else 'HardSoftRas'} silhouette fit, "
+                                f"{s}x{s} x {nviews} views, icosphere L{w.level} "
+                                f"({nv} v / {nf} f), {'' if aa else 'r=3 px, '}8 samples, "
                                 f"Adam lr {w.lr}"),
                    "screen": s, "views": nviews, "verts": nv, "faces": nf},
         "roofline": {"bound": "hbm", "kernel": dom,

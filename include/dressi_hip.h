@@ -140,6 +140,40 @@ int dressi_face_fetch_bwd(dressi_ctx* ctx, const float* gy, uint32_t n_comp,
                           const float* seed, float radius_px,
                           uint32_t n_samples, float* out);
 
+/* F::AntiAlias (src/core/f_ops.cpp:2480-2579; pair rule EvalAaPair,
+ * src/core/cpu_raster.cpp:371-454): 8-neighbour screen-space antialiasing of
+ * img {S,S} x n_comp (n_comp 1..4) given the face-id image tri {S,S} (float
+ * face + 1, 0 bg), clip {V,1} VEC4 and faces {F,3} float ids.
+ * c_aa = (c + sum_k [r c + (1 - r) c_n]) / 9. */
+int dressi_antialias(dressi_ctx* ctx, const float* img, uint32_t n_comp,
+                     const float* tri, const float* clip, uint32_t n_verts,
+                     const float* faces, uint32_t n_faces, uint32_t width,
+                     uint32_t height, float* out);
+/* AntiAliasBwdImg (src/core/f_ops.cpp:2220-2278): d c_aa / d img applied to
+ * gy {S,S} x n_comp. */
+int dressi_antialias_bwd_img(dressi_ctx* ctx, const float* gy, uint32_t n_comp,
+                             const float* tri, const float* clip,
+                             uint32_t n_verts, const float* faces,
+                             uint32_t n_faces, uint32_t width,
+                             uint32_t height, float* out);
+/* AntiAliasBwdVtx (src/core/f_ops.cpp:2284-2476): d c_aa / d clip applied
+ * to gy. n_samples > 0: the stochastic gather seeded by `seed` (device
+ * {1,1}); wide != 0 writes the {V, max_deg} VEC4 partials (row d * V + v, the
+ * input of ColSum), else {V,1}. n_samples == 0: the exact sum over every
+ * boundary pair, {V,1} VEC4 (wide must be 0). vtx_faces {V,max_deg} float,
+ * -1 pad (VertexFacesTex). */
+int dressi_antialias_bwd_vtx(dressi_ctx* ctx, const float* gy, const float* img,
+                             uint32_t n_comp, const float* tri,
+                             const float* clip, uint32_t n_verts,
+                             const float* faces, uint32_t n_faces,
+                             const float* vtx_faces, uint32_t max_deg,
+                             const float* seed, uint32_t n_samples, int wide,
+                             uint32_t width, uint32_t height, float* out);
+/* F::ColSum (src/core/f_ops.cpp:1218-1246): {W,H} x n_comp -> {W,1}, rows
+ * summed in order. */
+int dressi_col_sum(dressi_ctx* ctx, const float* x, uint32_t n_comp,
+                   uint32_t width, uint32_t height, float* out);
+
 /* ------------------------------------------------------------------------ */
 /* Host-side mesh topology and scene builders                               */
 /* ------------------------------------------------------------------------ */
@@ -200,6 +234,12 @@ typedef struct dressi_hsr_desc {
 /* Keep d loss / d pos of the last iteration readable (setGradOutputsEnabled,
  * include/dressi/dressi_ad.h:362-370). */
 #define DRESSI_HSR_KEEP_GRAD 2u
+/* Technique "aa" of the example (run.cpp:231-238, 352-356) instead of
+ * HardSoftRas: pred = AntiAlias(Rasterize(clip, 1), RasterizeFaceId(clip),
+ * ...), target = StopGradient(AntiAlias of the target mask), vertex
+ * gradients from AntiAliasBwdVtx (wide, n_samples, seed t) + ColSum.
+ * radius_px is unused; pred is always kept. */
+#define DRESSI_HSR_TECHNIQUE_AA 4u
 
 int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc,
                       dressi_hsr_plan** out);
@@ -235,7 +275,8 @@ enum dressi_hsr_buffer {
     DRESSI_HSR_TARGET = 2,  /* {N,S,S} float */
     DRESSI_HSR_FACE_ID = 3, /* {N,S,S} uint32: face + 1 of RasterizeSoft, 0 bg;
                                bit 31 set when the winning fragment lies
-                               outside its hard triangle (signed dist < 0) */
+                               outside its hard triangle (signed dist < 0).
+                               Technique aa: RasterizeFaceId, no flag bit */
     DRESSI_HSR_GRAD = 4,    /* {V,3} float (needs DRESSI_HSR_KEEP_GRAD) */
     DRESSI_HSR_POS = 5      /* {V,3} float */
 };

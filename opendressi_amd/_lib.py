@@ -33,6 +33,7 @@ class HsrDesc(C.Structure):
 
 HSR_KEEP_PRED = 1
 HSR_KEEP_GRAD = 2
+HSR_TECHNIQUE_AA = 4
 BUF_LOSS, BUF_PRED, BUF_TARGET, BUF_FACE_ID, BUF_GRAD, BUF_POS = range(6)
 FACE_ID_RIM = 0x80000000  # bit of a face-id entry: winner outside its hard triangle
 
@@ -59,6 +60,11 @@ _SIGS = {
     "dressi_lookup_faces_bwd": (_I, [_P, _P, _U, _P, _U, _P, _U, _U, _U, _P]),
     "dressi_face_fetch": (_I, [_P, _P, _U, _U, _P, _U, _U, _P]),
     "dressi_face_fetch_bwd": (_I, [_P, _P, _U, _P, _U, _U, _P, _P, _P, _U, _P, _F, _U, _P]),
+    "dressi_antialias": (_I, [_P, _P, _U, _P, _P, _U, _P, _U, _U, _U, _P]),
+    "dressi_antialias_bwd_img": (_I, [_P, _P, _U, _P, _P, _U, _P, _U, _U, _U, _P]),
+    "dressi_antialias_bwd_vtx": (_I, [_P, _P, _P, _U, _P, _P, _U, _P, _U, _P, _U, _P, _U, _I,
+                                      _U, _U, _P]),
+    "dressi_col_sum": (_I, [_P, _P, _U, _U, _U, _P]),
     "dressi_icosphere": (_I, [_U, _UP, _UP, _FP, _FP]),
     "dressi_vertex_faces_tex": (_I, [_FP, _U, _U, _UP, _FP, _S]),
     "dressi_look_at": (None, [_FP, _FP, _FP, _FP]),

@@ -1,0 +1,861 @@
+// aa.hip -- screen-space antialiasing (the reference's technique "aa",
+// Dr.Hair-style AA): the per-op AntiAlias / AntiAliasBwdImg /
+// AntiAliasBwdVtx / ColSum entry points and the kernels of the fused AA
+// silhouette iteration (hard raster -> AntiAlias -> L2 -> stochastic vertex
+// gather -> ColSum -> clip->pos -> Adam).
+#include "plan.h"
+
+namespace dressi {
+
+namespace {
+
+__device__ __forceinline__ uint32_t tri_id(const float* tri, size_t o) {
+    return (uint32_t)(int)(tri[o] + 0.5f);  // int(tri + 0.5f) (cpu_raster.cpp:374-375)
+}
+
+// Reference-layout accessors of the per-op kernels: faces as float ids
+// (int64(v + 0.5f), cpu_raster.cpp:395), clip {V,1} VEC4.
+struct FloatFaces {
+    const float* faces;
+    __device__ uint32_t operator()(uint32_t f, int k) const {
+        return (uint32_t)(int64_t)(faces[(size_t)f * 3 + k] + 0.5f);
+    }
+};
+
+// Owner triangles of the fused iteration: vertex ids from the int32 faces,
+// screen corners from the view's setup records (the same ProjectClipToScreen
+// values). Owners come from the face-id buffer, so every one of them won a
+// pixel and has all corners in front of the camera.
+struct TriFromRecs {
+    const int32_t* faces;
+    const AaRec* recs;
+    __device__ bool operator()(uint32_t f, uint32_t vi[3], float qx[3], float qy[3]) const {
+        const AaRec& r = recs[f];
+        for (int k = 0; k < 3; k++) {
+            vi[k] = (uint32_t)faces[f * 3 + k];
+            qx[k] = r.x[k];
+            qy[k] = r.y[k];
+        }
+        return true;
+    }
+};
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Per-op kernels (reference layouts: float face-id image, float faces)
+// ---------------------------------------------------------------------------
+
+// AntiAlias forward (f_ops.cpp:2544-2576), one thread per pixel.
+__global__ __launch_bounds__(256) void k_antialias_op(const float* img, uint32_t n_comp,
+                                                      const float* tri, const float4* clip,
+                                                      uint32_t n_verts, const float* faces,
+                                                      uint32_t n_faces, uint32_t w, uint32_t h,
+                                                      float* out) {
+    const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= w * h) {
+        return;
+    }
+    const int x = (int)(p % w), y = (int)(p / w);
+    const float W = (float)w, H = (float)h;
+    const size_t so = (size_t)p * n_comp;
+    float dst[4];
+    for (uint32_t c = 0; c < n_comp; c++) {
+        dst[c] = img[so + c];
+    }
+    const uint32_t its = tri_id(tri, p);
+    for (int k = 0; k < 8; k++) {
+        const int nx = x + kAaOffX[k], ny = y + kAaOffY[k];
+        AaPair pr;
+        const bool in = !(nx < 0 || ny < 0 || nx >= (int)w || ny >= (int)h);
+        if (!in || !eval_aa_pair(its, tri_id(tri, (size_t)ny * w + nx), x, y, nx, ny, n_faces,
+                                 TriFromClip{faces, clip, n_verts, W, H}, &pr)) {
+            for (uint32_t c = 0; c < n_comp; c++) {
+                dst[c] += img[so + c];
+            }
+            continue;
+        }
+        const size_t no = ((size_t)ny * w + nx) * n_comp;
+        for (uint32_t c = 0; c < n_comp; c++) {
+            dst[c] += pr.r * img[so + c] + (1.f - pr.r) * img[no + c];
+        }
+    }
+    for (uint32_t c = 0; c < n_comp; c++) {
+        out[so + c] = dst[c] / 9.f;
+    }
+}
+
+// AntiAliasBwdImg (f_ops.cpp:2231-2275), one thread per pixel.
+__global__ __launch_bounds__(256) void k_antialias_bwd_img_op(const float* gy, uint32_t n_comp,
+                                                              const float* tri, const float4* clip,
+                                                              uint32_t n_verts, const float* faces,
+                                                              uint32_t n_faces, uint32_t w,
+                                                              uint32_t h, float* out) {
+    const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= w * h) {
+        return;
+    }
+    const int x = (int)(p % w), y = (int)(p / w);
+    const float W = (float)w, H = (float)h;
+    const size_t so = (size_t)p * n_comp;
+    float dst[4] = {0.f, 0.f, 0.f, 0.f};
+    float alpha_sum = 0.f;
+    const uint32_t its = tri_id(tri, p);
+    for (int k = 0; k < 8; k++) {
+        const int nx = x + kAaOffX[k], ny = y + kAaOffY[k];
+        if (nx < 0 || ny < 0 || nx >= (int)w || ny >= (int)h) {
+            alpha_sum += 1.f;
+            continue;
+        }
+        const uint32_t itn = tri_id(tri, (size_t)ny * w + nx);
+        AaPair pr;
+        alpha_sum += eval_aa_pair(its, itn, x, y, nx, ny, n_faces,
+                                  TriFromClip{faces, clip, n_verts, W, H}, &pr)
+                             ? pr.r
+                             : 1.f;
+        AaPair pr2;
+        if (eval_aa_pair(itn, its, nx, ny, x, y, n_faces, TriFromClip{faces, clip, n_verts, W, H},
+                         &pr2)) {
+            const size_t no = ((size_t)ny * w + nx) * n_comp;
+            for (uint32_t c = 0; c < n_comp; c++) {
+                dst[c] += (1.f - pr2.r) * gy[no + c];
+            }
+        }
+    }
+    for (uint32_t c = 0; c < n_comp; c++) {
+        dst[c] += gy[so + c] * (1.f + alpha_sum);
+        out[so + c] = dst[c] / 9.f;
+    }
+}
+
+// One active pair's contribution to vertex v's row (f_ops.cpp:2345-2386,
+// only_v): gr = dot(gy(s), c(s) - c(n)) / 9, then each endpoint equal to v.
+__device__ __forceinline__ void aa_accumulate_v(const float* gy, const float* img,
+                                                uint32_t n_comp, const float4* clip, float W,
+                                                float H, uint32_t w, uint32_t v, int x, int y,
+                                                int nx, int ny, const AaPair& pr, float4* dst) {
+    const size_t so = ((size_t)y * w + x) * n_comp;
+    const size_t no = ((size_t)ny * w + nx) * n_comp;
+    float gr = 0.f;
+    for (uint32_t c = 0; c < n_comp; c++) {
+        gr += gy[so + c] * (img[so + c] - img[no + c]);
+    }
+    gr /= 9.f;
+    if (gr == 0.f) {
+        return;
+    }
+    float dqa[2], dqb[2];
+    aa_pair_dq(pr, x, y, dqa, dqb);
+    if (pr.ia == v) {
+        aa_add_endpoint(gr, dqa, clip[pr.ia], W, H, dst);
+    }
+    if (pr.ib == v) {
+        aa_add_endpoint(gr, dqb, clip[pr.ib], W, H, dst);
+    }
+}
+
+// AntiAliasBwdVtx, n_samples > 0 (f_ops.cpp:2410-2472): one thread per
+// (vertex, slot) row when `wide` (out {V, deg} VEC4, row d * V + v), else one
+// thread per vertex accumulating its slots in order (out {V,1}).
+__global__ __launch_bounds__(256) void k_antialias_bwd_vtx_op(
+        const float* gy, const float* img, uint32_t n_comp, const float* tri, const float4* clip,
+        uint32_t n_verts, const float* faces, uint32_t n_faces, const float* vtx_faces,
+        uint32_t max_deg, const float* seed, uint32_t n_samples, int wide, uint32_t w, uint32_t h,
+        float4* out) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t rows = wide ? max_deg : 1u;
+    if (i >= n_verts * rows) {
+        return;
+    }
+    const uint32_t v = wide ? i % n_verts : i;
+    const uint32_t d0 = wide ? i / n_verts : 0u;
+    const uint32_t d1 = wide ? d0 + 1 : max_deg;
+    const float W = (float)w, H = (float)h;
+    const uint32_t seed_u = (uint32_t)(int64_t)(*seed + 0.5f);
+    float4 dst = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t d = d0; d < d1; d++) {
+        const float fv = vtx_faces[(size_t)d * n_verts + v];
+        if (fv < -0.5f) {
+            continue;
+        }
+        const uint32_t f = (uint32_t)(int64_t)(fv + 0.5f);
+        if (f >= n_faces) {
+            continue;
+        }
+        float4 c[3];
+        bool ok = true;
+        for (int k = 0; k < 3; k++) {
+            const uint32_t vi = FloatFaces{faces}(f, k);
+            if (vi >= n_verts) {
+                ok = false;
+                break;
+            }
+            c[k] = clip[vi];
+        }
+        float s3x[3], s3y[3];
+        if (!ok || !aa_face_screen(c, W, H, s3x, s3y)) {
+            continue;
+        }
+        for (uint32_t smp = 0; smp < n_samples; smp++) {
+            int x, y;
+            if (!aa_sample_px(s3x, s3y, f, smp, seed_u, &x, &y) || x < 0 || y < 0 ||
+                x >= (int)w || y >= (int)h) {
+                continue;
+            }
+            const uint32_t its = tri_id(tri, (size_t)y * w + x);
+            for (int k = 0; k < 8; k++) {
+                const int nx = x + kAaOffX[k], ny = y + kAaOffY[k];
+                if (nx < 0 || ny < 0 || nx >= (int)w || ny >= (int)h) {
+                    continue;
+                }
+                AaPair pr;
+                if (!eval_aa_pair(its, tri_id(tri, (size_t)ny * w + nx), x, y, nx, ny, n_faces,
+                                  TriFromClip{faces, clip, n_verts, W, H}, &pr) ||
+                    pr.r >= 1.f) {
+                    continue;
+                }
+                if (pr.ia != v && pr.ib != v) {
+                    continue;
+                }
+                aa_accumulate_v(gy, img, n_comp, clip, W, H, w, v, x, y, nx, ny, pr, &dst);
+            }
+        }
+    }
+    out[i] = dst;
+}
+
+// AntiAliasBwdVtx, n_samples = 0 (f_ops.cpp:2389-2407): the exact scatter
+// over every active pair, restated as a gather per vertex that visits the
+// pixels of its incident faces' bboxes (+-1 px) in the scatter's raster order,
+// so every vertex's sum has the reference's order. An active pair's edge
+// belongs to a face covering s or its neighbour, so no pair of v's lies
+// outside those pixels.
+__global__ __launch_bounds__(128) void k_antialias_bwd_vtx_exact_op(
+        const float* gy, const float* img, uint32_t n_comp, const float* tri, const float4* clip,
+        uint32_t n_verts, const float* faces, uint32_t n_faces, const float* vtx_faces,
+        uint32_t max_deg, uint32_t w, uint32_t h, float4* out) {
+    const uint32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= n_verts) {
+        return;
+    }
+    const float W = (float)w, H = (float)h;
+    int bx0 = (int)w, by0 = (int)h, bx1 = -1, by1 = -1;
+    for (uint32_t d = 0; d < max_deg; d++) {
+        const float fv = vtx_faces[(size_t)d * n_verts + v];
+        if (fv < -0.5f) {
+            continue;
+        }
+        const uint32_t f = (uint32_t)(int64_t)(fv + 0.5f);
+        if (f >= n_faces) {
+            continue;
+        }
+        float qx[3], qy[3];
+        bool ok = true;
+        for (int k = 0; k < 3 && ok; k++) {
+            const uint32_t vi = FloatFaces{faces}(f, k);
+            ok = vi < n_verts && clip_w_valid(clip[vi].w);
+            if (ok) {
+                const float4 c = clip[vi];
+                const ScreenVert s = project_to_screen(c.x, c.y, c.z, c.w, W, H);
+                qx[k] = s.x;
+                qy[k] = s.y;
+            }
+        }
+        if (!ok) {
+            continue;  // never an owner (EvalAaPair skips it)
+        }
+        int fx0, fy0, fx1, fy1;
+        pixel_bbox(qx[0], qx[1], qx[2], qy[0], qy[1], qy[2], (int)w, (int)h, &fx0, &fy0, &fx1,
+                   &fy1);
+        bx0 = min(bx0, fx0 - 1);
+        by0 = min(by0, fy0 - 1);
+        bx1 = max(bx1, fx1 + 1);
+        by1 = max(by1, fy1 + 1);
+    }
+    bx0 = max(bx0, 0);
+    by0 = max(by0, 0);
+    bx1 = min(bx1, (int)w - 1);
+    by1 = min(by1, (int)h - 1);
+    float4 dst = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int y = by0; y <= by1; y++) {
+        for (int x = bx0; x <= bx1; x++) {
+            const uint32_t its = tri_id(tri, (size_t)y * w + x);
+            for (int k = 0; k < 8; k++) {
+                const int nx = x + kAaOffX[k], ny = y + kAaOffY[k];
+                if (nx < 0 || ny < 0 || nx >= (int)w || ny >= (int)h) {
+                    continue;
+                }
+                AaPair pr;
+                if (!eval_aa_pair(its, tri_id(tri, (size_t)ny * w + nx), x, y, nx, ny, n_faces,
+                                  TriFromClip{faces, clip, n_verts, W, H}, &pr) ||
+                    pr.r >= 1.f || (pr.ia != v && pr.ib != v)) {
+                    continue;
+                }
+                aa_accumulate_v(gy, img, n_comp, clip, W, H, w, v, x, y, nx, ny, pr, &dst);
+            }
+        }
+    }
+    out[v] = dst;
+}
+
+// ColSum (f_ops.cpp:1227-1244): rows summed in order per column and component.
+__global__ __launch_bounds__(256) void k_col_sum_op(const float* x, uint32_t n_comp, uint32_t w,
+                                                    uint32_t h, float* out) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= w * n_comp) {
+        return;
+    }
+    float acc = 0.f;
+    for (uint32_t r = 0; r < h; r++) {
+        acc += x[(size_t)r * w * n_comp + i];
+    }
+    out[i] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Fused AA iteration
+// ---------------------------------------------------------------------------
+
+// Per-view clip positions: TransformToClipVar of every vertex.
+__global__ __launch_bounds__(256) void k_aa_clip(HsrDev d) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= d.g.n_views * d.n_verts) {
+        return;
+    }
+    const uint32_t view = i / d.n_verts;
+    const uint32_t v = i - view * d.n_verts;
+    d.clip[i] = mvp_transform(d.mvps + view * 16, d.pos[v * 3 + 0], d.pos[v * 3 + 1],
+                              d.pos[v * 3 + 2]);
+}
+
+// Hard raster setup per (view, face) (RasterizeCore, cpu_raster.cpp:42-94)
+// with the coverage margin of the block cull, appended to the tile bins.
+__global__ __launch_bounds__(256) void k_aa_setup(HsrDev d) {
+    __shared__ BinLds blds;
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = i < d.g.n_views * d.g.n_faces;
+    const uint32_t view = live ? i / d.g.n_faces : 0;
+    const uint32_t f = live ? i - view * d.g.n_faces : 0;
+    AaRec r;
+    r.bx0 = 1;
+    r.bx1 = 0;
+    r.by0 = 1;
+    r.by1 = 0;
+    r.margin = -1.f;
+    if (live) {
+        const float W = (float)d.g.width, H = (float)d.g.height;
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            const float4 c = d.clip[(size_t)view * d.n_verts + d.faces[f * 3 + k]];
+            ok = ok && !(fabsf(c.w) <= kWEps || c.w < 0.f);
+            const ScreenVert s = project_to_screen(c.x, c.y, c.z, c.w, W, H);
+            r.x[k] = s.x;
+            r.y[k] = s.y;
+            r.z[k] = s.z;
+        }
+        if (ok) {
+            const float area = tri_area(r.x[0], r.y[0], r.x[1], r.y[1], r.x[2], r.y[2]);
+            if (!(fabsf(area) < kDistEps)) {
+                r.inv_area = 1.f / area;
+                // coverage margin: the soft raster's bound for the same
+                // barycentric formula (raster_core.h, soft_setup)
+                float q = 0.f;
+                for (int k = 0; k < 3; k++) {
+                    const int k1 = (k + 1) % 3;
+                    q += (fabsf(r.x[k]) + fabsf(r.x[k1]) + W) *
+                         (fabsf(r.y[k]) + fabsf(r.y[k1]) + H);
+                }
+                const float pa = fabsf(r.x[1] - r.x[0]) * fabsf(r.y[2] - r.y[0]) +
+                                 fabsf(r.y[1] - r.y[0]) * fabsf(r.x[2] - r.x[0]);
+                const float m = 0x1p-20f * (q + pa + fabsf(area));
+                r.margin = (fabsf(area) > 0x1p-20f * pa && m < INFINITY) ? m : -1.f;
+                pixel_bbox(r.x[0], r.x[1], r.x[2], r.y[0], r.y[1], r.y[2], (int)d.g.width,
+                           (int)d.g.height, &r.bx0, &r.by0, &r.bx1, &r.by1);
+            }
+        }
+        d.arecs[i] = r;
+    }
+    const bool valid = live && r.bx0 <= r.bx1 && r.by0 <= r.by1;
+    bin_append(d.bins, d.g, valid, view, f, r.bx0, r.by0, r.bx1, r.by1, blds);
+}
+
+// Separating-axis test of a hard triangle's coverage region (its
+// barycentrics >= 0 up to the record's margin) against the 8x8 block.
+__device__ __forceinline__ bool aa_tri_reaches_block(const AaRec* rec, int bx, int by) {
+    const float4 a = *(const float4*)&rec->x[0];  // x0 x1 x2 y0
+    const float4 b = *(const float4*)&rec->y[1];  // y1 y2 inv_area margin
+    const float m = b.w;
+    if (!(m >= 0.f)) {
+        return true;
+    }
+    const float x[3] = {a.x, a.y, a.z};
+    const float y[3] = {a.w, b.x, b.y};
+    const float s = b.z > 0.f ? 1.f : -1.f;
+    const float x0 = (float)bx + 0.5f, x1 = (float)bx + 7.5f;
+    const float y0 = (float)by + 0.5f, y1 = (float)by + 7.5f;
+    bool hit = true;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        const int k1 = (k + 1) % 3;
+        const float ex = s * (x[k1] - x[k]);
+        const float ey = s * (y[k1] - y[k]);
+        const float g = smax(ex * (y0 - y[k]), ex * (y1 - y[k])) +
+                        smax(-ey * (x0 - x[k]), -ey * (x1 - x[k]));
+        hit = hit && !(g < -m);
+    }
+    return hit;
+}
+
+typedef const __attribute__((address_space(4))) uint32_t* AaUniformWordPtr;
+
+__device__ __forceinline__ AaRec load_aa_rec_uniform(const AaRec* recs, uint32_t f) {
+    const AaUniformWordPtr src = (AaUniformWordPtr)(recs + f);
+    union {
+        AaRec r;
+        uint32_t w[16];
+    } u;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        u.w[i] = src[i];
+    }
+    return u.r;
+}
+
+// Visibility of the hard raster: one single-wave workgroup per (view, 8x8
+// block) folds (z | ~face) keys of the faces binned to its tile (coverage by
+// the reference's inclusive barycentrics, NDC z in [0,1], LessOrEqual: the
+// later face wins ties) and writes face + 1 (0 = background). Tiles are dealt
+// to the XCDs round robin, the four blocks of a tile on one XCD.
+__global__ __launch_bounds__(64) void k_aa_raster(HsrDev d) {
+    const uint32_t per = (d.g.n_tiles + 7u) / 8u;
+    const uint32_t k = blockIdx.x >> 3;
+    const uint32_t q = k & 3u;
+    const uint32_t view = (k >> 2) % d.g.n_views;
+    const uint32_t lt = (k >> 2) / d.g.n_views;
+    const uint32_t tile = lt * 8u + (blockIdx.x & 7u);
+    const int bx = (int)((tile % d.g.tiles_x) * kTile + (q & 1u) * 8u);
+    const int by = (int)((tile / d.g.tiles_x) * kTile + (q >> 1) * 8u);
+    if (lt >= per || tile >= d.g.n_tiles || bx >= (int)d.g.width || by >= (int)d.g.height) {
+        return;
+    }
+    const int lane = threadIdx.x & 63;
+    const int px = bx + (lane & 7);
+    const int py = by + (lane >> 3);
+    const float p0 = (float)px + 0.5f, p1 = (float)py + 0.5f;
+    const AaRec* recs = d.arecs + (size_t)view * d.g.n_faces;
+    const BinView bv = bin_view(d.bins, view * d.g.n_tiles + tile, d.g.n_faces);
+    uint64_t best = kEmptyKey;
+    for (uint32_t base = 0; base < bv.n; base += 64) {
+        const uint32_t e = base + (uint32_t)lane;
+        uint32_t f = 0;
+        bool keep = false;
+        if (e < bv.n) {
+            f = bv.implicit ? e : bv.list[e];
+            const int4 bb = *(const int4*)&recs[f].bx0;
+            keep = bb.x <= bx + 7 && bb.z >= bx && bb.y <= by + 7 && bb.w >= by &&
+                   aa_tri_reaches_block(recs + f, bx, by);
+        }
+        uint64_t m = __ballot(keep);
+        while (m) {
+            const int j = __builtin_ctzll(m);
+            m &= m - 1;
+            const uint32_t fj = (uint32_t)__builtin_amdgcn_readlane((int)f, j);
+            const AaRec r = load_aa_rec_uniform(recs, fj);
+            if (px < r.bx0 || px > r.bx1 || py < r.by0 || py > r.by1) {
+                continue;
+            }
+            float l0, l1, l2;
+            barycentric(p0, p1, r.x[0], r.y[0], r.x[1], r.y[1], r.x[2], r.y[2], r.inv_area,
+                        &l0, &l1, &l2);
+            if (l0 < 0.f || l1 < 0.f || l2 < 0.f) {
+                continue;
+            }
+            const float z = l0 * r.z[0] + l1 * r.z[1] + l2 * r.z[2];
+            if (z < 0.f || z > 1.f) {
+                continue;
+            }
+            const uint64_t key = depth_key(z, fj);
+            best = key < best ? key : best;
+        }
+    }
+    if (px < (int)d.g.width && py < (int)d.g.height) {
+        d.ids[(size_t)view * d.g.width * d.g.height + (size_t)py * d.g.width + px] =
+                best == kEmptyKey ? 0u : key_face(best) + 1;
+    }
+}
+
+// AntiAlias of the mask (Rasterize(clip, 1): 1 exactly where covered) and the
+// L2 loss: one wave per view over 64 pixels of a row, the views of the same
+// pixels in one workgroup, their SumPixelWise reduced through LDS. pred is
+// kept for the vertex gather (which rebuilds d loss / d pred from it).
+template <int NV>
+__global__ __launch_bounds__(64 * NV) void k_aa_fwd(HsrDev d) {
+    __shared__ float lv[NV][64];
+    const uint32_t view = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const uint32_t w = d.g.width, h = d.g.height;
+    const uint32_t x = blockIdx.x * 64 + (uint32_t)lane;
+    const uint32_t y = blockIdx.y;
+    const bool on = x < w;
+    const size_t npx = (size_t)w * h;
+    const size_t o = (size_t)y * w + x;
+    float l = 0.f;
+    if (on) {
+        const uint32_t* ids = d.ids + view * npx;
+        const TriFromRecs tris{d.faces, d.arecs + (size_t)view * d.g.n_faces};
+        const uint32_t its = ids[o];
+        // all eight neighbour ids first (one load latency); an off-screen
+        // neighbour adds c like an inactive pair, so it reads as its own id
+        uint32_t itn[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int nx = (int)x + kAaOffX[k], ny = (int)y + kAaOffY[k];
+            const bool in = !(nx < 0 || ny < 0 || nx >= (int)w || ny >= (int)h);
+            itn[k] = in ? ids[(size_t)ny * w + nx] : its;
+        }
+        const float cs = its ? 1.f : 0.f;
+        float dst = cs;
+        for (int k = 0; k < 8; k++) {
+            const int nx = (int)x + kAaOffX[k], ny = (int)y + kAaOffY[k];
+            AaPair pr;
+            if (!eval_aa_pair(its, itn[k], (int)x, (int)y, nx, ny, d.g.n_faces, tris, &pr)) {
+                dst += cs;
+                continue;
+            }
+            const float cn = itn[k] ? 1.f : 0.f;
+            dst += pr.r * cs + (1.f - pr.r) * cn;
+        }
+        const float pred = dst / 9.f;
+        d.pred[view * npx + o] = pred;
+        const float diff = d.targets[view * npx + o] - pred;
+        l = diff * diff * d.inv_px;
+    }
+    lv[view][lane] = l;
+    __syncthreads();
+    if (view == 0 && on) {
+        float in[NV][1];
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            in[k][0] = lv[k][lane];
+        }
+        float out[1];
+        Tree<NV, 1>::run(in, out);
+        d.loss[o] = out[0];
+    }
+}
+
+constexpr int kAaBatch = 8;  // samples whose loads are issued together
+
+// AntiAliasBwdVtx (stochastic, wide) fused per (view, face): the face's n
+// samples (salts 2 and 3, seed = t) are shared by its three corner slots, so
+// they are evaluated once and each active pair adds into the accumulator of
+// every corner that is an endpoint of its edge -- per corner the same
+// (sample, neighbour, endpoint) sequence as the reference's (vertex, slot)
+// row. Pairs whose two pixels have the same mask value carry gr = 0 and are
+// skipped before the pair evaluation. Also clears the bin counters.
+__global__ __launch_bounds__(256) void k_aa_face_bwd(HsrDev d) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    for (uint32_t b = i; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
+        d.bins.counts[b] = 0;
+    }
+    if (i >= d.g.n_views * d.g.n_faces) {
+        return;
+    }
+    const uint32_t view = i / d.g.n_faces;
+    const uint32_t f = i - view * d.g.n_faces;
+    const uint32_t w = d.g.width, h = d.g.height;
+    const float W = (float)w, H = (float)h;
+    const size_t npx = (size_t)w * h;
+    const uint32_t* ids = d.ids + view * npx;
+    const float* pred = d.pred + view * npx;
+    const float* tgt = d.targets + view * npx;
+    const float4* clip = d.clip + (size_t)view * d.n_verts;
+    uint32_t vc[3];
+    float4 c[3];
+    float4 acc[3];
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        vc[k] = (uint32_t)d.faces[f * 3 + k];
+        c[k] = clip[vc[k]];
+        acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float s3x[3], s3y[3];
+    if (d.n_samples > 0 && aa_face_screen(c, W, H, s3x, s3y)) {
+        const uint32_t seed_u = (uint32_t)(int64_t)(*d.t + 0.5f);
+        for (uint32_t s0 = 0; s0 < d.n_samples; s0 += kAaBatch) {
+            // a batch of samples: positions, then their pred / target loads
+            // together, then the pairs of the samples that carry gradient
+            int sx[kAaBatch], sy[kAaBatch];
+            float gys[kAaBatch];
+#pragma unroll
+            for (int b = 0; b < kAaBatch; b++) {
+                const uint32_t smp = s0 + b;
+                const bool ok = smp < d.n_samples &&
+                                aa_sample_px(s3x, s3y, f, smp, seed_u, &sx[b], &sy[b]) &&
+                                !(sx[b] < 0 || sy[b] < 0 || sx[b] >= (int)w || sy[b] >= (int)h);
+                if (!ok) {
+                    sx[b] = -1;
+                    gys[b] = 0.f;
+                    continue;
+                }
+                const size_t so = (size_t)sy[b] * w + sx[b];
+                // d loss / d pred at s: diff = target - pred, -(c diff + c diff)
+                const float diff = tgt[so] - pred[so];
+                const float cd = d.inv_px * diff;
+                gys[b] = -(cd + cd);
+            }
+#pragma unroll 1
+            for (int b = 0; b < kAaBatch; b++) {
+            // gy = 0 makes every pair's gr exactly 0
+            const float gy = gys[b];
+            if (sx[b] < 0 || gy == 0.f) {
+                continue;
+            }
+            const int x = sx[b], y = sy[b];
+            const size_t so = (size_t)y * w + x;
+            const uint32_t its = ids[so];
+            const float ms = its ? 1.f : 0.f;
+            for (int k = 0; k < 8; k++) {
+                const int nx = x + kAaOffX[k], ny = y + kAaOffY[k];
+                if (nx < 0 || ny < 0 || nx >= (int)w || ny >= (int)h) {
+                    continue;
+                }
+                const uint32_t itn = ids[(size_t)ny * w + nx];
+                const float mn = itn ? 1.f : 0.f;
+                float gr = 0.f;
+                gr += gy * (ms - mn);
+                gr /= 9.f;
+                if (gr == 0.f) {
+                    continue;
+                }
+                AaPair pr;
+                if (!eval_aa_pair(its, itn, x, y, nx, ny, d.g.n_faces,
+                                  TriFromRecs{d.faces, d.arecs + (size_t)view * d.g.n_faces},
+                                  &pr) ||
+                    pr.r >= 1.f) {
+                    continue;
+                }
+                float dqa[2], dqb[2];
+                aa_pair_dq(pr, x, y, dqa, dqb);
+#pragma unroll
+                for (int kc = 0; kc < 3; kc++) {
+                    if (pr.ia == vc[kc]) {
+                        aa_add_endpoint(gr, dqa, clip[pr.ia], W, H, &acc[kc]);
+                    }
+                    if (pr.ib == vc[kc]) {
+                        aa_add_endpoint(gr, dqb, clip[pr.ib], W, H, &acc[kc]);
+                    }
+                }
+            }
+            }
+        }
+    }
+    float4* dst = d.gtri + (size_t)view * 3 * d.g.n_faces;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        dst[(size_t)k * d.g.n_faces + f] = acc[k];
+    }
+}
+
+// ColSum of the (vertex, slot) rows per view -- the row of slot d is the
+// accumulator of face vf[d][v] at the corner holding v; padding rows are
+// zero -- then the shared clip->pos chain and Adam; the last workgroup
+// advances t.
+template <int NV>
+__global__ __launch_bounds__(256) void k_aa_vertex_adam(HsrDev d) {
+    const uint32_t vtx = blockIdx.x * blockDim.x + threadIdx.x;
+    const float t = *d.t;
+    if (vtx < d.n_verts) {
+        float gc[NV][4];
+#pragma unroll
+        for (int view = 0; view < NV; view++) {
+            const float4* gt = d.gtri + (size_t)view * 3 * d.g.n_faces;
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            for (uint32_t dd = 0; dd < d.max_deg; dd++) {
+                const int32_t f = d.vf[(size_t)dd * d.n_verts + vtx];
+                if (f < 0) {
+                    continue;  // a zero row: adding +0 leaves the sum unchanged
+                }
+                const uint32_t mask = d.vf_mask[(size_t)dd * d.n_verts + vtx];
+                const int k = (mask & 1u) ? 0 : ((mask & 2u) ? 1 : 2);
+                const float4 gg = gt[(size_t)k * d.g.n_faces + f];
+                acc[0] += gg.x;
+                acc[1] += gg.y;
+                acc[2] += gg.z;
+                acc[3] += gg.w;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                gc[view][r] = acc[r];
+            }
+        }
+        pos_grad_adam<NV>(d, vtx, gc, t);
+    }
+    advance_t(d, t);
+}
+
+const char* const kAaKernelNames[kAaKernels] = {"k_aa_setup", "k_aa_raster", "k_aa_fwd",
+                                                "k_aa_face_bwd", "k_aa_vertex_adam"};
+
+int launch_aa_kernel(const HsrDev& d, hipStream_t s, int k) {
+    const RasterGeom& g = d.g;
+    const uint32_t nvf = g.n_views * g.n_faces;
+    switch (k) {
+        case 0:
+            hipLaunchKernelGGL(k_aa_clip, dim3(div_up(g.n_views * d.n_verts, 256)), dim3(256), 0,
+                               s, d);
+            DRESSI_CHECK_LAUNCH();
+            hipLaunchKernelGGL(k_aa_setup, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
+            break;
+        case 1:
+            hipLaunchKernelGGL(k_aa_raster, dim3(32u * g.n_views * div_up(g.n_tiles, 8)),
+                               dim3(64), 0, s, d);
+            break;
+        case 2:
+        case 4: {
+            const dim3 grid = k == 2 ? dim3(div_up(g.width, 64), g.height)
+                                     : dim3(div_up(d.n_verts, 256));
+            switch (g.n_views) {
+#define DRESSI_NV(N)                                                                      \
+    case N:                                                                               \
+        if (k == 2) {                                                                     \
+            hipLaunchKernelGGL(k_aa_fwd<N>, grid, dim3(64 * N), 0, s, d);                 \
+        } else {                                                                          \
+            hipLaunchKernelGGL(k_aa_vertex_adam<N>, grid, dim3(256), 0, s, d);            \
+        }                                                                                 \
+        break;
+                DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
+                DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)
+#undef DRESSI_NV
+                default:
+                    set_error("n_views %u unsupported", g.n_views);
+                    return DRESSI_ERR_UNSUPPORTED;
+            }
+            break;
+        }
+        default:
+            hipLaunchKernelGGL(k_aa_face_bwd, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
+            break;
+    }
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+}  // namespace dressi
+
+using namespace dressi;
+
+namespace {
+
+int check_aa_args(dressi_ctx* ctx, uint32_t n_comp, uint32_t w, uint32_t h) {
+    DRESSI_REQUIRE(ctx, "NULL context");
+    DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "AntiAlias: n_comp must be 1..4");
+    DRESSI_REQUIRE(w > 0 && h > 0, "AntiAlias: empty image");
+    DRESSI_TRY_HIP(hipSetDevice(ctx->device));
+    return DRESSI_OK;
+}
+
+}  // namespace
+
+namespace dressi {
+
+int aa_render_target(dressi_ctx* ctx, const float* tgt_clip_dev, uint32_t n_tverts,
+                     const float* tgt_faces_dev, uint32_t n_tfaces, uint32_t w, uint32_t h,
+                     float* out) {
+    // mask = Rasterize(tgt, ones), tri = RasterizeFaceId(tgt) into context
+    // scratch (slots 4 .. 6), then the AntiAlias forward
+    void *ones = nullptr, *mask = nullptr, *tri = nullptr;
+    const size_t npx = (size_t)w * h;
+    if (int rc = ctx_workspace(ctx, 4, sizeof(float) * (n_tverts ? n_tverts : 1), &ones)) return rc;
+    if (int rc = ctx_workspace(ctx, 5, sizeof(float) * npx, &mask)) return rc;
+    if (int rc = ctx_workspace(ctx, 6, sizeof(float) * npx, &tri)) return rc;
+    std::vector<float> host_ones(n_tverts ? n_tverts : 1, 1.f);
+    DRESSI_TRY_HIP(hipMemcpyAsync(ones, host_ones.data(), sizeof(float) * host_ones.size(),
+                                  hipMemcpyHostToDevice, ctx->stream));
+    if (int rc = dressi_rasterize(ctx, tgt_clip_dev, n_tverts, (const float*)ones, 1,
+                                  tgt_faces_dev, n_tfaces, w, h, (float*)mask)) return rc;
+    if (int rc = dressi_rasterize_face_id(ctx, tgt_clip_dev, n_tverts, tgt_faces_dev, n_tfaces,
+                                          w, h, (float*)tri)) return rc;
+    if (int rc = dressi_antialias(ctx, (const float*)mask, 1, (const float*)tri, tgt_clip_dev,
+                                  n_tverts, tgt_faces_dev, n_tfaces, w, h, out)) return rc;
+    // the host vector must outlive the async copy
+    DRESSI_TRY_HIP(hipStreamSynchronize(ctx->stream));
+    return DRESSI_OK;
+}
+
+}  // namespace dressi
+
+extern "C" {
+
+int dressi_antialias(dressi_ctx* ctx, const float* img, uint32_t n_comp, const float* tri,
+                     const float* clip, uint32_t n_verts, const float* faces, uint32_t n_faces,
+                     uint32_t width, uint32_t height, float* out) {
+    if (int rc = check_aa_args(ctx, n_comp, width, height)) return rc;
+    DRESSI_REQUIRE(img && tri && clip && (faces || n_faces == 0) && out,
+                   "dressi_antialias: NULL buffer");
+    const uint32_t npx = width * height;
+    hipLaunchKernelGGL(k_antialias_op, dim3(div_up(npx, 256)), dim3(256), 0, ctx->stream, img,
+                       n_comp, tri, (const float4*)clip, n_verts, faces, n_faces, width, height,
+                       out);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+int dressi_antialias_bwd_img(dressi_ctx* ctx, const float* gy, uint32_t n_comp, const float* tri,
+                             const float* clip, uint32_t n_verts, const float* faces,
+                             uint32_t n_faces, uint32_t width, uint32_t height, float* out) {
+    if (int rc = check_aa_args(ctx, n_comp, width, height)) return rc;
+    DRESSI_REQUIRE(gy && tri && clip && (faces || n_faces == 0) && out,
+                   "dressi_antialias_bwd_img: NULL buffer");
+    const uint32_t npx = width * height;
+    hipLaunchKernelGGL(k_antialias_bwd_img_op, dim3(div_up(npx, 256)), dim3(256), 0, ctx->stream,
+                       gy, n_comp, tri, (const float4*)clip, n_verts, faces, n_faces, width,
+                       height, out);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+int dressi_antialias_bwd_vtx(dressi_ctx* ctx, const float* gy, const float* img, uint32_t n_comp,
+                             const float* tri, const float* clip, uint32_t n_verts,
+                             const float* faces, uint32_t n_faces, const float* vtx_faces,
+                             uint32_t max_deg, const float* seed, uint32_t n_samples, int wide,
+                             uint32_t width, uint32_t height, float* out) {
+    if (int rc = check_aa_args(ctx, n_comp, width, height)) return rc;
+    DRESSI_REQUIRE(gy && img && tri && clip && (faces || n_faces == 0) && vtx_faces && out,
+                   "dressi_antialias_bwd_vtx: NULL buffer");
+    DRESSI_REQUIRE(!wide || n_samples > 0, "AntiAliasBwdVtx: wide requires stochastic samples");
+    DRESSI_REQUIRE(n_samples == 0 || seed, "AntiAliasBwdVtx: NULL seed");
+    if (n_verts == 0) {
+        return DRESSI_OK;
+    }
+    if (n_samples == 0) {
+        hipLaunchKernelGGL(k_antialias_bwd_vtx_exact_op, dim3(div_up(n_verts, 128)), dim3(128), 0,
+                           ctx->stream, gy, img, n_comp, tri, (const float4*)clip, n_verts, faces,
+                           n_faces, vtx_faces, max_deg, width, height, (float4*)out);
+    } else {
+        const uint32_t rows = wide ? max_deg : 1u;
+        hipLaunchKernelGGL(k_antialias_bwd_vtx_op, dim3(div_up(n_verts * rows, 256)), dim3(256),
+                           0, ctx->stream, gy, img, n_comp, tri, (const float4*)clip, n_verts,
+                           faces, n_faces, vtx_faces, max_deg, seed, n_samples, wide, width,
+                           height, (float4*)out);
+    }
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+int dressi_col_sum(dressi_ctx* ctx, const float* x, uint32_t n_comp, uint32_t width,
+                   uint32_t height, float* out) {
+    DRESSI_REQUIRE(ctx && x && out, "dressi_col_sum: NULL buffer");
+    DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "ColSum: n_comp must be 1..4");
+    DRESSI_TRY_HIP(hipSetDevice(ctx->device));
+    if (width == 0) {
+        return DRESSI_OK;
+    }
+    hipLaunchKernelGGL(k_col_sum_op, dim3(div_up(width * n_comp, 256)), dim3(256), 0, ctx->stream,
+                       x, n_comp, width, height, out);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+}  // extern "C"

@@ -1,104 +1,14 @@
-// hsr.hip -- the fused HardSoftRas silhouette iteration (forward + backward +
-// Adam as one hipGraph) and the per-op LookupFaces / FaceFetch kernels.
+// hsr.hip -- the fused silhouette-fit plan (forward + backward + Adam as one
+// hipGraph; technique HardSoftRas here, the AA technique's kernels in aa.hip)
+// and the per-op LookupFaces / FaceFetch kernels.
 #include <cstring>
 #include <vector>
 
 #include "hsr_chain.h"
-#include "raster_core.h"
+#include "plan.h"
 #include "soft_clip.h"
 
 namespace dressi {
-
-constexpr uint32_t kMaxViews = 8;
-
-// ---------------------------------------------------------------------------
-// Static reduction trees: SumContribs / SumPixelWise (src/core/build_backward.cpp:41-58,
-// src/core/f_ops.cpp:921-948) fold n inputs in levels of <= 4-ary sequential
-// sums; a lone trailing input passes through unchanged.
-// ---------------------------------------------------------------------------
-template <int N, int D>
-struct Tree {
-    static __device__ __forceinline__ void run(const float (&v)[N][D], float (&out)[D]) {
-        constexpr int M = (N + 3) / 4;
-        float nxt[M][D];
-#pragma unroll
-        for (int i = 0; i < M; i++) {
-            const int cnt = (N - 4 * i) < 4 ? (N - 4 * i) : 4;
-#pragma unroll
-            for (int c = 0; c < D; c++) {
-                if (cnt == 1) {
-                    nxt[i][c] = v[4 * i][c];
-                } else {
-                    float acc = 0.f;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        if (j < cnt) {
-                            acc += v[4 * i + j][c];
-                        }
-                    }
-                    nxt[i][c] = acc;
-                }
-            }
-        }
-        Tree<M, D>::run(nxt, out);
-    }
-};
-template <int D>
-struct Tree<1, D> {
-    static __device__ __forceinline__ void run(const float (&v)[1][D], float (&out)[D]) {
-#pragma unroll
-        for (int c = 0; c < D; c++) {
-            out[c] = v[0][c];
-        }
-    }
-};
-
-// ---------------------------------------------------------------------------
-// Kernels of one iteration
-// ---------------------------------------------------------------------------
-struct HsrDev {
-    RasterGeom g;
-    uint32_t n_verts, max_deg, n_samples, flags;
-    float radius, sigma_scale, inv_px, lr, b1, b2, eps;
-    float* pos;
-    float* m;
-    float* v;
-    float* t;
-    uint32_t* done;
-    const int32_t* faces;     // [F][3]
-    const int32_t* vf;        // [deg][V], -1 pad
-    const uint8_t* vf_mask;   // [deg][V], bit k: faces[vf][k] == v
-    const float* mvps;        // [N][16]
-    const float* targets;     // [N][S][S]
-    SoftRec* recs;            // [N][F]
-    CullRec* cull;            // [N][F]
-    BinBuffers bins;          // fixed-capacity soft bins, N x tiles; the
-                              // face backward clears the counters
-    uint32_t* ids;            // [N][S][S] face + 1 (bit 31: rim winner), 0 bg
-    float* loss;              // [S][S]
-    float* pred;              // [N][S][S] or null
-    float4* gtri;             // [N][3][F]
-    float* grad;              // [V][3] or null
-    // Adam bias corrections 1 - b1^t, 1 - b2^t for t = 1 .. bc_len, filled
-    // on the host with the C library's powf (the reference evaluator's
-    // F::Pow), so the in-graph Adam matches it bit for bit
-    const float2* bc_tab;
-    uint32_t bc_len;
-};
-
-constexpr uint32_t kBiasTableLen = 1u << 16;
-constexpr uint32_t kRimFlag = 0x80000000u;
-
-// Corner clips of face f in one view: TransformToClipVar of its vertices.
-__device__ __forceinline__ void face_clips(const HsrDev& d, uint32_t view, uint32_t f,
-                                           float4 c[3]) {
-    const float* m = d.mvps + view * 16;
-#pragma unroll
-    for (int k = 0; k < 3; k++) {
-        const int32_t vi = d.faces[f * 3 + k];
-        c[k] = mvp_transform(m, d.pos[vi * 3 + 0], d.pos[vi * 3 + 1], d.pos[vi * 3 + 2]);
-    }
-}
 
 // SoftClip + RasterizeSoft setup per (view, face), appended to the soft bins.
 __global__ __launch_bounds__(256) void k_hsr_setup(HsrDev d) {
@@ -285,11 +195,9 @@ __global__ __launch_bounds__(256) void k_hsr_vertex_adam(HsrDev d) {
     const uint32_t vtx = blockIdx.x * blockDim.x + threadIdx.x;
     const float t = *d.t;
     if (vtx < d.n_verts) {
-        // contributions to pos, newest first: GetZ, GetY, GetX of view N-1 .. 0
-        float contrib[3 * NV][3];
+        float gc[NV][4];
 #pragma unroll
-        for (int vi = 0; vi < NV; vi++) {
-            const int view = NV - 1 - vi;
+        for (int view = 0; view < NV; view++) {
             const float4* gt = d.gtri + (size_t)view * 3 * d.g.n_faces;
             float lfb[3][4];
 #pragma unroll
@@ -314,77 +222,18 @@ __global__ __launch_bounds__(256) void k_hsr_vertex_adam(HsrDev d) {
                 }
             }
             // clip_v gradient: LookupFaces 2, 1, 0 (newest first), one 3-ary sum
-            float gc[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 float acc = 0.f;
                 acc += lfb[2][r];
                 acc += lfb[1][r];
                 acc += lfb[0][r];
-                gc[r] = acc;
-            }
-            const float* m = d.mvps + view * 16;
-            float gxyz[3];
-#pragma unroll
-            for (int comp = 0; comp < 3; comp++) {
-                float acc = 0.f;
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    acc += gc[r] * m[comp * 4 + r];
-                }
-                gxyz[comp] = acc;
-            }
-#pragma unroll
-            for (int q = 0; q < 3; q++) {
-                const int comp = 2 - q;
-                contrib[vi * 3 + q][0] = 0.f;
-                contrib[vi * 3 + q][1] = 0.f;
-                contrib[vi * 3 + q][2] = 0.f;
-                contrib[vi * 3 + q][comp] = gxyz[comp];
+                gc[view][r] = acc;
             }
         }
-        float g[3];
-        Tree<3 * NV, 3>::run(contrib, g);
-        if (d.grad) {
-#pragma unroll
-            for (int c = 0; c < 3; c++) {
-                d.grad[vtx * 3 + c] = g[c];
-            }
-        }
-        // in-graph Adam (examples/silhouette_optimization/run.cpp:421-436)
-        const float t_new = t + 1.f;
-        float bc1, bc2;
-        if (t_new >= 1.f && t_new <= (float)d.bc_len && t_new == floorf(t_new)) {
-            const float2 bc = d.bc_tab[(uint32_t)t_new - 1];
-            bc1 = bc.x;
-            bc2 = bc.y;
-        } else {
-            bc1 = 1.f - powf(d.b1, t_new);
-            bc2 = 1.f - powf(d.b2, t_new);
-        }
-        const float cb1 = 1.f - d.b1, cb2 = 1.f - d.b2;
-#pragma unroll
-        for (int c = 0; c < 3; c++) {
-            const size_t j = (size_t)vtx * 3 + c;
-            const float m_new = d.m[j] * d.b1 + g[c] * cb1;
-            const float v_new = d.v[j] * d.b2 + g[c] * g[c] * cb2;
-            const float step = (m_new / bc1) / (sqrtf(v_new / bc2) + d.eps) * d.lr;
-            d.pos[j] = d.pos[j] - step;
-            d.m[j] = m_new;
-            d.v[j] = v_new;
-        }
+        pos_grad_adam<NV>(d, vtx, gc, t);
     }
-    __shared__ bool last;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        last = atomicAdd(d.done, 1u) == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (last && threadIdx.x == 0) {
-        *d.t = t + 1.f;
-        *d.done = 0;
-    }
+    advance_t(d, t);
 }
 
 // Per-op kernels ------------------------------------------------------------
@@ -560,6 +409,9 @@ const char* const kIterKernelNames[kIterKernels] = {"k_hsr_setup", "k_hsr_raster
                                                     "k_hsr_face_bwd", "k_hsr_vertex_adam"};
 
 int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
+    if (d.technique == 1) {
+        return launch_aa_kernel(d, s, k);
+    }
     const RasterGeom& g = d.g;
     const uint32_t nvf = g.n_views * g.n_faces;
     switch (k) {
@@ -671,12 +523,20 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
     rc = rc ? rc : plan_alloc(p, &d.done, 1);
     rc = rc ? rc : plan_alloc(p, (float**)&d.mvps, N * 16);
     rc = rc ? rc : plan_alloc(p, (float**)&d.targets, N * npx);
-    rc = rc ? rc : plan_alloc(p, &d.recs, N * F);
-    rc = rc ? rc : plan_alloc(p, &d.cull, N * F);
+    d.technique = (desc->flags & DRESSI_HSR_TECHNIQUE_AA) ? 1u : 0u;
+    if (d.technique == 0) {
+        rc = rc ? rc : plan_alloc(p, &d.recs, N * F);
+        rc = rc ? rc : plan_alloc(p, &d.cull, N * F);
+    } else {
+        rc = rc ? rc : plan_alloc(p, &d.arecs, N * F);
+        rc = rc ? rc : plan_alloc(p, &d.clip, N * V);
+    }
     rc = rc ? rc : plan_alloc(p, &d.ids, N * npx);
     rc = rc ? rc : plan_alloc(p, &d.loss, npx);
     rc = rc ? rc : plan_alloc(p, &gtri, N * 3 * F);
-    if (!rc && (desc->flags & DRESSI_HSR_KEEP_PRED)) rc = plan_alloc(p, &d.pred, N * npx);
+    if (!rc && ((desc->flags & DRESSI_HSR_KEEP_PRED) || d.technique == 1)) {
+        rc = plan_alloc(p, &d.pred, N * npx);
+    }
     if (!rc && (desc->flags & DRESSI_HSR_KEEP_GRAD)) rc = plan_alloc(p, &d.grad, V * 3);
     d.gtri = gtri;
     float2* bc = nullptr;
@@ -833,6 +693,27 @@ int dressi_hsr_render_targets(dressi_hsr_plan* p, const float* tgt_pos, uint32_t
             o[2] = c.z;
             o[3] = c.w;
         }
+    }
+    if (p->d.technique == 1) {
+        // StopGradient(AntiAlias(Rasterize(tgt, 1), RasterizeFaceId(tgt), tgt_clip,
+        // tgt_faces, ..., zero seed, 0)) per view (run.cpp:346-357)
+        dressi_ctx* ctx = p->ctx;
+        void *dclip = nullptr, *dfaces = nullptr;
+        if (int rc = ctx_workspace(ctx, 7, clip.size() * 4, &dclip)) return rc;
+        if (int rc = ctx_workspace(ctx, 8, (size_t)n_tfaces * 3 * 4, &dfaces)) return rc;
+        DRESSI_TRY_HIP(hipMemcpy(dclip, clip.data(), clip.size() * 4, hipMemcpyHostToDevice));
+        DRESSI_TRY_HIP(hipMemcpy(dfaces, tgt_faces, (size_t)n_tfaces * 3 * 4,
+                                 hipMemcpyHostToDevice));
+        const size_t npx = (size_t)p->desc.width * p->desc.height;
+        for (uint32_t v = 0; v < N; v++) {
+            if (int rc = aa_render_target(ctx, (const float*)dclip + (size_t)v * n_tverts * 4,
+                                          n_tverts, (const float*)dfaces, n_tfaces,
+                                          p->desc.width, p->desc.height,
+                                          (float*)p->d.targets + v * npx)) return rc;
+        }
+        DRESSI_TRY_HIP(hipStreamSynchronize(ctx->stream));
+        p->targets_set = true;
+        return DRESSI_OK;
     }
     const RasterGeom g = make_geom(p->desc.width, p->desc.height, N, n_tfaces);
     const uint32_t cap = default_bin_cap(g, 8);
@@ -1039,7 +920,8 @@ int dressi_hsr_profile(dressi_hsr_plan* p, uint32_t iters, char* names, size_t n
             usec[k] = ms[k] * 1000.f;
         }
         if (names && name_stride > 0) {
-            snprintf(names + k * name_stride, name_stride, "%s", kIterKernelNames[k]);
+            snprintf(names + k * name_stride, name_stride, "%s",
+                     p->d.technique == 1 ? kAaKernelNames[k] : kIterKernelNames[k]);
         }
     }
     for (hipEvent_t e : ev) {

@@ -1,0 +1,200 @@
+// plan.h -- device-side state of the fused silhouette-fit plan (shared by
+// the HardSoftRas kernels in hsr.hip and the AA kernels in aa.hip).
+#pragma once
+
+#include "aa_core.h"
+#include "raster_core.h"
+
+namespace dressi {
+
+constexpr uint32_t kMaxViews = 8;
+
+// ---------------------------------------------------------------------------
+// Static reduction trees: SumContribs / SumPixelWise (src/core/build_backward.cpp:41-58,
+// src/core/f_ops.cpp:921-948) fold n inputs in levels of <= 4-ary sequential
+// sums; a lone trailing input passes through unchanged.
+// ---------------------------------------------------------------------------
+template <int N, int D>
+struct Tree {
+    static __device__ __forceinline__ void run(const float (&v)[N][D], float (&out)[D]) {
+        constexpr int M = (N + 3) / 4;
+        float nxt[M][D];
+#pragma unroll
+        for (int i = 0; i < M; i++) {
+            const int cnt = (N - 4 * i) < 4 ? (N - 4 * i) : 4;
+#pragma unroll
+            for (int c = 0; c < D; c++) {
+                if (cnt == 1) {
+                    nxt[i][c] = v[4 * i][c];
+                } else {
+                    float acc = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        if (j < cnt) {
+                            acc += v[4 * i + j][c];
+                        }
+                    }
+                    nxt[i][c] = acc;
+                }
+            }
+        }
+        Tree<M, D>::run(nxt, out);
+    }
+};
+template <int D>
+struct Tree<1, D> {
+    static __device__ __forceinline__ void run(const float (&v)[1][D], float (&out)[D]) {
+#pragma unroll
+        for (int c = 0; c < D; c++) {
+            out[c] = v[0][c];
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Kernels of one iteration
+// ---------------------------------------------------------------------------
+struct HsrDev {
+    RasterGeom g;
+    uint32_t n_verts, max_deg, n_samples, flags;
+    float radius, sigma_scale, inv_px, lr, b1, b2, eps;
+    float* pos;
+    float* m;
+    float* v;
+    float* t;
+    uint32_t* done;
+    const int32_t* faces;     // [F][3]
+    const int32_t* vf;        // [deg][V], -1 pad
+    const uint8_t* vf_mask;   // [deg][V], bit k: faces[vf][k] == v
+    const float* mvps;        // [N][16]
+    const float* targets;     // [N][S][S]
+    SoftRec* recs;            // [N][F]
+    CullRec* cull;            // [N][F]
+    BinBuffers bins;          // fixed-capacity soft bins, N x tiles; the
+                              // face backward clears the counters
+    uint32_t* ids;            // [N][S][S] face + 1 (bit 31: rim winner), 0 bg
+    float* loss;              // [S][S]
+    float* pred;              // [N][S][S] or null
+    float4* gtri;             // [N][3][F]
+    float* grad;              // [V][3] or null
+    // Adam bias corrections 1 - b1^t, 1 - b2^t for t = 1 .. bc_len, filled
+    // on the host with the C library's powf (the reference evaluator's
+    // F::Pow), so the in-graph Adam matches it bit for bit
+    const float2* bc_tab;
+    uint32_t bc_len;
+    // technique aa (DRESSI_HSR_TECHNIQUE_AA): per-view clip positions, hard
+    // raster records; pred is always kept (the vertex gather needs it)
+    uint32_t technique;       // 0 HardSoftRas, 1 AA
+    float4* clip;             // [N][V]
+    AaRec* arecs;             // [N][F]
+};
+
+constexpr uint32_t kBiasTableLen = 1u << 16;
+constexpr uint32_t kRimFlag = 0x80000000u;
+
+// Corner clips of face f in one view: TransformToClipVar of its vertices.
+__device__ __forceinline__ void face_clips(const HsrDev& d, uint32_t view, uint32_t f,
+                                           float4 c[3]) {
+    const float* m = d.mvps + view * 16;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        const int32_t vi = d.faces[f * 3 + k];
+        c[k] = mvp_transform(m, d.pos[vi * 3 + 0], d.pos[vi * 3 + 1], d.pos[vi * 3 + 2]);
+    }
+}
+
+
+// Vertex tail of both techniques: the per-view clip gradients of one vertex
+// through TransformToClipVar (examples/common/geometry_utils.cpp:391-402:
+// per view x / y / z get one 4-term sum over the clip rows; pos gets the
+// GetZ, GetY, GetX contributions of view N-1 .. 0, newest first, through
+// the SumContribs tree), then the in-graph Adam step
+// (examples/silhouette_optimization/run.cpp:421-436) reading t.
+template <int NV>
+__device__ __forceinline__ void pos_grad_adam(const HsrDev& d, uint32_t vtx,
+                                              const float (&gc)[NV][4], float t) {
+    float contrib[3 * NV][3];
+#pragma unroll
+    for (int vi = 0; vi < NV; vi++) {
+        const int view = NV - 1 - vi;
+        const float* m = d.mvps + view * 16;
+        float gxyz[3];
+#pragma unroll
+        for (int comp = 0; comp < 3; comp++) {
+            float acc = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                acc += gc[view][r] * m[comp * 4 + r];
+            }
+            gxyz[comp] = acc;
+        }
+#pragma unroll
+        for (int q = 0; q < 3; q++) {
+            const int comp = 2 - q;
+            contrib[vi * 3 + q][0] = 0.f;
+            contrib[vi * 3 + q][1] = 0.f;
+            contrib[vi * 3 + q][2] = 0.f;
+            contrib[vi * 3 + q][comp] = gxyz[comp];
+        }
+    }
+    float g[3];
+    Tree<3 * NV, 3>::run(contrib, g);
+    if (d.grad) {
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+            d.grad[vtx * 3 + c] = g[c];
+        }
+    }
+    const float t_new = t + 1.f;
+    float bc1, bc2;
+    if (t_new >= 1.f && t_new <= (float)d.bc_len && t_new == floorf(t_new)) {
+        const float2 bc = d.bc_tab[(uint32_t)t_new - 1];
+        bc1 = bc.x;
+        bc2 = bc.y;
+    } else {
+        bc1 = 1.f - powf(d.b1, t_new);
+        bc2 = 1.f - powf(d.b2, t_new);
+    }
+    const float cb1 = 1.f - d.b1, cb2 = 1.f - d.b2;
+#pragma unroll
+    for (int c = 0; c < 3; c++) {
+        const size_t j = (size_t)vtx * 3 + c;
+        const float m_new = d.m[j] * d.b1 + g[c] * cb1;
+        const float v_new = d.v[j] * d.b2 + g[c] * g[c] * cb2;
+        const float step = (m_new / bc1) / (sqrtf(v_new / bc2) + d.eps) * d.lr;
+        d.pos[j] = d.pos[j] - step;
+        d.m[j] = m_new;
+        d.v[j] = v_new;
+    }
+}
+
+// The last workgroup of the vertex kernel to finish advances t (every
+// workgroup read t before arriving on the counter). All threads call it.
+__device__ __forceinline__ void advance_t(const HsrDev& d, float t) {
+    __shared__ bool last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        last = atomicAdd(d.done, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (last && threadIdx.x == 0) {
+        *d.t = t + 1.f;
+        *d.done = 0;
+    }
+}
+
+// Launches kernel k (0 .. kAaKernels - 1) of one AA-technique iteration
+// (aa.hip): 0 clip + setup + binning, 1 visibility raster, 2 AntiAlias +
+// loss, 3 vertex-gradient gather, 4 ColSum + clip->pos + Adam.
+constexpr int kAaKernels = 5;
+extern const char* const kAaKernelNames[kAaKernels];
+int launch_aa_kernel(const HsrDev& d, hipStream_t s, int k);
+// Renders the AA target of one view into `out` ({S,S} float):
+// StopGradient(AntiAlias(Rasterize(tgt, 1), RasterizeFaceId(tgt), tgt_clip,
+// tgt_faces, ...)) with zero seed (run.cpp:346-357).
+int aa_render_target(dressi_ctx* ctx, const float* tgt_clip_dev, uint32_t n_tverts,
+                     const float* tgt_faces_dev, uint32_t n_tfaces, uint32_t w, uint32_t h,
+                     float* out);
+
+}  // namespace dressi

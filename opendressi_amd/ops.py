@@ -127,5 +127,63 @@ def face_fetch_bwd(ctx: Context, gy: torch.Tensor, idx: torch.Tensor, prj0: torc
     return out
 
 
+def _nc(img: torch.Tensor) -> int:
+    return 1 if img.dim() == 2 else img.shape[2]
+
+
+def antialias(ctx: Context, img: torch.Tensor, tri: torch.Tensor, clip: torch.Tensor,
+              faces: torch.Tensor) -> torch.Tensor:
+    """F::AntiAlias forward (src/core/f_ops.cpp:2480-2579): img (H, W[, C]),
+    tri (H, W) float face + 1, clip (V, 4), faces (F, 3) float ids."""
+    _prep(ctx)
+    h, w = tri.shape
+    out = torch.empty_like(img)
+    check(lib.dressi_antialias(ctx.handle, _ptr(img, "img"), _nc(img), _ptr(tri, "tri"),
+                               _ptr(clip, "clip"), clip.shape[0], _ptr(faces, "faces"),
+                               faces.shape[0], w, h, _ptr(out, "out")))
+    return out
+
+
+def antialias_bwd_img(ctx: Context, gy: torch.Tensor, tri: torch.Tensor, clip: torch.Tensor,
+                      faces: torch.Tensor) -> torch.Tensor:
+    """AntiAliasBwdImg (src/core/f_ops.cpp:2220-2278) -> like gy."""
+    _prep(ctx)
+    h, w = tri.shape
+    out = torch.empty_like(gy)
+    check(lib.dressi_antialias_bwd_img(ctx.handle, _ptr(gy, "gy"), _nc(gy), _ptr(tri, "tri"),
+                                       _ptr(clip, "clip"), clip.shape[0], _ptr(faces, "faces"),
+                                       faces.shape[0], w, h, _ptr(out, "out")))
+    return out
+
+
+def antialias_bwd_vtx(ctx: Context, gy: torch.Tensor, img: torch.Tensor, tri: torch.Tensor,
+                      clip: torch.Tensor, faces: torch.Tensor, vtx_faces: torch.Tensor,
+                      seed: torch.Tensor | None, n_samples: int, wide: bool = True) -> torch.Tensor:
+    """AntiAliasBwdVtx (src/core/f_ops.cpp:2284-2476): n_samples > 0 and wide
+    -> (deg, V, 4) partials; otherwise (V, 4). `seed` is a 1-element device
+    tensor (the in-graph counter), unused when n_samples == 0."""
+    _prep(ctx)
+    h, w = tri.shape
+    deg, nv = vtx_faces.shape
+    is_wide = bool(wide and n_samples > 0)
+    out = torch.empty((deg if is_wide else 1, nv, 4), dtype=torch.float32, device=gy.device)
+    check(lib.dressi_antialias_bwd_vtx(
+        ctx.handle, _ptr(gy, "gy"), _ptr(img, "img"), _nc(gy), _ptr(tri, "tri"),
+        _ptr(clip, "clip"), nv, _ptr(faces, "faces"), faces.shape[0],
+        _ptr(vtx_faces, "vtx_faces"), deg, _ptr(seed, "seed"), n_samples, 1 if is_wide else 0,
+        w, h, _ptr(out, "out")))
+    return out if is_wide else out[0]
+
+
+def col_sum(ctx: Context, x: torch.Tensor) -> torch.Tensor:
+    """F::ColSum (src/core/f_ops.cpp:1218-1246): (H, W, C) -> (W, C)."""
+    _prep(ctx)
+    h, w, nc = x.shape
+    out = torch.empty((w, nc), dtype=torch.float32, device=x.device)
+    check(lib.dressi_col_sum(ctx.handle, _ptr(x, "x"), nc, w, h, _ptr(out, "out")))
+    return out
+
+
 __all__ = ["soft_clip", "rasterize_soft", "rasterize", "rasterize_face_id", "lookup_faces",
-           "lookup_faces_bwd", "face_fetch", "face_fetch_bwd"]
+           "lookup_faces_bwd", "face_fetch", "face_fetch_bwd", "antialias", "antialias_bwd_img",
+           "antialias_bwd_vtx", "col_sum"]

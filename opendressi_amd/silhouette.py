@@ -1,18 +1,21 @@
-"""Host-side mirror of the reference's HardSoftRas silhouette fit
-(examples/silhouette_optimization/run.cpp, technique hardsoftras, peels = 1,
-no regularizers) over the fused plan of include/dressi_hip.h, plus the
-synthetic workloads it is benchmarked on.
+"""Host-side mirror of the reference's silhouette fit
+(examples/silhouette_optimization/run.cpp, technique hardsoftras with
+peels = 1, or aa; no regularizers) over the fused plan of
+include/dressi_hip.h, plus the synthetic workloads it is benchmarked on.
 
 Workloads (all fp32, r = 3 px, 8 backward samples per face, Adam b1 .9,
-b2 .999, eps 1e-8; target = StopGradient(Rasterize(target mesh)) per view):
+b2 .999, eps 1e-8; target = StopGradient(Rasterize(target mesh)) per view,
+AntiAlias'd for technique aa):
 
   c1      icosphere L3 (642 v / 1280 f), 256^2, 1 view (front, distance 3),
           target radius 1 + N(0, .05), lr 1e-3, 50 iterations
   c2      icosphere L4 (2562 v / 5120 f), 512^2, 4 orbit views (yaw
           0/90/180/270, pitch 15 deg, distance 3), noise N(0, .05), lr 1e-3,
           200 iterations
-  c4_hsr  icosphere L6 (40962 v / 81920 f), 2048^2, the same 4 orbit views,
-          noise N(0, .02) + 0.1 * P2(y) bump, lr 5e-4, 100 iterations
+  c4      icosphere L6 (40962 v / 81920 f), 2048^2, the same 4 orbit views,
+          noise N(0, .02) + 0.1 * P2(y) bump, lr 5e-4, 100 iterations,
+          technique aa (target = AntiAlias of the target mask)
+  c4_hsr  the same scene with HardSoftRas
 
 Cameras: PerspectiveVk(45 deg, 1, 0.1, 10) * LookAt(eye, 0, +y).
 """
@@ -49,11 +52,13 @@ class Workload:
     lr: float
     iters: int
     seed: int
+    technique: str = "hsr"  # "hsr" (HardSoftRas) or "aa" (screen-space AA)
 
 
 WORKLOADS = {
     "c1": Workload("c1", 3, 256, 1, 0.05, 0.0, 1e-3, 50, 1),
     "c2": Workload("c2", 4, 512, 4, 0.05, 0.0, 1e-3, 200, 2),
+    "c4": Workload("c4", 6, 2048, 4, 0.02, 0.1, 5e-4, 100, 4, "aa"),
     "c4_hsr": Workload("c4_hsr", 6, 2048, 4, 0.02, 0.1, 5e-4, 100, 4),
 }
 
@@ -91,17 +96,21 @@ class SilhouetteFit:
                  screen: int, targets: np.ndarray | None = None,
                  target_mesh: tuple[np.ndarray, np.ndarray] | None = None,
                  radius_px: float = 3.0, samples: int = 8, lr: float = 1e-3,
-                 keep_pred: bool = False, keep_grad: bool = False):
+                 keep_pred: bool = False, keep_grad: bool = False, technique: str = "hsr"):
         self.ctx = ctx
         pos0 = np.ascontiguousarray(pos0, np.float32)
         faces = np.ascontiguousarray(faces, np.float32)
         mvps = np.ascontiguousarray(mvps, np.float32).reshape(-1, 16)
         self.n_verts, self.n_faces, self.n_views = len(pos0), len(faces), len(mvps)
         self.screen = screen
+        if technique not in ("hsr", "aa"):
+            raise ValueError(f"technique must be 'hsr' or 'aa', got {technique!r}")
+        self.technique = technique
         d = _lib.HsrDesc(self.n_verts, self.n_faces, self.n_views, screen, screen,
                          radius_px, samples, lr, 0.9, 0.999, 1e-8,
                          (_lib.HSR_KEEP_PRED if keep_pred else 0)
-                         | (_lib.HSR_KEEP_GRAD if keep_grad else 0))
+                         | (_lib.HSR_KEEP_GRAD if keep_grad else 0)
+                         | (_lib.HSR_TECHNIQUE_AA if technique == "aa" else 0))
         h = C.c_void_p()
         check(lib.dressi_hsr_create(ctx.handle, C.byref(d), C.byref(h)))
         self.handle = h
@@ -120,6 +129,7 @@ class SilhouetteFit:
     def from_workload(cls, ctx: Context, name: str, **kw) -> "SilhouetteFit":
         w = WORKLOADS[name]
         pos, faces, tgt, mvps = make_scene(w)
+        kw.setdefault("technique", w.technique)
         return cls(ctx, pos, faces, mvps, w.screen, target_mesh=(tgt, faces), lr=w.lr, **kw)
 
     def close(self) -> None:
