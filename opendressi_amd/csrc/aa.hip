@@ -40,6 +40,10 @@ struct TriFromRecs {
     }
 };
 
+// kAaOffX / kAaOffY as compile-time constants (register-array indices)
+constexpr int kAaOffXh[8] = {-1, 0, 1, -1, 1, -1, 0, 1};
+constexpr int kAaOffYh[8] = {-1, -1, -1, 0, 0, 1, 1, 1};
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -485,176 +489,309 @@ __global__ __launch_bounds__(64) void k_aa_raster(HsrDev d) {
     }
 }
 
+// Sum c_s + sum_k [r c_s + (1 - r) c_n] of AntiAlias over the 8 neighbours
+// of mask pixel (x, y) (f_ops.cpp:2544-2576 with one channel), its = face +
+// 1 of the pixel. With c_s = c_n in {0, 1} an active pair adds r c + (1 - r)
+// c, which rounds to exactly c (1 - r is within half an ulp of its exact
+// value and r + fl(1 - r) rounds back to 1), so only pairs across the
+// silhouette evaluate their edge; the neighbour ids are read again here.
+__device__ float aa_mask_sum(const uint32_t* ids, const TriFromRecs& tris, uint32_t n_faces,
+                             int x, int y, int w, int h, uint32_t its) {
+    const float cs = its ? 1.f : 0.f;
+    float dst = cs;
+    for (int k = 0; k < 8; k++) {
+        const int nx = x + kAaOffX[k], ny = y + kAaOffY[k];
+        const uint32_t itn =
+                (nx < 0 || ny < 0 || nx >= w || ny >= h) ? its : ids[(size_t)ny * w + nx];
+        AaPair pr;
+        if ((its == 0u) == (itn == 0u) ||
+            !eval_aa_pair(its, itn, x, y, nx, ny, n_faces, tris, &pr)) {
+            dst += cs;
+            continue;
+        }
+        const float cn = itn ? 1.f : 0.f;
+        dst += pr.r * cs + (1.f - pr.r) * cn;
+    }
+    return dst;
+}
+
 // AntiAlias of the mask (Rasterize(clip, 1): 1 exactly where covered) and the
-// L2 loss: one wave per view over 64 pixels of a row, the views of the same
-// pixels in one workgroup, their SumPixelWise reduced through LDS. pred is
-// kept for the vertex gather (which rebuilds d loss / d pred from it).
-template <int NV>
+// L2 loss. A lane covers 4 consecutive pixels of a row in one view, a wave
+// 256 pixels, the NV waves of a workgroup the NV views of the same pixels,
+// their SumPixelWise reduced through LDS. A pixel whose 8 neighbours all
+// have its mask value sums 9 c exactly (pred = c); the others (the
+// silhouette) take aa_mask_sum. pred is kept for the face backward. VEC: the
+// row width is a multiple of 4 (16-byte loads and stores).
+template <int NV, bool VEC>
 __global__ __launch_bounds__(64 * NV) void k_aa_fwd(HsrDev d) {
-    __shared__ float lv[NV][64];
+    __shared__ float4 lv[NV][64];
     const uint32_t view = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
-    const uint32_t w = d.g.width, h = d.g.height;
-    const uint32_t x = blockIdx.x * 64 + (uint32_t)lane;
-    const uint32_t y = blockIdx.y;
-    const bool on = x < w;
+    const int w = (int)d.g.width, h = (int)d.g.height;
+    const int x0 = (int)blockIdx.x * 256 + lane * 4;
+    const int y = (int)blockIdx.y;
     const size_t npx = (size_t)w * h;
-    const size_t o = (size_t)y * w + x;
-    float l = 0.f;
-    if (on) {
-        const uint32_t* ids = d.ids + view * npx;
-        const TriFromRecs tris{d.faces, d.arecs + (size_t)view * d.g.n_faces};
-        const uint32_t its = ids[o];
-        // all eight neighbour ids first (one load latency); an off-screen
-        // neighbour adds c like an inactive pair, so it reads as its own id
-        uint32_t itn[8];
+    const size_t o = (size_t)y * w + x0;
+    const uint32_t* ids = d.ids + view * npx;
+    // ids of rows y-1, y, y+1 at x0-1 .. x0+4 (entry c + 1 is column x0 + c);
+    // off-screen entries are never used
+    uint32_t r[3][6];
+    float tg[4];
+    const bool any = x0 < w;
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int nx = (int)x + kAaOffX[k], ny = (int)y + kAaOffY[k];
-            const bool in = !(nx < 0 || ny < 0 || nx >= (int)w || ny >= (int)h);
-            itn[k] = in ? ids[(size_t)ny * w + nx] : its;
-        }
-        const float cs = its ? 1.f : 0.f;
-        float dst = cs;
-        for (int k = 0; k < 8; k++) {
-            const int nx = (int)x + kAaOffX[k], ny = (int)y + kAaOffY[k];
-            AaPair pr;
-            if (!eval_aa_pair(its, itn[k], (int)x, (int)y, nx, ny, d.g.n_faces, tris, &pr)) {
-                dst += cs;
-                continue;
+    for (int ry = 0; ry < 3; ry++) {
+        const int yy = y + ry - 1;
+        const bool row_ok = any && yy >= 0 && yy < h;
+        const uint32_t* row = ids + (size_t)(row_ok ? yy : 0) * w;
+        if (VEC) {
+            const uint4 q = row_ok ? *reinterpret_cast<const uint4*>(row + x0) : uint4{0, 0, 0, 0};
+            r[ry][1] = q.x;
+            r[ry][2] = q.y;
+            r[ry][3] = q.z;
+            r[ry][4] = q.w;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                r[ry][c + 1] = row_ok && x0 + c < w ? row[x0 + c] : 0u;
             }
-            const float cn = itn[k] ? 1.f : 0.f;
-            dst += pr.r * cs + (1.f - pr.r) * cn;
         }
-        const float pred = dst / 9.f;
-        d.pred[view * npx + o] = pred;
-        const float diff = d.targets[view * npx + o] - pred;
-        l = diff * diff * d.inv_px;
+        // the columns either side come from the neighbouring lanes; the
+        // wave's outer lanes load them
+        const uint32_t left = __shfl_up(r[ry][4], 1);
+        const uint32_t right = __shfl_down(r[ry][1], 1);
+        r[ry][0] = lane == 0 ? (row_ok && x0 > 0 ? row[x0 - 1] : 0u) : left;
+        r[ry][5] = lane == 63 ? (row_ok && x0 + 4 < w ? row[x0 + 4] : 0u) : right;
     }
-    lv[view][lane] = l;
-    __syncthreads();
-    if (view == 0 && on) {
-        float in[NV][1];
+    const float* tgt = d.targets + view * npx;
+    if (VEC) {
+        const float4 q = any ? *reinterpret_cast<const float4*>(tgt + o) : float4{0, 0, 0, 0};
+        tg[0] = q.x;
+        tg[1] = q.y;
+        tg[2] = q.z;
+        tg[3] = q.w;
+    } else {
 #pragma unroll
-        for (int k = 0; k < NV; k++) {
-            in[k][0] = lv[k][lane];
+        for (int c = 0; c < 4; c++) {
+            tg[c] = any && x0 + c < w ? tgt[o + c] : 0.f;
         }
-        float out[1];
-        Tree<NV, 1>::run(in, out);
-        d.loss[o] = out[0];
+    }
+    // 8-neighbour mask agreement of each pixel (off-screen neighbours agree)
+    float pred[4];
+    uint32_t edge = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const bool fg = r[1][c + 1] != 0u;
+        bool mixed = false;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int nx = x0 + c + kAaOffXh[k], ny = y + kAaOffYh[k];
+            const bool in = nx >= 0 && ny >= 0 && nx < w && ny < h;
+            mixed |= in && ((r[1 + kAaOffYh[k]][c + 1 + kAaOffXh[k]] != 0u) != fg);
+        }
+        edge |= mixed && x0 + c < w ? 1u << c : 0u;
+        // nine equal terms: 9 c / 9 = c
+        pred[c] = fg ? 1.f : 0.f;
+    }
+    if (edge) {
+        const TriFromRecs tris{d.faces, d.arecs + (size_t)view * d.g.n_faces};
+#pragma unroll 1
+        for (int c = 0; c < 4; c++) {
+            if (edge >> c & 1u) {
+                const uint32_t its = c == 0 ? r[1][1] : c == 1 ? r[1][2] : c == 2 ? r[1][3] : r[1][4];
+                const float v = aa_mask_sum(ids, tris, d.g.n_faces, x0 + c, y, w, h, its) / 9.f;
+                pred[0] = c == 0 ? v : pred[0];
+                pred[1] = c == 1 ? v : pred[1];
+                pred[2] = c == 2 ? v : pred[2];
+                pred[3] = c == 3 ? v : pred[3];
+            }
+        }
+    }
+    float l[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const float diff = tg[c] - pred[c];
+        l[c] = diff * diff * d.inv_px;
+    }
+    float* pd = d.pred + view * npx;
+    if (VEC) {
+        if (any) {
+            *reinterpret_cast<float4*>(pd + o) = make_float4(pred[0], pred[1], pred[2], pred[3]);
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            if (any && x0 + c < w) {
+                pd[o + c] = pred[c];
+            }
+        }
+    }
+    lv[view][lane] = make_float4(l[0], l[1], l[2], l[3]);
+    __syncthreads();
+    if (view == 0 && any) {
+        float out[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float in[NV][1];
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                const float4 q = lv[k][lane];
+                in[k][0] = c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w;
+            }
+            float one[1];
+            Tree<NV, 1>::run(in, one);
+            out[c] = one[0];
+        }
+        if (VEC) {
+            *reinterpret_cast<float4*>(d.loss + o) = make_float4(out[0], out[1], out[2], out[3]);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                if (x0 + c < w) {
+                    d.loss[o + c] = out[c];
+                }
+            }
+        }
     }
 }
 
-constexpr int kAaBatch = 8;  // samples whose loads are issued together
+// Lanes (8-lane group) g + src of a wave: lane-group shuffle.
+__device__ __forceinline__ float grp_shfl(float v, int src) { return __shfl(v, src, 64); }
+__device__ __forceinline__ int grp_shfl(int v, int src) { return __shfl(v, src, 64); }
 
-// AntiAliasBwdVtx (stochastic, wide) fused per (view, face): the face's n
-// samples (salts 2 and 3, seed = t) are shared by its three corner slots, so
-// they are evaluated once and each active pair adds into the accumulator of
-// every corner that is an endpoint of its edge -- per corner the same
-// (sample, neighbour, endpoint) sequence as the reference's (vertex, slot)
-// row. Pairs whose two pixels have the same mask value carry gr = 0 and are
-// skipped before the pair evaluation. Also clears the bin counters.
+// OR of the 8-bit fields of a wave ballot: the group slots (samples or
+// neighbours) that are set in at least one group.
+__device__ __forceinline__ uint32_t fold_groups(uint64_t m) {
+    m |= m >> 32;
+    m |= m >> 16;
+    m |= m >> 8;
+    return (uint32_t)m & 0xffu;
+}
+
+// AntiAliasBwdVtx (stochastic, wide) fused per (view, face) on an 8-lane
+// group: the face's n samples (salts 2 and 3, seed = t) are shared by its
+// three corner slots. Lane j computes sample s0 + j of each batch of 8; then,
+// sample by sample in order, lane k evaluates the pair of neighbour k and the
+// corner terms it adds, and the group adds them into its accumulators in
+// neighbour order -- per corner the same (sample, neighbour, endpoint)
+// sequence of additions as the reference's (vertex, slot) row. Pairs whose
+// two pixels have the same mask value carry gr = 0 and are skipped before the
+// pair evaluation. Every lane of a wave runs every shuffle (no early exit).
+// Also clears the bin counters.
 __global__ __launch_bounds__(256) void k_aa_face_bwd(HsrDev d) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    for (uint32_t b = i; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
+    const uint32_t gi = blockIdx.x * blockDim.x + threadIdx.x;
+    for (uint32_t b = gi; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
         d.bins.counts[b] = 0;
     }
-    if (i >= d.g.n_views * d.g.n_faces) {
-        return;
-    }
-    const uint32_t view = i / d.g.n_faces;
-    const uint32_t f = i - view * d.g.n_faces;
-    const uint32_t w = d.g.width, h = d.g.height;
+    const uint32_t nvf = d.g.n_views * d.g.n_faces;
+    const uint32_t item = gi >> 3;
+    const bool valid = item < nvf;
+    const int j = (int)(threadIdx.x & 7u);
+    const int gbase = (int)(threadIdx.x & 56u);  // first lane of the group in the wave
+    const uint32_t view = valid ? item / d.g.n_faces : 0u;
+    const uint32_t f = valid ? item - view * d.g.n_faces : 0u;
+    const int w = (int)d.g.width, h = (int)d.g.height;
     const float W = (float)w, H = (float)h;
     const size_t npx = (size_t)w * h;
     const uint32_t* ids = d.ids + view * npx;
     const float* pred = d.pred + view * npx;
     const float* tgt = d.targets + view * npx;
     const float4* clip = d.clip + (size_t)view * d.n_verts;
+    const TriFromRecs tris{d.faces, d.arecs + (size_t)view * d.g.n_faces};
     uint32_t vc[3];
     float4 c[3];
     float4 acc[3];
 #pragma unroll
     for (int k = 0; k < 3; k++) {
-        vc[k] = (uint32_t)d.faces[f * 3 + k];
-        c[k] = clip[vc[k]];
+        vc[k] = valid ? (uint32_t)d.faces[f * 3 + k] : 0u;
+        c[k] = valid ? clip[vc[k]] : make_float4(0.f, 0.f, 0.f, 1.f);
         acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float s3x[3], s3y[3];
-    if (d.n_samples > 0 && aa_face_screen(c, W, H, s3x, s3y)) {
-        const uint32_t seed_u = (uint32_t)(int64_t)(*d.t + 0.5f);
-        for (uint32_t s0 = 0; s0 < d.n_samples; s0 += kAaBatch) {
-            // a batch of samples: positions, then their pred / target loads
-            // together, then the pairs of the samples that carry gradient
-            int sx[kAaBatch], sy[kAaBatch];
-            float gys[kAaBatch];
+    const bool face_ok = valid && d.n_samples > 0 && aa_face_screen(c, W, H, s3x, s3y);
+    const uint32_t seed_u = (uint32_t)(int64_t)(*d.t + 0.5f);
+    for (uint32_t s0 = 0; s0 < d.n_samples; s0 += 8) {
+        // lane j: sample s0 + j and d loss / d pred there,
+        // diff = target - pred, -(c diff + c diff); gy = 0 zeroes every gr
+        int sx = -1, sy = -1;
+        float gy = 0.f;
+        if (face_ok && s0 + j < d.n_samples &&
+            aa_sample_px(s3x, s3y, f, s0 + j, seed_u, &sx, &sy) && sx >= 0 && sy >= 0 &&
+            sx < w && sy < h) {
+            const size_t so = (size_t)sy * w + sx;
+            const float diff = tgt[so] - pred[so];
+            const float cd = d.inv_px * diff;
+            gy = -(cd + cd);
+        }
+        const bool act = sx >= 0 && sy >= 0 && sx < w && sy < h && gy != 0.f;
+        uint32_t bmask = fold_groups(__ballot(act));
+        while (bmask) {
+            const int b = __builtin_ctz(bmask);
+            bmask &= bmask - 1;
+            const int x = grp_shfl(sx, gbase + b);
+            const int y = grp_shfl(sy, gbase + b);
+            const float gyb = grp_shfl(gy, gbase + b);
+            const bool on = grp_shfl((int)act, gbase + b) != 0;
+            // lane k = j: the pair with neighbour k and its corner terms
+            uint32_t tflag = 0;
+            float tx[3] = {0.f, 0.f, 0.f}, ty[3] = {0.f, 0.f, 0.f}, tw[3] = {0.f, 0.f, 0.f};
+            if (on) {
+                const int nx = x + kAaOffX[j], ny = y + kAaOffY[j];
+                if (!(nx < 0 || ny < 0 || nx >= w || ny >= h)) {
+                    const uint32_t its = ids[(size_t)y * w + x];
+                    const uint32_t itn = ids[(size_t)ny * w + nx];
+                    const float ms = its ? 1.f : 0.f;
+                    const float mn = itn ? 1.f : 0.f;
+                    float gr = 0.f;
+                    gr += gyb * (ms - mn);
+                    gr /= 9.f;
+                    AaPair pr;
+                    if (gr != 0.f && eval_aa_pair(its, itn, x, y, nx, ny, d.g.n_faces, tris, &pr) &&
+                        pr.r < 1.f) {
+                        float dqa[2], dqb[2];
+                        aa_pair_dq(pr, x, y, dqa, dqb);
+                        // an endpoint that is corner kc of this face has clip
+                        // c[kc]; an active edge has two distinct endpoints
 #pragma unroll
-            for (int b = 0; b < kAaBatch; b++) {
-                const uint32_t smp = s0 + b;
-                const bool ok = smp < d.n_samples &&
-                                aa_sample_px(s3x, s3y, f, smp, seed_u, &sx[b], &sy[b]) &&
-                                !(sx[b] < 0 || sy[b] < 0 || sx[b] >= (int)w || sy[b] >= (int)h);
-                if (!ok) {
-                    sx[b] = -1;
-                    gys[b] = 0.f;
-                    continue;
+                        for (int kc = 0; kc < 3; kc++) {
+                            const bool ea = pr.ia == vc[kc];
+                            if (ea || pr.ib == vc[kc]) {
+                                const float* dq = ea ? dqa : dqb;
+                                const float gqx = gr * dq[0];
+                                const float gqy = gr * dq[1];
+                                tx[kc] = gqx * 0.5f * W / c[kc].w;
+                                ty[kc] = gqy * 0.5f * H / c[kc].w;
+                                tw[kc] = -(gqx * 0.5f * W * c[kc].x + gqy * 0.5f * H * c[kc].y) /
+                                         (c[kc].w * c[kc].w);
+                                tflag |= 1u << kc;
+                            }
+                        }
+                    }
                 }
-                const size_t so = (size_t)sy[b] * w + sx[b];
-                // d loss / d pred at s: diff = target - pred, -(c diff + c diff)
-                const float diff = tgt[so] - pred[so];
-                const float cd = d.inv_px * diff;
-                gys[b] = -(cd + cd);
             }
-#pragma unroll 1
-            for (int b = 0; b < kAaBatch; b++) {
-            // gy = 0 makes every pair's gr exactly 0
-            const float gy = gys[b];
-            if (sx[b] < 0 || gy == 0.f) {
-                continue;
-            }
-            const int x = sx[b], y = sy[b];
-            const size_t so = (size_t)y * w + x;
-            const uint32_t its = ids[so];
-            const float ms = its ? 1.f : 0.f;
-            for (int k = 0; k < 8; k++) {
-                const int nx = x + kAaOffX[k], ny = y + kAaOffY[k];
-                if (nx < 0 || ny < 0 || nx >= (int)w || ny >= (int)h) {
-                    continue;
-                }
-                const uint32_t itn = ids[(size_t)ny * w + nx];
-                const float mn = itn ? 1.f : 0.f;
-                float gr = 0.f;
-                gr += gy * (ms - mn);
-                gr /= 9.f;
-                if (gr == 0.f) {
-                    continue;
-                }
-                AaPair pr;
-                if (!eval_aa_pair(its, itn, x, y, nx, ny, d.g.n_faces,
-                                  TriFromRecs{d.faces, d.arecs + (size_t)view * d.g.n_faces},
-                                  &pr) ||
-                    pr.r >= 1.f) {
-                    continue;
-                }
-                float dqa[2], dqb[2];
-                aa_pair_dq(pr, x, y, dqa, dqb);
+            // the group adds neighbour k's terms for k = 0..7 in order
+            uint32_t kmask = fold_groups(__ballot(tflag != 0));
+            while (kmask) {
+                const int k = __builtin_ctz(kmask);
+                kmask &= kmask - 1;
+                const int src = gbase + k;
+                const uint32_t fl = (uint32_t)grp_shfl((int)tflag, src);
 #pragma unroll
                 for (int kc = 0; kc < 3; kc++) {
-                    if (pr.ia == vc[kc]) {
-                        aa_add_endpoint(gr, dqa, clip[pr.ia], W, H, &acc[kc]);
-                    }
-                    if (pr.ib == vc[kc]) {
-                        aa_add_endpoint(gr, dqb, clip[pr.ib], W, H, &acc[kc]);
+                    const float vx = grp_shfl(tx[kc], src);
+                    const float vy = grp_shfl(ty[kc], src);
+                    const float vw = grp_shfl(tw[kc], src);
+                    if (fl >> kc & 1u) {
+                        acc[kc].x += vx;
+                        acc[kc].y += vy;
+                        acc[kc].w += vw;
                     }
                 }
-            }
             }
         }
     }
-    float4* dst = d.gtri + (size_t)view * 3 * d.g.n_faces;
-#pragma unroll
-    for (int k = 0; k < 3; k++) {
-        dst[(size_t)k * d.g.n_faces + f] = acc[k];
+    if (valid && j < 3) {
+        float4* dst = d.gtri + (size_t)view * 3 * d.g.n_faces;
+        dst[(size_t)j * d.g.n_faces + f] = j == 0 ? acc[0] : j == 1 ? acc[1] : acc[2];
     }
 }
 
@@ -714,13 +851,18 @@ int launch_aa_kernel(const HsrDev& d, hipStream_t s, int k) {
             break;
         case 2:
         case 4: {
-            const dim3 grid = k == 2 ? dim3(div_up(g.width, 64), g.height)
+            const dim3 grid = k == 2 ? dim3(div_up(g.width, 256), g.height)
                                      : dim3(div_up(d.n_verts, 256));
+            const bool vec = (g.width & 3u) == 0;
             switch (g.n_views) {
 #define DRESSI_NV(N)                                                                      \
     case N:                                                                               \
         if (k == 2) {                                                                     \
-            hipLaunchKernelGGL(k_aa_fwd<N>, grid, dim3(64 * N), 0, s, d);                 \
+            if (vec) {                                                                    \
+                hipLaunchKernelGGL((k_aa_fwd<N, true>), grid, dim3(64 * N), 0, s, d);     \
+            } else {                                                                      \
+                hipLaunchKernelGGL((k_aa_fwd<N, false>), grid, dim3(64 * N), 0, s, d);    \
+            }                                                                             \
         } else {                                                                          \
             hipLaunchKernelGGL(k_aa_vertex_adam<N>, grid, dim3(256), 0, s, d);            \
         }                                                                                 \
@@ -735,7 +877,7 @@ int launch_aa_kernel(const HsrDev& d, hipStream_t s, int k) {
             break;
         }
         default:
-            hipLaunchKernelGGL(k_aa_face_bwd, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
+            hipLaunchKernelGGL(k_aa_face_bwd, dim3(div_up(nvf, 32)), dim3(256), 0, s, d);
             break;
     }
     DRESSI_CHECK_LAUNCH();

@@ -402,6 +402,15 @@ int plan_alloc(dressi_hsr_plan* p, T** out, size_t count) {
     return DRESSI_OK;
 }
 
+// Zeroes the bin counters (what the face backward does in passing); used by
+// the per-kernel profile to time the setup on its own.
+__global__ __launch_bounds__(256) void k_clear_bin_counts(HsrDev d) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < d.bins.n_bins) {
+        d.bins.counts[i] = 0;
+    }
+}
+
 // Kernel k of one iteration: 0 setup + binning, 1 visibility raster,
 // 2 pred + loss, 3 face backward, 4 vertex backward + Adam.
 constexpr int kIterKernels = 5;
@@ -866,17 +875,18 @@ int dressi_hsr_profile(dressi_hsr_plan* p, uint32_t iters, char* names, size_t n
     // vertex kernels are each launched `iters` times back to back between
     // two HIP events on the plan stream (the first three are idempotent; the
     // vertex kernel advances Adam each time). The setup appends to the bins,
-    // so it is timed as `iters` (setup, face backward) pairs -- the face
-    // backward clears the bins -- minus the face backward's own time. The
-    // optimisation moves 2 iters + 1 steps.
+    // so it is timed as `iters` (bin clear, setup) pairs minus `iters` bin
+    // clears timed alone. The optimisation moves 2 iters + 1 steps.
     const uint32_t reps = iters ? iters : 1;
     *n = kIterKernels;
     hipStream_t s = p->ctx->stream;
-    // timed groups: raster, loss, face bwd, vertex, (setup + face bwd)
-    const int order[kIterKernels] = {1, 2, 3, 4, 0};
-    hipEvent_t ev[kIterKernels + 1] = {};
+    // timed groups: raster, loss, face bwd, vertex, bin clear,
+    // (bin clear + setup); -1 is the clear alone
+    constexpr int kGroups = kIterKernels + 1;
+    const int order[kGroups] = {1, 2, 3, 4, -1, 0};
+    hipEvent_t ev[kGroups + 1] = {};
     int rc = DRESSI_OK;
-    for (int i = 0; i <= kIterKernels && !rc; i++) {
+    for (int i = 0; i <= kGroups && !rc; i++) {
         if (hipEventCreate(&ev[i]) != hipSuccess) {
             set_error("hipEventCreate failed");
             rc = DRESSI_ERR_HIP;
@@ -884,36 +894,51 @@ int dressi_hsr_profile(dressi_hsr_plan* p, uint32_t iters, char* names, size_t n
     }
     if (!rc) rc = enqueue_iteration(p, s);
     if (!rc) rc = launch_iter_kernel(p->d, s, 0);
-    for (int i = 0; i < kIterKernels && !rc; i++) {
+    const dim3 clear_grid(div_up(p->d.bins.n_bins, 256));
+    for (int i = 0; i < kGroups && !rc; i++) {
         if (hipEventRecord(ev[i], s) != hipSuccess) {
             set_error("hipEventRecord failed");
             rc = DRESSI_ERR_HIP;
             break;
         }
         for (uint32_t r = 0; r < reps && !rc; r++) {
-            rc = launch_iter_kernel(p->d, s, order[i]);
-            if (!rc && order[i] == 0) {
-                rc = launch_iter_kernel(p->d, s, 3);
+            if (order[i] <= 0) {
+                hipLaunchKernelGGL(k_clear_bin_counts, clear_grid, dim3(256), 0, s, p->d);
+                if (hipGetLastError() != hipSuccess) {
+                    set_error("k_clear_bin_counts launch failed");
+                    rc = DRESSI_ERR_HIP;
+                }
+            }
+            if (!rc && order[i] >= 0) {
+                rc = launch_iter_kernel(p->d, s, order[i]);
             }
         }
     }
-    if (!rc && (hipEventRecord(ev[kIterKernels], s) != hipSuccess ||
-                hipEventSynchronize(ev[kIterKernels]) != hipSuccess)) {
+    if (!rc && (hipEventRecord(ev[kGroups], s) != hipSuccess ||
+                hipEventSynchronize(ev[kGroups]) != hipSuccess)) {
         set_error("event synchronisation failed");
         rc = DRESSI_ERR_HIP;
     }
     float ms[kIterKernels] = {};
-    for (int i = 0; i < kIterKernels && !rc; i++) {
+    float clear_ms = 0.f;
+    for (int i = 0; i < kGroups && !rc; i++) {
         float t = 0.f;
         if (hipEventElapsedTime(&t, ev[i], ev[i + 1]) != hipSuccess) {
             set_error("hipEventElapsedTime failed");
             rc = DRESSI_ERR_HIP;
             break;
         }
-        ms[order[i]] = t / reps;
+        (order[i] < 0 ? clear_ms : ms[order[i]]) = t / reps;
     }
     if (!rc) {
-        ms[0] = ms[0] > ms[3] ? ms[0] - ms[3] : 0.f;
+        ms[0] = ms[0] > clear_ms ? ms[0] - clear_ms : 0.f;
+        // the last setup left its faces in the bins: empty them for the
+        // next iteration
+        hipLaunchKernelGGL(k_clear_bin_counts, clear_grid, dim3(256), 0, s, p->d);
+        if (hipGetLastError() != hipSuccess) {
+            set_error("k_clear_bin_counts launch failed");
+            rc = DRESSI_ERR_HIP;
+        }
     }
     for (uint32_t k = 0; k < (uint32_t)kIterKernels && k < cap && !rc; k++) {
         if (usec) {

@@ -155,6 +155,35 @@ def test_aa_trajectory_matches_reference(ctx, golden, name):
     fit.close()
 
 
+@pytest.mark.parametrize("screen", [97, 301])
+def test_aa_odd_screen_matches_oracle(ctx, oracle, screen):
+    """Screens that are not a multiple of 4 px (scalar row path, a partial
+    last lane) and wider than one 256-px forward workgroup: ids, pred, loss
+    image and gradient of the first iteration, then 3 iterations of state."""
+    import opendressi_amd as od
+    from opendressi_amd import _lib as L
+    print(f"[aa odd screen] {screen}", flush=True)
+    w = od.Workload("odd", 3, screen, 4, 0.05, 0.1, 1e-3, 3, 7, "aa")
+    pos, faces, tgt, mvps = od.make_scene(w)
+    fit = od.SilhouetteFit(ctx, pos, faces, mvps, screen, target_mesh=(tgt, faces), lr=w.lr,
+                           keep_pred=True, keep_grad=True, technique="aa")
+    fit.step(1)
+    ctx.synchronize()
+    got = {k: fit.read(b) for k, b in (("tri0", L.BUF_FACE_ID), ("pred0", L.BUF_PRED),
+                                       ("lossimg0", L.BUF_LOSS), ("grad0", L.BUF_GRAD))}
+    fit.step(2)
+    pos_g, m_g, v_g, t_g = fit.state()
+    fit.close()
+    ref = oracle.aa_fit(pos, faces, tgt, faces, mvps, screen, lr=w.lr, iters=3)
+    _exact(got["tri0"].astype(np.float32), ref["tri0"], "face ids")
+    for k in ("pred0", "lossimg0", "grad0"):
+        _exact(got[k], ref[k], k)
+    assert t_g == 3.0
+    _exact(pos_g, ref["pos"], "pos")
+    _exact(m_g, ref["m"], "m")
+    _exact(v_g, ref["v"], "v")
+
+
 def test_aa_graph_replay_equals_eager(ctx):
     import opendressi_amd as od
     from opendressi_amd import _lib as L
