@@ -346,6 +346,7 @@ __global__ __launch_bounds__(256) void k_aa_setup(HsrDev d) {
     r.by0 = 1;
     r.by1 = 0;
     r.margin = -1.f;
+    r.zcull = 0.f;
     if (live) {
         const float W = (float)d.g.width, H = (float)d.g.height;
         bool ok = true;
@@ -376,6 +377,13 @@ __global__ __launch_bounds__(256) void k_aa_setup(HsrDev d) {
                 r.margin = (fabsf(area) > 0x1p-20f * pa && m < INFINITY) ? m : -1.f;
                 pixel_bbox(r.x[0], r.x[1], r.x[2], r.y[0], r.y[1], r.y[2], (int)d.g.width,
                            (int)d.g.height, &r.bx0, &r.by0, &r.bx1, &r.by1);
+                // At a covered pixel l0, l1, l2 >= 0 and l2 = (1 - l0) - l1
+                // make l0 + l1 + l2 >= 1 - 2.01u (u = 2^-24), so with all z
+                // positive the interpolated z (three roundings) is at least
+                // zmin (1 - 5.1u), and fl(zmin (1 - 2^-20)) < zmin (1 - 15u)
+                // lies strictly below it.
+                const float zmin = smin(smin(r.z[0], r.z[1]), r.z[2]);
+                r.zcull = zmin > 0.f ? zmin * (1.f - 0x1p-20f) : 0.f;
             }
         }
         d.arecs[i] = r;
@@ -386,9 +394,11 @@ __global__ __launch_bounds__(256) void k_aa_setup(HsrDev d) {
 
 // Separating-axis test of a hard triangle's coverage region (its
 // barycentrics >= 0 up to the record's margin) against the 8x8 block.
-__device__ __forceinline__ bool aa_tri_reaches_block(const AaRec* rec, int bx, int by) {
+__device__ __forceinline__ bool aa_tri_reaches_block(const AaRec* rec, int bx, int by,
+                                                     bool* neg) {
     const float4 a = *(const float4*)&rec->x[0];  // x0 x1 x2 y0
     const float4 b = *(const float4*)&rec->y[1];  // y1 y2 inv_area margin
+    *neg = b.z < 0.f;
     const float m = b.w;
     if (!(m >= 0.f)) {
         return true;
@@ -426,12 +436,40 @@ __device__ __forceinline__ AaRec load_aa_rec_uniform(const AaRec* recs, uint32_t
     return u.r;
 }
 
+// Folds face fj (its record r) into the lane's depth key: coverage by the
+// reference's inclusive barycentrics, NDC z in [0, 1], smaller key wins.
+__device__ __forceinline__ void aa_fold_face(const AaRec& r, uint32_t fj, int px, int py,
+                                             uint64_t* best) {
+    if (px < r.bx0 || px > r.bx1 || py < r.by0 || py > r.by1) {
+        return;
+    }
+    const float p0 = (float)px + 0.5f, p1 = (float)py + 0.5f;
+    float l0, l1, l2;
+    barycentric(p0, p1, r.x[0], r.y[0], r.x[1], r.y[1], r.x[2], r.y[2], r.inv_area, &l0, &l1,
+                &l2);
+    if (l0 < 0.f || l1 < 0.f || l2 < 0.f) {
+        return;
+    }
+    const float z = l0 * r.z[0] + l1 * r.z[1] + l2 * r.z[2];
+    if (z < 0.f || z > 1.f) {
+        return;
+    }
+    const uint64_t key = depth_key(z, fj);
+    *best = key < *best ? key : *best;
+}
+
 // Visibility of the hard raster: one single-wave workgroup per (view, 8x8
 // block) folds (z | ~face) keys of the faces binned to its tile (coverage by
 // the reference's inclusive barycentrics, NDC z in [0,1], LessOrEqual: the
-// later face wins ties) and writes face + 1 (0 = background). Tiles are dealt
-// to the XCDs round robin, the four blocks of a tile on one XCD.
+// later face wins ties) and writes face + 1 (0 = background). The key
+// minimum does not depend on the order the faces are folded in, so faces
+// with negative screen area (the front faces of a closed mesh in this
+// projection) go first and the others are kept in LDS; those whose zcull
+// lies above every lane's depth after the first pass cannot win a pixel and
+// are skipped. Tiles are dealt to the XCDs round robin, the four blocks of a
+// tile on one XCD.
 __global__ __launch_bounds__(64) void k_aa_raster(HsrDev d) {
+    __shared__ uint32_t later[kSoftBinCap];
     const uint32_t per = (d.g.n_tiles + 7u) / 8u;
     const uint32_t k = blockIdx.x >> 3;
     const uint32_t q = k & 3u;
@@ -446,41 +484,55 @@ __global__ __launch_bounds__(64) void k_aa_raster(HsrDev d) {
     const int lane = threadIdx.x & 63;
     const int px = bx + (lane & 7);
     const int py = by + (lane >> 3);
-    const float p0 = (float)px + 0.5f, p1 = (float)py + 0.5f;
     const AaRec* recs = d.arecs + (size_t)view * d.g.n_faces;
     const BinView bv = bin_view(d.bins, view * d.g.n_tiles + tile, d.g.n_faces);
+    // an overflowed bin (every face) is walked in one pass
+    const bool defer = !bv.implicit && bv.n <= kSoftBinCap;
+    uint32_t n_later = 0;
     uint64_t best = kEmptyKey;
     for (uint32_t base = 0; base < bv.n; base += 64) {
         const uint32_t e = base + (uint32_t)lane;
         uint32_t f = 0;
-        bool keep = false;
+        bool keep = false, neg = false;
         if (e < bv.n) {
             f = bv.implicit ? e : bv.list[e];
             const int4 bb = *(const int4*)&recs[f].bx0;
             keep = bb.x <= bx + 7 && bb.z >= bx && bb.y <= by + 7 && bb.w >= by &&
-                   aa_tri_reaches_block(recs + f, bx, by);
+                   aa_tri_reaches_block(recs + f, bx, by, &neg);
         }
-        uint64_t m = __ballot(keep);
+        const bool hold = defer && keep && !neg;
+        const uint64_t mh = __ballot(hold);
+        if (hold) {
+            const uint32_t below = __builtin_amdgcn_mbcnt_hi(
+                    (uint32_t)(mh >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mh, 0u));
+            later[n_later + below] = f;
+        }
+        n_later += (uint32_t)__popcll(mh);
+        uint64_t m = __ballot(keep && !hold);
         while (m) {
             const int j = __builtin_ctzll(m);
             m &= m - 1;
             const uint32_t fj = (uint32_t)__builtin_amdgcn_readlane((int)f, j);
+            aa_fold_face(load_aa_rec_uniform(recs, fj), fj, px, py, &best);
+        }
+    }
+    if (n_later) {
+        __syncthreads();
+        // the deepest lane depth (an empty lane: all ones, nothing is skipped)
+        uint32_t zmax = (uint32_t)(best >> 32);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const uint32_t other = (uint32_t)__shfl_xor((int)zmax, o);
+            zmax = other > zmax ? other : zmax;
+        }
+        zmax = (uint32_t)__builtin_amdgcn_readfirstlane((int)zmax);
+        for (uint32_t i = 0; i < n_later; i++) {
+            const uint32_t fj = (uint32_t)__builtin_amdgcn_readfirstlane((int)later[i]);
             const AaRec r = load_aa_rec_uniform(recs, fj);
-            if (px < r.bx0 || px > r.bx1 || py < r.by0 || py > r.by1) {
-                continue;
+            if (__float_as_uint(r.zcull) > zmax) {
+                continue;  // zcull >= 0: bit order is value order
             }
-            float l0, l1, l2;
-            barycentric(p0, p1, r.x[0], r.y[0], r.x[1], r.y[1], r.x[2], r.y[2], r.inv_area,
-                        &l0, &l1, &l2);
-            if (l0 < 0.f || l1 < 0.f || l2 < 0.f) {
-                continue;
-            }
-            const float z = l0 * r.z[0] + l1 * r.z[1] + l2 * r.z[2];
-            if (z < 0.f || z > 1.f) {
-                continue;
-            }
-            const uint64_t key = depth_key(z, fj);
-            best = key < best ? key : best;
+            aa_fold_face(r, fj, px, py, &best);
         }
     }
     if (px < (int)d.g.width && py < (int)d.g.height) {
@@ -489,79 +541,80 @@ __global__ __launch_bounds__(64) void k_aa_raster(HsrDev d) {
     }
 }
 
-// Sum c_s + sum_k [r c_s + (1 - r) c_n] of AntiAlias over the 8 neighbours
-// of mask pixel (x, y) (f_ops.cpp:2544-2576 with one channel), its = face +
-// 1 of the pixel. With c_s = c_n in {0, 1} an active pair adds r c + (1 - r)
-// c, which rounds to exactly c (1 - r is within half an ulp of its exact
-// value and r + fl(1 - r) rounds back to 1), so only pairs across the
-// silhouette evaluate their edge; the neighbour ids are read again here.
-__device__ float aa_mask_sum(const uint32_t* ids, const TriFromRecs& tris, uint32_t n_faces,
-                             int x, int y, int w, int h, uint32_t its) {
-    const float cs = its ? 1.f : 0.f;
-    float dst = cs;
-    for (int k = 0; k < 8; k++) {
-        const int nx = x + kAaOffX[k], ny = y + kAaOffY[k];
-        const uint32_t itn =
-                (nx < 0 || ny < 0 || nx >= w || ny >= h) ? its : ids[(size_t)ny * w + nx];
-        AaPair pr;
-        if ((its == 0u) == (itn == 0u) ||
-            !eval_aa_pair(its, itn, x, y, nx, ny, n_faces, tris, &pr)) {
-            dst += cs;
-            continue;
-        }
-        const float cn = itn ? 1.f : 0.f;
-        dst += pr.r * cs + (1.f - pr.r) * cn;
-    }
-    return dst;
+// Orders the LDS accesses of one wave around an exchange between its lanes
+// (a wave executes its LDS instructions in order).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Mask bits (1 = covered) of ids columns x0 .. x0+3 of one row.
+__device__ __forceinline__ uint32_t fg_bits4(uint32_t a, uint32_t b, uint32_t c, uint32_t e) {
+    return (a != 0u ? 1u : 0u) | (b != 0u ? 2u : 0u) | (c != 0u ? 4u : 0u) | (e != 0u ? 8u : 0u);
 }
 
 // AntiAlias of the mask (Rasterize(clip, 1): 1 exactly where covered) and the
-// L2 loss. A lane covers 4 consecutive pixels of a row in one view, a wave
-// 256 pixels, the NV waves of a workgroup the NV views of the same pixels,
-// their SumPixelWise reduced through LDS. A pixel whose 8 neighbours all
-// have its mask value sums 9 c exactly (pred = c); the others (the
-// silhouette) take aa_mask_sum. pred is kept for the face backward. VEC: the
-// row width is a multiple of 4 (16-byte loads and stores).
+// L2 loss (f_ops.cpp:2544-2576 with one channel). A lane covers 4
+// consecutive pixels of a row in one view, a wave 256 pixels, the NV waves of
+// a workgroup the NV views of the same pixels, their SumPixelWise reduced
+// through LDS. With c_s = c_n in {0, 1} an active pair adds r c + (1 - r) c,
+// which rounds to exactly c (1 - r is within half an ulp of its exact value
+// and r + fl(1 - r) rounds back to 1), so a pixel whose in-screen neighbours
+// all share its mask value sums 9 c exactly (pred = c); those are found from
+// 3x3 windows of mask bits (an off-screen neighbour counts as agreeing; it is
+// filled with a copy of an in-screen value of the same window). The other
+// pixels (the silhouette) are queued in LDS and evaluated 8 at a time, one
+// 8-lane group each, lane k taking neighbour k, the group then summing the
+// nine terms in the reference's order. pred is kept for the face backward.
+// VEC: the row width is a multiple of 4 (16-byte loads and stores).
 template <int NV, bool VEC>
 __global__ __launch_bounds__(64 * NV) void k_aa_fwd(HsrDev d) {
     __shared__ float4 lv[NV][64];
+    __shared__ uint32_t queue[NV][256];
+    __shared__ float epred[NV][256];
     const uint32_t view = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int w = (int)d.g.width, h = (int)d.g.height;
-    const int x0 = (int)blockIdx.x * 256 + lane * 4;
+    const int xw = (int)blockIdx.x * 256;
+    const int x0 = xw + lane * 4;
     const int y = (int)blockIdx.y;
     const size_t npx = (size_t)w * h;
     const size_t o = (size_t)y * w + x0;
     const uint32_t* ids = d.ids + view * npx;
-    // ids of rows y-1, y, y+1 at x0-1 .. x0+4 (entry c + 1 is column x0 + c);
-    // off-screen entries are never used
-    uint32_t r[3][6];
-    float tg[4];
     const bool any = x0 < w;
+    // rows y-1, y, y+1: 6-bit masks, bit i = column x0 - 1 + i
+    uint32_t row[3];
+    uint32_t fg4 = 0;
 #pragma unroll
     for (int ry = 0; ry < 3; ry++) {
         const int yy = y + ry - 1;
         const bool row_ok = any && yy >= 0 && yy < h;
-        const uint32_t* row = ids + (size_t)(row_ok ? yy : 0) * w;
+        const uint32_t* rp = ids + (size_t)(row_ok ? yy : 0) * w;
+        uint32_t m;
         if (VEC) {
-            const uint4 q = row_ok ? *reinterpret_cast<const uint4*>(row + x0) : uint4{0, 0, 0, 0};
-            r[ry][1] = q.x;
-            r[ry][2] = q.y;
-            r[ry][3] = q.z;
-            r[ry][4] = q.w;
+            const uint4 q = row_ok ? *reinterpret_cast<const uint4*>(rp + x0) : uint4{0, 0, 0, 0};
+            m = fg_bits4(q.x, q.y, q.z, q.w);
         } else {
+            uint32_t v[4];
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                r[ry][c + 1] = row_ok && x0 + c < w ? row[x0 + c] : 0u;
+                v[c] = row_ok && x0 + c < w ? rp[x0 + c] : 0u;
             }
+            m = fg_bits4(v[0], v[1], v[2], v[3]);
         }
-        // the columns either side come from the neighbouring lanes; the
-        // wave's outer lanes load them
-        const uint32_t left = __shfl_up(r[ry][4], 1);
-        const uint32_t right = __shfl_down(r[ry][1], 1);
-        r[ry][0] = lane == 0 ? (row_ok && x0 > 0 ? row[x0 - 1] : 0u) : left;
-        r[ry][5] = lane == 63 ? (row_ok && x0 + 4 < w ? row[x0 + 4] : 0u) : right;
+        // the wave's outer lanes read the columns beyond it
+        uint32_t lcol = 0, rcol = 0;
+        if (lane == 0 && row_ok && x0 > 0) {
+            lcol = rp[x0 - 1] != 0u ? 1u : 0u;
+        }
+        if (lane == 63 && row_ok && x0 + 4 < w) {
+            rcol = rp[x0 + 4] != 0u ? 1u : 0u;
+        }
+        row[ry] = m;
+        fg4 |= (lcol | rcol << 1) << (2 * ry);  // lane 0 / 63 only
     }
+    float tg[4];
     const float* tgt = d.targets + view * npx;
     if (VEC) {
         const float4 q = any ? *reinterpret_cast<const float4*>(tgt + o) : float4{0, 0, 0, 0};
@@ -575,53 +628,118 @@ __global__ __launch_bounds__(64 * NV) void k_aa_fwd(HsrDev d) {
             tg[c] = any && x0 + c < w ? tgt[o + c] : 0.f;
         }
     }
-    // 8-neighbour mask agreement of each pixel (off-screen neighbours agree)
-    float pred[4];
+    // neighbouring lanes' edge columns (12 bits: 4 per row)
+    const uint32_t own = row[0] | row[1] << 4 | row[2] << 8;
+    const uint32_t from_left = (uint32_t)__shfl_up((int)own, 1);
+    const uint32_t from_right = (uint32_t)__shfl_down((int)own, 1);
+    // columns in screen: x0 - 1 + i < w for i < ncol (>= 2 where any)
+    const int ncol = w - x0 + 1 < 6 ? w - x0 + 1 : 6;
     uint32_t edge = 0;
+    float pred[4];
+    if (any) {
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const bool fg = r[1][c + 1] != 0u;
-        bool mixed = false;
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int nx = x0 + c + kAaOffXh[k], ny = y + kAaOffYh[k];
-            const bool in = nx >= 0 && ny >= 0 && nx < w && ny < h;
-            mixed |= in && ((r[1 + kAaOffYh[k]][c + 1 + kAaOffXh[k]] != 0u) != fg);
+        for (int ry = 0; ry < 3; ry++) {
+            const uint32_t l = lane == 0 ? (fg4 >> (2 * ry)) & 1u : (from_left >> (4 * ry + 3)) & 1u;
+            const uint32_t r = lane == 63 ? (fg4 >> (2 * ry + 1)) & 1u : (from_right >> (4 * ry)) & 1u;
+            uint32_t m = l | row[ry] << 1 | r << 5;
+            if (x0 == 0) {
+                m = (m & ~1u) | ((m >> 1) & 1u);
+            }
+            if (ncol < 6) {
+                const uint32_t keep = (1u << ncol) - 1u;
+                m = (m & keep) | (((m >> (ncol - 1)) & 1u) ? (0x3fu & ~keep) : 0u);
+            }
+            row[ry] = m;
         }
-        edge |= mixed && x0 + c < w ? 1u << c : 0u;
-        // nine equal terms: 9 c / 9 = c
-        pred[c] = fg ? 1.f : 0.f;
-    }
-    if (edge) {
-        const TriFromRecs tris{d.faces, d.arecs + (size_t)view * d.g.n_faces};
-#pragma unroll 1
+        if (y == 0) {
+            row[0] = row[1];
+        }
+        if (y == h - 1) {
+            row[2] = row[1];
+        }
+#pragma unroll
         for (int c = 0; c < 4; c++) {
-            if (edge >> c & 1u) {
-                const uint32_t its = c == 0 ? r[1][1] : c == 1 ? r[1][2] : c == 2 ? r[1][3] : r[1][4];
-                const float v = aa_mask_sum(ids, tris, d.g.n_faces, x0 + c, y, w, h, its) / 9.f;
-                pred[0] = c == 0 ? v : pred[0];
-                pred[1] = c == 1 ? v : pred[1];
-                pred[2] = c == 2 ? v : pred[2];
-                pred[3] = c == 3 ? v : pred[3];
+            const uint32_t win = ((row[0] >> c) & 7u) | ((row[1] >> c) & 7u) << 3 |
+                                 ((row[2] >> c) & 7u) << 6;
+            edge |= (win != 0u && win != 0x1ffu && x0 + c < w) ? 1u << c : 0u;
+            // nine equal terms: 9 c / 9 = c
+            pred[c] = (row[1] >> (c + 1)) & 1u ? 1.f : 0.f;
+        }
+    }
+    if (__ballot(edge != 0u)) {
+        // queue the silhouette pixels of the wave as lane * 4 + c
+        uint32_t* qv = queue[view];
+        uint32_t n_q = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const bool e = (edge >> c) & 1u;
+            const uint64_t m = __ballot(e);
+            if (e) {
+                const uint32_t below = __builtin_amdgcn_mbcnt_hi(
+                        (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                qv[n_q + below] = (uint32_t)lane * 4u + (uint32_t)c;
+            }
+            n_q += (uint32_t)__popcll(m);
+        }
+        wave_lds_sync();
+        const TriFromRecs tris{d.faces, d.arecs + (size_t)view * d.g.n_faces};
+        const int k = lane & 7;
+        for (uint32_t q0 = 0; q0 < n_q; q0 += 8) {
+            const uint32_t qi = q0 + (uint32_t)(lane >> 3);
+            const bool ok = qi < n_q;
+            uint32_t slot = 0;
+            float cs = 0.f, term = 0.f;
+            if (ok) {
+                slot = qv[qi];
+                const int x = xw + (int)slot;
+                const uint32_t its = ids[(size_t)y * w + x];
+                cs = its ? 1.f : 0.f;
+                term = cs;
+                const int nx = x + kAaOffXh[k], ny = y + kAaOffYh[k];
+                if (!(nx < 0 || ny < 0 || nx >= w || ny >= h)) {
+                    const uint32_t itn = ids[(size_t)ny * w + nx];
+                    AaPair pr;
+                    if ((its == 0u) != (itn == 0u) &&
+                        eval_aa_pair(its, itn, x, y, nx, ny, d.g.n_faces, tris, &pr)) {
+                        const float cn = itn ? 1.f : 0.f;
+                        term = pr.r * cs + (1.f - pr.r) * cn;
+                    }
+                }
+            }
+            // c_s, then the eight neighbours' terms in order
+            float dst = cs;
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) {
+                dst += __shfl(term, (lane & 56) + kk);
+            }
+            if (ok && k == 0) {
+                epred[view][slot] = dst / 9.f;
+            }
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            if ((edge >> c) & 1u) {
+                pred[c] = epred[view][lane * 4 + c];
             }
         }
     }
-    float l[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const float diff = tg[c] - pred[c];
-        l[c] = diff * diff * d.inv_px;
-    }
-    float* pd = d.pred + view * npx;
-    if (VEC) {
-        if (any) {
-            *reinterpret_cast<float4*>(pd + o) = make_float4(pred[0], pred[1], pred[2], pred[3]);
-        }
-    } else {
+    float l[4] = {0.f, 0.f, 0.f, 0.f};
+    if (any) {
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            if (any && x0 + c < w) {
-                pd[o + c] = pred[c];
+            const float diff = tg[c] - pred[c];
+            l[c] = diff * diff * d.inv_px;
+        }
+        float* pd = d.pred + view * npx;
+        if (VEC) {
+            *reinterpret_cast<float4*>(pd + o) = make_float4(pred[0], pred[1], pred[2], pred[3]);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                if (x0 + c < w) {
+                    pd[o + c] = pred[c];
+                }
             }
         }
     }
@@ -633,9 +751,9 @@ __global__ __launch_bounds__(64 * NV) void k_aa_fwd(HsrDev d) {
         for (int c = 0; c < 4; c++) {
             float in[NV][1];
 #pragma unroll
-            for (int k = 0; k < NV; k++) {
-                const float4 q = lv[k][lane];
-                in[k][0] = c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w;
+            for (int v = 0; v < NV; v++) {
+                const float4 q = lv[v][lane];
+                in[v][0] = c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w;
             }
             float one[1];
             Tree<NV, 1>::run(in, one);

@@ -16,14 +16,15 @@ __device__ __constant__ const int kAaOffY[8] = {-1, -1, -1, 0, 0, 1, 1, 1};
 // Per (view, face) record of the fused hard raster (RasterizeCore,
 // cpu_raster.cpp:42-94): screen corners, 1 / area, coverage margin for the
 // block cull (as the soft raster's), inclusive pixel bbox (bx0 > bx1: no
-// fragment), NDC z. 16 words; words 0-7 and 8-11 are 16-byte loads of the cull.
+// fragment), NDC z and a depth below every z the face can produce at a
+// covered pixel. 16 words; words 0-7 and 8-11 are 16-byte loads of the cull.
 struct alignas(16) AaRec {
     float x[3], y[3];
     float inv_area;
     float margin;  // < 0: no cull bound
     int bx0, by0, bx1, by1;
     float z[3];
-    float pad;
+    float zcull;  // >= 0
 };
 static_assert(sizeof(AaRec) == 64, "AaRec layout");
 

@@ -155,16 +155,19 @@ def test_aa_trajectory_matches_reference(ctx, golden, name):
     fit.close()
 
 
-@pytest.mark.parametrize("screen", [97, 301])
-def test_aa_odd_screen_matches_oracle(ctx, oracle, screen):
+@pytest.mark.parametrize("screen,dist", [(97, 3.0), (301, 3.0), (130, 2.2), (128, 2.2)])
+def test_aa_odd_screen_matches_oracle(ctx, oracle, screen, dist):
     """Screens that are not a multiple of 4 px (scalar row path, a partial
-    last lane) and wider than one 256-px forward workgroup: ids, pred, loss
-    image and gradient of the first iteration, then 3 iterations of state."""
+    last lane), wider than one 256-px forward workgroup, and cameras close
+    enough (distance 2.2) for the silhouette to cross every image border: ids,
+    pred, loss image and gradient of the first iteration, then 3 iterations
+    of state."""
     import opendressi_amd as od
     from opendressi_amd import _lib as L
-    print(f"[aa odd screen] {screen}", flush=True)
+    print(f"[aa odd screen] {screen} camera distance {dist}", flush=True)
     w = od.Workload("odd", 3, screen, 4, 0.05, 0.1, 1e-3, 3, 7, "aa")
-    pos, faces, tgt, mvps = od.make_scene(w)
+    pos, faces, tgt, _ = od.make_scene(w)
+    mvps = od.camera_mvps(4, dist=dist)
     fit = od.SilhouetteFit(ctx, pos, faces, mvps, screen, target_mesh=(tgt, faces), lr=w.lr,
                            keep_pred=True, keep_grad=True, technique="aa")
     fit.step(1)
