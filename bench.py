@@ -171,7 +171,7 @@ def main() -> int:
     its = args.steps / dt
     loss_end = fit.loss()
 
-    # per-kernel durations: eager replays with HIP events on the plan stream
+    # per-kernel durations: eager iterations with HIP events between kernels
     prof = fit.profile(args.profile_iters)
     dom = max(prof, key=prof.get)
     dom_us = prof[dom]

@@ -286,9 +286,10 @@ int dressi_hsr_buffer(dressi_hsr_plan* plan, int which, void** ptr,
 /* Synchronous copy of a plan buffer to host memory. */
 int dressi_hsr_read(dressi_hsr_plan* plan, int which, void* host,
                     size_t bytes);
-/* Launch-time profile of one eager iteration: fills up to `cap` kernel
- * names / average microseconds (HIP events on the plan stream). Returns
- * the kernel count in *n. */
+/* Per-kernel profile of the iteration: `iters` (at most 256) eager
+ * iterations with HIP events between their kernels on the plan stream;
+ * fills up to `cap` kernel names / average microseconds and returns the
+ * kernel count in *n. Advances the optimisation by `iters` steps. */
 int dressi_hsr_profile(dressi_hsr_plan* plan, uint32_t iters, char* names,
                        size_t name_stride, float* usec, uint32_t cap,
                        uint32_t* n);

@@ -389,7 +389,15 @@ __global__ __launch_bounds__(256) void k_aa_setup(HsrDev d) {
         d.arecs[i] = r;
     }
     const bool valid = live && r.bx0 <= r.bx1 && r.by0 <= r.by1;
-    bin_append(d.bins, d.g, valid, view, f, r.bx0, r.by0, r.bx1, r.by1, blds);
+    BinTri t;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        t.x[k] = r.x[k];
+        t.y[k] = r.y[k];
+    }
+    t.s = r.inv_area > 0.f ? 1.f : -1.f;
+    t.m = r.margin;
+    bin_append(d.bins, d.g, valid, view, f, r.bx0, r.by0, r.bx1, r.by1, t, blds);
 }
 
 // Separating-axis test of a hard triangle's coverage region (its

@@ -31,7 +31,7 @@ __global__ __launch_bounds__(256) void k_hsr_setup(HsrDev d) {
         d.cull[i] = cull_setup(r);
     }
     const bool valid = live && r.bx0 <= r.bx1 && r.by0 <= r.by1;
-    bin_append(d.bins, d.g, valid, view, f, r.bx0, r.by0, r.bx1, r.by1, blds);
+    bin_append(d.bins, d.g, valid, view, f, r.bx0, r.by0, r.bx1, r.by1, soft_bin_tri(r), blds);
 }
 
 // Visibility: one single-wave workgroup per (view, 8x8 block) resolves the
@@ -57,8 +57,9 @@ __global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
     const int py = by + (lane >> 3);
     const size_t vf = (size_t)view * d.g.n_faces;
     const BinView bv = bin_view(d.bins, view * d.g.n_tiles + tile, d.g.n_faces);
+    __shared__ uint32_t later[kSoftBinCap];
     const PixelBest best = resolve_block(d.recs + vf, d.cull + vf, bv, bx, by, d.radius, nullptr,
-                                         d.g.width);
+                                         d.g.width, later);
     if (px < (int)d.g.width && py < (int)d.g.height) {
         uint32_t id = 0;
         if (best.key != kEmptyKey) {
@@ -400,15 +401,6 @@ int plan_alloc(dressi_hsr_plan* p, T** out, size_t count) {
     p->allocs.push_back(ptr);
     *out = (T*)ptr;
     return DRESSI_OK;
-}
-
-// Zeroes the bin counters (what the face backward does in passing); used by
-// the per-kernel profile to time the setup on its own.
-__global__ __launch_bounds__(256) void k_clear_bin_counts(HsrDev d) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < d.bins.n_bins) {
-        d.bins.counts[i] = 0;
-    }
 }
 
 // Kernel k of one iteration: 0 setup + binning, 1 visibility raster,
@@ -870,74 +862,52 @@ int dressi_hsr_profile(dressi_hsr_plan* p, uint32_t iters, char* names, size_t n
                        float* usec, uint32_t cap, uint32_t* n) {
     if (int rc = ready(p)) return rc;
     DRESSI_REQUIRE(n, "bad arguments");
-    // Average device time per launch of each kernel of the iteration: after
-    // one eager iteration and one setup, the raster, loss, face backward and
-    // vertex kernels are each launched `iters` times back to back between
-    // two HIP events on the plan stream (the first three are idempotent; the
-    // vertex kernel advances Adam each time). The setup appends to the bins,
-    // so it is timed as `iters` (bin clear, setup) pairs minus `iters` bin
-    // clears timed alone. The optimisation moves 2 iters + 1 steps.
-    const uint32_t reps = iters ? iters : 1;
+    // Average device time per launch of each kernel of the iteration, in
+    // place: `iters` eager iterations on the plan stream with a HIP event
+    // before each kernel and after the last (every kernel sees the state a
+    // normal iteration leaves). The optimisation moves `iters` steps.
+    const uint32_t reps = iters ? (iters < 256u ? iters : 256u) : 1u;
     *n = kIterKernels;
     hipStream_t s = p->ctx->stream;
-    // timed groups: raster, loss, face bwd, vertex, bin clear,
-    // (bin clear + setup); -1 is the clear alone
-    constexpr int kGroups = kIterKernels + 1;
-    const int order[kGroups] = {1, 2, 3, 4, -1, 0};
-    hipEvent_t ev[kGroups + 1] = {};
+    constexpr int kEv = kIterKernels + 1;
+    std::vector<hipEvent_t> ev((size_t)reps * kEv, nullptr);
     int rc = DRESSI_OK;
-    for (int i = 0; i <= kGroups && !rc; i++) {
-        if (hipEventCreate(&ev[i]) != hipSuccess) {
+    for (hipEvent_t& e : ev) {
+        if (hipEventCreate(&e) != hipSuccess) {
             set_error("hipEventCreate failed");
-            rc = DRESSI_ERR_HIP;
-        }
-    }
-    if (!rc) rc = enqueue_iteration(p, s);
-    if (!rc) rc = launch_iter_kernel(p->d, s, 0);
-    const dim3 clear_grid(div_up(p->d.bins.n_bins, 256));
-    for (int i = 0; i < kGroups && !rc; i++) {
-        if (hipEventRecord(ev[i], s) != hipSuccess) {
-            set_error("hipEventRecord failed");
             rc = DRESSI_ERR_HIP;
             break;
         }
-        for (uint32_t r = 0; r < reps && !rc; r++) {
-            if (order[i] <= 0) {
-                hipLaunchKernelGGL(k_clear_bin_counts, clear_grid, dim3(256), 0, s, p->d);
-                if (hipGetLastError() != hipSuccess) {
-                    set_error("k_clear_bin_counts launch failed");
-                    rc = DRESSI_ERR_HIP;
-                }
+    }
+    for (uint32_t r = 0; r < reps && !rc; r++) {
+        for (int k = 0; k < kIterKernels && !rc; k++) {
+            if (hipEventRecord(ev[(size_t)r * kEv + k], s) != hipSuccess) {
+                set_error("hipEventRecord failed");
+                rc = DRESSI_ERR_HIP;
+                break;
             }
-            if (!rc && order[i] >= 0) {
-                rc = launch_iter_kernel(p->d, s, order[i]);
-            }
+            rc = launch_iter_kernel(p->d, s, k);
+        }
+        if (!rc && hipEventRecord(ev[(size_t)r * kEv + kIterKernels], s) != hipSuccess) {
+            set_error("hipEventRecord failed");
+            rc = DRESSI_ERR_HIP;
         }
     }
-    if (!rc && (hipEventRecord(ev[kGroups], s) != hipSuccess ||
-                hipEventSynchronize(ev[kGroups]) != hipSuccess)) {
+    if (!rc && hipEventSynchronize(ev.back()) != hipSuccess) {
         set_error("event synchronisation failed");
         rc = DRESSI_ERR_HIP;
     }
     float ms[kIterKernels] = {};
-    float clear_ms = 0.f;
-    for (int i = 0; i < kGroups && !rc; i++) {
-        float t = 0.f;
-        if (hipEventElapsedTime(&t, ev[i], ev[i + 1]) != hipSuccess) {
-            set_error("hipEventElapsedTime failed");
-            rc = DRESSI_ERR_HIP;
-            break;
-        }
-        (order[i] < 0 ? clear_ms : ms[order[i]]) = t / reps;
-    }
-    if (!rc) {
-        ms[0] = ms[0] > clear_ms ? ms[0] - clear_ms : 0.f;
-        // the last setup left its faces in the bins: empty them for the
-        // next iteration
-        hipLaunchKernelGGL(k_clear_bin_counts, clear_grid, dim3(256), 0, s, p->d);
-        if (hipGetLastError() != hipSuccess) {
-            set_error("k_clear_bin_counts launch failed");
-            rc = DRESSI_ERR_HIP;
+    for (uint32_t r = 0; r < reps && !rc; r++) {
+        for (int k = 0; k < kIterKernels; k++) {
+            float t = 0.f;
+            if (hipEventElapsedTime(&t, ev[(size_t)r * kEv + k], ev[(size_t)r * kEv + k + 1]) !=
+                hipSuccess) {
+                set_error("hipEventElapsedTime failed");
+                rc = DRESSI_ERR_HIP;
+                break;
+            }
+            ms[k] += t / reps;
         }
     }
     for (uint32_t k = 0; k < (uint32_t)kIterKernels && k < cap && !rc; k++) {

@@ -89,6 +89,7 @@ struct alignas(16) SoftRec {
     int bx0, by0, bx1, by1;  // bx0 > bx1: face produces no fragment
     float s_margin;          // soft coverage margin for the block cull, < 0: none
     float fid;               // face_id value written to the output
+    float zc;                // >= 0, below the depth of every hard-branch fragment
 };
 static_assert(sizeof(SoftRec) == 44 * 4, "SoftRec layout");
 // SoftRec::flags: the hard triangle's |area| passes the 1e-6 test (hard z is

@@ -295,7 +295,7 @@ __global__ __launch_bounds__(256) void k_soft_setup_op(RasterGeom g, const float
         cull[f] = cull_setup(r);
     }
     const bool valid = f < g.n_faces && r.bx0 <= r.bx1 && r.by0 <= r.by1;
-    bin_append(b, g, valid, 0u, f, r.bx0, r.by0, r.bx1, r.by1, blds);
+    bin_append(b, g, valid, 0u, f, r.bx0, r.by0, r.bx1, r.by1, soft_bin_tri(r), blds);
 }
 
 // One wave per 8x8 block: resolves the winner, then re-evaluates its signed
@@ -312,7 +312,9 @@ __global__ __launch_bounds__(64) void k_raster_soft_op(RasterGeom g, const SoftR
     const int px = blk.bx + (lane & 7);
     const int py = blk.by + (lane >> 3);
     const BinView bv = bin_view(b, blk.tile, g.n_faces);
-    const PixelBest best = resolve_block(recs, cull, bv, blk.bx, blk.by, radius, prev, g.width);
+    __shared__ uint32_t later[kSoftBinCap];
+    const PixelBest best =
+            resolve_block(recs, cull, bv, blk.bx, blk.by, radius, prev, g.width, later);
     if (px >= (int)g.width || py >= (int)g.height) {
         return;
     }

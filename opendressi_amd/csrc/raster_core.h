@@ -158,6 +158,33 @@ __device__ __forceinline__ void soft_setup(const float4 sc[3], const float4 hc[3
                               ? mg
                               : INFINITY;
     }
+    // Depth floor of the hard branch (0.5 clamp(hard z), non-slivers; 0 for
+    // the others, which the resolver never skips). Its pixels lie within the
+    // hard bbox + 1 px, so each product of the barycentric formula is at
+    // most (wmax + 2)^2 and the computed barycentrics are >= -eps, eps
+    // covering the winding test's margin (thr) and their rounding (as the
+    // soft margin, with that product bound) twice over. With
+    // sum_k h_k = 1 +- 2.01u, hard z >= zmin - 2 eps (zmax - zmin) - 4u (1 +
+    // 6 eps) max |z|; the floor takes twice these terms and one more
+    // 2^-20 max |z|.
+    r->zc = 0.f;
+    if (!sliver) {
+        const float zmin = smin(smin(r->hz[0], r->hz[1]), r->hz[2]);
+        const float zmax = smax(smax(r->hz[0], r->hz[1]), r->hz[2]);
+        const float zabs = smax(fabsf(zmin), fabsf(zmax));
+        const float ah = fabsf(h_area);
+        const float pa = fabsf(hx[1] - hx[0]) * fabsf(hy[2] - hy[0]) +
+                         fabsf(hy[1] - hy[0]) * fabsf(hx[2] - hx[0]);
+        const float ext = wmax + 2.f;
+        const float eps =
+                2.f * (thr_max + 0x1p-20f * (6.f * ext * ext + pa + ah)) / ah;
+        const float zlb = zmin - 2.f * (2.f * eps * (zmax - zmin) +
+                                        0x1p-22f * (1.f + 6.f * eps) * zabs) -
+                          0x1p-20f * zabs;
+        if (zlb > 0.f && zlb < INFINITY && eps < 1e6f) {
+            r->zc = 0.5f * smin(zlb, 1.f) * (1.f - 0x1p-20f);
+        }
+    }
     pixel_bbox(sx[0], sx[1], sx[2], sy[0], sy[1], sy[2], (int)w, (int)h, &r->bx0, &r->by0,
                &r->bx1, &r->by1);
 }
@@ -447,7 +474,7 @@ __device__ __forceinline__ bool box_hits(int x0, int y0, int x1, int y1, int bx,
 // the block and its edges do not separate it (per lane, one face per lane).
 // `soft` = also test the soft bbox (phase B has tested it already).
 __device__ __forceinline__ bool block_in_a(const SoftRec* recs, const CullRec* cull, uint32_t f,
-                                           int bx, int by, bool soft) {
+                                           int bx, int by, bool soft, bool* pos = nullptr) {
     const CullRec c = cull[f];
     if (soft && !box_hits(c.sx0, c.sy0, c.sx1, c.sy1, bx, by)) {
         return false;
@@ -464,6 +491,9 @@ __device__ __forceinline__ bool block_in_a(const SoftRec* recs, const CullRec* c
         w[4 * i + 1] = v.y;
         w[4 * i + 2] = v.z;
         w[4 * i + 3] = v.w;
+    }
+    if (pos) {
+        *pos = w[12] > 0.f;  // sign of 1 / (2 hard area)
     }
     return edges_reach_block(w, bx, by);
 }
@@ -552,27 +582,64 @@ __device__ __forceinline__ SoftRec load_rec_uniform(const SoftRec* recs, uint32_
 __device__ __forceinline__ PixelBest resolve_block(const SoftRec* recs, const CullRec* cull,
                                                    const BinView& bv, int bx, int by,
                                                    float radius, const float* prev,
-                                                   uint32_t width) {
+                                                   uint32_t width, uint32_t* later) {
     const int lane = threadIdx.x & 63;
     const int px = bx + (lane & 7);
     const int py = by + (lane >> 3);
     PixelBest best;
     best.key = kEmptyKey;
     best.hard = false;
+    // Phase A folds faces whose hard area is negative (the front faces of a
+    // closed mesh under this projection) first and keeps the others in LDS
+    // (`later`, one wave's kSoftBinCap entries): the key minimum does not
+    // depend on the fold order, and a kept face whose depth floor zc lies
+    // above every lane's depth after the first pass can win no pixel -- its
+    // hard fragments are deeper and its rim fragments are >= 0.5 > zc -- nor
+    // can phase B need it (every lane's depth is then < 0.5).
+    const bool defer = !bv.implicit && bv.n <= kSoftBinCap;
+    uint32_t n_later = 0;
     for (uint32_t base = 0; base < bv.n; base += 64) {
         const uint32_t e = base + (uint32_t)lane;
         uint32_t f = 0;
-        bool keep = false;
+        bool keep = false, pos = false;
         if (e < bv.n) {
             f = bv.implicit ? e : bv.list[e];
-            keep = block_in_a(recs, cull, f, bx, by, true);
+            keep = block_in_a(recs, cull, f, bx, by, true, &pos);
         }
-        uint64_t m = __ballot(keep);
+        const bool hold = defer && keep && pos;
+        const uint64_t mh = __ballot(hold);
+        if (hold) {
+            const uint32_t below = __builtin_amdgcn_mbcnt_hi(
+                    (uint32_t)(mh >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mh, 0u));
+            later[n_later + below] = f;
+        }
+        n_later += (uint32_t)__popcll(mh);
+        uint64_t m = __ballot(keep && !hold);
         while (m) {
             const int j = __builtin_ctzll(m);
             m &= m - 1;
             const uint32_t fj = (uint32_t)__builtin_amdgcn_readlane((int)f, j);
             const SoftRec r = load_rec_uniform(recs, fj);
+            const bool inside = r.bx0 <= bx && r.bx1 >= bx + 7 && r.by0 <= by && r.by1 >= by + 7;
+            frag_phase_a(r, fj, px, py, inside, radius, prev, width, best);
+        }
+    }
+    if (n_later) {
+        __syncthreads();
+        // the deepest lane depth (an empty lane: all ones, nothing is skipped)
+        uint32_t zmax = (uint32_t)(best.key >> 32);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const uint32_t other = (uint32_t)__shfl_xor((int)zmax, o);
+            zmax = other > zmax ? other : zmax;
+        }
+        zmax = (uint32_t)__builtin_amdgcn_readfirstlane((int)zmax);
+        for (uint32_t i = 0; i < n_later; i++) {
+            const uint32_t fj = (uint32_t)__builtin_amdgcn_readfirstlane((int)later[i]);
+            const SoftRec r = load_rec_uniform(recs, fj);
+            if (__float_as_uint(r.zc) > zmax) {
+                continue;  // zc >= 0: bit order is value order
+            }
             const bool inside = r.bx0 <= bx && r.bx1 >= bx + 7 && r.by0 <= by && r.by1 >= by + 7;
             frag_phase_a(r, fj, px, py, inside, radius, prev, width, best);
         }
@@ -695,85 +762,197 @@ __device__ __forceinline__ void walk_bin(const Rec* recs, const BinBuffers& b, u
 }
 
 // ---------------------------------------------------------------------------
-// Fixed-capacity soft bins, appended from the setup kernels. Lanes of one
-// workgroup first count their tiles in an LDS window (one global atomic per
-// touched tile), then write their slots; lanes whose tiles fall outside the
-// window (or workgroups spanning two views) append with direct atomics.
-// All lanes of the workgroup must call it.
+// Fixed-capacity soft bins, appended from the setup kernels. A face goes to
+// the tiles of its pixel bbox that its triangle reaches (the separating-axis
+// test of the block culls, with the record's margin; every tile of the bbox
+// when it has none). A thread walks the tiles of its own face when they are
+// at most kBinBig; the (face, tile) pairs of larger faces are dealt to all
+// threads of the workgroup (a scan of their tile counts, a binary search
+// per pair), so a face spanning many tiles does not hold one thread. Pairs
+// in the workgroup's LDS window of tiles are counted in LDS (one global
+// atomic per touched window tile), then written; the others (outside the
+// window, or a workgroup spanning two views) append with direct atomics. All
+// threads of the workgroup (blockDim.x a multiple of 64, <= kBinThreads)
+// must call it.
 // ---------------------------------------------------------------------------
 constexpr int kBinWin = 32;  // LDS window of 32 x 32 tiles
+constexpr int kBinThreads = 256;
+constexpr int kBinBig = 64;
+
+// Triangle of the tile test: screen corners, orientation sign of its area
+// and the edge-function margin (< 0: bbox only).
+struct BinTri {
+    float x[3], y[3];
+    float s, m;
+};
 
 struct BinLds {
     uint32_t cnt[kBinWin * kBinWin];
     uint32_t base[kBinWin * kBinWin];
-    int win[4];  // tx0, ty0, view0, mixed-view flag
+    int win[4];                     // tx0, ty0, view0, mixed-view flag
+    uint32_t off[kBinThreads + 1];  // exclusive scan of the threads' tile counts
+    uint32_t f[kBinThreads], view[kBinThreads];
+    int tx0[kBinThreads], ty0[kBinThreads], nx[kBinThreads];
+    BinTri tri[kBinThreads];
 };
+
+// Whether triangle t can cover a pixel centre of tile (tx, ty): on every
+// edge the best corner of the tile's centre rectangle is not below -m.
+__device__ __forceinline__ bool tri_reaches_tile(const BinTri& t, int tx, int ty) {
+    if (!(t.m >= 0.f)) {
+        return true;
+    }
+    const float x0 = (float)(tx * kTile) + 0.5f, x1 = x0 + (float)(kTile - 1);
+    const float y0 = (float)(ty * kTile) + 0.5f, y1 = y0 + (float)(kTile - 1);
+    bool hit = true;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        const int k1 = (k + 1) % 3;
+        const float ex = t.s * (t.x[k1] - t.x[k]);
+        const float ey = t.s * (t.y[k1] - t.y[k]);
+        const float gk = smax(ex * (y0 - t.y[k]), ex * (y1 - t.y[k])) +
+                         smax(-ey * (x0 - t.x[k]), -ey * (x1 - t.x[k]));
+        hit = hit && !(gk < -t.m);
+    }
+    return hit;
+}
+
+// Tile-test triangle of a soft record: the soft triangle (every fragment
+// needs its coverage) with its coverage margin.
+__device__ __forceinline__ BinTri soft_bin_tri(const SoftRec& r) {
+    BinTri t;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        t.x[k] = r.sx[k];
+        t.y[k] = r.sy[k];
+    }
+    t.s = r.s_inv_area > 0.f ? 1.f : -1.f;
+    t.m = r.s_margin;
+    return t;
+}
+
+// One (face, tile) pair of bin_append's pass (0: count window pairs in LDS
+// and append the others, 1: write window pairs from their bases).
+__device__ __forceinline__ void bin_pair(const BinBuffers& b, const RasterGeom& g, BinLds& lds,
+                                         int pass, bool mixed, int wx0, int wy0, uint32_t f,
+                                         uint32_t view, const BinTri& tri, int tx, int ty) {
+    const bool local = !mixed && tx - wx0 < kBinWin && ty - wy0 < kBinWin;
+    if ((pass == 1 && !local) || !tri_reaches_tile(tri, tx, ty)) {
+        return;
+    }
+    const uint32_t bin = view * g.n_tiles + ty * g.tiles_x + tx;
+    uint32_t slot;
+    if (local) {
+        const int li = (ty - wy0) * kBinWin + (tx - wx0);
+        const uint32_t k = atomicAdd(&lds.cnt[li], 1u);
+        if (pass == 0) {
+            return;
+        }
+        slot = lds.base[li] + k;
+    } else {
+        slot = atomicAdd(&b.counts[bin], 1u);
+    }
+    if (slot < b.cap) {
+        b.list[(size_t)bin * b.cap + slot] = f;
+    }
+}
 
 __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom& g, bool valid,
                                            uint32_t view, uint32_t f, int bx0, int by0, int bx1,
-                                           int by1, BinLds& lds) {
+                                           int by1, const BinTri& tri, BinLds& lds) {
+    const int tid = (int)threadIdx.x;
+    const int nthr = (int)blockDim.x;
     const int tx0 = bx0 / kTile, tx1 = bx1 / kTile, ty0 = by0 / kTile, ty1 = by1 / kTile;
-    if (threadIdx.x == 0) {
+    const uint32_t nt = valid ? (uint32_t)((tx1 - tx0 + 1) * (ty1 - ty0 + 1)) : 0u;
+    const bool big = nt > (uint32_t)kBinBig;
+    if (tid == 0) {
         lds.win[0] = 0x7fffffff;
         lds.win[1] = 0x7fffffff;
         lds.win[2] = -1;
         lds.win[3] = 0;
     }
-    for (int i = threadIdx.x; i < kBinWin * kBinWin; i += blockDim.x) {
+    for (int i = tid; i < kBinWin * kBinWin; i += nthr) {
         lds.cnt[i] = 0;
     }
+    if (big) {
+        lds.f[tid] = f;
+        lds.view[tid] = view;
+        lds.tx0[tid] = tx0;
+        lds.ty0[tid] = ty0;
+        lds.nx[tid] = tx1 - tx0 + 1;
+        lds.tri[tid] = tri;
+    }
+    // inclusive scan of the large faces' tile counts: within each wave, then
+    // across waves
+    uint32_t incl = big ? nt : 0u;
+    const int lane = tid & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = (uint32_t)__shfl_up((int)incl, o);
+        incl += lane >= o ? v : 0u;
+    }
+    lds.off[tid + 1] = incl;
     __syncthreads();
     if (valid) {
         atomicMin(&lds.win[0], tx0);
         atomicMin(&lds.win[1], ty0);
         atomicMax(&lds.win[2], (int)view);
     }
+    uint32_t wave_base = 0;
+    for (int wv = 0; wv < (tid >> 6); wv++) {
+        wave_base += lds.off[wv * 64 + 64];
+    }
     __syncthreads();
+    lds.off[tid + 1] = wave_base + incl;
+    if (tid == 0) {
+        lds.off[0] = 0;
+    }
     if (valid && (int)view != lds.win[2]) {
         lds.win[3] = 1;
     }
     __syncthreads();
+    const uint32_t total = lds.off[nthr];
     const int wx0 = lds.win[0], wy0 = lds.win[1];
     const bool mixed = lds.win[3] != 0;
-    const bool local = valid && !mixed && tx1 - wx0 < kBinWin && ty1 - wy0 < kBinWin;
-    if (local) {
-        for (int ty = ty0; ty <= ty1; ty++) {
-            for (int tx = tx0; tx <= tx1; tx++) {
-                atomicAdd(&lds.cnt[(ty - wy0) * kBinWin + (tx - wx0)], 1u);
-            }
-        }
-    } else if (valid) {
-        for (int ty = ty0; ty <= ty1; ty++) {
-            for (int tx = tx0; tx <= tx1; tx++) {
-                const uint32_t bin = view * g.n_tiles + ty * g.tiles_x + tx;
-                const uint32_t slot = atomicAdd(&b.counts[bin], 1u);
-                if (slot < b.cap) {
-                    b.list[(size_t)bin * b.cap + slot] = f;
+    for (int pass = 0; pass < 2; pass++) {
+        if (valid && !big) {
+            // up to 2 x 2 tiles the test rarely rejects one: bbox only
+            BinTri t = tri;
+            t.m = nt <= 4u ? -1.f : t.m;
+            for (int ty = ty0; ty <= ty1; ty++) {
+                for (int tx = tx0; tx <= tx1; tx++) {
+                    bin_pair(b, g, lds, pass, mixed, wx0, wy0, f, view, t, tx, ty);
                 }
             }
         }
-    }
-    __syncthreads();
-    const uint32_t view0 = (uint32_t)max(lds.win[2], 0);
-    for (int i = threadIdx.x; i < kBinWin * kBinWin; i += blockDim.x) {
-        const uint32_t c = lds.cnt[i];
-        if (c) {
-            const int tx = wx0 + i % kBinWin, ty = wy0 + i / kBinWin;
-            lds.base[i] = atomicAdd(&b.counts[view0 * g.n_tiles + ty * g.tiles_x + tx], c);
-            lds.cnt[i] = 0;
-        }
-    }
-    __syncthreads();
-    if (local) {
-        for (int ty = ty0; ty <= ty1; ty++) {
-            for (int tx = tx0; tx <= tx1; tx++) {
-                const int li = (ty - wy0) * kBinWin + (tx - wx0);
-                const uint32_t slot = lds.base[li] + atomicAdd(&lds.cnt[li], 1u);
-                if (slot < b.cap) {
-                    const uint32_t bin = view * g.n_tiles + ty * g.tiles_x + tx;
-                    b.list[(size_t)bin * b.cap + slot] = f;
+        for (uint32_t p = (uint32_t)tid; p < total; p += (uint32_t)nthr) {
+            // the face q with off[q] <= p < off[q + 1]
+            int lo = 0, hi = nthr - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (lds.off[mid] <= p) {
+                    lo = mid;
+                } else {
+                    hi = mid - 1;
                 }
             }
+            const int i = (int)(p - lds.off[lo]);
+            const int qnx = lds.nx[lo];
+            bin_pair(b, g, lds, pass, mixed, wx0, wy0, lds.f[lo], lds.view[lo], lds.tri[lo],
+                     lds.tx0[lo] + i % qnx, lds.ty0[lo] + i / qnx);
+        }
+        if (pass == 0) {
+            __syncthreads();
+            const uint32_t view0 = (uint32_t)max(lds.win[2], 0);
+            for (int i = tid; i < kBinWin * kBinWin; i += nthr) {
+                const uint32_t c = lds.cnt[i];
+                if (c) {
+                    const int tx = wx0 + i % kBinWin, ty = wy0 + i / kBinWin;
+                    lds.base[i] = atomicAdd(&b.counts[view0 * g.n_tiles + ty * g.tiles_x + tx], c);
+                    lds.cnt[i] = 0;
+                }
+            }
+            __syncthreads();
         }
     }
 }
