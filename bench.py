@@ -1,14 +1,17 @@
-"""Benchmark of the fused HardSoftRas silhouette iteration (fwd + bwd + Adam)
-on one MI355X.
+"""Benchmark of the fused silhouette-fit iteration (fwd + bwd + Adam) on one
+MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--workload c4_hsr|c2|c1]
+    python bench.py [--steps K] [--warmup W] [--workload c4_hsr|c4|c2|c1]
 
-A step is one iteration of the silhouette fit: per view clip transform,
-SoftClip, tile-binned RasterizeSoft, the per-pixel soft-probability chain and
-L2 loss image, the stochastic FaceFetchBwd gather fused with the chain's
-backward, LookupFacesBwd + clip->pos chain, Adam -- one hipGraph launch.
-Inputs (mesh, Adam state, target silhouettes) are resident in HBM before the
-timed region. Prints ONE JSON line.
+A step is one iteration of the silhouette fit. HardSoftRas (c4_hsr, c2, c1):
+per view clip transform, SoftClip, tile-binned RasterizeSoft, the per-pixel
+soft-probability chain and L2 loss image, the stochastic FaceFetchBwd gather
+fused with the chain's backward, LookupFacesBwd + clip->pos chain, Adam. AA
+(c4): clip transform, tile-binned hard raster of face ids, AntiAlias of the
+mask + L2 loss image, the stochastic AntiAliasBwdVtx gather, ColSum +
+clip->pos chain, Adam. One hipGraph launch per step. Inputs (mesh, Adam
+state, target images) are resident in HBM before the timed region. Prints
+ONE JSON line.
 """
 from __future__ import annotations
 
@@ -89,17 +92,17 @@ def kernel_bytes(n_views: int, s: int, n_faces: int, n_verts: int, samples: int 
 
 def measured_traffic(kernel: str, workload: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
-    summary (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE per dispatch,
-    scaled by the counters' reading for a plain copy of known size), or None
-    when that summary is for another kernel or workload."""
+    summaries (profiles/traffic.json, per workload: FETCH_SIZE + WRITE_SIZE
+    per dispatch, scaled by the counters' reading for a plain copy of known
+    size), or None when no summary covers that kernel and workload."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as fh:
-            rec = json.load(fh)
-    except (OSError, ValueError):
+            rec = json.load(fh).get("workloads", {}).get(workload, {})
+    except (OSError, ValueError, AttributeError):
         return None
     for k in rec.get("kernels", []):
-        if k.get("kernel") == kernel and rec.get("workload") == workload:
+        if k.get("kernel") == kernel:
             return k["fetch_bytes"] + k["write_bytes"]
     return None
 
