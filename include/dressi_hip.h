@@ -174,9 +174,41 @@ int dressi_antialias_bwd_vtx(dressi_ctx* ctx, const float* gy, const float* img,
 int dressi_col_sum(dressi_ctx* ctx, const float* x, uint32_t n_comp,
                    uint32_t width, uint32_t height, float* out);
 
+/* ---- texture path (C3) ---- */
+/* F::TextureBilinear forward (src/core/f_ops.cpp:2736-2780, BilerpClamp
+ * src/core/ibl_math.h:91-115): tex {tw,th} x n_comp (1..4) sampled at
+ * uv {uw,uh} VEC2 (4-tap, clamp to edge, texel centres at +0.5) ->
+ * out {uw,uh} x n_comp. */
+int dressi_texture_bilinear(dressi_ctx* ctx, const float* tex, uint32_t tw,
+                            uint32_t th, uint32_t n_comp, const float* uv,
+                            uint32_t uw, uint32_t uh, float* out);
+/* Its backward w.r.t. the texture, GatherByInverseUVBilinear
+ * (src/core/f_ops.cpp:2650-2732): per texel the inverse-UV anchor (its own
+ * entry of inv_uv {tw,th} VEC4 when .z > 0.5, else the first such entry of
+ * the +-4 neighbourhood in row order) and the tent-weighted sum of gy
+ * {sw,sh} x n_comp over the 7 x 7 screen pixels around it, weights from
+ * uv {sw,sh} VEC2. out {tw,th} x n_comp. */
+int dressi_texture_bilinear_bwd(dressi_ctx* ctx, const float* gy,
+                                uint32_t n_comp, uint32_t sw, uint32_t sh,
+                                const float* inv_uv, uint32_t tw, uint32_t th,
+                                const float* uv, float* out);
+/* ScreenAttr (src/core/mesh_utils.cpp:191-203) on the device: clip {V,1}
+ * VEC4 -> {V,1} VEC4 (screen x, screen y, 1, 0). */
+int dressi_screen_attr(dressi_ctx* ctx, const float* clip, uint32_t n_verts,
+                       uint32_t width, uint32_t height, float* out);
+
 /* ------------------------------------------------------------------------ */
 /* Host-side mesh topology and scene builders                               */
 /* ------------------------------------------------------------------------ */
+/* GenerateUvSphere (examples/common/geometry_utils.cpp:86-131): stacks x
+ * slices quads with a duplicated seam column and the pole triangles
+ * skipped; pos {V,3}, uv {V,2} (u = j / slices, v = i / stacks), faces
+ * {F,3} float ids. Counts only when an output is NULL. */
+int dressi_uv_sphere(uint32_t stacks, uint32_t slices, uint32_t* n_verts,
+                     uint32_t* n_faces, float* pos, float* uv, float* faces);
+/* UvAsClip (src/core/mesh_utils.cpp:180-189): uv {V,2} -> clip {V,4}
+ * (2u - 1, 2v - 1, 0.5, 1). */
+void dressi_uv_as_clip(const float* uv, uint32_t n_verts, float* clip);
 /* GenerateIcosphere (examples/common/geometry_utils.cpp:24-84). Counts only
  * when pos/faces are NULL. pos {V,3}, faces {F,3} float ids. */
 int dressi_icosphere(uint32_t level, uint32_t* n_verts, uint32_t* n_faces,
@@ -291,6 +323,84 @@ int dressi_hsr_read(dressi_hsr_plan* plan, int which, void* host,
  * fills up to `cap` kernel names / average microseconds and returns the
  * kernel count in *n. Advances the optimisation by `iters` steps. */
 int dressi_hsr_profile(dressi_hsr_plan* plan, uint32_t iters, char* names,
+                       size_t name_stride, float* usec, uint32_t cap,
+                       uint32_t* n);
+
+/* ------------------------------------------------------------------------ */
+/* Fused texture-optimisation iteration (C3)                                */
+/* ------------------------------------------------------------------------ */
+/* One plan = the GpuPlan of the texture example's graph
+ * (examples/texture_optimization/run.cpp:112-145) with TextureBilinear, an
+ * RGBA texture, the RGB L2 image loss and the silhouette example's in-graph
+ * Adam (run.cpp:404-437): per iteration and view v, with the cameras of set
+ * (t mod n_sets) (the example's per-iteration sendImg of moving views):
+ *   clip = MVP * pos, inv_uv_attr = ScreenAttr(clip)
+ *   g_uv = Rasterize(clip, uv, S), g_mask = Rasterize(clip, 1, S)
+ *   inv_uv = Rasterize(UvAsClip(uv), inv_uv_attr, T)
+ *   target = g_mask * TextureBilinear(gt_tex, g_uv, inv_uv)  (StopGradient)
+ *   pred   = g_mask * TextureBilinear(tex, g_uv, inv_uv)
+ *   loss   = sum_v (target - pred)^2 * (c, c, c, 0), c = 1 / S^2  (image)
+ *   backward: GatherByInverseUVBilinear per view, summed over views; Adam
+ * captured once into a hipGraph. The UV-space raster (which face covers a
+ * texel, and its barycentrics) does not depend on the view and is computed
+ * once by set_mesh; each view only interpolates its screen attribute. */
+typedef struct dressi_tex_plan dressi_tex_plan;
+
+typedef struct dressi_tex_desc {
+    uint32_t n_verts;     /* V */
+    uint32_t n_faces;     /* F */
+    uint32_t n_views;     /* N views per iteration (1..8) */
+    uint32_t width;       /* screen S (square) */
+    uint32_t height;
+    uint32_t tex_w;       /* texture T */
+    uint32_t tex_h;
+    uint32_t n_sets;      /* camera sets, iteration t uses set t mod n_sets */
+    float lr;             /* Adam learning rate */
+    float beta1, beta2, eps;
+    uint32_t flags;       /* DRESSI_TEX_* */
+} dressi_tex_desc;
+
+/* Also write per-view pred / target images (markOutput). */
+#define DRESSI_TEX_KEEP_IMAGES 1u
+/* Keep d loss / d tex of the last iteration readable. */
+#define DRESSI_TEX_KEEP_GRAD 2u
+
+int dressi_tex_create(dressi_ctx* ctx, const dressi_tex_desc* desc,
+                      dressi_tex_plan** out);
+int dressi_tex_destroy(dressi_tex_plan* plan);
+/* Static leaves (sendImg): pos {V,3}, uv {V,2}, faces {F,3} float ids;
+ * computes the UV-space raster. */
+int dressi_tex_set_mesh(dressi_tex_plan* plan, const float* pos,
+                        const float* uv, const float* faces);
+/* Cameras: mvps {n_sets, N, 16} column-major. */
+int dressi_tex_set_cameras(dressi_tex_plan* plan, const float* mvps);
+/* The target texture {T} RGBA (gt_tex). */
+int dressi_tex_set_target(dressi_tex_plan* plan, const float* gt_tex);
+/* Texture and Adam state {T} RGBA from host (m, v may be NULL = 0). */
+int dressi_tex_set_state(dressi_tex_plan* plan, const float* tex,
+                         const float* m, const float* v, float t);
+int dressi_tex_get_state(dressi_tex_plan* plan, float* tex, float* m,
+                         float* v, float* t);
+/* Enqueue `n_iters` iterations (graph launches / eager launches). */
+int dressi_tex_step(dressi_tex_plan* plan, uint32_t n_iters);
+int dressi_tex_step_eager(dressi_tex_plan* plan, uint32_t n_iters);
+
+enum dressi_tex_buffer {
+    DRESSI_TEX_LOSS = 0,    /* {S,S} VEC4: the loss image */
+    DRESSI_TEX_PRED = 1,    /* {N,S,S} VEC4 (DRESSI_TEX_KEEP_IMAGES) */
+    DRESSI_TEX_TARGET = 2,  /* {N,S,S} VEC4 (DRESSI_TEX_KEEP_IMAGES) */
+    DRESSI_TEX_FACE_ID = 3, /* {N,S,S} uint32: face + 1 of the screen raster */
+    DRESSI_TEX_GRAD = 4,    /* {T} VEC4 (DRESSI_TEX_KEEP_GRAD) */
+    DRESSI_TEX_TEX = 5,     /* {T} VEC4: the texture */
+    DRESSI_TEX_UV = 6       /* {N,S,S} VEC2: g_uv */
+};
+int dressi_tex_buffer(dressi_tex_plan* plan, int which, void** ptr,
+                      size_t* bytes);
+int dressi_tex_read(dressi_tex_plan* plan, int which, void* host,
+                    size_t bytes);
+/* Per-kernel profile: `iters` (<= 256) eager iterations with HIP events
+ * between the kernels; advances the optimisation by `iters` steps. */
+int dressi_tex_profile(dressi_tex_plan* plan, uint32_t iters, char* names,
                        size_t name_stride, float* usec, uint32_t cap,
                        uint32_t* n);
 

@@ -1,4 +1,5 @@
-"""opendressi_amd -- MI355X-native Dressi-AD HardSoftRas silhouette hot path.
+"""opendressi_amd -- MI355X-native Dressi-AD hot path: the silhouette fit
+(HardSoftRas, screen-space AA) and the texture fit.
 
 Hand-written gfx950 HIP kernels behind the C ABI of include/dressi_hip.h
 (libdressi_hip.so, built in-tree by opendressi_amd.build). The first use of
@@ -14,6 +15,9 @@ _EXPORTS = {
     "vertex_faces_tex": ".runtime",
     "WORKLOADS": ".silhouette", "SilhouetteFit": ".silhouette", "Workload": ".silhouette",
     "camera_mvps": ".silhouette", "make_scene": ".silhouette",
+    "uniform": ".runtime", "uv_sphere": ".runtime",
+    "TEX_WORKLOADS": ".texture", "TexWorkload": ".texture", "TextureFit": ".texture",
+    "make_tex_scene": ".texture", "orbit_cameras": ".texture", "sinusoid_texture": ".texture",
 }
 
 __all__ = sorted(_EXPORTS)

@@ -31,6 +31,16 @@ class HsrDesc(C.Structure):
                 ("beta1", _F), ("beta2", _F), ("eps", _F), ("flags", _U)]
 
 
+class TexDesc(C.Structure):
+    _fields_ = [("n_verts", _U), ("n_faces", _U), ("n_views", _U), ("width", _U),
+                ("height", _U), ("tex_w", _U), ("tex_h", _U), ("n_sets", _U), ("lr", _F),
+                ("beta1", _F), ("beta2", _F), ("eps", _F), ("flags", _U)]
+
+
+TEX_KEEP_IMAGES = 1
+TEX_KEEP_GRAD = 2
+(TEX_LOSS, TEX_PRED, TEX_TARGET, TEX_FACE_ID, TEX_GRAD, TEX_TEX, TEX_UV) = range(7)
+
 HSR_KEEP_PRED = 1
 HSR_KEEP_GRAD = 2
 HSR_TECHNIQUE_AA = 4
@@ -65,6 +75,11 @@ _SIGS = {
     "dressi_antialias_bwd_vtx": (_I, [_P, _P, _P, _U, _P, _P, _U, _P, _U, _P, _U, _P, _U, _I,
                                       _U, _U, _P]),
     "dressi_col_sum": (_I, [_P, _P, _U, _U, _U, _P]),
+    "dressi_texture_bilinear": (_I, [_P, _P, _U, _U, _U, _P, _U, _U, _P]),
+    "dressi_texture_bilinear_bwd": (_I, [_P, _P, _U, _U, _U, _P, _U, _U, _P, _P]),
+    "dressi_screen_attr": (_I, [_P, _P, _U, _U, _U, _P]),
+    "dressi_uv_sphere": (_I, [_U, _U, _UP, _UP, _FP, _FP, _FP]),
+    "dressi_uv_as_clip": (None, [_FP, _U, _FP]),
     "dressi_icosphere": (_I, [_U, _UP, _UP, _FP, _FP]),
     "dressi_vertex_faces_tex": (_I, [_FP, _U, _U, _UP, _FP, _S]),
     "dressi_look_at": (None, [_FP, _FP, _FP, _FP]),
@@ -83,6 +98,18 @@ _SIGS = {
     "dressi_hsr_buffer": (_I, [_P, _I, C.POINTER(_P), C.POINTER(_S)]),
     "dressi_hsr_read": (_I, [_P, _I, _P, _S]),
     "dressi_hsr_profile": (_I, [_P, _U, C.c_char_p, _S, _FP, _U, _UP]),
+    "dressi_tex_create": (_I, [_P, C.POINTER(TexDesc), C.POINTER(_P)]),
+    "dressi_tex_destroy": (_I, [_P]),
+    "dressi_tex_set_mesh": (_I, [_P, _FP, _FP, _FP]),
+    "dressi_tex_set_cameras": (_I, [_P, _FP]),
+    "dressi_tex_set_target": (_I, [_P, _FP]),
+    "dressi_tex_set_state": (_I, [_P, _FP, _FP, _FP, _F]),
+    "dressi_tex_get_state": (_I, [_P, _FP, _FP, _FP, _FP]),
+    "dressi_tex_step": (_I, [_P, _U]),
+    "dressi_tex_step_eager": (_I, [_P, _U]),
+    "dressi_tex_buffer": (_I, [_P, _I, C.POINTER(_P), C.POINTER(_S)]),
+    "dressi_tex_read": (_I, [_P, _I, _P, _S]),
+    "dressi_tex_profile": (_I, [_P, _U, C.c_char_p, _S, _FP, _U, _UP]),
 }
 
 EXPORTED = tuple(_SIGS)

@@ -961,6 +961,20 @@ __global__ __launch_bounds__(256) void k_aa_vertex_adam(HsrDev d) {
 const char* const kAaKernelNames[kAaKernels] = {"k_aa_setup", "k_aa_raster", "k_aa_fwd",
                                                 "k_aa_face_bwd", "k_aa_vertex_adam"};
 
+int launch_aa_setup(const HsrDev& d, hipStream_t s) {
+    hipLaunchKernelGGL(k_aa_setup, dim3(div_up(d.g.n_views * d.g.n_faces, 256)), dim3(256), 0, s,
+                       d);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+int launch_aa_raster(const HsrDev& d, hipStream_t s) {
+    hipLaunchKernelGGL(k_aa_raster, dim3(32u * d.g.n_views * div_up(d.g.n_tiles, 8)), dim3(64),
+                       0, s, d);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
 int launch_aa_kernel(const HsrDev& d, hipStream_t s, int k) {
     const RasterGeom& g = d.g;
     const uint32_t nvf = g.n_views * g.n_faces;
@@ -969,12 +983,9 @@ int launch_aa_kernel(const HsrDev& d, hipStream_t s, int k) {
             hipLaunchKernelGGL(k_aa_clip, dim3(div_up(g.n_views * d.n_verts, 256)), dim3(256), 0,
                                s, d);
             DRESSI_CHECK_LAUNCH();
-            hipLaunchKernelGGL(k_aa_setup, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
-            break;
+            return launch_aa_setup(d, s);
         case 1:
-            hipLaunchKernelGGL(k_aa_raster, dim3(32u * g.n_views * div_up(g.n_tiles, 8)),
-                               dim3(64), 0, s, d);
-            break;
+            return launch_aa_raster(d, s);
         case 2:
         case 4: {
             const dim3 grid = k == 2 ? dim3(div_up(g.width, 256), g.height)

@@ -190,6 +190,12 @@ __device__ __forceinline__ void advance_t(const HsrDev& d, float t) {
 constexpr int kAaKernels = 5;
 extern const char* const kAaKernelNames[kAaKernels];
 int launch_aa_kernel(const HsrDev& d, hipStream_t s, int k);
+// The hard-raster part of that plan on its own, for any HsrDev whose g,
+// n_verts, faces, clip, arecs, bins and ids are set: the per-(view, face)
+// setup + bin append (bins empty on entry), and the face-id raster
+// (RasterizeCore's winner + 1, 0 = background). Used by the texture plan.
+int launch_aa_setup(const HsrDev& d, hipStream_t s);
+int launch_aa_raster(const HsrDev& d, hipStream_t s);
 // Renders the AA target of one view into `out` ({S,S} float):
 // StopGradient(AntiAlias(Rasterize(tgt, 1), RasterizeFaceId(tgt), tgt_clip,
 // tgt_faces, ...)) with zero seed (run.cpp:346-357).

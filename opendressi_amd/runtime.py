@@ -100,20 +100,38 @@ def mat4_mul(a, b) -> np.ndarray:
     return r
 
 
-def randn(seed: int, n: int) -> np.ndarray:
-    """Seeded standard normals: SplitMix64 uniforms in (0,1), Box-Muller
-    (cosine branch) in double, rounded once to float32."""
+def uniform(seed: int, n: int) -> np.ndarray:
+    """Seeded uniforms in (0, 1), float64: the SplitMix64 sequence of `seed`
+    (outputs 1 .. n), top 53 bits + 0.5 ulp."""
     mask = np.uint64(0xFFFFFFFFFFFFFFFF)
     with np.errstate(over="ignore"):
-        k = np.arange(1, 2 * n + 1, dtype=np.uint64)
+        k = np.arange(1, n + 1, dtype=np.uint64)
         z = (np.uint64(seed) + k * np.uint64(0x9E3779B97F4A7C15)) & mask
         z = ((z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)) & mask
         z = ((z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)) & mask
         z = z ^ (z >> np.uint64(31))
-    u = ((z >> np.uint64(11)).astype(np.float64) + 0.5) * 2.0 ** -53
+    return ((z >> np.uint64(11)).astype(np.float64) + 0.5) * 2.0 ** -53
+
+
+def randn(seed: int, n: int) -> np.ndarray:
+    """Seeded standard normals: SplitMix64 uniforms in (0,1), Box-Muller
+    (cosine branch) in double, rounded once to float32."""
+    u = uniform(seed, 2 * n)
     u1, u2 = u[0::2], u[1::2]
     return (np.sqrt(-2.0 * np.log(u1)) * np.cos(6.283185307179586 * u2)).astype(np.float32)
 
 
+def uv_sphere(stacks: int, slices: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """GenerateUvSphere: pos {V,3}, uv {V,2}, faces {F,3} (float ids)."""
+    nv, nf = C.c_uint32(), C.c_uint32()
+    check(lib.dressi_uv_sphere(stacks, slices, C.byref(nv), C.byref(nf), None, None, None))
+    pos = np.zeros((nv.value, 3), np.float32)
+    uv = np.zeros((nv.value, 2), np.float32)
+    faces = np.zeros((nf.value, 3), np.float32)
+    check(lib.dressi_uv_sphere(stacks, slices, C.byref(nv), C.byref(nf), _fp(pos), _fp(uv),
+                               _fp(faces)))
+    return pos, uv, faces
+
+
 __all__ = ["Context", "DressiError", "icosphere", "vertex_faces_tex", "look_at",
-           "perspective_vk", "mat4_mul", "randn"]
+           "perspective_vk", "mat4_mul", "randn", "uniform", "uv_sphere"]

@@ -1762,3 +1762,313 @@ int or_aa_fit(const float* pos0, uint32_t n_verts, const float* faces, uint32_t 
     free(lacc);
     return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Texture path (C3)                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* examples/common/geometry_utils.cpp:86-131 (GenerateUvSphere): (stacks + 1)
+ * rows of slices + 1 vertices (seam column duplicated), pole triangles
+ * skipped. Counts only when an output is NULL. */
+int or_uv_sphere(uint32_t stacks, uint32_t slices, uint32_t* n_verts, uint32_t* n_faces,
+                 float* pos, float* uv, float* faces) {
+    if (stacks < 2) stacks = 2;
+    if (slices < 3) slices = 3;
+    const uint32_t cols = slices + 1;
+    const uint32_t nv = cols * (stacks + 1);
+    const uint32_t nf = 2 * stacks * slices - 2 * slices;
+    if (n_verts) *n_verts = nv;
+    if (n_faces) *n_faces = nf;
+    if (!pos || !uv || !faces) {
+        return 0;
+    }
+    const float k_pi = 3.14159265358979323846f;
+    for (uint32_t i = 0; i <= stacks; i++) {
+        const float theta = k_pi * (float)i / (float)stacks;
+        const float st = sinf(theta), ct = cosf(theta);
+        for (uint32_t j = 0; j <= slices; j++) {
+            const float phi = 2.f * k_pi * (float)j / (float)slices;
+            const uint32_t v = i * cols + j;
+            pos[v * 3 + 0] = st * cosf(phi);
+            pos[v * 3 + 1] = ct;
+            pos[v * 3 + 2] = st * sinf(phi);
+            uv[v * 2 + 0] = (float)j / (float)slices;
+            uv[v * 2 + 1] = (float)i / (float)stacks;
+        }
+    }
+    uint32_t f = 0;
+    for (uint32_t i = 0; i < stacks; i++) {
+        for (uint32_t j = 0; j < slices; j++) {
+            const uint32_t tl = i * cols + j, tr = i * cols + j + 1;
+            const uint32_t bl = (i + 1) * cols + j, br = (i + 1) * cols + j + 1;
+            if (i != stacks - 1) {
+                faces[f * 3 + 0] = (float)tl;
+                faces[f * 3 + 1] = (float)br;
+                faces[f * 3 + 2] = (float)bl;
+                f++;
+            }
+            if (i != 0) {
+                faces[f * 3 + 0] = (float)tl;
+                faces[f * 3 + 1] = (float)tr;
+                faces[f * 3 + 2] = (float)br;
+                f++;
+            }
+        }
+    }
+    return 0;
+}
+
+/* src/core/mesh_utils.cpp:180-189 (UvAsClip) */
+void or_uv_as_clip(const float* uv, uint32_t n_verts, float* clip) {
+    for (uint32_t i = 0; i < n_verts; i++) {
+        clip[i * 4 + 0] = uv[i * 2 + 0] * 2.f - 1.f;
+        clip[i * 4 + 1] = uv[i * 2 + 1] * 2.f - 1.f;
+        clip[i * 4 + 2] = 0.5f;
+        clip[i * 4 + 3] = 1.f;
+    }
+}
+
+/* src/core/mesh_utils.cpp:191-203 (ScreenAttr) */
+void or_screen_attr(const float* clip, uint32_t n_verts, uint32_t w, uint32_t h, float* attr) {
+    for (uint32_t i = 0; i < n_verts; i++) {
+        const float cw = clip[i * 4 + 3];
+        const float ndc_x = clip[i * 4 + 0] / cw;
+        const float ndc_y = clip[i * 4 + 1] / cw;
+        attr[i * 4 + 0] = (ndc_x * 0.5f + 0.5f) * (float)w;
+        attr[i * 4 + 1] = (ndc_y * 0.5f + 0.5f) * (float)h;
+        attr[i * 4 + 2] = 1.f;
+        attr[i * 4 + 3] = 0.f;
+    }
+}
+
+/* src/core/ibl_math.h:91-115 (BilerpClamp) */
+static void bilerp_clamp(const float* data, uint32_t w, uint32_t h, uint32_t n, float u, float v,
+                         float* out) {
+    const float sx = u * (float)w - 0.5f;
+    const float sy = v * (float)h - 0.5f;
+    const int ix = (int)floorf(sx);
+    const int iy = (int)floorf(sy);
+    const float fx = sx - (float)ix;
+    const float fy = sy - (float)iy;
+    for (uint32_t c = 0; c < n; c++) {
+        out[c] = 0.f;
+    }
+    for (int dy = 0; dy <= 1; dy++) {
+        for (int dx = 0; dx <= 1; dx++) {
+            int x = ix + dx, y = iy + dy;
+            x = x < 0 ? 0 : (x > (int)w - 1 ? (int)w - 1 : x);
+            y = y < 0 ? 0 : (y > (int)h - 1 ? (int)h - 1 : y);
+            const float wgt = (dx == 0 ? 1.f - fx : fx) * (dy == 0 ? 1.f - fy : fy);
+            const float* p = data + ((size_t)y * w + (size_t)x) * n;
+            for (uint32_t c = 0; c < n; c++) {
+                out[c] += wgt * p[c];
+            }
+        }
+    }
+}
+
+/* src/core/f_ops.cpp:2764-2778 (TextureBilinear CPU kernel): tex {tw,th} x
+ * n_comp sampled at uv {n_px} VEC2 */
+void or_texture_bilinear(const float* tex, uint32_t tw, uint32_t th, uint32_t n_comp,
+                         const float* uv, size_t n_px, float* out) {
+    for (size_t p = 0; p < n_px; p++) {
+        bilerp_clamp(tex, tw, th, n_comp, uv[p * 2 + 0], uv[p * 2 + 1], out + p * n_comp);
+    }
+}
+
+/* src/core/f_ops.cpp:2665-2731 (GatherByInverseUVBilinear CPU kernel): per
+ * texel, the inverse-UV anchor (its own entry, or the first covered entry of
+ * the +-4 dilation in row order), then the tent-weighted gradient of the
+ * 7 x 7 screen pixels around it, rows then columns. */
+void or_gather_inv_uv_bilinear(const float* gy, uint32_t n_comp, uint32_t sw, uint32_t sh,
+                               const float* inv_uv, uint32_t tw, uint32_t th, const float* uv,
+                               float* out) {
+    memset(out, 0, sizeof(float) * (size_t)tw * th * n_comp);
+    for (int ty = 0; ty < (int)th; ty++) {
+        for (int tx = 0; tx < (int)tw; tx++) {
+            const float* iv0 = &inv_uv[((size_t)ty * tw + tx) * 4];
+            float iv[4] = {iv0[0], iv0[1], iv0[2], iv0[3]};
+            for (int ny = -4; ny <= 4 && iv[2] < 0.5f; ny++) {
+                for (int nx = -4; nx <= 4; nx++) {
+                    const int px = tx + nx, py = ty + ny;
+                    if (px < 0 || py < 0 || px >= (int)tw || py >= (int)th) {
+                        continue;
+                    }
+                    const float* q = &inv_uv[((size_t)py * tw + px) * 4];
+                    iv[0] = q[0];
+                    iv[1] = q[1];
+                    iv[2] = q[2];
+                    iv[3] = q[3];
+                    if (iv[2] > 0.5f) {
+                        break;
+                    }
+                }
+            }
+            if (iv[2] <= 0.5f) {
+                continue;
+            }
+            const int scx = (int)iv[0], scy = (int)iv[1];
+            float* o = &out[((size_t)ty * tw + tx) * n_comp];
+            for (int dy = -3; dy <= 3; dy++) {
+                for (int dx = -3; dx <= 3; dx++) {
+                    const int spx = scx + dx, spy = scy + dy;
+                    if (spx < 0 || spy < 0 || spx >= (int)sw || spy >= (int)sh) {
+                        continue;
+                    }
+                    const float* suv = &uv[((size_t)spy * sw + spx) * 2];
+                    const float stx = suv[0] * (float)tw - 0.5f;
+                    const float sty = suv[1] * (float)th - 0.5f;
+                    const float a = 1.f - fabsf(stx - (float)tx);
+                    const float b = 1.f - fabsf(sty - (float)ty);
+                    const float w = (a > 0.f ? a : 0.f) * (b > 0.f ? b : 0.f);
+                    if (w > 0.f) {
+                        const float* g = &gy[((size_t)spy * sw + spx) * n_comp];
+                        for (uint32_t c = 0; c < n_comp; c++) {
+                            o[c] += g[c] * w;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+/* The C3 texture fit (the graph of examples/texture_optimization/run.cpp:
+ * 112-145 with TextureBilinear, an RGBA texture and in-graph Adam as in
+ * examples/silhouette_optimization/run.cpp:404-437). Per iteration `it` and
+ * view v the cameras are mvps[(it % n_sets) * n_views + v]; the host sends
+ * clip = TransformToClip(pos, mvp) and inv_uv_attr = ScreenAttr(clip):
+ *   g_uv   = Rasterize(clip, uv, faces, S)      g_mask = Rasterize(clip, 1, faces, S)
+ *   inv_uv = Rasterize(UvAsClip(uv), inv_uv_attr, faces, T)
+ *   target = g_mask * TextureBilinear(gt_tex, g_uv, inv_uv)
+ *   pred   = g_mask * TextureBilinear(tex, g_uv, inv_uv)
+ *   diff   = StopGradient(target) - pred
+ *   loss   = SumPixelWise_v(diff * diff * Vec4(c, c, c, 0)),  c = 1 / S^2
+ * Backward (image loss seeded with 1): d diff = (0 + c diff) + c diff,
+ * d pred = -d diff, d sample = d pred * g_mask, the texel gradient of each
+ * view by GatherByInverseUVBilinear, summed over the views newest first
+ * through the <=4-ary tree; Adam on the texture. */
+int or_tex_fit(const float* pos, uint32_t n_verts, const float* uv, const float* faces,
+               uint32_t n_faces, const float* mvps, uint32_t n_sets, uint32_t n_views,
+               uint32_t screen_px, uint32_t tex_w, uint32_t tex_h, const float* gt_tex,
+               const float* tex0, float lr, uint32_t iters, float* out_tex, float* out_m,
+               float* out_v, float* out_t, float* out_loss, float* out_grad0, float* out_pred0,
+               float* out_target0, float* out_lossimg0, float* out_uv0, float* out_invuv0) {
+    const uint32_t s = screen_px;
+    const size_t npx = (size_t)s * s;
+    const size_t ntx = (size_t)tex_w * tex_h;
+    const float c = 1.f / (float)(s * s);
+    const float kw[4] = {c, c, c, 0.f};
+    float* clip = (float*)malloc(sizeof(float) * 4 * n_verts);
+    float* attr = (float*)malloc(sizeof(float) * 4 * n_verts);
+    float* uv_clip = (float*)malloc(sizeof(float) * 4 * n_verts);
+    float* ones = (float*)malloc(sizeof(float) * n_verts);
+    float* g_uv = (float*)malloc(sizeof(float) * 2 * npx);
+    float* g_mask = (float*)malloc(sizeof(float) * npx);
+    float* inv_uv = (float*)malloc(sizeof(float) * 4 * ntx);
+    float* smp_t = (float*)malloc(sizeof(float) * 4 * npx);
+    float* smp_p = (float*)malloc(sizeof(float) * 4 * npx);
+    float* gsmp = (float*)malloc(sizeof(float) * 4 * npx);
+    float* vloss = (float*)malloc(sizeof(float) * 4 * npx * n_views);
+    float* gview = (float*)malloc(sizeof(float) * 4 * ntx * n_views);
+    float* gtex = (float*)malloc(sizeof(float) * 4 * ntx);
+    float* lacc = (float*)malloc(sizeof(float) * 4 * n_views);
+    float* gacc = (float*)malloc(sizeof(float) * 4 * n_views);
+    float* tex = (float*)malloc(sizeof(float) * 4 * ntx);
+    float* m = (float*)calloc(4 * ntx, sizeof(float));
+    float* vv = (float*)calloc(4 * ntx, sizeof(float));
+    float t = 0.f;
+    memcpy(tex, tex0, sizeof(float) * 4 * ntx);
+    or_uv_as_clip(uv, n_verts, uv_clip);
+    for (uint32_t i = 0; i < n_verts; i++) {
+        ones[i] = 1.f;
+    }
+    for (uint32_t it = 0; it < iters; it++) {
+        const float* set = mvps + (size_t)(it % n_sets) * n_views * 16;
+        for (uint32_t v = 0; v < n_views; v++) {
+            or_transform_to_clip(pos, n_verts, set + 16 * v, clip);
+            or_screen_attr(clip, n_verts, s, s, attr);
+            or_rasterize(clip, n_verts, uv, 2, faces, n_faces, s, s, g_uv);
+            or_rasterize(clip, n_verts, ones, 1, faces, n_faces, s, s, g_mask);
+            or_rasterize(uv_clip, n_verts, attr, 4, faces, n_faces, tex_w, tex_h, inv_uv);
+            or_texture_bilinear(gt_tex, tex_w, tex_h, 4, g_uv, npx, smp_t);
+            or_texture_bilinear(tex, tex_w, tex_h, 4, g_uv, npx, smp_p);
+            for (size_t p = 0; p < npx; p++) {
+                for (int k = 0; k < 4; k++) {
+                    const float target = g_mask[p] * smp_t[p * 4 + k];
+                    const float pred = g_mask[p] * smp_p[p * 4 + k];
+                    const float diff = target - pred;
+                    vloss[(v * npx + p) * 4 + k] = diff * diff * kw[k];
+                    const float cd = kw[k] * diff;
+                    float gd = 0.f;
+                    gd += cd;
+                    gd += cd;
+                    gsmp[p * 4 + k] = -gd * g_mask[p];
+                    if (it == 0) {
+                        if (out_pred0) out_pred0[(v * npx + p) * 4 + k] = pred;
+                        if (out_target0) out_target0[(v * npx + p) * 4 + k] = target;
+                    }
+                }
+            }
+            or_gather_inv_uv_bilinear(gsmp, 4, s, s, inv_uv, tex_w, tex_h, g_uv,
+                                      gview + (size_t)v * 4 * ntx);
+            if (it == 0) {
+                if (out_uv0) memcpy(out_uv0 + v * 2 * npx, g_uv, sizeof(float) * 2 * npx);
+                if (out_invuv0) memcpy(out_invuv0 + v * 4 * ntx, inv_uv, sizeof(float) * 4 * ntx);
+            }
+        }
+        /* loss image: SumPixelWise over views (view order) */
+        double ltot = 0.0;
+        for (size_t p = 0; p < npx; p++) {
+            for (uint32_t v = 0; v < n_views; v++) {
+                memcpy(lacc + v * 4, vloss + (v * npx + p) * 4, sizeof(float) * 4);
+            }
+            sum_tree(lacc, n_views, 4);
+            for (int k = 0; k < 4; k++) {
+                ltot += lacc[k];
+            }
+            if (it == 0 && out_lossimg0) {
+                memcpy(out_lossimg0 + p * 4, lacc, sizeof(float) * 4);
+            }
+        }
+        if (out_loss) {
+            out_loss[it] = (float)ltot;
+        }
+        /* texel gradient: views newest first */
+        for (size_t q = 0; q < ntx; q++) {
+            for (uint32_t v = 0; v < n_views; v++) {
+                memcpy(gacc + v * 4, gview + ((size_t)(n_views - 1 - v) * ntx + q) * 4,
+                       sizeof(float) * 4);
+            }
+            sum_tree(gacc, n_views, 4);
+            memcpy(gtex + q * 4, gacc, sizeof(float) * 4);
+        }
+        if (it == 0 && out_grad0) {
+            memcpy(out_grad0, gtex, sizeof(float) * 4 * ntx);
+        }
+        adam_step(tex, m, vv, &t, gtex, (uint32_t)(4 * ntx), lr);
+    }
+    if (out_tex) memcpy(out_tex, tex, sizeof(float) * 4 * ntx);
+    if (out_m) memcpy(out_m, m, sizeof(float) * 4 * ntx);
+    if (out_v) memcpy(out_v, vv, sizeof(float) * 4 * ntx);
+    if (out_t) *out_t = t;
+    free(clip);
+    free(attr);
+    free(uv_clip);
+    free(ones);
+    free(g_uv);
+    free(g_mask);
+    free(inv_uv);
+    free(smp_t);
+    free(smp_p);
+    free(gsmp);
+    free(vloss);
+    free(gview);
+    free(gtex);
+    free(lacc);
+    free(gacc);
+    free(tex);
+    free(m);
+    free(vv);
+    return 0;
+}

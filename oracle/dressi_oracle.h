@@ -142,6 +142,31 @@ int or_aa_fit(const float* pos0, uint32_t n_verts, const float* faces, uint32_t 
               float* out_v, float* out_t, float* out_loss, float* out_grad0,
               float* out_pred0, float* out_target, float* out_tri0, float* out_lossimg0);
 
+/* ---- texture path (C3) ---- */
+/* examples/common/geometry_utils.cpp:86-131 (GenerateUvSphere); counts only
+ * when an output is NULL */
+int or_uv_sphere(uint32_t stacks, uint32_t slices, uint32_t* n_verts, uint32_t* n_faces,
+                 float* pos, float* uv, float* faces);
+/* src/core/mesh_utils.cpp:180-189 (UvAsClip) */
+void or_uv_as_clip(const float* uv, uint32_t n_verts, float* clip);
+/* src/core/mesh_utils.cpp:191-203 (ScreenAttr) */
+void or_screen_attr(const float* clip, uint32_t n_verts, uint32_t w, uint32_t h, float* attr);
+/* src/core/f_ops.cpp:2764-2778 (TextureBilinear), ibl_math.h:91-115 */
+void or_texture_bilinear(const float* tex, uint32_t tw, uint32_t th, uint32_t n_comp,
+                         const float* uv, size_t n_px, float* out);
+/* src/core/f_ops.cpp:2665-2731 (GatherByInverseUVBilinear) */
+void or_gather_inv_uv_bilinear(const float* gy, uint32_t n_comp, uint32_t sw, uint32_t sh,
+                               const float* inv_uv, uint32_t tw, uint32_t th, const float* uv,
+                               float* out);
+/* the C3 texture fit: examples/texture_optimization/run.cpp:112-145 with
+ * TextureBilinear, RGBA texture, L2 on RGB, in-graph Adam */
+int or_tex_fit(const float* pos, uint32_t n_verts, const float* uv, const float* faces,
+               uint32_t n_faces, const float* mvps, uint32_t n_sets, uint32_t n_views,
+               uint32_t screen_px, uint32_t tex_w, uint32_t tex_h, const float* gt_tex,
+               const float* tex0, float lr, uint32_t iters, float* out_tex, float* out_m,
+               float* out_v, float* out_t, float* out_loss, float* out_grad0, float* out_pred0,
+               float* out_target0, float* out_lossimg0, float* out_uv0, float* out_invuv0);
+
 #ifdef __cplusplus
 }
 #endif

@@ -155,6 +155,53 @@ class _Lib:
         return r
 
 
+    # ---- texture path ----------------------------------------------------
+    def uv_sphere(self, stacks, slices):
+        nv, nf = _U32(), _U32()
+        self._call("uv_sphere", _U32(stacks), _U32(slices), C.byref(nv), C.byref(nf), None,
+                   None, None)
+        pos = np.zeros((nv.value, 3), np.float32)
+        uv = np.zeros((nv.value, 2), np.float32)
+        faces = np.zeros((nf.value, 3), np.float32)
+        self._call("uv_sphere", _U32(stacks), _U32(slices), C.byref(nv), C.byref(nf), _fp(pos),
+                   _fp(uv), _fp(faces))
+        return pos, uv, faces
+
+    def gather_inv_uv_bilinear(self, gy, inv_uv, uv):
+        """gy {sh, sw, nc}, inv_uv {th, tw, 4}, uv {sh, sw, 2} -> {th, tw, nc}."""
+        gy, inv_uv, uv = _f32(gy), _f32(inv_uv), _f32(uv)
+        sh, sw, nc = gy.shape
+        th, tw = inv_uv.shape[:2]
+        out = np.zeros((th, tw, nc), np.float32)
+        self._call("gather_inv_uv_bilinear" if self.prefix == "or_" else "gather_bilinear",
+                   _fp(gy), _U32(nc), _U32(sw), _U32(sh), _fp(inv_uv), _U32(tw), _U32(th),
+                   _fp(uv), _fp(out))
+        return out
+
+    def tex_fit(self, pos, uv, faces, mvps, screen, gt_tex, tex0, lr=1e-2, iters=1,
+                want_images=True):
+        """The C3 texture fit; mvps {n_sets, n_views, 16}; textures {th, tw, 4}."""
+        pos, uv, faces, mvps = _f32(pos), _f32(uv), _f32(faces), _f32(mvps)
+        gt_tex, tex0 = _f32(gt_tex), _f32(tex0)
+        n_sets, n = mvps.shape[0], mvps.shape[1]
+        th, tw = gt_tex.shape[:2]
+        s = screen
+        z = lambda *sh: np.zeros(sh, np.float32)
+        r = dict(tex=z(th, tw, 4), m=z(th, tw, 4), v=z(th, tw, 4), t=z(1),
+                 loss=z(max(iters, 1)), grad0=z(th, tw, 4))
+        if want_images:
+            r.update(pred0=z(n, s, s, 4), target0=z(n, s, s, 4), lossimg0=z(s, s, 4),
+                     uv0=z(n, s, s, 2), invuv0=z(n, th, tw, 4))
+        g = r.get
+        self._call("tex_fit", _fp(pos), _U32(pos.shape[0]), _fp(uv), _fp(faces),
+                   _U32(faces.shape[0]), _fp(mvps), _U32(n_sets), _U32(n), _U32(s), _U32(tw),
+                   _U32(th), _fp(gt_tex), _fp(tex0), C.c_float(lr), _U32(iters), _fp(r["tex"]),
+                   _fp(r["m"]), _fp(r["v"]), _fp(r["t"]), _fp(r["loss"]), _fp(r["grad0"]),
+                   _fp(g("pred0")), _fp(g("target0")), _fp(g("lossimg0")), _fp(g("uv0")),
+                   _fp(g("invuv0")))
+        return r
+
+
 class Oracle(_Lib):
     """The C restatement (oracle/dressi_oracle.c)."""
 
@@ -279,6 +326,28 @@ class Oracle(_Lib):
         self.fn("col_sum")(_fp(x), _U32(nc), _U32(w), _U32(h), _fp(out))
         return out
 
+    def texture_bilinear(self, tex, uv):
+        """tex {th, tw, nc}, uv {..., 2} -> {..., nc}."""
+        tex, uv = _f32(tex), _f32(uv)
+        th, tw, nc = tex.shape
+        n_px = uv.size // 2
+        out = np.zeros(uv.shape[:-1] + (nc,), np.float32)
+        self.fn("texture_bilinear")(_fp(tex), _U32(tw), _U32(th), _U32(nc), _fp(uv),
+                                    C.c_size_t(n_px), _fp(out))
+        return out
+
+    def uv_as_clip(self, uv):
+        uv = _f32(uv)
+        out = np.zeros((uv.shape[0], 4), np.float32)
+        self.fn("uv_as_clip")(_fp(uv), _U32(uv.shape[0]), _fp(out))
+        return out
+
+    def screen_attr(self, clip, w, h):
+        clip = _f32(clip)
+        out = np.zeros((clip.shape[0], 4), np.float32)
+        self.fn("screen_attr")(_fp(clip), _U32(clip.shape[0]), _U32(w), _U32(h), _fp(out))
+        return out
+
     def hsr_forward(self, rs, tri0, tri1, tri2, target, radius):
         rs, target = _f32(rs), _f32(target)
         h, w = target.shape
@@ -373,6 +442,17 @@ def _ref_antialias_bwd(self, gy, img, tri, clip, faces, vtx_faces, seed, n_sampl
     return g_img, wide, g_vtx
 
 
+def _ref_texture_bilinear(self, tex, uv):
+    """tex {th, tw, nc}, uv {uh, uw, 2} -> {uh, uw, nc}."""
+    tex, uv = _f32(tex), _f32(uv)
+    th, tw, nc = tex.shape
+    uh, uw = uv.shape[:2]
+    out = np.zeros((uh, uw, nc), np.float32)
+    self._call("texture_bilinear", _fp(tex), _U32(tw), _U32(th), _U32(nc), _fp(uv), _U32(uw),
+               _U32(uh), _fp(out))
+    return out
+
+
 def face_id_buffer(rs):
     """The fused plan's face-id buffer for RasterizeSoft output `rs` (dist,
     fid, hard z, coverage): face + 1 where covered, 0 elsewhere, bit 31 set
@@ -389,3 +469,4 @@ def have_reference() -> bool:
 
 Reference.antialias = _ref_antialias
 Reference.antialias_bwd = _ref_antialias_bwd
+Reference.texture_bilinear = _ref_texture_bilinear

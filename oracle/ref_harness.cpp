@@ -760,4 +760,183 @@ int refh_aa_fit(const float* pos0, uint32_t n_verts, const float* faces,
     });
 }
 
+// TextureBilinear (src/core/f_ops.cpp:2736-2780) through the evaluator:
+// tex {tw,th} x n_comp, uv {uw,uh} VEC2 -> out {uw,uh} x n_comp.
+int refh_texture_bilinear(const float* tex, uint32_t tw, uint32_t th, uint32_t n_comp,
+                          const float* uv, uint32_t uw, uint32_t uh, float* out) {
+    return Guard([&] {
+        Variable t(VecOf(n_comp), {tw, th});
+        Variable u(VEC2, {uw, uh});
+        Variable iv(VEC4, {tw, th});
+        Variable y = F::TextureBilinear(t, u, iv);
+        CpuEvaluator ev;
+        ev.bind(t, Tensor(VecOf(n_comp), {tw, th}, tex));
+        ev.bind(u, Tensor(VEC2, {uw, uh}, uv));
+        ev.bind(iv, Fill(VEC4, {tw, th}, 0.f));
+        CopyOut(ev.eval(y), out);
+    });
+}
+
+// GatherByInverseUVBilinear (src/core/f_ops.cpp:2650-2732), reached as the
+// backward of TextureBilinear for the image loss TextureBilinear(tex) * gy
+// (its seed 1 gives the sampled image the gradient gy exactly):
+// gy {sw,sh} x n_comp, inv_uv {tw,th} VEC4, uv {sw,sh} VEC2 -> {tw,th}.
+int refh_gather_bilinear(const float* gy, uint32_t n_comp, uint32_t sw, uint32_t sh,
+                         const float* inv_uv, uint32_t tw, uint32_t th, const float* uv,
+                         float* out) {
+    return Guard([&] {
+        Variable t(VecOf(n_comp), {tw, th});
+        Variable u(VEC2, {sw, sh});
+        Variable iv(VEC4, {tw, th});
+        Variable g(VecOf(n_comp), {sw, sh});
+        Variable loss = F::TextureBilinear(t, u, iv) * g;
+        Variable t_mut = t;
+        t_mut.setRequiresGradRecursively();
+        auto [xs, gxs] = BuildBackward(loss);
+        DRESSI_CHECK(xs.size() == 1 && xs[0] == t, "expected the texture as the only leaf");
+        CpuEvaluator ev;
+        ev.bind(t, Fill(VecOf(n_comp), {tw, th}, 0.f));
+        ev.bind(u, Tensor(VEC2, {sw, sh}, uv));
+        ev.bind(iv, Tensor(VEC4, {tw, th}, inv_uv));
+        ev.bind(g, Tensor(VecOf(n_comp), {sw, sh}, gy));
+        CopyOut(ev.eval(gxs[0]), out);
+    });
+}
+
+// The C3 texture fit: the graph of examples/texture_optimization/run.cpp:
+// 112-145 with TextureBilinear, an RGBA texture, the RGB L2 image loss and
+// the silhouette example's in-graph Adam (run.cpp:404-437), on the
+// reference's CpuEvaluator with DressiAD's copy-back. Per iteration `it` the
+// host sends, per view v, clip = TransformToClip(pos, mvp) and
+// inv_uv_attr = ScreenAttr(clip) with mvp = mvps[(it % n_sets) * n_views + v]
+// (the example's per-iteration sendImg of moving cameras).
+//   pos {V,3}, uv {V,2}, faces {F,3}, gt_tex / tex0 {tw,th} VEC4.
+//   Outputs (nullable): out_tex/m/v {T,4}, out_t, out_loss {iters} (sum of
+//   the loss image), out_grad0 {T,4}, out_pred0 / out_target0 {N,S,S,4},
+//   out_lossimg0 {S,S,4}, out_uv0 {N,S,S,2}, out_invuv0 {N,T,4}.
+int refh_tex_fit(const float* pos, uint32_t n_verts, const float* uv, const float* faces,
+                 uint32_t n_faces, const float* mvps, uint32_t n_sets, uint32_t n_views,
+                 uint32_t screen_px, uint32_t tex_w, uint32_t tex_h, const float* gt_tex,
+                 const float* tex0, float lr, uint32_t iters, float* out_tex, float* out_m,
+                 float* out_v, float* out_t, float* out_loss, float* out_grad0,
+                 float* out_pred0, float* out_target0, float* out_lossimg0, float* out_uv0,
+                 float* out_invuv0) {
+    return Guard([&] {
+        const ImgSize screen = {screen_px, screen_px};
+        const ImgSize tex_size = {tex_w, tex_h};
+        Variable vtx_uv(VEC2, {n_verts, 1});
+        Variable faces_v(IVEC3, {n_faces, 1});
+        Variable uv_clip(VEC4, {n_verts, 1});
+        Variable ones(FLOAT, {n_verts, 1});
+        Variable gt_tex_v(VEC4, tex_size);
+        Variable tex(VEC4, tex_size);
+        Variable adam_m(VEC4, tex_size);
+        Variable adam_v(VEC4, tex_size);
+        Variable adam_t(FLOAT, {1, 1});
+        std::vector<Variable> clips, attrs, preds, targets, uvs, invs;
+        Variables view_losses;
+        const float c = 1.f / float(screen.w * screen.h);
+        for (uint32_t v = 0; v < n_views; v++) {
+            clips.emplace_back(VEC4, ImgSize{n_verts, 1});
+            attrs.emplace_back(VEC4, ImgSize{n_verts, 1});
+            Variable g_uv = F::Rasterize(clips[v], vtx_uv, faces_v, screen);
+            Variable g_mask = F::Rasterize(clips[v], ones, faces_v, screen);
+            Variable inv_uv = F::Rasterize(uv_clip, attrs[v], faces_v, tex_size);
+            uvs.push_back(g_uv);
+            invs.push_back(inv_uv);
+            targets.push_back(g_mask * F::TextureBilinear(gt_tex_v, g_uv, inv_uv));
+            preds.push_back(g_mask * F::TextureBilinear(tex, g_uv, inv_uv));
+            Variable diff = F::StopGradient(targets[v]) - preds[v];
+            view_losses.push_back(diff * diff * F::Vec4(c, c, c, 0.f));
+        }
+        Variable loss = F::SumPixelWise(view_losses);
+        Variable tex_mut = tex;
+        tex_mut.setRequiresGradRecursively();
+        auto [xs, gxs] = BuildBackward(loss);
+        DRESSI_CHECK(xs.size() == 1 && xs[0] == tex, "expected the texture as the only leaf");
+        const Variable g = gxs[0];
+        const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+        Variable t_new = adam_t + 1.f;
+        Variable m_new = adam_m * b1 + g * (1.f - b1);
+        Variable v_new = adam_v * b2 + g * g * (1.f - b2);
+        Variable bc1 = 1.f - F::Pow(F::Float(b1), t_new);
+        Variable bc2 = 1.f - F::Pow(F::Float(b2), t_new);
+        Variable step = (m_new / bc1) / (F::Sqrt(v_new / bc2) + eps) * lr;
+        Variable tex_new = tex - step;
+
+        CpuImage uv_img(n_verts, 1, 2);
+        std::memcpy(uv_img.data.data(), uv, sizeof(float) * 2 * n_verts);
+        const CpuImage uv_clip_img = UvAsClip(uv_img);
+        std::vector<float> ones_v(n_verts, 1.f);
+        const size_t ntx = size_t(tex_w) * tex_h;
+        CpuTensor t_tex = Tensor(VEC4, tex_size, tex0);
+        CpuTensor t_m = Fill(VEC4, tex_size, 0.f);
+        CpuTensor t_v = Fill(VEC4, tex_size, 0.f);
+        CpuTensor t_t = Fill(FLOAT, {1, 1}, 0.f);
+        for (uint32_t it = 0; it < iters; it++) {
+            CpuEvaluator ev;
+            ev.bind(vtx_uv, Tensor(VEC2, {n_verts, 1}, uv));
+            ev.bind(faces_v, Tensor(IVEC3, {n_faces, 1}, faces));
+            ev.bind(uv_clip, Tensor(VEC4, {n_verts, 1}, uv_clip_img.data.data()));
+            ev.bind(ones, Tensor(FLOAT, {n_verts, 1}, ones_v.data()));
+            ev.bind(gt_tex_v, Tensor(VEC4, tex_size, gt_tex));
+            const float* set = mvps + size_t(it % n_sets) * n_views * 16;
+            for (uint32_t v = 0; v < n_views; v++) {
+                const float* m = set + 16 * v;
+                CpuImage clip_img(n_verts, 1, 4);
+                for (uint32_t i = 0; i < n_verts; i++) {
+                    const float p[4] = {pos[i * 3 + 0], pos[i * 3 + 1], pos[i * 3 + 2], 1.f};
+                    for (int row = 0; row < 4; row++) {
+                        float acc = 0.f;
+                        for (int k = 0; k < 4; k++) {
+                            acc += m[k * 4 + row] * p[k];
+                        }
+                        clip_img.at(i, 0, uint32_t(row)) = acc;
+                    }
+                }
+                const CpuImage attr_img = ScreenAttr(clip_img, screen);
+                ev.bind(clips[v], Tensor(VEC4, {n_verts, 1}, clip_img.data.data()));
+                ev.bind(attrs[v], Tensor(VEC4, {n_verts, 1}, attr_img.data.data()));
+            }
+            ev.bind(tex, t_tex);
+            ev.bind(adam_m, t_m);
+            ev.bind(adam_v, t_v);
+            ev.bind(adam_t, t_t);
+            const CpuTensor li = ev.eval(loss);
+            if (out_loss) {
+                double acc = 0.0;
+                for (float x : li.data) {
+                    acc += x;
+                }
+                out_loss[it] = float(acc);
+            }
+            if (it == 0) {
+                CopyOut(li, out_lossimg0);
+                if (out_grad0) {
+                    CopyOut(ev.eval(g), out_grad0);
+                }
+                const size_t px = size_t(screen.w) * screen.h;
+                for (uint32_t v = 0; v < n_views; v++) {
+                    if (out_pred0) CopyOut(ev.eval(preds[v]), out_pred0 + v * px * 4);
+                    if (out_target0) CopyOut(ev.eval(targets[v]), out_target0 + v * px * 4);
+                    if (out_uv0) CopyOut(ev.eval(uvs[v]), out_uv0 + v * px * 2);
+                    if (out_invuv0) CopyOut(ev.eval(invs[v]), out_invuv0 + v * ntx * 4);
+                }
+            }
+            CpuTensor n_tex = ev.eval(tex_new);
+            CpuTensor n_m = ev.eval(m_new);
+            CpuTensor n_v = ev.eval(v_new);
+            CpuTensor n_t = ev.eval(t_new);
+            t_tex = std::move(n_tex);
+            t_m = std::move(n_m);
+            t_v = std::move(n_v);
+            t_t = std::move(n_t);
+        }
+        CopyOut(t_tex, out_tex);
+        CopyOut(t_m, out_m);
+        CopyOut(t_v, out_v);
+        CopyOut(t_t, out_t);
+    });
+}
+
 }  // extern "C"

@@ -3,7 +3,8 @@ build (oracle/_ref/libdressi_ref.so, compiled from the reference sources by
 oracle/Makefile). Inputs are generated with the oracle's seeded scene helpers
 and stored next to the outputs, so the fixtures are self-contained data.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py            # every fixture
+    python tests/golden/make_golden.py texture    # the texture path's only
 
 Each .npz holds `in_*` arrays (inputs) and `out_*` arrays (reference outputs).
 """
@@ -163,9 +164,79 @@ def aa_fit_fixture(o, r, name, level, noise, seed, mvps, screen, iters, lr, imag
     print("wrote", name, {k: v.shape for k, v in arrs.items()})
 
 
+def random_orbit_sets(o, n_sets, n_views, seed, dist=3.0):
+    """{n_sets, n_views, 16} MVPs of random orbit cameras (inputs only)."""
+    rng = np.random.default_rng(seed)
+    proj = o.perspective_vk(45.0 * 3.14159265 / 180.0, 1.0, 0.1, 10.0)
+    out = np.zeros((n_sets, n_views, 16), np.float32)
+    for s in range(n_sets):
+        for v in range(n_views):
+            yaw, pitch = rng.random() * 2 * math.pi, (rng.random() - 0.5) * 2.0
+            eye = [dist * math.cos(pitch) * math.sin(yaw), dist * math.sin(pitch),
+                   dist * math.cos(pitch) * math.cos(yaw)]
+            out[s, v] = o.mat4_mul(proj, o.look_at(eye))
+    return out
+
+
+def tex_fixtures(o, r):
+    """Per-op texture scenes: TextureBilinear (in and out of the clamp
+    region, 1 / 3 / 4 components), GatherByInverseUVBilinear (covered and
+    uncovered inverse-UV entries, anchors near and off the screen edges) and
+    the UV-sphere generator."""
+    rng = np.random.default_rng(11)
+    arrs = {}
+    for nc in (1, 3, 4):
+        tex = rng.random((5, 7, nc)).astype(np.float32)
+        uv = (rng.random((9, 11, 2)) * 1.4 - 0.2).astype(np.float32)
+        arrs[f"in_bl{nc}_tex"], arrs[f"in_bl{nc}_uv"] = tex, uv
+        arrs[f"out_bl{nc}"] = r.texture_bilinear(tex, uv)
+    for name, (sh, sw, th, tw, cov) in {"g_small": (12, 10, 6, 8, 0.7),
+                                        "g_sparse": (20, 24, 16, 12, 0.15)}.items():
+        gy = rng.standard_normal((sh, sw, 4)).astype(np.float32)
+        iv = np.zeros((th, tw, 4), np.float32)
+        iv[..., 0] = rng.random((th, tw)) * (sw + 4) - 2
+        iv[..., 1] = rng.random((th, tw)) * (sh + 4) - 2
+        iv[..., 2] = (rng.random((th, tw)) < cov).astype(np.float32)
+        uv = rng.random((sh, sw, 2)).astype(np.float32)
+        arrs[f"in_{name}_gy"], arrs[f"in_{name}_iv"], arrs[f"in_{name}_uv"] = gy, iv, uv
+        arrs[f"out_{name}"] = r.gather_inv_uv_bilinear(gy, iv, uv)
+    pos, uv, faces = r.uv_sphere(16, 8)
+    arrs.update(out_uvs16_pos=pos, out_uvs16_uv=uv, out_uvs16_faces=faces)
+    p2, _, f2 = r.uv_sphere(128, 64)
+    arrs["out_uvs128_counts"] = np.array([len(p2), len(f2)], np.int64)
+    np.savez_compressed(os.path.join(OUT, "tex_unit.npz"), **arrs)
+    print("wrote tex_unit.npz", len(arrs), "arrays")
+
+
+def tex_fit_fixture(o, r, name, stacks, slices, screen, tex, views, sets, iters, seed, images):
+    pos, uv, faces = o.uv_sphere(stacks, slices)
+    mvps = random_orbit_sets(o, sets, views, seed)
+    rng = np.random.default_rng(seed + 100)
+    gt = rng.random((tex, tex, 4)).astype(np.float32)
+    tex0 = np.full((tex, tex, 4), 0.5, np.float32)
+    res = r.tex_fit(pos, uv, faces, mvps, screen, gt, tex0, lr=1e-2, iters=iters,
+                    want_images=images)
+    arrs = dict(in_pos=pos, in_uv=uv, in_faces=faces, in_mvps=mvps, in_gt=gt, in_tex0=tex0,
+                in_cfg=np.array([screen, iters, 1e-2], np.float64))
+    arrs.update({"out_" + k: v for k, v in res.items()})
+    np.savez_compressed(os.path.join(OUT, name), **arrs)
+    print("wrote", name, {k: v.shape for k, v in arrs.items()})
+
+
+def texture_main(o, r):
+    tex_fixtures(o, r)
+    tex_fit_fixture(o, r, "tex_uvs16_64px_3view_3it.npz", 16, 8, 64, 32, 3, 2, 3, 5, True)
+    tex_fit_fixture(o, r, "tex_uvs32_8view_128px_3it.npz", 32, 16, 128, 64, 8, 3, 3, 6, False)
+    tex_fit_fixture(o, r, "tex_uvs16_64px_20it.npz", 16, 8, 64, 32, 2, 20, 20, 7, False)
+
+
 def main():
     build(ref=True)
     o, r = Oracle(), Reference()
+    if sys.argv[1:] == ["texture"]:
+        texture_main(o, r)
+        return
+    texture_main(o, r)
     op_fixtures(o, r)
     aa_fixtures(o, r)
     aa_fit_fixture(o, r, "aa_ico3_64px_5it.npz", 3, 0.05, 1, front_mvp(o), 64, 5, 1e-3, True)
