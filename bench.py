@@ -1,7 +1,7 @@
 """Benchmark of the fused silhouette-fit iteration (fwd + bwd + Adam) on one
 MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--workload c4_hsr|c4|c2|c1]
+    python bench.py [--steps K] [--warmup W] [--workload c4_hsr|c4|c3|c2|c1]
 
 A step is one iteration of the silhouette fit. HardSoftRas (c4_hsr, c2, c1):
 per view clip transform, SoftClip, tile-binned RasterizeSoft, the per-pixel
@@ -9,7 +9,10 @@ soft-probability chain and L2 loss image, the stochastic FaceFetchBwd gather
 fused with the chain's backward, LookupFacesBwd + clip->pos chain, Adam. AA
 (c4): clip transform, tile-binned hard raster of face ids, AntiAlias of the
 mask + L2 loss image, the stochastic AntiAliasBwdVtx gather, ColSum +
-clip->pos chain, Adam. One hipGraph launch per step. Inputs (mesh, Adam
+clip->pos chain, Adam. Texture (c3): per view clip transform + ScreenAttr,
+hard raster of face ids, g_uv / g_mask interpolation and bilinear samples of
+the texture and the target texture + RGB L2 loss image, then per texel the
+inverse-UV gather of every view and Adam. One hipGraph launch per step. Inputs (mesh, Adam
 state, target images) are resident in HBM before the timed region. Prints
 ONE JSON line.
 """
@@ -57,6 +60,37 @@ def kernel_bytes_aa(n_views: int, s: int, n_faces: int, n_verts: int, samples: i
         "k_aa_fwd": n * 12.0 * S2 + 4.0 * S2,
         "k_aa_face_bwd": n * F * (96.0 + 12.0 * samples),
         "k_aa_vertex_adam": n * 120.0 * V + 72.0 * V,
+    }
+
+
+def iteration_bytes_tex(n_views: int, s: int, n_faces: int, n_verts: int, texels: int) -> float:
+    """Compulsory bytes of one texture iteration (per pixel and view: 8-byte
+    visibility write and read; per view: faces, clip, uv, screen attribute;
+    the loss image; per texel: texture read, target texture read, gradient
+    write + read, Adam state 3 reads + 3 writes, 16 B each)."""
+    return (n_views * (16.0 * s * s + 12.0 * n_faces + 40.0 * n_verts) + 4.0 * s * s
+            + 160.0 * texels)
+
+
+def kernel_bytes_tex(n_views: int, s: int, n_faces: int, n_verts: int, texels: int) -> dict:
+    """Algorithmic bytes per launch of the texture-plan kernels.
+
+    clip:     positions in, clip (16 B) and screen attribute (8 B) out, per
+              vertex and view
+    setup:    clip in, faces and the screen triangles out, per view
+    raster:   screen triangles in, 4-byte face-id image out, per view
+    fwd:      face id in, g_uv (8 B) and d loss / d sample (16 B) out per
+              pixel and view, RGBA loss image out, both textures read once
+    bwd_adam: g_uv + d loss / d sample read once per view, the UV raster's
+              texel record, texture / m / v read + write, per texel
+    """
+    n, S2, F, V, T = n_views, float(s) * s, float(n_faces), float(n_verts), float(texels)
+    return {
+        "k_tex_clip": n * 36.0 * V,
+        "k_aa_setup": n * (16.0 * V + 48.0 * F),
+        "k_aa_raster": n * (4.0 * S2 + 36.0 * F),
+        "k_tex_fwd": n * 28.0 * S2 + 16.0 * S2 + 32.0 * T,
+        "k_tex_bwd_adam": n * 24.0 * S2 + 112.0 * T,
     }
 
 
@@ -118,6 +152,28 @@ def cpu_info() -> str:
     return platform.processor() or "unknown"
 
 
+def cpu_baseline_tex(workload) -> dict:
+    """The oracle's texture fit (single thread) on a bounded sample: one
+    iteration with ONE of the workload's views at full resolution, scaled to
+    iterations/s of all views (the views are independent until the texel
+    gradient; Adam is negligible)."""
+    import opendressi_amd as od
+    from oracle.pyoracle import ORACLE_SO, Oracle, build
+    if not os.path.exists(ORACLE_SO):
+        build()
+    pos, uv, faces, mvps, gt, tex0 = od.make_tex_scene(workload)
+    o = Oracle()
+    t0 = time.perf_counter()
+    o.tex_fit(pos, uv, faces, mvps[:1, :1], workload.screen, gt, tex0, lr=workload.lr, iters=1,
+              want_images=False)
+    dt = time.perf_counter() - t0
+    n = mvps.shape[1]
+    return {"value": 1.0 / (dt * n), "unit": "iterations/s", "cores": 1, "kind": "port",
+            "sample": (f"1 iteration of 1 of {n} views at {workload.screen}^2 with the "
+                       f"{workload.tex}^2 texture, {dt:.2f} s, scaled x{n}; host CPU: "
+                       f"{cpu_info()}, nproc {os.cpu_count()}")}
+
+
 def cpu_baseline(workload) -> dict:
     """The oracle (C restatement of the reference CPU evaluator, single
     thread) on a bounded sample: one iteration of ONE of the workload's views
@@ -160,9 +216,14 @@ def main() -> int:
         return 2
 
     import opendressi_amd as od
-    w = od.WORKLOADS[args.workload]
     ctx = od.Context(0)
-    fit = od.SilhouetteFit.from_workload(ctx, args.workload)
+    tex = args.workload in od.TEX_WORKLOADS
+    if tex:
+        w = od.TEX_WORKLOADS[args.workload]
+        fit = od.TextureFit.from_workload(ctx, args.workload)
+    else:
+        w = od.WORKLOADS[args.workload]
+        fit = od.SilhouetteFit.from_workload(ctx, args.workload)
     nv, nf, nviews, s = fit.n_verts, fit.n_faces, fit.n_views, fit.screen
 
     fit.step(args.warmup)
@@ -178,10 +239,21 @@ def main() -> int:
     prof = fit.profile(args.profile_iters)
     dom = max(prof, key=prof.get)
     dom_us = prof[dom]
-    aa = w.technique == "aa"
-    kbytes = (kernel_bytes_aa if aa else kernel_bytes)(nviews, s, nf, nv)
+    if tex:
+        texels = fit.tex_w * fit.tex_h
+        kbytes = kernel_bytes_tex(nviews, s, nf, nv, texels)
+        ibytes = iteration_bytes_tex(nviews, s, nf, nv, texels)
+        desc = (f"{w.name}: texture fit, {s}x{s} x {nviews} random orbit views per iteration, "
+                f"UV sphere {w.stacks}x{w.slices} ({nv} v / {nf} f), {fit.tex_w}x{fit.tex_h} "
+                f"RGBA texture, bilinear, Adam lr {w.lr}")
+    else:
+        aa = w.technique == "aa"
+        kbytes = (kernel_bytes_aa if aa else kernel_bytes)(nviews, s, nf, nv)
+        ibytes = (iteration_bytes_aa if aa else iteration_bytes)(nviews, s, nf, nv)
+        desc = (f"{w.name}: {'AA' if aa else 'HardSoftRas'} silhouette fit, "
+                f"{s}x{s} x {nviews} views, icosphere L{w.level} "
+                f"({nv} v / {nf} f), {'' if aa else 'r=3 px, '}8 samples, Adam lr {w.lr}")
     dbytes = kbytes[dom]
-    ibytes = (iteration_bytes_aa if aa else iteration_bytes)(nviews, s, nf, nv)
     achieved = dbytes / (dom_us * 1e-6)
     traffic = measured_traffic(dom, args.workload)
     fit.close()
@@ -199,11 +271,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": (f"{w.name}: {'AA' if aa else 'HardSoftRas'} silhouette fit, "
-                                f"{s}x{s} x {nviews} views, icosphere L{w.level} "
-                                f"({nv} v / {nf} f), {'' if aa else 'r=3 px, '}8 samples, "
-                                f"Adam lr {w.lr}"),
-                   "screen": s, "views": nviews, "verts": nv, "faces": nf},
+        "config": {"workload": desc, "screen": s, "views": nviews, "verts": nv, "faces": nf},
         "roofline": {"bound": "hbm", "kernel": dom,
                      "achieved": achieved / 1e9,
                      "peak": HBM_PEAK / 1e9, "unit": "GB/s",
@@ -219,7 +287,7 @@ def main() -> int:
         "loss_after": loss_end,
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(w)
+        line["cpu_baseline"] = cpu_baseline_tex(w) if tex else cpu_baseline(w)
     print(json.dumps(line), flush=True)
     ctx.close()
     if args.copy_mb > 0:

@@ -173,7 +173,8 @@ struct TexDev {
     const float2* uv;       // [V]
     const float* mvps;      // [n_sets][N][16]
     float2* sattr;          // [N][V] ScreenAttr x, y
-    const float4* texel;    // [T]: barycentrics l0, l1, l2 and bits(face + 1) of the UV raster
+    const float4* texel;    // [T]: the inverse-UV anchor's UV-raster record: barycentrics
+                            // l0, l1, l2 and bits(face + 1), zero when no anchor
     const float4* gt;       // [T] target texture
     float4* tex;            // [T]
     float4* m;
@@ -182,6 +183,7 @@ struct TexDev {
     uint32_t* done;
     float2* suv;            // [N][S][S] g_uv
     float4* gs;             // [N][S][S] d loss / d TextureBilinear(tex) output
+    uint32_t* key;          // [N][S][S] floor(uv * T - 0.5) + 1 as x | y << 16 (clamped)
     float4* loss;           // [S][S]
     float4* pred;           // [N][S][S] or null
     float4* target;         // [N][S][S] or null
@@ -209,6 +211,35 @@ __global__ __launch_bounds__(256) void k_tex_clip(TexDev d) {
     const float ndc_y = c.y / c.w;
     d.sattr[i] = make_float2((ndc_x * 0.5f + 0.5f) * (float)d.r.g.width,
                              (ndc_y * 0.5f + 0.5f) * (float)d.r.g.height);
+}
+
+// The inverse-UV anchor of every texel (view-independent, so computed once):
+// the texel's own UV-raster record when covered, else that of the first
+// covered texel of the +-4 neighbourhood in row order
+// (GatherByInverseUVBilinear's dilation, f_ops.cpp:2679-2697), else zero.
+__global__ __launch_bounds__(256) void k_tex_anchor(const float4* own, int tw, int th,
+                                                    float4* anchor) {
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= tw * th) {
+        return;
+    }
+    const int ty = q / tw, tx = q - ty * tw;
+    float4 rec = own[q];
+    bool cov = __float_as_uint(rec.w) != 0u;
+    for (int ny = -4; ny <= 4 && !cov; ny++) {
+        for (int nx = -4; nx <= 4; nx++) {
+            const int px = tx + nx, py = ty + ny;
+            if (px < 0 || py < 0 || px >= tw || py >= th) {
+                continue;
+            }
+            rec = own[(size_t)py * tw + px];
+            if (__float_as_uint(rec.w) != 0u) {
+                cov = true;
+                break;
+            }
+        }
+    }
+    anchor[q] = cov ? rec : make_float4(0.f, 0.f, 0.f, __uint_as_float(0u));
 }
 
 // Rasterize of the UV layout (UvAsClip: w = 1, so the perspective-correct
@@ -332,6 +363,12 @@ __global__ __launch_bounds__(64 * NV) void k_tex_fwd(TexDev d) {
         }
         d.suv[vo] = make_float2(u, v);
         d.gs[vo] = make_float4(gi[0], gi[1], gi[2], gi[3]);
+        // the texels this pixel's tent can weigh: floor(s) + {0, 1} at
+        // s = uv * T - 0.5 (exactly the backward's s); NaN and far values
+        // clamp to keys no texel matches (or to one whose exact weight is 0)
+        const float kx = fminf(fmaxf(floorf(u * (float)d.tw - 0.5f) + 1.f, 0.f), 65535.f);
+        const float ky = fminf(fmaxf(floorf(v * (float)d.th - 0.5f) + 1.f, 0.f), 65535.f);
+        d.key[vo] = (uint32_t)kx | ((uint32_t)ky << 16);
         if (d.pred) {
             d.pred[vo] = make_float4(pi[0], pi[1], pi[2], pi[3]);
             d.target[vo] = make_float4(ti[0], ti[1], ti[2], ti[3]);
@@ -356,72 +393,161 @@ __global__ __launch_bounds__(64 * NV) void k_tex_fwd(TexDev d) {
     }
 }
 
-// Per texel: GatherByInverseUVBilinear of every view (the anchor from the
-// UV raster and that view's ScreenAttr, the +-4 dilation for uncovered
-// texels, the 7 x 7 tent-weighted window), the views' contributions summed
-// newest first through the <= 4-ary tree, then Adam on the RGBA texel. The
-// last workgroup advances t.
+constexpr int kTexStage = 1024;  // tent keys of one view staged in LDS per wave
+
+// Per texel (one wave per 8 x 8 texel block): GatherByInverseUVBilinear of
+// every view -- the anchor from the UV raster and that view's ScreenAttr
+// (the +-4 dilation for uncovered texels), the 7 x 7 window in row order.
+// A window pixel can weigh the texel only when its tent key names it (every
+// pixel whose exact weight can be > 0 does): the keys of the union of the
+// wave's windows are staged in LDS when they fit, the candidates collected
+// as window bits, and their g_uv / gradient loaded four at a time, the
+// weights then added in window order. The views' contributions are summed
+// newest first through the <= 4-ary tree, then Adam on the
+// RGBA texel; the last workgroup advances t.
 template <int NV>
-__global__ __launch_bounds__(256) void k_tex_bwd_adam(TexDev d) {
-    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
-    const float t = *d.t;
+__global__ __launch_bounds__(64) void k_tex_bwd_adam(TexDev d) {
+    __shared__ uint32_t lk[kTexStage];
+    const int lane = (int)threadIdx.x;
     const int tw = d.tw, th = d.th;
     const int sw = (int)d.r.g.width, sh = (int)d.r.g.height;
     const size_t npx = (size_t)sw * sh;
-    if (q < (uint32_t)(tw * th)) {
-        const int ty = (int)q / tw, tx = (int)q - ty * tw;
-        // the anchor texel: this one, or the first covered one of the
-        // dilation in row order (the same for every view)
-        float4 rec = d.texel[q];
-        bool cov = __float_as_uint(rec.w) != 0u;
-        for (int ny = -4; ny <= 4 && !cov; ny++) {
-            for (int nx = -4; nx <= 4; nx++) {
-                const int px = tx + nx, py = ty + ny;
-                if (px < 0 || py < 0 || px >= tw || py >= th) {
+    const int bxn = (tw + 7) / 8;
+    const int tx = (int)(blockIdx.x % (uint32_t)bxn) * 8 + (lane & 7);
+    const int ty = (int)(blockIdx.x / (uint32_t)bxn) * 8 + (lane >> 3);
+    const bool valid = tx < tw && ty < th;
+    const uint32_t q = valid ? (uint32_t)(ty * tw + tx) : 0u;
+    const float t = *d.t;
+    // the anchor texel's UV-raster record (own or dilated, precomputed) and
+    // its face's corners
+    const float4 rec = valid ? d.texel[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const bool cov = __float_as_uint(rec.w) != 0u;
+    int32_t c0 = 0, c1 = 0, c2 = 0;
+    if (cov) {
+        const uint32_t f = __float_as_uint(rec.w) - 1u;
+        c0 = d.r.faces[f * 3 + 0];
+        c1 = d.r.faces[f * 3 + 1];
+        c2 = d.r.faces[f * 3 + 2];
+    }
+    float cin[NV][4];  // the views' contributions (constant indices: registers)
+#pragma unroll 1
+    for (int view = 0; view < NV; view++) {
+        int scx = 0, scy = 0;
+        bool act = false;
+        if (cov) {
+            // the view's inverse-UV entry: (sum_k l_k a_k) / (l0 + l1 + l2)
+            const float2* sa = d.sattr + (size_t)view * d.r.n_verts;
+            const float2 a0 = sa[c0], a1 = sa[c1], a2 = sa[c2];
+            const float denom = rec.x + rec.y + rec.z;
+            float nx = 0.f, ny = 0.f;
+            nx += rec.x * a0.x;
+            nx += rec.y * a1.x;
+            nx += rec.z * a2.x;
+            ny += rec.x * a0.y;
+            ny += rec.y * a1.y;
+            ny += rec.z * a2.y;
+            scx = (int)(nx / denom);
+            scy = (int)(ny / denom);
+            act = scx + 3 >= 0 && scx - 3 < sw && scy + 3 >= 0 && scy - 3 < sh;
+        }
+        // the wave's union of windows, clipped to the screen
+        int x0 = act ? max(scx - 3, 0) : 0x7fffffff;
+        int y0 = act ? max(scy - 3, 0) : 0x7fffffff;
+        int x1 = act ? min(scx + 3, sw - 1) : -1;
+        int y1 = act ? min(scy + 3, sh - 1) : -1;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            x0 = min(x0, __shfl_xor(x0, o));
+            y0 = min(y0, __shfl_xor(y0, o));
+            x1 = max(x1, __shfl_xor(x1, o));
+            y1 = max(y1, __shfl_xor(y1, o));
+        }
+        const int bw = x1 - x0 + 1, bh = y1 - y0 + 1;
+        const bool staged = x0 <= x1 && bw * bh <= kTexStage;
+        const uint32_t* keys = d.key + (size_t)view * npx;
+        if (staged) {
+            for (int i = lane; i < bw * bh; i += 64) {
+                const int ry = i / bw;
+                lk[i] = keys[(size_t)(y0 + ry) * sw + (x0 + i - ry * bw)];
+            }
+            __syncthreads();
+        }
+        // candidate window positions (bit (dy + 3) * 7 + dx + 3)
+        uint64_t cm = 0;
+        if (act) {
+#pragma unroll
+            for (int r = 0; r < 7; r++) {
+                const int spy = scy + r - 3;
+                if (spy < 0 || spy >= sh) {
                     continue;
                 }
-                rec = d.texel[(size_t)py * tw + px];
-                if (__float_as_uint(rec.w) != 0u) {
-                    cov = true;
-                    break;
+#pragma unroll
+                for (int i = 0; i < 7; i++) {
+                    const int spx = scx + i - 3;
+                    if (spx < 0 || spx >= sw) {
+                        continue;
+                    }
+                    const uint32_t k = staged ? lk[(spy - y0) * bw + (spx - x0)]
+                                              : keys[(size_t)spy * sw + spx];
+                    const uint32_t kx = k & 0xffffu, ky = k >> 16;
+                    if ((uint32_t)(tx + 1 - (int)kx) <= 1u && (uint32_t)(ty + 1 - (int)ky) <= 1u) {
+                        cm |= 1ull << (r * 7 + i);
+                    }
                 }
             }
         }
-        float in[NV][4];
+        float o4[4] = {0.f, 0.f, 0.f, 0.f};
+        const float2* suv = d.suv + (size_t)view * npx;
+        const float4* gs = d.gs + (size_t)view * npx;
+        while (cm) {
+            // up to four candidates: their loads in flight together, then
+            // the exact weights added in window order
+            size_t sp[4];
+            bool on[4];
+            float2 u4[4];
+            float4 g4[4];
 #pragma unroll
-        for (int vi = 0; vi < NV; vi++) {
-            const uint32_t view = NV - 1 - vi;  // newest first
-            float o[4] = {0.f, 0.f, 0.f, 0.f};
-            if (cov) {
-                const float2 iv = tex_inv_uv(d, view, rec);
-                const int scx = (int)iv.x, scy = (int)iv.y;
-                const float2* suv = d.suv + view * npx;
-                const float4* gs = d.gs + view * npx;
-                for (int dy = -3; dy <= 3; dy++) {
-                    const int spy = scy + dy;
-                    if (spy < 0 || spy >= sh) {
-                        continue;
-                    }
-                    for (int dx = -3; dx <= 3; dx++) {
-                        const int spx = scx + dx;
-                        if (spx < 0 || spx >= sw) {
-                            continue;
-                        }
-                        const size_t sp = (size_t)spy * sw + spx;
-                        const float wgt = tent_weight(suv[sp], tw, th, tx, ty);
-                        if (wgt > 0.f) {
-                            const float4 g = gs[sp];
-                            o[0] += g.x * wgt;
-                            o[1] += g.y * wgt;
-                            o[2] += g.z * wgt;
-                            o[3] += g.w * wgt;
-                        }
-                    }
-                }
+            for (int c = 0; c < 4; c++) {
+                on[c] = cm != 0;
+                const int kb = on[c] ? __builtin_ctzll(cm) : 0;
+                cm &= on[c] ? cm - 1 : cm;
+                const int r = kb / 7, i = kb - r * 7;
+                sp[c] = on[c] ? (size_t)(scy + r - 3) * sw + (size_t)(scx + i - 3) : 0;
+                u4[c] = on[c] ? suv[sp[c]] : make_float2(0.f, 0.f);
+                g4[c] = on[c] ? gs[sp[c]] : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                in[vi][c] = o[c];
+                if (on[c]) {
+                    const float wgt = tent_weight(u4[c], tw, th, tx, ty);
+                    if (wgt > 0.f) {
+                        o4[0] += g4[c].x * wgt;
+                        o4[1] += g4[c].y * wgt;
+                        o4[2] += g4[c].z * wgt;
+                        o4[3] += g4[c].w * wgt;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                cin[k][c] = k == view ? o4[c] : cin[k][c];
+            }
+        }
+        if (staged) {
+            __syncthreads();  // the next view restages lk
+        }
+    }
+    if (valid) {
+        // the views' contributions, newest first
+        float in[NV][4];
+#pragma unroll
+        for (int vi = 0; vi < NV; vi++) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                in[vi][c] = cin[NV - 1 - vi][c];
             }
         }
         float g[4];
@@ -487,14 +613,14 @@ int launch_tex_kernel(const TexDev& d, hipStream_t s, int k) {
             return launch_aa_raster(d.r, s);
         default: {
             const dim3 grid = k == 3 ? dim3(div_up(g.width, 64), g.height)
-                                     : dim3(div_up((uint32_t)(d.tw * d.th), 256));
+                                     : dim3(div_up((uint32_t)d.tw, 8) * div_up((uint32_t)d.th, 8));
             switch (g.n_views) {
 #define DRESSI_NV(N)                                                                      \
     case N:                                                                               \
         if (k == 3) {                                                                     \
             hipLaunchKernelGGL(k_tex_fwd<N>, grid, dim3(64 * N), 0, s, d);                \
         } else {                                                                          \
-            hipLaunchKernelGGL(k_tex_bwd_adam<N>, grid, dim3(256), 0, s, d);              \
+            hipLaunchKernelGGL(k_tex_bwd_adam<N>, grid, dim3(64), 0, s, d);               \
         }                                                                                 \
         break;
                 DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
@@ -719,6 +845,7 @@ int dressi_tex_create(dressi_ctx* ctx, const dressi_tex_desc* desc, dressi_tex_p
     rc = rc ? rc : tex_alloc(p, &d.done, 1);
     rc = rc ? rc : tex_alloc(p, &d.suv, N * npx);
     rc = rc ? rc : tex_alloc(p, &d.gs, N * npx);
+    rc = rc ? rc : tex_alloc(p, &d.key, N * npx);
     rc = rc ? rc : tex_alloc(p, &d.loss, npx);
     rc = rc ? rc : tex_alloc(p, &r.clip, N * V);
     rc = rc ? rc : tex_alloc(p, &r.arecs, std::max(N * F, F));
@@ -827,8 +954,16 @@ int dressi_tex_set_mesh(dressi_tex_plan* p, const float* pos, const float* uv,
     DRESSI_TRY_HIP(hipMemsetAsync(p->bin_mem, 0, p->bin_bytes, s));
     if (int rc = launch_aa_setup(u, s)) return rc;
     if (int rc = launch_aa_raster(u, s)) return rc;
-    hipLaunchKernelGGL(k_tex_texels, dim3(div_up(p->desc.tex_w * p->desc.tex_h, 256)), dim3(256),
-                       0, s, u, (float4*)d.texel);
+    // own records into the screen-gradient buffer (free until the first
+    // iteration), then the anchors
+    const uint32_t T = p->desc.tex_w * p->desc.tex_h;
+    DRESSI_REQUIRE((size_t)T <= (size_t)p->desc.n_views * p->desc.width * p->desc.height,
+                   "texture larger than the screen-gradient scratch");
+    float4* own = d.gs;
+    hipLaunchKernelGGL(k_tex_texels, dim3(div_up(T, 256)), dim3(256), 0, s, u, own);
+    DRESSI_CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_tex_anchor, dim3(div_up(T, 256)), dim3(256), 0, s, (const float4*)own,
+                       (int)p->desc.tex_w, (int)p->desc.tex_h, (float4*)d.texel);
     DRESSI_CHECK_LAUNCH();
     DRESSI_TRY_HIP(hipMemsetAsync(p->bin_mem, 0, p->bin_bytes, s));
     DRESSI_TRY_HIP(hipStreamSynchronize(s));
