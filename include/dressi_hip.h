@@ -174,6 +174,23 @@ int dressi_antialias_bwd_vtx(dressi_ctx* ctx, const float* gy, const float* img,
 int dressi_col_sum(dressi_ctx* ctx, const float* x, uint32_t n_comp,
                    uint32_t width, uint32_t height, float* out);
 
+/* GatherDistGrad (src/core/f_ops.cpp:1248-1358), the exact backward of
+ * RasterizeSoft's dist channel w.r.t. the hard clip positions (RasterizeSoft's
+ * own backward is ColSum of the wide form, f_ops.cpp:1448-1455): for every
+ * covered pixel of rs {S,S} VEC4 with gy.x != 0 (gy {S,S} VEC4), the
+ * argmin-edge gradient of its face's signed distance (envelope theorem)
+ * through the screen -> clip Jacobian. wide != 0: out {max_deg, V} VEC4, the
+ * contribution of face f to vertex u in u's adjacency row holding f; else
+ * out {V,1} VEC4. vtx_faces {V,max_deg} float (-1 pad). As on the
+ * reference's GPU path, radius_px bounds each face's pixel scan by its soft
+ * triangle's bbox: rs must be RasterizeSoft's output for these clips. */
+int dressi_gather_dist_grad(dressi_ctx* ctx, const float* gy, const float* rs,
+                            const float* clip, uint32_t n_verts,
+                            const float* faces, uint32_t n_faces,
+                            const float* vtx_faces, uint32_t max_deg,
+                            float radius_px, int wide, uint32_t width,
+                            uint32_t height, float* out);
+
 /* ---- texture path (C3) ---- */
 /* F::TextureBilinear forward (src/core/f_ops.cpp:2736-2780, BilerpClamp
  * src/core/ibl_math.h:91-115): tex {tw,th} x n_comp (1..4) sampled at

@@ -75,6 +75,7 @@ _SIGS = {
     "dressi_antialias_bwd_vtx": (_I, [_P, _P, _P, _U, _P, _P, _U, _P, _U, _P, _U, _P, _U, _I,
                                       _U, _U, _P]),
     "dressi_col_sum": (_I, [_P, _P, _U, _U, _U, _P]),
+    "dressi_gather_dist_grad": (_I, [_P, _P, _P, _P, _U, _P, _U, _P, _U, _F, _I, _U, _U, _P]),
     "dressi_texture_bilinear": (_I, [_P, _P, _U, _U, _U, _P, _U, _U, _P]),
     "dressi_texture_bilinear_bwd": (_I, [_P, _P, _U, _U, _U, _P, _U, _U, _P, _P]),
     "dressi_screen_attr": (_I, [_P, _P, _U, _U, _U, _P]),

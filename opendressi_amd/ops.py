@@ -222,3 +222,20 @@ def screen_attr(ctx: Context, clip: torch.Tensor, width: int, height: int) -> to
     check(lib.dressi_screen_attr(ctx.handle, _ptr(clip, "clip"), clip.shape[0], width, height,
                                  _ptr(out, "out")))
     return out
+
+
+def gather_dist_grad(ctx: Context, gy: torch.Tensor, rs: torch.Tensor, clip: torch.Tensor,
+                     faces: torch.Tensor, vtx_faces: torch.Tensor, radius_px: float = 3.0,
+                     wide: bool = True) -> torch.Tensor:
+    """GatherDistGrad (src/core/f_ops.cpp:1248-1358): gy, rs (H, W, 4), clip
+    (V, 4), faces (F, 3) float ids, vtx_faces (deg, V) -> (deg, V, 4) when
+    wide, else (V, 4)."""
+    _prep(ctx)
+    h, w = rs.shape[:2]
+    deg, nv = vtx_faces.shape
+    out = torch.empty((deg if wide else 1, nv, 4), dtype=torch.float32, device=rs.device)
+    check(lib.dressi_gather_dist_grad(ctx.handle, _ptr(gy, "gy"), _ptr(rs, "rs"),
+                                      _ptr(clip, "clip"), nv, _ptr(faces, "faces"),
+                                      faces.shape[0], _ptr(vtx_faces, "vtx_faces"), deg,
+                                      radius_px, 1 if wide else 0, w, h, _ptr(out, "out")))
+    return out if wide else out[0]

@@ -2072,3 +2072,102 @@ int or_tex_fit(const float* pos, uint32_t n_verts, const float* uv, const float*
     free(vv);
     return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* GatherDistGrad (exact backward of RasterizeSoft's dist channel)          */
+/* ------------------------------------------------------------------------ */
+
+/* cpu_raster.cpp:153-175 (SignedDistGradToTri): d dist / d s for the argmin
+ * edge with t held fixed (envelope theorem); 0 on the boundary. */
+static void signed_dist_grad(const float p[2], float s[3][2], tri_dist td, float g_s[3][2]) {
+    for (int k = 0; k < 3; k++) {
+        g_s[k][0] = 0.f;
+        g_s[k][1] = 0.f;
+    }
+    const float d = fabsf(td.dist);
+    if (d < K_DIST_EPS) {
+        return;
+    }
+    const int ia = td.edge;
+    const int ib = (td.edge + 1) % 3;
+    const float qx = s[ia][0] + td.t * (s[ib][0] - s[ia][0]);
+    const float qy = s[ia][1] + td.t * (s[ib][1] - s[ia][1]);
+    const float sgn = td.dist >= 0.f ? 1.f : -1.f;
+    const float nx = (p[0] - qx) / d;
+    const float ny = (p[1] - qy) / d;
+    g_s[ia][0] = -sgn * (1.f - td.t) * nx;
+    g_s[ia][1] = -sgn * (1.f - td.t) * ny;
+    g_s[ib][0] = -sgn * td.t * nx;
+    g_s[ib][1] = -sgn * td.t * ny;
+}
+
+/* src/core/f_ops.cpp:1281-1355 (GatherDistGrad CPU kernel): for every
+ * covered pixel (raster order) with gy.x != 0, the dist gradient of its
+ * face's projected corners through the screen -> clip Jacobian (x: 0.5 W /
+ * w, y: 0.5 H / w, w: -(gx 0.5 W c.x + gy 0.5 H c.y) / w^2, z untouched).
+ * wide: the contribution of face f to vertex u lands in u's adjacency row
+ * holding f, out {max_deg, V, 4}; else out {V, 4}. gy, ro {h, w, 4}. */
+void or_gather_dist_grad(const float* gy, const float* ro, const float* clip, uint32_t n_verts,
+                         const float* faces, uint32_t n_faces, const float* vtx_faces,
+                         uint32_t max_deg, int wide, uint32_t w, uint32_t h, float* out) {
+    (void)n_faces;
+    const size_t rows = wide ? max_deg : 1;
+    memset(out, 0, sizeof(float) * 4 * rows * n_verts);
+    const float ws = (float)w, hs = (float)h;
+    for (uint32_t y = 0; y < h; y++) {
+        for (uint32_t x = 0; x < w; x++) {
+            const size_t o = ((size_t)y * w + x) * 4;
+            if (ro[o + 3] < 0.5f) {
+                continue;
+            }
+            const float g = gy[o + 0];
+            if (g == 0.f) {
+                continue;
+            }
+            const uint32_t f = (uint32_t)(int64_t)(ro[o + 1] + 0.5f);
+            uint32_t idx[3];
+            float s[3][2];
+            int valid = 1;
+            for (int k = 0; k < 3; k++) {
+                idx[k] = (uint32_t)(int64_t)(faces[(size_t)f * 3 + k] + 0.5f);
+                const float* c = &clip[(size_t)idx[k] * 4];
+                if (fabsf(c[3]) <= K_W_EPS || c[3] < 0.f) {
+                    valid = 0;
+                    break;
+                }
+                const screen_vert v = project_to_screen(c, w, h);
+                s[k][0] = v.x;
+                s[k][1] = v.y;
+            }
+            if (!valid) {
+                continue;
+            }
+            const float p[2] = {(float)x + 0.5f, (float)y + 0.5f};
+            const tri_dist td = signed_dist_to_tri(p, s);
+            float g_s[3][2];
+            signed_dist_grad(p, s, td, g_s);
+            for (int k = 0; k < 3; k++) {
+                const float gsx = g * g_s[k][0];
+                const float gsy = g * g_s[k][1];
+                if (gsx == 0.f && gsy == 0.f) {
+                    continue;
+                }
+                const float* c = &clip[(size_t)idx[k] * 4];
+                size_t row = 0;
+                if (wide) {
+                    for (uint32_t d = 0; d < max_deg; d++) {
+                        const float fv = vtx_faces[(size_t)d * n_verts + idx[k]];
+                        if (fv >= -0.5f && (uint32_t)(int64_t)(fv + 0.5f) == f) {
+                            row = d;
+                            break;
+                        }
+                    }
+                }
+                float* dst = &out[(row * n_verts + idx[k]) * 4];
+                dst[0] += gsx * 0.5f * ws / c[3];
+                dst[1] += gsy * 0.5f * hs / c[3];
+                dst[3] += -(gsx * 0.5f * ws * c[0] + gsy * 0.5f * hs * c[1]) / (c[3] * c[3]);
+            }
+        }
+    }
+}

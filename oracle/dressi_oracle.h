@@ -167,6 +167,12 @@ int or_tex_fit(const float* pos, uint32_t n_verts, const float* uv, const float*
                float* out_v, float* out_t, float* out_loss, float* out_grad0, float* out_pred0,
                float* out_target0, float* out_lossimg0, float* out_uv0, float* out_invuv0);
 
+/* src/core/f_ops.cpp:1281-1355 (GatherDistGrad): gy, ro {h,w,4}; out wide
+ * ? {max_deg, V, 4} : {V, 4} */
+void or_gather_dist_grad(const float* gy, const float* ro, const float* clip, uint32_t n_verts,
+                         const float* faces, uint32_t n_faces, const float* vtx_faces,
+                         uint32_t max_deg, int wide, uint32_t w, uint32_t h, float* out);
+
 #ifdef __cplusplus
 }
 #endif

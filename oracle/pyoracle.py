@@ -326,6 +326,17 @@ class Oracle(_Lib):
         self.fn("col_sum")(_fp(x), _U32(nc), _U32(w), _U32(h), _fp(out))
         return out
 
+    def gather_dist_grad(self, gy, rs, clip, faces, vtx_faces, wide=True):
+        """gy, rs {h, w, 4}; -> wide {deg, V, 4} or {V, 4}."""
+        gy, rs, clip, faces, vf = (_f32(a) for a in (gy, rs, clip, faces, vtx_faces))
+        h, w = rs.shape[:2]
+        deg, nv = vf.shape
+        out = np.zeros((deg if wide else 1, nv, 4), np.float32)
+        self.fn("gather_dist_grad")(_fp(gy), _fp(rs), _fp(clip), _U32(nv), _fp(faces),
+                                    _U32(faces.shape[0]), _fp(vf), _U32(deg),
+                                    C.c_int(1 if wide else 0), _U32(w), _U32(h), _fp(out))
+        return out if wide else out[0]
+
     def texture_bilinear(self, tex, uv):
         """tex {th, tw, nc}, uv {..., 2} -> {..., nc}."""
         tex, uv = _f32(tex), _f32(uv)
@@ -442,6 +453,21 @@ def _ref_antialias_bwd(self, gy, img, tri, clip, faces, vtx_faces, seed, n_sampl
     return g_img, wide, g_vtx
 
 
+def _ref_rasterize_soft_bwd(self, soft_clip, face_id, faces_soft, hard_clip, faces_tex,
+                            vtx_faces, w, h, radius, gy):
+    """(wide {deg, V, 4}, g_clip {V, 4}) of RasterizeSoft's backward."""
+    sc, fi, fs, hc, ft, vf = (_f32(a) for a in (soft_clip, face_id, faces_soft, hard_clip,
+                                                 faces_tex, vtx_faces))
+    gy = _f32(gy)
+    deg, nv = vf.shape
+    wide = np.zeros((deg, nv, 4), np.float32)
+    g = np.zeros((nv, 4), np.float32)
+    self._call("rasterize_soft_bwd", _fp(sc), _fp(fi), _fp(fs), _fp(hc), _U32(nv), _fp(ft),
+               _fp(vf), _U32(deg), _U32(ft.shape[0]), _U32(w), _U32(h), C.c_float(radius),
+               _fp(gy), _fp(wide), _fp(g))
+    return wide, g
+
+
 def _ref_texture_bilinear(self, tex, uv):
     """tex {th, tw, nc}, uv {uh, uw, 2} -> {uh, uw, nc}."""
     tex, uv = _f32(tex), _f32(uv)
@@ -470,3 +496,4 @@ def have_reference() -> bool:
 Reference.antialias = _ref_antialias
 Reference.antialias_bwd = _ref_antialias_bwd
 Reference.texture_bilinear = _ref_texture_bilinear
+Reference.rasterize_soft_bwd = _ref_rasterize_soft_bwd

@@ -135,6 +135,43 @@ int refh_rasterize_soft(const float* soft_clip, const float* face_id,
     });
 }
 
+// RasterizeSoft's backward w.r.t. the hard clip positions (f_ops.cpp:
+// 1448-1455): ColSum(GatherDistGrad(gy, y, ..., wide)) for gy {w,h} VEC4
+// (only the dist channel is read); out_wide {max_deg, V, 4} the gather's
+// partials, out_vtx {V, 4} their ColSum.
+int refh_rasterize_soft_bwd(const float* soft_clip, const float* face_id,
+                            const float* faces_soft, const float* hard_clip,
+                            uint32_t n_verts, const float* faces_tex,
+                            const float* vtx_faces, uint32_t max_deg,
+                            uint32_t n_faces, uint32_t w, uint32_t h, float radius,
+                            const float* gy, float* out_wide, float* out_vtx) {
+    return Guard([&] {
+        Variable sc(VEC4, {3 * n_faces, 1});
+        Variable fid(FLOAT, {3 * n_faces, 1});
+        Variable fs(IVEC3, {n_faces, 1});
+        Variable hc(VEC4, {n_verts, 1});
+        Variable ft(VEC3, {n_faces, 1});
+        Variable vf(FLOAT, {n_verts, max_deg});
+        Variable vgy(VEC4, {w, h});
+        Variable y = F::RasterizeSoft(sc, fid, fs, hc, ft, vf, {w, h}, radius);
+        Variable g = y.getCreator().buildBwd(vgy, 3);
+        CpuEvaluator ev;
+        ev.bind(sc, Tensor(VEC4, {3 * n_faces, 1}, soft_clip));
+        ev.bind(fid, Tensor(FLOAT, {3 * n_faces, 1}, face_id));
+        ev.bind(fs, Tensor(IVEC3, {n_faces, 1}, faces_soft));
+        ev.bind(hc, Tensor(VEC4, {n_verts, 1}, hard_clip));
+        ev.bind(ft, Tensor(VEC3, {n_faces, 1}, faces_tex));
+        ev.bind(vf, Tensor(FLOAT, {n_verts, max_deg}, vtx_faces));
+        ev.bind(vgy, Tensor(VEC4, {w, h}, gy));
+        if (out_vtx) {
+            CopyOut(ev.eval(g), out_vtx);
+        }
+        if (out_wide) {
+            CopyOut(ev.eval(g.getCreator().getInputVars()[0]), out_wide);
+        }
+    });
+}
+
 // F::Rasterize (hard, perspective-correct attribute interpolation)
 int refh_rasterize(const float* clip, uint32_t n_verts, const float* attr,
                    uint32_t n_comp, const float* faces, uint32_t n_faces,

@@ -5,6 +5,7 @@ and stored next to the outputs, so the fixtures are self-contained data.
 
     python tests/golden/make_golden.py            # every fixture
     python tests/golden/make_golden.py texture    # the texture path's only
+    python tests/golden/make_golden.py dist       # GatherDistGrad's only
 
 Each .npz holds `in_*` arrays (inputs) and `out_*` arrays (reference outputs).
 """
@@ -223,6 +224,32 @@ def tex_fit_fixture(o, r, name, stacks, slices, screen, tex, views, sets, iters,
     print("wrote", name, {k: v.shape for k, v in arrs.items()})
 
 
+def ds_fixtures(o, r):
+    """GatherDistGrad (RasterizeSoft's backward w.r.t. the hard clips) on an
+    icosphere L2 at 48^2 for three cameras, gy with some zero pixels."""
+    rng = np.random.default_rng(21)
+    pos, faces = o.icosphere(2)
+    proj = o.perspective_vk(45.0 * 3.14159265 / 180.0, 1.0, 0.1, 10.0)
+    s = 48
+    nf = len(faces)
+    fid = np.repeat(np.arange(nf, dtype=np.float32), 3)[:, None]
+    fs = np.arange(3 * nf, dtype=np.float32).reshape(nf, 3)
+    vf = r.vertex_faces_tex(faces, len(pos))
+    arrs = dict(in_faces=faces, in_vf=vf, in_cfg=np.array([s, 3.0], np.float64))
+    for i in range(3):
+        eye = [rng.standard_normal() * 0.5, rng.standard_normal() * 0.5, 2.6 + 0.4 * i]
+        clip = o.transform_to_clip(pos, o.mat4_mul(proj, o.look_at(eye)))
+        soft = r.soft_clip(clip, faces, s, s, 3.0)
+        rs = r.rasterize_soft(soft, fid, fs, clip, faces, s, s, 3.0, vtx_faces=vf)
+        gy = rng.standard_normal((s, s, 4)).astype(np.float32)
+        gy[rng.random((s, s)) < 0.2, 0] = 0.0
+        wide, g = r.rasterize_soft_bwd(soft, fid, fs, clip, faces, vf, s, s, 3.0, gy)
+        arrs.update({f"in_clip{i}": clip, f"in_rs{i}": rs, f"in_gy{i}": gy,
+                     f"out_wide{i}": wide, f"out_g{i}": g})
+    np.savez_compressed(os.path.join(OUT, "ds_unit.npz"), **arrs)
+    print("wrote ds_unit.npz", len(arrs), "arrays")
+
+
 def texture_main(o, r):
     tex_fixtures(o, r)
     tex_fit_fixture(o, r, "tex_uvs16_64px_3view_3it.npz", 16, 8, 64, 32, 3, 2, 3, 5, True)
@@ -236,6 +263,10 @@ def main():
     if sys.argv[1:] == ["texture"]:
         texture_main(o, r)
         return
+    if sys.argv[1:] == ["dist"]:
+        ds_fixtures(o, r)
+        return
+    ds_fixtures(o, r)
     texture_main(o, r)
     op_fixtures(o, r)
     aa_fixtures(o, r)
