@@ -191,6 +191,66 @@ int dressi_gather_dist_grad(dressi_ctx* ctx, const float* gy, const float* rs,
                             float radius_px, int wide, uint32_t width,
                             uint32_t height, float* out);
 
+/* ---- split-sum IBL ops (C5) ---- */
+/* Maps are equirectangular {w,h} x n_comp (1..4) float images, row 0 at the
+ * +Y pole; directions are {dw,dh} VEC3 (any length; zero-length samples 0).
+ * Texel-centre directions follow DirFromEquirectUv (src/core/ibl_math.h:
+ * 48-54) with the C library's sinf / cosf, so the dense convolutions match
+ * the reference's CPU sums bit for bit; per-direction uv use atan2 / acos
+ * rounded once (the reference's float library calls can differ by an ulp). */
+/* F::EquirectSample (src/core/f_ops.cpp:2921-2964, BilerpWrap
+ * src/core/ibl_math.h:58-89): u wraps, v clamps -> out {dw,dh} x n_comp. */
+int dressi_equirect_sample(dressi_ctx* ctx, const float* map, uint32_t mw,
+                           uint32_t mh, uint32_t n_comp, const float* dir,
+                           uint32_t dw, uint32_t dh, float* out);
+/* Its VJP w.r.t. the map (EquirectSampleBwd + TileSum, f_ops.cpp:2786-2919):
+ * gy {dw,dh} x n_comp -> out {mw,mh} x n_comp, summed in 64-bit fixed point
+ * (exact, deterministic). */
+int dressi_equirect_sample_bwd(dressi_ctx* ctx, const float* gy,
+                               uint32_t n_comp, const float* dir, uint32_t dw,
+                               uint32_t dh, uint32_t mw, uint32_t mh,
+                               float* out);
+/* F::AvgPool2x2 = Reduce2x2Sum * 0.25 (f_ops.cpp:996-1033, 3411-3415):
+ * x {w,h} -> out {ceil(w/2), ceil(h/2)}; _bwd: gy {ceil(w/2),ceil(h/2)} ->
+ * out {w,h} (UpsampleNearest2x of gy * 0.25, f_ops.cpp:958-994). */
+int dressi_avg_pool2x2(dressi_ctx* ctx, const float* x, uint32_t w, uint32_t h,
+                       uint32_t n_comp, float* out);
+int dressi_avg_pool2x2_bwd(dressi_ctx* ctx, const float* gy, uint32_t w,
+                           uint32_t h, uint32_t n_comp, float* out);
+/* F::IrradianceConv (f_ops.cpp:3006-3087): env {sw,sh} -> out {ow,oh};
+ * _bwd: its transpose IrradianceConvBwd (f_ops.cpp:2970-3004),
+ * gy {ow,oh} -> out {sw,sh}. */
+int dressi_irradiance_conv(dressi_ctx* ctx, const float* env, uint32_t sw,
+                           uint32_t sh, uint32_t n_comp, uint32_t ow,
+                           uint32_t oh, float* out);
+int dressi_irradiance_conv_bwd(dressi_ctx* ctx, const float* gy, uint32_t ow,
+                               uint32_t oh, uint32_t n_comp, uint32_t sw,
+                               uint32_t sh, float* out);
+/* F::PrefilterConv at roughness r (alpha = max(r, 0.045)^2): its normaliser
+ * PrefilterConvNorm (f_ops.cpp:3166-3205) -> norm {ow,oh} FLOAT; the
+ * convolution (f_ops.cpp:3264-3348) env {sw,sh} -> out {ow,oh}; its
+ * transpose PrefilterConvBwd (f_ops.cpp:3207-3262) gy {ow,oh} -> out {sw,sh}. */
+int dressi_prefilter_conv_norm(dressi_ctx* ctx, uint32_t ow, uint32_t oh,
+                               uint32_t sw, uint32_t sh, float roughness,
+                               float* norm);
+int dressi_prefilter_conv(dressi_ctx* ctx, const float* env, uint32_t sw,
+                          uint32_t sh, uint32_t n_comp, uint32_t ow,
+                          uint32_t oh, float roughness, const float* norm,
+                          float* out);
+int dressi_prefilter_conv_bwd(dressi_ctx* ctx, const float* gy, uint32_t ow,
+                              uint32_t oh, uint32_t n_comp, uint32_t sw,
+                              uint32_t sh, float roughness, const float* norm,
+                              float* out);
+/* F::PrefilterEnv (f_ops.cpp:3089-3157): GGX importance-sampled prefilter
+ * with n_samples Hammersley samples, forward only -> out {ow,oh}. */
+int dressi_prefilter_env(dressi_ctx* ctx, const float* env, uint32_t sw,
+                         uint32_t sh, uint32_t n_comp, uint32_t ow,
+                         uint32_t oh, float roughness, uint32_t n_samples,
+                         float* out);
+/* F::BrdfIntegrationLut (f_ops.cpp:3350-3409): out {w,h} VEC2 (A, B). */
+int dressi_brdf_lut(dressi_ctx* ctx, uint32_t w, uint32_t h,
+                    uint32_t n_samples, float* out);
+
 /* ---- texture path (C3) ---- */
 /* F::TextureBilinear forward (src/core/f_ops.cpp:2736-2780, BilerpClamp
  * src/core/ibl_math.h:91-115): tex {tw,th} x n_comp (1..4) sampled at

@@ -76,6 +76,17 @@ _SIGS = {
                                       _U, _U, _P]),
     "dressi_col_sum": (_I, [_P, _P, _U, _U, _U, _P]),
     "dressi_gather_dist_grad": (_I, [_P, _P, _P, _P, _U, _P, _U, _P, _U, _F, _I, _U, _U, _P]),
+    "dressi_equirect_sample": (_I, [_P, _P, _U, _U, _U, _P, _U, _U, _P]),
+    "dressi_equirect_sample_bwd": (_I, [_P, _P, _U, _P, _U, _U, _U, _U, _P]),
+    "dressi_avg_pool2x2": (_I, [_P, _P, _U, _U, _U, _P]),
+    "dressi_avg_pool2x2_bwd": (_I, [_P, _P, _U, _U, _U, _P]),
+    "dressi_irradiance_conv": (_I, [_P, _P, _U, _U, _U, _U, _U, _P]),
+    "dressi_irradiance_conv_bwd": (_I, [_P, _P, _U, _U, _U, _U, _U, _P]),
+    "dressi_prefilter_conv_norm": (_I, [_P, _U, _U, _U, _U, _F, _P]),
+    "dressi_prefilter_conv": (_I, [_P, _P, _U, _U, _U, _U, _U, _F, _P, _P]),
+    "dressi_prefilter_conv_bwd": (_I, [_P, _P, _U, _U, _U, _U, _U, _F, _P, _P]),
+    "dressi_prefilter_env": (_I, [_P, _P, _U, _U, _U, _U, _U, _F, _U, _P]),
+    "dressi_brdf_lut": (_I, [_P, _U, _U, _U, _P]),
     "dressi_texture_bilinear": (_I, [_P, _P, _U, _U, _U, _P, _U, _U, _P]),
     "dressi_texture_bilinear_bwd": (_I, [_P, _P, _U, _U, _U, _P, _U, _U, _P, _P]),
     "dressi_screen_attr": (_I, [_P, _P, _U, _U, _U, _P]),

@@ -239,3 +239,128 @@ def gather_dist_grad(ctx: Context, gy: torch.Tensor, rs: torch.Tensor, clip: tor
                                       faces.shape[0], _ptr(vtx_faces, "vtx_faces"), deg,
                                       radius_px, 1 if wide else 0, w, h, _ptr(out, "out")))
     return out if wide else out[0]
+
+
+# ---- split-sum IBL ops (maps are (H, W, C) equirect images) ----------------
+
+def _map_nc(m: torch.Tensor) -> int:
+    return 1 if m.dim() == 2 else m.shape[2]
+
+
+def equirect_sample(ctx: Context, map_: torch.Tensor, dirs: torch.Tensor) -> torch.Tensor:
+    """F::EquirectSample (src/core/f_ops.cpp:2921-2964): map (mh, mw, C) at
+    dirs (H, W, 3) -> (H, W, C)."""
+    _prep(ctx)
+    mh, mw, nc = map_.shape[0], map_.shape[1], _map_nc(map_)
+    h, w = dirs.shape[0], dirs.shape[1]
+    out = torch.empty((h, w, nc), dtype=torch.float32, device=map_.device)
+    check(lib.dressi_equirect_sample(ctx.handle, _ptr(map_, "map"), mw, mh, nc,
+                                     _ptr(dirs, "dirs"), w, h, _ptr(out, "out")))
+    return out
+
+
+def equirect_sample_bwd(ctx: Context, gy: torch.Tensor, dirs: torch.Tensor, mw: int,
+                        mh: int) -> torch.Tensor:
+    """EquirectSample's VJP w.r.t. the map (f_ops.cpp:2786-2919) -> (mh, mw, C)."""
+    _prep(ctx)
+    nc = _map_nc(gy)
+    h, w = dirs.shape[0], dirs.shape[1]
+    out = torch.empty((mh, mw, nc), dtype=torch.float32, device=gy.device)
+    check(lib.dressi_equirect_sample_bwd(ctx.handle, _ptr(gy, "gy"), nc, _ptr(dirs, "dirs"), w,
+                                         h, mw, mh, _ptr(out, "out")))
+    return out
+
+
+def avg_pool2x2(ctx: Context, x: torch.Tensor) -> torch.Tensor:
+    """F::AvgPool2x2 (f_ops.cpp:3411-3415): (h, w, C) -> (ceil(h/2), ceil(w/2), C)."""
+    _prep(ctx)
+    h, w, nc = x.shape[0], x.shape[1], _map_nc(x)
+    out = torch.empty(((h + 1) // 2, (w + 1) // 2, nc), dtype=torch.float32, device=x.device)
+    check(lib.dressi_avg_pool2x2(ctx.handle, _ptr(x, "x"), w, h, nc, _ptr(out, "out")))
+    return out
+
+
+def avg_pool2x2_bwd(ctx: Context, gy: torch.Tensor, w: int, h: int) -> torch.Tensor:
+    """AvgPool2x2's VJP (UpsampleNearest2x of gy * 0.25) -> (h, w, C)."""
+    _prep(ctx)
+    nc = _map_nc(gy)
+    out = torch.empty((h, w, nc), dtype=torch.float32, device=gy.device)
+    check(lib.dressi_avg_pool2x2_bwd(ctx.handle, _ptr(gy, "gy"), w, h, nc, _ptr(out, "out")))
+    return out
+
+
+def irradiance_conv(ctx: Context, env: torch.Tensor, ow: int, oh: int) -> torch.Tensor:
+    """F::IrradianceConv (f_ops.cpp:3006-3087) -> (oh, ow, C)."""
+    _prep(ctx)
+    sh, sw, nc = env.shape[0], env.shape[1], _map_nc(env)
+    out = torch.empty((oh, ow, nc), dtype=torch.float32, device=env.device)
+    check(lib.dressi_irradiance_conv(ctx.handle, _ptr(env, "env"), sw, sh, nc, ow, oh,
+                                     _ptr(out, "out")))
+    return out
+
+
+def irradiance_conv_bwd(ctx: Context, gy: torch.Tensor, sw: int, sh: int) -> torch.Tensor:
+    """IrradianceConvBwd (f_ops.cpp:2970-3004): gy (oh, ow, C) -> (sh, sw, C)."""
+    _prep(ctx)
+    oh, ow, nc = gy.shape[0], gy.shape[1], _map_nc(gy)
+    out = torch.empty((sh, sw, nc), dtype=torch.float32, device=gy.device)
+    check(lib.dressi_irradiance_conv_bwd(ctx.handle, _ptr(gy, "gy"), ow, oh, nc, sw, sh,
+                                         _ptr(out, "out")))
+    return out
+
+
+def prefilter_conv_norm(ctx: Context, ow: int, oh: int, sw: int, sh: int, roughness: float,
+                        device=None) -> torch.Tensor:
+    """PrefilterConvNorm (f_ops.cpp:3166-3205) -> (oh, ow)."""
+    _prep(ctx)
+    out = torch.empty((oh, ow), dtype=torch.float32, device=device or f"cuda:{ctx.device}")
+    check(lib.dressi_prefilter_conv_norm(ctx.handle, ow, oh, sw, sh, float(roughness),
+                                         _ptr(out, "norm")))
+    return out
+
+
+def prefilter_conv(ctx: Context, env: torch.Tensor, ow: int, oh: int, roughness: float,
+                   norm: torch.Tensor | None = None) -> torch.Tensor:
+    """F::PrefilterConv (f_ops.cpp:3264-3348) -> (oh, ow, C); `norm` from
+    prefilter_conv_norm (computed when None)."""
+    sh, sw, nc = env.shape[0], env.shape[1], _map_nc(env)
+    if norm is None:
+        norm = prefilter_conv_norm(ctx, ow, oh, sw, sh, roughness, env.device)
+    _prep(ctx)
+    out = torch.empty((oh, ow, nc), dtype=torch.float32, device=env.device)
+    check(lib.dressi_prefilter_conv(ctx.handle, _ptr(env, "env"), sw, sh, nc, ow, oh,
+                                    float(roughness), _ptr(norm, "norm"), _ptr(out, "out")))
+    return out
+
+
+def prefilter_conv_bwd(ctx: Context, gy: torch.Tensor, sw: int, sh: int, roughness: float,
+                       norm: torch.Tensor | None = None) -> torch.Tensor:
+    """PrefilterConvBwd (f_ops.cpp:3207-3262): gy (oh, ow, C) -> (sh, sw, C)."""
+    oh, ow, nc = gy.shape[0], gy.shape[1], _map_nc(gy)
+    if norm is None:
+        norm = prefilter_conv_norm(ctx, ow, oh, sw, sh, roughness, gy.device)
+    _prep(ctx)
+    out = torch.empty((sh, sw, nc), dtype=torch.float32, device=gy.device)
+    check(lib.dressi_prefilter_conv_bwd(ctx.handle, _ptr(gy, "gy"), ow, oh, nc, sw, sh,
+                                        float(roughness), _ptr(norm, "norm"), _ptr(out, "out")))
+    return out
+
+
+def prefilter_env(ctx: Context, env: torch.Tensor, ow: int, oh: int, roughness: float,
+                  n_samples: int = 256) -> torch.Tensor:
+    """F::PrefilterEnv (f_ops.cpp:3089-3157) -> (oh, ow, C)."""
+    _prep(ctx)
+    sh, sw, nc = env.shape[0], env.shape[1], _map_nc(env)
+    out = torch.empty((oh, ow, nc), dtype=torch.float32, device=env.device)
+    check(lib.dressi_prefilter_env(ctx.handle, _ptr(env, "env"), sw, sh, nc, ow, oh,
+                                   float(roughness), n_samples, _ptr(out, "out")))
+    return out
+
+
+def brdf_lut(ctx: Context, w: int = 256, h: int = 256, n_samples: int = 512,
+             device=None) -> torch.Tensor:
+    """F::BrdfIntegrationLut (f_ops.cpp:3350-3409) -> (h, w, 2)."""
+    _prep(ctx)
+    out = torch.empty((h, w, 2), dtype=torch.float32, device=device or f"cuda:{ctx.device}")
+    check(lib.dressi_brdf_lut(ctx.handle, w, h, n_samples, _ptr(out, "out")))
+    return out

@@ -173,6 +173,41 @@ void or_gather_dist_grad(const float* gy, const float* ro, const float* clip, ui
                          const float* faces, uint32_t n_faces, const float* vtx_faces,
                          uint32_t max_deg, int wide, uint32_t w, uint32_t h, float* out);
 
+/* ---- PBR / IBL (pbr_oracle.c) ------------------------------------------- */
+/* EquirectSample (src/core/f_ops.cpp:2921-2964) map {mw,mh} x n at dir {dw,dh}
+ * VEC3 -> out {dw,dh} x n; with gy {dw,dh} x n instead the map VJP
+ * (EquirectSampleBwd + TileSum, f_ops.cpp:2786-2919) -> out {mw,mh} x n */
+int or_equirect_sample(const float* map, uint32_t mw, uint32_t mh, uint32_t n, const float* dir,
+                       uint32_t dw, uint32_t dh, const float* gy, float* out);
+/* AvgPool2x2 (f_ops.cpp:3411-3415); with gy its VJP -> out {w,h} x n */
+int or_avg_pool2x2(const float* x, uint32_t w, uint32_t h, uint32_t n, const float* gy,
+                   float* out);
+/* IrradianceConv (f_ops.cpp:3006-3087) env {sw,sh} -> {ow,oh}; with gy
+ * IrradianceConvBwd (f_ops.cpp:2970-3004) -> {sw,sh} */
+int or_irradiance_conv(const float* env, uint32_t sw, uint32_t sh, uint32_t n, uint32_t ow,
+                       uint32_t oh, const float* gy, float* out);
+/* PrefilterConv (+ PrefilterConvNorm) (f_ops.cpp:3166-3348); with gy
+ * PrefilterConvBwd (f_ops.cpp:3207-3262) */
+int or_prefilter_conv(const float* env, uint32_t sw, uint32_t sh, uint32_t n, uint32_t ow,
+                      uint32_t oh, float roughness, const float* gy, float* out);
+/* PrefilterEnv (f_ops.cpp:3089-3157), forward only */
+int or_prefilter_env(const float* env, uint32_t sw, uint32_t sh, uint32_t n, uint32_t ow,
+                     uint32_t oh, float roughness, uint32_t n_samples, float* out);
+/* BrdfIntegrationLut (f_ops.cpp:3350-3409): {w,h} VEC2 */
+int or_brdf_lut(uint32_t w, uint32_t h, uint32_t n_samples, float* out);
+/* the C5 split-sum PBR/IBL material + environment fit
+ * (examples/common/pbr_graph.cpp, src/core/ibl.cpp; in-graph Adam on albedo,
+ * mr and env, L1 loss on the Reinhard-mapped image) */
+int or_pbr_fit(const float* pos, const float* normal, uint32_t n_verts, const float* uv,
+               const float* faces, uint32_t n_faces, const float* mvps, const float* frames,
+               const float* light, uint32_t n_views, uint32_t screen_px, uint32_t tex_w,
+               uint32_t tex_h, uint32_t env_w, uint32_t env_h, uint32_t levels,
+               const float* gt_albedo, const float* gt_mr, const float* gt_env,
+               const float* albedo0, const float* mr0, const float* env0, float lr,
+               uint32_t iters, float* out_albedo, float* out_mr, float* out_env, float* out_loss,
+               float* out_g_albedo0, float* out_g_mr0, float* out_g_env0, float* out_pred0,
+               float* out_target0, float* out_mask0);
+
 #ifdef __cplusplus
 }
 #endif

@@ -201,6 +201,83 @@ class _Lib:
                    _fp(g("invuv0")))
         return r
 
+    # ---- PBR / IBL ops ----------------------------------------------------
+    def equirect_sample(self, map_, dirs, gy=None):
+        """map {mh, mw, n}, dirs {dh, dw, 3}; with gy {dh, dw, n} the map VJP."""
+        map_, dirs = _f32(map_), _f32(dirs)
+        mh, mw, n = map_.shape
+        dh, dw = dirs.shape[:2]
+        if gy is None:
+            out = np.zeros((dh, dw, n), np.float32)
+        else:
+            gy = _f32(gy)
+            out = np.zeros((mh, mw, n), np.float32)
+        self._call("equirect_sample", _fp(map_), _U32(mw), _U32(mh), _U32(n), _fp(dirs),
+                   _U32(dw), _U32(dh), _fp(gy), _fp(out))
+        return out
+
+    def avg_pool2x2(self, x, gy=None):
+        x = _f32(x)
+        h, w, n = x.shape
+        out = np.zeros(((h + 1) // 2, (w + 1) // 2, n) if gy is None else (h, w, n), np.float32)
+        self._call("avg_pool2x2", _fp(x), _U32(w), _U32(h), _U32(n),
+                   _fp(None if gy is None else _f32(gy)), _fp(out))
+        return out
+
+    def irradiance_conv(self, env, ow, oh, gy=None):
+        env = _f32(env)
+        sh, sw, n = env.shape
+        out = np.zeros((oh, ow, n) if gy is None else (sh, sw, n), np.float32)
+        self._call("irradiance_conv", _fp(env), _U32(sw), _U32(sh), _U32(n), _U32(ow), _U32(oh),
+                   _fp(None if gy is None else _f32(gy)), _fp(out))
+        return out
+
+    def prefilter_conv(self, env, ow, oh, roughness, gy=None):
+        env = _f32(env)
+        sh, sw, n = env.shape
+        out = np.zeros((oh, ow, n) if gy is None else (sh, sw, n), np.float32)
+        self._call("prefilter_conv", _fp(env), _U32(sw), _U32(sh), _U32(n), _U32(ow), _U32(oh),
+                   C.c_float(roughness), _fp(None if gy is None else _f32(gy)), _fp(out))
+        return out
+
+    def prefilter_env(self, env, ow, oh, roughness, n_samples):
+        env = _f32(env)
+        sh, sw, n = env.shape
+        out = np.zeros((oh, ow, n), np.float32)
+        self._call("prefilter_env", _fp(env), _U32(sw), _U32(sh), _U32(n), _U32(ow), _U32(oh),
+                   C.c_float(roughness), _U32(n_samples), _fp(out))
+        return out
+
+    def brdf_lut(self, w, h, n_samples):
+        out = np.zeros((h, w, 2), np.float32)
+        self._call("brdf_lut", _U32(w), _U32(h), _U32(n_samples), _fp(out))
+        return out
+
+    def pbr_fit(self, scene, iters=1, want_images=True):
+        """The C5 PBR/IBL fit on a scene dict (pos, normal, uv, faces, mvps
+        {N,16}, frames {N,12}, light {6}, screen, levels, lr, gt_albedo,
+        gt_mr {th,tw,3}, gt_env {eh,ew,3}, albedo0, mr0, env0)."""
+        a = {k: (_f32(v) if isinstance(v, np.ndarray) else v) for k, v in scene.items()}
+        n = a["mvps"].shape[0]
+        th, tw = a["gt_albedo"].shape[:2]
+        eh, ew = a["gt_env"].shape[:2]
+        s = a["screen"]
+        z = lambda *sh: np.zeros(sh, np.float32)
+        r = dict(albedo=z(th, tw, 3), mr=z(th, tw, 3), env=z(eh, ew, 3), loss=z(max(iters, 1)),
+                 g_albedo0=z(th, tw, 3), g_mr0=z(th, tw, 3), g_env0=z(eh, ew, 3))
+        if want_images:
+            r.update(pred0=z(n, s, s, 3), target0=z(n, s, s, 3), mask0=z(n, s, s))
+        g = r.get
+        self._call("pbr_fit", _fp(a["pos"]), _fp(a["normal"]), _U32(a["pos"].shape[0]),
+                   _fp(a["uv"]), _fp(a["faces"]), _U32(a["faces"].shape[0]), _fp(a["mvps"]),
+                   _fp(a["frames"]), _fp(a["light"]), _U32(n), _U32(s), _U32(tw), _U32(th),
+                   _U32(ew), _U32(eh), _U32(a["levels"]), _fp(a["gt_albedo"]), _fp(a["gt_mr"]),
+                   _fp(a["gt_env"]), _fp(a["albedo0"]), _fp(a["mr0"]), _fp(a["env0"]),
+                   C.c_float(a["lr"]), _U32(iters), _fp(r["albedo"]), _fp(r["mr"]), _fp(r["env"]),
+                   _fp(r["loss"]), _fp(r["g_albedo0"]), _fp(r["g_mr0"]), _fp(r["g_env0"]),
+                   _fp(g("pred0")), _fp(g("target0")), _fp(g("mask0")))
+        return r
+
 
 class Oracle(_Lib):
     """The C restatement (oracle/dressi_oracle.c)."""
@@ -213,8 +290,14 @@ class Oracle(_Lib):
         self.fn("wang_hash").restype = C.c_uint32
         self.fn("vertex_faces_tex").restype = C.c_uint32
 
+    # functions of the restatement that return a status (the rest are void)
+    _STATUS = frozenset(("equirect_sample", "avg_pool2x2", "irradiance_conv", "prefilter_conv",
+                         "prefilter_env", "brdf_lut", "pbr_fit"))
+
     def _call(self, name, *args):
-        self.fn(name)(*args)
+        rc = self.fn(name)(*args)
+        if name in self._STATUS and rc != 0:
+            raise RuntimeError(f"or_{name} failed ({rc})")
 
     def rasterize_soft(self, soft_clip, face_id, faces_soft, hard_clip, faces_tex, w, h, radius,
                        prev=None, vtx_faces=None):

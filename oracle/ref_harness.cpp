@@ -23,7 +23,9 @@
 #include "dressi/dressi.h"
 #include "dressi/mesh_utils.h"
 
+#include "dressi/ibl.h"
 #include "geometry_utils.h"
+#include "pbr_graph.h"
 
 using namespace dressi;
 
@@ -973,6 +975,368 @@ int refh_tex_fit(const float* pos, uint32_t n_verts, const float* uv, const floa
         CopyOut(t_m, out_m);
         CopyOut(t_v, out_v);
         CopyOut(t_t, out_t);
+    });
+}
+
+// ---------------------------------------------------------------------------
+// PBR / IBL ops (src/core/f_ops.cpp:2785-3415, src/core/ibl.cpp) and the C5
+// material + environment fit (examples/common/pbr_graph.cpp)
+// ---------------------------------------------------------------------------
+
+}  // extern "C"
+
+namespace {
+
+// VJP of `y = op(x)` w.r.t. x for the image loss y * gy (seed 1 per pixel
+// gives y the gradient gy exactly).
+template <typename Op>
+CpuTensor VjpOf(Op op, VType xt, ImgSize xs, const float* x, VType yt, ImgSize ys,
+                const float* gy) {
+    Variable xv(xt, xs);
+    Variable g(yt, ys);
+    Variable loss = op(xv) * g;
+    Variable x_mut = xv;
+    x_mut.setRequiresGradRecursively();
+    auto [leaves, gxs] = BuildBackward(loss);
+    DRESSI_CHECK(leaves.size() == 1 && leaves[0] == xv, "expected one leaf");
+    CpuEvaluator ev;
+    ev.bind(xv, Tensor(xt, xs, x));
+    ev.bind(g, Tensor(yt, ys, gy));
+    return ev.eval(gxs[0]);
+}
+
+template <typename Op>
+CpuTensor FwdOf(Op op, VType xt, ImgSize xs, const float* x) {
+    Variable xv(xt, xs);
+    Variable y = op(xv);
+    CpuEvaluator ev;
+    ev.bind(xv, Tensor(xt, xs, x));
+    return ev.eval(y);
+}
+
+}  // namespace
+
+extern "C" {
+
+// EquirectSample (f_ops.cpp:2921-2964): map {mw,mh} x n, dir {dw,dh} VEC3.
+// gy != nullptr: its VJP w.r.t. the map (EquirectSampleBwd + TileSum,
+// f_ops.cpp:2823-2919) for gy {dw,dh} x n, written to out {mw,mh} x n.
+int refh_equirect_sample(const float* map, uint32_t mw, uint32_t mh, uint32_t n_comp,
+                         const float* dir, uint32_t dw, uint32_t dh, const float* gy,
+                         float* out) {
+    return Guard([&] {
+        Variable d(VEC3, {dw, dh});
+        const auto op = [&](const Variable& m) { return F::EquirectSample(m, d); };
+        Variable m(VecOf(n_comp), {mw, mh});
+        Variable y = op(m);
+        if (!gy) {
+            CpuEvaluator ev;
+            ev.bind(m, Tensor(VecOf(n_comp), {mw, mh}, map));
+            ev.bind(d, Tensor(VEC3, {dw, dh}, dir));
+            CopyOut(ev.eval(y), out);
+            return;
+        }
+        Variable g(VecOf(n_comp), {dw, dh});
+        Variable loss = y * g;
+        Variable m_mut = m;
+        m_mut.setRequiresGradRecursively();
+        auto [leaves, gxs] = BuildBackward(loss);
+        DRESSI_CHECK(leaves.size() == 1 && leaves[0] == m, "expected the map as the leaf");
+        CpuEvaluator ev;
+        ev.bind(m, Tensor(VecOf(n_comp), {mw, mh}, map));
+        ev.bind(d, Tensor(VEC3, {dw, dh}, dir));
+        ev.bind(g, Tensor(VecOf(n_comp), {dw, dh}, gy));
+        CopyOut(ev.eval(gxs[0]), out);
+    });
+}
+
+// AvgPool2x2 (f_ops.cpp:3411-3415) and its VJP: x {w,h} x n -> {w/2,h/2}.
+int refh_avg_pool2x2(const float* x, uint32_t w, uint32_t h, uint32_t n_comp, const float* gy,
+                     float* out) {
+    return Guard([&] {
+        const auto op = [](const Variable& v) { return F::AvgPool2x2(v); };
+        const ImgSize half = {(w + 1) / 2, (h + 1) / 2};
+        CopyOut(gy ? VjpOf(op, VecOf(n_comp), {w, h}, x, VecOf(n_comp), half, gy)
+                   : FwdOf(op, VecOf(n_comp), {w, h}, x),
+                out);
+    });
+}
+
+// IrradianceConv (f_ops.cpp:3006-3087) env {sw,sh} -> {ow,oh}; with gy its
+// VJP (IrradianceConvBwd, f_ops.cpp:2970-3004).
+int refh_irradiance_conv(const float* env, uint32_t sw, uint32_t sh, uint32_t n_comp,
+                         uint32_t ow, uint32_t oh, const float* gy, float* out) {
+    return Guard([&] {
+        const auto op = [&](const Variable& v) { return F::IrradianceConv(v, {ow, oh}); };
+        CopyOut(gy ? VjpOf(op, VecOf(n_comp), {sw, sh}, env, VecOf(n_comp), {ow, oh}, gy)
+                   : FwdOf(op, VecOf(n_comp), {sw, sh}, env),
+                out);
+    });
+}
+
+// PrefilterConv (f_ops.cpp:3264-3348, its normaliser PrefilterConvNorm
+// :3166-3205) at `roughness`; with gy its VJP (PrefilterConvBwd :3207-3262).
+int refh_prefilter_conv(const float* env, uint32_t sw, uint32_t sh, uint32_t n_comp,
+                        uint32_t ow, uint32_t oh, float roughness, const float* gy,
+                        float* out) {
+    return Guard([&] {
+        const auto op = [&](const Variable& v) {
+            return F::PrefilterConv(v, {ow, oh}, roughness);
+        };
+        CopyOut(gy ? VjpOf(op, VecOf(n_comp), {sw, sh}, env, VecOf(n_comp), {ow, oh}, gy)
+                   : FwdOf(op, VecOf(n_comp), {sw, sh}, env),
+                out);
+    });
+}
+
+// PrefilterEnv (f_ops.cpp:3089-3157), forward only.
+int refh_prefilter_env(const float* env, uint32_t sw, uint32_t sh, uint32_t n_comp,
+                       uint32_t ow, uint32_t oh, float roughness, uint32_t n_samples,
+                       float* out) {
+    return Guard([&] {
+        const auto op = [&](const Variable& v) {
+            return F::PrefilterEnv(v, {ow, oh}, roughness, n_samples);
+        };
+        CopyOut(FwdOf(op, VecOf(n_comp), {sw, sh}, env), out);
+    });
+}
+
+// BrdfIntegrationLut (f_ops.cpp:3350-3409): {w,h} VEC2.
+int refh_brdf_lut(uint32_t w, uint32_t h, uint32_t n_samples, float* out) {
+    return Guard([&] {
+        Variable y = F::BrdfIntegrationLut({w, h}, n_samples);
+        CpuEvaluator ev;
+        CopyOut(ev.eval(y), out);
+    });
+}
+
+// The C5 split-sum PBR/IBL material + environment fit: per view the
+// G-buffer of BuildPbrGBuffer and the shading of BuildPbrShade (normal
+// mapping off; AO texture 1, emissive 0; the camera frame and light of
+// examples/pbr_material_optimization/run.cpp:189-236), IBL maps from
+// BuildIrradianceSample + BuildPrefEnvironmentSampleConv(env, levels) +
+// BuildBrdfIntegrationMap (the env is optimized, so the differentiable
+// prefilter), the L1 loss Mean(|StopGradient(target.mapped) - pred.mapped|)
+// summed over views, and in-graph Adam on albedo, mr and env with a shared
+// step counter; albedo / mr are clamped to [0,1] (run.cpp:285-288), the env
+// to >= 0 (pbr_envmap_optimization/run.cpp:312-317). The target is the same
+// graph with the ground-truth maps.
+//   pos / normal {V,3}, uv {V,2}, faces {F,3}, mvps {N,16}, frames {N,12}
+//   (cam_pos, cam_fwd, cam_right, cam_up), light {6} (pos, colour),
+//   gt_albedo / gt_mr / albedo0 / mr0 {T,3}, gt_env / env0 {E,3}.
+//   Outputs (nullable): out_albedo / out_mr {T,3}, out_env {E,3}, out_loss
+//   {iters}, out_g_albedo0 / out_g_mr0 {T,3}, out_g_env0 {E,3} (gradients of
+//   iteration 0), out_pred0 / out_target0 {N,S,S,3} (mapped), out_mask0
+//   {N,S,S}.
+int refh_pbr_fit(const float* pos, const float* normal, uint32_t n_verts, const float* uv,
+                 const float* faces, uint32_t n_faces, const float* mvps, const float* frames,
+                 const float* light, uint32_t n_views, uint32_t screen_px, uint32_t tex_w,
+                 uint32_t tex_h, uint32_t env_w, uint32_t env_h, uint32_t levels,
+                 const float* gt_albedo, const float* gt_mr, const float* gt_env,
+                 const float* albedo0, const float* mr0, const float* env0, float lr,
+                 uint32_t iters, float* out_albedo, float* out_mr, float* out_env,
+                 float* out_loss, float* out_g_albedo0, float* out_g_mr0, float* out_g_env0,
+                 float* out_pred0, float* out_target0, float* out_mask0) {
+    using namespace dressi_examples;
+    return Guard([&] {
+        const ImgSize screen = {screen_px, screen_px};
+        const ImgSize tex_size = {tex_w, tex_h};
+        const ImgSize env_size = {env_w, env_h};
+        PbrGeometryLeaves geom;
+        geom.uvh = Variable(VEC4, {n_verts, 1});
+        geom.normal = Variable(VEC3, {n_verts, 1});
+        geom.tangent = Variable(VEC3, {n_verts, 1});
+        geom.wpos = Variable(VEC3, {n_verts, 1});
+        geom.faces = Variable(IVEC3, {n_faces, 1});
+        PbrMaterialLeaves gt_mat;
+        gt_mat.albedo = Variable(VEC3, tex_size);
+        gt_mat.mr = Variable(VEC3, tex_size);
+        gt_mat.normal_map = Variable(VEC3, tex_size);
+        gt_mat.ao = Variable(VEC3, tex_size);
+        gt_mat.emissive = Variable(VEC3, tex_size);
+        PbrMaterialLeaves opt_mat = gt_mat;
+        Variable albedo(VEC3, tex_size), mr(VEC3, tex_size);
+        opt_mat.albedo = albedo;
+        opt_mat.mr = mr;
+        Variable env_gt(VEC3, env_size), env(VEC3, env_size);
+        const auto ibl_of = [&](const Variable& e) {
+            PbrIblMaps maps;
+            maps.env = e;
+            maps.irr = BuildIrradianceSample(e);
+            maps.pref = BuildPrefEnvironmentSampleConv(e, levels);
+            maps.lut = BuildBrdfIntegrationMap();
+            return maps;
+        };
+        const PbrIblMaps ibl_gt = ibl_of(env_gt);
+        const PbrIblMaps ibl = ibl_of(env);
+        Variable uv_clip(VEC4, {n_verts, 1});
+        Variable light_pos(VEC3, {1, 1}), light_col(VEC3, {1, 1});
+        std::vector<Variable> clips, attrs, preds, targets, masks;
+        std::vector<PbrFrameLeaves> frs(n_views);
+        Variables view_losses;
+        for (uint32_t v = 0; v < n_views; v++) {
+            clips.emplace_back(VEC4, ImgSize{n_verts, 1});
+            attrs.emplace_back(VEC4, ImgSize{n_verts, 1});
+            frs[v].cam_pos = Variable(VEC3, {1, 1});
+            frs[v].cam_fwd = Variable(VEC3, {1, 1});
+            frs[v].cam_right = Variable(VEC3, {1, 1});
+            frs[v].cam_up = Variable(VEC3, {1, 1});
+            frs[v].light_pos = light_pos;
+            frs[v].light_col = light_col;
+            PbrGeometryLeaves vg = geom;
+            vg.clip = clips[v];
+            const PbrGBuffer gbuf = BuildPbrGBuffer(vg, screen);
+            Variable inv_uv = F::Rasterize(uv_clip, attrs[v], geom.faces, tex_size);
+            const PbrOutputs tgt = BuildPbrShade(gbuf, gt_mat, frs[v], ibl_gt, inv_uv, screen,
+                                                 false);
+            const PbrOutputs prd = BuildPbrShade(gbuf, opt_mat, frs[v], ibl, inv_uv, screen,
+                                                 false);
+            targets.push_back(tgt.mapped);
+            preds.push_back(prd.mapped);
+            masks.push_back(prd.mask);
+            Variable diff = F::StopGradient(tgt.mapped) - prd.mapped;
+            view_losses.push_back(F::Mean(F::Abs(diff)));
+        }
+        Variable loss = F::SumPixelWise(view_losses);
+        Variable a_mut = albedo, m_mut = mr, e_mut = env;
+        a_mut.setRequiresGradRecursively();
+        m_mut.setRequiresGradRecursively();
+        e_mut.setRequiresGradRecursively();
+        auto [xs, gxs] = BuildBackward(loss);
+        DRESSI_CHECK(xs.size() == 3, "expected albedo, mr and env as the leaves");
+        Variable g_albedo{nullptr}, g_mr{nullptr}, g_env{nullptr};
+        for (size_t i = 0; i < xs.size(); i++) {
+            if (xs[i] == albedo) g_albedo = gxs[i];
+            if (xs[i] == mr) g_mr = gxs[i];
+            if (xs[i] == env) g_env = gxs[i];
+        }
+        DRESSI_CHECK(g_albedo && g_mr && g_env, "missing a leaf gradient");
+        const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+        Variable adam_t(FLOAT, {1, 1});
+        Variable t_new = adam_t + 1.f;
+        Variable bc1 = 1.f - F::Pow(F::Float(b1), t_new);
+        Variable bc2 = 1.f - F::Pow(F::Float(b2), t_new);
+        struct Adam {
+            Variable m, v, m_new, v_new, x_new;
+        };
+        const auto adam = [&](const Variable& x, const Variable& g, ImgSize sz, bool unit) {
+            Adam a{Variable(VEC3, sz), Variable(VEC3, sz), Variable(nullptr),
+                   Variable(nullptr), Variable(nullptr)};
+            a.m_new = a.m * b1 + g * (1.f - b1);
+            a.v_new = a.v * b2 + g * g * (1.f - b2);
+            Variable step = (a.m_new / bc1) / (F::Sqrt(a.v_new / bc2) + eps) * lr;
+            a.x_new = unit ? F::Clamp(x - step, F::Float(0.f), F::Float(1.f))
+                           : F::Max(x - step, F::Float(0.f));
+            return a;
+        };
+        Adam ad_a = adam(albedo, g_albedo, tex_size, true);
+        Adam ad_m = adam(mr, g_mr, tex_size, true);
+        Adam ad_e = adam(env, g_env, env_size, false);
+
+        const size_t ntx = size_t(tex_w) * tex_h, nev = size_t(env_w) * env_h;
+        std::vector<float> uvh(size_t(n_verts) * 4), zeros3(size_t(n_verts) * 3, 0.f);
+        for (uint32_t i = 0; i < n_verts; i++) {
+            uvh[i * 4 + 0] = uv[i * 2 + 0];
+            uvh[i * 4 + 1] = uv[i * 2 + 1];
+            uvh[i * 4 + 2] = 1.f;
+            uvh[i * 4 + 3] = 1.f;
+        }
+        CpuImage uv_img(n_verts, 1, 2);
+        std::memcpy(uv_img.data.data(), uv, sizeof(float) * 2 * n_verts);
+        const CpuImage uv_clip_img = UvAsClip(uv_img);
+        std::vector<CpuImage> clip_imgs, attr_imgs;
+        for (uint32_t v = 0; v < n_views; v++) {
+            const float* m = mvps + 16 * v;
+            CpuImage clip_img(n_verts, 1, 4);
+            for (uint32_t i = 0; i < n_verts; i++) {
+                const float p[4] = {pos[i * 3 + 0], pos[i * 3 + 1], pos[i * 3 + 2], 1.f};
+                for (int row = 0; row < 4; row++) {
+                    float acc = 0.f;
+                    for (int k = 0; k < 4; k++) {
+                        acc += m[k * 4 + row] * p[k];
+                    }
+                    clip_img.at(i, 0, uint32_t(row)) = acc;
+                }
+            }
+            attr_imgs.push_back(ScreenAttr(clip_img, screen));
+            clip_imgs.push_back(std::move(clip_img));
+        }
+        CpuTensor t_a = Tensor(VEC3, tex_size, albedo0), t_m = Tensor(VEC3, tex_size, mr0);
+        CpuTensor t_e = Tensor(VEC3, env_size, env0);
+        CpuTensor am = Fill(VEC3, tex_size, 0.f), av = am, mm = am, mv = am;
+        CpuTensor em = Fill(VEC3, env_size, 0.f), ev_ = em;
+        CpuTensor t_t = Fill(FLOAT, {1, 1}, 0.f);
+        const size_t px = size_t(screen_px) * screen_px;
+        for (uint32_t it = 0; it < iters; it++) {
+            CpuEvaluator ev;
+            ev.bind(geom.uvh, Tensor(VEC4, {n_verts, 1}, uvh.data()));
+            ev.bind(geom.normal, Tensor(VEC3, {n_verts, 1}, normal));
+            ev.bind(geom.tangent, Tensor(VEC3, {n_verts, 1}, zeros3.data()));
+            ev.bind(geom.wpos, Tensor(VEC3, {n_verts, 1}, pos));
+            ev.bind(geom.faces, Tensor(IVEC3, {n_faces, 1}, faces));
+            ev.bind(gt_mat.albedo, Tensor(VEC3, tex_size, gt_albedo));
+            ev.bind(gt_mat.mr, Tensor(VEC3, tex_size, gt_mr));
+            ev.bind(gt_mat.normal_map, Fill(VEC3, tex_size, 0.5f));
+            ev.bind(gt_mat.ao, Fill(VEC3, tex_size, 1.f));
+            ev.bind(gt_mat.emissive, Fill(VEC3, tex_size, 0.f));
+            ev.bind(env_gt, Tensor(VEC3, env_size, gt_env));
+            ev.bind(uv_clip, Tensor(VEC4, {n_verts, 1}, uv_clip_img.data.data()));
+            ev.bind(light_pos, Tensor(VEC3, {1, 1}, light));
+            ev.bind(light_col, Tensor(VEC3, {1, 1}, light + 3));
+            for (uint32_t v = 0; v < n_views; v++) {
+                ev.bind(clips[v], Tensor(VEC4, {n_verts, 1}, clip_imgs[v].data.data()));
+                ev.bind(attrs[v], Tensor(VEC4, {n_verts, 1}, attr_imgs[v].data.data()));
+                const float* fr = frames + 12 * v;
+                ev.bind(frs[v].cam_pos, Tensor(VEC3, {1, 1}, fr + 0));
+                ev.bind(frs[v].cam_fwd, Tensor(VEC3, {1, 1}, fr + 3));
+                ev.bind(frs[v].cam_right, Tensor(VEC3, {1, 1}, fr + 6));
+                ev.bind(frs[v].cam_up, Tensor(VEC3, {1, 1}, fr + 9));
+            }
+            ev.bind(albedo, t_a);
+            ev.bind(mr, t_m);
+            ev.bind(env, t_e);
+            ev.bind(ad_a.m, am);
+            ev.bind(ad_a.v, av);
+            ev.bind(ad_m.m, mm);
+            ev.bind(ad_m.v, mv);
+            ev.bind(ad_e.m, em);
+            ev.bind(ad_e.v, ev_);
+            ev.bind(adam_t, t_t);
+            const CpuTensor li = ev.eval(loss);
+            if (out_loss) out_loss[it] = li.data[0];
+            if (it == 0) {
+                if (out_g_albedo0) CopyOut(ev.eval(g_albedo), out_g_albedo0);
+                if (out_g_mr0) CopyOut(ev.eval(g_mr), out_g_mr0);
+                if (out_g_env0) CopyOut(ev.eval(g_env), out_g_env0);
+                for (uint32_t v = 0; v < n_views; v++) {
+                    if (out_pred0) CopyOut(ev.eval(preds[v]), out_pred0 + v * px * 3);
+                    if (out_target0) CopyOut(ev.eval(targets[v]), out_target0 + v * px * 3);
+                    if (out_mask0) CopyOut(ev.eval(masks[v]), out_mask0 + v * px);
+                }
+            }
+            CpuTensor n_a = ev.eval(ad_a.x_new), n_am = ev.eval(ad_a.m_new);
+            CpuTensor n_av = ev.eval(ad_a.v_new);
+            CpuTensor n_m = ev.eval(ad_m.x_new), n_mm = ev.eval(ad_m.m_new);
+            CpuTensor n_mv = ev.eval(ad_m.v_new);
+            CpuTensor n_e = ev.eval(ad_e.x_new), n_em = ev.eval(ad_e.m_new);
+            CpuTensor n_ev = ev.eval(ad_e.v_new);
+            CpuTensor n_t = ev.eval(t_new);
+            t_a = std::move(n_a);
+            am = std::move(n_am);
+            av = std::move(n_av);
+            t_m = std::move(n_m);
+            mm = std::move(n_mm);
+            mv = std::move(n_mv);
+            t_e = std::move(n_e);
+            em = std::move(n_em);
+            ev_ = std::move(n_ev);
+            t_t = std::move(n_t);
+        }
+        (void)ntx;
+        (void)nev;
+        CopyOut(t_a, out_albedo);
+        CopyOut(t_m, out_mr);
+        CopyOut(t_e, out_env);
     });
 }
 

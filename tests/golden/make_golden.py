@@ -6,6 +6,7 @@ and stored next to the outputs, so the fixtures are self-contained data.
     python tests/golden/make_golden.py            # every fixture
     python tests/golden/make_golden.py texture    # the texture path's only
     python tests/golden/make_golden.py dist       # GatherDistGrad's only
+    python tests/golden/make_golden.py pbr        # the PBR / IBL path's only
 
 Each .npz holds `in_*` arrays (inputs) and `out_*` arrays (reference outputs).
 """
@@ -257,16 +258,121 @@ def texture_main(o, r):
     tex_fit_fixture(o, r, "tex_uvs16_64px_20it.npz", 16, 8, 64, 32, 2, 20, 20, 7, False)
 
 
+def ibl_fixtures(o, r):
+    """Per-op IBL scenes: EquirectSample and its map VJP (1 / 3 / 4
+    components; zero-length, pole and seam directions), AvgPool2x2 and its
+    VJP (odd sizes), IrradianceConv / PrefilterConv (roughness 0, 0.5, 1) and
+    their transposes, PrefilterEnv and the BRDF LUT."""
+    rng = np.random.default_rng(31)
+    arrs = {}
+    for nc in (1, 3, 4):
+        m = rng.random((8, 16, nc)).astype(np.float32)
+        d = rng.standard_normal((9, 11, 3)).astype(np.float32)
+        d[0, 0] = 0.0
+        d[0, 1] = [0.0, 1.0, 0.0]
+        d[0, 2] = [0.0, -2.0, 0.0]
+        d[0, 3] = [-1.0, 0.3, 0.0]
+        d[0, 4] = [-1.0, 0.0, -1e-7]
+        gy = rng.standard_normal((9, 11, nc)).astype(np.float32)
+        arrs.update({f"in_eq{nc}_map": m, f"in_eq{nc}_dir": d, f"in_eq{nc}_gy": gy,
+                     f"out_eq{nc}": r.equirect_sample(m, d),
+                     f"out_eq{nc}_bwd": r.equirect_sample(m, d, gy)})
+    for name, (h, w) in {"pool_odd": (5, 7), "pool_even": (16, 32)}.items():
+        x = rng.random((h, w, 3)).astype(np.float32)
+        g = rng.standard_normal(((h + 1) // 2, (w + 1) // 2, 3)).astype(np.float32)
+        arrs.update({f"in_{name}_x": x, f"in_{name}_gy": g, f"out_{name}": r.avg_pool2x2(x),
+                     f"out_{name}_bwd": r.avg_pool2x2(x, g)})
+    env = rng.random((8, 16, 3)).astype(np.float32)
+    g84 = rng.standard_normal((4, 8, 3)).astype(np.float32)
+    g168 = rng.standard_normal((8, 16, 3)).astype(np.float32)
+    arrs.update(in_env=env, in_g84=g84, in_g168=g168,
+                out_irr=r.irradiance_conv(env, 8, 4), out_irr_bwd=r.irradiance_conv(env, 8, 4, g84))
+    for i, rough in enumerate((0.0, 0.5, 1.0)):
+        arrs[f"out_pref{i}_16"] = r.prefilter_conv(env, 16, 8, rough)
+        arrs[f"out_pref{i}_8"] = r.prefilter_conv(env, 8, 4, rough)
+        arrs[f"out_pref{i}_16_bwd"] = r.prefilter_conv(env, 16, 8, rough, g168)
+        arrs[f"out_pref{i}_8_bwd"] = r.prefilter_conv(env, 8, 4, rough, g84)
+    arrs["out_prefenv"] = r.prefilter_env(env, 8, 4, 0.5, 64)
+    arrs["out_lut16"] = r.brdf_lut(16, 16, 64)
+    arrs["out_lut64"] = r.brdf_lut(64, 64, 512)
+    np.savez_compressed(os.path.join(OUT, "ibl_unit.npz"), **arrs)
+    print("wrote ibl_unit.npz", len(arrs), "arrays")
+
+
+def pbr_scene(o, level, screen, views, tex, ew, eh, seed):
+    """A C5-style scene (the layout of opendressi_amd.pbr.make_pbr_scene):
+    unit icosphere with equirect uv, the material example's camera ring,
+    U[0.05, 0.95] materials, a smooth log-normal env with 3 lobes."""
+    pos, faces = o.icosphere(level)
+    d = pos.astype(np.float64) / np.linalg.norm(pos, axis=1, keepdims=True)
+    uv = np.stack([np.arctan2(d[:, 2], d[:, 0]) / (2 * math.pi) + 0.5,
+                   np.arccos(np.clip(d[:, 1], -1, 1)) / math.pi], 1).astype(np.float32)
+    fov = np.float32(45.0 * 3.14159265 / 180.0)
+    th = np.float32(math.tan(float(fov) * 0.5))
+    proj = o.perspective_vk(float(fov), 1.0, 0.1, 10.0)
+    mvps = np.zeros((views, 16), np.float32)
+    frames = np.zeros((views, 12), np.float32)
+    for i in range(views):
+        ang = np.float32(2.0 * 3.14159265 * i / views)
+        eye = np.array([2.2 * math.sin(ang) * 0.92, 0.85, 2.2 * math.cos(ang) * 0.92], np.float32)
+        vm = o.look_at(eye)
+        mvps[i] = o.mat4_mul(proj, vm)
+        frames[i] = np.concatenate([eye, [-vm[2], -vm[6], -vm[10]],
+                                    np.array([vm[0], vm[4], vm[8]], np.float32) * th,
+                                    np.array([vm[1], vm[5], vm[9]], np.float32) * th])
+    rng = np.random.default_rng(seed)
+    gt_albedo = (0.05 + 0.9 * rng.random((tex, tex, 3))).astype(np.float32)
+    gt_mr = np.zeros((tex, tex, 3), np.float32)
+    gt_mr[..., 1:] = 0.05 + 0.9 * rng.random((tex, tex, 2))
+    yy, xx = np.meshgrid((np.arange(eh) + 0.5) / eh, (np.arange(ew) + 0.5) / ew, indexing="ij")
+    env = 0.3 * np.exp(0.6 * (np.sin(2 * math.pi * (2 * xx + 0.3)) * np.sin(math.pi * yy * 3)))
+    env = env[..., None] * np.ones(3)
+    dirs = np.stack([np.sin(math.pi * yy) * np.cos((xx - 0.5) * 2 * math.pi),
+                     np.cos(math.pi * yy),
+                     np.sin(math.pi * yy) * np.sin((xx - 0.5) * 2 * math.pi)], -1)
+    for k in range(3):
+        mu = rng.standard_normal(3)
+        mu /= np.linalg.norm(mu)
+        ang = np.arccos(np.clip(dirs @ mu, -1, 1))
+        sig = 0.15 + 0.2 * rng.random()
+        env = env + np.exp(-ang ** 2 / (2 * sig * sig))[..., None] * (4 + 12 * rng.random(3))
+    return dict(pos=pos, normal=pos.copy(), uv=uv, faces=faces, mvps=mvps, frames=frames,
+                light=np.array([2, 2, 2, 20, 20, 20], np.float32), screen=screen, levels=6,
+                lr=1e-2, gt_albedo=gt_albedo, gt_mr=gt_mr, gt_env=env.astype(np.float32),
+                albedo0=np.full((tex, tex, 3), 0.5, np.float32),
+                mr0=np.full((tex, tex, 3), 0.5, np.float32),
+                env0=np.full((eh, ew, 3), 0.3, np.float32))
+
+
+def pbr_fit_fixture(o, r, name, level, screen, views, tex, ew, eh, iters, seed, images):
+    sc = pbr_scene(o, level, screen, views, tex, ew, eh, seed)
+    res = r.pbr_fit(sc, iters=iters, want_images=images)
+    arrs = {"in_" + k: (v if isinstance(v, np.ndarray) else np.array(v)) for k, v in sc.items()}
+    arrs.update({"out_" + k: v for k, v in res.items()})
+    np.savez_compressed(os.path.join(OUT, name), **arrs)
+    print("wrote", name, {k: v.shape for k, v in arrs.items()})
+
+
+def pbr_main(o, r):
+    ibl_fixtures(o, r)
+    pbr_fit_fixture(o, r, "pbr_ico2_48px_2view_3it.npz", 2, 48, 2, 16, 64, 32, 3, 41, True)
+    pbr_fit_fixture(o, r, "pbr_ico3_96px_3view_2it.npz", 3, 96, 3, 64, 256, 128, 2, 42, False)
+
+
 def main():
     build(ref=True)
     o, r = Oracle(), Reference()
     if sys.argv[1:] == ["texture"]:
         texture_main(o, r)
         return
+    if sys.argv[1:] == ["pbr"]:
+        pbr_main(o, r)
+        return
     if sys.argv[1:] == ["dist"]:
         ds_fixtures(o, r)
         return
     ds_fixtures(o, r)
+    pbr_main(o, r)
     texture_main(o, r)
     op_fixtures(o, r)
     aa_fixtures(o, r)
