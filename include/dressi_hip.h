@@ -251,6 +251,84 @@ int dressi_prefilter_env(dressi_ctx* ctx, const float* env, uint32_t sw,
 int dressi_brdf_lut(dressi_ctx* ctx, uint32_t w, uint32_t h,
                     uint32_t n_samples, float* out);
 
+/* ---- the fused PBR / IBL fit plan (C5) ---- */
+/* The material + environment fit of examples/common/pbr_graph.cpp (shading,
+ * normal mapping off, AO 1, emissive 0) with the maps of src/core/ibl.cpp
+ * (irradiance 32 x 16 from the env pooled to <= 64 x 32; `levels`
+ * PrefilterConv levels from <= 128 x 64, roughness i / (levels - 1); BRDF
+ * LUT 256^2 x 512), the L1 loss Mean(|target - pred|) of the Reinhard-mapped
+ * image summed over views, and in-graph Adam on the albedo and metallic-
+ * roughness textures (clamped to [0,1], as examples/pbr_material_optimization/
+ * run.cpp:285-288) and the env (>= 0, as examples/pbr_envmap_optimization/
+ * run.cpp:312-317) with one shared step counter. Replaces DressiAD::execStep
+ * on that graph (src/dressi_ad.cpp:280-530). Geometry and cameras are static:
+ * set_scene precomputes every geometry-only term per view; one step runs the
+ * IBL maps, shading forward + backward, the map transposes and Adam. The
+ * material gradients are GatherByInverseUVBilinear (f_ops.cpp:2650-2732) of
+ * the per-pixel gradients, as a static per-texel gather list. */
+typedef struct dressi_pbr_plan dressi_pbr_plan;
+
+typedef struct dressi_pbr_desc {
+    uint32_t n_verts, n_faces;
+    uint32_t n_views;     /* 1..16 */
+    uint32_t width;       /* screen S (square: width == height) */
+    uint32_t height;
+    uint32_t tex_w, tex_h;  /* albedo / mr textures */
+    uint32_t env_w, env_h;  /* equirect env */
+    uint32_t levels;      /* prefiltered levels, 2..8 */
+    float lr, beta1, beta2, eps;
+    uint32_t flags;       /* DRESSI_PBR_* */
+} dressi_pbr_desc;
+
+/* keep the predicted (mapped) images of the last step */
+#define DRESSI_PBR_KEEP_PRED 1u
+/* keep the last step's texture and env gradients */
+#define DRESSI_PBR_KEEP_GRAD 2u
+
+int dressi_pbr_create(dressi_ctx* ctx, const dressi_pbr_desc* desc,
+                      dressi_pbr_plan** out);
+int dressi_pbr_destroy(dressi_pbr_plan* plan);
+/* host arrays: pos / normal {V,3}, uv {V,2}, faces {F,3} (float ids),
+ * mvps {N,16} column-major, frames {N,12} (cam_pos, cam_fwd,
+ * cam_right * tan(fov/2) * aspect, cam_up * tan(fov/2); PbrFrameLeaves,
+ * examples/common/pbr_graph.h:46-53), light {6} (position, colour) */
+int dressi_pbr_set_scene(dressi_pbr_plan* plan, const float* pos,
+                         const float* normal, const float* uv,
+                         const float* faces, const float* mvps,
+                         const float* frames, const float* light);
+/* renders the static targets from the ground-truth maps (host VEC3:
+ * gt_albedo / gt_mr {tex_h, tex_w, 3}, gt_env {env_h, env_w, 3}); the state
+ * must be (re)set afterwards */
+int dressi_pbr_set_target(dressi_pbr_plan* plan, const float* gt_albedo,
+                          const float* gt_mr, const float* gt_env);
+/* parameters (host VEC3, as above), Adam moments cleared, step counter t */
+int dressi_pbr_set_state(dressi_pbr_plan* plan, const float* albedo,
+                         const float* mr, const float* env, float t);
+int dressi_pbr_get_state(dressi_pbr_plan* plan, float* albedo, float* mr,
+                         float* env, float* t);
+/* n_iters iterations (a captured hipGraph, replayed) / eager launches */
+int dressi_pbr_step(dressi_pbr_plan* plan, uint32_t n_iters);
+int dressi_pbr_step_eager(dressi_pbr_plan* plan, uint32_t n_iters);
+enum {
+    DRESSI_PBR_LOSS = 0,     /* float: the last step's loss */
+    DRESSI_PBR_PRED = 1,     /* {N,S,S} float4 mapped rgb (KEEP_PRED) */
+    DRESSI_PBR_TARGET = 2,   /* {N,S,S} float4 mapped rgb */
+    DRESSI_PBR_G_ALBEDO = 3, /* {T} float4 (KEEP_GRAD) */
+    DRESSI_PBR_G_MR = 4,     /* {T} float4 (KEEP_GRAD) */
+    DRESSI_PBR_G_ENV = 5,    /* {E} float4 (KEEP_GRAD) */
+    DRESSI_PBR_IRR = 6,      /* {32 x 16} float4: the last step's irradiance map */
+    DRESSI_PBR_PREF = 7      /* float4: the prefiltered levels, level-major */
+};
+int dressi_pbr_buffer(dressi_pbr_plan* plan, int which, void** ptr,
+                      size_t* bytes);
+int dressi_pbr_read(dressi_pbr_plan* plan, int which, void* host,
+                    size_t bytes);
+/* in-place eager iterations with a HIP event around each kernel: average
+ * microseconds per kernel (the pooling chain counts as one) */
+int dressi_pbr_profile(dressi_pbr_plan* plan, uint32_t iters, char* names,
+                       size_t name_stride, float* usec, uint32_t cap,
+                       uint32_t* n);
+
 /* ---- texture path (C3) ---- */
 /* F::TextureBilinear forward (src/core/f_ops.cpp:2736-2780, BilerpClamp
  * src/core/ibl_math.h:91-115): tex {tw,th} x n_comp (1..4) sampled at

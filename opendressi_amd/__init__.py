@@ -1,5 +1,5 @@
 """opendressi_amd -- MI355X-native Dressi-AD hot path: the silhouette fit
-(HardSoftRas, screen-space AA) and the texture fit.
+(HardSoftRas, screen-space AA), the texture fit and the PBR / IBL fit.
 
 Hand-written gfx950 HIP kernels behind the C ABI of include/dressi_hip.h
 (libdressi_hip.so, built in-tree by opendressi_amd.build). The first use of
@@ -18,6 +18,8 @@ _EXPORTS = {
     "uniform": ".runtime", "uv_sphere": ".runtime",
     "TEX_WORKLOADS": ".texture", "TexWorkload": ".texture", "TextureFit": ".texture",
     "make_tex_scene": ".texture", "orbit_cameras": ".texture", "sinusoid_texture": ".texture",
+    "PBR_WORKLOADS": ".pbr", "PbrWorkload": ".pbr", "PbrFit": ".pbr",
+    "make_pbr_scene": ".pbr", "ring_cameras": ".pbr", "synthetic_env": ".pbr",
 }
 
 __all__ = sorted(_EXPORTS)

@@ -37,6 +37,18 @@ class TexDesc(C.Structure):
                 ("beta1", _F), ("beta2", _F), ("eps", _F), ("flags", _U)]
 
 
+class PbrDesc(C.Structure):
+    _fields_ = [("n_verts", _U), ("n_faces", _U), ("n_views", _U), ("width", _U),
+                ("height", _U), ("tex_w", _U), ("tex_h", _U), ("env_w", _U), ("env_h", _U),
+                ("levels", _U), ("lr", _F), ("beta1", _F), ("beta2", _F), ("eps", _F),
+                ("flags", _U)]
+
+
+PBR_KEEP_PRED = 1
+PBR_KEEP_GRAD = 2
+(PBR_LOSS, PBR_PRED, PBR_TARGET, PBR_G_ALBEDO, PBR_G_MR, PBR_G_ENV, PBR_IRR,
+ PBR_PREF) = range(8)
+
 TEX_KEEP_IMAGES = 1
 TEX_KEEP_GRAD = 2
 (TEX_LOSS, TEX_PRED, TEX_TARGET, TEX_FACE_ID, TEX_GRAD, TEX_TEX, TEX_UV) = range(7)
@@ -110,6 +122,17 @@ _SIGS = {
     "dressi_hsr_buffer": (_I, [_P, _I, C.POINTER(_P), C.POINTER(_S)]),
     "dressi_hsr_read": (_I, [_P, _I, _P, _S]),
     "dressi_hsr_profile": (_I, [_P, _U, C.c_char_p, _S, _FP, _U, _UP]),
+    "dressi_pbr_create": (_I, [_P, C.POINTER(PbrDesc), C.POINTER(_P)]),
+    "dressi_pbr_destroy": (_I, [_P]),
+    "dressi_pbr_set_scene": (_I, [_P, _FP, _FP, _FP, _FP, _FP, _FP, _FP]),
+    "dressi_pbr_set_target": (_I, [_P, _FP, _FP, _FP]),
+    "dressi_pbr_set_state": (_I, [_P, _FP, _FP, _FP, _F]),
+    "dressi_pbr_get_state": (_I, [_P, _FP, _FP, _FP, _FP]),
+    "dressi_pbr_step": (_I, [_P, _U]),
+    "dressi_pbr_step_eager": (_I, [_P, _U]),
+    "dressi_pbr_buffer": (_I, [_P, _I, C.POINTER(_P), C.POINTER(_S)]),
+    "dressi_pbr_read": (_I, [_P, _I, _P, _S]),
+    "dressi_pbr_profile": (_I, [_P, _U, C.c_char_p, _S, _FP, _U, _UP]),
     "dressi_tex_create": (_I, [_P, C.POINTER(TexDesc), C.POINTER(_P)]),
     "dressi_tex_destroy": (_I, [_P]),
     "dressi_tex_set_mesh": (_I, [_P, _FP, _FP, _FP]),

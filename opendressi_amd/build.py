@@ -21,7 +21,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libdressi_hip.so")
-SOURCES = ["runtime.hip", "raster.hip", "hsr.hip", "aa.hip", "tex.hip", "ds.hip", "ibl.hip"]
+SOURCES = ["runtime.hip", "raster.hip", "hsr.hip", "aa.hip", "tex.hip", "ds.hip", "ibl.hip", "pbr.hip"]
 HEADERS = ["internal.h", "dressi_math.h", "raster_core.h", "soft_clip.h", "hsr_chain.h",
            "aa_core.h", "plan.h", "ibl_core.h"]
 ARCH = os.environ.get("DRESSI_OFFLOAD_ARCH", "gfx950")

@@ -23,12 +23,24 @@ iterations.
 """
 from __future__ import annotations
 
+import ctypes as C
 import math
 from dataclasses import dataclass
 
 import numpy as np
 
-from .runtime import icosphere, look_at, mat4_mul, perspective_vk, randn, uniform
+from . import _lib
+from ._lib import check, lib
+from .runtime import Context, icosphere, look_at, mat4_mul, perspective_vk, randn, uniform
+
+_FP = C.POINTER(C.c_float)
+
+
+def _fp(a):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_FP)
 
 
 @dataclass(frozen=True)
@@ -135,3 +147,106 @@ def make_pbr_scene(level: int, screen: int, n_views: int, tex: int, env_w: int, 
 def workload_scene(wl: PbrWorkload) -> dict:
     return make_pbr_scene(wl.level, wl.screen, wl.views, wl.tex, wl.env_w, wl.env_h, wl.levels,
                           wl.lr, wl.seed)
+
+
+class PbrFit:
+    """One fused PBR / IBL fit plan (the DressiAD GpuPlan of the material +
+    environment graph) on one device. `scene` is make_pbr_scene's dict."""
+
+    def __init__(self, ctx: Context, scene: dict, keep_pred: bool = False,
+                 keep_grad: bool = False):
+        self.ctx = ctx
+        a = {k: (np.ascontiguousarray(v, np.float32) if isinstance(v, np.ndarray) else v)
+             for k, v in scene.items()}
+        self.n_views = a["mvps"].shape[0]
+        self.screen = int(a["screen"])
+        self.tex_h, self.tex_w = a["gt_albedo"].shape[:2]
+        self.env_h, self.env_w = a["gt_env"].shape[:2]
+        self.levels = int(a["levels"])
+        d = _lib.PbrDesc(len(a["pos"]), len(a["faces"]), self.n_views, self.screen, self.screen,
+                         self.tex_w, self.tex_h, self.env_w, self.env_h, self.levels,
+                         float(a["lr"]), 0.9, 0.999, 1e-8,
+                         (_lib.PBR_KEEP_PRED if keep_pred else 0)
+                         | (_lib.PBR_KEEP_GRAD if keep_grad else 0))
+        h = C.c_void_p()
+        check(lib.dressi_pbr_create(ctx.handle, C.byref(d), C.byref(h)))
+        self.handle = h
+        check(lib.dressi_pbr_set_scene(h, _fp(a["pos"]), _fp(a["normal"]), _fp(a["uv"]),
+                                       _fp(a["faces"]), _fp(a["mvps"]), _fp(a["frames"]),
+                                       _fp(a["light"])))
+        check(lib.dressi_pbr_set_target(h, _fp(a["gt_albedo"]), _fp(a["gt_mr"]),
+                                        _fp(a["gt_env"])))
+        self.set_state(a["albedo0"], a["mr0"], a["env0"])
+
+    @classmethod
+    def from_workload(cls, ctx: Context, name: str, **kw) -> "PbrFit":
+        return cls(ctx, workload_scene(PBR_WORKLOADS[name]), **kw)
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib.dressi_pbr_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_state(self, albedo, mr, env, t: float = 0.0) -> None:
+        f = lambda x: _fp(np.ascontiguousarray(x, np.float32))
+        check(lib.dressi_pbr_set_state(self.handle, f(albedo), f(mr), f(env), float(t)))
+
+    def state(self):
+        alb = np.zeros((self.tex_h, self.tex_w, 3), np.float32)
+        mr = np.zeros_like(alb)
+        env = np.zeros((self.env_h, self.env_w, 3), np.float32)
+        t = np.zeros(1, np.float32)
+        check(lib.dressi_pbr_get_state(self.handle, _fp(alb), _fp(mr), _fp(env), _fp(t)))
+        return alb, mr, env, float(t[0])
+
+    def step(self, n: int = 1, graph: bool = True) -> None:
+        fn = lib.dressi_pbr_step if graph else lib.dressi_pbr_step_eager
+        check(fn(self.handle, n))
+
+    def synchronize(self) -> None:
+        self.ctx.synchronize()
+
+    def read(self, which: int) -> np.ndarray:
+        s, n = self.screen, self.n_views
+        t, e = (self.tex_h, self.tex_w), (self.env_h, self.env_w)
+        n_pref = 0
+        w, h = min(128, self._psrc()[0]), min(64, self._psrc()[1])
+        for _ in range(self.levels):
+            n_pref += w * h
+            w, h = max(w // 2, 1), max(h // 2, 1)
+        shapes = {_lib.PBR_LOSS: (1,), _lib.PBR_PRED: (n, s, s, 4),
+                  _lib.PBR_TARGET: (n, s, s, 4), _lib.PBR_G_ALBEDO: t + (4,),
+                  _lib.PBR_G_MR: t + (4,), _lib.PBR_G_ENV: e + (4,), _lib.PBR_IRR: (16, 32, 4),
+                  _lib.PBR_PREF: (n_pref, 4)}
+        out = np.zeros(shapes[which], np.float32)
+        check(lib.dressi_pbr_read(self.handle, which, out.ctypes.data_as(C.c_void_p),
+                                  out.nbytes))
+        return out
+
+    def _psrc(self):
+        w, h = self.env_w, self.env_h
+        while w > 128 or h > 64:
+            w, h = (w + 1) // 2, (h + 1) // 2
+        return w, h
+
+    def loss(self) -> float:
+        return float(self.read(_lib.PBR_LOSS)[0])
+
+    def profile(self, iters: int = 10) -> dict[str, float]:
+        cap = 16
+        names = C.create_string_buffer(64 * cap)
+        usec = np.zeros(cap, np.float32)
+        n = C.c_uint32()
+        check(lib.dressi_pbr_profile(self.handle, iters, names, 64, _fp(usec), cap, C.byref(n)))
+        return {names.raw[64 * i:64 * (i + 1)].split(b"\0")[0].decode(): float(usec[i])
+                for i in range(n.value)}
+
+
+__all__ = ["PbrWorkload", "PBR_WORKLOADS", "equirect_uv", "ring_cameras", "synthetic_env",
+           "make_pbr_scene", "workload_scene", "PbrFit"]
