@@ -454,6 +454,21 @@ __device__ __forceinline__ uint32_t wrap_idx(int x, int y, int w, int h) {
     return (uint32_t)(y * w + x);
 }
 
+// DPP moves within rows of 16 lanes: row_shr:S reads lane - S (lanes with
+// (lane & 15) < S read 0), row_shl:S reads lane + S
+template <int S>
+__device__ __forceinline__ int dpp_row_shr(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x110 + S, 0xf, 0xf, true);
+}
+template <int S>
+__device__ __forceinline__ int dpp_row_shl(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x100 + S, 0xf, 0xf, true);
+}
+template <int S>
+__device__ __forceinline__ float dpp_row_shr_f(float v) {
+    return __int_as_float(dpp_row_shr<S>(__float_as_int(v)));
+}
+
 // Per pixel (a 16 x 16 tile of one view per workgroup): the shading
 // forward, the L1 loss and its backward (the derivation of the reference's
 // autodiff of pbr_graph.cpp:47-137 through Div / Mul / Add / Max / Mix /
@@ -685,26 +700,61 @@ __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
     // ---- map gradient scatter ---------------------------------------------
     // map m: 0 irradiance, 1 + i prefilter level i, L + 1 env; the
     // irradiance / prefilter accumulators are striped over kStripes copies
-    // (by workgroup) so the few texels of the small maps are not one hot spot
+    // (by workgroup) so the few texels of the small maps are not one hot
+    // spot. Five passes (irradiance, the three prefilter slots, env): per
+    // pass, the 16 lanes of a pixel row are cut into runs of equal tap base
+    // (map, ix, iy); each run's 12 weighted values are summed along the row
+    // (DPP, a fixed order) and its last lane adds them to the workgroup's
+    // LDS window of the map (or to the global accumulators when the window
+    // would exceed kWin texels).
     const uint32_t stripe = blockIdx.x & (kStripes - 1);
     unsigned long long* acc_irr = d.acc_irr + (size_t)stripe * d.iw * d.ih * 3;
     unsigned long long* acc_pref = d.acc_pref + (size_t)stripe * d.n_pref * 3;
-    __syncthreads();  // box initialised
-    const auto note = [&](int m, const MapTaps& t) {
-        atomicMin(&box[m][0], t.ix);
-        atomicMax(&box[m][1], t.ix);
-        atomicMin(&box[m][2], t.iy);
-        atomicMax(&box[m][3], t.iy);
+    const int lane16 = (int)(threadIdx.x & 15);
+    const auto pass_has = [&](int ps) {
+        return ps == 0 ? use_irr : (ps == 4 ? use_bg : (act[ps - 1] && ws[ps - 1] != 0.f));
     };
-    const auto pref_on = [&](int j) { return act[j] && ws[j] != 0.f; };
-    if (use_irr) note(0, t_irr);
+    const auto pass_map = [&](int ps) { return ps == 0 ? 0 : (ps == 4 ? L + 1 : 1 + li[ps - 1]); };
+    const auto pass_taps = [&](int ps) -> const MapTaps& {
+        return ps == 0 ? t_irr : (ps == 4 ? t_bg : tp[ps - 1]);
+    };
+    // run ids and run tails per pass
+    int seg[5];
+    bool tail[5];
 #pragma unroll
-    for (int j = 0; j < 3; j++) {
-        if (pref_on(j)) note(1 + li[j], tp[j]);
+    for (int ps = 0; ps < 5; ps++) {
+        const bool has = pass_has(ps);
+        const MapTaps& t = pass_taps(ps);
+        // lanes without a contribution get a key of their own
+        const int key = has ? ((pass_map(ps) << 26) | ((t.iy + 1) << 13) | (t.ix + 1))
+                            : -1 - (int)threadIdx.x;
+        const int left = dpp_row_shr<1>(key);
+        int sg = (lane16 == 0 || left != key) ? 1 : 0;
+        sg += dpp_row_shr<1>(sg);
+        sg += dpp_row_shr<2>(sg);
+        sg += dpp_row_shr<4>(sg);
+        sg += dpp_row_shr<8>(sg);
+        const int right = dpp_row_shl<1>(sg);
+        seg[ps] = sg;
+        tail[ps] = has && (lane16 == 15 || right != sg);
     }
-    if (use_bg) note(L + 1, t_bg);
-    __syncthreads();
+    __syncthreads();  // box initialised
+#pragma unroll
+    for (int ps = 0; ps < 5; ps++) {
+        if (tail[ps]) {
+            const int m = pass_map(ps);
+            const MapTaps& t = pass_taps(ps);
+            atomicMin(&box[m][0], t.ix);
+            atomicMax(&box[m][1], t.ix);
+            atomicMin(&box[m][2], t.iy);
+            atomicMax(&box[m][3], t.iy);
+        }
+    }
     const int n_maps = L + 2;
+    for (int j = threadIdx.x; j < n_maps * kWin * 3; j += blockDim.x) {
+        (&win[0][0][0])[j] = 0ull;
+    }
+    __syncthreads();
     const auto map_wh = [&](int m, int* w, int* h, uint32_t* off) {
         if (m == 0) {
             *w = (int)d.iw;
@@ -731,45 +781,81 @@ __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
         *wy0 = y0;
         return w * (y1 - y0 + 1) <= kWin;
     };
-    for (int j = threadIdx.x; j < n_maps * kWin * 3; j += blockDim.x) {
-        (&win[0][0][0])[j] = 0ull;
-    }
-    __syncthreads();
     const int k = d.fix_k;
-    const auto add = [&](int m, const MapTaps& t, const float* g) {
-        int w, h, ww, wy0;
-        uint32_t off;
-        map_wh(m, &w, &h, &off);
-        const bool lds = win_ok(m, h, &ww, &wy0);
-        unsigned long long* gacc =
-                m == 0 ? acc_irr : (m <= L ? acc_pref + (size_t)off * 3 : d.acc_env);
+#pragma unroll
+    for (int ps = 0; ps < 5; ps++) {
+        if (!__any(tail[ps])) {
+            continue;
+        }
+        const MapTaps& t = pass_taps(ps);
+        float g3[3];
+        if (ps == 0) {
+            g3[0] = g_irr[0];
+            g3[1] = g_irr[1];
+            g3[2] = g_irr[2];
+        } else if (ps == 4) {
+            g3[0] = gh[0];
+            g3[1] = gh[1];
+            g3[2] = gh[2];
+        } else {
+            const float wj = ws[ps - 1];
+            g3[0] = gpref[0] * wj;
+            g3[1] = gpref[1] * wj;
+            g3[2] = gpref[2] * wj;
+        }
+        const bool has = pass_has(ps);
+        float v[12];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int xx = t.ix + (q & 1), yy0 = t.iy + (q >> 1);
-            const int yy = yy0 < 0 ? 0 : (yy0 > h - 1 ? h - 1 : yy0);
 #pragma unroll
             for (int c = 0; c < 3; c++) {
-                const long long v = to_fixed(g[c] * t.w[q], k);
-                if (!v) continue;
-                if (lds) {
-                    const int wi = (yy - wy0) * ww + (xx - box[m][0]);
-                    atomicAdd(&win[m][wi][c], (unsigned long long)v);
-                } else {
-                    atomicAdd(&gacc[(size_t)wrap_idx(xx, yy, w, h) * 3 + c],
-                              (unsigned long long)v);
+                v[q * 3 + c] = has ? g3[c] * t.w[q] : 0.f;
+            }
+        }
+        const int sg = seg[ps];
+        // segmented inclusive scan along the row (runs are contiguous)
+#pragma unroll
+        for (int sh = 1; sh < 16; sh <<= 1) {
+            const int osg = sh == 1 ? dpp_row_shr<1>(sg)
+                                    : (sh == 2 ? dpp_row_shr<2>(sg)
+                                               : (sh == 4 ? dpp_row_shr<4>(sg) : dpp_row_shr<8>(sg)));
+            const bool take = lane16 >= sh && osg == sg;
+#pragma unroll
+            for (int e = 0; e < 12; e++) {
+                const float o = sh == 1 ? dpp_row_shr_f<1>(v[e])
+                                        : (sh == 2 ? dpp_row_shr_f<2>(v[e])
+                                                   : (sh == 4 ? dpp_row_shr_f<4>(v[e])
+                                                              : dpp_row_shr_f<8>(v[e])));
+                v[e] += take ? o : 0.f;
+            }
+        }
+        if (tail[ps]) {
+            const int m = pass_map(ps);
+            int w, h, ww, wy0;
+            uint32_t off;
+            map_wh(m, &w, &h, &off);
+            const bool lds = win_ok(m, h, &ww, &wy0);
+            unsigned long long* gacc =
+                    m == 0 ? acc_irr : (m <= L ? acc_pref + (size_t)off * 3 : d.acc_env);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int xx = t.ix + (q & 1), yy0 = t.iy + (q >> 1);
+                const int yy = yy0 < 0 ? 0 : (yy0 > h - 1 ? h - 1 : yy0);
+#pragma unroll
+                for (int c = 0; c < 3; c++) {
+                    const long long val = to_fixed(v[q * 3 + c], k);
+                    if (!val) continue;
+                    if (lds) {
+                        const int wi = (yy - wy0) * ww + (xx - box[m][0]);
+                        atomicAdd(&win[m][wi][c], (unsigned long long)val);
+                    } else {
+                        atomicAdd(&gacc[(size_t)wrap_idx(xx, yy, w, h) * 3 + c],
+                                  (unsigned long long)val);
+                    }
                 }
             }
         }
-    };
-    if (use_irr) add(0, t_irr, g_irr);
-#pragma unroll
-    for (int j = 0; j < 3; j++) {
-        if (pref_on(j)) {
-            const float gi[3] = {gpref[0] * ws[j], gpref[1] * ws[j], gpref[2] * ws[j]};
-            add(1 + li[j], tp[j], gi);
-        }
     }
-    if (use_bg) add(L + 1, t_bg, gh);
     __syncthreads();
     // flush the LDS windows
     for (int j = threadIdx.x; j < n_maps * kWin; j += blockDim.x) {
@@ -783,9 +869,9 @@ __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
         unsigned long long* gacc =
                 m == 0 ? acc_irr : (m <= L ? acc_pref + (size_t)off * 3 : d.acc_env);
         for (int c = 0; c < 3; c++) {
-            const unsigned long long v = win[m][wi][c];
-            if (v) {
-                atomicAdd(&gacc[(size_t)wrap_idx(xx, yy, w, h) * 3 + c], v);
+            const unsigned long long val = win[m][wi][c];
+            if (val) {
+                atomicAdd(&gacc[(size_t)wrap_idx(xx, yy, w, h) * 3 + c], val);
             }
         }
     }
@@ -990,10 +1076,17 @@ __global__ __launch_bounds__(256) void k_pbr_tex_adam(PbrDev d) {
 // the step counter.
 __global__ __launch_bounds__(256) void k_pbr_loss(PbrDev d, uint32_t n_part) {
     __shared__ float red[4];
-    float v = 0.f;
-    for (uint32_t j = threadIdx.x; j < n_part; j += blockDim.x) {
-        v += d.loss_part[j];
+    // 8 independent loads in flight per thread (a single workgroup would
+    // otherwise wait one memory latency per partial)
+    float acc8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (uint32_t j0 = threadIdx.x; j0 < n_part; j0 += 8 * blockDim.x) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t j = j0 + (uint32_t)u * blockDim.x;
+            acc8[u] += j < n_part ? d.loss_part[j] : 0.f;
+        }
     }
+    float v = ((acc8[0] + acc8[1]) + (acc8[2] + acc8[3])) + ((acc8[4] + acc8[5]) + (acc8[6] + acc8[7]));
 #pragma unroll
     for (int s = 32; s >= 1; s >>= 1) {
         v += __shfl_xor(v, s);
@@ -1223,7 +1316,7 @@ int dressi_pbr_create(dressi_ctx* ctx, const dressi_pbr_desc* desc, dressi_pbr_p
                            (uint64_t)desc->tex_w * desc->tex_h < (1ull << 28),
                    "bad texture size");
     DRESSI_REQUIRE(desc->env_w > 0 && desc->env_h > 0 &&
-                           (uint64_t)desc->env_w * desc->env_h < (1ull << 26),
+                           desc->env_w < 8192 && desc->env_h < 8192,
                    "bad env size");
     DRESSI_REQUIRE(desc->levels >= 2 && desc->levels <= kPbrMaxLevels,
                    "levels must be in [2, %u]", kPbrMaxLevels);
