@@ -1,7 +1,7 @@
 """Benchmark of the fused silhouette-fit iteration (fwd + bwd + Adam) on one
 MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--workload c4_hsr|c4|c3|c2|c1]
+    python bench.py [--steps K] [--warmup W] [--workload c4_hsr|c4|c5|c3|c2|c1]
 
 A step is one iteration of the silhouette fit. HardSoftRas (c4_hsr, c2, c1):
 per view clip transform, SoftClip, tile-binned RasterizeSoft, the per-pixel
@@ -12,7 +12,11 @@ mask + L2 loss image, the stochastic AntiAliasBwdVtx gather, ColSum +
 clip->pos chain, Adam. Texture (c3): per view clip transform + ScreenAttr,
 hard raster of face ids, g_uv / g_mask interpolation and bilinear samples of
 the texture and the target texture + RGB L2 loss image, then per texel the
-inverse-UV gather of every view and Adam. One hipGraph launch per step. Inputs (mesh, Adam
+inverse-UV gather of every view and Adam. PBR / IBL (c5): the env's pooling
+chain, IrradianceConv + 6 PrefilterConv levels, per pixel the split-sum
+shading forward + L1 loss + backward with the map gradients scattered in
+fixed point, the convolutions' transposes, the static texture gather list,
+Adam on albedo / mr / env. One hipGraph launch per step. Inputs (mesh, Adam
 state, target images) are resident in HBM before the timed region. Prints
 ONE JSON line.
 """
@@ -91,6 +95,45 @@ def kernel_bytes_tex(n_views: int, s: int, n_faces: int, n_verts: int, texels: i
         "k_aa_raster": n * (4.0 * S2 + 36.0 * F),
         "k_tex_fwd": n * 28.0 * S2 + 16.0 * S2 + 32.0 * T,
         "k_tex_bwd_adam": n * 24.0 * S2 + 112.0 * T,
+    }
+
+
+def iteration_bytes_pbr(n_views: int, s: int, n_faces: int, n_verts: int, texels: int,
+                        env_texels: int) -> float:
+    """Compulsory bytes of one PBR / IBL iteration (per pixel and view: the
+    precomputed target RGB, the G-buffer and the material gradient; the loss;
+    per material texel: albedo + mr read and written, their Adam state and
+    gradient; per env texel: env, Adam state, gradient)."""
+    return (n_views * (28.0 * s * s + 12.0 * n_faces + 76.0 * n_verts) + 4.0 * s * s
+            + 200.0 * texels + 120.0 * env_texels)
+
+
+def kernel_bytes_pbr(n_views: int, s: int, texels: int, env_texels: int, pooled: int,
+                     map_texels: int) -> dict:
+    """Algorithmic bytes per launch of the PBR-plan kernels.
+
+    pool:      env read (12 B/texel), pooled sources written (12 B/texel)
+    conv_fwd:  pooled sources read, irradiance + prefilter maps written
+    shade:     per pixel and view the target RGB (12 B) and the G-buffer the
+               shading needs (material uv, normal, position: 16 B packed):
+               28 B; its per-pixel material gradient is counted in tex_adam
+    resolve:   map gradients (24 B/texel in, 12 B out)
+    conv_bwd:  map gradients read, source gradients written
+    env_adam:  background gradient, source gradients, env + m + v in and out
+    tex_adam:  per-pixel material gradients (20 B/pixel) gathered once,
+               albedo + mr with their Adam state in and out (96 B/texel)
+    loss:      one partial per workgroup
+    """
+    n, S2, T, E = n_views, float(s) * s, float(texels), float(env_texels)
+    return {
+        "k_pbr_pool": 12.0 * E + 12.0 * pooled,
+        "k_pbr_conv_fwd": 12.0 * pooled + 12.0 * map_texels,
+        "k_pbr_shade": n * 28.0 * S2,
+        "k_pbr_resolve": 36.0 * map_texels,
+        "k_pbr_conv_bwd": 12.0 * map_texels + 12.0 * pooled,
+        "k_pbr_env_adam": 24.0 * E + 72.0 * E,
+        "k_pbr_tex_adam": n * 20.0 * S2 + 96.0 * T,
+        "k_pbr_loss": 4.0 * n * S2 / 256.0,
     }
 
 
@@ -174,6 +217,33 @@ def cpu_baseline_tex(workload) -> dict:
                        f"{cpu_info()}, nproc {os.cpu_count()}")}
 
 
+def cpu_baseline_pbr(workload) -> dict:
+    """The oracle's PBR / IBL fit (single thread) on a bounded sample: ONE of
+    the workload's views at full resolution with the full maps, timed for 1
+    and for 2 iterations; the difference is one iteration of that view
+    (set-up excluded), scaled to all views (this counts the view-independent
+    env convolutions once per view, so it understates the CPU rate)."""
+    from opendressi_amd.pbr import workload_scene
+    from oracle.pyoracle import ORACLE_SO, Oracle, build
+    if not os.path.exists(ORACLE_SO):
+        build()
+    sc = workload_scene(workload)
+    sc1 = dict(sc, mvps=sc["mvps"][:1], frames=sc["frames"][:1])
+    o = Oracle()
+    times = []
+    for iters in (1, 2):
+        t0 = time.perf_counter()
+        o.pbr_fit(sc1, iters=iters, want_images=False)
+        times.append(time.perf_counter() - t0)
+    dt = max(times[1] - times[0], 1e-9)
+    n = len(sc["mvps"])
+    return {"value": 1.0 / (dt * n), "unit": "iterations/s", "cores": 1, "kind": "port",
+            "sample": (f"1 of {n} views at {workload.screen}^2, {workload.tex}^2 textures, "
+                       f"{workload.env_w}x{workload.env_h} env: 1 and 2 iterations "
+                       f"({times[0]:.1f} s, {times[1]:.1f} s), difference scaled x{n}; host "
+                       f"CPU: {cpu_info()}, nproc {os.cpu_count()}")}
+
+
 def cpu_baseline(workload) -> dict:
     """The oracle (C restatement of the reference CPU evaluator, single
     thread) on a bounded sample: one iteration of ONE of the workload's views
@@ -218,9 +288,13 @@ def main() -> int:
     import opendressi_amd as od
     ctx = od.Context(0)
     tex = args.workload in od.TEX_WORKLOADS
+    pbr = args.workload in od.PBR_WORKLOADS
     if tex:
         w = od.TEX_WORKLOADS[args.workload]
         fit = od.TextureFit.from_workload(ctx, args.workload)
+    elif pbr:
+        w = od.PBR_WORKLOADS[args.workload]
+        fit = od.PbrFit.from_workload(ctx, args.workload)
     else:
         w = od.WORKLOADS[args.workload]
         fit = od.SilhouetteFit.from_workload(ctx, args.workload)
@@ -239,7 +313,15 @@ def main() -> int:
     prof = fit.profile(args.profile_iters)
     dom = max(prof, key=prof.get)
     dom_us = prof[dom]
-    if tex:
+    if pbr:
+        texels, envt = fit.tex_w * fit.tex_h, fit.env_w * fit.env_h
+        kbytes = kernel_bytes_pbr(nviews, s, texels, envt, fit.pooled_texels, fit.map_texels)
+        ibytes = iteration_bytes_pbr(nviews, s, nf, nv, texels, envt)
+        desc = (f"{w.name}: PBR/IBL material + env fit, {s}x{s} x {nviews} views, icosphere "
+                f"L{w.level} ({nv} v / {nf} f) with equirect uv, {fit.tex_w}x{fit.tex_h} albedo "
+                f"+ metallic-roughness, {fit.env_w}x{fit.env_h} env, {fit.levels} prefilter "
+                f"levels, LUT 256^2, L1, Adam lr {w.lr}")
+    elif tex:
         texels = fit.tex_w * fit.tex_h
         kbytes = kernel_bytes_tex(nviews, s, nf, nv, texels)
         ibytes = iteration_bytes_tex(nviews, s, nf, nv, texels)
@@ -287,7 +369,8 @@ def main() -> int:
         "loss_after": loss_end,
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline_tex(w) if tex else cpu_baseline(w)
+        line["cpu_baseline"] = (cpu_baseline_pbr(w) if pbr else
+                                cpu_baseline_tex(w) if tex else cpu_baseline(w))
     print(json.dumps(line), flush=True)
     ctx.close()
     if args.copy_mb > 0:

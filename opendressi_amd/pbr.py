@@ -163,6 +163,7 @@ class PbrFit:
         self.tex_h, self.tex_w = a["gt_albedo"].shape[:2]
         self.env_h, self.env_w = a["gt_env"].shape[:2]
         self.levels = int(a["levels"])
+        self.n_verts, self.n_faces = len(a["pos"]), len(a["faces"])
         d = _lib.PbrDesc(len(a["pos"]), len(a["faces"]), self.n_views, self.screen, self.screen,
                          self.tex_w, self.tex_h, self.env_w, self.env_h, self.levels,
                          float(a["lr"]), 0.9, 0.999, 1e-8,
@@ -228,6 +229,25 @@ class PbrFit:
         check(lib.dressi_pbr_read(self.handle, which, out.ctypes.data_as(C.c_void_p),
                                   out.nbytes))
         return out
+
+    @property
+    def pooled_texels(self) -> int:
+        """Texels of the pooled env levels (the irradiance and prefilter sources)."""
+        w, h, n = self.env_w, self.env_h, 0
+        while w > 64 or h > 32:
+            w, h = (w + 1) // 2, (h + 1) // 2
+            n += w * h
+        return n
+
+    @property
+    def map_texels(self) -> int:
+        """Texels of the irradiance map and every prefiltered level."""
+        w, h = min(128, self._psrc()[0]), min(64, self._psrc()[1])
+        n = 32 * 16
+        for _ in range(self.levels):
+            n += w * h
+            w, h = max(w // 2, 1), max(h // 2, 1)
+        return n
 
     def _psrc(self):
         w, h = self.env_w, self.env_h
