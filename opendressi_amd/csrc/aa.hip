@@ -923,39 +923,42 @@ __global__ __launch_bounds__(256) void k_aa_face_bwd(HsrDev d) {
 
 // ColSum of the (vertex, slot) rows per view -- the row of slot d is the
 // accumulator of face vf[d][v] at the corner holding v; padding rows are
-// zero -- then the shared clip->pos chain and Adam; the last workgroup
-// advances t.
+// zero -- then the shared clip->pos chain and Adam: one lane per (vertex,
+// view) for the ColSum, the vertex's first lane for the rest; the last
+// workgroup advances t.
 template <int NV>
 __global__ __launch_bounds__(256) void k_aa_vertex_adam(HsrDev d) {
-    const uint32_t vtx = blockIdx.x * blockDim.x + threadIdx.x;
-    const float t = *d.t;
-    if (vtx < d.n_verts) {
-        float gc[NV][4];
+    vertex_views_adam<NV>(d, [&](uint32_t vtx, uint32_t view, float (&g4)[4]) {
+        const float4* gt = d.gtri + (size_t)view * 3 * d.g.n_faces;
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (uint32_t d0 = 0; d0 < d.max_deg; d0 += kDegBatch) {
+            AdjBatch ab;
+            load_adjacency(d, vtx, d0, ab);
+            float4 gg[kDegBatch];
 #pragma unroll
-        for (int view = 0; view < NV; view++) {
-            const float4* gt = d.gtri + (size_t)view * 3 * d.g.n_faces;
-            float acc[4] = {0.f, 0.f, 0.f, 0.f};
-            for (uint32_t dd = 0; dd < d.max_deg; dd++) {
-                const int32_t f = d.vf[(size_t)dd * d.n_verts + vtx];
-                if (f < 0) {
-                    continue;  // a zero row: adding +0 leaves the sum unchanged
+            for (int i = 0; i < kDegBatch; i++) {
+                gg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (ab.f[i] >= 0) {
+                    gg[i] = gt[(size_t)first_corner(ab.mask[i]) * d.g.n_faces + ab.f[i]];
                 }
-                const uint32_t mask = d.vf_mask[(size_t)dd * d.n_verts + vtx];
-                const int k = (mask & 1u) ? 0 : ((mask & 2u) ? 1 : 2);
-                const float4 gg = gt[(size_t)k * d.g.n_faces + f];
-                acc[0] += gg.x;
-                acc[1] += gg.y;
-                acc[2] += gg.z;
-                acc[3] += gg.w;
             }
+            // in slot order; a padding row is zero (adding +0 leaves the sum
+            // unchanged, so it is skipped)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                gc[view][r] = acc[r];
+            for (int i = 0; i < kDegBatch; i++) {
+                if (ab.f[i] >= 0) {
+                    acc[0] += gg[i].x;
+                    acc[1] += gg[i].y;
+                    acc[2] += gg[i].z;
+                    acc[3] += gg[i].w;
+                }
             }
         }
-        pos_grad_adam<NV>(d, vtx, gc, t);
-    }
-    advance_t(d, t);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            g4[r] = acc[r];
+        }
+    });
 }
 
 const char* const kAaKernelNames[kAaKernels] = {"k_aa_setup", "k_aa_raster", "k_aa_fwd",
@@ -988,8 +991,7 @@ int launch_aa_kernel(const HsrDev& d, hipStream_t s, int k) {
             return launch_aa_raster(d, s);
         case 2:
         case 4: {
-            const dim3 grid = k == 2 ? dim3(div_up(g.width, 256), g.height)
-                                     : dim3(div_up(d.n_verts, 256));
+            const dim3 grid = dim3(div_up(g.width, 256), g.height);
             const bool vec = (g.width & 3u) == 0;
             switch (g.n_views) {
 #define DRESSI_NV(N)                                                                      \
@@ -1001,7 +1003,8 @@ int launch_aa_kernel(const HsrDev& d, hipStream_t s, int k) {
                 hipLaunchKernelGGL((k_aa_fwd<N, false>), grid, dim3(64 * N), 0, s, d);    \
             }                                                                             \
         } else {                                                                          \
-            hipLaunchKernelGGL(k_aa_vertex_adam<N>, grid, dim3(256), 0, s, d);            \
+            hipLaunchKernelGGL(k_aa_vertex_adam<N>, dim3(vertex_grid<N>(d.n_verts)),       \
+                               dim3(256), 0, s, d);                                        \
         }                                                                                 \
         break;
                 DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)

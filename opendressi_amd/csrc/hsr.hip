@@ -10,6 +10,9 @@
 
 namespace dressi {
 
+// Samples of FaceFetchBwd whose face-id loads are issued together.
+constexpr int kSampleBatch = 8;
+
 // SoftClip + RasterizeSoft setup per (view, face), appended to the soft bins.
 __global__ __launch_bounds__(256) void k_hsr_setup(HsrDev d) {
     __shared__ BinLds blds;
@@ -57,9 +60,9 @@ __global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
     const int py = by + (lane >> 3);
     const size_t vf = (size_t)view * d.g.n_faces;
     const BinView bv = bin_view(d.bins, view * d.g.n_tiles + tile, d.g.n_faces);
-    __shared__ uint32_t later[kSoftBinCap];
+    __shared__ ResolveLds lds;
     const PixelBest best = resolve_block(d.recs + vf, d.cull + vf, bv, bx, by, d.radius, nullptr,
-                                         d.g.width, later);
+                                         d.g.width, lds);
     if (px < (int)d.g.width && py < (int)d.g.height) {
         uint32_t id = 0;
         if (best.key != kEmptyKey) {
@@ -83,14 +86,48 @@ __global__ __launch_bounds__(256) void k_hsr_loss(HsrDev d) {
     const size_t npx = (size_t)d.g.width * d.g.height;
     const size_t o = (size_t)y * d.g.width + x;
     const float W = (float)d.g.width, H = (float)d.g.height;
+    // every view's face id and target first, then the corner vertices of the
+    // rim winners, then their positions: each round of loads in flight together
+    uint32_t id[NV];
+    float tg[NV];
+#pragma unroll
+    for (int view = 0; view < NV; view++) {
+        id[view] = d.ids[view * npx + o];
+        tg[view] = d.targets[view * npx + o];
+    }
+    int32_t vi[NV][3];
+#pragma unroll
+    for (int view = 0; view < NV; view++) {
+        const bool rim = (id[view] & kRimFlag) != 0;
+        const uint32_t f = rim ? (id[view] & ~kRimFlag) - 1 : 0u;
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            vi[view][k] = rim ? d.faces[f * 3 + k] : 0;
+        }
+    }
+    float pp[NV][3][3];
+#pragma unroll
+    for (int view = 0; view < NV; view++) {
+        const bool rim = (id[view] & kRimFlag) != 0;
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+#pragma unroll
+            for (int c = 0; c < 3; c++) {
+                pp[view][k][c] = rim ? d.pos[vi[view][k] * 3 + c] : 0.f;
+            }
+        }
+    }
     float lv[NV][1];
 #pragma unroll
     for (int view = 0; view < NV; view++) {
-        const uint32_t id = d.ids[view * npx + o];
-        float pred = id ? 1.f : 0.f;
-        if (id & kRimFlag) {
+        float pred = id[view] ? 1.f : 0.f;
+        if (id[view] & kRimFlag) {
+            const float* m = d.mvps + view * 16;
             float4 c[3];
-            face_clips(d, view, (id & ~kRimFlag) - 1, c);
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                c[k] = mvp_transform(m, pp[view][k][0], pp[view][k][1], pp[view][k][2]);
+            }
             PixelFw st;
             pixel_fw(c, 1.f, -1.f, 1.f, (float)x + 0.5f, (float)y + 0.5f, W, H, d.sigma_scale,
                      st);
@@ -99,7 +136,7 @@ __global__ __launch_bounds__(256) void k_hsr_loss(HsrDev d) {
         if (d.pred) {
             d.pred[view * npx + o] = pred;
         }
-        const float diff = d.targets[view * npx + o] - pred;
+        const float diff = tg[view] - pred;
         lv[view][0] = diff * diff * d.inv_px;
     }
     float out[1];
@@ -144,41 +181,70 @@ __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
         const size_t npx = (size_t)d.g.width * d.g.height;
         const uint32_t* ids = d.ids + view * npx;
         const float* tgt = d.targets + view * npx;
-        for (uint32_t smp = 0; smp < d.n_samples; smp++) {
-            const int e = (int)(smp % 3);
-            const float* a = s[e];
-            const float* b = s[(e + 1) % 3];
-            const float ex = b[0] - a[0];
-            const float ey = b[1] - a[1];
-            const float len = sqrtf(ex * ex + ey * ey);
-            if (len < 1e-6f) {
-                continue;
-            }
-            const float u = hash_to_unit(f, smp, seed_u, 0);
-            const float off = (hash_to_unit(f, smp, seed_u, 1) * 2.f - 1.f) * d.radius;
-            const float spx = a[0] + u * ex - off * (ey / len);
-            const float spy = a[1] + u * ey + off * (ex / len);
-            const int ix = (int)floorf(spx);
-            const int iy = (int)floorf(spy);
-            if (ix < 0 || iy < 0 || ix >= (int)d.g.width || iy >= (int)d.g.height) {
-                continue;
-            }
-            const size_t p = (size_t)iy * d.g.width + ix;
-            const uint32_t id = ids[p];
-            if (id != ((f + 1) | kRimFlag)) {
-                continue;  // other face, or a hard-branch winner (zero gradient)
-            }
-            const float pcx = (float)ix + 0.5f, pcy = (float)iy + 0.5f;
-            PixelFw st;
-            pixel_fw(c, 1.f, -1.f, 1.f, pcx, pcy, W, H, d.sigma_scale, st);
-            float4 g[3];
-            pixel_bw(st, c, 1.f, tgt[p], d.inv_px, W, H, d.sigma_scale, g);
+        const uint32_t want = (f + 1) | kRimFlag;
+        // samples in batches of kSampleBatch: every sample's pixel first, then
+        // their face-id loads together, then the hits in sample order
+        for (uint32_t s0 = 0; s0 < d.n_samples; s0 += kSampleBatch) {
+            int64_t pix[kSampleBatch];
 #pragma unroll
-            for (int k = 0; k < 3; k++) {
-                acc[k].x += g[k].x;
-                acc[k].y += g[k].y;
-                acc[k].z += g[k].z;
-                acc[k].w += g[k].w;
+            for (int i = 0; i < kSampleBatch; i++) {
+                pix[i] = -1;
+                const uint32_t smp = s0 + (uint32_t)i;
+                if (smp >= d.n_samples) {
+                    continue;
+                }
+                const int e = (int)(smp % 3);
+                const float* a = s[e];
+                const float* b = s[(e + 1) % 3];
+                const float ex = b[0] - a[0];
+                const float ey = b[1] - a[1];
+                const float len = sqrtf(ex * ex + ey * ey);
+                if (len < 1e-6f) {
+                    continue;
+                }
+                const float u = hash_to_unit(f, smp, seed_u, 0);
+                const float off = (hash_to_unit(f, smp, seed_u, 1) * 2.f - 1.f) * d.radius;
+                const float spx = a[0] + u * ex - off * (ey / len);
+                const float spy = a[1] + u * ey + off * (ex / len);
+                const int ix = (int)floorf(spx);
+                const int iy = (int)floorf(spy);
+                if (ix < 0 || iy < 0 || ix >= (int)d.g.width || iy >= (int)d.g.height) {
+                    continue;
+                }
+                pix[i] = (int64_t)iy * d.g.width + ix;
+            }
+            uint32_t id[kSampleBatch];
+#pragma unroll
+            for (int i = 0; i < kSampleBatch; i++) {
+                id[i] = pix[i] >= 0 ? ids[pix[i]] : 0u;
+            }
+            // other faces and hard-branch winners (zero gradient) are skipped
+            uint32_t hits = 0;
+#pragma unroll
+            for (int i = 0; i < kSampleBatch; i++) {
+                hits |= (id[i] == want ? 1u : 0u) << i;
+            }
+            while (hits) {
+                const int i = __builtin_ctz(hits);
+                hits &= hits - 1;
+                int64_t p = 0;
+#pragma unroll
+                for (int j = 0; j < kSampleBatch; j++) {
+                    p = j == i ? pix[j] : p;
+                }
+                const int ix = (int)(p % d.g.width), iy = (int)(p / d.g.width);
+                const float pcx = (float)ix + 0.5f, pcy = (float)iy + 0.5f;
+                PixelFw st;
+                pixel_fw(c, 1.f, -1.f, 1.f, pcx, pcy, W, H, d.sigma_scale, st);
+                float4 g[3];
+                pixel_bw(st, c, 1.f, tgt[p], d.inv_px, W, H, d.sigma_scale, g);
+#pragma unroll
+                for (int k = 0; k < 3; k++) {
+                    acc[k].x += g[k].x;
+                    acc[k].y += g[k].y;
+                    acc[k].z += g[k].z;
+                    acc[k].w += g[k].w;
+                }
             }
         }
     }
@@ -188,53 +254,62 @@ __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
     }
 }
 
-// LookupFacesBwd x3 + clip->pos chain over all views + Adam, one thread per
-// vertex. The last workgroup to finish advances t (all reads of t precede
-// every workgroup's arrival on the counter).
+// LookupFacesBwd x3 + clip->pos chain over all views + Adam: one lane per
+// (vertex, view) gathers that view's corner gradients (the adjacency rows of
+// a batch of kDegBatch slots loaded together, then their gradients), the
+// vertex's first lane sums the views and steps Adam. The last workgroup to
+// finish advances t (all reads of t precede every workgroup's arrival on the
+// counter).
 template <int NV>
 __global__ __launch_bounds__(256) void k_hsr_vertex_adam(HsrDev d) {
-    const uint32_t vtx = blockIdx.x * blockDim.x + threadIdx.x;
-    const float t = *d.t;
-    if (vtx < d.n_verts) {
-        float gc[NV][4];
+    vertex_views_adam<NV>(d, [&](uint32_t vtx, uint32_t view, float (&g4)[4]) {
+        const float4* gt = d.gtri + (size_t)view * 3 * d.g.n_faces;
+        float lfb[3][4];
 #pragma unroll
-        for (int view = 0; view < NV; view++) {
-            const float4* gt = d.gtri + (size_t)view * 3 * d.g.n_faces;
-            float lfb[3][4];
+        for (int k = 0; k < 3; k++) {
+            lfb[k][0] = lfb[k][1] = lfb[k][2] = lfb[k][3] = 0.f;
+        }
+        for (uint32_t d0 = 0; d0 < d.max_deg; d0 += kDegBatch) {
+            AdjBatch ab;
+            load_adjacency(d, vtx, d0, ab);
+            float4 gg[kDegBatch];
 #pragma unroll
-            for (int k = 0; k < 3; k++) {
-                lfb[k][0] = lfb[k][1] = lfb[k][2] = lfb[k][3] = 0.f;
+            for (int i = 0; i < kDegBatch; i++) {
+                gg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (ab.f[i] >= 0) {
+                    gg[i] = gt[(size_t)first_corner(ab.mask[i]) * d.g.n_faces + ab.f[i]];
+                }
             }
-            for (uint32_t dd = 0; dd < d.max_deg; dd++) {
-                const int32_t f = d.vf[(size_t)dd * d.n_verts + vtx];
-                if (f < 0) {
+#pragma unroll
+            for (int i = 0; i < kDegBatch; i++) {
+                if (ab.f[i] < 0) {
                     continue;
                 }
-                const uint32_t mask = d.vf_mask[(size_t)dd * d.n_verts + vtx];
+                const int k0 = first_corner(ab.mask[i]);
 #pragma unroll
                 for (int k = 0; k < 3; k++) {
-                    if (mask & (1u << k)) {
-                        const float4 gg = gt[(size_t)k * d.g.n_faces + f];
-                        lfb[k][0] += gg.x;
-                        lfb[k][1] += gg.y;
-                        lfb[k][2] += gg.z;
-                        lfb[k][3] += gg.w;
+                    if (ab.mask[i] & (1u << k)) {
+                        // a face holding the vertex at two corners (degenerate)
+                        // reloads the other corner's gradient
+                        const float4 g = k == k0 ? gg[i] : gt[(size_t)k * d.g.n_faces + ab.f[i]];
+                        lfb[k][0] += g.x;
+                        lfb[k][1] += g.y;
+                        lfb[k][2] += g.z;
+                        lfb[k][3] += g.w;
                     }
                 }
             }
-            // clip_v gradient: LookupFaces 2, 1, 0 (newest first), one 3-ary sum
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                float acc = 0.f;
-                acc += lfb[2][r];
-                acc += lfb[1][r];
-                acc += lfb[0][r];
-                gc[view][r] = acc;
-            }
         }
-        pos_grad_adam<NV>(d, vtx, gc, t);
-    }
-    advance_t(d, t);
+        // clip_v gradient: LookupFaces 2, 1, 0 (newest first), one 3-ary sum
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float acc = 0.f;
+            acc += lfb[2][r];
+            acc += lfb[1][r];
+            acc += lfb[0][r];
+            g4[r] = acc;
+        }
+    });
 }
 
 // Per-op kernels ------------------------------------------------------------
@@ -445,8 +520,8 @@ int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
             switch (g.n_views) {
 #define DRESSI_NV(N)                                                                          \
     case N:                                                                                   \
-        hipLaunchKernelGGL(k_hsr_vertex_adam<N>, dim3(div_up(d.n_verts, 256)), dim3(256), 0,  \
-                           s, d);                                                             \
+        hipLaunchKernelGGL(k_hsr_vertex_adam<N>, dim3(vertex_grid<N>(d.n_verts)), dim3(256),  \
+                           0, s, d);                                                          \
         break;
                 DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
                 DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)

@@ -156,13 +156,21 @@ __device__ __forceinline__ void pos_grad_adam(const HsrDev& d, uint32_t vtx,
         bc2 = 1.f - powf(d.b2, t_new);
     }
     const float cb1 = 1.f - d.b1, cb2 = 1.f - d.b2;
+    float m0[3], v0[3], p0[3];
 #pragma unroll
     for (int c = 0; c < 3; c++) {
         const size_t j = (size_t)vtx * 3 + c;
-        const float m_new = d.m[j] * d.b1 + g[c] * cb1;
-        const float v_new = d.v[j] * d.b2 + g[c] * g[c] * cb2;
+        m0[c] = d.m[j];
+        v0[c] = d.v[j];
+        p0[c] = d.pos[j];
+    }
+#pragma unroll
+    for (int c = 0; c < 3; c++) {
+        const size_t j = (size_t)vtx * 3 + c;
+        const float m_new = m0[c] * d.b1 + g[c] * cb1;
+        const float v_new = v0[c] * d.b2 + g[c] * g[c] * cb2;
         const float step = (m_new / bc1) / (sqrtf(v_new / bc2) + d.eps) * d.lr;
-        d.pos[j] = d.pos[j] - step;
+        d.pos[j] = p0[c] - step;
         d.m[j] = m_new;
         d.v[j] = v_new;
     }
@@ -182,6 +190,78 @@ __device__ __forceinline__ void advance_t(const HsrDev& d, float t) {
         *d.t = t + 1.f;
         *d.done = 0;
     }
+}
+
+// A batch of kDegBatch adjacency slots of one vertex (VertexFacesTex rows
+// d0 .. d0 + kDegBatch - 1; -1 = padding or beyond max_deg), loaded
+// together so that their latencies overlap.
+constexpr int kDegBatch = 8;
+struct AdjBatch {
+    int32_t f[kDegBatch];
+    uint32_t mask[kDegBatch];
+};
+
+__device__ __forceinline__ void load_adjacency(const HsrDev& d, uint32_t vtx, uint32_t d0,
+                                               AdjBatch& ab) {
+#pragma unroll
+    for (int i = 0; i < kDegBatch; i++) {
+        const uint32_t dd = d0 + (uint32_t)i;
+        const bool in = dd < d.max_deg;
+        const size_t o = (size_t)(in ? dd : 0u) * d.n_verts + vtx;
+        const int32_t f = d.vf[o];
+        const uint32_t m = d.vf_mask[o];
+        ab.f[i] = in ? f : -1;
+        ab.mask[i] = in ? m : 0u;
+    }
+}
+
+// The first corner (0, 1, 2) whose bit is set in an adjacency corner mask.
+__device__ __forceinline__ int first_corner(uint32_t mask) {
+    return (mask & 1u) ? 0 : ((mask & 2u) ? 1 : 2);
+}
+
+// Lanes per vertex of the vertex kernels: the NV views of one vertex run on
+// L = next power of two >= NV adjacent lanes, so the per-view adjacency
+// gathers (the latency of the kernel) are spread over NV lanes.
+template <int NV>
+struct VertexLanes {
+    static constexpr int L = NV <= 1 ? 1 : NV <= 2 ? 2 : NV <= 4 ? 4 : 8;
+};
+
+template <int NV>
+inline uint32_t vertex_grid(uint32_t n_verts) {
+    return (uint32_t)(((uint64_t)n_verts * VertexLanes<NV>::L + 255) / 256);
+}
+
+// Body of both vertex kernels (blockDim.x = 256, grid vertex_grid<NV>):
+// lane (vertex, view) computes that view's clip gradient g4 through
+// `view_grad(vtx, view, g4)`; the vertex's first lane collects the NV
+// gradients (shuffles) and runs pos_grad_adam; the last workgroup advances t.
+template <int NV, typename ViewGrad>
+__device__ __forceinline__ void vertex_views_adam(const HsrDev& d, ViewGrad&& view_grad) {
+    constexpr int L = VertexLanes<NV>::L;
+    const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t vtx = gid / L;
+    const uint32_t view = gid % L;
+    const float t = *d.t;
+    const bool live = vtx < d.n_verts;
+    float g4[4] = {0.f, 0.f, 0.f, 0.f};
+    if (live && view < NV) {
+        view_grad(vtx, view, g4);
+    }
+    const int base = (int)(threadIdx.x & 63u) & ~(L - 1);
+    float gc[NV][4];
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            gc[v][r] = __shfl(g4[r], base + v);
+        }
+    }
+    if (live && view == 0) {
+        pos_grad_adam<NV>(d, vtx, gc, t);
+    }
+    advance_t(d, t);
 }
 
 // Launches kernel k (0 .. kAaKernels - 1) of one AA-technique iteration

@@ -312,9 +312,9 @@ __global__ __launch_bounds__(64) void k_raster_soft_op(RasterGeom g, const SoftR
     const int px = blk.bx + (lane & 7);
     const int py = blk.by + (lane >> 3);
     const BinView bv = bin_view(b, blk.tile, g.n_faces);
-    __shared__ uint32_t later[kSoftBinCap];
+    __shared__ ResolveLds lds;
     const PixelBest best =
-            resolve_block(recs, cull, bv, blk.bx, blk.by, radius, prev, g.width, later);
+            resolve_block(recs, cull, bv, blk.bx, blk.by, radius, prev, g.width, lds);
     if (px >= (int)g.width || py >= (int)g.height) {
         return;
     }

@@ -436,19 +436,16 @@ __device__ __forceinline__ bool edges_reach_block(const float* w, int bx, int by
     return hit;
 }
 
-// Separating-axis test of the soft triangle against the 8x8 block along its
-// three edge normals, with the record's soft margin: false only when no
-// pixel centre of the block can be covered (per lane, one face per lane).
-__device__ __forceinline__ bool soft_reaches_block(const SoftRec* rec, int bx, int by) {
-    const float m = rec->s_margin;
+// Separating-axis test of the soft triangle (corners x[k], y[k], orientation
+// sign of s_inv_area) against the 8x8 block along its three edge normals,
+// with the record's soft margin m: false only when no pixel centre of the
+// block can be covered (per lane, one face per lane).
+__device__ __forceinline__ bool soft_reaches_block(const float (&x)[3], const float (&y)[3],
+                                                   float s_inv_area, float m, int bx, int by) {
     if (!(m >= 0.f)) {
         return true;
     }
-    const float4 a = *(const float4*)&rec->sx[0];  // sx0 sx1 sx2 sy0
-    const float2 b = *(const float2*)&rec->sy[1];  // sy1 sy2
-    const float x[3] = {a.x, a.y, a.z};
-    const float y[3] = {a.w, b.x, b.y};
-    const float s = rec->s_inv_area > 0.f ? 1.f : -1.f;
+    const float s = s_inv_area > 0.f ? 1.f : -1.f;
     const float x0 = (float)bx + 0.5f, x1 = (float)bx + 7.5f;
     const float y0 = (float)by + 0.5f, y1 = (float)by + 7.5f;
     bool hit = true;
@@ -470,32 +467,65 @@ __device__ __forceinline__ bool box_hits(int x0, int y0, int x1, int y1, int bx,
     return x0 <= bx + 7 && x1 >= bx && y0 <= by + 7 && y1 >= by;
 }
 
-// The face takes part in phase A for the block: its soft bbox and A-box meet
-// the block and its edges do not separate it (per lane, one face per lane).
-// `soft` = also test the soft bbox (phase B has tested it already).
-__device__ __forceinline__ bool block_in_a(const SoftRec* recs, const CullRec* cull, uint32_t f,
-                                           int bx, int by, bool soft, bool* pos = nullptr) {
-    const CullRec c = cull[f];
-    if (soft && !box_hits(c.sx0, c.sy0, c.sx1, c.sy1, bx, by)) {
-        return false;
-    }
-    if (!box_hits(c.ax0, c.ay0, c.ax1, c.ay1, bx, by)) {
-        return false;
-    }
-    const float4* q = (const float4*)(recs + f);
+// What the block culls read of one face, loaded together (one round trip):
+// the cull record, the record's first 16 words (edge functions, orientation,
+// flags, hard-branch margin) and, for phase B, the soft triangle and its
+// coverage margin.
+struct CullLoad {
+    CullRec c;
     float w[16];
+    float sx[3], sy[3], s_margin;
+};
+
+template <bool kSoft>
+__device__ __forceinline__ CullLoad load_cull(const SoftRec* recs, const CullRec* cull,
+                                              uint32_t f) {
+    CullLoad l;
+    l.c = cull[f];
+    const float4* q = (const float4*)(recs + f);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const float4 v = q[i];
-        w[4 * i + 0] = v.x;
-        w[4 * i + 1] = v.y;
-        w[4 * i + 2] = v.z;
-        w[4 * i + 3] = v.w;
+        l.w[4 * i + 0] = v.x;
+        l.w[4 * i + 1] = v.y;
+        l.w[4 * i + 2] = v.z;
+        l.w[4 * i + 3] = v.w;
     }
-    if (pos) {
-        *pos = w[12] > 0.f;  // sign of 1 / (2 hard area)
+    if (kSoft) {
+        const float4 a = *(const float4*)&recs[f].sx[0];  // sx0 sx1 sx2 sy0
+        const float2 b = *(const float2*)&recs[f].sy[1];  // sy1 sy2
+        l.sx[0] = a.x;
+        l.sx[1] = a.y;
+        l.sx[2] = a.z;
+        l.sy[0] = a.w;
+        l.sy[1] = b.x;
+        l.sy[2] = b.y;
+        l.s_margin = recs[f].s_margin;
     }
-    return edges_reach_block(w, bx, by);
+    return l;
+}
+
+// The face takes part in phase A for the block: its A-box (and, with
+// `soft`, its soft bbox) meets the block and its edges do not separate it
+// (per lane, one face per lane).
+__device__ __forceinline__ bool cull_in_a(const CullLoad& l, int bx, int by, bool soft) {
+    if (soft && !box_hits(l.c.sx0, l.c.sy0, l.c.sx1, l.c.sy1, bx, by)) {
+        return false;
+    }
+    if (!box_hits(l.c.ax0, l.c.ay0, l.c.ax1, l.c.ay1, bx, by)) {
+        return false;
+    }
+    return edges_reach_block(l.w, bx, by);
+}
+
+// Sign of 1 / (2 hard area) of a loaded face: the faces with a positive
+// one are deferred by phase A.
+__device__ __forceinline__ bool cull_pos(const CullLoad& l) { return l.w[12] > 0.f; }
+
+// The soft triangle of a loaded face can cover a pixel centre of the block.
+__device__ __forceinline__ bool cull_soft(const CullLoad& l, int bx, int by) {
+    return box_hits(l.c.sx0, l.c.sy0, l.c.sx1, l.c.sy1, bx, by) &&
+           soft_reaches_block(l.sx, l.sy, l.w[14], l.s_margin, bx, by);
 }
 
 // Number of list entries of a bin and whether it overflowed (then every face
@@ -572,6 +602,51 @@ __device__ __forceinline__ SoftRec load_rec_uniform(const SoftRec* recs, uint32_
     return u.r;
 }
 
+// LDS of one resolving wave: survivor records staged per batch and the
+// deferred (back) faces of phase A.
+constexpr int kStage = 16;
+constexpr uint32_t kLaterCap = 512;
+struct ResolveLds {
+    SoftRec rec[kStage];
+    uint32_t later[kLaterCap];
+};
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Visits the faces of the lanes set in `m` (lane j holds face f), in lane
+// order. Their records are staged through LDS in batches of kStage: the
+// batch's lanes copy their own record with vector loads (all in flight at
+// once), then every lane reads each staged record (an LDS broadcast).
+// `visit(rec, face, lane j)`. Single-wave workgroups only.
+template <typename Visit>
+__device__ __forceinline__ void visit_staged(const SoftRec* recs, uint32_t f, uint64_t m,
+                                             ResolveLds& lds, Visit&& visit) {
+    const int lane = threadIdx.x & 63;
+    while (m) {
+        const uint32_t rank = lanes_below(m);
+        if (((m >> lane) & 1ull) && rank < (uint32_t)kStage) {
+            const float4* src = (const float4*)(recs + f);
+            float4* dst = (float4*)&lds.rec[rank];
+#pragma unroll
+            for (int i = 0; i < (int)(sizeof(SoftRec) / 16); i++) {
+                dst[i] = src[i];
+            }
+        }
+        __syncthreads();
+        for (int slot = 0; slot < kStage && m; slot++) {
+            const int j = __builtin_ctzll(m);
+            m &= m - 1;
+            const uint32_t fj = (uint32_t)__builtin_amdgcn_readlane((int)f, j);
+            const SoftRec r = lds.rec[slot];
+            visit(r, fj, j);
+        }
+        __syncthreads();
+    }
+}
+
 // Resolves the winner of every pixel of one 8x8 block (lane = pixel, one
 // wave, no cross-wave synchronisation). `recs` / `cull` point at the view's
 // records. Phase A folds the class 0 / 2 fragments of faces whose A-box
@@ -582,21 +657,25 @@ __device__ __forceinline__ SoftRec load_rec_uniform(const SoftRec* recs, uint32_
 __device__ __forceinline__ PixelBest resolve_block(const SoftRec* recs, const CullRec* cull,
                                                    const BinView& bv, int bx, int by,
                                                    float radius, const float* prev,
-                                                   uint32_t width, uint32_t* later) {
+                                                   uint32_t width, ResolveLds& lds) {
     const int lane = threadIdx.x & 63;
     const int px = bx + (lane & 7);
     const int py = by + (lane >> 3);
     PixelBest best;
     best.key = kEmptyKey;
     best.hard = false;
+    auto fold_a = [&](const SoftRec& r, uint32_t fj, int) {
+        const bool inside = r.bx0 <= bx && r.bx1 >= bx + 7 && r.by0 <= by && r.by1 >= by + 7;
+        frag_phase_a(r, fj, px, py, inside, radius, prev, width, best);
+    };
     // Phase A folds faces whose hard area is negative (the front faces of a
     // closed mesh under this projection) first and keeps the others in LDS
-    // (`later`, one wave's kSoftBinCap entries): the key minimum does not
-    // depend on the fold order, and a kept face whose depth floor zc lies
-    // above every lane's depth after the first pass can win no pixel -- its
-    // hard fragments are deeper and its rim fragments are >= 0.5 > zc -- nor
-    // can phase B need it (every lane's depth is then < 0.5).
-    const bool defer = !bv.implicit && bv.n <= kSoftBinCap;
+    // (up to kLaterCap; the rest are folded at once): the key minimum does
+    // not depend on the fold order, and a kept face whose depth floor zc
+    // lies above every lane's depth after the first pass can win no pixel --
+    // its hard fragments are deeper and its rim fragments are >= 0.5 > zc --
+    // nor can phase B need it (every lane's depth is then < 0.5).
+    const bool defer = !bv.implicit;
     uint32_t n_later = 0;
     for (uint32_t base = 0; base < bv.n; base += 64) {
         const uint32_t e = base + (uint32_t)lane;
@@ -604,25 +683,19 @@ __device__ __forceinline__ PixelBest resolve_block(const SoftRec* recs, const Cu
         bool keep = false, pos = false;
         if (e < bv.n) {
             f = bv.implicit ? e : bv.list[e];
-            keep = block_in_a(recs, cull, f, bx, by, true, &pos);
+            const CullLoad l = load_cull<false>(recs, cull, f);
+            keep = cull_in_a(l, bx, by, true);
+            pos = cull_pos(l);
         }
-        const bool hold = defer && keep && pos;
+        bool hold = defer && keep && pos;
+        const uint64_t mh0 = __ballot(hold);
+        hold = hold && n_later + lanes_below(mh0) < kLaterCap;
         const uint64_t mh = __ballot(hold);
         if (hold) {
-            const uint32_t below = __builtin_amdgcn_mbcnt_hi(
-                    (uint32_t)(mh >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mh, 0u));
-            later[n_later + below] = f;
+            lds.later[n_later + lanes_below(mh)] = f;
         }
         n_later += (uint32_t)__popcll(mh);
-        uint64_t m = __ballot(keep && !hold);
-        while (m) {
-            const int j = __builtin_ctzll(m);
-            m &= m - 1;
-            const uint32_t fj = (uint32_t)__builtin_amdgcn_readlane((int)f, j);
-            const SoftRec r = load_rec_uniform(recs, fj);
-            const bool inside = r.bx0 <= bx && r.bx1 >= bx + 7 && r.by0 <= by && r.by1 >= by + 7;
-            frag_phase_a(r, fj, px, py, inside, radius, prev, width, best);
-        }
+        visit_staged(recs, f, __ballot(keep && !hold), lds, fold_a);
     }
     if (n_later) {
         __syncthreads();
@@ -633,15 +706,16 @@ __device__ __forceinline__ PixelBest resolve_block(const SoftRec* recs, const Cu
             const uint32_t other = (uint32_t)__shfl_xor((int)zmax, o);
             zmax = other > zmax ? other : zmax;
         }
-        zmax = (uint32_t)__builtin_amdgcn_readfirstlane((int)zmax);
-        for (uint32_t i = 0; i < n_later; i++) {
-            const uint32_t fj = (uint32_t)__builtin_amdgcn_readfirstlane((int)later[i]);
-            const SoftRec r = load_rec_uniform(recs, fj);
-            if (__float_as_uint(r.zc) > zmax) {
-                continue;  // zc >= 0: bit order is value order
+        for (uint32_t base = 0; base < n_later; base += 64) {
+            const uint32_t i = base + (uint32_t)lane;
+            uint32_t f = 0;
+            bool keep = false;
+            if (i < n_later) {
+                f = lds.later[i];
+                // zc >= 0: bit order is value order
+                keep = __float_as_uint(recs[f].zc) <= zmax;
             }
-            const bool inside = r.bx0 <= bx && r.bx1 >= bx + 7 && r.by0 <= by && r.by1 >= by + 7;
-            frag_phase_a(r, fj, px, py, inside, radius, prev, width, best);
+            visit_staged(recs, f, __ballot(keep), lds, fold_a);
         }
     }
     const bool need = (uint32_t)(best.key >> 32) >= 0x3f000000u;  // best depth >= 0.5
@@ -657,17 +731,12 @@ __device__ __forceinline__ PixelBest resolve_block(const SoftRec* recs, const Cu
         bool keep = false, in_a = false;
         if (e < bv.n) {
             f = bv.implicit ? e : bv.list[e];
-            const CullRec c = cull[f];
-            keep = box_hits(c.sx0, c.sy0, c.sx1, c.sy1, bx, by) && soft_reaches_block(recs + f, bx, by);
-            in_a = keep && block_in_a(recs, cull, f, bx, by, false);
+            const CullLoad l = load_cull<true>(recs, cull, f);
+            keep = cull_soft(l, bx, by);
+            in_a = keep && cull_in_a(l, bx, by, false);
         }
-        uint64_t m = __ballot(keep);
         const uint64_t ma = __ballot(in_a);
-        while (m) {
-            const int j = __builtin_ctzll(m);
-            m &= m - 1;
-            const uint32_t fj = (uint32_t)__builtin_amdgcn_readlane((int)f, j);
-            const SoftRec r = load_rec_uniform(recs, fj);
+        visit_staged(recs, f, __ballot(keep), lds, [&](const SoftRec& r, uint32_t fj, int j) {
             const bool a = (ma >> j) & 1ull;
             // the far path (depth exactly 1.0) needs the pixel more than r
             // from the hard triangle: never for faces folded in phase A
@@ -675,7 +744,7 @@ __device__ __forceinline__ PixelBest resolve_block(const SoftRec* recs, const Cu
             if (need) {
                 frag_phase_b(r, fj, px, py, radius, prev, width, near, a, best);
             }
-        }
+        });
     }
     return best;
 }
