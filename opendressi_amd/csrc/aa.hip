@@ -805,6 +805,7 @@ __device__ __forceinline__ uint32_t fold_groups(uint64_t m) {
 // Also clears the bin counters.
 __global__ __launch_bounds__(256) void k_aa_face_bwd(HsrDev d) {
     const uint32_t gi = blockIdx.x * blockDim.x + threadIdx.x;
+    publish_t_next(d, gi);
     for (uint32_t b = gi; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
         d.bins.counts[b] = 0;
     }

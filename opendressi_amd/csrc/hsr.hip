@@ -32,6 +32,10 @@ __global__ __launch_bounds__(256) void k_hsr_setup(HsrDev d) {
         soft_setup(sc, hc, (float)f, d.g.width, d.g.height, &r);
         d.recs[i] = r;
         d.cull[i] = cull_setup(r);
+        float cs[3][2];
+        chain_screen(hc, (float)d.g.width, (float)d.g.height, cs);
+        d.fscr[(size_t)i * 2] = make_float4(cs[0][0], cs[0][1], cs[1][0], cs[1][1]);
+        d.fscr[(size_t)i * 2 + 1] = make_float4(cs[2][0], cs[2][1], 0.f, 0.f);
     }
     const bool valid = live && r.bx0 <= r.bx1 && r.by0 <= r.by1;
     bin_append(d.bins, d.g, valid, view, f, r.bx0, r.by0, r.bx1, r.by1, soft_bin_tri(r), blds);
@@ -85,9 +89,9 @@ __global__ __launch_bounds__(256) void k_hsr_loss(HsrDev d) {
     }
     const size_t npx = (size_t)d.g.width * d.g.height;
     const size_t o = (size_t)y * d.g.width + x;
-    const float W = (float)d.g.width, H = (float)d.g.height;
-    // every view's face id and target first, then the corner vertices of the
-    // rim winners, then their positions: each round of loads in flight together
+    // every view's face id and target first, then the rim winners' screen
+    // corners (the setup's chain_screen of the face): each round of loads in
+    // flight together
     uint32_t id[NV];
     float tg[NV];
 #pragma unroll
@@ -95,42 +99,27 @@ __global__ __launch_bounds__(256) void k_hsr_loss(HsrDev d) {
         id[view] = d.ids[view * npx + o];
         tg[view] = d.targets[view * npx + o];
     }
-    int32_t vi[NV][3];
+    float4 sc[NV][2];
 #pragma unroll
     for (int view = 0; view < NV; view++) {
         const bool rim = (id[view] & kRimFlag) != 0;
-        const uint32_t f = rim ? (id[view] & ~kRimFlag) - 1 : 0u;
-#pragma unroll
-        for (int k = 0; k < 3; k++) {
-            vi[view][k] = rim ? d.faces[f * 3 + k] : 0;
-        }
-    }
-    float pp[NV][3][3];
-#pragma unroll
-    for (int view = 0; view < NV; view++) {
-        const bool rim = (id[view] & kRimFlag) != 0;
-#pragma unroll
-        for (int k = 0; k < 3; k++) {
-#pragma unroll
-            for (int c = 0; c < 3; c++) {
-                pp[view][k][c] = rim ? d.pos[vi[view][k] * 3 + c] : 0.f;
-            }
-        }
+        const size_t fi = (size_t)view * d.g.n_faces + (rim ? (id[view] & ~kRimFlag) - 1 : 0u);
+        sc[view][0] = rim ? d.fscr[fi * 2] : make_float4(0.f, 0.f, 0.f, 0.f);
+        sc[view][1] = rim ? d.fscr[fi * 2 + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float lv[NV][1];
 #pragma unroll
     for (int view = 0; view < NV; view++) {
         float pred = id[view] ? 1.f : 0.f;
         if (id[view] & kRimFlag) {
-            const float* m = d.mvps + view * 16;
-            float4 c[3];
-#pragma unroll
-            for (int k = 0; k < 3; k++) {
-                c[k] = mvp_transform(m, pp[view][k][0], pp[view][k][1], pp[view][k][2]);
-            }
             PixelFw st;
-            pixel_fw(c, 1.f, -1.f, 1.f, (float)x + 0.5f, (float)y + 0.5f, W, H, d.sigma_scale,
-                     st);
+            st.s[0][0] = sc[view][0].x;
+            st.s[0][1] = sc[view][0].y;
+            st.s[1][0] = sc[view][0].z;
+            st.s[1][1] = sc[view][0].w;
+            st.s[2][0] = sc[view][1].x;
+            st.s[2][1] = sc[view][1].y;
+            pixel_fw_screen(1.f, -1.f, 1.f, (float)x + 0.5f, (float)y + 0.5f, d.sigma_scale, st);
             pred = st.pred;
         }
         if (d.pred) {
@@ -151,6 +140,7 @@ __global__ __launch_bounds__(256) void k_hsr_loss(HsrDev d) {
 // (pred = max(1, soft) passes no gradient to soft) and are skipped.
 __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    publish_t_next(d, i);
     // the raster is done with this iteration's bins: clear their counters
     for (uint32_t b = i; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
         d.bins.counts[b] = 0;
@@ -596,13 +586,14 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
     rc = rc ? rc : plan_alloc(p, &d.m, V * 3);
     rc = rc ? rc : plan_alloc(p, &d.v, V * 3);
     rc = rc ? rc : plan_alloc(p, &d.t, 1);
-    rc = rc ? rc : plan_alloc(p, &d.done, 1);
+    rc = rc ? rc : plan_alloc(p, &d.t_next, 1);
     rc = rc ? rc : plan_alloc(p, (float**)&d.mvps, N * 16);
     rc = rc ? rc : plan_alloc(p, (float**)&d.targets, N * npx);
     d.technique = (desc->flags & DRESSI_HSR_TECHNIQUE_AA) ? 1u : 0u;
     if (d.technique == 0) {
         rc = rc ? rc : plan_alloc(p, &d.recs, N * F);
         rc = rc ? rc : plan_alloc(p, &d.cull, N * F);
+        rc = rc ? rc : plan_alloc(p, &d.fscr, N * F * 2);
     } else {
         rc = rc ? rc : plan_alloc(p, &d.arecs, N * F);
         rc = rc ? rc : plan_alloc(p, &d.clip, N * V);
@@ -642,7 +633,6 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
     }
     if (!rc) {
         hipError_t e = hipMemsetAsync(d.bins.counts, 0, sizeof(uint32_t) * d.bins.n_bins, ctx->stream);
-        if (e == hipSuccess) e = hipMemsetAsync(d.done, 0, sizeof(uint32_t), ctx->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
         if (e != hipSuccess) {
             set_error("plan init failed: %s", hipGetErrorString(e));

@@ -83,18 +83,23 @@ struct PixelFw {
     float m01, dmin, inside, sig, soft_sil, hard, pred;
 };
 
-// Forward of the chain at pixel centre (pcx, pcy); `mask` / `cov` are 1 on
-// covered pixels. `dist_c` is the rasterizer's signed distance channel.
-__device__ __forceinline__ void pixel_fw(const float4 c[3], float mask, float dist_c, float cov,
-                                         float pcx, float pcy, float W, float H,
-                                         float sigma_scale, PixelFw& st) {
-    const float om = 1.f - mask;
+// The chain's screen corners of a face: s_k = ((c_k.xy / (c_k.w + 1 - mask))
+// * 0.5 + 0.5) * (W, H) with mask = 1 (the face covers the pixel).
+__device__ __forceinline__ void chain_screen(const float4 c[3], float W, float H,
+                                             float s[3][2]) {
 #pragma unroll
     for (int k = 0; k < 3; k++) {
-        st.w[k] = c[k].w + om;
-        st.s[k][0] = ((c[k].x / st.w[k]) * 0.5f + 0.5f) * W;
-        st.s[k][1] = ((c[k].y / st.w[k]) * 0.5f + 0.5f) * H;
+        const float w = c[k].w + 0.f;
+        s[k][0] = ((c[k].x / w) * 0.5f + 0.5f) * W;
+        s[k][1] = ((c[k].y / w) * 0.5f + 0.5f) * H;
     }
+}
+
+// Forward of the chain from the screen corners st.s at pixel centre
+// (pcx, pcy); `mask` / `cov` are 1 on covered pixels, `dist_c` is the
+// rasterizer's signed distance channel.
+__device__ __forceinline__ void pixel_fw_screen(float mask, float dist_c, float cov, float pcx,
+                                                float pcy, float sigma_scale, PixelFw& st) {
     edge_fw(st.s[0][0], st.s[0][1], st.s[1][0], st.s[1][1], pcx, pcy, st.ed[0]);
     edge_fw(st.s[1][0], st.s[1][1], st.s[2][0], st.s[2][1], pcx, pcy, st.ed[1]);
     edge_fw(st.s[2][0], st.s[2][1], st.s[0][0], st.s[0][1], pcx, pcy, st.ed[2]);
@@ -117,6 +122,21 @@ __device__ __forceinline__ void pixel_fw(const float4 c[3], float mask, float di
     st.soft_sil = 1.f - 1.f * (1.f - D);
     st.hard = cov * step_f(0.f, dist_c);
     st.pred = smax(st.hard, st.soft_sil);
+}
+
+// Forward of the chain at pixel centre (pcx, pcy) from the three fetched
+// corner clips.
+__device__ __forceinline__ void pixel_fw(const float4 c[3], float mask, float dist_c, float cov,
+                                         float pcx, float pcy, float W, float H,
+                                         float sigma_scale, PixelFw& st) {
+    const float om = 1.f - mask;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        st.w[k] = c[k].w + om;
+        st.s[k][0] = ((c[k].x / st.w[k]) * 0.5f + 0.5f) * W;
+        st.s[k][1] = ((c[k].y / st.w[k]) * 0.5f + 0.5f) * H;
+    }
+    pixel_fw_screen(mask, dist_c, cov, pcx, pcy, sigma_scale, st);
 }
 
 // Gradient of (target - pred)^2 * inv_px w.r.t. the three fetched corner

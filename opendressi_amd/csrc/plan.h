@@ -62,7 +62,7 @@ struct HsrDev {
     float* m;
     float* v;
     float* t;
-    uint32_t* done;
+    float* t_next;            // t + 1, written by the face backward for the vertex kernel
     const int32_t* faces;     // [F][3]
     const int32_t* vf;        // [deg][V], -1 pad
     const uint8_t* vf_mask;   // [deg][V], bit k: faces[vf][k] == v
@@ -76,6 +76,8 @@ struct HsrDev {
     float* loss;              // [S][S]
     float* pred;              // [N][S][S] or null
     float4* gtri;             // [N][3][F]
+    float4* fscr;             // [N][F][2] HardSoftRas: the chain's screen corners of
+                              // each face, (s0x, s0y, s1x, s1y), (s2x, s2y, 0, 0)
     float* grad;              // [V][3] or null
     // Adam bias corrections 1 - b1^t, 1 - b2^t for t = 1 .. bc_len, filled
     // on the host with the C library's powf (the reference evaluator's
@@ -109,10 +111,10 @@ __device__ __forceinline__ void face_clips(const HsrDev& d, uint32_t view, uint3
 // per view x / y / z get one 4-term sum over the clip rows; pos gets the
 // GetZ, GetY, GetX contributions of view N-1 .. 0, newest first, through
 // the SumContribs tree), then the in-graph Adam step
-// (examples/silhouette_optimization/run.cpp:421-436) reading t.
+// (examples/silhouette_optimization/run.cpp:421-436) at step t_new = t + 1.
 template <int NV>
 __device__ __forceinline__ void pos_grad_adam(const HsrDev& d, uint32_t vtx,
-                                              const float (&gc)[NV][4], float t) {
+                                              const float (&gc)[NV][4], float t_new) {
     float contrib[3 * NV][3];
 #pragma unroll
     for (int vi = 0; vi < NV; vi++) {
@@ -145,7 +147,6 @@ __device__ __forceinline__ void pos_grad_adam(const HsrDev& d, uint32_t vtx,
             d.grad[vtx * 3 + c] = g[c];
         }
     }
-    const float t_new = t + 1.f;
     float bc1, bc2;
     if (t_new >= 1.f && t_new <= (float)d.bc_len && t_new == floorf(t_new)) {
         const float2 bc = d.bc_tab[(uint32_t)t_new - 1];
@@ -173,22 +174,6 @@ __device__ __forceinline__ void pos_grad_adam(const HsrDev& d, uint32_t vtx,
         d.pos[j] = p0[c] - step;
         d.m[j] = m_new;
         d.v[j] = v_new;
-    }
-}
-
-// The last workgroup of the vertex kernel to finish advances t (every
-// workgroup read t before arriving on the counter). All threads call it.
-__device__ __forceinline__ void advance_t(const HsrDev& d, float t) {
-    __shared__ bool last;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        last = atomicAdd(d.done, 1u) == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (last && threadIdx.x == 0) {
-        *d.t = t + 1.f;
-        *d.done = 0;
     }
 }
 
@@ -236,14 +221,17 @@ inline uint32_t vertex_grid(uint32_t n_verts) {
 // Body of both vertex kernels (blockDim.x = 256, grid vertex_grid<NV>):
 // lane (vertex, view) computes that view's clip gradient g4 through
 // `view_grad(vtx, view, g4)`; the vertex's first lane collects the NV
-// gradients (shuffles) and runs pos_grad_adam; the last workgroup advances t.
+// gradients (shuffles) and runs pos_grad_adam. The step count t + 1 comes
+// from t_next (written by the face backward, which runs before), so this
+// kernel never reads t and its first thread can store t + 1 without racing
+// the others.
 template <int NV, typename ViewGrad>
 __device__ __forceinline__ void vertex_views_adam(const HsrDev& d, ViewGrad&& view_grad) {
     constexpr int L = VertexLanes<NV>::L;
     const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
     const uint32_t vtx = gid / L;
     const uint32_t view = gid % L;
-    const float t = *d.t;
+    const float t_new = *d.t_next;
     const bool live = vtx < d.n_verts;
     float g4[4] = {0.f, 0.f, 0.f, 0.f};
     if (live && view < NV) {
@@ -259,9 +247,18 @@ __device__ __forceinline__ void vertex_views_adam(const HsrDev& d, ViewGrad&& vi
         }
     }
     if (live && view == 0) {
-        pos_grad_adam<NV>(d, vtx, gc, t);
+        pos_grad_adam<NV>(d, vtx, gc, t_new);
     }
-    advance_t(d, t);
+    if (gid == 0) {
+        *d.t = t_new;
+    }
+}
+
+// The face backward's first thread publishes t + 1 for the vertex kernel.
+__device__ __forceinline__ void publish_t_next(const HsrDev& d, uint32_t gid) {
+    if (gid == 0) {
+        *d.t_next = *d.t + 1.f;
+    }
 }
 
 // Launches kernel k (0 .. kAaKernels - 1) of one AA-technique iteration
