@@ -180,7 +180,7 @@ struct TexDev {
     float4* m;
     float4* v;
     float* t;
-    uint32_t* done;
+    float* t_next;          // t + 1, written by k_tex_clip for k_tex_bwd_adam
     float2* suv;            // [N][S][S] g_uv
     float4* gs;             // [N][S][S] d loss / d TextureBilinear(tex) output
     uint32_t* key;          // [N][S][S] floor(uv * T - 0.5) + 1 as x | y << 16 (clamped)
@@ -200,6 +200,11 @@ __global__ __launch_bounds__(256) void k_tex_clip(TexDev d) {
     const uint32_t nv = d.r.n_verts;
     if (i >= d.r.g.n_views * nv) {
         return;
+    }
+    if (i == 0) {
+        // the backward never reads t itself, so its first thread may store
+        // t + 1 without racing the others
+        *d.t_next = *d.t + 1.f;
     }
     const uint32_t view = i / nv;
     const uint32_t vtx = i - view * nv;
@@ -404,7 +409,8 @@ constexpr int kTexStage = 1024;  // tent keys of one view staged in LDS per wave
 // as window bits, and their g_uv / gradient loaded four at a time, the
 // weights then added in window order. The views' contributions are summed
 // newest first through the <= 4-ary tree, then Adam on the
-// RGBA texel; the last workgroup advances t.
+// RGBA texel at step t + 1 (t_next, published by k_tex_clip); the first
+// thread stores t + 1.
 template <int NV>
 __global__ __launch_bounds__(64) void k_tex_bwd_adam(TexDev d) {
     __shared__ uint32_t lk[kTexStage];
@@ -417,7 +423,7 @@ __global__ __launch_bounds__(64) void k_tex_bwd_adam(TexDev d) {
     const int ty = (int)(blockIdx.x / (uint32_t)bxn) * 8 + (lane >> 3);
     const bool valid = tx < tw && ty < th;
     const uint32_t q = valid ? (uint32_t)(ty * tw + tx) : 0u;
-    const float t = *d.t;
+    const float t_new = *d.t_next;
     // the anchor texel's UV-raster record (own or dilated, precomputed) and
     // its face's corners
     const float4 rec = valid ? d.texel[q] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -555,7 +561,6 @@ __global__ __launch_bounds__(64) void k_tex_bwd_adam(TexDev d) {
         if (d.grad) {
             d.grad[q] = make_float4(g[0], g[1], g[2], g[3]);
         }
-        const float t_new = t + 1.f;
         float bc1, bc2;
         if (t_new >= 1.f && t_new <= (float)d.bc_len && t_new == floorf(t_new)) {
             const float2 bc = d.bc_tab[(uint32_t)t_new - 1];
@@ -583,16 +588,8 @@ __global__ __launch_bounds__(64) void k_tex_bwd_adam(TexDev d) {
         d.m[q] = make_float4(mi[0], mi[1], mi[2], mi[3]);
         d.v[q] = make_float4(vi4[0], vi4[1], vi4[2], vi4[3]);
     }
-    __shared__ bool last;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        last = atomicAdd(d.done, 1u) == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (last && threadIdx.x == 0) {
-        *d.t = t + 1.f;
-        *d.done = 0;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        *d.t = t_new;
     }
 }
 
@@ -842,7 +839,7 @@ int dressi_tex_create(dressi_ctx* ctx, const dressi_tex_desc* desc, dressi_tex_p
     rc = rc ? rc : tex_alloc(p, &d.m, T);
     rc = rc ? rc : tex_alloc(p, &d.v, T);
     rc = rc ? rc : tex_alloc(p, &d.t, 1);
-    rc = rc ? rc : tex_alloc(p, &d.done, 1);
+    rc = rc ? rc : tex_alloc(p, &d.t_next, 1);
     rc = rc ? rc : tex_alloc(p, &d.suv, N * npx);
     rc = rc ? rc : tex_alloc(p, &d.gs, N * npx);
     rc = rc ? rc : tex_alloc(p, &d.key, N * npx);
@@ -891,7 +888,6 @@ int dressi_tex_create(dressi_ctx* ctx, const dressi_tex_desc* desc, dressi_tex_p
     }
     if (!rc) {
         hipError_t e = hipMemsetAsync(p->bin_mem, 0, p->bin_bytes, ctx->stream);
-        if (e == hipSuccess) e = hipMemsetAsync(d.done, 0, sizeof(uint32_t), ctx->stream);
         if (e == hipSuccess) e = hipMemsetAsync(d.t, 0, sizeof(float), ctx->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
         if (e != hipSuccess) {
