@@ -475,6 +475,7 @@ struct CullLoad {
     CullRec c;
     float w[16];
     float sx[3], sy[3], s_margin;
+    float hx[3], hy[3];
 };
 
 template <bool kSoft>
@@ -501,6 +502,14 @@ __device__ __forceinline__ CullLoad load_cull(const SoftRec* recs, const CullRec
         l.sy[1] = b.x;
         l.sy[2] = b.y;
         l.s_margin = recs[f].s_margin;
+        const float4 h = *(const float4*)&recs[f].hx[0];  // hx0 hx1 hx2 hy0
+        const float2 g = *(const float2*)&recs[f].hy[1];  // hy1 hy2
+        l.hx[0] = h.x;
+        l.hx[1] = h.y;
+        l.hx[2] = h.z;
+        l.hy[0] = h.w;
+        l.hy[1] = g.x;
+        l.hy[2] = g.y;
     }
     return l;
 }
@@ -571,16 +580,17 @@ __device__ __forceinline__ BlockPos block_pos(uint32_t wg, const RasterGeom& g) 
 // The record's hard-triangle bbox widened by a_margin + `d` px overlaps the
 // pixel-centre rectangle [cx0, cx1] x [cy0, cy1] (always true without a
 // bound).
-__device__ __forceinline__ bool hard_bbox_near(const SoftRec& r, float cx0, float cx1, float cy0,
+__device__ __forceinline__ bool hard_bbox_near(const float (&hx)[3], const float (&hy)[3],
+                                               float a_margin, float cx0, float cx1, float cy0,
                                                float cy1, float d) {
-    if (!(r.a_margin < INFINITY)) {
+    if (!(a_margin < INFINITY)) {
         return true;
     }
-    d += r.a_margin;
-    const float mnx = smin(smin(r.hx[0], r.hx[1]), r.hx[2]);
-    const float mxx = smax(smax(r.hx[0], r.hx[1]), r.hx[2]);
-    const float mny = smin(smin(r.hy[0], r.hy[1]), r.hy[2]);
-    const float mxy = smax(smax(r.hy[0], r.hy[1]), r.hy[2]);
+    d += a_margin;
+    const float mnx = smin(smin(hx[0], hx[1]), hx[2]);
+    const float mxx = smax(smax(hx[0], hx[1]), hx[2]);
+    const float mny = smin(smin(hy[0], hy[1]), hy[2]);
+    const float mxy = smax(smax(hy[0], hy[1]), hy[2]);
     return !(cx0 > mxx + d || cx1 < mnx - d || cy0 > mxy + d || cy1 < mny - d);
 }
 
@@ -606,10 +616,54 @@ __device__ __forceinline__ SoftRec load_rec_uniform(const SoftRec* recs, uint32_
 // deferred (back) faces of phase A.
 constexpr int kStage = 16;
 constexpr uint32_t kLaterCap = 512;
+constexpr uint32_t kFarCap = 512;
 struct ResolveLds {
     SoftRec rec[kStage];
-    uint32_t later[kLaterCap];
+    union {
+        uint32_t later[kLaterCap];  // phase A: deferred faces
+        uint32_t far[kFarCap];      // phase B: far faces (as face + 1)
+    };
 };
+
+// Orders the LDS accesses of one wave around an exchange between its lanes
+// (a wave executes its LDS instructions in order).
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Sorts key[0 .. n) descending (bitonic network over the next power of two,
+// padded with zeros, which sort last). One wave; n <= kFarCap.
+__device__ __forceinline__ void sort_desc(uint32_t* key, uint32_t n) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t np = 2;
+    while (np < n) {
+        np <<= 1;
+    }
+    for (uint32_t i = n + lane; i < np; i += 64) {
+        key[i] = 0u;
+    }
+    wave_lds_fence();
+    for (uint32_t k = 2; k <= np; k <<= 1) {
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            for (uint32_t i = lane; i < np; i += 64) {
+                const uint32_t ixj = i ^ j;
+                if (ixj > i) {
+                    const uint32_t a = key[i], b = key[ixj];
+                    // runs with (i & k) == 0 descend, the others ascend; the
+                    // last merge (k = np) descends over the whole range
+                    const bool desc = (i & k) == 0u;
+                    if (desc ? a < b : a > b) {
+                        key[i] = b;
+                        key[ixj] = a;
+                    }
+                }
+            }
+            wave_lds_fence();
+        }
+    }
+}
 
 __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
@@ -725,26 +779,71 @@ __device__ __forceinline__ PixelBest resolve_block(const SoftRec* recs, const Cu
     const float near_d = radius;  // + the face's a_margin
     const float cx0 = (float)bx + 0.5f, cx1 = (float)bx + 7.5f;
     const float cy0 = (float)by + 0.5f, cy1 = (float)by + 7.5f;
+    // Near faces (the hard triangle within r + a_margin of the block, or
+    // folded in phase A) are folded as they come. Far faces give depth
+    // exactly 1.0 at every pixel they cover, so among them the highest face
+    // index wins: they are collected (up to kFarCap; the rest fold at once),
+    // sorted by descending index and folded until no pixel that needs
+    // phase B can still take a later (lower) one.
+    uint32_t n_far = 0;
     for (uint32_t base = 0; base < bv.n; base += 64) {
         const uint32_t e = base + (uint32_t)lane;
         uint32_t f = 0;
-        bool keep = false, in_a = false;
+        bool keep = false, in_a = false, near = false;
         if (e < bv.n) {
             f = bv.implicit ? e : bv.list[e];
             const CullLoad l = load_cull<true>(recs, cull, f);
             keep = cull_soft(l, bx, by);
             in_a = keep && cull_in_a(l, bx, by, false);
+            near = in_a || hard_bbox_near(l.hx, l.hy, l.w[15], cx0, cx1, cy0, cy1, near_d);
         }
+        bool far = keep && !near;
+        const uint64_t mf0 = __ballot(far);
+        far = far && n_far + lanes_below(mf0) < kFarCap;
+        const uint64_t mf = __ballot(far);
+        if (far) {
+            lds.far[n_far + lanes_below(mf)] = f + 1u;
+        }
+        n_far += (uint32_t)__popcll(mf);
         const uint64_t ma = __ballot(in_a);
-        visit_staged(recs, f, __ballot(keep), lds, [&](const SoftRec& r, uint32_t fj, int j) {
-            const bool a = (ma >> j) & 1ull;
-            // the far path (depth exactly 1.0) needs the pixel more than r
-            // from the hard triangle: never for faces folded in phase A
-            const bool near = a || hard_bbox_near(r, cx0, cx1, cy0, cy1, near_d);
+        const uint64_t mn = __ballot(near);
+        visit_staged(recs, f, __ballot(keep && !far), lds, [&](const SoftRec& r, uint32_t fj, int j) {
             if (need) {
-                frag_phase_b(r, fj, px, py, radius, prev, width, near, a, best);
+                frag_phase_b(r, fj, px, py, radius, prev, width, (mn >> j) & 1ull,
+                             (ma >> j) & 1ull, best);
             }
         });
+    }
+    if (n_far) {
+        __syncthreads();
+        sort_desc(lds.far, n_far);
+        for (uint32_t b0 = 0; b0 < n_far; b0 += (uint32_t)kStage) {
+            // the batch's first face has the highest index left
+            const uint32_t f0 = lds.far[b0] - 1u;
+            if (!__any(need && best.key > depth_key(1.f, f0))) {
+                break;
+            }
+            const uint32_t cnt = min((uint32_t)kStage, n_far - b0);
+            uint32_t f = 0;
+            if ((uint32_t)lane < cnt) {
+                f = lds.far[b0 + lane] - 1u;
+                const float4* src = (const float4*)(recs + f);
+                float4* dst = (float4*)&lds.rec[lane];
+#pragma unroll
+                for (int i = 0; i < (int)(sizeof(SoftRec) / 16); i++) {
+                    dst[i] = src[i];
+                }
+            }
+            __syncthreads();
+            for (uint32_t j = 0; j < cnt; j++) {
+                const uint32_t fj = (uint32_t)__builtin_amdgcn_readlane((int)f, (int)j);
+                const SoftRec r = lds.rec[j];
+                if (need) {
+                    frag_phase_b(r, fj, px, py, radius, prev, width, false, false, best);
+                }
+            }
+            __syncthreads();
+        }
     }
     return best;
 }
