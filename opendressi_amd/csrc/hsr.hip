@@ -38,25 +38,51 @@ __global__ __launch_bounds__(256) void k_hsr_setup(HsrDev d) {
         d.fscr[(size_t)i * 2 + 1] = make_float4(cs[2][0], cs[2][1], 0.f, 0.f);
     }
     const bool valid = live && r.bx0 <= r.bx1 && r.by0 <= r.by1;
-    bin_append(d.bins, d.g, valid, view, f, r.bx0, r.by0, r.bx1, r.by1, soft_bin_tri(r), blds);
+    bin_append(d.bins, d.g, valid, view, f, r.bx0, r.by0, r.bx1, r.by1, soft_bin_tri(r), blds,
+               &d.heavy);
 }
 
 // Visibility: one single-wave workgroup per (view, 8x8 block) resolves the
 // RasterizeSoft winner of every pixel and writes the face-id buffer (face +
-// 1, bit 31 for rim winners, 0 for background). Workgroup w runs on XCD
-// w % 8: tiles are dealt to the XCDs round robin (neighbouring tiles, and so
-// the costly silhouette bands, spread over all of them), and the four
-// blocks of a tile of a view are consecutive on one XCD.
+// 1, bit 31 for rim winners, 0 for background). The first 4 kHeavyCap
+// workgroups take the four blocks of each listed heavy bin (slot-major over
+// the segments); the others walk every (view, tile, block) and skip the
+// listed bins. Workgroup w runs on
+// XCD w % 8: tiles are dealt to the XCDs round robin (neighbouring tiles,
+// and so the costly silhouette bands, spread over all of them), and the
+// four blocks of a tile of a view are consecutive on one XCD.
 __global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
-    const uint32_t per = (d.g.n_tiles + 7u) / 8u;
-    const uint32_t k = blockIdx.x >> 3;
-    const uint32_t q = k & 3u;
-    const uint32_t view = (k >> 2) % d.g.n_views;
-    const uint32_t lt = (k >> 2) / d.g.n_views;
-    const uint32_t tile = lt * 8u + (blockIdx.x & 7u);
+    uint32_t view, tile, q;
+    if (blockIdx.x < 4u * kHeavyCap) {
+        const uint32_t k = blockIdx.x >> 3;
+        q = k & 3u;
+        const uint32_t j = (k >> 2) * 8u + (blockIdx.x & 7u);
+        const uint32_t seg = j % kHeavySegs, slot = j / kHeavySegs;
+        if (slot >= d.heavy.count[seg]) {
+            return;
+        }
+        const uint32_t bin = d.heavy.list[seg * kHeavySegCap + slot];
+        view = bin / d.g.n_tiles;
+        tile = bin - view * d.g.n_tiles;
+    } else {
+        const uint32_t b = blockIdx.x - 4u * kHeavyCap;
+        const uint32_t per = (d.g.n_tiles + 7u) / 8u;
+        const uint32_t k = b >> 3;
+        q = k & 3u;
+        view = (k >> 2) % d.g.n_views;
+        const uint32_t lt = (k >> 2) / d.g.n_views;
+        tile = lt * 8u + (b & 7u);
+        if (lt >= per || tile >= d.g.n_tiles) {
+            return;
+        }
+        const uint32_t bin = view * d.g.n_tiles + tile;
+        if (heavy_listed(d.heavy, d.bins.counts[bin], bin)) {
+            return;
+        }
+    }
     const int bx = (int)((tile % d.g.tiles_x) * kTile + (q & 1u) * 8u);
     const int by = (int)((tile / d.g.tiles_x) * kTile + (q >> 1) * 8u);
-    if (lt >= per || tile >= d.g.n_tiles || bx >= (int)d.g.width || by >= (int)d.g.height) {
+    if (bx >= (int)d.g.width || by >= (int)d.g.height) {
         return;
     }
     const int lane = threadIdx.x & 63;
@@ -144,6 +170,9 @@ __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
     // the raster is done with this iteration's bins: clear their counters
     for (uint32_t b = i; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
         d.bins.counts[b] = 0;
+    }
+    if (d.heavy.count && i < kHeavySegs) {
+        d.heavy.count[i] = 0;
     }
     if (i >= d.g.n_views * d.g.n_faces) {
         return;
@@ -485,7 +514,8 @@ int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
             hipLaunchKernelGGL(k_hsr_setup, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
             break;
         case 1:
-            hipLaunchKernelGGL(k_hsr_raster, dim3(block_grid(g) * g.n_views), dim3(64), 0, s, d);
+            hipLaunchKernelGGL(k_hsr_raster, dim3(4u * kHeavyCap + block_grid(g) * g.n_views),
+                               dim3(64), 0, s, d);
             break;
         case 2: {
             const dim3 grid(div_up(g.width, 64), div_up(g.height, 4));
@@ -594,6 +624,9 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
         rc = rc ? rc : plan_alloc(p, &d.recs, N * F);
         rc = rc ? rc : plan_alloc(p, &d.cull, N * F);
         rc = rc ? rc : plan_alloc(p, &d.fscr, N * F * 2);
+        rc = rc ? rc : plan_alloc(p, &d.heavy.count, kHeavySegs);
+        rc = rc ? rc : plan_alloc(p, &d.heavy.list, kHeavyCap);
+        rc = rc ? rc : plan_alloc(p, &d.heavy.slot, (size_t)N * d.g.n_tiles);
     } else {
         rc = rc ? rc : plan_alloc(p, &d.arecs, N * F);
         rc = rc ? rc : plan_alloc(p, &d.clip, N * V);
@@ -633,6 +666,9 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
     }
     if (!rc) {
         hipError_t e = hipMemsetAsync(d.bins.counts, 0, sizeof(uint32_t) * d.bins.n_bins, ctx->stream);
+        if (e == hipSuccess && d.heavy.count) {
+            e = hipMemsetAsync(d.heavy.count, 0, sizeof(uint32_t) * kHeavySegs, ctx->stream);
+        }
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
         if (e != hipSuccess) {
             set_error("plan init failed: %s", hipGetErrorString(e));

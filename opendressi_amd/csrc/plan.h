@@ -72,6 +72,9 @@ struct HsrDev {
     CullRec* cull;            // [N][F]
     BinBuffers bins;          // fixed-capacity soft bins, N x tiles; the
                               // face backward clears the counters
+    HeavyList heavy;          // the bins the raster resolves first (kept by the
+                              // setup's appends, segment counters cleared by the
+                              // face backward)
     uint32_t* ids;            // [N][S][S] face + 1 (bit 31: rim winner), 0 bg
     float* loss;              // [S][S]
     float* pred;              // [N][S][S] or null
@@ -92,6 +95,7 @@ struct HsrDev {
 };
 
 constexpr uint32_t kBiasTableLen = 1u << 16;
+
 constexpr uint32_t kRimFlag = 0x80000000u;
 
 // Corner clips of face f in one view: TransformToClipVar of its vertices.

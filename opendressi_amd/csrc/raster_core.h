@@ -999,11 +999,52 @@ __device__ __forceinline__ BinTri soft_bin_tri(const SoftRec& r) {
     return t;
 }
 
+// Heavy bins (at least kHeavyBin entries: the silhouette's limb, where the
+// soft triangles of edge-on faces pile up) take many times longer to
+// resolve than the rest, so the raster dispatches them first. The append
+// that takes a bin's count across kHeavyBin lists it: in segment
+// heavy_seg(bin) (a counter each, so no single counter takes every atomic;
+// a multiplicative hash spreads the limb's runs of neighbouring bins), at
+// the returned slot, which is also kept per bin. A bin past its segment's
+// capacity stays with the others. The consumer clears the segment counters
+// with the bin counters.
+constexpr uint32_t kHeavyBin = 192;
+constexpr uint32_t kHeavySegs = 64;
+constexpr uint32_t kHeavySegCap = 96;
+constexpr uint32_t kHeavyCap = kHeavySegs * kHeavySegCap;
+struct HeavyList {
+    uint32_t* count;  // [kHeavySegs]
+    uint32_t* list;   // [kHeavySegs][kHeavySegCap] bins
+    uint32_t* slot;   // [n_bins] slot of a bin whose count reached kHeavyBin
+};
+
+__device__ __forceinline__ uint32_t heavy_seg(uint32_t bin) {
+    return (bin * 2654435761u) >> 26;  // top 6 bits: kHeavySegs = 64
+}
+
+__device__ __forceinline__ void heavy_note(const HeavyList* h, uint32_t bin, uint32_t old,
+                                           uint32_t add) {
+    if (h && old < kHeavyBin && old + add >= kHeavyBin) {
+        const uint32_t seg = heavy_seg(bin);
+        const uint32_t s = atomicAdd(&h->count[seg], 1u);
+        h->slot[bin] = s;
+        if (s < kHeavySegCap) {
+            h->list[seg * kHeavySegCap + s] = bin;
+        }
+    }
+}
+
+// The bin is listed (resolved by the heavy part of the raster's grid).
+__device__ __forceinline__ bool heavy_listed(const HeavyList& h, uint32_t count, uint32_t bin) {
+    return count >= kHeavyBin && h.slot[bin] < kHeavySegCap;
+}
+
 // One (face, tile) pair of bin_append's pass (0: count window pairs in LDS
 // and append the others, 1: write window pairs from their bases).
 __device__ __forceinline__ void bin_pair(const BinBuffers& b, const RasterGeom& g, BinLds& lds,
                                          int pass, bool mixed, int wx0, int wy0, uint32_t f,
-                                         uint32_t view, const BinTri& tri, int tx, int ty) {
+                                         uint32_t view, const BinTri& tri, int tx, int ty,
+                                         const HeavyList* heavy) {
     const bool local = !mixed && tx - wx0 < kBinWin && ty - wy0 < kBinWin;
     if ((pass == 1 && !local) || !tri_reaches_tile(tri, tx, ty)) {
         return;
@@ -1019,6 +1060,7 @@ __device__ __forceinline__ void bin_pair(const BinBuffers& b, const RasterGeom& 
         slot = lds.base[li] + k;
     } else {
         slot = atomicAdd(&b.counts[bin], 1u);
+        heavy_note(heavy, bin, slot, 1u);
     }
     if (slot < b.cap) {
         b.list[(size_t)bin * b.cap + slot] = f;
@@ -1027,7 +1069,8 @@ __device__ __forceinline__ void bin_pair(const BinBuffers& b, const RasterGeom& 
 
 __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom& g, bool valid,
                                            uint32_t view, uint32_t f, int bx0, int by0, int bx1,
-                                           int by1, const BinTri& tri, BinLds& lds) {
+                                           int by1, const BinTri& tri, BinLds& lds,
+                                           const HeavyList* heavy = nullptr) {
     const int tid = (int)threadIdx.x;
     const int nthr = (int)blockDim.x;
     const int tx0 = bx0 / kTile, tx1 = bx1 / kTile, ty0 = by0 / kTile, ty1 = by1 / kTile;
@@ -1089,7 +1132,7 @@ __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom
             t.m = nt <= 4u ? -1.f : t.m;
             for (int ty = ty0; ty <= ty1; ty++) {
                 for (int tx = tx0; tx <= tx1; tx++) {
-                    bin_pair(b, g, lds, pass, mixed, wx0, wy0, f, view, t, tx, ty);
+                    bin_pair(b, g, lds, pass, mixed, wx0, wy0, f, view, t, tx, ty, heavy);
                 }
             }
         }
@@ -1107,7 +1150,7 @@ __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom
             const int i = (int)(p - lds.off[lo]);
             const int qnx = lds.nx[lo];
             bin_pair(b, g, lds, pass, mixed, wx0, wy0, lds.f[lo], lds.view[lo], lds.tri[lo],
-                     lds.tx0[lo] + i % qnx, lds.ty0[lo] + i / qnx);
+                     lds.tx0[lo] + i % qnx, lds.ty0[lo] + i / qnx, heavy);
         }
         if (pass == 0) {
             __syncthreads();
@@ -1116,7 +1159,10 @@ __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom
                 const uint32_t c = lds.cnt[i];
                 if (c) {
                     const int tx = wx0 + i % kBinWin, ty = wy0 + i / kBinWin;
-                    lds.base[i] = atomicAdd(&b.counts[view0 * g.n_tiles + ty * g.tiles_x + tx], c);
+                    const uint32_t bin = view0 * g.n_tiles + ty * g.tiles_x + tx;
+                    const uint32_t old = atomicAdd(&b.counts[bin], c);
+                    heavy_note(heavy, bin, old, c);
+                    lds.base[i] = old;
                     lds.cnt[i] = 0;
                 }
             }
