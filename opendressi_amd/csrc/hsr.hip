@@ -10,9 +10,6 @@
 
 namespace dressi {
 
-// Samples of FaceFetchBwd whose face-id loads are issued together.
-constexpr int kSampleBatch = 8;
-
 // SoftClip + RasterizeSoft setup per (view, face), appended to the soft bins.
 __global__ __launch_bounds__(256) void k_hsr_setup(HsrDev d) {
     __shared__ BinLds blds;
@@ -44,16 +41,17 @@ __global__ __launch_bounds__(256) void k_hsr_setup(HsrDev d) {
 
 // Visibility: one single-wave workgroup per (view, 8x8 block) resolves the
 // RasterizeSoft winner of every pixel and writes the face-id buffer (face +
-// 1, bit 31 for rim winners, 0 for background). The first 4 kHeavyCap
-// workgroups take the four blocks of each listed heavy bin (slot-major over
-// the segments); the others walk every (view, tile, block) and skip the
-// listed bins. Workgroup w runs on
+// 1, bit 31 for rim winners, 0 for background). The first 4 kHeavySegs
+// heavy.cap workgroups take the four blocks of each listed heavy bin
+// (slot-major over the segments); the others walk every (view, tile, block)
+// and skip the listed bins. Workgroup w runs on
 // XCD w % 8: tiles are dealt to the XCDs round robin (neighbouring tiles,
 // and so the costly silhouette bands, spread over all of them), and the
 // four blocks of a tile of a view are consecutive on one XCD.
 __global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
     uint32_t view, tile, q;
-    if (blockIdx.x < 4u * kHeavyCap) {
+    const uint32_t n_first = 4u * kHeavySegs * d.heavy.cap;
+    if (blockIdx.x < n_first) {
         const uint32_t k = blockIdx.x >> 3;
         q = k & 3u;
         const uint32_t j = (k >> 2) * 8u + (blockIdx.x & 7u);
@@ -65,7 +63,7 @@ __global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
         view = bin / d.g.n_tiles;
         tile = bin - view * d.g.n_tiles;
     } else {
-        const uint32_t b = blockIdx.x - 4u * kHeavyCap;
+        const uint32_t b = blockIdx.x - n_first;
         const uint32_t per = (d.g.n_tiles + 7u) / 8u;
         const uint32_t k = b >> 3;
         q = k & 3u;
@@ -97,6 +95,9 @@ __global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
         uint32_t id = 0;
         if (best.key != kEmptyKey) {
             id = (key_face(best.key) + 1) | (best.hard ? 0u : kRimFlag);
+            if (!best.hard) {
+                d.rimf[vf + key_face(best.key)] = 1;
+            }
         }
         d.ids[(size_t)view * d.g.width * d.g.height + (size_t)py * d.g.width + px] = id;
     }
@@ -161,115 +162,122 @@ __global__ __launch_bounds__(256) void k_hsr_loss(HsrDev d) {
 
 // FaceFetchBwd (stochastic, n samples, seed = t) fused with the pixel
 // chain's backward at each accepted sample: per (view, face) the three
-// corner-clip gradients (src/core/f_ops.cpp:1646-1729, 1700-1727). Samples on
+// corner-clip gradients (src/core/f_ops.cpp:1646-1729, 1700-1727). A group of
+// kSampleLanes lanes takes one (view, face): lane j evaluates samples j,
+// j + kSampleLanes, ..., then the group's first lane adds the lanes'
+// gradients in sample order (lanes without an accepted sample add +0, which
+// leaves the sum unchanged: it starts at +0 and never becomes -0). Samples on
 // pixels whose winner is a hard-branch fragment contribute exactly zero
-// (pred = max(1, soft) passes no gradient to soft) and are skipped.
+// (pred = max(1, soft) passes no gradient to soft) and are skipped; a face
+// that won no rim pixel (rimf = 0) has no other sample, so it reads none.
+constexpr int kSampleLanes = 8;
+
 __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    publish_t_next(d, i);
+    const uint32_t gi = blockIdx.x * blockDim.x + threadIdx.x;
+    publish_t_next(d, gi);
     // the raster is done with this iteration's bins: clear their counters
-    for (uint32_t b = i; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
+    for (uint32_t b = gi; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
         d.bins.counts[b] = 0;
     }
-    if (d.heavy.count && i < kHeavySegs) {
-        d.heavy.count[i] = 0;
+    if (d.heavy.count && gi < kHeavySegs) {
+        d.heavy.count[gi] = 0;
     }
-    if (i >= d.g.n_views * d.g.n_faces) {
-        return;
-    }
-    const uint32_t view = i / d.g.n_faces;
-    const uint32_t f = i - view * d.g.n_faces;
+    const uint32_t item = gi / kSampleLanes;
+    const bool valid = item < d.g.n_views * d.g.n_faces;
+    const int j = (int)(threadIdx.x % kSampleLanes);
+    const int gbase = (int)(threadIdx.x & 63u) - j;  // first lane of the group
+    const uint32_t view = valid ? item / d.g.n_faces : 0u;
+    const uint32_t f = valid ? item - view * d.g.n_faces : 0u;
     const float W = (float)d.g.width, H = (float)d.g.height;
+    const bool rim = valid && d.rimf[item] != 0;
     float4 c[3];
-    face_clips(d, view, f, c);
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        c[k] = make_float4(0.f, 0.f, 0.f, 1.f);
+    }
+    if (rim) {
+        face_clips(d, view, f, c);
+    }
     float4 acc[3];
 #pragma unroll
     for (int k = 0; k < 3; k++) {
         acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    float4* dst = d.gtri + (size_t)view * 3 * d.g.n_faces;
-    const bool ok = c[0].w > 1e-6f && c[1].w > 1e-6f && c[2].w > 1e-6f;
-    if (ok && d.n_samples > 0) {
-        float s[3][2];
+    const bool ok = rim && c[0].w > 1e-6f && c[1].w > 1e-6f && c[2].w > 1e-6f;
+    float s[3][2];
 #pragma unroll
-        for (int k = 0; k < 3; k++) {
-            s[k][0] = (c[k].x / c[k].w * 0.5f + 0.5f) * W;
-            s[k][1] = (c[k].y / c[k].w * 0.5f + 0.5f) * H;
-        }
-        const uint32_t seed_u = (uint32_t)(int64_t)(*d.t + 0.5f);
-        const size_t npx = (size_t)d.g.width * d.g.height;
-        const uint32_t* ids = d.ids + view * npx;
-        const float* tgt = d.targets + view * npx;
-        const uint32_t want = (f + 1) | kRimFlag;
-        // samples in batches of kSampleBatch: every sample's pixel first, then
-        // their face-id loads together, then the hits in sample order
-        for (uint32_t s0 = 0; s0 < d.n_samples; s0 += kSampleBatch) {
-            int64_t pix[kSampleBatch];
-#pragma unroll
-            for (int i = 0; i < kSampleBatch; i++) {
-                pix[i] = -1;
-                const uint32_t smp = s0 + (uint32_t)i;
-                if (smp >= d.n_samples) {
-                    continue;
-                }
-                const int e = (int)(smp % 3);
-                const float* a = s[e];
-                const float* b = s[(e + 1) % 3];
-                const float ex = b[0] - a[0];
-                const float ey = b[1] - a[1];
-                const float len = sqrtf(ex * ex + ey * ey);
-                if (len < 1e-6f) {
-                    continue;
-                }
+    for (int k = 0; k < 3; k++) {
+        s[k][0] = (c[k].x / c[k].w * 0.5f + 0.5f) * W;
+        s[k][1] = (c[k].y / c[k].w * 0.5f + 0.5f) * H;
+    }
+    const uint32_t seed_u = (uint32_t)(int64_t)(*d.t + 0.5f);
+    const size_t npx = (size_t)d.g.width * d.g.height;
+    const uint32_t* ids = d.ids + view * npx;
+    const float* tgt = d.targets + view * npx;
+    const uint32_t want = (f + 1) | kRimFlag;
+    for (uint32_t s0 = 0; s0 < d.n_samples && __any(ok); s0 += kSampleLanes) {
+        const uint32_t smp = s0 + (uint32_t)j;
+        int64_t pix = -1;
+        if (ok && smp < d.n_samples) {
+            const int e = (int)(smp % 3);
+            const float* a = s[e];
+            const float* b = s[(e + 1) % 3];
+            const float ex = b[0] - a[0];
+            const float ey = b[1] - a[1];
+            const float len = sqrtf(ex * ex + ey * ey);
+            if (!(len < 1e-6f)) {
                 const float u = hash_to_unit(f, smp, seed_u, 0);
                 const float off = (hash_to_unit(f, smp, seed_u, 1) * 2.f - 1.f) * d.radius;
                 const float spx = a[0] + u * ex - off * (ey / len);
                 const float spy = a[1] + u * ey + off * (ex / len);
                 const int ix = (int)floorf(spx);
                 const int iy = (int)floorf(spy);
-                if (ix < 0 || iy < 0 || ix >= (int)d.g.width || iy >= (int)d.g.height) {
-                    continue;
+                if (ix >= 0 && iy >= 0 && ix < (int)d.g.width && iy < (int)d.g.height) {
+                    pix = (int64_t)iy * d.g.width + ix;
                 }
-                pix[i] = (int64_t)iy * d.g.width + ix;
             }
-            uint32_t id[kSampleBatch];
+        }
+        // other faces and hard-branch winners (zero gradient) are skipped
+        const bool hit = pix >= 0 && ids[pix] == want;
+        float4 g[3];
 #pragma unroll
-            for (int i = 0; i < kSampleBatch; i++) {
-                id[i] = pix[i] >= 0 ? ids[pix[i]] : 0u;
-            }
-            // other faces and hard-branch winners (zero gradient) are skipped
-            uint32_t hits = 0;
+        for (int k = 0; k < 3; k++) {
+            g[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (hit) {
+            const int ix = (int)(pix % d.g.width), iy = (int)(pix / d.g.width);
+            const float pcx = (float)ix + 0.5f, pcy = (float)iy + 0.5f;
+            PixelFw st;
+            pixel_fw(c, 1.f, -1.f, 1.f, pcx, pcy, W, H, d.sigma_scale, st);
+            pixel_bw(st, c, 1.f, tgt[pix], d.inv_px, W, H, d.sigma_scale, g);
+        }
+        if (__any(hit)) {
+            // the group's first lane adds the samples in order
 #pragma unroll
-            for (int i = 0; i < kSampleBatch; i++) {
-                hits |= (id[i] == want ? 1u : 0u) << i;
-            }
-            while (hits) {
-                const int i = __builtin_ctz(hits);
-                hits &= hits - 1;
-                int64_t p = 0;
-#pragma unroll
-                for (int j = 0; j < kSampleBatch; j++) {
-                    p = j == i ? pix[j] : p;
-                }
-                const int ix = (int)(p % d.g.width), iy = (int)(p / d.g.width);
-                const float pcx = (float)ix + 0.5f, pcy = (float)iy + 0.5f;
-                PixelFw st;
-                pixel_fw(c, 1.f, -1.f, 1.f, pcx, pcy, W, H, d.sigma_scale, st);
-                float4 g[3];
-                pixel_bw(st, c, 1.f, tgt[p], d.inv_px, W, H, d.sigma_scale, g);
+            for (int q = 0; q < kSampleLanes; q++) {
 #pragma unroll
                 for (int k = 0; k < 3; k++) {
-                    acc[k].x += g[k].x;
-                    acc[k].y += g[k].y;
-                    acc[k].z += g[k].z;
-                    acc[k].w += g[k].w;
+                    const float gx = __shfl(g[k].x, gbase + q);
+                    const float gy = __shfl(g[k].y, gbase + q);
+                    const float gz = __shfl(g[k].z, gbase + q);
+                    const float gw = __shfl(g[k].w, gbase + q);
+                    acc[k].x += gx;
+                    acc[k].y += gy;
+                    acc[k].z += gz;
+                    acc[k].w += gw;
                 }
             }
         }
     }
+    if (valid && j == 0) {
+        if (rim) {
+            d.rimf[item] = 0;
+        }
+        float4* dst = d.gtri + (size_t)view * 3 * d.g.n_faces;
 #pragma unroll
-    for (int k = 0; k < 3; k++) {
-        dst[(size_t)k * d.g.n_faces + f] = acc[k];
+        for (int k = 0; k < 3; k++) {
+            dst[(size_t)k * d.g.n_faces + f] = acc[k];
+        }
     }
 }
 
@@ -514,7 +522,8 @@ int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
             hipLaunchKernelGGL(k_hsr_setup, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
             break;
         case 1:
-            hipLaunchKernelGGL(k_hsr_raster, dim3(4u * kHeavyCap + block_grid(g) * g.n_views),
+            hipLaunchKernelGGL(k_hsr_raster,
+                               dim3(4u * kHeavySegs * d.heavy.cap + block_grid(g) * g.n_views),
                                dim3(64), 0, s, d);
             break;
         case 2: {
@@ -534,7 +543,8 @@ int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
             break;
         }
         case 3:
-            hipLaunchKernelGGL(k_hsr_face_bwd, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
+            hipLaunchKernelGGL(k_hsr_face_bwd, dim3(div_up(nvf, 256 / kSampleLanes)), dim3(256),
+                               0, s, d);
             break;
         default:
             switch (g.n_views) {
@@ -624,6 +634,8 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
         rc = rc ? rc : plan_alloc(p, &d.recs, N * F);
         rc = rc ? rc : plan_alloc(p, &d.cull, N * F);
         rc = rc ? rc : plan_alloc(p, &d.fscr, N * F * 2);
+        rc = rc ? rc : plan_alloc(p, &d.rimf, N * F);
+        d.heavy.cap = heavy_seg_cap(d.g.n_tiles * d.g.n_views);
         rc = rc ? rc : plan_alloc(p, &d.heavy.count, kHeavySegs);
         rc = rc ? rc : plan_alloc(p, &d.heavy.list, kHeavyCap);
         rc = rc ? rc : plan_alloc(p, &d.heavy.slot, (size_t)N * d.g.n_tiles);
@@ -668,6 +680,9 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
         hipError_t e = hipMemsetAsync(d.bins.counts, 0, sizeof(uint32_t) * d.bins.n_bins, ctx->stream);
         if (e == hipSuccess && d.heavy.count) {
             e = hipMemsetAsync(d.heavy.count, 0, sizeof(uint32_t) * kHeavySegs, ctx->stream);
+        }
+        if (e == hipSuccess && d.rimf) {
+            e = hipMemsetAsync(d.rimf, 0, N * F, ctx->stream);
         }
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
         if (e != hipSuccess) {

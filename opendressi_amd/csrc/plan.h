@@ -76,6 +76,8 @@ struct HsrDev {
                               // setup's appends, segment counters cleared by the
                               // face backward)
     uint32_t* ids;            // [N][S][S] face + 1 (bit 31: rim winner), 0 bg
+    uint8_t* rimf;            // [N][F] HardSoftRas: 1 if the face won a rim pixel
+                              // (set by the raster, cleared by the face backward)
     float* loss;              // [S][S]
     float* pred;              // [N][S][S] or null
     float4* gtri;             // [N][3][F]

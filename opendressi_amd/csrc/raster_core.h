@@ -1016,7 +1016,15 @@ struct HeavyList {
     uint32_t* count;  // [kHeavySegs]
     uint32_t* list;   // [kHeavySegs][kHeavySegCap] bins
     uint32_t* slot;   // [n_bins] slot of a bin whose count reached kHeavyBin
+    uint32_t cap;     // slots per segment the consumer takes (<= kHeavySegCap)
 };
+
+// Slots per segment for a problem of n_bins bins: at most a quarter of the
+// bins go first (the rest of a segment stays with the others).
+inline uint32_t heavy_seg_cap(uint32_t n_bins) {
+    const uint32_t c = n_bins / (4u * kHeavySegs);
+    return c < 1u ? 1u : (c > kHeavySegCap ? kHeavySegCap : c);
+}
 
 __device__ __forceinline__ uint32_t heavy_seg(uint32_t bin) {
     return (bin * 2654435761u) >> 26;  // top 6 bits: kHeavySegs = 64
@@ -1036,7 +1044,7 @@ __device__ __forceinline__ void heavy_note(const HeavyList* h, uint32_t bin, uin
 
 // The bin is listed (resolved by the heavy part of the raster's grid).
 __device__ __forceinline__ bool heavy_listed(const HeavyList& h, uint32_t count, uint32_t bin) {
-    return count >= kHeavyBin && h.slot[bin] < kHeavySegCap;
+    return count >= kHeavyBin && h.slot[bin] < h.cap;
 }
 
 // One (face, tile) pair of bin_append's pass (0: count window pairs in LDS
