@@ -489,9 +489,11 @@ struct dressi_hsr_plan {
     std::vector<void*> allocs;
     void* bin_mem = nullptr;
     bool mesh_set = false, targets_set = false, state_set = false;
-    hipGraph_t graph = nullptr;
+    hipGraph_t graph = nullptr;  // one iteration
     hipGraphExec_t exec = nullptr;
-    hipStream_t graph_stream = nullptr;  // stream the exec was instantiated for
+    hipGraph_t graph_batch = nullptr;  // kGraphBatch iterations back to back
+    hipGraphExec_t exec_batch = nullptr;
+    hipStream_t graph_stream = nullptr;  // stream the execs were instantiated for
 };
 
 namespace {
@@ -504,6 +506,10 @@ int plan_alloc(dressi_hsr_plan* p, T** out, size_t count) {
     *out = (T*)ptr;
     return DRESSI_OK;
 }
+
+// Iterations per replay of the batched graph (dressi_hsr_step launches it
+// for every full batch of its count: fewer launch gaps between iterations).
+constexpr uint32_t kGraphBatch = 8;
 
 // Kernel k of one iteration: 0 setup + binning, 1 visibility raster,
 // 2 pred + loss, 3 face backward, 4 vertex backward + Adam.
@@ -580,13 +586,17 @@ int ready(dressi_hsr_plan* p) {
 }
 
 void drop_graph(dressi_hsr_plan* p) {
-    if (p->exec) {
-        hipGraphExecDestroy(p->exec);
-        p->exec = nullptr;
+    for (hipGraphExec_t* e : {&p->exec, &p->exec_batch}) {
+        if (*e) {
+            hipGraphExecDestroy(*e);
+            *e = nullptr;
+        }
     }
-    if (p->graph) {
-        hipGraphDestroy(p->graph);
-        p->graph = nullptr;
+    for (hipGraph_t* g : {&p->graph, &p->graph_batch}) {
+        if (*g) {
+            hipGraphDestroy(*g);
+            *g = nullptr;
+        }
     }
 }
 
@@ -910,31 +920,48 @@ int dressi_hsr_step(dressi_hsr_plan* p, uint32_t n_iters) {
     hipStream_t s = p->ctx->stream;
     if (!p->exec || p->graph_stream != s) {
         drop_graph(p);
-        // capture one iteration on a private stream, then replay on `s`
-        hipStream_t cap_stream = nullptr;
-        DRESSI_TRY_HIP(hipStreamCreateWithFlags(&cap_stream, hipStreamNonBlocking));
-        hipError_t e = hipStreamBeginCapture(cap_stream, hipStreamCaptureModeThreadLocal);
-        int rc = DRESSI_OK;
-        if (e == hipSuccess) {
-            rc = enqueue_iteration(p, cap_stream);
-            hipError_t e2 = hipStreamEndCapture(cap_stream, &p->graph);
-            if (!rc && e2 != hipSuccess) {
-                set_error("graph capture failed: %s", hipGetErrorString(e2));
+        // capture one iteration, and kGraphBatch of them, on a private
+        // stream, then replay on `s`
+        for (int which = 0; which < 2; which++) {
+            hipStream_t cap_stream = nullptr;
+            DRESSI_TRY_HIP(hipStreamCreateWithFlags(&cap_stream, hipStreamNonBlocking));
+            hipError_t e = hipStreamBeginCapture(cap_stream, hipStreamCaptureModeThreadLocal);
+            int rc = DRESSI_OK;
+            hipGraph_t g = nullptr;
+            if (e == hipSuccess) {
+                const uint32_t reps = which == 0 ? 1u : kGraphBatch;
+                for (uint32_t r = 0; r < reps && !rc; r++) {
+                    rc = enqueue_iteration(p, cap_stream);
+                }
+                hipError_t e2 = hipStreamEndCapture(cap_stream, &g);
+                if (!rc && e2 != hipSuccess) {
+                    set_error("graph capture failed: %s", hipGetErrorString(e2));
+                    rc = DRESSI_ERR_HIP;
+                }
+            } else {
+                set_error("hipStreamBeginCapture failed: %s", hipGetErrorString(e));
                 rc = DRESSI_ERR_HIP;
             }
-        } else {
-            set_error("hipStreamBeginCapture failed: %s", hipGetErrorString(e));
-            rc = DRESSI_ERR_HIP;
-        }
-        hipStreamDestroy(cap_stream);
-        if (rc) {
-            drop_graph(p);
-            return rc;
+            hipStreamDestroy(cap_stream);
+            if (which == 0) {
+                p->graph = g;
+            } else {
+                p->graph_batch = g;
+            }
+            if (rc) {
+                drop_graph(p);
+                return rc;
+            }
         }
         DRESSI_TRY_HIP(hipGraphInstantiate(&p->exec, p->graph, nullptr, nullptr, 0));
+        DRESSI_TRY_HIP(hipGraphInstantiate(&p->exec_batch, p->graph_batch, nullptr, nullptr, 0));
         p->graph_stream = s;
     }
-    for (uint32_t i = 0; i < n_iters; i++) {
+    uint32_t i = 0;
+    for (; i + kGraphBatch <= n_iters; i += kGraphBatch) {
+        DRESSI_TRY_HIP(hipGraphLaunch(p->exec_batch, s));
+    }
+    for (; i < n_iters; i++) {
         DRESSI_TRY_HIP(hipGraphLaunch(p->exec, s));
     }
     return DRESSI_OK;
