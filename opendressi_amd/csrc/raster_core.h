@@ -1111,11 +1111,21 @@ __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom
         incl += lane >= o ? v : 0u;
     }
     lds.off[tid + 1] = incl;
+    // the window's corner and the last view: reduced per wave, then one LDS
+    // atomic per wave
+    int wtx = valid ? tx0 : 0x7fffffff, wty = valid ? ty0 : 0x7fffffff;
+    int wview = valid ? (int)view : -1;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        wtx = min(wtx, __shfl_xor(wtx, o));
+        wty = min(wty, __shfl_xor(wty, o));
+        wview = max(wview, __shfl_xor(wview, o));
+    }
     __syncthreads();
-    if (valid) {
-        atomicMin(&lds.win[0], tx0);
-        atomicMin(&lds.win[1], ty0);
-        atomicMax(&lds.win[2], (int)view);
+    if (lane == 0) {
+        atomicMin(&lds.win[0], wtx);
+        atomicMin(&lds.win[1], wty);
+        atomicMax(&lds.win[2], wview);
     }
     uint32_t wave_base = 0;
     for (int wv = 0; wv < (tid >> 6); wv++) {
