@@ -933,10 +933,13 @@ __device__ __forceinline__ void walk_bin(const Rec* recs, const BinBuffers& b, u
 // Fixed-capacity soft bins, appended from the setup kernels. A face goes to
 // the tiles of its pixel bbox that its triangle reaches (the separating-axis
 // test of the block culls, with the record's margin; every tile of the bbox
-// when it has none). A thread walks the tiles of its own face when they are
-// at most kBinBig; the (face, tile) pairs of larger faces are dealt to all
-// threads of the workgroup (a scan of their tile counts, a binary search
-// per pair), so a face spanning many tiles does not hold one thread. Pairs
+// when it has none), walked row by row over the columns the triangle can
+// reach (tri_row_span: the thin, tilted soft triangles of edge-on faces have
+// bboxes of hundreds of tiles but touch a band of them). A thread walks the
+// tiles of its own face when its bbox holds at most kBinBig; the tile rows of
+// larger faces are dealt to all threads of the workgroup (a scan of their
+// row counts, a binary search per row), so a face spanning many tiles does
+// not hold one thread. Pairs
 // in the workgroup's LDS window of tiles are counted in LDS (one global
 // atomic per touched window tile), then written; the others (outside the
 // window, or a workgroup spanning two views) append with direct atomics. All
@@ -960,7 +963,7 @@ struct BinLds {
     int win[4];                     // tx0, ty0, view0, mixed-view flag
     uint32_t off[kBinThreads + 1];  // exclusive scan of the threads' tile counts
     uint32_t f[kBinThreads], view[kBinThreads];
-    int tx0[kBinThreads], ty0[kBinThreads], nx[kBinThreads];
+    int tx0[kBinThreads], ty0[kBinThreads], tx1[kBinThreads];
     BinTri tri[kBinThreads];
 };
 
@@ -983,6 +986,43 @@ __device__ __forceinline__ bool tri_reaches_tile(const BinTri& t, int tx, int ty
         hit = hit && !(gk < -t.m);
     }
     return hit;
+}
+
+// The tiles [*a, *b] of tile row ty (within [tx0, tx1]) that triangle t can
+// reach: along a row of tiles each edge's test in tri_reaches_tile is
+// monotone in the tile column, so every edge bounds the columns on one side;
+// the bounds are widened by one tile (rounding) and the tiles in the range
+// still take the exact test. Non-finite bounds leave the side open.
+__device__ __forceinline__ void tri_row_span(const BinTri& t, int ty, int tx0, int tx1, int* a,
+                                             int* b) {
+    *a = tx0;
+    *b = tx1;
+    if (!(t.m >= 0.f)) {
+        return;
+    }
+    const float y0 = (float)(ty * kTile) + 0.5f, y1 = y0 + (float)(kTile - 1);
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        const int k1 = (k + 1) % 3;
+        const float ex = t.s * (t.x[k1] - t.x[k]);
+        const float ey = t.s * (t.y[k1] - t.y[k]);
+        const float A = smax(ex * (y0 - t.y[k]), ex * (y1 - t.y[k]));
+        if (ey > 0.f) {
+            // the test's best column is the tile's first: x0 <= x_k + (A + m) / ey
+            const float c = ((t.x[k] + (A + t.m) / ey) - 0.5f) / (float)kTile;
+            if (c >= -1e6f && c <= 1e6f) {
+                *b = min(*b, (int)floorf(c) + 1);
+            }
+        } else if (ey < 0.f) {
+            // the tile's last column: x1 >= x_k + (A + m) / ey
+            const float c = ((t.x[k] + (A + t.m) / ey) - (float)kTile + 0.5f) / (float)kTile;
+            if (c >= -1e6f && c <= 1e6f) {
+                *a = max(*a, (int)ceilf(c) - 1);
+            }
+        } else if (A < -t.m) {
+            *a = tx1 + 1;  // the row is outside this edge
+        }
+    }
 }
 
 // Tile-test triangle of a soft record: the soft triangle (every fragment
@@ -1098,12 +1138,12 @@ __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom
         lds.view[tid] = view;
         lds.tx0[tid] = tx0;
         lds.ty0[tid] = ty0;
-        lds.nx[tid] = tx1 - tx0 + 1;
+        lds.tx1[tid] = tx1;
         lds.tri[tid] = tri;
     }
-    // inclusive scan of the large faces' tile counts: within each wave, then
-    // across waves
-    uint32_t incl = big ? nt : 0u;
+    // inclusive scan of the large faces' tile-row counts: within each wave,
+    // then across waves
+    uint32_t incl = big ? (uint32_t)(ty1 - ty0 + 1) : 0u;
     const int lane = tid & 63;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -1149,13 +1189,18 @@ __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom
             BinTri t = tri;
             t.m = nt <= 4u ? -1.f : t.m;
             for (int ty = ty0; ty <= ty1; ty++) {
-                for (int tx = tx0; tx <= tx1; tx++) {
+                // small bboxes: the per-tile test alone is cheaper
+                int ta = tx0, tb = tx1;
+                if (nt > 16u) {
+                    tri_row_span(t, ty, tx0, tx1, &ta, &tb);
+                }
+                for (int tx = ta; tx <= tb; tx++) {
                     bin_pair(b, g, lds, pass, mixed, wx0, wy0, f, view, t, tx, ty, heavy);
                 }
             }
         }
         for (uint32_t p = (uint32_t)tid; p < total; p += (uint32_t)nthr) {
-            // the face q with off[q] <= p < off[q + 1]
+            // the face q with off[q] <= p < off[q + 1], and its tile row
             int lo = 0, hi = nthr - 1;
             while (lo < hi) {
                 const int mid = (lo + hi + 1) >> 1;
@@ -1165,10 +1210,14 @@ __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom
                     hi = mid - 1;
                 }
             }
-            const int i = (int)(p - lds.off[lo]);
-            const int qnx = lds.nx[lo];
-            bin_pair(b, g, lds, pass, mixed, wx0, wy0, lds.f[lo], lds.view[lo], lds.tri[lo],
-                     lds.tx0[lo] + i % qnx, lds.ty0[lo] + i / qnx, heavy);
+            const int ty = lds.ty0[lo] + (int)(p - lds.off[lo]);
+            const BinTri t = lds.tri[lo];
+            int ta, tb;
+            tri_row_span(t, ty, lds.tx0[lo], lds.tx1[lo], &ta, &tb);
+            for (int tx = ta; tx <= tb; tx++) {
+                bin_pair(b, g, lds, pass, mixed, wx0, wy0, lds.f[lo], lds.view[lo], t, tx, ty,
+                         heavy);
+            }
         }
         if (pass == 0) {
             __syncthreads();
