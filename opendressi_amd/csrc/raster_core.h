@@ -474,6 +474,7 @@ __device__ __forceinline__ bool box_hits(int x0, int y0, int x1, int y1, int bx,
 struct CullLoad {
     CullRec c;
     float w[16];
+    float zc;  // phase A
     float sx[3], sy[3], s_margin;
     float hx[3], hy[3];
 };
@@ -491,6 +492,9 @@ __device__ __forceinline__ CullLoad load_cull(const SoftRec* recs, const CullRec
         l.w[4 * i + 1] = v.y;
         l.w[4 * i + 2] = v.z;
         l.w[4 * i + 3] = v.w;
+    }
+    if (!kSoft) {
+        l.zc = recs[f].zc;
     }
     if (kSoft) {
         const float4 a = *(const float4*)&recs[f].sx[0];  // sx0 sx1 sx2 sy0
@@ -539,18 +543,22 @@ __device__ __forceinline__ bool cull_soft(const CullLoad& l, int bx, int by) {
 
 // Number of list entries of a bin and whether it overflowed (then every face
 // of the view is walked; each face's own bbox keeps the result exact).
+// `pre` = the list's entry at the calling lane (a bin has room for at least
+// 64 entries), loaded together with the counter.
 struct BinView {
     const uint32_t* list;
     uint32_t n;
     bool implicit;
+    uint32_t pre;
 };
 
 __device__ __forceinline__ BinView bin_view(const BinBuffers& b, uint32_t bin, uint32_t n_faces) {
     BinView v;
+    v.list = b.list + (size_t)bin * b.cap;
     const uint32_t cnt = b.counts[bin];
+    v.pre = v.list[threadIdx.x & 63u];
     v.implicit = cnt > b.cap;
     v.n = v.implicit ? n_faces : cnt;
-    v.list = b.list + (size_t)bin * b.cap;
     return v;
 }
 
@@ -620,8 +628,11 @@ constexpr uint32_t kFarCap = 512;
 struct ResolveLds {
     SoftRec rec[kStage];
     union {
-        uint32_t later[kLaterCap];  // phase A: deferred faces
-        uint32_t far[kFarCap];      // phase B: far faces (as face + 1)
+        struct {
+            uint32_t later[kLaterCap];  // phase A: deferred faces
+            float later_zc[kLaterCap];  // and their depth floors
+        };
+        uint32_t far[kFarCap];  // phase B: far faces (as face + 1)
     };
 };
 
@@ -735,11 +746,13 @@ __device__ __forceinline__ PixelBest resolve_block(const SoftRec* recs, const Cu
         const uint32_t e = base + (uint32_t)lane;
         uint32_t f = 0;
         bool keep = false, pos = false;
+        float zc = 0.f;
         if (e < bv.n) {
-            f = bv.implicit ? e : bv.list[e];
+            f = bv.implicit ? e : (base == 0 ? bv.pre : bv.list[e]);
             const CullLoad l = load_cull<false>(recs, cull, f);
             keep = cull_in_a(l, bx, by, true);
             pos = cull_pos(l);
+            zc = l.zc;
         }
         bool hold = defer && keep && pos;
         const uint64_t mh0 = __ballot(hold);
@@ -747,6 +760,7 @@ __device__ __forceinline__ PixelBest resolve_block(const SoftRec* recs, const Cu
         const uint64_t mh = __ballot(hold);
         if (hold) {
             lds.later[n_later + lanes_below(mh)] = f;
+            lds.later_zc[n_later + lanes_below(mh)] = zc;
         }
         n_later += (uint32_t)__popcll(mh);
         visit_staged(recs, f, __ballot(keep && !hold), lds, fold_a);
@@ -767,7 +781,7 @@ __device__ __forceinline__ PixelBest resolve_block(const SoftRec* recs, const Cu
             if (i < n_later) {
                 f = lds.later[i];
                 // zc >= 0: bit order is value order
-                keep = __float_as_uint(recs[f].zc) <= zmax;
+                keep = __float_as_uint(lds.later_zc[i]) <= zmax;
             }
             visit_staged(recs, f, __ballot(keep), lds, fold_a);
         }
@@ -791,7 +805,7 @@ __device__ __forceinline__ PixelBest resolve_block(const SoftRec* recs, const Cu
         uint32_t f = 0;
         bool keep = false, in_a = false, near = false;
         if (e < bv.n) {
-            f = bv.implicit ? e : bv.list[e];
+            f = bv.implicit ? e : (base == 0 ? bv.pre : bv.list[e]);
             const CullLoad l = load_cull<true>(recs, cull, f);
             keep = cull_soft(l, bx, by);
             in_a = keep && cull_in_a(l, bx, by, false);
