@@ -57,8 +57,11 @@ typedef struct dressi_ctx dressi_ctx;
 int dressi_ctx_create(int device, dressi_ctx** out);
 int dressi_ctx_destroy(dressi_ctx* ctx);
 /* Use a caller-owned stream (e.g. the current torch stream) instead of the
- * context's own; NULL restores the context stream. */
+ * context's own, which is non-blocking. NULL selects the device's null
+ * stream, the handle torch reports for its default stream.
+ * dressi_ctx_reset_stream restores the context's own stream. */
 int dressi_ctx_set_stream(dressi_ctx* ctx, void* stream);
+int dressi_ctx_reset_stream(dressi_ctx* ctx);
 void* dressi_ctx_stream(dressi_ctx* ctx);
 /* Waits for all work queued on the context stream (the reference's fence
  * wait, src/vk/executor.cpp:1020-1027). */
@@ -347,6 +350,23 @@ int dressi_texture_bilinear_bwd(dressi_ctx* ctx, const float* gy,
                                 uint32_t n_comp, uint32_t sw, uint32_t sh,
                                 const float* inv_uv, uint32_t tw, uint32_t th,
                                 const float* uv, float* out);
+/* F::Texture forward, nearest (src/core/f_ops.cpp:2605-2639; the reference
+ * has only its GLSL texture() read through a nearest, clamp-to-edge sampler,
+ * src/vk/executor.cpp:192-202): tex {tw,th} x n_comp (1..4) at texel
+ * (clamp(floor(u tw), 0, tw - 1), clamp(floor(v th), 0, th - 1)) for each
+ * uv {uw,uh} VEC2 -> out {uw,uh} x n_comp. */
+int dressi_texture_nearest(dressi_ctx* ctx, const float* tex, uint32_t tw,
+                           uint32_t th, uint32_t n_comp, const float* uv,
+                           uint32_t uw, uint32_t uh, float* out);
+/* Its backward w.r.t. the texture, GatherByInverseUV (f_ops.cpp:2586-2601,
+ * GLSL src/codegen/glsl_codegen.cpp:657-703): per texel the inverse-UV
+ * anchor (as for the bilinear gather), then the first screen pixel of the
+ * 7 x 7 window around it (row order) whose uv truncates to the texel gives
+ * its gradient gy {sw,sh} x n_comp (zero when none). out {tw,th} x n_comp. */
+int dressi_texture_nearest_bwd(dressi_ctx* ctx, const float* gy,
+                               uint32_t n_comp, uint32_t sw, uint32_t sh,
+                               const float* inv_uv, uint32_t tw, uint32_t th,
+                               const float* uv, float* out);
 /* ScreenAttr (src/core/mesh_utils.cpp:191-203) on the device: clip {V,1}
  * VEC4 -> {V,1} VEC4 (screen x, screen y, 1, 0). */
 int dressi_screen_attr(dressi_ctx* ctx, const float* clip, uint32_t n_verts,

@@ -66,6 +66,7 @@ _SIGS = {
     "dressi_ctx_create": (_I, [_I, C.POINTER(_P)]),
     "dressi_ctx_destroy": (_I, [_P]),
     "dressi_ctx_set_stream": (_I, [_P, _P]),
+    "dressi_ctx_reset_stream": (_I, [_P]),
     "dressi_ctx_stream": (_P, [_P]),
     "dressi_ctx_synchronize": (_I, [_P]),
     "dressi_ctx_device_name": (_I, [_P, C.c_char_p, _S]),
@@ -101,6 +102,8 @@ _SIGS = {
     "dressi_brdf_lut": (_I, [_P, _U, _U, _U, _P]),
     "dressi_texture_bilinear": (_I, [_P, _P, _U, _U, _U, _P, _U, _U, _P]),
     "dressi_texture_bilinear_bwd": (_I, [_P, _P, _U, _U, _U, _P, _U, _U, _P, _P]),
+    "dressi_texture_nearest": (_I, [_P, _P, _U, _U, _U, _P, _U, _U, _P]),
+    "dressi_texture_nearest_bwd": (_I, [_P, _P, _U, _U, _U, _P, _U, _U, _P, _P]),
     "dressi_screen_attr": (_I, [_P, _P, _U, _U, _U, _P]),
     "dressi_uv_sphere": (_I, [_U, _U, _UP, _UP, _FP, _FP, _FP]),
     "dressi_uv_as_clip": (None, [_FP, _U, _FP]),

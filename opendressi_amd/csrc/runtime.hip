@@ -119,7 +119,14 @@ int dressi_ctx_destroy(dressi_ctx* ctx) {
 
 int dressi_ctx_set_stream(dressi_ctx* ctx, void* stream) {
     DRESSI_REQUIRE(ctx, "NULL context");
-    ctx->stream = stream ? (hipStream_t)stream : ctx->own_stream;
+    // NULL is the device's null stream: torch's default stream has handle 0
+    ctx->stream = (hipStream_t)stream;
+    return DRESSI_OK;
+}
+
+int dressi_ctx_reset_stream(dressi_ctx* ctx) {
+    DRESSI_REQUIRE(ctx, "NULL context");
+    ctx->stream = ctx->own_stream;
     return DRESSI_OK;
 }
 

@@ -146,6 +146,91 @@ __global__ __launch_bounds__(256) void k_gather_bilinear_op(const float* gy, uin
     }
 }
 
+// Anchor of texel (tx, ty) in the inverse-UV table: its own entry when
+// covered (.z > 0.5), else the first covered entry of the +-4 neighbourhood
+// in row order (f_ops.cpp:2665-2690; the GLSL of GatherByInverseUV,
+// src/codegen/glsl_codegen.cpp:664-685, uses the same search).
+__device__ __forceinline__ float4 inv_uv_anchor(const float4* inv_uv, int tw, int th, int tx,
+                                                int ty) {
+    float4 iv = inv_uv[(size_t)ty * tw + tx];
+    for (int ny = -4; ny <= 4 && iv.z < 0.5f; ny++) {
+        for (int nx = -4; nx <= 4; nx++) {
+            const int px = tx + nx, py = ty + ny;
+            if (px < 0 || py < 0 || px >= tw || py >= th) {
+                continue;
+            }
+            iv = inv_uv[(size_t)py * tw + px];
+            if (iv.z > 0.5f) {
+                break;
+            }
+        }
+    }
+    return iv;
+}
+
+// F::Texture forward (src/core/f_ops.cpp:2605-2639): the GLSL texture()
+// read of a nearest, clamp-to-edge sampler (src/vk/executor.cpp:192-202):
+// texel (clamp(floor(u tw), 0, tw - 1), clamp(floor(v th), 0, th - 1)).
+__global__ __launch_bounds__(256) void k_texture_nearest_op(const float* tex, int tw, int th,
+                                                            uint32_t n_comp, const float2* uv,
+                                                            size_t n_px, float* out) {
+    const size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= n_px) {
+        return;
+    }
+    const float2 q = uv[p];
+    const float fx = floorf(q.x * (float)tw), fy = floorf(q.y * (float)th);
+    // NaN compares false: it takes texel 0, as a clamp of NaN would
+    const int ix = fx >= (float)(tw - 1) ? tw - 1 : (fx > 0.f ? (int)fx : 0);
+    const int iy = fy >= (float)(th - 1) ? th - 1 : (fy > 0.f ? (int)fy : 0);
+    const float* t = tex + ((size_t)iy * tw + ix) * n_comp;
+    for (uint32_t c = 0; c < n_comp; c++) {
+        out[p * n_comp + c] = t[c];
+    }
+}
+
+// GatherByInverseUV, F::Texture's backward w.r.t. the texture (its GLSL,
+// src/codegen/glsl_codegen.cpp:657-703): per texel the anchor's screen
+// pixel (truncated), then the first pixel of the 7 x 7 window around it
+// (row order) whose uv truncates to this texel; the texel takes that
+// pixel's gradient (zero when none).
+__global__ __launch_bounds__(256) void k_gather_nearest_op(const float* gy, uint32_t n_comp,
+                                                           int sw, int sh, const float4* inv_uv,
+                                                           int tw, int th, const float2* uv,
+                                                           float* out) {
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= tw * th) {
+        return;
+    }
+    const int ty = q / tw, tx = q - ty * tw;
+    const float4 iv = inv_uv_anchor(inv_uv, tw, th, tx, ty);
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+    if (iv.z > 0.5f) {
+        const int scx = (int)iv.x, scy = (int)iv.y;
+        bool found = false;
+        for (int dy = -3; dy <= 3 && !found; dy++) {
+            for (int dx = -3; dx <= 3; dx++) {
+                const int spx = scx + dx, spy = scy + dy;
+                if (spx < 0 || spy < 0 || spx >= sw || spy >= sh) {
+                    continue;
+                }
+                const size_t sp = (size_t)spy * sw + spx;
+                const float2 su = uv[sp];
+                if ((int)(su.x * (float)tw) == tx && (int)(su.y * (float)th) == ty) {
+                    for (uint32_t c = 0; c < n_comp; c++) {
+                        o[c] = gy[sp * n_comp + c];
+                    }
+                    found = true;
+                    break;
+                }
+            }
+        }
+    }
+    for (uint32_t c = 0; c < n_comp; c++) {
+        out[(size_t)q * n_comp + c] = o[c];
+    }
+}
+
 // ScreenAttr (src/core/mesh_utils.cpp:191-203).
 __global__ __launch_bounds__(256) void k_screen_attr_op(const float4* clip, uint32_t n, float W,
                                                         float H, float4* out) {
@@ -718,6 +803,37 @@ int dressi_texture_bilinear_bwd(dressi_ctx* ctx, const float* gy, uint32_t n_com
     if (!tw || !th) return DRESSI_OK;
     DRESSI_TRY_HIP(hipSetDevice(ctx->device));
     hipLaunchKernelGGL(k_gather_bilinear_op, dim3(div_up(tw * th, 256)), dim3(256), 0,
+                       ctx->stream, gy, n_comp, (int)sw, (int)sh, (const float4*)inv_uv, (int)tw,
+                       (int)th, (const float2*)uv, out);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+int dressi_texture_nearest(dressi_ctx* ctx, const float* tex, uint32_t tw, uint32_t th,
+                           uint32_t n_comp, const float* uv, uint32_t uw, uint32_t uh,
+                           float* out) {
+    DRESSI_REQUIRE(ctx && tex && uv && out, "bad arguments");
+    DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "n_comp must be 1..4");
+    DRESSI_REQUIRE(tw > 0 && th > 0 && tw <= 65536 && th <= 65536, "bad texture size");
+    const size_t n = (size_t)uw * uh;
+    if (!n) return DRESSI_OK;
+    DRESSI_TRY_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(k_texture_nearest_op, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0,
+                       ctx->stream, tex, (int)tw, (int)th, n_comp, (const float2*)uv, n, out);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+int dressi_texture_nearest_bwd(dressi_ctx* ctx, const float* gy, uint32_t n_comp, uint32_t sw,
+                               uint32_t sh, const float* inv_uv, uint32_t tw, uint32_t th,
+                               const float* uv, float* out) {
+    DRESSI_REQUIRE(ctx && gy && inv_uv && uv && out, "bad arguments");
+    DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "n_comp must be 1..4");
+    DRESSI_REQUIRE((uint64_t)tw * th < (1ull << 31) && (uint64_t)sw * sh < (1ull << 40),
+                   "size too large");
+    if (!tw || !th) return DRESSI_OK;
+    DRESSI_TRY_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(k_gather_nearest_op, dim3(div_up(tw * th, 256)), dim3(256), 0,
                        ctx->stream, gy, n_comp, (int)sw, (int)sh, (const float4*)inv_uv, (int)tw,
                        (int)th, (const float2*)uv, out);
     DRESSI_CHECK_LAUNCH();

@@ -215,6 +215,32 @@ def texture_bilinear_bwd(ctx: Context, gy: torch.Tensor, inv_uv: torch.Tensor,
     return out
 
 
+def texture_nearest(ctx: Context, tex: torch.Tensor, uv: torch.Tensor) -> torch.Tensor:
+    """F::Texture forward (src/core/f_ops.cpp:2605-2639; nearest, clamp to
+    edge): tex (TH, TW, C), uv (H, W, 2) -> (H, W, C)."""
+    _prep(ctx)
+    th, tw, nc = tex.shape
+    uh, uw = uv.shape[:2]
+    out = torch.empty((uh, uw, nc), dtype=torch.float32, device=uv.device)
+    check(lib.dressi_texture_nearest(ctx.handle, _ptr(tex, "tex"), tw, th, nc, _ptr(uv, "uv"),
+                                     uw, uh, _ptr(out, "out")))
+    return out
+
+
+def texture_nearest_bwd(ctx: Context, gy: torch.Tensor, inv_uv: torch.Tensor,
+                        uv: torch.Tensor) -> torch.Tensor:
+    """GatherByInverseUV (src/core/f_ops.cpp:2586-2601): gy (H, W, C), inv_uv
+    (TH, TW, 4), uv (H, W, 2) -> d/d tex (TH, TW, C)."""
+    _prep(ctx)
+    sh, sw, nc = gy.shape
+    th, tw = inv_uv.shape[:2]
+    out = torch.empty((th, tw, nc), dtype=torch.float32, device=gy.device)
+    check(lib.dressi_texture_nearest_bwd(ctx.handle, _ptr(gy, "gy"), nc, sw, sh,
+                                         _ptr(inv_uv, "inv_uv"), tw, th, _ptr(uv, "uv"),
+                                         _ptr(out, "out")))
+    return out
+
+
 def screen_attr(ctx: Context, clip: torch.Tensor, width: int, height: int) -> torch.Tensor:
     """ScreenAttr (src/core/mesh_utils.cpp:191-203): clip (V, 4) -> (V, 4)."""
     _prep(ctx)

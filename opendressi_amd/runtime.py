@@ -39,7 +39,12 @@ class Context:
             pass
 
     def set_stream(self, stream_ptr: int | None) -> None:
-        check(lib.dressi_ctx_set_stream(self.handle, C.c_void_p(stream_ptr or 0)))
+        """Order the context's work on `stream_ptr` (0: the null stream, which
+        is torch's default stream); None restores the context's own."""
+        if stream_ptr is None:
+            check(lib.dressi_ctx_reset_stream(self.handle))
+        else:
+            check(lib.dressi_ctx_set_stream(self.handle, C.c_void_p(stream_ptr)))
 
     def use_torch_stream(self) -> None:
         """Order this context's work on torch's current HIP stream."""

@@ -1,0 +1,407 @@
+"""nvdiffrast-compatible differentiable ops over the library's HIP kernels
+(python/dressi/torch/ops.py:95-698).
+
+Each op runs the same per-op kernels the C ABI exports (rasterize,
+LookupFaces/FaceFetch, Texture, AntiAlias, SoftClip/RasterizeSoft and their
+backward kernels), stream-ordered on torch's current stream of the context's
+device, with no host round trip. The backward of every op composes the
+reference's backward kernels exactly as the reference's backward builder does
+(src/core/build_backward.cpp:62-149): the same kernels, the same operand
+order, gradient contributions summed in descending creation order of the
+nodes that produced them. A batch of N items runs the per-item kernels N
+times; per-signature constants live in the context's `_engines`.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import ops as K
+from .context import RasterizeHipContext
+from .convert import (
+    channels,
+    check_resolution,
+    clip_grad_vk_to_gl,
+    clip_gl_to_vk,
+    image_batch,
+    split_batch,
+    sum_contribs,
+    to_dev,
+)
+from .provenance import InterpInfo, RastInfo, attach, lookup
+
+
+def _needs_grad(*tensors) -> bool:
+    return torch.is_grad_enabled() and any(
+        isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
+
+
+class _Engine:
+    """Per-signature device constants (and the antialias backward's
+    iteration counter), built once per key."""
+
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+def _seed(device: torch.device, value: float) -> torch.Tensor:
+    return torch.full((1,), float(value), dtype=torch.float32, device=device)
+
+
+# ------------------------------- rasterize ---------------------------------
+
+
+def rasterize(ctx: RasterizeHipContext, pos: torch.Tensor, tri: torch.Tensor, resolution,
+              ranges=None, grad_db: bool = False):
+    """Drop-in nvdiffrast rasterize (python/dressi/torch/ops.py:118-166):
+    returns (rast, rast_db) with rast[..., :] = (u, v, z/w, triangle_id + 1),
+    0 = background, rast_db zeros.
+
+    The mesh is unwelded per corner and rasterized with the corner
+    barycentric constants (1,0), (0,1), (0,0) plus (z, w) as perspective-
+    correct attributes; z/w is guarded by the coverage mask (0 on
+    background). Not differentiable w.r.t. `pos` (geometry gradients come
+    from antialias / rasterize_soft)."""
+    if ranges is not None:
+        raise NotImplementedError("opendressi_amd.torch: range mode is not supported")
+    del grad_db
+    h, w = check_resolution(resolution)
+    pos_b = split_batch(to_dev(pos, ctx.device, "pos"))
+    if pos_b.shape[2] != 4:
+        raise ValueError(f"pos must have 4 components, got {pos_b.shape[2]}")
+    md = ctx.mesh(tri)
+    n = pos_b.shape[0]
+
+    def build():
+        corner = torch.tensor([[1.0, 0.0], [0.0, 1.0], [0.0, 0.0]], dtype=torch.float32)
+        return _Engine(corner_uv=corner.repeat(md.n_faces, 1).to(ctx.device))
+
+    eng = ctx.engine(("rasterize", h, w, md.n_faces, md.n_verts, n), build)
+    clip_vk = clip_gl_to_vk(pos_b)
+    outs = []
+    with ctx.lock:
+        for i in range(n):
+            clip3 = clip_vk[i][md.unweld].contiguous()
+            attr4 = torch.cat([eng.corner_uv, pos_b[i][md.unweld][:, 2:4]], dim=1).contiguous()
+            g = K.rasterize(ctx._ctx, clip3, attr4, md.faces_seq, w, h)
+            tid = K.rasterize_face_id(ctx._ctx, clip3, md.faces_seq, w, h)
+            mask = (tid > 0.5).to(torch.float32)
+            zw = g[..., 2] / (g[..., 3] + (1.0 - mask))
+            outs.append(torch.stack([g[..., 0], g[..., 1], zw, tid], dim=-1))
+    rast = torch.stack(outs, 0).to(pos.device)
+    attach(rast, RastInfo(clip_vk=clip_vk, tri=tri, resolution=(h, w), extra={"ctx": ctx}))
+    return rast, torch.zeros_like(rast)
+
+
+# ------------------------------ interpolate --------------------------------
+
+
+class _InterpolateFn(torch.autograd.Function):
+    @staticmethod
+    def forward(fctx, attr, rast, vctx, md, rinfo):
+        dev = vctx.device
+        attr_d = to_dev(attr, dev, "attr")
+        rast_d = to_dev(rast, dev, "rast")
+        shared = attr_d.dim() == 2
+        c = channels(attr_d.shape[-1], "attr")
+        n = rast_d.shape[0]
+        outs = []
+        with vctx.lock:
+            for i in range(n):
+                a = attr_d if shared else attr_d[i].contiguous()
+                u = rast_d[i, ..., 0:1]
+                v = rast_d[i, ..., 1:2]
+                tid = rast_d[i, ..., 3].contiguous()
+                pix = [K.face_fetch(vctx._ctx, K.lookup_faces(vctx._ctx, a, md.faces_f, k), tid)
+                       for k in range(3)]
+                outs.append(u * pix[0] + v * pix[1] + ((1.0 - u) - v) * pix[2])
+        fctx.dressi = (vctx, md, rinfo, shared, c)
+        fctx.save_for_backward(attr, rast)
+        return torch.stack(outs, 0).to(attr.device)
+
+    @staticmethod
+    def backward(fctx, grad_out):
+        vctx, md, rinfo, shared, c = fctx.dressi
+        attr, rast = fctx.saved_tensors
+        dev = vctx.device
+        rast_d = to_dev(rast, dev, "rast")
+        g = to_dev(grad_out, dev, "grad_out")
+        n = rast_d.shape[0]
+        clip_vk = rinfo.clip_vk
+        zero = _seed(dev, 0.0)
+        per_item = []
+        with vctx.lock:
+            for i in range(n):
+                clip = clip_vk[i if clip_vk.shape[0] > 1 else 0].contiguous()
+                prj = [K.lookup_faces(vctx._ctx, clip, md.faces_f, k) for k in range(3)]
+                u = rast_d[i, ..., 0:1]
+                v = rast_d[i, ..., 1:2]
+                tid = rast_d[i, ..., 3].contiguous()
+                gi = g[i]
+                g_pix = [gi * u, gi * v, gi * ((1.0 - u) - v)]
+                contribs = []
+                for k in (2, 1, 0):
+                    g_face = K.face_fetch_bwd(vctx._ctx, g_pix[k].contiguous(), tid, prj[0],
+                                              prj[1], prj[2], zero, 1.0, 0)
+                    contribs.append(K.lookup_faces_bwd(vctx._ctx, g_face, md.faces_f, md.vft, k))
+                per_item.append(contribs)
+        if shared:
+            # the shared leaf's consumers, latest-created (last item) first
+            g_attr = sum_contribs([cb for contribs in reversed(per_item) for cb in contribs])
+        else:
+            g_attr = torch.stack([sum_contribs(cb) for cb in per_item], 0)
+        return g_attr.to(attr.device), None, None, None, None
+
+
+def interpolate(attr, rast, tri, rast_db=None, diff_attrs=None):
+    """Drop-in nvdiffrast interpolate (python/dressi/torch/ops.py:279-301):
+    returns (pixel_attr, None). attr is [V, C] (shared by the batch) or
+    [N, V, C], C in 1..4; differentiable w.r.t. `attr` through the exact
+    FaceFetch / LookupFaces backward. `rast` must come from rasterize()."""
+    if rast_db is not None or diff_attrs is not None:
+        raise NotImplementedError(
+            "opendressi_amd.torch.interpolate: rast_db/diff_attrs are not supported")
+    rinfo: RastInfo = lookup(rast, "rasterize")
+    vctx = rinfo.extra["ctx"]
+    md = vctx.mesh(tri)
+    out = _InterpolateFn.apply(attr, rast, vctx, md, rinfo)
+    attach(out, InterpInfo(attr=attr, rast_info=rinfo))
+    return out, None
+
+
+# -------------------------------- texture ----------------------------------
+
+
+class _TextureFn(torch.autograd.Function):
+    @staticmethod
+    def forward(fctx, tex, uv, vctx, iinfo):
+        dev = vctx.device
+        tex_d = to_dev(tex, dev, "tex")
+        if tex_d.dim() == 4:
+            if tex_d.shape[0] != 1:
+                raise NotImplementedError(
+                    "opendressi_amd.torch.texture: per-item texture batches are not supported "
+                    "(pass [H, W, C] or [1, H, W, C])")
+            tex_d = tex_d[0]
+        if tex_d.dim() != 3:
+            raise ValueError(f"tex must be [H, W, C] or [1, H, W, C], got {tuple(tex.shape)}")
+        channels(tex_d.shape[2], "tex")
+        uv_d = to_dev(uv, dev, "uv")
+        n = uv_d.shape[0]
+        with vctx.lock:
+            outs = [K.texture_nearest(vctx._ctx, tex_d, uv_d[i].contiguous()) for i in range(n)]
+        fctx.dressi = (vctx, iinfo)
+        fctx.save_for_backward(tex, uv)
+        return torch.stack(outs, 0).to(tex.device)
+
+    @staticmethod
+    def backward(fctx, grad_out):
+        vctx, iinfo = fctx.dressi
+        tex, uv = fctx.saved_tensors
+        dev = vctx.device
+        th, tw = (tex.shape[1], tex.shape[2]) if tex.dim() == 4 else (tex.shape[0], tex.shape[1])
+        uv_d = to_dev(uv, dev, "uv")
+        g = to_dev(grad_out, dev, "grad_out")
+        rinfo = iinfo.rast_info
+        h, w = rinfo.resolution
+        md = vctx.mesh(rinfo.tri)
+        vtx_uv = to_dev(iinfo.attr, dev, "uv attr")
+        n = uv_d.shape[0]
+        contribs = []
+        with vctx.lock:
+            for i in reversed(range(n)):
+                vuv = vtx_uv if vtx_uv.dim() == 2 else vtx_uv[i if vtx_uv.shape[0] > 1 else 0]
+                if vuv.shape[-1] != 2:
+                    raise ValueError("texture backward: the interpolated uv attribute must be [V, 2]")
+                one = torch.ones_like(vuv[:, :1])
+                uv_clip = torch.cat([vuv * 2.0 - 1.0, one * 0.5, one], dim=1).contiguous()
+                clip = rinfo.clip_vk[i if rinfo.clip_vk.shape[0] > 1 else 0].contiguous()
+                sattr = K.screen_attr(vctx._ctx, clip, w, h)
+                inv_uv = K.rasterize(vctx._ctx, uv_clip, sattr, md.faces_f, tw, th)
+                contribs.append(K.texture_nearest_bwd(vctx._ctx, g[i].contiguous(), inv_uv,
+                                                      uv_d[i].contiguous()))
+        g_tex = sum_contribs(contribs)
+        if tex.dim() == 4:
+            g_tex = g_tex.unsqueeze(0)
+        return g_tex.to(tex.device), None, None, None
+
+
+def texture(tex, uv, uv_da=None, mip_level_bias=None, mip=None, filter_mode="auto",
+            boundary_mode="wrap", max_mip_level=None):
+    """Drop-in nvdiffrast texture, nearest filtering with clamp-to-edge
+    texel lookup (python/dressi/torch/ops.py:417-444). Differentiable w.r.t.
+    `tex` through the inverse-UV gather, whose table is the mesh rasterized
+    in UV space carrying its screen positions; `uv` must come from
+    interpolate() (its provenance names the mesh and context)."""
+    if uv_da is not None or mip_level_bias is not None or mip is not None:
+        raise NotImplementedError("opendressi_amd.torch.texture: mipmaps unsupported")
+    if filter_mode not in ("auto", "nearest"):
+        raise NotImplementedError(
+            f"opendressi_amd.torch.texture: filter_mode='{filter_mode}' unsupported "
+            "(nearest only)")
+    del boundary_mode, max_mip_level
+    try:
+        iinfo = lookup(uv, "interpolate")
+    except RuntimeError:
+        raise RuntimeError("opendressi_amd.torch.texture: `uv` must come from "
+                           "opendressi_amd.torch.interpolate (context discovery)") from None
+    vctx = iinfo.rast_info.extra["ctx"]
+    if uv.dim() == 3:
+        uv = uv.unsqueeze(0)
+    return _TextureFn.apply(tex, uv, vctx, iinfo)
+
+
+# ------------------------------- antialias ---------------------------------
+
+
+class _AntiAliasFn(torch.autograd.Function):
+    @staticmethod
+    def forward(fctx, color, rast, pos, vctx, md, rinfo, n_samples, boost):
+        dev = vctx.device
+        col_d = image_batch(to_dev(color, dev, "color"), "color")
+        rast_d = to_dev(rast, dev, "rast")
+        channels(col_d.shape[3], "color")
+        clip_vk = clip_gl_to_vk(split_batch(to_dev(pos, dev, "pos")))
+        n = col_d.shape[0]
+        with vctx.lock:
+            outs = []
+            for i in range(n):
+                tid = rast_d[i, ..., 3].contiguous()
+                clip = clip_vk[i if clip_vk.shape[0] > 1 else 0].contiguous()
+                outs.append(K.antialias(vctx._ctx, col_d[i].contiguous(), tid, clip, md.faces_f))
+        fctx.dressi = (vctx, md, n_samples, boost)
+        fctx.save_for_backward(color, rast, pos)
+        return torch.stack(outs, 0).to(color.device)
+
+    @staticmethod
+    def backward(fctx, grad_out):
+        vctx, md, n_samples, boost = fctx.dressi
+        color, rast, pos = fctx.saved_tensors
+        need_color, _, need_pos = fctx.needs_input_grad[:3]
+        dev = vctx.device
+        col_d = image_batch(to_dev(color, dev, "color"), "color")
+        rast_d = to_dev(rast, dev, "rast")
+        clip_vk = clip_gl_to_vk(split_batch(to_dev(pos, dev, "pos")))
+        g = image_batch(to_dev(grad_out, dev, "grad_out"), "grad_out")
+        n, h, w, c = col_d.shape
+        key = ("antialias", h, w, md.n_faces, md.n_verts, c, n, n_samples)
+        eng = vctx.engine(key, lambda: _Engine(iter_seed=0))
+        g_col, g_clip = [], []
+        with vctx.lock:
+            # each backward pass advances the stochastic sampler's jitter;
+            # items get distinct seeds so their sample patterns decorrelate
+            eng.iter_seed += 1
+            for i in range(n):
+                tid = rast_d[i, ..., 3].contiguous()
+                clip = clip_vk[i if clip_vk.shape[0] > 1 else 0].contiguous()
+                gi = g[i].contiguous()
+                if need_color:
+                    g_col.append(K.antialias_bwd_img(vctx._ctx, gi, tid, clip, md.faces_f))
+                if need_pos:
+                    seed = _seed(dev, eng.iter_seed * n + i)
+                    if n_samples > 0:
+                        wide = K.antialias_bwd_vtx(vctx._ctx, gi, col_d[i].contiguous(), tid, clip,
+                                                   md.faces_f, md.vft, seed, n_samples, True)
+                        g_clip.append(K.col_sum(vctx._ctx, wide))
+                    else:
+                        g_clip.append(K.antialias_bwd_vtx(vctx._ctx, gi, col_d[i].contiguous(),
+                                                          tid, clip, md.faces_f, md.vft, seed, 0,
+                                                          False))
+        out_gc = out_gp = None
+        if need_color:
+            gc = torch.stack(g_col, 0)
+            out_gc = (gc[0] if color.dim() == 3 else gc).to(color.device)
+        if need_pos:
+            gp = clip_grad_vk_to_gl(torch.stack(g_clip, 0)) * boost
+            out_gp = (gp.sum(dim=0) if pos.dim() == 2 else gp).to(pos.device)
+        return out_gc, None, out_gp, None, None, None, None, None
+
+
+def antialias(color, rast, pos, tri, topology_hash=None, pos_gradient_boost=1.0, n_samples=8):
+    """Drop-in nvdiffrast antialias, screen-space edge AA
+    (python/dressi/torch/ops.py:562-581). Differentiable w.r.t. `color` and
+    `pos`; `n_samples` selects the vertex backward: 0 = exact scan, > 0 =
+    n jittered edge samples per face per backward (wide partials + column
+    sum). `topology_hash` is accepted and ignored."""
+    del topology_hash
+    rinfo: RastInfo = lookup(rast, "rasterize")
+    vctx = rinfo.extra["ctx"]
+    md = vctx.mesh(tri)
+    return _AntiAliasFn.apply(color, rast, pos, vctx, md, rinfo, int(n_samples),
+                              float(pos_gradient_boost))
+
+
+# ------------------------------ rasterize_soft -----------------------------
+
+
+class _RasterizeSoftFn(torch.autograd.Function):
+    @staticmethod
+    def forward(fctx, pos, vctx, md, resolution, radius_px, peels):
+        h, w = resolution
+        dev = vctx.device
+        clip_vk = clip_gl_to_vk(split_batch(to_dev(pos, dev, "pos")))
+        n = clip_vk.shape[0]
+        layers = []
+        with vctx.lock:
+            for i in range(n):
+                clip = clip_vk[i].contiguous()
+                sc = K.soft_clip(vctx._ctx, clip, md.faces_f, w, h, radius_px)
+                prev = None
+                for k in range(peels):
+                    rs = K.rasterize_soft(vctx._ctx, sc, md.corner_face_id, md.faces_seq, clip,
+                                          md.faces_f, w, h, radius_px, prev)
+                    layers.append(rs)
+                    if k + 1 < peels:
+                        prev = _peel_threshold(rs, radius_px)
+        out = torch.stack(layers, 0).reshape(n, peels, h, w, 4)
+        fctx.dressi = (vctx, md, radius_px)
+        fctx.save_for_backward(pos, out)
+        return out.to(pos.device)
+
+    @staticmethod
+    def backward(fctx, grad_out):
+        vctx, md, radius_px = fctx.dressi
+        pos, out = fctx.saved_tensors
+        dev = vctx.device
+        clip_vk = clip_gl_to_vk(split_batch(to_dev(pos, dev, "pos")))
+        g = to_dev(grad_out, dev, "grad_out")
+        n, peels = out.shape[:2]
+        g_clip = []
+        with vctx.lock:
+            for i in range(n):
+                clip = clip_vk[i].contiguous()
+                contribs = []
+                for k in reversed(range(peels)):
+                    wide = K.gather_dist_grad(vctx._ctx, g[i, k].contiguous(), out[i, k], clip,
+                                              md.faces_f, md.vft, radius_px, True)
+                    contribs.append(K.col_sum(vctx._ctx, wide))
+                g_clip.append(sum_contribs(contribs))
+        g_pos = clip_grad_vk_to_gl(torch.stack(g_clip, 0))
+        if pos.dim() == 2:
+            g_pos = g_pos.sum(dim=0)
+        return g_pos.to(pos.device), None, None, None, None, None
+
+
+def _peel_threshold(rs: torch.Tensor, radius_px: float) -> torch.Tensor:
+    """The next peel's depth threshold: this layer's shifted depth rebuilt
+    from its output channels, 0 on background
+    (python/dressi/torch/ops.py:608-615)."""
+    dist, z, cov = rs[..., 0], rs[..., 2], rs[..., 3]
+    ge = (dist >= 0.0).to(torch.float32)
+    near = torch.clamp(z, 0.0, 1.0) * 0.5
+    far = torch.clamp(dist * (-1.0 / radius_px), 0.0, 1.0) * 0.5 + 0.5
+    return (cov * (ge * near + (1.0 - ge) * far)).contiguous()
+
+
+def rasterize_soft(ctx, pos, tri, resolution, radius_px=3.0, peels=1):
+    """HardSoftRas soft rasterization (python/dressi/torch/ops.py:682-698).
+
+    Returns [N, K, H, W, 4] with channels (signed_dist_px, face_id,
+    hard_depth, coverage) per depth-peel layer K. Differentiable w.r.t. `pos`
+    through the signed-distance channel (the exact adjacency-bounded gather
+    backward); compose silhouettes in torch, e.g.
+    `cov * torch.sigmoid(dist / sigma)`."""
+    h, w = check_resolution(resolution)
+    if peels < 1:
+        raise ValueError("peels must be >= 1")
+    md = ctx.mesh(tri)
+    return _RasterizeSoftFn.apply(pos, ctx, md, (h, w), float(radius_px), int(peels))

@@ -1876,6 +1876,103 @@ void or_texture_bilinear(const float* tex, uint32_t tw, uint32_t th, uint32_t n_
     }
 }
 
+/* src/core/f_ops.cpp:2605-2639 (F::Texture forward): GLSL texture() through
+ * the nearest, clamp-to-edge sampler the executor binds
+ * (src/vk/executor.cpp:192-202): texel (clamp(floor(u tw), 0, tw - 1),
+ * clamp(floor(v th), 0, th - 1)). */
+static int nearest_index(float u, uint32_t n) {
+    const float f = floorf(u * (float)n);
+    if (!(f > 0.f)) {
+        return 0;
+    }
+    return f >= (float)(n - 1) ? (int)n - 1 : (int)f;
+}
+
+void or_texture_nearest(const float* tex, uint32_t tw, uint32_t th, uint32_t n_comp,
+                        const float* uv, size_t n_px, float* out) {
+    for (size_t p = 0; p < n_px; p++) {
+        const int ix = nearest_index(uv[p * 2 + 0], tw);
+        const int iy = nearest_index(uv[p * 2 + 1], th);
+        const float* t = tex + ((size_t)iy * tw + (size_t)ix) * n_comp;
+        for (uint32_t c = 0; c < n_comp; c++) {
+            out[p * n_comp + c] = t[c];
+        }
+    }
+}
+
+/* GLSL int(x) of the gather's texel test: truncation toward zero, kept
+ * defined for out-of-range x */
+static int trunc_i32(float x) {
+    if (x != x) {
+        return 0;
+    }
+    if (x >= 2147483520.f) {
+        return 2147483647;
+    }
+    if (x <= -2147483648.f) {
+        return (-2147483647 - 1);
+    }
+    return (int)x;
+}
+
+/* GatherByInverseUV (src/core/f_ops.cpp:2586-2601; its GLSL,
+ * src/codegen/glsl_codegen.cpp:658-703): per texel, the inverse-UV anchor
+ * (its own entry, or the first covered entry of the +-4 dilation in row
+ * order), then the first pixel of the 7 x 7 window around the anchor's
+ * truncated screen position, rows then columns, whose uv truncates to this
+ * texel; the texel takes that pixel's gradient, zero when none matches. */
+void or_gather_inv_uv(const float* gy, uint32_t n_comp, uint32_t sw, uint32_t sh,
+                      const float* inv_uv, uint32_t tw, uint32_t th, const float* uv,
+                      float* out) {
+    memset(out, 0, sizeof(float) * (size_t)tw * th * n_comp);
+    for (int ty = 0; ty < (int)th; ty++) {
+        for (int tx = 0; tx < (int)tw; tx++) {
+            const float* iv0 = &inv_uv[((size_t)ty * tw + tx) * 4];
+            float iv[4] = {iv0[0], iv0[1], iv0[2], iv0[3]};
+            for (int ny = -4; ny <= 4 && iv[2] < 0.5f; ny++) {
+                for (int nx = -4; nx <= 4; nx++) {
+                    const int px = tx + nx, py = ty + ny;
+                    if (px < 0 || py < 0 || px >= (int)tw || py >= (int)th) {
+                        continue;
+                    }
+                    const float* q = &inv_uv[((size_t)py * tw + px) * 4];
+                    iv[0] = q[0];
+                    iv[1] = q[1];
+                    iv[2] = q[2];
+                    iv[3] = q[3];
+                    if (iv[2] > 0.5f) {
+                        break;
+                    }
+                }
+            }
+            if (!(iv[2] > 0.5f)) {
+                continue;
+            }
+            const int scx = trunc_i32(iv[0]), scy = trunc_i32(iv[1]);
+            float* o = &out[((size_t)ty * tw + tx) * n_comp];
+            int found = 0;
+            for (int dy = -3; dy <= 3 && !found; dy++) {
+                for (int dx = -3; dx <= 3; dx++) {
+                    const long spx = (long)scx + dx, spy = (long)scy + dy;
+                    if (spx < 0 || spy < 0 || spx >= (long)sw || spy >= (long)sh) {
+                        continue;
+                    }
+                    const float* suv = &uv[((size_t)spy * sw + (size_t)spx) * 2];
+                    if (trunc_i32(suv[0] * (float)tw) == tx &&
+                        trunc_i32(suv[1] * (float)th) == ty) {
+                        const float* g = &gy[((size_t)spy * sw + (size_t)spx) * n_comp];
+                        for (uint32_t c = 0; c < n_comp; c++) {
+                            o[c] = g[c];
+                        }
+                        found = 1;
+                        break;
+                    }
+                }
+            }
+        }
+    }
+}
+
 /* src/core/f_ops.cpp:2665-2731 (GatherByInverseUVBilinear CPU kernel): per
  * texel, the inverse-UV anchor (its own entry, or the first covered entry of
  * the +-4 dilation in row order), then the tent-weighted gradient of the

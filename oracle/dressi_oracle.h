@@ -154,6 +154,13 @@ void or_screen_attr(const float* clip, uint32_t n_verts, uint32_t w, uint32_t h,
 /* src/core/f_ops.cpp:2764-2778 (TextureBilinear), ibl_math.h:91-115 */
 void or_texture_bilinear(const float* tex, uint32_t tw, uint32_t th, uint32_t n_comp,
                          const float* uv, size_t n_px, float* out);
+/* src/core/f_ops.cpp:2605-2639 (F::Texture, nearest clamp-to-edge) */
+void or_texture_nearest(const float* tex, uint32_t tw, uint32_t th, uint32_t n_comp,
+                        const float* uv, size_t n_px, float* out);
+/* src/core/f_ops.cpp:2586-2601 (GatherByInverseUV), glsl_codegen.cpp:658-703 */
+void or_gather_inv_uv(const float* gy, uint32_t n_comp, uint32_t sw, uint32_t sh,
+                      const float* inv_uv, uint32_t tw, uint32_t th, const float* uv,
+                      float* out);
 /* src/core/f_ops.cpp:2665-2731 (GatherByInverseUVBilinear) */
 void or_gather_inv_uv_bilinear(const float* gy, uint32_t n_comp, uint32_t sw, uint32_t sh,
                                const float* inv_uv, uint32_t tw, uint32_t th, const float* uv,

@@ -430,6 +430,27 @@ class Oracle(_Lib):
                                     C.c_size_t(n_px), _fp(out))
         return out
 
+    def texture_nearest(self, tex, uv):
+        """tex {th, tw, nc}, uv {..., 2} -> {..., nc} (nearest, clamp to edge)."""
+        tex, uv = _f32(tex), _f32(uv)
+        th, tw, nc = tex.shape
+        n_px = uv.size // 2
+        out = np.zeros(uv.shape[:-1] + (nc,), np.float32)
+        self.fn("texture_nearest")(_fp(tex), _U32(tw), _U32(th), _U32(nc), _fp(uv),
+                                   C.c_size_t(n_px), _fp(out))
+        return out
+
+    def gather_inv_uv(self, gy, inv_uv, uv):
+        """GatherByInverseUV: gy {sh, sw, nc}, inv_uv {th, tw, 4}, uv {sh, sw, 2}
+        -> {th, tw, nc}."""
+        gy, inv_uv, uv = _f32(gy), _f32(inv_uv), _f32(uv)
+        sh, sw, nc = gy.shape
+        th, tw = inv_uv.shape[:2]
+        out = np.zeros((th, tw, nc), np.float32)
+        self.fn("gather_inv_uv")(_fp(gy), _U32(nc), _U32(sw), _U32(sh), _fp(inv_uv), _U32(tw),
+                                 _U32(th), _fp(uv), _fp(out))
+        return out
+
     def uv_as_clip(self, uv):
         uv = _f32(uv)
         out = np.zeros((uv.shape[0], 4), np.float32)

@@ -76,6 +76,28 @@ def test_texture_ops_match_oracle(ctx, oracle, seed):
            "screen attr")
 
 
+@pytest.mark.parametrize("seed", [0, 1])
+def test_texture_nearest_ops_match_oracle(ctx, oracle, seed):
+    """F::Texture (nearest, clamp to edge) and GatherByInverseUV, bit-exact,
+    on random uv (some outside [0, 1]) and a half-empty inverse-UV table."""
+    from opendressi_amd import ops
+    print(f"[tex nearest ops] random seed={seed}", flush=True)
+    rng = np.random.default_rng(100 + seed)
+    for nc in (1, 3, 4):
+        tex = rng.random((37, 53, nc)).astype(np.float32)
+        uv = (rng.random((61, 47, 2)) * 1.2 - 0.1).astype(np.float32)
+        _exact(host(ops.texture_nearest(ctx, dev(tex), dev(uv))),
+               oracle.texture_nearest(tex, uv), f"nearest nc={nc}")
+        gy = rng.standard_normal((61, 47, nc)).astype(np.float32)
+        iv = np.zeros((37, 53, 4), np.float32)
+        iv[..., 0] = rng.random((37, 53)) * 51 - 2
+        iv[..., 1] = rng.random((37, 53)) * 65 - 2
+        iv[..., 2] = (rng.random((37, 53)) < 0.5).astype(np.float32)
+        uv2 = rng.random((61, 47, 2)).astype(np.float32)
+        _exact(host(ops.texture_nearest_bwd(ctx, dev(gy), dev(iv), dev(uv2))),
+               oracle.gather_inv_uv(gy, iv, uv2), f"gather nearest nc={nc}")
+
+
 def _fit(ctx, g, images=True):
     import opendressi_amd as od
     return od.TextureFit(ctx, g["in_pos"], g["in_uv"], g["in_faces"], g["in_mvps"],

@@ -135,3 +135,72 @@ def test_screen_attr_closed_form(oracle):
     clip = np.array([[0.5, -0.25, 0.3, 2.0], [-1.0, 1.0, 0.0, 1.0]], np.float32)
     a = oracle.screen_attr(clip, 64, 32)
     assert np.array_equal(a, np.array([[40.0, 14.0, 1, 0], [0.0, 32.0, 1, 0]], np.float32))
+
+
+def test_texture_nearest_closed_forms(oracle):
+    """Nearest, clamp-to-edge: pixel (x, y) of an identity uv grid reads
+    texel (x, y); uv outside [0, 1) clamps to the edge texels; u = k / tw
+    exactly reads texel k."""
+    tex = np.arange(6 * 5 * 2, dtype=np.float32).reshape(5, 6, 2)
+    ys, xs = np.mgrid[0:5, 0:6]
+    uv = np.stack([(xs + 0.5) / 6, (ys + 0.5) / 5], -1).astype(np.float32)
+    assert np.array_equal(oracle.texture_nearest(tex, uv), tex)
+    uv = np.array([[-0.1, -3.0], [1.0, 1.0], [1.5, 0.2], [2 / 6, 3 / 5], [0.0, 0.999]],
+                  np.float32)
+    want = np.stack([tex[0, 0], tex[4, 5], tex[1, 5], tex[3, 2], tex[4, 0]])
+    assert np.array_equal(oracle.texture_nearest(tex, uv), want)
+
+
+def _identity_scene(n=8):
+    ys, xs = np.mgrid[0:n, 0:n]
+    uv = np.stack([(xs + 0.5) / n, (ys + 0.5) / n], -1).astype(np.float32)
+    iv = np.zeros((n, n, 4), np.float32)
+    iv[..., 0], iv[..., 1], iv[..., 2] = xs + 0.5, ys + 0.5, 1.0
+    return uv, iv
+
+
+def test_gather_inv_uv_is_the_adjoint_on_a_one_to_one_map(oracle):
+    """Screen pixel p samples exactly texel p: the gather is the exact
+    transpose of the sampling, so <T(t), g> == <t, G(g)> and G(g) == g."""
+    uv, iv = _identity_scene()
+    rng = np.random.default_rng(3)
+    for _ in range(3):
+        t = rng.standard_normal((8, 8, 3)).astype(np.float32)
+        gy = rng.standard_normal((8, 8, 3)).astype(np.float32)
+        g = oracle.gather_inv_uv(gy, iv, uv)
+        assert np.array_equal(g, gy)
+        lhs = float((oracle.texture_nearest(t, uv).astype(np.float64) * gy).sum())
+        rhs = float((t.astype(np.float64) * g).sum())
+        assert abs(lhs - rhs) <= 1e-9 * (abs(lhs) + 1.0)
+
+
+def test_gather_inv_uv_many_to_one_takes_the_first_sampling_pixel(oracle):
+    """16x16 screen over a 4x4 texture (each texel sampled by a 4x4 pixel
+    block), anchors at the block centres: the 7x7 window's first sampling
+    pixel in row order is the block's top-left pixel; a texel whose table
+    entry is empty borrows the first covered entry of its +-4 neighbourhood in
+    row order (dilation): found for texel (1, 0), whose borrowed window still
+    reaches its block, zero for texel (2, 1), whose does not; a texel no pixel
+    samples gets zero."""
+    n, t = 16, 4
+    ys, xs = np.mgrid[0:n, 0:n]
+    uv = np.stack([(xs + 0.5) / n, (ys + 0.5) / n], -1).astype(np.float32)
+    tys, txs = np.mgrid[0:t, 0:t]
+    iv = np.zeros((t, t, 4), np.float32)
+    iv[..., 0], iv[..., 1], iv[..., 2] = txs * 4 + 2, tys * 4 + 2, 1.0
+    gy = np.random.default_rng(5).standard_normal((n, n, 2)).astype(np.float32)
+    g = oracle.gather_inv_uv(gy, iv, uv)
+    assert np.array_equal(g, gy[0::4, 0::4])
+    iv2 = iv.copy()
+    iv2[0, 1, 2] = 0.0  # texel (1, 0) borrows texel (0, 0)'s anchor (2, 2)
+    iv2[1, 2, 2] = 0.0  # texel (2, 1) borrows texel (0, 0)'s anchor too
+    g2 = oracle.gather_inv_uv(gy, iv2, uv)
+    assert np.array_equal(g2[0, 1], gy[0, 4])
+    assert (g2[1, 2] == 0).all()
+    keep = np.ones((t, t), bool)
+    keep[0, 1] = keep[1, 2] = False
+    assert np.array_equal(g2[keep], g[keep])
+    uv3 = uv.copy()
+    uv3[0:4, 0:4] = uv3[0:4, 4:8]  # nobody samples texel (0, 0) any more
+    g3 = oracle.gather_inv_uv(gy, iv, uv3)
+    assert (g3[0, 0] == 0).all() and np.array_equal(g3[1:, 1:], g[1:, 1:])
