@@ -1,12 +1,13 @@
-// graph_c1.cpp -- the HardSoftRas silhouette fit written with the graph API
+// graph_c1.cpp -- the silhouette fit written with the graph API
 // (include/dressi_graph.h) and run by its generic executor: the graph of
-// examples/silhouette_optimization/run.cpp:229-437 (technique hardsoftras,
-// one peel, no regularisers), built with the same C++ expressions so that
-// node creation order -- hence the backward's summation order -- is the
-// reference build's.
+// examples/silhouette_optimization/run.cpp:229-437 (technique hardsoftras
+// with one peel, or aa; no regularisers), built with the same C++
+// expressions so that node creation order -- hence the backward's
+// summation order -- is the reference build's.
 //
 //   graph_c1 <in.bin> <out.bin>
-// in.bin: u32 V, F, Vt, Ft, N, S, samples, iters; f32 radius, lr;
+// in.bin: u32 V, F, Vt, Ft, N, S, samples, iters, technique (0 hsr, 1 aa);
+//         f32 radius, lr;
 //         pos0 {V,3}, faces {F,3}, tgt_pos {Vt,3}, tgt_faces {Ft,3}, mvps N x 16
 // out.bin: pos, m, v {V,3}, t, loss[iters] (sum of the loss image), grad0 {V,3}
 #include <cstdio>
@@ -71,12 +72,13 @@ int main(int argc, char** argv) {
         if (!fi) {
             throw DressiError("cannot open input");
         }
-        uint32_t hdr[8];
+        uint32_t hdr[9];
         float fp[2];
-        get(fi, hdr, 8);
+        get(fi, hdr, 9);
         get(fi, fp, 2);
         const uint32_t n_verts = hdr[0], n_faces = hdr[1], n_tverts = hdr[2], n_tfaces = hdr[3];
         const uint32_t n_views = hdr[4], S = hdr[5], samples = hdr[6], iters = hdr[7];
+        const bool aa = hdr[8] == 1;
         const float radius_px = fp[0], lr = fp[1];
         std::vector<float> pos0(n_verts * 3), faces(n_faces * 3), tgt_pos(n_tverts * 3),
                 tgt_faces(n_tfaces * 3), mvps(n_views * 16);
@@ -163,13 +165,39 @@ int main(int argc, char** argv) {
             return F::Max(hard, soft_sil);
         };
 
+        // technique aa (run.cpp:320-357): the prediction and the target are
+        // AntiAlias'd hard masks
+        uint32_t tdeg = 0;
+        const std::vector<float> tvf = VertexFaces(tgt_faces, n_tverts, &tdeg);
+        Variable b_faces_f(VEC3, {n_tfaces, 1});
+        Variable b_vtx_faces(FLOAT, {n_tverts, tdeg});
+        Variable s_ones(FLOAT, {n_verts, 1});
+        Variable s_faces_i(IVEC3, {n_faces, 1});
+        Variable zero_seed(FLOAT, {1, 1});
+        const auto build_pred_aa = [&](const Variable& clip_v) -> Variable {
+            Variable mask = F::Rasterize(clip_v, s_ones, s_faces_i, screen);
+            Variable tri = F::RasterizeFaceId(clip_v, s_ones, s_faces_i, screen);
+            return F::AntiAlias(mask, tri, clip_v, s_faces_f, s_vtx_faces, adam_t, samples);
+        };
+        const auto build_target_aa = [&](const Variable& tgt_clip) -> Variable {
+            Variable t_mask = F::Rasterize(tgt_clip, b_ones, b_faces_i, screen);
+            Variable t_tri = F::RasterizeFaceId(tgt_clip, b_ones, b_faces_i, screen);
+            return F::StopGradient(
+                    F::AntiAlias(t_mask, t_tri, tgt_clip, b_faces_f, b_vtx_faces, zero_seed, 0));
+        };
+
         Variables targets, preds, view_losses;
         std::vector<Variable> tgt_clips;
         for (uint32_t v = 0; v < n_views; v++) {
             tgt_clips.emplace_back(VEC4, ImgSize{n_tverts, 1});
-            targets.push_back(
-                    F::StopGradient(F::Rasterize(tgt_clips.back(), b_ones, b_faces_i, screen)));
-            preds.push_back(build_pred(ClipOf(pos, mvps.data() + 16 * v)));
+            if (aa) {
+                targets.push_back(build_target_aa(tgt_clips.back()));
+                preds.push_back(build_pred_aa(ClipOf(pos, mvps.data() + 16 * v)));
+            } else {
+                targets.push_back(F::StopGradient(
+                        F::Rasterize(tgt_clips.back(), b_ones, b_faces_i, screen)));
+                preds.push_back(build_pred(ClipOf(pos, mvps.data() + 16 * v)));
+            }
             Variable diff = targets[v] - preds[v];
             view_losses.push_back(diff * diff * (1.f / float(screen.w * screen.h)));
         }
@@ -215,6 +243,14 @@ int main(int argc, char** argv) {
         ad.sendImg(s_vtx_faces, vf.data());
         ad.sendImg(s_face_id, fid.data());
         ad.sendImg(s_faces_soft, fsoft.data());
+        if (aa) {
+            std::vector<float> s_ones_v(n_verts, 1.f), zero_v(1, 0.f);
+            ad.sendImg(b_faces_f, tgt_faces.data());
+            ad.sendImg(b_vtx_faces, tvf.data());
+            ad.sendImg(s_ones, s_ones_v.data());
+            ad.sendImg(s_faces_i, faces.data());
+            ad.sendImg(zero_seed, zero_v.data());
+        }
         for (uint32_t v = 0; v < n_views; v++) {
             const float* m = mvps.data() + 16 * v;
             std::vector<float> c(size_t(n_tverts) * 4);

@@ -23,9 +23,10 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 EXE = os.path.join(ROOT, "tests", "_bin", "graph_c1")
 
 
-def _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, radius, lr):
+def _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, radius, lr, aa=False):
     nv, nf = len(pos), len(faces)
-    hdr = np.array([nv, nf, len(tgt), nf, len(mvps), screen, samples, iters], np.uint32)
+    hdr = np.array([nv, nf, len(tgt), nf, len(mvps), screen, samples, iters, 1 if aa else 0],
+                   np.uint32)
     inp = tmp_path / "in.bin"
     out = tmp_path / "out.bin"
     with open(inp, "wb") as f:
@@ -95,3 +96,26 @@ def test_graph_executor_matches_fused_plan(tmp_path):
     assert np.array_equal(g["grad0"], fit.read(_lib.BUF_GRAD)), "gradient differs"
     assert g["loss"][0] == np.float32(fit.loss()), (g["loss"][0], fit.loss())
     np.testing.assert_allclose(g["pos"], fit.read(_lib.BUF_POS), rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("samples", [8, 0])
+def test_graph_executor_aa_fit_matches_oracle(tmp_path, oracle, samples):
+    """Technique aa (AntiAlias'd hard masks; stochastic wide vertex backward
+    + ColSum, or the exact one) through the generic executor."""
+    import opendressi_amd as od
+    print(f"[graph] aa, c1 mesh, 2 views, 96px, samples={samples}, 3 iterations", flush=True)
+    w = od.WORKLOADS["c1"]
+    pos, faces, tgt, _ = od.make_scene(w)
+    mvps = np.ascontiguousarray(np.asarray(od.camera_mvps(2), np.float32))
+    iters, lr = 3, 1e-3
+    g = _run_graph(tmp_path, pos, faces, tgt, mvps, 96, samples, iters, 3.0, lr, aa=True)
+    want = oracle.aa_fit(pos, faces, tgt, faces, mvps, 96, samples=samples, lr=lr, iters=iters,
+                         want_images=False)
+    assert np.array_equal(g["grad0"], want["grad0"]), \
+        f"grad0 differs: max {np.abs(g['grad0'] - want['grad0']).max():.3g}"
+    assert g["loss"][0] == want["loss"][0], (g["loss"], want["loss"])
+    assert np.abs(want["grad0"]).max() > 0
+    np.testing.assert_allclose(g["loss"], want["loss"], rtol=1e-6, atol=0)
+    for k in ("pos", "m", "v"):
+        np.testing.assert_allclose(g[k], want[k], rtol=0, atol=1e-6 * max(1.0, np.abs(want[k]).max()),
+                                   err_msg=k)
