@@ -267,6 +267,63 @@ def cpu_baseline(workload) -> dict:
                        f"host CPU: {cpu_info()}, nproc {os.cpu_count()}")}
 
 
+def bench_record(workload: str, path: str, warmup: int) -> None:
+    """The reference example's bench.json record (examples/common/bench.cpp:
+    165-209, fields of examples/silhouette_optimization/run.cpp:686-703) for
+    a silhouette workload: the fit run from its start for the workload's
+    iteration count, each execStep timed with a host synchronisation (the
+    reference's median steady-state wall time), warm-up iterations excluded;
+    loss drop = first / last loss; mean IoU of the final prediction and the
+    target masks (> 0.5) over the views."""
+    import platform
+    import time
+
+    import numpy as np
+
+    import opendressi_amd as od
+    from opendressi_amd import _lib
+    w = od.WORKLOADS[workload]
+    ctx = od.Context(0)
+    t0 = time.perf_counter()
+    fit = od.SilhouetteFit.from_workload(ctx, workload, keep_pred=True)
+    fit.step(1, graph=False)
+    fit.synchronize()
+    first_build_ms = (time.perf_counter() - t0) * 1e3
+    first_loss = fit.loss()
+    warm, samples = [], []
+    for i in range(1, w.iters):
+        t = time.perf_counter()
+        fit.step(1)
+        fit.synchronize()
+        (warm if i <= warmup else samples).append((time.perf_counter() - t) * 1e3)
+    last_loss = fit.loss()
+    median = float(np.median(samples)) if samples else float("nan")
+    warm_ms = max(0.0, sum(warm) - median * len(warm))
+    pred, tgt = fit.read(_lib.BUF_PRED) > 0.5, fit.read(_lib.BUF_TARGET) > 0.5
+    ious = [float((p & t).sum()) / max(float((p | t).sum()), 1.0) for p, t in zip(pred, tgt)]
+    try:
+        ram_gb = os.sysconf("SC_PAGE_SIZE") * os.sysconf("SC_PHYS_PAGES") / 2**30
+    except (ValueError, OSError):
+        ram_gb = 0.0
+    fields = [
+        ("example", "silhouette_optimization"), ("device", ctx.device_name),
+        ("platform", "linux"), ("os", f"{platform.system()} {platform.release()}"),
+        ("cpu", cpu_info()), ("cpu_cores", os.cpu_count() or 0), ("ram_gb", round(ram_gb, 1)),
+        ("funcs", 5), ("substages", 5), ("stages", 5),
+        ("technique", "hardsoftras" if w.technique == "hsr" else "aa"), ("screen", w.screen),
+        ("views", w.views), ("iters", w.iters), ("samples", 8), ("peels", 1),
+        ("single_view", w.views == 1), ("median_ms_per_iter", round(median, 4)),
+        ("warmup_excluded", warmup), ("warmup_ms", round(warm_ms, 1)),
+        ("first_build_ms", round(first_build_ms, 1)),
+        ("mean_iou", round(float(np.mean(ious)), 4)),
+        ("loss_drop", round(first_loss / max(last_loss, 1e-12), 1)),
+    ]
+    with open(path, "w") as fh:
+        fh.write(json.dumps(dict(fields), separators=(",", ":")) + "\n")
+    fit.close()
+    ctx.close()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -278,6 +335,9 @@ def main() -> int:
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="after the JSON line, run a plain device copy of this many MiB "
                          "(the reference kernel for scaling rocprofv3 FETCH/WRITE_SIZE)")
+    ap.add_argument("--bench-json", default=None,
+                    help="after the JSON line, run the silhouette workload's whole fit and write "
+                         "the reference example's bench.json record to this path")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the multi-GPU path "
@@ -373,6 +433,12 @@ def main() -> int:
                                 cpu_baseline_tex(w) if tex else cpu_baseline(w))
     print(json.dumps(line), flush=True)
     ctx.close()
+    if args.bench_json:
+        if tex or pbr:
+            print("--bench-json: the record covers the silhouette workloads", file=sys.stderr)
+        else:
+            bench_record(args.workload, args.bench_json, min(20, max(1, od.WORKLOADS[
+                args.workload].iters // 5)))
     if args.copy_mb > 0:
         import torch
         n = args.copy_mb * (1 << 20) // 4
