@@ -53,7 +53,7 @@ typedef struct dressi_ctx dressi_ctx;
 
 /* Creates a context on `device` with its own default-priority stream.
  * Replaces DressiAD::createContext / CreateVkContext
- * (include/dressi/dressi_ad.h:336-338, src/vk/context.h:11-40). */
+ * (include/dressi/dressi_ad.h:53-55, src/vk/context.h:11-40). */
 int dressi_ctx_create(int device, dressi_ctx** out);
 int dressi_ctx_destroy(dressi_ctx* ctx);
 /* Use a caller-owned stream (e.g. the current torch stream) instead of the
@@ -66,7 +66,7 @@ void* dressi_ctx_stream(dressi_ctx* ctx);
 /* Waits for all work queued on the context stream (the reference's fence
  * wait, src/vk/executor.cpp:1020-1027). */
 int dressi_ctx_synchronize(dressi_ctx* ctx);
-/* Device name (DressiAD::getDeviceName, include/dressi/dressi_ad.h:380-382). */
+/* Device name (DressiAD::getDeviceName, include/dressi/dressi_ad.h:94-96). */
 int dressi_ctx_device_name(dressi_ctx* ctx, char* buf, size_t len);
 
 int dressi_malloc(dressi_ctx* ctx, void** ptr, size_t bytes);
@@ -439,7 +439,7 @@ typedef struct dressi_hsr_desc {
 /* Also write per-view pred images each iteration (markOutput(pred)). */
 #define DRESSI_HSR_KEEP_PRED 1u
 /* Keep d loss / d pos of the last iteration readable (setGradOutputsEnabled,
- * include/dressi/dressi_ad.h:362-370). */
+ * include/dressi/dressi_ad.h:78-87). */
 #define DRESSI_HSR_KEEP_GRAD 2u
 /* Technique "aa" of the example (run.cpp:231-238, 352-356) instead of
  * HardSoftRas: pred = AntiAlias(Rasterize(clip, 1), RasterizeFaceId(clip),

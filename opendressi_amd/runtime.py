@@ -1,7 +1,7 @@
 """Device context and host-side scene builders over the C ABI.
 
 `Context` mirrors the reference's shared Vulkan context
-(DressiAD::createContext, include/dressi/dressi_ad.h:336-338): one HIP device +
+(DressiAD::createContext, include/dressi/dressi_ad.h:53-55): one HIP device +
 one stream; every op and plan created from it is stream-ordered on it.
 """
 from __future__ import annotations

@@ -1,5 +1,6 @@
-"""Tensor-shape and clip-space conventions of the surface
-(python/dressi/torch/convert.py:74-125), on device tensors."""
+"""Tensor-shape and clip-space conventions of the surface on device
+tensors (the reference surface's conventions: python/dressi/torch/
+convert.py:74-125)."""
 from __future__ import annotations
 
 import torch
@@ -30,29 +31,39 @@ def clip_grad_vk_to_gl(g_vk: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def check_resolution(resolution) -> tuple[int, int]:
-    h, w = int(resolution[0]), int(resolution[1])
-    if h <= 0 or w <= 0:
-        raise ValueError(f"resolution must be positive [H, W], got {resolution}")
-    return h, w
+def resolution_hw(resolution) -> tuple[int, int]:
+    """(H, W) from an nvdiffrast `resolution` argument, which must name
+    exactly two positive sizes."""
+    try:
+        dims = [int(x) for x in resolution]
+    except (TypeError, ValueError):
+        dims = []
+    if len(dims) != 2 or min(dims) < 1:
+        raise ValueError(f"opendressi_amd.torch: resolution must be two positive sizes "
+                         f"[H, W]; got {resolution!r}")
+    return dims[0], dims[1]
 
 
-def split_batch(pos: torch.Tensor, name: str = "pos") -> torch.Tensor:
-    """Accept [V, C] or [N, V, C]; return [N, V, C]."""
-    if pos.dim() == 2:
-        return pos.unsqueeze(0)
-    if pos.dim() == 3:
-        return pos
-    raise ValueError(f"{name} must be [V, C] or [N, V, C], got {tuple(pos.shape)}")
+def batched(t: torch.Tensor, item_rank: int, name: str, layout: str) -> torch.Tensor:
+    """`t` with a leading batch axis. An item has `item_rank` dimensions
+    (`layout` names them, e.g. "V, C"); a single item becomes a batch of
+    one, a batch passes through unchanged."""
+    if t.dim() == item_rank + 1:
+        return t
+    if t.dim() == item_rank:
+        return t.unsqueeze(0)
+    raise ValueError(f"opendressi_amd.torch: {name} has shape {tuple(t.shape)}; expected "
+                     f"[{layout}] or [N, {layout}]")
+
+
+def vertex_batch(t: torch.Tensor, name: str = "pos") -> torch.Tensor:
+    """[N, V, C] from [V, C] or [N, V, C]."""
+    return batched(t, 2, name, "V, C")
 
 
 def image_batch(t: torch.Tensor, name: str) -> torch.Tensor:
-    """Accept [H, W, C] or [N, H, W, C]; return [N, H, W, C]."""
-    if t.dim() == 3:
-        return t.unsqueeze(0)
-    if t.dim() == 4:
-        return t
-    raise ValueError(f"{name} must be [H, W, C] or [N, H, W, C], got {tuple(t.shape)}")
+    """[N, H, W, C] from [H, W, C] or [N, H, W, C]."""
+    return batched(t, 3, name, "H, W, C")
 
 
 def channels(c: int, what: str) -> int:

@@ -19,15 +19,15 @@ from .. import ops as K
 from .context import RasterizeHipContext
 from .convert import (
     channels,
-    check_resolution,
     clip_grad_vk_to_gl,
     clip_gl_to_vk,
     image_batch,
-    split_batch,
+    resolution_hw,
     sum_contribs,
     to_dev,
+    vertex_batch,
 )
-from .provenance import InterpInfo, RastInfo, attach, lookup
+from .provenance import InterpOrigin, RasterOrigin, origin, stamp
 
 
 def _needs_grad(*tensors) -> bool:
@@ -64,8 +64,8 @@ def rasterize(ctx: RasterizeHipContext, pos: torch.Tensor, tri: torch.Tensor, re
     if ranges is not None:
         raise NotImplementedError("opendressi_amd.torch: range mode is not supported")
     del grad_db
-    h, w = check_resolution(resolution)
-    pos_b = split_batch(to_dev(pos, ctx.device, "pos"))
+    h, w = resolution_hw(resolution)
+    pos_b = vertex_batch(to_dev(pos, ctx.device, "pos"))
     if pos_b.shape[2] != 4:
         raise ValueError(f"pos must have 4 components, got {pos_b.shape[2]}")
     md = ctx.mesh(tri)
@@ -88,7 +88,7 @@ def rasterize(ctx: RasterizeHipContext, pos: torch.Tensor, tri: torch.Tensor, re
             zw = g[..., 2] / (g[..., 3] + (1.0 - mask))
             outs.append(torch.stack([g[..., 0], g[..., 1], zw, tid], dim=-1))
     rast = torch.stack(outs, 0).to(pos.device)
-    attach(rast, RastInfo(clip_vk=clip_vk, tri=tri, resolution=(h, w), extra={"ctx": ctx}))
+    stamp(rast, RasterOrigin(clip_vk=clip_vk, tri=tri, resolution=(h, w), ctx=ctx))
     return rast, torch.zeros_like(rast)
 
 
@@ -160,11 +160,11 @@ def interpolate(attr, rast, tri, rast_db=None, diff_attrs=None):
     if rast_db is not None or diff_attrs is not None:
         raise NotImplementedError(
             "opendressi_amd.torch.interpolate: rast_db/diff_attrs are not supported")
-    rinfo: RastInfo = lookup(rast, "rasterize")
-    vctx = rinfo.extra["ctx"]
+    rinfo = origin(rast, RasterOrigin, "rasterize")
+    vctx = rinfo.ctx
     md = vctx.mesh(tri)
     out = _InterpolateFn.apply(attr, rast, vctx, md, rinfo)
-    attach(out, InterpInfo(attr=attr, rast_info=rinfo))
+    stamp(out, InterpOrigin(attr=attr, raster=rinfo))
     return out, None
 
 
@@ -201,7 +201,7 @@ class _TextureFn(torch.autograd.Function):
         th, tw = (tex.shape[1], tex.shape[2]) if tex.dim() == 4 else (tex.shape[0], tex.shape[1])
         uv_d = to_dev(uv, dev, "uv")
         g = to_dev(grad_out, dev, "grad_out")
-        rinfo = iinfo.rast_info
+        rinfo = iinfo.raster
         h, w = rinfo.resolution
         md = vctx.mesh(rinfo.tri)
         vtx_uv = to_dev(iinfo.attr, dev, "uv attr")
@@ -239,12 +239,8 @@ def texture(tex, uv, uv_da=None, mip_level_bias=None, mip=None, filter_mode="aut
             f"opendressi_amd.torch.texture: filter_mode='{filter_mode}' unsupported "
             "(nearest only)")
     del boundary_mode, max_mip_level
-    try:
-        iinfo = lookup(uv, "interpolate")
-    except RuntimeError:
-        raise RuntimeError("opendressi_amd.torch.texture: `uv` must come from "
-                           "opendressi_amd.torch.interpolate (context discovery)") from None
-    vctx = iinfo.rast_info.extra["ctx"]
+    iinfo = origin(uv, InterpOrigin, "interpolate")
+    vctx = iinfo.raster.ctx
     if uv.dim() == 3:
         uv = uv.unsqueeze(0)
     return _TextureFn.apply(tex, uv, vctx, iinfo)
@@ -260,7 +256,7 @@ class _AntiAliasFn(torch.autograd.Function):
         col_d = image_batch(to_dev(color, dev, "color"), "color")
         rast_d = to_dev(rast, dev, "rast")
         channels(col_d.shape[3], "color")
-        clip_vk = clip_gl_to_vk(split_batch(to_dev(pos, dev, "pos")))
+        clip_vk = clip_gl_to_vk(vertex_batch(to_dev(pos, dev, "pos")))
         n = col_d.shape[0]
         with vctx.lock:
             outs = []
@@ -280,7 +276,7 @@ class _AntiAliasFn(torch.autograd.Function):
         dev = vctx.device
         col_d = image_batch(to_dev(color, dev, "color"), "color")
         rast_d = to_dev(rast, dev, "rast")
-        clip_vk = clip_gl_to_vk(split_batch(to_dev(pos, dev, "pos")))
+        clip_vk = clip_gl_to_vk(vertex_batch(to_dev(pos, dev, "pos")))
         g = image_batch(to_dev(grad_out, dev, "grad_out"), "grad_out")
         n, h, w, c = col_d.shape
         key = ("antialias", h, w, md.n_faces, md.n_verts, c, n, n_samples)
@@ -323,8 +319,8 @@ def antialias(color, rast, pos, tri, topology_hash=None, pos_gradient_boost=1.0,
     n jittered edge samples per face per backward (wide partials + column
     sum). `topology_hash` is accepted and ignored."""
     del topology_hash
-    rinfo: RastInfo = lookup(rast, "rasterize")
-    vctx = rinfo.extra["ctx"]
+    rinfo = origin(rast, RasterOrigin, "rasterize")
+    vctx = rinfo.ctx
     md = vctx.mesh(tri)
     return _AntiAliasFn.apply(color, rast, pos, vctx, md, rinfo, int(n_samples),
                               float(pos_gradient_boost))
@@ -338,7 +334,7 @@ class _RasterizeSoftFn(torch.autograd.Function):
     def forward(fctx, pos, vctx, md, resolution, radius_px, peels):
         h, w = resolution
         dev = vctx.device
-        clip_vk = clip_gl_to_vk(split_batch(to_dev(pos, dev, "pos")))
+        clip_vk = clip_gl_to_vk(vertex_batch(to_dev(pos, dev, "pos")))
         n = clip_vk.shape[0]
         layers = []
         with vctx.lock:
@@ -362,7 +358,7 @@ class _RasterizeSoftFn(torch.autograd.Function):
         vctx, md, radius_px = fctx.dressi
         pos, out = fctx.saved_tensors
         dev = vctx.device
-        clip_vk = clip_gl_to_vk(split_batch(to_dev(pos, dev, "pos")))
+        clip_vk = clip_gl_to_vk(vertex_batch(to_dev(pos, dev, "pos")))
         g = to_dev(grad_out, dev, "grad_out")
         n, peels = out.shape[:2]
         g_clip = []
@@ -400,7 +396,7 @@ def rasterize_soft(ctx, pos, tri, resolution, radius_px=3.0, peels=1):
     through the signed-distance channel (the exact adjacency-bounded gather
     backward); compose silhouettes in torch, e.g.
     `cov * torch.sigmoid(dist / sigma)`."""
-    h, w = check_resolution(resolution)
+    h, w = resolution_hw(resolution)
     if peels < 1:
         raise ValueError("peels must be >= 1")
     md = ctx.mesh(tri)

@@ -1,6 +1,7 @@
 """Host-side logic of opendressi_amd.torch (no GPU): clip-space conventions,
 the gradient-sum order, provenance lifetime, argument checks."""
 import gc
+import weakref
 
 import numpy as np
 import pytest
@@ -39,24 +40,30 @@ def test_sum_contribs_groups_of_four_left_to_right():
 
 def test_provenance_lives_with_the_tensor():
     t = torch.zeros(3)
-    info = provenance.RastInfo(clip_vk=None, tri=None, resolution=(1, 1))
-    provenance.attach(t, info)
-    assert provenance.lookup(t, "rasterize") is info
+    rec = provenance.RasterOrigin(clip_vk=None, tri=None, resolution=(1, 1), ctx=None)
+    provenance.stamp(t, rec)
+    assert provenance.origin(t, provenance.RasterOrigin, "rasterize") is rec
+    for other in (t.clone(), t.detach(), t[:2], t + 0):
+        with pytest.raises(RuntimeError):
+            provenance.origin(other, provenance.RasterOrigin, "rasterize")
     with pytest.raises(RuntimeError):
-        provenance.lookup(t.clone(), "rasterize")
-    n = len(provenance._table)
-    del t
+        provenance.origin(t, provenance.InterpOrigin, "interpolate")
+    ref = weakref.ref(rec)
+    del t, rec
     gc.collect()
-    assert len(provenance._table) == n - 1
+    assert ref() is None  # the stamp dies with its tensor
 
 
 def test_argument_checks():
-    assert convert.check_resolution([4, 6]) == (4, 6)
+    assert convert.resolution_hw([4, 6]) == (4, 6)
+    assert convert.resolution_hw((np.int64(2), 3)) == (2, 3)
+    for bad in ([0, 6], [4], [4, 6, 1], None, ["a", 2]):
+        with pytest.raises(ValueError):
+            convert.resolution_hw(bad)
+    assert convert.vertex_batch(torch.zeros(3, 4)).shape == (1, 3, 4)
+    assert convert.vertex_batch(torch.zeros(2, 3, 4)).shape == (2, 3, 4)
     with pytest.raises(ValueError):
-        convert.check_resolution([0, 6])
-    assert convert.split_batch(torch.zeros(3, 4)).shape == (1, 3, 4)
-    with pytest.raises(ValueError):
-        convert.split_batch(torch.zeros(3))
+        convert.vertex_batch(torch.zeros(3))
     assert convert.image_batch(torch.zeros(2, 3, 1), "c").shape == (1, 2, 3, 1)
     with pytest.raises(ValueError):
         convert.channels(5, "attr")
