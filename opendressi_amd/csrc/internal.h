@@ -20,9 +20,13 @@ struct dressi_ctx {
     // device word the kernels OR error bits into (bad indices); checked and
     // cleared by dressi_ctx_synchronize
     uint32_t* d_err = nullptr;
-    // grow-only scratch for the per-op entry points (stream-ordered reuse)
+    // grow-only scratch for the per-op entry points. Each slot remembers the
+    // stream of its last use: a call on another stream first waits (event)
+    // for that stream, so reuse stays ordered across streams.
     std::vector<void*> ws_ptr;
     std::vector<size_t> ws_size;
+    std::vector<hipStream_t> ws_stream;
+    std::vector<hipEvent_t> ws_event;
 };
 
 namespace dressi {
@@ -60,7 +64,9 @@ void clear_error();
     } while (0)
 
 // Workspace slot `i` of at least `bytes` (grow-only; contents undefined, or
-// zero-filled on (re)allocation with ctx_workspace_zeroed).
+// zero-filled on (re)allocation with ctx_workspace_zeroed), ordered on the
+// context's current stream after every earlier use of the slot, whatever
+// stream that use ran on.
 int ctx_workspace(dressi_ctx* ctx, int slot, size_t bytes, void** out);
 int ctx_workspace_zeroed(dressi_ctx* ctx, int slot, size_t bytes, void** out);
 

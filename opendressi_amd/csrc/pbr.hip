@@ -63,6 +63,7 @@ struct PbrDev {
     float alpha[kPbrMaxLevels];
     float lr, b1, b2, eps, inv_n, irr_scale;
     int fix_k;  // fixed point: value * 2^fix_k
+    uint32_t* err;  // the context's error word (kErrFixedRange)
     float light_col[3];
     // static per (view, pixel)
     const float4* st0;  // fg: (u, v, n.v, n.l); bg: (bg u, bg v, -1, 0)
@@ -123,8 +124,22 @@ __device__ __forceinline__ void fetch4(const Taps& t, const float4* data, float*
     out3[2] = a2;
 }
 
-__device__ __forceinline__ long long to_fixed(float v, int k) {
-    return __double2ll_rn(ldexp((double)v, k));
+// Largest fixed-point term a scatter may add: every map-gradient term is
+// bounded by inv_n before the 16-lane row pre-sum (see dressi_pbr_create), so
+// a term is below 16 x 2^29 = 2^33 units; 2^34 leaves a factor of 2, and
+// 2^28 such terms (2^26 pixels x 4 taps) still sum below 2^63.
+constexpr double kFixLimit = 17179869184.0;  // 2^34
+// Error bit: a fixed-point term exceeded kFixLimit (or was not finite) and
+// was clamped; reported by dressi_ctx_synchronize.
+constexpr uint32_t kErrFixedRange = 0x100u;
+
+__device__ __forceinline__ long long to_fixed(float v, int k, uint32_t* err) {
+    double s = ldexp((double)v, k);
+    if (!(fabs(s) <= kFixLimit)) {
+        atomicOr(err, kErrFixedRange);
+        s = s != s ? 0.0 : copysign(kFixLimit, s);
+    }
+    return __double2ll_rn(s);
 }
 
 __device__ __forceinline__ float from_fixed(unsigned long long a, int k) {
@@ -843,7 +858,7 @@ __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
                 const int yy = yy0 < 0 ? 0 : (yy0 > h - 1 ? h - 1 : yy0);
 #pragma unroll
                 for (int c = 0; c < 3; c++) {
-                    const long long val = to_fixed(v[q * 3 + c], k);
+                    const long long val = to_fixed(v[q * 3 + c], k, d.err);
                     if (!val) continue;
                     if (lds) {
                         const int wi = (yy - wy0) * ww + (xx - box[m][0]);
@@ -1310,8 +1325,9 @@ int dressi_pbr_create(dressi_ctx* ctx, const dressi_pbr_desc* desc, dressi_pbr_p
                    "n_views must be in [1, %u]", kPbrMaxViews);
     DRESSI_REQUIRE(desc->width > 0 && desc->width == desc->height,
                    "the screen must be square (width == height > 0)");
-    DRESSI_REQUIRE((uint64_t)desc->n_views * desc->width * desc->height < (1ull << 31),
-                   "too many pixels");
+    // <= 2^26 pixels: the fixed-point map-gradient sums (kFixLimit) cannot wrap
+    DRESSI_REQUIRE((uint64_t)desc->n_views * desc->width * desc->height <= (1ull << 26),
+                   "too many pixels (views x width x height must be <= 2^26)");
     DRESSI_REQUIRE(desc->tex_w > 0 && desc->tex_h > 0 &&
                            (uint64_t)desc->tex_w * desc->tex_h < (1ull << 28),
                    "bad texture size");
@@ -1337,10 +1353,14 @@ int dressi_pbr_create(dressi_ctx* ctx, const dressi_pbr_desc* desc, dressi_pbr_p
     d.b2 = desc->beta2;
     d.eps = desc->eps;
     d.inv_n = 1.f / ((float)d.S * (float)d.S * 3.f);
-    // |d loss / d hdr| <= inv_n and every scattered term is bounded by it
-    // (materials in [0,1], env >= 0): 2^28 units per inv_n leaves > 2^5
-    // headroom below 2^63 at 2^26 pixels x 4 taps
+    // |d loss / d hdr| <= inv_n (L1 on the Reinhard-mapped image of
+    // non-negative radiance: d ldr / d hdr = 1 / (1 + hdr)^2 <= 1) and every
+    // scattered term is that times a coefficient in [0, 1] (material terms
+    // and split-sum factors in [0, 1], bilinear weights): with 2^28 units per
+    // inv_n a term stays below 2^29 units, a 16-lane pre-sum below 2^33, and
+    // to_fixed flags and clamps anything beyond 2^34 (kFixLimit)
     d.fix_k = 28 - ilogbf(d.inv_n);
+    d.err = ctx->d_err;
     // pooling chain (src/core/ibl.cpp:14-20): irradiance source <= 64 x 32,
     // prefilter source <= 128 x 64 (halving, sizes rounding up)
     d.pw[0] = d.ew;

@@ -36,11 +36,24 @@ int ctx_workspace(dressi_ctx* ctx, int slot, size_t bytes, void** out) {
     if ((int)ctx->ws_ptr.size() <= slot) {
         ctx->ws_ptr.resize(slot + 1, nullptr);
         ctx->ws_size.resize(slot + 1, 0);
+        ctx->ws_stream.resize(slot + 1, nullptr);
+        ctx->ws_event.resize(slot + 1, nullptr);
     }
+    hipStream_t cur = ctx->stream;
+    if (ctx->ws_ptr[slot] && ctx->ws_stream[slot] != cur) {
+        // the slot's last user ran on another stream: order this stream after it
+        if (!ctx->ws_event[slot]) {
+            DRESSI_TRY_HIP(hipEventCreateWithFlags(&ctx->ws_event[slot], hipEventDisableTiming));
+        }
+        DRESSI_TRY_HIP(hipEventRecord(ctx->ws_event[slot], ctx->ws_stream[slot]));
+        DRESSI_TRY_HIP(hipStreamWaitEvent(cur, ctx->ws_event[slot], 0));
+    }
+    ctx->ws_stream[slot] = cur;
     if (ctx->ws_size[slot] < bytes) {
         if (ctx->ws_ptr[slot]) {
-            // earlier work on the stream may still use the old buffer
-            DRESSI_TRY_HIP(hipStreamSynchronize(ctx->stream));
+            // earlier work may still use the old buffer: every earlier user is
+            // ordered before `cur` (above), so draining `cur` drains them all
+            DRESSI_TRY_HIP(hipStreamSynchronize(cur));
             DRESSI_TRY_HIP(hipFree(ctx->ws_ptr[slot]));
             ctx->ws_ptr[slot] = nullptr;
             ctx->ws_size[slot] = 0;
@@ -102,9 +115,13 @@ int dressi_ctx_destroy(dressi_ctx* ctx) {
     }
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
-    for (void* p : ctx->ws_ptr) {
-        if (p) {
-            hipFree(p);
+    for (size_t i = 0; i < ctx->ws_ptr.size(); ++i) {
+        if (ctx->ws_ptr[i]) {
+            hipStreamSynchronize(ctx->ws_stream[i]);
+            hipFree(ctx->ws_ptr[i]);
+        }
+        if (ctx->ws_event[i]) {
+            hipEventDestroy(ctx->ws_event[i]);
         }
     }
     if (ctx->d_err) {
@@ -139,7 +156,11 @@ int dressi_ctx_synchronize(dressi_ctx* ctx) {
     DRESSI_TRY_HIP(hipMemcpy(&err, ctx->d_err, sizeof(err), hipMemcpyDeviceToHost));
     if (err) {
         DRESSI_TRY_HIP(hipMemset(ctx->d_err, 0, sizeof(uint32_t)));
-        set_error("index out of range in a kernel input (error bits 0x%x)", err);
+        if (err & 0x100u) {
+            set_error("fixed-point gradient term out of range (clamped; error bits 0x%x)", err);
+        } else {
+            set_error("index out of range in a kernel input (error bits 0x%x)", err);
+        }
         return DRESSI_ERR_INVALID;
     }
     return DRESSI_OK;

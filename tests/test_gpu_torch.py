@@ -682,3 +682,46 @@ def test_rasterize_soft_matches_oracle(dr, ctx, oracle):
     want = _grad_vk_to_gl((g1 + g0)[None]).sum(0)
     _exact(_np(pos.grad), want, "rasterize_soft grad")
     assert np.abs(want).max() > 0
+
+
+# ------------------------------ two streams --------------------------------
+
+
+def _stream_case(dr, ctx, pos, tri, res):
+    """rasterize + antialias (colour and position gradients) + rasterize_soft
+    of one scene, all on torch's current stream."""
+    rast, _ = dr.rasterize(ctx, pos, tri, resolution=res)
+    col = torch.ones(1, res[0], res[1], 1, device=pos.device)
+    pos_g = pos.clone().requires_grad_(True)
+    out = dr.antialias(col, rast, pos_g, tri, n_samples=0)
+    out.backward(torch.ones_like(out))
+    soft = dr.rasterize_soft(ctx, pos, tri, res, radius_px=3.0)
+    return [rast, out.detach(), pos_g.grad, soft]
+
+
+def test_ops_on_two_streams_match_one_stream(dr, ctx):
+    """The per-op entry points share the context's workspace slots (records,
+    bins, face ids); calls issued from two torch streams, back to back with
+    no host synchronisation, must give the single-stream results (each slot
+    orders its next user after its last one, on whichever stream)."""
+    print("[torch] two streams", flush=True)
+    big = _sphere(level=3, seed=5)
+    small = _sphere(level=1, seed=6)
+    cases = [(torch.from_numpy(c).cuda(), torch.from_numpy(f).cuda(), r)
+             for (c, f), r in ((big, [96, 112]), (small, [40, 36]), (big, [64, 64]))]
+    want = [[_np(t) for t in _stream_case(dr, ctx, *c)] for c in cases]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    got = []
+    for rep in range(2):
+        for i, c in enumerate(cases):
+            s = streams[(i + rep) % 2]
+            with torch.cuda.stream(s):
+                got.append((i, _stream_case(dr, ctx, *c)))
+    for s in streams:
+        torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for i, outs in got:
+        for k, (a, b) in enumerate(zip(outs, want[i])):
+            _exact(a.detach().cpu().numpy(), b, f"case {i} output {k}")
