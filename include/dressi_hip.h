@@ -103,6 +103,23 @@ int dressi_rasterize_soft(dressi_ctx* ctx, const float* soft_clip,
                           uint32_t width, uint32_t height, float radius_px,
                           const float* prev_shifted_depth, float* out);
 
+/* dressi_rasterize_soft without any allocation: no counterpart in the
+ * reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and results as dressi_rasterize_soft; its face records and
+ * tile bins live in one fixed 32 MiB device array per GPU instead of the
+ * context workspace, so a call needs 256-byte-aligned 176 B + 16 B per face
+ * plus 4100 B per 16x16 tile (+256) within 32 MiB (e.g. a 1024x1024 screen
+ * with up to ~79k faces) and returns DRESSI_ERR_INVALID beyond that. Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, threads or contexts) race. */
+int dressi_rasterize_soft_noalloc(dressi_ctx* ctx, const float* soft_clip,
+                                  const float* face_id, const float* faces_soft,
+                                  const float* hard_clip, uint32_t n_verts,
+                                  const float* faces_tex, uint32_t n_faces,
+                                  uint32_t width, uint32_t height, float radius_px,
+                                  const float* prev_shifted_depth, float* out);
+
 /* F::Rasterize (src/core/f_ops.cpp:1182-1207, CPU RasterizeHardCpu
  * src/core/cpu_raster.cpp:195-225): depth-tested, perspective-correct
  * attribute interpolation; out {S,S} x n_comp, background 0. */

@@ -77,6 +77,7 @@ _SIGS = {
     "dressi_memset": (_I, [_P, _P, _I, _S]),
     "dressi_soft_clip": (_I, [_P, _P, _U, _P, _U, _U, _U, _F, _P]),
     "dressi_rasterize_soft": (_I, [_P, _P, _P, _P, _P, _U, _P, _U, _U, _U, _F, _P, _P]),
+    "dressi_rasterize_soft_noalloc": (_I, [_P, _P, _P, _P, _P, _U, _P, _U, _U, _U, _F, _P, _P]),
     "dressi_rasterize": (_I, [_P, _P, _U, _P, _U, _P, _U, _U, _U, _P]),
     "dressi_rasterize_face_id": (_I, [_P, _P, _U, _P, _U, _U, _U, _P]),
     "dressi_lookup_faces": (_I, [_P, _P, _U, _U, _P, _U, _U, _P]),

@@ -1,5 +1,7 @@
 // raster.hip -- tile binning, the per-op rasterizers (RasterizeSoft,
 // Rasterize, RasterizeFaceId) and SoftClip.
+#include <mutex>
+
 #include "raster_core.h"
 #include "soft_clip.h"
 
@@ -367,6 +369,15 @@ __global__ void k_faces_to_i32(const float* faces, uint32_t n, uint32_t n_verts,
 
 }  // namespace dressi
 
+// Scratch of dressi_rasterize_soft_noalloc: one fixed array per GPU (each
+// GPU the library runs on holds its own copy until the process ends). In
+// host code the name `scratch` is a host-side stand-in, never the device
+// array: kernels take the per-device address that hipGetSymbolAddress
+// returns (noalloc_scratch below). Every call on a GPU shares that GPU's
+// array, so calls that overlap on one GPU race.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 using namespace dressi;
 
 namespace {
@@ -374,6 +385,64 @@ namespace {
 int check_ctx(dressi_ctx* ctx) {
     DRESSI_REQUIRE(ctx != nullptr, "NULL context");
     DRESSI_TRY_HIP(hipSetDevice(ctx->device));
+    return DRESSI_OK;
+}
+
+int check_soft_args(const float* soft_clip, const float* face_id, const float* faces_soft,
+                    const float* hard_clip, const float* faces_tex, uint32_t width,
+                    uint32_t height, float radius_px, const float* out) {
+    DRESSI_REQUIRE(soft_clip && face_id && faces_soft && hard_clip && faces_tex && out,
+                   "dressi_rasterize_soft: NULL buffer");
+    DRESSI_REQUIRE(radius_px > 0.f, "RasterizeSoft: radius_px must be > 0");
+    DRESSI_REQUIRE(width > 0 && height > 0, "RasterizeSoft: empty screen");
+    return DRESSI_OK;
+}
+
+// RasterizeSoft over caller-provided scratch: `recs` / `cull` hold one record
+// per face, `bins` fixed_bin_bytes(tiles, kSoftBinCap) bytes (counts cleared
+// here by a fill kernel, so the scratch may hold anything on entry).
+int launch_rasterize_soft(dressi_ctx* ctx, const RasterGeom& g, const float* soft_clip,
+                          const float* face_id, const float* faces_soft, const float* hard_clip,
+                          uint32_t n_verts, const float* faces_tex, float radius_px,
+                          const float* prev_shifted_depth, SoftRec* recs, void* bins,
+                          CullRec* cull, float* out) {
+    BinBuffers b;
+    fixed_bin_carve(bins, g.n_tiles, kSoftBinCap, &b);
+    hipLaunchKernelGGL(k_fill_u32, dim3(div_up(g.n_tiles, 256)), dim3(256), 0, ctx->stream,
+                       b.counts, g.n_tiles, 0u);
+    DRESSI_CHECK_LAUNCH();
+    if (g.n_faces) {
+        hipLaunchKernelGGL(k_soft_setup_op, dim3(div_up(g.n_faces, 256)), dim3(256), 0,
+                           ctx->stream, g, (const float4*)soft_clip, face_id, faces_soft,
+                           (const float4*)hard_clip, n_verts, faces_tex, b, ctx->d_err, recs,
+                           cull);
+        DRESSI_CHECK_LAUNCH();
+    }
+    hipLaunchKernelGGL(k_raster_soft_op, dim3(block_grid(g)), dim3(64), 0, ctx->stream, g,
+                       (const SoftRec*)recs, (const CullRec*)cull, b, radius_px,
+                       prev_shifted_depth, (float4*)out);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_noalloc_mu;
+char* g_noalloc_ptr[kNoAllocMaxDevices] = {};
+
+// The device address of this GPU's scratch array, looked up once per device
+// with that device current (the caller has made it current).
+int noalloc_scratch(int device, char** out) {
+    DRESSI_REQUIRE(device >= 0 && device < kNoAllocMaxDevices, "device %d out of range", device);
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[device]) {
+        void* p = nullptr;
+        DRESSI_TRY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        DRESSI_REQUIRE(p != nullptr, "hipGetSymbolAddress returned NULL");
+        g_noalloc_ptr[device] = (char*)p;
+    }
+    *out = g_noalloc_ptr[device];
     return DRESSI_OK;
 }
 
@@ -401,33 +470,43 @@ int dressi_rasterize_soft(dressi_ctx* ctx, const float* soft_clip, const float* 
                           uint32_t height, float radius_px, const float* prev_shifted_depth,
                           float* out) {
     if (int rc = check_ctx(ctx)) return rc;
-    DRESSI_REQUIRE(soft_clip && face_id && faces_soft && hard_clip && faces_tex && out,
-                   "dressi_rasterize_soft: NULL buffer");
-    DRESSI_REQUIRE(radius_px > 0.f, "RasterizeSoft: radius_px must be > 0");
-    DRESSI_REQUIRE(width > 0 && height > 0, "RasterizeSoft: empty screen");
+    if (int rc = check_soft_args(soft_clip, face_id, faces_soft, hard_clip, faces_tex, width,
+                                 height, radius_px, out)) return rc;
     const RasterGeom g = make_geom(width, height, 1, n_faces);
     void *recs = nullptr, *bins = nullptr, *cull = nullptr;
     const size_t nf1 = n_faces ? n_faces : 1;
     if (int rc = ctx_workspace(ctx, 0, sizeof(SoftRec) * nf1, &recs)) return rc;
     if (int rc = ctx_workspace(ctx, 1, fixed_bin_bytes(g.n_tiles, kSoftBinCap), &bins)) return rc;
     if (int rc = ctx_workspace(ctx, 3, sizeof(CullRec) * nf1, &cull)) return rc;
-    BinBuffers b;
-    fixed_bin_carve(bins, g.n_tiles, kSoftBinCap, &b);
-    hipLaunchKernelGGL(k_fill_u32, dim3(div_up(g.n_tiles, 256)), dim3(256), 0, ctx->stream,
-                       b.counts, g.n_tiles, 0u);
-    DRESSI_CHECK_LAUNCH();
-    if (n_faces) {
-        hipLaunchKernelGGL(k_soft_setup_op, dim3(div_up(n_faces, 256)), dim3(256), 0,
-                           ctx->stream, g, (const float4*)soft_clip, face_id, faces_soft,
-                           (const float4*)hard_clip, n_verts, faces_tex, b, ctx->d_err,
-                           (SoftRec*)recs, (CullRec*)cull);
-        DRESSI_CHECK_LAUNCH();
-    }
-    hipLaunchKernelGGL(k_raster_soft_op, dim3(block_grid(g)), dim3(64), 0, ctx->stream, g,
-                       (const SoftRec*)recs, (const CullRec*)cull, b, radius_px,
-                       prev_shifted_depth, (float4*)out);
-    DRESSI_CHECK_LAUNCH();
-    return DRESSI_OK;
+    return launch_rasterize_soft(ctx, g, soft_clip, face_id, faces_soft, hard_clip, n_verts,
+                                 faces_tex, radius_px, prev_shifted_depth, (SoftRec*)recs, bins,
+                                 (CullRec*)cull, out);
+}
+
+int dressi_rasterize_soft_noalloc(dressi_ctx* ctx, const float* soft_clip, const float* face_id,
+                                  const float* faces_soft, const float* hard_clip,
+                                  uint32_t n_verts, const float* faces_tex, uint32_t n_faces,
+                                  uint32_t width, uint32_t height, float radius_px,
+                                  const float* prev_shifted_depth, float* out) {
+    if (int rc = check_ctx(ctx)) return rc;
+    if (int rc = check_soft_args(soft_clip, face_id, faces_soft, hard_clip, faces_tex, width,
+                                 height, radius_px, out)) return rc;
+    const RasterGeom g = make_geom(width, height, 1, n_faces);
+    const size_t nf1 = n_faces ? n_faces : 1;
+    const size_t rec_bytes = align256(sizeof(SoftRec) * nf1);
+    const size_t cull_bytes = align256(sizeof(CullRec) * nf1);
+    const size_t bin_bytes_ = fixed_bin_bytes(g.n_tiles, kSoftBinCap);
+    const size_t need = rec_bytes + cull_bytes + bin_bytes_;
+    DRESSI_REQUIRE(need <= kNoAllocScratchBytes,
+                   "dressi_rasterize_soft_noalloc: %u faces on a %ux%u screen need %zu bytes of "
+                   "scratch, above the fixed %zu (use dressi_rasterize_soft)",
+                   n_faces, width, height, need, kNoAllocScratchBytes);
+    char* base = nullptr;
+    if (int rc = noalloc_scratch(ctx->device, &base)) return rc;
+    return launch_rasterize_soft(ctx, g, soft_clip, face_id, faces_soft, hard_clip, n_verts,
+                                 faces_tex, radius_px, prev_shifted_depth, (SoftRec*)base,
+                                 base + rec_bytes + cull_bytes, (CullRec*)(base + rec_bytes),
+                                 out);
 }
 
 static int rasterize_hard_common(dressi_ctx* ctx, const float* clip, uint32_t n_verts,
