@@ -77,24 +77,31 @@ def iteration_bytes_tex(n_views: int, s: int, n_faces: int, n_verts: int, texels
 
 
 def kernel_bytes_tex(n_views: int, s: int, n_faces: int, n_verts: int, texels: int) -> dict:
-    """Algorithmic bytes per launch of the texture-plan kernels.
+    """Compulsory bytes per launch of the texture-plan kernels, the
+    iteration's compulsory traffic (iteration_bytes_tex) split over the
+    kernels that need it; the plan's own intermediates (per-pixel g_uv and
+    d loss / d sample) are not counted.
 
-    clip:     positions in, clip (16 B) and screen attribute (8 B) out, per
-              vertex and view
-    setup:    clip in, faces and the screen triangles out, per view
-    raster:   screen triangles in, 4-byte face-id image out, per view
-    fwd:      face id in, g_uv (8 B) and d loss / d sample (16 B) out per
-              pixel and view, RGBA loss image out, both textures read once
-    bwd_adam: g_uv + d loss / d sample read once per view, the UV raster's
-              texel record, texture / m / v read + write, per texel
+    clip:     positions and uv in, clip (16 B) and screen attribute (8 B) out,
+              per vertex and view
+    setup:    clip in, faces in, per view
+    raster:   the 8-byte visibility word (depth | id) written per pixel and
+              view
+    fwd:      the visibility word read per pixel and view, the loss image
+              out, the texture and the target texture read (16 B + 16 B per
+              texel)
+    bwd_adam: the texel gradient written and read (32 B per texel, as the
+              iteration model counts it; here it stays in registers) and
+              texture / m / v read and written (96 B per texel)
+    The shares add up to iteration_bytes_tex.
     """
     n, S2, F, V, T = n_views, float(s) * s, float(n_faces), float(n_verts), float(texels)
     return {
-        "k_tex_clip": n * 36.0 * V,
-        "k_aa_setup": n * (16.0 * V + 48.0 * F),
-        "k_aa_raster": n * (4.0 * S2 + 36.0 * F),
-        "k_tex_fwd": n * 28.0 * S2 + 16.0 * S2 + 32.0 * T,
-        "k_tex_bwd_adam": n * 24.0 * S2 + 112.0 * T,
+        "k_tex_clip": n * 32.0 * V,
+        "k_aa_setup": n * (8.0 * V + 12.0 * F),
+        "k_aa_raster": n * 8.0 * S2,
+        "k_tex_fwd": n * 8.0 * S2 + 4.0 * S2 + 32.0 * T,
+        "k_tex_bwd_adam": 128.0 * T,
     }
 
 
@@ -246,82 +253,139 @@ def cpu_baseline_pbr(workload) -> dict:
 
 def cpu_baseline(workload) -> dict:
     """The oracle (C restatement of the reference CPU evaluator, single
-    thread) on a bounded sample: one iteration of ONE of the workload's views
-    at full resolution, scaled to iterations/s of all views (views are
-    independent until the per-vertex gradient; the Adam step is negligible)."""
+    thread) on a bounded sample: ONE of the workload's views at full
+    resolution, timed for 1 and for 2 iterations; the difference is one
+    steady-state iteration of that view (the static target raster, which
+    the reference prunes after its warm-up, and the set-up drop out),
+    scaled to iterations/s of all views (views are independent until the
+    per-vertex gradient; the Adam step is negligible)."""
     import opendressi_amd as od
     from oracle.pyoracle import ORACLE_SO, Oracle, build
     if not os.path.exists(ORACLE_SO):
         build()
     pos, faces, tgt, mvps = od.make_scene(workload)
     o = Oracle()
-    t0 = time.perf_counter()
     fit = o.aa_fit if workload.technique == "aa" else o.hsr_fit
-    fit(pos, faces, tgt, faces, mvps[:1], workload.screen, lr=workload.lr, iters=1,
-        want_images=False)
-    dt = time.perf_counter() - t0
-    per_iter = dt * len(mvps)
-    return {"value": 1.0 / per_iter, "unit": "iterations/s", "cores": 1, "kind": "port",
-            "sample": (f"1 iteration of 1 of {len(mvps)} views at {workload.screen}^2 "
-                       f"(incl. its target raster), {dt:.2f} s, scaled x{len(mvps)}; "
-                       f"host CPU: {cpu_info()}, nproc {os.cpu_count()}")}
+    times = []
+    for iters in (1, 2):
+        t0 = time.perf_counter()
+        fit(pos, faces, tgt, faces, mvps[:1], workload.screen, lr=workload.lr, iters=iters,
+            want_images=False)
+        times.append(time.perf_counter() - t0)
+    dt = max(times[1] - times[0], 1e-9)
+    n = len(mvps)
+    return {"value": 1.0 / (dt * n), "unit": "iterations/s", "cores": 1, "kind": "port",
+            "sample": (f"1 of {n} views at {workload.screen}^2: 1 and 2 iterations "
+                       f"({times[0]:.2f} s, {times[1]:.2f} s), the difference (one iteration "
+                       f"without the static target raster) scaled x{n}; host CPU: "
+                       f"{cpu_info()}, nproc {os.cpu_count()}")}
 
 
-def bench_record(workload: str, path: str, warmup: int) -> None:
-    """The reference example's bench.json record (examples/common/bench.cpp:
-    165-209, fields of examples/silhouette_optimization/run.cpp:686-703) for
-    a silhouette workload: the fit run from its start for the workload's
-    iteration count, each execStep timed with a host synchronisation (the
-    reference's median steady-state wall time), warm-up iterations excluded;
-    loss drop = first / last loss; mean IoU of the final prediction and the
-    target masks (> 0.5) over the views."""
-    import platform
-    import time
+BENCH_KEYS = ("example", "device", "platform", "os", "cpu", "cpu_cores", "ram_gb", "funcs",
+              "substages", "stages", "technique", "screen", "views", "iters", "samples", "peels",
+              "single_view", "median_ms_per_iter", "warmup_excluded", "warmup_ms",
+              "first_build_ms", "mean_iou", "loss_drop")
 
-    import numpy as np
 
+def median_upper(samples) -> float:
+    """The reference's MedianMs (examples/common/bench.cpp:145-151): the
+    element at n / 2 of the sorted samples (the upper median), 0 if none."""
+    s = sorted(samples)
+    return float(s[len(s) // 2]) if s else 0.0
+
+
+def bench_fields(device: str, cpu: str, cores: int, ram_gb: float, kernels: int,
+                 technique: str, screen: int, views: int, iters: int, iter_ms,
+                 mean_iou: float, first_loss: float, last_loss: float) -> dict:
+    """The silhouette example's bench.json record
+    (examples/silhouette_optimization/run.cpp:573-587, 676-702;
+    examples/common/bench.cpp:145-209) from per-execStep wall times
+    `iter_ms` of the whole run: the first min(20, iters / 2) are the warm-up
+    (the first of them is first_build_ms), the median of the rest is the
+    upper median. The packing counts describe this executor: `funcs` and
+    `substages` are the fused kernels of one iteration, `stages` the one
+    hipGraph launch per iteration."""
+    warm_n = min(20, iters // 2)
+    warm, steady = list(iter_ms[:warm_n]), list(iter_ms[warm_n:])
+    median = median_upper(steady)
+    warm_ms = max(0.0, sum(warm) - median * len(warm))
+    fields = {
+        "example": "silhouette_optimization", "device": device, "platform": "linux",
+        "os": f"{platform.system()} {platform.release()}", "cpu": cpu, "cpu_cores": int(cores),
+        "ram_gb": round(float(ram_gb), 1), "funcs": int(kernels), "substages": int(kernels),
+        "stages": 1, "technique": technique, "screen": int(screen), "views": int(views),
+        "iters": int(iters), "samples": 8, "peels": 1, "single_view": views == 1,
+        "median_ms_per_iter": round(median, 6), "warmup_excluded": int(warm_n),
+        "warmup_ms": round(warm_ms, 1), "first_build_ms": round(warm[0] if warm else 0.0, 1),
+        "mean_iou": round(float(mean_iou), 6),
+        "loss_drop": round(first_loss / max(last_loss, 1e-12), 1),
+    }
+    assert tuple(fields) == BENCH_KEYS
+    return fields
+
+
+def bench_record(workload: str, path: str) -> None:
+    """The reference example's bench.json record for a silhouette workload:
+    the fit run from its start for the workload's iteration count, each
+    execStep timed to a host synchronisation; after the loop one more
+    execStep, then the mean IoU of the predictions and the target masks
+    (> 0.5) over the views and the last loss (run.cpp:640-662)."""
     import opendressi_amd as od
     from opendressi_amd import _lib
     w = od.WORKLOADS[workload]
     ctx = od.Context(0)
-    t0 = time.perf_counter()
     fit = od.SilhouetteFit.from_workload(ctx, workload, keep_pred=True)
-    fit.step(1, graph=False)
-    fit.synchronize()
-    first_build_ms = (time.perf_counter() - t0) * 1e3
-    first_loss = fit.loss()
-    warm, samples = [], []
-    for i in range(1, w.iters):
+    iter_ms = []
+    first_loss = None
+    for i in range(w.iters):
         t = time.perf_counter()
         fit.step(1)
         fit.synchronize()
-        (warm if i <= warmup else samples).append((time.perf_counter() - t) * 1e3)
+        iter_ms.append((time.perf_counter() - t) * 1e3)
+        if i == 0:
+            first_loss = fit.loss()
+    fit.step(1)
+    fit.synchronize()
     last_loss = fit.loss()
-    median = float(np.median(samples)) if samples else float("nan")
-    warm_ms = max(0.0, sum(warm) - median * len(warm))
     pred, tgt = fit.read(_lib.BUF_PRED) > 0.5, fit.read(_lib.BUF_TARGET) > 0.5
     ious = [float((p & t).sum()) / max(float((p | t).sum()), 1.0) for p, t in zip(pred, tgt)]
     try:
         ram_gb = os.sysconf("SC_PAGE_SIZE") * os.sysconf("SC_PHYS_PAGES") / 2**30
     except (ValueError, OSError):
         ram_gb = 0.0
-    fields = [
-        ("example", "silhouette_optimization"), ("device", ctx.device_name),
-        ("platform", "linux"), ("os", f"{platform.system()} {platform.release()}"),
-        ("cpu", cpu_info()), ("cpu_cores", os.cpu_count() or 0), ("ram_gb", round(ram_gb, 1)),
-        ("funcs", 5), ("substages", 5), ("stages", 5),
-        ("technique", "hardsoftras" if w.technique == "hsr" else "aa"), ("screen", w.screen),
-        ("views", w.views), ("iters", w.iters), ("samples", 8), ("peels", 1),
-        ("single_view", w.views == 1), ("median_ms_per_iter", round(median, 4)),
-        ("warmup_excluded", warmup), ("warmup_ms", round(warm_ms, 1)),
-        ("first_build_ms", round(first_build_ms, 1)),
-        ("mean_iou", round(float(np.mean(ious)), 4)),
-        ("loss_drop", round(first_loss / max(last_loss, 1e-12), 1)),
-    ]
+    fields = bench_fields(ctx.device_name, cpu_info(), os.cpu_count() or 0, ram_gb,
+                          len(fit.profile(1)), "hardsoftras" if w.technique == "hsr" else "aa",
+                          w.screen, w.views, w.iters, iter_ms, float(np.mean(ious)), first_loss,
+                          last_loss)
     with open(path, "w") as fh:
-        fh.write(json.dumps(dict(fields), separators=(",", ":")) + "\n")
+        fh.write(json.dumps(fields, separators=(",", ":")) + "\n")
     fit.close()
     ctx.close()
+
+
+def metric_point(name: str, steps: int, warmup: int) -> dict:
+    """Iterations/s of another silhouette workload (graph replays, inputs
+    resident), for the metric's other resolution points."""
+    import opendressi_amd as od
+    w = od.WORKLOADS[name]
+    ctx = od.Context(0)
+    fit = od.SilhouetteFit.from_workload(ctx, name)
+    fit.step(warmup)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    fit.step(steps)
+    ctx.synchronize()
+    dt = time.perf_counter() - t0
+    nb = (iteration_bytes_aa if w.technique == "aa" else iteration_bytes)(
+        fit.n_views, fit.screen, fit.n_faces, fit.n_verts)
+    fit.close()
+    ctx.close()
+    its = steps / dt
+    return {"workload": f"{name}: {'AA' if w.technique == 'aa' else 'HardSoftRas'} "
+                        f"{w.screen}^2 x {w.views} views, icosphere L{w.level}",
+            "value": its, "unit": "iterations/s", "ms_per_step": 1e3 / its, "steps": steps,
+            "mpixels_per_s": w.views * w.screen * w.screen * its / 1e6,
+            "iteration_frac_of_hbm_peak": nb * its / HBM_PEAK}
 
 
 def main() -> int:
@@ -331,6 +395,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c4_hsr")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-points", action="store_true",
+                    help="skip the metric's other points (c2 at 512^2, c4 AA at 2048^2)")
     ap.add_argument("--profile-iters", type=int, default=20)
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="after the JSON line, run a plain device copy of this many MiB "
@@ -428,6 +494,10 @@ def main() -> int:
         "kernel_us": prof,
         "loss_after": loss_end,
     }
+    if args.workload == "c4_hsr" and not args.no_points:
+        # the metric's 512^2 point and the AA technique at 2048^2
+        line["metric_points"] = {"c2": metric_point("c2", 400, 20),
+                                 "c4": metric_point("c4", 100, 10)}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = (cpu_baseline_pbr(w) if pbr else
                                 cpu_baseline_tex(w) if tex else cpu_baseline(w))
@@ -437,8 +507,7 @@ def main() -> int:
         if tex or pbr:
             print("--bench-json: the record covers the silhouette workloads", file=sys.stderr)
         else:
-            bench_record(args.workload, args.bench_json, min(20, max(1, od.WORKLOADS[
-                args.workload].iters // 5)))
+            bench_record(args.workload, args.bench_json)
     if args.copy_mb > 0:
         import torch
         n = args.copy_mb * (1 << 20) // 4

@@ -6,6 +6,9 @@ workload's full size for its full iteration count.
     python tests/golden/make_final_params.py              # every workload
     python tests/golden/make_final_params.py c2 c4_hsr    # the named ones
 
+`final_c5_first.npz` holds C5's first two iterations (images and gradients
+of the first, parameters after the second) at full size, sampled.
+
 The reference example stops after a fixed iteration count and reports the
 optimised parameters (examples/silhouette_optimization/run.cpp:574-637,
 examples/texture_optimization/run.cpp:205-250,
@@ -110,7 +113,28 @@ def pbr(name: str) -> dict:
     return arrs
 
 
-KINDS = {"c2": silhouette, "c4_hsr": silhouette, "c4": silhouette, "c3": texture, "c5": pbr}
+def pbr_first(name: str) -> dict:
+    """C5's first iterations at full size: the first iteration's target and
+    prediction images and parameter gradients, the parameters after two
+    iterations (sampled: the images alone are 75 MB each)."""
+    import opendressi_amd as od
+    from opendressi_amd.pbr import workload_scene
+    from oracle.pyoracle import Oracle
+    w = od.PBR_WORKLOADS[name.split("_")[0]]
+    sc = workload_scene(w)
+    r = Oracle().pbr_fit(sc, iters=2, want_images=True)
+    arrs = {"in_sha_" + k: sha(v) for k, v in sc.items() if isinstance(v, np.ndarray)}
+    arrs.update(out_loss=r["loss"])
+    for i, k in enumerate(("pred0", "target0", "mask0", "g_albedo0", "g_mr0", "g_env0",
+                           "albedo", "mr", "env")):
+        a = r[k] if r[k].ndim == 4 or k != "mask0" else r[k][..., None]
+        put_param(arrs, k, a, False, 20 + i)
+        arrs["out_max_" + k] = np.array([np.abs(a).max()], np.float64)
+    return arrs
+
+
+KINDS = {"c2": silhouette, "c4_hsr": silhouette, "c4": silhouette, "c3": texture, "c5": pbr,
+         "c5_first": pbr_first}
 
 
 def run(name: str) -> str:
