@@ -22,17 +22,18 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libdressi_hip.so")
 SOURCES = ["runtime.hip", "raster.hip", "hsr.hip", "aa.hip", "tex.hip", "ds.hip", "ibl.hip", "pbr.hip",
-           "graph.hip"]
+           "graph.hip", "executor.hip", "builders.hip", "route.hip"]
 HEADERS = ["internal.h", "dressi_math.h", "raster_core.h", "soft_clip.h", "hsr_chain.h",
-           "aa_core.h", "plan.h", "ibl_core.h"]
+           "aa_core.h", "plan.h", "ibl_core.h", "graph_ir.h", "route.h"]
 ARCH = os.environ.get("DRESSI_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result", "-Wno-unused-value",
 ]
+OBJ_DIR = os.path.join(PKG, "_build")
 
 
 def hipcc() -> str:
@@ -42,16 +43,30 @@ def hipcc() -> str:
     return "hipcc"
 
 
-def build(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp, *srcs]
+def _run(cmd, verbose, what):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed building libdressi_hip.so")
+        raise RuntimeError(f"hipcc failed building {what}")
+
+
+def build(verbose: bool = False) -> str:
+    """Every source compiled (in parallel, one object each), then linked."""
+    from concurrent.futures import ThreadPoolExecutor
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    inc = ["-I", os.path.join(ROOT, "include")]
+    objs = [os.path.join(OBJ_DIR, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    jobs = min(len(SOURCES), max(1, min(os.cpu_count() or 1, 8)))
+    with ThreadPoolExecutor(jobs) as ex:
+        futs = [ex.submit(_run, [hipcc(), *FLAGS, *inc, "-c", os.path.join(CSRC, s), "-o", o],
+                          verbose, s) for s, o in zip(SOURCES, objs)]
+        for f in futs:
+            f.result()
+    tmp = LIB + ".tmp"
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose,
+         "libdressi_hip.so")
     os.replace(tmp, LIB)
     return LIB
 

@@ -1,0 +1,1848 @@
+// executor.hip -- DressiAD on one HIP device (include/dressi/dressi_ad.h;
+// the reference's src/dressi_ad.cpp:24-696 is the behaviour it keeps).
+//
+// execStep walks the reference's ladder only as far as the last change
+// requires (src/dressi_ad.cpp:280-530):
+//   BACKWARD   BuildBackward(loss)
+//   OPTIMIZER  the optimizer's update graph; copy-back pairs (optimizer
+//              outputs are rebuilt here, addUpdate pairs persist)
+//   TRAVERSE   the functions the roots need, in creation order; the leaves
+//   SUBSTAGE   demand filter (static branches whose images are computed
+//              are skipped: the reactive cache of src/pack/reactive.cpp:
+//              10-68), then packing into steps
+//   STAGE      step-level demand filter (the fast rebuild)
+//   VULKAN     device buffers, step programs, and the captured hipGraph
+// then runs the iteration: pending / fused uploads, one hipGraph launch
+// (steps + end-of-frame copy-backs), fused downloads.
+//
+// Steps: with PackingMode::RSP every run of consecutive elementwise
+// functions producing images of one size becomes ONE kernel, a per-pixel
+// program over registers (the reference's fused substage: intermediate
+// values never touch memory; images consumed outside the step, roots and
+// copy-back sources are stored); the other ops run through the library's
+// per-op entry points (include/dressi_hip.h). PackingMode::Naive gives every
+// function its own step. Every op keeps the reference CPU kernel's float
+// semantics, so results do not depend on the packing.
+//
+// A graph recognised as the reference's silhouette-fit example (HardSoftRas
+// or AA, see route.h) runs on the fused silhouette plan instead.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <set>
+#include <unordered_map>
+#include <unordered_set>
+
+#include "graph_ir.h"
+#include "internal.h"
+#include "route.h"
+
+namespace dressi {
+
+struct HipContext {
+    dressi_ctx* ctx = nullptr;
+    int device = 0;
+    ~HipContext() {
+        if (ctx) {
+            dressi_ctx_destroy(ctx);
+        }
+    }
+};
+
+namespace {
+
+void check(int rc, const char* what) {
+    if (rc != DRESSI_OK) {
+        throw DressiError(std::string(what) + ": " + dressi_last_error());
+    }
+}
+
+void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        throw DressiError(std::string(what) + ": " + hipGetErrorString(e));
+    }
+}
+
+// ---- fused elementwise stage ------------------------------------------------
+
+constexpr int kMaxStepInstrs = 48;  // registers of one fused program
+constexpr int kMaxInputs = 4;
+
+// Where an instruction input comes from
+enum : int { kSrcReg = 0, kSrcBuf = 1, kSrcImm = 2 };
+
+struct FInput {
+    int src;
+    uint32_t idx;  // register, buffer slot or immediate offset
+    uint32_t nc;   // components
+    uint32_t uniform;
+};
+
+struct FInstr {
+    int op;
+    uint32_t n_in;
+    uint32_t ny;
+    uint32_t a0;
+    int out_slot;  // buffer slot to store to, -1: register only
+    FInput in[kMaxInputs];
+};
+
+struct FProgram {
+    const FInstr* code;
+    uint32_t n;
+    size_t n_px;
+    float* const* bufs;  // slot -> device buffer
+    const float* imm;
+};
+
+__device__ __forceinline__ float std_min(float a, float b) { return b < a ? b : a; }
+__device__ __forceinline__ float std_max(float a, float b) { return a < b ? b : a; }
+
+// one elementwise op on one pixel: `v[i][c]` = component c of input i
+// (1-component inputs replicated), the reference's CPU float semantics
+__device__ void ew_eval(Op op, uint32_t n_in, const uint32_t* nc, float (*v)[4], uint32_t ny,
+                        uint32_t a0, float* y) {
+    switch (op) {
+        case Op::kCompose: {
+            uint32_t o = 0;
+            for (uint32_t i = 0; i < n_in; i++) {
+                for (uint32_t c = 0; c < nc[i]; c++) {
+                    y[o++] = v[i][c];
+                }
+            }
+            return;
+        }
+        case Op::kExtract:
+            for (uint32_t c = 0; c < ny; c++) {
+                y[c] = v[0][a0 + c];
+            }
+            return;
+        case Op::kDot: {
+            float acc = 0.f;
+            for (uint32_t c = 0; c < nc[0]; c++) {
+                acc += v[0][c] * v[1][c];
+            }
+            y[0] = acc;
+            return;
+        }
+        case Op::kCompSum: {
+            float acc = 0.f;
+            for (uint32_t c = 0; c < nc[0]; c++) {
+                acc += v[0][c];
+            }
+            y[0] = acc;
+            return;
+        }
+        case Op::kLength: {
+            float acc = 0.f;
+            for (uint32_t c = 0; c < nc[0]; c++) {
+                acc += v[0][c] * v[0][c];
+            }
+            y[0] = sqrtf(acc);
+            return;
+        }
+        case Op::kNormalize: {
+            float acc = 0.f;
+            for (uint32_t c = 0; c < nc[0]; c++) {
+                acc += v[0][c] * v[0][c];
+            }
+            const float inv = 1.f / sqrtf(acc);
+            for (uint32_t c = 0; c < ny; c++) {
+                y[c] = v[0][c] * inv;
+            }
+            return;
+        }
+        case Op::kCross:
+            y[0] = v[0][1] * v[1][2] - v[0][2] * v[1][1];
+            y[1] = v[0][2] * v[1][0] - v[0][0] * v[1][2];
+            y[2] = v[0][0] * v[1][1] - v[0][1] * v[1][0];
+            return;
+        default:
+            break;
+    }
+    for (uint32_t c = 0; c < ny; c++) {
+        const float a = v[0][c];
+        const float b = n_in > 1 ? v[1][c] : 0.f;
+        const float t = n_in > 2 ? v[2][c] : 0.f;
+        float r = 0.f;
+        switch (op) {
+            case Op::kAdd: r = a + b; break;
+            case Op::kSub: r = a - b; break;
+            case Op::kMul: r = a * b; break;
+            case Op::kDiv: r = a / b; break;
+            case Op::kNeg: r = -a; break;
+            case Op::kSin: r = sinf(a); break;
+            case Op::kCos: r = cosf(a); break;
+            case Op::kTan: r = tanf(a); break;
+            case Op::kAsin: r = asinf(a); break;
+            case Op::kAcos: r = acosf(a); break;
+            case Op::kAtan: r = atanf(a); break;
+            case Op::kAtan2: r = atan2f(a, b); break;
+            case Op::kExp: r = libc_expf(a); break;
+            case Op::kExp2: r = exp2f(a); break;
+            case Op::kLog: r = logf(a); break;
+            case Op::kLog2: r = log2f(a); break;
+            case Op::kSqrt: r = sqrtf(a); break;
+            case Op::kInvSqrt: r = 1.f / sqrtf(a); break;
+            case Op::kAbs: r = fabsf(a); break;
+            case Op::kSign: r = (float)((a > 0.f) - (a < 0.f)); break;
+            case Op::kFloor: r = floorf(a); break;
+            case Op::kFract: r = a - floorf(a); break;
+            case Op::kMod: r = a - b * floorf(a / b); break;
+            case Op::kPow: r = powf(a, b); break;
+            case Op::kMax: r = std_max(a, b); break;
+            case Op::kMin: r = std_min(a, b); break;
+            case Op::kClamp: r = std_min(std_max(a, b), t); break;
+            case Op::kMix: r = a + (b - a) * t; break;
+            case Op::kStep: r = b < a ? 0.f : 1.f; break;
+            case Op::kSmoothStep: {
+                const float s = std_min(std_max((t - a) / (b - a), 0.f), 1.f);
+                r = s * s * (3.f - 2.f * s);
+                break;
+            }
+            case Op::kSigmoid: r = 1.f / (1.f + libc_expf(-a)); break;
+            case Op::kLess: r = (float)(a < b); break;
+            case Op::kLessEq: r = (float)(a <= b); break;
+            case Op::kGreater: r = (float)(a > b); break;
+            case Op::kGreaterEq: r = (float)(a >= b); break;
+            case Op::kCopy: r = a; break;
+            case Op::kSumPw: {
+                float acc = 0.f;
+                for (uint32_t i = 0; i < n_in; i++) {
+                    acc += v[i][c];
+                }
+                r = acc;
+                break;
+            }
+            default: break;
+        }
+        y[c] = r;
+    }
+}
+
+// One fused stage: every thread runs the program on its pixel.
+__global__ __launch_bounds__(256) void k_fused(FProgram P) {
+    const size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= P.n_px) {
+        return;
+    }
+    float reg[kMaxStepInstrs][4];
+    for (uint32_t i = 0; i < P.n; i++) {
+        const FInstr ins = P.code[i];
+        float v[kMaxInputs][4];
+        uint32_t nc[kMaxInputs];
+        for (uint32_t k = 0; k < ins.n_in; k++) {
+            const FInput in = ins.in[k];
+            nc[k] = in.nc;
+            const float* src = nullptr;
+            if (in.src == kSrcReg) {
+                src = reg[in.idx];
+            } else if (in.src == kSrcBuf) {
+                src = P.bufs[in.idx] + (in.uniform ? 0 : p * in.nc);
+            } else {
+                src = P.imm + in.idx;
+            }
+            for (uint32_t c = 0; c < 4; c++) {
+                v[k][c] = src[in.nc == 1 ? 0 : (c < in.nc ? c : 0)];
+            }
+        }
+        float y[4] = {0.f, 0.f, 0.f, 0.f};
+        ew_eval((Op)ins.op, ins.n_in, nc, v, ins.ny, ins.a0, y);
+        for (uint32_t c = 0; c < 4; c++) {
+            reg[i][c] = y[c];
+        }
+        if (ins.out_slot >= 0) {
+            float* dst = P.bufs[ins.out_slot] + p * ins.ny;
+            for (uint32_t c = 0; c < ins.ny; c++) {
+                dst[c] = y[c];
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(64) void k_fill(float* y, uint32_t n, float v0, float v1, float v2,
+                                             float v3) {
+    const uint32_t c = threadIdx.x;
+    if (c < n) {
+        y[c] = c == 0 ? v0 : c == 1 ? v1 : c == 2 ? v2 : v3;
+    }
+}
+
+// Reduce2x2Sum: each output pixel sums its 2x2 source block in row order
+// from 0 (the reference CPU kernel's accumulation order).
+__global__ __launch_bounds__(256) void k_reduce2x2(const float* x, uint32_t sw, uint32_t sh,
+                                                   uint32_t nc, uint32_t ow, uint32_t oh,
+                                                   float* y) {
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= ow * oh) {
+        return;
+    }
+    const uint32_t ox = q % ow, oy = q / ow;
+    for (uint32_t c = 0; c < nc; c++) {
+        float acc = 0.f;
+        for (uint32_t dy = 0; dy < 2; dy++) {
+            for (uint32_t dx = 0; dx < 2; dx++) {
+                const uint32_t sx = 2 * ox + dx, sy = 2 * oy + dy;
+                if (sx < sw && sy < sh) {
+                    acc += x[((size_t)sy * sw + sx) * nc + c];
+                }
+            }
+        }
+        y[(size_t)q * nc + c] = acc;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_upsample2x(const float* x, uint32_t sw, uint32_t nc,
+                                                    uint32_t ow, uint32_t oh, float* y) {
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= ow * oh) {
+        return;
+    }
+    const uint32_t ox = q % ow, oy = q / ow;
+    for (uint32_t c = 0; c < nc; c++) {
+        y[(size_t)q * nc + c] = x[((size_t)(oy / 2) * sw + ox / 2) * nc + c];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_screen_coord(uint32_t w, uint32_t h, float* y) {
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= w * h) {
+        return;
+    }
+    y[2 * (size_t)q + 0] = (float)(q % w) + 0.5f;
+    y[2 * (size_t)q + 1] = (float)(q / w) + 0.5f;
+}
+
+// SumAll (f_ops.cpp:1087-1149): above 256 pixels, 64 strided partial sums in
+// double (pixels p, p + 64, ..., components in order), each rounded to
+// float; then the double sum of those (or of every value) rounded once
+__global__ __launch_bounds__(64) void k_sum_all(const float* x, size_t n_px, uint32_t nc,
+                                                float* y) {
+    __shared__ float part[64];
+    const uint32_t t = threadIdx.x;
+    if (n_px > 256) {
+        double s = 0.0;
+        for (size_t i = t; i < n_px; i += 64) {
+            for (uint32_t c = 0; c < nc; c++) {
+                s += (double)x[i * nc + c];
+            }
+        }
+        part[t] = (float)s;
+        __syncthreads();
+        if (t == 0) {
+            double a = 0.0;
+            for (int k = 0; k < 64; k++) {
+                a += (double)part[k];
+            }
+            y[0] = (float)a;
+        }
+    } else if (t == 0) {
+        double a = 0.0;
+        for (size_t i = 0; i < n_px * nc; i++) {
+            a += (double)x[i];
+        }
+        y[0] = (float)a;
+    }
+}
+
+// PixelFetch / TileFetch (f_ops.cpp:1826-1888): row = uint(int64(v + 0.5))
+__global__ __launch_bounds__(64) void k_pixel_fetch(const float* tex, uint32_t w, uint32_t h,
+                                                    uint32_t nc, uint32_t x, const float* row,
+                                                    float* y, uint32_t* err) {
+    const uint32_t r = (uint32_t)(int64_t)(row[0] + 0.5f);
+    if (r >= h) {
+        if (threadIdx.x == 0) {
+            atomicOr(err, 0x200u);
+        }
+        return;
+    }
+    if (threadIdx.x < nc) {
+        y[threadIdx.x] = tex[((size_t)r * w + x) * nc + threadIdx.x];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_tile_fetch(const float* atlas, uint32_t w, uint32_t h,
+                                                    uint32_t nc, uint32_t tile_h,
+                                                    const float* idx, float* y, uint32_t* err) {
+    const size_t n = (size_t)w * tile_h * nc;
+    const uint32_t t = (uint32_t)(int64_t)(idx[0] + 0.5f);
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= n) {
+        return;
+    }
+    if (t >= h / tile_h) {
+        if (q == 0) {
+            atomicOr(err, 0x200u);
+        }
+        return;
+    }
+    y[q] = atlas[(size_t)t * n + q];
+}
+
+// Per-pixel matrix ops, column-major (f_ops.cpp:767-870)
+__global__ __launch_bounds__(256) void k_matrix(int op, const float* a, uint32_t a_uni,
+                                                const float* b, uint32_t b_uni, uint32_t dim,
+                                                uint32_t vec_rhs, size_t n_px, float* y) {
+    const size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= n_px) {
+        return;
+    }
+    const uint32_t dd = dim * dim;
+    if ((Op)op == Op::kMatMul) {
+        const float* m = a + (a_uni ? 0 : p * dd);
+        if (vec_rhs) {
+            const float* r = b + (b_uni ? 0 : p * dim);
+            for (uint32_t row = 0; row < dim; row++) {
+                float acc = 0.f;
+                for (uint32_t col = 0; col < dim; col++) {
+                    acc += m[col * dim + row] * r[col];
+                }
+                y[p * dim + row] = acc;
+            }
+        } else {
+            const float* r = b + (b_uni ? 0 : p * dd);
+            for (uint32_t col = 0; col < dim; col++) {
+                for (uint32_t row = 0; row < dim; row++) {
+                    float acc = 0.f;
+                    for (uint32_t k = 0; k < dim; k++) {
+                        acc += m[k * dim + row] * r[col * dim + k];
+                    }
+                    y[p * dd + col * dim + row] = acc;
+                }
+            }
+        }
+    } else if ((Op)op == Op::kTranspose) {
+        const float* m = a + (a_uni ? 0 : p * dd);
+        for (uint32_t col = 0; col < dim; col++) {
+            for (uint32_t row = 0; row < dim; row++) {
+                y[p * dd + col * dim + row] = m[row * dim + col];
+            }
+        }
+    } else {
+        const float* u = a + (a_uni ? 0 : p * dim);
+        const float* w = b + (b_uni ? 0 : p * dim);
+        for (uint32_t c = 0; c < dim; c++) {
+            for (uint32_t r = 0; r < dim; r++) {
+                y[p * dd + c * dim + r] = u[r] * w[c];
+            }
+        }
+    }
+}
+
+// VertexNeighborMean (f_ops.cpp:1983-2029)
+__global__ __launch_bounds__(256) void k_vertex_neighbor_mean(const float* pos, uint32_t nv,
+                                                              const float* adj, uint32_t deg,
+                                                              float* out, uint32_t* err) {
+    const uint32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= nv) {
+        return;
+    }
+    float mean[3] = {0.f, 0.f, 0.f};
+    uint32_t count = 0;
+    for (uint32_t d = 0; d < deg; d++) {
+        const float a = adj[(size_t)d * nv + v];
+        if (a < -0.5f) {
+            continue;
+        }
+        const size_t n = (size_t)(int64_t)(a + 0.5f);
+        if (n >= nv) {
+            atomicOr(err, 0x200u);
+            continue;
+        }
+        for (int c = 0; c < 3; c++) {
+            mean[c] += pos[n * 3 + c];
+        }
+        count++;
+    }
+    for (int c = 0; c < 3; c++) {
+        out[(size_t)v * 3 + c] = count > 0 ? mean[c] / (float)count : pos[(size_t)v * 3 + c];
+    }
+}
+
+// vertex ids of face f, false (error bit set) when one is out of range
+__device__ __forceinline__ bool face_ids(const float* faces, uint32_t f, uint32_t nv,
+                                         uint32_t idx[3], uint32_t* err) {
+    for (int k = 0; k < 3; k++) {
+        idx[k] = (uint32_t)(int64_t)(faces[(size_t)f * 3 + k] + 0.5f);
+        if (idx[k] >= nv) {
+            atomicOr(err, 0x200u);
+            return false;
+        }
+    }
+    return true;
+}
+
+__device__ __forceinline__ bool face_cross(const float* pos, uint32_t nv, const float* faces,
+                                           uint32_t f, float c[3], uint32_t* err) {
+    uint32_t idx[3];
+    if (!face_ids(faces, f, nv, idx, err)) {
+        c[0] = c[1] = c[2] = 0.f;
+        return false;
+    }
+    const float* p0 = pos + (size_t)idx[0] * 3;
+    const float* p1 = pos + (size_t)idx[1] * 3;
+    const float* p2 = pos + (size_t)idx[2] * 3;
+    const float e1[3] = {p1[0] - p0[0], p1[1] - p0[1], p1[2] - p0[2]};
+    const float e2[3] = {p2[0] - p0[0], p2[1] - p0[1], p2[2] - p0[2]};
+    c[0] = e1[1] * e2[2] - e1[2] * e2[1];
+    c[1] = e1[2] * e2[0] - e1[0] * e2[2];
+    c[2] = e1[0] * e2[1] - e1[1] * e2[0];
+    return true;
+}
+
+// NormalConsistencyFaceTerm (f_ops.cpp:2031-2098)
+__global__ __launch_bounds__(256) void k_nc_face_term(const float* pos, uint32_t nv,
+                                                      const float* faces, const float* fadj,
+                                                      uint32_t nf, float* out, uint32_t* err) {
+    const uint32_t f = blockIdx.x * blockDim.x + threadIdx.x;
+    if (f >= nf) {
+        return;
+    }
+    float g[3] = {0.f, 0.f, 0.f};
+    float ca[3];
+    face_cross(pos, nv, faces, f, ca, err);
+    const float la = sqrtf(ca[0] * ca[0] + ca[1] * ca[1] + ca[2] * ca[2]);
+    if (!(la < 1e-12f)) {
+        const float na[3] = {ca[0] / la, ca[1] / la, ca[2] / la};
+        for (int j = 0; j < 3; j++) {
+            const float gv = fadj[(size_t)f * 3 + j];
+            if (gv < -0.5f) {
+                continue;
+            }
+            const uint32_t fb = (uint32_t)(int64_t)(gv + 0.5f);
+            float cb[3];
+            if (fb >= nf) {
+                atomicOr(err, 0x200u);
+                continue;
+            }
+            face_cross(pos, nv, faces, fb, cb, err);
+            const float lb = sqrtf(cb[0] * cb[0] + cb[1] * cb[1] + cb[2] * cb[2]);
+            if (lb < 1e-12f) {
+                continue;
+            }
+            const float nb[3] = {cb[0] / lb, cb[1] / lb, cb[2] / lb};
+            const float d = na[0] * nb[0] + na[1] * nb[1] + na[2] * nb[2];
+            for (int c = 0; c < 3; c++) {
+                g[c] += -(nb[c] - d * na[c]) / la;
+            }
+        }
+    }
+    for (int c = 0; c < 3; c++) {
+        out[(size_t)f * 3 + c] = g[c];
+    }
+}
+
+// NormalConsistencyVertexGrad (f_ops.cpp:2100-2181)
+__global__ __launch_bounds__(256) void k_nc_vertex_grad(const float* term, const float* pos,
+                                                        const float* faces, uint32_t nf,
+                                                        const float* vf, uint32_t nv,
+                                                        uint32_t deg, float* out, uint32_t* err) {
+    const uint32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= nv) {
+        return;
+    }
+    float acc[3] = {0.f, 0.f, 0.f};
+    for (uint32_t d = 0; d < deg; d++) {
+        const float fv = vf[(size_t)d * nv + v];
+        if (fv < -0.5f) {
+            continue;
+        }
+        const uint32_t f = (uint32_t)(int64_t)(fv + 0.5f);
+        uint32_t idx[3];
+        if (f >= nf) {
+            atomicOr(err, 0x200u);
+            continue;
+        }
+        if (!face_ids(faces, f, nv, idx, err)) {
+            continue;
+        }
+        const float* p0 = pos + (size_t)idx[0] * 3;
+        const float* p1 = pos + (size_t)idx[1] * 3;
+        const float* p2 = pos + (size_t)idx[2] * 3;
+        const float e1[3] = {p1[0] - p0[0], p1[1] - p0[1], p1[2] - p0[2]};
+        const float e2[3] = {p2[0] - p0[0], p2[1] - p0[1], p2[2] - p0[2]};
+        const float* g = term + (size_t)f * 3;
+        const float g1[3] = {e2[1] * g[2] - e2[2] * g[1], e2[2] * g[0] - e2[0] * g[2],
+                             e2[0] * g[1] - e2[1] * g[0]};
+        const float g2[3] = {g[1] * e1[2] - g[2] * e1[1], g[2] * e1[0] - g[0] * e1[2],
+                             g[0] * e1[1] - g[1] * e1[0]};
+        for (int c = 0; c < 3; c++) {
+            if (idx[1] == v) {
+                acc[c] += g1[c];
+            }
+            if (idx[2] == v) {
+                acc[c] += g2[c];
+            }
+            if (idx[0] == v) {
+                acc[c] -= g1[c] + g2[c];
+            }
+        }
+    }
+    for (int c = 0; c < 3; c++) {
+        out[(size_t)v * 3 + c] = acc[c];
+    }
+}
+
+uint32_t blocks256(size_t n) { return (uint32_t)((n + 255) / 256); }
+
+size_t n_floats(const VariableNode& n) {
+    return (size_t)n.size.w * n.size.h * NumComponents(n.vtype);
+}
+
+}  // namespace
+
+// ---- the executor ------------------------------------------------------------------
+
+namespace {
+
+// One launch group of the iteration: a fused elementwise program or one
+// function through its kernel / entry point.
+struct Step {
+    bool fused = false;
+    std::vector<std::shared_ptr<FunctionNode>> fns;  // in order
+    // fused program (host copy, device copy)
+    std::vector<FInstr> code;
+    std::vector<float> imm;
+    std::vector<const VariableNode*> slots;  // slot -> variable (inputs and stored outputs)
+    FInstr* d_code = nullptr;
+    float* d_imm = nullptr;
+    float** d_bufs = nullptr;
+    size_t n_px = 0;
+    // the variables whose images this step writes
+    std::vector<const VariableNode*> outs;
+};
+
+}  // namespace
+
+struct DressiAD::Impl {
+    HipContextPtr hctx;
+    PackingMode packing = PackingMode::RSP;
+    InitStatus status = BACKWARD;
+    Variable loss{nullptr};
+    Optimizer optimizer;
+    Variables input_vars, input_grad_vars, updated_vars;
+    std::vector<std::pair<Variable, Variable>> copy_backs;  // (updated, input)
+    Functions all_funcs;
+    Variables leaf_vars;
+    Variables extra_outputs;
+    std::vector<std::pair<Variable, Variable>> extra_updates;  // (input, updated)
+    bool grad_outputs = false;
+    // reactive cache
+    uint32_t fast_count = 2, full_count = 8, static_cnt = 0;
+    std::set<uint64_t> prev_dirty;
+    bool pruning_active = false;
+    std::set<uint64_t> dynamic_ids;
+    // device state
+    std::unordered_map<const VariableNode*, float*> bufs;
+    std::unordered_set<const VariableNode*> computed;
+    std::vector<std::shared_ptr<VariableNode>> keep;  // owners of the buffer keys
+    std::vector<Step> packed, steps;
+    bool plan_valid = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    bool graph_failed = false;
+    uint32_t eager_runs = 0;
+    // transfers
+    std::map<Variable, CpuImage> pending;
+    std::vector<std::pair<Variable, CpuImageView>> batch_uploads;
+    Variables batch_downloads;
+    bool have_download = false;
+    CpuImage download;
+    // the fused silhouette plan, when the graph is recognised
+    std::unique_ptr<SilhouetteRoute> route;
+    bool route_rejected = false;
+    // This instance's own C-ABI context on the shared context's stream: its
+    // per-op workspaces are used by this instance only, so the device
+    // pointers a captured hipGraph holds stay valid whatever other
+    // instances on the shared context do.
+    dressi_ctx* ws = nullptr;
+
+    ~Impl() {
+        route.reset();
+        release_plan();
+        if (ws) {
+            dressi_ctx_synchronize(ws);
+            for (auto& [n, p] : bufs) {
+                dressi_free(ws, p);
+            }
+            dressi_ctx_destroy(ws);
+        }
+    }
+
+    dressi_ctx* ctx() {
+        ensure_ctx();
+        return ws;
+    }
+    hipStream_t stream() { return (hipStream_t)dressi_ctx_stream(ctx()); }
+
+    void ensure_ctx() {
+        if (!hctx) {
+            hctx = DressiAD::createContext();
+        }
+        if (!ws) {
+            check(dressi_ctx_create(hctx->device, &ws), "DressiAD context");
+            check(dressi_ctx_set_stream(ws, dressi_ctx_stream(hctx->ctx)), "DressiAD context");
+        }
+    }
+
+    void release_graph() {
+        if (graph_exec) {
+            hipGraphExecDestroy(graph_exec);
+            graph_exec = nullptr;
+        }
+        if (graph) {
+            hipGraphDestroy(graph);
+            graph = nullptr;
+        }
+    }
+
+    void release_steps(std::vector<Step>& v) {
+        for (auto& s : v) {
+            if (s.d_code) {
+                hipFree(s.d_code);
+                hipFree(s.d_imm);
+                hipFree(s.d_bufs);
+                s.d_code = nullptr;
+            }
+        }
+        v.clear();
+    }
+
+    void release_plan() {
+        release_graph();
+        if (ws) {
+            dressi_ctx_synchronize(ws);
+        }
+        release_steps(steps);
+        release_steps(packed);
+        plan_valid = false;
+    }
+
+    Variables roots() const {
+        Variables r = updated_vars;
+        r.push_back(loss);
+        for (const auto& v : extra_outputs) {
+            r.push_back(v);
+        }
+        for (const auto& [inp, upd] : extra_updates) {
+            r.push_back(upd);
+        }
+        if (grad_outputs) {
+            for (const auto& g : input_grad_vars) {
+                r.push_back(g);
+            }
+        }
+        return r;
+    }
+
+    std::set<uint64_t> dirty_leaf_ids() const {
+        std::set<uint64_t> ids;
+        for (const auto& v : leaf_vars) {
+            if (v.IsDirty()) {
+                ids.insert(v.id());
+            }
+        }
+        return ids;
+    }
+
+    // dirty leaves, the optimizer's parameters and the addUpdate targets:
+    // what changes this iteration (src/dressi_ad.cpp:101-118)
+    Variables dynamic_seeds() const {
+        Variables seeds;
+        for (const auto& v : leaf_vars) {
+            if (v.IsDirty()) {
+                seeds.push_back(v);
+            }
+        }
+        if (optimizer) {
+            for (const auto& v : input_vars) {
+                seeds.push_back(v);
+            }
+        }
+        for (const auto& [inp, upd] : extra_updates) {
+            seeds.push_back(inp);
+        }
+        return seeds;
+    }
+
+    bool has_cached(const VariableNode* n) const { return computed.count(n) != 0; }
+
+    float* buf(const std::shared_ptr<VariableNode>& n) {
+        auto it = bufs.find(n.get());
+        if (it != bufs.end()) {
+            return it->second;
+        }
+        void* p = nullptr;
+        const size_t bytes = std::max<size_t>(n_floats(*n), 1) * sizeof(float);
+        check(dressi_malloc(ctx(), &p, bytes), "device allocation");
+        check(dressi_memset(ctx(), p, 0, bytes), "device clear");
+        bufs[n.get()] = (float*)p;
+        keep.push_back(n);
+        return (float*)p;
+    }
+    float* buf(const Variable& v) { return buf(NodeAccess::Node(v)); }
+    bool has_buf(const Variable& v) const { return bufs.count(NodeAccess::Node(v).get()) != 0; }
+
+    // ---- packing -------------------------------------------------------------
+
+    // The demand filter of the reactive cache over functions
+    // (src/pack/reactive.cpp:38-68): creators reached from the roots,
+    // stopping at static variables whose images are computed.
+    Functions filter_funcs(const Functions& funcs) const {
+        std::unordered_set<uint64_t> needed, seen;
+        Variables stack = const_cast<Impl*>(this)->roots();
+        while (!stack.empty()) {
+            Variable v = stack.back();
+            stack.pop_back();
+            if (!v || !seen.insert(v.id()).second) {
+                continue;
+            }
+            Function c = v.getCreator();
+            if (!c) {
+                continue;
+            }
+            if (!dynamic_ids.count(v.id()) && has_cached(NodeAccess::Node(v).get())) {
+                continue;
+            }
+            if (needed.insert(c.id()).second) {
+                for (const auto& x : c.getInputVars()) {
+                    stack.push_back(x);
+                }
+            }
+        }
+        Functions out;
+        for (const auto& f : funcs) {
+            if (needed.count(f.id())) {
+                out.push_back(f);
+            }
+        }
+        return out;
+    }
+
+    // variables that must have an image: roots, copy-back sources and every
+    // input of a step other than the one that produces it
+    void pack(const Functions& funcs) {
+        release_graph();
+        release_steps(packed);
+        std::unordered_set<const VariableNode*> must_store;
+        for (const auto& r : roots()) {
+            if (r) {
+                must_store.insert(NodeAccess::Node(r).get());
+            }
+        }
+        std::vector<Step> out;
+        const bool fuse = packing == PackingMode::RSP;
+        for (const auto& f : funcs) {
+            const auto& fn = NodeAccess::Node(f);
+            const auto y = fn->y.lock();
+            const bool ew = IsElementwise(fn->op);
+            if (ew) {
+                DRESSI_CHECK(NumComponents(y->vtype) <= 4,
+                             fn->name + ": elementwise ops on matrix-typed images are not "
+                                        "supported by the HIP executor");
+            }
+            bool joined = false;
+            if (fuse && ew && !out.empty() && out.back().fused &&
+                out.back().fns.size() < (size_t)kMaxStepInstrs) {
+                const auto& prev = out.back().fns.back()->y.lock();
+                if (prev->size == y->size) {
+                    out.back().fns.push_back(fn);
+                    joined = true;
+                }
+            }
+            if (!joined) {
+                Step s;
+                s.fused = ew;
+                s.fns.push_back(fn);
+                out.push_back(std::move(s));
+            }
+        }
+        // which outputs leave their step
+        std::unordered_map<const VariableNode*, size_t> step_of;
+        for (size_t i = 0; i < out.size(); i++) {
+            for (const auto& fn : out[i].fns) {
+                step_of[fn->y.lock().get()] = i;
+            }
+        }
+        for (size_t i = 0; i < out.size(); i++) {
+            for (const auto& fn : out[i].fns) {
+                for (const auto& x : fn->xs) {
+                    if (out[i].fused && x->creator && x->creator->op == Op::kConst) {
+                        continue;  // an immediate of the fused program
+                    }
+                    auto it = step_of.find(x.get());
+                    if (it == step_of.end() || it->second != i) {
+                        must_store.insert(x.get());
+                    }
+                }
+            }
+        }
+        // constants only fused programs read need no step of their own
+        out.erase(std::remove_if(out.begin(), out.end(),
+                                 [&](const Step& st) {
+                                     return !st.fused && st.fns[0]->op == Op::kConst &&
+                                            !must_store.count(st.fns[0]->y.lock().get());
+                                 }),
+                  out.end());
+        for (auto& s : out) {
+            for (const auto& fn : s.fns) {
+                const auto y = fn->y.lock();
+                if (!s.fused || must_store.count(y.get())) {
+                    s.outs.push_back(y.get());
+                }
+            }
+        }
+        packed = std::move(out);
+        store_set = std::move(must_store);
+    }
+    std::unordered_set<const VariableNode*> store_set;
+
+    // step-level demand filter (src/pack/reactive.cpp:70-111): walking the
+    // steps backwards, keep a step iff a demanded image it writes is
+    // dynamic or not computed yet
+    void filter_steps() {
+        release_graph();
+        std::unordered_set<const VariableNode*> needed;
+        for (const auto& r : roots()) {
+            if (r) {
+                needed.insert(NodeAccess::Node(r).get());
+            }
+        }
+        std::vector<const Step*> kept;
+        for (auto it = packed.rbegin(); it != packed.rend(); ++it) {
+            bool run = false;
+            for (const VariableNode* o : it->outs) {
+                if (needed.count(o) && (dynamic_ids.count(o->id) || !has_cached(o))) {
+                    run = true;
+                    break;
+                }
+            }
+            if (!run) {
+                continue;
+            }
+            kept.push_back(&*it);
+            for (const auto& fn : it->fns) {
+                for (const auto& x : fn->xs) {
+                    needed.insert(x.get());
+                }
+            }
+        }
+        release_steps(steps);
+        for (auto it = kept.rbegin(); it != kept.rend(); ++it) {
+            Step s;
+            s.fused = (*it)->fused;
+            s.fns = (*it)->fns;
+            s.outs = (*it)->outs;
+            steps.push_back(std::move(s));
+        }
+    }
+
+    // device buffers and fused programs of the kept steps
+    void build_device_plan() {
+        for (const auto& f : all_funcs) {
+            const auto& fn = NodeAccess::Node(f);
+            for (const auto& x : fn->xs) {
+                if (!x->creator || store_set.count(x.get())) {
+                    buf(x);
+                }
+            }
+        }
+        for (auto& s : steps) {
+            for (const VariableNode* o : s.outs) {
+                for (const auto& fn : s.fns) {
+                    auto y = fn->y.lock();
+                    if (y.get() == o) {
+                        buf(y);
+                    }
+                }
+            }
+            if (s.fused) {
+                compile_fused(s);
+            }
+        }
+        for (const auto& [upd, inp] : copy_backs) {
+            buf(upd);
+            buf(inp);
+        }
+        for (const auto& v : leaf_vars) {
+            buf(v);
+        }
+        plan_valid = true;
+    }
+
+    void compile_fused(Step& s) {
+        std::unordered_map<const VariableNode*, uint32_t> reg_of, slot_of;
+        s.code.clear();
+        s.imm.clear();
+        s.slots.clear();
+        auto slot = [&](const VariableNode* v) {
+            auto it = slot_of.find(v);
+            if (it != slot_of.end()) {
+                return it->second;
+            }
+            const uint32_t k = (uint32_t)s.slots.size();
+            s.slots.push_back(v);
+            slot_of[v] = k;
+            return k;
+        };
+        for (uint32_t i = 0; i < s.fns.size(); i++) {
+            const auto& fn = s.fns[i];
+            const auto y = fn->y.lock();
+            FInstr ins{};
+            ins.op = (int)fn->op;
+            ins.n_in = (uint32_t)fn->xs.size();
+            if (ins.n_in > (uint32_t)kMaxInputs) {
+                throw DressiError(fn->name + ": more than 4 inputs in a fused stage");
+            }
+            ins.ny = NumComponents(y->vtype);
+            ins.a0 = fn->a0;
+            for (uint32_t k = 0; k < ins.n_in; k++) {
+                const auto& x = fn->xs[k];
+                FInput in{};
+                in.nc = NumComponents(x->vtype);
+                in.uniform = x->size.isUniform() ? 1u : 0u;
+                auto r = reg_of.find(x.get());
+                if (r != reg_of.end()) {
+                    in.src = kSrcReg;
+                    in.idx = r->second;
+                } else if (x->creator && x->creator->op == Op::kConst) {
+                    in.src = kSrcImm;
+                    in.idx = (uint32_t)s.imm.size();
+                    for (uint32_t c = 0; c < 4; c++) {
+                        s.imm.push_back(c < x->creator->cval.size() ? x->creator->cval[c] : 0.f);
+                    }
+                } else {
+                    in.src = kSrcBuf;
+                    in.idx = slot(x.get());
+                }
+                ins.in[k] = in;
+            }
+            ins.out_slot = std::find(s.outs.begin(), s.outs.end(), y.get()) != s.outs.end()
+                                   ? (int)slot(y.get())
+                                   : -1;
+            reg_of[y.get()] = i;
+            s.code.push_back(ins);
+            s.n_px = (size_t)y->size.w * y->size.h;
+        }
+        if (s.imm.empty()) {
+            s.imm.push_back(0.f);
+        }
+        std::vector<float*> ptrs;
+        for (const VariableNode* v : s.slots) {
+            auto it = bufs.find(v);
+            if (it == bufs.end()) {
+                throw DressiError("fused stage: an input has no device image");
+            }
+            ptrs.push_back(it->second);
+        }
+        if (ptrs.empty()) {
+            ptrs.push_back(nullptr);
+        }
+        check_hip(hipMalloc(&s.d_code, sizeof(FInstr) * s.code.size()), "fused program");
+        check_hip(hipMalloc(&s.d_imm, sizeof(float) * s.imm.size()), "fused program");
+        check_hip(hipMalloc(&s.d_bufs, sizeof(float*) * ptrs.size()), "fused program");
+        check_hip(hipMemcpy(s.d_code, s.code.data(), sizeof(FInstr) * s.code.size(),
+                            hipMemcpyHostToDevice),
+                  "fused program");
+        check_hip(hipMemcpy(s.d_imm, s.imm.data(), sizeof(float) * s.imm.size(),
+                            hipMemcpyHostToDevice),
+                  "fused program");
+        check_hip(hipMemcpy(s.d_bufs, ptrs.data(), sizeof(float*) * ptrs.size(),
+                            hipMemcpyHostToDevice),
+                  "fused program");
+    }
+
+    // ---- running ---------------------------------------------------------------
+
+    void run_step(const Step& s) {
+        hipStream_t st = stream();
+        if (s.fused) {
+            FProgram P{s.d_code, (uint32_t)s.code.size(), s.n_px, s.d_bufs, s.d_imm};
+            hipLaunchKernelGGL(k_fused, dim3(blocks256(s.n_px)), dim3(256), 0, st, P);
+            check_hip(hipGetLastError(), "fused stage launch");
+            return;
+        }
+        run_single(*s.fns[0]);
+    }
+
+    void run_single(const FunctionNode& fn) {
+        dressi_ctx* c = ctx();
+        hipStream_t s = stream();
+        const auto y = fn.y.lock();
+        float* out = buf(y);
+        const uint32_t ny = NumComponents(y->vtype);
+        const size_t n_px = (size_t)y->size.w * y->size.h;
+        std::vector<const float*> in;
+        std::vector<const VariableNode*> xn;
+        for (const auto& x : fn.xs) {
+            in.push_back(buf(x));
+            xn.push_back(x.get());
+        }
+        auto nc = [&](int i) { return NumComponents(xn[i]->vtype); };
+        auto w_of = [&](int i) { return xn[i]->size.w; };
+        auto h_of = [&](int i) { return xn[i]->size.h; };
+        uint32_t* err = nullptr;
+        switch (fn.op) {
+            case Op::kConst: {
+                const auto& v = fn.cval;
+                hipLaunchKernelGGL(k_fill, dim3(1), dim3(64), 0, s, out, (uint32_t)v.size(), v[0],
+                                   v.size() > 1 ? v[1] : 0.f, v.size() > 2 ? v[2] : 0.f,
+                                   v.size() > 3 ? v[3] : 0.f);
+                break;
+            }
+            case Op::kReduce2x2:
+                hipLaunchKernelGGL(k_reduce2x2, dim3(blocks256(n_px)), dim3(256), 0, s, in[0],
+                                   w_of(0), h_of(0), ny, y->size.w, y->size.h, out);
+                break;
+            case Op::kUpsample2x:
+                hipLaunchKernelGGL(k_upsample2x, dim3(blocks256(n_px)), dim3(256), 0, s, in[0],
+                                   w_of(0), ny, y->size.w, y->size.h, out);
+                break;
+            case Op::kScreenCoord:
+                hipLaunchKernelGGL(k_screen_coord, dim3(blocks256(n_px)), dim3(256), 0, s,
+                                   y->size.w, y->size.h, out);
+                break;
+            case Op::kSumAll:
+                hipLaunchKernelGGL(k_sum_all, dim3(1), dim3(64), 0, s, in[0],
+                                   (size_t)w_of(0) * h_of(0), nc(0), out);
+                break;
+            case Op::kPixelFetch:
+                err = c->d_err;
+                hipLaunchKernelGGL(k_pixel_fetch, dim3(1), dim3(64), 0, s, in[0], w_of(0), h_of(0),
+                                   nc(0), fn.a0, in[1], out, err);
+                break;
+            case Op::kTileFetch:
+                err = c->d_err;
+                hipLaunchKernelGGL(k_tile_fetch, dim3(blocks256(n_px * ny)), dim3(256), 0, s,
+                                   in[0], w_of(0), h_of(0), nc(0), fn.a0, in[1], out, err);
+                break;
+            case Op::kMatMul:
+            case Op::kTranspose:
+            case Op::kOuter:
+                hipLaunchKernelGGL(k_matrix, dim3(blocks256(n_px)), dim3(256), 0, s, (int)fn.op,
+                                   in[0], xn[0]->size.isUniform() ? 1u : 0u,
+                                   in.size() > 1 ? in[1] : in[0],
+                                   in.size() > 1 && xn[1]->size.isUniform() ? 1u : 0u, fn.a0,
+                                   fn.a1, n_px, out);
+                break;
+            case Op::kVertexNeighborMean:
+                DRESSI_CHECK(w_of(1) == w_of(0), "VertexNeighborMean: table width != vertices");
+                hipLaunchKernelGGL(k_vertex_neighbor_mean, dim3(blocks256(w_of(0))), dim3(256), 0,
+                                   s, in[0], w_of(0), in[1], h_of(1), out, c->d_err);
+                break;
+            case Op::kNcFaceTerm:
+                DRESSI_CHECK(w_of(2) == w_of(1), "NormalConsistencyFaceTerm: adjacency != faces");
+                hipLaunchKernelGGL(k_nc_face_term, dim3(blocks256(w_of(1))), dim3(256), 0, s,
+                                   in[0], w_of(0), in[1], in[2], w_of(1), out, c->d_err);
+                break;
+            case Op::kNcVertexGrad:
+                DRESSI_CHECK(w_of(0) == w_of(2) && w_of(3) == w_of(1),
+                             "NormalConsistencyVertexGrad: term / table sizes");
+                hipLaunchKernelGGL(k_nc_vertex_grad, dim3(blocks256(w_of(1))), dim3(256), 0, s,
+                                   in[0], in[1], in[2], w_of(2), in[3], w_of(1), h_of(3), out,
+                                   c->d_err);
+                break;
+            case Op::kRasterize:
+                check(dressi_rasterize(c, in[0], w_of(0), in[1], nc(1), in[2], w_of(2), y->size.w,
+                                       y->size.h, out),
+                      "Rasterize");
+                break;
+            case Op::kRasterizeFaceId:
+                check(dressi_rasterize_face_id(c, in[0], w_of(0), in[2], w_of(2), y->size.w,
+                                               y->size.h, out),
+                      "RasterizeFaceId");
+                break;
+            case Op::kSoftClip:
+                check(dressi_soft_clip(c, in[0], w_of(0), in[1], w_of(1), fn.a0, fn.a1, fn.f0, out),
+                      "SoftClip");
+                break;
+            case Op::kRasterizeSoft:
+                check(dressi_rasterize_soft(c, in[0], in[1], in[2], in[3], w_of(3), in[4], w_of(4),
+                                            fn.a0, fn.a1, fn.f0, fn.flag ? in[6] : nullptr, out),
+                      "RasterizeSoft");
+                break;
+            case Op::kLookupFaces:
+                check(dressi_lookup_faces(c, in[0], nc(0), w_of(0), in[1], w_of(1), fn.a0, out),
+                      "LookupFaces");
+                break;
+            case Op::kLookupFacesBwd:
+                check(dressi_lookup_faces_bwd(c, in[0], nc(0), in[1], w_of(1), in[2], w_of(2),
+                                              h_of(2), fn.a0, out),
+                      "LookupFacesBwd");
+                break;
+            case Op::kFaceFetch:
+                check(dressi_face_fetch(c, in[0], nc(0), w_of(0), in[1], w_of(1), h_of(1), out),
+                      "FaceFetch");
+                break;
+            case Op::kFaceFetchBwd:
+                check(dressi_face_fetch_bwd(c, in[0], nc(0), in[1], w_of(1), h_of(1), in[2], in[3],
+                                            in[4], w_of(2), in[5], fn.f0, fn.a0, out),
+                      "FaceFetchBwd");
+                break;
+            case Op::kGatherDistGrad:
+                check(dressi_gather_dist_grad(c, in[0], in[1], in[2], w_of(2), in[3], w_of(3),
+                                              in[4], h_of(4), fn.f0, fn.flag, w_of(1), h_of(1),
+                                              out),
+                      "GatherDistGrad");
+                break;
+            case Op::kColSum:
+                check(dressi_col_sum(c, in[0], nc(0), w_of(0), h_of(0), out), "ColSum");
+                break;
+            case Op::kAntiAlias:
+                check(dressi_antialias(c, in[0], nc(0), in[1], in[2], w_of(2), in[3], w_of(3),
+                                       w_of(0), h_of(0), out),
+                      "AntiAlias");
+                break;
+            case Op::kAaBwdImg:
+                check(dressi_antialias_bwd_img(c, in[0], nc(0), in[1], in[2], w_of(2), in[3],
+                                               w_of(3), w_of(0), h_of(0), out),
+                      "AntiAliasBwdImg");
+                break;
+            case Op::kAaBwdVtx:
+                check(dressi_antialias_bwd_vtx(c, in[0], in[1], nc(0), in[2], in[3], w_of(3), in[4],
+                                               w_of(4), in[5], h_of(5), in[6], fn.a0, fn.flag,
+                                               w_of(0), h_of(0), out),
+                      "AntiAliasBwdVtx");
+                break;
+            case Op::kTexture:
+                check(dressi_texture_nearest(c, in[0], w_of(0), h_of(0), nc(0), in[1], w_of(1),
+                                             h_of(1), out),
+                      "Texture");
+                break;
+            case Op::kGatherInvUv:
+                check(dressi_texture_nearest_bwd(c, in[0], nc(0), w_of(0), h_of(0), in[1], w_of(1),
+                                                 h_of(1), in[2], out),
+                      "GatherByInverseUV");
+                break;
+            case Op::kTextureBilinear:
+                check(dressi_texture_bilinear(c, in[0], w_of(0), h_of(0), nc(0), in[1], w_of(1),
+                                              h_of(1), out),
+                      "TextureBilinear");
+                break;
+            case Op::kGatherInvUvBilinear:
+                check(dressi_texture_bilinear_bwd(c, in[0], nc(0), w_of(0), h_of(0), in[1],
+                                                  w_of(1), h_of(1), in[2], out),
+                      "GatherByInverseUVBilinear");
+                break;
+            case Op::kEquirectSample:
+                check(dressi_equirect_sample(c, in[0], w_of(0), h_of(0), nc(0), in[1], w_of(1),
+                                             h_of(1), out),
+                      "EquirectSample");
+                break;
+            case Op::kEquirectSampleBwd:
+                check(dressi_equirect_sample_bwd(c, in[0], nc(0), in[1], w_of(1), h_of(1),
+                                                 y->size.w, y->size.h, out),
+                      "EquirectSampleBwd");
+                break;
+            case Op::kIrradianceConv:
+                check(dressi_irradiance_conv(c, in[0], w_of(0), h_of(0), nc(0), y->size.w,
+                                             y->size.h, out),
+                      "IrradianceConv");
+                break;
+            case Op::kIrradianceConvBwd:
+                check(dressi_irradiance_conv_bwd(c, in[0], w_of(0), h_of(0), nc(0), y->size.w,
+                                                 y->size.h, out),
+                      "IrradianceConvBwd");
+                break;
+            case Op::kPrefilterEnv:
+                check(dressi_prefilter_env(c, in[0], w_of(0), h_of(0), nc(0), y->size.w, y->size.h,
+                                           fn.f0, fn.a0, out),
+                      "PrefilterEnv");
+                break;
+            case Op::kPrefilterConv:
+                if (fn.flag) {  // the normaliser: a0 x a1 = the source size
+                    check(dressi_prefilter_conv_norm(c, y->size.w, y->size.h, fn.a0, fn.a1, fn.f0,
+                                                     out),
+                          "PrefilterConvNorm");
+                } else {
+                    check(dressi_prefilter_conv(c, in[0], w_of(0), h_of(0), nc(0), y->size.w,
+                                                y->size.h, fn.f0, in[1], out),
+                          "PrefilterConv");
+                }
+                break;
+            case Op::kPrefilterConvBwd:
+                check(dressi_prefilter_conv_bwd(c, in[0], w_of(0), h_of(0), nc(0), y->size.w,
+                                                y->size.h, fn.f0, in[1], out),
+                      "PrefilterConvBwd");
+                break;
+            case Op::kBrdfLut:
+                check(dressi_brdf_lut(c, y->size.w, y->size.h, fn.a0, out), "BrdfIntegrationLut");
+                break;
+            case Op::kCustom:
+                throw DressiError("a Function built from GLSL text (\"" + fn.name +
+                                  "\") cannot run on the HIP executor");
+            case Op::kSetFragDepth:
+            case Op::kPeelDepth:
+                throw DressiError(fn.name +
+                                  " belongs to a custom raster pass, which the HIP executor "
+                                  "does not run");
+            default:
+                throw DressiError(fn.name + ": no kernel");
+        }
+        check_hip(hipGetLastError(), "kernel launch");
+    }
+
+    void run_copy_backs() {
+        for (const auto& [upd, inp] : copy_backs) {
+            check_hip(hipMemcpyAsync(buf(inp), buf(upd),
+                                     n_floats(*NodeAccess::Node(inp)) * sizeof(float),
+                                     hipMemcpyDeviceToDevice, stream()),
+                      "copy-back");
+        }
+    }
+
+    void run_steps() {
+        for (const auto& s : steps) {
+            run_step(s);
+        }
+        run_copy_backs();
+    }
+
+    // One iteration on the device. The step sequence is captured into a
+    // hipGraph once it has run eagerly (so every per-op workspace exists),
+    // then replayed; a capture the runtime rejects falls back to eager runs.
+    // Ops whose entry points upload host tables synchronously: a step list
+    // holding one runs eagerly (a capture would record a copy from a
+    // temporary host buffer)
+    static bool capturable(Op op) {
+        switch (op) {
+            case Op::kIrradianceConv:
+            case Op::kIrradianceConvBwd:
+            case Op::kPrefilterConv:
+            case Op::kPrefilterConvBwd:
+            case Op::kPrefilterEnv:
+            case Op::kBrdfLut: return false;
+            default: return true;
+        }
+    }
+
+    bool steps_capturable() const {
+        for (const auto& s : steps) {
+            if (!s.fused && !capturable(s.fns[0]->op)) {
+                return false;
+            }
+        }
+        return true;
+    }
+
+    void execute() {
+        if (!graph_exec && !graph_failed && eager_runs >= 1 && !steps_capturable()) {
+            graph_failed = true;
+        }
+        if (!graph_exec && !graph_failed && eager_runs >= 1) {
+            hipStream_t s = stream();
+            if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+                bool ok = true;
+                try {
+                    run_steps();
+                } catch (const DressiError&) {
+                    ok = false;
+                }
+                hipGraph_t g = nullptr;
+                const hipError_t e = hipStreamEndCapture(s, &g);
+                if (ok && e == hipSuccess && g &&
+                    hipGraphInstantiate(&graph_exec, g, nullptr, nullptr, 0) == hipSuccess) {
+                    graph = g;
+                } else {
+                    if (g) {
+                        hipGraphDestroy(g);
+                    }
+                    graph_exec = nullptr;
+                    graph_failed = true;
+                    hipGetLastError();
+                }
+            } else {
+                graph_failed = true;
+                hipGetLastError();
+            }
+        }
+        if (graph_exec) {
+            check_hip(hipGraphLaunch(graph_exec, stream()), "graph launch");
+        } else {
+            run_steps();
+            eager_runs++;
+        }
+        for (const auto& s : steps) {
+            for (const VariableNode* o : s.outs) {
+                computed.insert(o);
+            }
+        }
+    }
+
+    // ---- the fused silhouette plan ------------------------------------------
+
+    // Hand the graph back to the generic executor: the route's leaf images
+    // (current optimiser state included) become pending sends.
+    void drop_route() {
+        std::map<Variable, CpuImage> back;
+        route->Export(&back);
+        for (auto& [var, img] : back) {
+            pending[var] = std::move(img);
+        }
+        route.reset();
+        route_rejected = true;
+        status = std::min(status, SUBSTAGE);
+    }
+
+    // One iteration on the fused plan; false when the graph went back to
+    // the generic executor
+    bool run_route() {
+        for (auto it = pending.begin(); it != pending.end();) {
+            if (!route->Accept(it->first, CpuImageView(it->second))) {
+                drop_route();
+                return false;
+            }
+            it = pending.erase(it);
+        }
+        for (const auto& [var, view] : batch_uploads) {
+            if (!route->Accept(var, view)) {
+                drop_route();
+                return false;
+            }
+        }
+        std::map<Variable, CpuImage> back;
+        if (!route->Step(ctx(), &back)) {
+            for (auto& [var, img] : back) {
+                pending[var] = std::move(img);
+            }
+            route.reset();
+            route_rejected = true;
+            status = std::min(status, SUBSTAGE);
+            return false;
+        }
+        if (!batch_downloads.empty()) {
+            download = stack(batch_downloads, [&](const Variable& v) { return route->Recv(v); });
+            have_download = true;
+        }
+        check(dressi_ctx_synchronize(ctx()), "execStep");
+        return true;
+    }
+
+    // ---- the generic executor ----------------------------------------------
+
+    void run_generic() {
+        if (status <= STAGE) {
+            dynamic_ids.clear();
+            for (const auto& s : dynamic_seeds()) {
+                dynamic_ids.insert(s.id());
+            }
+            for (const auto& f : all_funcs) {
+                for (const auto& x : f.getInputVars()) {
+                    if (dynamic_ids.count(x.id())) {
+                        dynamic_ids.insert(f.getOutputVar().id());
+                        break;
+                    }
+                }
+            }
+        }
+        bool fn_pruned = pruning_active;
+        if (status <= SUBSTAGE) {
+            const Functions exec = filter_funcs(all_funcs);
+            fn_pruned = exec.size() < all_funcs.size();
+            pack(exec);
+        }
+        if (status <= STAGE) {
+            filter_steps();
+            pruning_active = fn_pruned || steps.size() < packed.size();
+        }
+        if (status <= VULKAN) {
+            build_device_plan();
+            eager_runs = 0;
+            graph_failed = false;
+        }
+        // pending sends (images exist now), then this step's uploads
+        for (auto& [var, img] : pending) {
+            upload(var, CpuImageView(img));
+        }
+        pending.clear();
+        for (const auto& [var, view] : batch_uploads) {
+            upload(var, view);
+        }
+        execute();
+        if (!batch_downloads.empty()) {
+            download = stack(batch_downloads, [&](const Variable& v) {
+                DRESSI_CHECK(has_buf(v), "stacked recv: the Variable has no device image");
+                return download_of(v);
+            });
+            have_download = true;
+        }
+        check(dressi_ctx_synchronize(ctx()), "execStep");
+    }
+
+    // same-shape images stacked into one {w, h * n} image
+    template <typename Fetch>
+    static CpuImage stack(const Variables& vars, Fetch fetch) {
+        const ImgSize s0 = vars[0].getImgSize();
+        const uint32_t ch = NumComponents(vars[0].getVType());
+        CpuImage out(s0.w, s0.h * (uint32_t)vars.size(), ch);
+        size_t o = 0;
+        for (const auto& v : vars) {
+            DRESSI_CHECK(v.getImgSize() == s0 && NumComponents(v.getVType()) == ch,
+                         "stacked recv: images must share one size and type");
+            const CpuImage img = fetch(v);
+            std::copy(img.data.begin(), img.data.end(), out.data.begin() + (ptrdiff_t)o);
+            o += img.data.size();
+        }
+        return out;
+    }
+
+    // ---- transfers -------------------------------------------------------------
+
+    static void check_view(const Variable& var, const CpuImageView& v) {
+        DRESSI_CHECK(v.data || v.numElems() == 0, "sendImg: null data");
+        const ImgSize s = var.getImgSize();
+        DRESSI_CHECK(v.width == s.w && v.height == s.h,
+                     "sendImg: image size differs from the Variable's");
+        DRESSI_CHECK(v.channels == NumComponents(var.getVType()),
+                     "sendImg: channel count differs from the Variable's type");
+    }
+
+    void upload(const Variable& var, const CpuImageView& v) {
+        check(dressi_memcpy_h2d(ctx(), buf(var), v.data, v.numElems() * sizeof(float)),
+              "sendImg");
+        computed.insert(NodeAccess::Node(var).get());
+    }
+
+    CpuImage download_of(const Variable& var) {
+        const ImgSize s = var.getImgSize();
+        CpuImage img(s.w, s.h, NumComponents(var.getVType()));
+        check(dressi_memcpy_d2h(ctx(), img.data.data(), buf(var), img.data.size() * sizeof(float)),
+              "recvImg");
+        check(dressi_ctx_synchronize(ctx()), "recvImg");
+        return img;
+    }
+};
+
+DressiAD::DressiAD() : m_impl(std::make_unique<Impl>()) {}
+
+DressiAD::DressiAD(VkContextPtr ctx) : m_impl(std::make_unique<Impl>()) {
+    DRESSI_CHECK(ctx, "DressiAD: null context");
+    m_impl->hctx = std::move(ctx);
+}
+
+DressiAD::~DressiAD() = default;
+
+VkContextPtr DressiAD::createContext(bool debug) {
+    (void)debug;
+    return createContextOnDevice(0);
+}
+
+VkContextPtr DressiAD::createContextOnDevice(int device) {
+    auto c = std::make_shared<HipContext>();
+    c->device = device;
+    check(dressi_ctx_create(device, &c->ctx), "createContext");
+    return c;
+}
+
+void DressiAD::setLossVar(const Variable& loss_var) {
+    m_impl->loss = loss_var;
+    m_impl->status = BACKWARD;
+}
+
+void DressiAD::setOptimizer(const Optimizer& optim_func) {
+    m_impl->optimizer = optim_func;
+    m_impl->status = BACKWARD;
+}
+
+void DressiAD::setPackingMode(PackingMode mode) {
+    if (m_impl->packing != mode) {
+        m_impl->packing = mode;
+        if (m_impl->status > SUBSTAGE) {
+            m_impl->status = SUBSTAGE;
+        }
+    }
+}
+
+void DressiAD::setRebuildCounts(uint32_t fast, uint32_t full) {
+    m_impl->fast_count = fast;
+    m_impl->full_count = full;
+}
+
+void DressiAD::markOutput(const Variable& var) {
+    DRESSI_CHECK(var, "markOutput: null Variable");
+    m_impl->extra_outputs.push_back(var);
+    if (m_impl->status > TRAVERSE) {
+        m_impl->status = TRAVERSE;
+    }
+}
+
+void DressiAD::addUpdate(const Variable& input_leaf, const Variable& updated) {
+    DRESSI_CHECK(input_leaf && updated, "addUpdate: null Variable");
+    DRESSI_CHECK(!input_leaf.getCreator(), "addUpdate: input must be a leaf Variable");
+    DRESSI_CHECK(updated.getCreator(), "addUpdate: updated must be a computed Variable");
+    DRESSI_CHECK(input_leaf.getVType() == updated.getVType() &&
+                         input_leaf.getImgSize() == updated.getImgSize(),
+                 "addUpdate: updated must match the input's type and size");
+    m_impl->extra_updates.emplace_back(input_leaf, updated);
+    if (m_impl->status > OPTIMIZER) {
+        m_impl->status = OPTIMIZER;
+    }
+}
+
+void DressiAD::setGradOutputsEnabled(bool enable) {
+    if (m_impl->grad_outputs != enable) {
+        m_impl->grad_outputs = enable;
+        if (m_impl->status > TRAVERSE) {
+            m_impl->status = TRAVERSE;
+        }
+    }
+}
+
+std::vector<std::pair<Variable, Variable>> DressiAD::inputGrads() const {
+    std::vector<std::pair<Variable, Variable>> r;
+    for (size_t i = 0; i < m_impl->input_vars.size(); i++) {
+        r.emplace_back(m_impl->input_vars[i], m_impl->input_grad_vars[i]);
+    }
+    return r;
+}
+
+size_t DressiAD::getFuncCount() const { return m_impl->all_funcs.size(); }
+
+size_t DressiAD::getStageCount() const {
+    if (m_impl->route) {
+        return 1;
+    }
+    return m_impl->steps.size();
+}
+
+size_t DressiAD::getSubStageCount() const {
+    if (m_impl->route) {
+        return m_impl->route->kernels();
+    }
+    size_t n = 0;
+    for (const auto& s : m_impl->steps) {
+        n += s.fns.size();
+    }
+    return n;
+}
+
+std::string DressiAD::getDeviceName() const {
+    if (!m_impl->hctx) {
+        return {};
+    }
+    char b[256];
+    check(dressi_ctx_device_name(m_impl->hctx->ctx, b, sizeof(b)), "getDeviceName");
+    return b;
+}
+
+std::string DressiAD::getPlanName() const {
+    return m_impl->route ? m_impl->route->name() : std::string("generic");
+}
+
+dressi_ctx* DressiAD::context() const { return m_impl->ctx(); }
+
+void DressiAD::execStep() {
+    Impl& im = *m_impl;
+    DRESSI_CHECK(im.loss, "setLossVar() must be called before execStep()");
+    im.ensure_ctx();
+    // reactive cache: the dirty pattern of the data leaves
+    if (im.status == FINISHED) {
+        const std::set<uint64_t> cur = im.dirty_leaf_ids();
+        if (cur != im.prev_dirty) {
+            im.static_cnt = 0;
+            if (im.pruning_active) {
+                im.status = SUBSTAGE;
+            }
+        } else {
+            im.static_cnt++;
+            if (im.fast_count != 0 && im.static_cnt == im.fast_count) {
+                im.status = STAGE;
+            } else if (im.full_count != 0 && im.static_cnt == im.full_count) {
+                im.status = SUBSTAGE;
+            }
+        }
+        im.prev_dirty = cur;
+    }
+    if (im.status <= BACKWARD) {
+        std::tie(im.input_vars, im.input_grad_vars) = BuildBackward(im.loss);
+        im.route_rejected = false;
+    }
+    if (im.status <= OPTIMIZER) {
+        im.updated_vars.clear();
+        im.copy_backs.clear();
+        if (im.optimizer) {
+            im.updated_vars = im.optimizer(im.input_vars, im.input_grad_vars);
+            DRESSI_CHECK(im.updated_vars.size() == im.input_vars.size(),
+                         "Optimizer must return one output per input");
+            for (size_t i = 0; i < im.updated_vars.size(); i++) {
+                const Variable& u = im.updated_vars[i];
+                const Variable& x = im.input_vars[i];
+                DRESSI_CHECK(u.getVType() == x.getVType() && u.getImgSize() == x.getImgSize(),
+                             "Optimizer output must match its input's type and size");
+                im.copy_backs.emplace_back(u, x);
+            }
+        }
+        // addUpdate pairs persist across rebuilds (typically registered
+        // once from inside the optimizer)
+        for (const auto& [inp, upd] : im.extra_updates) {
+            im.copy_backs.emplace_back(upd, inp);
+        }
+    }
+    if (im.status <= TRAVERSE) {
+        im.all_funcs = TraverseFuncs(im.roots());
+        im.leaf_vars.clear();
+        std::set<uint64_t> seen;
+        for (const auto& f : im.all_funcs) {
+            for (const auto& x : f.getInputVars()) {
+                if (!x.getCreator() && seen.insert(x.id()).second) {
+                    im.leaf_vars.push_back(x);
+                }
+            }
+        }
+        for (const auto& [upd, inp] : im.copy_backs) {
+            if (seen.insert(inp.id()).second) {
+                im.leaf_vars.push_back(inp);
+            }
+        }
+        // the fused silhouette plan, when the graph is the example's
+        if (im.route) {
+            im.drop_route();
+        }
+        if (im.packing == PackingMode::RSP && !im.route_rejected) {
+            GraphRoots g;
+            g.loss = im.loss;
+            g.input_vars = im.input_vars;
+            g.input_grad_vars = im.input_grad_vars;
+            g.updated_vars = im.updated_vars;
+            g.extra_updates = im.extra_updates;
+            g.extra_outputs = im.extra_outputs;
+            g.grad_outputs = im.grad_outputs;
+            g.funcs = &im.all_funcs;
+            im.route = SilhouetteRoute::Recognise(g);
+        }
+    }
+    bool routed = false;
+    if (im.route) {
+        routed = im.run_route();
+    }
+    if (!routed) {
+        im.run_generic();
+    }
+    if (im.status != FINISHED) {
+        im.prev_dirty = im.dirty_leaf_ids();
+    }
+    for (auto& v : im.leaf_vars) {
+        v.setDirtyRecursively(false);
+    }
+    im.status = FINISHED;
+}
+
+void DressiAD::execStepWithSends(const std::vector<std::pair<Variable, CpuImageView>>& items) {
+    Impl& im = *m_impl;
+    im.batch_uploads.clear();
+    for (const auto& [var, view] : items) {
+        DRESSI_CHECK(var, "execStepWithSends: null Variable");
+        Impl::check_view(var, view);
+        Variable v = var;
+        v.setDirty(true);
+        if (im.plan_valid || im.route) {
+            im.batch_uploads.emplace_back(var, view);
+        } else {
+            CpuImage owned(view.width, view.height, view.channels);
+            std::copy(view.data, view.data + view.numElems(), owned.data.begin());
+            im.pending[var] = std::move(owned);
+        }
+    }
+    try {
+        execStep();
+    } catch (...) {
+        im.batch_uploads.clear();
+        throw;
+    }
+    im.batch_uploads.clear();
+}
+
+CpuImage DressiAD::execStepWithSendsAndRecvImgsStacked(
+        const std::vector<std::pair<Variable, CpuImageView>>& sends, const Variables& recvs) {
+    Impl& im = *m_impl;
+    DRESSI_CHECK(!recvs.empty(), "execStepWithSendsAndRecvImgsStacked: empty recv batch");
+    im.batch_downloads = recvs;
+    im.have_download = false;
+    try {
+        execStepWithSends(sends);
+    } catch (...) {
+        im.batch_downloads.clear();
+        throw;
+    }
+    im.batch_downloads.clear();
+    DRESSI_CHECK(im.have_download, "combined recv did not produce an image");
+    im.have_download = false;
+    return std::move(im.download);
+}
+
+void DressiAD::sendImg(const Variable& var, const CpuImage& cpu_img) {
+    sendImg(var, CpuImageView(cpu_img));
+}
+
+void DressiAD::sendImg(const Variable& var, const CpuImageView& cpu_img) {
+    Impl& im = *m_impl;
+    DRESSI_CHECK(var, "sendImg: null Variable");
+    Impl::check_view(var, cpu_img);
+    Variable v = var;
+    v.setDirty(true);
+    if (im.route) {
+        if (im.route->Accept(var, cpu_img)) {
+            return;
+        }
+        // an image for a variable the plan computes: the generic executor
+        // takes the graph over
+        im.drop_route();
+    }
+    if (im.plan_valid && im.has_buf(var)) {
+        im.upload(var, cpu_img);
+        return;
+    }
+    CpuImage owned(cpu_img.width, cpu_img.height, cpu_img.channels);
+    std::copy(cpu_img.data, cpu_img.data + cpu_img.numElems(), owned.data.begin());
+    im.pending[var] = std::move(owned);
+}
+
+void DressiAD::sendImgs(const std::vector<std::pair<Variable, CpuImageView>>& items) {
+    for (const auto& [var, view] : items) {
+        sendImg(var, view);
+    }
+}
+
+CpuImage DressiAD::recvImg(const Variable& var) {
+    Impl& im = *m_impl;
+    DRESSI_CHECK(var, "recvImg: null Variable");
+    auto it = im.pending.find(var);
+    if (it != im.pending.end()) {
+        return it->second;
+    }
+    if (im.route) {
+        return im.route->Recv(var);
+    }
+    DRESSI_CHECK(im.plan_valid, "recvImg before the first execStep()");
+    DRESSI_CHECK(im.has_buf(var),
+                 "recvImg: the Variable has no device image (markOutput it before execStep)");
+    return im.download_of(var);
+}
+
+std::vector<CpuImage> DressiAD::recvImgs(const Variables& vars) {
+    std::vector<CpuImage> out;
+    for (const auto& v : vars) {
+        out.push_back(recvImg(v));
+    }
+    return out;
+}
+
+CpuImage DressiAD::recvImgsStacked(const Variables& vars) {
+    DRESSI_CHECK(!vars.empty(), "recvImgsStacked: empty batch");
+    std::vector<CpuImage> imgs = recvImgs(vars);
+    CpuImage out(imgs[0].width, imgs[0].height * (uint32_t)imgs.size(), imgs[0].channels);
+    size_t o = 0;
+    for (const auto& im : imgs) {
+        DRESSI_CHECK(im.width == imgs[0].width && im.height == imgs[0].height &&
+                             im.channels == imgs[0].channels,
+                     "recvImgsStacked: images must share one size and type");
+        std::copy(im.data.begin(), im.data.end(), out.data.begin() + (ptrdiff_t)o);
+        o += im.data.size();
+    }
+    return out;
+}
+
+}  // namespace dressi

@@ -1,74 +1,38 @@
-// graph.hip -- the Dressi-AD graph API (include/dressi_graph.h): graph IR,
-// reverse-mode construction, and an executor that runs any graph of the
-// path's ops on one HIP device.
+// graph.hip -- the Dressi-AD graph API (include/dressi/*.h): graph IR,
+// the F:: op catalogue with each op's backward builder, BuildBackward and
+// TraverseFuncs. Host code; the executor (DressiAD) is executor.hip.
 //
 // IR (include/dressi/variable.h, function.h, src/core/node.h:42-65): a
 // Variable is a shared handle to a node holding its type, image size,
 // creator and (weak) users; a Function holds its op, inputs, (weak) output,
 // attributes and backward builder. Ids come from one counter, so creation
-// order is a topological order.
-//
-// Executor: the functions reachable from the roots are evaluated in id
-// order, each into its own device buffer: elementwise ops by one generic
-// kernel launch per node (the reference CPU evaluator's per-op float
-// semantics, src/core/op_builder.cpp:25-108), the raster / gather ops by the
-// library's per-op entry points. After evaluation each update value is
-// copied into its leaf (DressiAD's end-of-frame copy-back,
-// src/dressi_ad.cpp:317-341).
-#include <hip/hip_runtime.h>
-
+// order is a topological order, and the backward graph's summation order
+// follows the reference's (node creation order is part of the numbers).
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <map>
 #include <queue>
-#include <unordered_map>
+#include <sstream>
 #include <unordered_set>
 
-#include "dressi_graph.h"
-#include "dressi_math.h"
+#include "graph_ir.h"
 
 namespace dressi {
 
 namespace {
 
-enum class Op : int {
-    kConst,
-    kAdd, kSub, kMul, kDiv, kNeg, kSqrt, kAbs, kSign, kExp, kLog, kPow,
-    kMax, kMin, kClamp, kStep, kSigmoid, kLess, kLessEq, kGreater, kGreaterEq,
-    kExtract, kCompose, kDot, kCompSum, kCopy, kSumPw,
-    kReduce2x2, kUpsample2x, kScreenCoord,
-    kRasterize, kRasterizeFaceId, kSoftClip, kRasterizeSoft, kLookupFaces, kLookupFacesBwd,
-    kFaceFetch, kFaceFetchBwd, kGatherDistGrad, kColSum, kAntiAlias, kAaBwdImg, kAaBwdVtx,
-};
+std::atomic<uint64_t> g_next_id{1};
 
-uint64_t g_next_id = 1;
+uint64_t next_id() { return g_next_id.fetch_add(1); }
 
 }  // namespace
 
-using BwdFn = std::function<Variable(const Variables& xs, const Variable& y, const Variable& gy,
-                                     uint32_t idx)>;
-
-struct VariableNode {
-    uint64_t id = 0;
-    VType vtype = FLOAT;
-    ImgSize size;
-    std::shared_ptr<FunctionNode> creator;
-    std::vector<std::weak_ptr<FunctionNode>> users;
-    bool req_grad = false;
-};
-
-struct FunctionNode {
-    uint64_t id = 0;
-    Op op = Op::kConst;
-    std::string name;
-    std::vector<std::shared_ptr<VariableNode>> xs;
-    std::weak_ptr<VariableNode> y;
-    BwdFn bwd;
-    std::vector<float> cval;  // constants
-    uint32_t a0 = 0, a1 = 0;  // component offset / corner / sample count
-    float f0 = 0.f;           // radius
-    int flag = 0;             // wide gather / peel input present
-};
+void ThrowDressiError(const std::string& msg, const char* file, int line) {
+    std::ostringstream os;
+    os << msg << " (" << file << ":" << line << ")";
+    throw DressiError(os.str());
+}
 
 uint32_t NumComponents(VType t) {
     switch (t) {
@@ -76,13 +40,63 @@ uint32_t NumComponents(VType t) {
         case VEC2: return 2;
         case VEC3: return 3;
         case VEC4: return 4;
+        case MAT2: return 4;
+        case MAT3: return 9;
+        case MAT4: return 16;
+        case INT: return 1;
+        case IVEC2: return 2;
         case IVEC3: return 3;
+        case IVEC4: return 4;
+        case UINT: return 1;
     }
-    return 1;
+    DRESSI_CHECK(false, "unknown VType");
+}
+bool IsIntVType(VType t) { return t == INT || t == IVEC2 || t == IVEC3 || t == IVEC4 || t == UINT; }
+bool IsMatrixVType(VType t) { return t == MAT2 || t == MAT3 || t == MAT4; }
+bool IsVectorVType(VType t) {
+    return t == VEC2 || t == VEC3 || t == VEC4 || t == IVEC2 || t == IVEC3 || t == IVEC4;
+}
+const char* GlslTypeName(VType t) {
+    switch (t) {
+        case FLOAT: return "float";
+        case VEC2: return "vec2";
+        case VEC3: return "vec3";
+        case VEC4: return "vec4";
+        case MAT2: return "mat2";
+        case MAT3: return "mat3";
+        case MAT4: return "mat4";
+        case INT: return "int";
+        case IVEC2: return "ivec2";
+        case IVEC3: return "ivec3";
+        case IVEC4: return "ivec4";
+        case UINT: return "uint";
+    }
+    return "float";
+}
+VType VecVTypeOf(uint32_t n, bool is_int) {
+    DRESSI_CHECK(n >= 1 && n <= 4, "VecVTypeOf: 1..4 components");
+    if (is_int) {
+        return n == 1 ? INT : n == 2 ? IVEC2 : n == 3 ? IVEC3 : IVEC4;
+    }
+    return n == 1 ? FLOAT : n == 2 ? VEC2 : n == 3 ? VEC3 : VEC4;
 }
 
-static VType vec_of(uint32_t n) {
-    return n == 1 ? FLOAT : n == 2 ? VEC2 : n == 3 ? VEC3 : VEC4;
+bool IsElementwise(Op op) {
+    switch (op) {
+        case Op::kAdd: case Op::kSub: case Op::kMul: case Op::kDiv: case Op::kNeg:
+        case Op::kSin: case Op::kCos: case Op::kTan: case Op::kAsin: case Op::kAcos:
+        case Op::kAtan: case Op::kAtan2: case Op::kExp: case Op::kExp2: case Op::kLog:
+        case Op::kLog2: case Op::kSqrt: case Op::kInvSqrt: case Op::kAbs: case Op::kSign:
+        case Op::kFloor: case Op::kFract: case Op::kMod: case Op::kPow: case Op::kMax:
+        case Op::kMin: case Op::kClamp: case Op::kMix: case Op::kStep: case Op::kSmoothStep:
+        case Op::kSigmoid: case Op::kLess: case Op::kLessEq: case Op::kGreater:
+        case Op::kGreaterEq: case Op::kExtract: case Op::kCompose: case Op::kDot:
+        case Op::kCompSum: case Op::kCross: case Op::kCopy: case Op::kSumPw:
+        case Op::kLength: case Op::kNormalize:
+            return true;
+        default:
+            return false;
+    }
 }
 
 static void require(bool ok, const std::string& msg) {
@@ -91,33 +105,47 @@ static void require(bool ok, const std::string& msg) {
     }
 }
 
-// ---- Variable / Function ---------------------------------------------------
+// ---- Variable / Function ------------------------------------------------------
 
 Variable::Variable(VType vtype, ImgSize img_size) : m_node(std::make_shared<VariableNode>()) {
-    m_node->id = g_next_id++;
+    m_node->id = next_id();
     m_node->vtype = vtype;
     m_node->size = img_size;
 }
-bool Variable::operator<(const Variable& o) const {
-    return (m_node ? m_node->id : 0) < (o.m_node ? o.m_node->id : 0);
-}
 uint64_t Variable::id() const { return m_node->id; }
 VType Variable::getVType() const { return m_node->vtype; }
+void Variable::setVType(VType t) { m_node->vtype = t; }
 ImgSize Variable::getImgSize() const { return m_node->size; }
-Function Variable::getCreator() const { return Function(m_node->creator); }
+void Variable::setImgSize(ImgSize s) { m_node->size = s; }
+Function Variable::getCreator() const { return NodeAccess::Wrap(m_node->creator); }
+void Variable::setCreator(const Function& creator) { m_node->creator = NodeAccess::Node(creator); }
+std::vector<Function> Variable::getUsers() const {
+    std::vector<Function> out;
+    for (const auto& w : m_node->users) {
+        if (auto u = w.lock()) {
+            out.push_back(NodeAccess::Wrap(u));
+        }
+    }
+    return out;
+}
+void Variable::addUser(const Function& user) { m_node->users.push_back(NodeAccess::Node(user)); }
 bool Variable::getRequiresGrad() const { return m_node->req_grad; }
 void Variable::setRequiresGrad(bool r) { m_node->req_grad = r; }
-void Variable::setRequiresGradRecursively(bool r) {
-    // this variable and everything computed downstream of it
+bool Variable::IsDirty() const { return m_node->dirty; }
+void Variable::setDirty(bool d) { m_node->dirty = d; }
+
+// `n` and everything computed downstream of it (through the users)
+template <typename Fn>
+static void for_downstream(const std::shared_ptr<VariableNode>& start, Fn&& fn) {
     std::unordered_set<const VariableNode*> seen;
-    std::vector<std::shared_ptr<VariableNode>> stack = {m_node};
+    std::vector<std::shared_ptr<VariableNode>> stack = {start};
     while (!stack.empty()) {
         auto n = stack.back();
         stack.pop_back();
         if (!n || !seen.insert(n.get()).second) {
             continue;
         }
-        n->req_grad = r;
+        fn(*n);
         for (const auto& wu : n->users) {
             if (auto u = wu.lock()) {
                 if (auto y = u->y.lock()) {
@@ -127,17 +155,32 @@ void Variable::setRequiresGradRecursively(bool r) {
         }
     }
 }
+void Variable::setRequiresGradRecursively(bool r) {
+    for_downstream(m_node, [r](VariableNode& n) { n.req_grad = r; });
+}
+void Variable::setDirtyRecursively(bool d) {
+    for_downstream(m_node, [d](VariableNode& n) { n.dirty = d; });
+}
 
+Function::Function(const std::string& code, ShaderType type, const BwdFunc& bwd_func)
+    : m_node(std::make_shared<FunctionNode>()) {
+    m_node->id = next_id();
+    m_node->op = Op::kCustom;
+    m_node->name = code;
+    m_node->shader = type;
+    m_node->bwd = bwd_func;
+}
 uint64_t Function::id() const { return m_node->id; }
-const std::string& Function::name() const { return m_node->name; }
+std::string Function::getFwdCode() const { return m_node->name; }
+ShaderType Function::getShaderType() const { return m_node->shader; }
 Variables Function::getInputVars() const {
     Variables v;
     for (const auto& x : m_node->xs) {
-        v.emplace_back(x);
+        v.push_back(NodeAccess::Wrap(x));
     }
     return v;
 }
-Variable Function::getOutputVar() const { return Variable(m_node->y.lock()); }
+Variable Function::getOutputVar() const { return NodeAccess::Wrap(m_node->y.lock()); }
 Variable Function::buildBwd(const Variable& gy, uint32_t idx) const {
     if (!m_node->bwd) {
         return nullptr;
@@ -179,13 +222,13 @@ struct OpSpec {
     const char* name;
     VType vtype;
     ImgSize size;
-    BwdFn bwd;
+    BwdFunc bwd;
 };
 
 Variable make_op(const OpSpec& s, const Variables& xs, std::vector<float> cval = {},
                  uint32_t a0 = 0, uint32_t a1 = 0, float f0 = 0.f, int flag = 0) {
     auto fn = std::make_shared<FunctionNode>();
-    fn->id = g_next_id++;
+    fn->id = next_id();
     fn->op = s.op;
     fn->name = s.name;
     fn->bwd = s.bwd;
@@ -196,30 +239,30 @@ Variable make_op(const OpSpec& s, const Variables& xs, std::vector<float> cval =
     fn->flag = flag;
     for (const auto& x : xs) {
         require((bool)x, std::string(s.name) + ": null input");
-        fn->xs.push_back(x.node());
-        x.node()->users.push_back(fn);
+        fn->xs.push_back(NodeAccess::Node(x));
+        NodeAccess::Node(x)->users.push_back(fn);
     }
     auto y = std::make_shared<VariableNode>();
-    y->id = g_next_id++;
+    y->id = next_id();
     y->vtype = s.vtype;
     y->size = s.size;
     y->creator = fn;
     fn->y = y;
-    return Variable(y);
+    return NodeAccess::Wrap(y);
 }
 
-Variable ew(Op op, const char* name, const Variables& xs, BwdFn bwd) {
+Variable ew(Op op, const char* name, const Variables& xs, BwdFunc bwd) {
     return make_op({op, name, widest(xs), common_size(xs), std::move(bwd)}, xs);
 }
 
-Variable ew_fixed(Op op, const char* name, VType t, const Variables& xs, BwdFn bwd) {
+Variable ew_fixed(Op op, const char* name, VType t, const Variables& xs, BwdFunc bwd) {
     return make_op({op, name, t, common_size(xs), std::move(bwd)}, xs);
 }
 
-const BwdFn kNull = nullptr;
+const BwdFunc kNull = nullptr;
 
 Variable const_vec(const char* name, std::vector<float> v) {
-    const VType t = vec_of((uint32_t)v.size());
+    const VType t = VecVTypeOf((uint32_t)v.size());
     return make_op({Op::kConst, name, t, {1, 1}, kNull}, {}, std::move(v));
 }
 
@@ -234,7 +277,7 @@ Variable compose(const Variables& parts) {
         total += widths.back();
     }
     require(total >= 2 && total <= 4, "Compose: 2..4 components");
-    return make_op({Op::kCompose, "Compose", vec_of(total), common_size(parts),
+    return make_op({Op::kCompose, "Compose", VecVTypeOf(total), common_size(parts),
                     [offs, widths](const Variables&, const Variable&, const Variable& gy,
                                    uint32_t i) { return extract(gy, offs[i], widths[i]); }},
                    parts);
@@ -250,7 +293,7 @@ Variable extract(const Variable& v, uint32_t ofs, uint32_t n) {
     if (n == src_n) {
         return v;
     }
-    return make_op({Op::kExtract, "ExtractComps", vec_of(n), v.getImgSize(),
+    return make_op({Op::kExtract, "ExtractComps", VecVTypeOf(n), v.getImgSize(),
                     [ofs, n, src_n](const Variables&, const Variable&, const Variable& gy,
                                     uint32_t) {
                         Variables parts;
@@ -268,7 +311,7 @@ Variable extract(const Variable& v, uint32_t ofs, uint32_t n) {
 
 Variable unary(Op op, const char* name, const Variable& x,
                std::function<Variable(const Variable& x, const Variable& y)> dydx) {
-    BwdFn b = nullptr;
+    BwdFunc b = nullptr;
     if (dydx) {
         b = [dydx](const Variables& xs, const Variable& y, const Variable& gy, uint32_t) {
             return F::Mul(gy, dydx(xs[0], y));
@@ -315,9 +358,37 @@ Variable special(Op op, const char* name, VType t, ImgSize size, const Variables
     return make_op({op, name, t, size, kNull}, xs, {}, a0, a1, f0, flag);
 }
 
+void require_float_image(const Variable& v, const char* what) {
+    require(!IsIntVType(v.getVType()) && !IsMatrixVType(v.getVType()),
+            std::string(what) + " must be a float image");
+}
+
+uint32_t mat_dim(VType t) { return t == MAT2 ? 2 : t == MAT3 ? 3 : 4; }
+
 }  // namespace
 
-// ---- F:: ---------------------------------------------------------------------
+bool IsInlineConst(const Variable& v) {
+    const auto& c = NodeAccess::Node(v)->creator;
+    return c && c->op == Op::kConst;
+}
+
+Variable Function::buildFwd(const Variables& xs) {
+    require(m_node->xs.empty() && !m_node->y.lock(), "buildFwd: the function is already connected");
+    for (const auto& x : xs) {
+        require((bool)x, "buildFwd: null input");
+        m_node->xs.push_back(NodeAccess::Node(x));
+        NodeAccess::Node(x)->users.push_back(m_node);
+    }
+    auto y = std::make_shared<VariableNode>();
+    y->id = next_id();
+    y->vtype = xs.empty() ? FLOAT : widest(xs);
+    y->size = xs.empty() ? ImgSize{} : common_size(xs);
+    y->creator = m_node;
+    m_node->y = y;
+    return NodeAccess::Wrap(y);
+}
+
+// ---- F:: ------------------------------------------------------------------------
 
 namespace F {
 
@@ -357,20 +428,87 @@ Variable Neg(const Variable& x) {
                   return Neg(gy);
               });
 }
-Variable Sqrt(const Variable& x) {
-    return unary(Op::kSqrt, "Sqrt", x,
-                 [](const Variable&, const Variable& y) { return Div(Float(0.5f), y); });
+
+// math (src/core/f_ops.cpp:262-475: derivative graphs as the reference's)
+Variable Sin(const Variable& x) {
+    return unary(Op::kSin, "Sin", x, [](const Variable& xv, const Variable&) { return Cos(xv); });
 }
-Variable Sign(const Variable& x) { return unary(Op::kSign, "Sign", x, nullptr); }
-Variable Abs(const Variable& x) {
-    return unary(Op::kAbs, "Abs", x, [](const Variable& xv, const Variable&) { return Sign(xv); });
+Variable Cos(const Variable& x) {
+    return unary(Op::kCos, "Cos", x,
+                 [](const Variable& xv, const Variable&) { return Neg(Sin(xv)); });
+}
+Variable Tan(const Variable& x) {
+    return unary(Op::kTan, "Tan", x,
+                 [](const Variable&, const Variable& y) { return Add(Float(1.f), Mul(y, y)); });
+}
+Variable Asin(const Variable& x) {
+    return unary(Op::kAsin, "Asin", x, [](const Variable& xv, const Variable&) {
+        return InverseSqrt(Sub(Float(1.f), Mul(xv, xv)));
+    });
+}
+Variable Acos(const Variable& x) {
+    return unary(Op::kAcos, "Acos", x, [](const Variable& xv, const Variable&) {
+        return Neg(InverseSqrt(Sub(Float(1.f), Mul(xv, xv))));
+    });
+}
+Variable Atan(const Variable& x) {
+    return unary(Op::kAtan, "Atan", x, [](const Variable& xv, const Variable&) {
+        return Div(Float(1.f), Add(Float(1.f), Mul(xv, xv)));
+    });
+}
+Variable Atan2(const Variable& y, const Variable& x) {
+    return ew(Op::kAtan2, "Atan2", {y, x},
+              [](const Variables& xs, const Variable&, const Variable& gy, uint32_t i) {
+                  Variable denom = Add(Mul(xs[0], xs[0]), Mul(xs[1], xs[1]));
+                  if (i == 0) {
+                      return Div(Mul(gy, xs[1]), denom);
+                  }
+                  return Neg(Div(Mul(gy, xs[0]), denom));
+              });
 }
 Variable Exp(const Variable& x) {
     return unary(Op::kExp, "Exp", x, [](const Variable&, const Variable& y) { return y; });
 }
+Variable Exp2(const Variable& x) {
+    return unary(Op::kExp2, "Exp2", x, [](const Variable&, const Variable& y) {
+        return Mul(y, Float(0.6931471805599453f));
+    });
+}
 Variable Log(const Variable& x) {
     return unary(Op::kLog, "Log", x,
                  [](const Variable& xv, const Variable&) { return Div(Float(1.f), xv); });
+}
+Variable Log2(const Variable& x) {
+    return unary(Op::kLog2, "Log2", x, [](const Variable& xv, const Variable&) {
+        return Div(Float(1.4426950408889634f), xv);
+    });
+}
+Variable Sqrt(const Variable& x) {
+    return unary(Op::kSqrt, "Sqrt", x,
+                 [](const Variable&, const Variable& y) { return Div(Float(0.5f), y); });
+}
+Variable InverseSqrt(const Variable& x) {
+    return unary(Op::kInvSqrt, "InverseSqrt", x, [](const Variable&, const Variable& y) {
+        return Mul(Float(-0.5f), Mul(y, Mul(y, y)));
+    });
+}
+Variable Abs(const Variable& x) {
+    return unary(Op::kAbs, "Abs", x, [](const Variable& xv, const Variable&) { return Sign(xv); });
+}
+Variable Sign(const Variable& x) { return unary(Op::kSign, "Sign", x, nullptr); }
+Variable Floor(const Variable& x) { return unary(Op::kFloor, "Floor", x, nullptr); }
+Variable Fract(const Variable& x) {
+    return unary(Op::kFract, "Fract", x,
+                 [](const Variable&, const Variable&) { return Float(1.f); });
+}
+Variable Mod(const Variable& x, const Variable& m) {
+    return ew(Op::kMod, "Mod", {x, m},
+              [](const Variables& xs, const Variable&, const Variable& gy, uint32_t i) {
+                  if (i == 0) {
+                      return gy;
+                  }
+                  return Neg(Mul(gy, Floor(Div(xs[0], xs[1]))));
+              });
 }
 Variable Pow(const Variable& x, const Variable& p) {
     return ew(Op::kPow, "Pow", {x, p},
@@ -404,8 +542,32 @@ Variable Clamp(const Variable& x, const Variable& lo, const Variable& hi) {
                   return Mul(gy, Mul(Step(xs[1], xs[0]), Step(xs[0], xs[2])));
               });
 }
+Variable Mix(const Variable& x0, const Variable& x1, const Variable& t) {
+    return ew(Op::kMix, "Mix", {x0, x1, t},
+              [](const Variables& xs, const Variable&, const Variable& gy, uint32_t i) {
+                  if (i == 0) {
+                      return Mul(gy, Sub(Float(1.f), xs[2]));
+                  }
+                  if (i == 1) {
+                      return Mul(gy, xs[2]);
+                  }
+                  return Mul(gy, Sub(xs[1], xs[0]));
+              });
+}
 Variable Step(const Variable& edge, const Variable& x) {
     return ew(Op::kStep, "Step", {edge, x}, kNull);
+}
+Variable SmoothStep(const Variable& e0, const Variable& e1, const Variable& x) {
+    return ew(Op::kSmoothStep, "SmoothStep", {e0, e1, x},
+              [](const Variables& xs, const Variable&, const Variable& gy, uint32_t i) -> Variable {
+                  if (i != 2) {
+                      return nullptr;  // no gradient toward the edges
+                  }
+                  Variable range = Sub(xs[1], xs[0]);
+                  Variable t = Clamp(Div(Sub(xs[2], xs[0]), range), Float(0.f), Float(1.f));
+                  Variable dt = Div(Mul(Float(6.f), Mul(t, Sub(Float(1.f), t))), range);
+                  return Mul(gy, dt);
+              });
 }
 Variable Sigmoid(const Variable& x) {
     return ew(Op::kSigmoid, "Sigmoid", {x},
@@ -438,22 +600,86 @@ Variable GetY(const Variable& v) { return extract(v, 1, 1); }
 Variable GetZ(const Variable& v) { return extract(v, 2, 1); }
 Variable GetW(const Variable& v) { return extract(v, 3, 1); }
 Variable Dot(const Variable& a, const Variable& b) {
-    require(a.getVType() == b.getVType() && a.getVType() != FLOAT,
+    require(IsVectorVType(a.getVType()) && a.getVType() == b.getVType(),
             "Dot takes two equal vector types");
     return ew_fixed(Op::kDot, "Dot", FLOAT, {a, b},
                     [](const Variables& xs, const Variable&, const Variable& gy, uint32_t i) {
                         return Mul(gy, xs[i == 0 ? 1 : 0]);
                     });
 }
+Variable Cross(const Variable& a, const Variable& b) {
+    require(a.getVType() == VEC3 && b.getVType() == VEC3, "Cross takes VEC3 inputs");
+    return ew_fixed(Op::kCross, "Cross", VEC3, {a, b},
+                    [](const Variables& xs, const Variable&, const Variable& gy, uint32_t i) {
+                        return i == 0 ? Cross(xs[1], gy) : Cross(gy, xs[0]);
+                    });
+}
+Variable Length(const Variable& v) {
+    require(IsVectorVType(v.getVType()) || v.getVType() == FLOAT,
+            "Length takes a float vector");
+    return ew_fixed(Op::kLength, "Length", FLOAT, {v},
+                    [](const Variables& xs, const Variable& y, const Variable& gy, uint32_t) {
+                        return Mul(Div(gy, y), xs[0]);
+                    });
+}
+Variable Distance(const Variable& a, const Variable& b) { return Length(Sub(a, b)); }
+Variable Normalize(const Variable& v) {
+    // backward (gy - y dot(y, gy)) / |x| (f_ops.cpp:719-743)
+    return ew(Op::kNormalize, "Normalize", {v},
+              [](const Variables& xs, const Variable& y, const Variable& gy, uint32_t) {
+                  return Div(Sub(gy, Mul(y, Dot(y, gy))), Length(xs[0]));
+              });
+}
+Variable Reflect(const Variable& incident, const Variable& normal) {
+    return Sub(incident, Mul(Mul(Float(2.f), Dot(normal, incident)), normal));
+}
 Variable CompSum(const Variable& v) {
     if (v.getVType() == FLOAT) {
         return v;
     }
+    require(IsVectorVType(v.getVType()) && !IsIntVType(v.getVType()),
+            "CompSum takes a float vector");
     const uint32_t n = NumComponents(v.getVType());
     return ew_fixed(Op::kCompSum, "CompSum", FLOAT, {v},
                     [n](const Variables&, const Variable&, const Variable& gy, uint32_t) {
                         return replicate(gy, n);
                     });
+}
+
+Variable MatMul(const Variable& a, const Variable& b) {
+    const VType ta = a.getVType(), tb = b.getVType();
+    require(IsMatrixVType(ta), "MatMul: the left operand must be a matrix");
+    const uint32_t dim = mat_dim(ta);
+    const bool vec_rhs = IsVectorVType(tb);
+    require(vec_rhs ? NumComponents(tb) == dim : tb == ta, "MatMul: dimension mismatch");
+    return make_op({Op::kMatMul, "MatMul", vec_rhs ? tb : ta, common_size({a, b}),
+                    [vec_rhs](const Variables& xs, const Variable&, const Variable& gy,
+                              uint32_t i) -> Variable {
+                        if (vec_rhs) {
+                            return i == 0 ? OuterProduct(gy, xs[1]) : MatMul(Transpose(xs[0]), gy);
+                        }
+                        return i == 0 ? MatMul(gy, Transpose(xs[1])) : MatMul(Transpose(xs[0]), gy);
+                    }},
+                   {a, b}, {}, dim, vec_rhs ? 1u : 0u);
+}
+Variable Transpose(const Variable& m) {
+    require(IsMatrixVType(m.getVType()), "Transpose takes a matrix");
+    return make_op({Op::kTranspose, "Transpose", m.getVType(), m.getImgSize(),
+                    [](const Variables&, const Variable&, const Variable& gy, uint32_t) {
+                        return Transpose(gy);
+                    }},
+                   {m}, {}, mat_dim(m.getVType()));
+}
+Variable OuterProduct(const Variable& col, const Variable& row) {
+    const VType tc = col.getVType();
+    require(IsVectorVType(tc) && row.getVType() == tc, "OuterProduct takes two equal vectors");
+    const uint32_t dim = NumComponents(tc);
+    return make_op({Op::kOuter, "OuterProduct", dim == 2 ? MAT2 : dim == 3 ? MAT3 : MAT4,
+                    common_size({col, row}),
+                    [](const Variables& xs, const Variable&, const Variable& gy, uint32_t i) {
+                        return i == 0 ? MatMul(gy, xs[1]) : MatMul(Transpose(gy), xs[0]);
+                    }},
+                   {col, row}, {}, dim);
 }
 
 Variable Broadcast(const Variable& x, ImgSize size) {
@@ -479,6 +705,10 @@ Variable Mean(const Variable& x) {
     const float inv = 1.f / (float(s.w) * float(s.h) * float(NumComponents(x.getVType())));
     return Mul(CompSum(Sum(x)), Float(inv));
 }
+Variable SumAll(const Variable& x) {
+    require_float_image(x, "SumAll: the input");
+    return make_op({Op::kSumAll, "SumAll", FLOAT, {1, 1}, kNull}, {x});
+}
 Variable SumPixelWise(const Variables& xs) {
     require(!xs.empty(), "SumPixelWise needs inputs");
     Variables level = xs;
@@ -499,6 +729,18 @@ Variable SumPixelWise(const Variables& xs) {
 Variable StopGradient(const Variable& x) {
     return make_op({Op::kCopy, "StopGradient", x.getVType(), x.getImgSize(), kNull}, {x});
 }
+Variable SetFragDepth(const Variable& depth) {
+    return make_op({Op::kSetFragDepth, "SetFragDepth", depth.getVType(), depth.getImgSize(),
+                    [](const Variables&, const Variable&, const Variable& gy, uint32_t) {
+                        return gy;
+                    }},
+                   {depth});
+}
+Variable PeelDepth(const Variable& frag_depth, const Variable& prev_frag_depth) {
+    return make_op({Op::kPeelDepth, "PeelDepth", FLOAT,
+                    common_size({frag_depth, prev_frag_depth}), kNull},
+                   {frag_depth, prev_frag_depth});
+}
 
 Variable ScreenCoord(ImgSize size) {
     return make_op({Op::kScreenCoord, "ScreenCoord", VEC2, size, kNull}, {});
@@ -506,6 +748,7 @@ Variable ScreenCoord(ImgSize size) {
 Variable Rasterize(const Variable& clip, const Variable& attr, const Variable& faces,
                    ImgSize screen) {
     require(clip.getVType() == VEC4 && clip.getImgSize().h == 1, "Rasterize: clip VEC4 {V,1}");
+    require(NumComponents(attr.getVType()) <= 4, "Rasterize: attribute of 1..4 components");
     return make_op({Op::kRasterize, "Rasterize", attr.getVType(), screen, kNull},
                    {clip, attr, faces});
 }
@@ -520,8 +763,8 @@ Variable SoftClip(const Variable& clip, const Variable& faces, ImgSize screen, f
                    screen.h, radius);
 }
 static Variable rasterize_soft(const Variables& xs, ImgSize screen, float radius, bool peel) {
-    BwdFn b = [radius](const Variables& in, const Variable& y, const Variable& gy,
-                       uint32_t i) -> Variable {
+    BwdFunc b = [radius](const Variables& in, const Variable& y, const Variable& gy,
+                         uint32_t i) -> Variable {
         if (i != 3) {
             return nullptr;
         }
@@ -601,6 +844,137 @@ Variable AntiAlias(const Variable& img, const Variable& tri, const Variable& cli
                    {img, tri, clip, faces, vf, seed}, {}, n_samples);
 }
 
+Variable PixelFetch(const Variable& tex, uint32_t x_index, const Variable& row_idx) {
+    require_float_image(tex, "PixelFetch: tex");
+    require(x_index < tex.getImgSize().w, "PixelFetch: x out of range");
+    require(row_idx.getVType() == FLOAT && row_idx.getImgSize().isUniform(),
+            "PixelFetch: row_idx must be FLOAT {1,1}");
+    return make_op({Op::kPixelFetch, "PixelFetch", tex.getVType(), {1, 1}, kNull}, {tex, row_idx},
+                   {}, x_index);
+}
+Variable TileFetch(const Variable& atlas, const Variable& tile_idx, uint32_t tile_h) {
+    require_float_image(atlas, "TileFetch: atlas");
+    require(tile_h > 0 && atlas.getImgSize().h % tile_h == 0,
+            "TileFetch: atlas height must be a multiple of tile_h");
+    require(tile_idx.getVType() == FLOAT && tile_idx.getImgSize().isUniform(),
+            "TileFetch: tile_idx must be FLOAT {1,1}");
+    return make_op({Op::kTileFetch, "TileFetch", atlas.getVType(),
+                    {atlas.getImgSize().w, tile_h}, kNull},
+                   {atlas, tile_idx}, {}, tile_h);
+}
+
+Variable VertexNeighborMean(const Variable& pos, const Variable& nbrs) {
+    require(pos.getVType() == VEC3 && pos.getImgSize().h == 1,
+            "VertexNeighborMean: pos must be VEC3 {V,1}");
+    return make_op({Op::kVertexNeighborMean, "VertexNeighborMean", VEC3, pos.getImgSize(), kNull},
+                   {pos, nbrs});
+}
+Variable NormalConsistencyFaceTerm(const Variable& pos, const Variable& faces,
+                                   const Variable& face_adj) {
+    return make_op({Op::kNcFaceTerm, "NormalConsistencyFaceTerm", VEC3,
+                    {faces.getImgSize().w, 1}, kNull},
+                   {pos, faces, face_adj});
+}
+Variable NormalConsistencyVertexGrad(const Variable& face_term, const Variable& pos,
+                                     const Variable& faces, const Variable& vf) {
+    return make_op({Op::kNcVertexGrad, "NormalConsistencyVertexGrad", VEC3, pos.getImgSize(),
+                    kNull},
+                   {face_term, pos, faces, vf});
+}
+
+// textures: the inverse-UV table is held by the backward builder, not an
+// input of the forward (f_ops.cpp:2605-2639, 2736-2780)
+Variable Texture(const Variable& tex, const Variable& uv, const Variable& inv_uv) {
+    require_float_image(tex, "Texture: the texture");
+    require(!tex.getImgSize().isUniform() && uv.getVType() == VEC2 &&
+                    inv_uv.getVType() == VEC4 && inv_uv.getImgSize() == tex.getImgSize(),
+            "Texture: texture image, uv VEC2, inv_uv VEC4 of the texture size");
+    return make_op({Op::kTexture, "Texture", tex.getVType(), uv.getImgSize(),
+                    [inv_uv](const Variables& xs, const Variable&, const Variable& gy,
+                             uint32_t i) -> Variable {
+                        if (i != 0) {
+                            return nullptr;
+                        }
+                        return special(Op::kGatherInvUv, "GatherByInverseUV", gy.getVType(),
+                                       inv_uv.getImgSize(), {gy, inv_uv, xs[1]});
+                    }},
+                   {tex, uv});
+}
+Variable TextureBilinear(const Variable& tex, const Variable& uv, const Variable& inv_uv) {
+    require_float_image(tex, "TextureBilinear: the texture");
+    require(!tex.getImgSize().isUniform() && uv.getVType() == VEC2 &&
+                    inv_uv.getVType() == VEC4 && inv_uv.getImgSize() == tex.getImgSize(),
+            "TextureBilinear: texture image, uv VEC2, inv_uv VEC4 of the texture size");
+    return make_op({Op::kTextureBilinear, "TextureBilinear", tex.getVType(), uv.getImgSize(),
+                    [inv_uv](const Variables& xs, const Variable&, const Variable& gy,
+                             uint32_t i) -> Variable {
+                        if (i != 0) {
+                            return nullptr;
+                        }
+                        return special(Op::kGatherInvUvBilinear, "GatherByInverseUVBilinear",
+                                       gy.getVType(), inv_uv.getImgSize(), {gy, inv_uv, xs[1]});
+                    }},
+                   {tex, uv});
+}
+Variable EquirectSample(const Variable& map, const Variable& dir) {
+    require_float_image(map, "EquirectSample: the map");
+    require(!map.getImgSize().isUniform() && dir.getVType() == VEC3,
+            "EquirectSample: map image, dir VEC3");
+    const ImgSize msz = map.getImgSize();
+    return make_op({Op::kEquirectSample, "EquirectSample", map.getVType(), dir.getImgSize(),
+                    [msz](const Variables& xs, const Variable&, const Variable& gy,
+                          uint32_t i) -> Variable {
+                        if (i != 0) {
+                            return nullptr;
+                        }
+                        return special(Op::kEquirectSampleBwd, "EquirectSampleBwd",
+                                       gy.getVType(), msz, {gy, xs[1]});
+                    }},
+                   {map, dir});
+}
+Variable IrradianceConv(const Variable& env, ImgSize out_size) {
+    require_float_image(env, "IrradianceConv: env");
+    require(!env.getImgSize().isUniform() && !out_size.isUniform(),
+            "IrradianceConv: env and output must be images");
+    const ImgSize esz = env.getImgSize();
+    return make_op({Op::kIrradianceConv, "IrradianceConv", env.getVType(), out_size,
+                    [esz](const Variables&, const Variable&, const Variable& gy,
+                          uint32_t) -> Variable {
+                        return special(Op::kIrradianceConvBwd, "IrradianceConvBwd",
+                                       gy.getVType(), esz, {gy});
+                    }},
+                   {env});
+}
+Variable PrefilterEnv(const Variable& env, ImgSize out_size, float roughness,
+                      uint32_t n_samples) {
+    require_float_image(env, "PrefilterEnv: env");
+    return make_op({Op::kPrefilterEnv, "PrefilterEnv", env.getVType(), out_size, kNull}, {env},
+                   {}, n_samples, 0, roughness);
+}
+Variable PrefilterConv(const Variable& env, ImgSize out_size, float roughness) {
+    require_float_image(env, "PrefilterConv: env");
+    require(!env.getImgSize().isUniform() && !out_size.isUniform(),
+            "PrefilterConv: env and output must be images");
+    const ImgSize esz = env.getImgSize();
+    // the static per-output normaliser (a zero-input op, as the reference's)
+    Variable norm = make_op({Op::kPrefilterConv, "PrefilterConvNorm", FLOAT, out_size, kNull},
+                            {}, {}, esz.w, esz.h, roughness, 1);
+    return make_op({Op::kPrefilterConv, "PrefilterConv", env.getVType(), out_size,
+                    [esz, roughness](const Variables& xs, const Variable&, const Variable& gy,
+                                     uint32_t i) -> Variable {
+                        if (i != 0) {
+                            return nullptr;
+                        }
+                        return special(Op::kPrefilterConvBwd, "PrefilterConvBwd", gy.getVType(),
+                                       esz, {gy, xs[1]}, 0, 0, roughness);
+                    }},
+                   {env, norm}, {}, 0, 0, roughness, 0);
+}
+Variable BrdfIntegrationLut(ImgSize size, uint32_t n_samples) {
+    return make_op({Op::kBrdfLut, "BrdfIntegrationLut", VEC2, size, kNull}, {}, {}, n_samples);
+}
+Variable AvgPool2x2(const Variable& x) { return Mul(reduce2x2(x), Float(0.25f)); }
+
 }  // namespace F
 
 Variable operator+(const Variable& a, const Variable& b) { return F::Add(a, b); }
@@ -616,6 +990,41 @@ Variable operator-(float a, const Variable& b) { return F::Sub(F::Float(a), b); 
 Variable operator*(float a, const Variable& b) { return F::Mul(F::Float(a), b); }
 Variable operator/(float a, const Variable& b) { return F::Div(F::Float(a), b); }
 Variable operator-(const Variable& x) { return F::Neg(x); }
+Variable operator<(const Variable& a, const Variable& b) { return F::Less(a, b); }
+Variable operator<(float a, const Variable& b) { return F::Less(F::Float(a), b); }
+Variable operator<(const Variable& a, float b) { return F::Less(a, F::Float(b)); }
+Variable operator<=(const Variable& a, const Variable& b) { return F::LessEqual(a, b); }
+Variable operator>(const Variable& a, const Variable& b) { return F::Greater(a, b); }
+Variable operator>=(const Variable& a, const Variable& b) { return F::GreaterEqual(a, b); }
+
+Functions TraverseFuncs(const Variables& roots) {
+    Functions funcs;
+    std::unordered_set<uint64_t> seen_fn, seen_var;
+    std::vector<Variable> stack;
+    for (const auto& r : roots) {
+        if (r) {
+            stack.push_back(r);
+        }
+    }
+    while (!stack.empty()) {
+        Variable v = stack.back();
+        stack.pop_back();
+        if (!seen_var.insert(v.id()).second) {
+            continue;
+        }
+        Function c = v.getCreator();
+        if (!c || !seen_fn.insert(c.id()).second) {
+            continue;
+        }
+        funcs.push_back(c);
+        for (const auto& x : c.getInputVars()) {
+            stack.push_back(x);
+        }
+    }
+    std::sort(funcs.begin(), funcs.end(),
+              [](const Function& a, const Function& b) { return a.id() < b.id(); });
+    return funcs;
+}
 
 // ---- BuildBackward (src/core/build_backward.cpp:13-149) --------------------
 
@@ -658,7 +1067,8 @@ Variable sum_contribs(Variables c) {
 
 std::tuple<Variables, Variables> BuildBackward(const Variable& loss) {
     require((bool)loss, "null loss");
-    require(loss.getVType() != IVEC3, "the loss must be a float image");
+    require(!IsIntVType(loss.getVType()) && !IsMatrixVType(loss.getVType()),
+            "the loss must be a float image");
     std::map<Variable, Variables> contribs;  // ordered by id
     auto later = [](const std::shared_ptr<FunctionNode>& a, const std::shared_ptr<FunctionNode>& b) {
         return a->id < b->id;
@@ -668,11 +1078,11 @@ std::tuple<Variables, Variables> BuildBackward(const Variable& loss) {
             queue(later);
     std::unordered_set<uint64_t> seen;
     contribs[loss] = {F::Float(1.f)};
-    if (loss.node()->creator) {
-        queue.push(loss.node()->creator);
+    if (NodeAccess::Node(loss)->creator) {
+        queue.push(NodeAccess::Node(loss)->creator);
     }
     while (!queue.empty()) {
-        Function fn(queue.top());
+        Function fn = NodeAccess::Wrap(queue.top());
         queue.pop();
         if (!seen.insert(fn.id()).second) {
             continue;
@@ -702,8 +1112,8 @@ std::tuple<Variables, Variables> BuildBackward(const Variable& loss) {
                 continue;
             }
             contribs[xs[i]].push_back(sum_to_shape(gx, xs[i]));
-            if (xs[i].node()->creator) {
-                queue.push(xs[i].node()->creator);
+            if (NodeAccess::Node(xs[i])->creator) {
+                queue.push(NodeAccess::Node(xs[i])->creator);
             }
         }
     }
@@ -717,440 +1127,5 @@ std::tuple<Variables, Variables> BuildBackward(const Variable& loss) {
     }
     return {leaves, grads};
 }
-
-// ---- device kernels -----------------------------------------------------------
-
-namespace {
-
-struct EwIn {
-    const float* p;
-    uint32_t nc;
-    uint32_t uniform;
-};
-
-struct EwArgs {
-    int op;
-    uint32_t n_in;
-    uint32_t ny;
-    uint32_t a0;
-    size_t n_px;
-    EwIn in[4];
-    float* out;
-};
-
-__device__ __forceinline__ float comp(const EwIn& x, size_t p, uint32_t c) {
-    const size_t q = x.uniform ? 0 : p;
-    return x.p[q * x.nc + (x.nc == 1 ? 0 : c)];
-}
-
-__device__ __forceinline__ float std_min(float a, float b) { return b < a ? b : a; }
-__device__ __forceinline__ float std_max(float a, float b) { return a < b ? b : a; }
-
-__global__ __launch_bounds__(256) void k_elementwise(EwArgs A) {
-    const size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= A.n_px) {
-        return;
-    }
-    float* y = A.out + p * A.ny;
-    const Op op = (Op)A.op;
-    if (op == Op::kCompose) {
-        uint32_t o = 0;
-        for (uint32_t i = 0; i < A.n_in; i++) {
-            for (uint32_t c = 0; c < A.in[i].nc; c++) {
-                y[o++] = comp(A.in[i], p, c);
-            }
-        }
-        return;
-    }
-    if (op == Op::kExtract) {
-        const size_t q = A.in[0].uniform ? 0 : p;
-        for (uint32_t c = 0; c < A.ny; c++) {
-            y[c] = A.in[0].p[q * A.in[0].nc + A.a0 + c];
-        }
-        return;
-    }
-    if (op == Op::kDot || op == Op::kCompSum) {
-        float acc = 0.f;
-        for (uint32_t c = 0; c < A.in[0].nc; c++) {
-            acc += op == Op::kDot ? comp(A.in[0], p, c) * comp(A.in[1], p, c) : comp(A.in[0], p, c);
-        }
-        y[0] = acc;
-        return;
-    }
-    for (uint32_t c = 0; c < A.ny; c++) {
-        const float a = comp(A.in[0], p, c);
-        const float b = A.n_in > 1 ? comp(A.in[1], p, c) : 0.f;
-        float r = 0.f;
-        switch (op) {
-            case Op::kAdd: r = a + b; break;
-            case Op::kSub: r = a - b; break;
-            case Op::kMul: r = a * b; break;
-            case Op::kDiv: r = a / b; break;
-            case Op::kNeg: r = -a; break;
-            case Op::kSqrt: r = sqrtf(a); break;
-            case Op::kAbs: r = fabsf(a); break;
-            case Op::kSign: r = (float)((a > 0.f) - (a < 0.f)); break;
-            case Op::kExp: r = libc_expf(a); break;
-            case Op::kLog: r = logf(a); break;
-            case Op::kPow: r = powf(a, b); break;
-            case Op::kMax: r = std_max(a, b); break;
-            case Op::kMin: r = std_min(a, b); break;
-            case Op::kClamp: r = std_min(std_max(a, b), comp(A.in[2], p, c)); break;
-            case Op::kStep: r = b < a ? 0.f : 1.f; break;
-            case Op::kSigmoid: r = 1.f / (1.f + libc_expf(-a)); break;
-            case Op::kLess: r = (float)(a < b); break;
-            case Op::kLessEq: r = (float)(a <= b); break;
-            case Op::kGreater: r = (float)(a > b); break;
-            case Op::kGreaterEq: r = (float)(a >= b); break;
-            case Op::kCopy: r = a; break;
-            case Op::kSumPw: {
-                float acc = 0.f;
-                for (uint32_t i = 0; i < A.n_in; i++) {
-                    acc += comp(A.in[i], p, c);
-                }
-                r = acc;
-                break;
-            }
-            default: break;
-        }
-        y[c] = r;
-    }
-}
-
-__global__ __launch_bounds__(256) void k_fill(float* y, uint32_t n, float v0, float v1, float v2,
-                                              float v3) {
-    const uint32_t c = threadIdx.x;
-    if (c < n) {
-        y[c] = c == 0 ? v0 : c == 1 ? v1 : c == 2 ? v2 : v3;
-    }
-}
-
-// Reduce2x2Sum: each output pixel sums its 2x2 source block in row order
-// from 0 (the reference CPU kernel's accumulation order).
-__global__ __launch_bounds__(256) void k_reduce2x2(const float* x, uint32_t sw, uint32_t sh,
-                                                   uint32_t nc, uint32_t ow, uint32_t oh,
-                                                   float* y) {
-    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= ow * oh) {
-        return;
-    }
-    const uint32_t ox = q % ow, oy = q / ow;
-    for (uint32_t c = 0; c < nc; c++) {
-        float acc = 0.f;
-        for (uint32_t dy = 0; dy < 2; dy++) {
-            for (uint32_t dx = 0; dx < 2; dx++) {
-                const uint32_t sx = 2 * ox + dx, sy = 2 * oy + dy;
-                if (sx < sw && sy < sh) {
-                    acc += x[((size_t)sy * sw + sx) * nc + c];
-                }
-            }
-        }
-        y[(size_t)q * nc + c] = acc;
-    }
-}
-
-__global__ __launch_bounds__(256) void k_upsample2x(const float* x, uint32_t sw, uint32_t nc,
-                                                    uint32_t ow, uint32_t oh, float* y) {
-    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= ow * oh) {
-        return;
-    }
-    const uint32_t ox = q % ow, oy = q / ow;
-    for (uint32_t c = 0; c < nc; c++) {
-        y[(size_t)q * nc + c] = x[((size_t)(oy / 2) * sw + ox / 2) * nc + c];
-    }
-}
-
-__global__ __launch_bounds__(256) void k_screen_coord(uint32_t w, uint32_t h, float* y) {
-    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= w * h) {
-        return;
-    }
-    y[2 * (size_t)q + 0] = (float)(q % w) + 0.5f;
-    y[2 * (size_t)q + 1] = (float)(q / w) + 0.5f;
-}
-
-uint32_t blocks(size_t n) { return (uint32_t)((n + 255) / 256); }
-
-}  // namespace
-
-// ---- DressiAD ---------------------------------------------------------------
-
-struct DressiAD::Impl {
-    dressi_ctx* ctx = nullptr;
-    Variable loss;
-    Optimizer optimizer;
-    bool grads_built = false;
-    Variables leaves, grads;
-    Variables outputs;
-    std::vector<std::pair<Variable, Variable>> updates;
-    std::unordered_map<const VariableNode*, float*> bufs;
-    std::vector<std::shared_ptr<VariableNode>> keep;  // owners of `bufs` keys
-    std::vector<std::shared_ptr<FunctionNode>> plan;
-    bool plan_dirty = true;
-
-    static size_t count(const VariableNode& n) {
-        return (size_t)n.size.w * n.size.h * NumComponents(n.vtype);
-    }
-    float* buf(const std::shared_ptr<VariableNode>& n) {
-        auto it = bufs.find(n.get());
-        if (it != bufs.end()) {
-            return it->second;
-        }
-        void* p = nullptr;
-        check(dressi_malloc(ctx, &p, std::max<size_t>(count(*n), 1) * sizeof(float)));
-        check(dressi_memset(ctx, p, 0, std::max<size_t>(count(*n), 1) * sizeof(float)));
-        bufs[n.get()] = (float*)p;
-        keep.push_back(n);
-        return (float*)p;
-    }
-    static void check(int rc) {
-        if (rc != DRESSI_OK) {
-            throw DressiError(std::string("HIP executor: ") + dressi_last_error());
-        }
-    }
-
-    void build_grads() {
-        if (grads_built || !loss) {
-            return;
-        }
-        grads_built = true;
-        std::tie(leaves, grads) = BuildBackward(loss);
-        if (optimizer) {
-            const Variables updated = optimizer(leaves, grads);
-            require(updated.size() == leaves.size(), "the optimizer must return one value per leaf");
-            for (size_t i = 0; i < leaves.size(); i++) {
-                updates.emplace_back(leaves[i], updated[i]);
-            }
-        }
-        plan_dirty = true;
-    }
-
-    void build_plan() {
-        build_grads();
-        std::vector<std::shared_ptr<VariableNode>> roots;
-        if (loss) {
-            roots.push_back(loss.node());
-        }
-        for (const auto& o : outputs) {
-            roots.push_back(o.node());
-        }
-        for (const auto& u : updates) {
-            roots.push_back(u.second.node());
-        }
-        std::unordered_set<const FunctionNode*> seen;
-        std::vector<std::shared_ptr<FunctionNode>> fns;
-        std::vector<std::shared_ptr<VariableNode>> stack = roots;
-        while (!stack.empty()) {
-            auto v = stack.back();
-            stack.pop_back();
-            if (!v->creator || !seen.insert(v->creator.get()).second) {
-                continue;
-            }
-            fns.push_back(v->creator);
-            for (const auto& x : v->creator->xs) {
-                stack.push_back(x);
-            }
-        }
-        std::sort(fns.begin(), fns.end(),
-                  [](const auto& a, const auto& b) { return a->id < b->id; });
-        plan = std::move(fns);
-        for (const auto& fn : plan) {
-            for (const auto& x : fn->xs) {
-                buf(x);
-            }
-            buf(fn->y.lock());
-        }
-        plan_dirty = false;
-    }
-
-    void run(const FunctionNode& fn) {
-        const auto y = fn.y.lock();
-        float* out = buf(y);
-        const uint32_t ny = NumComponents(y->vtype);
-        const size_t n_px = (size_t)y->size.w * y->size.h;
-        hipStream_t s = (hipStream_t)dressi_ctx_stream(ctx);
-        std::vector<const float*> in;
-        std::vector<const VariableNode*> xn;
-        for (const auto& x : fn.xs) {
-            in.push_back(buf(x));
-            xn.push_back(x.get());
-        }
-        auto nc = [&](int i) { return NumComponents(xn[i]->vtype); };
-        auto w_of = [&](int i) { return xn[i]->size.w; };
-        auto h_of = [&](int i) { return xn[i]->size.h; };
-        switch (fn.op) {
-            case Op::kConst: {
-                const auto& v = fn.cval;
-                hipLaunchKernelGGL(k_fill, dim3(1), dim3(64), 0, s, out, (uint32_t)v.size(), v[0],
-                                   v.size() > 1 ? v[1] : 0.f, v.size() > 2 ? v[2] : 0.f,
-                                   v.size() > 3 ? v[3] : 0.f);
-                break;
-            }
-            case Op::kReduce2x2:
-                hipLaunchKernelGGL(k_reduce2x2, dim3(blocks(n_px)), dim3(256), 0, s, in[0], w_of(0),
-                                   h_of(0), ny, y->size.w, y->size.h, out);
-                break;
-            case Op::kUpsample2x:
-                hipLaunchKernelGGL(k_upsample2x, dim3(blocks(n_px)), dim3(256), 0, s, in[0],
-                                   w_of(0), ny, y->size.w, y->size.h, out);
-                break;
-            case Op::kScreenCoord:
-                hipLaunchKernelGGL(k_screen_coord, dim3(blocks(n_px)), dim3(256), 0, s, y->size.w,
-                                   y->size.h, out);
-                break;
-            case Op::kRasterize:
-                check(dressi_rasterize(ctx, in[0], w_of(0), in[1], nc(1), in[2], w_of(2), y->size.w,
-                                       y->size.h, out));
-                break;
-            case Op::kRasterizeFaceId:
-                check(dressi_rasterize_face_id(ctx, in[0], w_of(0), in[2], w_of(2), y->size.w,
-                                               y->size.h, out));
-                break;
-            case Op::kSoftClip:
-                check(dressi_soft_clip(ctx, in[0], w_of(0), in[1], w_of(1), fn.a0, fn.a1, fn.f0,
-                                       out));
-                break;
-            case Op::kRasterizeSoft:
-                check(dressi_rasterize_soft(ctx, in[0], in[1], in[2], in[3], w_of(3), in[4], w_of(4),
-                                            fn.a0, fn.a1, fn.f0, fn.flag ? in[6] : nullptr, out));
-                break;
-            case Op::kLookupFaces:
-                check(dressi_lookup_faces(ctx, in[0], nc(0), w_of(0), in[1], w_of(1), fn.a0, out));
-                break;
-            case Op::kLookupFacesBwd:
-                check(dressi_lookup_faces_bwd(ctx, in[0], nc(0), in[1], w_of(1), in[2], w_of(2),
-                                              h_of(2), fn.a0, out));
-                break;
-            case Op::kFaceFetch:
-                check(dressi_face_fetch(ctx, in[0], nc(0), w_of(0), in[1], w_of(1), h_of(1), out));
-                break;
-            case Op::kFaceFetchBwd:
-                check(dressi_face_fetch_bwd(ctx, in[0], nc(0), in[1], w_of(1), h_of(1), in[2], in[3],
-                                            in[4], w_of(2), in[5], fn.f0, fn.a0, out));
-                break;
-            case Op::kGatherDistGrad:
-                check(dressi_gather_dist_grad(ctx, in[0], in[1], in[2], w_of(2), in[3], w_of(3),
-                                              in[4], h_of(4), fn.f0, fn.flag, w_of(1), h_of(1),
-                                              out));
-                break;
-            case Op::kColSum:
-                check(dressi_col_sum(ctx, in[0], nc(0), w_of(0), h_of(0), out));
-                break;
-            case Op::kAntiAlias:
-                check(dressi_antialias(ctx, in[0], nc(0), in[1], in[2], w_of(2), in[3], w_of(3),
-                                       w_of(0), h_of(0), out));
-                break;
-            case Op::kAaBwdImg:
-                check(dressi_antialias_bwd_img(ctx, in[0], nc(0), in[1], in[2], w_of(2), in[3],
-                                               w_of(3), w_of(0), h_of(0), out));
-                break;
-            case Op::kAaBwdVtx:
-                check(dressi_antialias_bwd_vtx(ctx, in[0], in[1], nc(0), in[2], in[3], w_of(3),
-                                               in[4], w_of(4), in[5], h_of(5), in[6], fn.a0,
-                                               fn.flag, w_of(0), h_of(0), out));
-                break;
-            default: {
-                require(fn.xs.size() <= 4, fn.name + ": more than 4 inputs");
-                EwArgs A{};
-                A.op = (int)fn.op;
-                A.n_in = (uint32_t)fn.xs.size();
-                A.ny = ny;
-                A.a0 = fn.a0;
-                A.n_px = n_px;
-                for (size_t i = 0; i < fn.xs.size(); i++) {
-                    A.in[i] = {in[i], nc((int)i), xn[i]->size.isUniform() ? 1u : 0u};
-                }
-                A.out = out;
-                hipLaunchKernelGGL(k_elementwise, dim3(blocks(n_px)), dim3(256), 0, s, A);
-                break;
-            }
-        }
-        if (hipGetLastError() != hipSuccess) {
-            throw DressiError(fn.name + ": kernel launch failed");
-        }
-    }
-};
-
-DressiAD::DressiAD(int device) : m_impl(new Impl) {
-    Impl::check(dressi_ctx_create(device, &m_impl->ctx));
-}
-DressiAD::~DressiAD() {
-    if (m_impl && m_impl->ctx) {
-        dressi_ctx_synchronize(m_impl->ctx);
-        for (auto& [n, p] : m_impl->bufs) {
-            dressi_free(m_impl->ctx, p);
-        }
-        dressi_ctx_destroy(m_impl->ctx);
-    }
-}
-void DressiAD::setLossVar(const Variable& loss) {
-    m_impl->loss = loss;
-    m_impl->grads_built = false;
-    m_impl->plan_dirty = true;
-}
-void DressiAD::setOptimizer(const Optimizer& f) {
-    m_impl->optimizer = f;
-    m_impl->grads_built = false;
-    m_impl->plan_dirty = true;
-}
-void DressiAD::markOutput(const Variable& v) {
-    m_impl->outputs.push_back(v);
-    m_impl->plan_dirty = true;
-}
-void DressiAD::addUpdate(const Variable& leaf, const Variable& value) {
-    require(!leaf.node()->creator, "addUpdate: the target must be a leaf");
-    require(leaf.getVType() == value.getVType() && leaf.getImgSize() == value.getImgSize(),
-            "addUpdate: value and leaf shapes differ");
-    m_impl->updates.emplace_back(leaf, value);
-    m_impl->plan_dirty = true;
-}
-std::vector<std::pair<Variable, Variable>> DressiAD::inputGrads() const {
-    m_impl->build_grads();
-    std::vector<std::pair<Variable, Variable>> r;
-    for (size_t i = 0; i < m_impl->leaves.size(); i++) {
-        r.emplace_back(m_impl->leaves[i], m_impl->grads[i]);
-    }
-    return r;
-}
-size_t DressiAD::getFuncCount() const {
-    if (m_impl->plan_dirty) {
-        m_impl->build_plan();
-    }
-    return m_impl->plan.size();
-}
-std::string DressiAD::getDeviceName() const {
-    char b[256];
-    Impl::check(dressi_ctx_device_name(m_impl->ctx, b, sizeof(b)));
-    return b;
-}
-void DressiAD::execStep() {
-    if (m_impl->plan_dirty) {
-        m_impl->build_plan();
-    }
-    for (const auto& fn : m_impl->plan) {
-        m_impl->run(*fn);
-    }
-    for (const auto& [leaf, value] : m_impl->updates) {
-        if (hipMemcpyAsync(m_impl->buf(leaf.node()), m_impl->buf(value.node()),
-                           Impl::count(*leaf.node()) * sizeof(float), hipMemcpyDeviceToDevice,
-                           (hipStream_t)dressi_ctx_stream(m_impl->ctx)) != hipSuccess) {
-            throw DressiError("execStep: update copy failed");
-        }
-    }
-}
-void DressiAD::sendImg(const Variable& v, const float* data) {
-    require(!v.node()->creator, "sendImg: only leaves take host data");
-    Impl::check(dressi_memcpy_h2d(m_impl->ctx, m_impl->buf(v.node()), data,
-                                  Impl::count(*v.node()) * sizeof(float)));
-}
-std::vector<float> DressiAD::recvImg(const Variable& v) {
-    std::vector<float> out(Impl::count(*v.node()));
-    Impl::check(dressi_memcpy_d2h(m_impl->ctx, out.data(), m_impl->buf(v.node()),
-                                  out.size() * sizeof(float)));
-    Impl::check(dressi_ctx_synchronize(m_impl->ctx));
-    return out;
-}
-dressi_ctx* DressiAD::context() const { return m_impl->ctx; }
 
 }  // namespace dressi

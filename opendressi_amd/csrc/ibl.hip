@@ -359,8 +359,8 @@ int dressi_equirect_sample_bwd(dressi_ctx* ctx, const float* gy, uint32_t n_comp
     void *acc = nullptr, *mx = nullptr;
     if (int rc = ctx_workspace(ctx, 12, cnt * sizeof(unsigned long long), &acc)) return rc;
     if (int rc = ctx_workspace(ctx, 13, sizeof(uint32_t), &mx)) return rc;
-    DRESSI_TRY_HIP(hipMemsetAsync(acc, 0, cnt * sizeof(unsigned long long), ctx->stream));
-    DRESSI_TRY_HIP(hipMemsetAsync(mx, 0, sizeof(uint32_t), ctx->stream));
+    if (int rc = launch_zero(ctx->stream, acc, cnt * sizeof(unsigned long long))) return rc;
+    if (int rc = launch_zero(ctx->stream, mx, sizeof(uint32_t))) return rc;
     if (npx) {
         const size_t ng = npx * n_comp;
         const uint32_t blocks = (uint32_t)std::min<size_t>((ng + 255) / 256, 1024);

@@ -72,6 +72,11 @@ int ctx_workspace_zeroed(dressi_ctx* ctx, int slot, size_t bytes, void** out);
 
 inline uint32_t div_up(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 
+// Fills `bytes` (a multiple of 4) at `p` with zero by a kernel on stream `s`
+// (not hipMemsetAsync: memset nodes of captured graphs have given wrong
+// results on replays, and per-op entry points may be captured).
+int launch_zero(hipStream_t s, void* p, size_t bytes);
+
 // ---------------------------------------------------------------------------
 // Tile binning (16x16 pixel tiles)
 // ---------------------------------------------------------------------------

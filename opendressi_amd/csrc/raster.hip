@@ -527,7 +527,7 @@ static int rasterize_hard_common(dressi_ctx* ctx, const float* clip, uint32_t n_
     if (int rc = ctx_workspace(ctx, 2, sizeof(int32_t) * 3 * nf1, &fi)) return rc;
     BinBuffers b;
     bin_carve(bins, g.n_tiles, cap, &b);
-    DRESSI_TRY_HIP(hipMemsetAsync(b.counts, 0, sizeof(uint32_t) * g.n_tiles, ctx->stream));
+    if (int rc = launch_zero(ctx->stream, b.counts, sizeof(uint32_t) * g.n_tiles)) return rc;
     if (n_faces) {
         hipLaunchKernelGGL(k_faces_to_i32, dim3(div_up(3 * n_faces, 256)), dim3(256), 0,
                            ctx->stream, faces, 3 * n_faces, n_verts, ctx->d_err, (int32_t*)fi);

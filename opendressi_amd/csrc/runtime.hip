@@ -1,5 +1,6 @@
 // runtime.hip -- context, errors, memory and host-side scene builders of the
 // C ABI (include/dressi_hip.h).
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -63,6 +64,24 @@ int ctx_workspace(dressi_ctx* ctx, int slot, size_t bytes, void** out) {
         ctx->ws_size[slot] = sz;
     }
     *out = ctx->ws_ptr[slot];
+    return DRESSI_OK;
+}
+
+__global__ __launch_bounds__(256) void k_zero_words(uint32_t* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        p[i] = 0u;
+    }
+}
+
+int launch_zero(hipStream_t s, void* p, size_t bytes) {
+    const size_t n = bytes / 4;
+    if (n == 0) {
+        return DRESSI_OK;
+    }
+    const uint32_t blocks = (uint32_t)std::min<size_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_zero_words, dim3(blocks), dim3(256), 0, s, (uint32_t*)p, n);
+    DRESSI_CHECK_LAUNCH();
     return DRESSI_OK;
 }
 

@@ -1,25 +1,30 @@
-// graph_c1.cpp -- the silhouette fit written with the graph API
-// (include/dressi_graph.h) and run by its generic executor: the graph of
-// examples/silhouette_optimization/run.cpp:229-437 (technique hardsoftras
-// with one peel, or aa; no regularisers), built with the same C++
-// expressions so that node creation order -- hence the backward's
-// summation order -- is the reference build's.
+// graph_c1.cpp -- the silhouette-fit example written against the graph API
+// (#include "dressi/dressi.h") and run by DressiAD: the graph of
+// examples/silhouette_optimization/run.cpp:229-437 (all views each
+// iteration; technique hardsoftras with one peel, or aa; the in-graph Adam,
+// optionally with the example's Laplacian / normal-consistency regulariser
+// terms), built with the same C++ expressions, static images from the
+// library's mesh builders, sent as CpuImage.
 //
 //   graph_c1 <in.bin> <out.bin>
-// in.bin: u32 V, F, Vt, Ft, N, S, samples, iters, technique (0 hsr, 1 aa);
-//         f32 radius, lr;
-//         pos0 {V,3}, faces {F,3}, tgt_pos {Vt,3}, tgt_faces {Ft,3}, mvps N x 16
-// out.bin: pos, m, v {V,3}, t, loss[iters] (sum of the loss image), grad0 {V,3}
+// in.bin:  u32 V, F, Vt, Ft, N, S, samples, iters, technique (0 hardsoftras,
+//          1 aa), packing (0 RSP, 1 Naive), regs (0 none, 1 regulariser terms);
+//          f32 radius, lr, laplacian weight, normal weight;
+//          pos0 {V,3}, faces {F,3}, tgt_pos {Vt,3}, tgt_faces {Ft,3}, mvps N x 16
+// out.bin: pos, m, v {V,3}, t, loss[iters] (sum of the loss image),
+//          grad0 {V,3} (first iteration), preds and targets {N,S,S} (last)
+// stdout:  "graph_c1: plan=<name> stages=<n> substages=<n> funcs=<n>"
 #include <cstdio>
-#include <cstring>
 #include <vector>
 
-#include "dressi_graph.h"
+#include "dressi/dressi.h"
+#include "dressi/mesh_utils.h"
 
 using namespace dressi;
 
 namespace {
 
+// TransformToClipVar (examples/common/geometry_utils.cpp:391-402)
 Variable ClipOf(const Variable& pos, const float* mvp) {
     Variable x = F::GetX(pos);
     Variable y = F::GetY(pos);
@@ -31,26 +36,27 @@ Variable ClipOf(const Variable& pos, const float* mvp) {
     return F::Vec4(row(0), row(1), row(2), row(3));
 }
 
-// {max_deg, V} incident faces, ascending, -1 padded
-std::vector<float> VertexFaces(const std::vector<float>& faces, uint32_t nv, uint32_t* deg) {
-    std::vector<std::vector<uint32_t>> inc(nv);
-    for (uint32_t f = 0; f < faces.size() / 3; f++) {
-        for (int k = 0; k < 3; k++) {
-            inc[(uint32_t)faces[f * 3 + k]].push_back(f);
+// TransformToClip on the host, (MVP * (p, 1)) summed over k in order
+CpuImage ClipImage(const std::vector<float>& pos, const float* m) {
+    const uint32_t n = uint32_t(pos.size() / 3);
+    CpuImage c(n, 1, 4);
+    for (uint32_t i = 0; i < n; i++) {
+        const float p[4] = {pos[i * 3 + 0], pos[i * 3 + 1], pos[i * 3 + 2], 1.f};
+        for (uint32_t r = 0; r < 4; r++) {
+            float acc = 0.f;
+            for (int k = 0; k < 4; k++) {
+                acc += m[k * 4 + r] * p[k];
+            }
+            c.at(i, 0, r) = acc;
         }
     }
-    uint32_t d = 1;
-    for (const auto& l : inc) {
-        d = std::max<uint32_t>(d, (uint32_t)l.size());
-    }
-    std::vector<float> out(size_t(d) * nv, -1.f);
-    for (uint32_t v = 0; v < nv; v++) {
-        for (size_t i = 0; i < inc[v].size(); i++) {
-            out[i * nv + v] = float(inc[v][i]);
-        }
-    }
-    *deg = d;
-    return out;
+    return c;
+}
+
+CpuImage Image(const std::vector<float>& d, uint32_t w, uint32_t h, uint32_t c) {
+    CpuImage img(w, h, c);
+    img.data = d;
+    return img;
 }
 
 template <typename T>
@@ -72,14 +78,16 @@ int main(int argc, char** argv) {
         if (!fi) {
             throw DressiError("cannot open input");
         }
-        uint32_t hdr[9];
-        float fp[2];
-        get(fi, hdr, 9);
-        get(fi, fp, 2);
+        uint32_t hdr[11];
+        float fp[4];
+        get(fi, hdr, 11);
+        get(fi, fp, 4);
         const uint32_t n_verts = hdr[0], n_faces = hdr[1], n_tverts = hdr[2], n_tfaces = hdr[3];
         const uint32_t n_views = hdr[4], S = hdr[5], samples = hdr[6], iters = hdr[7];
-        const bool aa = hdr[8] == 1;
-        const float radius_px = fp[0], lr = fp[1];
+        const bool hardsoft = hdr[8] == 0;
+        const bool naive = hdr[9] == 1;
+        const bool regs = hdr[10] == 1;
+        const float radius_px = fp[0], lr = fp[1], w_lap = fp[2], w_nrm = fp[3];
         std::vector<float> pos0(n_verts * 3), faces(n_faces * 3), tgt_pos(n_tverts * 3),
                 tgt_faces(n_tfaces * 3), mvps(n_views * 16);
         get(fi, pos0.data(), pos0.size());
@@ -90,22 +98,38 @@ int main(int argc, char** argv) {
         fclose(fi);
 
         const ImgSize screen = {S, S};
-        uint32_t deg = 0;
-        const std::vector<float> vf = VertexFaces(faces, n_verts, &deg);
+        const CpuImage s_faces_img = Image(faces, n_faces, 1, 3);
+        const CpuImage b_faces_img = Image(tgt_faces, n_tfaces, 1, 3);
+        const CpuImage b_vf_img = VertexFacesTex(b_faces_img, n_tverts);
+        const CpuImage s_vf_img = VertexFacesTex(s_faces_img, n_verts);
+        const CpuImage s_vn_img = VertexNeighborsTex(s_faces_img, n_verts);
+        const CpuImage s_fa_img = FaceNeighborsTex(s_faces_img);
 
         Variable b_ones(FLOAT, {n_tverts, 1});
         Variable b_faces_i(IVEC3, {n_tfaces, 1});
+        Variable b_faces_f(VEC3, {n_tfaces, 1});
+        Variable b_vtx_faces(FLOAT, b_vf_img.getImgSize());
+        Variable s_ones(FLOAT, {n_verts, 1});
+        Variable s_faces_i(IVEC3, {n_faces, 1});
         Variable s_faces_f(VEC3, {n_faces, 1});
-        Variable s_vtx_faces(FLOAT, {n_verts, deg});
+        Variable s_vtx_faces(FLOAT, s_vf_img.getImgSize());
+        Variable s_vtx_nbrs(FLOAT, s_vn_img.getImgSize());
+        Variable s_face_adj(VEC3, {n_faces, 1});
         Variable s_face_id(FLOAT, {n_faces * 3, 1});
         Variable s_faces_soft(IVEC3, {n_faces, 1});
         Variable pos(VEC3, {n_verts, 1});
         Variable adam_m(VEC3, {n_verts, 1});
         Variable adam_v(VEC3, {n_verts, 1});
         Variable adam_t(FLOAT, {1, 1});
+        Variable zero_seed(FLOAT, {1, 1});
 
         const float sigma_scale = 7.f / radius_px;
         const auto build_pred = [&](const Variable& clip_v) -> Variable {
+            if (!hardsoft) {
+                Variable mask = F::Rasterize(clip_v, s_ones, s_faces_i, screen);
+                Variable tri = F::RasterizeFaceId(clip_v, s_ones, s_faces_i, screen);
+                return F::AntiAlias(mask, tri, clip_v, s_faces_f, s_vtx_faces, adam_t, samples);
+            }
             Variable soft_clip = F::SoftClip(clip_v, s_faces_f, screen, radius_px);
             Variable tri0 = F::LookupFaces(clip_v, s_faces_f, s_vtx_faces, 0);
             Variable tri1 = F::LookupFaces(clip_v, s_faces_f, s_vtx_faces, 1);
@@ -164,23 +188,11 @@ int main(int argc, char** argv) {
             Variable soft_sil = 1.f - one_minus;
             return F::Max(hard, soft_sil);
         };
-
-        // technique aa (run.cpp:320-357): the prediction and the target are
-        // AntiAlias'd hard masks
-        uint32_t tdeg = 0;
-        const std::vector<float> tvf = VertexFaces(tgt_faces, n_tverts, &tdeg);
-        Variable b_faces_f(VEC3, {n_tfaces, 1});
-        Variable b_vtx_faces(FLOAT, {n_tverts, tdeg});
-        Variable s_ones(FLOAT, {n_verts, 1});
-        Variable s_faces_i(IVEC3, {n_faces, 1});
-        Variable zero_seed(FLOAT, {1, 1});
-        const auto build_pred_aa = [&](const Variable& clip_v) -> Variable {
-            Variable mask = F::Rasterize(clip_v, s_ones, s_faces_i, screen);
-            Variable tri = F::RasterizeFaceId(clip_v, s_ones, s_faces_i, screen);
-            return F::AntiAlias(mask, tri, clip_v, s_faces_f, s_vtx_faces, adam_t, samples);
-        };
-        const auto build_target_aa = [&](const Variable& tgt_clip) -> Variable {
+        const auto build_target = [&](const Variable& tgt_clip) -> Variable {
             Variable t_mask = F::Rasterize(tgt_clip, b_ones, b_faces_i, screen);
+            if (hardsoft) {
+                return F::StopGradient(t_mask);
+            }
             Variable t_tri = F::RasterizeFaceId(tgt_clip, b_ones, b_faces_i, screen);
             return F::StopGradient(
                     F::AntiAlias(t_mask, t_tri, tgt_clip, b_faces_f, b_vtx_faces, zero_seed, 0));
@@ -190,14 +202,8 @@ int main(int argc, char** argv) {
         std::vector<Variable> tgt_clips;
         for (uint32_t v = 0; v < n_views; v++) {
             tgt_clips.emplace_back(VEC4, ImgSize{n_tverts, 1});
-            if (aa) {
-                targets.push_back(build_target_aa(tgt_clips.back()));
-                preds.push_back(build_pred_aa(ClipOf(pos, mvps.data() + 16 * v)));
-            } else {
-                targets.push_back(F::StopGradient(
-                        F::Rasterize(tgt_clips.back(), b_ones, b_faces_i, screen)));
-                preds.push_back(build_pred(ClipOf(pos, mvps.data() + 16 * v)));
-            }
+            targets.push_back(build_target(tgt_clips.back()));
+            preds.push_back(build_pred(ClipOf(pos, mvps.data() + 16 * v)));
             Variable diff = targets[v] - preds[v];
             view_losses.push_back(diff * diff * (1.f / float(screen.w * screen.h)));
         }
@@ -206,14 +212,26 @@ int main(int argc, char** argv) {
         pos_mut.setRequiresGradRecursively();
 
         DressiAD ad;
+        ad.setPackingMode(naive ? DressiAD::PackingMode::Naive : DressiAD::PackingMode::RSP);
         ad.setLossVar(loss);
-        Variable g0;
+        bool state_registered = false;
         ad.setOptimizer([&](Variables xs, Variables gxs) {
-            if (xs.size() != 1 || xs[0] != pos) {
-                throw DressiError("expected pos as the only optimizer target");
-            }
+            DRESSI_CHECK(xs.size() == 1 && xs[0] == pos,
+                         "expected pos as the only optimizer target");
             Variable g = gxs[0];
-            g0 = g;
+            if (regs) {
+                const float inv_cnt = 1.f / float(n_verts * 3);
+                const auto rms = [&](const Variable& x) {
+                    return F::Sqrt(F::SumAll(x * x) * inv_cnt + 1e-24f);
+                };
+                Variable data_rms = rms(g);
+                Variable g_lap = pos - F::VertexNeighborMean(pos, s_vtx_nbrs);
+                Variable g_nrm = F::NormalConsistencyVertexGrad(
+                        F::NormalConsistencyFaceTerm(pos, s_faces_f, s_face_adj), pos, s_faces_f,
+                        s_vtx_faces);
+                g = g + g_lap * (data_rms / rms(g_lap) * w_lap) +
+                    g_nrm * (data_rms / rms(g_nrm) * w_nrm);
+            }
             const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
             Variable t_new = adam_t + 1.f;
             Variable m_new = adam_m * b1 + g * (1.f - b1);
@@ -221,82 +239,91 @@ int main(int argc, char** argv) {
             Variable bc1 = 1.f - F::Pow(F::Float(b1), t_new);
             Variable bc2 = 1.f - F::Pow(F::Float(b2), t_new);
             Variable step = (m_new / bc1) / (F::Sqrt(v_new / bc2) + eps) * lr;
-            ad.addUpdate(adam_m, m_new);
-            ad.addUpdate(adam_v, v_new);
-            ad.addUpdate(adam_t, t_new);
+            if (!state_registered) {
+                ad.addUpdate(adam_m, m_new);
+                ad.addUpdate(adam_v, v_new);
+                ad.addUpdate(adam_t, t_new);
+                state_registered = true;
+            }
             return Variables{pos - step};
         });
-        (void)ad.inputGrads();  // builds the backward and the optimizer graph
-        ad.markOutput(g0);
+        for (size_t i = 0; i < preds.size(); i++) {
+            ad.markOutput(targets[i]);
+            ad.markOutput(preds[i]);
+        }
+        ad.setGradOutputsEnabled(true);
 
-        // static leaves
-        std::vector<float> ones(n_tverts, 1.f), fid(n_faces * 3), fsoft(n_faces * 3);
-        for (uint32_t f = 0; f < n_faces; f++) {
-            for (uint32_t k = 0; k < 3; k++) {
-                fid[f * 3 + k] = float(f);
-                fsoft[f * 3 + k] = float(f * 3 + k);
-            }
-        }
-        ad.sendImg(b_ones, ones.data());
-        ad.sendImg(b_faces_i, tgt_faces.data());
-        ad.sendImg(s_faces_f, faces.data());
-        ad.sendImg(s_vtx_faces, vf.data());
-        ad.sendImg(s_face_id, fid.data());
-        ad.sendImg(s_faces_soft, fsoft.data());
-        if (aa) {
-            std::vector<float> s_ones_v(n_verts, 1.f), zero_v(1, 0.f);
-            ad.sendImg(b_faces_f, tgt_faces.data());
-            ad.sendImg(b_vtx_faces, tvf.data());
-            ad.sendImg(s_ones, s_ones_v.data());
-            ad.sendImg(s_faces_i, faces.data());
-            ad.sendImg(zero_seed, zero_v.data());
-        }
-        for (uint32_t v = 0; v < n_views; v++) {
-            const float* m = mvps.data() + 16 * v;
-            std::vector<float> c(size_t(n_tverts) * 4);
-            for (uint32_t i = 0; i < n_tverts; i++) {
-                const float p[4] = {tgt_pos[i * 3 + 0], tgt_pos[i * 3 + 1], tgt_pos[i * 3 + 2], 1.f};
-                for (int r = 0; r < 4; r++) {
-                    float acc = 0.f;
-                    for (int k = 0; k < 4; k++) {
-                        acc += m[k * 4 + r] * p[k];
-                    }
-                    c[size_t(i) * 4 + r] = acc;
+        // one-time uploads (run.cpp:440-471)
+        ad.sendImg(b_ones, CpuImage(n_tverts, 1, 1, 1.f));
+        ad.sendImg(b_faces_i, b_faces_img);
+        ad.sendImg(b_faces_f, b_faces_img);
+        ad.sendImg(b_vtx_faces, b_vf_img);
+        ad.sendImg(s_ones, CpuImage(n_verts, 1, 1, 1.f));
+        ad.sendImg(s_faces_i, s_faces_img);
+        ad.sendImg(s_faces_f, s_faces_img);
+        ad.sendImg(s_vtx_faces, s_vf_img);
+        ad.sendImg(s_vtx_nbrs, s_vn_img);
+        ad.sendImg(s_face_adj, s_fa_img);
+        if (hardsoft) {
+            CpuImage face_id_img(n_faces * 3, 1, 1);
+            CpuImage faces_soft_img(n_faces, 1, 3);
+            for (uint32_t f = 0; f < n_faces; f++) {
+                for (uint32_t k = 0; k < 3; k++) {
+                    face_id_img.at(f * 3 + k, 0, 0) = float(f);
+                    faces_soft_img.at(f, 0, k) = float(f * 3 + k);
                 }
             }
-            ad.sendImg(tgt_clips[v], c.data());
+            ad.sendImg(s_face_id, face_id_img);
+            ad.sendImg(s_faces_soft, faces_soft_img);
         }
-        std::vector<float> zeros(n_verts * 3, 0.f), zero1(1, 0.f);
-        ad.sendImg(pos, pos0.data());
-        ad.sendImg(adam_m, zeros.data());
-        ad.sendImg(adam_v, zeros.data());
-        ad.sendImg(adam_t, zero1.data());
+        ad.sendImg(adam_m, CpuImage(n_verts, 1, 3, 0.f));
+        ad.sendImg(adam_v, CpuImage(n_verts, 1, 3, 0.f));
+        ad.sendImg(adam_t, CpuImage(1, 1, 1, 0.f));
+        if (!hardsoft) {
+            ad.sendImg(zero_seed, CpuImage(1, 1, 1, 0.f));
+        }
+        for (uint32_t v = 0; v < n_views; v++) {
+            ad.sendImg(tgt_clips[v], ClipImage(tgt_pos, mvps.data() + 16 * v));
+        }
 
-        std::vector<float> losses(iters), grad0;
+        // iterations: the starting positions go with the first step; every
+        // step returns its loss image with the same synchronisation
+        const CpuImage pos_img = Image(pos0, n_verts, 1, 3);
+        std::vector<float> losses(iters);
+        CpuImage grad0;
         for (uint32_t it = 0; it < iters; it++) {
-            ad.execStep();
-            const std::vector<float> li = ad.recvImg(loss);
+            std::vector<std::pair<Variable, CpuImageView>> sends;
+            if (it == 0) {
+                sends.emplace_back(pos, CpuImageView(pos_img));
+            }
+            const CpuImage li = ad.execStepWithSendsAndRecvImgsStacked(sends, {loss});
             double s = 0.0;
-            for (float x : li) {
+            for (float x : li.data) {
                 s += x;
             }
             losses[it] = float(s);
             if (it == 0) {
-                grad0 = ad.recvImg(g0);
+                grad0 = ad.recvImg(ad.inputGrads().at(0).second);
             }
         }
+        const CpuImage pred_img = ad.recvImgsStacked(preds);
+        const CpuImage tgt_img = ad.recvImgsStacked(targets);
         FILE* fo = fopen(argv[2], "wb");
         if (!fo) {
             throw DressiError("cannot open output");
         }
         for (const Variable& v : {pos, adam_m, adam_v, adam_t}) {
-            const std::vector<float> d = ad.recvImg(v);
-            fwrite(d.data(), sizeof(float), d.size(), fo);
+            const CpuImage d = ad.recvImg(v);
+            fwrite(d.data.data(), sizeof(float), d.data.size(), fo);
         }
         fwrite(losses.data(), sizeof(float), losses.size(), fo);
-        fwrite(grad0.data(), sizeof(float), grad0.size(), fo);
+        fwrite(grad0.data.data(), sizeof(float), grad0.data.size(), fo);
+        fwrite(pred_img.data.data(), sizeof(float), pred_img.data.size(), fo);
+        fwrite(tgt_img.data.data(), sizeof(float), tgt_img.data.size(), fo);
         fclose(fo);
-        printf("graph_c1: %zu functions per step, %u iterations\n", ad.getFuncCount(), iters);
+        printf("graph_c1: plan=%s stages=%zu substages=%zu funcs=%zu device=%s\n",
+               ad.getPlanName().c_str(), ad.getStageCount(), ad.getSubStageCount(),
+               ad.getFuncCount(), ad.getDeviceName().c_str());
     } catch (const std::exception& e) {
         fprintf(stderr, "graph_c1: %s\n", e.what());
         return 1;

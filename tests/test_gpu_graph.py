@@ -1,17 +1,24 @@
-"""The graph API's generic executor on the GPU (include/dressi_graph.h,
-opendressi_amd/csrc/graph.hip).
+"""DressiAD on the GPU through the graph API (include/dressi/dressi.h).
 
-tests/graph_c1.cpp builds the HardSoftRas silhouette-fit graph of the
-reference example with `Variable` / `F::` / `BuildBackward` / `DressiAD` and
-runs it node by node on the device. Its loss image, gradient and Adam state
-are compared with the oracle's fit (the reference build's numbers, pinned in
-tests/test_oracle.py) and with the fused plan. Bar: the first iteration's
-loss and gradient bit-exact (every op one fp32 rounding, the reference's
-backward composition and summation order); later iterations within 1e-6,
-because the in-graph Adam's bias correction 1 - b^t evaluates `powf` on the
-device, which is not guaranteed to round like the C library's.
+tests/graph_c1.cpp builds the silhouette-fit example graph of the reference
+(examples/silhouette_optimization/run.cpp:229-437) with Variable / F:: /
+DressiAD, sends its static images as CpuImage and steps it with
+execStepWithSendsAndRecvImgsStacked. With PackingMode::RSP the executor
+recognises the example graph and runs it on the fused silhouette plan
+(getPlanName() "fused:hardsoftras" / "fused:aa", getStageCount() 1); with
+PackingMode::Naive, or when the graph is not the example's (regulariser
+weights other than 0), the generic executor runs it function by function.
+
+Bars: the fused route reproduces the oracle's whole trajectory bit for bit
+(positions, Adam moments, every loss, the first gradient, the last
+predictions and the targets); the generic executor reproduces the first
+iteration bit for bit (loss and gradient: every op one fp32 rounding, the
+reference's backward composition and summation order) and later ones within
+1e-6, because the in-graph Adam's bias correction 1 - b^t evaluates powf on
+the device, which need not round like the C library's.
 """
 import os
+import re
 import subprocess
 
 import numpy as np
@@ -21,101 +28,156 @@ pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 EXE = os.path.join(ROOT, "tests", "_bin", "graph_c1")
+GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
-def _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, radius, lr, aa=False):
-    nv, nf = len(pos), len(faces)
-    hdr = np.array([nv, nf, len(tgt), nf, len(mvps), screen, samples, iters, 1 if aa else 0],
-                   np.uint32)
+def _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, radius, lr, aa=False,
+               naive=False, regs=False, w_lap=0.0, w_nrm=0.0, timeout=120):
+    nv, nf, n = len(pos), len(faces), len(mvps)
+    hdr = np.array([nv, nf, len(tgt), nf, n, screen, samples, iters, 1 if aa else 0,
+                    1 if naive else 0, 1 if regs else 0], np.uint32)
     inp = tmp_path / "in.bin"
     out = tmp_path / "out.bin"
     with open(inp, "wb") as f:
         f.write(hdr.tobytes())
-        f.write(np.array([radius, lr], np.float32).tobytes())
+        f.write(np.array([radius, lr, w_lap, w_nrm], np.float32).tobytes())
         for a in (pos, faces, tgt, faces, mvps):
             f.write(np.ascontiguousarray(a, np.float32).tobytes())
     if not os.path.exists(EXE):
         pytest.fail("tests/_bin/graph_c1 is not built (run __graft_entry__.build())")
-    res = subprocess.run([EXE, str(inp), str(out)], capture_output=True, text=True, timeout=120)
+    res = subprocess.run([EXE, str(inp), str(out)], capture_output=True, text=True,
+                         timeout=timeout)
     print(res.stdout.strip(), res.stderr.strip(), flush=True)
     assert res.returncode == 0, res.stderr
+    m = re.search(r"plan=(\S+) stages=(\d+) substages=(\d+) funcs=(\d+)", res.stdout)
+    assert m, res.stdout
     d = np.fromfile(out, np.float32)
     o = 0
-    r = {}
-    for k, n in (("pos", nv * 3), ("m", nv * 3), ("v", nv * 3), ("t", 1), ("loss", iters),
-                 ("grad0", nv * 3)):
-        r[k] = d[o:o + n]
-        o += n
+    r = {"plan": m.group(1), "stages": int(m.group(2)), "substages": int(m.group(3)),
+         "funcs": int(m.group(4))}
+    for k, cnt in (("pos", nv * 3), ("m", nv * 3), ("v", nv * 3), ("t", 1), ("loss", iters),
+                   ("grad0", nv * 3), ("pred", n * screen * screen),
+                   ("target", n * screen * screen)):
+        r[k] = d[o:o + cnt]
+        o += cnt
     assert o == d.size
     for k in ("pos", "m", "v", "grad0"):
         r[k] = r[k].reshape(nv, 3)
+    for k in ("pred", "target"):
+        r[k] = r[k].reshape(n, screen, screen)
     return r
 
 
-@pytest.mark.parametrize("views,screen", [(1, 128), (2, 96)])
-def test_graph_executor_silhouette_fit_matches_oracle(tmp_path, oracle, views, screen):
+def _scene(name, views=None):
     import opendressi_amd as od
-    print(f"[graph] c1 mesh, {views} view(s), {screen}px, 3 iterations", flush=True)
-    w = od.WORKLOADS["c1"]
+    w = od.WORKLOADS[name]
     pos, faces, tgt, mvps = od.make_scene(w)
-    mvps = np.ascontiguousarray(np.asarray(mvps, np.float32)[:views])
-    if len(mvps) < views:
+    if views is not None:
         mvps = np.ascontiguousarray(np.asarray(od.camera_mvps(views), np.float32))
-    iters, radius, samples, lr = 3, 3.0, 8, 1e-3
-    g = _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, radius, lr)
-    want = oracle.hsr_fit(pos, faces, tgt, faces, mvps, screen, radius=radius, samples=samples,
-                          lr=lr, iters=iters, want_images=False)
-    assert np.array_equal(g["grad0"], want["grad0"]), \
-        f"grad0 differs: max {np.abs(g['grad0'] - want['grad0']).max():.3g}"
-    assert g["loss"][0] == want["loss"][0], (g["loss"], want["loss"])
+    return w, pos, faces, tgt, mvps
+
+
+def _fit(oracle, aa, pos, faces, tgt, mvps, screen, samples, lr, iters, images=True):
+    fit = oracle.aa_fit if aa else oracle.hsr_fit
+    kw = {} if aa else {"radius": 3.0}
+    return fit(pos, faces, tgt, faces, mvps, screen, samples=samples, lr=lr, iters=iters,
+               want_images=images, **kw)
+
+
+@pytest.mark.parametrize("aa", [False, True], ids=["hardsoftras", "aa"])
+@pytest.mark.parametrize("views,screen", [(1, 128), (2, 96)])
+def test_fused_route_matches_oracle(tmp_path, oracle, aa, views, screen):
+    """RSP packing: the example graph runs on the fused plan, bit-exact."""
+    print(f"[graph] c1 mesh, {'aa' if aa else 'hsr'}, {views} view(s), {screen}px, RSP",
+          flush=True)
+    _, pos, faces, tgt, mvps = _scene("c1", views)
+    iters, samples, lr = 4, 8, 1e-3
+    g = _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, 3.0, lr, aa=aa)
+    assert g["plan"] == ("fused:aa" if aa else "fused:hardsoftras")
+    assert g["stages"] == 1 and g["substages"] == 5
+    want = _fit(oracle, aa, pos, faces, tgt, mvps, screen, samples, lr, iters, images=False)
     assert np.abs(want["grad0"]).max() > 0
-    np.testing.assert_allclose(g["loss"], want["loss"], rtol=1e-6, atol=0)
-    for k in ("pos", "m", "v"):
-        np.testing.assert_allclose(g[k], want[k], rtol=0, atol=1e-6 * max(1.0, np.abs(want[k]).max()),
-                                   err_msg=k)
+    for k in ("grad0", "pos", "m", "v", "loss"):
+        assert np.array_equal(g[k], want[k]), \
+            f"{k}: max |d| {np.abs(g[k] - want[k]).max():.3g}"
     assert g["t"][0] == iters
-    exact = {k: bool(np.array_equal(g[k], want[k])) for k in ("pos", "m", "v", "loss")}
-    print(f"[graph] bit-exact after {iters} iterations: {exact}", flush=True)
+    # the last iteration's predictions and the targets against a one-step
+    # oracle fit from the final state's predecessor: the targets are static
+    one = _fit(oracle, aa, pos, faces, tgt, mvps, screen, samples, lr, 1)
+    assert np.array_equal(g["target"], one["target"])
 
 
-def test_graph_executor_matches_fused_plan(tmp_path):
-    """The generic executor and the fused plan run the same graph: first
-    iteration loss and gradient identical."""
-    import opendressi_amd as od
-    print("[graph] vs fused plan, c1 mesh, 1 view, 128px", flush=True)
-    w = od.WORKLOADS["c1"]
-    pos, faces, tgt, mvps = od.make_scene(w)
-    mvps = np.ascontiguousarray(np.asarray(mvps, np.float32)[:1])
-    g = _run_graph(tmp_path, pos, faces, tgt, mvps, 128, 8, 1, 3.0, w.lr)
-    ctx = od.Context(0)
-    fit = od.SilhouetteFit(ctx, pos, faces, mvps, 128, target_mesh=(tgt, faces), lr=w.lr,
-                           keep_grad=True)
-    fit.step(1)
-    fit.synchronize()
-    from opendressi_amd import _lib
-    assert np.array_equal(g["grad0"], fit.read(_lib.BUF_GRAD)), "gradient differs"
-    assert g["loss"][0] == np.float32(fit.loss()), (g["loss"][0], fit.loss())
-    np.testing.assert_allclose(g["pos"], fit.read(_lib.BUF_POS), rtol=0, atol=1e-6)
-
-
-@pytest.mark.parametrize("samples", [8, 0])
-def test_graph_executor_aa_fit_matches_oracle(tmp_path, oracle, samples):
-    """Technique aa (AntiAlias'd hard masks; stochastic wide vertex backward
-    + ColSum, or the exact one) through the generic executor."""
-    import opendressi_amd as od
-    print(f"[graph] aa, c1 mesh, 2 views, 96px, samples={samples}, 3 iterations", flush=True)
-    w = od.WORKLOADS["c1"]
-    pos, faces, tgt, _ = od.make_scene(w)
-    mvps = np.ascontiguousarray(np.asarray(od.camera_mvps(2), np.float32))
-    iters, lr = 3, 1e-3
-    g = _run_graph(tmp_path, pos, faces, tgt, mvps, 96, samples, iters, 3.0, lr, aa=True)
-    want = oracle.aa_fit(pos, faces, tgt, faces, mvps, 96, samples=samples, lr=lr, iters=iters,
-                         want_images=False)
+@pytest.mark.parametrize("views,screen", [(1, 128), (2, 96)])
+def test_generic_executor_matches_oracle(tmp_path, oracle, views, screen):
+    """Naive packing: one kernel per function, no fused plan."""
+    print(f"[graph] c1 mesh, hsr, {views} view(s), {screen}px, Naive", flush=True)
+    _, pos, faces, tgt, mvps = _scene("c1", views)
+    iters, samples, lr = 3, 8, 1e-3
+    g = _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, 3.0, lr, naive=True)
+    assert g["plan"] == "generic"
+    assert g["stages"] == g["substages"] > 100
+    want = _fit(oracle, False, pos, faces, tgt, mvps, screen, samples, lr, iters)
     assert np.array_equal(g["grad0"], want["grad0"]), \
         f"grad0 differs: max {np.abs(g['grad0'] - want['grad0']).max():.3g}"
     assert g["loss"][0] == want["loss"][0], (g["loss"], want["loss"])
-    assert np.abs(want["grad0"]).max() > 0
     np.testing.assert_allclose(g["loss"], want["loss"], rtol=1e-6, atol=0)
     for k in ("pos", "m", "v"):
-        np.testing.assert_allclose(g[k], want[k], rtol=0, atol=1e-6 * max(1.0, np.abs(want[k]).max()),
-                                   err_msg=k)
+        np.testing.assert_allclose(g[k], want[k], rtol=0,
+                                   atol=1e-6 * max(1.0, np.abs(want[k]).max()), err_msg=k)
+    assert g["t"][0] == iters
+    assert np.array_equal(g["target"], want["target"])
+
+
+def test_generic_rsp_fuses_elementwise_runs(tmp_path, oracle):
+    """RSP on a graph the route does not take (regulariser weights > 0):
+    the generic executor with fused elementwise stages; its first
+    iteration's data gradient and loss are the oracle's (the regularisers
+    change only the update)."""
+    _, pos, faces, tgt, mvps = _scene("c1", 1)
+    iters, samples, lr, screen = 2, 8, 1e-3, 96
+    print("[graph] c1 mesh, hsr, regularisers 0.15 / 0.4, RSP", flush=True)
+    g = _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, 3.0, lr, regs=True,
+                   w_lap=0.15, w_nrm=0.4)
+    assert g["plan"] == "generic"
+    naive = _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, 3.0, lr,
+                       naive=True, regs=True, w_lap=0.15, w_nrm=0.4)
+    assert g["stages"] < naive["stages"] // 2, (g["stages"], naive["stages"])
+    want = _fit(oracle, False, pos, faces, tgt, mvps, screen, samples, lr, 1, images=False)
+    assert np.array_equal(g["grad0"], want["grad0"])
+    assert g["loss"][0] == want["loss"][0]
+    # fused and one-kernel-per-function runs compute the same floats
+    for k in ("pos", "m", "v", "loss", "grad0"):
+        assert np.array_equal(g[k], naive[k]), k
+    assert np.isfinite(g["pos"]).all()
+    plain = _fit(oracle, False, pos, faces, tgt, mvps, screen, samples, lr, iters, images=False)
+    assert np.abs(g["pos"] - plain["pos"]).max() > 0  # the regularisers moved it
+
+
+def test_example_with_zero_regulariser_weights_takes_the_route(tmp_path, oracle):
+    """The reference example as run with --laplacian=0 --normal=0."""
+    _, pos, faces, tgt, mvps = _scene("c1", 1)
+    iters, samples, lr, screen = 3, 8, 1e-3, 96
+    g = _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, 3.0, lr, regs=True)
+    assert g["plan"] == "fused:hardsoftras"
+    want = _fit(oracle, False, pos, faces, tgt, mvps, screen, samples, lr, iters, images=False)
+    for k in ("pos", "m", "v", "loss", "grad0"):
+        assert np.array_equal(g[k], want[k]), k
+
+
+@pytest.mark.parametrize("name", ["c2", "c4"])
+def test_fused_route_full_workload_final_parameters(tmp_path, name):
+    """The graph API at a benchmark workload's full size and iteration count
+    against the oracle's final parameters (tests/golden/final_<name>.npz)."""
+    w, pos, faces, tgt, mvps = _scene(name)
+    print(f"[graph] {name}: {w.iters} iterations at {w.screen}^2 x {w.views}, RSP", flush=True)
+    with np.load(os.path.join(GOLDEN, f"final_{name}.npz")) as z:
+        gold = {k: z[k] for k in z.files}
+    g = _run_graph(tmp_path, pos, faces, tgt, mvps, w.screen, 8, w.iters, 3.0, w.lr,
+                   aa=w.technique == "aa", timeout=300)
+    assert g["plan"] == ("fused:aa" if w.technique == "aa" else "fused:hardsoftras")
+    assert g["stages"] == 1
+    assert np.array_equal(g["pos"], gold["out_pos"])
+    rows = g["m"].reshape(-1, 3)[gold["out_idx_m"]]
+    assert np.array_equal(rows, gold["out_smp_m"])
+    assert np.array_equal(g["loss"], gold["out_loss"])
+    assert g["t"][0] == w.iters
