@@ -72,23 +72,26 @@ def build(verbose: bool = False) -> str:
 
 
 def build_graph_test(verbose: bool = False) -> str:
-    """The graph-API test program (tests/graph_c1.cpp), linked against the
-    library; plain C++ (the graph API header needs no HIP headers)."""
-    src = os.path.join(ROOT, "tests", "graph_c1.cpp")
+    """The graph-API test programs (tests/graph_c1.cpp, tests/graph_ops.cpp),
+    linked against the library; plain C++ (the graph API headers need no HIP
+    headers)."""
     out_dir = os.path.join(ROOT, "tests", "_bin")
     os.makedirs(out_dir, exist_ok=True)
-    exe = os.path.join(out_dir, "graph_c1")
-    cmd = ["g++", "-std=c++17", "-O2", "-ffp-contract=off", "-I", os.path.join(ROOT, "include"),
-           "-o", exe + ".tmp", src, "-L", PKG, "-ldressi_hip",
-           "-Wl,-rpath,$ORIGIN/../../opendressi_amd"]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("g++ failed building tests/_bin/graph_c1")
-    os.replace(exe + ".tmp", exe)
-    return exe
+    exe = ""
+    for name in ("graph_c1", "graph_ops"):
+        src = os.path.join(ROOT, "tests", name + ".cpp")
+        exe = os.path.join(out_dir, name)
+        cmd = ["g++", "-std=c++17", "-O2", "-ffp-contract=off", "-I", os.path.join(ROOT, "include"),
+               "-o", exe + ".tmp", src, "-L", PKG, "-ldressi_hip",
+               "-Wl,-rpath,$ORIGIN/../../opendressi_amd"]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            sys.stderr.write(res.stdout + res.stderr)
+            raise RuntimeError(f"g++ failed building tests/_bin/{name}")
+        os.replace(exe + ".tmp", exe)
+    return out_dir
 
 
 if __name__ == "__main__":

@@ -271,6 +271,54 @@ __global__ __launch_bounds__(64) void k_fill(float* y, uint32_t n, float v0, flo
     }
 }
 
+// Elementwise ops on matrix-typed images (more than 4 components): one
+// thread per (pixel, component); 1-component and {1,1} inputs broadcast
+struct WideIn {
+    const float* p;
+    uint32_t nc;
+    uint32_t uniform;
+};
+struct WideArgs {
+    int op;
+    uint32_t n_in, ny;
+    size_t n_px;
+    WideIn in[kMaxInputs];
+    float* y;
+};
+
+__global__ __launch_bounds__(256) void k_wide(WideArgs A) {
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= A.n_px * A.ny) {
+        return;
+    }
+    const size_t p = q / A.ny;
+    const uint32_t c = (uint32_t)(q % A.ny);
+    float v[kMaxInputs];
+    for (uint32_t k = 0; k < A.n_in; k++) {
+        const WideIn in = A.in[k];
+        v[k] = in.p[(in.uniform ? 0 : p * in.nc) + (in.nc == 1 ? 0 : c)];
+    }
+    float r = 0.f;
+    switch ((Op)A.op) {
+        case Op::kAdd: r = v[0] + v[1]; break;
+        case Op::kSub: r = v[0] - v[1]; break;
+        case Op::kMul: r = v[0] * v[1]; break;
+        case Op::kDiv: r = v[0] / v[1]; break;
+        case Op::kNeg: r = -v[0]; break;
+        case Op::kCopy: r = v[0]; break;
+        case Op::kSumPw: {
+            float acc = 0.f;
+            for (uint32_t k = 0; k < A.n_in; k++) {
+                acc += v[k];
+            }
+            r = acc;
+            break;
+        }
+        default: break;
+    }
+    A.y[q] = r;
+}
+
 // Reduce2x2Sum: each output pixel sums its 2x2 source block in row order
 // from 0 (the reference CPU kernel's accumulation order).
 __global__ __launch_bounds__(256) void k_reduce2x2(const float* x, uint32_t sw, uint32_t sh,
@@ -838,12 +886,8 @@ struct DressiAD::Impl {
         for (const auto& f : funcs) {
             const auto& fn = NodeAccess::Node(f);
             const auto y = fn->y.lock();
-            const bool ew = IsElementwise(fn->op);
-            if (ew) {
-                DRESSI_CHECK(NumComponents(y->vtype) <= 4,
-                             fn->name + ": elementwise ops on matrix-typed images are not "
-                                        "supported by the HIP executor");
-            }
+            // matrix-typed elementwise ops run alone (k_wide)
+            const bool ew = IsElementwise(fn->op) && NumComponents(y->vtype) <= 4;
             bool joined = false;
             if (fuse && ew && !out.empty() && out.back().fused &&
                 out.back().fns.size() < (size_t)kMaxStepInstrs) {
@@ -1279,8 +1323,32 @@ struct DressiAD::Impl {
                 throw DressiError(fn.name +
                                   " belongs to a custom raster pass, which the HIP executor "
                                   "does not run");
+            case Op::kAdd:
+            case Op::kSub:
+            case Op::kMul:
+            case Op::kDiv:
+            case Op::kNeg:
+            case Op::kCopy:
+            case Op::kSumPw: {
+                WideArgs A{};
+                A.op = (int)fn.op;
+                A.n_in = (uint32_t)fn.xs.size();
+                A.ny = ny;
+                A.n_px = n_px;
+                DRESSI_CHECK(A.n_in <= (uint32_t)kMaxInputs, fn.name + ": more than 4 inputs");
+                for (uint32_t k = 0; k < A.n_in; k++) {
+                    A.in[k] = {in[k], nc((int)k), xn[k]->size.isUniform() ? 1u : 0u};
+                    DRESSI_CHECK(A.in[k].nc == 1 || A.in[k].nc == ny,
+                                 fn.name + ": component count mismatch");
+                }
+                A.y = out;
+                hipLaunchKernelGGL(k_wide, dim3(blocks256(n_px * ny)), dim3(256), 0, s, A);
+                break;
+            }
             default:
-                throw DressiError(fn.name + ": no kernel");
+                throw DressiError(fn.name + (IsElementwise(fn.op)
+                                                     ? ": not defined on matrix-typed images"
+                                                     : ": no kernel"));
         }
         check_hip(hipGetLastError(), "kernel launch");
     }
