@@ -712,6 +712,86 @@ __device__ __forceinline__ void visit_staged(const SoftRec* recs, uint32_t f, ui
     }
 }
 
+// Phase B of one 8x8 block (lane = pixel): for the lanes with `need` (best
+// depth >= 0.5 after phase A), the fragments phase A did not fold.
+__device__ __forceinline__ void phase_b(const SoftRec* recs, const CullRec* cull, const BinView& bv,
+                                        int bx, int by, float radius, const float* prev,
+                                        uint32_t width, bool need, ResolveLds& lds,
+                                        PixelBest& best) {
+    const int lane = threadIdx.x & 63;
+    const int px = bx + (lane & 7);
+    const int py = by + (lane >> 3);
+    const float near_d = radius;  // + the face's a_margin
+    const float cx0 = (float)bx + 0.5f, cx1 = (float)bx + 7.5f;
+    const float cy0 = (float)by + 0.5f, cy1 = (float)by + 7.5f;
+    // Near faces (the hard triangle within r + a_margin of the block, or
+    // folded in phase A) are folded as they come. Far faces give depth
+    // exactly 1.0 at every pixel they cover, so among them the highest face
+    // index wins: they are collected (up to kFarCap; the rest fold at once),
+    // sorted by descending index and folded until no pixel that needs
+    // phase B can still take a later (lower) one.
+    uint32_t n_far = 0;
+    for (uint32_t base = 0; base < bv.n; base += 64) {
+        const uint32_t e = base + (uint32_t)lane;
+        uint32_t f = 0;
+        bool keep = false, in_a = false, near = false;
+        if (e < bv.n) {
+            f = bv.implicit ? e : (base == 0 ? bv.pre : bv.list[e]);
+            const CullLoad l = load_cull<true>(recs, cull, f);
+            keep = cull_soft(l, bx, by);
+            in_a = keep && cull_in_a(l, bx, by, false);
+            near = in_a || hard_bbox_near(l.hx, l.hy, l.w[15], cx0, cx1, cy0, cy1, near_d);
+        }
+        bool far = keep && !near;
+        const uint64_t mf0 = __ballot(far);
+        far = far && n_far + lanes_below(mf0) < kFarCap;
+        const uint64_t mf = __ballot(far);
+        if (far) {
+            lds.far[n_far + lanes_below(mf)] = f + 1u;
+        }
+        n_far += (uint32_t)__popcll(mf);
+        const uint64_t ma = __ballot(in_a);
+        const uint64_t mn = __ballot(near);
+        visit_staged(recs, f, __ballot(keep && !far), lds, [&](const SoftRec& r, uint32_t fj, int j) {
+            if (need) {
+                frag_phase_b(r, fj, px, py, radius, prev, width, (mn >> j) & 1ull,
+                             (ma >> j) & 1ull, best);
+            }
+        });
+    }
+    if (n_far) {
+        __syncthreads();
+        sort_desc(lds.far, n_far);
+        for (uint32_t b0 = 0; b0 < n_far; b0 += (uint32_t)kStage) {
+            // the batch's first face has the highest index left
+            const uint32_t f0 = lds.far[b0] - 1u;
+            if (!__any(need && best.key > depth_key(1.f, f0))) {
+                break;
+            }
+            const uint32_t cnt = min((uint32_t)kStage, n_far - b0);
+            uint32_t f = 0;
+            if ((uint32_t)lane < cnt) {
+                f = lds.far[b0 + lane] - 1u;
+                const float4* src = (const float4*)(recs + f);
+                float4* dst = (float4*)&lds.rec[lane];
+#pragma unroll
+                for (int i = 0; i < (int)(sizeof(SoftRec) / 16); i++) {
+                    dst[i] = src[i];
+                }
+            }
+            __syncthreads();
+            for (uint32_t j = 0; j < cnt; j++) {
+                const uint32_t fj = (uint32_t)__builtin_amdgcn_readlane((int)f, (int)j);
+                const SoftRec r = lds.rec[j];
+                if (need) {
+                    frag_phase_b(r, fj, px, py, radius, prev, width, false, false, best);
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
 // Resolves the winner of every pixel of one 8x8 block (lane = pixel, one
 // wave, no cross-wave synchronisation). `recs` / `cull` point at the view's
 // records. Phase A folds the class 0 / 2 fragments of faces whose A-box
@@ -790,75 +870,7 @@ __device__ __forceinline__ PixelBest resolve_block(const SoftRec* recs, const Cu
     if (!__any(need)) {
         return best;
     }
-    const float near_d = radius;  // + the face's a_margin
-    const float cx0 = (float)bx + 0.5f, cx1 = (float)bx + 7.5f;
-    const float cy0 = (float)by + 0.5f, cy1 = (float)by + 7.5f;
-    // Near faces (the hard triangle within r + a_margin of the block, or
-    // folded in phase A) are folded as they come. Far faces give depth
-    // exactly 1.0 at every pixel they cover, so among them the highest face
-    // index wins: they are collected (up to kFarCap; the rest fold at once),
-    // sorted by descending index and folded until no pixel that needs
-    // phase B can still take a later (lower) one.
-    uint32_t n_far = 0;
-    for (uint32_t base = 0; base < bv.n; base += 64) {
-        const uint32_t e = base + (uint32_t)lane;
-        uint32_t f = 0;
-        bool keep = false, in_a = false, near = false;
-        if (e < bv.n) {
-            f = bv.implicit ? e : (base == 0 ? bv.pre : bv.list[e]);
-            const CullLoad l = load_cull<true>(recs, cull, f);
-            keep = cull_soft(l, bx, by);
-            in_a = keep && cull_in_a(l, bx, by, false);
-            near = in_a || hard_bbox_near(l.hx, l.hy, l.w[15], cx0, cx1, cy0, cy1, near_d);
-        }
-        bool far = keep && !near;
-        const uint64_t mf0 = __ballot(far);
-        far = far && n_far + lanes_below(mf0) < kFarCap;
-        const uint64_t mf = __ballot(far);
-        if (far) {
-            lds.far[n_far + lanes_below(mf)] = f + 1u;
-        }
-        n_far += (uint32_t)__popcll(mf);
-        const uint64_t ma = __ballot(in_a);
-        const uint64_t mn = __ballot(near);
-        visit_staged(recs, f, __ballot(keep && !far), lds, [&](const SoftRec& r, uint32_t fj, int j) {
-            if (need) {
-                frag_phase_b(r, fj, px, py, radius, prev, width, (mn >> j) & 1ull,
-                             (ma >> j) & 1ull, best);
-            }
-        });
-    }
-    if (n_far) {
-        __syncthreads();
-        sort_desc(lds.far, n_far);
-        for (uint32_t b0 = 0; b0 < n_far; b0 += (uint32_t)kStage) {
-            // the batch's first face has the highest index left
-            const uint32_t f0 = lds.far[b0] - 1u;
-            if (!__any(need && best.key > depth_key(1.f, f0))) {
-                break;
-            }
-            const uint32_t cnt = min((uint32_t)kStage, n_far - b0);
-            uint32_t f = 0;
-            if ((uint32_t)lane < cnt) {
-                f = lds.far[b0 + lane] - 1u;
-                const float4* src = (const float4*)(recs + f);
-                float4* dst = (float4*)&lds.rec[lane];
-#pragma unroll
-                for (int i = 0; i < (int)(sizeof(SoftRec) / 16); i++) {
-                    dst[i] = src[i];
-                }
-            }
-            __syncthreads();
-            for (uint32_t j = 0; j < cnt; j++) {
-                const uint32_t fj = (uint32_t)__builtin_amdgcn_readlane((int)f, (int)j);
-                const SoftRec r = lds.rec[j];
-                if (need) {
-                    frag_phase_b(r, fj, px, py, radius, prev, width, false, false, best);
-                }
-            }
-            __syncthreads();
-        }
-    }
+    phase_b(recs, cull, bv, bx, by, radius, prev, width, need, lds, best);
     return best;
 }
 
