@@ -285,6 +285,10 @@ BENCH_KEYS = ("example", "device", "platform", "os", "cpu", "cpu_cores", "ram_gb
               "substages", "stages", "technique", "screen", "views", "iters", "samples", "peels",
               "single_view", "median_ms_per_iter", "warmup_excluded", "warmup_ms",
               "first_build_ms", "mean_iou", "loss_drop")
+# decimals of the record's fixed-notation reals (BenchRecord::add(key, double,
+# precision), default 4: examples/common/bench.h:33, run.cpp:686-703)
+BENCH_DECIMALS = {"ram_gb": 1, "median_ms_per_iter": 4, "warmup_ms": 1, "first_build_ms": 1,
+                  "mean_iou": 4, "loss_drop": 1}
 
 
 def median_upper(samples) -> float:
@@ -312,16 +316,35 @@ def bench_fields(device: str, cpu: str, cores: int, ram_gb: float, kernels: int,
     fields = {
         "example": "silhouette_optimization", "device": device, "platform": "linux",
         "os": f"{platform.system()} {platform.release()}", "cpu": cpu, "cpu_cores": int(cores),
-        "ram_gb": round(float(ram_gb), 1), "funcs": int(kernels), "substages": int(kernels),
+        "ram_gb": float(ram_gb), "funcs": int(kernels), "substages": int(kernels),
         "stages": 1, "technique": technique, "screen": int(screen), "views": int(views),
         "iters": int(iters), "samples": 8, "peels": 1, "single_view": views == 1,
-        "median_ms_per_iter": round(median, 6), "warmup_excluded": int(warm_n),
-        "warmup_ms": round(warm_ms, 1), "first_build_ms": round(warm[0] if warm else 0.0, 1),
-        "mean_iou": round(float(mean_iou), 6),
-        "loss_drop": round(first_loss / max(last_loss, 1e-12), 1),
+        "median_ms_per_iter": float(median), "warmup_excluded": int(warm_n),
+        "warmup_ms": float(warm_ms), "first_build_ms": float(warm[0] if warm else 0.0),
+        "mean_iou": float(mean_iou),
+        "loss_drop": float(first_loss / max(last_loss, 1e-12)),
     }
     assert tuple(fields) == BENCH_KEYS
     return fields
+
+
+def bench_json_text(fields: dict) -> str:
+    """The record as the reference writes it (examples/common/bench.cpp:
+    187-209): one object, no spaces, strings quoted as given, integers plain,
+    booleans true / false, reals in fixed notation with their key's
+    decimals."""
+    parts = []
+    for k, v in fields.items():
+        if isinstance(v, bool):
+            val = "true" if v else "false"
+        elif isinstance(v, int):
+            val = str(v)
+        elif isinstance(v, float):
+            val = f"{v:.{BENCH_DECIMALS[k]}f}"
+        else:
+            val = f'"{v}"'
+        parts.append(f'"{k}":{val}')
+    return "{" + ",".join(parts) + "}\n"
 
 
 def bench_record(workload: str, path: str) -> None:
@@ -358,7 +381,7 @@ def bench_record(workload: str, path: str) -> None:
                           w.screen, w.views, w.iters, iter_ms, float(np.mean(ious)), first_loss,
                           last_loss)
     with open(path, "w") as fh:
-        fh.write(json.dumps(fields, separators=(",", ":")) + "\n")
+        fh.write(bench_json_text(fields))
     fit.close()
     ctx.close()
 

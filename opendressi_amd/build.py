@@ -23,6 +23,9 @@ CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libdressi_hip.so")
 SOURCES = ["runtime.hip", "raster.hip", "hsr.hip", "aa.hip", "tex.hip", "ds.hip", "ibl.hip", "pbr.hip",
            "graph.hip", "executor.hip", "builders.hip", "route.hip"]
+# host-only sources (the examples' asset and geometry helpers), built with g++; zlib is
+# linked for their deflate streams
+HOST_SOURCES = ["assets.cpp", "geometry.cpp"]
 HEADERS = ["internal.h", "dressi_math.h", "raster_core.h", "soft_clip.h", "hsr_chain.h",
            "aa_core.h", "plan.h", "ibl_core.h", "graph_ir.h", "route.h"]
 ARCH = os.environ.get("DRESSI_OFFLOAD_ARCH", "gfx950")
@@ -58,27 +61,31 @@ def build(verbose: bool = False) -> str:
     os.makedirs(OBJ_DIR, exist_ok=True)
     inc = ["-I", os.path.join(ROOT, "include")]
     objs = [os.path.join(OBJ_DIR, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    host_objs = [os.path.join(OBJ_DIR, os.path.splitext(s)[0] + ".o") for s in HOST_SOURCES]
     jobs = min(len(SOURCES), max(1, min(os.cpu_count() or 1, 8)))
     with ThreadPoolExecutor(jobs) as ex:
         futs = [ex.submit(_run, [hipcc(), *FLAGS, *inc, "-c", os.path.join(CSRC, s), "-o", o],
                           verbose, s) for s, o in zip(SOURCES, objs)]
+        futs += [ex.submit(_run, ["g++", "-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", *inc,
+                                  "-c", os.path.join(CSRC, s), "-o", o], verbose, s)
+                 for s, o in zip(HOST_SOURCES, host_objs)]
         for f in futs:
             f.result()
     tmp = LIB + ".tmp"
-    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose,
-         "libdressi_hip.so")
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, *host_objs,
+          "-lz"], verbose, "libdressi_hip.so")
     os.replace(tmp, LIB)
     return LIB
 
 
 def build_graph_test(verbose: bool = False) -> str:
-    """The graph-API test programs (tests/graph_c1.cpp, tests/graph_ops.cpp),
-    linked against the library; plain C++ (the graph API headers need no HIP
-    headers)."""
+    """The test programs (tests/graph_c1.cpp, tests/graph_ops.cpp over the
+    graph API, tests/assets_cli.cpp over the examples' helpers), linked
+    against the library; plain C++ (those headers need no HIP headers)."""
     out_dir = os.path.join(ROOT, "tests", "_bin")
     os.makedirs(out_dir, exist_ok=True)
     exe = ""
-    for name in ("graph_c1", "graph_ops"):
+    for name in ("graph_c1", "graph_ops", "assets_cli"):
         src = os.path.join(ROOT, "tests", name + ".cpp")
         exe = os.path.join(out_dir, name)
         cmd = ["g++", "-std=c++17", "-O2", "-ffp-contract=off", "-I", os.path.join(ROOT, "include"),

@@ -14,43 +14,34 @@
 // out.bin: pos, m, v {V,3}, t, loss[iters] (sum of the loss image),
 //          grad0 {V,3} (first iteration), preds and targets {N,S,S} (last)
 // stdout:  "graph_c1: plan=<name> stages=<n> substages=<n> funcs=<n>"
+#include <algorithm>
 #include <cstdio>
 #include <vector>
 
 #include "dressi/dressi.h"
 #include "dressi/mesh_utils.h"
+#include "dressi_examples/geometry_utils.h"
 
 using namespace dressi;
 
 namespace {
 
-// TransformToClipVar (examples/common/geometry_utils.cpp:391-402)
-Variable ClipOf(const Variable& pos, const float* mvp) {
-    Variable x = F::GetX(pos);
-    Variable y = F::GetY(pos);
-    Variable z = F::GetZ(pos);
-    const auto row = [&](int r) {
-        return x * mvp[size_t(0 * 4 + r)] + y * mvp[size_t(1 * 4 + r)] +
-               z * mvp[size_t(2 * 4 + r)] + mvp[size_t(3 * 4 + r)];
-    };
-    return F::Vec4(row(0), row(1), row(2), row(3));
+// the example's in-graph vertex transform and host clip images, from the
+// library's example helpers (dressi_examples/geometry_utils.h)
+dressi_examples::Mat4 MatOf(const float* m) {
+    dressi_examples::Mat4 r{};
+    std::copy(m, m + 16, r.begin());
+    return r;
 }
 
-// TransformToClip on the host, (MVP * (p, 1)) summed over k in order
+Variable ClipOf(const Variable& pos, const float* mvp) {
+    return dressi_examples::TransformToClipVar(pos, MatOf(mvp));
+}
+
 CpuImage ClipImage(const std::vector<float>& pos, const float* m) {
-    const uint32_t n = uint32_t(pos.size() / 3);
-    CpuImage c(n, 1, 4);
-    for (uint32_t i = 0; i < n; i++) {
-        const float p[4] = {pos[i * 3 + 0], pos[i * 3 + 1], pos[i * 3 + 2], 1.f};
-        for (uint32_t r = 0; r < 4; r++) {
-            float acc = 0.f;
-            for (int k = 0; k < 4; k++) {
-                acc += m[k * 4 + r] * p[k];
-            }
-            c.at(i, 0, r) = acc;
-        }
-    }
-    return c;
+    CpuImage p(uint32_t(pos.size() / 3), 1, 3);
+    p.data = pos;
+    return dressi_examples::TransformToClip(p, MatOf(m));
 }
 
 CpuImage Image(const std::vector<float>& d, uint32_t w, uint32_t h, uint32_t c) {

@@ -4,6 +4,7 @@ run.cpp:573-587, 676-702): key order and types, the upper median, the
 warm-up split and the first-build time. CPU only."""
 import json
 import os
+import re
 import sys
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -11,17 +12,14 @@ sys.path.insert(0, ROOT)
 
 import bench  # noqa: E402
 
-# the reference record's keys in the order it writes them: BenchRecord's
-# constructor, addPacking, then run.cpp's adds
-REF_KEYS = ["example", "device", "platform", "os", "cpu", "cpu_cores", "ram_gb", "funcs",
-            "substages", "stages", "technique", "screen", "views", "iters", "samples", "peels",
-            "single_view", "median_ms_per_iter", "warmup_excluded", "warmup_ms",
-            "first_build_ms", "mean_iou", "loss_drop"]
-TYPES = {"example": str, "device": str, "platform": str, "os": str, "cpu": str, "cpu_cores": int,
-         "ram_gb": float, "funcs": int, "substages": int, "stages": int, "technique": str,
-         "screen": int, "views": int, "iters": int, "samples": int, "peels": int,
-         "single_view": bool, "median_ms_per_iter": float, "warmup_excluded": int,
-         "warmup_ms": float, "first_build_ms": float, "mean_iou": float, "loss_drop": float}
+# key order, value kinds and decimals as the reference's writer and call
+# site declare them (tests/golden/bench_json_keys.json, written from
+# examples/common/bench.{h,cpp} and run.cpp by tests/golden/make_bench_keys.py)
+with open(os.path.join(ROOT, "tests", "golden", "bench_json_keys.json")) as _f:
+    GOLDEN = json.load(_f)
+REF_KEYS = GOLDEN["keys"]
+TYPES = {k: {"str": str, "int": int, "float": float, "bool": bool}[v]
+         for k, v in GOLDEN["kinds"].items()}
 
 
 def test_upper_median():
@@ -43,11 +41,29 @@ def test_record_keys_types_and_definitions():
     assert rec["warmup_excluded"] == 20
     assert rec["first_build_ms"] == 50.0
     steady = sorted(ms[20:])
-    assert rec["median_ms_per_iter"] == round(steady[len(steady) // 2], 6)
-    assert rec["warmup_ms"] == round(sum(ms[:20]) - 20 * rec["median_ms_per_iter"], 1)
+    assert rec["median_ms_per_iter"] == steady[len(steady) // 2]
+    assert rec["warmup_ms"] == sum(ms[:20]) - 20 * rec["median_ms_per_iter"]
     assert rec["loss_drop"] == 4.0
     assert rec["single_view"] is False
     # a short run: warm-up is iters / 2
     short = bench.bench_fields("d", "c", 1, 1.0, 5, "aa", 64, 1, 10, [1.0] * 10, 1.0, 1.0, 1.0)
     assert short["warmup_excluded"] == 5 and short["single_view"] is True
-    json.dumps(rec)  # serialisable as written
+
+
+def test_record_text_matches_the_reference_format():
+    ms = [12.345] + [1.0] * 19 + [0.123456 + 1e-4 * i for i in range(30)]
+    rec = bench.bench_fields("AMD Instinct MI355X", "x86", 16, 31.4159, 5, "hardsoftras", 2048, 4,
+                             50, ms, 0.955555, 0.2, 0.05)
+    text = bench.bench_json_text(rec)
+    assert text.endswith("}\n") and '", "' not in text and '": ' not in text
+    parsed = json.loads(text)
+    assert list(parsed) == REF_KEYS
+    for k, t in TYPES.items():
+        assert isinstance(parsed[k], t), (k, type(parsed[k]))
+    # reals in fixed notation with the reference's decimals
+    for k, d in GOLDEN["precision"].items():
+        m = re.search(rf'"{k}":(-?\d+)\.(\d+)[,}}]', text)
+        assert m and len(m.group(2)) == d, (k, text)
+    assert '"median_ms_per_iter":0.1250,' in text and '"mean_iou":0.9556,' in text
+    assert '"ram_gb":31.4,' in text and '"first_build_ms":12.3,' in text
+    assert '"single_view":false,' in text and '"stages":1,' in text
