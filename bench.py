@@ -144,6 +144,35 @@ def kernel_bytes_pbr(n_views: int, s: int, texels: int, env_texels: int, pooled:
     }
 
 
+# FP32 operations (add, sub, mul, div, abs) per pixel of k_pbr_shade, counted
+# from the shading arithmetic of one pixel:
+#   foreground: forward 349 (material bilinear weights 12 + albedo / mr taps
+#     48 + ao 8; irradiance weights and taps 36; two active prefilter levels
+#     2 x 45; LUT weights and taps 28; GGX D / G / denominators 27; per
+#     channel Fresnel, diffuse, specular, ambient 3 x 31; lod 1; tone map 6),
+#     L1 loss and d loss / d hdr 30, backward to albedo / metallic /
+#     roughness 205, map-gradient VJP of the irradiance and two prefilter tap
+#     sets 78 (12 weighted taps and their accumulation each, + 6)
+#   background with env: env weights and taps 36, tone map 6, loss 30, env
+#     map-gradient VJP 24
+#   neither: tone map of zero 6, loss 30
+SHADE_FLOPS = {"fg": 662.0, "env": 96.0, "none": 36.0}
+# per (output texel, source texel) pair of the dense IBL convolutions: the
+# direction dot product, the GGX (or cosine) weight, the weighted RGB sum
+CONV_FLOPS_PER_PAIR = 30.0
+VALU_PEAK = 157.3e12  # MI355X dense FP32 vector, FLOP/s
+
+
+def kernel_flops_pbr(pixel_classes: dict, conv_pairs: float) -> dict:
+    """Algorithmic FP32 operations per launch of the PBR plan's VALU-bound
+    kernels: the shading kernel per pixel class, each convolution per
+    (output, source) pair (irradiance + every prefilter level)."""
+    shade = sum(SHADE_FLOPS[k] * float(n) for k, n in pixel_classes.items())
+    return {"k_pbr_shade": shade,
+            "k_pbr_conv_fwd": CONV_FLOPS_PER_PAIR * conv_pairs,
+            "k_pbr_conv_bwd": CONV_FLOPS_PER_PAIR * conv_pairs}
+
+
 def iteration_bytes(n_views: int, s: int, n_faces: int, n_verts: int) -> float:
     """Compulsory bytes of one HSR iteration (per pixel and view: target read,
     8-byte visibility write and read; per view: clip, soft clip, corner clips,
@@ -487,6 +516,24 @@ def main() -> int:
     dbytes = kbytes[dom]
     achieved = dbytes / (dom_us * 1e-6)
     traffic = measured_traffic(dom, args.workload)
+    valu = None
+    if pbr:
+        # pixel classes from the static G-buffer (n.v < 0: background; its
+        # u < 0: no env behind it); convolution pairs from the map sizes
+        g = fit.read(od._lib.PBR_GBUF0)
+        fg = g[..., 2] >= 0.0
+        env = ~fg & (g[..., 0] >= 0.0)
+        classes = {"fg": int(fg.sum()), "env": int(env.sum()), "none": int(g[..., 0].size
+                                                                            - fg.sum() - env.sum())}
+        psw, psh = fit.prefilter_source
+        isw, ish = fit.irradiance_source
+        pairs = (fit.map_texels - 32 * 16) * psw * psh + 32 * 16 * isw * ish
+        kfl = kernel_flops_pbr(classes, pairs)
+        valu = {k: {"achieved": f / (prof[k] * 1e-6) / 1e12, "frac": f / (prof[k] * 1e-6) / VALU_PEAK,
+                    "algorithmic_flops_per_launch": f, "avg_launch_us": prof[k]}
+                for k, f in kfl.items() if k in prof}
+        valu["pixel_classes"] = classes
+        valu["conv_pairs"] = pairs
     fit.close()
 
     line = {
@@ -503,13 +550,23 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": desc, "screen": s, "views": nviews, "verts": nv, "faces": nf},
-        "roofline": {"bound": "hbm", "kernel": dom,
-                     "achieved": achieved / 1e9,
-                     "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK,
-                     "traffic": traffic,
-                     "algorithmic_bytes_per_launch": dbytes,
-                     "avg_launch_us": dom_us},
+        "roofline": ({"bound": "hbm", "kernel": dom,
+                      "achieved": achieved / 1e9,
+                      "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                      "frac": achieved / HBM_PEAK,
+                      "traffic": traffic,
+                      "algorithmic_bytes_per_launch": dbytes,
+                      "avg_launch_us": dom_us}
+                     if valu is None or dom not in valu else
+                     {"bound": "valu", "kernel": dom,
+                      "achieved": valu[dom]["achieved"],
+                      "peak": VALU_PEAK / 1e12, "unit": "TFLOP/s",
+                      "frac": valu[dom]["frac"],
+                      "traffic": traffic,
+                      "algorithmic_flops_per_launch": valu[dom]["algorithmic_flops_per_launch"],
+                      "algorithmic_bytes_per_launch": dbytes,
+                      "hbm_frac": achieved / HBM_PEAK,
+                      "avg_launch_us": dom_us}),
         "iteration_roofline": {"algorithmic_bytes": ibytes,
                                "achieved_GBps": ibytes * its / 1e9,
                                "frac": ibytes * its / HBM_PEAK},
@@ -517,6 +574,8 @@ def main() -> int:
         "kernel_us": prof,
         "loss_after": loss_end,
     }
+    if valu is not None:
+        line["valu_rooflines"] = valu
     if args.workload == "c4_hsr" and not args.no_points:
         # the metric's 512^2 point and the AA technique at 2048^2
         line["metric_points"] = {"c2": metric_point("c2", 400, 20),

@@ -337,7 +337,10 @@ enum {
     DRESSI_PBR_G_MR = 4,     /* {T} float4 (KEEP_GRAD) */
     DRESSI_PBR_G_ENV = 5,    /* {E} float4 (KEEP_GRAD) */
     DRESSI_PBR_IRR = 6,      /* {32 x 16} float4: the last step's irradiance map */
-    DRESSI_PBR_PREF = 7      /* float4: the prefiltered levels, level-major */
+    DRESSI_PBR_PREF = 7,     /* float4: the prefiltered levels, level-major */
+    DRESSI_PBR_GBUF0 = 8     /* {N,S,S} float4 static G-buffer word 0: material
+                                uv, n.v, n.l; n.v < 0 marks a background pixel,
+                                whose (u, v) is its env lookup (u < 0: none) */
 };
 int dressi_pbr_buffer(dressi_pbr_plan* plan, int which, void** ptr,
                       size_t* bytes);

@@ -47,7 +47,7 @@ class PbrDesc(C.Structure):
 PBR_KEEP_PRED = 1
 PBR_KEEP_GRAD = 2
 (PBR_LOSS, PBR_PRED, PBR_TARGET, PBR_G_ALBEDO, PBR_G_MR, PBR_G_ENV, PBR_IRR,
- PBR_PREF) = range(8)
+ PBR_PREF, PBR_GBUF0) = range(9)
 
 TEX_KEEP_IMAGES = 1
 TEX_KEEP_GRAD = 2

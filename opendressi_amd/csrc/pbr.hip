@@ -1807,6 +1807,7 @@ int dressi_pbr_buffer(dressi_pbr_plan* p, int which, void** ptr, size_t* bytes) 
         case DRESSI_PBR_G_ENV: q = d.g_env; b = E * 16; break;
         case DRESSI_PBR_IRR: q = d.irr; b = (size_t)d.iw * d.ih * 16; break;
         case DRESSI_PBR_PREF: q = d.pref; b = (size_t)d.n_pref * 16; break;
+        case DRESSI_PBR_GBUF0: q = const_cast<float4*>(d.st0); b = N * npx * 16; break;
         default: DRESSI_REQUIRE(false, "unknown buffer %d", which);
     }
     DRESSI_REQUIRE(q, "buffer %d not kept (see the DRESSI_PBR_KEEP_* flags)", which);

@@ -224,7 +224,7 @@ class PbrFit:
         shapes = {_lib.PBR_LOSS: (1,), _lib.PBR_PRED: (n, s, s, 4),
                   _lib.PBR_TARGET: (n, s, s, 4), _lib.PBR_G_ALBEDO: t + (4,),
                   _lib.PBR_G_MR: t + (4,), _lib.PBR_G_ENV: e + (4,), _lib.PBR_IRR: (16, 32, 4),
-                  _lib.PBR_PREF: (n_pref, 4)}
+                  _lib.PBR_PREF: (n_pref, 4), _lib.PBR_GBUF0: (n, s, s, 4)}
         out = np.zeros(shapes[which], np.float32)
         check(lib.dressi_pbr_read(self.handle, which, out.ctypes.data_as(C.c_void_p),
                                   out.nbytes))
@@ -248,6 +248,19 @@ class PbrFit:
             n += w * h
             w, h = max(w // 2, 1), max(h // 2, 1)
         return n
+
+    @property
+    def prefilter_source(self) -> tuple[int, int]:
+        """(w, h) of the pooled env level the prefilter convolution reads."""
+        return self._psrc()
+
+    @property
+    def irradiance_source(self) -> tuple[int, int]:
+        """(w, h) of the pooled env level the irradiance convolution reads."""
+        w, h = self.env_w, self.env_h
+        while w > 64 or h > 32:
+            w, h = (w + 1) // 2, (h + 1) // 2
+        return w, h
 
     def _psrc(self):
         w, h = self.env_w, self.env_h
