@@ -677,6 +677,10 @@ struct DressiAD::Impl {
     Variables leaf_vars;
     Variables extra_outputs;
     std::vector<std::pair<Variable, Variable>> extra_updates;  // (input, updated)
+    // extra_updates[opt_updates_from ..) were added by the optimizer's last
+    // call (addUpdate from inside it); the next optimizer rebuild replaces them
+    size_t opt_updates_from = 0;
+    bool in_optimizer = false;
     bool grad_outputs = false;
     // reactive cache
     uint32_t fast_count = 2, full_count = 8, static_cnt = 0;
@@ -1644,7 +1648,15 @@ void DressiAD::addUpdate(const Variable& input_leaf, const Variable& updated) {
     DRESSI_CHECK(input_leaf.getVType() == updated.getVType() &&
                          input_leaf.getImgSize() == updated.getImgSize(),
                  "addUpdate: updated must match the input's type and size");
-    m_impl->extra_updates.emplace_back(input_leaf, updated);
+    if (!m_impl->in_optimizer) {
+        // a pair added outside the optimizer goes before the optimizer's own
+        m_impl->extra_updates.insert(
+                m_impl->extra_updates.begin() + (ptrdiff_t)m_impl->opt_updates_from,
+                {input_leaf, updated});
+        m_impl->opt_updates_from++;
+    } else {
+        m_impl->extra_updates.emplace_back(input_leaf, updated);
+    }
     if (m_impl->status > OPTIMIZER) {
         m_impl->status = OPTIMIZER;
     }
@@ -1731,8 +1743,21 @@ void DressiAD::execStep() {
     if (im.status <= OPTIMIZER) {
         im.updated_vars.clear();
         im.copy_backs.clear();
+        // pairs the previous optimizer call registered belong to the graph
+        // it built; the call below registers the current graph's
+        if (im.opt_updates_from < im.extra_updates.size()) {
+            im.extra_updates.resize(im.opt_updates_from);
+        }
+        im.opt_updates_from = im.extra_updates.size();
         if (im.optimizer) {
-            im.updated_vars = im.optimizer(im.input_vars, im.input_grad_vars);
+            im.in_optimizer = true;
+            try {
+                im.updated_vars = im.optimizer(im.input_vars, im.input_grad_vars);
+            } catch (...) {
+                im.in_optimizer = false;
+                throw;
+            }
+            im.in_optimizer = false;
             DRESSI_CHECK(im.updated_vars.size() == im.input_vars.size(),
                          "Optimizer must return one output per input");
             for (size_t i = 0; i < im.updated_vars.size(); i++) {
@@ -1743,8 +1768,7 @@ void DressiAD::execStep() {
                 im.copy_backs.emplace_back(u, x);
             }
         }
-        // addUpdate pairs persist across rebuilds (typically registered
-        // once from inside the optimizer)
+        // addUpdate pairs made outside the optimizer persist across rebuilds
         for (const auto& [inp, upd] : im.extra_updates) {
             im.copy_backs.emplace_back(upd, inp);
         }

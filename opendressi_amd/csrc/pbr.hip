@@ -943,15 +943,32 @@ __global__ __launch_bounds__(256) void k_pbr_conv_bwd(PbrDev d) {
         acc[o][0] = acc[o][1] = acc[o][2] = 0.f;
     }
     const uint32_t n_t = irr ? d.iw * d.ih : d.n_pref;
+    const float4* tdir = irr ? d.idir : d.pdir;
+    const float4* tg = irr ? d.g_irr : d.g_pref;
+    // the next texel's direction, gradient and norm are loaded before the
+    // current one is used (the loop is bound by these loads' latency)
+    float4 r_n = make_float4(0.f, 0.f, 0.f, 0.f), g_n = r_n;
+    float nt_n = 1.f;
+    if (threadIdx.x < n_t) {
+        r_n = tdir[threadIdx.x];
+        g_n = tg[threadIdx.x];
+        nt_n = irr ? 1.f : d.pnorm[threadIdx.x];
+    }
     for (uint32_t t = threadIdx.x; t < n_t; t += blockDim.x) {
-        const float4 r = irr ? d.idir[t] : d.pdir[t];
-        const float4 g = irr ? d.g_irr[t] : d.g_pref[t];
+        const float4 r = r_n;
+        const float4 g = g_n;
+        const float nt = nt_n;
+        const uint32_t tn = t + blockDim.x;
+        if (tn < n_t) {
+            r_n = tdir[tn];
+            g_n = tg[tn];
+            nt_n = irr ? 1.f : d.pnorm[tn];
+        }
         if (g.x == 0.f && g.y == 0.f && g.z == 0.f) {
             continue;
         }
         float inv = 1.f;
         if (!irr) {
-            const float nt = d.pnorm[t];
             inv = nt > 1e-12f ? nt : 1e-12f;
         }
 #pragma unroll

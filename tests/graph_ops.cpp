@@ -187,6 +187,72 @@ void build(const std::string& which, Case& c) {
     }
 }
 
+// Re-setting the loss after a step: the optimizer (momentum SGD whose state
+// m is carried by addUpdate from inside it) runs again for the new graph. A:
+// one step on loss 1, then two on loss 2 in the same DressiAD; B: a fresh
+// DressiAD on loss 2 from A's state after its first step, two steps. A and
+// B must agree on x, m and the function count (no stale update pairs).
+int run_rebuild(const char* packing, const char* in_path, const char* out_path) {
+    const Images in = load(in_path);
+    const CpuImage& x0 = in.at("x");
+    const CpuImage& tgt0 = in.at("tgt");
+    const ImgSize sz = x0.getImgSize();
+    struct Net {
+        Variable x{VEC3, {1, 1}}, m{VEC3, {1, 1}}, tgt{VEC3, {1, 1}}, loss1, loss2;
+    };
+    auto make = [&]() {
+        Net n;
+        n.x = Variable(VEC3, sz);
+        n.m = Variable(VEC3, sz);
+        n.tgt = Variable(VEC3, sz);
+        const Variable d1 = n.x - n.tgt;
+        n.loss1 = F::Sum(F::CompSum(d1 * d1));
+        const Variable d2 = n.x * 2.f - n.tgt;
+        n.loss2 = F::Sum(F::CompSum(d2 * d2 * 0.5f));
+        n.x.setRequiresGradRecursively();
+        return n;
+    };
+    const auto mode = std::string(packing) == "naive" ? DressiAD::PackingMode::Naive
+                                                      : DressiAD::PackingMode::RSP;
+    auto setup = [&](DressiAD& ad, Net& n, const Variable& loss) {
+        ad.setPackingMode(mode);
+        ad.setLossVar(loss);
+        ad.setOptimizer([&ad, &n](Variables xs, Variables gs) {
+            const Variable m_new = n.m * 0.9f + gs[0];
+            ad.addUpdate(n.m, m_new);
+            return Variables{xs[0] - m_new * 0.1f};
+        });
+    };
+    Images out;
+    Net a = make();
+    DressiAD ad_a(DressiAD::createContext());
+    setup(ad_a, a, a.loss1);
+    ad_a.sendImg(a.x, x0);
+    ad_a.sendImg(a.m, CpuImage(sz.w, sz.h, 3, 0.f));
+    ad_a.sendImg(a.tgt, tgt0);
+    ad_a.execStep();
+    const CpuImage x1 = ad_a.recvImg(a.x), m1 = ad_a.recvImg(a.m);
+    ad_a.setLossVar(a.loss2);
+    ad_a.execStep();
+    ad_a.execStep();
+    out["xa"] = ad_a.recvImg(a.x);
+    out["ma"] = ad_a.recvImg(a.m);
+    Net b = make();
+    DressiAD ad_b(DressiAD::createContext());
+    setup(ad_b, b, b.loss2);
+    ad_b.sendImg(b.x, x1);
+    ad_b.sendImg(b.m, m1);
+    ad_b.sendImg(b.tgt, tgt0);
+    ad_b.execStep();
+    ad_b.execStep();
+    out["xb"] = ad_b.recvImg(b.x);
+    out["mb"] = ad_b.recvImg(b.m);
+    save(out_path, out);
+    printf("graph_ops rebuild: funcs_a=%zu funcs_b=%zu plan=%s\n", ad_a.getFuncCount(),
+           ad_b.getFuncCount(), ad_a.getPlanName().c_str());
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -195,6 +261,9 @@ int main(int argc, char** argv) {
         return 2;
     }
     try {
+        if (std::string(argv[1]) == "rebuild") {
+            return run_rebuild(argv[2], argv[3], argv[4]);
+        }
         Case c;
         c.in = load(argv[3]);
         build(argv[1], c);

@@ -413,3 +413,27 @@ def test_regulariser_ops(tmp_path, oracle):
                     acc[c] = F32(acc[c] - F32(g1[c] + g2[c]))
         grad[v] = acc
     _exact(r["grad"], grad.reshape(1, nv, 3), "NormalConsistencyVertexGrad")
+
+
+@pytest.mark.gpu
+def test_loss_reset_replaces_the_optimizer_updates(tmp_path):
+    """setLossVar after a step re-runs the optimizer for the new graph; the
+    update pairs it registered for the old graph are dropped: the same
+    DressiAD then matches a fresh one built on the new loss (state and
+    function count)."""
+    rng = np.random.default_rng(12)
+    imgs = {"x": rng.standard_normal((3, 5, 3)).astype(F32),
+            "tgt": rng.standard_normal((3, 5, 3)).astype(F32)}
+    for packing in ("rsp", "naive"):
+        inp = tmp_path / "rebuild_in.bin"
+        out = tmp_path / f"rebuild_{packing}.bin"
+        _write(inp, imgs)
+        r = subprocess.run([EXE, "rebuild", packing, str(inp), str(out)], capture_output=True,
+                           text=True, timeout=120)
+        print(r.stdout.strip(), r.stderr.strip(), flush=True)
+        assert r.returncode == 0, r.stderr
+        o = _read(out)
+        assert np.array_equal(o["xa"], o["xb"]) and np.array_equal(o["ma"], o["mb"])
+        assert not np.array_equal(o["xa"], imgs["x"])
+        fa, fb = (int(t.split("=")[1]) for t in r.stdout.split()[2:4])
+        assert fa == fb, r.stdout
