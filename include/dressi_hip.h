@@ -520,6 +520,14 @@ int dressi_hsr_read(dressi_hsr_plan* plan, int which, void* host,
 int dressi_hsr_profile(dressi_hsr_plan* plan, uint32_t iters, char* names,
                        size_t name_stride, float* usec, uint32_t cap,
                        uint32_t* n);
+/* Entries per soft bin (a 16x16 tile of one view) of the plan. No
+ * counterpart in the reference (its binning is the Vulkan rasteriser's): the
+ * bins start at 1024 entries; when an iteration's face backward finds a bin
+ * past its capacity (that iteration's raster walked every face of the view
+ * there: exact but slow), the next dressi_hsr_step / _step_eager grows them
+ * to the next power of two holding that count, at most 16384. For tests and
+ * diagnostics. */
+int dressi_hsr_bin_capacity(dressi_hsr_plan* plan, uint32_t* entries);
 
 /* ------------------------------------------------------------------------ */
 /* Fused texture-optimisation iteration (C3)                                */

@@ -126,6 +126,7 @@ _SIGS = {
     "dressi_hsr_buffer": (_I, [_P, _I, C.POINTER(_P), C.POINTER(_S)]),
     "dressi_hsr_read": (_I, [_P, _I, _P, _S]),
     "dressi_hsr_profile": (_I, [_P, _U, C.c_char_p, _S, _FP, _U, _UP]),
+    "dressi_hsr_bin_capacity": (_I, [_P, _UP]),
     "dressi_pbr_create": (_I, [_P, C.POINTER(PbrDesc), C.POINTER(_P)]),
     "dressi_pbr_destroy": (_I, [_P]),
     "dressi_pbr_set_scene": (_I, [_P, _FP, _FP, _FP, _FP, _FP, _FP, _FP]),

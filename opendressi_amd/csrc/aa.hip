@@ -807,6 +807,10 @@ __global__ __launch_bounds__(256) void k_aa_face_bwd(HsrDev d) {
     const uint32_t gi = blockIdx.x * blockDim.x + threadIdx.x;
     publish_t_next(d, gi);
     for (uint32_t b = gi; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
+        const uint32_t c = d.bins.counts[b];
+        if (c > d.bins.cap && d.bin_over) {
+            *d.bin_over = c;  // rare: the host grows the bins before the next step
+        }
         d.bins.counts[b] = 0;
     }
     const uint32_t nvf = d.g.n_views * d.g.n_faces;

@@ -177,6 +177,10 @@ __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
     publish_t_next(d, gi);
     // the raster is done with this iteration's bins: clear their counters
     for (uint32_t b = gi; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
+        const uint32_t c = d.bins.counts[b];
+        if (c > d.bins.cap && d.bin_over) {
+            *d.bin_over = c;  // rare: the host grows the bins before the next step
+        }
         d.bins.counts[b] = 0;
     }
     if (d.heavy.count && gi < kHeavySegs) {
@@ -487,7 +491,8 @@ struct dressi_hsr_plan {
     dressi_hsr_desc desc{};
     HsrDev d{};
     std::vector<void*> allocs;
-    void* bin_mem = nullptr;
+    void* bin_mem = nullptr;     // the soft bins (resized by grow_bins)
+    uint32_t* over_host = nullptr;  // host-mapped: d.bin_over
     bool mesh_set = false, targets_set = false, state_set = false;
     hipGraph_t graph = nullptr;  // one iteration
     hipGraphExec_t exec = nullptr;
@@ -600,6 +605,44 @@ void drop_graph(dressi_hsr_plan* p) {
     }
 }
 
+// A bin overflowed in an earlier iteration (its raster walked every face of
+// the view: exact but slow): the bins grow to the next power of two that
+// holds the reported count (at most kSoftBinCapMax entries), so the
+// following iterations walk lists again. The report is read without waiting
+// for the stream; a grow waits for it before swapping the memory.
+int grow_bins(dressi_hsr_plan* p) {
+    if (!p->over_host) {
+        return DRESSI_OK;
+    }
+    const uint32_t need = __atomic_load_n(p->over_host, __ATOMIC_ACQUIRE);
+    if (need <= p->d.bins.cap || p->d.bins.cap >= kSoftBinCapMax) {
+        return DRESSI_OK;
+    }
+    uint32_t cap = p->d.bins.cap;
+    while (cap < need && cap < kSoftBinCapMax) {
+        cap *= 2;
+    }
+    hipStream_t s = p->ctx->stream;
+    DRESSI_TRY_HIP(hipStreamSynchronize(s));
+    const uint32_t n_bins = p->d.bins.n_bins;
+    const size_t bytes = fixed_bin_bytes(n_bins, cap);
+    void* mem = nullptr;
+    if (hipMalloc(&mem, bytes) != hipSuccess) {
+        // keep the current bins (overflowed bins stay exact, walking every face)
+        (void)hipGetLastError();
+        *p->over_host = 0;
+        return DRESSI_OK;
+    }
+    DRESSI_TRY_HIP(hipMemsetAsync(mem, 0, sizeof(uint32_t) * n_bins, s));
+    DRESSI_TRY_HIP(hipStreamSynchronize(s));
+    DRESSI_TRY_HIP(hipFree(p->bin_mem));
+    p->bin_mem = mem;
+    fixed_bin_carve(mem, n_bins, cap, &p->d.bins);
+    __atomic_store_n(p->over_host, 0u, __ATOMIC_RELEASE);
+    drop_graph(p);  // the graphs hold the old bins
+    return DRESSI_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -679,11 +722,28 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
         d.bc_len = kBiasTableLen;
     }
     if (!rc) {
-        uint32_t* bm = nullptr;
         const size_t bytes = fixed_bin_bytes(d.g.n_tiles * d.g.n_views, kSoftBinCap);
-        rc = plan_alloc(p, &bm, bytes / sizeof(uint32_t) + 1);
-        if (!rc) {
-            fixed_bin_carve(bm, d.g.n_tiles * d.g.n_views, kSoftBinCap, &d.bins);
+        if (hipMalloc(&p->bin_mem, bytes) != hipSuccess) {
+            p->bin_mem = nullptr;
+            set_error("out of device memory for the bins (%zu bytes)", bytes);
+            rc = DRESSI_ERR_HIP;
+        } else {
+            fixed_bin_carve(p->bin_mem, d.g.n_tiles * d.g.n_views, kSoftBinCap, &d.bins);
+        }
+    }
+    if (!rc) {
+        // host-mapped overflow report (see grow_bins)
+        void* h = nullptr;
+        void* dp = nullptr;
+        if (hipHostMalloc(&h, sizeof(uint32_t), hipHostMallocMapped) != hipSuccess ||
+            hipHostGetDevicePointer(&dp, h, 0) != hipSuccess) {
+            if (h) hipHostFree(h);
+            set_error("hipHostMalloc failed for the bin overflow report");
+            rc = DRESSI_ERR_HIP;
+        } else {
+            p->over_host = (uint32_t*)h;
+            *p->over_host = 0;
+            d.bin_over = (uint32_t*)dp;
         }
     }
     if (!rc) {
@@ -717,6 +777,12 @@ int dressi_hsr_destroy(dressi_hsr_plan* p) {
     drop_graph(p);
     for (void* a : p->allocs) {
         hipFree(a);
+    }
+    if (p->bin_mem) {
+        hipFree(p->bin_mem);
+    }
+    if (p->over_host) {
+        hipHostFree(p->over_host);
     }
     delete p;
     return DRESSI_OK;
@@ -909,6 +975,7 @@ int dressi_hsr_get_state(dressi_hsr_plan* p, float* pos, float* m, float* v, flo
 
 int dressi_hsr_step_eager(dressi_hsr_plan* p, uint32_t n_iters) {
     if (int rc = ready(p)) return rc;
+    if (int rc = grow_bins(p)) return rc;
     for (uint32_t i = 0; i < n_iters; i++) {
         if (int rc = enqueue_iteration(p, p->ctx->stream)) return rc;
     }
@@ -917,6 +984,7 @@ int dressi_hsr_step_eager(dressi_hsr_plan* p, uint32_t n_iters) {
 
 int dressi_hsr_step(dressi_hsr_plan* p, uint32_t n_iters) {
     if (int rc = ready(p)) return rc;
+    if (int rc = grow_bins(p)) return rc;
     hipStream_t s = p->ctx->stream;
     if (!p->exec || p->graph_stream != s) {
         drop_graph(p);
@@ -964,6 +1032,12 @@ int dressi_hsr_step(dressi_hsr_plan* p, uint32_t n_iters) {
     for (; i < n_iters; i++) {
         DRESSI_TRY_HIP(hipGraphLaunch(p->exec, s));
     }
+    return DRESSI_OK;
+}
+
+int dressi_hsr_bin_capacity(dressi_hsr_plan* p, uint32_t* entries) {
+    DRESSI_REQUIRE(p && entries, "bad arguments");
+    *entries = p->d.bins.cap;
     return DRESSI_OK;
 }
 

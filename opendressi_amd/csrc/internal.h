@@ -153,6 +153,10 @@ inline void fixed_bin_carve(void* base, uint32_t n_bins, uint32_t cap, BinBuffer
 // Entries per soft bin (a 16x16 tile of one view).
 constexpr uint32_t kSoftBinCap = 1024;
 static_assert(kSoftBinCap >= 64, "bin_view reads a bin's first 64 entries unconditionally");
+// Largest entries per bin a fit plan grows its bins to (after an iteration
+// whose face backward saw an overflowed bin); past it an overflowed bin
+// walks every face of its view.
+constexpr uint32_t kSoftBinCapMax = 16384;
 
 struct RasterGeom {
     uint32_t width, height, tiles_x, tiles_y, n_tiles, n_views, n_faces;

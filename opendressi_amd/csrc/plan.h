@@ -94,6 +94,9 @@ struct HsrDev {
     uint32_t technique;       // 0 HardSoftRas, 1 AA
     float4* clip;             // [N][V]
     AaRec* arecs;             // [N][F]
+    // a bin count the face backward found above bins.cap (host-mapped, written
+    // only when a bin overflowed; the plan's next step grows the bins)
+    uint32_t* bin_over;
 };
 
 constexpr uint32_t kBiasTableLen = 1u << 16;

@@ -163,6 +163,13 @@ class SilhouetteFit:
     def synchronize(self) -> None:
         self.ctx.synchronize()
 
+    @property
+    def bin_capacity(self) -> int:
+        """Entries per soft bin (grows after an iteration overflowed one)."""
+        n = C.c_uint32()
+        check(lib.dressi_hsr_bin_capacity(self.handle, C.byref(n)))
+        return n.value
+
     def buffer(self, which: int) -> tuple[int, int]:
         p = C.c_void_p()
         b = C.c_size_t()

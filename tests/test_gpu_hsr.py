@@ -169,3 +169,44 @@ def test_c4_hsr_full_size_matches_oracle(ctx, oracle):
     """2048^2 x 4 views, icosphere L6 (the benchmark workload): face ids,
     pred, loss image and the gradient of one iteration."""
     _oracle_check(ctx, oracle, "c4_hsr", 1, True)
+
+
+@pytest.mark.parametrize("technique", ["hsr", "aa"])
+def test_overflowing_bins_grow(ctx, oracle, technique):
+    """A 20 480-face sphere seen from afar covers a few 16 x 16 tiles, so each
+    of their bins receives thousands of faces, past the 1 024-entry lists.
+    The first iteration walks every face for those tiles (exact); its face
+    backward reports the overflow and the next step grows the bins to hold
+    them. Face ids, prediction and gradient of the first iteration and the
+    parameters after three, against the oracle, bit for bit."""
+    import opendressi_amd as od
+    from opendressi_amd import _lib as L
+    pos, faces = oracle.icosphere(5)
+    tgt = (pos * np.float32(1.1)).astype(np.float32)
+    proj = oracle.perspective_vk(45.0 * 3.14159265 / 180.0, 1.0, 0.1, 100.0)
+    mvps = np.stack([oracle.mat4_mul(proj, oracle.look_at(e))
+                     for e in ((0.0, 3.0, 19.0), (17.0, -4.0, 9.0))])
+    s = 128
+    print(f"[hsr bins grow] {technique} ico5 {s}px 2 views", flush=True)
+    fit = od.SilhouetteFit(ctx, pos, faces, mvps, s, target_mesh=(tgt, faces), lr=1e-3,
+                           keep_pred=True, keep_grad=True, technique=technique)
+    assert fit.bin_capacity == 1024
+    fit.step(1)
+    ctx.synchronize()
+    ids, grad, pred = fit.read(L.BUF_FACE_ID), fit.read(L.BUF_GRAD), fit.read(L.BUF_PRED)
+    fit.step(1)
+    grown = fit.bin_capacity
+    fit.step(1)
+    pos_gpu = fit.state()[0]
+    fit.close()
+    assert grown > 1024, grown
+    fitter = oracle.hsr_fit if technique == "hsr" else oracle.aa_fit
+    ref = fitter(pos, faces, tgt, faces, mvps, s, lr=1e-3, iters=3, want_images=True)
+    assert (ids != 0).sum() > 50, "the sphere must cover some pixels"
+    if technique == "hsr":
+        assert np.array_equal(ids, ids_of_rs(ref["rs0"]))
+    else:
+        assert np.array_equal(ids.astype(np.float32), ref["tri0"])
+    assert np.array_equal(pred, ref["pred0"])
+    assert np.array_equal(grad, ref["grad0"]), rel_err(grad, ref["grad0"])
+    assert np.array_equal(pos_gpu, ref["pos"]), float(np.abs(pos_gpu - ref["pos"]).max())
