@@ -440,6 +440,65 @@ def metric_point(name: str, steps: int, warmup: int) -> dict:
             "iteration_frac_of_hbm_peak": nb * its / HBM_PEAK}
 
 
+def torch_surface(views: int = 8, screen: int = 256, level: int = 3, steps: int = 50,
+                  warmup: int = 5) -> dict:
+    """Iterations/s of the silhouette fit written against the
+    nvdiffrast-compatible torch surface (the loop of the reference's
+    examples/python/silhouette_optimization.py, technique aa, without its
+    regularisers): per iteration rasterize + antialias of the N views' masks,
+    the L2 loss against fixed target masks, autograd backward and
+    torch.optim.Adam on the vertex positions. The ops loop over the batch
+    items on the device (no host round trip)."""
+    import numpy as np
+    import torch
+
+    import opendressi_amd as od
+    import opendressi_amd.torch as dr
+    dev = torch.device("cuda", 0)
+    pos0, faces = od.icosphere(level)
+    w = od.Workload("torch", level, screen, views, 0.05, 0.1, 1e-3, steps, 3, "aa")
+    _, _, tgt, mvps = od.make_scene(w)
+    tri = torch.as_tensor(faces.astype(np.int32), device=dev)
+    # the column-major MVPs read row-major are M^T: clip rows = (x, y, z, 1) M^T
+    m = torch.as_tensor(np.asarray(mvps, np.float32).reshape(-1, 4, 4), device=dev)
+    ctx = dr.RasterizeHipContext(device=dev)
+
+    def clips(p):
+        ph = torch.cat([p, torch.ones_like(p[:, :1])], 1)
+        return torch.matmul(ph.unsqueeze(0), m)
+
+    def render(p):
+        c = clips(p)
+        rast, _ = dr.rasterize(ctx, c, tri, resolution=[screen, screen])
+        mask = (rast[..., 3:4] > 0).float()
+        return dr.antialias(mask, rast, c, tri)
+
+    with torch.no_grad():
+        target = render(torch.as_tensor(tgt, device=dev)).detach()
+    pos = torch.as_tensor(pos0, device=dev).clone().requires_grad_(True)
+    opt = torch.optim.Adam([pos], lr=1e-3)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        loss = ((render(pos) - target) ** 2).mean()
+        loss.backward()
+        opt.step()
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t
+    return {"workload": f"torch surface silhouette fit (aa): {screen}x{screen} x {views} views, "
+                        f"icosphere L{level} ({len(pos0)} v / {len(faces)} f), torch Adam",
+            "value": steps / dt, "unit": "iterations/s", "ms_per_step": 1e3 * dt / steps,
+            "steps": steps, "loss_after": float(loss)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -453,6 +512,9 @@ def main() -> int:
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="after the JSON line, run a plain device copy of this many MiB "
                          "(the reference kernel for scaling rocprofv3 FETCH/WRITE_SIZE)")
+    ap.add_argument("--torch-surface", action="store_true",
+                    help="also time the silhouette fit written against opendressi_amd.torch "
+                         "(rasterize + antialias + autograd + torch Adam) as `torch_surface`")
     ap.add_argument("--bench-json", default=None,
                     help="after the JSON line, run the silhouette workload's whole fit and write "
                          "the reference example's bench.json record to this path")
@@ -580,6 +642,8 @@ def main() -> int:
         # the metric's 512^2 point and the AA technique at 2048^2
         line["metric_points"] = {"c2": metric_point("c2", 400, 20),
                                  "c4": metric_point("c4", 100, 10)}
+    if args.torch_surface:
+        line["torch_surface"] = torch_surface()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = (cpu_baseline_pbr(w) if pbr else
                                 cpu_baseline_tex(w) if tex else cpu_baseline(w))
