@@ -158,18 +158,25 @@ __device__ __forceinline__ void aa_accumulate_v(const float* gy, const float* im
     }
 }
 
-// AntiAliasBwdVtx, n_samples > 0 (f_ops.cpp:2410-2472): one thread per
-// (vertex, slot) row when `wide` (out {V, deg} VEC4, row d * V + v), else one
-// thread per vertex accumulating its slots in order (out {V,1}).
+// AntiAliasBwdVtx, n_samples > 0 (f_ops.cpp:2410-2472): one 8-lane group per
+// (vertex, slot) row when `wide` (out {V, deg} VEC4, row d * V + v), else
+// per vertex accumulating its slots in order (out {V,1}). The group walks
+// the row's faces and samples together; at each sample lane k evaluates the
+// pair with neighbour k and the term it gives v (at most one: an edge's two
+// endpoints differ), then the group adds the eight terms in neighbour order,
+// so the row sums its terms in the reference's (slot, sample, neighbour)
+// order.
 __global__ __launch_bounds__(256) void k_antialias_bwd_vtx_op(
         const float* gy, const float* img, uint32_t n_comp, const float* tri, const float4* clip,
         uint32_t n_verts, const float* faces, uint32_t n_faces, const float* vtx_faces,
         uint32_t max_deg, const float* seed, uint32_t n_samples, int wide, uint32_t w, uint32_t h,
         float4* out) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t i = (blockIdx.x * blockDim.x + threadIdx.x) >> 3;
+    const int k = (int)(threadIdx.x & 7u);
+    const int gbase = (int)(threadIdx.x & 56u);  // the group's first lane in the wave
     const uint32_t rows = wide ? max_deg : 1u;
     if (i >= n_verts * rows) {
-        return;
+        return;  // the whole group: its lanes share i
     }
     const uint32_t v = wide ? i % n_verts : i;
     const uint32_t d0 = wide ? i / n_verts : 0u;
@@ -188,13 +195,13 @@ __global__ __launch_bounds__(256) void k_antialias_bwd_vtx_op(
         }
         float4 c[3];
         bool ok = true;
-        for (int k = 0; k < 3; k++) {
-            const uint32_t vi = FloatFaces{faces}(f, k);
+        for (int q = 0; q < 3; q++) {
+            const uint32_t vi = FloatFaces{faces}(f, q);
             if (vi >= n_verts) {
                 ok = false;
                 break;
             }
-            c[k] = clip[vi];
+            c[q] = clip[vi];
         }
         float s3x[3], s3y[3];
         if (!ok || !aa_face_screen(c, W, H, s3x, s3y)) {
@@ -206,26 +213,66 @@ __global__ __launch_bounds__(256) void k_antialias_bwd_vtx_op(
                 x >= (int)w || y >= (int)h) {
                 continue;
             }
-            const uint32_t its = tri_id(tri, (size_t)y * w + x);
-            for (int k = 0; k < 8; k++) {
-                const int nx = x + kAaOffX[k], ny = y + kAaOffY[k];
-                if (nx < 0 || ny < 0 || nx >= (int)w || ny >= (int)h) {
-                    continue;
-                }
+            // lane k: neighbour k's terms for v, endpoint a then endpoint b
+            // (both only for an edge whose two endpoints are v: a face that
+            // repeats a vertex)
+            float ta[3] = {0.f, 0.f, 0.f}, tb[3] = {0.f, 0.f, 0.f};
+            int has = 0;
+            const int nx = x + kAaOffX[k], ny = y + kAaOffY[k];
+            if (!(nx < 0 || ny < 0 || nx >= (int)w || ny >= (int)h)) {
+                const uint32_t its = tri_id(tri, (size_t)y * w + x);
                 AaPair pr;
-                if (!eval_aa_pair(its, tri_id(tri, (size_t)ny * w + nx), x, y, nx, ny, n_faces,
-                                  TriFromClip{faces, clip, n_verts, W, H}, &pr) ||
-                    pr.r >= 1.f) {
-                    continue;
+                if (eval_aa_pair(its, tri_id(tri, (size_t)ny * w + nx), x, y, nx, ny, n_faces,
+                                 TriFromClip{faces, clip, n_verts, W, H}, &pr) &&
+                    pr.r < 1.f && (pr.ia == v || pr.ib == v)) {
+                    const size_t so = ((size_t)y * w + x) * n_comp;
+                    const size_t no = ((size_t)ny * w + nx) * n_comp;
+                    float gr = 0.f;
+                    for (uint32_t cc = 0; cc < n_comp; cc++) {
+                        gr += gy[so + cc] * (img[so + cc] - img[no + cc]);
+                    }
+                    gr /= 9.f;
+                    if (gr != 0.f) {
+                        float dqa[2], dqb[2];
+                        aa_pair_dq(pr, x, y, dqa, dqb);
+                        const auto term = [&](const float dq[2], float4 ce, float* t) {
+                            const float gqx = gr * dq[0];
+                            const float gqy = gr * dq[1];
+                            t[0] = gqx * 0.5f * W / ce.w;
+                            t[1] = gqy * 0.5f * H / ce.w;
+                            t[2] = -(gqx * 0.5f * W * ce.x + gqy * 0.5f * H * ce.y) /
+                                   (ce.w * ce.w);
+                        };
+                        if (pr.ia == v) {
+                            term(dqa, clip[pr.ia], ta);
+                            has |= 1;
+                        }
+                        if (pr.ib == v) {
+                            term(dqb, clip[pr.ib], tb);
+                            has |= 2;
+                        }
+                    }
                 }
-                if (pr.ia != v && pr.ib != v) {
-                    continue;
+            }
+            for (int kk = 0; kk < 8; kk++) {
+                const int src = gbase + kk;
+                const int fl = __shfl(has, src, 64);
+                if (fl & 1) {
+                    dst.x += __shfl(ta[0], src, 64);
+                    dst.y += __shfl(ta[1], src, 64);
+                    dst.w += __shfl(ta[2], src, 64);
                 }
-                aa_accumulate_v(gy, img, n_comp, clip, W, H, w, v, x, y, nx, ny, pr, &dst);
+                if (fl & 2) {
+                    dst.x += __shfl(tb[0], src, 64);
+                    dst.y += __shfl(tb[1], src, 64);
+                    dst.w += __shfl(tb[2], src, 64);
+                }
             }
         }
     }
-    out[i] = dst;
+    if (k == 0) {
+        out[i] = dst;
+    }
 }
 
 // AntiAliasBwdVtx, n_samples = 0 (f_ops.cpp:2389-2407): the exact scatter
@@ -1122,7 +1169,8 @@ int dressi_antialias_bwd_vtx(dressi_ctx* ctx, const float* gy, const float* img,
                            n_faces, vtx_faces, max_deg, width, height, (float4*)out);
     } else {
         const uint32_t rows = wide ? max_deg : 1u;
-        hipLaunchKernelGGL(k_antialias_bwd_vtx_op, dim3(div_up(n_verts * rows, 256)), dim3(256),
+        DRESSI_REQUIRE((uint64_t)n_verts * rows * 8 < (1ull << 32), "AntiAliasBwdVtx: too many rows");
+        hipLaunchKernelGGL(k_antialias_bwd_vtx_op, dim3(div_up(n_verts * rows * 8, 256)), dim3(256),
                            0, ctx->stream, gy, img, n_comp, tri, (const float4*)clip, n_verts,
                            faces, n_faces, vtx_faces, max_deg, seed, n_samples, wide, width,
                            height, (float4*)out);
