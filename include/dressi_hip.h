@@ -134,6 +134,20 @@ int dressi_rasterize_face_id(dressi_ctx* ctx, const float* clip,
                              uint32_t n_verts, const float* faces,
                              uint32_t n_faces, uint32_t width,
                              uint32_t height, float* out);
+/* A batch of F::Rasterize in one pass: n_items clip sets clip
+ * {n_items, n_verts} x 4 over one face list, attributes shared by the items
+ * (attr_per_item 0: {n_verts} x n_comp) or one set per item (1:
+ * {n_items, n_verts} x n_comp); out {n_items, S, S} x n_comp, each item's
+ * image equal to dressi_rasterize's. face_id (optional, NULL to skip)
+ * {n_items, S, S} gets dressi_rasterize_face_id's image of each item from
+ * the same pass. No counterpart in the reference (its torch surface batches
+ * through one engine graph per batch): the batch entry the torch surface's
+ * rasterize uses. */
+int dressi_rasterize_batch(dressi_ctx* ctx, const float* clip, uint32_t n_verts,
+                           uint32_t n_items, const float* attr, uint32_t n_comp,
+                           int attr_per_item, const float* faces, uint32_t n_faces,
+                           uint32_t width, uint32_t height, float* out,
+                           float* face_id);
 
 /* F::LookupFaces forward / backward (src/core/f_ops.cpp:1521-1619):
  * out{F} = attr[faces[f][corner]]; bwd: per vertex, rows d ascending of

@@ -80,6 +80,7 @@ _SIGS = {
     "dressi_rasterize_soft_noalloc": (_I, [_P, _P, _P, _P, _P, _U, _P, _U, _U, _U, _F, _P, _P]),
     "dressi_rasterize": (_I, [_P, _P, _U, _P, _U, _P, _U, _U, _U, _P]),
     "dressi_rasterize_face_id": (_I, [_P, _P, _U, _P, _U, _U, _U, _P]),
+    "dressi_rasterize_batch": (_I, [_P, _P, _U, _U, _P, _U, _I, _P, _U, _U, _U, _P, _P]),
     "dressi_lookup_faces": (_I, [_P, _P, _U, _U, _P, _U, _U, _P]),
     "dressi_lookup_faces_bwd": (_I, [_P, _P, _U, _P, _U, _P, _U, _U, _U, _P]),
     "dressi_face_fetch": (_I, [_P, _P, _U, _U, _P, _U, _U, _P]),

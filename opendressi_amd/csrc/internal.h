@@ -185,7 +185,7 @@ int launch_hard_setup(hipStream_t s, const RasterGeom& g, const float* clip, uin
                       const int32_t* faces, HardRec* recs);
 int launch_raster_hard(hipStream_t s, const RasterGeom& g, const HardRec* recs,
                        const BinBuffers& b, const float* attr, uint32_t n_comp, int mode,
-                       float* out);
+                       float* out, size_t attr_view = 0, float* ids = nullptr);
 
 // Sizes of the binning buffers for a problem; `cap` = list capacity.
 size_t bin_bytes(uint32_t n_bins, uint32_t cap);

@@ -176,7 +176,8 @@ int launch_hard_setup(hipStream_t s, const RasterGeom& g, const float* clip, uin
 __global__ __launch_bounds__(kTileThreads) void k_raster_hard(RasterGeom g, const HardRec* recs,
                                                               BinBuffers b, const float* attr,
                                                               uint32_t n_comp, int mode,
-                                                              float* out) {
+                                                              float* out, size_t attr_view,
+                                                              float* ids) {
     __shared__ HardRec lds_rec[kTileThreads];
     __shared__ uint32_t lds_face[kTileThreads];
     const uint32_t tile = blockIdx.x;
@@ -191,6 +192,9 @@ __global__ __launch_bounds__(kTileThreads) void k_raster_hard(RasterGeom g, cons
         return;
     }
     const size_t o = ((size_t)view * g.height + py) * g.width + px;
+    if (ids) {
+        ids[o] = best == kEmptyKey ? 0.f : (float)key_face(best) + 1.f;
+    }
     if (best == kEmptyKey) {
         for (uint32_t c = 0; c < n_comp; c++) {
             out[o * n_comp + c] = 0.f;
@@ -202,6 +206,7 @@ __global__ __launch_bounds__(kTileThreads) void k_raster_hard(RasterGeom g, cons
         out[o] = (float)f + 1.f;
         return;
     }
+    attr += (size_t)view * attr_view;
     const HardRec& r = vrec[f];
     float l[3];
     barycentric((float)px + 0.5f, (float)py + 0.5f, r.x[0], r.y[0], r.x[1], r.y[1], r.x[2],
@@ -218,9 +223,9 @@ __global__ __launch_bounds__(kTileThreads) void k_raster_hard(RasterGeom g, cons
 
 int launch_raster_hard(hipStream_t s, const RasterGeom& g, const HardRec* recs,
                        const BinBuffers& b, const float* attr, uint32_t n_comp, int mode,
-                       float* out) {
+                       float* out, size_t attr_view, float* ids) {
     hipLaunchKernelGGL(k_raster_hard, dim3(g.n_tiles, g.n_views), dim3(kTileThreads), 0, s, g,
-                       recs, b, attr, n_comp, mode, out);
+                       recs, b, attr, n_comp, mode, out, attr_view, ids);
     DRESSI_CHECK_LAUNCH();
     return DRESSI_OK;
 }
@@ -509,25 +514,33 @@ int dressi_rasterize_soft_noalloc(dressi_ctx* ctx, const float* soft_clip, const
                                  out);
 }
 
+// `n_items` clip sets [n_items][n_verts] over one face list; attributes
+// shared by the items (attr_view 0) or per item (attr_view = n_verts * n_comp
+// floats apart); `ids` (optional) gets RasterizeFaceId's output alongside.
 static int rasterize_hard_common(dressi_ctx* ctx, const float* clip, uint32_t n_verts,
                                  const float* attr, uint32_t n_comp, const float* faces,
                                  uint32_t n_faces, uint32_t width, uint32_t height, int mode,
-                                 float* out) {
+                                 float* out, uint32_t n_items = 1, size_t attr_view = 0,
+                                 float* ids = nullptr) {
     if (int rc = check_ctx(ctx)) return rc;
     DRESSI_REQUIRE(clip && (faces || n_faces == 0) && out && (mode == 1 || attr),
                    "rasterize: NULL buffer");
     DRESSI_REQUIRE(width > 0 && height > 0, "rasterize: empty screen");
     DRESSI_REQUIRE(mode == 1 || (n_comp >= 1 && n_comp <= 4), "rasterize: n_comp must be 1..4");
-    const RasterGeom g = make_geom(width, height, 1, n_faces);
+    DRESSI_REQUIRE(n_items >= 1 && (uint64_t)n_items * n_faces < (1ull << 31) &&
+                           (uint64_t)n_items * n_verts < (1ull << 31),
+                   "rasterize: too many items");
+    const RasterGeom g = make_geom(width, height, n_items, n_faces);
     const uint32_t cap = default_bin_cap(g, 8);
     void *recs = nullptr, *bins = nullptr, *fi = nullptr;
     const size_t nf1 = n_faces ? n_faces : 1;
-    if (int rc = ctx_workspace(ctx, 0, sizeof(HardRec) * nf1, &recs)) return rc;
-    if (int rc = ctx_workspace(ctx, 1, bin_bytes(g.n_tiles, cap), &bins)) return rc;
+    if (int rc = ctx_workspace(ctx, 0, sizeof(HardRec) * nf1 * n_items, &recs)) return rc;
+    if (int rc = ctx_workspace(ctx, 1, bin_bytes(g.n_tiles * n_items, cap), &bins)) return rc;
     if (int rc = ctx_workspace(ctx, 2, sizeof(int32_t) * 3 * nf1, &fi)) return rc;
     BinBuffers b;
-    bin_carve(bins, g.n_tiles, cap, &b);
-    if (int rc = launch_zero(ctx->stream, b.counts, sizeof(uint32_t) * g.n_tiles)) return rc;
+    bin_carve(bins, g.n_tiles * n_items, cap, &b);
+    if (int rc = launch_zero(ctx->stream, b.counts, sizeof(uint32_t) * g.n_tiles * n_items))
+        return rc;
     if (n_faces) {
         hipLaunchKernelGGL(k_faces_to_i32, dim3(div_up(3 * n_faces, 256)), dim3(256), 0,
                            ctx->stream, faces, 3 * n_faces, n_verts, ctx->d_err, (int32_t*)fi);
@@ -541,7 +554,7 @@ static int rasterize_hard_common(dressi_ctx* ctx, const float* clip, uint32_t n_
         if (int rc = launch_bin_hard(ctx->stream, g, (const HardRec*)recs, b)) return rc;
     }
     return launch_raster_hard(ctx->stream, g, (const HardRec*)recs, b, attr, mode == 1 ? 1 : n_comp,
-                              mode, out);
+                              mode, out, attr_view, ids);
 }
 
 int dressi_rasterize(dressi_ctx* ctx, const float* clip, uint32_t n_verts, const float* attr,
@@ -556,6 +569,15 @@ int dressi_rasterize_face_id(dressi_ctx* ctx, const float* clip, uint32_t n_vert
                              uint32_t height, float* out) {
     return rasterize_hard_common(ctx, clip, n_verts, nullptr, 1, faces, n_faces, width, height,
                                  1, out);
+}
+
+int dressi_rasterize_batch(dressi_ctx* ctx, const float* clip, uint32_t n_verts,
+                           uint32_t n_items, const float* attr, uint32_t n_comp,
+                           int attr_per_item, const float* faces, uint32_t n_faces,
+                           uint32_t width, uint32_t height, float* out, float* face_id) {
+    return rasterize_hard_common(ctx, clip, n_verts, attr, n_comp, faces, n_faces, width, height,
+                                 0, out, n_items, attr_per_item ? (size_t)n_verts * n_comp : 0,
+                                 face_id);
 }
 
 }  // extern "C"

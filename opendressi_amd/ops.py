@@ -80,6 +80,25 @@ def rasterize_face_id(ctx: Context, clip: torch.Tensor, faces: torch.Tensor, wid
     return out
 
 
+def rasterize_batch(ctx: Context, clip: torch.Tensor, attr: torch.Tensor, faces: torch.Tensor,
+                    width: int, height: int, with_face_id: bool = False):
+    """dressi_rasterize_batch: clip (N, V, 4), attr (V, C) shared or (N, V, C)
+    per item -> (N, H, W, C) and, with `with_face_id`, the (N, H, W) face
+    ids from the same pass (each item as rasterize / rasterize_face_id)."""
+    _prep(ctx)
+    n, nv = clip.shape[0], clip.shape[1]
+    per_item = attr.dim() == 3
+    nc = attr.shape[-1]
+    out = torch.empty((n, height, width, nc), dtype=torch.float32, device=clip.device)
+    ids = (torch.empty((n, height, width), dtype=torch.float32, device=clip.device)
+           if with_face_id else None)
+    check(lib.dressi_rasterize_batch(ctx.handle, _ptr(clip, "clip"), nv, n, _ptr(attr, "attr"),
+                                     nc, 1 if per_item else 0, _ptr(faces, "faces"),
+                                     faces.shape[0], width, height, _ptr(out, "out"),
+                                     _ptr(ids, "face_id")))
+    return (out, ids) if with_face_id else out
+
+
 def lookup_faces(ctx: Context, attr: torch.Tensor, faces: torch.Tensor, corner: int) -> torch.Tensor:
     """F::LookupFaces (src/core/f_ops.cpp:1568-1619) -> (F, C)."""
     _prep(ctx)

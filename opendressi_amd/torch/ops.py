@@ -8,8 +8,9 @@ device, with no host round trip. The backward of every op composes the
 reference's backward kernels exactly as the reference's backward builder does
 (src/core/build_backward.cpp:62-149): the same kernels, the same operand
 order, gradient contributions summed in descending creation order of the
-nodes that produced them. A batch of N items runs the per-item kernels N
-times; per-signature constants live in the context's `_engines`.
+nodes that produced them. rasterize runs the whole batch in one raster
+pass; the other ops run their per-item kernels for each item; per-signature
+constants live in the context's `_engines`.
 """
 from __future__ import annotations
 
@@ -77,17 +78,17 @@ def rasterize(ctx: RasterizeHipContext, pos: torch.Tensor, tri: torch.Tensor, re
 
     eng = ctx.engine(("rasterize", h, w, md.n_faces, md.n_verts, n), build)
     clip_vk = clip_gl_to_vk(pos_b)
-    outs = []
     with ctx.lock:
-        for i in range(n):
-            clip3 = clip_vk[i][md.unweld].contiguous()
-            attr4 = torch.cat([eng.corner_uv, pos_b[i][md.unweld][:, 2:4]], dim=1).contiguous()
-            g = K.rasterize(ctx._ctx, clip3, attr4, md.faces_seq, w, h)
-            tid = K.rasterize_face_id(ctx._ctx, clip3, md.faces_seq, w, h)
-            mask = (tid > 0.5).to(torch.float32)
-            zw = g[..., 2] / (g[..., 3] + (1.0 - mask))
-            outs.append(torch.stack([g[..., 0], g[..., 1], zw, tid], dim=-1))
-    rast = torch.stack(outs, 0).to(pos.device)
+        # every item in one pass: attributes and face ids from the same raster
+        clip3 = clip_vk[:, md.unweld].contiguous()
+        attr4 = torch.cat([eng.corner_uv.expand(n, -1, -1), pos_b[:, md.unweld][:, :, 2:4]],
+                          dim=2).contiguous()
+        g, tid = K.rasterize_batch(ctx._ctx, clip3, attr4, md.faces_seq, w, h,
+                                   with_face_id=True)
+        mask = (tid > 0.5).to(torch.float32)
+        zw = g[..., 2] / (g[..., 3] + (1.0 - mask))
+        rast = torch.stack([g[..., 0], g[..., 1], zw, tid], dim=-1)
+    rast = rast.to(pos.device)
     stamp(rast, RasterOrigin(clip_vk=clip_vk, tri=tri, resolution=(h, w), ctx=ctx))
     return rast, torch.zeros_like(rast)
 
