@@ -513,7 +513,9 @@ int dressi_hsr_step_eager(dressi_hsr_plan* plan, uint32_t n_iters);
 enum dressi_hsr_buffer {
     DRESSI_HSR_LOSS = 0,    /* {S,S} float: the loss image */
     DRESSI_HSR_PRED = 1,    /* {N,S,S} float (needs DRESSI_HSR_KEEP_PRED) */
-    DRESSI_HSR_TARGET = 2,  /* {N,S,S} float */
+    DRESSI_HSR_TARGET = 2,  /* {N,S,S} float (read only: set_targets and
+                               render_targets are its writers, they also
+                               refresh the plan's byte copy of 0 / 1 targets) */
     DRESSI_HSR_FACE_ID = 3, /* {N,S,S} uint32: face + 1 of RasterizeSoft, 0 bg;
                                bit 31 set when the winning fragment lies
                                outside its hard triangle (signed dist < 0).

@@ -106,58 +106,184 @@ __global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
 // Forward tail per pixel: pred of every view from its face-id entry
 // (background 0; a hard-branch winner gives cov * step(0, dist) = 1 >= the
 // soft silhouette, so max(hard, soft) = 1; a rim winner evaluates the pixel
-// chain), the L2 loss per view and their SumPixelWise over views.
-template <int NV>
+// chain), the L2 loss per view and their SumPixelWise over views. A lane
+// takes P pixels of a row (width % P == 0): the face ids of every view as
+// one P-word load, the targets as P bytes (0 / 1 targets) or P floats, pred
+// and loss as P-word stores.
+template <int P>
+struct LossVec;
+template <>
+struct LossVec<1> {
+    static __device__ __forceinline__ void ids(const uint32_t* p, uint32_t (&v)[1]) { v[0] = *p; }
+    static __device__ __forceinline__ void bytes(const uint8_t* p, float (&v)[1]) {
+        v[0] = (float)*p;
+    }
+    static __device__ __forceinline__ void floats(const float* p, float (&v)[1]) { v[0] = *p; }
+    static __device__ __forceinline__ void store(float* p, const float (&v)[1]) { *p = v[0]; }
+};
+template <>
+struct LossVec<4> {
+    static __device__ __forceinline__ void ids(const uint32_t* p, uint32_t (&v)[4]) {
+        const uint4 q = *reinterpret_cast<const uint4*>(p);
+        v[0] = q.x;
+        v[1] = q.y;
+        v[2] = q.z;
+        v[3] = q.w;
+    }
+    static __device__ __forceinline__ void bytes(const uint8_t* p, float (&v)[4]) {
+        const uint32_t q = *reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            v[c] = (float)((q >> (8 * c)) & 0xffu);
+        }
+    }
+    static __device__ __forceinline__ void floats(const float* p, float (&v)[4]) {
+        const float4 q = *reinterpret_cast<const float4*>(p);
+        v[0] = q.x;
+        v[1] = q.y;
+        v[2] = q.z;
+        v[3] = q.w;
+    }
+    static __device__ __forceinline__ void store(float* p, const float (&v)[4]) {
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+};
+
+template <int NV, int P>
 __global__ __launch_bounds__(256) void k_hsr_loss(HsrDev d) {
-    const uint32_t x = blockIdx.x * 64 + (threadIdx.x & 63);
-    const uint32_t y = blockIdx.y * 4 + (threadIdx.x >> 6);
-    if (x >= d.g.width || y >= d.g.height) {
+    static_assert(NV * P <= 32, "rim bits");
+    const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
+    const uint32_t x0 = (blockIdx.x * 64 + lane) * P;
+    const uint32_t y = blockIdx.y * 4 + wv;
+    // lanes past the edge stay for the wave's exchanges (no rim, no stores)
+    const bool valid = x0 < d.g.width && y < d.g.height;
+    const size_t npx = (size_t)d.g.width * d.g.height;
+    const size_t o = valid ? (size_t)y * d.g.width + x0 : 0;
+    uint32_t id[NV][P];
+    float tg[NV][P];
+    // the loads of every view issued together (invalid lanes read pixel 0)
+#pragma unroll
+    for (int view = 0; view < NV; view++) {
+        LossVec<P>::ids(d.ids + view * npx + o, id[view]);
+    }
+    if (d.tgt8) {
+#pragma unroll
+        for (int view = 0; view < NV; view++) {
+            LossVec<P>::bytes(d.tgt8 + view * npx + o, tg[view]);
+        }
+    } else {
+#pragma unroll
+        for (int view = 0; view < NV; view++) {
+            LossVec<P>::floats(d.targets + view * npx + o, tg[view]);
+        }
+    }
+#pragma unroll
+    for (int view = 0; view < NV; view++) {
+#pragma unroll
+        for (int c = 0; c < P; c++) {
+            id[view][c] = valid ? id[view][c] : 0u;
+        }
+    }
+    // hard-branch winners and background directly; the rim winners (a few
+    // per silhouette crossing) are dealt out one per lane, 64 per round, so a
+    // wave evaluates its rim pixels side by side instead of one after another
+    __shared__ uint2 s_item[4][64];  // (face id, lane | c << 6 | view << 8)
+    __shared__ float s_pred[4][64];
+    float pred[NV][P];
+    uint32_t rim = 0;  // bit view * P + c
+#pragma unroll
+    for (int view = 0; view < NV; view++) {
+#pragma unroll
+        for (int c = 0; c < P; c++) {
+            pred[view][c] = id[view][c] ? 1.f : 0.f;
+            rim |= (id[view][c] >> 31) << (view * P + c);
+        }
+    }
+    if (__ballot(rim != 0)) {
+        // exclusive prefix of the lanes' rim counts
+        const uint32_t cnt = __popc(rim);
+        uint32_t incl = cnt;
+#pragma unroll
+        for (int k = 1; k < 64; k <<= 1) {
+            const uint32_t t = (uint32_t)__shfl_up((int)incl, k);
+            incl += lane >= (uint32_t)k ? t : 0u;
+        }
+        const uint32_t first = incl - cnt;
+        const uint32_t total = (uint32_t)__shfl((int)incl, 63);
+        for (uint32_t base = 0; base < total; base += 64) {
+            uint32_t k = first;
+#pragma unroll
+            for (int view = 0; view < NV; view++) {
+#pragma unroll
+                for (int c = 0; c < P; c++) {
+                    if ((rim >> (view * P + c)) & 1u) {
+                        if (k - base < 64u) {
+                            s_item[wv][k - base] = make_uint2(
+                                id[view][c], lane | (uint32_t)c << 6 | (uint32_t)view << 8);
+                        }
+                        k++;
+                    }
+                }
+            }
+            wave_lds_fence();
+            if (base + lane < total) {
+                const uint2 it = s_item[wv][lane];
+                const uint32_t view = it.y >> 8, c = (it.y >> 6) & 3u, owner = it.y & 63u;
+                const size_t fi = (size_t)view * d.g.n_faces + (it.x & ~kRimFlag) - 1;
+                const float4 a = d.fscr[fi * 2];
+                const float4 b = d.fscr[fi * 2 + 1];
+                PixelFw st;
+                st.s[0][0] = a.x;
+                st.s[0][1] = a.y;
+                st.s[1][0] = a.z;
+                st.s[1][1] = a.w;
+                st.s[2][0] = b.x;
+                st.s[2][1] = b.y;
+                const uint32_t px = (blockIdx.x * 64 + owner) * P + c;
+                pixel_fw_screen(1.f, -1.f, 1.f, (float)px + 0.5f, (float)y + 0.5f,
+                                d.sigma_scale, st);
+                s_pred[wv][lane] = st.pred;
+            }
+            wave_lds_fence();
+            k = first;
+#pragma unroll
+            for (int view = 0; view < NV; view++) {
+#pragma unroll
+                for (int c = 0; c < P; c++) {
+                    if ((rim >> (view * P + c)) & 1u) {
+                        if (k - base < 64u) {
+                            pred[view][c] = s_pred[wv][k - base];
+                        }
+                        k++;
+                    }
+                }
+            }
+            wave_lds_fence();
+        }
+    }
+    if (!valid) {
         return;
     }
-    const size_t npx = (size_t)d.g.width * d.g.height;
-    const size_t o = (size_t)y * d.g.width + x;
-    // every view's face id and target first, then the rim winners' screen
-    // corners (the setup's chain_screen of the face): each round of loads in
-    // flight together
-    uint32_t id[NV];
-    float tg[NV];
+    if (d.pred) {
 #pragma unroll
-    for (int view = 0; view < NV; view++) {
-        id[view] = d.ids[view * npx + o];
-        tg[view] = d.targets[view * npx + o];
-    }
-    float4 sc[NV][2];
-#pragma unroll
-    for (int view = 0; view < NV; view++) {
-        const bool rim = (id[view] & kRimFlag) != 0;
-        const size_t fi = (size_t)view * d.g.n_faces + (rim ? (id[view] & ~kRimFlag) - 1 : 0u);
-        sc[view][0] = rim ? d.fscr[fi * 2] : make_float4(0.f, 0.f, 0.f, 0.f);
-        sc[view][1] = rim ? d.fscr[fi * 2 + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    float lv[NV][1];
-#pragma unroll
-    for (int view = 0; view < NV; view++) {
-        float pred = id[view] ? 1.f : 0.f;
-        if (id[view] & kRimFlag) {
-            PixelFw st;
-            st.s[0][0] = sc[view][0].x;
-            st.s[0][1] = sc[view][0].y;
-            st.s[1][0] = sc[view][0].z;
-            st.s[1][1] = sc[view][0].w;
-            st.s[2][0] = sc[view][1].x;
-            st.s[2][1] = sc[view][1].y;
-            pixel_fw_screen(1.f, -1.f, 1.f, (float)x + 0.5f, (float)y + 0.5f, d.sigma_scale, st);
-            pred = st.pred;
+        for (int view = 0; view < NV; view++) {
+            LossVec<P>::store(d.pred + view * npx + o, pred[view]);
         }
-        if (d.pred) {
-            d.pred[view * npx + o] = pred;
-        }
-        const float diff = tg[view] - pred;
-        lv[view][0] = diff * diff * d.inv_px;
     }
-    float out[1];
-    Tree<NV, 1>::run(lv, out);
-    d.loss[o] = out[0];
+    float outp[P];
+#pragma unroll
+    for (int c = 0; c < P; c++) {
+        float lv[NV][1];
+#pragma unroll
+        for (int view = 0; view < NV; view++) {
+            const float diff = tg[view][c] - pred[view][c];
+            lv[view][0] = diff * diff * d.inv_px;
+        }
+        float out[1];
+        Tree<NV, 1>::run(lv, out);
+        outp[c] = out[0];
+    }
+    LossVec<P>::store(d.loss + o, outp);
 }
 
 // FaceFetchBwd (stochastic, n samples, seed = t) fused with the pixel
@@ -218,6 +344,7 @@ __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
     const size_t npx = (size_t)d.g.width * d.g.height;
     const uint32_t* ids = d.ids + view * npx;
     const float* tgt = d.targets + view * npx;
+    const uint8_t* tgt8 = d.tgt8 ? d.tgt8 + view * npx : nullptr;
     const uint32_t want = (f + 1) | kRimFlag;
     for (uint32_t s0 = 0; s0 < d.n_samples && __any(ok); s0 += kSampleLanes) {
         const uint32_t smp = s0 + (uint32_t)j;
@@ -253,7 +380,8 @@ __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
             const float pcx = (float)ix + 0.5f, pcy = (float)iy + 0.5f;
             PixelFw st;
             pixel_fw(c, 1.f, -1.f, 1.f, pcx, pcy, W, H, d.sigma_scale, st);
-            pixel_bw(st, c, 1.f, tgt[pix], d.inv_px, W, H, d.sigma_scale, g);
+            pixel_bw(st, c, 1.f, tgt8 ? (float)tgt8[pix] : tgt[pix], d.inv_px, W, H,
+                     d.sigma_scale, g);
         }
         if (__any(hit)) {
             // the group's first lane adds the samples in order
@@ -493,6 +621,8 @@ struct dressi_hsr_plan {
     std::vector<void*> allocs;
     void* bin_mem = nullptr;     // the soft bins (resized by grow_bins)
     uint32_t* over_host = nullptr;  // host-mapped: d.bin_over
+    uint8_t* tgt_bytes = nullptr;   // HardSoftRas: d.tgt8 when the targets are all 0 / 1
+    uint32_t* nonbinary = nullptr;  // set by k_target_bytes on a target other than 0 / 1
     bool mesh_set = false, targets_set = false, state_set = false;
     hipGraph_t graph = nullptr;  // one iteration
     hipGraphExec_t exec = nullptr;
@@ -510,6 +640,22 @@ int plan_alloc(dressi_hsr_plan* p, T** out, size_t count) {
     p->allocs.push_back(ptr);
     *out = (T*)ptr;
     return DRESSI_OK;
+}
+
+// Byte copy of the targets for the loss and face backward: out[i] = t[i]
+// (0 or 1); any other bit pattern (-0, fractions, NaN) sets *nonbinary and
+// the plan keeps reading the float targets.
+__global__ __launch_bounds__(256) void k_target_bytes(const float* t, size_t n, uint8_t* out,
+                                                      uint32_t* nonbinary) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) {
+        return;
+    }
+    const uint32_t u = __float_as_uint(t[i]);
+    out[i] = u == 0x3f800000u ? 1u : 0u;
+    if (u != 0u && u != 0x3f800000u) {
+        *nonbinary = 1u;
+    }
 }
 
 // Iterations per replay of the batched graph (dressi_hsr_step launches it
@@ -538,11 +684,18 @@ int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
                                dim3(64), 0, s, d);
             break;
         case 2: {
-            const dim3 grid(div_up(g.width, 64), div_up(g.height, 4));
+            // four pixels per lane where the grid still fills the chip
+            const bool vec = g.width % 4 == 0 &&
+                             (size_t)div_up(g.width, 256) * div_up(g.height, 4) >= 2048;
+            const dim3 grid(div_up(g.width, vec ? 256 : 64), div_up(g.height, 4));
             switch (g.n_views) {
 #define DRESSI_NV(N)                                                                          \
     case N:                                                                                   \
-        hipLaunchKernelGGL(k_hsr_loss<N>, grid, dim3(256), 0, s, d);                          \
+        if (vec) {                                                                            \
+            hipLaunchKernelGGL((k_hsr_loss<N, 4>), grid, dim3(256), 0, s, d);                 \
+        } else {                                                                              \
+            hipLaunchKernelGGL((k_hsr_loss<N, 1>), grid, dim3(256), 0, s, d);                 \
+        }                                                                                     \
         break;
                 DRESSI_NV(1) DRESSI_NV(2) DRESSI_NV(3) DRESSI_NV(4)
                 DRESSI_NV(5) DRESSI_NV(6) DRESSI_NV(7) DRESSI_NV(8)
@@ -643,6 +796,31 @@ int grow_bins(dressi_hsr_plan* p) {
     return DRESSI_OK;
 }
 
+// After the targets change (HardSoftRas): the byte copy and d.tgt8, which
+// is null unless every target is exactly 0 or 1. The captured graphs hold
+// d by value, so a change of d.tgt8 drops them.
+int refresh_target_bytes(dressi_hsr_plan* p) {
+    if (!p->tgt_bytes) {
+        return DRESSI_OK;
+    }
+    hipStream_t s = p->ctx->stream;
+    const size_t n = (size_t)p->desc.n_views * p->desc.width * p->desc.height;
+    DRESSI_TRY_HIP(hipMemsetAsync(p->nonbinary, 0, sizeof(uint32_t), s));
+    hipLaunchKernelGGL(k_target_bytes, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                       p->d.targets, n, p->tgt_bytes, p->nonbinary);
+    DRESSI_TRY_HIP(hipGetLastError());
+    uint32_t nonbinary = 1;
+    DRESSI_TRY_HIP(hipMemcpyAsync(&nonbinary, p->nonbinary, sizeof(uint32_t),
+                                  hipMemcpyDeviceToHost, s));
+    DRESSI_TRY_HIP(hipStreamSynchronize(s));
+    const uint8_t* t8 = nonbinary ? nullptr : p->tgt_bytes;
+    if (t8 != p->d.tgt8) {
+        p->d.tgt8 = t8;
+        drop_graph(p);
+    }
+    return DRESSI_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -688,6 +866,8 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
         rc = rc ? rc : plan_alloc(p, &d.cull, N * F);
         rc = rc ? rc : plan_alloc(p, &d.fscr, N * F * 2);
         rc = rc ? rc : plan_alloc(p, &d.rimf, N * F);
+        rc = rc ? rc : plan_alloc(p, &p->tgt_bytes, N * npx);
+        rc = rc ? rc : plan_alloc(p, &p->nonbinary, 1);
         d.heavy.cap = heavy_seg_cap(d.g.n_tiles * d.g.n_views);
         rc = rc ? rc : plan_alloc(p, &d.heavy.count, kHeavySegs);
         rc = rc ? rc : plan_alloc(p, &d.heavy.list, kHeavyCap);
@@ -856,6 +1036,7 @@ int dressi_hsr_set_targets(dressi_hsr_plan* p, const float* targets) {
     DRESSI_TRY_HIP(hipMemcpyAsync((void*)p->d.targets, targets, n * 4, hipMemcpyHostToDevice,
                                   p->ctx->stream));
     DRESSI_TRY_HIP(hipStreamSynchronize(p->ctx->stream));
+    if (int rc = refresh_target_bytes(p)) return rc;
     p->targets_set = true;
     return DRESSI_OK;
 }
@@ -933,6 +1114,7 @@ int dressi_hsr_render_targets(dressi_hsr_plan* p, const float* tgt_pos, uint32_t
     if (int rc = launch_raster_hard(s, g, (const HardRec*)recs, b, (const float*)ones, 1, 0,
                                     (float*)p->d.targets)) return rc;
     DRESSI_TRY_HIP(hipStreamSynchronize(s));
+    if (int rc = refresh_target_bytes(p)) return rc;
     p->targets_set = true;
     return DRESSI_OK;
 }

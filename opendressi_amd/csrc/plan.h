@@ -68,6 +68,8 @@ struct HsrDev {
     const uint8_t* vf_mask;   // [deg][V], bit k: faces[vf][k] == v
     const float* mvps;        // [N][16]
     const float* targets;     // [N][S][S]
+    const uint8_t* tgt8;      // [N][S][S] the same targets as bytes when every one is
+                              // exactly 0 or 1 (hard-rasterized silhouettes), else null
     SoftRec* recs;            // [N][F]
     CullRec* cull;            // [N][F]
     BinBuffers bins;          // fixed-capacity soft bins, N x tiles; the

@@ -211,3 +211,77 @@ def test_overflowing_bins_grow(ctx, oracle, technique):
     assert np.array_equal(pred, ref["pred0"])
     assert np.array_equal(grad, ref["grad0"]), rel_err(grad, ref["grad0"])
     assert np.array_equal(pos_gpu, ref["pos"]), float(np.abs(pos_gpu - ref["pos"]).max())
+
+
+def _small_scene(oracle):
+    pos, faces = oracle.icosphere(3)
+    tgt = (pos * np.float32(1.05)).astype(np.float32)
+    proj = oracle.perspective_vk(45.0 * 3.14159265 / 180.0, 1.0, 0.1, 100.0)
+    mvps = np.stack([oracle.mat4_mul(proj, oracle.look_at(e))
+                     for e in ((0.0, 0.6, 3.0), (2.5, -0.8, 1.5))])
+    return pos, faces, tgt, mvps
+
+
+def test_width_not_multiple_of_four_matches_oracle(ctx, oracle):
+    """98 x 98 (the loss kernel's one-pixel-per-lane form; partial tiles):
+    face ids, pred, loss image and gradient of the first iteration and the
+    parameters after three, bit for bit."""
+    import opendressi_amd as od
+    from opendressi_amd import _lib as L
+    pos, faces, tgt, mvps = _small_scene(oracle)
+    s = 98
+    print(f"[hsr width] ico3 {s}px 2 views", flush=True)
+    fit = od.SilhouetteFit(ctx, pos, faces, mvps, s, target_mesh=(tgt, faces), lr=1e-3,
+                           keep_pred=True, keep_grad=True)
+    fit.step(1)
+    ctx.synchronize()
+    ids, pred, loss = fit.read(L.BUF_FACE_ID), fit.read(L.BUF_PRED), fit.read(L.BUF_LOSS)
+    grad = fit.read(L.BUF_GRAD)
+    fit.step(2)
+    pos_gpu = fit.state()[0]
+    fit.close()
+    ref = oracle.hsr_fit(pos, faces, tgt, faces, mvps, s, lr=1e-3, iters=3, want_images=True)
+    assert (ids != 0).sum() > 500
+    assert np.array_equal(ids, ids_of_rs(ref["rs0"]))
+    assert np.array_equal(pred, ref["pred0"])
+    assert np.array_equal(loss, ref["lossimg0"])
+    assert np.array_equal(grad, ref["grad0"]), rel_err(grad, ref["grad0"])
+    assert np.array_equal(pos_gpu, ref["pos"])
+
+
+@pytest.mark.parametrize("s", [96, 2048])
+def test_float_targets_match_byte_targets(ctx, oracle, s):
+    """Targets that are all 0 / 1 are read as bytes; any other bit pattern
+    keeps the float targets. The rendered targets with each 0 stored as -0
+    take the float path and give the same fit bit for bit (the loss squares
+    the difference; every sampled pixel has pred > 0). 96 px: one pixel per
+    lane in the loss kernel; 2048 px: four."""
+    import opendressi_amd as od
+    from opendressi_amd import _lib as L
+    pos, faces, tgt, mvps = _small_scene(oracle)
+    print(f"[hsr float targets] ico3 {s}px 2 views", flush=True)
+    runs = []
+    rendered = None
+    for neg_zero in (False, True):
+        kw = dict(target_mesh=(tgt, faces)) if not neg_zero else dict(
+            targets=np.where(rendered == 0, np.float32(-0.0), rendered).astype(np.float32))
+        fit = od.SilhouetteFit(ctx, pos, faces, mvps, s, lr=1e-3, keep_pred=True,
+                               keep_grad=True, **kw)
+        if not neg_zero:
+            rendered = fit.read(L.BUF_TARGET)
+            assert set(np.unique(rendered).tolist()) == {0.0, 1.0}
+        else:
+            assert np.signbit(fit.read(L.BUF_TARGET)).any()
+        fit.step(1)
+        ctx.synchronize()
+        out = [fit.read(L.BUF_FACE_ID), fit.read(L.BUF_PRED), fit.read(L.BUF_LOSS),
+               fit.read(L.BUF_GRAD)]
+        fit.step(2)
+        out.append(fit.state()[0])
+        fit.close()
+        runs.append(out)
+    for a, b in zip(*runs):
+        assert np.array_equal(a, b)
+    ref = oracle.hsr_fit(pos, faces, tgt, faces, mvps, s, lr=1e-3, iters=3, want_images=False)
+    assert np.array_equal(runs[1][3], ref["grad0"])
+    assert np.array_equal(runs[1][4], ref["pos"])
