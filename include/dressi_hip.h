@@ -208,6 +208,38 @@ int dressi_antialias_bwd_vtx(dressi_ctx* ctx, const float* gy, const float* img,
 int dressi_col_sum(dressi_ctx* ctx, const float* x, uint32_t n_comp,
                    uint32_t width, uint32_t height, float* out);
 
+/* Batched forms of the four entry points above (an extension with no
+ * counterpart in the reference, which evaluates one image per graph: the
+ * torch surface's antialias runs a whole batch per launch). n_items images
+ * back to back ([item][H][W] x n_comp, face ids [item][H][W]); clip is
+ * [item][V] VEC4 when clip_per_item, else one {V,1} shared by the items;
+ * seeds [item] (device); outputs [item][...] of the single-item shape. Each
+ * item's result equals the single-item call's. n_items <= 65535. */
+int dressi_antialias_batch(dressi_ctx* ctx, const float* img, uint32_t n_comp,
+                           const float* tri, const float* clip, uint32_t n_verts,
+                           int clip_per_item, const float* faces,
+                           uint32_t n_faces, uint32_t width, uint32_t height,
+                           uint32_t n_items, float* out);
+int dressi_antialias_bwd_img_batch(dressi_ctx* ctx, const float* gy,
+                                   uint32_t n_comp, const float* tri,
+                                   const float* clip, uint32_t n_verts,
+                                   int clip_per_item, const float* faces,
+                                   uint32_t n_faces, uint32_t width,
+                                   uint32_t height, uint32_t n_items,
+                                   float* out);
+int dressi_antialias_bwd_vtx_batch(dressi_ctx* ctx, const float* gy,
+                                   const float* img, uint32_t n_comp,
+                                   const float* tri, const float* clip,
+                                   uint32_t n_verts, int clip_per_item,
+                                   const float* faces, uint32_t n_faces,
+                                   const float* vtx_faces, uint32_t max_deg,
+                                   const float* seeds, uint32_t n_samples,
+                                   int wide, uint32_t width, uint32_t height,
+                                   uint32_t n_items, float* out);
+int dressi_col_sum_batch(dressi_ctx* ctx, const float* x, uint32_t n_comp,
+                         uint32_t width, uint32_t height, uint32_t n_items,
+                         float* out);
+
 /* GatherDistGrad (src/core/f_ops.cpp:1248-1358), the exact backward of
  * RasterizeSoft's dist channel w.r.t. the hard clip positions (RasterizeSoft's
  * own backward is ColSum of the wide form, f_ops.cpp:1448-1455): for every

@@ -90,6 +90,11 @@ _SIGS = {
     "dressi_antialias_bwd_vtx": (_I, [_P, _P, _P, _U, _P, _P, _U, _P, _U, _P, _U, _P, _U, _I,
                                       _U, _U, _P]),
     "dressi_col_sum": (_I, [_P, _P, _U, _U, _U, _P]),
+    "dressi_antialias_batch": (_I, [_P, _P, _U, _P, _P, _U, _I, _P, _U, _U, _U, _U, _P]),
+    "dressi_antialias_bwd_img_batch": (_I, [_P, _P, _U, _P, _P, _U, _I, _P, _U, _U, _U, _U, _P]),
+    "dressi_antialias_bwd_vtx_batch": (_I, [_P, _P, _P, _U, _P, _P, _U, _I, _P, _U, _P, _U, _P, _U,
+                                            _I, _U, _U, _U, _P]),
+    "dressi_col_sum_batch": (_I, [_P, _P, _U, _U, _U, _U, _P]),
     "dressi_gather_dist_grad": (_I, [_P, _P, _P, _P, _U, _P, _U, _P, _U, _F, _I, _U, _U, _P]),
     "dressi_equirect_sample": (_I, [_P, _P, _U, _U, _U, _P, _U, _U, _P]),
     "dressi_equirect_sample_bwd": (_I, [_P, _P, _U, _P, _U, _U, _U, _U, _P]),

@@ -50,16 +50,34 @@ constexpr int kAaOffYh[8] = {-1, -1, -1, 0, 0, 1, 1, 1};
 // Per-op kernels (reference layouts: float face-id image, float faces)
 // ---------------------------------------------------------------------------
 
+// Batched per-op kernels: blockIdx.y is the item; images are [item][H][W]
+// (x n_comp), clips [item][V] when `clip_per_item`, else shared.
+struct AaItem {
+    uint32_t item;
+    size_t npx;
+    __device__ AaItem(uint32_t w, uint32_t h) : item(blockIdx.y), npx((size_t)w * h) {}
+    template <typename T>
+    __device__ T* img(T* p, uint32_t n_comp) const { return p + item * npx * n_comp; }
+    __device__ const float4* clip(const float4* p, uint32_t n_verts, int per_item) const {
+        return per_item ? p + (size_t)item * n_verts : p;
+    }
+};
+
 // AntiAlias forward (f_ops.cpp:2544-2576), one thread per pixel.
 __global__ __launch_bounds__(256) void k_antialias_op(const float* img, uint32_t n_comp,
                                                       const float* tri, const float4* clip,
-                                                      uint32_t n_verts, const float* faces,
-                                                      uint32_t n_faces, uint32_t w, uint32_t h,
-                                                      float* out) {
+                                                      uint32_t n_verts, int clip_per_item,
+                                                      const float* faces, uint32_t n_faces,
+                                                      uint32_t w, uint32_t h, float* out) {
     const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= w * h) {
         return;
     }
+    const AaItem it(w, h);
+    img = it.img(img, n_comp);
+    tri = it.img(tri, 1);
+    out = it.img(out, n_comp);
+    clip = it.clip(clip, n_verts, clip_per_item);
     const int x = (int)(p % w), y = (int)(p / w);
     const float W = (float)w, H = (float)h;
     const size_t so = (size_t)p * n_comp;
@@ -92,13 +110,19 @@ __global__ __launch_bounds__(256) void k_antialias_op(const float* img, uint32_t
 // AntiAliasBwdImg (f_ops.cpp:2231-2275), one thread per pixel.
 __global__ __launch_bounds__(256) void k_antialias_bwd_img_op(const float* gy, uint32_t n_comp,
                                                               const float* tri, const float4* clip,
-                                                              uint32_t n_verts, const float* faces,
+                                                              uint32_t n_verts, int clip_per_item,
+                                                              const float* faces,
                                                               uint32_t n_faces, uint32_t w,
                                                               uint32_t h, float* out) {
     const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= w * h) {
         return;
     }
+    const AaItem it(w, h);
+    gy = it.img(gy, n_comp);
+    tri = it.img(tri, 1);
+    out = it.img(out, n_comp);
+    clip = it.clip(clip, n_verts, clip_per_item);
     const int x = (int)(p % w), y = (int)(p / w);
     const float W = (float)w, H = (float)h;
     const size_t so = (size_t)p * n_comp;
@@ -168,9 +192,9 @@ __device__ __forceinline__ void aa_accumulate_v(const float* gy, const float* im
 // order.
 __global__ __launch_bounds__(256) void k_antialias_bwd_vtx_op(
         const float* gy, const float* img, uint32_t n_comp, const float* tri, const float4* clip,
-        uint32_t n_verts, const float* faces, uint32_t n_faces, const float* vtx_faces,
-        uint32_t max_deg, const float* seed, uint32_t n_samples, int wide, uint32_t w, uint32_t h,
-        float4* out) {
+        uint32_t n_verts, int clip_per_item, const float* faces, uint32_t n_faces,
+        const float* vtx_faces, uint32_t max_deg, const float* seed, uint32_t n_samples, int wide,
+        uint32_t w, uint32_t h, float4* out) {
     const uint32_t i = (blockIdx.x * blockDim.x + threadIdx.x) >> 3;
     const int k = (int)(threadIdx.x & 7u);
     const int gbase = (int)(threadIdx.x & 56u);  // the group's first lane in the wave
@@ -178,6 +202,13 @@ __global__ __launch_bounds__(256) void k_antialias_bwd_vtx_op(
     if (i >= n_verts * rows) {
         return;  // the whole group: its lanes share i
     }
+    const AaItem it(w, h);
+    gy = it.img(gy, n_comp);
+    img = it.img(img, n_comp);
+    tri = it.img(tri, 1);
+    clip = it.clip(clip, n_verts, clip_per_item);
+    seed += it.item;
+    out += (size_t)it.item * rows * n_verts;
     const uint32_t v = wide ? i % n_verts : i;
     const uint32_t d0 = wide ? i / n_verts : 0u;
     const uint32_t d1 = wide ? d0 + 1 : max_deg;
@@ -283,12 +314,18 @@ __global__ __launch_bounds__(256) void k_antialias_bwd_vtx_op(
 // outside those pixels.
 __global__ __launch_bounds__(128) void k_antialias_bwd_vtx_exact_op(
         const float* gy, const float* img, uint32_t n_comp, const float* tri, const float4* clip,
-        uint32_t n_verts, const float* faces, uint32_t n_faces, const float* vtx_faces,
-        uint32_t max_deg, uint32_t w, uint32_t h, float4* out) {
+        uint32_t n_verts, int clip_per_item, const float* faces, uint32_t n_faces,
+        const float* vtx_faces, uint32_t max_deg, uint32_t w, uint32_t h, float4* out) {
     const uint32_t v = blockIdx.x * blockDim.x + threadIdx.x;
     if (v >= n_verts) {
         return;
     }
+    const AaItem it(w, h);
+    gy = it.img(gy, n_comp);
+    img = it.img(img, n_comp);
+    tri = it.img(tri, 1);
+    clip = it.clip(clip, n_verts, clip_per_item);
+    out += (size_t)it.item * n_verts;
     const float W = (float)w, H = (float)h;
     int bx0 = (int)w, by0 = (int)h, bx1 = -1, by1 = -1;
     for (uint32_t d = 0; d < max_deg; d++) {
@@ -350,12 +387,15 @@ __global__ __launch_bounds__(128) void k_antialias_bwd_vtx_exact_op(
 }
 
 // ColSum (f_ops.cpp:1227-1244): rows summed in order per column and component.
+// blockIdx.y: the item of a batch ([item][H][W] -> [item][W]).
 __global__ __launch_bounds__(256) void k_col_sum_op(const float* x, uint32_t n_comp, uint32_t w,
                                                     uint32_t h, float* out) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= w * n_comp) {
         return;
     }
+    x += (size_t)blockIdx.y * h * w * n_comp;
+    out += (size_t)blockIdx.y * w * n_comp;
     float acc = 0.f;
     for (uint32_t r = 0; r < h; r++) {
         acc += x[(size_t)r * w * n_comp + i];
@@ -1122,16 +1162,49 @@ int aa_render_target(dressi_ctx* ctx, const float* tgt_clip_dev, uint32_t n_tver
 
 extern "C" {
 
-int dressi_antialias(dressi_ctx* ctx, const float* img, uint32_t n_comp, const float* tri,
-                     const float* clip, uint32_t n_verts, const float* faces, uint32_t n_faces,
-                     uint32_t width, uint32_t height, float* out) {
+int dressi_antialias_batch(dressi_ctx* ctx, const float* img, uint32_t n_comp, const float* tri,
+                           const float* clip, uint32_t n_verts, int clip_per_item,
+                           const float* faces, uint32_t n_faces, uint32_t width, uint32_t height,
+                           uint32_t n_items, float* out) {
     if (int rc = check_aa_args(ctx, n_comp, width, height)) return rc;
     DRESSI_REQUIRE(img && tri && clip && (faces || n_faces == 0) && out,
                    "dressi_antialias: NULL buffer");
+    DRESSI_REQUIRE(n_items <= kMaxBatchItems, "batch of %u items exceeds %u", n_items,
+                   kMaxBatchItems);
+    if (n_items == 0) {
+        return DRESSI_OK;
+    }
     const uint32_t npx = width * height;
-    hipLaunchKernelGGL(k_antialias_op, dim3(div_up(npx, 256)), dim3(256), 0, ctx->stream, img,
-                       n_comp, tri, (const float4*)clip, n_verts, faces, n_faces, width, height,
-                       out);
+    hipLaunchKernelGGL(k_antialias_op, dim3(div_up(npx, 256), n_items), dim3(256), 0,
+                       ctx->stream, img, n_comp, tri, (const float4*)clip, n_verts, clip_per_item,
+                       faces, n_faces, width, height, out);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+int dressi_antialias(dressi_ctx* ctx, const float* img, uint32_t n_comp, const float* tri,
+                     const float* clip, uint32_t n_verts, const float* faces, uint32_t n_faces,
+                     uint32_t width, uint32_t height, float* out) {
+    return dressi_antialias_batch(ctx, img, n_comp, tri, clip, n_verts, 0, faces, n_faces, width,
+                                  height, 1, out);
+}
+
+int dressi_antialias_bwd_img_batch(dressi_ctx* ctx, const float* gy, uint32_t n_comp,
+                                   const float* tri, const float* clip, uint32_t n_verts,
+                                   int clip_per_item, const float* faces, uint32_t n_faces,
+                                   uint32_t width, uint32_t height, uint32_t n_items, float* out) {
+    if (int rc = check_aa_args(ctx, n_comp, width, height)) return rc;
+    DRESSI_REQUIRE(gy && tri && clip && (faces || n_faces == 0) && out,
+                   "dressi_antialias_bwd_img: NULL buffer");
+    DRESSI_REQUIRE(n_items <= kMaxBatchItems, "batch of %u items exceeds %u", n_items,
+                   kMaxBatchItems);
+    if (n_items == 0) {
+        return DRESSI_OK;
+    }
+    const uint32_t npx = width * height;
+    hipLaunchKernelGGL(k_antialias_bwd_img_op, dim3(div_up(npx, 256), n_items), dim3(256), 0,
+                       ctx->stream, gy, n_comp, tri, (const float4*)clip, n_verts, clip_per_item,
+                       faces, n_faces, width, height, out);
     DRESSI_CHECK_LAUNCH();
     return DRESSI_OK;
 }
@@ -1139,13 +1212,39 @@ int dressi_antialias(dressi_ctx* ctx, const float* img, uint32_t n_comp, const f
 int dressi_antialias_bwd_img(dressi_ctx* ctx, const float* gy, uint32_t n_comp, const float* tri,
                              const float* clip, uint32_t n_verts, const float* faces,
                              uint32_t n_faces, uint32_t width, uint32_t height, float* out) {
+    return dressi_antialias_bwd_img_batch(ctx, gy, n_comp, tri, clip, n_verts, 0, faces, n_faces,
+                                          width, height, 1, out);
+}
+
+int dressi_antialias_bwd_vtx_batch(dressi_ctx* ctx, const float* gy, const float* img,
+                                   uint32_t n_comp, const float* tri, const float* clip,
+                                   uint32_t n_verts, int clip_per_item, const float* faces,
+                                   uint32_t n_faces, const float* vtx_faces, uint32_t max_deg,
+                                   const float* seeds, uint32_t n_samples, int wide,
+                                   uint32_t width, uint32_t height, uint32_t n_items, float* out) {
     if (int rc = check_aa_args(ctx, n_comp, width, height)) return rc;
-    DRESSI_REQUIRE(gy && tri && clip && (faces || n_faces == 0) && out,
-                   "dressi_antialias_bwd_img: NULL buffer");
-    const uint32_t npx = width * height;
-    hipLaunchKernelGGL(k_antialias_bwd_img_op, dim3(div_up(npx, 256)), dim3(256), 0, ctx->stream,
-                       gy, n_comp, tri, (const float4*)clip, n_verts, faces, n_faces, width,
-                       height, out);
+    DRESSI_REQUIRE(gy && img && tri && clip && (faces || n_faces == 0) && vtx_faces && out,
+                   "dressi_antialias_bwd_vtx: NULL buffer");
+    DRESSI_REQUIRE(!wide || n_samples > 0, "AntiAliasBwdVtx: wide requires stochastic samples");
+    DRESSI_REQUIRE(n_samples == 0 || seeds, "AntiAliasBwdVtx: NULL seed");
+    DRESSI_REQUIRE(n_items <= kMaxBatchItems, "batch of %u items exceeds %u", n_items,
+                   kMaxBatchItems);
+    if (n_verts == 0 || n_items == 0) {
+        return DRESSI_OK;
+    }
+    if (n_samples == 0) {
+        hipLaunchKernelGGL(k_antialias_bwd_vtx_exact_op, dim3(div_up(n_verts, 128), n_items),
+                           dim3(128), 0, ctx->stream, gy, img, n_comp, tri, (const float4*)clip,
+                           n_verts, clip_per_item, faces, n_faces, vtx_faces, max_deg, width,
+                           height, (float4*)out);
+    } else {
+        const uint32_t rows = wide ? max_deg : 1u;
+        DRESSI_REQUIRE((uint64_t)n_verts * rows * 8 < (1ull << 32), "AntiAliasBwdVtx: too many rows");
+        hipLaunchKernelGGL(k_antialias_bwd_vtx_op, dim3(div_up(n_verts * rows * 8, 256), n_items),
+                           dim3(256), 0, ctx->stream, gy, img, n_comp, tri, (const float4*)clip,
+                           n_verts, clip_per_item, faces, n_faces, vtx_faces, max_deg, seeds,
+                           n_samples, wide, width, height, (float4*)out);
+    }
     DRESSI_CHECK_LAUNCH();
     return DRESSI_OK;
 }
@@ -1155,42 +1254,30 @@ int dressi_antialias_bwd_vtx(dressi_ctx* ctx, const float* gy, const float* img,
                              const float* faces, uint32_t n_faces, const float* vtx_faces,
                              uint32_t max_deg, const float* seed, uint32_t n_samples, int wide,
                              uint32_t width, uint32_t height, float* out) {
-    if (int rc = check_aa_args(ctx, n_comp, width, height)) return rc;
-    DRESSI_REQUIRE(gy && img && tri && clip && (faces || n_faces == 0) && vtx_faces && out,
-                   "dressi_antialias_bwd_vtx: NULL buffer");
-    DRESSI_REQUIRE(!wide || n_samples > 0, "AntiAliasBwdVtx: wide requires stochastic samples");
-    DRESSI_REQUIRE(n_samples == 0 || seed, "AntiAliasBwdVtx: NULL seed");
-    if (n_verts == 0) {
+    return dressi_antialias_bwd_vtx_batch(ctx, gy, img, n_comp, tri, clip, n_verts, 0, faces,
+                                          n_faces, vtx_faces, max_deg, seed, n_samples, wide,
+                                          width, height, 1, out);
+}
+
+int dressi_col_sum_batch(dressi_ctx* ctx, const float* x, uint32_t n_comp, uint32_t width,
+                         uint32_t height, uint32_t n_items, float* out) {
+    DRESSI_REQUIRE(ctx && x && out, "dressi_col_sum: NULL buffer");
+    DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "ColSum: n_comp must be 1..4");
+    DRESSI_REQUIRE(n_items <= kMaxBatchItems, "batch of %u items exceeds %u", n_items,
+                   kMaxBatchItems);
+    DRESSI_TRY_HIP(hipSetDevice(ctx->device));
+    if (width == 0 || n_items == 0) {
         return DRESSI_OK;
     }
-    if (n_samples == 0) {
-        hipLaunchKernelGGL(k_antialias_bwd_vtx_exact_op, dim3(div_up(n_verts, 128)), dim3(128), 0,
-                           ctx->stream, gy, img, n_comp, tri, (const float4*)clip, n_verts, faces,
-                           n_faces, vtx_faces, max_deg, width, height, (float4*)out);
-    } else {
-        const uint32_t rows = wide ? max_deg : 1u;
-        DRESSI_REQUIRE((uint64_t)n_verts * rows * 8 < (1ull << 32), "AntiAliasBwdVtx: too many rows");
-        hipLaunchKernelGGL(k_antialias_bwd_vtx_op, dim3(div_up(n_verts * rows * 8, 256)), dim3(256),
-                           0, ctx->stream, gy, img, n_comp, tri, (const float4*)clip, n_verts,
-                           faces, n_faces, vtx_faces, max_deg, seed, n_samples, wide, width,
-                           height, (float4*)out);
-    }
+    hipLaunchKernelGGL(k_col_sum_op, dim3(div_up(width * n_comp, 256), n_items), dim3(256), 0,
+                       ctx->stream, x, n_comp, width, height, out);
     DRESSI_CHECK_LAUNCH();
     return DRESSI_OK;
 }
 
 int dressi_col_sum(dressi_ctx* ctx, const float* x, uint32_t n_comp, uint32_t width,
                    uint32_t height, float* out) {
-    DRESSI_REQUIRE(ctx && x && out, "dressi_col_sum: NULL buffer");
-    DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "ColSum: n_comp must be 1..4");
-    DRESSI_TRY_HIP(hipSetDevice(ctx->device));
-    if (width == 0) {
-        return DRESSI_OK;
-    }
-    hipLaunchKernelGGL(k_col_sum_op, dim3(div_up(width * n_comp, 256)), dim3(256), 0, ctx->stream,
-                       x, n_comp, width, height, out);
-    DRESSI_CHECK_LAUNCH();
-    return DRESSI_OK;
+    return dressi_col_sum_batch(ctx, x, n_comp, width, height, 1, out);
 }
 
 }  // extern "C"

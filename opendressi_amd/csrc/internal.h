@@ -31,6 +31,9 @@ struct dressi_ctx {
 
 namespace dressi {
 
+// Items of a batched per-op launch (grid y dimension).
+constexpr uint32_t kMaxBatchItems = 65535;
+
 // thread-local last error; every C entry point returns a dressi_status
 void set_error(const char* fmt, ...);
 void clear_error();

@@ -203,9 +203,76 @@ def col_sum(ctx: Context, x: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def _batch_clip(clip: torch.Tensor, n: int) -> tuple[int, int]:
+    """(n_verts, clip_per_item) of a (V, 4) shared or (N, V, 4) clip."""
+    if clip.dim() == 3:
+        if clip.shape[0] != n:
+            raise ValueError(f"clip: {clip.shape[0]} items for a batch of {n}")
+        return clip.shape[1], 1
+    return clip.shape[0], 0
+
+
+def antialias_batch(ctx: Context, img: torch.Tensor, tri: torch.Tensor, clip: torch.Tensor,
+                    faces: torch.Tensor) -> torch.Tensor:
+    """dressi_antialias_batch: img (N, H, W, C), tri (N, H, W), clip (V, 4)
+    shared or (N, V, 4) -> (N, H, W, C); each item as antialias()."""
+    _prep(ctx)
+    n, h, w, nc = img.shape
+    nv, per_item = _batch_clip(clip, n)
+    out = torch.empty_like(img)
+    check(lib.dressi_antialias_batch(ctx.handle, _ptr(img, "img"), nc, _ptr(tri, "tri"),
+                                     _ptr(clip, "clip"), nv, per_item, _ptr(faces, "faces"),
+                                     faces.shape[0], w, h, n, _ptr(out, "out")))
+    return out
+
+
+def antialias_bwd_img_batch(ctx: Context, gy: torch.Tensor, tri: torch.Tensor,
+                            clip: torch.Tensor, faces: torch.Tensor) -> torch.Tensor:
+    """dressi_antialias_bwd_img_batch: gy (N, H, W, C) -> like gy."""
+    _prep(ctx)
+    n, h, w, nc = gy.shape
+    nv, per_item = _batch_clip(clip, n)
+    out = torch.empty_like(gy)
+    check(lib.dressi_antialias_bwd_img_batch(ctx.handle, _ptr(gy, "gy"), nc, _ptr(tri, "tri"),
+                                             _ptr(clip, "clip"), nv, per_item,
+                                             _ptr(faces, "faces"), faces.shape[0], w, h, n,
+                                             _ptr(out, "out")))
+    return out
+
+
+def antialias_bwd_vtx_batch(ctx: Context, gy: torch.Tensor, img: torch.Tensor,
+                            tri: torch.Tensor, clip: torch.Tensor, faces: torch.Tensor,
+                            vtx_faces: torch.Tensor, seeds: torch.Tensor | None, n_samples: int,
+                            wide: bool = True) -> torch.Tensor:
+    """dressi_antialias_bwd_vtx_batch: gy, img (N, H, W, C), seeds (N,) ->
+    (N, deg, V, 4) partials when n_samples > 0 and wide, else (N, V, 4)."""
+    _prep(ctx)
+    n, h, w, nc = gy.shape
+    nv, per_item = _batch_clip(clip, n)
+    deg = vtx_faces.shape[0]
+    is_wide = bool(wide and n_samples > 0)
+    out = torch.empty((n, deg if is_wide else 1, vtx_faces.shape[1], 4), dtype=torch.float32,
+                      device=gy.device)
+    check(lib.dressi_antialias_bwd_vtx_batch(
+        ctx.handle, _ptr(gy, "gy"), _ptr(img, "img"), nc, _ptr(tri, "tri"), _ptr(clip, "clip"),
+        nv, per_item, _ptr(faces, "faces"), faces.shape[0], _ptr(vtx_faces, "vtx_faces"), deg,
+        _ptr(seeds, "seeds"), n_samples, 1 if is_wide else 0, w, h, n, _ptr(out, "out")))
+    return out if is_wide else out[:, 0]
+
+
+def col_sum_batch(ctx: Context, x: torch.Tensor) -> torch.Tensor:
+    """dressi_col_sum_batch: (N, H, W, C) -> (N, W, C)."""
+    _prep(ctx)
+    n, h, w, nc = x.shape
+    out = torch.empty((n, w, nc), dtype=torch.float32, device=x.device)
+    check(lib.dressi_col_sum_batch(ctx.handle, _ptr(x, "x"), nc, w, h, n, _ptr(out, "out")))
+    return out
+
+
 __all__ = ["soft_clip", "rasterize_soft", "rasterize", "rasterize_face_id", "lookup_faces",
            "lookup_faces_bwd", "face_fetch", "face_fetch_bwd", "antialias", "antialias_bwd_img",
-           "antialias_bwd_vtx", "col_sum"]
+           "antialias_bwd_vtx", "col_sum", "rasterize_batch", "antialias_batch",
+           "antialias_bwd_img_batch", "antialias_bwd_vtx_batch", "col_sum_batch"]
 
 
 def texture_bilinear(ctx: Context, tex: torch.Tensor, uv: torch.Tensor) -> torch.Tensor:

@@ -250,6 +250,11 @@ def texture(tex, uv, uv_da=None, mip_level_bias=None, mip=None, filter_mode="aut
 # ------------------------------- antialias ---------------------------------
 
 
+def _batch_clip(clip_vk: torch.Tensor) -> torch.Tensor:
+    """Per-item clips (N, V, 4), or the one (V, 4) every item shares."""
+    return clip_vk.contiguous() if clip_vk.shape[0] > 1 else clip_vk[0].contiguous()
+
+
 class _AntiAliasFn(torch.autograd.Function):
     @staticmethod
     def forward(fctx, color, rast, pos, vctx, md, rinfo, n_samples, boost):
@@ -258,16 +263,13 @@ class _AntiAliasFn(torch.autograd.Function):
         rast_d = to_dev(rast, dev, "rast")
         channels(col_d.shape[3], "color")
         clip_vk = clip_gl_to_vk(vertex_batch(to_dev(pos, dev, "pos")))
-        n = col_d.shape[0]
         with vctx.lock:
-            outs = []
-            for i in range(n):
-                tid = rast_d[i, ..., 3].contiguous()
-                clip = clip_vk[i if clip_vk.shape[0] > 1 else 0].contiguous()
-                outs.append(K.antialias(vctx._ctx, col_d[i].contiguous(), tid, clip, md.faces_f))
+            # the whole batch in one launch
+            out = K.antialias_batch(vctx._ctx, col_d.contiguous(), rast_d[..., 3].contiguous(),
+                                    _batch_clip(clip_vk), md.faces_f)
         fctx.dressi = (vctx, md, n_samples, boost)
         fctx.save_for_backward(color, rast, pos)
-        return torch.stack(outs, 0).to(color.device)
+        return out.to(color.device)
 
     @staticmethod
     def backward(fctx, grad_out):
@@ -282,33 +284,30 @@ class _AntiAliasFn(torch.autograd.Function):
         n, h, w, c = col_d.shape
         key = ("antialias", h, w, md.n_faces, md.n_verts, c, n, n_samples)
         eng = vctx.engine(key, lambda: _Engine(iter_seed=0))
-        g_col, g_clip = [], []
         with vctx.lock:
             # each backward pass advances the stochastic sampler's jitter;
             # items get distinct seeds so their sample patterns decorrelate
             eng.iter_seed += 1
-            for i in range(n):
-                tid = rast_d[i, ..., 3].contiguous()
-                clip = clip_vk[i if clip_vk.shape[0] > 1 else 0].contiguous()
-                gi = g[i].contiguous()
-                if need_color:
-                    g_col.append(K.antialias_bwd_img(vctx._ctx, gi, tid, clip, md.faces_f))
-                if need_pos:
-                    seed = _seed(dev, eng.iter_seed * n + i)
-                    if n_samples > 0:
-                        wide = K.antialias_bwd_vtx(vctx._ctx, gi, col_d[i].contiguous(), tid, clip,
-                                                   md.faces_f, md.vft, seed, n_samples, True)
-                        g_clip.append(K.col_sum(vctx._ctx, wide))
-                    else:
-                        g_clip.append(K.antialias_bwd_vtx(vctx._ctx, gi, col_d[i].contiguous(),
-                                                          tid, clip, md.faces_f, md.vft, seed, 0,
-                                                          False))
+            tid = rast_d[..., 3].contiguous()
+            clip = _batch_clip(clip_vk)
+            gc = g.contiguous()
+            if need_color:
+                g_col = K.antialias_bwd_img_batch(vctx._ctx, gc, tid, clip, md.faces_f)
+            if need_pos:
+                seeds = torch.tensor([float(eng.iter_seed * n + i) for i in range(n)],
+                                     dtype=torch.float32, device=dev)
+                if n_samples > 0:
+                    wide = K.antialias_bwd_vtx_batch(vctx._ctx, gc, col_d.contiguous(), tid, clip,
+                                                     md.faces_f, md.vft, seeds, n_samples, True)
+                    g_clip = K.col_sum_batch(vctx._ctx, wide)
+                else:
+                    g_clip = K.antialias_bwd_vtx_batch(vctx._ctx, gc, col_d.contiguous(), tid,
+                                                       clip, md.faces_f, md.vft, seeds, 0, False)
         out_gc = out_gp = None
         if need_color:
-            gc = torch.stack(g_col, 0)
-            out_gc = (gc[0] if color.dim() == 3 else gc).to(color.device)
+            out_gc = (g_col[0] if color.dim() == 3 else g_col).to(color.device)
         if need_pos:
-            gp = clip_grad_vk_to_gl(torch.stack(g_clip, 0)) * boost
+            gp = clip_grad_vk_to_gl(g_clip) * boost
             out_gp = (gp.sum(dim=0) if pos.dim() == 2 else gp).to(pos.device)
         return out_gc, None, out_gp, None, None, None, None, None
 

@@ -106,6 +106,55 @@ def test_aa_ops_match_oracle(ctx, oracle, seed, level, s):
         _exact(got, want, f"bwd vtx n={n}")
 
 
+def test_aa_batch_ops_match_oracle(ctx, oracle):
+    """The batched AntiAlias / AntiAliasBwdImg / AntiAliasBwdVtx / ColSum
+    entry points: three items (own cameras; per-item clips, and one clip
+    shared by all), 2-channel images at an odd screen size, each item equal
+    to the oracle's single-image op; the stochastic backward with a seed per
+    item, the exact one, and ColSum of the wide partials."""
+    import torch
+
+    from opendressi_amd import ops
+    s = 97
+    print(f"[aa batch ops] 3 items screen={s}", flush=True)
+    scenes = [_random_scene(oracle, seed, 3, s) for seed in (11, 12, 13)]
+    faces = scenes[0][1]
+    vf = oracle.vertex_faces_tex(faces, len(scenes[0][0]))
+    rng = np.random.default_rng(4)
+    for shared in (False, True):
+        clips = [scenes[0][0] if shared else sc[0] for sc in scenes]
+        ones = np.ones(len(clips[0]), np.float32)
+        masks = [oracle.rasterize(c, ones, faces, s, s)[..., 0] for c in clips]
+        tris = np.stack([oracle.rasterize_face_id(c, faces, s, s) for c in clips])
+        img = np.stack([np.stack([m, m * rng.uniform(0.2, 1.0)], -1) for m in masks]).astype(
+            np.float32)
+        gy = rng.standard_normal(img.shape).astype(np.float32)
+        seeds = np.array([3.0, 4.0, 9.0], np.float32)
+        d_clip = dev(clips[0]) if shared else dev(np.stack(clips))
+        d_img, d_tri, d_gy, d_faces = dev(img), dev(tris), dev(gy), dev(faces)
+        fwd = host(ops.antialias_batch(ctx, d_img, d_tri, d_clip, d_faces))
+        bimg = host(ops.antialias_bwd_img_batch(ctx, d_gy, d_tri, d_clip, d_faces))
+        wide = ops.antialias_bwd_vtx_batch(ctx, d_gy, d_img, d_tri, d_clip, d_faces, dev(vf),
+                                           dev(seeds), 8, wide=True)
+        summed = host(ops.col_sum_batch(ctx, wide))
+        wide = host(wide)
+        exact = host(ops.antialias_bwd_vtx_batch(ctx, d_gy, d_img, d_tri, d_clip, d_faces,
+                                                 dev(vf), None, 0))
+        for i in range(3):
+            what = f"item {i} shared={shared}"
+            _exact(fwd[i], oracle.antialias(img[i], tris[i], clips[i], faces), f"{what} fwd")
+            _exact(bimg[i], oracle.antialias_bwd_img(gy[i], tris[i], clips[i], faces),
+                   f"{what} bwd img")
+            want = oracle.antialias_bwd_vtx(gy[i], img[i], tris[i], clips[i], faces, vf,
+                                            float(seeds[i]), 8)
+            _exact(wide[i], want, f"{what} bwd vtx n=8")
+            _exact(summed[i], oracle.col_sum(want), f"{what} col sum")
+            _exact(exact[i], oracle.antialias_bwd_vtx(gy[i], img[i], tris[i], clips[i], faces,
+                                                      vf, 0.0, 0), f"{what} bwd vtx exact")
+        assert (tris > 0).sum() > 300
+    ctx.synchronize()
+
+
 def _fit(ctx, g, keep=True):
     import opendressi_amd as od
     screen = int(g["in_cfg"][0])
