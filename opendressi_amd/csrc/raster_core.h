@@ -964,8 +964,9 @@ __device__ __forceinline__ void walk_bin(const Rec* recs, const BinBuffers& b, u
 // bboxes of hundreds of tiles but touch a band of them). A thread walks the
 // tiles of its own face when its bbox holds at most kBinBig; the tile rows of
 // larger faces are dealt to all threads of the workgroup (a scan of their
-// row counts, a binary search per row), so a face spanning many tiles does
-// not hold one thread. Pairs
+// row counts, a binary search per row), so the lanes of a wave share the
+// work evenly whatever the faces' sizes (a face spanning many tiles would
+// otherwise hold its wave). Pairs
 // in the workgroup's LDS window of tiles are counted in LDS (one global
 // atomic per touched window tile), then written; the others (outside the
 // window, or a workgroup spanning two views) append with direct atomics. All
@@ -974,7 +975,7 @@ __device__ __forceinline__ void walk_bin(const Rec* recs, const BinBuffers& b, u
 // ---------------------------------------------------------------------------
 constexpr int kBinWin = 32;  // LDS window of 32 x 32 tiles
 constexpr int kBinThreads = 256;
-constexpr int kBinBig = 64;
+constexpr int kBinBig = 2;
 
 // Triangle of the tile test: screen corners, orientation sign of its area
 // and the edge-function margin (< 0: bbox only).
@@ -1113,14 +1114,14 @@ __device__ __forceinline__ bool heavy_listed(const HeavyList& h, uint32_t count,
     return count >= kHeavyBin && h.slot[bin] < h.cap;
 }
 
-// One (face, tile) pair of bin_append's pass (0: count window pairs in LDS
-// and append the others, 1: write window pairs from their bases).
-__device__ __forceinline__ void bin_pair(const BinBuffers& b, const RasterGeom& g, BinLds& lds,
-                                         int pass, bool mixed, int wx0, int wy0, uint32_t f,
-                                         uint32_t view, const BinTri& tri, int tx, int ty,
-                                         const HeavyList* heavy) {
+// One (face, tile) pair that the tile test passed, in bin_append's pass (0:
+// count window pairs in LDS and append the others, 1: write window pairs
+// from their bases).
+__device__ __forceinline__ void bin_put(const BinBuffers& b, const RasterGeom& g, BinLds& lds,
+                                        int pass, bool mixed, int wx0, int wy0, uint32_t f,
+                                        uint32_t view, int tx, int ty, const HeavyList* heavy) {
     const bool local = !mixed && tx - wx0 < kBinWin && ty - wy0 < kBinWin;
-    if ((pass == 1 && !local) || !tri_reaches_tile(tri, tx, ty)) {
+    if (pass == 1 && !local) {
         return;
     }
     const uint32_t bin = view * g.n_tiles + ty * g.tiles_x + tx;
@@ -1139,6 +1140,32 @@ __device__ __forceinline__ void bin_pair(const BinBuffers& b, const RasterGeom& 
     if (slot < b.cap) {
         b.list[(size_t)bin * b.cap + slot] = f;
     }
+}
+
+// The same for a pair the tile test has not seen yet.
+__device__ __forceinline__ void bin_pair(const BinBuffers& b, const RasterGeom& g, BinLds& lds,
+                                         int pass, bool mixed, int wx0, int wy0, uint32_t f,
+                                         uint32_t view, const BinTri& tri, int tx, int ty,
+                                         const HeavyList* heavy) {
+    if ((pass == 1 && (mixed || tx - wx0 >= kBinWin || ty - wy0 >= kBinWin)) ||
+        !tri_reaches_tile(tri, tx, ty)) {
+        return;
+    }
+    bin_put(b, g, lds, pass, mixed, wx0, wy0, f, view, tx, ty, heavy);
+}
+
+// Face slot q of the workgroup's dealt rows with off[q] <= p < off[q + 1].
+__device__ __forceinline__ int dealt_face(const BinLds& lds, uint32_t p, int nthr) {
+    int lo = 0, hi = nthr - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (lds.off[mid] <= p) {
+            lo = mid;
+        } else {
+            hi = mid - 1;
+        }
+    }
+    return lo;
 }
 
 __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom& g, bool valid,
@@ -1209,6 +1236,20 @@ __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom
     const uint32_t total = lds.off[nthr];
     const int wx0 = lds.win[0], wy0 = lds.win[1];
     const bool mixed = lds.win[3] != 0;
+    // the first kKeepRows dealt rows of each thread: pass 0 keeps the face
+    // slot, row, first column and a mask of the columns whose test passed
+    // (spans of at most 32 tiles), so pass 1 repeats neither the search nor
+    // the tests
+    constexpr int kKeepRows = 4;
+    int keep_lo[kKeepRows], keep_ty[kKeepRows], keep_ta[kKeepRows];
+    uint32_t keep_mask[kKeepRows];
+    bool keep_ok[kKeepRows];
+#pragma unroll
+    for (int it = 0; it < kKeepRows; it++) {
+        keep_lo[it] = keep_ty[it] = keep_ta[it] = 0;
+        keep_mask[it] = 0u;
+        keep_ok[it] = false;
+    }
     for (int pass = 0; pass < 2; pass++) {
         if (valid && !big) {
             // up to 2 x 2 tiles the test rarely rejects one: bbox only
@@ -1225,17 +1266,46 @@ __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom
                 }
             }
         }
-        for (uint32_t p = (uint32_t)tid; p < total; p += (uint32_t)nthr) {
-            // the face q with off[q] <= p < off[q + 1], and its tile row
-            int lo = 0, hi = nthr - 1;
-            while (lo < hi) {
-                const int mid = (lo + hi + 1) >> 1;
-                if (lds.off[mid] <= p) {
-                    lo = mid;
-                } else {
-                    hi = mid - 1;
-                }
+#pragma unroll
+        for (int it = 0; it < kKeepRows; it++) {
+            const uint32_t p = (uint32_t)tid + (uint32_t)(it * nthr);
+            if (p >= total) {
+                break;
             }
+            if (pass == 1 && keep_ok[it]) {
+                const int lo = keep_lo[it];
+                const uint32_t fq = lds.f[lo], vq = lds.view[lo];
+                for (uint32_t m = keep_mask[it]; m; m &= m - 1u) {
+                    bin_put(b, g, lds, 1, mixed, wx0, wy0, fq, vq,
+                            keep_ta[it] + (int)__builtin_ctz(m), keep_ty[it], heavy);
+                }
+                continue;
+            }
+            // the face q with off[q] <= p < off[q + 1], and its tile row
+            const int lo = dealt_face(lds, p, nthr);
+            const int ty = lds.ty0[lo] + (int)(p - lds.off[lo]);
+            const BinTri t = lds.tri[lo];
+            int ta, tb;
+            tri_row_span(t, ty, lds.tx0[lo], lds.tx1[lo], &ta, &tb);
+            uint32_t mask = 0u;
+            for (int tx = ta; tx <= tb; tx++) {
+                if (!tri_reaches_tile(t, tx, ty)) {
+                    continue;
+                }
+                mask |= tx - ta < 32 ? 1u << (tx - ta) : 0u;
+                bin_put(b, g, lds, pass, mixed, wx0, wy0, lds.f[lo], lds.view[lo], tx, ty,
+                        heavy);
+            }
+            if (pass == 0) {
+                keep_lo[it] = lo;
+                keep_ty[it] = ty;
+                keep_ta[it] = ta;
+                keep_mask[it] = mask;
+                keep_ok[it] = tb - ta < 32;
+            }
+        }
+        for (uint32_t p = (uint32_t)(tid + kKeepRows * nthr); p < total; p += (uint32_t)nthr) {
+            const int lo = dealt_face(lds, p, nthr);
             const int ty = lds.ty0[lo] + (int)(p - lds.off[lo]);
             const BinTri t = lds.tri[lo];
             int ta, tb;
