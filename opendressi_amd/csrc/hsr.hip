@@ -869,6 +869,7 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
         rc = rc ? rc : plan_alloc(p, &p->tgt_bytes, N * npx);
         rc = rc ? rc : plan_alloc(p, &p->nonbinary, 1);
         d.heavy.cap = heavy_seg_cap(d.g.n_tiles * d.g.n_views);
+        d.heavy.min_count = heavy_min_count(d.g.n_tiles * d.g.n_views);
         rc = rc ? rc : plan_alloc(p, &d.heavy.count, kHeavySegs);
         rc = rc ? rc : plan_alloc(p, &d.heavy.list, kHeavyCap);
         rc = rc ? rc : plan_alloc(p, &d.heavy.slot, (size_t)N * d.g.n_tiles);

@@ -1066,25 +1066,32 @@ __device__ __forceinline__ BinTri soft_bin_tri(const SoftRec& r) {
     return t;
 }
 
-// Heavy bins (at least kHeavyBin entries: the silhouette's limb, where the
-// soft triangles of edge-on faces pile up) take many times longer to
-// resolve than the rest, so the raster dispatches them first. The append
-// that takes a bin's count across kHeavyBin lists it: in segment
+// Heavy bins (at least HeavyList::min_count entries: the silhouette's limb,
+// where the soft triangles of edge-on faces pile up) take many times longer
+// to resolve than the rest, so the raster dispatches them first. The append
+// that takes a bin's count across min_count lists it: in segment
 // heavy_seg(bin) (a counter each, so no single counter takes every atomic;
 // a multiplicative hash spreads the limb's runs of neighbouring bins), at
 // the returned slot, which is also kept per bin. A bin past its segment's
 // capacity stays with the others. The consumer clears the segment counters
 // with the bin counters.
-constexpr uint32_t kHeavyBin = 192;
 constexpr uint32_t kHeavySegs = 64;
 constexpr uint32_t kHeavySegCap = 96;
 constexpr uint32_t kHeavyCap = kHeavySegs * kHeavySegCap;
 struct HeavyList {
     uint32_t* count;  // [kHeavySegs]
     uint32_t* list;   // [kHeavySegs][kHeavySegCap] bins
-    uint32_t* slot;   // [n_bins] slot of a bin whose count reached kHeavyBin
+    uint32_t* slot;   // [n_bins] slot of a bin whose count reached min_count
     uint32_t cap;     // slots per segment the consumer takes (<= kHeavySegCap)
+    uint32_t min_count;
 };
+
+// The entry count that makes a bin heavy, for a problem of n_bins bins. A
+// short raster (few bins) ends on the tail of its longest blocks, so more of
+// them go first; in a long one the first-dispatched bins lose the tile
+// order's cache locality, so only the longest do (measured: 512 x 512 x 4
+// views, 4 096 bins: 48 entries; 2048 x 2048 x 4 views, 65 536 bins: 96).
+inline uint32_t heavy_min_count(uint32_t n_bins) { return n_bins <= 16384u ? 48u : 96u; }
 
 // Slots per segment for a problem of n_bins bins: at most a quarter of the
 // bins go first (the rest of a segment stays with the others).
@@ -1099,7 +1106,7 @@ __device__ __forceinline__ uint32_t heavy_seg(uint32_t bin) {
 
 __device__ __forceinline__ void heavy_note(const HeavyList* h, uint32_t bin, uint32_t old,
                                            uint32_t add) {
-    if (h && old < kHeavyBin && old + add >= kHeavyBin) {
+    if (h && old < h->min_count && old + add >= h->min_count) {
         const uint32_t seg = heavy_seg(bin);
         const uint32_t s = atomicAdd(&h->count[seg], 1u);
         h->slot[bin] = s;
@@ -1111,7 +1118,7 @@ __device__ __forceinline__ void heavy_note(const HeavyList* h, uint32_t bin, uin
 
 // The bin is listed (resolved by the heavy part of the raster's grid).
 __device__ __forceinline__ bool heavy_listed(const HeavyList& h, uint32_t count, uint32_t bin) {
-    return count >= kHeavyBin && h.slot[bin] < h.cap;
+    return count >= h.min_count && h.slot[bin] < h.cap;
 }
 
 // One (face, tile) pair that the tile test passed, in bin_append's pass (0:
