@@ -327,8 +327,8 @@ __device__ __forceinline__ void frag_phase_a(const SoftRec& r, uint32_t f, int p
 // Phase B fragment (lanes whose best depth is >= 0.5): every fragment phase
 // A did not fold. `in_a`: the face passed phase A's cull for this block (its
 // class 0 / 2 fragments were folded there). `near`: the face's hard triangle
-// is within r + 1 px of the wave's block; otherwise every covered pixel of
-// the block is more than r + 1 px from it and its depth is exactly 1.0.
+// is within r + a_margin px of the pixels phase B folds; otherwise every
+// covered one of them is farther and its depth is exactly 1.0.
 __device__ __forceinline__ void frag_phase_b(const SoftRec& r, uint32_t f, int px, int py,
                                              float radius, const float* prev, uint32_t width,
                                              bool near, bool in_a, PixelBest& b) {
@@ -437,17 +437,19 @@ __device__ __forceinline__ bool edges_reach_block(const float* w, int bx, int by
 }
 
 // Separating-axis test of the soft triangle (corners x[k], y[k], orientation
-// sign of s_inv_area) against the 8x8 block along its three edge normals,
-// with the record's soft margin m: false only when no pixel centre of the
-// block can be covered (per lane, one face per lane).
-__device__ __forceinline__ bool soft_reaches_block(const float (&x)[3], const float (&y)[3],
-                                                   float s_inv_area, float m, int bx, int by) {
+// sign of s_inv_area) against the pixel centres of a rectangle of pixels
+// [px0, px1] x [py0, py1] along its three edge normals, with the record's
+// soft margin m: false only when no pixel centre of the rectangle can be
+// covered (per lane, one face per lane).
+__device__ __forceinline__ bool soft_reaches_rect(const float (&x)[3], const float (&y)[3],
+                                                  float s_inv_area, float m, int px0, int py0,
+                                                  int px1, int py1) {
     if (!(m >= 0.f)) {
         return true;
     }
     const float s = s_inv_area > 0.f ? 1.f : -1.f;
-    const float x0 = (float)bx + 0.5f, x1 = (float)bx + 7.5f;
-    const float y0 = (float)by + 0.5f, y1 = (float)by + 7.5f;
+    const float x0 = (float)px0 + 0.5f, x1 = (float)px1 + 0.5f;
+    const float y0 = (float)py0 + 0.5f, y1 = (float)py1 + 0.5f;
     bool hit = true;
 #pragma unroll
     for (int k = 0; k < 3; k++) {
@@ -465,6 +467,27 @@ __device__ __forceinline__ bool soft_reaches_block(const float (&x)[3], const fl
 // Inclusive box [x0, x1] x [y0, y1] meets the 8x8 block at (bx, by).
 __device__ __forceinline__ bool box_hits(int x0, int y0, int x1, int y1, int bx, int by) {
     return x0 <= bx + 7 && x1 >= bx && y0 <= by + 7 && y1 >= by;
+}
+
+// Pixel rectangle [x0, x1] x [y0, y1] of a block: the lanes of a wave mask
+// (lane = 8 * row + column) span it; the whole block for a full mask.
+struct PixRect {
+    int x0, y0, x1, y1;
+};
+__device__ __forceinline__ PixRect lanes_rect(uint64_t m, int bx, int by) {
+    uint32_t cols = 0u, rows = 0u;
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        const uint32_t row = (uint32_t)(m >> (8 * r)) & 0xffu;
+        cols |= row;
+        rows |= row ? 1u << r : 0u;
+    }
+    PixRect q;
+    q.x0 = bx + (int)__builtin_ctz(cols | 0x100u);
+    q.x1 = bx + 31 - (int)__builtin_clz(cols | 1u);
+    q.y0 = by + (int)__builtin_ctz(rows | 0x100u);
+    q.y1 = by + 31 - (int)__builtin_clz(rows | 1u);
+    return q;
 }
 
 // What the block culls read of one face, loaded together (one round trip):
@@ -535,10 +558,11 @@ __device__ __forceinline__ bool cull_in_a(const CullLoad& l, int bx, int by, boo
 // one are deferred by phase A.
 __device__ __forceinline__ bool cull_pos(const CullLoad& l) { return l.w[12] > 0.f; }
 
-// The soft triangle of a loaded face can cover a pixel centre of the block.
-__device__ __forceinline__ bool cull_soft(const CullLoad& l, int bx, int by) {
-    return box_hits(l.c.sx0, l.c.sy0, l.c.sx1, l.c.sy1, bx, by) &&
-           soft_reaches_block(l.sx, l.sy, l.w[14], l.s_margin, bx, by);
+// The soft triangle of a loaded face can cover a pixel centre of the
+// rectangle.
+__device__ __forceinline__ bool cull_soft(const CullLoad& l, const PixRect& q) {
+    return l.c.sx0 <= q.x1 && l.c.sx1 >= q.x0 && l.c.sy0 <= q.y1 && l.c.sy1 >= q.y0 &&
+           soft_reaches_rect(l.sx, l.sy, l.w[14], l.s_margin, q.x0, q.y0, q.x1, q.y1);
 }
 
 // Number of list entries of a bin and whether it overflowed (then every face
@@ -722,8 +746,13 @@ __device__ __forceinline__ void phase_b(const SoftRec* recs, const CullRec* cull
     const int px = bx + (lane & 7);
     const int py = by + (lane >> 3);
     const float near_d = radius;  // + the face's a_margin
-    const float cx0 = (float)bx + 0.5f, cx1 = (float)bx + 7.5f;
-    const float cy0 = (float)by + 0.5f, cy1 = (float)by + 7.5f;
+    // Only the lanes with `need` fold here, so the culls and the near / far
+    // split below take the rectangle those lanes span (at the limb often a
+    // few pixels of the block): a face that cannot cover it, or whose hard
+    // triangle lies more than r + a_margin from it, changes no such lane.
+    const PixRect nr = lanes_rect(__ballot(need), bx, by);
+    const float cx0 = (float)nr.x0 + 0.5f, cx1 = (float)nr.x1 + 0.5f;
+    const float cy0 = (float)nr.y0 + 0.5f, cy1 = (float)nr.y1 + 0.5f;
     // Near faces (the hard triangle within r + a_margin of the block, or
     // folded in phase A) are folded as they come. Far faces give depth
     // exactly 1.0 at every pixel they cover, so among them the highest face
@@ -738,7 +767,7 @@ __device__ __forceinline__ void phase_b(const SoftRec* recs, const CullRec* cull
         if (e < bv.n) {
             f = bv.implicit ? e : (base == 0 ? bv.pre : bv.list[e]);
             const CullLoad l = load_cull<true>(recs, cull, f);
-            keep = cull_soft(l, bx, by);
+            keep = cull_soft(l, nr);
             in_a = keep && cull_in_a(l, bx, by, false);
             near = in_a || hard_bbox_near(l.hx, l.hy, l.w[15], cx0, cx1, cy0, cy1, near_d);
         }
