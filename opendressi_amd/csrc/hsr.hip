@@ -288,52 +288,36 @@ __global__ __launch_bounds__(256) void k_hsr_loss(HsrDev d) {
 
 // FaceFetchBwd (stochastic, n samples, seed = t) fused with the pixel
 // chain's backward at each accepted sample: per (view, face) the three
-// corner-clip gradients (src/core/f_ops.cpp:1646-1729, 1700-1727). A group of
-// kSampleLanes lanes takes one (view, face): lane j evaluates samples j,
-// j + kSampleLanes, ..., then the group's first lane adds the lanes'
-// gradients in sample order (lanes without an accepted sample add +0, which
-// leaves the sum unchanged: it starts at +0 and never becomes -0). Samples on
-// pixels whose winner is a hard-branch fragment contribute exactly zero
-// (pred = max(1, soft) passes no gradient to soft) and are skipped; a face
-// that won no rim pixel (rimf = 0) has no other sample, so it reads none.
+// corner-clip gradients (src/core/f_ops.cpp:1646-1729, 1700-1727). Samples
+// on pixels whose winner is a hard-branch fragment contribute exactly zero
+// (pred = max(1, soft) passes no gradient to soft) and are skipped, so a
+// face that won no rim pixel (rimf = 0; most faces) has no sample that
+// counts: one lane per (view, face) writes its zero gradient, and the
+// workgroup queues its rim faces in LDS. A group of kSampleLanes lanes then
+// takes each queued face: lane j evaluates samples j, j + kSampleLanes, ...,
+// and the group's first lane adds the lanes' gradients in sample order
+// (lanes without an accepted sample add +0, which leaves the sum unchanged:
+// it starts at +0 and never becomes -0).
 constexpr int kSampleLanes = 8;
+// (view, face) items above which the face backward queues its rim faces
+// (measured: 2048 x 2048 x 4 views, 327 680 items: 36 -> 26 us; 512 x 512 x 4
+// views, 20 480 items: 11 -> 20 us, so the form with a group per item stays)
+constexpr uint32_t kFaceBwdQueueMin = 131072;
 
-__global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
-    const uint32_t gi = blockIdx.x * blockDim.x + threadIdx.x;
-    publish_t_next(d, gi);
-    // the raster is done with this iteration's bins: clear their counters
-    for (uint32_t b = gi; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
-        const uint32_t c = d.bins.counts[b];
-        if (c > d.bins.cap && d.bin_over) {
-            *d.bin_over = c;  // rare: the host grows the bins before the next step
-        }
-        d.bins.counts[b] = 0;
-    }
-    if (d.heavy.count && gi < kHeavySegs) {
-        d.heavy.count[gi] = 0;
-    }
-    const uint32_t item = gi / kSampleLanes;
-    const bool valid = item < d.g.n_views * d.g.n_faces;
-    const int j = (int)(threadIdx.x % kSampleLanes);
-    const int gbase = (int)(threadIdx.x & 63u) - j;  // first lane of the group
-    const uint32_t view = valid ? item / d.g.n_faces : 0u;
-    const uint32_t f = valid ? item - view * d.g.n_faces : 0u;
+// One queued rim face (item = view * F + face) on the kSampleLanes lanes of
+// a group (lane j of the group; gbase: the group's first lane in the wave).
+__device__ __forceinline__ void face_bwd_item(const HsrDev& d, uint32_t item, int j, int gbase) {
+    const uint32_t view = item / d.g.n_faces;
+    const uint32_t f = item - view * d.g.n_faces;
     const float W = (float)d.g.width, H = (float)d.g.height;
-    const bool rim = valid && d.rimf[item] != 0;
     float4 c[3];
-#pragma unroll
-    for (int k = 0; k < 3; k++) {
-        c[k] = make_float4(0.f, 0.f, 0.f, 1.f);
-    }
-    if (rim) {
-        face_clips(d, view, f, c);
-    }
+    face_clips(d, view, f, c);
     float4 acc[3];
 #pragma unroll
     for (int k = 0; k < 3; k++) {
         acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    const bool ok = rim && c[0].w > 1e-6f && c[1].w > 1e-6f && c[2].w > 1e-6f;
+    const bool ok = c[0].w > 1e-6f && c[1].w > 1e-6f && c[2].w > 1e-6f;
     float s[3][2];
 #pragma unroll
     for (int k = 0; k < 3; k++) {
@@ -401,14 +385,98 @@ __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
             }
         }
     }
-    if (valid && j == 0) {
-        if (rim) {
-            d.rimf[item] = 0;
-        }
+    if (j == 0) {
+        d.rimf[item] = 0;
         float4* dst = d.gtri + (size_t)view * 3 * d.g.n_faces;
 #pragma unroll
         for (int k = 0; k < 3; k++) {
             dst[(size_t)k * d.g.n_faces + f] = acc[k];
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
+    __shared__ uint32_t queue[256];
+    __shared__ uint32_t wave_n[4];
+    const uint32_t gi = blockIdx.x * blockDim.x + threadIdx.x;
+    publish_t_next(d, gi);
+    // the raster is done with this iteration's bins: clear their counters
+    for (uint32_t b = gi; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
+        const uint32_t c = d.bins.counts[b];
+        if (c > d.bins.cap && d.bin_over) {
+            *d.bin_over = c;  // rare: the host grows the bins before the next step
+        }
+        d.bins.counts[b] = 0;
+    }
+    if (d.heavy.count && gi < kHeavySegs) {
+        d.heavy.count[gi] = 0;
+    }
+    const uint32_t F = d.g.n_faces;
+    const bool valid = gi < d.g.n_views * F;
+    const bool rim = valid && d.rimf[gi] != 0;
+    if (valid && !rim) {
+        const uint32_t view = gi / F, f = gi - view * F;
+        float4* dst = d.gtri + (size_t)view * 3 * F;
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            dst[(size_t)k * F + f] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    // the workgroup's rim faces, in item order
+    const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
+    const uint64_t m = __ballot(rim);
+    if (lane == 0) {
+        wave_n[wv] = (uint32_t)__popcll(m);
+    }
+    __syncthreads();
+    uint32_t before = 0, n = 0;
+    for (uint32_t w = 0; w < blockDim.x / 64; w++) {
+        before += w < wv ? wave_n[w] : 0u;
+        n += wave_n[w];
+    }
+    if (rim) {
+        queue[before + lanes_below(m)] = gi;
+    }
+    __syncthreads();
+    const int j = (int)(threadIdx.x % kSampleLanes);
+    const int gbase = (int)lane - j;
+    for (uint32_t qi = threadIdx.x / kSampleLanes; qi < n; qi += blockDim.x / kSampleLanes) {
+        face_bwd_item(d, queue[qi], j, gbase);
+    }
+}
+
+// The same with a group of kSampleLanes lanes for every (view, face), rim
+// or not (each group reads its face's flag): the form for small problems,
+// whose few workgroups would otherwise take their queued faces in turn.
+__global__ __launch_bounds__(256) void k_hsr_face_bwd_all(HsrDev d) {
+    const uint32_t gi = blockIdx.x * blockDim.x + threadIdx.x;
+    publish_t_next(d, gi);
+    // the raster is done with this iteration's bins: clear their counters
+    for (uint32_t b = gi; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
+        const uint32_t c = d.bins.counts[b];
+        if (c > d.bins.cap && d.bin_over) {
+            *d.bin_over = c;  // rare: the host grows the bins before the next step
+        }
+        d.bins.counts[b] = 0;
+    }
+    if (d.heavy.count && gi < kHeavySegs) {
+        d.heavy.count[gi] = 0;
+    }
+    const uint32_t item = gi / kSampleLanes;
+    const uint32_t F = d.g.n_faces;
+    if (item >= d.g.n_views * F) {
+        return;  // the whole group
+    }
+    const int j = (int)(threadIdx.x % kSampleLanes);
+    const int gbase = (int)(threadIdx.x & 63u) - j;
+    if (d.rimf[item] != 0) {
+        face_bwd_item(d, item, j, gbase);
+    } else if (j == 0) {
+        const uint32_t view = item / F, f = item - view * F;
+        float4* dst = d.gtri + (size_t)view * 3 * F;
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            dst[(size_t)k * F + f] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
 }
@@ -707,8 +775,12 @@ int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
             break;
         }
         case 3:
-            hipLaunchKernelGGL(k_hsr_face_bwd, dim3(div_up(nvf, 256 / kSampleLanes)), dim3(256),
-                               0, s, d);
+            if (nvf > kFaceBwdQueueMin) {
+                hipLaunchKernelGGL(k_hsr_face_bwd, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
+            } else {
+                hipLaunchKernelGGL(k_hsr_face_bwd_all, dim3(div_up(nvf, 256 / kSampleLanes)),
+                                   dim3(256), 0, s, d);
+            }
             break;
         default:
             switch (g.n_views) {
