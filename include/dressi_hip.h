@@ -174,6 +174,39 @@ int dressi_face_fetch_bwd(dressi_ctx* ctx, const float* gy, uint32_t n_comp,
                           const float* seed, float radius_px,
                           uint32_t n_samples, float* out);
 
+/* Batched forms of the four entry points above (an extension with no
+ * counterpart in the reference: the torch surface's interpolate runs a whole
+ * batch per launch). n_items items back to back: attr [item][n_attr] (or
+ * [item][n_faces] for FaceFetch) when attr_per_item, else shared; idx and gy
+ * images [item][H][W] (x n_comp); prj* [item][F] VEC4 when prj_per_item;
+ * seeds [item] (device); gy of LookupFacesBwd [item][F]; outputs [item][...]
+ * of the single-item shape. Each item's result equals the single-item
+ * call's. n_items <= 65535. */
+int dressi_lookup_faces_batch(dressi_ctx* ctx, const float* attr,
+                              uint32_t n_comp, uint32_t n_attr,
+                              int attr_per_item, const float* faces,
+                              uint32_t n_faces, uint32_t corner,
+                              uint32_t n_items, float* out);
+int dressi_lookup_faces_bwd_batch(dressi_ctx* ctx, const float* gy,
+                                  uint32_t n_comp, const float* faces,
+                                  uint32_t n_faces, const float* vtx_faces,
+                                  uint32_t n_verts, uint32_t max_deg,
+                                  uint32_t corner, uint32_t n_items,
+                                  float* out);
+int dressi_face_fetch_batch(dressi_ctx* ctx, const float* attr,
+                            uint32_t n_comp, uint32_t n_faces,
+                            int attr_per_item, const float* idx,
+                            uint32_t width, uint32_t height, uint32_t n_items,
+                            float* out);
+int dressi_face_fetch_bwd_batch(dressi_ctx* ctx, const float* gy,
+                                uint32_t n_comp, const float* idx,
+                                uint32_t width, uint32_t height,
+                                const float* prj0, const float* prj1,
+                                const float* prj2, int prj_per_item,
+                                uint32_t n_faces, const float* seeds,
+                                float radius_px, uint32_t n_samples,
+                                uint32_t n_items, float* out);
+
 /* F::AntiAlias (src/core/f_ops.cpp:2480-2579; pair rule EvalAaPair,
  * src/core/cpu_raster.cpp:371-454): 8-neighbour screen-space antialiasing of
  * img {S,S} x n_comp (n_comp 1..4) given the face-id image tri {S,S} (float

@@ -85,6 +85,11 @@ _SIGS = {
     "dressi_lookup_faces_bwd": (_I, [_P, _P, _U, _P, _U, _P, _U, _U, _U, _P]),
     "dressi_face_fetch": (_I, [_P, _P, _U, _U, _P, _U, _U, _P]),
     "dressi_face_fetch_bwd": (_I, [_P, _P, _U, _P, _U, _U, _P, _P, _P, _U, _P, _F, _U, _P]),
+    "dressi_lookup_faces_batch": (_I, [_P, _P, _U, _U, _I, _P, _U, _U, _U, _P]),
+    "dressi_lookup_faces_bwd_batch": (_I, [_P, _P, _U, _P, _U, _P, _U, _U, _U, _U, _P]),
+    "dressi_face_fetch_batch": (_I, [_P, _P, _U, _U, _I, _P, _U, _U, _U, _P]),
+    "dressi_face_fetch_bwd_batch": (_I, [_P, _P, _U, _P, _U, _U, _P, _P, _P, _I, _U, _P, _F, _U,
+                                         _U, _P]),
     "dressi_antialias": (_I, [_P, _P, _U, _P, _P, _U, _P, _U, _U, _U, _P]),
     "dressi_antialias_bwd_img": (_I, [_P, _P, _U, _P, _P, _U, _P, _U, _U, _U, _P]),
     "dressi_antialias_bwd_vtx": (_I, [_P, _P, _P, _U, _P, _P, _U, _P, _U, _P, _U, _P, _U, _I,

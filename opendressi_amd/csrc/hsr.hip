@@ -541,13 +541,18 @@ __global__ __launch_bounds__(256) void k_hsr_vertex_adam(HsrDev d) {
 
 // Per-op kernels ------------------------------------------------------------
 
+// The per-op kernels below take a batch on the grid's y dimension: item
+// blockIdx.y reads and writes at the given per-item strides (in elements; a
+// stride of 0 shares the buffer among the items).
 __global__ void k_lookup_faces(const float* attr, uint32_t n_comp, const float* faces,
                                uint32_t n_faces, uint32_t n_attr, uint32_t corner, uint32_t* err,
-                               float* out) {
+                               float* out, size_t attr_stride) {
     const uint32_t f = blockIdx.x * blockDim.x + threadIdx.x;
     if (f >= n_faces) {
         return;
     }
+    attr += blockIdx.y * attr_stride;
+    out += (size_t)blockIdx.y * n_faces * n_comp;
     const uint32_t vi = fid_u(faces[(size_t)f * 3 + corner]);
     if (vi >= n_attr) {
         atomicOr(err, 32u);
@@ -566,6 +571,8 @@ __global__ void k_lookup_faces_bwd(const float* gy, uint32_t n_comp, const float
     if (v >= n_verts) {
         return;
     }
+    gy += (size_t)blockIdx.y * n_faces * n_comp;
+    out += (size_t)blockIdx.y * n_verts * n_comp;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     for (uint32_t dd = 0; dd < max_deg; dd++) {
         const float fv = vtx_faces[(size_t)dd * n_verts + v];
@@ -590,11 +597,14 @@ __global__ void k_lookup_faces_bwd(const float* gy, uint32_t n_comp, const float
 }
 
 __global__ void k_face_fetch(const float* attr, uint32_t n_comp, uint32_t n_faces,
-                             const float* idx, size_t npx, float* out) {
+                             const float* idx, size_t npx, float* out, size_t attr_stride) {
     const size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= npx) {
         return;
     }
+    attr += blockIdx.y * attr_stride;
+    idx += blockIdx.y * npx;
+    out += blockIdx.y * npx * n_comp;
     const int f = (int)(idx[p] + 0.5f) - 1;
     const bool ok = f >= 0 && (uint32_t)f < n_faces;
     for (uint32_t c = 0; c < n_comp; c++) {
@@ -605,11 +615,19 @@ __global__ void k_face_fetch(const float* attr, uint32_t n_comp, uint32_t n_face
 __global__ void k_face_fetch_bwd(const float* gy, uint32_t n_comp, const float* idx, uint32_t w,
                                  uint32_t h, const float4* prj0, const float4* prj1,
                                  const float4* prj2, uint32_t n_faces, const float* seed,
-                                 float radius, uint32_t n_samples, float* out) {
+                                 float radius, uint32_t n_samples, float* out, size_t prj_stride) {
     const uint32_t f = blockIdx.x * blockDim.x + threadIdx.x;
     if (f >= n_faces) {
         return;
     }
+    const size_t npx = (size_t)w * h;
+    gy += blockIdx.y * npx * n_comp;
+    idx += blockIdx.y * npx;
+    prj0 += blockIdx.y * prj_stride;
+    prj1 += blockIdx.y * prj_stride;
+    prj2 += blockIdx.y * prj_stride;
+    seed += blockIdx.y;
+    out += (size_t)blockIdx.y * n_faces * n_comp;
     const float4 c[3] = {prj0[f], prj1[f], prj2[f]};
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     bool ok = c[0].w > 1e-6f && c[1].w > 1e-6f && c[2].w > 1e-6f;
@@ -1404,15 +1422,43 @@ int dressi_hsr_profile(dressi_hsr_plan* p, uint32_t iters, char* names, size_t n
 
 // Per-op entry points --------------------------------------------------------
 
-int dressi_lookup_faces(dressi_ctx* ctx, const float* attr, uint32_t n_comp, uint32_t n_attr,
-                        const float* faces, uint32_t n_faces, uint32_t corner, float* out) {
+int dressi_lookup_faces_batch(dressi_ctx* ctx, const float* attr, uint32_t n_comp,
+                              uint32_t n_attr, int attr_per_item, const float* faces,
+                              uint32_t n_faces, uint32_t corner, uint32_t n_items, float* out) {
     DRESSI_REQUIRE(ctx && attr && faces && out, "bad arguments");
     DRESSI_REQUIRE(corner < 3, "LookupFaces: corner must be 0, 1 or 2");
     DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "n_comp must be 1..4");
-    if (!n_faces) return DRESSI_OK;
+    DRESSI_REQUIRE(n_items <= kMaxBatchItems, "batch of %u items exceeds %u", n_items,
+                   kMaxBatchItems);
+    if (!n_faces || !n_items) return DRESSI_OK;
     DRESSI_TRY_HIP(hipSetDevice(ctx->device));
-    hipLaunchKernelGGL(k_lookup_faces, dim3(div_up(n_faces, 256)), dim3(256), 0, ctx->stream,
-                       attr, n_comp, faces, n_faces, n_attr, corner, ctx->d_err, out);
+    hipLaunchKernelGGL(k_lookup_faces, dim3(div_up(n_faces, 256), n_items), dim3(256), 0,
+                       ctx->stream, attr, n_comp, faces, n_faces, n_attr, corner, ctx->d_err, out,
+                       attr_per_item ? (size_t)n_attr * n_comp : (size_t)0);
+    DRESSI_CHECK_LAUNCH();
+    return DRESSI_OK;
+}
+
+int dressi_lookup_faces(dressi_ctx* ctx, const float* attr, uint32_t n_comp, uint32_t n_attr,
+                        const float* faces, uint32_t n_faces, uint32_t corner, float* out) {
+    return dressi_lookup_faces_batch(ctx, attr, n_comp, n_attr, 0, faces, n_faces, corner, 1,
+                                     out);
+}
+
+int dressi_lookup_faces_bwd_batch(dressi_ctx* ctx, const float* gy, uint32_t n_comp,
+                                  const float* faces, uint32_t n_faces, const float* vtx_faces,
+                                  uint32_t n_verts, uint32_t max_deg, uint32_t corner,
+                                  uint32_t n_items, float* out) {
+    DRESSI_REQUIRE(ctx && gy && faces && vtx_faces && out, "bad arguments");
+    DRESSI_REQUIRE(corner < 3, "LookupFacesBwd: corner must be 0, 1 or 2");
+    DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "n_comp must be 1..4");
+    DRESSI_REQUIRE(n_items <= kMaxBatchItems, "batch of %u items exceeds %u", n_items,
+                   kMaxBatchItems);
+    if (!n_verts || !n_items) return DRESSI_OK;
+    DRESSI_TRY_HIP(hipSetDevice(ctx->device));
+    hipLaunchKernelGGL(k_lookup_faces_bwd, dim3(div_up(n_verts, 256), n_items), dim3(256), 0,
+                       ctx->stream, gy, n_comp, faces, n_faces, vtx_faces, n_verts, max_deg,
+                       corner, ctx->d_err, out);
     DRESSI_CHECK_LAUNCH();
     return DRESSI_OK;
 }
@@ -1420,27 +1466,50 @@ int dressi_lookup_faces(dressi_ctx* ctx, const float* attr, uint32_t n_comp, uin
 int dressi_lookup_faces_bwd(dressi_ctx* ctx, const float* gy, uint32_t n_comp,
                             const float* faces, uint32_t n_faces, const float* vtx_faces,
                             uint32_t n_verts, uint32_t max_deg, uint32_t corner, float* out) {
-    DRESSI_REQUIRE(ctx && gy && faces && vtx_faces && out, "bad arguments");
-    DRESSI_REQUIRE(corner < 3, "LookupFacesBwd: corner must be 0, 1 or 2");
+    return dressi_lookup_faces_bwd_batch(ctx, gy, n_comp, faces, n_faces, vtx_faces, n_verts,
+                                         max_deg, corner, 1, out);
+}
+
+int dressi_face_fetch_batch(dressi_ctx* ctx, const float* attr, uint32_t n_comp,
+                            uint32_t n_faces, int attr_per_item, const float* idx,
+                            uint32_t width, uint32_t height, uint32_t n_items, float* out) {
+    DRESSI_REQUIRE(ctx && attr && idx && out, "bad arguments");
     DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "n_comp must be 1..4");
-    if (!n_verts) return DRESSI_OK;
+    DRESSI_REQUIRE(n_items <= kMaxBatchItems, "batch of %u items exceeds %u", n_items,
+                   kMaxBatchItems);
+    const size_t npx = (size_t)width * height;
+    if (!npx || !n_items) return DRESSI_OK;
     DRESSI_TRY_HIP(hipSetDevice(ctx->device));
-    hipLaunchKernelGGL(k_lookup_faces_bwd, dim3(div_up(n_verts, 256)), dim3(256), 0, ctx->stream,
-                       gy, n_comp, faces, n_faces, vtx_faces, n_verts, max_deg, corner,
-                       ctx->d_err, out);
+    hipLaunchKernelGGL(k_face_fetch, dim3((unsigned)((npx + 255) / 256), n_items), dim3(256), 0,
+                       ctx->stream, attr, n_comp, n_faces, idx, npx, out,
+                       attr_per_item ? (size_t)n_faces * n_comp : (size_t)0);
     DRESSI_CHECK_LAUNCH();
     return DRESSI_OK;
 }
 
 int dressi_face_fetch(dressi_ctx* ctx, const float* attr, uint32_t n_comp, uint32_t n_faces,
                       const float* idx, uint32_t width, uint32_t height, float* out) {
-    DRESSI_REQUIRE(ctx && attr && idx && out, "bad arguments");
+    return dressi_face_fetch_batch(ctx, attr, n_comp, n_faces, 0, idx, width, height, 1, out);
+}
+
+int dressi_face_fetch_bwd_batch(dressi_ctx* ctx, const float* gy, uint32_t n_comp,
+                                const float* idx, uint32_t width, uint32_t height,
+                                const float* prj0, const float* prj1, const float* prj2,
+                                int prj_per_item, uint32_t n_faces, const float* seeds,
+                                float radius_px, uint32_t n_samples, uint32_t n_items,
+                                float* out) {
+    DRESSI_REQUIRE(ctx && gy && idx && prj0 && prj1 && prj2 && seeds && out, "bad arguments");
     DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "n_comp must be 1..4");
-    const size_t npx = (size_t)width * height;
-    if (!npx) return DRESSI_OK;
+    DRESSI_REQUIRE(radius_px > 0.f || n_samples == 0,
+                   "FaceFetch: radius must be positive (or n_samples == 0)");
+    DRESSI_REQUIRE(n_items <= kMaxBatchItems, "batch of %u items exceeds %u", n_items,
+                   kMaxBatchItems);
+    if (!n_faces || !n_items) return DRESSI_OK;
     DRESSI_TRY_HIP(hipSetDevice(ctx->device));
-    hipLaunchKernelGGL(k_face_fetch, dim3((unsigned)((npx + 255) / 256)), dim3(256), 0,
-                       ctx->stream, attr, n_comp, n_faces, idx, npx, out);
+    hipLaunchKernelGGL(k_face_fetch_bwd, dim3(div_up(n_faces, 256), n_items), dim3(256), 0,
+                       ctx->stream, gy, n_comp, idx, width, height, (const float4*)prj0,
+                       (const float4*)prj1, (const float4*)prj2, n_faces, seeds, radius_px,
+                       n_samples, out, prj_per_item ? (size_t)n_faces : (size_t)0);
     DRESSI_CHECK_LAUNCH();
     return DRESSI_OK;
 }
@@ -1449,17 +1518,8 @@ int dressi_face_fetch_bwd(dressi_ctx* ctx, const float* gy, uint32_t n_comp, con
                           uint32_t width, uint32_t height, const float* prj0, const float* prj1,
                           const float* prj2, uint32_t n_faces, const float* seed,
                           float radius_px, uint32_t n_samples, float* out) {
-    DRESSI_REQUIRE(ctx && gy && idx && prj0 && prj1 && prj2 && seed && out, "bad arguments");
-    DRESSI_REQUIRE(n_comp >= 1 && n_comp <= 4, "n_comp must be 1..4");
-    DRESSI_REQUIRE(radius_px > 0.f || n_samples == 0,
-                   "FaceFetch: radius must be positive (or n_samples == 0)");
-    if (!n_faces) return DRESSI_OK;
-    DRESSI_TRY_HIP(hipSetDevice(ctx->device));
-    hipLaunchKernelGGL(k_face_fetch_bwd, dim3(div_up(n_faces, 256)), dim3(256), 0, ctx->stream,
-                       gy, n_comp, idx, width, height, (const float4*)prj0, (const float4*)prj1,
-                       (const float4*)prj2, n_faces, seed, radius_px, n_samples, out);
-    DRESSI_CHECK_LAUNCH();
-    return DRESSI_OK;
+    return dressi_face_fetch_bwd_batch(ctx, gy, n_comp, idx, width, height, prj0, prj1, prj2, 0,
+                                       n_faces, seed, radius_px, n_samples, 1, out);
 }
 
 }  // extern "C"

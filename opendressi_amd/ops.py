@@ -260,6 +260,64 @@ def antialias_bwd_vtx_batch(ctx: Context, gy: torch.Tensor, img: torch.Tensor,
     return out if is_wide else out[:, 0]
 
 
+def lookup_faces_batch(ctx: Context, attr: torch.Tensor, faces: torch.Tensor, corner: int,
+                       n_items: int) -> torch.Tensor:
+    """dressi_lookup_faces_batch: attr (V, C) shared or (N, V, C) per item ->
+    (N, F, C); each item as lookup_faces()."""
+    _prep(ctx)
+    per_item = attr.dim() == 3
+    nv, nc = attr.shape[-2], attr.shape[-1]
+    out = torch.empty((n_items, faces.shape[0], nc), dtype=torch.float32, device=attr.device)
+    check(lib.dressi_lookup_faces_batch(ctx.handle, _ptr(attr, "attr"), nc, nv,
+                                        1 if per_item else 0, _ptr(faces, "faces"),
+                                        faces.shape[0], corner, n_items, _ptr(out, "out")))
+    return out
+
+
+def lookup_faces_bwd_batch(ctx: Context, gy: torch.Tensor, faces: torch.Tensor,
+                           vtx_faces: torch.Tensor, corner: int) -> torch.Tensor:
+    """dressi_lookup_faces_bwd_batch: gy (N, F, C) -> (N, V, C)."""
+    _prep(ctx)
+    n, nf, nc = gy.shape
+    deg, nv = vtx_faces.shape
+    out = torch.empty((n, nv, nc), dtype=torch.float32, device=gy.device)
+    check(lib.dressi_lookup_faces_bwd_batch(ctx.handle, _ptr(gy, "gy"), nc, _ptr(faces, "faces"),
+                                            faces.shape[0], _ptr(vtx_faces, "vtx_faces"), nv,
+                                            deg, corner, n, _ptr(out, "out")))
+    return out
+
+
+def face_fetch_batch(ctx: Context, attr: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """dressi_face_fetch_batch: attr (F, C) shared or (N, F, C) per item, idx
+    (N, H, W) -> (N, H, W, C)."""
+    _prep(ctx)
+    n, h, w = idx.shape
+    per_item = attr.dim() == 3
+    nf, nc = attr.shape[-2], attr.shape[-1]
+    out = torch.empty((n, h, w, nc), dtype=torch.float32, device=attr.device)
+    check(lib.dressi_face_fetch_batch(ctx.handle, _ptr(attr, "attr"), nc, nf,
+                                      1 if per_item else 0, _ptr(idx, "idx"), w, h, n,
+                                      _ptr(out, "out")))
+    return out
+
+
+def face_fetch_bwd_batch(ctx: Context, gy: torch.Tensor, idx: torch.Tensor, prj0: torch.Tensor,
+                         prj1: torch.Tensor, prj2: torch.Tensor, seeds: torch.Tensor,
+                         radius_px: float, n_samples: int) -> torch.Tensor:
+    """dressi_face_fetch_bwd_batch: gy (N, H, W, C), idx (N, H, W), prj* (F, 4)
+    shared or (N, F, 4), seeds (N,) -> (N, F, C)."""
+    _prep(ctx)
+    n, h, w, nc = gy.shape
+    per_item = prj0.dim() == 3
+    nf = prj0.shape[-2]
+    out = torch.empty((n, nf, nc), dtype=torch.float32, device=gy.device)
+    check(lib.dressi_face_fetch_bwd_batch(
+        ctx.handle, _ptr(gy, "gy"), nc, _ptr(idx, "idx"), w, h, _ptr(prj0, "prj0"),
+        _ptr(prj1, "prj1"), _ptr(prj2, "prj2"), 1 if per_item else 0, nf, _ptr(seeds, "seeds"),
+        float(radius_px), n_samples, n, _ptr(out, "out")))
+    return out
+
+
 def col_sum_batch(ctx: Context, x: torch.Tensor) -> torch.Tensor:
     """dressi_col_sum_batch: (N, H, W, C) -> (N, W, C)."""
     _prep(ctx)
@@ -272,7 +330,9 @@ def col_sum_batch(ctx: Context, x: torch.Tensor) -> torch.Tensor:
 __all__ = ["soft_clip", "rasterize_soft", "rasterize", "rasterize_face_id", "lookup_faces",
            "lookup_faces_bwd", "face_fetch", "face_fetch_bwd", "antialias", "antialias_bwd_img",
            "antialias_bwd_vtx", "col_sum", "rasterize_batch", "antialias_batch",
-           "antialias_bwd_img_batch", "antialias_bwd_vtx_batch", "col_sum_batch"]
+           "antialias_bwd_img_batch", "antialias_bwd_vtx_batch", "col_sum_batch",
+           "lookup_faces_batch", "lookup_faces_bwd_batch", "face_fetch_batch",
+           "face_fetch_bwd_batch"]
 
 
 def texture_bilinear(ctx: Context, tex: torch.Tensor, uv: torch.Tensor) -> torch.Tensor:

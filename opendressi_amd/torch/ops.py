@@ -44,10 +44,6 @@ class _Engine:
         self.__dict__.update(kw)
 
 
-def _seed(device: torch.device, value: float) -> torch.Tensor:
-    return torch.full((1,), float(value), dtype=torch.float32, device=device)
-
-
 # ------------------------------- rasterize ---------------------------------
 
 
@@ -96,6 +92,14 @@ def rasterize(ctx: RasterizeHipContext, pos: torch.Tensor, tri: torch.Tensor, re
 # ------------------------------ interpolate --------------------------------
 
 
+def _faces_of(ctx, attr: torch.Tensor, faces: torch.Tensor, corner: int, n: int) -> torch.Tensor:
+    """LookupFaces of a shared (V, C) attribute -> (F, C), or of per-item
+    (N, V, C) attributes -> (N, F, C), in one launch."""
+    if attr.dim() == 2:
+        return K.lookup_faces(ctx, attr, faces, corner)
+    return K.lookup_faces_batch(ctx, attr, faces, corner, n)
+
+
 class _InterpolateFn(torch.autograd.Function):
     @staticmethod
     def forward(fctx, attr, rast, vctx, md, rinfo):
@@ -105,19 +109,18 @@ class _InterpolateFn(torch.autograd.Function):
         shared = attr_d.dim() == 2
         c = channels(attr_d.shape[-1], "attr")
         n = rast_d.shape[0]
-        outs = []
         with vctx.lock:
-            for i in range(n):
-                a = attr_d if shared else attr_d[i].contiguous()
-                u = rast_d[i, ..., 0:1]
-                v = rast_d[i, ..., 1:2]
-                tid = rast_d[i, ..., 3].contiguous()
-                pix = [K.face_fetch(vctx._ctx, K.lookup_faces(vctx._ctx, a, md.faces_f, k), tid)
-                       for k in range(3)]
-                outs.append(u * pix[0] + v * pix[1] + ((1.0 - u) - v) * pix[2])
+            # each op once for the whole batch
+            a = attr_d.contiguous()
+            tid = rast_d[..., 3].contiguous()
+            pix = [K.face_fetch_batch(vctx._ctx, _faces_of(vctx._ctx, a, md.faces_f, k, n), tid)
+                   for k in range(3)]
+        u = rast_d[..., 0:1]
+        v = rast_d[..., 1:2]
+        out = u * pix[0] + v * pix[1] + ((1.0 - u) - v) * pix[2]
         fctx.dressi = (vctx, md, rinfo, shared, c)
         fctx.save_for_backward(attr, rast)
-        return torch.stack(outs, 0).to(attr.device)
+        return out.to(attr.device)
 
     @staticmethod
     def backward(fctx, grad_out):
@@ -128,23 +131,21 @@ class _InterpolateFn(torch.autograd.Function):
         g = to_dev(grad_out, dev, "grad_out")
         n = rast_d.shape[0]
         clip_vk = rinfo.clip_vk
-        zero = _seed(dev, 0.0)
-        per_item = []
+        u = rast_d[..., 0:1]
+        v = rast_d[..., 1:2]
+        g_pix = [g * u, g * v, g * ((1.0 - u) - v)]
+        seeds = torch.zeros(n, dtype=torch.float32, device=dev)
         with vctx.lock:
-            for i in range(n):
-                clip = clip_vk[i if clip_vk.shape[0] > 1 else 0].contiguous()
-                prj = [K.lookup_faces(vctx._ctx, clip, md.faces_f, k) for k in range(3)]
-                u = rast_d[i, ..., 0:1]
-                v = rast_d[i, ..., 1:2]
-                tid = rast_d[i, ..., 3].contiguous()
-                gi = g[i]
-                g_pix = [gi * u, gi * v, gi * ((1.0 - u) - v)]
-                contribs = []
-                for k in (2, 1, 0):
-                    g_face = K.face_fetch_bwd(vctx._ctx, g_pix[k].contiguous(), tid, prj[0],
-                                              prj[1], prj[2], zero, 1.0, 0)
-                    contribs.append(K.lookup_faces_bwd(vctx._ctx, g_face, md.faces_f, md.vft, k))
-                per_item.append(contribs)
+            clip = clip_vk.contiguous() if clip_vk.shape[0] > 1 else clip_vk[0].contiguous()
+            prj = [_faces_of(vctx._ctx, clip, md.faces_f, k, n) for k in range(3)]
+            tid = rast_d[..., 3].contiguous()
+            # per corner k = 2, 1, 0: the (N, V, C) vertex contributions
+            contribs = []
+            for k in (2, 1, 0):
+                g_face = K.face_fetch_bwd_batch(vctx._ctx, g_pix[k].contiguous(), tid, prj[0],
+                                                prj[1], prj[2], seeds, 1.0, 0)
+                contribs.append(K.lookup_faces_bwd_batch(vctx._ctx, g_face, md.faces_f, md.vft, k))
+        per_item = [[cb[i] for cb in contribs] for i in range(n)]
         if shared:
             # the shared leaf's consumers, latest-created (last item) first
             g_attr = sum_contribs([cb for contribs in reversed(per_item) for cb in contribs])

@@ -159,6 +159,55 @@ def test_rasterize_batch_matches_per_item(ctx, oracle):
     ctx.synchronize()
 
 
+def test_lookup_and_fetch_batches_match_per_item(ctx, oracle):
+    """The batched LookupFaces / FaceFetch and their backwards: three items
+    (own cameras; per-item and shared attributes / clips; the exact and the
+    stochastic FaceFetchBwd with a seed per item) equal the single-item entry
+    points item by item, bit for bit."""
+    import torch
+
+    from opendressi_amd import ops
+    s = 61
+    items = [_random_scene(seed, 3, s) for seed in (21, 22, 23)]
+    faces = items[0][1]
+    clip = np.stack([it[0] for it in items])
+    nv = clip.shape[1]
+    rng = np.random.default_rng(5)
+    attr = rng.standard_normal((3, nv, 3)).astype(np.float32)
+    ids = np.stack([oracle.rasterize_face_id(c, faces, s, s) for c in clip])
+    gy = rng.standard_normal((3, s, s, 3)).astype(np.float32)
+    vf = oracle.vertex_faces_tex(faces, nv)
+    seeds = np.array([0.0, 5.0, 11.0], np.float32)
+    print(f"[fetch batch] 3 items screen={s}", flush=True)
+    d_faces, d_ids, d_vf, d_gy = dev(faces), dev(ids), dev(vf), dev(gy)
+    for k in range(3):
+        lf = host(ops.lookup_faces_batch(ctx, dev(attr), d_faces, k, 3))
+        lf_shared = host(ops.lookup_faces_batch(ctx, dev(attr[1]), d_faces, k, 3))
+        prj = [ops.lookup_faces_batch(ctx, dev(clip), d_faces, q, 3) for q in range(3)]
+        ff = host(ops.face_fetch_batch(ctx, dev(lf), d_ids))
+        ff_shared = host(ops.face_fetch_batch(ctx, dev(lf_shared[0]), d_ids))
+        bwd = {n: host(ops.face_fetch_bwd_batch(ctx, d_gy, d_ids, prj[0], prj[1], prj[2],
+                                                dev(seeds), 2.0, n)) for n in (0, 8)}
+        lb = host(ops.lookup_faces_bwd_batch(ctx, dev(bwd[0]), d_faces, d_vf, k))
+        for i in range(3):
+            what = f"corner {k} item {i}"
+            _exact(lf[i], host(ops.lookup_faces(ctx, dev(attr[i]), d_faces, k)), what + " lookup")
+            _exact(lf_shared[i], host(ops.lookup_faces(ctx, dev(attr[1]), d_faces, k)),
+                   what + " lookup shared")
+            _exact(ff[i], host(ops.face_fetch(ctx, dev(lf[i]), dev(ids[i]))), what + " fetch")
+            _exact(ff_shared[i], host(ops.face_fetch(ctx, dev(lf_shared[0]), dev(ids[i]))),
+                   what + " fetch shared")
+            pi = [p[i].contiguous() for p in prj]
+            for n in (0, 8):
+                one = ops.face_fetch_bwd(ctx, dev(gy[i]), dev(ids[i]), pi[0], pi[1], pi[2],
+                                         dev(seeds[i:i + 1]), 2.0, n)
+                _exact(bwd[n][i], host(one), f"{what} fetch bwd n={n}")
+            _exact(lb[i], host(ops.lookup_faces_bwd(ctx, dev(bwd[0][i]), d_faces, d_vf, k)),
+                   what + " lookup bwd")
+    assert (ids > 0).sum() > 300
+    ctx.synchronize()
+
+
 def test_raster_edge_cases(ctx, oracle):
     """Empty mesh, a screen-filling triangle (its bins overflow the list
     capacity and take the full-scan path), faces behind the camera, a
