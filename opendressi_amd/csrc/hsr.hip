@@ -824,6 +824,35 @@ int enqueue_iteration(dressi_hsr_plan* p, hipStream_t s) {
     return DRESSI_OK;
 }
 
+// Screen pixels from which the captured graph runs the loss on a branch.
+constexpr uint64_t kForkLossMinPixels = 1ull << 20;
+
+// `reps` iterations for graph capture on `s`, the loss of each on `side`
+// (HardSoftRas: the loss reads the face ids, targets and the setup's screen
+// corners and writes only pred and the loss image, which the face backward,
+// the vertex kernel and the next setup never read): it overlaps the face
+// backward, the vertex kernel and the next setup, and joins before the next
+// raster rewrites the face ids, and at the end. `ev` holds 2 * reps events.
+int enqueue_iterations_forked(dressi_hsr_plan* p, hipStream_t s, hipStream_t side,
+                              uint32_t reps, hipEvent_t* ev) {
+    hipEvent_t joined = nullptr;
+    for (uint32_t r = 0; r < reps; r++) {
+        if (int rc = launch_iter_kernel(p->d, s, 0)) return rc;  // setup
+        if (joined) DRESSI_TRY_HIP(hipStreamWaitEvent(s, joined, 0));
+        if (int rc = launch_iter_kernel(p->d, s, 1)) return rc;  // raster
+        DRESSI_TRY_HIP(hipEventRecord(ev[2 * r], s));
+        DRESSI_TRY_HIP(hipStreamWaitEvent(side, ev[2 * r], 0));
+        if (int rc = launch_iter_kernel(p->d, side, 2)) return rc;  // loss
+        DRESSI_TRY_HIP(hipEventRecord(ev[2 * r + 1], side));
+        joined = ev[2 * r + 1];
+        for (int k = 3; k < kIterKernels; k++) {
+            if (int rc = launch_iter_kernel(p->d, s, k)) return rc;
+        }
+    }
+    if (joined) DRESSI_TRY_HIP(hipStreamWaitEvent(s, joined, 0));
+    return DRESSI_OK;
+}
+
 int ready(dressi_hsr_plan* p) {
     DRESSI_REQUIRE(p, "NULL plan");
     DRESSI_REQUIRE(p->mesh_set, "dressi_hsr_set_mesh() must be called before stepping");
@@ -1264,26 +1293,50 @@ int dressi_hsr_step(dressi_hsr_plan* p, uint32_t n_iters) {
         // capture one iteration, and kGraphBatch of them, on a private
         // stream, then replay on `s`
         for (int which = 0; which < 2; which++) {
-            hipStream_t cap_stream = nullptr;
-            DRESSI_TRY_HIP(hipStreamCreateWithFlags(&cap_stream, hipStreamNonBlocking));
-            hipError_t e = hipStreamBeginCapture(cap_stream, hipStreamCaptureModeThreadLocal);
+            hipStream_t cap_stream = nullptr, side = nullptr;
+            hipEvent_t ev[2 * kGraphBatch] = {};
             int rc = DRESSI_OK;
+            if (hipStreamCreateWithFlags(&cap_stream, hipStreamNonBlocking) != hipSuccess ||
+                hipStreamCreateWithFlags(&side, hipStreamNonBlocking) != hipSuccess) {
+                set_error("hipStreamCreate failed");
+                rc = DRESSI_ERR_HIP;
+            }
+            for (hipEvent_t& x : ev) {
+                if (!rc && hipEventCreateWithFlags(&x, hipEventDisableTiming) != hipSuccess) {
+                    set_error("hipEventCreate failed");
+                    rc = DRESSI_ERR_HIP;
+                }
+            }
             hipGraph_t g = nullptr;
-            if (e == hipSuccess) {
+            const hipError_t e =
+                rc ? hipSuccess : hipStreamBeginCapture(cap_stream, hipStreamCaptureModeThreadLocal);
+            if (!rc && e == hipSuccess) {
                 const uint32_t reps = which == 0 ? 1u : kGraphBatch;
-                for (uint32_t r = 0; r < reps && !rc; r++) {
-                    rc = enqueue_iteration(p, cap_stream);
+                // the loss on its own branch pays at large screens (2048 x 2048 x 4
+                // views: 468 -> 454 us per iteration); at 512 x 512 the extra graph
+                // edges cost more than the overlap gains (106 -> 113 us)
+                if (p->d.technique == 0 &&
+                    (uint64_t)p->desc.width * p->desc.height >= kForkLossMinPixels) {
+                    rc = enqueue_iterations_forked(p, cap_stream, side, reps, ev);
+                } else {
+                    for (uint32_t r = 0; r < reps && !rc; r++) {
+                        rc = enqueue_iteration(p, cap_stream);
+                    }
                 }
                 hipError_t e2 = hipStreamEndCapture(cap_stream, &g);
                 if (!rc && e2 != hipSuccess) {
                     set_error("graph capture failed: %s", hipGetErrorString(e2));
                     rc = DRESSI_ERR_HIP;
                 }
-            } else {
+            } else if (!rc) {
                 set_error("hipStreamBeginCapture failed: %s", hipGetErrorString(e));
                 rc = DRESSI_ERR_HIP;
             }
-            hipStreamDestroy(cap_stream);
+            for (hipEvent_t x : ev) {
+                if (x) hipEventDestroy(x);
+            }
+            if (side) hipStreamDestroy(side);
+            if (cap_stream) hipStreamDestroy(cap_stream);
             if (which == 0) {
                 p->graph = g;
             } else {
