@@ -1005,6 +1005,10 @@ __device__ __forceinline__ void walk_bin(const Rec* recs, const BinBuffers& b, u
 constexpr int kBinWin = 32;  // LDS window of 32 x 32 tiles
 constexpr int kBinThreads = 256;
 constexpr int kBinBig = 2;
+// Dealt rows whose face slot a lookup table holds (beyond it: a binary
+// search over the row scan).
+constexpr uint32_t kBinRowCap = 2048;
+static_assert(kBinThreads <= 256, "face slots fit a byte");
 
 // Triangle of the tile test: screen corners, orientation sign of its area
 // and the edge-function margin (< 0: bbox only).
@@ -1021,6 +1025,7 @@ struct BinLds {
     uint32_t f[kBinThreads], view[kBinThreads];
     int tx0[kBinThreads], ty0[kBinThreads], tx1[kBinThreads];
     BinTri tri[kBinThreads];
+    uint8_t row_face[kBinRowCap];  // face slot of dealt row p (p < kBinRowCap)
 };
 
 // Whether triangle t can cover a pixel centre of tile (tx, ty): on every
@@ -1192,6 +1197,9 @@ __device__ __forceinline__ void bin_pair(const BinBuffers& b, const RasterGeom& 
 
 // Face slot q of the workgroup's dealt rows with off[q] <= p < off[q + 1].
 __device__ __forceinline__ int dealt_face(const BinLds& lds, uint32_t p, int nthr) {
+    if (p < kBinRowCap) {
+        return lds.row_face[p];
+    }
     int lo = 0, hi = nthr - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -1270,6 +1278,14 @@ __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom
     }
     __syncthreads();
     const uint32_t total = lds.off[nthr];
+    // the row -> face table of the first kBinRowCap dealt rows
+    if (big) {
+        const uint32_t r1 = min(lds.off[tid + 1], kBinRowCap);
+        for (uint32_t r = lds.off[tid]; r < r1; r++) {
+            lds.row_face[r] = (uint8_t)tid;
+        }
+    }
+    __syncthreads();
     const int wx0 = lds.win[0], wy0 = lds.win[1];
     const bool mixed = lds.win[3] != 0;
     // the first kKeepRows dealt rows of each thread: pass 0 keeps the face
