@@ -1255,6 +1255,26 @@ int pbr_enqueue(dressi_pbr_plan* p, hipStream_t s) {
     return DRESSI_OK;
 }
 
+// One iteration for graph capture: after the shading, the texture gather +
+// Adam runs on `side` beside the environment's chain (resolve, transposed
+// convolutions, env Adam): the two read and write disjoint buffers (both
+// only read t), and both join before the loss kernel advances t.
+int pbr_enqueue_forked(dressi_pbr_plan* p, hipStream_t s, hipStream_t side, hipEvent_t fork,
+                       hipEvent_t join) {
+    for (int k = 0; k <= 2; k++) {  // pool, conv_fwd, shade
+        if (int rc = launch_pbr_kernel(p->d, s, k)) return rc;
+    }
+    DRESSI_TRY_HIP(hipEventRecord(fork, s));
+    DRESSI_TRY_HIP(hipStreamWaitEvent(side, fork, 0));
+    if (int rc = launch_pbr_kernel(p->d, side, 6)) return rc;  // tex_adam
+    DRESSI_TRY_HIP(hipEventRecord(join, side));
+    for (int k = 3; k <= 5; k++) {  // resolve, conv_bwd, env_adam
+        if (int rc = launch_pbr_kernel(p->d, s, k)) return rc;
+    }
+    DRESSI_TRY_HIP(hipStreamWaitEvent(s, join, 0));
+    return launch_pbr_kernel(p->d, s, 7);  // loss, t + 1
+}
+
 // host VEC3 {n} -> device float4 {n} (w = 0)
 int upload3(float4* dst, const float* src, size_t n) {
     std::vector<float4> v(n);
@@ -1779,22 +1799,33 @@ int dressi_pbr_step(dressi_pbr_plan* p, uint32_t n_iters) {
     hipStream_t s = p->ctx->stream;
     if (!p->exec || p->graph_stream != s) {
         pbr_drop_graph(p);
-        hipStream_t cap_stream = nullptr;
-        DRESSI_TRY_HIP(hipStreamCreateWithFlags(&cap_stream, hipStreamNonBlocking));
-        hipError_t e = hipStreamBeginCapture(cap_stream, hipStreamCaptureModeThreadLocal);
+        hipStream_t cap_stream = nullptr, side = nullptr;
+        hipEvent_t fork = nullptr, join = nullptr;
         int rc = DRESSI_OK;
-        if (e == hipSuccess) {
-            rc = pbr_enqueue(p, cap_stream);
+        if (hipStreamCreateWithFlags(&cap_stream, hipStreamNonBlocking) != hipSuccess ||
+            hipStreamCreateWithFlags(&side, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&fork, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&join, hipEventDisableTiming) != hipSuccess) {
+            set_error("stream / event creation failed");
+            rc = DRESSI_ERR_HIP;
+        }
+        const hipError_t e =
+            rc ? hipSuccess : hipStreamBeginCapture(cap_stream, hipStreamCaptureModeThreadLocal);
+        if (!rc && e == hipSuccess) {
+            rc = pbr_enqueue_forked(p, cap_stream, side, fork, join);
             hipError_t e2 = hipStreamEndCapture(cap_stream, &p->graph);
             if (!rc && e2 != hipSuccess) {
                 set_error("graph capture failed: %s", hipGetErrorString(e2));
                 rc = DRESSI_ERR_HIP;
             }
-        } else {
+        } else if (!rc) {
             set_error("hipStreamBeginCapture failed: %s", hipGetErrorString(e));
             rc = DRESSI_ERR_HIP;
         }
-        hipStreamDestroy(cap_stream);
+        if (fork) hipEventDestroy(fork);
+        if (join) hipEventDestroy(join);
+        if (side) hipStreamDestroy(side);
+        if (cap_stream) hipStreamDestroy(cap_stream);
         if (rc) {
             pbr_drop_graph(p);
             return rc;
