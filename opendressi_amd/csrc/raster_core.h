@@ -1292,7 +1292,7 @@ __device__ __forceinline__ void bin_append(const BinBuffers& b, const RasterGeom
     // slot, row, first column and a mask of the columns whose test passed
     // (spans of at most 32 tiles), so pass 1 repeats neither the search nor
     // the tests
-    constexpr int kKeepRows = 4;
+    constexpr int kKeepRows = 8;
     int keep_lo[kKeepRows], keep_ty[kKeepRows], keep_ta[kKeepRows];
     uint32_t keep_mask[kKeepRows];
     bool keep_ok[kKeepRows];
