@@ -2,7 +2,7 @@
 the reference's own outputs (golden fixtures from oracle/_ref) and the oracle
 at full size, through the C ABI.
 
-Bars (north star): face-id buffers bit-exact; rendered images within 1e-5
+Bars: face-id buffers bit-exact; rendered images within 1e-5
 relative; vertex gradients within 1e-4 relative; optimised parameters within
 1e-3 after the fixed iteration count. The kernels replay the reference's
 float operations in its order, so the fixture cases are checked bit-exactly.

@@ -2,7 +2,7 @@
 through opendressi_amd.SilhouetteFit) against the reference's own numbers
 (golden fixtures written from oracle/_ref) and the oracle at full size.
 
-Bars (north star): face-id / coverage buffers bit-exact; rendered images
+Bars: face-id / coverage buffers bit-exact; rendered images
 within 1e-5 relative; vertex gradients within 1e-4 relative; optimised
 parameters within 1e-3 after the fixed iteration count. Relative errors are
 taken against the array's largest magnitude (the reference's own GPU tests
