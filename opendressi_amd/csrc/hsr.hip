@@ -150,11 +150,11 @@ struct LossVec<4> {
 };
 
 template <int NV, int P>
-__global__ __launch_bounds__(256) void k_hsr_loss(HsrDev d) {
+__device__ __forceinline__ void loss_block(const HsrDev& d, uint32_t bkx, uint32_t bky) {
     static_assert(NV * P <= 32, "rim bits");
     const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
-    const uint32_t x0 = (blockIdx.x * 64 + lane) * P;
-    const uint32_t y = blockIdx.y * 4 + wv;
+    const uint32_t x0 = (bkx * 64 + lane) * P;
+    const uint32_t y = bky * 4 + wv;
     // lanes past the edge stay for the wave's exchanges (no rim, no stores)
     const bool valid = x0 < d.g.width && y < d.g.height;
     const size_t npx = (size_t)d.g.width * d.g.height;
@@ -239,7 +239,7 @@ __global__ __launch_bounds__(256) void k_hsr_loss(HsrDev d) {
                 st.s[1][1] = a.w;
                 st.s[2][0] = b.x;
                 st.s[2][1] = b.y;
-                const uint32_t px = (blockIdx.x * 64 + owner) * P + c;
+                const uint32_t px = (bkx * 64 + owner) * P + c;
                 pixel_fw_screen(1.f, -1.f, 1.f, (float)px + 0.5f, (float)y + 0.5f,
                                 d.sigma_scale, st);
                 s_pred[wv][lane] = st.pred;
@@ -284,6 +284,11 @@ __global__ __launch_bounds__(256) void k_hsr_loss(HsrDev d) {
         outp[c] = out[0];
     }
     LossVec<P>::store(d.loss + o, outp);
+}
+
+template <int NV, int P>
+__global__ __launch_bounds__(256) void k_hsr_loss(HsrDev d) {
+    loss_block<NV, P>(d, blockIdx.x, blockIdx.y);
 }
 
 // FaceFetchBwd (stochastic, n samples, seed = t) fused with the pixel
@@ -448,11 +453,12 @@ __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
 // The same with a group of kSampleLanes lanes for every (view, face), rim
 // or not (each group reads its face's flag): the form for small problems,
 // whose few workgroups would otherwise take their queued faces in turn.
-__global__ __launch_bounds__(256) void k_hsr_face_bwd_all(HsrDev d) {
-    const uint32_t gi = blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void face_bwd_all_block(const HsrDev& d, uint32_t blk,
+                                                   uint32_t n_blk) {
+    const uint32_t gi = blk * blockDim.x + threadIdx.x;
     publish_t_next(d, gi);
     // the raster is done with this iteration's bins: clear their counters
-    for (uint32_t b = gi; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
+    for (uint32_t b = gi; b < d.bins.n_bins; b += n_blk * blockDim.x) {
         const uint32_t c = d.bins.counts[b];
         if (c > d.bins.cap && d.bin_over) {
             *d.bin_over = c;  // rare: the host grows the bins before the next step
@@ -478,6 +484,24 @@ __global__ __launch_bounds__(256) void k_hsr_face_bwd_all(HsrDev d) {
         for (int k = 0; k < 3; k++) {
             dst[(size_t)k * F + f] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_hsr_face_bwd_all(HsrDev d) {
+    face_bwd_all_block(d, blockIdx.x, gridDim.x);
+}
+
+// Small problems: the loss (one pixel per lane) and the group-per-face
+// backward in one launch -- they read the raster's output and write disjoint
+// buffers -- the first n_loss workgroups taking the loss's blocks, the rest
+// the backward's (one kernel boundary less in a latency-bound iteration).
+template <int NV>
+__global__ __launch_bounds__(256) void k_hsr_loss_face_bwd(HsrDev d, uint32_t loss_gx,
+                                                           uint32_t n_loss) {
+    if (blockIdx.x < n_loss) {
+        loss_block<NV, 1>(d, blockIdx.x % loss_gx, blockIdx.x / loss_gx);
+    } else {
+        face_bwd_all_block(d, blockIdx.x - n_loss, gridDim.x - n_loss);
     }
 }
 
@@ -754,12 +778,28 @@ constexpr int kIterKernels = 5;
 const char* const kIterKernelNames[kIterKernels] = {"k_hsr_setup", "k_hsr_raster", "k_hsr_loss",
                                                     "k_hsr_face_bwd", "k_hsr_vertex_adam"};
 
+// Screen pixels from which the captured graph runs the loss on a branch.
+constexpr uint64_t kForkLossMinPixels = 1ull << 20;
+
+// The loss takes four pixels per lane where its grid still fills the chip.
+bool loss_vec(const RasterGeom& g) {
+    return g.width % 4 == 0 && (size_t)div_up(g.width, 256) * div_up(g.height, 4) >= 2048;
+}
+
+// Small problems run the loss and the face backward as one launch (kernel 2;
+// kernel 3 is then empty). Measured at 512 x 512 x 4 views.
+bool fused_loss_bwd(const RasterGeom& g) {
+    return !loss_vec(g) && g.n_views * g.n_faces <= kFaceBwdQueueMin &&
+           (uint64_t)g.width * g.height < kForkLossMinPixels;
+}
+
 int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
     if (d.technique == 1) {
         return launch_aa_kernel(d, s, k);
     }
     const RasterGeom& g = d.g;
     const uint32_t nvf = g.n_views * g.n_faces;
+    const bool fused = fused_loss_bwd(g);
     switch (k) {
         case 0:
             hipLaunchKernelGGL(k_hsr_setup, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
@@ -770,14 +810,17 @@ int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
                                dim3(64), 0, s, d);
             break;
         case 2: {
-            // four pixels per lane where the grid still fills the chip
-            const bool vec = g.width % 4 == 0 &&
-                             (size_t)div_up(g.width, 256) * div_up(g.height, 4) >= 2048;
+            const bool vec = loss_vec(g);
             const dim3 grid(div_up(g.width, vec ? 256 : 64), div_up(g.height, 4));
+            const uint32_t n_loss = grid.x * grid.y;
+            const uint32_t n_bwd = div_up(nvf, 256 / kSampleLanes);
             switch (g.n_views) {
 #define DRESSI_NV(N)                                                                          \
     case N:                                                                                   \
-        if (vec) {                                                                            \
+        if (fused) {                                                                          \
+            hipLaunchKernelGGL((k_hsr_loss_face_bwd<N>), dim3(n_loss + n_bwd), dim3(256), 0,  \
+                               s, d, grid.x, n_loss);                                         \
+        } else if (vec) {                                                                     \
             hipLaunchKernelGGL((k_hsr_loss<N, 4>), grid, dim3(256), 0, s, d);                 \
         } else {                                                                              \
             hipLaunchKernelGGL((k_hsr_loss<N, 1>), grid, dim3(256), 0, s, d);                 \
@@ -793,6 +836,9 @@ int launch_iter_kernel(const HsrDev& d, hipStream_t s, int k) {
             break;
         }
         case 3:
+            if (fused) {
+                return DRESSI_OK;  // ran with the loss
+            }
             if (nvf > kFaceBwdQueueMin) {
                 hipLaunchKernelGGL(k_hsr_face_bwd, dim3(div_up(nvf, 256)), dim3(256), 0, s, d);
             } else {
@@ -823,9 +869,6 @@ int enqueue_iteration(dressi_hsr_plan* p, hipStream_t s) {
     }
     return DRESSI_OK;
 }
-
-// Screen pixels from which the captured graph runs the loss on a branch.
-constexpr uint64_t kForkLossMinPixels = 1ull << 20;
 
 // `reps` iterations for graph capture on `s`, the loss of each on `side`
 // (HardSoftRas: the loss reads the face ids, targets and the setup's screen
