@@ -410,6 +410,9 @@ __global__ __launch_bounds__(256) void k_col_sum_op(const float* x, uint32_t n_c
 // Per-view clip positions: TransformToClipVar of every vertex.
 __global__ __launch_bounds__(256) void k_aa_clip(HsrDev d) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i == 0 && d.aa_count) {
+        *d.aa_count = 0u;  // the face scan of this iteration appends from 0
+    }
     if (i >= d.g.n_views * d.n_verts) {
         return;
     }
@@ -890,21 +893,8 @@ __device__ __forceinline__ uint32_t fold_groups(uint64_t m) {
 // two pixels have the same mask value carry gr = 0 and are skipped before the
 // pair evaluation. Every lane of a wave runs every shuffle (no early exit).
 // Also clears the bin counters.
-__global__ __launch_bounds__(256) void k_aa_face_bwd(HsrDev d) {
-    const uint32_t gi = blockIdx.x * blockDim.x + threadIdx.x;
-    publish_t_next(d, gi);
-    for (uint32_t b = gi; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
-        const uint32_t c = d.bins.counts[b];
-        if (c > d.bins.cap && d.bin_over) {
-            *d.bin_over = c;  // rare: the host grows the bins before the next step
-        }
-        d.bins.counts[b] = 0;
-    }
-    const uint32_t nvf = d.g.n_views * d.g.n_faces;
-    const uint32_t item = gi >> 3;
-    const bool valid = item < nvf;
-    const int j = (int)(threadIdx.x & 7u);
-    const int gbase = (int)(threadIdx.x & 56u);  // first lane of the group in the wave
+__device__ __forceinline__ void aa_face_bwd_item(const HsrDev& d, uint32_t item, bool valid,
+                                                 int j, int gbase) {
     const uint32_t view = valid ? item / d.g.n_faces : 0u;
     const uint32_t f = valid ? item - view * d.g.n_faces : 0u;
     const int w = (int)d.g.width, h = (int)d.g.height;
@@ -1013,6 +1003,98 @@ __global__ __launch_bounds__(256) void k_aa_face_bwd(HsrDev d) {
     }
 }
 
+// Faces whose samples all carry gy = 0 (pred = target at every sample; most
+// faces, away from both silhouettes) add nothing: they get their zero
+// corner gradients here, one 8-lane group per (view, face) with the sample
+// positions and gy of aa_face_bwd_item, and the others are listed (per
+// workgroup in LDS, one global append per workgroup) for k_aa_face_bwd.
+// Also clears the bin counters and publishes t + 1.
+__global__ __launch_bounds__(256) void k_aa_face_scan(HsrDev d) {
+    __shared__ uint32_t queue[32];
+    __shared__ uint32_t n_q, base_q;
+    const uint32_t gi = blockIdx.x * blockDim.x + threadIdx.x;
+    publish_t_next(d, gi);
+    for (uint32_t b = gi; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
+        const uint32_t c = d.bins.counts[b];
+        if (c > d.bins.cap && d.bin_over) {
+            *d.bin_over = c;  // rare: the host grows the bins before the next step
+        }
+        d.bins.counts[b] = 0;
+    }
+    if (threadIdx.x == 0) {
+        n_q = 0;
+    }
+    __syncthreads();
+    const uint32_t nvf = d.g.n_views * d.g.n_faces;
+    const uint32_t item = gi >> 3;
+    const bool valid = item < nvf;
+    const int j = (int)(threadIdx.x & 7u);
+    const uint32_t view = valid ? item / d.g.n_faces : 0u;
+    const uint32_t f = valid ? item - view * d.g.n_faces : 0u;
+    const int w = (int)d.g.width, h = (int)d.g.height;
+    const size_t npx = (size_t)w * h;
+    bool act = false;
+    if (valid && d.n_samples > 0) {
+        const float4* clip = d.clip + (size_t)view * d.n_verts;
+        float4 c[3];
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            c[k] = clip[(uint32_t)d.faces[f * 3 + k]];
+        }
+        float s3x[3], s3y[3];
+        if (aa_face_screen(c, (float)w, (float)h, s3x, s3y)) {
+            const uint32_t seed_u = (uint32_t)(int64_t)(*d.t + 0.5f);
+            const float* pred = d.pred + view * npx;
+            const float* tgt = d.targets + view * npx;
+            for (uint32_t smp = (uint32_t)j; smp < d.n_samples && !act; smp += 8) {
+                int sx = -1, sy = -1;
+                if (aa_sample_px(s3x, s3y, f, smp, seed_u, &sx, &sy) && sx >= 0 && sy >= 0 &&
+                    sx < w && sy < h) {
+                    const size_t so = (size_t)sy * w + sx;
+                    const float diff = tgt[so] - pred[so];
+                    const float cd = d.inv_px * diff;
+                    act = -(cd + cd) != 0.f;
+                }
+            }
+        }
+    }
+    // the group's verdict on its first lane
+    const uint64_t m = __ballot(act);
+    const bool any = ((m >> (threadIdx.x & 56u)) & 0xffull) != 0ull;
+    if (valid && j == 0) {
+        if (any) {
+            queue[atomicAdd(&n_q, 1u)] = item;
+        } else {
+            float4* dst = d.gtri + (size_t)view * 3 * d.g.n_faces;
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                dst[(size_t)k * d.g.n_faces + f] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0 && n_q) {
+        base_q = atomicAdd(d.aa_count, n_q);
+    }
+    __syncthreads();
+    if (threadIdx.x < n_q) {
+        d.aa_list[base_q + threadIdx.x] = queue[threadIdx.x];
+    }
+}
+
+// AntiAliasBwdVtx (stochastic, wide) of the listed faces: 8-lane groups walk
+// the list (aa_face_bwd_item on each).
+constexpr uint32_t kAaFaceBwdGrid = 2048;
+__global__ __launch_bounds__(256) void k_aa_face_bwd(HsrDev d) {
+    const uint32_t n = *d.aa_count;
+    const uint32_t n_groups = gridDim.x * blockDim.x / 8u;
+    const int j = (int)(threadIdx.x & 7u);
+    const int gbase = (int)(threadIdx.x & 56u);
+    for (uint32_t li = (blockIdx.x * blockDim.x + threadIdx.x) >> 3; li < n; li += n_groups) {
+        aa_face_bwd_item(d, d.aa_list[li], true, j, gbase);
+    }
+}
+
 // ColSum of the (vertex, slot) rows per view -- the row of slot d is the
 // accumulator of face vf[d][v] at the corner holding v; padding rows are
 // zero -- then the shared clip->pos chain and Adam: one lane per (vertex,
@@ -1109,7 +1191,10 @@ int launch_aa_kernel(const HsrDev& d, hipStream_t s, int k) {
             break;
         }
         default:
-            hipLaunchKernelGGL(k_aa_face_bwd, dim3(div_up(nvf, 32)), dim3(256), 0, s, d);
+            hipLaunchKernelGGL(k_aa_face_scan, dim3(div_up(nvf, 32)), dim3(256), 0, s, d);
+            DRESSI_CHECK_LAUNCH();
+            hipLaunchKernelGGL(k_aa_face_bwd, dim3(std::min(div_up(nvf, 32), kAaFaceBwdGrid)),
+                               dim3(256), 0, s, d);
             break;
     }
     DRESSI_CHECK_LAUNCH();

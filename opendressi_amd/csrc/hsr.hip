@@ -1037,6 +1037,8 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
         rc = rc ? rc : plan_alloc(p, &d.heavy.slot, (size_t)N * d.g.n_tiles);
     } else {
         rc = rc ? rc : plan_alloc(p, &d.arecs, N * F);
+        rc = rc ? rc : plan_alloc(p, &d.aa_list, N * F);
+        rc = rc ? rc : plan_alloc(p, &d.aa_count, 1);
         rc = rc ? rc : plan_alloc(p, &d.clip, N * V);
     }
     rc = rc ? rc : plan_alloc(p, &d.ids, N * npx);

@@ -96,6 +96,8 @@ struct HsrDev {
     uint32_t technique;       // 0 HardSoftRas, 1 AA
     float4* clip;             // [N][V]
     AaRec* arecs;             // [N][F]
+    uint32_t* aa_list;        // [N * F] faces with a sample where d loss / d pred != 0
+    uint32_t* aa_count;       // entries of aa_list (reset by the clip kernel)
     // a bin count the face backward found above bins.cap (host-mapped, written
     // only when a bin overflowed; the plan's next step grows the bins)
     uint32_t* bin_over;
