@@ -79,13 +79,13 @@ def build(verbose: bool = False) -> str:
 
 
 def build_graph_test(verbose: bool = False) -> str:
-    """The test programs (tests/graph_c1.cpp, tests/graph_ops.cpp over the
+    """The test programs (tests/graph_c1.cpp, graph_ops.cpp, graph_tex.cpp over the
     graph API, tests/assets_cli.cpp over the examples' helpers), linked
     against the library; plain C++ (those headers need no HIP headers)."""
     out_dir = os.path.join(ROOT, "tests", "_bin")
     os.makedirs(out_dir, exist_ok=True)
     exe = ""
-    for name in ("graph_c1", "graph_ops", "assets_cli"):
+    for name in ("graph_c1", "graph_ops", "graph_tex", "assets_cli"):
         src = os.path.join(ROOT, "tests", name + ".cpp")
         exe = os.path.join(out_dir, name)
         cmd = ["g++", "-std=c++17", "-O2", "-ffp-contract=off", "-I", os.path.join(ROOT, "include"),

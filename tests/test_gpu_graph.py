@@ -181,3 +181,56 @@ def test_fused_route_full_workload_final_parameters(tmp_path, name):
     assert np.array_equal(rows, gold["out_smp_m"])
     assert np.array_equal(g["loss"], gold["out_loss"])
     assert g["t"][0] == w.iters
+
+
+TEX_EXE = os.path.join(ROOT, "tests", "_bin", "graph_tex")
+
+
+@pytest.mark.parametrize("naive", [False, True])
+def test_texture_example_graph_matches_oracle(tmp_path, oracle, naive):
+    """The texture fit's graph (examples/texture_optimization/run.cpp:112-145
+    with TextureBilinear, the RGB L2 loss and the in-graph Adam) written with
+    the graph API (tests/graph_tex.cpp) and run by DressiAD with the cameras
+    sent every step: the first iteration's loss and texture gradient bit for
+    bit against the oracle's texture fit, the later losses and the Adam state
+    within 1e-6 (the bias correction's device powf)."""
+    import opendressi_amd as od
+    w = od.TexWorkload("graph", 16, 8, 64, 32, 2, 3, 1e-2, 3, 7)
+    pos, uv, faces, mvps, gt, tex0 = od.make_tex_scene(w)
+    iters = 3
+    print(f"[graph tex] uv sphere 16x8, {w.views} views, {w.screen}px, tex {w.tex}, "
+          f"naive={naive}", flush=True)
+    nv, nf = len(pos), len(faces)
+    hdr = np.array([nv, nf, w.views, w.screen, w.tex, w.tex, iters, w.sets, 1 if naive else 0],
+                   np.uint32)
+    inp, out = tmp_path / "in.bin", tmp_path / "out.bin"
+    with open(inp, "wb") as f:
+        f.write(hdr.tobytes())
+        f.write(np.float32(w.lr).tobytes())
+        for a in (pos, uv, faces, mvps, gt, tex0):
+            f.write(np.ascontiguousarray(a, np.float32).tobytes())
+    res = subprocess.run([TEX_EXE, str(inp), str(out)], capture_output=True, text=True,
+                         timeout=120)
+    assert res.returncode == 0, res.stderr
+    print(" ", res.stdout.strip(), flush=True)
+    d = np.fromfile(out, np.float32)
+    t_n = w.tex * w.tex * 4
+    got = {}
+    o = 0
+    for k, cnt in (("tex", t_n), ("m", t_n), ("v", t_n), ("t", 1), ("loss", iters),
+                   ("grad0", t_n)):
+        got[k] = d[o:o + cnt]
+        o += cnt
+    assert o == d.size
+    ref = oracle.tex_fit(pos, uv, faces, mvps, w.screen, gt, tex0, lr=w.lr, iters=iters,
+                         want_images=False)
+    assert np.abs(got["grad0"]).max() > 0
+    assert np.array_equal(got["grad0"], ref["grad0"].reshape(-1)), \
+        f"grad0: max |d| {np.abs(got['grad0'] - ref['grad0'].reshape(-1)).max():.3g}"
+    assert got["loss"][0] == ref["loss"][0], (got["loss"], ref["loss"])
+    np.testing.assert_allclose(got["loss"], ref["loss"], rtol=1e-6, atol=0)
+    for k in ("tex", "m", "v"):
+        want = ref[k].reshape(-1)
+        np.testing.assert_allclose(got[k], want, rtol=0,
+                                   atol=1e-6 * max(1.0, np.abs(want).max()), err_msg=k)
+    assert got["t"][0] == iters
