@@ -23,9 +23,9 @@ CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libdressi_hip.so")
 SOURCES = ["runtime.hip", "raster.hip", "hsr.hip", "aa.hip", "tex.hip", "ds.hip", "ibl.hip", "pbr.hip",
            "graph.hip", "executor.hip", "builders.hip", "route.hip"]
-# host-only sources (the examples' asset and geometry helpers), built with g++; zlib is
-# linked for their deflate streams
-HOST_SOURCES = ["assets.cpp", "geometry.cpp"]
+# host-only sources (the examples' asset, geometry and PBR-graph helpers), built with g++;
+# zlib is linked for their deflate streams
+HOST_SOURCES = ["assets.cpp", "geometry.cpp", "pbr_graph.cpp"]
 HEADERS = ["internal.h", "dressi_math.h", "raster_core.h", "soft_clip.h", "hsr_chain.h",
            "aa_core.h", "plan.h", "ibl_core.h", "graph_ir.h", "route.h"]
 ARCH = os.environ.get("DRESSI_OFFLOAD_ARCH", "gfx950")
@@ -79,13 +79,13 @@ def build(verbose: bool = False) -> str:
 
 
 def build_graph_test(verbose: bool = False) -> str:
-    """The test programs (tests/graph_c1.cpp, graph_ops.cpp, graph_tex.cpp over the
+    """The test programs (tests/graph_c1.cpp, graph_ops.cpp, graph_tex.cpp, graph_pbr.cpp over the
     graph API, tests/assets_cli.cpp over the examples' helpers), linked
     against the library; plain C++ (those headers need no HIP headers)."""
     out_dir = os.path.join(ROOT, "tests", "_bin")
     os.makedirs(out_dir, exist_ok=True)
     exe = ""
-    for name in ("graph_c1", "graph_ops", "graph_tex", "assets_cli"):
+    for name in ("graph_c1", "graph_ops", "graph_tex", "graph_pbr", "assets_cli"):
         src = os.path.join(ROOT, "tests", name + ".cpp")
         exe = os.path.join(out_dir, name)
         cmd = ["g++", "-std=c++17", "-O2", "-ffp-contract=off", "-I", os.path.join(ROOT, "include"),

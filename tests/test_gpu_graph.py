@@ -234,3 +234,65 @@ def test_texture_example_graph_matches_oracle(tmp_path, oracle, naive):
         np.testing.assert_allclose(got[k], want, rtol=0,
                                    atol=1e-6 * max(1.0, np.abs(want).max()), err_msg=k)
     assert got["t"][0] == iters
+
+
+PBR_EXE = os.path.join(ROOT, "tests", "_bin", "graph_pbr")
+
+
+@pytest.mark.parametrize("naive", [False, True])
+def test_pbr_example_graph_matches_reference_fixture(tmp_path, golden, naive):
+    """The PBR material + environment fit's graph written with the graph API
+    and the examples' PBR graph builders (tests/graph_pbr.cpp over
+    dressi_examples/pbr_graph.h) and run by DressiAD, against the reference's
+    own outputs for the ico2 48 px 2-view scene: the first loss 1e-5, the
+    first-iteration albedo / mr / env gradients 1e-4 (relative to the largest
+    entry) and the parameters after the fixture's iterations 1e-3 absolute --
+    the bars of the fused PBR plan on the same fixture (the executor's
+    reductions and the device's atan2 / acos / pow round differently from the
+    reference's CPU evaluation)."""
+    g = golden("pbr_ico2_48px_2view_3it.npz")
+    keys = ("pos", "normal", "uv", "faces", "mvps", "frames", "light", "gt_albedo", "gt_mr",
+            "gt_env", "albedo0", "mr0", "env0")
+    a = {k: np.ascontiguousarray(g["in_" + k], np.float32) for k in keys}
+    iters = len(g["out_loss"])
+    th, tw = a["gt_albedo"].shape[:2]
+    eh, ew = a["gt_env"].shape[:2]
+    nv, nf, n = len(a["pos"]), len(a["faces"]), len(a["mvps"])
+    s, levels = int(g["in_screen"]), int(g["in_levels"])
+    print(f"[graph pbr] ico2 {s}px {n} views, tex {tw}x{th}, env {ew}x{eh}, naive={naive}",
+          flush=True)
+    hdr = np.array([nv, nf, n, s, tw, th, ew, eh, levels, iters, 1 if naive else 0], np.uint32)
+    inp, out = tmp_path / "in.bin", tmp_path / "out.bin"
+    with open(inp, "wb") as f:
+        f.write(hdr.tobytes())
+        f.write(np.float32(g["in_lr"]).tobytes())
+        for k in keys:
+            f.write(a[k].tobytes())
+    res = subprocess.run([PBR_EXE, str(inp), str(out)], capture_output=True, text=True,
+                         timeout=120)
+    assert res.returncode == 0, res.stderr
+    print(" ", res.stdout.strip(), flush=True)
+    d = np.fromfile(out, np.float32)
+    t_n, e_n = tw * th * 3, ew * eh * 3
+    got = {}
+    o = 0
+    for k, cnt in (("albedo", t_n), ("mr", t_n), ("env", e_n), ("t", 1), ("loss", iters),
+                   ("g_albedo0", t_n), ("g_mr0", t_n), ("g_env0", e_n)):
+        got[k] = d[o:o + cnt]
+        o += cnt
+    assert o == d.size
+    assert got["t"][0] == iters
+
+    def close(x, want, tol, what):
+        want = np.asarray(want, np.float64).reshape(-1)
+        diff = np.abs(x.astype(np.float64) - want).max()
+        m = float(np.abs(want).max())
+        assert m > 0, what
+        assert diff <= tol * m, f"{what}: max diff {diff:.3g} vs max {m:.3g} (tol {tol})"
+
+    close(got["loss"][:1], g["out_loss"][:1], 1e-5, "loss")
+    for k in ("g_albedo0", "g_mr0", "g_env0"):
+        close(got[k], g["out_" + k], 1e-4, k)
+    for k in ("albedo", "mr", "env"):
+        diff = float(np.abs(got[k].astype(np.float64) - g["out_" + k].reshape(-1)).max())
+        assert diff <= 1e-3, f"{k}: max diff {diff:.3g} (tol 1e-3)"
