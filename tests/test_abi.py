@@ -36,6 +36,38 @@ def test_library_exports_every_declared_symbol():
     assert set(L.EXPORTED) == _declared(), set(L.EXPORTED) ^ _declared()
 
 
+def _declared_example_helpers():
+    """(header, name) of every function declared at namespace scope in
+    include/dressi_examples/*.h (the examples' C++ helpers)."""
+    pat = re.compile(r"^(?!\s|#|struct|namespace|using|}|template|inline|enum|constexpr|static)"
+                     r"[A-Za-z_:<>,\s]*?\b([A-Z][A-Za-z0-9_]*)\(([^;{]*?)\)\s*(const)?\s*;", re.M)
+    out = set()
+    d = os.path.join(ROOT, "include", "dressi_examples")
+    for fn in sorted(os.listdir(d)):
+        text = open(os.path.join(d, fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        out |= {(fn, m.group(1)) for m in pat.finditer(text)}
+    return out
+
+
+def test_library_defines_every_example_helper():
+    """The examples' helper headers (asset, geometry and PBR-graph helpers)
+    are implemented in the library, not left to the example programs."""
+    import shutil
+    import subprocess
+    import opendressi_amd._lib as L
+    names = _declared_example_helpers()
+    assert {n for _, n in names} >= {"LoadObjMesh", "GenerateIcosphere", "BuildPbrShade",
+                                     "BuildPbrGBuffer", "BuildPbrIblMaps", "BuildPbrForward"}
+    if shutil.which("nm") is None:
+        pytest.skip("nm is not installed")
+    syms = subprocess.run(["nm", "-DC", "--defined-only", L.LIB_PATH], capture_output=True,
+                          text=True, check=True).stdout
+    missing = sorted(f"{h}: {n}" for h, n in names if f"dressi_examples::{n}(" not in syms)
+    assert not missing, missing
+
+
 def test_library_is_built_for_gfx950():
     import opendressi_amd._lib as L
     blob = open(L.LIB_PATH, "rb").read()
