@@ -239,18 +239,20 @@ def test_texture_example_graph_matches_oracle(tmp_path, oracle, naive):
 PBR_EXE = os.path.join(ROOT, "tests", "_bin", "graph_pbr")
 
 
-@pytest.mark.parametrize("naive", [False, True])
-def test_pbr_example_graph_matches_reference_fixture(tmp_path, golden, naive):
+@pytest.mark.parametrize("name,naive", [("pbr_ico2_48px_2view_3it.npz", False),
+                                        ("pbr_ico2_48px_2view_3it.npz", True),
+                                        ("pbr_ico3_96px_3view_2it.npz", False)])
+def test_pbr_example_graph_matches_reference_fixture(tmp_path, golden, name, naive):
     """The PBR material + environment fit's graph written with the graph API
     and the examples' PBR graph builders (tests/graph_pbr.cpp over
     dressi_examples/pbr_graph.h) and run by DressiAD, against the reference's
-    own outputs for the ico2 48 px 2-view scene: the first loss 1e-5, the
+    own outputs for the ico2 48 px 2-view and ico3 96 px 3-view scenes: the first loss 1e-5, the
     first-iteration albedo / mr / env gradients 1e-4 (relative to the largest
     entry) and the parameters after the fixture's iterations 1e-3 absolute --
     the bars of the fused PBR plan on the same fixture (the executor's
     reductions and the device's atan2 / acos / pow round differently from the
     reference's CPU evaluation)."""
-    g = golden("pbr_ico2_48px_2view_3it.npz")
+    g = golden(name)
     keys = ("pos", "normal", "uv", "faces", "mvps", "frames", "light", "gt_albedo", "gt_mr",
             "gt_env", "albedo0", "mr0", "env0")
     a = {k: np.ascontiguousarray(g["in_" + k], np.float32) for k in keys}
@@ -259,7 +261,7 @@ def test_pbr_example_graph_matches_reference_fixture(tmp_path, golden, naive):
     eh, ew = a["gt_env"].shape[:2]
     nv, nf, n = len(a["pos"]), len(a["faces"]), len(a["mvps"])
     s, levels = int(g["in_screen"]), int(g["in_levels"])
-    print(f"[graph pbr] ico2 {s}px {n} views, tex {tw}x{th}, env {ew}x{eh}, naive={naive}",
+    print(f"[graph pbr] {name}: {s}px {n} views, tex {tw}x{th}, env {ew}x{eh}, naive={naive}",
           flush=True)
     hdr = np.array([nv, nf, n, s, tw, th, ew, eh, levels, iters, 1 if naive else 0], np.uint32)
     inp, out = tmp_path / "in.bin", tmp_path / "out.bin"
