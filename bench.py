@@ -416,28 +416,80 @@ def bench_record(workload: str, path: str) -> None:
 
 
 def metric_point(name: str, steps: int, warmup: int) -> dict:
-    """Iterations/s of another silhouette workload (graph replays, inputs
-    resident), for the metric's other resolution points."""
+    """Iterations/s of another workload (graph replays, inputs resident):
+    the metric's other resolution points (c1, c2, c4) and the texture (c3)
+    and PBR / IBL (c5) fits, each with its iteration's fraction of the HBM
+    roofline; c5 adds its shading kernel's FP32 VALU fraction (from a short
+    eager profile, HIP events between the kernels)."""
     import opendressi_amd as od
-    w = od.WORKLOADS[name]
     ctx = od.Context(0)
-    fit = od.SilhouetteFit.from_workload(ctx, name)
+    extra = {}
+    if name in od.TEX_WORKLOADS:
+        w = od.TEX_WORKLOADS[name]
+        fit = od.TextureFit.from_workload(ctx, name)
+        nb = iteration_bytes_tex(fit.n_views, fit.screen, fit.n_faces, fit.n_verts,
+                                 fit.tex_w * fit.tex_h)
+        desc = (f"{name}: texture {w.screen}^2 x {w.views} views, UV sphere "
+                f"{w.stacks}x{w.slices}, {w.tex}^2 RGBA")
+    elif name in od.PBR_WORKLOADS:
+        w = od.PBR_WORKLOADS[name]
+        fit = od.PbrFit.from_workload(ctx, name)
+        nb = iteration_bytes_pbr(fit.n_views, fit.screen, fit.n_faces, fit.n_verts,
+                                 fit.tex_w * fit.tex_h, fit.env_w * fit.env_h)
+        desc = (f"{name}: PBR/IBL {w.screen}^2 x {w.views} views, icosphere L{w.level}, "
+                f"{fit.tex_w}^2 materials, {fit.env_w}x{fit.env_h} env")
+    else:
+        w = od.WORKLOADS[name]
+        fit = od.SilhouetteFit.from_workload(ctx, name)
+        nb = (iteration_bytes_aa if w.technique == "aa" else iteration_bytes)(
+            fit.n_views, fit.screen, fit.n_faces, fit.n_verts)
+        desc = (f"{name}: {'AA' if w.technique == 'aa' else 'HardSoftRas'} "
+                f"{w.screen}^2 x {w.views} views, icosphere L{w.level}")
     fit.step(warmup)
     ctx.synchronize()
     t0 = time.perf_counter()
     fit.step(steps)
     ctx.synchronize()
     dt = time.perf_counter() - t0
-    nb = (iteration_bytes_aa if w.technique == "aa" else iteration_bytes)(
-        fit.n_views, fit.screen, fit.n_faces, fit.n_verts)
+    its = steps / dt
+    if name in od.PBR_WORKLOADS:
+        prof = fit.profile(5)
+        g = fit.read(od._lib.PBR_GBUF0)
+        fg = g[..., 2] >= 0.0
+        env = ~fg & (g[..., 0] >= 0.0)
+        classes = {"fg": int(fg.sum()), "env": int(env.sum()),
+                   "none": int(g[..., 0].size - fg.sum() - env.sum())}
+        flops = kernel_flops_pbr(classes, 0.0)["k_pbr_shade"]
+        extra = {"k_pbr_shade_us": prof["k_pbr_shade"],
+                 "k_pbr_shade_valu_frac": flops / (prof["k_pbr_shade"] * 1e-6) / VALU_PEAK}
+    nviews, screen = fit.n_views, fit.screen
     fit.close()
     ctx.close()
-    its = steps / dt
-    return {"workload": f"{name}: {'AA' if w.technique == 'aa' else 'HardSoftRas'} "
-                        f"{w.screen}^2 x {w.views} views, icosphere L{w.level}",
-            "value": its, "unit": "iterations/s", "ms_per_step": 1e3 / its, "steps": steps,
-            "mpixels_per_s": w.views * w.screen * w.screen * its / 1e6,
-            "iteration_frac_of_hbm_peak": nb * its / HBM_PEAK}
+    return {"workload": desc, "value": its, "unit": "iterations/s", "ms_per_step": 1e3 / its,
+            "steps": steps, "mpixels_per_s": nviews * screen * screen * its / 1e6,
+            "iteration_frac_of_hbm_peak": nb * its / HBM_PEAK, **extra}
+
+
+def reference_cpu_c1() -> dict:
+    """The reference's own CPU evaluator (oracle/_ref: the reference's
+    src/core built in place, BuildBackward + CpuEvaluator with DressiAD's
+    copy-back; single-threaded, as the reference's evaluator is) on the whole
+    C1 fit: 256^2, 1 view, icosphere L3, 50 iterations. None when the
+    reference build is absent."""
+    import opendressi_amd as od
+    from oracle.pyoracle import REF_SO, Reference
+    if not os.path.exists(REF_SO):
+        return None
+    w = od.WORKLOADS["c1"]
+    pos, faces, tgt, mvps = od.make_scene(w)
+    t0 = time.perf_counter()
+    Reference().hsr_fit(pos, faces, tgt, faces, mvps, w.screen, lr=w.lr, iters=w.iters,
+                        want_images=False)
+    dt = time.perf_counter() - t0
+    return {"value": w.iters / dt, "unit": "iterations/s", "cores": 1, "kind": "reference",
+            "sample": (f"the whole c1 fit: {w.screen}^2 x 1 view, icosphere L{w.level}, "
+                       f"{w.iters} iterations in {dt:.1f} s (the static target raster "
+                       f"included); host CPU: {cpu_info()}, nproc {os.cpu_count()}")}
 
 
 def torch_surface(views: int = 8, screen: int = 256, level: int = 3, steps: int = 50,
@@ -640,13 +692,23 @@ def main() -> int:
         line["valu_rooflines"] = valu
     if args.workload == "c4_hsr" and not args.no_points:
         # the metric's 512^2 point and the AA technique at 2048^2
-        line["metric_points"] = {"c2": metric_point("c2", 400, 20),
-                                 "c4": metric_point("c4", 100, 10)}
+        line["metric_points"] = {"c1": metric_point("c1", 400, 20),
+                                 "c2": metric_point("c2", 400, 20),
+                                 "c3": metric_point("c3", 100, 10),
+                                 "c4": metric_point("c4", 100, 10),
+                                 "c5": metric_point("c5", 50, 5)}
     if args.torch_surface:
         line["torch_surface"] = torch_surface()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = (cpu_baseline_pbr(w) if pbr else
                                 cpu_baseline_tex(w) if tex else cpu_baseline(w))
+        if not (tex or pbr):
+            try:
+                ref = reference_cpu_c1()
+            except Exception as exc:  # the reference build is a baseline, not the product
+                ref = {"error": str(exc)}
+            if ref is not None:
+                line["cpu_baseline"]["reference_c1"] = ref
     print(json.dumps(line), flush=True)
     ctx.close()
     if args.bench_json:

@@ -66,6 +66,12 @@ void* dressi_ctx_stream(dressi_ctx* ctx);
 /* Waits for all work queued on the context stream (the reference's fence
  * wait, src/vk/executor.cpp:1020-1027). */
 int dressi_ctx_synchronize(dressi_ctx* ctx);
+/* Generation of the context's per-op workspaces: it changes whenever a call
+ * needs a larger workspace than the context holds and the old one is freed.
+ * Device addresses taken from the workspaces (e.g. captured into a hipGraph)
+ * are valid only while it stays the same. No reference counterpart (the
+ * reference's GpuPlan owns fixed images, src/vk/executor.h:16-38). */
+uint64_t dressi_ctx_workspace_generation(dressi_ctx* ctx);
 /* Device name (DressiAD::getDeviceName, include/dressi/dressi_ad.h:94-96). */
 int dressi_ctx_device_name(dressi_ctx* ctx, char* buf, size_t len);
 

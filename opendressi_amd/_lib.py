@@ -68,6 +68,7 @@ _SIGS = {
     "dressi_ctx_set_stream": (_I, [_P, _P]),
     "dressi_ctx_reset_stream": (_I, [_P]),
     "dressi_ctx_stream": (_P, [_P]),
+    "dressi_ctx_workspace_generation": (C.c_uint64, [_P]),
     "dressi_ctx_synchronize": (_I, [_P]),
     "dressi_ctx_device_name": (_I, [_P, C.c_char_p, _S]),
     "dressi_malloc": (_I, [_P, C.POINTER(_P), _S]),

@@ -695,6 +695,7 @@ struct DressiAD::Impl {
     bool plan_valid = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
+    uint64_t graph_ws_gen = 0;  // workspace generation the graph was captured at
     bool graph_failed = false;
     uint32_t eager_runs = 0;
     // transfers
@@ -1401,6 +1402,12 @@ struct DressiAD::Impl {
     }
 
     void execute() {
+        if (graph_exec && dressi_ctx_workspace_generation(ctx()) != graph_ws_gen) {
+            // a per-op call through context() regrew a workspace the graph
+            // holds: run eagerly (which re-sizes them) and capture again
+            release_graph();
+            eager_runs = 0;
+        }
         if (!graph_exec && !graph_failed && eager_runs >= 1 && !steps_capturable()) {
             graph_failed = true;
         }
@@ -1418,6 +1425,7 @@ struct DressiAD::Impl {
                 if (ok && e == hipSuccess && g &&
                     hipGraphInstantiate(&graph_exec, g, nullptr, nullptr, 0) == hipSuccess) {
                     graph = g;
+                    graph_ws_gen = dressi_ctx_workspace_generation(ctx());
                 } else {
                     if (g) {
                         hipGraphDestroy(g);

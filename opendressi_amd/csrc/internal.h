@@ -27,6 +27,9 @@ struct dressi_ctx {
     std::vector<size_t> ws_size;
     std::vector<hipStream_t> ws_stream;
     std::vector<hipEvent_t> ws_event;
+    // bumped whenever a slot is freed and reallocated: a captured hipGraph
+    // holding the old addresses is stale once this changes
+    uint64_t ws_generation = 0;
 };
 
 namespace dressi {

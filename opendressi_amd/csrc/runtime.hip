@@ -58,6 +58,7 @@ int ctx_workspace(dressi_ctx* ctx, int slot, size_t bytes, void** out) {
             DRESSI_TRY_HIP(hipFree(ctx->ws_ptr[slot]));
             ctx->ws_ptr[slot] = nullptr;
             ctx->ws_size[slot] = 0;
+            ctx->ws_generation++;
         }
         size_t sz = bytes < 256 ? 256 : bytes;
         DRESSI_TRY_HIP(hipMalloc(&ctx->ws_ptr[slot], sz));
@@ -167,6 +168,8 @@ int dressi_ctx_reset_stream(dressi_ctx* ctx) {
 }
 
 void* dressi_ctx_stream(dressi_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+uint64_t dressi_ctx_workspace_generation(dressi_ctx* ctx) { return ctx ? ctx->ws_generation : 0; }
 
 int dressi_ctx_synchronize(dressi_ctx* ctx) {
     DRESSI_REQUIRE(ctx, "NULL context");

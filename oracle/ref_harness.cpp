@@ -346,6 +346,15 @@ int refh_uv_sphere(uint32_t stacks, uint32_t slices, uint32_t* n_verts,
 //   out_grad0 {V,3}: d loss / d pos at iteration 0, out_pred0 {N,S,S},
 //   out_target {N,S,S}, out_rs0 {N,S,S,4}: RasterizeSoft at iteration 0,
 //   out_lossimg0 {S,S}.
+// Depth peels of the HardSoftRas graph built by refh_hsr_fit (the example's
+// --peels option, run.cpp:307); 1 unless set.
+static uint32_t g_peels = 1;
+
+int refh_set_peels(uint32_t peels) {
+    g_peels = peels < 1 ? 1 : peels;
+    return 0;
+}
+
 int refh_hsr_fit(const float* pos0, uint32_t n_verts, const float* faces,
                  uint32_t n_faces, const float* tgt_pos, uint32_t n_tverts,
                  const float* tgt_faces, uint32_t n_tfaces, const float* mvps,
@@ -431,17 +440,41 @@ int refh_hsr_fit(const float* pos0, uint32_t n_verts, const float* faces,
                 Variable dist = (inside * 2.f - 1.f) * dmin;
                 return mask * F::Sigmoid(dist * sigma_scale);
             };
+            // Alg. 2 depth peeling (run.cpp:302-343): peel k rejects
+            // fragments at or in front of peel k - 1's shifted depth
             Variable one_minus = one;
-            Variable rs = F::StopGradient(F::RasterizeSoft(
-                    soft_clip, s_face_id, s_faces_soft, clip_v, s_faces_f,
-                    s_vtx_faces, screen, radius_px));
-            rs_vars.push_back(rs);
-            Variable dist_c = F::GetX(rs);
-            Variable cov = F::GetW(rs);
-            Variable ge = F::Step(zero, dist_c);
-            Variable idx = (F::GetY(rs) + 1.f) * cov;
-            one_minus = one_minus * (1.f - soft_prob(idx));
-            Variable hard = cov * ge;
+            Variable prev_shift(nullptr);
+            Variable hard(nullptr);
+            for (uint32_t peel = 0; peel < g_peels; peel++) {
+                Variable rs = F::StopGradient(
+                        peel == 0 ? F::RasterizeSoft(soft_clip, s_face_id,
+                                                     s_faces_soft, clip_v,
+                                                     s_faces_f, s_vtx_faces,
+                                                     screen, radius_px)
+                                  : F::RasterizeSoft(soft_clip, s_face_id,
+                                                     s_faces_soft, clip_v,
+                                                     s_faces_f, s_vtx_faces,
+                                                     prev_shift, screen,
+                                                     radius_px));
+                if (peel == 0) {
+                    rs_vars.push_back(rs);
+                }
+                Variable dist_c = F::GetX(rs);
+                Variable cov = F::GetW(rs);
+                Variable ge = F::Step(zero, dist_c);
+                prev_shift =
+                        cov * (ge * (F::Clamp(F::GetZ(rs), zero, one) * 0.5f) +
+                               (1.f - ge) *
+                                       (F::Clamp(-dist_c * (1.f / radius_px),
+                                                 zero, one) *
+                                                0.5f +
+                                        0.5f));
+                Variable idx = (F::GetY(rs) + 1.f) * cov;
+                one_minus = one_minus * (1.f - soft_prob(idx));
+                if (peel == 0) {
+                    hard = cov * ge;
+                }
+            }
             Variable soft_sil = 1.f - one_minus;
             return F::Max(hard, soft_sil);
         };

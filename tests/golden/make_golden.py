@@ -7,6 +7,7 @@ and stored next to the outputs, so the fixtures are self-contained data.
     python tests/golden/make_golden.py texture    # the texture path's only
     python tests/golden/make_golden.py dist       # GatherDistGrad's only
     python tests/golden/make_golden.py pbr        # the PBR / IBL path's only
+    python tests/golden/make_golden.py peels      # the depth-peeled fits' only
 
 Each .npz holds `in_*` arrays (inputs) and `out_*` arrays (reference outputs).
 """
@@ -353,6 +354,20 @@ def pbr_fit_fixture(o, r, name, level, screen, views, tex, ew, eh, iters, seed, 
     print("wrote", name, {k: v.shape for k, v in arrs.items()})
 
 
+def peel_main(o, r):
+    """HardSoftRas fits with K = 2 and 3 depth peels (the example's --peels,
+    examples/silhouette_optimization/run.cpp:302-343): ico3, 2 orbit views,
+    96 px, 3 iterations, from the reference build with the peel loop."""
+    import ctypes as C
+    for k in (2, 3):
+        r.fn("set_peels")(C.c_uint32(k))
+        try:
+            fit_fixture(o, r, f"hsr_peel{k}_ico3_2view_96px_3it.npz", 3, 0.05, 3,
+                        orbit_mvps(o, 2), 96, 3, 1e-3, True)
+        finally:
+            r.fn("set_peels")(C.c_uint32(1))
+
+
 def pbr_main(o, r):
     ibl_fixtures(o, r)
     pbr_fit_fixture(o, r, "pbr_ico2_48px_2view_3it.npz", 2, 48, 2, 16, 64, 32, 3, 41, True)
@@ -371,7 +386,11 @@ def main():
     if sys.argv[1:] == ["dist"]:
         ds_fixtures(o, r)
         return
+    if sys.argv[1:] == ["peels"]:
+        peel_main(o, r)
+        return
     ds_fixtures(o, r)
+    peel_main(o, r)
     pbr_main(o, r)
     texture_main(o, r)
     op_fixtures(o, r)

@@ -8,17 +8,26 @@
 //
 //   graph_c1 <in.bin> <out.bin>
 // in.bin:  u32 V, F, Vt, Ft, N, S, samples, iters, technique (0 hardsoftras,
-//          1 aa), packing (0 RSP, 1 Naive), regs (0 none, 1 regulariser terms);
+//          1 aa), packing (0 RSP, 1 Naive), regs (0 none, 1 regulariser terms),
+//          peels (HardSoftRas depth peels, >= 1: run.cpp:302-343),
+//          rebuild (0 the default reactive rebuild counts, 1
+//          setRebuildCounts(0, 0)), regrow (1: after the third step, a
+//          per-op call through DressiAD::context() that needs larger
+//          workspaces than the graph's);
 //          f32 radius, lr, laplacian weight, normal weight;
 //          pos0 {V,3}, faces {F,3}, tgt_pos {Vt,3}, tgt_faces {Ft,3}, mvps N x 16
 // out.bin: pos, m, v {V,3}, t, loss[iters] (sum of the loss image),
-//          grad0 {V,3} (first iteration), preds and targets {N,S,S} (last)
+//          grad0 {V,3} (first iteration), preds and targets {N,S,S} (last),
+//          kernels[iters] (getSubStageCount() after each step), ms[iters]
+//          (each step's wall time, upload + step + loss download)
 // stdout:  "graph_c1: plan=<name> stages=<n> substages=<n> funcs=<n>"
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <vector>
 
 #include "dressi/dressi.h"
+#include "dressi_hip.h"
 #include "dressi/mesh_utils.h"
 #include "dressi_examples/geometry_utils.h"
 
@@ -69,15 +78,18 @@ int main(int argc, char** argv) {
         if (!fi) {
             throw DressiError("cannot open input");
         }
-        uint32_t hdr[11];
+        uint32_t hdr[14];
         float fp[4];
-        get(fi, hdr, 11);
+        get(fi, hdr, 14);
         get(fi, fp, 4);
         const uint32_t n_verts = hdr[0], n_faces = hdr[1], n_tverts = hdr[2], n_tfaces = hdr[3];
         const uint32_t n_views = hdr[4], S = hdr[5], samples = hdr[6], iters = hdr[7];
         const bool hardsoft = hdr[8] == 0;
         const bool naive = hdr[9] == 1;
         const bool regs = hdr[10] == 1;
+        const uint32_t peels = hdr[11] < 1 ? 1 : hdr[11];
+        const bool no_rebuild = hdr[12] == 1;
+        const bool regrow = hdr[13] == 1;
         const float radius_px = fp[0], lr = fp[1], w_lap = fp[2], w_nrm = fp[3];
         std::vector<float> pos0(n_verts * 3), faces(n_faces * 3), tgt_pos(n_tverts * 3),
                 tgt_faces(n_tfaces * 3), mvps(n_views * 16);
@@ -166,16 +178,30 @@ int main(int argc, char** argv) {
                 Variable dist = (inside * 2.f - 1.f) * dmin;
                 return mask * F::Sigmoid(dist * sigma_scale);
             };
+            // Alg. 2 depth peeling: peel k rejects fragments at or in front of
+            // peel k - 1's shifted depth; Eq. 6: 1 - prod_k (1 - D_k)
             Variable one_minus = one;
-            Variable rs = F::StopGradient(F::RasterizeSoft(soft_clip, s_face_id, s_faces_soft,
-                                                           clip_v, s_faces_f, s_vtx_faces, screen,
-                                                           radius_px));
-            Variable dist_c = F::GetX(rs);
-            Variable cov = F::GetW(rs);
-            Variable ge = F::Step(zero, dist_c);
-            Variable idx = (F::GetY(rs) + 1.f) * cov;
-            one_minus = one_minus * (1.f - soft_prob(idx));
-            Variable hard = cov * ge;
+            Variable prev_shift(nullptr);
+            Variable hard(nullptr);
+            for (uint32_t peel = 0; peel < peels; peel++) {
+                Variable rs = F::StopGradient(
+                        peel == 0 ? F::RasterizeSoft(soft_clip, s_face_id, s_faces_soft, clip_v,
+                                                     s_faces_f, s_vtx_faces, screen, radius_px)
+                                  : F::RasterizeSoft(soft_clip, s_face_id, s_faces_soft, clip_v,
+                                                     s_faces_f, s_vtx_faces, prev_shift, screen,
+                                                     radius_px));
+                Variable dist_c = F::GetX(rs);
+                Variable cov = F::GetW(rs);
+                Variable ge = F::Step(zero, dist_c);
+                prev_shift = cov * (ge * (F::Clamp(F::GetZ(rs), zero, one) * 0.5f) +
+                                    (1.f - ge) * (F::Clamp(-dist_c * (1.f / radius_px), zero,
+                                                           one) * 0.5f + 0.5f));
+                Variable idx = (F::GetY(rs) + 1.f) * cov;
+                one_minus = one_minus * (1.f - soft_prob(idx));
+                if (peel == 0) {
+                    hard = cov * ge;
+                }
+            }
             Variable soft_sil = 1.f - one_minus;
             return F::Max(hard, soft_sil);
         };
@@ -204,6 +230,9 @@ int main(int argc, char** argv) {
 
         DressiAD ad;
         ad.setPackingMode(naive ? DressiAD::PackingMode::Naive : DressiAD::PackingMode::RSP);
+        if (no_rebuild) {
+            ad.setRebuildCounts(0, 0);
+        }
         ad.setLossVar(loss);
         bool state_registered = false;
         ad.setOptimizer([&](Variables xs, Variables gxs) {
@@ -280,14 +309,50 @@ int main(int argc, char** argv) {
         // iterations: the starting positions go with the first step; every
         // step returns its loss image with the same synchronisation
         const CpuImage pos_img = Image(pos0, n_verts, 1, 3);
-        std::vector<float> losses(iters);
+        std::vector<float> losses(iters), kernels(iters), step_ms(iters);
         CpuImage grad0;
         for (uint32_t it = 0; it < iters; it++) {
             std::vector<std::pair<Variable, CpuImageView>> sends;
             if (it == 0) {
                 sends.emplace_back(pos, CpuImageView(pos_img));
             }
+            if (regrow && it == 3) {
+                // a per-op call on the instance's own C-ABI context whose
+                // screen needs larger tile bins than any step so far
+                dressi_ctx* c = ad.context();
+                const uint32_t big = 4 * S + 64;
+                std::vector<float> clip(n_verts * 4, 0.f);
+                for (uint32_t i = 0; i < n_verts; i++) {
+                    clip[i * 4 + 0] = pos0[i * 3 + 0] * 0.5f;
+                    clip[i * 4 + 1] = pos0[i * 3 + 1] * 0.5f;
+                    clip[i * 4 + 2] = 0.5f;
+                    clip[i * 4 + 3] = 1.f;
+                }
+                void *d_clip = nullptr, *d_faces = nullptr, *d_ones = nullptr, *d_out = nullptr;
+                const std::vector<float> ones(n_verts, 1.f);
+                if (dressi_malloc(c, &d_clip, clip.size() * 4) ||
+                    dressi_malloc(c, &d_faces, faces.size() * 4) ||
+                    dressi_malloc(c, &d_ones, ones.size() * 4) ||
+                    dressi_malloc(c, &d_out, size_t(big) * big * 4) ||
+                    dressi_memcpy_h2d(c, d_clip, clip.data(), clip.size() * 4) ||
+                    dressi_memcpy_h2d(c, d_faces, faces.data(), faces.size() * 4) ||
+                    dressi_memcpy_h2d(c, d_ones, ones.data(), ones.size() * 4) ||
+                    dressi_rasterize(c, (const float*)d_clip, n_verts, (const float*)d_ones, 1,
+                                     (const float*)d_faces, n_faces, big, big, (float*)d_out) ||
+                    dressi_ctx_synchronize(c)) {
+                    throw DressiError(std::string("regrow call: ") + dressi_last_error());
+                }
+                dressi_free(c, d_clip);
+                dressi_free(c, d_faces);
+                dressi_free(c, d_ones);
+                dressi_free(c, d_out);
+            }
+            const auto t0 = std::chrono::steady_clock::now();
             const CpuImage li = ad.execStepWithSendsAndRecvImgsStacked(sends, {loss});
+            step_ms[it] = std::chrono::duration<float, std::milli>(
+                                  std::chrono::steady_clock::now() - t0)
+                                  .count();
+            kernels[it] = float(ad.getSubStageCount());
             double s = 0.0;
             for (float x : li.data) {
                 s += x;
@@ -311,6 +376,8 @@ int main(int argc, char** argv) {
         fwrite(grad0.data.data(), sizeof(float), grad0.data.size(), fo);
         fwrite(pred_img.data.data(), sizeof(float), pred_img.data.size(), fo);
         fwrite(tgt_img.data.data(), sizeof(float), tgt_img.data.size(), fo);
+        fwrite(kernels.data(), sizeof(float), kernels.size(), fo);
+        fwrite(step_ms.data(), sizeof(float), step_ms.size(), fo);
         fclose(fo);
         printf("graph_c1: plan=%s stages=%zu substages=%zu funcs=%zu device=%s\n",
                ad.getPlanName().c_str(), ad.getStageCount(), ad.getSubStageCount(),

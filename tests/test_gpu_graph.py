@@ -32,10 +32,12 @@ GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
 def _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, radius, lr, aa=False,
-               naive=False, regs=False, w_lap=0.0, w_nrm=0.0, timeout=120):
+               naive=False, regs=False, w_lap=0.0, w_nrm=0.0, peels=1, no_rebuild=False,
+               regrow=False, timeout=120):
     nv, nf, n = len(pos), len(faces), len(mvps)
     hdr = np.array([nv, nf, len(tgt), nf, n, screen, samples, iters, 1 if aa else 0,
-                    1 if naive else 0, 1 if regs else 0], np.uint32)
+                    1 if naive else 0, 1 if regs else 0, peels, 1 if no_rebuild else 0,
+                    1 if regrow else 0], np.uint32)
     inp = tmp_path / "in.bin"
     out = tmp_path / "out.bin"
     with open(inp, "wb") as f:
@@ -57,7 +59,7 @@ def _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, radius, 
          "funcs": int(m.group(4))}
     for k, cnt in (("pos", nv * 3), ("m", nv * 3), ("v", nv * 3), ("t", 1), ("loss", iters),
                    ("grad0", nv * 3), ("pred", n * screen * screen),
-                   ("target", n * screen * screen)):
+                   ("target", n * screen * screen), ("kernels", iters), ("ms", iters)):
         r[k] = d[o:o + cnt]
         o += cnt
     assert o == d.size
@@ -162,6 +164,78 @@ def test_example_with_zero_regulariser_weights_takes_the_route(tmp_path, oracle)
     want = _fit(oracle, False, pos, faces, tgt, mvps, screen, samples, lr, iters, images=False)
     for k in ("pos", "m", "v", "loss", "grad0"):
         assert np.array_equal(g[k], want[k]), k
+
+
+@pytest.mark.parametrize("peels", [2, 3])
+def test_depth_peels_through_dressi_ad(tmp_path, peels):
+    """The example's --peels K graph (run.cpp:302-343: K RasterizeSoft layers,
+    each rejecting fragments at or in front of the previous layer's shifted
+    depth, Eq. 6 composition) through DressiAD, against the reference build's
+    own fit (tests/golden/hsr_peel<K>_*.npz): the first iteration's loss and
+    gradient bit for bit, the predictions and targets bit for bit, the later
+    iterations within 1e-6 (device powf in the in-graph Adam)."""
+    with np.load(os.path.join(GOLDEN, f"hsr_peel{peels}_ico3_2view_96px_3it.npz")) as z:
+        gold = {k: z[k] for k in z.files}
+    screen, iters = int(gold["in_cfg"][0]), int(gold["in_cfg"][1])
+    print(f"[graph] peels {peels}: ico3, 2 views, {screen}px, {iters} iterations, RSP",
+          flush=True)
+    g = _run_graph(tmp_path, gold["in_pos"], gold["in_faces"], gold["in_tgt_pos"],
+                   gold["in_mvps"], screen, 8, iters, 3.0, 1e-3, peels=peels)
+    assert g["plan"] == "generic"
+    assert np.array_equal(g["grad0"], gold["out_grad0"]), \
+        f"grad0 differs: max {np.abs(g['grad0'] - gold['out_grad0']).max():.3g}"
+    assert g["loss"][0] == gold["out_loss"][0], (g["loss"], gold["out_loss"])
+    np.testing.assert_allclose(g["loss"], gold["out_loss"], rtol=1e-6, atol=0)
+    for k in ("pos", "m", "v"):
+        np.testing.assert_allclose(g[k], gold["out_" + k], rtol=0,
+                                   atol=1e-6 * max(1.0, np.abs(gold["out_" + k]).max()),
+                                   err_msg=k)
+    assert np.array_equal(g["target"], gold["out_target"])
+    one = _run_graph(tmp_path, gold["in_pos"], gold["in_faces"], gold["in_tgt_pos"],
+                     gold["in_mvps"], screen, 8, 1, 3.0, 1e-3, peels=1)
+    assert not np.array_equal(one["grad0"], g["grad0"])  # the extra layers count
+
+
+def test_reactive_cache_prunes_static_branches(tmp_path, oracle):
+    """Reactive rebuilds (src/pack/reactive.cpp:10-68, driven from
+    src/dressi_ad.cpp:287-308,363-372): with the default counts the per-step
+    kernel count falls after the fast rebuild (2 steps with the same dirty
+    pattern) and again after the full rebuild (8), as the static target
+    branch is served from its cached images; every loss and the final
+    parameters equal a run with setRebuildCounts(0, 0), which never prunes."""
+    _, pos, faces, tgt, mvps = _scene("c1", 2)
+    iters, samples, lr, screen = 12, 8, 1e-3, 96
+    print("[graph] reactive rebuilds: c1 mesh, 2 views, 96px, 12 iterations, Naive", flush=True)
+    g = _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, 3.0, lr, naive=True)
+    flat = _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, 3.0, lr,
+                      naive=True, no_rebuild=True)
+    k, kf = g["kernels"].astype(int), flat["kernels"].astype(int)
+    print("kernels per step:", list(k), "without rebuilds:", list(kf), flush=True)
+    assert len(set(kf)) == 1, kf
+    assert k[0] == kf[0]
+    assert k[-1] < k[0], k
+    assert (np.diff(k) <= 0).all(), k
+    for key in ("pos", "m", "v", "loss", "grad0", "pred", "target"):
+        assert np.array_equal(g[key], flat[key]), key
+    want = _fit(oracle, False, pos, faces, tgt, mvps, screen, samples, lr, 1, images=False)
+    assert np.array_equal(g["grad0"], want["grad0"])
+
+
+def test_captured_graph_survives_workspace_regrow(tmp_path):
+    """A per-op C-ABI call through DressiAD::context() that needs larger
+    workspaces than the captured step graph frees and reallocates them; the
+    next execStep notices the new workspace generation, runs eagerly and
+    captures again, so the results equal a run without that call."""
+    _, pos, faces, tgt, mvps = _scene("c1", 1)
+    iters, samples, lr, screen = 6, 8, 1e-3, 96
+    print("[graph] workspace regrow through context(): c1 mesh, 96px, 6 iterations, Naive",
+          flush=True)
+    g = _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, 3.0, lr, naive=True,
+                   regrow=True)
+    base = _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, 3.0, lr,
+                      naive=True)
+    for key in ("pos", "m", "v", "loss", "grad0", "pred", "target"):
+        assert np.array_equal(g[key], base[key]), key
 
 
 @pytest.mark.parametrize("name", ["c2", "c4"])
