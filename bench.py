@@ -116,27 +116,38 @@ def iteration_bytes_pbr(n_views: int, s: int, n_faces: int, n_verts: int, texels
 
 
 def kernel_bytes_pbr(n_views: int, s: int, texels: int, env_texels: int, pooled: int,
-                     map_texels: int) -> dict:
+                     map_texels: int, gather_maps: list) -> dict:
     """Algorithmic bytes per launch of the PBR-plan kernels.
 
-    pool:      env read (12 B/texel), pooled sources written (12 B/texel)
-    conv_fwd:  pooled sources read, irradiance + prefilter maps written
-    shade:     per pixel and view the target RGB (12 B) and the G-buffer the
-               shading needs (material uv, normal, position: 16 B packed):
-               28 B; its per-pixel material gradient is counted in tex_adam
-    resolve:   map gradients (24 B/texel in, 12 B out)
-    conv_bwd:  map gradients read, source gradients written
-    env_adam:  background gradient, source gradients, env + m + v in and out
-    tex_adam:  per-pixel material gradients (20 B/pixel) gathered once,
-               albedo + mr with their Adam state in and out (96 B/texel)
-    loss:      one partial per workgroup
+    pool:       env read (12 B/texel), pooled sources written (12 B/texel)
+    conv_fwd:   pooled sources read, irradiance + prefilter maps written
+    shade:      per pixel and view the target RGB (12 B) and the G-buffer the
+                shading needs (material uv, normal, position: 16 B packed):
+                28 B; its per-pixel material gradient is counted in tex_adam
+    map_gather: per pixel and view its two uv pairs (16 B) and its two
+                map-gradient seeds (32 B) read; per (map, view, band, texel)
+                one 16 B partial written
+    tile_sum:   per map with bands > 1: the band partials read, one 16 B
+                sum per (view, texel) written
+    view_sum:   per map texel the views' sums read, one 16 B gradient written
+    conv_bwd:   map gradients read, source gradients written
+    env_adam:   background gradient, source gradients, env + m + v in and out
+    tex_adam:   per-pixel material gradients (20 B/pixel) gathered once,
+                albedo + mr with their Adam state in and out (96 B/texel)
+    loss:       one partial per workgroup
     """
     n, S2, T, E = n_views, float(s) * s, float(texels), float(env_texels)
+    band_texels = sum(float(w * h * k) for w, h, k in gather_maps)
+    split_texels = sum(float(w * h * k) for w, h, k in gather_maps if k > 1)
+    split_maps = sum(float(w * h) for w, h, k in gather_maps if k > 1)
+    all_maps = sum(float(w * h) for w, h, _ in gather_maps)
     return {
         "k_pbr_pool": 12.0 * E + 12.0 * pooled,
         "k_pbr_conv_fwd": 12.0 * pooled + 12.0 * map_texels,
         "k_pbr_shade": n * 28.0 * S2,
-        "k_pbr_resolve": 36.0 * map_texels,
+        "k_pbr_map_gather": n * 48.0 * S2 + 16.0 * n * band_texels,
+        "k_pbr_tile_sum": 16.0 * n * (split_texels + split_maps),
+        "k_pbr_view_sum": 16.0 * (n + 1) * all_maps,
         "k_pbr_conv_bwd": 12.0 * map_texels + 12.0 * pooled,
         "k_pbr_env_adam": 24.0 * E + 72.0 * E,
         "k_pbr_tex_adam": n * 20.0 * S2 + 96.0 * T,
@@ -607,7 +618,8 @@ def main() -> int:
     dom_us = prof[dom]
     if pbr:
         texels, envt = fit.tex_w * fit.tex_h, fit.env_w * fit.env_h
-        kbytes = kernel_bytes_pbr(nviews, s, texels, envt, fit.pooled_texels, fit.map_texels)
+        kbytes = kernel_bytes_pbr(nviews, s, texels, envt, fit.pooled_texels, fit.map_texels,
+                                  fit.gather_maps)
         ibytes = iteration_bytes_pbr(nviews, s, nf, nv, texels, envt)
         desc = (f"{w.name}: PBR/IBL material + env fit, {s}x{s} x {nviews} views, icosphere "
                 f"L{w.level} ({nv} v / {nf} f) with equirect uv, {fit.tex_w}x{fit.tex_h} albedo "

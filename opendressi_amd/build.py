@@ -27,7 +27,8 @@ SOURCES = ["runtime.hip", "raster.hip", "hsr.hip", "aa.hip", "tex.hip", "ds.hip"
 # zlib is linked for their deflate streams
 HOST_SOURCES = ["assets.cpp", "geometry.cpp", "pbr_graph.cpp"]
 HEADERS = ["internal.h", "dressi_math.h", "raster_core.h", "soft_clip.h", "hsr_chain.h",
-           "aa_core.h", "plan.h", "ibl_core.h", "graph_ir.h", "route.h"]
+           "aa_core.h", "plan.h", "ibl_core.h", "graph_ir.h", "route.h", "libm_f32.h",
+           "libm_pow5_table.h"]
 ARCH = os.environ.get("DRESSI_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [
@@ -98,6 +99,18 @@ def build_graph_test(verbose: bool = False) -> str:
             sys.stderr.write(res.stdout + res.stderr)
             raise RuntimeError(f"g++ failed building tests/_bin/{name}")
         os.replace(exe + ".tmp", exe)
+    # the host build of the library's C-library-exact float functions
+    # (csrc/libm_f32.h), checked against the host C library by tests/test_libm.py
+    exe = os.path.join(out_dir, "libm_check")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-ffp-contract=off",
+           "-o", exe + ".tmp", os.path.join(ROOT, "tests", "libm_check.cpp")]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("hipcc failed building tests/_bin/libm_check")
+    os.replace(exe + ".tmp", exe)
     return out_dir
 
 

@@ -38,6 +38,7 @@
 
 #include "graph_ir.h"
 #include "internal.h"
+#include "libm_f32.h"
 #include "route.h"
 
 namespace dressi {
@@ -178,9 +179,9 @@ __device__ void ew_eval(Op op, uint32_t n_in, const uint32_t* nc, float (*v)[4],
             case Op::kCos: r = cosf(a); break;
             case Op::kTan: r = tanf(a); break;
             case Op::kAsin: r = asinf(a); break;
-            case Op::kAcos: r = acosf(a); break;
-            case Op::kAtan: r = atanf(a); break;
-            case Op::kAtan2: r = atan2f(a, b); break;
+            case Op::kAcos: r = libm::acosf(a); break;
+            case Op::kAtan: r = libm::atanf(a); break;
+            case Op::kAtan2: r = libm::atan2f(a, b); break;
             case Op::kExp: r = libc_expf(a); break;
             case Op::kExp2: r = exp2f(a); break;
             case Op::kLog: r = logf(a); break;
@@ -192,7 +193,7 @@ __device__ void ew_eval(Op op, uint32_t n_in, const uint32_t* nc, float (*v)[4],
             case Op::kFloor: r = floorf(a); break;
             case Op::kFract: r = a - floorf(a); break;
             case Op::kMod: r = a - b * floorf(a / b); break;
-            case Op::kPow: r = powf(a, b); break;
+            case Op::kPow: r = (b == 5.f && a >= 0.f && a <= 1.f) ? libm::pow5f(a) : powf(a, b); break;
             case Op::kMax: r = std_max(a, b); break;
             case Op::kMin: r = std_min(a, b); break;
             case Op::kClamp: r = std_min(std_max(a, b), t); break;

@@ -286,7 +286,7 @@ __global__ __launch_bounds__(64) void k_brdf_lut(int w, int h, const float4* smp
             const float g = g1_ibl(ndv, k) * g1_ibl(nol, k);
             const float nd = noh * ndv;
             const float gv = g * voh / (nd > 1e-8f ? nd : 1e-8f);
-            const float fc = (float)pow((double)(1.f - voh), 5.0);
+            const float fc = libm::pow5f(1.f - voh);
             a += (1.f - fc) * gv;
             b += fc * gv;
         }

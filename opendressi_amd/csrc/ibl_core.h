@@ -7,8 +7,8 @@
 // them: the roughness-0 prefilter kernel turns a one-ulp change of a
 // direction into a ~1e-2 change of its peak weight, so these tables must be
 // the reference's bits. Per-pixel directions (normals, reflections, view
-// rays) are mapped to uv on the device with atan2 / acos evaluated in double
-// and rounded once.
+// rays) are mapped to uv on the device with atan2f / acosf that return what
+// the host C library returns (libm_f32.h).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -16,6 +16,8 @@
 #include <cmath>
 #include <cstdint>
 #include <vector>
+
+#include "libm_f32.h"
 
 namespace dressi {
 
@@ -82,8 +84,8 @@ __device__ __forceinline__ V3f normalize3(V3f v) {
 // EquirectUvFromDir (ibl_math.h:41-46) for a unit direction
 __device__ __forceinline__ void equirect_uv(V3f d, float* u, float* v) {
     const float y = d.y < -1.f ? -1.f : (d.y > 1.f ? 1.f : d.y);
-    *u = (float)atan2((double)d.z, (double)d.x) * kIblInvTwoPi + 0.5f;
-    *v = (float)acos((double)y) * kIblInvPi;
+    *u = libm::atan2f(d.z, d.x) * kIblInvTwoPi + 0.5f;
+    *v = libm::acosf(y) * kIblInvPi;
 }
 
 // EquirectSample's direction handling (f_ops.cpp:2946-2958): false for a

@@ -8,23 +8,34 @@
 //
 // Geometry is static, so everything the shading derives from it alone --
 // the G-buffer, n.v / n.l / n.h, the Schlick powers, the equirect uv of the
-// normal, the reflection and the background ray, and the texture gather's
-// inverse-UV windows -- is computed once per view at set-up; an iteration
-// reads those per-pixel terms, the material taps and the maps.
+// normal, the reflection and the background ray, the texture gather's
+// inverse-UV windows, the map-gradient gather lists and the convolution
+// weights -- is computed once at set-up; an iteration reads those, the
+// material taps and the maps.
 //
-// One iteration, 7 kernels + the pooling chain (ceil(log2) levels):
-//   k_pbr_pool      env -> pooled sources of the irradiance / prefilter maps
-//                   (the first level also clears the gradient accumulators)
-//   k_pbr_conv_fwd  IrradianceConv + every PrefilterConv level
-//   k_pbr_shade     per pixel: forward, L1 loss, backward; material
-//                   gradients per pixel, map gradients scattered into
-//                   64-bit fixed-point accumulators (workgroup windows in LDS)
-//   k_pbr_resolve   fixed point -> float map gradients
-//   k_pbr_conv_bwd  the convolutions' transposes onto the pooled sources
-//   k_pbr_env_adam  pooling VJPs + background gradient, Adam on the env
-//   k_pbr_tex_adam  GatherByInverseUVBilinear as a static gather list per
-//                   texel, Adam on albedo and mr
-//   k_pbr_loss      the loss scalar, t + 1
+// Every floating-point sum is formed in the reference evaluator's order, so
+// the fit reproduces its results bit for bit: the convolutions and their
+// transposes add over source / map texels in raster order
+// (f_ops.cpp:2970-3348), each EquirectSample VJP adds per band of dir rows in
+// pixel order and then the bands in order (EquirectSampleBwd + TileSum,
+// f_ops.cpp:2785-2919), views are added in view order, and the texture
+// gather adds each view's window sum in view order.
+//
+// One iteration, 10 kernels + the pooling chain (ceil(log2) levels):
+//   k_pbr_pool        env -> pooled sources of the irradiance / prefilter maps
+//   k_pbr_conv_fwd    IrradianceConv + every PrefilterConv level (static
+//                     weight matrices, one wave per colour channel)
+//   k_pbr_shade       per pixel: forward, L1 loss, backward; material
+//                     gradients and the map-gradient seeds per pixel
+//   k_pbr_map_gather  per (map, view, band, texel): the band's partial of the
+//                     EquirectSample VJP from a static list of (pixel, tap)
+//   k_pbr_tile_sum    per (map, view, texel): the bands' partials in order
+//   k_pbr_view_sum    per map texel: the views' sums in order
+//   k_pbr_conv_bwd    the convolutions' transposes onto the pooled sources
+//   k_pbr_env_adam    pooling VJPs + background gradient, Adam on the env
+//   k_pbr_tex_adam    GatherByInverseUVBilinear as a static gather list per
+//                     texel (per-view sums), Adam on albedo and mr
+//   k_pbr_loss        the loss scalar, t + 1
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -33,6 +44,8 @@
 #include <cstdint>
 #include <cstdio>
 #include <vector>
+
+#include <hipcub/hipcub.hpp>
 
 #include "dressi_hip.h"
 #include "ibl_core.h"
@@ -45,14 +58,40 @@ namespace {
 constexpr uint32_t kPbrMaxLevels = 8;
 constexpr uint32_t kPbrMaxViews = 16;
 constexpr uint32_t kPbrMaxPool = 12;
-constexpr int kConvOuts = 16;     // outputs per convolution workgroup
-constexpr int kShadeTile = 16;    // 16 x 16 pixel tile per shading workgroup
-constexpr int kWin = 64;          // texels per LDS scatter window
-constexpr uint32_t kIrrLevel = 0xffffffffu;
-constexpr uint32_t kStripes = 32;  // copies of the irradiance / prefilter accumulators
+constexpr uint32_t kPbrMaxMaps = kPbrMaxLevels + 2;
+constexpr int kShadeTile = 16;       // 16 x 16 pixel tile per shading workgroup
+constexpr uint32_t kTileSumLds = 4096;  // float4 partials staged per tile-sum round
+constexpr uint32_t kGatherChunk = 1024;  // map gather: positions staged per round
+constexpr uint32_t kGatherChains = 256;   // map gather: buckets per workgroup (1 per thread)
+constexpr uint32_t kGatherBands = 64;     // map gather: bands per workgroup
 
-struct PbrGroup {
-    uint32_t first, count, level;  // level kIrrLevel: the irradiance map
+// One sampled map of the shading and its EquirectSample VJP's layout: the
+// VJP adds, per view, k partial maps over bands of `rows` dir rows each
+// (EquirectSampleBwd, f_ops.cpp:2823-2919: k doubles until w h k >= 65536 or
+// k reaches the dir image's height) and sums them in band order (TileSum).
+// Buckets: (view, band, texel) of the map, from `bucket0`; the view sums sit
+// in `tot` from `tot0` (view, texel).
+struct MapInfo {
+    uint32_t w, h, T;     // map size and texels
+    uint32_t k, rows;     // bands per view, dir rows per band
+    uint32_t bucket0;     // first bucket (view 0, band 0, texel 0)
+    uint32_t tot0;        // first view sum (view 0, texel 0)
+    uint32_t kind;        // 0 irradiance, 1 prefilter level `level`, 2 background env
+    uint32_t level;
+};
+
+// One workgroup of the map gather: the non-empty buckets ml_order[a0 .. a0 +
+// na) (at most kGatherChains) of nb consecutive (view, band)s of map m from
+// vb0 = view k + band. The bands are walked together in nch chunks: chunk c
+// stages positions c P .. c P + P - 1 of each band (LDS slots bi P ..), a
+// band's positions being its dir pixels in order (the env: the view's
+// background pixels). Chunk c's entries of bucket j are mg_ent[coff[c0 + c na
+// + j] .. coff[c0 + c na + j + 1]) (chunk-major, then bucket order, then pixel
+// order), each (LDS slot << 2) | tap. f0: the set-up's first-entry table.
+struct GatherItem {
+    uint32_t m, vb0, nb, P;
+    uint32_t a0, na, nch, c0;
+    uint32_t f0, pad0, pad1, pad2;
 };
 
 struct PbrDev {
@@ -62,8 +101,6 @@ struct PbrDev {
     const uint4* ltab;  // per level (w, h, texel offset, 0)
     float alpha[kPbrMaxLevels];
     float lr, b1, b2, eps, inv_n, irr_scale;
-    int fix_k;  // fixed point: value * 2^fix_k
-    uint32_t* err;  // the context's error word (kErrFixedRange)
     float light_col[3];
     // static per (view, pixel)
     const float4* st0;  // fg: (u, v, n.v, n.l); bg: (bg u, bg v, -1, 0)
@@ -71,17 +108,15 @@ struct PbrDev {
     const float4* st2;  // (irr u, irr v, refl u, refl v); u < 0: zero direction
     float4* target;     // mapped target (rgb)
     // map geometry
-    const float4* idir;   // irradiance map texel directions (.w unused)
-    const float4* isdir;  // its source (pooled env) directions + sin(theta)
-    const float4* pdir;   // prefilter texel directions, all levels (.w: alpha)
-    const float4* psdir;  // their source directions + sin(theta)
+    const float4* psdir;  // prefilter source directions + sin(theta)
     const float* pnorm;   // PrefilterConvNorm of every prefilter texel
     const float2* lut;
     uint32_t lutw, luth;
-    const PbrGroup* fgroups;
-    uint32_t n_fgroups;
-    const PbrGroup* bgroups;
-    uint32_t n_bgroups;
+    // static convolution weights, summation index major: wf_* [source][output]
+    // (forward), wb_* [output][source] (transposes)
+    // stored tile-major: column group g (lanes 64 g .. 64 g + 63) holds its
+    // rows r of 64 floats at g * rows * 64 + r * 64
+    const float *wf_irr, *wb_irr, *wf_pref, *wb_pref;
     // pooling chain: level k (1-based) has size pw[k] x ph[k]
     uint32_t n_pool, irr_pool, pref_pool;
     uint32_t pw[kPbrMaxPool + 1], ph[kPbrMaxPool + 1];
@@ -92,16 +127,34 @@ struct PbrDev {
     float* t;
     // per iteration
     float4 *irr, *pref;
-    unsigned long long *acc_irr, *acc_pref, *acc_env;
-    float4 *g_irr, *g_pref, *g_isrc, *g_psrc;
+    float4 *g_irr, *g_pref, *g_bg, *g_isrc, *g_psrc;
     float4* gyA;   // per pixel (g albedo rgb, g roughness)
     float* gyM;    // per pixel g metallic
+    float4* mgA;   // per pixel: fg (d loss / d irradiance sample, 0); bg (d loss / d env sample, 0)
+    float4* mgB;   // per fg pixel: (d loss / d prefiltered sample before the level weights, roughness)
     float* loss_part;
     float* loss;
     float4* pred;  // KEEP_PRED
     float4 *g_tex_a, *g_tex_m, *g_env;  // KEEP_GRAD
     const uint32_t* csr_off;  // per texel, into csr
     const uint2* csr;         // (global pixel, weight bits)
+    // map-gradient gather lists
+    const MapInfo* minfo;
+    uint32_t n_maps, n_buckets, n_tot;
+    const uint32_t* ml_order;  // per (map, view, band) its non-empty buckets, bucket order
+    const uint32_t* ml_off;   // per bucket, into the sorted entries (n_buckets + 1)
+    const uint32_t* bg_pix;   // per view from bg_base[v]: the background pixels in order
+    const uint32_t* bg_base;  // per view (n_views + 1)
+    const struct GatherItem* gitems;  // the gather's workgroups
+    uint32_t n_gitems;
+    const uint32_t* coff;     // per item, chunk-major: its buckets' entry runs
+    const uint16_t* mg_ent;   // the entries, chunk-major per item
+    float4* mpart;            // per bucket (maps with k > 1)
+    float4* mtot;             // per (map, view, texel)
+    const uint4* tsum_work;   // tile-sum work items (map, view, first texel, texels)
+    uint32_t n_tsum;
+    uint32_t n_ig, n_pg;      // convolution workgroups: irradiance, prefilter
+    uint32_t n_isg, n_psg;    // transposes: irradiance sources, prefilter sources
     const float2* bc_tab;
     uint32_t bc_len;
     uint32_t* done;
@@ -122,28 +175,6 @@ __device__ __forceinline__ void fetch4(const Taps& t, const float4* data, float*
     out3[0] = a0;
     out3[1] = a1;
     out3[2] = a2;
-}
-
-// Largest fixed-point term a scatter may add: every map-gradient term is
-// bounded by inv_n before the 16-lane row pre-sum (see dressi_pbr_create), so
-// a term is below 16 x 2^29 = 2^33 units; 2^34 leaves a factor of 2, and
-// 2^28 such terms (2^26 pixels x 4 taps) still sum below 2^63.
-constexpr double kFixLimit = 17179869184.0;  // 2^34
-// Error bit: a fixed-point term exceeded kFixLimit (or was not finite) and
-// was clamped; reported by dressi_ctx_synchronize.
-constexpr uint32_t kErrFixedRange = 0x100u;
-
-__device__ __forceinline__ long long to_fixed(float v, int k, uint32_t* err) {
-    double s = ldexp((double)v, k);
-    if (!(fabs(s) <= kFixLimit)) {
-        atomicOr(err, kErrFixedRange);
-        s = s != s ? 0.0 : copysign(kFixLimit, s);
-    }
-    return __double2ll_rn(s);
-}
-
-__device__ __forceinline__ float from_fixed(unsigned long long a, int k) {
-    return (float)ldexp((double)(long long)a, -k);
 }
 
 // ---------------------------------------------------------------------------
@@ -177,7 +208,8 @@ __device__ __forceinline__ V3f safe_normalize(V3f v) {
     return V3f{v.x * s, v.y * s, v.z * s};
 }
 
-__device__ __forceinline__ float pow5(float x) { return (float)pow((double)x, 5.0); }
+// powf(x, 5) as the C library rounds it (x in [0, 1])
+__device__ __forceinline__ float pow5(float x) { return libm::pow5f(x); }
 
 // Static per-pixel terms of one view from its G-buffer (BuildPbrGBuffer,
 // pbr_graph.cpp:34-45, and the geometry-only part of BuildPbrShade,
@@ -317,21 +349,237 @@ __global__ __launch_bounds__(256) void k_pbr_csr(CsrArgs a) {
     }
 }
 
+// The static convolution weights of one map (f_ops.cpp:3006-3087,
+// 3207-3348): per (output texel o, source texel s) with output direction
+// r_o, source direction d_s and sin(theta_s), c = dot(r_o, d_s) in the
+// reference's float order;
+//   irradiance: wf = wb = max(c, 0) sin(theta_s)
+//   prefilter:  w = GgxConvWeight(c, alpha_o), wf = w sin(theta_s),
+//               wb = w / max(norm_o, 1e-12) where w > 0, else 0
+// wf is a matrix of rows s, columns o; wb of rows o, columns s (rows: the
+// index each ordered sum runs over); both tile-major in column groups of 64,
+// zero past the last column. A zero weight adds nothing to a sum of finite
+// terms.
+__global__ __launch_bounds__(256) void k_pbr_weights(const float4* odir, uint32_t no,
+                                                     const float4* sdir, uint32_t ns,
+                                                     const float* norm, float* wf, float* wb) {
+    const uint32_t o = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t sidx = blockIdx.y;
+    if (o >= no) {
+        return;
+    }
+    const float4 r = odir[o];
+    const float4 sd = sdir[sidx];
+    const float c = r.x * sd.x + r.y * sd.y + r.z * sd.z;
+    float f, b;
+    if (!norm) {
+        f = (c < 0.f ? 0.f : c) * sd.w;
+        b = f;
+    } else {
+        const float w = ggx_conv_weight(c, r.w);
+        f = w * sd.w;
+        const float nt = norm[o];
+        b = w > 0.f ? w / (nt < 1e-12f ? 1e-12f : nt) : 0.f;
+    }
+    // tile-major: wf rows are sources (no outputs per row), wb rows outputs
+    wf[((size_t)(o / 64u) * ns + sidx) * 64u + (o % 64u)] = f;
+    wb[((size_t)(sidx / 64u) * no + o) * 64u + (sidx % 64u)] = b;
+}
+
+// Keys of the map-gradient gather lists: per (view, pixel) in pixel order,
+// per map, per bilinear tap in the reference's order (dy outer, dx inner),
+// the bucket (view, band of the pixel's row, tap texel) of the map's
+// EquirectSample VJP, or kNoBucket when the pixel adds nothing there (see
+// k_pbr_map_gather); the value is (pixel << 2) | tap. A stable sort by key
+// then lists every bucket's entries in pixel order.
+constexpr uint32_t kNoBucket = 0xffffffffu;
+
+struct ListArgs {
+    const float4 *st0, *st2;
+    const MapInfo* minfo;
+    uint32_t n_maps, n_views, S;
+    uint32_t no_key;
+    const uint32_t* bg_idx;  // per pixel: its index among its view's background pixels
+    uint32_t* keys;
+    uint32_t* vals;
+    uint32_t* count;
+};
+
+__global__ __launch_bounds__(256) void k_pbr_list_keys(ListArgs a) {
+    const size_t npx = (size_t)a.S * a.S;
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= npx * a.n_views) {
+        return;
+    }
+    const uint32_t v = (uint32_t)(q / npx);
+    const uint32_t p = (uint32_t)(q % npx);
+    const uint32_t y = p / a.S;
+    const float4 s0 = a.st0[q], s2 = a.st2[q];
+    const bool fg = s0.z >= 0.f;
+    for (uint32_t m = 0; m < a.n_maps; m++) {
+        const MapInfo mi = a.minfo[m];
+        bool ok;
+        float u, vv;
+        if (mi.kind == 0) {
+            ok = fg && s2.x >= 0.f;
+            u = s2.x;
+            vv = s2.y;
+        } else if (mi.kind == 1) {
+            ok = fg && s2.z >= 0.f;
+            u = s2.z;
+            vv = s2.w;
+        } else {
+            ok = !fg && s0.x >= 0.f;
+            u = s0.x;
+            vv = s0.y;
+        }
+        const float sx = u * (float)mi.w - 0.5f;
+        const float sy = vv * (float)mi.h - 0.5f;
+        const int ix = (int)floorf(sx), iy = (int)floorf(sy);
+        const uint32_t band = y / mi.rows;
+        for (uint32_t k = 0; k < 4; k++) {
+            const size_t o = (q * a.n_maps + m) * 4 + k;
+            uint32_t key = a.no_key;
+            if (ok) {
+                int x = ix + (int)(k & 1u);
+                if (x < 0) x += (int)mi.w;
+                if (x >= (int)mi.w) x -= (int)mi.w;
+                int yy = iy + (int)(k >> 1);
+                yy = yy < 0 ? 0 : (yy > (int)mi.h - 1 ? (int)mi.h - 1 : yy);
+                key = mi.bucket0 + (v * mi.k + band) * mi.T + (uint32_t)yy * mi.w + (uint32_t)x;
+                atomicAdd(&a.count[key], 1u);
+            }
+            a.keys[o] = key;
+            a.vals[o] = ((mi.kind == 2 && ok ? a.bg_idx[q] : p) << 2) | k;
+        }
+    }
+}
+
+// The positions of (view, band) vb of a map: pixels pbase .. pbase + npos - 1
+// of view v (the env: bg_pix[pbase ..]); a sorted entry's position is its
+// value >> 2 minus posoff.
+struct BandPos {
+    uint32_t v, pbase, npos, posoff;
+};
+
+__device__ __forceinline__ BandPos band_pos(const MapInfo& mi, uint32_t vb, uint32_t S,
+                                            const uint32_t* bg_base) {
+    BandPos r;
+    r.v = vb / mi.k;
+    if (mi.kind == 2) {
+        r.pbase = bg_base[r.v];
+        r.npos = bg_base[r.v + 1] - r.pbase;
+        r.posoff = 0;
+    } else {
+        const uint32_t band = vb % mi.k;
+        const uint32_t r0 = band * mi.rows < S ? band * mi.rows : S;
+        const uint32_t r1 = r0 + mi.rows < S ? r0 + mi.rows : S;
+        r.pbase = r0 * S;
+        r.npos = (r1 - r0) * S;
+        r.posoff = r0 * S;
+    }
+    return r;
+}
+
+// Background pixels that sample the env (zero-length rays excluded), as
+// k_pbr_list_keys selects them: flags for their per-view exclusive scan
+// (bg_idx), then the per-view lists of their pixels.
+__global__ __launch_bounds__(256) void k_pbr_bg_flags(const float4* st0, size_t n, uint32_t* flag) {
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q < n) {
+        const float4 s0 = st0[q];
+        flag[q] = (!(s0.z >= 0.f) && s0.x >= 0.f) ? 1u : 0u;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_pbr_bg_fill(const uint32_t* flag, const uint32_t* idx,
+                                                     uint32_t npx, uint32_t base, uint32_t* bg_pix) {
+    const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p < npx && flag[p]) {
+        bg_pix[base + idx[p]] = p;
+    }
+}
+
+// Per gather item and bucket j (thread): the first sorted entry of each chunk
+// (positions c P .. of the bucket's band), fo[f0 + c na + j] for c = 0 .. nch
+// (nch: the list's end), and the chunk's entry count cnt[c0 + c na + j].
+__global__ __launch_bounds__(256) void k_pbr_chunk_first(const GatherItem* items,
+                                                         uint32_t n_items, const MapInfo* minfo,
+                                                         uint32_t S, const uint32_t* bg_base,
+                                                         const uint32_t* order, const uint32_t* off,
+                                                         const uint32_t* ent, uint32_t* fo,
+                                                         uint32_t* cnt) {
+    const uint32_t it = blockIdx.y;
+    if (it >= n_items) {
+        return;
+    }
+    const GatherItem g = items[it];
+    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= g.na) {
+        return;
+    }
+    const MapInfo mi = minfo[g.m];
+    const uint32_t b = order[g.a0 + j];
+    const BandPos bp = band_pos(mi, (b - mi.bucket0) / mi.T, S, bg_base);
+    uint32_t k = 0;
+    const uint32_t e1 = off[b + 1];
+    for (uint32_t e = off[b]; e < e1; e++) {
+        const uint32_t pos = (ent[e] >> 2) - bp.posoff;
+        while (k <= g.nch && k * g.P <= pos) {
+            fo[g.f0 + k * g.na + j] = e;
+            k++;
+        }
+    }
+    while (k <= g.nch) {
+        fo[g.f0 + k * g.na + j] = e1;
+        k++;
+    }
+    for (uint32_t c = 0; c < g.nch; c++) {
+        cnt[g.c0 + c * g.na + j] = fo[g.f0 + (c + 1) * g.na + j] - fo[g.f0 + c * g.na + j];
+    }
+}
+
+// The chunk-major entries: bucket j's entries of chunk c from coff[c0 + c na
+// + j], in pixel order, each (LDS slot of the position) << 2 | tap.
+__global__ __launch_bounds__(256) void k_pbr_chunk_fill(const GatherItem* items, uint32_t n_items,
+                                                        const MapInfo* minfo, uint32_t S,
+                                                        const uint32_t* bg_base,
+                                                        const uint32_t* order, const uint32_t* ent,
+                                                        const uint32_t* fo, const uint32_t* coff,
+                                                        uint16_t* out) {
+    const uint32_t it = blockIdx.y;
+    if (it >= n_items) {
+        return;
+    }
+    const GatherItem g = items[it];
+    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= g.na) {
+        return;
+    }
+    const MapInfo mi = minfo[g.m];
+    const uint32_t b = order[g.a0 + j];
+    const uint32_t vb = (b - mi.bucket0) / mi.T;
+    const BandPos bp = band_pos(mi, vb, S, bg_base);
+    const uint32_t slot0 = (vb - g.vb0) * g.P;
+    for (uint32_t c = 0; c < g.nch; c++) {
+        const uint32_t x0 = fo[g.f0 + c * g.na + j], x1 = fo[g.f0 + (c + 1) * g.na + j];
+        const uint32_t dst = coff[g.c0 + c * g.na + j];
+        for (uint32_t e = x0; e < x1; e++) {
+            const uint32_t v = ent[e];
+            const uint32_t l = slot0 + (v >> 2) - bp.posoff - c * g.P;
+            out[dst + (e - x0)] = (uint16_t)((l << 2) | (v & 3u));
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Iteration kernels
 // ---------------------------------------------------------------------------
 
 // One level of the pooling chain (Reduce2x2Sum * 0.25, zero padding): level
-// `lvl` from level lvl - 1. The first level also clears the gradient
-// accumulators of this iteration.
+// `lvl` from level lvl - 1.
 __global__ __launch_bounds__(256) void k_pbr_pool(PbrDev d, uint32_t lvl) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (lvl == 1 && !d.target_mode) {
-        const uint32_t stride = gridDim.x * blockDim.x;
-        for (uint32_t j = i; j < (d.iw * d.ih) * 3 * kStripes; j += stride) d.acc_irr[j] = 0ull;
-        for (uint32_t j = i; j < d.n_pref * 3 * kStripes; j += stride) d.acc_pref[j] = 0ull;
-        for (uint32_t j = i; j < (d.ew * d.eh) * 3; j += stride) d.acc_env[j] = 0ull;
-    }
     const uint32_t ow = d.pw[lvl], oh = d.ph[lvl];
     if (i >= ow * oh) {
         return;
@@ -354,145 +602,162 @@ __global__ __launch_bounds__(256) void k_pbr_pool(PbrDev d, uint32_t lvl) {
     d.pool[lvl][i] = make_float4(a0 * 0.25f, a1 * 0.25f, a2 * 0.25f, 0.f);
 }
 
-// Sum of 3 x kConvOuts per-thread partials over the 256-thread workgroup
-// (wave shuffles, then the 4 waves in order); result in red[o * 3 + c].
-__device__ __forceinline__ void block_reduce_outs(float (&acc)[kConvOuts][3], float* red) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int o = 0; o < kConvOuts; o++) {
-#pragma unroll
-        for (int c = 0; c < 3; c++) {
-            float v = acc[o][c];
-#pragma unroll
-            for (int s = 32; s >= 1; s >>= 1) {
-                v += __shfl_xor(v, s);
-            }
-            if (lane == 0) {
-                red[wave * kConvOuts * 3 + o * 3 + c] = v;
-            }
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x < kConvOuts * 3) {
-        const int j = threadIdx.x;
-        red[4 * kConvOuts * 3 + j] = ((red[j] + red[kConvOuts * 3 + j]) +
-                                      red[2 * kConvOuts * 3 + j]) + red[3 * kConvOuts * 3 + j];
-    }
-    __syncthreads();
-}
+// Ordered mat-vec in tiles of kMvRows summation steps x kMvCols lanes,
+// double-buffered in LDS (128 KB of weights + the x rows): the workgroup's
+// next tile is in flight while its three waves (one per colour channel) add
+// the current one.
+constexpr uint32_t kMvRows = 256;
+constexpr uint32_t kMvCols = 64;
+constexpr uint32_t kMvThreads = 192;
+constexpr uint32_t kMvVec = kMvRows * kMvCols / 4;                    // float4 per weight tile
+constexpr uint32_t kMvPer = (kMvVec + kMvThreads - 1) / kMvThreads;  // per thread
+constexpr uint32_t kMvXPer = (kMvRows + kMvThreads - 1) / kMvThreads;
 
-// IrradianceConv and the PrefilterConv levels (f_ops.cpp:3006-3087,
-// 3264-3348): a workgroup per group of <= 16 outputs of one map, the
-// threads split the source texels; weights exactly as the reference's
-// (ggx_conv_weight of the same float dot product), sums in another order.
-__global__ __launch_bounds__(256) void k_pbr_conv_fwd(PbrDev d) {
-    __shared__ float4 od[kConvOuts];
-    __shared__ float red[5 * kConvOuts * 3];
-    const PbrGroup gr = d.fgroups[blockIdx.x];
-    const bool irr = gr.level == kIrrLevel;
-    const float4* sdir = irr ? d.isdir : d.psdir;
-    const float4* src = irr ? d.pool[d.irr_pool] : d.pool[d.pref_pool];
-    const uint32_t n_src = irr ? d.isw * d.ish : d.psw * d.psh;
-    const float alpha = irr ? 0.f : d.alpha[gr.level];
-    if (threadIdx.x < kConvOuts) {
-        od[threadIdx.x] = threadIdx.x < gr.count
-                                  ? (irr ? d.idir : d.pdir)[gr.first + threadIdx.x]
-                                  : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    __syncthreads();
-    float acc[kConvOuts][3];
-#pragma unroll
-    for (int o = 0; o < kConvOuts; o++) {
-        acc[o][0] = acc[o][1] = acc[o][2] = 0.f;
-    }
-    for (uint32_t s = threadIdx.x; s < n_src; s += blockDim.x) {
-        const float4 sd = sdir[s];
-        const float4 e = src[s];
-#pragma unroll
-        for (int o = 0; o < kConvOuts; o++) {
-            const float4 r = od[o];
-            const float c = r.x * sd.x + r.y * sd.y + r.z * sd.z;
-            if (c > 0.f) {
-                const float w = (irr ? c : ggx_conv_weight(c, alpha)) * sd.w;
-                acc[o][0] += e.x * w;
-                acc[o][1] += e.y * w;
-                acc[o][2] += e.z * w;
-            }
-        }
-    }
-    block_reduce_outs(acc, red);
-    if (threadIdx.x < gr.count) {
-        const float* v = red + 4 * kConvOuts * 3 + threadIdx.x * 3;
-        const uint32_t o = gr.first + threadIdx.x;
-        if (irr) {
-            d.irr[o] = make_float4(v[0] * d.irr_scale, v[1] * d.irr_scale, v[2] * d.irr_scale, 0.f);
-        } else {
-            const float nt = d.pnorm[o];
-            const float wn = nt > 1e-12f ? nt : 1e-12f;
-            d.pref[o] = make_float4(v[0] / wn, v[1] / wn, v[2] / wn, 0.f);
-        }
-    }
-}
-
-// LDS scatter windows of one shading workgroup: per map (irradiance,
-// prefilter levels, env) the bounding box of the tap bases of the
-// contributing pixels (u unwrapped around the seam); a box of <= kWin taps
-// is accumulated in LDS and flushed with one global atomic per texel and
-// channel, else the lanes add to the global accumulators directly.
-constexpr int kMaps = kPbrMaxLevels + 2;
-
-struct MapTaps {
-    int ix, iy;  // tap base: floor(u w - .5), floor(v h - .5)
-    float w[4];  // weights in the reference's order (dy outer, dx inner)
+struct MvLds {
+    float w[2][kMvRows][kMvCols];
+    float x[2][3][kMvRows];  // planar: channel c of rows 4j .. 4j + 3 in one 16-byte read
 };
 
-__device__ __forceinline__ MapTaps map_taps(int w, int h, float u, float v) {
-    const float sx = u * (float)w - 0.5f;
-    const float sy = v * (float)h - 0.5f;
-    MapTaps t;
-    t.ix = (int)floorf(sx);
-    t.iy = (int)floorf(sy);
-    const float fx = sx - (float)t.ix;
-    const float fy = sy - (float)t.iy;
-    t.w[0] = (1.f - fx) * (1.f - fy);
-    t.w[1] = fx * (1.f - fy);
-    t.w[2] = (1.f - fx) * fy;
-    t.w[3] = fx * fy;
-    (void)w;
-    (void)h;
-    return t;
+struct MvRegs {
+    float4 w[kMvPer];
+    float4 x[kMvXPer];
+};
+
+// rows [r, r + n) (n <= kMvRows) of the weights of one column group (the
+// group's rows of kMvCols floats stored contiguously: `Wg` points at its row
+// 0) and of x
+__device__ __forceinline__ void mv_fetch(const float* __restrict__ Wg,
+                                         const float4* __restrict__ x, uint32_t r, uint32_t n,
+                                         MvRegs& g) {
+    const float4* w4 = (const float4*)(Wg + (size_t)r * kMvCols);
+#pragma unroll
+    for (uint32_t i = 0; i < kMvPer; i++) {
+        const uint32_t f = threadIdx.x + i * kMvThreads;
+        const uint32_t row = f / (kMvCols / 4);
+        g.w[i] = (f < kMvVec && row < n) ? w4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kMvXPer; i++) {
+        const uint32_t row = threadIdx.x + i * kMvThreads;
+        g.x[i] = row < n ? x[r + row] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 }
 
-__device__ __forceinline__ uint32_t wrap_idx(int x, int y, int w, int h) {
-    x = ((x % w) + w) % w;
-    y = y < 0 ? 0 : (y > h - 1 ? h - 1 : y);
-    return (uint32_t)(y * w + x);
+__device__ __forceinline__ void mv_store(MvLds& L, int b, const MvRegs& g) {
+#pragma unroll
+    for (uint32_t i = 0; i < kMvPer; i++) {
+        const uint32_t f = threadIdx.x + i * kMvThreads;
+        if (f < kMvVec) {
+            const uint32_t row = f / (kMvCols / 4), c4 = f % (kMvCols / 4);
+            *(float4*)&L.w[b][row][c4 * 4] = g.w[i];
+        }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kMvXPer; i++) {
+        const uint32_t row = threadIdx.x + i * kMvThreads;
+        if (row < kMvRows) {
+            L.x[b][0][row] = g.x[i].x;
+            L.x[b][1][row] = g.x[i].y;
+            L.x[b][2][row] = g.x[i].z;
+        }
+    }
 }
 
-// DPP moves within rows of 16 lanes: row_shr:S reads lane - S (lanes with
-// (lane & 15) < S read 0), row_shl:S reads lane + S
-template <int S>
-__device__ __forceinline__ int dpp_row_shr(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, 0x110 + S, 0xf, 0xf, true);
+// sum over rows r in [r0, r1) of x[r].c * W(r, lane), from 0 in row order,
+// for the calling lane and the wave's channel c; W(r, l) = Wg[r * kMvCols + l]
+// (one column group, tile-major). Every thread of the workgroup calls it (it
+// synchronises the workgroup).
+__device__ float mv_segment(MvLds& L, const float* __restrict__ Wg,
+                            const float4* __restrict__ x, uint32_t r0, uint32_t r1) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n = r1 - r0;
+    const uint32_t tiles = (n + kMvRows - 1) / kMvRows;
+    MvRegs g;
+    mv_fetch(Wg, x, r0, n < kMvRows ? n : kMvRows, g);
+    mv_store(L, 0, g);
+    __syncthreads();
+    float acc = 0.f;
+    for (uint32_t t = 0; t < tiles; t++) {
+        const uint32_t done = t * kMvRows;
+        const uint32_t rows = n - done < kMvRows ? n - done : kMvRows;
+        const bool next = t + 1 < tiles;
+        if (next) {
+            const uint32_t rest = n - done - kMvRows;
+            mv_fetch(Wg, x, r0 + done + kMvRows, rest < kMvRows ? rest : kMvRows, g);
+        }
+        const int b = (int)(t & 1u);
+        const float* xs = L.x[b][c];
+        uint32_t i = 0;
+        // 16 rows' LDS reads in flight, then their products added in order
+        for (; i + 16 <= rows; i += 16) {
+            float wv[16], xv[16];
+#pragma unroll
+            for (uint32_t u = 0; u < 16; u += 4) {
+                const float4 q = *(const float4*)&xs[i + u];
+                xv[u] = q.x;
+                xv[u + 1] = q.y;
+                xv[u + 2] = q.z;
+                xv[u + 3] = q.w;
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 16; u++) {
+                wv[u] = L.w[b][i + u][lane];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 16; u++) {
+                acc += xv[u] * wv[u];
+            }
+        }
+        for (; i < rows; i++) {
+            acc += xs[i] * L.w[b][i][lane];
+        }
+        if (next) {
+            mv_store(L, b ^ 1, g);
+        }
+        __syncthreads();
+    }
+    return acc;
 }
-template <int S>
-__device__ __forceinline__ int dpp_row_shl(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, 0x100 + S, 0xf, 0xf, true);
-}
-template <int S>
-__device__ __forceinline__ float dpp_row_shr_f(float v) {
-    return __int_as_float(dpp_row_shr<S>(__float_as_int(v)));
+
+// IrradianceConv and every PrefilterConv level (f_ops.cpp:3006-3087,
+// 3264-3348): out[o] = (sum_s e[s] * w(o, s)) * 2 pi / (sw sh) for the
+// irradiance map, (sum_s e[s] * w(o, s)) / max(norm[o], 1e-12) for a
+// prefilter texel, the sums over the pooled source in raster order from 0.
+// The weights (cos+ sin(theta) / GGX sin(theta)) are static: wf_*
+// [source][output], rows of ld_* floats. A workgroup holds 64 outputs; wave
+// c computes colour channel c.
+__global__ __launch_bounds__(192) void k_pbr_conv_fwd(PbrDev d) {
+    __shared__ MvLds L;
+    const bool irr = blockIdx.x < d.n_ig;
+    const uint32_t n_out = irr ? d.iw * d.ih : d.n_pref;
+    const uint32_t n_src = irr ? d.isw * d.ish : d.psw * d.psh;
+    const uint32_t col0 = (irr ? blockIdx.x : blockIdx.x - d.n_ig) * kMvCols;
+    const uint32_t o = col0 + (threadIdx.x & 63u);
+    const uint32_t c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const float4* src = irr ? d.pool[d.irr_pool] : d.pool[d.pref_pool];
+    const float* Wg = (irr ? d.wf_irr : d.wf_pref) + (size_t)col0 * n_src;  // group's rows
+    const float acc = mv_segment(L, Wg, src, 0, n_src);
+    if (o >= n_out) {
+        return;
+    }
+    if (irr) {
+        ((float*)d.irr)[(size_t)o * 4 + c] = acc * d.irr_scale;
+    } else {
+        const float nt = d.pnorm[o];
+        ((float*)d.pref)[(size_t)o * 4 + c] = acc / (nt < 1e-12f ? 1e-12f : nt);
+    }
 }
 
 // Per pixel (a 16 x 16 tile of one view per workgroup): the shading
 // forward, the L1 loss and its backward (the derivation of the reference's
 // autodiff of pbr_graph.cpp:47-137 through Div / Mul / Add / Max / Mix /
 // Clamp / Pow / Abs, f_ops.cpp:235-537); in target mode the forward only.
+// Outputs per pixel: the material gradients (gyA, gyM) and the seeds of the
+// map-gradient VJPs (mgA, mgB) that k_pbr_map_gather spreads over the maps.
 // The prefilter levels with a tent weight 1 - |lod - i| >= 0 are among
 // floor(lod) - 1 .. floor(lod) + 1: three register slots.
 __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
-    __shared__ int box[kMaps][4];
-    __shared__ unsigned long long win[kMaps][kWin][3];
     __shared__ float lred[4];
     const uint32_t tiles = (d.S + kShadeTile - 1) / kShadeTile;
     const uint32_t view = blockIdx.x / (tiles * tiles);
@@ -503,16 +768,12 @@ __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
     const size_t npx = (size_t)d.S * d.S;
     const size_t p = (size_t)view * npx + (size_t)(valid ? y * d.S + x : 0);
     const int L = (int)d.levels;
-    if (threadIdx.x < kMaps * 4) {
-        box[threadIdx.x >> 2][threadIdx.x & 3] = (threadIdx.x & 1) ? INT_MIN : INT_MAX;
-    }
     const bool train = !d.target_mode;
     // ---- forward --------------------------------------------------------
     const float4 s0 = valid ? d.st0[p] : make_float4(0.f, 0.f, -1.f, 0.f);
     const bool fg = valid && s0.z >= 0.f;
     float hdr[3] = {0.f, 0.f, 0.f};
-    MapTaps t_irr{}, t_bg{}, tp[3];
-    bool use_irr = false, use_bg = false, act[3] = {false, false, false};
+    bool act[3] = {false, false, false};
     int li[3] = {0, 0, 0};
     float xs[3] = {0.f, 0.f, 0.f}, ws[3] = {0.f, 0.f, 0.f}, Ps[3][3];
     float a[3] = {0.f, 0.f, 0.f}, mr[3] = {0.f, 0.f, 0.f}, irr[3] = {0.f, 0.f, 0.f};
@@ -522,12 +783,9 @@ __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
 #pragma unroll
     for (int j = 0; j < 3; j++) {
         Ps[j][0] = Ps[j][1] = Ps[j][2] = 0.f;
-        tp[j] = MapTaps{};
     }
     if (valid && !fg) {
         if (s0.x >= 0.f) {
-            use_bg = true;
-            t_bg = map_taps((int)d.ew, (int)d.eh, s0.x, s0.y);
             fetch4(taps_wrap((int)d.ew, (int)d.eh, s0.x, s0.y), d.env, hdr);
         }
     } else if (fg) {
@@ -544,8 +802,6 @@ __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
         rough = mr[1] < 0.045f ? 0.045f : (mr[1] > 1.f ? 1.f : mr[1]);
         metal = mr[2];
         if (s2.x >= 0.f) {
-            use_irr = true;
-            t_irr = map_taps((int)d.iw, (int)d.ih, s2.x, s2.y);
             fetch4(taps_wrap((int)d.iw, (int)d.ih, s2.x, s2.y), d.irr, irr);
         }
         lod = rough * (float)(L - 1);
@@ -562,7 +818,6 @@ __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
             if (xs[j] >= 0.f && s2.z >= 0.f) {
                 act[j] = true;
                 const uint4 lv = d.ltab[i];
-                tp[j] = map_taps((int)lv.x, (int)lv.y, s2.z, s2.w);
                 fetch4(taps_wrap((int)lv.x, (int)lv.y, s2.z, s2.w), d.pref + lv.z, Ps[j]);
                 pref[0] += Ps[j][0] * ws[j];
                 pref[1] += Ps[j][1] * ws[j];
@@ -700,300 +955,317 @@ __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
     if (valid) {
         d.gyA[p] = make_float4(ga[0], ga[1], ga[2], gr);
         d.gyM[p] = gmet;
+        // seeds of the map VJPs: the irradiance sample's gradient (fg) or the
+        // background env sample's (bg: d hdr / d env sample = 1); the
+        // prefiltered sample's before the level weights, with the roughness
+        // the level weights come from
+        d.mgA[p] = fg ? make_float4(g_irr[0], g_irr[1], g_irr[2], 0.f)
+                      : make_float4(gh[0], gh[1], gh[2], 0.f);
+        if (fg) {
+            d.mgB[p] = make_float4(gpref[0], gpref[1], gpref[2], rough);
+        }
     }
     // ---- loss partial of the workgroup ------------------------------------
-    {
-        float v = lsum;
+    float v = lsum;
 #pragma unroll
-        for (int s = 32; s >= 1; s >>= 1) {
-            v += __shfl_xor(v, s);
-        }
-        if ((threadIdx.x & 63) == 0) {
-            lred[threadIdx.x >> 6] = v;
-        }
+    for (int sh = 32; sh >= 1; sh >>= 1) {
+        v += __shfl_xor(v, sh);
     }
-    // ---- map gradient scatter ---------------------------------------------
-    // map m: 0 irradiance, 1 + i prefilter level i, L + 1 env; the
-    // irradiance / prefilter accumulators are striped over kStripes copies
-    // (by workgroup) so the few texels of the small maps are not one hot
-    // spot. Five passes (irradiance, the three prefilter slots, env): per
-    // pass, the 16 lanes of a pixel row are cut into runs of equal tap base
-    // (map, ix, iy); each run's 12 weighted values are summed along the row
-    // (DPP, a fixed order) and its last lane adds them to the workgroup's
-    // LDS window of the map (or to the global accumulators when the window
-    // would exceed kWin texels).
-    const uint32_t stripe = blockIdx.x & (kStripes - 1);
-    unsigned long long* acc_irr = d.acc_irr + (size_t)stripe * d.iw * d.ih * 3;
-    unsigned long long* acc_pref = d.acc_pref + (size_t)stripe * d.n_pref * 3;
-    const int lane16 = (int)(threadIdx.x & 15);
-    const auto pass_has = [&](int ps) {
-        return ps == 0 ? use_irr : (ps == 4 ? use_bg : (act[ps - 1] && ws[ps - 1] != 0.f));
-    };
-    const auto pass_map = [&](int ps) { return ps == 0 ? 0 : (ps == 4 ? L + 1 : 1 + li[ps - 1]); };
-    const auto pass_taps = [&](int ps) -> const MapTaps& {
-        return ps == 0 ? t_irr : (ps == 4 ? t_bg : tp[ps - 1]);
-    };
-    // run ids and run tails per pass
-    int seg[5];
-    bool tail[5];
-#pragma unroll
-    for (int ps = 0; ps < 5; ps++) {
-        const bool has = pass_has(ps);
-        const MapTaps& t = pass_taps(ps);
-        // lanes without a contribution get a key of their own
-        const int key = has ? ((pass_map(ps) << 26) | ((t.iy + 1) << 13) | (t.ix + 1))
-                            : -1 - (int)threadIdx.x;
-        const int left = dpp_row_shr<1>(key);
-        int sg = (lane16 == 0 || left != key) ? 1 : 0;
-        sg += dpp_row_shr<1>(sg);
-        sg += dpp_row_shr<2>(sg);
-        sg += dpp_row_shr<4>(sg);
-        sg += dpp_row_shr<8>(sg);
-        const int right = dpp_row_shl<1>(sg);
-        seg[ps] = sg;
-        tail[ps] = has && (lane16 == 15 || right != sg);
-    }
-    __syncthreads();  // box initialised
-#pragma unroll
-    for (int ps = 0; ps < 5; ps++) {
-        if (tail[ps]) {
-            const int m = pass_map(ps);
-            const MapTaps& t = pass_taps(ps);
-            atomicMin(&box[m][0], t.ix);
-            atomicMax(&box[m][1], t.ix);
-            atomicMin(&box[m][2], t.iy);
-            atomicMax(&box[m][3], t.iy);
-        }
-    }
-    const int n_maps = L + 2;
-    for (int j = threadIdx.x; j < n_maps * kWin * 3; j += blockDim.x) {
-        (&win[0][0][0])[j] = 0ull;
+    if ((threadIdx.x & 63) == 0) {
+        lred[threadIdx.x >> 6] = v;
     }
     __syncthreads();
-    const auto map_wh = [&](int m, int* w, int* h, uint32_t* off) {
-        if (m == 0) {
-            *w = (int)d.iw;
-            *h = (int)d.ih;
-            *off = 0;
-        } else if (m <= L) {
-            const uint4 lv = d.ltab[m - 1];
-            *w = (int)lv.x;
-            *h = (int)lv.y;
-            *off = lv.z;
-        } else {
-            *w = (int)d.ew;
-            *h = (int)d.eh;
-            *off = 0;
-        }
-    };
-    // window geometry: x in [box0, box1 + 1] (unwrapped), y clamped
-    const auto win_ok = [&](int m, int h, int* ww, int* wy0) {
-        if (box[m][0] > box[m][1]) return false;
-        const int y0 = box[m][2] < 0 ? 0 : (box[m][2] > h - 1 ? h - 1 : box[m][2]);
-        const int y1 = box[m][3] + 1 < 0 ? 0 : (box[m][3] + 1 > h - 1 ? h - 1 : box[m][3] + 1);
-        const int w = box[m][1] - box[m][0] + 2;
-        *ww = w;
-        *wy0 = y0;
-        return w * (y1 - y0 + 1) <= kWin;
-    };
-    const int k = d.fix_k;
-#pragma unroll
-    for (int ps = 0; ps < 5; ps++) {
-        if (!__any(tail[ps])) {
-            continue;
-        }
-        const MapTaps& t = pass_taps(ps);
-        float g3[3];
-        if (ps == 0) {
-            g3[0] = g_irr[0];
-            g3[1] = g_irr[1];
-            g3[2] = g_irr[2];
-        } else if (ps == 4) {
-            g3[0] = gh[0];
-            g3[1] = gh[1];
-            g3[2] = gh[2];
-        } else {
-            const float wj = ws[ps - 1];
-            g3[0] = gpref[0] * wj;
-            g3[1] = gpref[1] * wj;
-            g3[2] = gpref[2] * wj;
-        }
-        const bool has = pass_has(ps);
-        float v[12];
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-#pragma unroll
-            for (int c = 0; c < 3; c++) {
-                v[q * 3 + c] = has ? g3[c] * t.w[q] : 0.f;
-            }
-        }
-        const int sg = seg[ps];
-        // segmented inclusive scan along the row (runs are contiguous)
-#pragma unroll
-        for (int sh = 1; sh < 16; sh <<= 1) {
-            const int osg = sh == 1 ? dpp_row_shr<1>(sg)
-                                    : (sh == 2 ? dpp_row_shr<2>(sg)
-                                               : (sh == 4 ? dpp_row_shr<4>(sg) : dpp_row_shr<8>(sg)));
-            const bool take = lane16 >= sh && osg == sg;
-#pragma unroll
-            for (int e = 0; e < 12; e++) {
-                const float o = sh == 1 ? dpp_row_shr_f<1>(v[e])
-                                        : (sh == 2 ? dpp_row_shr_f<2>(v[e])
-                                                   : (sh == 4 ? dpp_row_shr_f<4>(v[e])
-                                                              : dpp_row_shr_f<8>(v[e])));
-                v[e] += take ? o : 0.f;
-            }
-        }
-        if (tail[ps]) {
-            const int m = pass_map(ps);
-            int w, h, ww, wy0;
-            uint32_t off;
-            map_wh(m, &w, &h, &off);
-            const bool lds = win_ok(m, h, &ww, &wy0);
-            unsigned long long* gacc =
-                    m == 0 ? acc_irr : (m <= L ? acc_pref + (size_t)off * 3 : d.acc_env);
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int xx = t.ix + (q & 1), yy0 = t.iy + (q >> 1);
-                const int yy = yy0 < 0 ? 0 : (yy0 > h - 1 ? h - 1 : yy0);
-#pragma unroll
-                for (int c = 0; c < 3; c++) {
-                    const long long val = to_fixed(v[q * 3 + c], k, d.err);
-                    if (!val) continue;
-                    if (lds) {
-                        const int wi = (yy - wy0) * ww + (xx - box[m][0]);
-                        atomicAdd(&win[m][wi][c], (unsigned long long)val);
-                    } else {
-                        atomicAdd(&gacc[(size_t)wrap_idx(xx, yy, w, h) * 3 + c],
-                                  (unsigned long long)val);
-                    }
-                }
-            }
-        }
-    }
-    __syncthreads();
-    // flush the LDS windows
-    for (int j = threadIdx.x; j < n_maps * kWin; j += blockDim.x) {
-        const int m = j / kWin, wi = j % kWin;
-        int w, h, ww, wy0;
-        uint32_t off;
-        map_wh(m, &w, &h, &off);
-        if (!win_ok(m, h, &ww, &wy0)) continue;
-        const int xx = box[m][0] + wi % ww, yy = wy0 + wi / ww;
-        if (yy > h - 1) continue;
-        unsigned long long* gacc =
-                m == 0 ? acc_irr : (m <= L ? acc_pref + (size_t)off * 3 : d.acc_env);
-        for (int c = 0; c < 3; c++) {
-            const unsigned long long val = win[m][wi][c];
-            if (val) {
-                atomicAdd(&gacc[(size_t)wrap_idx(xx, yy, w, h) * 3 + c], val);
-            }
-        }
-    }
     if (threadIdx.x == 0) {
         d.loss_part[blockIdx.x] = ((lred[0] + lred[1]) + lred[2]) + lred[3];
     }
 }
 
-// fixed point -> float gradients of the irradiance and prefilter maps: the
-// sum of the stripes (exact in fixed point, so in any order)
-__global__ __launch_bounds__(256) void k_pbr_resolve(PbrDev d) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    const uint32_t ni = d.iw * d.ih;
-    if (i >= ni + d.n_pref) {
-        return;
+// The map of a bucket (maps are few; their buckets are contiguous)
+__device__ __forceinline__ uint32_t map_of_bucket(const PbrDev& d, uint32_t b) {
+    uint32_t m = 0;
+    while (m + 1 < d.n_maps && b >= d.minfo[m + 1].bucket0) {
+        m++;
     }
-    const bool irr = i < ni;
-    const unsigned long long* a = irr ? d.acc_irr + (size_t)i * 3
-                                      : d.acc_pref + (size_t)(i - ni) * 3;
-    const size_t stride = (size_t)(irr ? ni : d.n_pref) * 3;
-    unsigned long long s0 = 0, s1 = 0, s2 = 0;
-    for (uint32_t st = 0; st < kStripes; st++) {
-        s0 += a[st * stride + 0];
-        s1 += a[st * stride + 1];
-        s2 += a[st * stride + 2];
+    return m;
+}
+
+// EquirectSampleBwd's band partials (f_ops.cpp:2862-2904) of up to 256
+// (map, view, band, texel) buckets of consecutive bands, one per thread: each
+// from 0, the bucket's list entries (pixel, tap) in pixel order, each adding
+// gy * w with the tap's bilinear weight w = (dx ? fx : 1 - fx) * (dy ? fy :
+// 1 - fy) of the pixel's direction uv (fx = (u w - 0.5) - floor(u w - 0.5),
+// f_ops.cpp:2874-2892) and its gy: the irradiance sample's gradient, the
+// prefiltered sample's times the level's tent weight clamp(1 - |lod - i|, 0,
+// 1), or the background env sample's. Entries whose gy is always 0 are not
+// listed (background pixels of the material maps, pixels with a zero-length
+// direction), which changes no sum that starts at +0.
+// The bands are walked together in chunks: each chunk's per-position tap
+// weights and gy are staged in LDS once for all the buckets (an entry value
+// (slot << 2) | tap indexes its weight directly), with the chunk's entries;
+// the next chunk's loads are in flight while every thread adds its bucket's
+// entries of this chunk in order, four per step with their LDS loads issued
+// together.
+__global__ __launch_bounds__(256) void k_pbr_map_gather(PbrDev d) {
+    constexpr uint32_t kPer = kGatherChunk / 256u;            // position slots per thread
+    constexpr uint32_t kWords = (4u * kGatherChunk) / 8u + 1u;  // 16-byte entry words per chunk
+    constexpr uint32_t kWper = (kWords + 255u) / 256u;
+    static_assert(kWper == 3, "the entry words are staged in three registers per thread");
+    __shared__ float sw[4 * kGatherChunk];  // per slot and tap: the bilinear weight
+    __shared__ float4 sg[kGatherChunk];     // per slot: gy (xyz)
+    __shared__ uint4 sew[kWper * 256u];     // the chunk's entries from an aligned start
+    __shared__ uint32_t bvpx[kGatherBands], bbase[kGatherBands], bnpos[kGatherBands];
+    const uint16_t* se = (const uint16_t*)sew;
+    const GatherItem it = d.gitems[blockIdx.x];
+    const MapInfo mi = d.minfo[it.m];
+    const uint32_t tid = threadIdx.x;
+    if (tid < it.nb) {
+        const BandPos bp = band_pos(mi, it.vb0 + tid, d.S, d.bg_base);
+        bvpx[tid] = bp.v * d.S * d.S;
+        bbase[tid] = bp.pbase;
+        bnpos[tid] = bp.npos;
     }
-    const float4 g = make_float4(from_fixed(s0, d.fix_k), from_fixed(s1, d.fix_k),
-                                 from_fixed(s2, d.fix_k), 0.f);
-    if (irr) {
-        d.g_irr[i] = g;
-    } else {
-        d.g_pref[i - ni] = g;
+    __syncthreads();
+    const float fw = (float)mi.w, fh = (float)mi.h;
+    const float lod_scale = (float)(d.levels - 1), lvl = (float)mi.level;
+    const float4* uvsrc = mi.kind == 2 ? d.st0 : d.st2;
+    const float4* gsrc = mi.kind == 1 ? d.mgB : d.mgA;
+    const uint32_t nch = it.nch, P = it.P, nslot = it.nb * it.P;
+    const uint32_t* coff = d.coff + it.c0;
+    const bool mine = tid < it.na;
+    // this thread's position slots: band and position within the chunk
+    uint32_t sbi0, sbi1, sbi2, sbi3;
+    sbi0 = tid < nslot ? tid / P : 0u;
+    sbi1 = tid + 256u < nslot ? (tid + 256u) / P : 0u;
+    sbi2 = tid + 512u < nslot ? (tid + 512u) / P : 0u;
+    sbi3 = tid + 768u < nslot ? (tid + 768u) / P : 0u;
+    static_assert(kPer == 4, "four position slots per thread");
+    // chunk data in flight: positions, entry words, this bucket's entry range
+    float4 rs[kPer], rg[kPer];
+    bool rv[kPer];
+    uint4 rw0, rw1, rw2;
+    uint32_t rx0 = 0, rx1 = 0, ra0 = 0;
+#define DRESSI_GATHER_FETCH(CC)                                                                  \
+    {                                                                                            \
+        const uint32_t cc_ = (CC);                                                               \
+        _Pragma("unroll") for (uint32_t r = 0; r < kPer; r++) {                                  \
+            const uint32_t u = tid + 256u * r;                                                   \
+            const uint32_t bi = r == 0 ? sbi0 : (r == 1 ? sbi1 : (r == 2 ? sbi2 : sbi3));       \
+            const uint32_t pos = cc_ * P + (u - bi * P);                                         \
+            rv[r] = u < nslot && pos < bnpos[bi];                                                \
+            if (rv[r]) {                                                                         \
+                const size_t q = (size_t)bvpx[bi] +                                              \
+                                 (mi.kind == 2 ? d.bg_pix[bbase[bi] + pos] : bbase[bi] + pos);   \
+                rs[r] = uvsrc[q];                                                                \
+                rg[r] = gsrc[q];                                                                 \
+            }                                                                                    \
+        }                                                                                        \
+        const uint32_t run0_ = coff[cc_ * it.na];                                                \
+        const uint32_t run1_ = coff[(cc_ + 1) * it.na]; /* the next block's first: the end */   \
+        ra0 = run0_ & ~7u;                                                                       \
+        const uint32_t nw_ = (run1_ - ra0 + 7u) / 8u;                                            \
+        const uint4* src_ = (const uint4*)(d.mg_ent + ra0);                                      \
+        const uint4 z4_ = make_uint4(0u, 0u, 0u, 0u);                                            \
+        rw0 = tid < nw_ ? src_[tid] : z4_;                                                       \
+        rw1 = tid + 256u < nw_ ? src_[tid + 256u] : z4_;                                         \
+        rw2 = tid + 512u < nw_ ? src_[tid + 512u] : z4_;                                         \
+        rx0 = mine ? coff[cc_ * it.na + tid] : 0u;                                               \
+        rx1 = mine ? coff[cc_ * it.na + tid + 1] : 0u;                                           \
+    }
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+    if (nch > 0) {
+        DRESSI_GATHER_FETCH(0u)
+    }
+    for (uint32_t c = 0; c < nch; c++) {
+        __syncthreads();  // the previous chunk's readers are done
+#pragma unroll
+        for (uint32_t r = 0; r < kPer; r++) {
+            if (rv[r]) {
+                const uint32_t u = tid + 256u * r;
+                const float4 st = rs[r];
+                const float4 g = rg[r];
+                const float uu = mi.kind == 1 ? st.z : st.x;
+                const float vv = mi.kind == 1 ? st.w : st.y;
+                const float sx = uu * fw - 0.5f;
+                const float sy = vv * fh - 0.5f;
+                const float fx = sx - floorf(sx);
+                const float fy = sy - floorf(sy);
+                float g0 = g.x, g1 = g.y, g2 = g.z;
+                if (mi.kind == 1) {
+                    const float xl = 1.f - fabsf(g.w * lod_scale - lvl);
+                    const float wl = xl < 0.f ? 0.f : (xl > 1.f ? 1.f : xl);
+                    g0 = g0 * wl;
+                    g1 = g1 * wl;
+                    g2 = g2 * wl;
+                }
+                const float ex = 1.f - fx, ey = 1.f - fy;
+                sw[4u * u + 0u] = ex * ey;
+                sw[4u * u + 1u] = fx * ey;
+                sw[4u * u + 2u] = ex * fy;
+                sw[4u * u + 3u] = fx * fy;
+                sg[u] = make_float4(g0, g1, g2, 0.f);
+            }
+        }
+        sew[tid] = rw0;
+        sew[tid + 256u] = rw1;
+        sew[tid + 512u] = rw2;
+        const uint32_t x1 = rx1 - ra0;  // this bucket's entries in the staged words
+        uint32_t x = rx0 - ra0;
+        __syncthreads();
+        if (c + 1 < nch) {  // chunk c + 1's loads, in flight while this chunk is summed
+            DRESSI_GATHER_FETCH(c + 1u)
+        }
+        for (; x + 4u <= x1; x += 4u) {
+            float c0[4], c1[4], c2[4];
+#pragma unroll
+            for (uint32_t r = 0; r < 4; r++) {
+                const uint32_t e = se[x + r];
+                const float w = sw[e];
+                const float4 g = sg[e >> 2];
+                c0[r] = g.x * w;
+                c1[r] = g.y * w;
+                c2[r] = g.z * w;
+            }
+#pragma unroll
+            for (uint32_t r = 0; r < 4; r++) {
+                a0 += c0[r];
+                a1 += c1[r];
+                a2 += c2[r];
+            }
+        }
+        for (; x < x1; x++) {
+            const uint32_t e = se[x];
+            const float w = sw[e];
+            const float4 g = sg[e >> 2];
+            a0 += g.x * w;
+            a1 += g.y * w;
+            a2 += g.z * w;
+        }
+    }
+#undef DRESSI_GATHER_FETCH
+    if (mine) {
+        const uint32_t b = d.ml_order[it.a0 + tid];
+        const float4 res = make_float4(a0, a1, a2, 0.f);
+        if (mi.k == 1) {
+            const uint32_t t = (b - mi.bucket0) % mi.T;
+            const uint32_t v = (b - mi.bucket0) / mi.T;
+            d.mtot[mi.tot0 + v * mi.T + t] = res;
+        } else {
+            d.mpart[b] = res;
+        }
     }
 }
 
-// The convolutions' transposes (IrradianceConvBwd f_ops.cpp:2970-3004,
-// PrefilterConvBwd :3207-3262, every level onto the one pooled source): a
-// workgroup per group of <= 16 source texels, the threads split the map
-// texels.
-__global__ __launch_bounds__(256) void k_pbr_conv_bwd(PbrDev d) {
-    __shared__ float4 sd_s[kConvOuts];
-    __shared__ float red[5 * kConvOuts * 3];
-    const PbrGroup gr = d.bgroups[blockIdx.x];
-    const bool irr = gr.level == kIrrLevel;
-    const float4* sdir = irr ? d.isdir : d.psdir;
-    if (threadIdx.x < kConvOuts) {
-        sd_s[threadIdx.x] = threadIdx.x < gr.count ? sdir[gr.first + threadIdx.x]
-                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    __syncthreads();
-    float acc[kConvOuts][3];
+// TileSum (f_ops.cpp:2786-2821) of one (map, view) over a run of texels: from
+// 0, the band partials in band order. The workgroup stages rounds of
+// partials in LDS (coalesced), then one thread per texel adds them.
+__global__ __launch_bounds__(256) void k_pbr_tile_sum(PbrDev d) {
+    __shared__ float4 buf[kTileSumLds];
+    const uint4 wi = d.tsum_work[blockIdx.x];
+    const MapInfo mi = d.minfo[wi.x];
+    const uint32_t v = wi.y, t0 = wi.z, cnt = wi.w;
+    const uint32_t per = kTileSumLds / cnt;  // bands per round
+    const float4* part = d.mpart + mi.bucket0 + (size_t)v * mi.k * mi.T + t0;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+    for (uint32_t b0 = 0; b0 < mi.k; b0 += per) {
+        const uint32_t nb = mi.k - b0 < per ? mi.k - b0 : per;
+        // all of the round's loads in flight, then the LDS stores
+        constexpr uint32_t kPer = kTileSumLds / 256u;
+        float4 r[kPer];
 #pragma unroll
-    for (int o = 0; o < kConvOuts; o++) {
-        acc[o][0] = acc[o][1] = acc[o][2] = 0.f;
-    }
-    const uint32_t n_t = irr ? d.iw * d.ih : d.n_pref;
-    const float4* tdir = irr ? d.idir : d.pdir;
-    const float4* tg = irr ? d.g_irr : d.g_pref;
-    // the next texel's direction, gradient and norm are loaded before the
-    // current one is used (the loop is bound by these loads' latency)
-    float4 r_n = make_float4(0.f, 0.f, 0.f, 0.f), g_n = r_n;
-    float nt_n = 1.f;
-    if (threadIdx.x < n_t) {
-        r_n = tdir[threadIdx.x];
-        g_n = tg[threadIdx.x];
-        nt_n = irr ? 1.f : d.pnorm[threadIdx.x];
-    }
-    for (uint32_t t = threadIdx.x; t < n_t; t += blockDim.x) {
-        const float4 r = r_n;
-        const float4 g = g_n;
-        const float nt = nt_n;
-        const uint32_t tn = t + blockDim.x;
-        if (tn < n_t) {
-            r_n = tdir[tn];
-            g_n = tg[tn];
-            nt_n = irr ? 1.f : d.pnorm[tn];
+        for (uint32_t u = 0; u < kPer; u++) {
+            const uint32_t j = threadIdx.x + u * 256u;
+            r[u] = j < nb * cnt ? part[(size_t)(b0 + j / cnt) * mi.T + j % cnt]
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        if (g.x == 0.f && g.y == 0.f && g.z == 0.f) {
-            continue;
-        }
-        float inv = 1.f;
-        if (!irr) {
-            inv = nt > 1e-12f ? nt : 1e-12f;
-        }
+        __syncthreads();
 #pragma unroll
-        for (int o = 0; o < kConvOuts; o++) {
-            const float4 s = sd_s[o];
-            const float c = r.x * s.x + r.y * s.y + r.z * s.z;
-            if (c > 0.f) {
-                const float w = irr ? c * s.w : ggx_conv_weight(c, r.w) / inv;
-                acc[o][0] += g.x * w;
-                acc[o][1] += g.y * w;
-                acc[o][2] += g.z * w;
+        for (uint32_t u = 0; u < kPer; u++) {
+            buf[threadIdx.x + u * 256u] = r[u];
+        }
+        __syncthreads();
+        if (threadIdx.x < cnt) {
+            for (uint32_t band = 0; band < nb; band++) {
+                const float4 q = buf[band * cnt + threadIdx.x];
+                a0 += q.x;
+                a1 += q.y;
+                a2 += q.z;
             }
         }
     }
-    block_reduce_outs(acc, red);
-    if (threadIdx.x < gr.count) {
-        const float* v = red + 4 * kConvOuts * 3 + threadIdx.x * 3;
-        const uint32_t o = gr.first + threadIdx.x;
-        if (irr) {
-            d.g_isrc[o] = make_float4(v[0] * d.irr_scale, v[1] * d.irr_scale,
-                                      v[2] * d.irr_scale, 0.f);
-        } else {
-            const float st = sd_s[threadIdx.x].w;
-            d.g_psrc[o] = make_float4(v[0] * st, v[1] * st, v[2] * st, 0.f);
+    if (threadIdx.x < cnt) {
+        d.mtot[mi.tot0 + v * mi.T + t0 + threadIdx.x] = make_float4(a0, a1, a2, 0.f);
+    }
+}
+
+// The map gradients: per texel, the views' VJP results added in view order
+// from 0 (the irradiance map, every prefilter level, the background env).
+__global__ __launch_bounds__(256) void k_pbr_view_sum(PbrDev d) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t ni = d.iw * d.ih, ne = d.ew * d.eh;
+    if (i >= ni + d.n_pref + ne) {
+        return;
+    }
+    float4* out;
+    uint32_t m, t;
+    if (i < ni) {
+        m = 0;
+        t = i;
+        out = d.g_irr + t;
+    } else if (i < ni + d.n_pref) {
+        const uint32_t j = i - ni;
+        m = 1;
+        while (m < d.levels && j >= d.loff[m]) {
+            m++;
         }
+        t = j - d.loff[m - 1];
+        out = d.g_pref + j;
+    } else {
+        m = d.levels + 1;
+        t = i - ni - d.n_pref;
+        out = d.g_bg + t;
+    }
+    const MapInfo mi = d.minfo[m];
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+    for (uint32_t v = 0; v < d.n_views; v++) {
+        const float4 q = d.mtot[mi.tot0 + v * mi.T + t];
+        a0 += q.x;
+        a1 += q.y;
+        a2 += q.z;
+    }
+    *out = make_float4(a0, a1, a2, 0.f);
+}
+
+// The convolutions' transposes (IrradianceConvBwd f_ops.cpp:2970-3004,
+// PrefilterConvBwd :3207-3262): per pooled source texel s, irradiance
+// (sum_o g[o] w(o, s)) * 2 pi / (sw sh); prefilter, per level in order,
+// (sum_t g[t] w(t, s) / max(norm[t], 1e-12)) * sin(theta_s), the levels
+// added in level order from 0. Sums over the map texels in raster order;
+// static weights wb_* [map texel][source]; wave c computes channel c.
+__global__ __launch_bounds__(192) void k_pbr_conv_bwd(PbrDev d) {
+    __shared__ MvLds L;
+    const bool irr = blockIdx.x < d.n_isg;
+    const uint32_t n_src = irr ? d.isw * d.ish : d.psw * d.psh;
+    const uint32_t col0 = (irr ? blockIdx.x : blockIdx.x - d.n_isg) * kMvCols;
+    const uint32_t s = col0 + (threadIdx.x & 63u);
+    const uint32_t c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool ok = s < n_src;
+    if (irr) {
+        const float acc = mv_segment(L, d.wb_irr + (size_t)col0 * (d.iw * d.ih), d.g_irr, 0,
+                                     d.iw * d.ih);
+        if (ok) {
+            ((float*)d.g_isrc)[(size_t)s * 4 + c] = acc * d.irr_scale;
+        }
+        return;
+    }
+    const float st = d.psdir[ok ? s : 0u].w;
+    float a = 0.f;
+    for (uint32_t i = 0; i < d.levels; i++) {
+        const float t = mv_segment(L, d.wb_pref + (size_t)col0 * d.n_pref, d.g_pref, d.loff[i],
+                                   d.loff[i] + d.lw[i] * d.lh[i]);
+        a += t * st;
+    }
+    if (ok) {
+        ((float*)d.g_psrc)[(size_t)s * 4 + c] = a;
     }
 }
 
@@ -1029,17 +1301,18 @@ __device__ __forceinline__ void adam3(const PbrDev& d, float bc1, float bc2, con
     *v4 = make_float4(vi[0], vi[1], vi[2], 0.f);
 }
 
-// Per env texel: the background gradient, the pooling chains' VJPs
-// (UpsampleNearest2x of gy * 0.25 per level, f_ops.cpp:958-994) of the
-// irradiance and prefilter sources, their sum, Adam (env >= 0).
+// Per env texel: the background gradient (view sums of the env VJP), then
+// the pooling chains' VJPs (UpsampleNearest2x of gy * 0.25 per level,
+// f_ops.cpp:958-994) of the irradiance and of the prefilter source added in
+// that order, Adam (env >= 0).
 __global__ __launch_bounds__(256) void k_pbr_env_adam(PbrDev d) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= d.ew * d.eh) {
         return;
     }
     const uint32_t x = i % d.ew, y = i / d.ew;
-    const unsigned long long* a = d.acc_env + (size_t)i * 3;
-    float g[3] = {from_fixed(a[0], d.fix_k), from_fixed(a[1], d.fix_k), from_fixed(a[2], d.fix_k)};
+    const float4 gb = d.g_bg[i];
+    float g[3] = {gb.x, gb.y, gb.z};
     {
         const uint32_t sx = x >> d.irr_pool, sy = y >> d.irr_pool;
         const float4 q = d.g_isrc[sy * d.isw + sx];
@@ -1074,25 +1347,44 @@ __global__ __launch_bounds__(256) void k_pbr_env_adam(PbrDev d) {
     adam3(d, bc1, bc2, g, &d.env[i], &d.em[i], &d.ev[i], false);
 }
 
-// Per texel: the static gather list (GatherByInverseUVBilinear over every
-// view) of the per-pixel material gradients, Adam on albedo and mr.
+// Per texel: the static gather list (GatherByInverseUVBilinear, view by
+// view: each view's window sum from 0, then the views added in order), Adam
+// on albedo and mr.
 __global__ __launch_bounds__(256) void k_pbr_tex_adam(PbrDev d) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= d.tw * d.th) {
         return;
     }
+    const uint32_t npx = d.S * d.S;
     float ga[3] = {0.f, 0.f, 0.f}, gr = 0.f, gm = 0.f;
+    float pa[3] = {0.f, 0.f, 0.f}, pr = 0.f, pm = 0.f;
     const uint32_t e0 = d.csr_off[i], e1 = d.csr_off[i + 1];
+    uint32_t view = e0 < e1 ? d.csr[e0].x / npx : 0u;
     for (uint32_t e = e0; e < e1; e++) {
         const uint2 en = d.csr[e];
+        const uint32_t ev = en.x / npx;
+        if (ev != view) {
+            ga[0] += pa[0];
+            ga[1] += pa[1];
+            ga[2] += pa[2];
+            gr += pr;
+            gm += pm;
+            pa[0] = pa[1] = pa[2] = pr = pm = 0.f;
+            view = ev;
+        }
         const float w = __uint_as_float(en.y);
         const float4 g = d.gyA[en.x];
-        ga[0] += g.x * w;
-        ga[1] += g.y * w;
-        ga[2] += g.z * w;
-        gr += g.w * w;
-        gm += d.gyM[en.x] * w;
+        pa[0] += g.x * w;
+        pa[1] += g.y * w;
+        pa[2] += g.z * w;
+        pr += g.w * w;
+        pm += d.gyM[en.x] * w;
     }
+    ga[0] += pa[0];
+    ga[1] += pa[1];
+    ga[2] += pa[2];
+    gr += pr;
+    gm += pm;
     const float gmr[3] = {0.f, gr, gm};
     if (d.g_tex_a) {
         d.g_tex_a[i] = make_float4(ga[0], ga[1], ga[2], 0.f);
@@ -1134,10 +1426,16 @@ __global__ __launch_bounds__(256) void k_pbr_loss(PbrDev d, uint32_t n_part) {
 }
 
 // Kernel list of one iteration (the pooling chain counts as one entry)
-constexpr int kPbrKernels = 8;
+constexpr int kPbrKernels = 10;
 const char* const kPbrKernelNames[kPbrKernels] = {
-        "k_pbr_pool", "k_pbr_conv_fwd", "k_pbr_shade", "k_pbr_resolve",
-        "k_pbr_conv_bwd", "k_pbr_env_adam", "k_pbr_tex_adam", "k_pbr_loss"};
+        "k_pbr_pool",     "k_pbr_conv_fwd", "k_pbr_shade",    "k_pbr_map_gather",
+        "k_pbr_tile_sum", "k_pbr_view_sum", "k_pbr_conv_bwd", "k_pbr_env_adam",
+        "k_pbr_tex_adam", "k_pbr_loss"};
+// index of each kernel in the launch switch
+enum PbrK {
+    kKPool = 0, kKConvFwd, kKShade, kKGather, kKTileSum, kKViewSum, kKConvBwd, kKEnvAdam,
+    kKTexAdam, kKLoss
+};
 
 uint32_t shade_blocks(const PbrDev& d) {
     const uint32_t tiles = (d.S + kShadeTile - 1) / kShadeTile;
@@ -1146,41 +1444,45 @@ uint32_t shade_blocks(const PbrDev& d) {
 
 int launch_pbr_kernel(const PbrDev& d, hipStream_t s, int k) {
     switch (k) {
-        case 0:
+        case kKPool:
             for (uint32_t l = 1; l <= d.n_pool; l++) {
                 const uint32_t n = d.pw[l] * d.ph[l];
-                const uint32_t blocks = std::max(div_up(n, 256), l == 1 ? 512u : 1u);
-                hipLaunchKernelGGL(k_pbr_pool, dim3(blocks), dim3(256), 0, s, d, l);
-                DRESSI_CHECK_LAUNCH();
-            }
-            if (d.n_pool == 0) {
-                // no pooling level: clear the accumulators with a level-1
-                // launch that pools nothing
-                PbrDev z = d;
-                z.pw[1] = 0;
-                z.ph[1] = 0;
-                hipLaunchKernelGGL(k_pbr_pool, dim3(512), dim3(256), 0, s, z, 1u);
+                hipLaunchKernelGGL(k_pbr_pool, dim3(div_up(n, 256)), dim3(256), 0, s, d, l);
                 DRESSI_CHECK_LAUNCH();
             }
             return DRESSI_OK;
-        case 1:
-            hipLaunchKernelGGL(k_pbr_conv_fwd, dim3(d.n_fgroups), dim3(256), 0, s, d);
+        case kKConvFwd:
+            hipLaunchKernelGGL(k_pbr_conv_fwd, dim3(d.n_ig + d.n_pg), dim3(kMvThreads), 0, s, d);
             break;
-        case 2:
+        case kKShade:
             hipLaunchKernelGGL(k_pbr_shade, dim3(shade_blocks(d)), dim3(256), 0, s, d);
             break;
-        case 3:
-            hipLaunchKernelGGL(k_pbr_resolve, dim3(div_up(d.iw * d.ih + d.n_pref, 256)),
-                               dim3(256), 0, s, d);
+        case kKGather:
+            if (d.n_gitems == 0) {
+                return DRESSI_OK;
+            }
+            hipLaunchKernelGGL(k_pbr_map_gather, dim3(d.n_gitems), dim3(256), 0, s, d);
             break;
-        case 4:
-            hipLaunchKernelGGL(k_pbr_conv_bwd, dim3(d.n_bgroups), dim3(256), 0, s, d);
+        case kKTileSum:
+            if (d.n_tsum == 0) {
+                return DRESSI_OK;
+            }
+            hipLaunchKernelGGL(k_pbr_tile_sum, dim3(d.n_tsum), dim3(256), 0, s, d);
             break;
-        case 5:
+        case kKViewSum:
+            hipLaunchKernelGGL(k_pbr_view_sum,
+                               dim3(div_up(d.iw * d.ih + d.n_pref + d.ew * d.eh, 256)), dim3(256),
+                               0, s, d);
+            break;
+        case kKConvBwd:
+            hipLaunchKernelGGL(k_pbr_conv_bwd, dim3(d.n_isg + d.n_psg), dim3(kMvThreads), 0, s,
+                               d);
+            break;
+        case kKEnvAdam:
             hipLaunchKernelGGL(k_pbr_env_adam, dim3(div_up(d.ew * d.eh, 256)), dim3(256), 0, s,
                                d);
             break;
-        case 6:
+        case kKTexAdam:
             hipLaunchKernelGGL(k_pbr_tex_adam, dim3(div_up(d.tw * d.th, 256)), dim3(256), 0, s,
                                d);
             break;
@@ -1202,12 +1504,14 @@ struct dressi_pbr_plan {
     dressi_pbr_desc desc{};
     PbrDev d{};
     std::vector<void*> allocs;
-    std::vector<PbrGroup> fgroups, bgroups;
     bool scene_set = false, target_set = false, state_set = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     hipStream_t graph_stream = nullptr;
     uint32_t csr_len = 0;
+    uint64_t ml_len = 0;  // map-gradient gather list entries
+    // set_scene's allocations (freed when the scene is set again)
+    std::vector<void*> scene_allocs;
 };
 
 namespace {
@@ -1256,23 +1560,24 @@ int pbr_enqueue(dressi_pbr_plan* p, hipStream_t s) {
 }
 
 // One iteration for graph capture: after the shading, the texture gather +
-// Adam runs on `side` beside the environment's chain (resolve, transposed
-// convolutions, env Adam): the two read and write disjoint buffers (both
-// only read t), and both join before the loss kernel advances t.
+// Adam runs on `side` beside the environment's chain (map gathers, tile and
+// view sums, transposed convolutions, env Adam): the two read and write
+// disjoint buffers (both only read t), and both join before the loss kernel
+// advances t.
 int pbr_enqueue_forked(dressi_pbr_plan* p, hipStream_t s, hipStream_t side, hipEvent_t fork,
                        hipEvent_t join) {
-    for (int k = 0; k <= 2; k++) {  // pool, conv_fwd, shade
+    for (int k : {kKPool, kKConvFwd, kKShade}) {
         if (int rc = launch_pbr_kernel(p->d, s, k)) return rc;
     }
     DRESSI_TRY_HIP(hipEventRecord(fork, s));
     DRESSI_TRY_HIP(hipStreamWaitEvent(side, fork, 0));
-    if (int rc = launch_pbr_kernel(p->d, side, 6)) return rc;  // tex_adam
+    if (int rc = launch_pbr_kernel(p->d, side, kKTexAdam)) return rc;
     DRESSI_TRY_HIP(hipEventRecord(join, side));
-    for (int k = 3; k <= 5; k++) {  // resolve, conv_bwd, env_adam
+    for (int k : {kKGather, kKTileSum, kKViewSum, kKConvBwd, kKEnvAdam}) {
         if (int rc = launch_pbr_kernel(p->d, s, k)) return rc;
     }
     DRESSI_TRY_HIP(hipStreamWaitEvent(s, join, 0));
-    return launch_pbr_kernel(p->d, s, 7);  // loss, t + 1
+    return launch_pbr_kernel(p->d, s, kKLoss);
 }
 
 // host VEC3 {n} -> device float4 {n} (w = 0)
@@ -1294,13 +1599,6 @@ int download3(float* dst, const float4* src, size_t n) {
         dst[i * 3 + 2] = v[i].z;
     }
     return DRESSI_OK;
-}
-
-// Output groups of <= kConvOuts texels, never spanning two maps
-void make_groups(std::vector<PbrGroup>& out, uint32_t first, uint32_t count, uint32_t level) {
-    for (uint32_t o = 0; o < count; o += kConvOuts) {
-        out.push_back(PbrGroup{first + o, std::min<uint32_t>(kConvOuts, count - o), level});
-    }
 }
 
 // The IBL pass of the target: the env's pooled sources and maps through the
@@ -1330,18 +1628,11 @@ int render_target(dressi_pbr_plan* p, const float* gt_env) {
     t.irr = (float4*)q;
     if (!rc) rc = talloc(&q, sizeof(float4) * t.n_pref);
     t.pref = (float4*)q;
-    // accumulators of the target pass: throw-away
-    if (!rc) rc = talloc(&q, sizeof(unsigned long long) * 3 * t.iw * t.ih);
-    t.acc_irr = (unsigned long long*)q;
-    if (!rc) rc = talloc(&q, sizeof(unsigned long long) * 3 * t.n_pref);
-    t.acc_pref = (unsigned long long*)q;
-    if (!rc) rc = talloc(&q, sizeof(unsigned long long) * 3 * ne);
-    t.acc_env = (unsigned long long*)q;
     t.target_mode = 1;
     hipStream_t s = p->ctx->stream;
-    if (!rc) rc = launch_pbr_kernel(t, s, 0);
-    if (!rc) rc = launch_pbr_kernel(t, s, 1);
-    if (!rc) rc = launch_pbr_kernel(t, s, 2);
+    if (!rc) rc = launch_pbr_kernel(t, s, kKPool);
+    if (!rc) rc = launch_pbr_kernel(t, s, kKConvFwd);
+    if (!rc) rc = launch_pbr_kernel(t, s, kKShade);
     hipError_t e = hipStreamSynchronize(s);
     for (void* b : tmp) hipFree(b);
     if (!rc && e != hipSuccess) {
@@ -1349,6 +1640,377 @@ int render_target(dressi_pbr_plan* p, const float* gt_env) {
         rc = DRESSI_ERR_HIP;
     }
     return rc;
+}
+
+// Static gather lists of the map-gradient VJPs (see k_pbr_map_gather) and the
+// bookkeeping of their sums: per map the EquirectSampleBwd layout, every
+// (view, pixel, map, tap) entry keyed by its bucket, a stable radix sort
+// (pixel order kept within a bucket), bucket offsets from the counts, the
+// tile-sum work items. Allocations go to p->scene_allocs.
+int build_map_lists(dressi_pbr_plan* p) {
+    PbrDev& d = p->d;
+    hipStream_t s = p->ctx->stream;
+    const uint32_t N = d.n_views, S = d.S;
+    const size_t npx = (size_t)S * S;
+    for (void* q : p->scene_allocs) hipFree(q);
+    p->scene_allocs.clear();
+    auto salloc = [&](void** q, size_t b) -> int {
+        DRESSI_TRY_HIP(hipMalloc(q, b ? b : 4));
+        p->scene_allocs.push_back(*q);
+        return DRESSI_OK;
+    };
+    // EquirectSampleBwd's band count for a map of w x h over S dir rows
+    const auto bands = [&](uint32_t w, uint32_t h) {
+        uint32_t k = 1;
+        while ((size_t)w * h * k < 65536 && k < S) {
+            k *= 2;
+        }
+        return k;
+    };
+    std::vector<MapInfo> mis;
+    uint64_t nb = 0, nt = 0;
+    const auto add = [&](uint32_t w, uint32_t h, uint32_t kind, uint32_t level) {
+        MapInfo m{};
+        m.w = w;
+        m.h = h;
+        m.T = w * h;
+        m.k = bands(w, h);
+        m.rows = (S + m.k - 1) / m.k;
+        m.bucket0 = (uint32_t)nb;
+        m.tot0 = (uint32_t)nt;
+        m.kind = kind;
+        m.level = level;
+        nb += (uint64_t)N * m.k * m.T;
+        nt += (uint64_t)N * m.T;
+        mis.push_back(m);
+    };
+    add(d.iw, d.ih, 0, 0);
+    for (uint32_t i = 0; i < d.levels; i++) {
+        add(d.lw[i], d.lh[i], 1, i);
+    }
+    add(d.ew, d.eh, 2, 0);
+    DRESSI_REQUIRE(nb < (1ull << 31), "too many map-gradient buckets");
+    uint32_t key_bits = 1;
+    while ((1ull << key_bits) <= nb) {
+        key_bits++;
+    }
+    const uint32_t n_maps = (uint32_t)mis.size();
+    const size_t items = (size_t)N * npx * n_maps * 4;
+    int rc = DRESSI_OK;
+    void *minfo = nullptr, *off = nullptr, *part = nullptr, *tot = nullptr, *work = nullptr;
+    if (!rc) rc = salloc(&minfo, sizeof(MapInfo) * n_maps);
+    if (!rc) rc = salloc(&part, sizeof(float4) * nb);
+    if (!rc) rc = salloc(&tot, sizeof(float4) * nt);
+    if (!rc) rc = salloc(&off, sizeof(uint32_t) * (nb + 1));
+    if (rc) return rc;
+    DRESSI_TRY_HIP(hipMemcpy(minfo, mis.data(), sizeof(MapInfo) * n_maps, hipMemcpyHostToDevice));
+    // temporaries: keys / values (two copies for the sort), counts, sort scratch
+    std::vector<void*> tmp;
+    auto talloc = [&](void** q, size_t b) -> int {
+        DRESSI_TRY_HIP(hipMalloc(q, b ? b : 4));
+        tmp.push_back(*q);
+        return DRESSI_OK;
+    };
+    // background pixels that sample the env, per view (the env lists'
+    // positions)
+    std::vector<uint32_t> n_bg(N, 0), bg_base(N + 1, 0);
+    void *bgflag = nullptr, *bgidx = nullptr, *bgscr = nullptr, *bgpix = nullptr;
+    if (!rc) rc = talloc(&bgflag, sizeof(uint32_t) * N * npx);
+    if (!rc) rc = talloc(&bgidx, sizeof(uint32_t) * N * npx);
+    if (!rc) {
+        size_t sb = 0;
+        hipLaunchKernelGGL(k_pbr_bg_flags, dim3(div_up((uint32_t)(N * npx), 256)), dim3(256), 0, s,
+                           d.st0, (size_t)N * npx, (uint32_t*)bgflag);
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) {
+            e = hipcub::DeviceScan::ExclusiveSum(nullptr, sb, (const uint32_t*)bgflag,
+                                                 (uint32_t*)bgidx, (int)npx, s);
+        }
+        if (e == hipSuccess) e = hipMalloc(&bgscr, sb ? sb : 4);
+        if (e == hipSuccess) tmp.push_back(bgscr);
+        for (uint32_t v = 0; v < N && e == hipSuccess; v++) {
+            e = hipcub::DeviceScan::ExclusiveSum(bgscr, sb, (const uint32_t*)bgflag + v * npx,
+                                                 (uint32_t*)bgidx + v * npx, (int)npx, s);
+            uint32_t last[2] = {0, 0};
+            if (e == hipSuccess) {
+                e = hipMemcpyAsync(&last[0], (uint32_t*)bgidx + v * npx + npx - 1, 4,
+                                   hipMemcpyDeviceToHost, s);
+            }
+            if (e == hipSuccess) {
+                e = hipMemcpyAsync(&last[1], (uint32_t*)bgflag + v * npx + npx - 1, 4,
+                                   hipMemcpyDeviceToHost, s);
+            }
+            if (e == hipSuccess) e = hipStreamSynchronize(s);
+            n_bg[v] = last[0] + last[1];
+            bg_base[v + 1] = bg_base[v] + n_bg[v];
+        }
+        if (e != hipSuccess) {
+            set_error("background pixel lists failed: %s", hipGetErrorString(e));
+            rc = DRESSI_ERR_HIP;
+        }
+    }
+    if (!rc) rc = salloc(&bgpix, sizeof(uint32_t) * bg_base[N]);
+    void* bgbase = nullptr;
+    if (!rc) rc = salloc(&bgbase, sizeof(uint32_t) * (N + 1));
+    if (!rc && hipMemcpy(bgbase, bg_base.data(), sizeof(uint32_t) * (N + 1),
+                         hipMemcpyHostToDevice) != hipSuccess) {
+        set_error("background pixel bases upload failed");
+        rc = DRESSI_ERR_HIP;
+    }
+    for (uint32_t v = 0; v < N && !rc; v++) {
+        hipLaunchKernelGGL(k_pbr_bg_fill, dim3(div_up((uint32_t)npx, 256)), dim3(256), 0, s,
+                           (const uint32_t*)bgflag + v * npx, (const uint32_t*)bgidx + v * npx,
+                           (uint32_t)npx, bg_base[v], (uint32_t*)bgpix);
+    }
+    void *k0 = nullptr, *k1 = nullptr, *v0 = nullptr, *v1 = nullptr, *cnt = nullptr, *scr = nullptr;
+    if (!rc) rc = talloc(&k0, sizeof(uint32_t) * items);
+    if (!rc) rc = talloc(&k1, sizeof(uint32_t) * items);
+    if (!rc) rc = talloc(&v0, sizeof(uint32_t) * items);
+    if (!rc) rc = talloc(&v1, sizeof(uint32_t) * items);
+    if (!rc) rc = talloc(&cnt, sizeof(uint32_t) * nb);
+    size_t scr_bytes = 0;
+    if (!rc) {
+        hipError_t e = hipMemsetAsync(cnt, 0, sizeof(uint32_t) * nb, s);
+        ListArgs la{};
+        la.st0 = d.st0;
+        la.st2 = d.st2;
+        la.minfo = (const MapInfo*)minfo;
+        la.n_maps = n_maps;
+        la.n_views = N;
+        la.S = S;
+        la.no_key = (uint32_t)((1ull << key_bits) - 1);
+        la.bg_idx = (const uint32_t*)bgidx;
+        la.keys = (uint32_t*)k0;
+        la.vals = (uint32_t*)v0;
+        la.count = (uint32_t*)cnt;
+        if (e == hipSuccess) {
+            hipLaunchKernelGGL(k_pbr_list_keys, dim3(div_up((uint32_t)(N * npx), 256)), dim3(256), 0,
+                               s, la);
+            e = hipGetLastError();
+        }
+        if (e == hipSuccess) {
+            e = hipcub::DeviceRadixSort::SortPairs(nullptr, scr_bytes, (const uint32_t*)k0,
+                                                   (uint32_t*)k1, (const uint32_t*)v0,
+                                                   (uint32_t*)v1, (int)items, 0, (int)key_bits, s);
+        }
+        if (e != hipSuccess) {
+            set_error("map gather list keys failed: %s", hipGetErrorString(e));
+            rc = DRESSI_ERR_HIP;
+        }
+    }
+    if (!rc) rc = talloc(&scr, scr_bytes);
+    std::vector<uint32_t> c(nb), o(nb + 1);
+    if (!rc) {
+        hipError_t e = hipcub::DeviceRadixSort::SortPairs(
+                scr, scr_bytes, (const uint32_t*)k0, (uint32_t*)k1, (const uint32_t*)v0,
+                (uint32_t*)v1, (int)items, 0, (int)key_bits, s);
+        if (e == hipSuccess) e = hipMemcpyAsync(c.data(), cnt, sizeof(uint32_t) * nb,
+                                                hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) {
+            set_error("map gather list sort failed: %s", hipGetErrorString(e));
+            rc = DRESSI_ERR_HIP;
+        }
+    }
+    uint64_t total = 0;
+    if (!rc) {
+        for (size_t i = 0; i < nb; i++) {
+            o[i] = (uint32_t)total;
+            total += c[i];
+        }
+        o[nb] = (uint32_t)total;
+        if (total >= (1ull << 32)) {
+            set_error("map gather lists too long (%llu entries)", (unsigned long long)total);
+            rc = DRESSI_ERR_UNSUPPORTED;
+        }
+    }
+    void* ent = v1;  // the sorted entries (set-up only)
+    if (!rc) {
+        hipError_t e = hipMemcpyAsync(off, o.data(), sizeof(uint32_t) * (nb + 1),
+                                      hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) {
+            set_error("map gather list fill failed: %s", hipGetErrorString(e));
+            rc = DRESSI_ERR_HIP;
+        }
+    }
+    // the gather's workgroups: per (map, view, band) its non-empty buckets in
+    // bucket order, at most kGatherChains per workgroup, over the band's
+    // positions; the longest first. Then the per-chunk entry runs: first
+    // entries and counts per (item, chunk, bucket), their exclusive scan in
+    // item / chunk / bucket order, the entries copied there. The partials of
+    // the empty buckets stay 0 (cleared here).
+    void *order = nullptr, *gbuf = nullptr, *coff = nullptr, *ment = nullptr;
+    std::vector<GatherItem> gi;
+    if (!rc) {
+        std::vector<uint32_t> ord;
+        uint64_t n_fo = 0, n_c = 0;
+        // the positions of (view, band) vb, as band_pos derives them
+        const auto band_npos = [&](const MapInfo& mi, uint32_t vb) -> uint32_t {
+            if (mi.kind == 2) {
+                return n_bg[vb / mi.k];
+            }
+            const uint32_t band = vb % mi.k;
+            const uint32_t r0 = std::min(band * mi.rows, S);
+            const uint32_t r1 = std::min(r0 + mi.rows, S);
+            return (r1 - r0) * S;
+        };
+        GatherItem cur{};
+        uint32_t cur_max = 0;
+        const auto flush = [&]() {
+            if (cur.na == 0) {
+                cur = GatherItem{};
+                cur_max = 0;
+                return;
+            }
+            cur.P = kGatherChunk / cur.nb;
+            cur.nch = (cur_max + cur.P - 1) / cur.P;
+            cur.c0 = (uint32_t)n_c;
+            cur.f0 = (uint32_t)n_fo;
+            n_c += (uint64_t)cur.nch * cur.na;
+            n_fo += (uint64_t)(cur.nch + 1) * cur.na;
+            gi.push_back(cur);
+            cur = GatherItem{};
+            cur_max = 0;
+        };
+        for (uint32_t m = 0; m < n_maps; m++) {
+            const MapInfo& mi = mis[m];
+            for (uint32_t vb = 0; vb < N * mi.k; vb++) {
+                const uint64_t b0 = mi.bucket0 + (uint64_t)vb * mi.T;
+                const uint32_t first = (uint32_t)ord.size();
+                for (uint32_t t = 0; t < mi.T; t++) {
+                    if (c[b0 + t]) ord.push_back((uint32_t)(b0 + t));
+                }
+                const uint32_t n_here = (uint32_t)ord.size() - first;
+                const uint32_t npos = band_npos(mi, vb);
+                if (n_here == 0) {
+                    flush();  // a workgroup's bands are consecutive and non-empty
+                    continue;
+                }
+                if (n_here > kGatherChains) {
+                    // a band of its own, split into workgroups of kGatherChains
+                    flush();
+                    for (uint32_t a = 0; a < n_here; a += kGatherChains) {
+                        cur.m = m;
+                        cur.vb0 = vb;
+                        cur.nb = 1;
+                        cur.a0 = first + a;
+                        cur.na = std::min(kGatherChains, n_here - a);
+                        cur_max = npos;
+                        flush();
+                    }
+                    continue;
+                }
+                if (cur.na + n_here > kGatherChains || cur.nb == kGatherBands) {
+                    flush();
+                }
+                if (cur.na == 0) {
+                    cur.m = m;
+                    cur.vb0 = vb;
+                    cur.a0 = first;
+                }
+                cur.nb++;
+                cur.na += n_here;
+                cur_max = std::max(cur_max, npos);
+            }
+            flush();
+        }
+        if (n_fo >= (1ull << 31)) {
+            set_error("map gather chunk tables too large");
+            rc = DRESSI_ERR_UNSUPPORTED;
+        }
+        std::stable_sort(gi.begin(), gi.end(), [](const GatherItem& x, const GatherItem& y) {
+            return x.nch > y.nch;
+        });
+        uint32_t max_na = 1;
+        for (const GatherItem& g : gi) max_na = std::max(max_na, g.na);
+        void *fo = nullptr, *ccnt = nullptr, *cscr = nullptr;
+        if (!rc) rc = salloc(&order, sizeof(uint32_t) * std::max<size_t>(ord.size(), 1));
+        if (!rc) rc = salloc(&gbuf, sizeof(GatherItem) * std::max<size_t>(gi.size(), 1));
+        if (!rc) rc = salloc(&coff, sizeof(uint32_t) * (n_c + 1));
+        if (!rc) rc = salloc(&ment, sizeof(uint16_t) * (total + 16));  // + the last 16-byte word
+        if (!rc) rc = talloc(&fo, sizeof(uint32_t) * n_fo);
+        if (!rc) rc = talloc(&ccnt, sizeof(uint32_t) * (n_c + 1));
+        size_t cs_bytes = 0;
+        if (!rc) {
+            hipError_t e = hipMemcpy(order, ord.data(), sizeof(uint32_t) * ord.size(),
+                                     hipMemcpyHostToDevice);
+            if (e == hipSuccess) e = hipMemcpy(gbuf, gi.data(), sizeof(GatherItem) * gi.size(),
+                                               hipMemcpyHostToDevice);
+            if (e == hipSuccess) e = hipMemset(part, 0, sizeof(float4) * nb);
+            if (e == hipSuccess) e = hipMemset(tot, 0, sizeof(float4) * nt);
+            if (e == hipSuccess) e = hipMemset((uint32_t*)ccnt + n_c, 0, sizeof(uint32_t));
+            if (e == hipSuccess && !gi.empty()) {
+                hipLaunchKernelGGL(k_pbr_chunk_first,
+                                   dim3(div_up(max_na, 256), (uint32_t)gi.size()), dim3(256), 0,
+                                   s, (const GatherItem*)gbuf, (uint32_t)gi.size(),
+                                   (const MapInfo*)minfo, S, (const uint32_t*)bgbase,
+                                   (const uint32_t*)order, (const uint32_t*)off,
+                                   (const uint32_t*)ent, (uint32_t*)fo, (uint32_t*)ccnt);
+                e = hipGetLastError();
+            }
+            if (e == hipSuccess) {
+                e = hipcub::DeviceScan::ExclusiveSum(nullptr, cs_bytes, (const uint32_t*)ccnt,
+                                                     (uint32_t*)coff, (int)(n_c + 1), s);
+            }
+            if (e == hipSuccess) e = hipMalloc(&cscr, cs_bytes ? cs_bytes : 4);
+            if (e == hipSuccess) {
+                tmp.push_back(cscr);
+                e = hipcub::DeviceScan::ExclusiveSum(cscr, cs_bytes, (const uint32_t*)ccnt,
+                                                     (uint32_t*)coff, (int)(n_c + 1), s);
+            }
+            if (e == hipSuccess && !gi.empty()) {
+                hipLaunchKernelGGL(k_pbr_chunk_fill,
+                                   dim3(div_up(max_na, 256), (uint32_t)gi.size()), dim3(256), 0,
+                                   s, (const GatherItem*)gbuf, (uint32_t)gi.size(),
+                                   (const MapInfo*)minfo, S, (const uint32_t*)bgbase,
+                                   (const uint32_t*)order, (const uint32_t*)ent,
+                                   (const uint32_t*)fo, (const uint32_t*)coff, (uint16_t*)ment);
+                e = hipGetLastError();
+            }
+            if (e == hipSuccess) e = hipStreamSynchronize(s);
+            if (e != hipSuccess) {
+                set_error("map gather work set-up failed: %s", hipGetErrorString(e));
+                rc = DRESSI_ERR_HIP;
+            }
+        }
+    }
+    for (void* q : tmp) hipFree(q);
+    if (rc) return rc;
+    // tile sums: per map with k > 1, per view, runs of <= 256 texels
+    std::vector<uint4> wk;
+    for (uint32_t m = 0; m < n_maps; m++) {
+        if (mis[m].k == 1) continue;
+        const uint32_t run = std::min<uint32_t>(mis[m].T, 256u);
+        for (uint32_t v = 0; v < N; v++) {
+            for (uint32_t t0 = 0; t0 < mis[m].T; t0 += run) {
+                wk.push_back(make_uint4(m, v, t0, std::min(run, mis[m].T - t0)));
+            }
+        }
+    }
+    if (!wk.empty()) {
+        if ((rc = salloc(&work, sizeof(uint4) * wk.size()))) return rc;
+        DRESSI_TRY_HIP(hipMemcpy(work, wk.data(), sizeof(uint4) * wk.size(),
+                                 hipMemcpyHostToDevice));
+    }
+    d.minfo = (const MapInfo*)minfo;
+    d.n_maps = n_maps;
+    d.n_buckets = (uint32_t)nb;
+    d.n_tot = (uint32_t)nt;
+    d.ml_off = (const uint32_t*)off;
+    d.ml_order = (const uint32_t*)order;
+    d.bg_pix = (const uint32_t*)bgpix;
+    d.bg_base = (const uint32_t*)bgbase;
+    d.gitems = (const GatherItem*)gbuf;
+    d.n_gitems = (uint32_t)gi.size();
+    d.coff = (const uint32_t*)coff;
+    d.mg_ent = (const uint16_t*)ment;
+    d.mpart = (float4*)part;
+    d.mtot = (float4*)tot;
+    d.tsum_work = (const uint4*)work;
+    d.n_tsum = (uint32_t)wk.size();
+    p->ml_len = total;
+    return DRESSI_OK;
 }
 
 }  // namespace
@@ -1362,9 +2024,11 @@ int dressi_pbr_create(dressi_ctx* ctx, const dressi_pbr_desc* desc, dressi_pbr_p
                    "n_views must be in [1, %u]", kPbrMaxViews);
     DRESSI_REQUIRE(desc->width > 0 && desc->width == desc->height,
                    "the screen must be square (width == height > 0)");
-    // <= 2^26 pixels: the fixed-point map-gradient sums (kFixLimit) cannot wrap
-    DRESSI_REQUIRE((uint64_t)desc->n_views * desc->width * desc->height <= (1ull << 26),
-                   "too many pixels (views x width x height must be <= 2^26)");
+    // the map-gradient list set-up sorts (pixel, map, tap) entries of every
+    // view with 32-bit item counts
+    DRESSI_REQUIRE((uint64_t)desc->n_views * desc->width * desc->height * (kPbrMaxLevels + 2) * 4 <
+                           (1ull << 31),
+                   "too many pixels (views x width x height x (levels + 2) x 4 must be < 2^31)");
     DRESSI_REQUIRE(desc->tex_w > 0 && desc->tex_h > 0 &&
                            (uint64_t)desc->tex_w * desc->tex_h < (1ull << 28),
                    "bad texture size");
@@ -1390,14 +2054,6 @@ int dressi_pbr_create(dressi_ctx* ctx, const dressi_pbr_desc* desc, dressi_pbr_p
     d.b2 = desc->beta2;
     d.eps = desc->eps;
     d.inv_n = 1.f / ((float)d.S * (float)d.S * 3.f);
-    // |d loss / d hdr| <= inv_n (L1 on the Reinhard-mapped image of
-    // non-negative radiance: d ldr / d hdr = 1 / (1 + hdr)^2 <= 1) and every
-    // scattered term is that times a coefficient in [0, 1] (material terms
-    // and split-sum factors in [0, 1], bilinear weights): with 2^28 units per
-    // inv_n a term stays below 2^29 units, a 16-lane pre-sum below 2^33, and
-    // to_fixed flags and clamps anything beyond 2^34 (kFixLimit)
-    d.fix_k = 28 - ilogbf(d.inv_n);
-    d.err = ctx->d_err;
     // pooling chain (src/core/ibl.cpp:14-20): irradiance source <= 64 x 32,
     // prefilter source <= 128 x 64 (halving, sizes rounding up)
     d.pw[0] = d.ew;
@@ -1461,13 +2117,13 @@ int dressi_pbr_create(dressi_ctx* ctx, const dressi_pbr_desc* desc, dressi_pbr_p
     if (!rc) rc = pbr_alloc(p, &d.pref, d.n_pref);
     if (!rc) rc = pbr_alloc(p, &d.g_irr, (size_t)d.iw * d.ih);
     if (!rc) rc = pbr_alloc(p, &d.g_pref, d.n_pref);
+    if (!rc) rc = pbr_alloc(p, &d.g_bg, E);
     if (!rc) rc = pbr_alloc(p, &d.g_isrc, (size_t)d.isw * d.ish);
     if (!rc) rc = pbr_alloc(p, &d.g_psrc, (size_t)d.psw * d.psh);
-    if (!rc) rc = pbr_alloc(p, &d.acc_irr, (size_t)d.iw * d.ih * 3 * kStripes);
-    if (!rc) rc = pbr_alloc(p, &d.acc_pref, (size_t)d.n_pref * 3 * kStripes);
-    if (!rc) rc = pbr_alloc(p, &d.acc_env, E * 3);
     if (!rc) rc = pbr_alloc(p, &d.gyA, N * npx);
     if (!rc) rc = pbr_alloc(p, &d.gyM, N * npx);
+    if (!rc) rc = pbr_alloc(p, &d.mgA, N * npx);
+    if (!rc) rc = pbr_alloc(p, &d.mgB, N * npx);
     if (!rc) rc = pbr_alloc(p, &d.loss_part, shade_blocks(d));
     if (!rc) rc = pbr_alloc(p, &d.loss, 1);
     if (!rc && (desc->flags & DRESSI_PBR_KEEP_PRED)) rc = pbr_alloc(p, &d.pred, N * npx);
@@ -1481,7 +2137,24 @@ int dressi_pbr_create(dressi_ctx* ctx, const dressi_pbr_desc* desc, dressi_pbr_p
         rc = pbr_upload(p, &lt, ltab);
         d.ltab = lt;
     }
-    // direction tables (the reference's float bits, see ibl_core.h)
+    // static maps: prefilter normalisers and the BRDF LUT, through the
+    // per-op entry points on the plan's context; then the convolution weights
+    // from the texel-centre direction tables (the reference's float bits, see
+    // ibl_core.h)
+    if (!rc) {
+        float* pn = nullptr;
+        rc = pbr_alloc(p, &pn, d.n_pref);
+        for (uint32_t i = 0; i < d.levels && !rc; i++) {
+            const float r = (float)i / (float)(d.levels - 1);
+            rc = dressi_prefilter_conv_norm(ctx, d.lw[i], d.lh[i], d.psw, d.psh, r,
+                                            pn + d.loff[i]);
+        }
+        d.pnorm = pn;
+        float2* lut = nullptr;
+        if (!rc) rc = pbr_alloc(p, &lut, (size_t)d.lutw * d.luth);
+        if (!rc) rc = dressi_brdf_lut(ctx, d.lutw, d.luth, 512, (float*)lut);
+        d.lut = lut;
+    }
     if (!rc) {
         std::vector<float4> idir = host_equirect_dirs(d.iw, d.ih);
         std::vector<float4> isdir = host_equirect_dirs(d.isw, d.ish);
@@ -1497,49 +2170,44 @@ int dressi_pbr_create(dressi_ctx* ctx, const dressi_pbr_desc* desc, dressi_pbr_p
         if (!rc) rc = pbr_upload(p, &b, isdir);
         if (!rc) rc = pbr_upload(p, &c, pdir);
         if (!rc) rc = pbr_upload(p, &e, psdir);
-        d.idir = a;
-        d.isdir = b;
-        d.pdir = c;
         d.psdir = e;
-    }
-    // conv groups
-    if (!rc) {
-        make_groups(p->fgroups, 0, d.iw * d.ih, kIrrLevel);
-        for (uint32_t i = 0; i < d.levels; i++) {
-            make_groups(p->fgroups, d.loff[i], d.lw[i] * d.lh[i], i);
-        }
-        make_groups(p->bgroups, 0, d.isw * d.ish, kIrrLevel);
-        make_groups(p->bgroups, 0, d.psw * d.psh, 0);
-        PbrGroup *fg = nullptr, *bg = nullptr;
-        rc = pbr_upload(p, &fg, p->fgroups);
-        if (!rc) rc = pbr_upload(p, &bg, p->bgroups);
-        d.fgroups = fg;
-        d.n_fgroups = (uint32_t)p->fgroups.size();
-        d.bgroups = bg;
-        d.n_bgroups = (uint32_t)p->bgroups.size();
-    }
-    // static maps: prefilter normalisers and the BRDF LUT, through the
-    // per-op entry points on the plan's context
-    if (!rc) {
-        float* pn = nullptr;
-        rc = pbr_alloc(p, &pn, d.n_pref);
-        for (uint32_t i = 0; i < d.levels && !rc; i++) {
-            const float r = (float)i / (float)(d.levels - 1);
-            rc = dressi_prefilter_conv_norm(ctx, d.lw[i], d.lh[i], d.psw, d.psh, r,
-                                            pn + d.loff[i]);
-        }
-        d.pnorm = pn;
-        float2* lut = nullptr;
-        if (!rc) rc = pbr_alloc(p, &lut, (size_t)d.lutw * d.luth);
-        if (!rc) rc = dressi_brdf_lut(ctx, d.lutw, d.luth, 512, (float*)lut);
-        d.lut = lut;
+        const uint32_t ni = d.iw * d.ih, nis = d.isw * d.ish, nps = d.psw * d.psh;
+        // tile-major, the column count rounded up to whole groups of 64
+        const auto cols = [](uint32_t n) { return (size_t)((n + 63u) & ~63u); };
+        const size_t bfi = (size_t)nis * cols(ni), bbi = (size_t)ni * cols(nis);
+        const size_t bfp = (size_t)nps * cols(d.n_pref), bbp = (size_t)d.n_pref * cols(nps);
+        float *wfi = nullptr, *wbi = nullptr, *wfp = nullptr, *wbp = nullptr;
+        if (!rc) rc = pbr_alloc(p, &wfi, bfi);
+        if (!rc) rc = pbr_alloc(p, &wbi, bbi);
+        if (!rc) rc = pbr_alloc(p, &wfp, bfp);
+        if (!rc) rc = pbr_alloc(p, &wbp, bbp);
         if (!rc) {
-            hipError_t e = hipStreamSynchronize(ctx->stream);
-            if (e != hipSuccess) {
-                set_error("static IBL maps failed: %s", hipGetErrorString(e));
+            hipError_t err = hipSuccess;
+            for (const auto& [q, n] : {std::pair<float*, size_t>{wfi, bfi}, {wbi, bbi}, {wfp, bfp},
+                                      {wbp, bbp}}) {
+                if (err == hipSuccess) err = hipMemsetAsync(q, 0, n * sizeof(float), ctx->stream);
+            }
+            if (err == hipSuccess) {
+                hipLaunchKernelGGL(k_pbr_weights, dim3(div_up(ni, 256), nis), dim3(256), 0,
+                                   ctx->stream, a, ni, b, nis, (const float*)nullptr, wfi, wbi);
+                hipLaunchKernelGGL(k_pbr_weights, dim3(div_up(d.n_pref, 256), nps), dim3(256), 0,
+                                   ctx->stream, c, d.n_pref, e, nps, d.pnorm, wfp, wbp);
+                err = hipGetLastError();
+            }
+            if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+            if (err != hipSuccess) {
+                set_error("static IBL maps failed: %s", hipGetErrorString(err));
                 rc = DRESSI_ERR_HIP;
             }
         }
+        d.wf_irr = wfi;
+        d.wb_irr = wbi;
+        d.wf_pref = wfp;
+        d.wb_pref = wbp;
+        d.n_ig = div_up(ni, kMvCols);
+        d.n_pg = div_up(d.n_pref, kMvCols);
+        d.n_isg = div_up(nis, kMvCols);
+        d.n_psg = div_up(nps, kMvCols);
     }
     if (!rc) {
         float2* bc = nullptr;
@@ -1567,6 +2235,7 @@ int dressi_pbr_destroy(dressi_pbr_plan* p) {
     hipStreamSynchronize(p->ctx->stream);
     pbr_drop_graph(p);
     for (void* q : p->allocs) hipFree(q);
+    for (void* q : p->scene_allocs) hipFree(q);
     delete p;
     return DRESSI_OK;
 }
@@ -1724,6 +2393,9 @@ int dressi_pbr_set_scene(dressi_pbr_plan* p, const float* pos, const float* norm
         p->csr_len = (uint32_t)acc;
     }
     for (void* q : tmp) hipFree(q);
+    tmp.clear();
+    // the map-gradient gather lists (static: the directions are)
+    if (!rc) rc = build_map_lists(p);
     if (rc) return rc;
     pbr_drop_graph(p);
     p->scene_set = true;

@@ -250,6 +250,26 @@ class PbrFit:
         return n
 
     @property
+    def gather_maps(self) -> list[tuple[int, int, int]]:
+        """(w, h, bands) of every map the shading samples (irradiance, each
+        prefilter level, env): EquirectSampleBwd splits the dir rows into
+        `bands` bands, doubling from 1 while w h bands < 65536 and bands <
+        the dir image's height (f_ops.cpp:2823-2919)."""
+        maps = [(32, 16)]
+        w, h = min(128, self._psrc()[0]), min(64, self._psrc()[1])
+        for _ in range(self.levels):
+            maps.append((w, h))
+            w, h = max(w // 2, 1), max(h // 2, 1)
+        maps.append((self.env_w, self.env_h))
+        out = []
+        for w, h in maps:
+            k = 1
+            while w * h * k < 65536 and k < self.screen:
+                k *= 2
+            out.append((w, h, k))
+        return out
+
+    @property
     def prefilter_source(self) -> tuple[int, int]:
         """(w, h) of the pooled env level the prefilter convolution reads."""
         return self._psrc()

@@ -121,18 +121,13 @@ def test_texture_final_parameters(ctx):
 
 
 def test_pbr_final_parameters(ctx):
-    """C5 after its 100 iterations. The PBR plan sums its map gradients in
-    exact fixed point where the reference adds floats pixel after pixel, so
-    its gradients differ from the oracle's by float rounding (within 1e-4,
-    test_pbr_c5_first_iterations). Adam's normalised step turns a rounding
-    difference in a near-zero gradient into a step of up to lr (1e-2) in
-    either direction, and the L1 loss's gradient flips sign wherever the
-    prediction crosses the target, so over 100 iterations some texels drift
-    apart element-wise (measured: 2.2% of albedo, 1.8% of metallic-roughness
-    and 0.3% of env entries beyond 1e-3, the largest 0.059). The parameters
-    as a whole stay within 1e-3: relative L2 norm of the difference <= 1e-3,
-    |.| sums within 1e-4 and every loss within 1e-3; the share of entries
-    beyond 1e-3 is held under 5% so that a regression shows."""
+    """C5 after its 100 iterations against the oracle: every sampled entry of
+    the final albedo, metallic-roughness and env within 1e-3 (the north
+    star's bar for final parameters), every loss within 1e-4 relative (the
+    oracle adds each view's |diff| terms one by one, the plan in a tree; the
+    loss feeds nothing back). The plan adds every sum of the fit in the
+    reference's order, so the trajectory is the oracle's; the count of
+    entries that are not bit-identical is printed."""
     import opendressi_amd as od
     from opendressi_amd.pbr import workload_scene
     g = _load("c5")
@@ -149,17 +144,12 @@ def test_pbr_final_parameters(ctx):
     for k, a in (("albedo", alb), ("mr", mr), ("env", env)):
         x, y = _rows(g, k, a)
         d = np.abs(x - y)
-        _, _, srel = _param(g, k, a)
-        report[k] = (float(np.linalg.norm(d) / np.linalg.norm(y)), float(d.max()),
-                     float((d > 1e-3).mean()), srel)
-    print(f"  loss rel err max {lrel.max():.3g}; (rel L2, max |d|, share > 1e-3, |.| sum rel): "
-          + ", ".join(f"{k} {r[0]:.2g}/{r[1]:.2g}/{r[2]:.2g}/{r[3]:.2g}"
-                      for k, r in report.items()), flush=True)
-    assert lrel.max() <= 1e-3
-    for k, (l2, _, share, srel) in report.items():
-        assert l2 <= 1e-3, f"c5: final {k} relative L2 {l2:.3g}"
-        assert share <= 5e-2, f"c5: {share:.3g} of final {k} entries off by > 1e-3"
-        assert srel <= 1e-4, f"c5: final {k} |.| sum off by {srel:.3g} relative"
+        report[k] = (float(d.max()), int((d != 0).sum()), d.size)
+    print(f"  loss rel err max {lrel.max():.3g}; (max |d|, entries not identical / sampled): "
+          + ", ".join(f"{k} {r[0]:.3g} {r[1]}/{r[2]}" for k, r in report.items()), flush=True)
+    assert lrel.max() <= 1e-4
+    for k, (dmax, _, _) in report.items():
+        assert dmax <= 1e-3, f"c5: final {k} max |d| {dmax:.3g}"
 
 
 def _rows(g, name, got):
@@ -170,9 +160,11 @@ def _rows(g, name, got):
 
 def test_pbr_c5_first_iterations(ctx):
     """C5 at its full size (1024^2 x 6 views, icosphere L5, 512^2 textures,
-    512 x 256 env, 6 prefilter levels): target and prediction of the first
-    iteration within 1e-5, its texture / env gradients within 1e-4 of the
-    largest entry, the parameters after two iterations within 1e-3."""
+    512 x 256 env, 6 prefilter levels) against the oracle, entry by entry:
+    target and prediction of the first iteration within 1e-5 relative, its
+    albedo / metallic-roughness / env gradients within
+    1e-4 |ref| + 1e-7 max |ref|, the parameters after two iterations within
+    1e-3. The count of entries that are not bit-identical is printed."""
     import opendressi_amd as od
     from opendressi_amd import _lib as L
     from opendressi_amd.pbr import workload_scene
@@ -196,27 +188,24 @@ def test_pbr_c5_first_iterations(ctx):
     got.update(albedo=alb, mr=mr, env=env)
     assert t == 2.0
     # the loss is a mean of 6 x 1024^2 x 3 terms: the oracle adds each view's
-    # channel sums one term at a time in float (rounding ~1e-5 .. 1e-4 of the
-    # sum at 2^20 terms), the plan in a tree, so 1e-4 relative
+    # channel sums one term at a time, the plan in a tree
     lrel = abs(loss0 - float(g["out_loss"][0])) / abs(float(g["out_loss"][0]))
     report = {}
+    fails = []
     for k, a in got.items():
         x, y = _rows(g, k, a)
         scale = float(g["out_max_" + k][0])
         d = np.abs(x - y)
-        elem = float((d / (np.abs(y) + 1e-3 * scale)).max())
-        report[k] = (float(d.max()) / max(scale, 1e-30), elem)
-    print(f"  loss rel err {lrel:.3g}; (max |d| / max |ref|, element-wise rel): "
-          + ", ".join(f"{k} {a:.2g}/{b:.2g}" for k, (a, b) in report.items()), flush=True)
-    assert lrel <= 1e-4
-    for k, (a, b) in report.items():
         if k in ("target0", "pred0"):
-            assert a * float(g["out_max_" + k][0]) <= 1e-5, f"{k}: max |d| {a:.3g} of max"
+            bad = d > 1e-5 * np.abs(y)
         elif k.startswith("g_"):
-            # relative to the gradient's scale: an entry that is a sum of
-            # terms of both signs keeps the absolute error of its summands,
-            # so entry by entry the relative error is unbounded (measured
-            # 5.7e-4 for g_mr0 at the 1e-3-of-max floor; reported above)
-            assert a <= 1e-4, f"{k}: max |d| / max |ref| {a:.3g}"
+            bad = d > 1e-4 * np.abs(y) + 1e-7 * scale
         else:
-            assert a * float(g["out_max_" + k][0]) <= 1e-3, f"{k} after 2 iterations: {a:.3g}"
+            bad = d > 1e-3
+        report[k] = (float(d.max()), int((d != 0).sum()), d.size)
+        if bad.any():
+            fails.append(f"{k}: {int(bad.sum())} entries beyond the bar (max |d| {d.max():.3g})")
+    print(f"  loss rel err {lrel:.3g}; (max |d|, entries not identical / sampled): "
+          + ", ".join(f"{k} {r[0]:.3g} {r[1]}/{r[2]}" for k, r in report.items()), flush=True)
+    assert lrel <= 1e-4
+    assert not fails, "; ".join(fails)
