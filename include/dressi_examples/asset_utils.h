@@ -43,7 +43,27 @@ struct Mesh {
 Mesh LoadObjMesh(const std::string& path);
 Mesh LoadGltfMesh(const std::string& path);
 
-// RGB in [0, 1] (PNG)
+// The first node that has a mesh (its local matrix applied on the CPU), that
+// mesh's first primitive and its metallic-roughness material
+// (asset_utils.h:30-52 of the reference's examples). uv keeps glTF's V
+// (whole-period offsets removed); normal is unit, tangent xyz unit + w the
+// handedness, both generated when the file lacks them. Texture slots are
+// 3-channel [0, 1] images (width 0 when absent); base_color and emissive
+// stay sRGB-encoded.
+struct GltfScene {
+    Mesh mesh;
+    dressi::CpuImage normal;              // {V,1,3}
+    dressi::CpuImage tangent;             // {V,1,4}
+    dressi::CpuImage base_color;          // sRGB-encoded
+    dressi::CpuImage metallic_roughness;  // G = roughness, B = metallic
+    dressi::CpuImage normal_map;          // tangent space
+    dressi::CpuImage occlusion;           // R = AO
+    dressi::CpuImage emissive;            // sRGB-encoded
+};
+// `normalize`: positions centred with maximum extent 1, as LoadGltfMesh.
+GltfScene LoadGltfScene(const std::string& path, bool normalize = true);
+
+// RGB in [0, 1] (PNG or baseline / extended-sequential JPEG)
 dressi::CpuImage LoadImageRgb(const std::string& path);
 // 3-channel float (EXR)
 dressi::CpuImage LoadImageExr(const std::string& path);

@@ -25,10 +25,10 @@ SOURCES = ["runtime.hip", "raster.hip", "hsr.hip", "aa.hip", "tex.hip", "ds.hip"
            "graph.hip", "executor.hip", "builders.hip", "route.hip"]
 # host-only sources (the examples' asset, geometry and PBR-graph helpers), built with g++;
 # zlib is linked for their deflate streams
-HOST_SOURCES = ["assets.cpp", "geometry.cpp", "pbr_graph.cpp"]
+HOST_SOURCES = ["assets.cpp", "jpeg.cpp", "geometry.cpp", "pbr_graph.cpp"]
 HEADERS = ["internal.h", "dressi_math.h", "raster_core.h", "soft_clip.h", "hsr_chain.h",
            "aa_core.h", "plan.h", "ibl_core.h", "graph_ir.h", "route.h", "libm_f32.h",
-           "libm_pow5_table.h"]
+           "libm_pow5_table.h", "image_codecs.h"]
 ARCH = os.environ.get("DRESSI_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [

@@ -22,6 +22,7 @@
 #include <stdexcept>
 
 #include "dressi_examples/asset_utils.h"
+#include "image_codecs.h"
 #include "dressi_hip.h"
 
 namespace dressi_examples {
@@ -927,14 +928,378 @@ Mesh LoadGltfMesh(const std::string& path) {
     return m;
 }
 
+namespace {
+
+// Column-major node-local matrix: `matrix`, else T * R * S from
+// translation, rotation (unit quaternion x, y, z, w) and scale
+// (asset_utils.cpp:177-213).
+Mat4 node_local_matrix(const Json& node) {
+    Mat4 m{};
+    if (const Json* mat = node.get("matrix")) {
+        if (mat->arr.size() == 16) {
+            for (size_t i = 0; i < 16; i++) {
+                m[i] = (float)mat->arr[i].number(0.0);
+            }
+            return m;
+        }
+    }
+    m[0] = m[5] = m[10] = m[15] = 1.f;
+    if (const Json* r = node.get("rotation")) {
+        if (r->arr.size() == 4) {
+            const float x = (float)r->arr[0].number(0.0), y = (float)r->arr[1].number(0.0);
+            const float z = (float)r->arr[2].number(0.0), w = (float)r->arr[3].number(0.0);
+            m[0] = 1.f - 2.f * (y * y + z * z);
+            m[1] = 2.f * (x * y + z * w);
+            m[2] = 2.f * (x * z - y * w);
+            m[4] = 2.f * (x * y - z * w);
+            m[5] = 1.f - 2.f * (x * x + z * z);
+            m[6] = 2.f * (y * z + x * w);
+            m[8] = 2.f * (x * z + y * w);
+            m[9] = 2.f * (y * z - x * w);
+            m[10] = 1.f - 2.f * (x * x + y * y);
+        }
+    }
+    if (const Json* sc = node.get("scale")) {
+        if (sc->arr.size() == 3) {
+            for (int col = 0; col < 3; col++) {
+                const float k = (float)sc->arr[(size_t)col].number(1.0);
+                for (int row = 0; row < 3; row++) {
+                    m[(size_t)(col * 4 + row)] *= k;
+                }
+            }
+        }
+    }
+    if (const Json* t = node.get("translation")) {
+        if (t->arr.size() == 3) {
+            m[12] = (float)t->arr[0].number(0.0);
+            m[13] = (float)t->arr[1].number(0.0);
+            m[14] = (float)t->arr[2].number(0.0);
+        }
+    }
+    return m;
+}
+
+// Inverse transpose of the upper-left 3x3 of m (the normal matrix),
+// column-major, by cofactors; a zero determinant divides by 1e-12
+// (asset_utils.cpp:215-231).
+std::array<float, 9> normal_matrix(const Mat4& m) {
+    const float a = m[0], b = m[4], c = m[8];
+    const float d = m[1], e = m[5], f = m[9];
+    const float g = m[2], h = m[6], i = m[10];
+    const float det = a * (e * i - f * h) - b * (d * i - f * g) + c * (d * h - e * g);
+    const float inv = 1.f / (det == 0.f ? 1e-12f : det);
+    return {(e * i - f * h) * inv, (c * h - b * i) * inv, (b * f - c * e) * inv,
+            (f * g - d * i) * inv, (a * i - c * g) * inv, (c * d - a * f) * inv,
+            (d * h - e * g) * inv, (b * g - a * h) * inv, (a * e - b * d) * inv};
+}
+
+std::array<float, 3> cross3(const std::array<float, 3>& a, const std::array<float, 3>& b) {
+    return {a[1] * b[2] - a[2] * b[1], a[2] * b[0] - a[0] * b[2], a[0] * b[1] - a[1] * b[0]};
+}
+
+float dot3(const std::array<float, 3>& a, const std::array<float, 3>& b) {
+    return a[0] * b[0] + a[1] * b[1] + a[2] * b[2];
+}
+
+std::array<float, 3> unit3(const std::array<float, 3>& v) {
+    const float len = std::sqrt(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+    return {v[0] / len, v[1] / len, v[2] / len};
+}
+
+// The bytes of glTF image `i`: a file next to the asset, a base64 data
+// URI, or a bufferView.
+std::vector<uint8_t> gltf_image_bytes(const Gltf& g, size_t i, const std::string& path) {
+    const Json& im = g.doc.at("images").at(i);
+    if (const Json* uri = im.get("uri")) {
+        if (uri->str.rfind("data:", 0) == 0) {
+            const size_t comma = uri->str.find(',');
+            if (comma == std::string::npos ||
+                uri->str.substr(0, comma).find(";base64") == std::string::npos) {
+                fail("glTF: unsupported image data uri in " + path);
+            }
+            return base64_decode(uri->str.substr(comma + 1));
+        }
+        return read_file(dir_of(path) + uri_decode(uri->str));
+    }
+    const Json& bv = g.doc.at("bufferViews").at((size_t)im.at("bufferView").number(0.0));
+    const size_t buf = (size_t)bv.at("buffer").number(0.0);
+    const size_t off = bv.get("byteOffset") ? (size_t)bv.get("byteOffset")->number(0.0) : 0;
+    const size_t len = (size_t)bv.at("byteLength").number(0.0);
+    if (buf >= g.buffers.size() || off + len > g.buffers[buf].size()) {
+        fail("glTF: image bufferView out of range in " + path);
+    }
+    return std::vector<uint8_t>(g.buffers[buf].begin() + (ptrdiff_t)off,
+                                g.buffers[buf].begin() + (ptrdiff_t)(off + len));
+}
+
+// Texture `tex` decoded to 3 channels in [0, 1]: channel c reads the
+// image's component min(c, components - 1) (asset_utils.cpp:233-260);
+// empty when the slot or its source is absent; 16-bit images are refused.
+CpuImage gltf_texture(const Gltf& g, int tex, const std::string& path) {
+    if (tex < 0) {
+        return CpuImage();
+    }
+    const Json& t = g.doc.at("textures").at((size_t)tex);
+    const Json* src = t.get("source");
+    if (!src || src->number(-1.0) < 0.0) {
+        return CpuImage();
+    }
+    const size_t idx = (size_t)src->number(0.0);
+    const std::vector<uint8_t> bytes = gltf_image_bytes(g, idx, path);
+    const codec::Image8 d =
+            codec::DecodeImage(bytes.data(), bytes.size(), path + " image " + std::to_string(idx));
+    if (d.bits != 8) {
+        fail("glTF: only 8-bit textures supported");
+    }
+    CpuImage out(d.width, d.height, 3);
+    const size_t np = (size_t)d.width * d.height;
+    for (size_t p = 0; p < np; p++) {
+        for (uint32_t c = 0; c < 3; c++) {
+            out.data[p * 3 + c] = (float)d.px[p * d.comp + std::min(c, d.comp - 1)] / 255.f;
+        }
+    }
+    return out;
+}
+
+int texture_index(const Json* slot) {
+    if (!slot) {
+        return -1;
+    }
+    const Json* i = slot->get("index");
+    return i ? (int)i->number(-1.0) : -1;
+}
+
+}  // namespace
+
+GltfScene LoadGltfScene(const std::string& path, bool normalize) {
+    Gltf g;
+    try {
+        g = load_gltf(path);
+    } catch (const std::runtime_error& e) {
+        fail("Failed to load glTF: " + path + " " + e.what());
+    }
+    // the first node with a mesh (its own transform; parents are not
+    // composed), else mesh 0 untransformed (asset_utils.cpp:280-294)
+    int mesh_idx = -1;
+    Mat4 xform{};
+    xform[0] = xform[5] = xform[10] = xform[15] = 1.f;
+    if (const Json* nodes = g.doc.get("nodes")) {
+        for (const Json& node : nodes->arr) {
+            const Json* mi = node.get("mesh");
+            if (mi && mi->number(-1.0) >= 0.0) {
+                mesh_idx = (int)mi->number(0.0);
+                xform = node_local_matrix(node);
+                break;
+            }
+        }
+    }
+    const Json* meshes = g.doc.get("meshes");
+    if (mesh_idx < 0 && meshes && !meshes->arr.empty()) {
+        mesh_idx = 0;
+    }
+    if (mesh_idx < 0 || !meshes || (size_t)mesh_idx >= meshes->arr.size() ||
+        !meshes->arr[(size_t)mesh_idx].get("primitives") ||
+        meshes->arr[(size_t)mesh_idx].at("primitives").arr.empty()) {
+        fail("glTF has no mesh primitives: " + path);
+    }
+    const Json& prim = meshes->arr[(size_t)mesh_idx].at("primitives").at(0);
+    const Json* attrs = prim.get("attributes");
+    const Json* pos_i = attrs ? attrs->get("POSITION") : nullptr;
+    const Json* idx_i = prim.get("indices");
+    if (!pos_i || !idx_i) {
+        fail("glTF primitive needs POSITION + indices");
+    }
+    const Accessor pa = accessor(g, (size_t)pos_i->number(0.0));
+    const Accessor ia = accessor(g, (size_t)idx_i->number(0.0));
+    const uint32_t nv = (uint32_t)pa.count, nf = (uint32_t)(ia.count / 3);
+    GltfScene sc;
+    Mesh& m = sc.mesh;
+    m.pos = CpuImage(nv, 1, 3);
+    m.uv = CpuImage(nv, 1, 2, 0.f);
+    m.faces = CpuImage(nf, 1, 3);
+    sc.normal = CpuImage(nv, 1, 3, 0.f);
+    sc.tangent = CpuImage(nv, 1, 4, 0.f);
+    for (uint32_t v = 0; v < nv; v++) {
+        for (uint32_t c = 0; c < 3; c++) {
+            m.pos.at(v, 0, c) = pa.read(v, c);
+        }
+    }
+    if (const Json* uv_i = attrs->get("TEXCOORD_0")) {
+        const Accessor ua = accessor(g, (size_t)uv_i->number(0.0));
+        for (uint32_t v = 0; v < nv; v++) {
+            m.uv.at(v, 0, 0) = ua.read(v, 0);  // glTF's V: no flip
+            m.uv.at(v, 0, 1) = ua.read(v, 1);
+        }
+        // whole-period offsets (REPEAT-wrapped coordinates) removed per axis
+        for (uint32_t c = 0; c < 2; c++) {
+            float lo = 1e30f;
+            for (uint32_t v = 0; v < nv; v++) {
+                lo = std::min(lo, m.uv.at(v, 0, c));
+            }
+            const float shift = std::floor(lo);
+            if (shift != 0.f) {
+                for (uint32_t v = 0; v < nv; v++) {
+                    m.uv.at(v, 0, c) -= shift;
+                }
+            }
+        }
+    }
+    for (uint32_t fi = 0; fi < nf; fi++) {
+        for (uint32_t k = 0; k < 3; k++) {
+            m.faces.at(fi, 0, k) = ia.read((size_t)fi * 3 + k, 0);
+        }
+    }
+    auto corner = [&](uint32_t fi, uint32_t k) {
+        const float x = m.faces.at(fi, 0, k);
+        if (!(x >= 0.f) || x >= (float)nv) {
+            fail("glTF: face index out of range in " + path);
+        }
+        return (uint32_t)x;
+    };
+    if (const Json* n_i = attrs->get("NORMAL")) {
+        const Accessor na = accessor(g, (size_t)n_i->number(0.0));
+        for (uint32_t v = 0; v < nv; v++) {
+            for (uint32_t c = 0; c < 3; c++) {
+                sc.normal.at(v, 0, c) = na.read(v, c);
+            }
+        }
+    } else {
+        // area-weighted: each face's (p1 - p0) x (p2 - p0) added to its corners
+        for (uint32_t fi = 0; fi < nf; fi++) {
+            uint32_t vi[3];
+            std::array<float, 3> p[3];
+            for (uint32_t k = 0; k < 3; k++) {
+                vi[k] = corner(fi, k);
+                for (uint32_t c = 0; c < 3; c++) {
+                    p[k][c] = m.pos.at(vi[k], 0, c);
+                }
+            }
+            const std::array<float, 3> e1 = {p[1][0] - p[0][0], p[1][1] - p[0][1], p[1][2] - p[0][2]};
+            const std::array<float, 3> e2 = {p[2][0] - p[0][0], p[2][1] - p[0][1], p[2][2] - p[0][2]};
+            const std::array<float, 3> fn = cross3(e1, e2);
+            for (uint32_t k = 0; k < 3; k++) {
+                for (uint32_t c = 0; c < 3; c++) {
+                    sc.normal.at(vi[k], 0, c) += fn[c];
+                }
+            }
+        }
+    }
+    if (const Json* t_i = attrs->get("TANGENT")) {
+        const Accessor ta = accessor(g, (size_t)t_i->number(0.0));
+        for (uint32_t v = 0; v < nv; v++) {
+            for (uint32_t c = 0; c < 4; c++) {
+                sc.tangent.at(v, 0, c) = ta.read(v, c);
+            }
+        }
+    } else {
+        // Lengyel's per-face tangent / bitangent from the uv gradients,
+        // summed per vertex, Gram-Schmidt against the normal, w the
+        // handedness (asset_utils.cpp:401-463)
+        std::vector<float> tan((size_t)nv * 3, 0.f), bit((size_t)nv * 3, 0.f);
+        for (uint32_t fi = 0; fi < nf; fi++) {
+            uint32_t vi[3];
+            std::array<float, 3> p[3];
+            float tu[3], tv[3];
+            for (uint32_t k = 0; k < 3; k++) {
+                vi[k] = corner(fi, k);
+                for (uint32_t c = 0; c < 3; c++) {
+                    p[k][c] = m.pos.at(vi[k], 0, c);
+                }
+                tu[k] = m.uv.at(vi[k], 0, 0);
+                tv[k] = m.uv.at(vi[k], 0, 1);
+            }
+            const float du1 = tu[1] - tu[0], dv1 = tv[1] - tv[0];
+            const float du2 = tu[2] - tu[0], dv2 = tv[2] - tv[0];
+            const float det = du1 * dv2 - du2 * dv1;
+            if (std::fabs(det) < 1e-12f) {
+                continue;
+            }
+            const float r = 1.f / det;
+            for (uint32_t c = 0; c < 3; c++) {
+                const float e1 = p[1][c] - p[0][c];
+                const float e2 = p[2][c] - p[0][c];
+                const float tc = (e1 * dv2 - e2 * dv1) * r;
+                const float bc = (e2 * du1 - e1 * du2) * r;
+                for (uint32_t k = 0; k < 3; k++) {
+                    tan[(size_t)vi[k] * 3 + c] += tc;
+                    bit[(size_t)vi[k] * 3 + c] += bc;
+                }
+            }
+        }
+        for (uint32_t v = 0; v < nv; v++) {
+            const std::array<float, 3> n = {sc.normal.at(v, 0, 0), sc.normal.at(v, 0, 1),
+                                            sc.normal.at(v, 0, 2)};
+            std::array<float, 3> t = {tan[(size_t)v * 3], tan[(size_t)v * 3 + 1],
+                                      tan[(size_t)v * 3 + 2]};
+            const float ndt = dot3(n, t);
+            for (uint32_t c = 0; c < 3; c++) {
+                t[c] -= n[c] * ndt;
+            }
+            const float len = std::sqrt(dot3(t, t));
+            if (len < 1e-12f) {
+                // degenerate uv: a unit vector perpendicular to n
+                t = std::fabs(n[0]) < 0.9f ? unit3(cross3(n, {1.f, 0.f, 0.f}))
+                                           : unit3(cross3(n, {0.f, 1.f, 0.f}));
+            } else {
+                for (uint32_t c = 0; c < 3; c++) {
+                    t[c] /= len;
+                }
+            }
+            const std::array<float, 3> b = {bit[(size_t)v * 3], bit[(size_t)v * 3 + 1],
+                                            bit[(size_t)v * 3 + 2]};
+            for (uint32_t c = 0; c < 3; c++) {
+                sc.tangent.at(v, 0, c) = t[c];
+            }
+            sc.tangent.at(v, 0, 3) = dot3(cross3(n, t), b) < 0.f ? -1.f : 1.f;
+        }
+    }
+    // the node transform: positions by M, normals by its normal matrix,
+    // tangent xyz by M as a direction; normals and tangents renormalised
+    const std::array<float, 9> nm = normal_matrix(xform);
+    for (uint32_t v = 0; v < nv; v++) {
+        const float p[3] = {m.pos.at(v, 0, 0), m.pos.at(v, 0, 1), m.pos.at(v, 0, 2)};
+        const float n[3] = {sc.normal.at(v, 0, 0), sc.normal.at(v, 0, 1), sc.normal.at(v, 0, 2)};
+        const float t[3] = {sc.tangent.at(v, 0, 0), sc.tangent.at(v, 0, 1), sc.tangent.at(v, 0, 2)};
+        std::array<float, 3> np{}, nn{}, nt{};
+        for (uint32_t r = 0; r < 3; r++) {
+            np[r] = xform[0 * 4 + r] * p[0] + xform[1 * 4 + r] * p[1] + xform[2 * 4 + r] * p[2] +
+                    xform[3 * 4 + r];
+            nn[r] = nm[0 * 3 + r] * n[0] + nm[1 * 3 + r] * n[1] + nm[2 * 3 + r] * n[2];
+            nt[r] = xform[0 * 4 + r] * t[0] + xform[1 * 4 + r] * t[1] + xform[2 * 4 + r] * t[2];
+        }
+        nn = unit3(nn);
+        nt = unit3(nt);
+        for (uint32_t c = 0; c < 3; c++) {
+            m.pos.at(v, 0, c) = np[c];
+            sc.normal.at(v, 0, c) = nn[c];
+            sc.tangent.at(v, 0, c) = nt[c];
+        }
+    }
+    if (normalize) {
+        normalise_divide(m);
+    }
+    if (const Json* mi = prim.get("material")) {
+        const Json& mat = g.doc.at("materials").at((size_t)mi->number(0.0));
+        const Json* pbr = mat.get("pbrMetallicRoughness");
+        sc.base_color = gltf_texture(g, texture_index(pbr ? pbr->get("baseColorTexture") : nullptr),
+                                     path);
+        sc.metallic_roughness = gltf_texture(
+                g, texture_index(pbr ? pbr->get("metallicRoughnessTexture") : nullptr), path);
+        sc.normal_map = gltf_texture(g, texture_index(mat.get("normalTexture")), path);
+        sc.occlusion = gltf_texture(g, texture_index(mat.get("occlusionTexture")), path);
+        sc.emissive = gltf_texture(g, texture_index(mat.get("emissiveTexture")), path);
+    }
+    return sc;
+}
+
 // ---- images -----------------------------------------------------------------------------
 
-CpuImage LoadImageRgb(const std::string& path) {
-    const std::vector<uint8_t> f = read_file(path);
+codec::Image8 codec::DecodePng(const uint8_t* fdata, size_t fsize, const std::string& path) {
     static const uint8_t sig[8] = {137, 80, 78, 71, 13, 10, 26, 10};
-    if (f.size() < 8 || std::memcmp(f.data(), sig, 8) != 0) {
-        fail("Failed to load image: " + path + " (only PNG is read)");
+    if (fsize < 8 || std::memcmp(fdata, sig, 8) != 0) {
+        fail("Failed to load image: " + path + " (not a PNG)");
     }
+    const std::vector<uint8_t> f(fdata, fdata + fsize);
     uint32_t w = 0, h = 0;
     int depth = 0, color = -1, interlace = 0;
     std::vector<uint8_t> idat, palette;
@@ -975,7 +1340,14 @@ CpuImage LoadImageRgb(const std::string& path) {
     const size_t bpp = std::max<size_t>(1, bits / 8);    // filter distance
     const std::vector<uint8_t> raw = inflate_stream(idat);
     size_t pos = 0;
-    CpuImage img(w, h, 3);
+    // native components: gray, gray + alpha, RGB (also palette), RGBA
+    const uint32_t out_c = color == 3 ? 3u : (uint32_t)chans;
+    codec::Image8 img;
+    img.width = w;
+    img.height = h;
+    img.comp = out_c;
+    img.bits = (uint32_t)depth;
+    img.px.assign((size_t)w * h * out_c, 0);
     // one (sub-)image: rows filtered and packed at `bits` per pixel;
     // pixel (i, j) lands on (x0 + i dx, y0 + j dy)
     auto decode = [&](uint32_t x0, uint32_t y0, uint32_t dx, uint32_t dy) {
@@ -1019,27 +1391,21 @@ CpuImage LoadImageRgb(const std::string& path) {
                     return (uint32_t)(cur[bit >> 3] >> (8 - depth - (int)(bit & 7))) &
                            ((1u << depth) - 1u);
                 };
-                uint32_t rgb[3];
+                uint8_t* o = &img.px[((size_t)(y0 + j * dy) * w + (x0 + i * dx)) * out_c];
                 if (color == 3) {
                     const size_t e = (size_t)sample(0) * 3;
                     if (e + 2 >= palette.size()) {
                         fail("Failed to load image: " + path + " palette index out of range");
                     }
-                    rgb[0] = palette[e];
-                    rgb[1] = palette[e + 1];
-                    rgb[2] = palette[e + 2];
-                } else if (chans <= 2) {
+                    o[0] = palette[e];
+                    o[1] = palette[e + 1];
+                    o[2] = palette[e + 2];
+                } else {
                     const uint32_t scale = depth == 1 ? 0xffu : depth == 2 ? 0x55u
                                            : depth == 4 ? 0x11u : 1u;
-                    rgb[0] = rgb[1] = rgb[2] = sample(0) * scale;
-                } else {
-                    rgb[0] = sample(0);
-                    rgb[1] = sample(1);
-                    rgb[2] = sample(2);
-                }
-                const size_t p = (size_t)(y0 + j * dy) * w + (x0 + i * dx);
-                for (int c = 0; c < 3; c++) {
-                    img.data[p * 3 + c] = (float)rgb[c] / 255.f;
+                    for (int c = 0; c < chans; c++) {
+                        o[c] = (uint8_t)(sample(c) * (depth < 8 ? scale : 1u));
+                    }
                 }
             }
             std::swap(cur, prev);
@@ -1052,6 +1418,24 @@ CpuImage LoadImageRgb(const std::string& path) {
                                             {0, 2, 2, 4}, {1, 0, 2, 2}, {0, 1, 1, 2}};
         for (const auto& q : pass) {
             decode(q[0], q[1], q[2], q[3]);
+        }
+    }
+    return img;
+}
+
+
+// stb_image's 8-bit load with 3 components asked for (what the reference
+// calls, asset_utils.cpp:598-609): gray and gray + alpha replicate the gray
+// sample, RGBA drops alpha; 16-bit PNG samples keep their high byte.
+CpuImage LoadImageRgb(const std::string& path) {
+    const std::vector<uint8_t> f = read_file(path);
+    const codec::Image8 d = codec::DecodeImage(f.data(), f.size(), path);
+    CpuImage img(d.width, d.height, 3);
+    const size_t np = (size_t)d.width * d.height;
+    for (size_t p = 0; p < np; p++) {
+        for (uint32_t c = 0; c < 3; c++) {
+            const uint32_t src = d.comp <= 2 ? 0u : c;
+            img.data[p * 3 + c] = (float)d.px[p * d.comp + src] / 255.f;
         }
     }
     return img;

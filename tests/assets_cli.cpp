@@ -4,7 +4,9 @@
 // height, channels, then width * height * channels float32.
 //
 //   assets_cli obj|gltf <mesh> <out prefix>       -> prefix.pos/.uv/.faces
-//   assets_cli png_load|exr_load <file> <out>
+//   assets_cli gltf_scene <file> <out prefix> [raw]  -> LoadGltfScene: prefix.pos/.uv/
+//              .faces/.normal/.tangent/.base/.mr/.nmap/.occ/.emis (raw: normalize off)
+//   assets_cli png_load|exr_load <file> <out>      (png_load: LoadImageRgb, PNG or JPEG)
 //   assets_cli png_save|exr_save <in> <file>
 //   assets_cli srgb|down <in> <out>
 //   assets_cli tile <cols> <out> <in>...
@@ -97,6 +99,17 @@ int run(int argc, char** argv) {
         write_mesh(arg(3), LoadObjMesh(arg(2)));
     } else if (cmd == "gltf") {
         write_mesh(arg(3), LoadGltfMesh(arg(2)));
+    } else if (cmd == "gltf_scene") {
+        const GltfScene sc = LoadGltfScene(argv[2], !(argc > 4 && std::string(argv[4]) == "raw"));
+        const std::string pre = argv[3];
+        write_mesh(pre, sc.mesh);
+        write_img(pre + ".normal", sc.normal);
+        write_img(pre + ".tangent", sc.tangent);
+        write_img(pre + ".base", sc.base_color);
+        write_img(pre + ".mr", sc.metallic_roughness);
+        write_img(pre + ".nmap", sc.normal_map);
+        write_img(pre + ".occ", sc.occlusion);
+        write_img(pre + ".emis", sc.emissive);
     } else if (cmd == "png_load") {
         write_img(arg(3), LoadImageRgb(arg(2)));
     } else if (cmd == "exr_load") {

@@ -854,3 +854,441 @@ def test_save_obj_and_textured_obj(cli, tmp_path):
     cli("obj", tmp_path / "t.obj", tmp_path / "back")
     _, back_uv, back_f = read_mesh(str(tmp_path / "back"))
     assert np.array_equal(back_uv, uv) and np.array_equal(back_f, [[0, 1, 2]])
+
+
+# --------------------------------------------------------------------- JPEG
+#
+# The reference decodes JPEG with stb_image (absent here), so decoder parity
+# with it is unpinned. What ITU-T T.81 fixes is pinned instead: the test
+# writes baseline files itself from quantised DCT blocks (its own Huffman
+# tables, byte stuffing, restart markers) and checks the decoded samples
+# against closed forms of the inverse DCT (DC-only blocks: F q / 8 + 128;
+# one AC term: a product of two cosines) and against the definition
+# evaluated with numpy, the JFIF colour transform, and the triangle
+# upsampling filter on a two-level chroma edge.
+
+
+def zigzag_natural():
+    """Natural index of the k-th zig-zag coefficient: diagonals r + c = s,
+    odd ones walked with the row rising, even ones with it falling."""
+    out = []
+    for s in range(15):
+        rows = range(max(0, s - 7), min(s, 7) + 1)
+        rows = rows if s % 2 else reversed(rows)
+        out += [r * 8 + (s - r) for r in rows]
+    return out
+
+
+ZZ = zigzag_natural()
+
+
+class _Bits:
+    def __init__(self):
+        self.acc, self.n, self.out = 0, 0, bytearray()
+
+    def put(self, v, n):
+        for i in range(n - 1, -1, -1):
+            self.acc = (self.acc << 1) | ((v >> i) & 1)
+            self.n += 1
+            if self.n == 8:
+                self._byte(self.acc)
+                self.acc, self.n = 0, 0
+
+    def _byte(self, b):
+        self.out.append(b)
+        if b == 0xFF:
+            self.out.append(0x00)
+
+    def flush(self):
+        if self.n:
+            self.put((1 << (8 - self.n)) - 1, 8 - self.n)  # pad with ones
+
+
+def _cat(v):
+    return int(abs(int(v))).bit_length()
+
+
+def _flat_huffman(symbols):
+    """Every symbol the same code length L with 2^L > count (the all-ones
+    code unused): (BITS, HUFFVAL, {symbol: (code, L)})."""
+    syms = sorted(set(symbols)) or [0]
+    L = max(1, int(np.ceil(np.log2(len(syms) + 1))))
+    counts = [0] * 16
+    counts[L - 1] = len(syms)
+    return counts, syms, {s: (i, L) for i, s in enumerate(syms)}
+
+
+def _block_symbols(coef, pred):
+    """(dc category, dc bits) and the AC (run/size, bits) list of one block
+    (natural-order ints)."""
+    zz = [int(coef[ZZ[k]]) for k in range(64)]
+    diff = zz[0] - pred
+    s = _cat(diff)
+    dc = (s, diff if diff >= 0 else diff + (1 << s) - 1)
+    ac, run = [], 0
+    for k in range(1, 64):
+        v = zz[k]
+        if v == 0:
+            run += 1
+            continue
+        while run > 15:
+            ac.append((0xF0, 0, 0))
+            run -= 16
+        s = _cat(v)
+        ac.append(((run << 4) | s, v if v >= 0 else v + (1 << s) - 1, s))
+        run = 0
+    if run:
+        ac.append((0x00, 0, 0))
+    return dc, ac, zz[0]
+
+
+def write_jpeg(path, comps, width, height, q, restart=0, sof=0xC0, app14=None, ids=None):
+    """comps: [(h, v, blocks)] with blocks {rows, cols, 64} natural-order
+    quantised coefficients (interleaved scan for several components, each
+    covering its MCUs; one component: its own blocks); q: {64} zig-zag
+    quantisation table shared by all."""
+    ids = ids or list(range(1, len(comps) + 1))
+    hmax = max(c[0] for c in comps)
+    vmax = max(c[1] for c in comps)
+    units = []  # per restart unit: [(comp index, block)]
+    if len(comps) == 1:
+        b = comps[0][2]
+        units = [[(0, b[r, c])] for r in range(b.shape[0]) for c in range(b.shape[1])]
+    else:
+        mx = -(-width // (8 * hmax))
+        my = -(-height // (8 * vmax))
+        for y in range(my):
+            for x in range(mx):
+                u = []
+                for ci, (h, v, b) in enumerate(comps):
+                    u += [(ci, b[y * v + j, x * h + i]) for j in range(v) for i in range(h)]
+                units.append(u)
+    # symbols, with the DC predictions (reset at restarts)
+    coded, dcs, acs = [], [], []
+    pred = [0] * len(comps)
+    for n, u in enumerate(units):
+        if restart and n and n % restart == 0:
+            pred = [0] * len(comps)
+            coded.append(None)
+        for ci, blk in u:
+            dc, ac, pred[ci] = _block_symbols(blk, pred[ci])
+            coded.append((dc, ac))
+            dcs.append(dc[0])
+            acs += [a[0] for a in ac]
+    dbits, dvals, dcode = _flat_huffman(dcs)
+    abits, avals, acode = _flat_huffman(acs)
+    bw, seg, rst = _Bits(), bytearray(), 0
+    for c in coded:
+        if c is None:
+            bw.flush()
+            seg += bw.out + bytes([0xFF, 0xD0 + rst % 8])
+            bw, rst = _Bits(), rst + 1
+            continue
+        (s, bits), ac = c
+        bw.put(*dcode[s])
+        bw.put(bits, s)
+        for rs, b, s2 in ac:
+            bw.put(*acode[rs])
+            bw.put(b, s2)
+    bw.flush()
+    seg += bw.out
+
+    def marker(m, body):
+        return bytes([0xFF, m]) + struct.pack(">H", len(body) + 2) + body
+
+    out = b"\xff\xd8" + marker(0xE0, b"JFIF\x00\x01\x01\x00\x00\x01\x00\x01\x00\x00")
+    if app14 is not None:
+        out += marker(0xEE, b"Adobe" + bytes([0, 100, 0, 0, 0, 0, app14]))
+    out += marker(0xDB, bytes([0]) + bytes(int(x) for x in q))
+    sofb = struct.pack(">BHHB", 8, height, width, len(comps))
+    for ci, (h, v, _) in enumerate(comps):
+        sofb += bytes([ids[ci], (h << 4) | v, 0])
+    out += marker(sof, sofb)
+    out += marker(0xC4, bytes([0x00]) + bytes(dbits) + bytes(dvals))
+    out += marker(0xC4, bytes([0x10]) + bytes(abits) + bytes(avals))
+    if restart:
+        out += marker(0xDD, struct.pack(">H", restart))
+    sos = bytes([len(comps)]) + b"".join(bytes([ids[ci], 0x00]) for ci in range(len(comps)))
+    out += marker(0xDA, sos + bytes([0, 63, 0])) + bytes(seg) + b"\xff\xd9"
+    open(path, "wb").write(out)
+
+
+def idct_ref(blk, qn):
+    """T.81 A.3.3 in float64 for one block (natural-order coefficients,
+    natural-order quantisation), + 128, rounded half up, clamped."""
+    F = blk.astype(np.float64).reshape(8, 8) * qn.reshape(8, 8)
+    x = np.arange(8)
+    C = np.where(np.arange(8) == 0, 1 / np.sqrt(2), 1.0)
+    T = 0.5 * C[None, :] * np.cos((2 * x[:, None] + 1) * np.arange(8)[None, :] * np.pi / 16)
+    s = T @ F @ T.T  # s[y, x] = sum_v sum_u T[y, v] F[v, u] T[x, u]
+    return np.clip(np.floor(s + 128.5), 0, 255)
+
+
+def plane_of(blocks, qn):
+    r, c = blocks.shape[:2]
+    out = np.zeros((r * 8, c * 8))
+    for i in range(r):
+        for j in range(c):
+            out[i * 8:i * 8 + 8, j * 8:j * 8 + 8] = idct_ref(blocks[i, j], qn)
+    return out
+
+
+def jfif_rgb(y, cb, cr):
+    cb, cr = cb - 128.0, cr - 128.0
+    r = y + 1.402 * cr
+    g = y - 0.344136 * cb - 0.714136 * cr
+    b = y + 1.772 * cb
+    return np.clip(np.floor(np.stack([r, g, b], -1) + 0.5), 0, 255)
+
+
+def _load_rgb8(cli, tmp_path, path):
+    cli("png_load", path, tmp_path / "o.img")
+    return np.rint(read_img(tmp_path / "o.img") * 255).astype(np.int64)
+
+
+def test_jpeg_closed_forms_gray(cli, tmp_path):
+    q = np.full(64, 1, np.int64)
+    q[ZZ.index(1)] = 3  # (v, u) = (0, 1) dequantised by 3
+    blocks = np.zeros((2, 3, 64), np.int64)
+    blocks[0, 0, 0] = 8 * 40        # DC only: 40 + 128 everywhere
+    blocks[0, 1, 0] = -8 * 100      # 28
+    blocks[0, 2, 0] = 8 * 200       # clamps at 255
+    blocks[1, 0, 1] = 50            # one AC term along x
+    blocks[1, 1, 0] = -8 * 300      # clamps at 0
+    blocks[1, 2, 8] = -20           # (v, u) = (1, 0): along y
+    write_jpeg(tmp_path / "g.jpg", [(1, 1, blocks)], 20, 13, np.asarray(
+        [q[ZZ[k]] for k in range(64)]))
+    got = _load_rgb8(cli, tmp_path, tmp_path / "g.jpg")
+    assert got.shape == (13, 20, 3)
+    assert (got[..., 0] == got[..., 1]).all() and (got[..., 0] == got[..., 2]).all()
+    g = got[..., 0]
+    assert (g[0:8, 0:8] == 168).all() and (g[0:8, 8:16] == 28).all()
+    assert (g[0:8, 16:20] == 255).all() and (g[8:13, 8:16] == 0).all()
+    x = np.arange(8)
+    ax = 128 + 0.25 * (1 / np.sqrt(2)) * 150 * np.cos((2 * x + 1) * np.pi / 16)
+    assert (g[8:13, 0:8] == np.floor(ax + 0.5)[None, :]).all()
+    ay = 128 + 0.25 * (1 / np.sqrt(2)) * -20 * np.cos((2 * np.arange(5) + 1) * np.pi / 16)
+    assert (g[8:13, 16:20] == np.floor(ay + 0.5)[:, None]).all()
+
+
+def _rand_blocks(rng, r, c, dc_scale=30, ac=6):
+    b = np.zeros((r, c, 64), np.int64)
+    b[..., 0] = rng.integers(-dc_scale, dc_scale + 1, (r, c))
+    for k in rng.integers(1, 64, 6):
+        b[..., ZZ[k]] = rng.integers(-ac, ac + 1, (r, c))
+    return b
+
+
+def test_jpeg_444_random_blocks_restarts_and_stuffing(cli, tmp_path):
+    rng = np.random.default_rng(3)
+    qz = rng.integers(1, 9, 64)
+    qn = np.zeros(64)
+    qn[ZZ] = qz
+    Y, Cb, Cr = (_rand_blocks(rng, 2, 3) for _ in range(3))
+    comps = [(1, 1, Y), (1, 1, Cb), (1, 1, Cr)]
+    want = jfif_rgb(plane_of(Y, qn), plane_of(Cb, qn), plane_of(Cr, qn))[:16, :24]
+    outs = []
+    for restart in (0, 1, 4):
+        write_jpeg(tmp_path / f"c{restart}.jpg", comps, 24, 16, qz, restart=restart)
+        outs.append(_load_rgb8(cli, tmp_path, tmp_path / f"c{restart}.jpg"))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    d = np.abs(outs[0] - want)
+    assert d.max() <= 1 and (d == 0).mean() > 0.99
+
+
+def test_jpeg_byte_stuffing(cli, tmp_path):
+    # DC differences of +-255 (eight one bits, or eight zero bits) at every
+    # bit alignment: the coded data holds 0xFF bytes, written as 0xFF 0x00
+    # (+255, -255) pairs with a 1..7-bit difference between them to walk
+    # through the alignments
+    diffs = [0]
+    for k in range(1, 8):
+        diffs += [255, -255, (1 << k) - 1]
+    dc = np.cumsum(diffs)
+    blocks = np.zeros((1, len(dc), 64), np.int64)
+    blocks[0, :, 0] = dc
+    q = np.ones(64, np.int64)
+    write_jpeg(tmp_path / "f.jpg", [(1, 1, blocks)], 8 * len(dc), 8, q)
+    data = open(tmp_path / "f.jpg", "rb").read()
+    assert b"\xff\x00" in data[data.index(b"\xff\xda"):data.index(b"\xff\xd9")]
+    g = _load_rgb8(cli, tmp_path, tmp_path / "f.jpg")[..., 0]
+    want = np.clip(np.floor(dc / 8.0 + 128.5), 0, 255)
+    assert (g == np.repeat(want, 8)[None, :]).all()
+
+
+def test_jpeg_420_constant_chroma_and_triangle_filter(cli, tmp_path):
+    rng = np.random.default_rng(4)
+    qz = np.ones(64, np.int64)
+    qn = np.ones(64)
+    Y = _rand_blocks(rng, 2, 4)
+    cb = np.zeros((1, 2, 64), np.int64)
+    cr = np.zeros((1, 2, 64), np.int64)
+    cb[0, :, 0] = 8 * 20      # Cb 148 everywhere
+    cr[0, 0, 0] = -8 * 16     # Cr 112 on the left chroma block,
+    cr[0, 1, 0] = 8 * 48      # 176 on the right one
+    write_jpeg(tmp_path / "s.jpg", [(2, 2, Y), (1, 1, cb), (1, 1, cr)], 32, 16, qz)
+    got = _load_rgb8(cli, tmp_path, tmp_path / "s.jpg")
+    y = plane_of(Y, qn)[:16, :32]
+    # columns 0..14 see Cr 112 only, 17..31 Cr 176 only; the filter mixes
+    # 3:1 at the edge: col(i) = 4 c, out(15) = (12 a + 4 b + 7) >> 4,
+    # out(16) = (12 b + 4 a + 8) >> 4
+    a, b = 112, 176
+    crs = np.where(np.arange(32) < 16, a, b).astype(np.float64)
+    crs[15] = (12 * a + 4 * b + 7) >> 4
+    crs[16] = (12 * b + 4 * a + 8) >> 4
+    want = jfif_rgb(y, np.full_like(y, 148.0), np.broadcast_to(crs, y.shape))
+    d = np.abs(got - want)
+    assert d.max() <= 1 and (d == 0).mean() > 0.99
+    assert (np.abs(got[:, :15] - jfif_rgb(y[:, :15], 148.0 + 0 * y[:, :15], 112.0 + 0 * y[:, :15])) <= 1).all()
+
+
+def test_jpeg_rgb_components_progressive_and_truncated(cli, tmp_path):
+    b = np.zeros((1, 1, 64), np.int64)
+    comps = [(1, 1, b + np.eye(1, 64, 0, dtype=np.int64) * 8 * k) for k in (10, -20, 30)]
+    qz = np.ones(64, np.int64)
+    write_jpeg(tmp_path / "a.jpg", comps, 8, 8, qz, app14=0)
+    assert (_load_rgb8(cli, tmp_path, tmp_path / "a.jpg") == [138, 108, 158]).all()
+    write_jpeg(tmp_path / "n.jpg", comps, 8, 8, qz, ids=[ord("R"), ord("G"), ord("B")])
+    assert (_load_rgb8(cli, tmp_path, tmp_path / "n.jpg") == [138, 108, 158]).all()
+    write_jpeg(tmp_path / "p.jpg", comps, 8, 8, qz, sof=0xC2)
+    r = cli("png_load", tmp_path / "p.jpg", tmp_path / "x", ok=False)
+    assert r.returncode != 0 and "baseline" in r.stderr
+    data = open(tmp_path / "a.jpg", "rb").read()
+    (tmp_path / "t.jpg").write_bytes(data[:data.index(b"\xff\xc4")])
+    r = cli("png_load", tmp_path / "t.jpg", tmp_path / "x", ok=False)
+    assert r.returncode != 0 and "JPEG" in r.stderr
+
+
+# ---------------------------------------------------------- glTF scenes
+#
+# LoadGltfScene on hand-built files: the node transform is chosen so that
+# float32 evaluates it exactly (a 180-degree turn about z, scales 2, 3, 4),
+# so positions, normals (area-weighted, through the normal matrix) and
+# generated tangents have closed forms; textures come from a data URI PNG,
+# a bufferView JPEG (one gray component, replicated), a gray + alpha PNG
+# (channel c reads component min(c, 1)) and absent slots.
+
+
+def _b64(data):
+    return "data:application/octet-stream;base64," + base64.b64encode(data).decode()
+
+
+def _scene_doc(pos, uv, idx, extra_attrs=None, node=None, images=None, material=None,
+               extra_views=b""):
+    blob = np.asarray(pos, F32).tobytes()
+    views = [{"buffer": 0, "byteOffset": 0, "byteLength": len(blob)}]
+    acc = [{"bufferView": 0, "componentType": 5126, "count": len(pos), "type": "VEC3"}]
+    attrs = {"POSITION": 0}
+    for name, arr, typ in ([("TEXCOORD_0", uv, "VEC2")] + (extra_attrs or [])):
+        data = np.asarray(arr, F32).tobytes()
+        views.append({"buffer": 0, "byteOffset": len(blob), "byteLength": len(data)})
+        blob += data
+        acc.append({"bufferView": len(views) - 1, "componentType": 5126, "count": len(arr),
+                    "type": typ})
+        attrs[name] = len(acc) - 1
+    ib = np.asarray(idx, np.uint16).tobytes()
+    views.append({"buffer": 0, "byteOffset": len(blob), "byteLength": len(ib)})
+    blob += ib
+    acc.append({"bufferView": len(views) - 1, "componentType": 5123, "count": len(idx),
+                "type": "SCALAR"})
+    prim = {"attributes": attrs, "indices": len(acc) - 1}
+    doc = {"asset": {"version": "2.0"}, "accessors": acc, "bufferViews": views,
+           "meshes": [{"primitives": [prim]}], "nodes": [{"name": "empty"}, node or {"mesh": 0}]}
+    if images is not None:
+        doc["images"], doc["textures"] = [], []
+        for kind, data in images:
+            if kind == "uri":
+                doc["images"].append({"uri": _b64(data)})
+            else:
+                doc["bufferViews"].append({"buffer": 0, "byteOffset": len(blob),
+                                           "byteLength": len(data)})
+                blob += data + b"\0" * (-len(data) % 4)
+                doc["images"].append({"bufferView": len(doc["bufferViews"]) - 1,
+                                      "mimeType": kind})
+            doc["textures"].append({"source": len(doc["images"]) - 1})
+        doc["textures"].append({"sampler": 0})  # a texture without a source
+    if material is not None:
+        doc["materials"] = [material]
+        prim["material"] = 0
+    doc["buffers"] = [{"byteLength": len(blob)}]
+    return blob, doc
+
+
+def test_gltf_scene_transform_generated_frames_and_textures(cli, tmp_path):
+    pos = np.array([[0, 0, 0], [1, 0, 0], [1, 1, 0], [0, 1, 0]], F32)
+    uv = np.array([[0, 1.25], [1, 1.25], [1, 2], [0, 2]], F32)  # V offset by a whole period
+    idx = [0, 1, 2, 0, 2, 3]
+    node = {"mesh": 0, "translation": [1, 2, 3], "rotation": [0, 0, 1, 0], "scale": [2, 3, 4]}
+    base = np.array([[[255, 0, 10], [1, 2, 3]], [[9, 99, 200], [0, 128, 255]]])
+    write_png(tmp_path / "b.png", base, 2, 8)
+    occ = np.array([[[10, 200], [20, 100]], [[30, 0], [40, 255]]])
+    write_png(tmp_path / "o.png", occ, 4, 8)
+    blocks = np.zeros((1, 1, 64), np.int64)
+    blocks[0, 0, 0] = 8 * 50
+    write_jpeg(tmp_path / "m.jpg", [(1, 1, blocks)], 8, 8, np.ones(64, np.int64))
+    images = [("uri", open(tmp_path / "b.png", "rb").read()),
+              ("image/jpeg", open(tmp_path / "m.jpg", "rb").read()),
+              ("image/png", open(tmp_path / "o.png", "rb").read())]
+    material = {"pbrMetallicRoughness": {"baseColorTexture": {"index": 0},
+                                         "metallicRoughnessTexture": {"index": 1}},
+                "occlusionTexture": {"index": 2}, "emissiveTexture": {"index": 3}}
+    blob, doc = _scene_doc(pos, uv, idx, node=node, images=images, material=material)
+    doc["buffers"][0]["uri"] = _b64(blob)
+    (tmp_path / "s.gltf").write_text(json.dumps(doc))
+    cli("gltf_scene", tmp_path / "s.gltf", tmp_path / "r", "raw")
+    p, u, f = read_mesh(str(tmp_path / "r"))
+    want = np.stack([-2 * pos[:, 0] + 1, -3 * pos[:, 1] + 2, 4 * pos[:, 2] + 3], 1)
+    assert np.array_equal(p, want) and np.array_equal(f, np.reshape(idx, (-1, 3)))
+    assert np.array_equal(u, uv - np.array([0, 1], F32))
+    n = read_img(str(tmp_path / "r.normal"))[0]
+    t = read_img(str(tmp_path / "r.tangent"))[0]
+    assert np.array_equal(n, np.tile([0, 0, 1], (4, 1)).astype(F32))
+    # uv u runs along +x: tangent +x (w = +1 for this winding), turned to -x
+    assert np.array_equal(t, np.tile([-1, 0, 0, 1], (4, 1)).astype(F32))
+    assert np.array_equal(np.rint(read_img(str(tmp_path / "r.base")) * 255), base)
+    assert np.array_equal(np.rint(read_img(str(tmp_path / "r.mr")) * 255), np.full((8, 8, 3), 178))
+    o = np.rint(read_img(str(tmp_path / "r.occ")) * 255)
+    assert np.array_equal(o, np.stack([occ[..., 0], occ[..., 1], occ[..., 1]], -1))
+    for slot in ("nmap", "emis"):
+        assert read_img(str(tmp_path / f"r.{slot}")).size == 0
+    # normalised: centred, maximum extent 1 (as LoadGltfMesh)
+    cli("gltf_scene", tmp_path / "s.gltf", tmp_path / "q")
+    assert np.array_equal(read_mesh(str(tmp_path / "q"))[0], normalise_div(want))
+
+
+def test_gltf_scene_given_frames_matrix_glb_and_errors(cli, tmp_path):
+    pos = np.array([[0, 0, 0], [2, 0, 0], [0, 2, 0]], F32)
+    nrm = np.array([[0, 0, 1], [0, 0, 1], [0, 0, 1]], F32)
+    tan = np.array([[1, 0, 0, -1], [1, 0, 0, -1], [0, 1, 0, 1]], F32)
+    # matrix: x -> y, y -> -x, z -> 2 z, translated by (5, 0, 0) (column-major)
+    m = [0, 1, 0, 0, -1, 0, 0, 0, 0, 0, 2, 0, 5, 0, 0, 1]
+    blob, doc = _scene_doc(pos, np.zeros((3, 2), F32), [0, 1, 2],
+                           extra_attrs=[("NORMAL", nrm, "VEC3"), ("TANGENT", tan, "VEC4")],
+                           node={"mesh": 0, "matrix": m})
+    js = json.dumps(doc).encode()
+    js += b" " * (-len(js) % 4)
+    blob += b"\0" * (-len(blob) % 4)
+    body = struct.pack("<II", len(js), 0x4E4F534A) + js + struct.pack("<II", len(blob), 0x004E4942) + blob
+    (tmp_path / "g.glb").write_bytes(struct.pack("<III", 0x46546C67, 2, 12 + len(body)) + body)
+    cli("gltf_scene", tmp_path / "g.glb", tmp_path / "r", "raw")
+    p = read_mesh(str(tmp_path / "r"))[0]
+    assert np.array_equal(p, np.stack([5 - pos[:, 1], pos[:, 0], 2 * pos[:, 2]], 1))
+    assert np.array_equal(read_img(str(tmp_path / "r.normal"))[0], nrm)
+    t = read_img(str(tmp_path / "r.tangent"))[0]
+    assert np.array_equal(t[:, :3], np.array([[0, 1, 0], [0, 1, 0], [-1, 0, 0]], F32))
+    assert np.array_equal(t[:, 3], tan[:, 3])
+    for slot in ("base", "mr", "nmap", "occ", "emis"):
+        assert read_img(str(tmp_path / f"r.{slot}")).size == 0  # no material
+    # a 16-bit texture is refused
+    write_png(tmp_path / "w.png", np.full((2, 2, 3), 1000), 2, 16)
+    blob, doc = _scene_doc(pos, np.zeros((3, 2), F32), [0, 1, 2],
+                           images=[("uri", open(tmp_path / "w.png", "rb").read())],
+                           material={"pbrMetallicRoughness": {"baseColorTexture": {"index": 0}}})
+    doc["buffers"][0]["uri"] = _b64(blob)
+    (tmp_path / "w.gltf").write_text(json.dumps(doc))
+    r = cli("gltf_scene", tmp_path / "w.gltf", tmp_path / "x", ok=False)
+    assert r.returncode != 0 and "8-bit" in r.stderr
+    doc["meshes"] = []
+    (tmp_path / "e.gltf").write_text(json.dumps(doc))
+    r = cli("gltf_scene", tmp_path / "e.gltf", tmp_path / "x", ok=False)
+    assert r.returncode != 0 and "no mesh primitives" in r.stderr
