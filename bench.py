@@ -481,6 +481,41 @@ def metric_point(name: str, steps: int, warmup: int) -> dict:
             "iteration_frac_of_hbm_peak": nb * its / HBM_PEAK, **extra}
 
 
+def dressi_ad_point(name: str, naive: bool, steps: int, warmup: int) -> dict:
+    """Iterations/s of the texture fit driven through the DressiAD graph API
+    (tests/graph_tex.cpp: the example's graph written with F:: ops; every
+    step sends each view's clip and ScreenAttr images and runs execStep,
+    which synchronises, as the reference example's loop does). RSP packing
+    runs it on the fused texture plan (the route), Naive on the generic
+    per-op executor."""
+    import tempfile
+    import opendressi_amd as od
+    w = od.TEX_WORKLOADS[name]
+    pos, uv, faces, mvps, gt, tex0 = od.make_tex_scene(w)
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "_bin", "graph_tex")
+    if not os.path.exists(exe):
+        return {"error": "tests/_bin/graph_tex is not built"}
+    hdr = np.array([len(pos), len(faces), w.views, w.screen, w.tex, w.tex, steps, w.sets,
+                    1 if naive else 0], np.uint32)
+    with tempfile.TemporaryDirectory() as d:
+        inp, out = os.path.join(d, "in.bin"), os.path.join(d, "out.bin")
+        with open(inp, "wb") as f:
+            f.write(hdr.tobytes())
+            f.write(np.float32(w.lr).tobytes())
+            for a in (pos, uv, faces, mvps, gt, tex0):
+                f.write(np.ascontiguousarray(a, np.float32).tobytes())
+        res = subprocess.run([exe, inp, out, str(warmup)], capture_output=True, text=True,
+                             timeout=900)
+    if res.returncode != 0:
+        return {"error": res.stderr.strip()[-400:]}
+    info = dict(kv.split("=", 1) for kv in res.stdout.split() if "=" in kv)
+    ms = float(info["ms_per_step"])
+    return {"workload": f"{name}: texture {w.screen}^2 x {w.views} views through DressiAD "
+                        f"({'Naive' if naive else 'RSP'} packing)",
+            "plan": info.get("plan"), "stages": int(info.get("stages", 0)),
+            "value": 1e3 / ms, "unit": "iterations/s", "ms_per_step": ms, "steps": steps}
+
+
 def reference_cpu_c1() -> dict:
     """The reference's own CPU evaluator (oracle/_ref: the reference's
     src/core built in place, BuildBackward + CpuEvaluator with DressiAD's
@@ -708,7 +743,9 @@ def main() -> int:
                                  "c2": metric_point("c2", 400, 20),
                                  "c3": metric_point("c3", 100, 10),
                                  "c4": metric_point("c4", 100, 10),
-                                 "c5": metric_point("c5", 50, 5)}
+                                 "c5": metric_point("c5", 50, 5),
+                                 "c3_dressi_ad": dressi_ad_point("c3", False, 30, 5),
+                                 "c3_dressi_ad_generic": dressi_ad_point("c3", True, 3, 2)}
     if args.torch_surface:
         line["torch_surface"] = torch_surface()
     if not args.no_cpu_baseline:

@@ -654,6 +654,12 @@ typedef struct dressi_tex_desc {
 #define DRESSI_TEX_KEEP_IMAGES 1u
 /* Keep d loss / d tex of the last iteration readable. */
 #define DRESSI_TEX_KEEP_GRAD 2u
+/* The per-view clip positions and ScreenAttr images are the caller's
+ * (dressi_tex_set_clips, before each step that changes them) instead of
+ * MVP * pos: the example graph's per-iteration sendImg of each view's
+ * clip and inverse-UV attribute (texture_optimization/run.cpp:106-109,
+ * 166-178). The cameras are then not used. */
+#define DRESSI_TEX_EXTERNAL_CLIP 4u
 
 int dressi_tex_create(dressi_ctx* ctx, const dressi_tex_desc* desc,
                       dressi_tex_plan** out);
@@ -664,6 +670,10 @@ int dressi_tex_set_mesh(dressi_tex_plan* plan, const float* pos,
                         const float* uv, const float* faces);
 /* Cameras: mvps {n_sets, N, 16} column-major. */
 int dressi_tex_set_cameras(dressi_tex_plan* plan, const float* mvps);
+/* DRESSI_TEX_EXTERNAL_CLIP: clip {N,V} VEC4 and attrs {N,V} VEC4 =
+ * ScreenAttr(clip) (z = 1, w = 0 checked), view-major; synchronous. */
+int dressi_tex_set_clips(dressi_tex_plan* plan, const float* clips,
+                         const float* attrs);
 /* The target texture {T} RGBA (gt_tex). */
 int dressi_tex_set_target(dressi_tex_plan* plan, const float* gt_tex);
 /* Texture and Adam state {T} RGBA from host (m, v may be NULL = 0). */

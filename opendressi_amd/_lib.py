@@ -51,6 +51,7 @@ PBR_KEEP_GRAD = 2
 
 TEX_KEEP_IMAGES = 1
 TEX_KEEP_GRAD = 2
+TEX_EXTERNAL_CLIP = 4
 (TEX_LOSS, TEX_PRED, TEX_TARGET, TEX_FACE_ID, TEX_GRAD, TEX_TEX, TEX_UV) = range(7)
 
 HSR_KEEP_PRED = 1
@@ -154,6 +155,7 @@ _SIGS = {
     "dressi_tex_destroy": (_I, [_P]),
     "dressi_tex_set_mesh": (_I, [_P, _FP, _FP, _FP]),
     "dressi_tex_set_cameras": (_I, [_P, _FP]),
+    "dressi_tex_set_clips": (_I, [_P, _FP, _FP]),
     "dressi_tex_set_target": (_I, [_P, _FP]),
     "dressi_tex_set_state": (_I, [_P, _FP, _FP, _FP, _F]),
     "dressi_tex_get_state": (_I, [_P, _FP, _FP, _FP, _FP]),

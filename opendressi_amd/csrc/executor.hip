@@ -25,7 +25,7 @@
 // semantics, so results do not depend on the packing.
 //
 // A graph recognised as the reference's silhouette-fit example (HardSoftRas
-// or AA, see route.h) runs on the fused silhouette plan instead.
+// or AA) or as the texture fit (see route.h) runs on its fused plan instead.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -705,8 +705,8 @@ struct DressiAD::Impl {
     Variables batch_downloads;
     bool have_download = false;
     CpuImage download;
-    // the fused silhouette plan, when the graph is recognised
-    std::unique_ptr<SilhouetteRoute> route;
+    // the fused plan (silhouette or texture fit), when the graph is recognised
+    std::unique_ptr<FusedRoute> route;
     bool route_rejected = false;
     // This instance's own C-ABI context on the shared context's stream: its
     // per-op workspaces are used by this instance only, so the device
@@ -1453,7 +1453,7 @@ struct DressiAD::Impl {
         }
     }
 
-    // ---- the fused silhouette plan ------------------------------------------
+    // ---- the fused plans (route.h) ------------------------------------------
 
     // Hand the graph back to the generic executor: the route's leaf images
     // (current optimiser state included) become pending sends.
@@ -1798,7 +1798,7 @@ void DressiAD::execStep() {
                 im.leaf_vars.push_back(inp);
             }
         }
-        // the fused silhouette plan, when the graph is the example's
+        // a fused plan, when the graph is one of the examples'
         if (im.route) {
             im.drop_route();
         }
@@ -1812,7 +1812,7 @@ void DressiAD::execStep() {
             g.extra_outputs = im.extra_outputs;
             g.grad_outputs = im.grad_outputs;
             g.funcs = &im.all_funcs;
-            im.route = SilhouetteRoute::Recognise(g);
+            im.route = RecogniseFusedRoute(g);
         }
     }
     bool routed = false;

@@ -1,4 +1,5 @@
-// route.h -- hands a DressiAD graph that is the silhouette-fit example's
+// route.h -- hands a DressiAD graph that is one of the fit examples' to its
+// fused plan. The silhouette fit: a graph that is the silhouette-fit example's
 // (examples/silhouette_optimization/run.cpp:229-437: technique hardsoftras
 // with one peel, or aa; all views each iteration; the in-graph Adam, with
 // or without its regularisers at weight 0) to the fused silhouette plan
@@ -37,32 +38,72 @@ struct GraphRoots {
     const Functions* funcs = nullptr;
 };
 
-class SilhouetteRoute {
+// A fused plan standing in for the generic executor on a recognised graph.
+class FusedRoute {
 public:
-    // nullptr unless the graph is the example's
-    static std::unique_ptr<SilhouetteRoute> Recognise(const GraphRoots& g);
-    ~SilhouetteRoute();
+    virtual ~FusedRoute() = default;
 
-    std::string name() const;  // "fused:hardsoftras" / "fused:aa"
-    size_t kernels() const;    // kernels per iteration
+    virtual std::string name() const = 0;  // "fused:<plan>"
+    virtual size_t kernels() const = 0;    // kernels per iteration
 
     // Leaf image from sendImg. false: `var` is computed by the graph (the
     // plan cannot take an image for it). Images of variables outside the
     // graph are ignored, as the generic executor never reads them.
-    bool Accept(const Variable& var, const CpuImageView& img);
+    virtual bool Accept(const Variable& var, const CpuImageView& img) = 0;
     // One iteration on `ctx`'s stream. false: the leaf images do not fit
     // the plan; `back` then holds every leaf image the route has (current
     // optimiser state included) and the caller runs the graph itself.
-    bool Step(dressi_ctx* ctx, std::map<Variable, CpuImage>* back);
+    virtual bool Step(dressi_ctx* ctx, std::map<Variable, CpuImage>* back) = 0;
     // Every leaf image the route holds, current state included
-    void Export(std::map<Variable, CpuImage>* back);
+    virtual void Export(std::map<Variable, CpuImage>* back) = 0;
 
-    bool Readable(const Variable& var) const;
-    CpuImage Recv(const Variable& var);
+    virtual bool Readable(const Variable& var) const = 0;
+    virtual CpuImage Recv(const Variable& var) = 0;
+};
+
+// The silhouette route, else the texture route (tests/graph_tex.cpp's form
+// of examples/texture_optimization/run.cpp:112-145: TextureBilinear on an
+// RGBA texture, the RGB L2 image loss, the in-graph Adam, per-view clip and
+// ScreenAttr images sent each step, on dressi_tex_* with
+// DRESSI_TEX_EXTERNAL_CLIP); nullptr when neither recognises the graph.
+std::unique_ptr<FusedRoute> RecogniseFusedRoute(const GraphRoots& g);
+
+class SilhouetteRoute : public FusedRoute {
+public:
+    // nullptr unless the graph is the example's
+    static std::unique_ptr<SilhouetteRoute> Recognise(const GraphRoots& g);
+    ~SilhouetteRoute() override;
+
+    std::string name() const override;  // "fused:hardsoftras" / "fused:aa"
+    size_t kernels() const override;
+    bool Accept(const Variable& var, const CpuImageView& img) override;
+    bool Step(dressi_ctx* ctx, std::map<Variable, CpuImage>* back) override;
+    void Export(std::map<Variable, CpuImage>* back) override;
+    bool Readable(const Variable& var) const override;
+    CpuImage Recv(const Variable& var) override;
 
 private:
     struct State;
     explicit SilhouetteRoute(std::unique_ptr<State> st);
+    std::unique_ptr<State> st_;
+};
+
+class TextureRoute : public FusedRoute {
+public:
+    static std::unique_ptr<TextureRoute> Recognise(const GraphRoots& g);
+    ~TextureRoute() override;
+
+    std::string name() const override;  // "fused:texture"
+    size_t kernels() const override;
+    bool Accept(const Variable& var, const CpuImageView& img) override;
+    bool Step(dressi_ctx* ctx, std::map<Variable, CpuImage>* back) override;
+    void Export(std::map<Variable, CpuImage>* back) override;
+    bool Readable(const Variable& var) const override;
+    CpuImage Recv(const Variable& var) override;
+
+private:
+    struct State;
+    explicit TextureRoute(std::unique_ptr<State> st);
     std::unique_ptr<State> st_;
 };
 

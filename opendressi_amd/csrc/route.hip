@@ -1,6 +1,6 @@
-// route.hip -- recognition of the silhouette-fit example graph and its
-// execution on the fused silhouette plan (route.h). Host code: the plan's
-// kernels live in hsr.hip / aa.hip.
+// route.hip -- recognition of the silhouette-fit and texture-fit example
+// graphs and their execution on the fused plans (route.h). Host code: the
+// plans' kernels live in hsr.hip / aa.hip / tex.hip.
 #include <algorithm>
 #include <cstring>
 #include <set>
@@ -309,15 +309,17 @@ bool read_params(const GraphRoots& g, Params* p) {
            p->Ft > 0;
 }
 
-// Structural comparison of a user graph with the template, from the roots
-struct Matcher {
-    const Template& T;
+// Structural comparison of a user graph with a template (free_slot, n_slots),
+// from the roots
+template <typename TT>
+struct MatcherT {
+    const TT& T;
     std::set<std::pair<const VariableNode*, const VariableNode*>> done;  // (user, template)
     std::unordered_map<const VariableNode*, const VariableNode*> leaf_of;  // template -> user
     std::vector<float> slot_val;
     std::vector<bool> slot_set;
 
-    explicit Matcher(const Template& t)
+    explicit MatcherT(const TT& t)
         : T(t), slot_val(t.n_slots, 0.f), slot_set(t.n_slots, false) {}
 
     bool match(const std::shared_ptr<VariableNode>& u, const std::shared_ptr<VariableNode>& t) {
@@ -385,6 +387,8 @@ struct Matcher {
         return match(NodeAccess::Node(u), NodeAccess::Node(t));
     }
 };
+
+using Matcher = MatcherT<Template>;
 
 bool is_integer_below(float x, uint32_t n) {
     return x >= 0.f && x < (float)n && x == (float)(uint32_t)x;
@@ -874,6 +878,566 @@ CpuImage SilhouetteRoute::Recv(const Variable& var) {
         return read(DRESSI_HSR_TARGET, npx * (size_t)(k - kServeTarget0), CpuImage(W, H, 1));
     }
     return read(DRESSI_HSR_PRED, npx * (size_t)(k - kServePred0), CpuImage(W, H, 1));
+}
+
+// ---- the texture fit ---------------------------------------------------------
+
+namespace {
+
+// Leaf roles of the texture graph (tests/graph_tex.cpp: the deferred unlit
+// graph of examples/texture_optimization/run.cpp:112-145 with
+// TextureBilinear, the RGB L2 image loss and the in-graph Adam of the
+// silhouette example, run.cpp:404-437)
+enum TexRole : int {
+    kTUv,      // VEC2 {V,1}: vertex uv
+    kTFaces,   // IVEC3 {F,1}
+    kTUvClip,  // VEC4 {V,1}: UvAsClip(uv)
+    kTOnes,    // FLOAT {V,1}: 1
+    kTGt,      // VEC4 {T}: the target texture
+    kTTex,     // VEC4 {T}: the optimised texture
+    kTM,
+    kTV,
+    kTT,
+    kTClip0 = 16,  // + view: the view's clip positions, sent each step
+    kTAttr0 = 32,  // + view: ScreenAttr of them
+};
+
+enum TexServe : int { kTServeLoss, kTServeGrad, kTServeTex, kTServeM, kTServeV, kTServeT,
+                      kTServePred0 = 16, kTServeTarget0 = 32 };
+
+struct TexParams {
+    uint32_t V = 0, F = 0, N = 0;
+    ImgSize S, T;
+};
+
+struct TexTemplate {
+    std::map<int, Variable> leaves;
+    Variable g{nullptr};
+    Variables targets, preds;
+    Variables g_uvs, inv_uvs;  // per view
+    Variable loss{nullptr}, updated{nullptr};
+    std::vector<std::pair<Variable, Variable>> updates;
+    std::unordered_map<const FunctionNode*, int> free_slot;
+    int slot_lr = 0, n_slots = 1;
+};
+
+TexTemplate build_tex_template(const TexParams& p) {
+    TexTemplate T;
+    auto leaf = [&](int role, VType t, ImgSize s) {
+        Variable v(t, s);
+        T.leaves[role] = v;
+        return v;
+    };
+    const Variable vtx_uv = leaf(kTUv, VEC2, {p.V, 1});
+    const Variable faces = leaf(kTFaces, IVEC3, {p.F, 1});
+    const Variable uv_clip = leaf(kTUvClip, VEC4, {p.V, 1});
+    const Variable ones = leaf(kTOnes, FLOAT, {p.V, 1});
+    const Variable gt_tex = leaf(kTGt, VEC4, p.T);
+    const Variable tex = leaf(kTTex, VEC4, p.T);
+    const Variable adam_m = leaf(kTM, VEC4, p.T);
+    const Variable adam_v = leaf(kTV, VEC4, p.T);
+    const Variable adam_t = leaf(kTT, FLOAT, {1, 1});
+    const float c = 1.f / float(p.S.w * p.S.h);
+    Variables view_losses;
+    for (uint32_t v = 0; v < p.N; v++) {
+        const Variable clip = leaf(kTClip0 + (int)v, VEC4, {p.V, 1});
+        const Variable attr = leaf(kTAttr0 + (int)v, VEC4, {p.V, 1});
+        const Variable g_uv = F::Rasterize(clip, vtx_uv, faces, p.S);
+        const Variable g_mask = F::Rasterize(clip, ones, faces, p.S);
+        const Variable inv_uv = F::Rasterize(uv_clip, attr, faces, p.T);
+        const Variable target = g_mask * F::TextureBilinear(gt_tex, g_uv, inv_uv);
+        const Variable pred = g_mask * F::TextureBilinear(tex, g_uv, inv_uv);
+        const Variable diff = F::StopGradient(target) - pred;
+        view_losses.push_back(diff * diff * F::Vec4(c, c, c, 0.f));
+        T.targets.push_back(target);
+        T.preds.push_back(pred);
+        T.g_uvs.push_back(g_uv);
+        T.inv_uvs.push_back(inv_uv);
+    }
+    T.loss = F::SumPixelWise(view_losses);
+    T.g = Variable(VEC4, p.T);
+    const Variable g = T.g;
+    const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+    const Variable t_new = adam_t + 1.f;
+    const Variable m_new = adam_m * b1 + g * (1.f - b1);
+    const Variable v_new = adam_v * b2 + g * g * (1.f - b2);
+    const Variable bc1 = 1.f - F::Pow(F::Float(b1), t_new);
+    const Variable bc2 = 1.f - F::Pow(F::Float(b2), t_new);
+    const Variable lr = F::Float(0.f);
+    T.free_slot[NodeAccess::Node(lr)->creator.get()] = T.slot_lr;
+    const Variable step = F::Mul((m_new / bc1) / (F::Sqrt(v_new / bc2) + eps), lr);
+    T.updates = {{adam_m, m_new}, {adam_v, v_new}, {adam_t, t_new}};
+    T.updated = tex - step;
+    return T;
+}
+
+bool read_tex_params(const GraphRoots& g, TexParams* p) {
+    if (g.input_vars.size() != 1 || g.updated_vars.size() != 1 || g.input_grad_vars.size() != 1) {
+        return false;
+    }
+    const Variable& tex = g.input_vars[0];
+    if (tex.getVType() != VEC4) {
+        return false;
+    }
+    p->T = tex.getImgSize();
+    std::vector<const FunctionNode*> tb;
+    for (const auto& f : *g.funcs) {
+        const auto& n = NodeAccess::Node(f);
+        switch (n->op) {
+            case Op::kTextureBilinear: tb.push_back(n.get()); break;
+            case Op::kCustom:
+            case Op::kSetFragDepth:
+            case Op::kPeelDepth: return false;
+            default: break;
+        }
+    }
+    // TextureBilinear(tex, uv): inv_uv is held by its backward
+    if (tb.empty() || tb.size() % 2 != 0 || tb[0]->xs.size() != 2) {
+        return false;
+    }
+    p->N = (uint32_t)(tb.size() / 2);
+    const auto& uv = tb[0]->xs[1];
+    if (!uv->creator || uv->creator->op != Op::kRasterize || uv->creator->xs.size() != 3) {
+        return false;
+    }
+    p->S = uv->size;
+    p->V = uv->creator->xs[0]->size.w;
+    p->F = uv->creator->xs[2]->size.w;
+    return p->N >= 1 && p->N <= 8 && p->V > 0 && p->F > 0 && p->S.w == p->S.h && p->S.w > 0 &&
+           p->T.w > 0 && p->T.h > 0;
+}
+
+}  // namespace
+
+struct TextureRoute::State {
+    TexParams p;
+    float lr = 0.f;
+    std::map<int, Variable> user_leaf;
+    std::unordered_map<const VariableNode*, std::vector<int>> roles_of;
+    std::unordered_map<const VariableNode*, int> serve;
+    std::unordered_set<const VariableNode*> in_graph;
+    bool keep_pred = false, keep_grad = false;
+    std::map<int, CpuImage> data;
+    bool mesh_dirty = true, target_dirty = true, clips_dirty = true;
+    std::set<int> state_dirty;
+    dressi_ctx* ctx = nullptr;
+    dressi_tex_plan* plan = nullptr;
+    bool state_on_plan = false;
+    uint32_t steps = 0;
+
+    ~State() { drop_plan(); }
+
+    void drop_plan() {
+        if (plan) {
+            dressi_tex_destroy(plan);
+            plan = nullptr;
+        }
+        state_on_plan = false;
+    }
+
+    bool have(int role) const { return data.count(role) != 0; }
+
+    // the static leaves the plan derives from uv and faces
+    bool mesh_fits() const {
+        if (!have(kTUv) || !have(kTFaces) || !have(kTUvClip) || !have(kTOnes)) {
+            return false;
+        }
+        for (float x : data.at(kTFaces).data) {
+            if (!is_integer_below(x, p.V)) {
+                return false;
+            }
+        }
+        if (UvAsClip(data.at(kTUv)).data != data.at(kTUvClip).data) {
+            return false;
+        }
+        for (float x : data.at(kTOnes).data) {
+            if (x != 1.f) {
+                return false;
+            }
+        }
+        return true;
+    }
+
+    // every view's clip and ScreenAttr image (z = 1, w = 0)
+    bool clips_fit() const {
+        for (uint32_t v = 0; v < p.N; v++) {
+            if (!have(kTClip0 + (int)v) || !have(kTAttr0 + (int)v)) {
+                return false;
+            }
+            const std::vector<float>& a = data.at(kTAttr0 + (int)v).data;
+            for (size_t i = 0; i + 3 < a.size(); i += 4) {
+                if (a[i + 2] != 1.f || a[i + 3] != 0.f) {
+                    return false;
+                }
+            }
+        }
+        return true;
+    }
+
+    void read_state(CpuImage* tex, CpuImage* m, CpuImage* v, float* t) {
+        *tex = CpuImage(p.T.w, p.T.h, 4);
+        *m = CpuImage(p.T.w, p.T.h, 4);
+        *v = CpuImage(p.T.w, p.T.h, 4);
+        check_hip_rc(dressi_tex_get_state(plan, tex->data.data(), m->data.data(), v->data.data(),
+                                          t),
+                     "dressi_tex_get_state");
+    }
+
+    void pull_state() {
+        if (!plan || !state_on_plan) {
+            return;
+        }
+        CpuImage tex, m, v;
+        float t = 0.f;
+        read_state(&tex, &m, &v, &t);
+        if (!state_dirty.count(kTTex)) data[kTTex] = tex;
+        if (!state_dirty.count(kTM)) data[kTM] = m;
+        if (!state_dirty.count(kTV)) data[kTV] = v;
+        if (!state_dirty.count(kTT)) data[kTT] = CpuImage(1, 1, 1, t);
+    }
+
+    void push_state() {
+        for (int r : {kTTex, kTM, kTV, kTT}) {
+            if (!have(r)) {
+                data[r] = r == kTT ? CpuImage(1, 1, 1) : CpuImage(p.T.w, p.T.h, 4);
+            }
+        }
+        check_hip_rc(dressi_tex_set_state(plan, data.at(kTTex).data.data(), data.at(kTM).data.data(),
+                                          data.at(kTV).data.data(), data.at(kTT).data[0]),
+                     "dressi_tex_set_state");
+        state_dirty.clear();
+        state_on_plan = true;
+    }
+
+    void create_plan() {
+        dressi_tex_desc d{};
+        d.n_verts = p.V;
+        d.n_faces = p.F;
+        d.n_views = p.N;
+        d.width = p.S.w;
+        d.height = p.S.h;
+        d.tex_w = p.T.w;
+        d.tex_h = p.T.h;
+        d.n_sets = 1;
+        d.lr = lr;
+        d.beta1 = 0.9f;
+        d.beta2 = 0.999f;
+        d.eps = 1e-8f;
+        d.flags = DRESSI_TEX_EXTERNAL_CLIP | (keep_pred ? DRESSI_TEX_KEEP_IMAGES : 0u) |
+                  (keep_grad ? DRESSI_TEX_KEEP_GRAD : 0u);
+        check_hip_rc(dressi_tex_create(ctx, &d, &plan), "dressi_tex_create");
+        const std::vector<float> pos((size_t)p.V * 3, 0.f);  // unused with external clips
+        check_hip_rc(dressi_tex_set_mesh(plan, pos.data(), data.at(kTUv).data.data(),
+                                         data.at(kTFaces).data.data()),
+                     "dressi_tex_set_mesh");
+    }
+
+    void upload_clips() {
+        const size_t nv = (size_t)p.V * 4;
+        std::vector<float> clips(nv * p.N), attrs(nv * p.N);
+        for (uint32_t v = 0; v < p.N; v++) {
+            std::copy(data.at(kTClip0 + (int)v).data.begin(), data.at(kTClip0 + (int)v).data.end(),
+                      clips.begin() + (ptrdiff_t)(nv * v));
+            std::copy(data.at(kTAttr0 + (int)v).data.begin(), data.at(kTAttr0 + (int)v).data.end(),
+                      attrs.begin() + (ptrdiff_t)(nv * v));
+        }
+        check_hip_rc(dressi_tex_set_clips(plan, clips.data(), attrs.data()), "dressi_tex_set_clips");
+    }
+};
+
+TextureRoute::TextureRoute(std::unique_ptr<State> st) : st_(std::move(st)) {}
+TextureRoute::~TextureRoute() = default;
+
+std::string TextureRoute::name() const { return "fused:texture"; }
+
+size_t TextureRoute::kernels() const { return 5; }
+
+std::unique_ptr<TextureRoute> TextureRoute::Recognise(const GraphRoots& g) {
+    TexParams p;
+    if (!g.funcs || !g.loss || !read_tex_params(g, &p)) {
+        return nullptr;
+    }
+    std::unique_ptr<TexTemplate> T;
+    try {
+        T = std::make_unique<TexTemplate>(build_tex_template(p));
+    } catch (const DressiError&) {
+        return nullptr;
+    }
+    MatcherT<TexTemplate> M(*T);
+    const Variable& g_user = g.input_grad_vars[0];
+    if (g_user.getVType() != VEC4 || !(g_user.getImgSize() == T->g.getImgSize())) {
+        return nullptr;
+    }
+    M.leaf_of[NodeAccess::Node(T->g).get()] = NodeAccess::Node(g_user).get();
+    if (!M.match(g.loss, T->loss) || !M.match(g.updated_vars[0], T->updated)) {
+        return nullptr;
+    }
+    if (g.extra_updates.size() != T->updates.size()) {
+        return nullptr;
+    }
+    for (size_t i = 0; i < T->updates.size(); i++) {
+        const auto& [leaf_u, upd_u] = g.extra_updates[i];
+        const auto& [leaf_t, upd_t] = T->updates[i];
+        if (!M.match(upd_u, upd_t) || !M.match(leaf_u, leaf_t)) {
+            return nullptr;
+        }
+    }
+    // The inverse-UV rasters: TextureBilinear keeps inv_uv for its backward,
+    // so the graph holds them as the inputs of the GatherByInverseUVBilinear
+    // nodes built for the prediction of each view: (gy, inv_uv, g_uv).
+    {
+        std::unordered_map<const VariableNode*, const VariableNode*> user_of;  // template -> user
+        for (const auto& [u, t] : M.done) {
+            user_of[t] = u;
+        }
+        std::vector<int> seen(p.N, 0);
+        for (const auto& f : *g.funcs) {
+            const auto& n = NodeAccess::Node(f);
+            if (n->op != Op::kGatherInvUvBilinear) {
+                continue;
+            }
+            if (n->xs.size() != 3) {
+                return nullptr;
+            }
+            uint32_t v = 0;
+            while (v < p.N) {
+                auto it = user_of.find(NodeAccess::Node(T->g_uvs[v]).get());
+                if (it != user_of.end() && it->second == n->xs[2].get()) {
+                    break;
+                }
+                v++;
+            }
+            if (v == p.N || !M.match(n->xs[1], NodeAccess::Node(T->inv_uvs[v]))) {
+                return nullptr;
+            }
+            seen[v]++;
+        }
+        for (uint32_t v = 0; v < p.N; v++) {
+            if (!seen[v]) {
+                return nullptr;  // no backward through a view's prediction
+            }
+        }
+    }
+    auto tex_leaf = M.leaf_of.find(NodeAccess::Node(T->leaves.at(kTTex)).get());
+    if (tex_leaf == M.leaf_of.end() ||
+        tex_leaf->second != NodeAccess::Node(g.input_vars[0]).get() || !M.slot_set[T->slot_lr]) {
+        return nullptr;
+    }
+    auto st = std::make_unique<State>();
+    st->p = p;
+    st->lr = M.slot_val[T->slot_lr];
+    for (const auto& [role, tv] : T->leaves) {
+        auto it = M.leaf_of.find(NodeAccess::Node(tv).get());
+        if (it != M.leaf_of.end()) {
+            st->roles_of[it->second].push_back(role);
+        }
+    }
+    std::unordered_map<const VariableNode*, int> serve_t;
+    serve_t[NodeAccess::Node(T->loss).get()] = kTServeLoss;
+    serve_t[NodeAccess::Node(T->updated).get()] = kTServeTex;
+    serve_t[NodeAccess::Node(T->updates[0].second).get()] = kTServeM;
+    serve_t[NodeAccess::Node(T->updates[1].second).get()] = kTServeV;
+    serve_t[NodeAccess::Node(T->updates[2].second).get()] = kTServeT;
+    for (uint32_t v = 0; v < p.N; v++) {
+        serve_t[NodeAccess::Node(T->preds[v]).get()] = kTServePred0 + (int)v;
+        serve_t[NodeAccess::Node(T->targets[v]).get()] = kTServeTarget0 + (int)v;
+    }
+    for (const auto& [u, t] : M.done) {
+        st->in_graph.insert(u);
+        auto s = serve_t.find(t);
+        if (s != serve_t.end()) {
+            st->serve[u] = s->second;
+        }
+    }
+    st->serve[NodeAccess::Node(g_user).get()] = kTServeGrad;
+    st->in_graph.insert(NodeAccess::Node(g_user).get());
+    st->keep_grad = g.grad_outputs;
+    for (const auto& v : g.extra_outputs) {
+        const VariableNode* n = NodeAccess::Node(v).get();
+        auto s = st->serve.find(n);
+        if (s != st->serve.end()) {
+            st->keep_pred |= s->second >= kTServePred0;
+            st->keep_grad |= s->second == kTServeGrad;
+        } else if (!st->roles_of.count(n)) {
+            return nullptr;  // an output the plan does not keep
+        }
+    }
+    for (const auto& f : *g.funcs) {
+        for (const auto& x : f.getInputVars()) {
+            auto it = st->roles_of.find(NodeAccess::Node(x).get());
+            if (it != st->roles_of.end()) {
+                for (int r : it->second) {
+                    st->user_leaf.emplace(r, x);
+                }
+            }
+        }
+    }
+    for (const auto& [leaf_u, upd_u] : g.extra_updates) {
+        auto it = st->roles_of.find(NodeAccess::Node(leaf_u).get());
+        if (it != st->roles_of.end()) {
+            for (int r : it->second) {
+                st->user_leaf.emplace(r, leaf_u);
+            }
+        }
+    }
+    return std::unique_ptr<TextureRoute>(new TextureRoute(std::move(st)));
+}
+
+bool TextureRoute::Accept(const Variable& var, const CpuImageView& img) {
+    State& s = *st_;
+    const VariableNode* n = NodeAccess::Node(var).get();
+    auto it = s.roles_of.find(n);
+    if (it == s.roles_of.end()) {
+        return !s.in_graph.count(n);
+    }
+    CpuImage copy(img.width, img.height, img.channels);
+    std::copy(img.data, img.data + img.numElems(), copy.data.begin());
+    for (int r : it->second) {
+        s.data[r] = copy;
+        if (r == kTTex || r == kTM || r == kTV || r == kTT) {
+            s.state_dirty.insert(r);
+        } else if (r == kTGt) {
+            s.target_dirty = true;
+        } else if (r >= kTClip0) {
+            s.clips_dirty = true;
+        } else {
+            s.mesh_dirty = true;
+        }
+    }
+    return true;
+}
+
+void TextureRoute::Export(std::map<Variable, CpuImage>* back) {
+    State& s = *st_;
+    s.pull_state();
+    for (const auto& [role, var] : s.user_leaf) {
+        auto d = s.data.find(role);
+        if (d != s.data.end()) {
+            (*back)[var] = d->second;
+        }
+    }
+}
+
+bool TextureRoute::Step(dressi_ctx* ctx, std::map<Variable, CpuImage>* back) {
+    State& s = *st_;
+    if (s.plan && s.ctx != ctx) {
+        throw DressiError("the fused texture plan moved to another context");
+    }
+    s.ctx = ctx;
+    if (s.mesh_dirty) {
+        if (!s.mesh_fits()) {
+            Export(back);
+            return false;
+        }
+        if (s.plan) {
+            s.pull_state();
+            for (int r : {kTTex, kTM, kTV, kTT}) {
+                s.state_dirty.insert(r);
+            }
+            s.drop_plan();
+        }
+    }
+    if (!s.clips_fit() || !s.have(kTGt)) {
+        Export(back);
+        return false;
+    }
+    if (!s.plan) {
+        s.create_plan();
+        s.target_dirty = true;
+        s.clips_dirty = true;
+        for (int r : {kTTex, kTM, kTV, kTT}) {
+            s.state_dirty.insert(r);
+        }
+    }
+    s.mesh_dirty = false;
+    if (s.target_dirty) {
+        check_hip_rc(dressi_tex_set_target(s.plan, s.data.at(kTGt).data.data()),
+                     "dressi_tex_set_target");
+        s.target_dirty = false;
+    }
+    if (s.clips_dirty) {
+        s.upload_clips();
+        s.clips_dirty = false;
+    }
+    if (!s.state_dirty.empty()) {
+        s.pull_state();
+        s.push_state();
+    }
+    check_hip_rc(dressi_tex_step(s.plan, 1), "dressi_tex_step");
+    s.steps++;
+    return true;
+}
+
+bool TextureRoute::Readable(const Variable& var) const {
+    const VariableNode* n = NodeAccess::Node(var).get();
+    auto it = st_->serve.find(n);
+    if (it != st_->serve.end()) {
+        const int k = it->second;
+        if (k >= kTServePred0) {
+            return st_->keep_pred;
+        }
+        return k != kTServeGrad || st_->keep_grad;
+    }
+    return st_->roles_of.count(n) != 0;
+}
+
+CpuImage TextureRoute::Recv(const Variable& var) {
+    State& s = *st_;
+    const VariableNode* n = NodeAccess::Node(var).get();
+    DRESSI_CHECK(Readable(var),
+                 "recvImg: the fused texture plan does not keep this Variable (markOutput it "
+                 "before the first execStep)");
+    DRESSI_CHECK(s.plan && s.steps > 0, "recvImg before the first execStep()");
+    auto sv = s.serve.find(n);
+    if (sv == s.serve.end()) {
+        s.pull_state();
+        auto d = s.data.find(s.roles_of.at(n)[0]);
+        DRESSI_CHECK(d != s.data.end(), "recvImg: no image was sent to this leaf");
+        return d->second;
+    }
+    const int k = sv->second;
+    const size_t npx4 = (size_t)s.p.S.w * s.p.S.h * 4;
+    auto read = [&](int which, size_t off, CpuImage img) {
+        void* dev = nullptr;
+        size_t bytes = 0;
+        check_hip_rc(dressi_tex_buffer(s.plan, which, &dev, &bytes), "dressi_tex_buffer");
+        std::vector<float> all(bytes / sizeof(float));
+        DRESSI_CHECK(off + img.data.size() <= all.size(), "recvImg: plan buffer size");
+        check_hip_rc(dressi_tex_read(s.plan, which, all.data(), bytes), "dressi_tex_read");
+        std::copy(all.begin() + (ptrdiff_t)off, all.begin() + (ptrdiff_t)(off + img.data.size()),
+                  img.data.begin());
+        return img;
+    };
+    switch (k) {
+        case kTServeLoss: return read(DRESSI_TEX_LOSS, 0, CpuImage(s.p.S.w, s.p.S.h, 4));
+        case kTServeGrad: return read(DRESSI_TEX_GRAD, 0, CpuImage(s.p.T.w, s.p.T.h, 4));
+        case kTServeTex:
+        case kTServeM:
+        case kTServeV:
+        case kTServeT: {
+            CpuImage tex, m, v;
+            float t = 0.f;
+            s.read_state(&tex, &m, &v, &t);
+            return k == kTServeTex ? tex : k == kTServeM ? m : k == kTServeV ? v
+                                                                           : CpuImage(1, 1, 1, t);
+        }
+        default: break;
+    }
+    if (k >= kTServeTarget0) {
+        return read(DRESSI_TEX_TARGET, npx4 * (size_t)(k - kTServeTarget0),
+                    CpuImage(s.p.S.w, s.p.S.h, 4));
+    }
+    return read(DRESSI_TEX_PRED, npx4 * (size_t)(k - kTServePred0), CpuImage(s.p.S.w, s.p.S.h, 4));
+}
+
+std::unique_ptr<FusedRoute> RecogniseFusedRoute(const GraphRoots& g) {
+    if (auto r = SilhouetteRoute::Recognise(g)) {
+        return r;
+    }
+    if (auto r = TextureRoute::Recognise(g)) {
+        return r;
+    }
+    return nullptr;
 }
 
 }  // namespace dressi

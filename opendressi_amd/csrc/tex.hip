@@ -275,6 +275,7 @@ struct TexDev {
     float4* grad;           // [T] or null
     const float2* bc_tab;
     uint32_t bc_len;
+    uint32_t ext_clip;      // clip and sattr come from dressi_tex_set_clips
 };
 
 // Per (view, vertex): clip = MVP * (pos, 1) with the cameras of set
@@ -290,6 +291,9 @@ __global__ __launch_bounds__(256) void k_tex_clip(TexDev d) {
         // the backward never reads t itself, so its first thread may store
         // t + 1 without racing the others
         *d.t_next = *d.t + 1.f;
+    }
+    if (d.ext_clip) {
+        return;  // the caller's clip and ScreenAttr images
     }
     const uint32_t view = i / nv;
     const uint32_t vtx = i - view * nv;
@@ -731,7 +735,7 @@ struct dressi_tex_plan {
     std::vector<void*> allocs;
     void* bin_mem = nullptr;
     size_t bin_bytes = 0;
-    bool mesh_set = false, cams_set = false, target_set = false;
+    bool mesh_set = false, cams_set = false, target_set = false, clips_set = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     hipStream_t graph_stream = nullptr;
@@ -762,7 +766,11 @@ void tex_drop_graph(dressi_tex_plan* p) {
 int tex_ready(dressi_tex_plan* p) {
     DRESSI_REQUIRE(p, "NULL plan");
     DRESSI_REQUIRE(p->mesh_set, "dressi_tex_set_mesh() must be called before stepping");
-    DRESSI_REQUIRE(p->cams_set, "dressi_tex_set_cameras() must be called before stepping");
+    if (p->d.ext_clip) {
+        DRESSI_REQUIRE(p->clips_set, "dressi_tex_set_clips() must be called before stepping");
+    } else {
+        DRESSI_REQUIRE(p->cams_set, "dressi_tex_set_cameras() must be called before stepping");
+    }
     DRESSI_REQUIRE(p->target_set, "dressi_tex_set_target() must be called before stepping");
     return DRESSI_OK;
 }
@@ -936,6 +944,7 @@ int dressi_tex_create(dressi_ctx* ctx, const dressi_tex_desc* desc, dressi_tex_p
     d.b1 = desc->beta1;
     d.b2 = desc->beta2;
     d.eps = desc->eps;
+    d.ext_clip = (desc->flags & DRESSI_TEX_EXTERNAL_CLIP) ? 1u : 0u;
     const size_t V = desc->n_verts, F = desc->n_faces, N = desc->n_views;
     const size_t npx = (size_t)desc->width * desc->height;
     const size_t T = (size_t)desc->tex_w * desc->tex_h;
@@ -1091,6 +1100,27 @@ int dressi_tex_set_cameras(dressi_tex_plan* p, const float* mvps) {
                                   p->ctx->stream));
     DRESSI_TRY_HIP(hipStreamSynchronize(p->ctx->stream));
     p->cams_set = true;
+    return DRESSI_OK;
+}
+
+int dressi_tex_set_clips(dressi_tex_plan* p, const float* clips, const float* attrs) {
+    DRESSI_REQUIRE(p && clips && attrs, "bad arguments");
+    DRESSI_REQUIRE(p->d.ext_clip, "the plan was not created with DRESSI_TEX_EXTERNAL_CLIP");
+    DRESSI_TRY_HIP(hipSetDevice(p->ctx->device));
+    const size_t nv = (size_t)p->desc.n_views * p->desc.n_verts;
+    std::vector<float2> xy(nv);
+    for (size_t i = 0; i < nv; i++) {
+        DRESSI_REQUIRE(attrs[i * 4 + 2] == 1.f && attrs[i * 4 + 3] == 0.f,
+                       "attribute %zu is not a ScreenAttr (z = 1, w = 0)", i);
+        xy[i] = make_float2(attrs[i * 4], attrs[i * 4 + 1]);
+    }
+    hipStream_t s = p->ctx->stream;
+    DRESSI_TRY_HIP(hipMemcpyAsync((void*)p->d.r.clip, clips, nv * sizeof(float4),
+                                  hipMemcpyHostToDevice, s));
+    DRESSI_TRY_HIP(hipMemcpyAsync((void*)p->d.sattr, xy.data(), nv * sizeof(float2),
+                                  hipMemcpyHostToDevice, s));
+    DRESSI_TRY_HIP(hipStreamSynchronize(s));
+    p->clips_set = true;
     return DRESSI_OK;
 }
 

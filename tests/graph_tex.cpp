@@ -6,7 +6,7 @@
 // clip / inverse-UV attribute images every iteration (the example's
 // per-iteration sendImg of moving cameras).
 //
-//   graph_tex <in.bin> <out.bin>
+//   graph_tex <in.bin> <out.bin> [warmup]
 // in.bin:  u32 V, F, N, S, tex_w, tex_h, iters, n_sets, packing (0 RSP,
 //          1 Naive); f32 lr; pos {V,3}, uv {V,2}, faces {F,3},
 //          mvps {n_sets, N, 16}, gt_tex {T,4}, tex0 {T,4}
@@ -14,8 +14,14 @@
 // out.bin: tex, m, v {T,4}, t, loss[iters] (sum of the loss image),
 //          grad0 {T,4} (first iteration)
 // stdout:  "graph_tex: plan=<name> stages=<n> substages=<n> funcs=<n>"
+// With `warmup` (timing, the example's loop: each step sends its cameras'
+// images and runs execStep, nothing is read back): `warmup` untimed steps,
+// then `iters` timed ones, "graph_tex: ms_per_step=<ms>"; out.bin as above
+// with the losses zero.
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
+#include <cstdlib>
 #include <vector>
 
 #include "dressi/dressi.h"
@@ -49,9 +55,10 @@ CpuImage Read(FILE* f, uint32_t w, uint32_t h, uint32_t c) {
 
 int main(int argc, char** argv) {
     try {
-        if (argc != 3) {
-            throw DressiError("usage: graph_tex <in.bin> <out.bin>");
+        if (argc != 3 && argc != 4) {
+            throw DressiError("usage: graph_tex <in.bin> <out.bin> [warmup]");
         }
+        const int warmup = argc == 4 ? std::atoi(argv[3]) : 0;
         FILE* fi = fopen(argv[1], "rb");
         if (!fi) {
             throw DressiError("cannot open input");
@@ -141,7 +148,7 @@ int main(int argc, char** argv) {
         std::vector<float> losses(iters);
         CpuImage grad0;
         std::vector<CpuImage> clip_imgs(n_views), attr_imgs(n_views);
-        for (uint32_t it = 0; it < iters; it++) {
+        auto sends_of = [&](uint32_t it) {
             const float* set = mvps.data() + size_t(it % n_sets) * n_views * 16;
             std::vector<std::pair<Variable, CpuImageView>> sends;
             for (uint32_t v = 0; v < n_views; v++) {
@@ -150,6 +157,22 @@ int main(int argc, char** argv) {
                 sends.emplace_back(clips[v], CpuImageView(clip_imgs[v]));
                 sends.emplace_back(attrs[v], CpuImageView(attr_imgs[v]));
             }
+            return sends;
+        };
+        if (warmup > 0) {
+            for (int it = 0; it < warmup; it++) {
+                ad.execStepWithSends(sends_of((uint32_t)it));
+            }
+            const auto t0 = std::chrono::steady_clock::now();
+            for (uint32_t it = 0; it < iters; it++) {
+                ad.execStepWithSends(sends_of((uint32_t)warmup + it));
+            }
+            const auto t1 = std::chrono::steady_clock::now();
+            printf("graph_tex: ms_per_step=%.5f\n",
+                   std::chrono::duration<double, std::milli>(t1 - t0).count() / iters);
+        }
+        for (uint32_t it = 0; it < iters && warmup <= 0; it++) {
+            const auto sends = sends_of(it);
             const CpuImage li = ad.execStepWithSendsAndRecvImgsStacked(sends, {loss});
             double acc = 0.0;
             for (float x : li.data) {
@@ -159,6 +182,9 @@ int main(int argc, char** argv) {
             if (it == 0) {
                 grad0 = ad.recvImg(ad.inputGrads().at(0).second);
             }
+        }
+        if (warmup > 0) {
+            grad0 = CpuImage(tw, th, 4, 0.f);
         }
         FILE* fo = fopen(argv[2], "wb");
         if (!fo) {

@@ -265,9 +265,10 @@ def test_texture_example_graph_matches_oracle(tmp_path, oracle, naive):
     """The texture fit's graph (examples/texture_optimization/run.cpp:112-145
     with TextureBilinear, the RGB L2 loss and the in-graph Adam) written with
     the graph API (tests/graph_tex.cpp) and run by DressiAD with the cameras
-    sent every step: the first iteration's loss and texture gradient bit for
+    sent every step -- on the fused texture plan (RSP) or the generic
+    executor (Naive): the first iteration's loss and texture gradient bit for
     bit against the oracle's texture fit, the later losses and the Adam state
-    within 1e-6 (the bias correction's device powf)."""
+    within 1e-6 (the generic executor's bias correction is a device powf)."""
     import opendressi_amd as od
     w = od.TexWorkload("graph", 16, 8, 64, 32, 2, 3, 1e-2, 3, 7)
     pos, uv, faces, mvps, gt, tex0 = od.make_tex_scene(w)
@@ -287,6 +288,10 @@ def test_texture_example_graph_matches_oracle(tmp_path, oracle, naive):
                          timeout=120)
     assert res.returncode == 0, res.stderr
     print(" ", res.stdout.strip(), flush=True)
+    # RSP packing: the graph runs on the fused texture plan (one stage of its
+    # five kernels), the cameras' clip and ScreenAttr images sent each step
+    want_plan = "plan=generic" if naive else "plan=fused:texture stages=1 substages=5"
+    assert want_plan in res.stdout, res.stdout
     d = np.fromfile(out, np.float32)
     t_n = w.tex * w.tex * 4
     got = {}
@@ -302,6 +307,10 @@ def test_texture_example_graph_matches_oracle(tmp_path, oracle, naive):
     assert np.array_equal(got["grad0"], ref["grad0"].reshape(-1)), \
         f"grad0: max |d| {np.abs(got['grad0'] - ref['grad0'].reshape(-1)).max():.3g}"
     assert got["loss"][0] == ref["loss"][0], (got["loss"], ref["loss"])
+    if not naive:
+        # the fused plan: every iteration bit for bit
+        for k in ("tex", "m", "v", "loss"):
+            assert np.array_equal(got[k], ref[k].reshape(-1)), k
     np.testing.assert_allclose(got["loss"], ref["loss"], rtol=1e-6, atol=0)
     for k in ("tex", "m", "v"):
         want = ref[k].reshape(-1)
