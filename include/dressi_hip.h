@@ -117,8 +117,9 @@ int dressi_rasterize_soft(dressi_ctx* ctx, const float* soft_clip,
  * context workspace, so a call needs 256-byte-aligned 176 B + 16 B per face
  * plus 4100 B per 16x16 tile (+256) within 32 MiB (e.g. a 1024x1024 screen
  * with up to ~79k faces) and returns DRESSI_ERR_INVALID beyond that. Every
- * call on one GPU shares that GPU's array: calls that overlap on one GPU
- * (other streams, threads or contexts) race. */
+ * call on one GPU shares that GPU's array: a call on another stream than
+ * the GPU's previous call waits for that call's work first (not under
+ * graph capture); calls that overlap in host time (other threads) race. */
 int dressi_rasterize_soft_noalloc(dressi_ctx* ctx, const float* soft_clip,
                                   const float* face_id, const float* faces_soft,
                                   const float* hard_clip, uint32_t n_verts,

@@ -1016,8 +1016,8 @@ __global__ __launch_bounds__(256) void k_aa_face_scan(HsrDev d) {
     publish_t_next(d, gi);
     for (uint32_t b = gi; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
         const uint32_t c = d.bins.counts[b];
-        if (c > d.bins.cap && d.bin_over) {
-            *d.bin_over = c;  // rare: the host grows the bins before the next step
+        if (c > d.bins.cap && d.bin_over_max) {
+            atomicMax(d.bin_over_max, c);  // rare: the host grows the bins before the next step
         }
         d.bins.counts[b] = 0;
     }
@@ -1102,6 +1102,7 @@ __global__ __launch_bounds__(256) void k_aa_face_bwd(HsrDev d) {
 // workgroup advances t.
 template <int NV>
 __global__ __launch_bounds__(256) void k_aa_vertex_adam(HsrDev d) {
+    publish_bin_over(d);
     vertex_views_adam<NV>(d, [&](uint32_t vtx, uint32_t view, float (&g4)[4]) {
         const float4* gt = d.gtri + (size_t)view * 3 * d.g.n_faces;
         float acc[4] = {0.f, 0.f, 0.f, 0.f};

@@ -838,6 +838,55 @@ struct DressiAD::Impl {
         return (float*)p;
     }
     float* buf(const Variable& v) { return buf(NodeAccess::Node(v)); }
+
+    // Frees the device images of variables the current traversal no longer
+    // reaches (setting the loss or the optimiser again builds new backward
+    // and update nodes), with their cache entries and owners; the plan that
+    // referred to them is released first.
+    void prune_buffers() {
+        std::unordered_set<const VariableNode*> live;
+        auto add = [&](const Variable& v) {
+            if (v) live.insert(NodeAccess::Node(v).get());
+        };
+        for (const auto& f : all_funcs) {
+            for (const auto& x : f.getInputVars()) {
+                add(x);
+            }
+            if (const auto y = NodeAccess::Node(f)->y.lock()) {
+                live.insert(y.get());
+            }
+        }
+        for (const auto& v : leaf_vars) add(v);
+        for (const auto& [upd, inp] : copy_backs) {
+            add(upd);
+            add(inp);
+        }
+        for (const auto& v : extra_outputs) add(v);
+        for (const auto& v : input_grad_vars) add(v);
+        for (const auto& v : updated_vars) add(v);
+        add(loss);
+        bool released = false;
+        for (auto it = bufs.begin(); it != bufs.end();) {
+            if (live.count(it->first)) {
+                ++it;
+                continue;
+            }
+            if (!released) {
+                release_plan();
+                released = true;
+            }
+            dressi_free(ctx(), it->second);
+            computed.erase(it->first);
+            it = bufs.erase(it);
+        }
+        if (released) {
+            keep.erase(std::remove_if(keep.begin(), keep.end(),
+                                      [&](const std::shared_ptr<VariableNode>& n) {
+                                          return !bufs.count(n.get());
+                                      }),
+                       keep.end());
+        }
+    }
     bool has_buf(const Variable& v) const { return bufs.count(NodeAccess::Node(v).get()) != 0; }
 
     // ---- packing -------------------------------------------------------------
@@ -1798,6 +1847,7 @@ void DressiAD::execStep() {
                 im.leaf_vars.push_back(inp);
             }
         }
+        im.prune_buffers();
         // a fused plan, when the graph is one of the examples'
         if (im.route) {
             im.drop_route();

@@ -408,8 +408,8 @@ __global__ __launch_bounds__(256) void k_hsr_face_bwd(HsrDev d) {
     // the raster is done with this iteration's bins: clear their counters
     for (uint32_t b = gi; b < d.bins.n_bins; b += gridDim.x * blockDim.x) {
         const uint32_t c = d.bins.counts[b];
-        if (c > d.bins.cap && d.bin_over) {
-            *d.bin_over = c;  // rare: the host grows the bins before the next step
+        if (c > d.bins.cap && d.bin_over_max) {
+            atomicMax(d.bin_over_max, c);  // rare: the host grows the bins before the next step
         }
         d.bins.counts[b] = 0;
     }
@@ -460,8 +460,8 @@ __device__ __forceinline__ void face_bwd_all_block(const HsrDev& d, uint32_t blk
     // the raster is done with this iteration's bins: clear their counters
     for (uint32_t b = gi; b < d.bins.n_bins; b += n_blk * blockDim.x) {
         const uint32_t c = d.bins.counts[b];
-        if (c > d.bins.cap && d.bin_over) {
-            *d.bin_over = c;  // rare: the host grows the bins before the next step
+        if (c > d.bins.cap && d.bin_over_max) {
+            atomicMax(d.bin_over_max, c);  // rare: the host grows the bins before the next step
         }
         d.bins.counts[b] = 0;
     }
@@ -513,6 +513,7 @@ __global__ __launch_bounds__(256) void k_hsr_loss_face_bwd(HsrDev d, uint32_t lo
 // counter).
 template <int NV>
 __global__ __launch_bounds__(256) void k_hsr_vertex_adam(HsrDev d) {
+    publish_bin_over(d);
     vertex_views_adam<NV>(d, [&](uint32_t vtx, uint32_t view, float (&g4)[4]) {
         const float4* gt = d.gtri + (size_t)view * 3 * d.g.n_faces;
         float lfb[3][4];
@@ -1090,6 +1091,15 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
             *p->over_host = 0;
             d.bin_over = (uint32_t*)dp;
         }
+    }
+    if (!rc) {
+        uint32_t* mx = nullptr;
+        rc = plan_alloc(p, &mx, 1);
+        if (!rc && hipMemset(mx, 0, sizeof(uint32_t)) != hipSuccess) {
+            set_error("bin overflow word init failed");
+            rc = DRESSI_ERR_HIP;
+        }
+        d.bin_over_max = mx;
     }
     if (!rc) {
         hipError_t e = hipMemsetAsync(d.bins.counts, 0, sizeof(uint32_t) * d.bins.n_bins, ctx->stream);

@@ -98,10 +98,25 @@ struct HsrDev {
     AaRec* arecs;             // [N][F]
     uint32_t* aa_list;        // [N * F] faces with a sample where d loss / d pred != 0
     uint32_t* aa_count;       // entries of aa_list (reset by the clip kernel)
-    // a bin count the face backward found above bins.cap (host-mapped, written
-    // only when a bin overflowed; the plan's next step grows the bins)
+    // the largest bin count above bins.cap this iteration: the kernels that
+    // clear the bins take the maximum in bin_over_max (device memory), and
+    // one thread of the vertex Adam kernel, which runs after them, hands it
+    // to bin_over (host-mapped, written only when a bin overflowed; the
+    // plan's next step grows the bins from it) and clears bin_over_max
     uint32_t* bin_over;
+    uint32_t* bin_over_max;
 };
+
+// The iteration's bin overflow (see HsrDev::bin_over) to the host report.
+__device__ __forceinline__ void publish_bin_over(const HsrDev& d) {
+    if (d.bin_over && d.bin_over_max && blockIdx.x == 0 && threadIdx.x == 0) {
+        const uint32_t m = *d.bin_over_max;
+        if (m) {
+            *d.bin_over = m;
+            *d.bin_over_max = 0;
+        }
+    }
+}
 
 constexpr uint32_t kBiasTableLen = 1u << 16;
 

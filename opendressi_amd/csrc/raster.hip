@@ -379,7 +379,11 @@ __global__ void k_faces_to_i32(const float* faces, uint32_t n, uint32_t n_verts,
 // host code the name `scratch` is a host-side stand-in, never the device
 // array: kernels take the per-device address that hipGetSymbolAddress
 // returns (noalloc_scratch below). Every call on a GPU shares that GPU's
-// array, so calls that overlap on one GPU race.
+// array: calls on one stream run in order, and a call on another stream
+// than the GPU's previous call first waits for that call's work (an event
+// created with the array's address, recorded after every call; not while
+// the stream is being captured into a graph). Calls that overlap in host
+// time on one GPU still race.
 constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
@@ -435,20 +439,29 @@ inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 constexpr int kNoAllocMaxDevices = 64;
 std::mutex g_noalloc_mu;
 char* g_noalloc_ptr[kNoAllocMaxDevices] = {};
+hipEvent_t g_noalloc_done[kNoAllocMaxDevices] = {};      // after the GPU's last call
+hipStream_t g_noalloc_stream[kNoAllocMaxDevices] = {};   // the stream of that call
+bool g_noalloc_used[kNoAllocMaxDevices] = {};
 
 // The device address of this GPU's scratch array, looked up once per device
-// with that device current (the caller has made it current).
+// with that device current (the caller has made it current), with its
+// ordering event; the caller holds g_noalloc_mu.
 int noalloc_scratch(int device, char** out) {
     DRESSI_REQUIRE(device >= 0 && device < kNoAllocMaxDevices, "device %d out of range", device);
-    std::lock_guard<std::mutex> lock(g_noalloc_mu);
     if (!g_noalloc_ptr[device]) {
         void* p = nullptr;
         DRESSI_TRY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
         DRESSI_REQUIRE(p != nullptr, "hipGetSymbolAddress returned NULL");
+        DRESSI_TRY_HIP(hipEventCreateWithFlags(&g_noalloc_done[device], hipEventDisableTiming));
         g_noalloc_ptr[device] = (char*)p;
     }
     *out = g_noalloc_ptr[device];
     return DRESSI_OK;
+}
+
+bool stream_capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
 }
 
 }  // namespace
@@ -506,12 +519,24 @@ int dressi_rasterize_soft_noalloc(dressi_ctx* ctx, const float* soft_clip, const
                    "dressi_rasterize_soft_noalloc: %u faces on a %ux%u screen need %zu bytes of "
                    "scratch, above the fixed %zu (use dressi_rasterize_soft)",
                    n_faces, width, height, need, kNoAllocScratchBytes);
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
     char* base = nullptr;
     if (int rc = noalloc_scratch(ctx->device, &base)) return rc;
-    return launch_rasterize_soft(ctx, g, soft_clip, face_id, faces_soft, hard_clip, n_verts,
-                                 faces_tex, radius_px, prev_shifted_depth, (SoftRec*)base,
-                                 base + rec_bytes + cull_bytes, (CullRec*)(base + rec_bytes),
-                                 out);
+    const int dev = ctx->device;
+    const bool capturing = stream_capturing(ctx->stream);
+    if (!capturing && g_noalloc_used[dev] && g_noalloc_stream[dev] != ctx->stream) {
+        DRESSI_TRY_HIP(hipStreamWaitEvent(ctx->stream, g_noalloc_done[dev], 0));
+    }
+    const int rc = launch_rasterize_soft(ctx, g, soft_clip, face_id, faces_soft, hard_clip,
+                                         n_verts, faces_tex, radius_px, prev_shifted_depth,
+                                         (SoftRec*)base, base + rec_bytes + cull_bytes,
+                                         (CullRec*)(base + rec_bytes), out);
+    if (rc == DRESSI_OK && !capturing) {
+        DRESSI_TRY_HIP(hipEventRecord(g_noalloc_done[dev], ctx->stream));
+        g_noalloc_stream[dev] = ctx->stream;
+        g_noalloc_used[dev] = true;
+    }
+    return rc;
 }
 
 // `n_items` clip sets [n_items][n_verts] over one face list; attributes

@@ -96,3 +96,41 @@ def _call_no_out(ctx, args, s):
     check(lib.dressi_rasterize_soft_noalloc(ctx.handle, p(soft), p(fid), p(fsoft), p(clip),
                                             clip.shape[0], p(faces), faces.shape[0], s, s, 3.0,
                                             None, p(out)))
+
+
+def test_noalloc_orders_calls_on_two_streams(ctx):
+    """Two calls on two streams (two contexts) with no host synchronisation
+    between them: the second waits for the first's use of the shared
+    scratch, so both match the workspace entry point."""
+    import torch
+
+    import opendressi_amd as od
+    from opendressi_amd._lib import check, lib
+    r = 3.0
+    ctx2 = od.Context(0)  # its own stream
+    try:
+        cases = [(4, 320, 21), (3, 192, 22)]
+        args = []
+        for level, s, seed in cases:
+            clip, faces = _scene(level, s, seed)
+            args.append(_inputs(ctx, clip, faces, s, r))
+        torch.cuda.synchronize()
+        outs = []
+        p = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
+        ctx.use_torch_stream()
+        for c, (level, s, _), a in zip((ctx, ctx2), cases, args):
+            print(f"[noalloc 2 streams] level={level} screen={s}", flush=True)
+            soft, fid, fsoft, clip, faces = a
+            out = torch.full((s, s, 4), float("nan"), dtype=torch.float32, device="cuda")
+            check(lib.dressi_rasterize_soft_noalloc(
+                c.handle, p(soft), p(fid), p(fsoft), p(clip), clip.shape[0], p(faces),
+                faces.shape[0], s, s, r, None, p(out)))
+            outs.append(out)
+        ctx2.synchronize()
+        ctx.synchronize()
+        torch.cuda.synchronize()
+        for (level, s, _), a, out in zip(cases, args, outs):
+            want = _call(ctx, "dressi_rasterize_soft", a, s, r)
+            assert np.array_equal(out.cpu().numpy(), want), f"level {level} screen {s}"
+    finally:
+        ctx2.close()
