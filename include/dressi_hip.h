@@ -402,6 +402,14 @@ int dressi_pbr_set_scene(dressi_pbr_plan* plan, const float* pos,
                          const float* normal, const float* uv,
                          const float* faces, const float* mvps,
                          const float* frames, const float* light);
+/* dressi_pbr_set_scene with each view's clip positions given, clips {N,V,4}
+ * view-major, instead of MVP * pos: the example graph's per-view
+ * sendImg(clip) (pbr_material_optimization/run.cpp:189-236). No reference
+ * counterpart as a call: what DressiAD's route of that graph uses. */
+int dressi_pbr_set_scene_clips(dressi_pbr_plan* plan, const float* pos,
+                               const float* normal, const float* uv,
+                               const float* faces, const float* clips,
+                               const float* frames, const float* light);
 /* renders the static targets from the ground-truth maps (host VEC3:
  * gt_albedo / gt_mr {tex_h, tex_w, 3}, gt_env {env_h, env_w, 3}); the state
  * must be (re)set afterwards */
@@ -412,6 +420,17 @@ int dressi_pbr_set_state(dressi_pbr_plan* plan, const float* albedo,
                          const float* mr, const float* env, float t);
 int dressi_pbr_get_state(dressi_pbr_plan* plan, float* albedo, float* mr,
                          float* env, float* t);
+/* The Adam moments m / v of albedo, mr {tex_h, tex_w, 3} and env
+ * {env_h, env_w, 3} (host VEC3), in and out: the in-graph Adam's state
+ * leaves (addUpdate of run.cpp's optimizer); set after dressi_pbr_set_state,
+ * which clears them. No reference counterpart as a call. */
+int dressi_pbr_set_adam(dressi_pbr_plan* plan, const float* m_albedo,
+                        const float* v_albedo, const float* m_mr,
+                        const float* v_mr, const float* m_env,
+                        const float* v_env);
+int dressi_pbr_get_adam(dressi_pbr_plan* plan, float* m_albedo,
+                        float* v_albedo, float* m_mr, float* v_mr,
+                        float* m_env, float* v_env);
 /* n_iters iterations (a captured hipGraph, replayed) / eager launches */
 int dressi_pbr_step(dressi_pbr_plan* plan, uint32_t n_iters);
 int dressi_pbr_step_eager(dressi_pbr_plan* plan, uint32_t n_iters);

@@ -143,6 +143,9 @@ _SIGS = {
     "dressi_pbr_create": (_I, [_P, C.POINTER(PbrDesc), C.POINTER(_P)]),
     "dressi_pbr_destroy": (_I, [_P]),
     "dressi_pbr_set_scene": (_I, [_P, _FP, _FP, _FP, _FP, _FP, _FP, _FP]),
+    "dressi_pbr_set_scene_clips": (_I, [_P, _FP, _FP, _FP, _FP, _FP, _FP, _FP]),
+    "dressi_pbr_set_adam": (_I, [_P, _FP, _FP, _FP, _FP, _FP, _FP]),
+    "dressi_pbr_get_adam": (_I, [_P, _FP, _FP, _FP, _FP, _FP, _FP]),
     "dressi_pbr_set_target": (_I, [_P, _FP, _FP, _FP]),
     "dressi_pbr_set_state": (_I, [_P, _FP, _FP, _FP, _F]),
     "dressi_pbr_get_state": (_I, [_P, _FP, _FP, _FP, _FP]),

@@ -2240,10 +2240,14 @@ int dressi_pbr_destroy(dressi_pbr_plan* p) {
     return DRESSI_OK;
 }
 
-int dressi_pbr_set_scene(dressi_pbr_plan* p, const float* pos, const float* normal,
-                         const float* uv, const float* faces, const float* mvps,
-                         const float* frames, const float* light) {
-    DRESSI_REQUIRE(p && pos && normal && uv && faces && mvps && frames && light, "bad arguments");
+namespace {
+
+// set_scene with the clip positions from MVP * pos (mvps) or given (clips)
+int pbr_set_scene(dressi_pbr_plan* p, const float* pos, const float* normal, const float* uv,
+                  const float* faces, const float* mvps, const float* clips,
+                  const float* frames, const float* light) {
+    DRESSI_REQUIRE(p && pos && normal && uv && faces && (mvps || clips) && frames && light,
+                   "bad arguments");
     DRESSI_TRY_HIP(hipSetDevice(p->ctx->device));
     PbrDev& d = p->d;
     dressi_ctx* ctx = p->ctx;
@@ -2297,11 +2301,16 @@ int dressi_pbr_set_scene(dressi_pbr_plan* p, const float* pos, const float* norm
     if (!rc) rc = h2d(d_uvh, uvh.data(), sizeof(float) * 4 * V);
     if (!rc) rc = h2d(d_uvc, uvc.data(), sizeof(float) * 4 * V);
     if (!rc) rc = h2d(d_faces, faces, sizeof(float) * 3 * Fn);
-    if (!rc) rc = h2d(d_mvp, mvps, sizeof(float) * 16 * N);
+    if (!rc && mvps) rc = h2d(d_mvp, mvps, sizeof(float) * 16 * N);
     for (uint32_t v = 0; v < N && !rc; v++) {
-        hipLaunchKernelGGL(k_pbr_clip, dim3(div_up(V, 256)), dim3(256), 0, s,
-                           (const float*)d_pos, V, (const float*)d_mvp + 16 * v,
-                           (float4*)d_clip);
+        if (clips) {
+            rc = h2d(d_clip, clips + (size_t)v * V * 4, sizeof(float4) * V);
+            if (rc) break;
+        } else {
+            hipLaunchKernelGGL(k_pbr_clip, dim3(div_up(V, 256)), dim3(256), 0, s,
+                               (const float*)d_pos, V, (const float*)d_mvp + 16 * v,
+                               (float4*)d_clip);
+        }
         // the G-buffer (BuildPbrGBuffer's Rasterize calls)
         rc = dressi_rasterize(ctx, (const float*)d_clip, V, (const float*)d_uvh, 4,
                               (const float*)d_faces, Fn, S, S, (float*)g_uvh);
@@ -2402,6 +2411,22 @@ int dressi_pbr_set_scene(dressi_pbr_plan* p, const float* pos, const float* norm
     return DRESSI_OK;
 }
 
+}  // namespace
+
+int dressi_pbr_set_scene(dressi_pbr_plan* p, const float* pos, const float* normal,
+                         const float* uv, const float* faces, const float* mvps,
+                         const float* frames, const float* light) {
+    DRESSI_REQUIRE(mvps, "bad arguments");
+    return pbr_set_scene(p, pos, normal, uv, faces, mvps, nullptr, frames, light);
+}
+
+int dressi_pbr_set_scene_clips(dressi_pbr_plan* p, const float* pos, const float* normal,
+                               const float* uv, const float* faces, const float* clips,
+                               const float* frames, const float* light) {
+    DRESSI_REQUIRE(clips, "bad arguments");
+    return pbr_set_scene(p, pos, normal, uv, faces, nullptr, clips, frames, light);
+}
+
 int dressi_pbr_set_target(dressi_pbr_plan* p, const float* gt_albedo, const float* gt_mr,
                           const float* gt_env) {
     DRESSI_REQUIRE(p && gt_albedo && gt_mr && gt_env, "bad arguments");
@@ -2456,6 +2481,37 @@ int dressi_pbr_get_state(dressi_pbr_plan* p, float* albedo, float* mr, float* en
     }
     if (t) DRESSI_TRY_HIP(hipMemcpy(t, d.t, sizeof(float), hipMemcpyDeviceToHost));
     return DRESSI_OK;
+}
+
+int dressi_pbr_set_adam(dressi_pbr_plan* p, const float* m_albedo, const float* v_albedo,
+                        const float* m_mr, const float* v_mr, const float* m_env,
+                        const float* v_env) {
+    DRESSI_REQUIRE(p && m_albedo && v_albedo && m_mr && v_mr && m_env && v_env, "bad arguments");
+    DRESSI_TRY_HIP(hipSetDevice(p->ctx->device));
+    DRESSI_TRY_HIP(hipStreamSynchronize(p->ctx->stream));
+    PbrDev& d = p->d;
+    const size_t T = (size_t)d.tw * d.th, E = (size_t)d.ew * d.eh;
+    if (int rc = upload3(d.am, m_albedo, T)) return rc;
+    if (int rc = upload3(d.av, v_albedo, T)) return rc;
+    if (int rc = upload3(d.mm, m_mr, T)) return rc;
+    if (int rc = upload3(d.mv, v_mr, T)) return rc;
+    if (int rc = upload3(d.em, m_env, E)) return rc;
+    return upload3(d.ev, v_env, E);
+}
+
+int dressi_pbr_get_adam(dressi_pbr_plan* p, float* m_albedo, float* v_albedo, float* m_mr,
+                        float* v_mr, float* m_env, float* v_env) {
+    DRESSI_REQUIRE(p && m_albedo && v_albedo && m_mr && v_mr && m_env && v_env, "bad arguments");
+    DRESSI_TRY_HIP(hipSetDevice(p->ctx->device));
+    DRESSI_TRY_HIP(hipStreamSynchronize(p->ctx->stream));
+    PbrDev& d = p->d;
+    const size_t T = (size_t)d.tw * d.th, E = (size_t)d.ew * d.eh;
+    if (int rc = download3(m_albedo, d.am, T)) return rc;
+    if (int rc = download3(v_albedo, d.av, T)) return rc;
+    if (int rc = download3(m_mr, d.mm, T)) return rc;
+    if (int rc = download3(v_mr, d.mv, T)) return rc;
+    if (int rc = download3(m_env, d.em, E)) return rc;
+    return download3(v_env, d.ev, E);
 }
 
 int dressi_pbr_step_eager(dressi_pbr_plan* p, uint32_t n_iters) {

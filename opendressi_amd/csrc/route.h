@@ -65,7 +65,11 @@ public:
 // of examples/texture_optimization/run.cpp:112-145: TextureBilinear on an
 // RGBA texture, the RGB L2 image loss, the in-graph Adam, per-view clip and
 // ScreenAttr images sent each step, on dressi_tex_* with
-// DRESSI_TEX_EXTERNAL_CLIP); nullptr when neither recognises the graph.
+// DRESSI_TEX_EXTERNAL_CLIP), else the PBR route (tests/graph_pbr.cpp: the
+// material + environment fit of examples/pbr_material_optimization/
+// run.cpp:189-288 built with the examples' PBR graph builders, normal
+// mapping off, AO 1, emissive 0, on dressi_pbr_* with the views' clip
+// images); nullptr when none recognises the graph.
 std::unique_ptr<FusedRoute> RecogniseFusedRoute(const GraphRoots& g);
 
 class SilhouetteRoute : public FusedRoute {
@@ -104,6 +108,25 @@ public:
 private:
     struct State;
     explicit TextureRoute(std::unique_ptr<State> st);
+    std::unique_ptr<State> st_;
+};
+
+class PbrRoute : public FusedRoute {
+public:
+    static std::unique_ptr<PbrRoute> Recognise(const GraphRoots& g);
+    ~PbrRoute() override;
+
+    std::string name() const override;  // "fused:pbr"
+    size_t kernels() const override;
+    bool Accept(const Variable& var, const CpuImageView& img) override;
+    bool Step(dressi_ctx* ctx, std::map<Variable, CpuImage>* back) override;
+    void Export(std::map<Variable, CpuImage>* back) override;
+    bool Readable(const Variable& var) const override;
+    CpuImage Recv(const Variable& var) override;
+
+private:
+    struct State;
+    explicit PbrRoute(std::unique_ptr<State> st);
     std::unique_ptr<State> st_;
 };
 

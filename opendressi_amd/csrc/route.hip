@@ -2,13 +2,16 @@
 // graphs and their execution on the fused plans (route.h). Host code: the
 // plans' kernels live in hsr.hip / aa.hip / tex.hip.
 #include <algorithm>
+#include <functional>
 #include <cstring>
 #include <set>
 #include <unordered_map>
 #include <unordered_set>
 
 #include "dressi/f.h"
+#include "dressi/ibl.h"
 #include "dressi/mesh_utils.h"
+#include "dressi_examples/pbr_graph.h"
 #include "dressi_hip.h"
 #include "route.h"
 
@@ -1430,11 +1433,717 @@ CpuImage TextureRoute::Recv(const Variable& var) {
     return read(DRESSI_TEX_PRED, npx4 * (size_t)(k - kTServePred0), CpuImage(s.p.S.w, s.p.S.h, 4));
 }
 
+// ---- the PBR material + environment fit -------------------------------------------
+
+namespace {
+
+// Leaf roles of the PBR fit graph (tests/graph_pbr.cpp: per view the
+// G-buffer and the shading of examples/common/pbr_graph.cpp with normal
+// mapping off, the target from the ground-truth maps, the L1 loss
+// Mean(|StopGradient(target) - pred|) summed over views, in-graph Adam on
+// albedo, mr and env with one step counter, albedo / mr clamped to [0,1] and
+// env to >= 0; examples/pbr_material_optimization/run.cpp:189-288)
+enum PbrRole : int {
+    kQUvh, kQNormal, kQTangent, kQWpos, kQFaces,
+    kQGtAlbedo, kQGtMr, kQNmap, kQAo, kQEmis,
+    kQAlbedo, kQMr, kQEnvGt, kQEnv, kQUvClip, kQLightPos, kQLightCol,
+    kQT, kQM0, kQV0 = kQM0 + 3,  // + param (0 albedo, 1 mr, 2 env)
+    kQClip0 = 32, kQAttr0 = 64, kQCamPos0 = 96, kQCamFwd0 = 128, kQCamRight0 = 160,
+    kQCamUp0 = 192,  // + view
+};
+
+enum PbrServe : int { kQServeLoss, kQServeGrad0 = 1, kQServeP0 = 4, kQServeM0 = 7, kQServeV0 = 10,
+                      kQServeT = 13 };  // + param where it applies
+
+constexpr int kQParamRole[3] = {kQAlbedo, kQMr, kQEnv};
+// the optimiser's state: parameters, moments, step counter
+constexpr int kQStateRoles[10] = {kQAlbedo, kQMr, kQEnv, kQT, kQM0, kQM0 + 1, kQM0 + 2,
+                                  kQV0, kQV0 + 1, kQV0 + 2};
+
+struct PbrParams {
+    uint32_t V = 0, F = 0, N = 0, levels = 0;
+    ImgSize S, T, E;
+};
+
+struct PbrTemplate {
+    std::map<int, Variable> leaves;
+    Variable g[3] = {Variable(nullptr), Variable(nullptr), Variable(nullptr)};
+    Variable loss{nullptr}, t_new{nullptr};
+    Variable updated[3] = {Variable(nullptr), Variable(nullptr), Variable(nullptr)};
+    Variable m_new[3] = {Variable(nullptr), Variable(nullptr), Variable(nullptr)};
+    Variable v_new[3] = {Variable(nullptr), Variable(nullptr), Variable(nullptr)};
+    Variables g_uvs, inv_uvs;  // per view
+    std::unordered_map<const FunctionNode*, int> free_slot;
+    int slot_lr = 0, n_slots = 1;
+};
+
+PbrTemplate build_pbr_template(const PbrParams& p) {
+    using namespace dressi_examples;
+    PbrTemplate T;
+    auto leaf = [&](int role, VType t, ImgSize s) {
+        Variable v(t, s);
+        T.leaves[role] = v;
+        return v;
+    };
+    PbrGeometryLeaves geom;
+    geom.uvh = leaf(kQUvh, VEC4, {p.V, 1});
+    geom.normal = leaf(kQNormal, VEC3, {p.V, 1});
+    geom.tangent = leaf(kQTangent, VEC3, {p.V, 1});
+    geom.wpos = leaf(kQWpos, VEC3, {p.V, 1});
+    geom.faces = leaf(kQFaces, IVEC3, {p.F, 1});
+    PbrMaterialLeaves gt_mat;
+    gt_mat.albedo = leaf(kQGtAlbedo, VEC3, p.T);
+    gt_mat.mr = leaf(kQGtMr, VEC3, p.T);
+    gt_mat.normal_map = leaf(kQNmap, VEC3, p.T);
+    gt_mat.ao = leaf(kQAo, VEC3, p.T);
+    gt_mat.emissive = leaf(kQEmis, VEC3, p.T);
+    PbrMaterialLeaves mat = gt_mat;
+    mat.albedo = leaf(kQAlbedo, VEC3, p.T);
+    mat.mr = leaf(kQMr, VEC3, p.T);
+    const Variable env_gt = leaf(kQEnvGt, VEC3, p.E);
+    const Variable env = leaf(kQEnv, VEC3, p.E);
+    const auto maps_of = [&](const Variable& e) {
+        PbrIblMaps m;
+        m.env = e;
+        m.irr = BuildIrradianceSample(e);
+        m.pref = BuildPrefEnvironmentSampleConv(e, p.levels);
+        m.lut = BuildBrdfIntegrationMap();
+        return m;
+    };
+    const PbrIblMaps ibl_gt = maps_of(env_gt), ibl = maps_of(env);
+    const Variable uv_clip = leaf(kQUvClip, VEC4, {p.V, 1});
+    const Variable light_pos = leaf(kQLightPos, VEC3, {1, 1});
+    const Variable light_col = leaf(kQLightCol, VEC3, {1, 1});
+    Variables view_losses;
+    for (uint32_t v = 0; v < p.N; v++) {
+        const Variable clip = leaf(kQClip0 + (int)v, VEC4, {p.V, 1});
+        const Variable attr = leaf(kQAttr0 + (int)v, VEC4, {p.V, 1});
+        PbrFrameLeaves fr;
+        fr.cam_pos = leaf(kQCamPos0 + (int)v, VEC3, {1, 1});
+        fr.cam_fwd = leaf(kQCamFwd0 + (int)v, VEC3, {1, 1});
+        fr.cam_right = leaf(kQCamRight0 + (int)v, VEC3, {1, 1});
+        fr.cam_up = leaf(kQCamUp0 + (int)v, VEC3, {1, 1});
+        fr.light_pos = light_pos;
+        fr.light_col = light_col;
+        PbrGeometryLeaves vg = geom;
+        vg.clip = clip;
+        const PbrGBuffer gb = BuildPbrGBuffer(vg, p.S);
+        const Variable inv_uv = F::Rasterize(uv_clip, attr, geom.faces, p.T);
+        const PbrOutputs target = BuildPbrShade(gb, gt_mat, fr, ibl_gt, inv_uv, p.S, false);
+        const PbrOutputs pred = BuildPbrShade(gb, mat, fr, ibl, inv_uv, p.S, false);
+        view_losses.push_back(F::Mean(F::Abs(F::StopGradient(target.mapped) - pred.mapped)));
+        T.g_uvs.push_back(gb.uv);
+        T.inv_uvs.push_back(inv_uv);
+    }
+    T.loss = F::SumPixelWise(view_losses);
+    const Variable adam_t = leaf(kQT, FLOAT, {1, 1});
+    const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+    T.t_new = adam_t + 1.f;
+    const Variable bc1 = 1.f - F::Pow(F::Float(b1), T.t_new);
+    const Variable bc2 = 1.f - F::Pow(F::Float(b2), T.t_new);
+    const Variable params[3] = {mat.albedo, mat.mr, env};
+    for (int k = 0; k < 3; k++) {
+        const ImgSize sz = k < 2 ? p.T : p.E;
+        const Variable adam_m = leaf(kQM0 + k, VEC3, sz);
+        const Variable adam_v = leaf(kQV0 + k, VEC3, sz);
+        T.g[k] = Variable(VEC3, sz);
+        const Variable& g = T.g[k];
+        T.m_new[k] = adam_m * b1 + g * (1.f - b1);
+        T.v_new[k] = adam_v * b2 + g * g * (1.f - b2);
+        const Variable lr = F::Float(0.f);
+        T.free_slot[NodeAccess::Node(lr)->creator.get()] = T.slot_lr;
+        const Variable step = F::Mul((T.m_new[k] / bc1) / (F::Sqrt(T.v_new[k] / bc2) + eps), lr);
+        T.updated[k] = k < 2 ? F::Clamp(params[k] - step, F::Float(0.f), F::Float(1.f))
+                             : F::Max(params[k] - step, F::Float(0.f));
+    }
+    return T;
+}
+
+bool read_pbr_params(const GraphRoots& g, PbrParams* p) {
+    if (g.input_vars.size() != 3 || g.updated_vars.size() != 3 || g.input_grad_vars.size() != 3) {
+        return false;
+    }
+    std::set<std::pair<uint32_t, uint32_t>> pref_sizes;  // one per prefilter level
+    std::unordered_set<const VariableNode*> raster_pos;  // the rasters' position inputs
+    const FunctionNode* inv = nullptr;
+    for (const auto& f : *g.funcs) {
+        const auto& n = NodeAccess::Node(f);
+        switch (n->op) {
+            case Op::kRasterize:
+                if (!n->xs.empty()) {
+                    raster_pos.insert(n->xs[0].get());
+                }
+                break;
+            case Op::kPrefilterConv:
+                if (const auto y = n->y.lock()) {
+                    pref_sizes.insert({y->size.w, y->size.h});
+                }
+                break;
+            case Op::kTextureBilinear:
+                // TextureBilinear(tex, uv) at the G-buffer's pixels
+                if (n->xs.size() == 2 && n->xs[1]->creator) {
+                    inv = n.get();
+                }
+                break;
+            case Op::kCustom:
+            case Op::kSetFragDepth:
+            case Op::kPeelDepth: return false;
+            default: break;
+        }
+    }
+    if (!inv || raster_pos.size() < 2 || pref_sizes.empty()) {
+        return false;
+    }
+    // the rasters read each view's clip positions and UvAsClip(uv) (the
+    // inverse-UV tables, reached through TextureBilinear's backward)
+    p->N = (uint32_t)raster_pos.size() - 1;
+    p->levels = (uint32_t)pref_sizes.size();
+    p->S = inv->xs[1]->size;
+    // the optimised images: albedo and mr of one size, the env (or all three alike)
+    for (const auto& x : g.input_vars) {
+        if (x.getVType() != VEC3) {
+            return false;
+        }
+    }
+    const ImgSize s0 = g.input_vars[0].getImgSize(), s1 = g.input_vars[1].getImgSize(),
+                  s2 = g.input_vars[2].getImgSize();
+    if (s0 == s1) {
+        p->T = s0;
+        p->E = s2;
+    } else if (s0 == s2) {
+        p->T = s0;
+        p->E = s1;
+    } else if (s1 == s2) {
+        p->T = s1;
+        p->E = s0;
+    } else {
+        return false;
+    }
+    // the G-buffer's uv raster: Rasterize(clip, uvh, faces)
+    std::function<const FunctionNode*(const VariableNode*, int)> find_raster =
+            [&](const VariableNode* v, int depth) -> const FunctionNode* {
+        if (!v || !v->creator || depth > 4) return nullptr;
+        if (v->creator->op == Op::kRasterize) return v->creator.get();
+        for (const auto& x : v->creator->xs) {
+            if (auto r = find_raster(x.get(), depth + 1)) return r;
+        }
+        return nullptr;
+    };
+    const FunctionNode* r = find_raster(inv->xs[1].get(), 0);
+    if (!r || r->xs.size() != 3) {
+        return false;
+    }
+    p->V = r->xs[0]->size.w;
+    p->F = r->xs[2]->size.w;
+    return p->N >= 1 && p->N <= 16 && p->levels >= 2 && p->levels <= 8 && p->V > 0 &&
+           p->F > 0 && p->S.w > 0 && p->S.w == p->S.h && p->T.w > 0 && p->E.w > 0;
+}
+
+}  // namespace
+
+struct PbrRoute::State {
+    PbrParams p;
+    float lr = 0.f;
+    int order[3] = {0, 1, 2};  // param of the user's optimizer input i
+    std::map<int, Variable> user_leaf;
+    std::unordered_map<const VariableNode*, std::vector<int>> roles_of;
+    std::unordered_map<const VariableNode*, int> serve;
+    std::unordered_set<const VariableNode*> in_graph;
+    bool keep_grad = false;
+    std::map<int, CpuImage> data;
+    bool scene_dirty = true, target_dirty = true;
+    std::set<int> state_dirty;
+    dressi_ctx* ctx = nullptr;
+    dressi_pbr_plan* plan = nullptr;
+    bool state_on_plan = false;
+    uint32_t steps = 0;
+
+    ~State() { drop_plan(); }
+
+    void drop_plan() {
+        if (plan) {
+            dressi_pbr_destroy(plan);
+            plan = nullptr;
+        }
+        state_on_plan = false;
+    }
+
+    bool have(int role) const { return data.count(role) != 0; }
+    ImgSize size_of(int k) const { return k < 2 ? p.T : p.E; }
+
+    static bool all_equal(const CpuImage& img, float x) {
+        for (float y : img.data) {
+            if (y != x) {
+                return false;
+            }
+        }
+        return true;
+    }
+
+    // the static leaves: the plan derives the G-buffer from them, with
+    // normal mapping off, AO 1 and emissive 0
+    bool scene_fits() const {
+        // what the plan reads must have been sent; the maps it assumes
+        // (normal map, AO, emissive, tangents) only where the graph reads them
+        for (int r : {kQUvh, kQNormal, kQWpos, kQFaces, kQUvClip, kQLightPos, kQLightCol}) {
+            if (!have(r)) {
+                return false;
+            }
+        }
+        for (int r : {kQNmap, kQAo, kQEmis, kQTangent}) {
+            if (user_leaf.count(r) && !have(r)) {
+                return false;
+            }
+        }
+        if (have(kQTangent) && user_leaf.count(kQTangent) && !all_equal(data.at(kQTangent), 0.f)) {
+            return false;
+        }
+        for (float x : data.at(kQFaces).data) {
+            if (!is_integer_below(x, p.V)) {
+                return false;
+            }
+        }
+        const CpuImage& uvh = data.at(kQUvh);
+        CpuImage uv(p.V, 1, 2);
+        for (uint32_t i = 0; i < p.V; i++) {
+            if (uvh.at(i, 0, 2) != 1.f || uvh.at(i, 0, 3) != 1.f) {
+                return false;
+            }
+            uv.at(i, 0, 0) = uvh.at(i, 0, 0);
+            uv.at(i, 0, 1) = uvh.at(i, 0, 1);
+        }
+        if (UvAsClip(uv).data != data.at(kQUvClip).data) {
+            return false;
+        }
+        if ((have(kQAo) && user_leaf.count(kQAo) && !all_equal(data.at(kQAo), 1.f)) ||
+            (have(kQEmis) && user_leaf.count(kQEmis) && !all_equal(data.at(kQEmis), 0.f))) {
+            return false;
+        }
+        for (uint32_t v = 0; v < p.N; v++) {
+            for (int base : {kQClip0, kQAttr0, kQCamPos0, kQCamFwd0, kQCamRight0, kQCamUp0}) {
+                if (!have(base + (int)v)) {
+                    return false;
+                }
+            }
+            if (ScreenAttr(data.at(kQClip0 + (int)v), p.S).data != data.at(kQAttr0 + (int)v).data) {
+                return false;
+            }
+        }
+        return true;
+    }
+
+    void create_plan() {
+        dressi_pbr_desc d{};
+        d.n_verts = p.V;
+        d.n_faces = p.F;
+        d.n_views = p.N;
+        d.width = p.S.w;
+        d.height = p.S.h;
+        d.tex_w = p.T.w;
+        d.tex_h = p.T.h;
+        d.env_w = p.E.w;
+        d.env_h = p.E.h;
+        d.levels = p.levels;
+        d.lr = lr;
+        d.beta1 = 0.9f;
+        d.beta2 = 0.999f;
+        d.eps = 1e-8f;
+        d.flags = keep_grad ? DRESSI_PBR_KEEP_GRAD : 0u;
+        check_hip_rc(dressi_pbr_create(ctx, &d, &plan), "dressi_pbr_create");
+        const CpuImage& uvh = data.at(kQUvh);
+        std::vector<float> uv((size_t)p.V * 2), clips((size_t)p.N * p.V * 4), frames(p.N * 12);
+        for (uint32_t i = 0; i < p.V; i++) {
+            uv[i * 2] = uvh.at(i, 0, 0);
+            uv[i * 2 + 1] = uvh.at(i, 0, 1);
+        }
+        for (uint32_t v = 0; v < p.N; v++) {
+            const std::vector<float>& c = data.at(kQClip0 + (int)v).data;
+            std::copy(c.begin(), c.end(), clips.begin() + (ptrdiff_t)((size_t)v * p.V * 4));
+            int j = 0;
+            for (int base : {kQCamPos0, kQCamFwd0, kQCamRight0, kQCamUp0}) {
+                for (int c3 = 0; c3 < 3; c3++) {
+                    frames[v * 12 + j++] = data.at(base + (int)v).data[c3];
+                }
+            }
+        }
+        const float light[6] = {data.at(kQLightPos).data[0], data.at(kQLightPos).data[1],
+                                data.at(kQLightPos).data[2], data.at(kQLightCol).data[0],
+                                data.at(kQLightCol).data[1], data.at(kQLightCol).data[2]};
+        check_hip_rc(dressi_pbr_set_scene_clips(plan, data.at(kQWpos).data.data(),
+                                                data.at(kQNormal).data.data(), uv.data(),
+                                                data.at(kQFaces).data.data(), clips.data(),
+                                                frames.data(), light),
+                     "dressi_pbr_set_scene_clips");
+    }
+
+    void pull_state() {
+        if (!plan || !state_on_plan) {
+            return;
+        }
+        CpuImage x[3], m[3], v[3];
+        for (int k = 0; k < 3; k++) {
+            const ImgSize sz = size_of(k);
+            x[k] = CpuImage(sz.w, sz.h, 3);
+            m[k] = CpuImage(sz.w, sz.h, 3);
+            v[k] = CpuImage(sz.w, sz.h, 3);
+        }
+        float t = 0.f;
+        check_hip_rc(dressi_pbr_get_state(plan, x[0].data.data(), x[1].data.data(),
+                                          x[2].data.data(), &t),
+                     "dressi_pbr_get_state");
+        check_hip_rc(dressi_pbr_get_adam(plan, m[0].data.data(), v[0].data.data(),
+                                         m[1].data.data(), v[1].data.data(), m[2].data.data(),
+                                         v[2].data.data()),
+                     "dressi_pbr_get_adam");
+        for (int k = 0; k < 3; k++) {
+            if (!state_dirty.count(kQParamRole[k])) data[kQParamRole[k]] = x[k];
+            if (!state_dirty.count(kQM0 + k)) data[kQM0 + k] = m[k];
+            if (!state_dirty.count(kQV0 + k)) data[kQV0 + k] = v[k];
+        }
+        if (!state_dirty.count(kQT)) data[kQT] = CpuImage(1, 1, 1, t);
+    }
+
+    void push_state() {
+        for (int k = 0; k < 3; k++) {
+            const ImgSize sz = size_of(k);
+            for (int r : {kQParamRole[k], kQM0 + k, kQV0 + k}) {
+                if (!have(r)) {
+                    data[r] = CpuImage(sz.w, sz.h, 3);
+                }
+            }
+        }
+        if (!have(kQT)) {
+            data[kQT] = CpuImage(1, 1, 1);
+        }
+        check_hip_rc(dressi_pbr_set_state(plan, data.at(kQAlbedo).data.data(),
+                                          data.at(kQMr).data.data(), data.at(kQEnv).data.data(),
+                                          data.at(kQT).data[0]),
+                     "dressi_pbr_set_state");
+        check_hip_rc(dressi_pbr_set_adam(plan, data.at(kQM0).data.data(), data.at(kQV0).data.data(),
+                                         data.at(kQM0 + 1).data.data(),
+                                         data.at(kQV0 + 1).data.data(),
+                                         data.at(kQM0 + 2).data.data(),
+                                         data.at(kQV0 + 2).data.data()),
+                     "dressi_pbr_set_adam");
+        state_dirty.clear();
+        state_on_plan = true;
+    }
+};
+
+PbrRoute::PbrRoute(std::unique_ptr<State> st) : st_(std::move(st)) {}
+PbrRoute::~PbrRoute() = default;
+
+std::string PbrRoute::name() const { return "fused:pbr"; }
+
+size_t PbrRoute::kernels() const { return 10; }
+
+std::unique_ptr<PbrRoute> PbrRoute::Recognise(const GraphRoots& g) {
+    PbrParams p;
+    if (!g.funcs || !g.loss || !read_pbr_params(g, &p)) {
+        return nullptr;
+    }
+    std::unique_ptr<PbrTemplate> T;
+    try {
+        T = std::make_unique<PbrTemplate>(build_pbr_template(p));
+    } catch (const DressiError&) {
+        return nullptr;
+    }
+    MatcherT<PbrTemplate> M(*T);
+    if (!M.match(g.loss, T->loss)) {
+        return nullptr;
+    }
+    // the user's optimizer inputs: which parameter each is
+    auto st = std::make_unique<State>();
+    for (int i = 0; i < 3; i++) {
+        const VariableNode* u = NodeAccess::Node(g.input_vars[i]).get();
+        int k = -1;
+        for (int q = 0; q < 3; q++) {
+            auto it = M.leaf_of.find(NodeAccess::Node(T->leaves.at(kQParamRole[q])).get());
+            if (it != M.leaf_of.end() && it->second == u) {
+                k = q;
+            }
+        }
+        if (k < 0) {
+            return nullptr;
+        }
+        st->order[i] = k;
+        const Variable& gu = g.input_grad_vars[i];
+        if (gu.getVType() != VEC3 || !(gu.getImgSize() == T->g[k].getImgSize())) {
+            return nullptr;
+        }
+        M.leaf_of[NodeAccess::Node(T->g[k]).get()] = NodeAccess::Node(gu).get();
+    }
+    for (int i = 0; i < 3; i++) {
+        if (!M.match(g.updated_vars[i], T->updated[st->order[i]])) {
+            return nullptr;
+        }
+    }
+    // addUpdate pairs in the optimizer's input order, then the step counter
+    if (g.extra_updates.size() != 7) {
+        return nullptr;
+    }
+    for (int i = 0; i < 3; i++) {
+        const int k = st->order[i];
+        const auto& [lm, um] = g.extra_updates[2 * i];
+        const auto& [lv, uv] = g.extra_updates[2 * i + 1];
+        if (!M.match(um, T->m_new[k]) || !M.match(lm, T->leaves.at(kQM0 + k)) ||
+            !M.match(uv, T->v_new[k]) || !M.match(lv, T->leaves.at(kQV0 + k))) {
+            return nullptr;
+        }
+    }
+    if (!M.match(g.extra_updates[6].second, T->t_new) ||
+        !M.match(g.extra_updates[6].first, T->leaves.at(kQT)) || !M.slot_set[T->slot_lr]) {
+        return nullptr;
+    }
+    // the inverse-UV rasters, held by TextureBilinear's backward: every
+    // GatherByInverseUVBilinear (gy, inv_uv, uv) reads a view's G-buffer uv
+    // and that view's inv_uv
+    {
+        std::unordered_map<const VariableNode*, const VariableNode*> user_of;
+        for (const auto& [u, t] : M.done) {
+            user_of[t] = u;
+        }
+        std::vector<int> seen(p.N, 0);
+        for (const auto& f : *g.funcs) {
+            const auto& n = NodeAccess::Node(f);
+            if (n->op != Op::kGatherInvUvBilinear) {
+                continue;
+            }
+            if (n->xs.size() != 3) {
+                return nullptr;
+            }
+            uint32_t v = 0;
+            while (v < p.N) {
+                auto it = user_of.find(NodeAccess::Node(T->g_uvs[v]).get());
+                if (it != user_of.end() && it->second == n->xs[2].get()) {
+                    break;
+                }
+                v++;
+            }
+            if (v == p.N || !M.match(n->xs[1], NodeAccess::Node(T->inv_uvs[v]))) {
+                return nullptr;
+            }
+            seen[v]++;
+        }
+        for (uint32_t v = 0; v < p.N; v++) {
+            if (!seen[v]) {
+                return nullptr;
+            }
+        }
+    }
+    st->p = p;
+    st->lr = M.slot_val[T->slot_lr];
+    for (const auto& [role, tv] : T->leaves) {
+        auto it = M.leaf_of.find(NodeAccess::Node(tv).get());
+        if (it != M.leaf_of.end()) {
+            st->roles_of[it->second].push_back(role);
+        }
+    }
+    std::unordered_map<const VariableNode*, int> serve_t;
+    serve_t[NodeAccess::Node(T->loss).get()] = kQServeLoss;
+    serve_t[NodeAccess::Node(T->t_new).get()] = kQServeT;
+    for (int k = 0; k < 3; k++) {
+        serve_t[NodeAccess::Node(T->updated[k]).get()] = kQServeP0 + k;
+        serve_t[NodeAccess::Node(T->m_new[k]).get()] = kQServeM0 + k;
+        serve_t[NodeAccess::Node(T->v_new[k]).get()] = kQServeV0 + k;
+    }
+    for (const auto& [u, t] : M.done) {
+        st->in_graph.insert(u);
+        auto s = serve_t.find(t);
+        if (s != serve_t.end()) {
+            st->serve[u] = s->second;
+        }
+    }
+    for (int i = 0; i < 3; i++) {
+        const VariableNode* gn = NodeAccess::Node(g.input_grad_vars[i]).get();
+        st->serve[gn] = kQServeGrad0 + st->order[i];
+        st->in_graph.insert(gn);
+    }
+    st->keep_grad = g.grad_outputs;
+    for (const auto& v : g.extra_outputs) {
+        const VariableNode* n = NodeAccess::Node(v).get();
+        auto s = st->serve.find(n);
+        if (s != st->serve.end()) {
+            st->keep_grad |= s->second >= kQServeGrad0 && s->second < kQServeP0;
+        } else if (!st->roles_of.count(n)) {
+            return nullptr;  // an output the plan does not keep
+        }
+    }
+    for (const auto& f : *g.funcs) {
+        for (const auto& x : f.getInputVars()) {
+            auto it = st->roles_of.find(NodeAccess::Node(x).get());
+            if (it != st->roles_of.end()) {
+                for (int r : it->second) {
+                    st->user_leaf.emplace(r, x);
+                }
+            }
+        }
+    }
+    for (const auto& [leaf_u, upd_u] : g.extra_updates) {
+        auto it = st->roles_of.find(NodeAccess::Node(leaf_u).get());
+        if (it != st->roles_of.end()) {
+            for (int r : it->second) {
+                st->user_leaf.emplace(r, leaf_u);
+            }
+        }
+    }
+    return std::unique_ptr<PbrRoute>(new PbrRoute(std::move(st)));
+}
+
+bool PbrRoute::Accept(const Variable& var, const CpuImageView& img) {
+    State& s = *st_;
+    const VariableNode* n = NodeAccess::Node(var).get();
+    auto it = s.roles_of.find(n);
+    if (it == s.roles_of.end()) {
+        return !s.in_graph.count(n);
+    }
+    CpuImage copy(img.width, img.height, img.channels);
+    std::copy(img.data, img.data + img.numElems(), copy.data.begin());
+    for (int r : it->second) {
+        s.data[r] = copy;
+        if (r == kQAlbedo || r == kQMr || r == kQEnv || r == kQT ||
+            (r >= kQM0 && r < kQV0 + 3)) {
+            s.state_dirty.insert(r);
+        } else if (r == kQGtAlbedo || r == kQGtMr || r == kQEnvGt) {
+            s.target_dirty = true;
+        } else {
+            s.scene_dirty = true;
+        }
+    }
+    return true;
+}
+
+void PbrRoute::Export(std::map<Variable, CpuImage>* back) {
+    State& s = *st_;
+    s.pull_state();
+    for (const auto& [role, var] : s.user_leaf) {
+        auto d = s.data.find(role);
+        if (d != s.data.end()) {
+            (*back)[var] = d->second;
+        }
+    }
+}
+
+bool PbrRoute::Step(dressi_ctx* ctx, std::map<Variable, CpuImage>* back) {
+    State& s = *st_;
+    if (s.plan && s.ctx != ctx) {
+        throw DressiError("the fused PBR plan moved to another context");
+    }
+    s.ctx = ctx;
+    if (s.scene_dirty) {
+        if (!s.scene_fits()) {
+            Export(back);
+            return false;
+        }
+        if (s.plan) {
+            // a new scene: a new plan, with the current state
+            s.pull_state();
+            for (int r : kQStateRoles) {
+                s.state_dirty.insert(r);
+            }
+            s.drop_plan();
+        }
+    }
+    if (!s.have(kQGtAlbedo) || !s.have(kQGtMr) || !s.have(kQEnvGt)) {
+        Export(back);
+        return false;
+    }
+    if (!s.plan) {
+        s.create_plan();
+        s.target_dirty = true;
+        for (int r : kQStateRoles) {
+            s.state_dirty.insert(r);
+        }
+    }
+    s.scene_dirty = false;
+    if (s.target_dirty) {
+        // set_target renders the targets through the plan; the state goes back after it
+        s.pull_state();
+        check_hip_rc(dressi_pbr_set_target(s.plan, s.data.at(kQGtAlbedo).data.data(),
+                                           s.data.at(kQGtMr).data.data(),
+                                           s.data.at(kQEnvGt).data.data()),
+                     "dressi_pbr_set_target");
+        s.target_dirty = false;
+        for (int r : kQStateRoles) {
+            s.state_dirty.insert(r);
+        }
+    }
+    if (!s.state_dirty.empty()) {
+        s.pull_state();
+        s.push_state();
+    }
+    check_hip_rc(dressi_pbr_step(s.plan, 1), "dressi_pbr_step");
+    s.steps++;
+    return true;
+}
+
+bool PbrRoute::Readable(const Variable& var) const {
+    const VariableNode* n = NodeAccess::Node(var).get();
+    auto it = st_->serve.find(n);
+    if (it != st_->serve.end()) {
+        const int k = it->second;
+        return k < kQServeGrad0 || k >= kQServeP0 || st_->keep_grad;
+    }
+    return st_->roles_of.count(n) != 0;
+}
+
+CpuImage PbrRoute::Recv(const Variable& var) {
+    State& s = *st_;
+    const VariableNode* n = NodeAccess::Node(var).get();
+    DRESSI_CHECK(Readable(var),
+                 "recvImg: the fused PBR plan does not keep this Variable (markOutput it before "
+                 "the first execStep)");
+    DRESSI_CHECK(s.plan && s.steps > 0, "recvImg before the first execStep()");
+    auto sv = s.serve.find(n);
+    if (sv == s.serve.end()) {
+        s.pull_state();
+        auto d = s.data.find(s.roles_of.at(n)[0]);
+        DRESSI_CHECK(d != s.data.end(), "recvImg: no image was sent to this leaf");
+        return d->second;
+    }
+    const int k = sv->second;
+    if (k == kQServeLoss) {
+        CpuImage out(1, 1, 1);
+        check_hip_rc(dressi_pbr_read(s.plan, DRESSI_PBR_LOSS, out.data.data(), sizeof(float)),
+                     "dressi_pbr_read");
+        return out;
+    }
+    if (k >= kQServeGrad0 && k < kQServeP0) {
+        const int q = k - kQServeGrad0;
+        const ImgSize sz = s.size_of(q);
+        std::vector<float> rgba((size_t)sz.w * sz.h * 4);
+        const int which = q == 0 ? DRESSI_PBR_G_ALBEDO : q == 1 ? DRESSI_PBR_G_MR : DRESSI_PBR_G_ENV;
+        check_hip_rc(dressi_pbr_read(s.plan, which, rgba.data(), rgba.size() * sizeof(float)),
+                     "dressi_pbr_read");
+        CpuImage out(sz.w, sz.h, 3);
+        for (size_t i = 0; i < (size_t)sz.w * sz.h; i++) {
+            for (int c = 0; c < 3; c++) {
+                out.data[i * 3 + c] = rgba[i * 4 + c];
+            }
+        }
+        return out;
+    }
+    s.pull_state();
+    if (k == kQServeT) {
+        return s.data.at(kQT);
+    }
+    if (k >= kQServeV0) {
+        return s.data.at(kQV0 + (k - kQServeV0));
+    }
+    if (k >= kQServeM0) {
+        return s.data.at(kQM0 + (k - kQServeM0));
+    }
+    return s.data.at(kQParamRole[k - kQServeP0]);
+}
+
 std::unique_ptr<FusedRoute> RecogniseFusedRoute(const GraphRoots& g) {
     if (auto r = SilhouetteRoute::Recognise(g)) {
         return r;
     }
     if (auto r = TextureRoute::Recognise(g)) {
+        return r;
+    }
+    if (auto r = PbrRoute::Recognise(g)) {
         return r;
     }
     return nullptr;

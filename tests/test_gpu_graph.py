@@ -378,6 +378,26 @@ def test_pbr_example_graph_matches_reference_fixture(tmp_path, golden, name, nai
     close(got["loss"][:1], g["out_loss"][:1], 1e-5, "loss")
     for k in ("g_albedo0", "g_mr0", "g_env0"):
         close(got[k], g["out_" + k], 1e-4, k)
+    if not naive:
+        # RSP: the graph runs on the fused PBR plan (the route), and gives
+        # the plan's own results bit for bit
+        assert "plan=fused:pbr stages=1" in res.stdout, res.stdout
+        import opendressi_amd as od
+        from opendressi_amd import _lib
+        ctx = od.Context(0)
+        sc = {k: a[k] for k in keys}
+        sc.update(screen=s, levels=levels, lr=float(g["in_lr"]))
+        fit = od.PbrFit(ctx, sc, keep_grad=True)
+        fit.step(1, graph=False)
+        for k, which in (("g_albedo0", _lib.PBR_G_ALBEDO), ("g_mr0", _lib.PBR_G_MR),
+                         ("g_env0", _lib.PBR_G_ENV)):
+            assert np.array_equal(got[k], fit.read(which)[..., :3].reshape(-1)), k
+        fit.step(iters - 1)
+        alb, mr, env, t = fit.state()
+        for k, want in (("albedo", alb), ("mr", mr), ("env", env)):
+            assert np.array_equal(got[k], want[..., :3].reshape(-1)), k
+        fit.close()
+        ctx.close()
     for k in ("albedo", "mr", "env"):
         diff = float(np.abs(got[k].astype(np.float64) - g["out_" + k].reshape(-1)).max())
         assert diff <= 1e-3, f"{k}: max diff {diff:.3g} (tol 1e-3)"
