@@ -117,9 +117,11 @@ int dressi_rasterize_soft(dressi_ctx* ctx, const float* soft_clip,
  * context workspace, so a call needs 256-byte-aligned 176 B + 16 B per face
  * plus 4100 B per 16x16 tile (+256) within 32 MiB (e.g. a 1024x1024 screen
  * with up to ~79k faces) and returns DRESSI_ERR_INVALID beyond that. Every
- * call on one GPU shares that GPU's array: a call on another stream than
- * the GPU's previous call waits for that call's work first (not under
- * graph capture); calls that overlap in host time (other threads) race. */
+ * call on one GPU shares that GPU's array: host calls (from any thread)
+ * are taken one at a time, and a call on another stream than the GPU's
+ * previous call waits for that call's work first. A call made while its
+ * stream is captured into a graph is not ordered that way: replays of such
+ * a graph race with every other call on the GPU. */
 int dressi_rasterize_soft_noalloc(dressi_ctx* ctx, const float* soft_clip,
                                   const float* face_id, const float* faces_soft,
                                   const float* hard_clip, uint32_t n_verts,

@@ -132,7 +132,7 @@ struct PbrDev {
     float* gyM;    // per pixel g metallic
     float4* mgA;   // per pixel: fg (d loss / d irradiance sample, 0); bg (d loss / d env sample, 0)
     float4* mgB;   // per fg pixel: (d loss / d prefiltered sample before the level weights, roughness)
-    float* loss_part;
+    float4* loss_part;  // per shading tile: its |diff| sum (Reduce2x2Sum order)
     float* loss;
     float4* pred;  // KEEP_PRED
     float4 *g_tex_a, *g_tex_m, *g_env;  // KEEP_GRAD
@@ -749,6 +749,53 @@ __global__ __launch_bounds__(192) void k_pbr_conv_fwd(PbrDev d) {
     }
 }
 
+// F::Sum (f_ops.cpp:1037-1043) reduces an image by Reduce2x2Sum levels
+// (f_ops.cpp:999-1033: each output texel adds its 2x2 source block from 0
+// in row order, a missing row or column adding nothing) down to 1 x 1. On a
+// 16 x 16-aligned block that is a quadtree whose four lowest levels lie in
+// the block; zero padding is exact (the sums start at +0).
+struct QuadLds {
+    float4 q[256], q1[64], q2[16], q3[4];
+};
+
+__device__ __forceinline__ float4 quad4(const float4& a, const float4& b, const float4& c,
+                                        const float4& e) {
+    float4 r;
+    r.x = (((0.f + a.x) + b.x) + c.x) + e.x;
+    r.y = (((0.f + a.y) + b.y) + c.y) + e.y;
+    r.z = (((0.f + a.z) + b.z) + c.z) + e.z;
+    r.w = 0.f;
+    return r;
+}
+
+// The 16 x 16 block in L.q (row-major) reduced by four Reduce2x2Sum levels;
+// the result in thread 0. Every thread of the 256-thread workgroup calls it.
+__device__ float4 quad_reduce16(QuadLds& L) {
+    const uint32_t t = threadIdx.x;
+    __syncthreads();
+    if (t < 64) {
+        const uint32_t i = (t >> 3) * 32u + (t & 7u) * 2u;
+        L.q1[t] = quad4(L.q[i], L.q[i + 1], L.q[i + 16], L.q[i + 17]);
+    }
+    __syncthreads();
+    if (t < 16) {
+        const uint32_t i = (t >> 2) * 16u + (t & 3u) * 2u;
+        L.q2[t] = quad4(L.q1[i], L.q1[i + 1], L.q1[i + 8], L.q1[i + 9]);
+    }
+    __syncthreads();
+    if (t < 4) {
+        const uint32_t i = (t >> 1) * 8u + (t & 1u) * 2u;
+        L.q3[t] = quad4(L.q2[i], L.q2[i + 1], L.q2[i + 4], L.q2[i + 5]);
+    }
+    __syncthreads();
+    float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t == 0) {
+        r = quad4(L.q3[0], L.q3[1], L.q3[2], L.q3[3]);
+    }
+    __syncthreads();  // L is reused by the caller
+    return r;
+}
+
 // Per pixel (a 16 x 16 tile of one view per workgroup): the shading
 // forward, the L1 loss and its backward (the derivation of the reference's
 // autodiff of pbr_graph.cpp:47-137 through Div / Mul / Add / Max / Mix /
@@ -758,7 +805,7 @@ __global__ __launch_bounds__(192) void k_pbr_conv_fwd(PbrDev d) {
 // The prefilter levels with a tent weight 1 - |lod - i| >= 0 are among
 // floor(lod) - 1 .. floor(lod) + 1: three register slots.
 __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
-    __shared__ float lred[4];
+    __shared__ QuadLds lq;
     const uint32_t tiles = (d.S + kShadeTile - 1) / kShadeTile;
     const uint32_t view = blockIdx.x / (tiles * tiles);
     const uint32_t tile = blockIdx.x % (tiles * tiles);
@@ -884,14 +931,14 @@ __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
     }
     // ---- loss and d loss / d hdr -----------------------------------------
     float gh[3] = {0.f, 0.f, 0.f};
-    float lsum = 0.f;
+    float lc[3] = {0.f, 0.f, 0.f};  // |diff| per channel (0 off the screen)
     if (valid) {
         const float4 tg = d.target[p];
         const float tv[3] = {tg.x, tg.y, tg.z};
 #pragma unroll
         for (int c = 0; c < 3; c++) {
             const float diff = tv[c] - mapped[c];
-            lsum += fabsf(diff);
+            lc[c] = fabsf(diff);
             const float sg = (float)((diff > 0.f) - (diff < 0.f));
             const float gm = -(d.inv_n * sg);
             gh[c] = gm / (hdr[c] + 1.f) - gm * hdr[c] / ((hdr[c] + 1.f) * (hdr[c] + 1.f));
@@ -938,6 +985,21 @@ __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
             const float sgn = (float)((dl > 0.f) - (dl < 0.f));
             glod -= gw * sgn;
         }
+        {
+            // level floor(lod) + 2: lod - i rounds to exactly -1 when lod lies
+            // within half an ulp below an integer, and its weight clamp(0, 0,
+            // 1) = 0 adds nothing forward, but Clamp's backward passes the
+            // gradient at its bounds (Step(lo, x) * Step(x, hi)); it comes
+            // last in level order, with dl < 0
+            const int i = li[2] + 1;
+            if (i < L && s2.z >= 0.f && 1.f - fabsf(lod - (float)i) >= 0.f) {
+                const uint4 lv = d.ltab[i];
+                float P3[3];
+                fetch4(taps_wrap((int)lv.x, (int)lv.y, s2.z, s2.w), d.pref + lv.z, P3);
+                const float gw = gpref[0] * P3[0] + gpref[1] * P3[1] + gpref[2] * P3[2];
+                glod -= gw * -1.f;
+            }
+        }
         gr += glod * (float)(L - 1);
         const float gD = gS * g_v * g_l / den;
         const float ggv = gS * D * g_l / den;
@@ -965,18 +1027,11 @@ __global__ __launch_bounds__(256) void k_pbr_shade(PbrDev d) {
             d.mgB[p] = make_float4(gpref[0], gpref[1], gpref[2], rough);
         }
     }
-    // ---- loss partial of the workgroup ------------------------------------
-    float v = lsum;
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) {
-        v += __shfl_xor(v, sh);
-    }
-    if ((threadIdx.x & 63) == 0) {
-        lred[threadIdx.x >> 6] = v;
-    }
-    __syncthreads();
+    // ---- loss partial of the tile: Sum's first four Reduce2x2Sum levels ---
+    lq.q[threadIdx.x] = make_float4(lc[0], lc[1], lc[2], 0.f);
+    const float4 tsum = quad_reduce16(lq);
     if (threadIdx.x == 0) {
-        d.loss_part[blockIdx.x] = ((lred[0] + lred[1]) + lred[2]) + lred[3];
+        d.loss_part[blockIdx.x] = tsum;
     }
 }
 
@@ -1396,31 +1451,76 @@ __global__ __launch_bounds__(256) void k_pbr_tex_adam(PbrDev d) {
     adam3(d, bc1, bc2, gmr, &d.mr[i], &d.mm[i], &d.mv[i], true);
 }
 
-// The loss scalar (the workgroups' partial |diff| sums * 1 / (W H 3)) and
-// the step counter.
-__global__ __launch_bounds__(256) void k_pbr_loss(PbrDev d, uint32_t n_part) {
-    __shared__ float red[4];
-    // 8 independent loads in flight per thread (a single workgroup would
-    // otherwise wait one memory latency per partial)
-    float acc8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (uint32_t j0 = threadIdx.x; j0 < n_part; j0 += 8 * blockDim.x) {
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const uint32_t j = j0 + (uint32_t)u * blockDim.x;
-            acc8[u] += j < n_part ? d.loss_part[j] : 0.f;
+// The loss scalar and the step counter. Per view, F::Mean of the |diff|
+// image (f_ops.cpp:1045-1050): Sum's remaining Reduce2x2Sum levels over the
+// shading tiles' partials (a `tiles` x `tiles` grid, reduced 16 x 16 blocks
+// at a time, block-aligned, so the quadtree is Sum's), then CompSum (from 0,
+// components in order, f_ops.cpp:743-770) times 1 / (W H 3); the views'
+// losses added by SumPixelWise's tree (f_ops.cpp:893-950: groups of at most
+// four, each from 0 in order, a lone entry passed up).
+constexpr uint32_t kLossGrid = 1024;  // a level's grid of block sums in LDS
+__global__ __launch_bounds__(256) void k_pbr_loss(PbrDev d, uint32_t tiles) {
+    __shared__ QuadLds L;
+    __shared__ float4 grid[2][kLossGrid];
+    __shared__ float vl[kPbrMaxViews];
+    const uint32_t t = threadIdx.x;
+    for (uint32_t view = 0; view < d.n_views; view++) {
+        uint32_t side = tiles, cur = 0;
+        const float4* src = d.loss_part + (size_t)view * tiles * tiles;
+        bool global = true;
+        while (side > 1) {
+            const uint32_t nside = (side + 15u) / 16u;
+            for (uint32_t b = 0; b < nside * nside; b++) {
+                const uint32_t x = (b % nside) * 16u + (t & 15u);
+                const uint32_t y = (b / nside) * 16u + (t >> 4);
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (x < side && y < side) {
+                    v = global ? src[(size_t)y * side + x] : grid[cur][y * side + x];
+                }
+                L.q[t] = v;
+                const float4 r = quad_reduce16(L);
+                if (t == 0) {
+                    grid[cur ^ 1u][b] = r;
+                }
+            }
+            __syncthreads();
+            cur ^= 1u;
+            global = false;
+            side = nside;
         }
+        if (t == 0) {
+            const float4 s = global ? src[0] : grid[cur][0];
+            float acc = 0.f;
+            acc += s.x;
+            acc += s.y;
+            acc += s.z;
+            vl[view] = acc * d.inv_n;
+        }
+        __syncthreads();
     }
-    float v = ((acc8[0] + acc8[1]) + (acc8[2] + acc8[3])) + ((acc8[4] + acc8[5]) + (acc8[6] + acc8[7]));
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) {
-        v += __shfl_xor(v, s);
-    }
-    if ((threadIdx.x & 63) == 0) {
-        red[threadIdx.x >> 6] = v;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        d.loss[0] = (((red[0] + red[1]) + red[2]) + red[3]) * d.inv_n;
+    if (t == 0) {
+        float lv[kPbrMaxViews];
+        uint32_t n = d.n_views;
+        for (uint32_t i = 0; i < n; i++) {
+            lv[i] = vl[i];
+        }
+        while (n > 1) {
+            uint32_t m = 0;
+            for (uint32_t i = 0; i < n; i += 4) {
+                const uint32_t k = n - i < 4u ? n - i : 4u;
+                if (k == 1) {
+                    lv[m++] = lv[i];
+                } else {
+                    float acc = 0.f;
+                    for (uint32_t j = 0; j < k; j++) {
+                        acc += lv[i + j];
+                    }
+                    lv[m++] = acc;
+                }
+            }
+            n = m;
+        }
+        d.loss[0] = lv[0];
         *d.t = *d.t + 1.f;
     }
 }
@@ -1487,7 +1587,8 @@ int launch_pbr_kernel(const PbrDev& d, hipStream_t s, int k) {
                                d);
             break;
         default:
-            hipLaunchKernelGGL(k_pbr_loss, dim3(1), dim3(256), 0, s, d, shade_blocks(d));
+            hipLaunchKernelGGL(k_pbr_loss, dim3(1), dim3(256), 0, s, d,
+                               (d.S + kShadeTile - 1) / kShadeTile);
             break;
     }
     DRESSI_CHECK_LAUNCH();
@@ -2029,6 +2130,8 @@ int dressi_pbr_create(dressi_ctx* ctx, const dressi_pbr_desc* desc, dressi_pbr_p
     DRESSI_REQUIRE((uint64_t)desc->n_views * desc->width * desc->height * (kPbrMaxLevels + 2) * 4 <
                            (1ull << 31),
                    "too many pixels (views x width x height x (levels + 2) x 4 must be < 2^31)");
+    // the loss kernel keeps a level of 16 x 16-tile block sums in LDS
+    DRESSI_REQUIRE(desc->width <= 8192, "the screen must be at most 8192 px wide");
     DRESSI_REQUIRE(desc->tex_w > 0 && desc->tex_h > 0 &&
                            (uint64_t)desc->tex_w * desc->tex_h < (1ull << 28),
                    "bad texture size");

@@ -379,11 +379,12 @@ __global__ void k_faces_to_i32(const float* faces, uint32_t n, uint32_t n_verts,
 // host code the name `scratch` is a host-side stand-in, never the device
 // array: kernels take the per-device address that hipGetSymbolAddress
 // returns (noalloc_scratch below). Every call on a GPU shares that GPU's
-// array: calls on one stream run in order, and a call on another stream
-// than the GPU's previous call first waits for that call's work (an event
-// created with the array's address, recorded after every call; not while
-// the stream is being captured into a graph). Calls that overlap in host
-// time on one GPU still race.
+// array: host calls are taken one at a time (g_noalloc_mu), calls on one
+// stream run in order, and a call on another stream than the GPU's previous
+// call first waits for that call's work (an event created with the array's
+// address, recorded after every call). A call made while its stream is
+// captured into a graph records no wait and no event, so replays of that
+// graph race with every other call on the GPU.
 constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 

@@ -767,6 +767,49 @@ static void shade_px(const ShadeCtx* s, const Gpx* g, const float* gh, ShadeOut*
 }
 
 /* See the header: the C5 split-sum PBR/IBL material + environment fit. */
+/* F::Sum (f_ops.cpp:1037-1043): Reduce2x2Sum (f_ops.cpp:999-1033: each
+ * output texel of the (w + 1) / 2 x (h + 1) / 2 image adds, from 0, the
+ * source texels in row order) until the image is 1 x 1. `img` (w x h x n) is
+ * overwritten; out[n] receives the sums. */
+static void sum_image(float* img, uint32_t w, uint32_t h, uint32_t n, float* out) {
+    while (w > 1 || h > 1) {
+        const uint32_t ow = (w + 1) / 2, oh = (h + 1) / 2;
+        float* y = (float*)calloc((size_t)ow * oh * n, sizeof(float));
+        for (uint32_t py = 0; py < h; py++) {
+            for (uint32_t px = 0; px < w; px++) {
+                const size_t si = ((size_t)py * w + px) * n;
+                const size_t di = ((size_t)(py / 2) * ow + px / 2) * n;
+                for (uint32_t c = 0; c < n; c++) y[di + c] += img[si + c];
+            }
+        }
+        memcpy(img, y, sizeof(float) * (size_t)ow * oh * n);
+        free(y);
+        w = ow;
+        h = oh;
+    }
+    for (uint32_t c = 0; c < n; c++) out[c] = img[c];
+}
+
+/* SumPixelWise over scalars (f_ops.cpp:893-950): groups of at most four,
+ * each added from 0 in order (a lone entry passed up), until one is left. */
+static float sum_pixelwise(float* v, uint32_t n) {
+    while (n > 1) {
+        uint32_t m = 0;
+        for (uint32_t i = 0; i < n; i += 4) {
+            const uint32_t k = n - i < 4 ? n - i : 4;
+            if (k == 1) {
+                v[m++] = v[i];
+            } else {
+                float acc = 0.f;
+                for (uint32_t j = 0; j < k; j++) acc += v[i + j];
+                v[m++] = acc;
+            }
+        }
+        n = m;
+    }
+    return v[0];
+}
+
 int or_pbr_fit(const float* pos, const float* normal, uint32_t n_verts, const float* uv,
                const float* faces, uint32_t n_faces, const float* mvps, const float* frames,
                const float* light, uint32_t n_views, uint32_t screen_px, uint32_t tex_w,
@@ -776,7 +819,7 @@ int or_pbr_fit(const float* pos, const float* normal, uint32_t n_verts, const fl
                uint32_t iters, float* out_albedo, float* out_mr, float* out_env, float* out_loss,
                float* out_g_albedo0, float* out_g_mr0, float* out_g_env0, float* out_pred0,
                float* out_target0, float* out_mask0) {
-    if (levels < 2 || levels > 16 || n_views == 0) return -1;
+    if (levels < 2 || levels > 16 || n_views == 0 || n_views > 64) return -1;
     const uint32_t S = screen_px;
     const size_t px = (size_t)S * S, ntx = (size_t)tex_w * tex_h, nev = (size_t)env_w * env_h;
     const uint32_t lutw = 256, luth = 256;
@@ -921,6 +964,8 @@ int or_pbr_fit(const float* pos, const float* normal, uint32_t n_verts, const fl
     float* dr = (float*)malloc(sizeof(float) * px * 3);
     float* dy = (float*)malloc(sizeof(float) * px * 3);
     const float inv_n = 1.f / ((float)S * (float)S * 3.f);
+    float* adiff = (float*)malloc(sizeof(float) * px * 3);  /* |diff| image of a view */
+    float vloss[64];
     float t_state = 0.f;
     for (uint32_t it = 0; it < iters; it++) {
         ibl_build(&maps, env);
@@ -935,9 +980,7 @@ int or_pbr_fit(const float* pos, const float* normal, uint32_t n_verts, const fl
         memset(g_env, 0, sizeof(float) * nev * 3);
         memset(g_irr, 0, sizeof(float) * maps.iw * maps.ih * 3);
         memset(g_pref, 0, sizeof(float) * npref);
-        float loss = 0.f;
         for (uint32_t view = 0; view < n_views; view++) {
-            float ssum[3] = {0.f, 0.f, 0.f};
             for (size_t p = 0; p < px; p++) {
                 const size_t q = view * px + p;
                 shade_px(&sc, &gb[q], NULL, &so);
@@ -947,7 +990,7 @@ int or_pbr_fit(const float* pos, const float* normal, uint32_t n_verts, const fl
                     const float mapped = hdr / (hdr + 1.f);
                     if (it == 0 && out_pred0) out_pred0[q * 3 + c] = mapped;
                     const float diff = target[q * 3 + c] - mapped;
-                    ssum[c] += fabsf(diff);
+                    adiff[p * 3 + c] = fabsf(diff);
                     const float sg = (float)((diff > 0.f) - (diff < 0.f));
                     const float gmp = -(inv_n * sg);
                     gh[c] = gmp / (hdr + 1.f) - gmp * hdr / ((hdr + 1.f) * (hdr + 1.f));
@@ -972,7 +1015,13 @@ int or_pbr_fit(const float* pos, const float* normal, uint32_t n_verts, const fl
                 dy[p * 3 + 1] = so.ray.y;
                 dy[p * 3 + 2] = so.ray.z;
             }
-            loss += (ssum[0] + ssum[1] + ssum[2]) * inv_n;
+            /* the view's loss: Mean = CompSum(Sum(|diff|)) * inv_n
+             * (f_ops.cpp:743-770, 1045-1050) */
+            float ssum[3];
+            sum_image(adiff, S, S, 3, ssum);
+            float cs = 0.f;
+            for (int c = 0; c < 3; c++) cs += ssum[c];
+            vloss[view] = cs * inv_n;
             /* texture gradients: inverse-UV gathers */
             const float* ivv = inv + ntx * 4 * view;
             const float* uvv = g_uv + px * 2 * view;
@@ -994,6 +1043,7 @@ int or_pbr_fit(const float* pos, const float* normal, uint32_t n_verts, const fl
             for (size_t i = 0; i < nev * 3; i++) g_env[i] += tmp[i];
         }
         ibl_backward(&maps, g_irr, g_pref, g_env);
+        const float loss = sum_pixelwise(vloss, n_views);
         if (out_loss) out_loss[it] = loss;
         if (it == 0) {
             if (out_g_albedo0) memcpy(out_g_albedo0, g_alb, sizeof(float) * ntx * 3);
@@ -1037,6 +1087,7 @@ int or_pbr_fit(const float* pos, const float* normal, uint32_t n_verts, const fl
         free(st_m[j]);
         free(st_v[j]);
     }
+    free(adiff);
     free(gya);
     free(gym);
     free(gt);
