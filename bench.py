@@ -151,7 +151,8 @@ def kernel_bytes_pbr(n_views: int, s: int, texels: int, env_texels: int, pooled:
         "k_pbr_conv_bwd": 12.0 * map_texels + 12.0 * pooled,
         "k_pbr_env_adam": 24.0 * E + 72.0 * E,
         "k_pbr_tex_adam": n * 20.0 * S2 + 96.0 * T,
-        "k_pbr_loss": 4.0 * n * S2 / 256.0,
+        "k_pbr_loss_blocks": 16.0 * n * S2 / 256.0,
+        "k_pbr_loss": 16.0 * n * S2 / 65536.0,
     }
 
 

@@ -21,7 +21,7 @@
 // f_ops.cpp:2785-2919), views are added in view order, and the texture
 // gather adds each view's window sum in view order.
 //
-// One iteration, 10 kernels + the pooling chain (ceil(log2) levels):
+// One iteration, 11 kernels + the pooling chain (ceil(log2) levels):
 //   k_pbr_pool        env -> pooled sources of the irradiance / prefilter maps
 //   k_pbr_conv_fwd    IrradianceConv + every PrefilterConv level (static
 //                     weight matrices, one wave per colour channel)
@@ -35,7 +35,10 @@
 //   k_pbr_env_adam    pooling VJPs + background gradient, Adam on the env
 //   k_pbr_tex_adam    GatherByInverseUVBilinear as a static gather list per
 //                     texel (per-view sums), Adam on albedo and mr
-//   k_pbr_loss        the loss scalar, t + 1
+//   k_pbr_loss_blocks the loss's Reduce2x2Sum levels over 16 x 16 blocks of
+//                     the shading tiles' partials
+//   k_pbr_loss        the loss scalar (the remaining levels, CompSum, the
+//                     views' SumPixelWise tree), t + 1
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -43,6 +46,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <vector>
 
 #include <hipcub/hipcub.hpp>
@@ -61,9 +65,16 @@ constexpr uint32_t kPbrMaxPool = 12;
 constexpr uint32_t kPbrMaxMaps = kPbrMaxLevels + 2;
 constexpr int kShadeTile = 16;       // 16 x 16 pixel tile per shading workgroup
 constexpr uint32_t kTileSumLds = 4096;  // float4 partials staged per tile-sum round
+constexpr uint32_t kMvRows = 256;         // ordered mat-vec: summation steps per LDS tile
+constexpr uint32_t kMvCols = 32;          // ordered mat-vec: columns per workgroup (the lanes
+                                          // past kMvCols repeat the first ones' work)
 constexpr uint32_t kGatherChunk = 1024;  // map gather: positions staged per round
 constexpr uint32_t kGatherChains = 256;   // map gather: buckets per workgroup (1 per thread)
 constexpr uint32_t kGatherBands = 64;     // map gather: bands per workgroup
+constexpr uint32_t kGatherMaxChunks = 32;  // map gather: position chunks per workgroup (bands
+                                          // with more positions take position lists)
+constexpr uint32_t kGatherTile = 16;      // map gather: texel tile of a position-list workgroup
+constexpr uint32_t kBandMode = 0xffffffffu;
 
 // One sampled map of the shading and its EquirectSample VJP's layout: the
 // VJP adds, per view, k partial maps over bands of `rows` dir rows each
@@ -88,11 +99,24 @@ struct MapInfo {
 // background pixels). Chunk c's entries of bucket j are mg_ent[coff[c0 + c na
 // + j] .. coff[c0 + c na + j + 1]) (chunk-major, then bucket order, then pixel
 // order), each (LDS slot << 2) | tap. f0: the set-up's first-entry table.
+// A band with more than kGatherMaxChunks chunks of positions is split by
+// texel tile instead (position-list mode, nb = 1, bmo != kBandMode): the
+// workgroup's positions are only those its buckets read, in order --
+// plist[pl0 .. pl0 + npl) as global pixel indices; at set-up a position's
+// index in that list is its rank in the workgroup's bitmap of band positions
+// (words bm[bmo ..], with exclusive popcount prefixes wpre[bmo ..]).
 struct GatherItem {
     uint32_t m, vb0, nb, P;
     uint32_t a0, na, nch, c0;
-    uint32_t f0, pad0, pad1, pad2;
+    uint32_t f0, npl, pl0, bmo;
 };
+
+// Index of band position `pos` in a position-list workgroup's list
+__device__ __forceinline__ uint32_t list_rank(const uint32_t* bm, const uint32_t* wpre,
+                                              uint32_t bmo, uint32_t pos) {
+    const uint32_t w = bm[bmo + (pos >> 5)];
+    return wpre[bmo + (pos >> 5)] + (uint32_t)__popc(w & ((1u << (pos & 31u)) - 1u));
+}
 
 struct PbrDev {
     uint32_t n_views, S, tw, th, ew, eh, levels;
@@ -133,6 +157,7 @@ struct PbrDev {
     float4* mgA;   // per pixel: fg (d loss / d irradiance sample, 0); bg (d loss / d env sample, 0)
     float4* mgB;   // per fg pixel: (d loss / d prefiltered sample before the level weights, roughness)
     float4* loss_part;  // per shading tile: its |diff| sum (Reduce2x2Sum order)
+    float4* loss_blk;   // per 16 x 16 block of shading tiles: its sum (same order)
     float* loss;
     float4* pred;  // KEEP_PRED
     float4 *g_tex_a, *g_tex_m, *g_env;  // KEEP_GRAD
@@ -144,6 +169,7 @@ struct PbrDev {
     const uint32_t* ml_order;  // per (map, view, band) its non-empty buckets, bucket order
     const uint32_t* ml_off;   // per bucket, into the sorted entries (n_buckets + 1)
     const uint32_t* bg_pix;   // per view from bg_base[v]: the background pixels in order
+    const uint32_t* plist;    // position-list workgroups' positions (global pixel indices)
     const uint32_t* bg_base;  // per view (n_views + 1)
     const struct GatherItem* gitems;  // the gather's workgroups
     uint32_t n_gitems;
@@ -357,8 +383,8 @@ __global__ __launch_bounds__(256) void k_pbr_csr(CsrArgs a) {
 //   prefilter:  w = GgxConvWeight(c, alpha_o), wf = w sin(theta_s),
 //               wb = w / max(norm_o, 1e-12) where w > 0, else 0
 // wf is a matrix of rows s, columns o; wb of rows o, columns s (rows: the
-// index each ordered sum runs over); both tile-major in column groups of 64,
-// zero past the last column. A zero weight adds nothing to a sum of finite
+// index each ordered sum runs over); both tile-major in column groups of
+// kMvCols, zero past the last column. A zero weight adds nothing to a sum of finite
 // terms.
 __global__ __launch_bounds__(256) void k_pbr_weights(const float4* odir, uint32_t no,
                                                      const float4* sdir, uint32_t ns,
@@ -382,8 +408,8 @@ __global__ __launch_bounds__(256) void k_pbr_weights(const float4* odir, uint32_
         b = w > 0.f ? w / (nt < 1e-12f ? 1e-12f : nt) : 0.f;
     }
     // tile-major: wf rows are sources (no outputs per row), wb rows outputs
-    wf[((size_t)(o / 64u) * ns + sidx) * 64u + (o % 64u)] = f;
-    wb[((size_t)(sidx / 64u) * no + o) * 64u + (sidx % 64u)] = b;
+    wf[((size_t)(o / kMvCols) * ns + sidx) * kMvCols + (o % kMvCols)] = f;
+    wb[((size_t)(sidx / kMvCols) * no + o) * kMvCols + (sidx % kMvCols)] = b;
 }
 
 // Keys of the map-gradient gather lists: per (view, pixel) in pixel order,
@@ -500,6 +526,105 @@ __global__ __launch_bounds__(256) void k_pbr_bg_fill(const uint32_t* flag, const
     }
 }
 
+// Position-list workgroups, step 1: the band positions their buckets' sorted
+// entries read, as bits of the workgroup's bitmap (cleared before).
+__global__ __launch_bounds__(256) void k_pbr_list_bits(const GatherItem* items, uint32_t n_items,
+                                                       const MapInfo* minfo, uint32_t S,
+                                                       const uint32_t* bg_base,
+                                                       const uint32_t* order, const uint32_t* off,
+                                                       const uint32_t* ent, uint32_t* bm) {
+    const uint32_t it = blockIdx.y;
+    if (it >= n_items) {
+        return;
+    }
+    const GatherItem g = items[it];
+    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g.bmo == kBandMode || j >= g.na) {
+        return;
+    }
+    const MapInfo mi = minfo[g.m];
+    const uint32_t b = order[g.a0 + j];
+    const BandPos bp = band_pos(mi, (b - mi.bucket0) / mi.T, S, bg_base);
+    for (uint32_t e = off[b]; e < off[b + 1]; e++) {
+        const uint32_t pos = (ent[e] >> 2) - bp.posoff;
+        atomicOr(&bm[g.bmo + (pos >> 5)], 1u << (pos & 31u));
+    }
+}
+
+// Step 2, one workgroup per item: the exclusive popcount prefix of every
+// bitmap word and the list length npl[item].
+__global__ __launch_bounds__(256) void k_pbr_list_count(const GatherItem* items,
+                                                        uint32_t n_items, const MapInfo* minfo,
+                                                        uint32_t S, const uint32_t* bg_base,
+                                                        const uint32_t* bm, uint32_t* wpre,
+                                                        uint32_t* npl) {
+    __shared__ uint32_t sc[256];
+    const uint32_t it = blockIdx.x;
+    if (it >= n_items) {
+        return;
+    }
+    const GatherItem g = items[it];
+    if (g.bmo == kBandMode) {
+        return;
+    }
+    const MapInfo mi = minfo[g.m];
+    const uint32_t words = (band_pos(mi, g.vb0, S, bg_base).npos + 31u) / 32u;
+    const uint32_t t = threadIdx.x;
+    uint32_t carry = 0;
+    for (uint32_t w0 = 0; w0 < words; w0 += 256u) {
+        const uint32_t c = w0 + t < words ? (uint32_t)__popc(bm[g.bmo + w0 + t]) : 0u;
+        sc[t] = c;
+        __syncthreads();
+        // inclusive Hillis-Steele scan
+        for (uint32_t o = 1; o < 256u; o <<= 1) {
+            const uint32_t add = t >= o ? sc[t - o] : 0u;
+            __syncthreads();
+            sc[t] += add;
+            __syncthreads();
+        }
+        if (w0 + t < words) {
+            wpre[g.bmo + w0 + t] = carry + sc[t] - c;
+        }
+        carry += sc[255];
+        __syncthreads();
+    }
+    if (t == 0) {
+        npl[it] = carry;
+    }
+}
+
+// Step 3: the lists themselves, in band-position order, as global pixel
+// indices (view base + the position's pixel, the env's via bg_pix).
+__global__ __launch_bounds__(256) void k_pbr_list_fill(const GatherItem* items, uint32_t n_items,
+                                                       const MapInfo* minfo, uint32_t S,
+                                                       const uint32_t* bg_base,
+                                                       const uint32_t* bg_pix, const uint32_t* bm,
+                                                       const uint32_t* wpre, uint32_t* plist) {
+    const uint32_t it = blockIdx.y;
+    if (it >= n_items) {
+        return;
+    }
+    const GatherItem g = items[it];
+    if (g.bmo == kBandMode) {
+        return;
+    }
+    const MapInfo mi = minfo[g.m];
+    const BandPos bp = band_pos(mi, g.vb0, S, bg_base);
+    const uint32_t words = (bp.npos + 31u) / 32u;
+    const size_t vbase = (size_t)bp.v * S * S;
+    for (uint32_t w = blockIdx.x * blockDim.x + threadIdx.x; w < words;
+         w += gridDim.x * blockDim.x) {
+        uint32_t bits = bm[g.bmo + w];
+        uint32_t r = g.pl0 + wpre[g.bmo + w];
+        while (bits) {
+            const uint32_t pos = w * 32u + (uint32_t)__builtin_ctz(bits);
+            bits &= bits - 1u;
+            plist[r++] = (uint32_t)(vbase + (mi.kind == 2 ? bg_pix[bp.pbase + pos]
+                                                          : bp.pbase + pos));
+        }
+    }
+}
+
 // Per gather item and bucket j (thread): the first sorted entry of each chunk
 // (positions c P .. of the bucket's band), fo[f0 + c na + j] for c = 0 .. nch
 // (nch: the list's end), and the chunk's entry count cnt[c0 + c na + j].
@@ -507,7 +632,8 @@ __global__ __launch_bounds__(256) void k_pbr_chunk_first(const GatherItem* items
                                                          uint32_t n_items, const MapInfo* minfo,
                                                          uint32_t S, const uint32_t* bg_base,
                                                          const uint32_t* order, const uint32_t* off,
-                                                         const uint32_t* ent, uint32_t* fo,
+                                                         const uint32_t* ent, const uint32_t* bm,
+                                                         const uint32_t* wpre, uint32_t* fo,
                                                          uint32_t* cnt) {
     const uint32_t it = blockIdx.y;
     if (it >= n_items) {
@@ -524,7 +650,10 @@ __global__ __launch_bounds__(256) void k_pbr_chunk_first(const GatherItem* items
     uint32_t k = 0;
     const uint32_t e1 = off[b + 1];
     for (uint32_t e = off[b]; e < e1; e++) {
-        const uint32_t pos = (ent[e] >> 2) - bp.posoff;
+        uint32_t pos = (ent[e] >> 2) - bp.posoff;
+        if (g.bmo != kBandMode) {
+            pos = list_rank(bm, wpre, g.bmo, pos);
+        }
         while (k <= g.nch && k * g.P <= pos) {
             fo[g.f0 + k * g.na + j] = e;
             k++;
@@ -545,6 +674,7 @@ __global__ __launch_bounds__(256) void k_pbr_chunk_fill(const GatherItem* items,
                                                         const MapInfo* minfo, uint32_t S,
                                                         const uint32_t* bg_base,
                                                         const uint32_t* order, const uint32_t* ent,
+                                                        const uint32_t* bm, const uint32_t* wpre,
                                                         const uint32_t* fo, const uint32_t* coff,
                                                         uint16_t* out) {
     const uint32_t it = blockIdx.y;
@@ -566,7 +696,11 @@ __global__ __launch_bounds__(256) void k_pbr_chunk_fill(const GatherItem* items,
         const uint32_t dst = coff[g.c0 + c * g.na + j];
         for (uint32_t e = x0; e < x1; e++) {
             const uint32_t v = ent[e];
-            const uint32_t l = slot0 + (v >> 2) - bp.posoff - c * g.P;
+            uint32_t pos = (v >> 2) - bp.posoff;
+            if (g.bmo != kBandMode) {
+                pos = list_rank(bm, wpre, g.bmo, pos);
+            }
+            const uint32_t l = slot0 + pos - c * g.P;
             out[dst + (e - x0)] = (uint16_t)((l << 2) | (v & 3u));
         }
     }
@@ -606,8 +740,6 @@ __global__ __launch_bounds__(256) void k_pbr_pool(PbrDev d, uint32_t lvl) {
 // double-buffered in LDS (128 KB of weights + the x rows): the workgroup's
 // next tile is in flight while its three waves (one per colour channel) add
 // the current one.
-constexpr uint32_t kMvRows = 256;
-constexpr uint32_t kMvCols = 64;
 constexpr uint32_t kMvThreads = 192;
 constexpr uint32_t kMvVec = kMvRows * kMvCols / 4;                    // float4 per weight tile
 constexpr uint32_t kMvPer = (kMvVec + kMvThreads - 1) / kMvThreads;  // per thread
@@ -669,7 +801,7 @@ __device__ __forceinline__ void mv_store(MvLds& L, int b, const MvRegs& g) {
 // synchronises the workgroup).
 __device__ float mv_segment(MvLds& L, const float* __restrict__ Wg,
                             const float4* __restrict__ x, uint32_t r0, uint32_t r1) {
-    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t lane = (threadIdx.x & 63u) % kMvCols;
     const uint32_t c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n = r1 - r0;
     const uint32_t tiles = (n + kMvRows - 1) / kMvRows;
@@ -733,12 +865,12 @@ __global__ __launch_bounds__(192) void k_pbr_conv_fwd(PbrDev d) {
     const uint32_t n_out = irr ? d.iw * d.ih : d.n_pref;
     const uint32_t n_src = irr ? d.isw * d.ish : d.psw * d.psh;
     const uint32_t col0 = (irr ? blockIdx.x : blockIdx.x - d.n_ig) * kMvCols;
-    const uint32_t o = col0 + (threadIdx.x & 63u);
+    const uint32_t o = col0 + (threadIdx.x & 63u) % kMvCols;
     const uint32_t c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const float4* src = irr ? d.pool[d.irr_pool] : d.pool[d.pref_pool];
     const float* Wg = (irr ? d.wf_irr : d.wf_pref) + (size_t)col0 * n_src;  // group's rows
     const float acc = mv_segment(L, Wg, src, 0, n_src);
-    if (o >= n_out) {
+    if (o >= n_out || (threadIdx.x & 63u) >= kMvCols) {
         return;
     }
     if (irr) {
@@ -1087,6 +1219,7 @@ __global__ __launch_bounds__(256) void k_pbr_map_gather(PbrDev d) {
     const uint32_t nch = it.nch, P = it.P, nslot = it.nb * it.P;
     const uint32_t* coff = d.coff + it.c0;
     const bool mine = tid < it.na;
+    const bool listed = it.bmo != kBandMode;  // positions from the workgroup's list (nb = 1)
     // this thread's position slots: band and position within the chunk
     uint32_t sbi0, sbi1, sbi2, sbi3;
     sbi0 = tid < nslot ? tid / P : 0u;
@@ -1106,12 +1239,22 @@ __global__ __launch_bounds__(256) void k_pbr_map_gather(PbrDev d) {
             const uint32_t u = tid + 256u * r;                                                   \
             const uint32_t bi = r == 0 ? sbi0 : (r == 1 ? sbi1 : (r == 2 ? sbi2 : sbi3));       \
             const uint32_t pos = cc_ * P + (u - bi * P);                                         \
-            rv[r] = u < nslot && pos < bnpos[bi];                                                \
-            if (rv[r]) {                                                                         \
-                const size_t q = (size_t)bvpx[bi] +                                              \
-                                 (mi.kind == 2 ? d.bg_pix[bbase[bi] + pos] : bbase[bi] + pos);   \
-                rs[r] = uvsrc[q];                                                                \
-                rg[r] = gsrc[q];                                                                 \
+            if (listed) {                                                                        \
+                rv[r] = pos < it.npl;                                                            \
+                if (rv[r]) {                                                                     \
+                    const uint32_t q = d.plist[it.pl0 + pos];                                    \
+                    rs[r] = uvsrc[q];                                                            \
+                    rg[r] = gsrc[q];                                                             \
+                }                                                                                \
+            } else {                                                                             \
+                rv[r] = u < nslot && pos < bnpos[bi];                                            \
+                if (rv[r]) {                                                                     \
+                    const size_t q =                                                             \
+                            (size_t)bvpx[bi] +                                                   \
+                            (mi.kind == 2 ? d.bg_pix[bbase[bi] + pos] : bbase[bi] + pos);        \
+                    rs[r] = uvsrc[q];                                                            \
+                    rg[r] = gsrc[q];                                                             \
+                }                                                                                \
             }                                                                                    \
         }                                                                                        \
         const uint32_t run0_ = coff[cc_ * it.na];                                                \
@@ -1168,6 +1311,24 @@ __global__ __launch_bounds__(256) void k_pbr_map_gather(PbrDev d) {
         __syncthreads();
         if (c + 1 < nch) {  // chunk c + 1's loads, in flight while this chunk is summed
             DRESSI_GATHER_FETCH(c + 1u)
+        }
+        for (; x + 8u <= x1; x += 8u) {
+            float c0[8], c1[8], c2[8];
+#pragma unroll
+            for (uint32_t r = 0; r < 8; r++) {
+                const uint32_t e = se[x + r];
+                const float w = sw[e];
+                const float4 g = sg[e >> 2];
+                c0[r] = g.x * w;
+                c1[r] = g.y * w;
+                c2[r] = g.z * w;
+            }
+#pragma unroll
+            for (uint32_t r = 0; r < 8; r++) {
+                a0 += c0[r];
+                a1 += c1[r];
+                a2 += c2[r];
+            }
         }
         for (; x + 4u <= x1; x += 4u) {
             float c0[4], c1[4], c2[4];
@@ -1301,9 +1462,9 @@ __global__ __launch_bounds__(192) void k_pbr_conv_bwd(PbrDev d) {
     const bool irr = blockIdx.x < d.n_isg;
     const uint32_t n_src = irr ? d.isw * d.ish : d.psw * d.psh;
     const uint32_t col0 = (irr ? blockIdx.x : blockIdx.x - d.n_isg) * kMvCols;
-    const uint32_t s = col0 + (threadIdx.x & 63u);
+    const uint32_t s = col0 + (threadIdx.x & 63u) % kMvCols;
     const uint32_t c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const bool ok = s < n_src;
+    const bool ok = s < n_src && (threadIdx.x & 63u) < kMvCols;
     if (irr) {
         const float acc = mv_segment(L, d.wb_irr + (size_t)col0 * (d.iw * d.ih), d.g_irr, 0,
                                      d.iw * d.ih);
@@ -1451,33 +1612,50 @@ __global__ __launch_bounds__(256) void k_pbr_tex_adam(PbrDev d) {
     adam3(d, bc1, bc2, gmr, &d.mr[i], &d.mm[i], &d.mv[i], true);
 }
 
+// The loss's next four Reduce2x2Sum levels: one workgroup per 16 x 16 block
+// of a view's shading-tile partials (a `tiles` x `tiles` grid, zero outside).
+__global__ __launch_bounds__(256) void k_pbr_loss_blocks(PbrDev d, uint32_t tiles) {
+    __shared__ QuadLds L;
+    const uint32_t nside = (tiles + 15u) / 16u;
+    const uint32_t view = blockIdx.x / (nside * nside), b = blockIdx.x % (nside * nside);
+    const uint32_t x = (b % nside) * 16u + (threadIdx.x & 15u);
+    const uint32_t y = (b / nside) * 16u + (threadIdx.x >> 4);
+    L.q[threadIdx.x] = x < tiles && y < tiles
+                               ? d.loss_part[((size_t)view * tiles + y) * tiles + x]
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 r = quad_reduce16(L);
+    if (threadIdx.x == 0) {
+        d.loss_blk[blockIdx.x] = r;
+    }
+}
+
 // The loss scalar and the step counter. Per view, F::Mean of the |diff|
 // image (f_ops.cpp:1045-1050): Sum's remaining Reduce2x2Sum levels over the
-// shading tiles' partials (a `tiles` x `tiles` grid, reduced 16 x 16 blocks
-// at a time, block-aligned, so the quadtree is Sum's), then CompSum (from 0,
-// components in order, f_ops.cpp:743-770) times 1 / (W H 3); the views'
-// losses added by SumPixelWise's tree (f_ops.cpp:893-950: groups of at most
-// four, each from 0 in order, a lone entry passed up).
-constexpr uint32_t kLossGrid = 1024;  // a level's grid of block sums in LDS
-__global__ __launch_bounds__(256) void k_pbr_loss(PbrDev d, uint32_t tiles) {
+// block sums (an `nside` x `nside` grid, reduced 16 x 16 blocks at a time,
+// block-aligned, so the quadtree is Sum's), then CompSum (from 0, components
+// in order, f_ops.cpp:743-770) times 1 / (W H 3); the views' losses added by
+// SumPixelWise's tree (f_ops.cpp:893-950: groups of at most four, each from 0
+// in order, a lone entry passed up).
+constexpr uint32_t kLossGrid = 1024;  // a level's block sums in LDS
+__global__ __launch_bounds__(256) void k_pbr_loss(PbrDev d, uint32_t nside) {
     __shared__ QuadLds L;
     __shared__ float4 grid[2][kLossGrid];
     __shared__ float vl[kPbrMaxViews];
     const uint32_t t = threadIdx.x;
     for (uint32_t view = 0; view < d.n_views; view++) {
-        uint32_t side = tiles, cur = 0;
-        const float4* src = d.loss_part + (size_t)view * tiles * tiles;
-        bool global = true;
+        uint32_t side = nside, cur = 0;
+        // the view's block sums into LDS
+        for (uint32_t i = t; i < nside * nside; i += 256u) {
+            grid[0][i] = d.loss_blk[(size_t)view * nside * nside + i];
+        }
+        __syncthreads();
         while (side > 1) {
-            const uint32_t nside = (side + 15u) / 16u;
-            for (uint32_t b = 0; b < nside * nside; b++) {
-                const uint32_t x = (b % nside) * 16u + (t & 15u);
-                const uint32_t y = (b / nside) * 16u + (t >> 4);
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (x < side && y < side) {
-                    v = global ? src[(size_t)y * side + x] : grid[cur][y * side + x];
-                }
-                L.q[t] = v;
+            const uint32_t ns = (side + 15u) / 16u;
+            for (uint32_t b = 0; b < ns * ns; b++) {
+                const uint32_t x = (b % ns) * 16u + (t & 15u);
+                const uint32_t y = (b / ns) * 16u + (t >> 4);
+                L.q[t] = x < side && y < side ? grid[cur][y * side + x]
+                                              : make_float4(0.f, 0.f, 0.f, 0.f);
                 const float4 r = quad_reduce16(L);
                 if (t == 0) {
                     grid[cur ^ 1u][b] = r;
@@ -1485,11 +1663,10 @@ __global__ __launch_bounds__(256) void k_pbr_loss(PbrDev d, uint32_t tiles) {
             }
             __syncthreads();
             cur ^= 1u;
-            global = false;
-            side = nside;
+            side = ns;
         }
         if (t == 0) {
-            const float4 s = global ? src[0] : grid[cur][0];
+            const float4 s = grid[cur][0];
             float acc = 0.f;
             acc += s.x;
             acc += s.y;
@@ -1526,16 +1703,19 @@ __global__ __launch_bounds__(256) void k_pbr_loss(PbrDev d, uint32_t tiles) {
 }
 
 // Kernel list of one iteration (the pooling chain counts as one entry)
-constexpr int kPbrKernels = 10;
+constexpr int kPbrKernels = 11;
 const char* const kPbrKernelNames[kPbrKernels] = {
-        "k_pbr_pool",     "k_pbr_conv_fwd", "k_pbr_shade",    "k_pbr_map_gather",
-        "k_pbr_tile_sum", "k_pbr_view_sum", "k_pbr_conv_bwd", "k_pbr_env_adam",
-        "k_pbr_tex_adam", "k_pbr_loss"};
+        "k_pbr_pool",     "k_pbr_conv_fwd", "k_pbr_shade",       "k_pbr_map_gather",
+        "k_pbr_tile_sum", "k_pbr_view_sum", "k_pbr_conv_bwd",    "k_pbr_env_adam",
+        "k_pbr_tex_adam", "k_pbr_loss_blocks", "k_pbr_loss"};
 // index of each kernel in the launch switch
 enum PbrK {
     kKPool = 0, kKConvFwd, kKShade, kKGather, kKTileSum, kKViewSum, kKConvBwd, kKEnvAdam,
-    kKTexAdam, kKLoss
+    kKTexAdam, kKLossBlocks, kKLoss
 };
+
+uint32_t loss_tiles(const PbrDev& d) { return (d.S + kShadeTile - 1) / kShadeTile; }
+uint32_t loss_nside(const PbrDev& d) { return (loss_tiles(d) + 15u) / 16u; }
 
 uint32_t shade_blocks(const PbrDev& d) {
     const uint32_t tiles = (d.S + kShadeTile - 1) / kShadeTile;
@@ -1586,9 +1766,13 @@ int launch_pbr_kernel(const PbrDev& d, hipStream_t s, int k) {
             hipLaunchKernelGGL(k_pbr_tex_adam, dim3(div_up(d.tw * d.th, 256)), dim3(256), 0, s,
                                d);
             break;
+        case kKLossBlocks:
+            hipLaunchKernelGGL(k_pbr_loss_blocks,
+                               dim3(d.n_views * loss_nside(d) * loss_nside(d)), dim3(256), 0, s, d,
+                               loss_tiles(d));
+            break;
         default:
-            hipLaunchKernelGGL(k_pbr_loss, dim3(1), dim3(256), 0, s, d,
-                               (d.S + kShadeTile - 1) / kShadeTile);
+            hipLaunchKernelGGL(k_pbr_loss, dim3(1), dim3(256), 0, s, d, loss_nside(d));
             break;
     }
     DRESSI_CHECK_LAUNCH();
@@ -1661,10 +1845,10 @@ int pbr_enqueue(dressi_pbr_plan* p, hipStream_t s) {
 }
 
 // One iteration for graph capture: after the shading, the texture gather +
-// Adam runs on `side` beside the environment's chain (map gathers, tile and
-// view sums, transposed convolutions, env Adam): the two read and write
-// disjoint buffers (both only read t), and both join before the loss kernel
-// advances t.
+// Adam and the loss's block sums run on `side` beside the environment's chain
+// (map gathers, tile and view sums, transposed convolutions, env Adam): the
+// two read and write disjoint buffers (both only read t), and both join
+// before the loss kernel advances t.
 int pbr_enqueue_forked(dressi_pbr_plan* p, hipStream_t s, hipStream_t side, hipEvent_t fork,
                        hipEvent_t join) {
     for (int k : {kKPool, kKConvFwd, kKShade}) {
@@ -1673,6 +1857,7 @@ int pbr_enqueue_forked(dressi_pbr_plan* p, hipStream_t s, hipStream_t side, hipE
     DRESSI_TRY_HIP(hipEventRecord(fork, s));
     DRESSI_TRY_HIP(hipStreamWaitEvent(side, fork, 0));
     if (int rc = launch_pbr_kernel(p->d, side, kKTexAdam)) return rc;
+    if (int rc = launch_pbr_kernel(p->d, side, kKLossBlocks)) return rc;
     DRESSI_TRY_HIP(hipEventRecord(join, side));
     for (int k : {kKGather, kKTileSum, kKViewSum, kKConvBwd, kKEnvAdam}) {
         if (int rc = launch_pbr_kernel(p->d, s, k)) return rc;
@@ -1958,6 +2143,15 @@ int build_map_lists(dressi_pbr_plan* p) {
         };
         GatherItem cur{};
         uint32_t cur_max = 0;
+        uint64_t n_bmw = 0;  // bitmap words of the position-list workgroups
+        // chunks per workgroup: kGatherMaxChunks, or DRESSI_PBR_GATHER_CHUNKS
+        // (tests use 1 to take position lists at small sizes)
+        uint64_t max_chunks = kGatherMaxChunks;
+        if (const char* ev = getenv("DRESSI_PBR_GATHER_CHUNKS")) {
+            const long v = strtol(ev, nullptr, 10);
+            if (v >= 1 && v <= 4096) max_chunks = (uint64_t)v;
+        }
+        const uint64_t pos_cap = (uint64_t)kGatherChunk * max_chunks;
         const auto flush = [&]() {
             if (cur.na == 0) {
                 cur = GatherItem{};
@@ -1966,10 +2160,7 @@ int build_map_lists(dressi_pbr_plan* p) {
             }
             cur.P = kGatherChunk / cur.nb;
             cur.nch = (cur_max + cur.P - 1) / cur.P;
-            cur.c0 = (uint32_t)n_c;
-            cur.f0 = (uint32_t)n_fo;
-            n_c += (uint64_t)cur.nch * cur.na;
-            n_fo += (uint64_t)(cur.nch + 1) * cur.na;
+            cur.bmo = kBandMode;
             gi.push_back(cur);
             cur = GatherItem{};
             cur_max = 0;
@@ -1988,6 +2179,36 @@ int build_map_lists(dressi_pbr_plan* p) {
                     flush();  // a workgroup's bands are consecutive and non-empty
                     continue;
                 }
+                if ((uint64_t)npos > pos_cap) {
+                    // position-list workgroups: the band's buckets by texel
+                    // tile (at most kGatherTile^2 = kGatherChains each)
+                    flush();
+                    const uint32_t tx = (mi.w + kGatherTile - 1) / kGatherTile;
+                    const auto tile_of = [&](uint32_t b) {
+                        const uint32_t t = (b - mi.bucket0) % mi.T;
+                        return (t / mi.w) / kGatherTile * tx + (t % mi.w) / kGatherTile;
+                    };
+                    std::stable_sort(ord.begin() + first, ord.end(),
+                                     [&](uint32_t x, uint32_t y) { return tile_of(x) < tile_of(y); });
+                    for (uint32_t a = 0; a < n_here;) {
+                        uint32_t e = a + 1;
+                        while (e < n_here && tile_of(ord[first + e]) == tile_of(ord[first + a])) {
+                            e++;
+                        }
+                        GatherItem li{};
+                        li.m = m;
+                        li.vb0 = vb;
+                        li.nb = 1;
+                        li.P = kGatherChunk;
+                        li.a0 = first + a;
+                        li.na = e - a;
+                        li.bmo = (uint32_t)n_bmw;
+                        n_bmw += (npos + 31u) / 32u;
+                        gi.push_back(li);
+                        a = e;
+                    }
+                    continue;
+                }
                 if (n_here > kGatherChains) {
                     // a band of its own, split into workgroups of kGatherChains
                     flush();
@@ -2002,7 +2223,8 @@ int build_map_lists(dressi_pbr_plan* p) {
                     }
                     continue;
                 }
-                if (cur.na + n_here > kGatherChains || cur.nb == kGatherBands) {
+                if (cur.na + n_here > kGatherChains || cur.nb == kGatherBands ||
+                    (uint64_t)(cur.nb + 1) * std::max(cur_max, npos) > pos_cap) {
                     flush();
                 }
                 if (cur.na == 0) {
@@ -2016,6 +2238,91 @@ int build_map_lists(dressi_pbr_plan* p) {
             }
             flush();
         }
+        // position-list workgroups: bitmaps of the positions their entries
+        // read, the word prefixes, the lengths (to the host: they set nch)
+        // and the lists
+        void *bm = nullptr, *wpre = nullptr, *lgi = nullptr, *lnpl = nullptr, *plist = nullptr;
+        if (!rc) rc = salloc(&order, sizeof(uint32_t) * std::max<size_t>(ord.size(), 1));
+        if (!rc && hipMemcpy(order, ord.data(), sizeof(uint32_t) * ord.size(),
+                             hipMemcpyHostToDevice) != hipSuccess) {
+            set_error("map gather bucket order upload failed");
+            rc = DRESSI_ERR_HIP;
+        }
+        uint32_t max_na0 = 1;
+        for (const GatherItem& g : gi) max_na0 = std::max(max_na0, g.na);
+        if (!rc && n_bmw) {
+            std::vector<uint32_t> npl(gi.size(), 0);
+            rc = talloc(&bm, sizeof(uint32_t) * n_bmw);
+            if (!rc) rc = talloc(&wpre, sizeof(uint32_t) * n_bmw);
+            if (!rc) rc = talloc(&lgi, sizeof(GatherItem) * gi.size());
+            if (!rc) rc = talloc(&lnpl, sizeof(uint32_t) * gi.size());
+            hipError_t e = hipSuccess;
+            if (!rc) {
+                e = hipMemcpy(lgi, gi.data(), sizeof(GatherItem) * gi.size(),
+                              hipMemcpyHostToDevice);
+                if (e == hipSuccess) e = hipMemsetAsync(bm, 0, sizeof(uint32_t) * n_bmw, s);
+                if (e == hipSuccess) e = hipMemsetAsync(lnpl, 0, sizeof(uint32_t) * gi.size(), s);
+                if (e == hipSuccess) {
+                    hipLaunchKernelGGL(k_pbr_list_bits,
+                                       dim3(div_up(max_na0, 256), (uint32_t)gi.size()), dim3(256),
+                                       0, s, (const GatherItem*)lgi, (uint32_t)gi.size(),
+                                       (const MapInfo*)minfo, S, (const uint32_t*)bgbase,
+                                       (const uint32_t*)order, (const uint32_t*)off,
+                                       (const uint32_t*)ent, (uint32_t*)bm);
+                    e = hipGetLastError();
+                }
+                if (e == hipSuccess) {
+                    hipLaunchKernelGGL(k_pbr_list_count, dim3((uint32_t)gi.size()), dim3(256), 0,
+                                       s, (const GatherItem*)lgi, (uint32_t)gi.size(),
+                                       (const MapInfo*)minfo, S, (const uint32_t*)bgbase,
+                                       (const uint32_t*)bm, (uint32_t*)wpre, (uint32_t*)lnpl);
+                    e = hipGetLastError();
+                }
+                if (e == hipSuccess) e = hipMemcpyAsync(npl.data(), lnpl,
+                                                        sizeof(uint32_t) * gi.size(),
+                                                        hipMemcpyDeviceToHost, s);
+                if (e == hipSuccess) e = hipStreamSynchronize(s);
+            }
+            uint64_t n_pl = 0;
+            if (!rc && e == hipSuccess) {
+                for (size_t i = 0; i < gi.size(); i++) {
+                    if (gi[i].bmo == kBandMode) continue;
+                    gi[i].npl = npl[i];
+                    gi[i].pl0 = (uint32_t)n_pl;
+                    gi[i].nch = (npl[i] + gi[i].P - 1) / gi[i].P;
+                    n_pl += npl[i];
+                }
+                if (n_pl >= (1ull << 31)) {
+                    set_error("map gather position lists too long");
+                    rc = DRESSI_ERR_UNSUPPORTED;
+                }
+            }
+            if (!rc && e == hipSuccess) rc = salloc(&plist, sizeof(uint32_t) * n_pl);
+            if (!rc && e == hipSuccess) {
+                e = hipMemcpy(lgi, gi.data(), sizeof(GatherItem) * gi.size(),
+                              hipMemcpyHostToDevice);
+                if (e == hipSuccess) {
+                    hipLaunchKernelGGL(k_pbr_list_fill, dim3(16, (uint32_t)gi.size()), dim3(256), 0,
+                                       s, (const GatherItem*)lgi, (uint32_t)gi.size(),
+                                       (const MapInfo*)minfo, S, (const uint32_t*)bgbase,
+                                       (const uint32_t*)bgpix, (const uint32_t*)bm,
+                                       (const uint32_t*)wpre, (uint32_t*)plist);
+                    e = hipGetLastError();
+                }
+            }
+            if (!rc && e != hipSuccess) {
+                set_error("map gather position lists failed: %s", hipGetErrorString(e));
+                rc = DRESSI_ERR_HIP;
+            }
+        }
+        d.plist = (const uint32_t*)plist;
+        // chunk tables: per item (nch + 1) first entries and nch counts per bucket
+        for (GatherItem& g : gi) {
+            g.c0 = (uint32_t)n_c;
+            g.f0 = (uint32_t)n_fo;
+            n_c += (uint64_t)g.nch * g.na;
+            n_fo += (uint64_t)(g.nch + 1) * g.na;
+        }
         if (n_fo >= (1ull << 31)) {
             set_error("map gather chunk tables too large");
             rc = DRESSI_ERR_UNSUPPORTED;
@@ -2026,7 +2333,6 @@ int build_map_lists(dressi_pbr_plan* p) {
         uint32_t max_na = 1;
         for (const GatherItem& g : gi) max_na = std::max(max_na, g.na);
         void *fo = nullptr, *ccnt = nullptr, *cscr = nullptr;
-        if (!rc) rc = salloc(&order, sizeof(uint32_t) * std::max<size_t>(ord.size(), 1));
         if (!rc) rc = salloc(&gbuf, sizeof(GatherItem) * std::max<size_t>(gi.size(), 1));
         if (!rc) rc = salloc(&coff, sizeof(uint32_t) * (n_c + 1));
         if (!rc) rc = salloc(&ment, sizeof(uint16_t) * (total + 16));  // + the last 16-byte word
@@ -2034,10 +2340,8 @@ int build_map_lists(dressi_pbr_plan* p) {
         if (!rc) rc = talloc(&ccnt, sizeof(uint32_t) * (n_c + 1));
         size_t cs_bytes = 0;
         if (!rc) {
-            hipError_t e = hipMemcpy(order, ord.data(), sizeof(uint32_t) * ord.size(),
+            hipError_t e = hipMemcpy(gbuf, gi.data(), sizeof(GatherItem) * gi.size(),
                                      hipMemcpyHostToDevice);
-            if (e == hipSuccess) e = hipMemcpy(gbuf, gi.data(), sizeof(GatherItem) * gi.size(),
-                                               hipMemcpyHostToDevice);
             if (e == hipSuccess) e = hipMemset(part, 0, sizeof(float4) * nb);
             if (e == hipSuccess) e = hipMemset(tot, 0, sizeof(float4) * nt);
             if (e == hipSuccess) e = hipMemset((uint32_t*)ccnt + n_c, 0, sizeof(uint32_t));
@@ -2047,7 +2351,8 @@ int build_map_lists(dressi_pbr_plan* p) {
                                    s, (const GatherItem*)gbuf, (uint32_t)gi.size(),
                                    (const MapInfo*)minfo, S, (const uint32_t*)bgbase,
                                    (const uint32_t*)order, (const uint32_t*)off,
-                                   (const uint32_t*)ent, (uint32_t*)fo, (uint32_t*)ccnt);
+                                   (const uint32_t*)ent, (const uint32_t*)bm,
+                                   (const uint32_t*)wpre, (uint32_t*)fo, (uint32_t*)ccnt);
                 e = hipGetLastError();
             }
             if (e == hipSuccess) {
@@ -2066,6 +2371,7 @@ int build_map_lists(dressi_pbr_plan* p) {
                                    s, (const GatherItem*)gbuf, (uint32_t)gi.size(),
                                    (const MapInfo*)minfo, S, (const uint32_t*)bgbase,
                                    (const uint32_t*)order, (const uint32_t*)ent,
+                                   (const uint32_t*)bm, (const uint32_t*)wpre,
                                    (const uint32_t*)fo, (const uint32_t*)coff, (uint16_t*)ment);
                 e = hipGetLastError();
             }
@@ -2228,6 +2534,7 @@ int dressi_pbr_create(dressi_ctx* ctx, const dressi_pbr_desc* desc, dressi_pbr_p
     if (!rc) rc = pbr_alloc(p, &d.mgA, N * npx);
     if (!rc) rc = pbr_alloc(p, &d.mgB, N * npx);
     if (!rc) rc = pbr_alloc(p, &d.loss_part, shade_blocks(d));
+    if (!rc) rc = pbr_alloc(p, &d.loss_blk, (size_t)d.n_views * loss_nside(d) * loss_nside(d));
     if (!rc) rc = pbr_alloc(p, &d.loss, 1);
     if (!rc && (desc->flags & DRESSI_PBR_KEEP_PRED)) rc = pbr_alloc(p, &d.pred, N * npx);
     if (!rc && (desc->flags & DRESSI_PBR_KEEP_GRAD)) {
@@ -2275,8 +2582,8 @@ int dressi_pbr_create(dressi_ctx* ctx, const dressi_pbr_desc* desc, dressi_pbr_p
         if (!rc) rc = pbr_upload(p, &e, psdir);
         d.psdir = e;
         const uint32_t ni = d.iw * d.ih, nis = d.isw * d.ish, nps = d.psw * d.psh;
-        // tile-major, the column count rounded up to whole groups of 64
-        const auto cols = [](uint32_t n) { return (size_t)((n + 63u) & ~63u); };
+        // tile-major, the column count rounded up to whole groups of kMvCols
+        const auto cols = [](uint32_t n) { return (size_t)div_up(n, kMvCols) * kMvCols; };
         const size_t bfi = (size_t)nis * cols(ni), bbi = (size_t)ni * cols(nis);
         const size_t bfp = (size_t)nps * cols(d.n_pref), bbp = (size_t)d.n_pref * cols(nps);
         float *wfi = nullptr, *wbi = nullptr, *wfp = nullptr, *wbp = nullptr;

@@ -1835,7 +1835,7 @@ PbrRoute::~PbrRoute() = default;
 
 std::string PbrRoute::name() const { return "fused:pbr"; }
 
-size_t PbrRoute::kernels() const { return 10; }
+size_t PbrRoute::kernels() const { return 11; }
 
 std::unique_ptr<PbrRoute> PbrRoute::Recognise(const GraphRoots& g) {
     PbrParams p;

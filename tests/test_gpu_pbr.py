@@ -186,15 +186,22 @@ def test_pbr_plan_matches_reference_fixtures(ctx, golden, name):
     fit.close()
 
 
-@pytest.mark.parametrize("name", ["pbr_ico2_48px_2view_3it.npz", "pbr_ico3_96px_3view_2it.npz"])
-def test_pbr_plan_matches_oracle_bit_for_bit(ctx, oracle, golden, name):
+@pytest.mark.parametrize("name,chunks", [("pbr_ico2_48px_2view_3it.npz", None),
+                                         ("pbr_ico3_96px_3view_2it.npz", None),
+                                         ("pbr_ico3_96px_3view_2it.npz", "1")])
+def test_pbr_plan_matches_oracle_bit_for_bit(ctx, oracle, golden, monkeypatch, name, chunks):
     """The fused plan against the oracle's C5 fit (or_pbr_fit: the reference's
     per-pixel order, band partials + TileSum, view order, sequential
     convolutions, the C library's atan2f / acosf / powf) on the fixture
     scenes: target, prediction, the loss, first-iteration gradients and the
-    parameters after the fixture's iterations identical bit for bit."""
+    parameters after the fixture's iterations identical bit for bit. With
+    `chunks` = 1 the map gather takes per-tile position lists for every band
+    of more than 1024 positions (at 96 px: prefilter level 0 and the env),
+    as it does for the large bands at full size."""
     from opendressi_amd.pbr import PbrFit
     import opendressi_amd._lib as L
+    if chunks is not None:
+        monkeypatch.setenv("DRESSI_PBR_GATHER_CHUNKS", chunks)
     g = golden(name)
     iters = len(g["out_loss"])
     sc = _scene(g)
