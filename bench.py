@@ -517,6 +517,43 @@ def dressi_ad_point(name: str, naive: bool, steps: int, warmup: int) -> dict:
             "value": 1e3 / ms, "unit": "iterations/s", "ms_per_step": ms, "steps": steps}
 
 
+def peel_point(name: str, peels: int, iters: int, skip: int) -> dict:
+    """Median execStep wall time of the silhouette fit driven through the
+    DressiAD graph API (tests/graph_c1.cpp: the example's graph with `peels`
+    RasterizeSoft layers, run.cpp:302-343; each step uploads the clip images,
+    runs, and downloads the loss, as the reference example's loop does).
+    K = 1 runs on the fused plan (the route), K > 1 on the generic executor;
+    the reference reports K = 1 against K = 3 (docs/benchmarks.md:150-156)."""
+    import tempfile
+    import opendressi_amd as od
+    w = od.WORKLOADS[name]
+    pos, faces, tgt, mvps = od.make_scene(w)
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "_bin", "graph_c1")
+    if not os.path.exists(exe):
+        return {"error": "tests/_bin/graph_c1 is not built"}
+    nv, nf, n = len(pos), len(faces), len(mvps)
+    hdr = np.array([nv, nf, len(tgt), nf, n, w.screen, 8, iters, 0, 0, 0, peels, 0, 0],
+                   np.uint32)
+    with tempfile.TemporaryDirectory() as d:
+        inp, out = os.path.join(d, "in.bin"), os.path.join(d, "out.bin")
+        with open(inp, "wb") as f:
+            f.write(hdr.tobytes())
+            f.write(np.array([3.0, w.lr, 0.0, 0.0], np.float32).tobytes())
+            for a in (pos, faces, tgt, faces, mvps):
+                f.write(np.ascontiguousarray(a, np.float32).tobytes())
+        res = subprocess.run([exe, inp, out], capture_output=True, text=True, timeout=900)
+        if res.returncode != 0:
+            return {"error": res.stderr.strip()[-400:]}
+        ms = np.fromfile(out, np.float32)[-iters:]
+    info = dict(kv.split("=", 1) for kv in res.stdout.split() if "=" in kv)
+    med = float(np.median(ms[skip:]))
+    return {"workload": f"{name}: HardSoftRas K={peels} {w.screen}^2 x {w.views} views through "
+                        "DressiAD (median execStep, uploads included)",
+            "plan": info.get("plan"), "stages": int(info.get("stages", 0)),
+            "value": 1e3 / med, "unit": "iterations/s", "ms_per_step": med,
+            "steps": iters - skip}
+
+
 def reference_cpu_c1() -> dict:
     """The reference's own CPU evaluator (oracle/_ref: the reference's
     src/core built in place, BuildBackward + CpuEvaluator with DressiAD's
@@ -746,7 +783,9 @@ def main() -> int:
                                  "c4": metric_point("c4", 100, 10),
                                  "c5": metric_point("c5", 50, 5),
                                  "c3_dressi_ad": dressi_ad_point("c3", False, 30, 5),
-                                 "c3_dressi_ad_generic": dressi_ad_point("c3", True, 3, 2)}
+                                 "c3_dressi_ad_generic": dressi_ad_point("c3", True, 3, 2),
+                                 "c2_dressi_ad_k1": peel_point("c2", 1, 60, 10),
+                                 "c2_dressi_ad_k3": peel_point("c2", 3, 30, 10)}
     if args.torch_surface:
         line["torch_surface"] = torch_surface()
     if not args.no_cpu_baseline:

@@ -102,57 +102,94 @@ struct FProgram {
 __device__ __forceinline__ float std_min(float a, float b) { return b < a ? b : a; }
 __device__ __forceinline__ float std_max(float a, float b) { return a < b ? b : a; }
 
+// component i (0..3) of a 4-vector without run-time indexing (which would
+// place the array in private memory)
+__device__ __forceinline__ float sel4(const float (&a)[4], uint32_t i) {
+    return i == 0 ? a[0] : (i == 1 ? a[1] : (i == 2 ? a[2] : a[3]));
+}
+
 // one elementwise op on one pixel: `v[i][c]` = component c of input i
-// (1-component inputs replicated), the reference's CPU float semantics
-__device__ void ew_eval(Op op, uint32_t n_in, const uint32_t* nc, float (*v)[4], uint32_t ny,
-                        uint32_t a0, float* y) {
+// (1-component inputs replicated), the reference's CPU float semantics.
+// Every array index is a compile-time constant (unrolled loops with
+// predicates), so v and y stay in registers.
+__device__ __forceinline__ void ew_eval(Op op, uint32_t n_in, const uint32_t (&nc)[kMaxInputs],
+                                        const float (&v)[kMaxInputs][4], uint32_t ny,
+                                        uint32_t a0, float (&y)[4]) {
     switch (op) {
         case Op::kCompose: {
             uint32_t o = 0;
-            for (uint32_t i = 0; i < n_in; i++) {
-                for (uint32_t c = 0; c < nc[i]; c++) {
-                    y[o++] = v[i][c];
+#pragma unroll
+            for (uint32_t i = 0; i < kMaxInputs; i++) {
+#pragma unroll
+                for (uint32_t c = 0; c < 4; c++) {
+                    if (i < n_in && c < nc[i]) {
+#pragma unroll
+                        for (uint32_t j = 0; j < 4; j++) {
+                            if (o == j) {
+                                y[j] = v[i][c];
+                            }
+                        }
+                        o++;
+                    }
                 }
             }
             return;
         }
         case Op::kExtract:
-            for (uint32_t c = 0; c < ny; c++) {
-                y[c] = v[0][a0 + c];
+#pragma unroll
+            for (uint32_t c = 0; c < 4; c++) {
+                if (c < ny) {
+                    y[c] = sel4(v[0], a0 + c);
+                }
             }
             return;
         case Op::kDot: {
             float acc = 0.f;
-            for (uint32_t c = 0; c < nc[0]; c++) {
-                acc += v[0][c] * v[1][c];
+#pragma unroll
+            for (uint32_t c = 0; c < 4; c++) {
+                if (c < nc[0]) {
+                    acc += v[0][c] * v[1][c];
+                }
             }
             y[0] = acc;
             return;
         }
         case Op::kCompSum: {
             float acc = 0.f;
-            for (uint32_t c = 0; c < nc[0]; c++) {
-                acc += v[0][c];
+#pragma unroll
+            for (uint32_t c = 0; c < 4; c++) {
+                if (c < nc[0]) {
+                    acc += v[0][c];
+                }
             }
             y[0] = acc;
             return;
         }
         case Op::kLength: {
             float acc = 0.f;
-            for (uint32_t c = 0; c < nc[0]; c++) {
-                acc += v[0][c] * v[0][c];
+#pragma unroll
+            for (uint32_t c = 0; c < 4; c++) {
+                if (c < nc[0]) {
+                    acc += v[0][c] * v[0][c];
+                }
             }
             y[0] = sqrtf(acc);
             return;
         }
         case Op::kNormalize: {
             float acc = 0.f;
-            for (uint32_t c = 0; c < nc[0]; c++) {
-                acc += v[0][c] * v[0][c];
+#pragma unroll
+            for (uint32_t c = 0; c < 4; c++) {
+                if (c < nc[0]) {
+                    acc += v[0][c] * v[0][c];
+                }
             }
             const float inv = 1.f / sqrtf(acc);
-            for (uint32_t c = 0; c < ny; c++) {
-                y[c] = v[0][c] * inv;
+#pragma unroll
+            for (uint32_t c = 0; c < 4; c++) {
+                if (c < ny) {
+                    y[c] = v[0][c] * inv;
+                }
             }
             return;
         }
@@ -164,7 +201,11 @@ __device__ void ew_eval(Op op, uint32_t n_in, const uint32_t* nc, float (*v)[4],
         default:
             break;
     }
-    for (uint32_t c = 0; c < ny; c++) {
+#pragma unroll
+    for (uint32_t c = 0; c < 4; c++) {
+        if (c >= ny) {
+            continue;
+        }
         const float a = v[0][c];
         const float b = n_in > 1 ? v[1][c] : 0.f;
         const float t = n_in > 2 ? v[2][c] : 0.f;
@@ -212,8 +253,11 @@ __device__ void ew_eval(Op op, uint32_t n_in, const uint32_t* nc, float (*v)[4],
             case Op::kCopy: r = a; break;
             case Op::kSumPw: {
                 float acc = 0.f;
-                for (uint32_t i = 0; i < n_in; i++) {
-                    acc += v[i][c];
+#pragma unroll
+                for (uint32_t i = 0; i < kMaxInputs; i++) {
+                    if (i < n_in) {
+                        acc += v[i][c];
+                    }
                 }
                 r = acc;
                 break;
@@ -225,40 +269,59 @@ __device__ void ew_eval(Op op, uint32_t n_in, const uint32_t* nc, float (*v)[4],
 }
 
 // One fused stage: every thread runs the program on its pixel.
-__global__ __launch_bounds__(256) void k_fused(FProgram P) {
+// The program's registers live in LDS (P.n x kFusedThreads float4, a
+// thread's own slots only): indexed at run time they would otherwise be
+// private memory.
+constexpr uint32_t kFusedThreads = 64;
+__global__ __launch_bounds__(kFusedThreads) void k_fused(FProgram P) {
+    extern __shared__ float4 sreg[];  // [register][thread]
     const size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= P.n_px) {
         return;
     }
-    float reg[kMaxStepInstrs][4];
     for (uint32_t i = 0; i < P.n; i++) {
         const FInstr ins = P.code[i];
         float v[kMaxInputs][4];
         uint32_t nc[kMaxInputs];
-        for (uint32_t k = 0; k < ins.n_in; k++) {
+#pragma unroll
+        for (uint32_t k = 0; k < kMaxInputs; k++) {
+            nc[k] = 0;
+#pragma unroll
+            for (uint32_t c = 0; c < 4; c++) {
+                v[k][c] = 0.f;
+            }
+            if (k >= ins.n_in) {
+                continue;
+            }
             const FInput in = ins.in[k];
             nc[k] = in.nc;
-            const float* src = nullptr;
             if (in.src == kSrcReg) {
-                src = reg[in.idx];
-            } else if (in.src == kSrcBuf) {
-                src = P.bufs[in.idx] + (in.uniform ? 0 : p * in.nc);
+                const float4 r = sreg[in.idx * kFusedThreads + threadIdx.x];
+                const float rc[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+                for (uint32_t c = 0; c < 4; c++) {
+                    v[k][c] = sel4(rc, in.nc == 1 ? 0 : (c < in.nc ? c : 0));
+                }
             } else {
-                src = P.imm + in.idx;
-            }
-            for (uint32_t c = 0; c < 4; c++) {
-                v[k][c] = src[in.nc == 1 ? 0 : (c < in.nc ? c : 0)];
+                const float* src = in.src == kSrcBuf
+                                           ? P.bufs[in.idx] + (in.uniform ? 0 : p * in.nc)
+                                           : P.imm + in.idx;
+#pragma unroll
+                for (uint32_t c = 0; c < 4; c++) {
+                    v[k][c] = src[in.nc == 1 ? 0 : (c < in.nc ? c : 0)];
+                }
             }
         }
         float y[4] = {0.f, 0.f, 0.f, 0.f};
         ew_eval((Op)ins.op, ins.n_in, nc, v, ins.ny, ins.a0, y);
-        for (uint32_t c = 0; c < 4; c++) {
-            reg[i][c] = y[c];
-        }
+        sreg[i * kFusedThreads + threadIdx.x] = make_float4(y[0], y[1], y[2], y[3]);
         if (ins.out_slot >= 0) {
             float* dst = P.bufs[ins.out_slot] + p * ins.ny;
-            for (uint32_t c = 0; c < ins.ny; c++) {
-                dst[c] = y[c];
+#pragma unroll
+            for (uint32_t c = 0; c < 4; c++) {
+                if (c < ins.ny) {
+                    dst[c] = y[c];
+                }
             }
         }
     }
@@ -792,6 +855,33 @@ struct DressiAD::Impl {
         return r;
     }
 
+    // Clears the dirty flag of every leaf and of everything computed
+    // downstream of one: the result of setDirtyRecursively(false) on each
+    // leaf (src/dressi_ad.cpp:526-528) in one walk, so a node downstream of
+    // several leaves is visited once.
+    void clear_dirty() {
+        std::unordered_set<const VariableNode*> seen;
+        std::vector<VariableNode*> stack;
+        for (const auto& v : leaf_vars) {
+            stack.push_back(NodeAccess::Node(v).get());
+        }
+        while (!stack.empty()) {
+            VariableNode* n = stack.back();
+            stack.pop_back();
+            if (!n || !seen.insert(n).second) {
+                continue;
+            }
+            n->dirty = false;
+            for (const auto& wu : n->users) {
+                if (const auto u = wu.lock()) {
+                    if (const auto y = u->y.lock()) {
+                        stack.push_back(y.get());
+                    }
+                }
+            }
+        }
+    }
+
     std::set<uint64_t> dirty_leaf_ids() const {
         std::set<uint64_t> ids;
         for (const auto& v : leaf_vars) {
@@ -1160,7 +1250,8 @@ struct DressiAD::Impl {
         hipStream_t st = stream();
         if (s.fused) {
             FProgram P{s.d_code, (uint32_t)s.code.size(), s.n_px, s.d_bufs, s.d_imm};
-            hipLaunchKernelGGL(k_fused, dim3(blocks256(s.n_px)), dim3(256), 0, st, P);
+            hipLaunchKernelGGL(k_fused, dim3((uint32_t)((s.n_px + kFusedThreads - 1) / kFusedThreads)),
+                               dim3(kFusedThreads), sizeof(float4) * kFusedThreads * P.n, st, P);
             check_hip(hipGetLastError(), "fused stage launch");
             return;
         }
@@ -1875,9 +1966,7 @@ void DressiAD::execStep() {
     if (im.status != FINISHED) {
         im.prev_dirty = im.dirty_leaf_ids();
     }
-    for (auto& v : im.leaf_vars) {
-        v.setDirtyRecursively(false);
-    }
+    im.clear_dirty();
     im.status = FINISHED;
 }
 
