@@ -69,7 +69,7 @@ void check_hip(hipError_t e, const char* what) {
 
 // ---- fused elementwise stage ------------------------------------------------
 
-constexpr int kMaxStepInstrs = 48;  // registers of one fused program
+constexpr int kMaxStepInstrs = 48;  // instructions of one fused program
 constexpr int kMaxInputs = 4;
 
 // Where an instruction input comes from
@@ -88,12 +88,14 @@ struct FInstr {
     uint32_t ny;
     uint32_t a0;
     int out_slot;  // buffer slot to store to, -1: register only
+    uint32_t reg;  // register (LDS slot) of the result
     FInput in[kMaxInputs];
 };
 
 struct FProgram {
     const FInstr* code;
     uint32_t n;
+    uint32_t n_regs;  // LDS register slots
     size_t n_px;
     float* const* bufs;  // slot -> device buffer
     const float* imm;
@@ -269,9 +271,9 @@ __device__ __forceinline__ void ew_eval(Op op, uint32_t n_in, const uint32_t (&n
 }
 
 // One fused stage: every thread runs the program on its pixel.
-// The program's registers live in LDS (P.n x kFusedThreads float4, a
-// thread's own slots only): indexed at run time they would otherwise be
-// private memory.
+// The program's registers live in LDS (P.n_regs x kFusedThreads float4, a
+// thread's own slots only; slots reused once their value is dead): indexed
+// at run time they would otherwise be private memory.
 constexpr uint32_t kFusedThreads = 64;
 __global__ __launch_bounds__(kFusedThreads) void k_fused(FProgram P) {
     extern __shared__ float4 sreg[];  // [register][thread]
@@ -296,7 +298,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FProgram P) {
             const FInput in = ins.in[k];
             nc[k] = in.nc;
             if (in.src == kSrcReg) {
-                const float4 r = sreg[in.idx * kFusedThreads + threadIdx.x];
+                const float4 r = sreg[in.idx * kFusedThreads + threadIdx.x];  // slot
                 const float rc[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
                 for (uint32_t c = 0; c < 4; c++) {
@@ -314,7 +316,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FProgram P) {
         }
         float y[4] = {0.f, 0.f, 0.f, 0.f};
         ew_eval((Op)ins.op, ins.n_in, nc, v, ins.ny, ins.a0, y);
-        sreg[i * kFusedThreads + threadIdx.x] = make_float4(y[0], y[1], y[2], y[3]);
+        sreg[ins.reg * kFusedThreads + threadIdx.x] = make_float4(y[0], y[1], y[2], y[3]);
         if (ins.out_slot >= 0) {
             float* dst = P.bufs[ins.out_slot] + p * ins.ny;
 #pragma unroll
@@ -723,6 +725,7 @@ struct Step {
     float* d_imm = nullptr;
     float** d_bufs = nullptr;
     size_t n_px = 0;
+    uint32_t n_regs = 0;  // fused program: LDS register slots
     // the variables whose images this step writes
     std::vector<const VariableNode*> outs;
 };
@@ -1015,9 +1018,94 @@ struct DressiAD::Impl {
         return out;
     }
 
+    // A topological order for RSP fusion: constants first (a fused program
+    // reads them as immediates), then elementwise functions (pure, per
+    // pixel) as soon as their inputs exist, those of the current run's image
+    // size first, so that fewer runs break; every other function keeps its
+    // place in the original order relative to the others of its kind. Any
+    // topological order computes the same images.
+    static Functions fusion_order(const Functions& funcs) {
+        const size_t n = funcs.size();
+        std::unordered_map<const FunctionNode*, size_t> idx;
+        for (size_t i = 0; i < n; i++) {
+            idx[NodeAccess::Node(funcs[i]).get()] = i;
+        }
+        std::vector<uint32_t> waiting(n, 0);
+        std::vector<std::vector<size_t>> users(n);
+        std::vector<char> ew(n, 0);
+        std::vector<size_t> others, consts;  // non-elementwise, original order
+        for (size_t i = 0; i < n; i++) {
+            const auto& fn = NodeAccess::Node(funcs[i]);
+            const auto y = fn->y.lock();
+            ew[i] = IsElementwise(fn->op) && y && NumComponents(y->vtype) <= 4;
+            if (fn->op == Op::kConst) {
+                consts.push_back(i);
+            } else if (!ew[i]) {
+                others.push_back(i);
+            }
+            std::unordered_set<size_t> deps;
+            for (const auto& x : fn->xs) {
+                if (x->creator) {
+                    auto it = idx.find(x->creator.get());
+                    if (it != idx.end() && deps.insert(it->second).second) {
+                        users[it->second].push_back(i);
+                        waiting[i]++;
+                    }
+                }
+            }
+        }
+        Functions out;
+        out.reserve(n);
+        std::vector<size_t> ready_ew;  // kept in original order
+        std::vector<char> done(n, 0);
+        size_t next_other = 0;
+        ImgSize run_size{0, 0};
+        const auto emit = [&](size_t i) {
+            done[i] = 1;
+            out.push_back(funcs[i]);
+            for (size_t u : users[i]) {
+                if (--waiting[u] == 0 && ew[u]) {
+                    ready_ew.insert(std::upper_bound(ready_ew.begin(), ready_ew.end(), u), u);
+                }
+            }
+        };
+        for (size_t i = 0; i < n; i++) {
+            if (ew[i] && waiting[i] == 0) {
+                ready_ew.push_back(i);
+            }
+        }
+        for (size_t i : consts) {
+            emit(i);
+        }
+        while (out.size() < n) {
+            if (!ready_ew.empty()) {
+                // the earliest ready one of the current run's size, else the earliest
+                size_t pick = 0;
+                for (size_t k = 0; k < ready_ew.size(); k++) {
+                    const auto y = NodeAccess::Node(funcs[ready_ew[k]])->y.lock();
+                    if (y->size == run_size) {
+                        pick = k;
+                        break;
+                    }
+                }
+                const size_t i = ready_ew[pick];
+                ready_ew.erase(ready_ew.begin() + (ptrdiff_t)pick);
+                run_size = NodeAccess::Node(funcs[i])->y.lock()->size;
+                emit(i);
+                continue;
+            }
+            DRESSI_CHECK(next_other < others.size() && waiting[others[next_other]] == 0,
+                         "fusion order: the function graph is not acyclic");
+            run_size = ImgSize{0, 0};
+            emit(others[next_other++]);
+        }
+        return out;
+    }
+
     // variables that must have an image: roots, copy-back sources and every
     // input of a step other than the one that produces it
-    void pack(const Functions& funcs) {
+    void pack(const Functions& funcs_in) {
+        const Functions funcs = packing == PackingMode::RSP ? fusion_order(funcs_in) : funcs_in;
         release_graph();
         release_steps(packed);
         std::unordered_set<const VariableNode*> must_store;
@@ -1216,6 +1304,47 @@ struct DressiAD::Impl {
             s.code.push_back(ins);
             s.n_px = (size_t)y->size.w * y->size.h;
         }
+        // registers: each result gets the lowest slot free when it is written
+        // (a value is free after its last reader, which reads its inputs
+        // before writing)
+        {
+            const uint32_t n = (uint32_t)s.code.size();
+            std::vector<uint32_t> last(n, 0);
+            for (uint32_t i = 0; i < n; i++) {
+                last[i] = i;
+                for (uint32_t k = 0; k < s.code[i].n_in; k++) {
+                    if (s.code[i].in[k].src == kSrcReg) {
+                        last[s.code[i].in[k].idx] = i;
+                    }
+                }
+            }
+            std::vector<uint32_t> slot_of_reg(n, 0);
+            std::vector<int> holder;  // slot -> instruction holding it, -1 free
+            for (uint32_t i = 0; i < n; i++) {
+                for (size_t q = 0; q < holder.size(); q++) {
+                    if (holder[q] >= 0 && last[(uint32_t)holder[q]] <= i) {
+                        holder[q] = -1;
+                    }
+                }
+                for (uint32_t k = 0; k < s.code[i].n_in; k++) {
+                    FInput& in = s.code[i].in[k];
+                    if (in.src == kSrcReg) {
+                        in.idx = slot_of_reg[in.idx];
+                    }
+                }
+                size_t q = 0;
+                while (q < holder.size() && holder[q] >= 0) {
+                    q++;
+                }
+                if (q == holder.size()) {
+                    holder.push_back(-1);
+                }
+                holder[q] = (int)i;
+                slot_of_reg[i] = (uint32_t)q;
+                s.code[i].reg = (uint32_t)q;
+            }
+            s.n_regs = (uint32_t)std::max<size_t>(holder.size(), 1);
+        }
         if (s.imm.empty()) {
             s.imm.push_back(0.f);
         }
@@ -1249,9 +1378,10 @@ struct DressiAD::Impl {
     void run_step(const Step& s) {
         hipStream_t st = stream();
         if (s.fused) {
-            FProgram P{s.d_code, (uint32_t)s.code.size(), s.n_px, s.d_bufs, s.d_imm};
+            FProgram P{s.d_code, (uint32_t)s.code.size(), s.n_regs, s.n_px, s.d_bufs, s.d_imm};
             hipLaunchKernelGGL(k_fused, dim3((uint32_t)((s.n_px + kFusedThreads - 1) / kFusedThreads)),
-                               dim3(kFusedThreads), sizeof(float4) * kFusedThreads * P.n, st, P);
+                               dim3(kFusedThreads), sizeof(float4) * kFusedThreads * P.n_regs, st,
+                               P);
             check_hip(hipGetLastError(), "fused stage launch");
             return;
         }
