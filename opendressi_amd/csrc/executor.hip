@@ -281,8 +281,25 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FProgram P) {
     if (p >= P.n_px) {
         return;
     }
+    // the program and the buffer table are the same for every lane: read
+    // through the constant address space (scalar loads)
+    typedef const __attribute__((address_space(4))) uint32_t* UniformWords;
+    typedef const __attribute__((address_space(4))) uint64_t* UniformPtrs;
+    const auto buf_at = [&](uint32_t k) {
+        return (float*)((UniformPtrs)P.bufs)[k];
+    };
     for (uint32_t i = 0; i < P.n; i++) {
-        const FInstr ins = P.code[i];
+        constexpr int kWords = (int)(sizeof(FInstr) / 4);
+        union {
+            FInstr f;
+            uint32_t w[kWords];
+        } u;
+        const UniformWords src = (UniformWords)(P.code + i);
+#pragma unroll
+        for (int k = 0; k < kWords; k++) {
+            u.w[k] = src[k];
+        }
+        const FInstr ins = u.f;
         float v[kMaxInputs][4];
         uint32_t nc[kMaxInputs];
 #pragma unroll
@@ -306,7 +323,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FProgram P) {
                 }
             } else {
                 const float* src = in.src == kSrcBuf
-                                           ? P.bufs[in.idx] + (in.uniform ? 0 : p * in.nc)
+                                           ? buf_at(in.idx) + (in.uniform ? 0 : p * in.nc)
                                            : P.imm + in.idx;
 #pragma unroll
                 for (uint32_t c = 0; c < 4; c++) {
@@ -318,7 +335,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FProgram P) {
         ew_eval((Op)ins.op, ins.n_in, nc, v, ins.ny, ins.a0, y);
         sreg[ins.reg * kFusedThreads + threadIdx.x] = make_float4(y[0], y[1], y[2], y[3]);
         if (ins.out_slot >= 0) {
-            float* dst = P.bufs[ins.out_slot] + p * ins.ny;
+            float* dst = buf_at((uint32_t)ins.out_slot) + p * ins.ny;
 #pragma unroll
             for (uint32_t c = 0; c < 4; c++) {
                 if (c < ins.ny) {
