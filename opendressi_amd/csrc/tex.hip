@@ -5,6 +5,7 @@
 // src/core/mesh_utils.cpp:180-203, examples/texture_optimization/run.cpp:
 // 112-145).
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -494,15 +495,19 @@ constexpr int kTexStage = 1024;  // tent keys of one view staged in LDS per wave
 // (the +-4 dilation for uncovered texels), the 7 x 7 window in row order.
 // A window pixel can weigh the texel only when its tent key names it (every
 // pixel whose exact weight can be > 0 does): the keys of the union of the
-// wave's windows are staged in LDS when they fit, the candidates collected
-// as window bits, and their g_uv / gradient loaded four at a time, the
-// weights then added in window order. The views' contributions are summed
+// wave's windows are staged in LDS when they fit, and each staged pixel sets
+// its window bit in the masks of the (at most four) texels of the block its
+// key names whose window holds it (else each texel scans its window); the
+// candidates' g_uv / gradient are then loaded four at a time and the weights
+// added in window order. The views' contributions are summed
 // newest first through the <= 4-ary tree, then Adam on the
 // RGBA texel at step t + 1 (t_next, published by k_tex_clip); the first
 // thread stores t + 1.
 template <int NV>
 __global__ __launch_bounds__(64) void k_tex_bwd_adam(TexDev d) {
     __shared__ uint32_t lk[kTexStage];
+    __shared__ int lsx[64], lsy[64];              // the texels' window centres (INT_MIN: none)
+    __shared__ unsigned long long lcm[64];        // the texels' candidate window bits
     const int lane = (int)threadIdx.x;
     const int tw = d.tw, th = d.th;
     const int sw = (int)d.r.g.width, sh = (int)d.r.g.height;
@@ -569,7 +574,42 @@ __global__ __launch_bounds__(64) void k_tex_bwd_adam(TexDev d) {
         }
         // candidate window positions (bit (dy + 3) * 7 + dx + 3)
         uint64_t cm = 0;
-        if (act) {
+        if (staged) {
+            lsx[lane] = act ? scx : INT_MIN;
+            lsy[lane] = scy;
+            lcm[lane] = 0ull;
+            __syncthreads();
+            const int bx0 = (int)(blockIdx.x % (uint32_t)bxn) * 8;
+            const int by0 = (int)(blockIdx.x / (uint32_t)bxn) * 8;
+            for (int i = lane; i < bw * bh; i += 64) {
+                const int ry = i / bw;
+                const int px = x0 + i - ry * bw, py = y0 + ry;
+                const uint32_t k = lk[i];
+                const int kx = (int)(k & 0xffffu), ky = (int)(k >> 16);
+#pragma unroll
+                for (int dy = 0; dy < 2; dy++) {
+#pragma unroll
+                    for (int dx = 0; dx < 2; dx++) {
+                        // texel (kx - 1 + dx, ky - 1 + dy): tx + 1 - kx in {0, 1}
+                        const int lx = kx - 1 + dx - bx0, ly = ky - 1 + dy - by0;
+                        if (lx < 0 || lx >= 8 || ly < 0 || ly >= 8) {
+                            continue;
+                        }
+                        const int t = ly * 8 + lx;
+                        const int cx = lsx[t];
+                        if (cx == INT_MIN) {
+                            continue;
+                        }
+                        const int wx = px - cx + 3, wy = py - lsy[t] + 3;
+                        if (wx >= 0 && wx < 7 && wy >= 0 && wy < 7) {
+                            atomicOr(&lcm[t], 1ull << (wy * 7 + wx));
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            cm = act ? (uint64_t)lcm[lane] : 0ull;
+        } else if (act) {
 #pragma unroll
             for (int r = 0; r < 7; r++) {
                 const int spy = scy + r - 3;
