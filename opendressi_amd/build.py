@@ -74,7 +74,7 @@ def build(verbose: bool = False) -> str:
             f.result()
     tmp = LIB + ".tmp"
     _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, *host_objs,
-          "-lz"], verbose, "libdressi_hip.so")
+          "-lz", "-lhiprtc"], verbose, "libdressi_hip.so")
     os.replace(tmp, LIB)
     return LIB
 

@@ -26,12 +26,21 @@
 //
 // A graph recognised as the reference's silhouette-fit example (HardSoftRas
 // or AA) or as the texture fit (see route.h) runs on its fused plan instead.
+#include <dlfcn.h>
 #include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <fstream>
+#include <functional>
 #include <map>
+#include <mutex>
+#include <sstream>
+#include <string>
 #include <set>
 #include <unordered_map>
 #include <unordered_set>
@@ -731,6 +740,355 @@ namespace {
 
 // One launch group of the iteration: a fused elementwise program or one
 // function through its kernel / entry point.
+// ---- compiled fused programs ---------------------------------------------
+// A fused program can also be compiled at run time (hipRTC) into a kernel
+// of straight-line code: the same operations in the same order as ew_eval,
+// the same device math (libc_expf, libm::*), built with the library's own
+// floating-point flags, so its results are the interpreter's bit for bit.
+// Programs are compiled per device, all new ones of a packing in one unit,
+// and cached for the process by their text. Any failure falls back to the
+// interpreter (as does DRESSI_NO_JIT=1).
+
+std::string f32_lit(float v) {
+    uint32_t u;
+    std::memcpy(&u, &v, 4);
+    char b[64];
+    snprintf(b, sizeof b, "__builtin_bit_cast(float, 0x%08xu)", u);
+    return b;
+}
+
+// The statements of one program: r<i>_<c> = component c of instruction i's
+// result; B[k] the program's buffer table; p the pixel.
+std::string jit_body(const std::vector<FInstr>& code, const std::vector<float>& imm,
+                     bool* uses_libm) {
+    std::ostringstream o;
+    *uses_libm = false;
+    for (size_t i = 0; i < code.size(); i++) {
+        const FInstr& ins = code[i];
+        const Op op = (Op)ins.op;
+        // operand component c of input k
+        auto v = [&](uint32_t k, uint32_t c) -> std::string {
+            const FInput& in = ins.in[k];
+            const uint32_t ci = in.nc == 1 ? 0 : (c < in.nc ? c : 0);
+            std::ostringstream e;
+            if (in.src == kSrcReg) {
+                e << "r" << in.idx << "_" << ci;
+            } else if (in.src == kSrcBuf) {
+                if (in.uniform) {
+                    e << "B[" << in.idx << "][" << ci << "]";
+                } else {
+                    e << "B[" << in.idx << "][p * " << in.nc << "ull + " << ci << "]";
+                }
+            } else {
+                e << f32_lit(imm[in.idx + ci]);
+            }
+            return e.str();
+        };
+        std::string y[4] = {"0.f", "0.f", "0.f", "0.f"};
+        o << "float r" << i << "_0, r" << i << "_1, r" << i << "_2, r" << i << "_3;\n{\n";
+        auto acc_loop = [&](const std::string& init, uint32_t n,
+                            const std::function<std::string(uint32_t)>& term) {
+            o << "float acc = " << init << ";\n";
+            for (uint32_t c = 0; c < n; c++) {
+                o << "acc += " << term(c) << ";\n";
+            }
+        };
+        switch (op) {
+            case Op::kCompose: {
+                uint32_t q = 0;
+                for (uint32_t k = 0; k < ins.n_in; k++) {
+                    for (uint32_t c = 0; c < ins.in[k].nc && q < 4; c++) {
+                        y[q++] = v(k, c);
+                    }
+                }
+                break;
+            }
+            case Op::kExtract:
+                for (uint32_t c = 0; c < ins.ny && c < 4; c++) {
+                    y[c] = v(0, std::min<uint32_t>(ins.a0 + c, 3));
+                }
+                break;
+            case Op::kDot:
+                acc_loop("0.f", ins.in[0].nc,
+                         [&](uint32_t c) { return v(0, c) + " * " + v(1, c); });
+                y[0] = "acc";
+                break;
+            case Op::kCompSum:
+                acc_loop("0.f", ins.in[0].nc, [&](uint32_t c) { return v(0, c); });
+                y[0] = "acc";
+                break;
+            case Op::kLength:
+                acc_loop("0.f", ins.in[0].nc,
+                         [&](uint32_t c) { return v(0, c) + " * " + v(0, c); });
+                y[0] = "sqrtf(acc)";
+                break;
+            case Op::kNormalize:
+                acc_loop("0.f", ins.in[0].nc,
+                         [&](uint32_t c) { return v(0, c) + " * " + v(0, c); });
+                o << "const float inv = 1.f / sqrtf(acc);\n";
+                for (uint32_t c = 0; c < ins.ny && c < 4; c++) {
+                    y[c] = v(0, c) + " * inv";
+                }
+                break;
+            case Op::kCross:
+                y[0] = v(0, 1) + " * " + v(1, 2) + " - " + v(0, 2) + " * " + v(1, 1);
+                y[1] = v(0, 2) + " * " + v(1, 0) + " - " + v(0, 0) + " * " + v(1, 2);
+                y[2] = v(0, 0) + " * " + v(1, 1) + " - " + v(0, 1) + " * " + v(1, 0);
+                break;
+            default:
+                for (uint32_t c = 0; c < ins.ny && c < 4; c++) {
+                    const std::string a = "(" + v(0, c) + ")";
+                    const std::string b = ins.n_in > 1 ? "(" + v(1, c) + ")" : "0.f";
+                    const std::string t = ins.n_in > 2 ? "(" + v(2, c) + ")" : "0.f";
+                    std::string r;
+                    switch (op) {
+                        case Op::kAdd: r = a + " + " + b; break;
+                        case Op::kSub: r = a + " - " + b; break;
+                        case Op::kMul: r = a + " * " + b; break;
+                        case Op::kDiv: r = a + " / " + b; break;
+                        case Op::kNeg: r = "-" + a; break;
+                        case Op::kSin: r = "sinf" + a; break;
+                        case Op::kCos: r = "cosf" + a; break;
+                        case Op::kTan: r = "tanf" + a; break;
+                        case Op::kAsin: r = "asinf" + a; break;
+                        case Op::kAcos: r = "dressi::libm::acosf" + a; *uses_libm = true; break;
+                        case Op::kAtan: r = "dressi::libm::atanf" + a; *uses_libm = true; break;
+                        case Op::kAtan2:
+                            r = "dressi::libm::atan2f(" + a + ", " + b + ")";
+                            *uses_libm = true;
+                            break;
+                        case Op::kExp: r = "dressi::libc_expf" + a; break;
+                        case Op::kExp2: r = "exp2f" + a; break;
+                        case Op::kLog: r = "logf" + a; break;
+                        case Op::kLog2: r = "log2f" + a; break;
+                        case Op::kSqrt: r = "sqrtf" + a; break;
+                        case Op::kInvSqrt: r = "1.f / sqrtf" + a; break;
+                        case Op::kAbs: r = "fabsf" + a; break;
+                        case Op::kSign: r = "(float)((" + a + " > 0.f) - (" + a + " < 0.f))"; break;
+                        case Op::kFloor: r = "floorf" + a; break;
+                        case Op::kFract: r = a + " - floorf" + a; break;
+                        case Op::kMod: r = a + " - " + b + " * floorf(" + a + " / " + b + ")"; break;
+                        case Op::kPow:
+                            r = "((" + b + " == 5.f && " + a + " >= 0.f && " + a +
+                                " <= 1.f) ? dressi::libm::pow5f(" + a + ") : powf(" + a + ", " +
+                                b + "))";
+                            *uses_libm = true;
+                            break;
+                        case Op::kMax: r = "jit_max(" + a + ", " + b + ")"; break;
+                        case Op::kMin: r = "jit_min(" + a + ", " + b + ")"; break;
+                        case Op::kClamp: r = "jit_min(jit_max(" + a + ", " + b + "), " + t + ")"; break;
+                        case Op::kMix: r = a + " + (" + b + " - " + a + ") * " + t; break;
+                        case Op::kStep: r = "(" + b + " < " + a + " ? 0.f : 1.f)"; break;
+                        case Op::kSmoothStep:
+                            r = "jit_smooth(" + a + ", " + b + ", " + t + ")";
+                            break;
+                        case Op::kSigmoid: r = "1.f / (1.f + dressi::libc_expf(-" + a + "))"; break;
+                        case Op::kLess: r = "(float)(" + a + " < " + b + ")"; break;
+                        case Op::kLessEq: r = "(float)(" + a + " <= " + b + ")"; break;
+                        case Op::kGreater: r = "(float)(" + a + " > " + b + ")"; break;
+                        case Op::kGreaterEq: r = "(float)(" + a + " >= " + b + ")"; break;
+                        case Op::kCopy: r = a; break;
+                        case Op::kSumPw: {
+                            o << "float s" << c << " = 0.f;\n";
+                            for (uint32_t k = 0; k < ins.n_in; k++) {
+                                o << "s" << c << " += " << v(k, c) << ";\n";
+                            }
+                            r = "s" + std::to_string(c);
+                            break;
+                        }
+                        default: return std::string();  // not compiled: interpreted
+                    }
+                    y[c] = r;
+                }
+                break;
+        }
+        for (uint32_t c = 0; c < 4; c++) {
+            o << "r" << i << "_" << c << " = " << (c < ins.ny ? y[c] : std::string("0.f"))
+              << ";\n";
+        }
+        o << "}\n";
+        if (ins.out_slot >= 0) {
+            for (uint32_t c = 0; c < ins.ny && c < 4; c++) {
+                o << "B[" << ins.out_slot << "][p * " << ins.ny << "ull + " << c << "] = r" << i
+                  << "_" << c << ";\n";
+            }
+        }
+    }
+    return o.str();
+}
+
+std::string read_text(const std::string& path) {
+    std::ifstream f(path);
+    if (!f) {
+        return std::string();
+    }
+    std::stringstream s;
+    s << f.rdbuf();
+    return s.str();
+}
+
+// the library's csrc directory (the headers the programs include)
+std::string csrc_dir() {
+    Dl_info info{};
+    if (!dladdr((void*)&csrc_dir, &info) || !info.dli_fname) {
+        return std::string();
+    }
+    std::string p = info.dli_fname;
+    const size_t k = p.find_last_of('/');
+    return (k == std::string::npos ? std::string(".") : p.substr(0, k)) + "/csrc/";
+}
+
+struct JitCache {
+    std::mutex mu;
+    std::map<std::pair<int, std::string>, hipFunction_t> fns;  // (device, body)
+    bool disabled = false;
+};
+
+JitCache& jit_cache() {
+    static JitCache c;
+    return c;
+}
+
+bool jit_enabled() {
+    const char* e = getenv("DRESSI_NO_JIT");
+    return !(e && e[0] && e[0] != '0');
+}
+
+// Compiles the steps' new programs for `device` in one unit; sets jit_fn of
+// every step whose program is compiled (cached or new).
+template <typename StepT>
+void jit_compile(std::vector<StepT>& steps, int device) {
+    if (!jit_enabled()) {
+        return;
+    }
+    JitCache& jc = jit_cache();
+    std::lock_guard<std::mutex> lock(jc.mu);
+    if (jc.disabled) {
+        return;
+    }
+    std::map<std::string, std::string> todo;  // body -> kernel name
+    bool libm = false;
+    for (auto& s : steps) {
+        if (s.jit_body.empty()) {
+            continue;
+        }
+        auto it = jc.fns.find({device, s.jit_body});
+        if (it != jc.fns.end()) {
+            s.jit_fn = it->second;
+            continue;
+        }
+        if (!todo.count(s.jit_body)) {
+            const std::string name = "dressi_fp_" + std::to_string(todo.size());
+            todo.emplace(s.jit_body, name);
+        }
+        libm = libm || s.jit_body.find("dressi::libm::") != std::string::npos;
+    }
+    if (todo.empty()) {
+        return;
+    }
+    const std::string dir = csrc_dir();
+    std::vector<std::string> names = {"dressi_math.h", "hip/hip_runtime.h", "stdint.h", "cstdint"};
+    const std::string stdint_stub =
+            "#pragma once\nusing __hip_internal::uint8_t; using __hip_internal::uint16_t; "
+            "using __hip_internal::uint32_t; using __hip_internal::uint64_t; "
+            "using __hip_internal::int8_t; using __hip_internal::int16_t; "
+            "using __hip_internal::int32_t; using __hip_internal::int64_t;\n";
+    std::vector<std::string> texts = {read_text(dir + "dressi_math.h"), "#pragma once\n",
+                                      stdint_stub, stdint_stub};
+    if (libm) {
+        names.push_back("libm_f32.h");
+        texts.push_back(read_text(dir + "libm_f32.h"));
+        names.push_back("libm_pow5_table.h");
+        texts.push_back(read_text(dir + "libm_pow5_table.h"));
+    }
+    for (size_t i = 0; i < texts.size(); i++) {
+        if (texts[i].empty()) {
+            fprintf(stderr, "dressi: run-time compilation off (no %s in %s)\n", names[i].c_str(),
+                    dir.c_str());
+            jc.disabled = true;
+            return;
+        }
+    }
+    std::ostringstream src;
+    src << "#include \"dressi_math.h\"\n";
+    if (libm) {
+        src << "#include \"libm_f32.h\"\n";
+    }
+    src << "__device__ __forceinline__ float jit_min(float a, float b) { return b < a ? b : a; }\n"
+           "__device__ __forceinline__ float jit_max(float a, float b) { return a < b ? b : a; }\n"
+           "__device__ __forceinline__ float jit_smooth(float a, float b, float t) {\n"
+           "    const float s = jit_min(jit_max((t - a) / (b - a), 0.f), 1.f);\n"
+           "    return s * s * (3.f - 2.f * s);\n}\n";
+    for (const auto& [body, name] : todo) {
+        src << "extern \"C\" __global__ void __launch_bounds__(256) " << name
+            << "(float* const* __restrict__ B, unsigned long long n) {\n"
+               "const unsigned long long p = (unsigned long long)blockIdx.x * 256ull + threadIdx.x;\n"
+               "if (p >= n) return;\n"
+            << body << "}\n";
+    }
+    const std::string text = src.str();
+    std::vector<const char*> hn, ht;
+    for (size_t i = 0; i < names.size(); i++) {
+        hn.push_back(names[i].c_str());
+        ht.push_back(texts[i].c_str());
+    }
+    hipDeviceProp_t prop{};
+    std::string arch = "--offload-arch=gfx950";
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.gcnArchName[0]) {
+        std::string a = prop.gcnArchName;
+        arch = "--offload-arch=" + a.substr(0, a.find(':'));
+    }
+    const char* opts[] = {arch.c_str(), "-O3", "-std=c++17", "-ffp-contract=off",
+                          "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang",
+                          "-target-feature", "-Xclang", "-packed-fp32-ops"};
+    hiprtcProgram prog = nullptr;
+    bool ok = hiprtcCreateProgram(&prog, text.c_str(), "dressi_fused.hip", (int)names.size(),
+                                  ht.data(), hn.data()) == HIPRTC_SUCCESS;
+    ok = ok && hiprtcCompileProgram(prog, (int)(sizeof(opts) / sizeof(opts[0])), opts) ==
+                       HIPRTC_SUCCESS;
+    std::vector<char> code;
+    if (ok) {
+        size_t n = 0;
+        ok = hiprtcGetCodeSize(prog, &n) == HIPRTC_SUCCESS && n > 0;
+        code.resize(n);
+        ok = ok && hiprtcGetCode(prog, code.data()) == HIPRTC_SUCCESS;
+    } else if (prog) {
+        size_t n = 0;
+        hiprtcGetProgramLogSize(prog, &n);
+        std::string log(n, '\0');
+        hiprtcGetProgramLog(prog, &log[0]);
+        fprintf(stderr, "dressi: run-time compilation failed, fused programs interpreted:\n%s\n",
+                log.substr(0, 2000).c_str());
+    }
+    if (prog) {
+        hiprtcDestroyProgram(&prog);
+    }
+    hipModule_t mod = nullptr;
+    ok = ok && hipModuleLoadData(&mod, code.data()) == hipSuccess;
+    if (!ok) {
+        hipGetLastError();
+        jc.disabled = true;
+        return;
+    }
+    for (const auto& [body, name] : todo) {
+        hipFunction_t f = nullptr;
+        if (hipModuleGetFunction(&f, mod, name.c_str()) != hipSuccess) {
+            hipGetLastError();
+            jc.disabled = true;
+            return;
+        }
+        jc.fns[{device, body}] = f;
+    }
+    for (auto& s : steps) {
+        if (!s.jit_body.empty() && !s.jit_fn) {
+            auto it = jc.fns.find({device, s.jit_body});
+            if (it != jc.fns.end()) {
+                s.jit_fn = it->second;
+            }
+        }
+    }
+}
+
 struct Step {
     bool fused = false;
     std::vector<std::shared_ptr<FunctionNode>> fns;  // in order
@@ -743,6 +1101,8 @@ struct Step {
     float** d_bufs = nullptr;
     size_t n_px = 0;
     uint32_t n_regs = 0;  // fused program: LDS register slots
+    std::string jit_body;          // fused program as HIP statements (empty: interpreted)
+    hipFunction_t jit_fn = nullptr;  // its compiled kernel
     // the variables whose images this step writes
     std::vector<const VariableNode*> outs;
 };
@@ -1257,6 +1617,7 @@ struct DressiAD::Impl {
                 compile_fused(s);
             }
         }
+        jit_compile(steps, ctx()->device);
         for (const auto& [upd, inp] : copy_backs) {
             buf(upd);
             buf(inp);
@@ -1320,6 +1681,13 @@ struct DressiAD::Impl {
             reg_of[y.get()] = i;
             s.code.push_back(ins);
             s.n_px = (size_t)y->size.w * y->size.h;
+        }
+        // the program as straight-line code for run-time compilation (SSA:
+        // instruction indices, before the interpreter's slot reuse)
+        {
+            bool lm = false;
+            s.jit_body = jit_body(s.code, s.imm, &lm);
+            s.jit_fn = nullptr;
         }
         // registers: each result gets the lowest slot free when it is written
         // (a value is free after its last reader, which reads its inputs
@@ -1394,6 +1762,15 @@ struct DressiAD::Impl {
 
     void run_step(const Step& s) {
         hipStream_t st = stream();
+        if (s.fused && s.jit_fn) {
+            float** bufs = s.d_bufs;
+            unsigned long long n = s.n_px;
+            void* args[] = {&bufs, &n};
+            check_hip(hipModuleLaunchKernel(s.jit_fn, (uint32_t)((s.n_px + 255) / 256), 1, 1, 256, 1,
+                                            1, 0, st, args, nullptr),
+                      "compiled fused stage launch");
+            return;
+        }
         if (s.fused) {
             FProgram P{s.d_code, (uint32_t)s.code.size(), s.n_regs, s.n_px, s.d_bufs, s.d_imm};
             hipLaunchKernelGGL(k_fused, dim3((uint32_t)((s.n_px + kFusedThreads - 1) / kFusedThreads)),

@@ -33,7 +33,7 @@ GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 def _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, radius, lr, aa=False,
                naive=False, regs=False, w_lap=0.0, w_nrm=0.0, peels=1, no_rebuild=False,
-               regrow=False, timeout=120):
+               regrow=False, timeout=120, env=None):
     nv, nf, n = len(pos), len(faces), len(mvps)
     hdr = np.array([nv, nf, len(tgt), nf, n, screen, samples, iters, 1 if aa else 0,
                     1 if naive else 0, 1 if regs else 0, peels, 1 if no_rebuild else 0,
@@ -48,7 +48,7 @@ def _run_graph(tmp_path, pos, faces, tgt, mvps, screen, samples, iters, radius, 
     if not os.path.exists(EXE):
         pytest.fail("tests/_bin/graph_c1 is not built (run __graft_entry__.build())")
     res = subprocess.run([EXE, str(inp), str(out)], capture_output=True, text=True,
-                         timeout=timeout)
+                         timeout=timeout, env=None if env is None else {**os.environ, **env})
     print(res.stdout.strip(), res.stderr.strip(), flush=True)
     assert res.returncode == 0, res.stderr
     m = re.search(r"plan=(\S+) stages=(\d+) substages=(\d+) funcs=(\d+)", res.stdout)
@@ -194,6 +194,28 @@ def test_depth_peels_through_dressi_ad(tmp_path, peels):
     one = _run_graph(tmp_path, gold["in_pos"], gold["in_faces"], gold["in_tgt_pos"],
                      gold["in_mvps"], screen, 8, 1, 3.0, 1e-3, peels=1)
     assert not np.array_equal(one["grad0"], g["grad0"])  # the extra layers count
+
+
+def test_compiled_fused_programs_match_the_interpreter(tmp_path):
+    """The generic executor's fused elementwise programs compiled at run time
+    (hipRTC, the default) and interpreted (DRESSI_NO_JIT=1) give the same
+    floats: the two-peel example graph (sigmoids, square roots, divisions,
+    minima, steps) over 12 iterations, through both reactive rebuilds."""
+    with np.load(os.path.join(GOLDEN, "hsr_peel2_ico3_2view_96px_3it.npz")) as z:
+        gold = {k: z[k] for k in z.files}
+    screen = int(gold["in_cfg"][0])
+    print(f"[graph] compiled vs interpreted fused programs: 2 peels, {screen}px, 12 iterations",
+          flush=True)
+    runs = []
+    for env in ({}, {"DRESSI_NO_JIT": "1"}):
+        d = tmp_path / ("jit" if not env else "interp")
+        d.mkdir()
+        runs.append(_run_graph(d, gold["in_pos"], gold["in_faces"], gold["in_tgt_pos"],
+                               gold["in_mvps"], screen, 8, 12, 3.0, 1e-3, peels=2, env=env))
+    a, b = runs
+    assert a["plan"] == b["plan"] == "generic"
+    for k in ("pos", "m", "v", "loss", "grad0", "pred", "target"):
+        assert np.array_equal(a[k], b[k]), k
 
 
 def test_reactive_cache_prunes_static_branches(tmp_path, oracle):
