@@ -71,6 +71,8 @@ constexpr uint32_t kMvCols = 32;          // ordered mat-vec: columns per workgr
 constexpr uint32_t kGatherChunk = 1024;  // map gather: positions staged per round
 constexpr uint32_t kGatherChains = 256;   // map gather: buckets per workgroup (1 per thread)
 constexpr uint32_t kGatherBands = 64;     // map gather: bands per workgroup
+// map gather: a workgroup's cost per chunk in units of one sequential entry
+constexpr uint32_t kGatherChunkCost = 163;
 constexpr uint32_t kGatherMaxChunks = 32;  // map gather: position chunks per workgroup (bands
                                           // with more positions take position lists)
 constexpr uint32_t kGatherTile = 16;      // map gather: texel tile of a position-list workgroup
@@ -2376,6 +2378,37 @@ int build_map_lists(dressi_pbr_plan* p) {
                 e = hipGetLastError();
             }
             if (e == hipSuccess) e = hipStreamSynchronize(s);
+            // dispatch order: the longest workgroups first. A workgroup's
+            // time is close to kGatherChunkCost per chunk (staging and
+            // synchronisation) plus one unit per entry of each chunk's
+            // longest bucket (its lanes wait for the longest sequential
+            // sum): measured on the 1024^2 x 6-view fit, 6.0 us per chunk
+            // and 37 ns per entry.
+            std::vector<uint32_t> hc(n_c);
+            if (e == hipSuccess && n_c) {
+                e = hipMemcpy(hc.data(), ccnt, sizeof(uint32_t) * n_c, hipMemcpyDeviceToHost);
+            }
+            if (e == hipSuccess && !gi.empty()) {
+                std::vector<uint64_t> cost(gi.size());
+                for (size_t i = 0; i < gi.size(); i++) {
+                    const GatherItem& g = gi[i];
+                    uint64_t t = (uint64_t)kGatherChunkCost * g.nch;
+                    for (uint32_t c = 0; c < g.nch; c++) {
+                        const uint32_t* q = hc.data() + g.c0 + (size_t)c * g.na;
+                        t += *std::max_element(q, q + g.na);
+                    }
+                    cost[i] = t;
+                }
+                std::vector<uint32_t> idx(gi.size());
+                for (uint32_t i = 0; i < (uint32_t)gi.size(); i++) idx[i] = i;
+                std::stable_sort(idx.begin(), idx.end(),
+                                 [&](uint32_t x, uint32_t y) { return cost[x] > cost[y]; });
+                std::vector<GatherItem> sorted(gi.size());
+                for (size_t i = 0; i < gi.size(); i++) sorted[i] = gi[idx[i]];
+                gi.swap(sorted);
+                e = hipMemcpy(gbuf, gi.data(), sizeof(GatherItem) * gi.size(),
+                              hipMemcpyHostToDevice);
+            }
             if (e != hipSuccess) {
                 set_error("map gather work set-up failed: %s", hipGetErrorString(e));
                 rc = DRESSI_ERR_HIP;
