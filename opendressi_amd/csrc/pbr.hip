@@ -1314,23 +1314,50 @@ __global__ __launch_bounds__(256) void k_pbr_map_gather(PbrDev d) {
         if (c + 1 < nch) {  // chunk c + 1's loads, in flight while this chunk is summed
             DRESSI_GATHER_FETCH(c + 1u)
         }
-        for (; x + 8u <= x1; x += 8u) {
-            float c0[8], c1[8], c2[8];
+        if (x + 8u <= x1) {
+            // batches of 8 entries, software-pipelined: the next batch's LDS
+            // reads are in flight while this batch's products are added in
+            // order
+            float w[8];
+            float4 g[8];
 #pragma unroll
             for (uint32_t r = 0; r < 8; r++) {
                 const uint32_t e = se[x + r];
-                const float w = sw[e];
-                const float4 g = sg[e >> 2];
-                c0[r] = g.x * w;
-                c1[r] = g.y * w;
-                c2[r] = g.z * w;
+                w[r] = sw[e];
+                g[r] = sg[e >> 2];
+            }
+            for (; x + 16u <= x1; x += 8u) {
+                uint32_t en[8];
+#pragma unroll
+                for (uint32_t r = 0; r < 8; r++) {
+                    en[r] = se[x + 8u + r];
+                }
+                float c0[8], c1[8], c2[8];
+#pragma unroll
+                for (uint32_t r = 0; r < 8; r++) {
+                    c0[r] = g[r].x * w[r];
+                    c1[r] = g[r].y * w[r];
+                    c2[r] = g[r].z * w[r];
+                }
+#pragma unroll
+                for (uint32_t r = 0; r < 8; r++) {
+                    w[r] = sw[en[r]];
+                    g[r] = sg[en[r] >> 2];
+                }
+#pragma unroll
+                for (uint32_t r = 0; r < 8; r++) {
+                    a0 += c0[r];
+                    a1 += c1[r];
+                    a2 += c2[r];
+                }
             }
 #pragma unroll
             for (uint32_t r = 0; r < 8; r++) {
-                a0 += c0[r];
-                a1 += c1[r];
-                a2 += c2[r];
+                a0 += g[r].x * w[r];
+                a1 += g[r].y * w[r];
+                a2 += g[r].z * w[r];
             }
+            x += 8u;
         }
         for (; x + 4u <= x1; x += 4u) {
             float c0[4], c1[4], c2[4];
