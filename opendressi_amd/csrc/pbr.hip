@@ -1234,35 +1234,44 @@ __global__ __launch_bounds__(256) void k_pbr_map_gather(PbrDev d) {
     bool rv[kPer];
     uint4 rw0, rw1, rw2;
     uint32_t rx0 = 0, rx1 = 0, ra0 = 0;
+    // one chunk further ahead: the positions' pixel indices (from the
+    // position list or the background list) and the chunk's entry run, so
+    // that a chunk's loads depend on no load of their own
+    uint32_t pq[kPer];
+    bool pv[kPer];
+    uint32_t prun0 = 0, prun1 = 0;
+#define DRESSI_GATHER_PRE(CC)                                                                    \
+    {                                                                                            \
+        const uint32_t cp_ = (CC);                                                               \
+        _Pragma("unroll") for (uint32_t r = 0; r < kPer; r++) {                                  \
+            const uint32_t u = tid + 256u * r;                                                   \
+            const uint32_t bi = r == 0 ? sbi0 : (r == 1 ? sbi1 : (r == 2 ? sbi2 : sbi3));       \
+            const uint32_t pos = cp_ * P + (u - bi * P);                                         \
+            if (listed) {                                                                        \
+                pv[r] = pos < it.npl;                                                            \
+                pq[r] = pv[r] ? d.plist[it.pl0 + pos] : 0u;                                      \
+            } else {                                                                             \
+                pv[r] = u < nslot && pos < bnpos[bi];                                            \
+                pq[r] = pv[r] ? bvpx[bi] + (mi.kind == 2 ? d.bg_pix[bbase[bi] + pos]             \
+                                                         : bbase[bi] + pos)                      \
+                              : 0u;                                                              \
+            }                                                                                    \
+        }                                                                                        \
+        prun0 = coff[cp_ * it.na];                                                               \
+        prun1 = coff[(cp_ + 1) * it.na]; /* the next block's first: the end */                   \
+    }
 #define DRESSI_GATHER_FETCH(CC)                                                                  \
     {                                                                                            \
         const uint32_t cc_ = (CC);                                                               \
         _Pragma("unroll") for (uint32_t r = 0; r < kPer; r++) {                                  \
-            const uint32_t u = tid + 256u * r;                                                   \
-            const uint32_t bi = r == 0 ? sbi0 : (r == 1 ? sbi1 : (r == 2 ? sbi2 : sbi3));       \
-            const uint32_t pos = cc_ * P + (u - bi * P);                                         \
-            if (listed) {                                                                        \
-                rv[r] = pos < it.npl;                                                            \
-                if (rv[r]) {                                                                     \
-                    const uint32_t q = d.plist[it.pl0 + pos];                                    \
-                    rs[r] = uvsrc[q];                                                            \
-                    rg[r] = gsrc[q];                                                             \
-                }                                                                                \
-            } else {                                                                             \
-                rv[r] = u < nslot && pos < bnpos[bi];                                            \
-                if (rv[r]) {                                                                     \
-                    const size_t q =                                                             \
-                            (size_t)bvpx[bi] +                                                   \
-                            (mi.kind == 2 ? d.bg_pix[bbase[bi] + pos] : bbase[bi] + pos);        \
-                    rs[r] = uvsrc[q];                                                            \
-                    rg[r] = gsrc[q];                                                             \
-                }                                                                                \
+            rv[r] = pv[r];                                                                       \
+            if (rv[r]) {                                                                         \
+                rs[r] = uvsrc[pq[r]];                                                            \
+                rg[r] = gsrc[pq[r]];                                                             \
             }                                                                                    \
         }                                                                                        \
-        const uint32_t run0_ = coff[cc_ * it.na];                                                \
-        const uint32_t run1_ = coff[(cc_ + 1) * it.na]; /* the next block's first: the end */   \
-        ra0 = run0_ & ~7u;                                                                       \
-        const uint32_t nw_ = (run1_ - ra0 + 7u) / 8u;                                            \
+        ra0 = prun0 & ~7u;                                                                       \
+        const uint32_t nw_ = (prun1 - ra0 + 7u) / 8u;                                            \
         const uint4* src_ = (const uint4*)(d.mg_ent + ra0);                                      \
         const uint4 z4_ = make_uint4(0u, 0u, 0u, 0u);                                            \
         rw0 = tid < nw_ ? src_[tid] : z4_;                                                       \
@@ -1270,9 +1279,13 @@ __global__ __launch_bounds__(256) void k_pbr_map_gather(PbrDev d) {
         rw2 = tid + 512u < nw_ ? src_[tid + 512u] : z4_;                                         \
         rx0 = mine ? coff[cc_ * it.na + tid] : 0u;                                               \
         rx1 = mine ? coff[cc_ * it.na + tid + 1] : 0u;                                           \
+        if (cc_ + 1 < nch) {                                                                     \
+            DRESSI_GATHER_PRE(cc_ + 1u)                                                          \
+        }                                                                                        \
     }
     float a0 = 0.f, a1 = 0.f, a2 = 0.f;
     if (nch > 0) {
+        DRESSI_GATHER_PRE(0u)
         DRESSI_GATHER_FETCH(0u)
     }
     for (uint32_t c = 0; c < nch; c++) {
@@ -1387,6 +1400,7 @@ __global__ __launch_bounds__(256) void k_pbr_map_gather(PbrDev d) {
         }
     }
 #undef DRESSI_GATHER_FETCH
+#undef DRESSI_GATHER_PRE
     if (mine) {
         const uint32_t b = d.ml_order[it.a0 + tid];
         const float4 res = make_float4(a0, a1, a2, 0.f);
