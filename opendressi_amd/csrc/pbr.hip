@@ -1443,7 +1443,22 @@ __global__ __launch_bounds__(256) void k_pbr_tile_sum(PbrDev d) {
         }
         __syncthreads();
         if (threadIdx.x < cnt) {
-            for (uint32_t band = 0; band < nb; band++) {
+            // eight bands' LDS reads in flight, then added in band order
+            uint32_t band = 0;
+            for (; band + 8u <= nb; band += 8u) {
+                float4 q[8];
+#pragma unroll
+                for (uint32_t u = 0; u < 8; u++) {
+                    q[u] = buf[(band + u) * cnt + threadIdx.x];
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < 8; u++) {
+                    a0 += q[u].x;
+                    a1 += q[u].y;
+                    a2 += q[u].z;
+                }
+            }
+            for (; band < nb; band++) {
                 const float4 q = buf[band * cnt + threadIdx.x];
                 a0 += q.x;
                 a1 += q.y;
@@ -2458,11 +2473,14 @@ int build_map_lists(dressi_pbr_plan* p) {
     }
     for (void* q : tmp) hipFree(q);
     if (rc) return rc;
-    // tile sums: per map with k > 1, per view, runs of <= 256 texels
+    // tile sums: per map with k > 1, per view, runs of <= 256 texels, short
+    // enough that a workgroup stages its k bands in about two rounds (a
+    // round's loads are a round trip; maps with many bands take short runs)
     std::vector<uint4> wk;
     for (uint32_t m = 0; m < n_maps; m++) {
         if (mis[m].k == 1) continue;
-        const uint32_t run = std::min<uint32_t>(mis[m].T, 256u);
+        const uint32_t fit = std::max<uint32_t>(8u, 2u * kTileSumLds / mis[m].k);
+        const uint32_t run = std::min<uint32_t>({mis[m].T, 256u, fit});
         for (uint32_t v = 0; v < N; v++) {
             for (uint32_t t0 = 0; t0 < mis[m].T; t0 += run) {
                 wk.push_back(make_uint4(m, v, t0, std::min(run, mis[m].T - t0)));
