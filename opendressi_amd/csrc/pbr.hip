@@ -1216,7 +1216,9 @@ __global__ __launch_bounds__(256) void k_pbr_map_gather(PbrDev d) {
     __syncthreads();
     const float fw = (float)mi.w, fh = (float)mi.h;
     const float lod_scale = (float)(d.levels - 1), lvl = (float)mi.level;
-    const float4* uvsrc = mi.kind == 2 ? d.st0 : d.st2;
+    // the map's uv pair of a position: st0.xy (background env), st2.xy
+    // (irradiance) or st2.zw (prefilter levels)
+    const float2* uvsrc = (const float2*)(mi.kind == 2 ? d.st0 : d.st2) + (mi.kind == 1 ? 1 : 0);
     const float4* gsrc = mi.kind == 1 ? d.mgB : d.mgA;
     const uint32_t nch = it.nch, P = it.P, nslot = it.nb * it.P;
     const uint32_t* coff = d.coff + it.c0;
@@ -1230,7 +1232,8 @@ __global__ __launch_bounds__(256) void k_pbr_map_gather(PbrDev d) {
     sbi3 = tid + 768u < nslot ? (tid + 768u) / P : 0u;
     static_assert(kPer == 4, "four position slots per thread");
     // chunk data in flight: positions, entry words, this bucket's entry range
-    float4 rs[kPer], rg[kPer];
+    float2 rs[kPer];
+    float4 rg[kPer];
     bool rv[kPer];
     uint4 rw0, rw1, rw2;
     uint32_t rx0 = 0, rx1 = 0, ra0 = 0;
@@ -1266,7 +1269,7 @@ __global__ __launch_bounds__(256) void k_pbr_map_gather(PbrDev d) {
         _Pragma("unroll") for (uint32_t r = 0; r < kPer; r++) {                                  \
             rv[r] = pv[r];                                                                       \
             if (rv[r]) {                                                                         \
-                rs[r] = uvsrc[pq[r]];                                                            \
+                rs[r] = uvsrc[2u * pq[r]];                                                       \
                 rg[r] = gsrc[pq[r]];                                                             \
             }                                                                                    \
         }                                                                                        \
@@ -1294,10 +1297,10 @@ __global__ __launch_bounds__(256) void k_pbr_map_gather(PbrDev d) {
         for (uint32_t r = 0; r < kPer; r++) {
             if (rv[r]) {
                 const uint32_t u = tid + 256u * r;
-                const float4 st = rs[r];
+                const float2 st = rs[r];
                 const float4 g = rg[r];
-                const float uu = mi.kind == 1 ? st.z : st.x;
-                const float vv = mi.kind == 1 ? st.w : st.y;
+                const float uu = st.x;
+                const float vv = st.y;
                 const float sx = uu * fw - 0.5f;
                 const float sy = vv * fh - 0.5f;
                 const float fx = sx - floorf(sx);
