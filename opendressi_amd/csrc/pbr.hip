@@ -854,6 +854,86 @@ __device__ float mv_segment(MvLds& L, const float* __restrict__ Wg,
     return acc;
 }
 
+// Adds rows [i0, i1) of tile b to acc (lane's column, channel c) in row
+// order, 16 rows' LDS reads in flight where the rows are 4-aligned.
+__device__ __forceinline__ void mv_rows(const MvLds& L, int b, uint32_t c, uint32_t lane,
+                                        uint32_t i0, uint32_t i1, float& acc) {
+    const float* xs = L.x[b][c];
+    uint32_t i = i0;
+    for (; i < i1 && (i & 3u); i++) {
+        acc += xs[i] * L.w[b][i][lane];
+    }
+    for (; i + 16 <= i1; i += 16) {
+        float wv[16], xv[16];
+#pragma unroll
+        for (uint32_t u = 0; u < 16; u += 4) {
+            const float4 q = *(const float4*)&xs[i + u];
+            xv[u] = q.x;
+            xv[u + 1] = q.y;
+            xv[u + 2] = q.z;
+            xv[u + 3] = q.w;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 16; u++) {
+            wv[u] = L.w[b][i + u][lane];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 16; u++) {
+            acc += xv[u] * wv[u];
+        }
+    }
+    for (; i < i1; i++) {
+        acc += xs[i] * L.w[b][i][lane];
+    }
+}
+
+// The prefilter transpose's per-level sums in one tile stream: rows [0, n)
+// are the levels' texels, level-major (level i ends at lend(i)); each
+// level's sum runs from 0 in row order and is added to `a` times st at the
+// level's end, in level order -- the sums of one mv_segment per level, with
+// the next level's first tile in flight while the previous level ends.
+__device__ float mv_levels(MvLds& L, const float* __restrict__ Wg, const float4* __restrict__ x,
+                           const PbrDev& d, float st) {
+    const uint32_t lane = (threadIdx.x & 63u) % kMvCols;
+    const uint32_t c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n = d.n_pref;
+    const uint32_t tiles = (n + kMvRows - 1) / kMvRows;
+    const auto lend = [&](uint32_t i) { return d.loff[i] + d.lw[i] * d.lh[i]; };
+    MvRegs g;
+    mv_fetch(Wg, x, 0u, n < kMvRows ? n : kMvRows, g);
+    mv_store(L, 0, g);
+    __syncthreads();
+    float a = 0.f, acc = 0.f;
+    uint32_t lvl = 0, le = lend(0);
+    for (uint32_t t = 0; t < tiles; t++) {
+        const uint32_t base = t * kMvRows;
+        const uint32_t rows = n - base < kMvRows ? n - base : kMvRows;
+        const bool next = t + 1 < tiles;
+        if (next) {
+            const uint32_t rest = n - base - kMvRows;
+            mv_fetch(Wg, x, base + kMvRows, rest < kMvRows ? rest : kMvRows, g);
+        }
+        const int b = (int)(t & 1u);
+        uint32_t i = 0;
+        while (i < rows) {
+            const uint32_t e = le - base < rows ? le - base : rows;
+            mv_rows(L, b, c, lane, i, e, acc);
+            i = e;
+            if (base + i == le) {
+                a += acc * st;
+                acc = 0.f;
+                lvl++;
+                le = lvl < d.levels ? lend(lvl) : 0xffffffffu;
+            }
+        }
+        if (next) {
+            mv_store(L, b ^ 1, g);
+        }
+        __syncthreads();
+    }
+    return a;
+}
+
 // IrradianceConv and every PrefilterConv level (f_ops.cpp:3006-3087,
 // 3264-3348): out[o] = (sum_s e[s] * w(o, s)) * 2 pi / (sw sh) for the
 // irradiance map, (sum_s e[s] * w(o, s)) / max(norm[o], 1e-12) for a
@@ -1535,12 +1615,7 @@ __global__ __launch_bounds__(192) void k_pbr_conv_bwd(PbrDev d) {
         return;
     }
     const float st = d.psdir[ok ? s : 0u].w;
-    float a = 0.f;
-    for (uint32_t i = 0; i < d.levels; i++) {
-        const float t = mv_segment(L, d.wb_pref + (size_t)col0 * d.n_pref, d.g_pref, d.loff[i],
-                                   d.loff[i] + d.lw[i] * d.lh[i]);
-        a += t * st;
-    }
+    const float a = mv_levels(L, d.wb_pref + (size_t)col0 * d.n_pref, d.g_pref, d, st);
     if (ok) {
         ((float*)d.g_psrc)[(size_t)s * 4 + c] = a;
     }
