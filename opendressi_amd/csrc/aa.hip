@@ -440,9 +440,11 @@ __global__ __launch_bounds__(256) void k_aa_setup(HsrDev d) {
     if (live) {
         const float W = (float)d.g.width, H = (float)d.g.height;
         bool ok = true;
+        float iw[3];
 #pragma unroll
         for (int k = 0; k < 3; k++) {
             const float4 c = d.clip[(size_t)view * d.n_verts + d.faces[f * 3 + k]];
+            iw[k] = 1.f / c.w;
             ok = ok && !(fabsf(c.w) <= kWEps || c.w < 0.f);
             const ScreenVert s = project_to_screen(c.x, c.y, c.z, c.w, W, H);
             r.x[k] = s.x;
@@ -477,6 +479,15 @@ __global__ __launch_bounds__(256) void k_aa_setup(HsrDev d) {
             }
         }
         d.arecs[i] = r;
+        if (d.tface) {
+            const float2 a0 = d.tf_uv[d.faces[f * 3 + 0]];
+            const float2 a1 = d.tf_uv[d.faces[f * 3 + 1]];
+            const float2 a2 = d.tf_uv[d.faces[f * 3 + 2]];
+            float4* tf = d.tface + (size_t)i * 3;
+            tf[0] = make_float4(iw[0], iw[1], iw[2], 0.f);
+            tf[1] = make_float4(a0.x, a0.y, a1.x, a1.y);
+            tf[2] = make_float4(a2.x, a2.y, 0.f, 0.f);
+        }
     }
     const bool valid = live && r.bx0 <= r.bx1 && r.by0 <= r.by1;
     BinTri t;

@@ -96,6 +96,12 @@ struct HsrDev {
     uint32_t technique;       // 0 HardSoftRas, 1 AA
     float4* clip;             // [N][V]
     AaRec* arecs;             // [N][F]
+    // texture plan: per (view, face) the attribute corners of the screen
+    // raster's perspective-correct interpolation, written by the AA setup:
+    // (1 / w0, 1 / w1, 1 / w2, 0), (u0, v0, u1, v1), (u2, v2, 0, 0); null
+    // elsewhere
+    const float2* tf_uv;      // [V] uv of the vertices
+    float4* tface;            // [N][F][3]
     uint32_t* aa_list;        // [N * F] faces with a sample where d loss / d pred != 0
     uint32_t* aa_count;       // entries of aa_list (reset by the clip kernel)
     // the largest bin count above bins.cap this iteration: the kernels that

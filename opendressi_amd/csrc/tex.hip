@@ -410,18 +410,20 @@ __global__ __launch_bounds__(64 * NV) void k_tex_fwd(TexDev d) {
         float u = 0.f, v = 0.f, mask = 0.f;
         if (id) {
             const uint32_t f = id - 1;
-            const AaRec& rec = d.r.arecs[(size_t)view * d.r.g.n_faces + f];
+            const size_t vf = (size_t)view * d.r.g.n_faces + f;
+            const AaRec& rec = d.r.arecs[vf];
+            // the face's 1 / w and uv corners, beside its record (AA setup)
+            const float4 t0 = d.r.tface[vf * 3], t1 = d.r.tface[vf * 3 + 1],
+                         t2 = d.r.tface[vf * 3 + 2];
             float l0, l1, l2;
             barycentric((float)x + 0.5f, (float)y + 0.5f, rec.x[0], rec.y[0], rec.x[1], rec.y[1],
                         rec.x[2], rec.y[2], rec.inv_area, &l0, &l1, &l2);
-            const float4* clip = d.r.clip + (size_t)view * d.r.n_verts;
-            const int32_t i0 = d.r.faces[f * 3 + 0], i1 = d.r.faces[f * 3 + 1],
-                          i2 = d.r.faces[f * 3 + 2];
-            const float lw0 = l0 * (1.f / clip[i0].w);
-            const float lw1 = l1 * (1.f / clip[i1].w);
-            const float lw2 = l2 * (1.f / clip[i2].w);
+            const float lw0 = l0 * t0.x;
+            const float lw1 = l1 * t0.y;
+            const float lw2 = l2 * t0.z;
             const float denom = lw0 + lw1 + lw2;
-            const float2 a0 = d.uv[i0], a1 = d.uv[i1], a2 = d.uv[i2];
+            const float2 a0 = make_float2(t1.x, t1.y), a1 = make_float2(t1.z, t1.w),
+                         a2 = make_float2(t2.x, t2.y);
             float nu = 0.f, nvv = 0.f, nm = 0.f;
             nu += lw0 * a0.x;
             nu += lw1 * a1.x;
@@ -1011,6 +1013,7 @@ int dressi_tex_create(dressi_ctx* ctx, const dressi_tex_desc* desc, dressi_tex_p
     rc = rc ? rc : tex_alloc(p, &d.loss, npx);
     rc = rc ? rc : tex_alloc(p, &r.clip, N * V);
     rc = rc ? rc : tex_alloc(p, &r.arecs, std::max(N * F, F));
+    rc = rc ? rc : tex_alloc(p, &r.tface, (size_t)N * F * 3);
     rc = rc ? rc : tex_alloc(p, &r.ids, std::max(N * npx, T));
     if (!rc && (desc->flags & DRESSI_TEX_KEEP_IMAGES)) {
         rc = tex_alloc(p, &d.pred, N * npx);
@@ -1019,6 +1022,7 @@ int dressi_tex_create(dressi_ctx* ctx, const dressi_tex_desc* desc, dressi_tex_p
     if (!rc && (desc->flags & DRESSI_TEX_KEEP_GRAD)) rc = tex_alloc(p, &d.grad, T);
     d.pos = pos;
     d.uv = uv;
+    r.tf_uv = uv;
     d.mvps = mvps;
     d.texel = texel;
     d.gt = gt;
@@ -1109,6 +1113,7 @@ int dressi_tex_set_mesh(dressi_tex_plan* p, const float* pos, const float* uv,
     // the UV-space raster (static): UvAsClip positions in the clip buffer,
     // one "view" of T x T, the bins carved for its tiles
     HsrDev u = d.r;
+    u.tface = nullptr;  // the attribute corners are the screen raster's
     u.g = make_geom(p->desc.tex_w, p->desc.tex_h, 1, F);
     fixed_bin_carve(p->bin_mem, u.g.n_tiles, kSoftBinCap, &u.bins);
     DRESSI_TRY_HIP(hipMemcpyAsync(u.clip, uvc.data(), uvc.size() * 4, hipMemcpyHostToDevice, s));
