@@ -834,11 +834,14 @@ __global__ __launch_bounds__(64 * NV) void k_aa_fwd(HsrDev d) {
         }
     }
     float l[4] = {0.f, 0.f, 0.f, 0.f};
+    bool gnz = false;  // a pixel of the lane has the face scan's gy != 0
     if (any) {
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const float diff = tg[c] - pred[c];
             l[c] = diff * diff * d.inv_px;
+            const float cd = d.inv_px * diff;
+            gnz = gnz || (x0 + c < w && -(cd + cd) != 0.f);
         }
         float* pd = d.pred + view * npx;
         if (VEC) {
@@ -852,6 +855,7 @@ __global__ __launch_bounds__(64 * NV) void k_aa_fwd(HsrDev d) {
             }
         }
     }
+    const bool seg_nz = __ballot(gnz) != 0ull;
     lv[view][lane] = make_float4(l[0], l[1], l[2], l[3]);
     __syncthreads();
     if (view == 0 && any) {
@@ -878,6 +882,9 @@ __global__ __launch_bounds__(64 * NV) void k_aa_fwd(HsrDev d) {
                 }
             }
         }
+    }
+    if (lane == 0 && d.gflag) {
+        d.gflag[((size_t)view * h + y) * gridDim.x + blockIdx.x] = seg_nz ? 1u : 0u;
     }
 }
 
@@ -1060,7 +1067,10 @@ __global__ __launch_bounds__(256) void k_aa_face_scan(HsrDev d) {
             for (uint32_t smp = (uint32_t)j; smp < d.n_samples && !act; smp += 8) {
                 int sx = -1, sy = -1;
                 if (aa_sample_px(s3x, s3y, f, smp, seed_u, &sx, &sy) && sx >= 0 && sy >= 0 &&
-                    sx < w && sy < h) {
+                    sx < w && sy < h &&
+                    (!d.gflag ||
+                     d.gflag[((size_t)view * h + sy) * (uint32_t)((w + 255) / 256) + sx / 256])) {
+                    // a segment without the flag has gy = 0 at every pixel
                     const size_t so = (size_t)sy * w + sx;
                     const float diff = tgt[so] - pred[so];
                     const float cd = d.inv_px * diff;

@@ -1039,6 +1039,7 @@ int dressi_hsr_create(dressi_ctx* ctx, const dressi_hsr_desc* desc, dressi_hsr_p
     } else {
         rc = rc ? rc : plan_alloc(p, &d.arecs, N * F);
         rc = rc ? rc : plan_alloc(p, &d.aa_list, N * F);
+        rc = rc ? rc : plan_alloc(p, &d.gflag, (size_t)N * d.g.height * div_up(d.g.width, 256));
         rc = rc ? rc : plan_alloc(p, &d.aa_count, 1);
         rc = rc ? rc : plan_alloc(p, &d.clip, N * V);
     }

@@ -104,6 +104,9 @@ struct HsrDev {
     float4* tface;            // [N][F][3]
     uint32_t* aa_list;        // [N * F] faces with a sample where d loss / d pred != 0
     uint32_t* aa_count;       // entries of aa_list (reset by the clip kernel)
+    uint32_t* gflag;          // [N][H][ceil(W / 256)] AA: 1 when a pixel of the 256-pixel row
+                              // segment has d loss / d pred != 0 (the forward writes every
+                              // segment each iteration; the face scan reads only those)
     // the largest bin count above bins.cap this iteration: the kernels that
     // clear the bins take the maximum in bin_over_max (device memory), and
     // one thread of the vertex Adam kernel, which runs after them, hands it
