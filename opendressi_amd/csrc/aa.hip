@@ -582,11 +582,12 @@ __global__ __launch_bounds__(64) void k_aa_raster(HsrDev d) {
     const uint32_t per = (d.g.n_tiles + 7u) / 8u;
     const uint32_t k = blockIdx.x >> 3;
     const uint32_t q = k & 3u;
-    const uint32_t view = (k >> 2) % d.g.n_views;
-    const uint32_t lt = (k >> 2) / d.g.n_views;
+    const uint32_t lt = geom_div(k >> 2, d.g.n_views, d.g.views_m);
+    const uint32_t view = (k >> 2) - lt * d.g.n_views;
     const uint32_t tile = lt * 8u + (blockIdx.x & 7u);
-    const int bx = (int)((tile % d.g.tiles_x) * kTile + (q & 1u) * 8u);
-    const int by = (int)((tile / d.g.tiles_x) * kTile + (q >> 1) * 8u);
+    const uint32_t trow = geom_div(tile, d.g.tiles_x, d.g.tiles_x_m);
+    const int bx = (int)((tile - trow * d.g.tiles_x) * kTile + (q & 1u) * 8u);
+    const int by = (int)(trow * kTile + (q >> 1) * 8u);
     if (lt >= per || tile >= d.g.n_tiles || bx >= (int)d.g.width || by >= (int)d.g.height) {
         return;
     }

@@ -60,15 +60,15 @@ __global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
             return;
         }
         const uint32_t bin = d.heavy.list[seg * kHeavySegCap + slot];
-        view = bin / d.g.n_tiles;
+        view = geom_div(bin, d.g.n_tiles, d.g.tiles_m);
         tile = bin - view * d.g.n_tiles;
     } else {
         const uint32_t b = blockIdx.x - n_first;
         const uint32_t per = (d.g.n_tiles + 7u) / 8u;
         const uint32_t k = b >> 3;
         q = k & 3u;
-        view = (k >> 2) % d.g.n_views;
-        const uint32_t lt = (k >> 2) / d.g.n_views;
+        const uint32_t lt = geom_div(k >> 2, d.g.n_views, d.g.views_m);
+        view = (k >> 2) - lt * d.g.n_views;
         tile = lt * 8u + (b & 7u);
         if (lt >= per || tile >= d.g.n_tiles) {
             return;
@@ -78,8 +78,9 @@ __global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
             return;
         }
     }
-    const int bx = (int)((tile % d.g.tiles_x) * kTile + (q & 1u) * 8u);
-    const int by = (int)((tile / d.g.tiles_x) * kTile + (q >> 1) * 8u);
+    const uint32_t trow = geom_div(tile, d.g.tiles_x, d.g.tiles_x_m);
+    const int bx = (int)((tile - trow * d.g.tiles_x) * kTile + (q & 1u) * 8u);
+    const int by = (int)(trow * kTile + (q >> 1) * 8u);
     if (bx >= (int)d.g.width || by >= (int)d.g.height) {
         return;
     }

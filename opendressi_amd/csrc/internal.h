@@ -166,7 +166,25 @@ constexpr uint32_t kSoftBinCapMax = 16384;
 
 struct RasterGeom {
     uint32_t width, height, tiles_x, tiles_y, n_tiles, n_views, n_faces;
+    // multipliers for the launch decoders' divisions by n_views, tiles_x and
+    // n_tiles (geom_div); 0 where the short form is not exact
+    uint32_t views_m, tiles_x_m, tiles_m;
 };
+
+// ceil(2^32 / d): then n / d = (n * m) >> 32 exactly for every n with
+// n * d < 2^32 (the error n * (m d - 2^32) / (d 2^32) stays below 1 / d);
+// 0 when d < 2 or when n_max * d reaches 2^32
+inline uint32_t div_magic(uint32_t d, uint64_t n_max) {
+    if (d < 2 || n_max * d >= (1ull << 32)) {
+        return 0u;
+    }
+    return (uint32_t)(((1ull << 32) + d - 1) / d);
+}
+
+// n / d with the multiplier m of div_magic (m = 0: the plain division)
+__host__ __device__ inline uint32_t geom_div(uint32_t n, uint32_t d, uint32_t m) {
+    return m ? (uint32_t)(((uint64_t)n * m) >> 32) : n / d;
+}
 
 inline RasterGeom make_geom(uint32_t w, uint32_t h, uint32_t views, uint32_t faces) {
     RasterGeom g;
@@ -177,6 +195,13 @@ inline RasterGeom make_geom(uint32_t w, uint32_t h, uint32_t views, uint32_t fac
     g.n_tiles = g.tiles_x * g.tiles_y;
     g.n_views = views;
     g.n_faces = faces;
+    // the decoders divide tile indices (< n_tiles + 8: a grid's last group
+    // of 8 may pass the end) by tiles_x, bin indices (< n_tiles n_views) by
+    // n_tiles, and tile-group indices (< n_tiles n_views) by n_views
+    const uint64_t bins = (uint64_t)g.n_tiles * views;
+    g.views_m = div_magic(views, bins);
+    g.tiles_x_m = div_magic(g.tiles_x, (uint64_t)g.n_tiles + 8u);
+    g.tiles_m = div_magic(g.n_tiles, bins);
     return g;
 }
 

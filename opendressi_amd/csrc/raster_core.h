@@ -603,8 +603,9 @@ __device__ __forceinline__ BlockPos block_pos(uint32_t wg, const RasterGeom& g) 
     BlockPos b;
     b.tile = (k >> 2) * 8u + (wg & 7u);
     const uint32_t q = k & 3u;
-    b.bx = (int)((b.tile % g.tiles_x) * kTile + (q & 1u) * 8u);
-    b.by = (int)((b.tile / g.tiles_x) * kTile + (q >> 1) * 8u);
+    const uint32_t trow = geom_div(b.tile, g.tiles_x, g.tiles_x_m);
+    b.bx = (int)((b.tile - trow * g.tiles_x) * kTile + (q & 1u) * 8u);
+    b.by = (int)(trow * kTile + (q >> 1) * 8u);
     b.valid = (k >> 2) < per && b.tile < g.n_tiles && b.bx < (int)g.width && b.by < (int)g.height;
     return b;
 }
