@@ -50,6 +50,7 @@ __global__ __launch_bounds__(256) void k_hsr_setup(HsrDev d) {
 // four blocks of a tile of a view are consecutive on one XCD.
 __global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
     uint32_t view, tile, q;
+    BinView bv;
     const uint32_t n_first = 4u * kHeavySegs * d.heavy.cap;
     if (blockIdx.x < n_first) {
         const uint32_t k = blockIdx.x >> 3;
@@ -62,6 +63,7 @@ __global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
         const uint32_t bin = d.heavy.list[seg * kHeavySegCap + slot];
         view = geom_div(bin, d.g.n_tiles, d.g.tiles_m);
         tile = bin - view * d.g.n_tiles;
+        bv = bin_view(d.bins, bin, d.g.n_faces);
     } else {
         const uint32_t b = blockIdx.x - n_first;
         const uint32_t per = (d.g.n_tiles + 7u) / 8u;
@@ -74,7 +76,10 @@ __global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
             return;
         }
         const uint32_t bin = view * d.g.n_tiles + tile;
-        if (heavy_listed(d.heavy, d.bins.counts[bin], bin)) {
+        // the counter and this lane's list entry in one round trip, before
+        // the heavy-list test that reads the counter
+        bv = bin_view(d.bins, bin, d.g.n_faces);
+        if (heavy_listed(d.heavy, bv.count, bin)) {
             return;
         }
     }
@@ -88,7 +93,6 @@ __global__ __launch_bounds__(64) void k_hsr_raster(HsrDev d) {
     const int px = bx + (lane & 7);
     const int py = by + (lane >> 3);
     const size_t vf = (size_t)view * d.g.n_faces;
-    const BinView bv = bin_view(d.bins, view * d.g.n_tiles + tile, d.g.n_faces);
     __shared__ ResolveLds lds;
     const PixelBest best = resolve_block(d.recs + vf, d.cull + vf, bv, bx, by, d.radius, nullptr,
                                          d.g.width, lds);

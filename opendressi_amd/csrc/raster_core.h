@@ -574,6 +574,7 @@ struct BinView {
     uint32_t n;
     bool implicit;
     uint32_t pre;
+    uint32_t count;  // the bin's counter
 };
 
 __device__ __forceinline__ BinView bin_view(const BinBuffers& b, uint32_t bin, uint32_t n_faces) {
@@ -583,6 +584,7 @@ __device__ __forceinline__ BinView bin_view(const BinBuffers& b, uint32_t bin, u
     v.pre = v.list[threadIdx.x & 63u];
     v.implicit = cnt > b.cap;
     v.n = v.implicit ? n_faces : cnt;
+    v.count = cnt;
     return v;
 }
 
